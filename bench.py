@@ -1,0 +1,220 @@
+"""Benchmark of the frozen quantised-matmul hot path on one MI355X.
+
+Workload: one Qwen3-0.6B gate_proj frozen linear, Q4_0 W 3072x1024
+(N(0, 0.02), ggml reference quantiser), X 256x1024 and dy 256x3072 ~ N(0, 1), LoRA r=16 alpha=32
+(A ~ N(0, 1/1024), B ~ N(0, 0.01)); seeds 1..5 of the reference Rng.  One step = one pass of the
+hot path over the batch: Linear forward (y) and Linear backward (dx, dA, dB), device-resident
+inputs, through the C ABI's device-pointer entry points on torch's current stream.  Operand sets
+rotate over >256 MB so neither L2 nor the Infinity Cache holds a step's inputs.
+
+Prints one JSON line: metric/value (tokens/s = T / step time), per-kernel average durations from
+HIP events recorded by the library on the launch stream, the roofline of the dominant kernel, and
+the CPU oracle's time on the host cores (cpu_baseline, bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "trained tokens/s fwd+bwd, Qwen3-0.6B Q4_0 LoRA r16; quant-matmul % roofline"
+N, K, T, R, ALPHA = 3072, 1024, 256, 16, 32.0
+HBM_PEAK_GBS = 8000.0
+F16_PEAK_TFLOPS = 2500.0  # dense f16 MFMA (the forward's integer block dots and dx run on it)
+
+
+def kernel_work(name: str) -> tuple[float, float] | None:
+    """(algorithmic bytes, flops) of one launch of a kernel at the bench shape."""
+    w_bytes = N * K // 32 * 18
+    if name.startswith("rtq_fwd_"):
+        acts = T * K + T * (K // 32) * 2  # int8 codes + fp16 scales
+        return float(w_bytes + acts + T * N * 4 + N * R * 4 + T * R * 4), float(2 * T * N * K + 2 * T * N * R)
+    if name.startswith("rtq_dx_"):
+        return float(w_bytes + T * N * 4 + T * K * 4 + R * K * 4 + T * R * 4), float(2 * T * N * K + 2 * T * R * K)
+    if name == "rtq_quant_q8_0":
+        return float(T * K * 4 + T * K + T * (K // 32) * 2), 0.0
+    if name == "rtq_dy_prep":
+        return float(T * N * 4 + T * N * 2 + T * K * 4), 0.0
+    if name == "rtq_lora_down":
+        return float(T * K * 4 + R * K * 4 + T * R * 4), float(2 * T * K * R)
+    if name == "rtq_lora_g":
+        return float(T * N * 4 + N * R * 4 + T * R * 4), float(2 * T * N * R)
+    if name == "rtq_lora_grads":
+        return float(T * N * 4 + T * K * 4 + 2 * T * R * 4 + 2 * (N * R + R * K) * 4), float(2 * T * R * (N + K))
+    return None
+
+
+def roofline(name: str, avg_ms: float) -> dict:
+    work = kernel_work(name)
+    bytes_, flops = work
+    ai = flops / bytes_ if bytes_ else 0.0
+    ridge = F16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+    sec = avg_ms * 1e-3
+    if ai < ridge:
+        ach = bytes_ / sec / 1e9
+        out = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+               "frac": round(ach / HBM_PEAK_GBS, 4)}
+    else:
+        ach = flops / sec / 1e12
+        out = {"bound": "mfma", "achieved": round(ach, 2), "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+               "frac": round(ach / F16_PEAK_TFLOPS, 4)}
+    out["kernel"] = name
+    out["algorithmic_bytes"] = int(bytes_)
+    out["flops"] = int(flops)
+    out["avg_us"] = round(avg_ms * 1e3, 3)
+    out["traffic"] = measured_traffic(name)
+    return out
+
+
+def measured_traffic(name: str):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary, if any."""
+    p = os.path.join(ROOT, "profiles", f"traffic_{name}_config1.json")
+    if os.path.exists(p):
+        try:
+            return json.load(open(p)).get("bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def cpu_baseline(inputs, seconds: float) -> dict:
+    """The CPU oracle (C restatement of the reference algorithm) on the host cores, bounded sample."""
+    import numpy as np
+
+    import oracle as O
+
+    blocks, x, dy, A, B = inputs
+    threads = max(1, min(16, os.cpu_count() or 1))
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        O.linear_forward(O.Q4_0, blocks, N, K, x, A=A, B=B, alpha=ALPHA, nthreads=threads)
+        O.linear_backward(O.Q4_0, blocks, N, K, x, dy, A=A, B=B, alpha=ALPHA, nthreads=threads)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or steps >= 1000:
+            break
+    del np
+    return {"value": round(T * steps / el, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} config-1 steps (Linear forward + backward, T={T}) in {el:.1f} s; "
+                      f"C restatement of RieFrozen/Linear (oracle/rtq_oracle.c, -O3 AVX2, OpenMP)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sets", type=int, default=40, help="rotating operand sets (~10 MB each)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs the hot path on one GPU only; --gpus {args.gpus} "
+              f"(WORLD_SIZE={world}) is not supported (the multi-GPU sharding is design-only)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import rust_trainer_amd as rt
+    from rust_trainer_amd import _ffi, synth
+
+    W = synth.Rng(1).vec_normal(N * K, 0.02).reshape(N, K)
+    X = synth.Rng(2).vec_normal(T * K, 1.0).reshape(T, K)
+    DY = synth.Rng(3).vec_normal(T * N, 1.0).reshape(T, N)
+    A = synth.Rng(4).vec_normal(R * K, 1.0 / 32.0).reshape(R, K)
+    B = synth.Rng(5).vec_normal(N * R, 0.01).reshape(N, R)
+    blocks = synth.quantize_q4_0(W)
+
+    dev = torch.device("cuda", 0)
+    ctx = rt.Context(0)
+    ctx.reserve(T, N, K, R)
+    sets = []
+    for _ in range(args.sets):
+        s = {
+            "w": rt.HipFrozen(rt.TYPE_Q4_0, blocks, N, K, ctx=ctx),
+            "x": torch.from_numpy(X).to(dev), "dy": torch.from_numpy(DY).to(dev),
+            "y": torch.empty(T, N, device=dev), "dx": torch.empty(T, K, device=dev),
+            "a": torch.from_numpy(A).to(dev), "b": torch.from_numpy(B).to(dev),
+            "ga": torch.zeros(R, K, device=dev), "gb": torch.zeros(N, R, device=dev),
+        }
+        s["lora"] = _ffi.RtqLora(R, ALPHA, s["a"].data_ptr(), s["b"].data_ptr(), 1)
+        sets.append(s)
+    torch.cuda.synchronize()
+    L = _ffi.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step(i: int) -> None:
+        s = sets[i % len(sets)]
+        lp = ctypes.byref(s["lora"])
+        _ffi.check(L.rtq_linear_forward_d(ctx.handle, s["w"].handle, None, lp, s["x"].data_ptr(), T,
+                                          s["y"].data_ptr(), stream), "forward")
+        _ffi.check(L.rtq_linear_backward_d(ctx.handle, s["w"].handle, lp, s["x"].data_ptr(), s["dy"].data_ptr(), T,
+                                           s["dx"].data_ptr(), s["ga"].data_ptr(), s["gb"].data_ptr(), stream),
+                   "backward")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # per-kernel breakdown: HIP events around every launch (separate pass, not the timed one)
+    ctx.set_timing(True)
+    ctx.reset_timing()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    per = {name: (cnt, ms) for name, (cnt, ms) in ctx.timing().items()}
+    ctx.set_timing(False)
+    dominant = max(per, key=lambda k: per[k][1])
+
+    # timed region: events only around the dominant kernel
+    ctx.set_timing(True, dominant)
+    ctx.reset_timing()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    dom_cnt, dom_ms = ctx.timing()[dominant]
+    ctx.set_timing(False)
+    ms_per_step = elapsed * 1e3 / args.steps
+
+    result = {
+        "metric": METRIC,
+        "value": round(T / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0 x q8_0 int block dots -> f32 (fwd); f16 (dx); f32 (LoRA)",
+        "data": "synthetic",
+        "config": {"workload": "configs[0]: Qwen3-0.6B gate_proj frozen linear, Q4_0 W 3072x1024, T=256, "
+                               "LoRA r=16 alpha=32; Linear forward (y) + backward (dx, dA, dB)",
+                   "rows": N, "cols": K, "tokens": T, "rank": R, "operand_sets": args.sets},
+        "roofline": roofline(dominant, dom_ms / dom_cnt),
+        "kernels_avg_us": {k: round(ms * 1e3 / c, 3) for k, (c, ms) in sorted(per.items())},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline((blocks, X, DY, A, B), args.cpu_seconds)
+    for s in sets:
+        s["w"].close()
+    ctx.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,123 @@
+/*
+ * rtq.h — C ABI of the MI355X (gfx950) frozen quantised-matmul library (librtq.so).
+ *
+ * Drop-in boundary for Rust_Trainer's frozen-weight plugin point:
+ *   trait FrozenMatmul            src/frozen.rs:14-25  (out_dim, in_dim, forward, backward_input, row, nbytes)
+ *   impl FrozenMatmul for RieFrozen  src/rie.rs:66-129 (the engine-backed GGUF implementation this replaces)
+ *   RieFrozen::new / loader `fz`  src/rie.rs:58-60, :183 (constructed from a GGUF Weight's packed bytes)
+ *   Linear::forward / backward    src/linear.rs:73-121 (the LoRA math above the frozen weight)
+ *
+ * Conventions (mirroring the reference):
+ *   - all matrices are row-major f32; a weight is [rows = out x cols = in] in GGUF block format;
+ *   - forward OVERWRITES y; backward_input ACCUMULATES into dx (dx += dy . W);
+ *     linear_backward returns a fresh dx (overwrites) and ACCUMULATES ga / gb;
+ *   - errors are status codes (the reference asserts; a Rust wrapper panics on non-zero);
+ *   - host-pointer entry points are synchronous; `_d` entry points take device pointers and a
+ *     HIP stream (hipStream_t passed as void*, NULL = the context's own stream) and only enqueue.
+ *     Calls on one context are serialised by a lock; `_d` calls that share a context must be
+ *     issued on one stream (they share the context's device workspace).
+ */
+#ifndef RTQ_H
+#define RTQ_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int rtq_status;
+#define RTQ_OK 0
+#define RTQ_ERR_INVALID 1     /* bad argument / shape mismatch (reference: assert!) */
+#define RTQ_ERR_UNSUPPORTED 2 /* weight type not implemented on the GPU path */
+#define RTQ_ERR_HIP 3         /* HIP runtime error (message in rtq_last_error) */
+#define RTQ_ERR_NO_DEVICE 4   /* no usable gfx950 device / code object failed to load */
+
+/* GGUF / ggml type ids accepted by rtq_weight_create */
+#define RTQ_TYPE_Q4_0 2
+#define RTQ_TYPE_Q8_0 8
+#define RTQ_TYPE_Q4_K 12
+#define RTQ_TYPE_Q6_K 14
+
+typedef struct rtq_ctx rtq_ctx;
+typedef struct rtq_weight rtq_weight;
+
+/* LoRA adapter view (src/linear.rs:8-16): a is [rank x in], b is [out x rank], scale = alpha/rank.
+ * enabled = 0 bypasses the adapter (Linear::lora_enabled, src/linear.rs:45). */
+typedef struct rtq_lora {
+  int64_t rank;
+  float alpha;
+  const float* a;
+  const float* b;
+  int enabled;
+} rtq_lora;
+
+/* ---- library / context ---- */
+const char* rtq_version(void);
+const char* rtq_last_error(void); /* thread-local message of the last failing call */
+/* Opens device `device`, loads the embedded gfx950 code object (hipModuleLoadData), creates a stream.
+ * Replaces the engine ThreadPool the reference threads through RieFrozen (src/rie.rs:53,182). */
+rtq_status rtq_ctx_create(int device, rtq_ctx** out);
+void rtq_ctx_destroy(rtq_ctx* ctx);
+void* rtq_ctx_stream(rtq_ctx* ctx); /* the context's hipStream_t */
+/* Pre-sizes the device workspace for calls up to t tokens on any weight of this context. */
+rtq_status rtq_ctx_reserve(rtq_ctx* ctx, int64_t max_t, int64_t max_rows, int64_t max_cols, int64_t max_rank);
+/* Per-kernel timing with HIP events recorded around launches (off by default); only_kernel (may be
+ * NULL) restricts the events to launches of the kernel with that name. */
+rtq_status rtq_ctx_set_timing(rtq_ctx* ctx, int enable, const char* only_kernel);
+/* Synchronises, folds the recorded events into per-kernel totals, returns the number of kernels seen. */
+int rtq_ctx_timing_count(rtq_ctx* ctx);
+rtq_status rtq_ctx_timing_get(rtq_ctx* ctx, int i, const char** name, int64_t* launches, double* total_ms);
+void rtq_ctx_timing_reset(rtq_ctx* ctx);
+
+/* ---- weights (RieFrozen::new, src/rie.rs:58-60; Weight::data() bytes, src/rie.rs:186) ---- */
+/* blocks: rows * row_bytes(type, cols) bytes of GGUF blocks on the host; uploaded once into the
+ * device fragment layout (same byte count, padded to 64-row / 128|256-column tiles). */
+rtq_status rtq_weight_create(rtq_ctx* ctx, int ggml_type, const void* blocks, size_t nbytes, int64_t rows,
+                             int64_t cols, rtq_weight** out);
+void rtq_weight_destroy(rtq_weight* w);
+int64_t rtq_weight_out_dim(const rtq_weight* w); /* FrozenMatmul::out_dim, src/frozen.rs:15 */
+int64_t rtq_weight_in_dim(const rtq_weight* w);  /* FrozenMatmul::in_dim,  src/frozen.rs:16 */
+size_t rtq_weight_nbytes(const rtq_weight* w);   /* FrozenMatmul::nbytes (GGUF bytes), src/frozen.rs:24 */
+int rtq_weight_type(const rtq_weight* w);
+
+/* ---- FrozenMatmul (host pointers, synchronous) ---- */
+/* y[t x out] = x[t x in] . W^T    (src/frozen.rs:17-18; RieFrozen::forward src/rie.rs:74-82) */
+rtq_status rtq_frozen_forward(rtq_ctx* ctx, const rtq_weight* w, const float* x, int64_t t, float* y);
+/* dx[t x in] += dy[t x out] . W   (src/frozen.rs:19-20; RieFrozen::backward_input src/rie.rs:84-120) */
+rtq_status rtq_frozen_backward_input(rtq_ctx* ctx, const rtq_weight* w, const float* dy, int64_t t, float* dx);
+/* out[in] = dequant(W[r])          (src/frozen.rs:21-22; RieFrozen::row src/rie.rs:122-124) */
+rtq_status rtq_frozen_row(rtq_ctx* ctx, const rtq_weight* w, int64_t r, float* out);
+
+/* ---- Linear (host pointers, synchronous) ---- */
+/* y = x.W^T (+ bias) (+ (alpha/r) (x.A^T).B^T)     (Linear::forward, src/linear.rs:73-93) */
+rtq_status rtq_linear_forward(rtq_ctx* ctx, const rtq_weight* w, const float* bias, const rtq_lora* lora,
+                              const float* x, int64_t t, float* y);
+/* dx = dy.W (+ s (dy.B).A); ga += (s dy.B)^T x; gb += (s dy)^T (x.A^T)   (Linear::backward, src/linear.rs:97-121) */
+rtq_status rtq_linear_backward(rtq_ctx* ctx, const rtq_weight* w, const rtq_lora* lora, const float* x,
+                               const float* dy, int64_t t, float* dx, float* ga, float* gb);
+
+/* ---- device-pointer variants (enqueue only; same semantics) ---- */
+rtq_status rtq_frozen_forward_d(rtq_ctx* ctx, const rtq_weight* w, const float* x, int64_t t, float* y, void* stream);
+rtq_status rtq_frozen_backward_input_d(rtq_ctx* ctx, const rtq_weight* w, const float* dy, int64_t t, float* dx,
+                                       void* stream);
+rtq_status rtq_frozen_rows_d(rtq_ctx* ctx, const rtq_weight* w, int64_t r0, int64_t count, float* out, void* stream);
+/* lora->a / lora->b and bias are device pointers here */
+rtq_status rtq_linear_forward_d(rtq_ctx* ctx, const rtq_weight* w, const float* bias, const rtq_lora* lora,
+                                const float* x, int64_t t, float* y, void* stream);
+rtq_status rtq_linear_backward_d(rtq_ctx* ctx, const rtq_weight* w, const rtq_lora* lora, const float* x,
+                                 const float* dy, int64_t t, float* dx, float* ga, float* gb, void* stream);
+
+/* ---- parity / debug (host pointers, synchronous) ---- */
+/* The activation blocks the GPU forward actually uses for x, in ggml layout (block_q8_0: 34 B per
+ * 32 elements for Q4_0/Q8_0 weights; block_q8_K: 292 B per 256 for Q4_K/Q6_K), t * act_row_bytes. */
+rtq_status rtq_debug_quantize_acts(rtq_ctx* ctx, const rtq_weight* w, const float* x, int64_t t, void* out);
+int64_t rtq_debug_isums_per_row(const rtq_weight* w);
+/* The integer block sums computed by the GPU forward kernel itself: int32 [t][out][isums_per_row]
+ * (Q4_0/Q8_0: one per 32-block; Q4_K: (S1, S2) per super-block; Q6_K: S per super-block). */
+rtq_status rtq_debug_block_isums(rtq_ctx* ctx, const rtq_weight* w, const float* x, int64_t t, int32_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,278 @@
+"""CPU oracle for the frozen quantised-matmul path (TEST INFRASTRUCTURE ONLY).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+this package, and only as the checker or the timed CPU baseline.  The product library
+(``rust_trainer_amd``) never imports it and has no CPU fallback.
+
+It wraps ``oracle/liboracle.so`` (built from ``rtq_oracle.c`` by ``oracle/Makefile``), a C
+restatement of the reference's CPU path:
+
+* ``src/frozen.rs:14-25`` FrozenMatmul contract; ``src/rie.rs:74-124`` RieFrozen forward
+  (activation quantisation + integer block dots), backward_input (32-row dequant + axpy),
+  row (dequant_row);
+* ``src/linear.rs:73-121`` Linear LoRA forward/backward; ``src/tensor.rs:24-120`` primitives;
+* ``src/tensor.rs:155-199`` Rng;
+* ggml block semantics for Q4_0 / Q8_0 / Q4_K / Q6_K weights and Q8_0 / Q8_K activations
+  (rie-core, pinned at f3be365b41f929cc81ee08afaa994d02bbeee2f5 in Cargo.lock:529-540, is
+  absent from the container; parity against it is unpinned).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K = 0, 1, 2, 8, 12, 14, 15
+TYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_K: "Q8_K"}
+BLOCK_ELEMS = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256}
+BLOCK_BYTES = {F32: 4, F16: 2, Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210, Q8_K: 292}
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_f = ctypes.c_float
+_i = ctypes.c_int
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "liboracle.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built; run __graft_entry__.build() (or make -C oracle)")
+        L = ctypes.CDLL(path)
+        sig = {
+            "or_rng_seed": (ctypes.c_uint64, [ctypes.c_uint64]),
+            "or_rng_next_u64": (ctypes.c_uint64, [_p]),
+            "or_rng_uniform": (_f, [_p]),
+            "or_rng_normal": (_f, [_p]),
+            "or_rng_fill_normal": (None, [_p, _p, _i64, _f]),
+            "or_rng_fill_uniform_sym": (None, [_p, _p, _i64, _f]),
+            "or_fp32_to_fp16": (ctypes.c_uint16, [_f]),
+            "or_fp16_to_fp32": (_f, [ctypes.c_uint16]),
+            "or_row_bytes": (_i64, [_i, _i64]),
+            "or_quantize": (_i, [_i, _p, _i64, _p]),
+            "or_dequant_row": (_i, [_i, _p, _i64, _p]),
+            "or_act_type_for": (_i, [_i]),
+            "or_quantize_acts_q8_0": (None, [_p, _i64, _p]),
+            "or_quantize_acts_q8_k": (None, [_p, _i64, _p]),
+            "or_isums_per_row": (_i64, [_i, _i64]),
+            "or_block_isums": (_i, [_i, _p, _p, _i64, _p]),
+            "or_frozen_forward": (_i, [_i, _p, _i64, _i64, _p, _i64, _p, _i]),
+            "or_frozen_forward_f64": (_i, [_i, _p, _i64, _i64, _p, _i64, _p]),
+            "or_frozen_backward_input": (_i, [_i, _p, _i64, _i64, _p, _i64, _p, _i]),
+            "or_frozen_row": (_i, [_i, _p, _i64, _i64, _i64, _p]),
+            "or_dot": (_f, [_p, _p, _i64]),
+            "or_matmul_nt": (None, [_p, _p, _i64, _i64, _i64, _p, _i]),
+            "or_matmul_nn": (None, [_p, _p, _i64, _i64, _i64, _p, _i]),
+            "or_matmul_tn_acc": (None, [_p, _p, _p, _i64, _i64, _i64, _i]),
+            "or_linear_forward": (_i, [_i, _p, _i64, _i64, _p, _i64, _f, _p, _p, _i, _p, _i64, _p, _i]),
+            "or_linear_backward": (_i, [_i, _p, _i64, _i64, _i64, _f, _p, _p, _i, _p, _p, _i64, _p, _p, _p, _i]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def _ptr(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _check(rc: int, what: str):
+    if rc != 0:
+        raise ValueError(f"oracle {what} failed with code {rc}")
+
+
+class Rng:
+    """SplitMix64 + Box-Muller, src/tensor.rs:155-199 (same seeds give the same streams)."""
+
+    def __init__(self, seed: int):
+        self._state = np.array([lib().or_rng_seed(seed)], dtype=np.uint64)
+
+    @property
+    def state(self) -> int:
+        return int(self._state[0])
+
+    def next_u64(self) -> int:
+        return int(lib().or_rng_next_u64(_ptr(self._state)))
+
+    def uniform(self) -> float:
+        return float(lib().or_rng_uniform(_ptr(self._state)))
+
+    def normal(self) -> float:
+        return float(lib().or_rng_normal(_ptr(self._state)))
+
+    def vec_normal(self, n: int, std: float) -> np.ndarray:
+        out = np.empty(n, dtype=np.float32)
+        lib().or_rng_fill_normal(_ptr(self._state), _ptr(out), n, std)
+        return out
+
+    def vec_uniform_sym(self, n: int, bound: float) -> np.ndarray:
+        out = np.empty(n, dtype=np.float32)
+        lib().or_rng_fill_uniform_sym(_ptr(self._state), _ptr(out), n, bound)
+        return out
+
+
+def fp32_to_fp16_bits(v: float) -> int:
+    return int(lib().or_fp32_to_fp16(v))
+
+
+def fp16_bits_to_fp32(h: int) -> float:
+    return float(lib().or_fp16_to_fp32(h))
+
+
+def row_bytes(wtype: int, k: int) -> int:
+    return int(lib().or_row_bytes(wtype, k))
+
+
+def quantize(wtype: int, w: np.ndarray) -> np.ndarray:
+    """Quantise an [n x k] f32 matrix row-major into GGUF blocks (uint8 [n, row_bytes])."""
+    w = _f32(w)
+    n, k = w.shape
+    out = np.empty((n, row_bytes(wtype, k)), dtype=np.uint8)
+    _check(lib().or_quantize(wtype, _ptr(w), w.size, _ptr(out)), "quantize")
+    return out
+
+
+def dequantize(wtype: int, blocks: np.ndarray, k: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    n = blocks.size // row_bytes(wtype, k)
+    out = np.empty((n, k), dtype=np.float32)
+    _check(lib().or_dequant_row(wtype, _ptr(blocks), n * k, _ptr(out)), "dequant")
+    return out
+
+
+def act_type_for(wtype: int) -> int:
+    return int(lib().or_act_type_for(wtype))
+
+
+def quantize_acts(wtype: int, x: np.ndarray) -> np.ndarray:
+    """QuantActs::prepare for the activation format paired with ``wtype``: uint8 [t, act_row_bytes]."""
+    x = _f32(x)
+    t, k = x.shape
+    at = act_type_for(wtype)
+    out = np.empty((t, row_bytes(at, k)), dtype=np.uint8)
+    fn = lib().or_quantize_acts_q8_0 if at == Q8_0 else lib().or_quantize_acts_q8_k
+    for i in range(t):
+        fn(_ptr(x[i]), k, _ptr(out[i]))
+    return out
+
+
+def block_isums(wtype: int, wblocks: np.ndarray, acts: np.ndarray, k: int) -> np.ndarray:
+    """Integer block sums for every (token, row): int32 [t, n, isums_per_row]."""
+    wblocks = np.ascontiguousarray(wblocks, dtype=np.uint8)
+    acts = np.ascontiguousarray(acts, dtype=np.uint8)
+    n, t = wblocks.shape[0], acts.shape[0]
+    m = int(lib().or_isums_per_row(wtype, k))
+    out = np.empty((t, n, m), dtype=np.int32)
+    for i in range(t):
+        for o in range(n):
+            _check(lib().or_block_isums(wtype, _ptr(wblocks[o]), _ptr(acts[i]), k, _ptr(out[i, o])), "isums")
+    return out
+
+
+def frozen_forward(wtype, wblocks, n, k, x, nthreads=1) -> np.ndarray:
+    x = _f32(x).reshape(-1, k)
+    t = x.shape[0]
+    y = np.empty((t, n), dtype=np.float32)
+    _check(lib().or_frozen_forward(wtype, _ptr(np.ascontiguousarray(wblocks)), n, k, _ptr(x), t, _ptr(y), nthreads),
+           "forward")
+    return y
+
+
+def frozen_forward_f64(wtype, wblocks, n, k, x) -> np.ndarray:
+    x = _f32(x).reshape(-1, k)
+    t = x.shape[0]
+    y = np.empty((t, n), dtype=np.float64)
+    _check(lib().or_frozen_forward_f64(wtype, _ptr(np.ascontiguousarray(wblocks)), n, k, _ptr(x), t, _ptr(y)),
+           "forward_f64")
+    return y
+
+
+def frozen_backward_input(wtype, wblocks, n, k, dy, dx=None, nthreads=1) -> np.ndarray:
+    dy = _f32(dy).reshape(-1, n)
+    t = dy.shape[0]
+    dx = np.zeros((t, k), dtype=np.float32) if dx is None else _f32(dx).copy()
+    _check(lib().or_frozen_backward_input(wtype, _ptr(np.ascontiguousarray(wblocks)), n, k, _ptr(dy), t, _ptr(dx),
+                                          nthreads), "backward_input")
+    return dx
+
+
+def frozen_row(wtype, wblocks, n, k, r) -> np.ndarray:
+    out = np.empty(k, dtype=np.float32)
+    _check(lib().or_frozen_row(wtype, _ptr(np.ascontiguousarray(wblocks)), n, k, r, _ptr(out)), "row")
+    return out
+
+
+def dot(a, b) -> float:
+    a, b = _f32(a), _f32(b)
+    return float(lib().or_dot(_ptr(a), _ptr(b), a.size))
+
+
+def matmul_nt(a, b, nthreads=1):
+    a, b = _f32(a), _f32(b)
+    m, k = a.shape
+    n = b.shape[0]
+    out = np.empty((m, n), dtype=np.float32)
+    lib().or_matmul_nt(_ptr(a), _ptr(b), m, k, n, _ptr(out), nthreads)
+    return out
+
+
+def matmul_nn(a, b, nthreads=1):
+    a, b = _f32(a), _f32(b)
+    m, k = a.shape
+    n = b.shape[1]
+    out = np.empty((m, n), dtype=np.float32)
+    lib().or_matmul_nn(_ptr(a), _ptr(b), m, k, n, _ptr(out), nthreads)
+    return out
+
+
+def matmul_tn_acc(out, a, b, nthreads=1):
+    a, b = _f32(a), _f32(b)
+    k, m = a.shape
+    n = b.shape[1]
+    assert out.shape == (m, n) and out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
+    lib().or_matmul_tn_acc(_ptr(out), _ptr(a), _ptr(b), k, m, n, nthreads)
+    return out
+
+
+def linear_forward(wtype, wblocks, n, k, x, bias=None, A=None, B=None, alpha=0.0, lora_enabled=True, nthreads=1):
+    x = _f32(x).reshape(-1, k)
+    t = x.shape[0]
+    rank = 0 if A is None else A.shape[0]
+    y = np.empty((t, n), dtype=np.float32)
+    _check(lib().or_linear_forward(wtype, _ptr(np.ascontiguousarray(wblocks)), n, k,
+                                   _ptr(None if bias is None else _f32(bias)), rank, alpha,
+                                   _ptr(None if A is None else _f32(A)), _ptr(None if B is None else _f32(B)),
+                                   int(lora_enabled), _ptr(x), t, _ptr(y), nthreads), "linear_forward")
+    return y
+
+
+def linear_backward(wtype, wblocks, n, k, x, dy, A=None, B=None, alpha=0.0, ga=None, gb=None, lora_enabled=True,
+                    nthreads=1):
+    """Returns (dx, ga, gb); ga/gb accumulate into copies of the given arrays (zeros if None)."""
+    x = _f32(x).reshape(-1, k)
+    dy = _f32(dy).reshape(-1, n)
+    t = x.shape[0]
+    rank = 0 if A is None else A.shape[0]
+    dx = np.empty((t, k), dtype=np.float32)
+    ga = np.zeros((rank, k), np.float32) if ga is None else _f32(ga).copy()
+    gb = np.zeros((n, rank), np.float32) if gb is None else _f32(gb).copy()
+    _check(lib().or_linear_backward(wtype, _ptr(np.ascontiguousarray(wblocks)), n, k, rank, alpha,
+                                    _ptr(None if A is None else _f32(A)), _ptr(None if B is None else _f32(B)),
+                                    int(lora_enabled), _ptr(x), _ptr(dy), t, _ptr(dx), _ptr(ga), _ptr(gb), nthreads),
+           "linear_backward")
+    return dx, ga, gb

@@ -1,0 +1,106 @@
+/*
+ * rtq_oracle.h — CPU restatement of Rust_Trainer's frozen quantised-matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker / the timed CPU
+ * baseline.  The product path (librtq.so) never links or calls it.
+ *
+ * Reference sources restated (files under the reference repository):
+ *   src/frozen.rs:14-25     FrozenMatmul contract (forward overwrites y, backward_input accumulates dx)
+ *   src/rie.rs:74-82        RieFrozen::forward   = activation quantisation + integer block dots
+ *   src/rie.rs:84-120       RieFrozen::backward_input = 32-row dequant chunks + f32 axpy, reduced
+ *   src/rie.rs:122-124      RieFrozen::row       = Weight::dequant_row
+ *   src/linear.rs:73-121    Linear::forward / Linear::backward (LoRA order)
+ *   src/tensor.rs:24-120    dot / axpy / matmul_nt / matmul_nn / matmul_tn_acc
+ *   src/tensor.rs:155-199   Rng (SplitMix64 + Box-Muller)
+ *   ggml block formats Q4_0, Q8_0, Q4_K, Q6_K and activation blocks Q8_0 / Q8_K; rie-core
+ *   (git dependency pinned at f3be365b41f929cc81ee08afaa994d02bbeee2f5, Cargo.lock:529-540,
+ *   absent from the container) follows ggml's public block semantics for these formats.
+ */
+#ifndef RTQ_ORACLE_H
+#define RTQ_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (same numbering as the GGUF format) */
+enum {
+  OR_F32 = 0,
+  OR_F16 = 1,
+  OR_Q4_0 = 2,
+  OR_Q8_0 = 8,
+  OR_Q4_K = 12,
+  OR_Q6_K = 14,
+  OR_Q8_K = 15
+};
+
+/* ---- Rng: src/tensor.rs:155-199 ---- */
+uint64_t or_rng_seed(uint64_t seed);
+uint64_t or_rng_next_u64(uint64_t* state);
+float or_rng_uniform(uint64_t* state);
+float or_rng_normal(uint64_t* state);
+void or_rng_fill_normal(uint64_t* state, float* out, int64_t n, float std);
+void or_rng_fill_uniform_sym(uint64_t* state, float* out, int64_t n, float bound);
+
+/* ---- IEEE half ---- */
+uint16_t or_fp32_to_fp16(float f);
+float or_fp16_to_fp32(uint16_t h);
+
+/* ---- block formats ---- */
+int64_t or_block_elems(int type);
+int64_t or_block_bytes(int type);
+int64_t or_row_bytes(int type, int64_t k);
+/* weight quantisers; n must be a multiple of the block size */
+int or_quantize(int type, const float* x, int64_t n, void* out);
+/* one row of k elements -> f32; returns 0 on success */
+int or_dequant_row(int type, const void* row, int64_t k, float* out);
+
+/* ---- activation quantisation (QuantActs::prepare, src/rie.rs:77-78) ---- */
+/* act type paired with a weight type: Q8_0 for Q4_0/Q8_0, Q8_K for Q4_K/Q6_K, F32 otherwise */
+int or_act_type_for(int wtype);
+void or_quantize_acts_q8_0(const float* x, int64_t k, void* out); /* k % 32 == 0, 34 B blocks */
+void or_quantize_acts_q8_k(const float* x, int64_t k, void* out); /* k % 256 == 0, 292 B blocks */
+
+/* ---- integer block dots ----
+ * number of int32 outputs per row pair: Q4_0/Q8_0 -> k/32 (one isum per block);
+ * Q4_K -> 2*k/256 (S1 = sum_j sc_j*isum_j, S2 = sum_j m_j*(bsum_2j + bsum_2j+1));
+ * Q6_K -> k/256 (S = sum_s sc_s*isum_s). */
+int64_t or_isums_per_row(int wtype, int64_t k);
+int or_block_isums(int wtype, const void* wrow, const void* arow, int64_t k, int32_t* out);
+
+/* ---- FrozenMatmul (src/frozen.rs:14-25, src/rie.rs:74-124) ---- */
+/* y[t x n] = x[t x k] . W^T   (y overwritten) */
+int or_frozen_forward(int wtype, const void* w, int64_t n, int64_t k, const float* x, int64_t t, float* y,
+                      int nthreads);
+/* same operands, f64 accumulation of the f32-exact block terms (pins the f32 epilogue) */
+int or_frozen_forward_f64(int wtype, const void* w, int64_t n, int64_t k, const float* x, int64_t t,
+                          double* y);
+/* dx[t x k] += dy[t x n] . W */
+int or_frozen_backward_input(int wtype, const void* w, int64_t n, int64_t k, const float* dy, int64_t t,
+                             float* dx, int nthreads);
+int or_frozen_row(int wtype, const void* w, int64_t n, int64_t k, int64_t r, float* out);
+
+/* ---- dense primitives (src/tensor.rs:24-120) ---- */
+float or_dot(const float* a, const float* b, int64_t n);
+void or_matmul_nt(const float* a, const float* b, int64_t m, int64_t k, int64_t n, float* out, int nthreads);
+void or_matmul_nn(const float* a, const float* b, int64_t m, int64_t k, int64_t n, float* out, int nthreads);
+void or_matmul_tn_acc(float* out, const float* a, const float* b, int64_t k, int64_t m, int64_t n,
+                      int nthreads);
+
+/* ---- Linear + LoRA (src/linear.rs:73-121) ----
+ * A is [r x k], B is [n x r]; scale = alpha / r; lora_enabled 0 bypasses the adapter. */
+int or_linear_forward(int wtype, const void* w, int64_t n, int64_t k, const float* bias, int64_t rank,
+                      float alpha, const float* A, const float* B, int lora_enabled, const float* x, int64_t t,
+                      float* y, int nthreads);
+/* dx overwritten (Linear::backward returns a fresh dx); ga [r x k] and gb [n x r] accumulate */
+int or_linear_backward(int wtype, const void* w, int64_t n, int64_t k, int64_t rank, float alpha,
+                       const float* A, const float* B, int lora_enabled, const float* x, const float* dy,
+                       int64_t t, float* dx, float* ga, float* gb, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

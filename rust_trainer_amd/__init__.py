@@ -1,0 +1,13 @@
+"""rust_trainer_amd — MI355X (gfx950) frozen quantised-matmul path for Rust_Trainer-style LoRA training.
+
+The product is ``librtq.so`` (C ABI, ``include/rtq.h``): hand-written gfx950 kernels for the GGUF
+frozen linear's forward (``y = W_q.x + (alpha/r) B.A.x``), input gradient (``dx = W_q^T.dy``) and
+LoRA gradients.  This package is the host-side mirror of the reference's plugin interface
+(``FrozenMatmul``, ``Lora``, ``Linear``) over that C ABI.
+"""
+from ._ffi import RtqError, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, lib  # noqa: F401
+from .frozen import Context, FrozenMatmul, HipFrozen, default_context  # noqa: F401
+from .linear import Linear, Lora  # noqa: F401
+
+__all__ = ["Context", "FrozenMatmul", "HipFrozen", "Linear", "Lora", "RtqError", "default_context", "lib",
+           "TYPE_Q4_0", "TYPE_Q8_0", "TYPE_Q4_K", "TYPE_Q6_K"]

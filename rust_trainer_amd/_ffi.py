@@ -1,0 +1,94 @@
+"""ctypes binding of librtq.so (include/rtq.h).
+
+The library is built in-tree by ``__graft_entry__.build()`` (``rust_trainer_amd/csrc/build.py``).
+There is no CPU fallback: a missing library, a missing device or a failing call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "librtq.so")
+
+RTQ_OK = 0
+STATUS_NAMES = {0: "OK", 1: "ERR_INVALID", 2: "ERR_UNSUPPORTED", 3: "ERR_HIP", 4: "ERR_NO_DEVICE"}
+
+TYPE_Q4_0, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 2, 8, 12, 14
+
+# every symbol include/rtq.h declares, with (restype, argtypes)
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i = ctypes.c_int
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+
+
+class RtqLora(ctypes.Structure):
+    _fields_ = [("rank", ctypes.c_int64), ("alpha", ctypes.c_float), ("a", ctypes.c_void_p),
+                ("b", ctypes.c_void_p), ("enabled", ctypes.c_int)]
+
+
+_LP = ctypes.POINTER(RtqLora)
+
+SIGNATURES = {
+    "rtq_version": (ctypes.c_char_p, []),
+    "rtq_last_error": (ctypes.c_char_p, []),
+    "rtq_ctx_create": (_i, [_i, ctypes.POINTER(_p)]),
+    "rtq_ctx_destroy": (None, [_p]),
+    "rtq_ctx_stream": (_p, [_p]),
+    "rtq_ctx_reserve": (_i, [_p, _i64, _i64, _i64, _i64]),
+    "rtq_ctx_set_timing": (_i, [_p, _i, ctypes.c_char_p]),
+    "rtq_ctx_timing_count": (_i, [_p]),
+    "rtq_ctx_timing_get": (_i, [_p, _i, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i64),
+                                ctypes.POINTER(ctypes.c_double)]),
+    "rtq_ctx_timing_reset": (None, [_p]),
+    "rtq_weight_create": (_i, [_p, _i, _p, _sz, _i64, _i64, ctypes.POINTER(_p)]),
+    "rtq_weight_destroy": (None, [_p]),
+    "rtq_weight_out_dim": (_i64, [_p]),
+    "rtq_weight_in_dim": (_i64, [_p]),
+    "rtq_weight_nbytes": (_sz, [_p]),
+    "rtq_weight_type": (_i, [_p]),
+    "rtq_frozen_forward": (_i, [_p, _p, _p, _i64, _p]),
+    "rtq_frozen_backward_input": (_i, [_p, _p, _p, _i64, _p]),
+    "rtq_frozen_row": (_i, [_p, _p, _i64, _p]),
+    "rtq_linear_forward": (_i, [_p, _p, _p, _LP, _p, _i64, _p]),
+    "rtq_linear_backward": (_i, [_p, _p, _LP, _p, _p, _i64, _p, _p, _p]),
+    "rtq_frozen_forward_d": (_i, [_p, _p, _p, _i64, _p, _p]),
+    "rtq_frozen_backward_input_d": (_i, [_p, _p, _p, _i64, _p, _p]),
+    "rtq_frozen_rows_d": (_i, [_p, _p, _i64, _i64, _p, _p]),
+    "rtq_linear_forward_d": (_i, [_p, _p, _p, _LP, _p, _i64, _p, _p]),
+    "rtq_linear_backward_d": (_i, [_p, _p, _LP, _p, _p, _i64, _p, _p, _p, _p]),
+    "rtq_debug_quantize_acts": (_i, [_p, _p, _p, _i64, _p]),
+    "rtq_debug_isums_per_row": (_i64, [_p]),
+    "rtq_debug_block_isums": (_i, [_p, _p, _p, _i64, _p]),
+}
+
+_LIB = None
+
+
+class RtqError(RuntimeError):
+    def __init__(self, status: int, what: str, msg: str):
+        super().__init__(f"{what} failed: {STATUS_NAMES.get(status, status)}: {msg}")
+        self.status = status
+
+
+def lib() -> ctypes.CDLL:
+    """Loads librtq.so (raises if it has not been built)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def check(status: int, what: str) -> None:
+    if status != RTQ_OK:
+        msg = lib().rtq_last_error()
+        raise RtqError(status, what, msg.decode() if msg else "")

@@ -1,0 +1,936 @@
+// rtq_runtime.cpp — host runtime of librtq.so: the C ABI declared in include/rtq.h.
+//
+// Owns the HIP context pieces (device, stream, the gfx950 code object loaded with
+// hipModuleLoadData from bytes embedded at build time), the device copies of the frozen weights
+// in their fragment layout, and a grow-only device workspace for per-call intermediates.
+// Every launch goes through hipModuleLaunchKernel with one argument block (rtq_kargs.h).
+//
+// There is no CPU fallback: every entry point fails with a status code when the device or the
+// code object is unavailable.
+#include "rtq.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "rtq_kargs.h"
+
+#ifndef RTQ_HSACO_PATH
+#error "RTQ_HSACO_PATH must name the gfx950 code object to embed"
+#endif
+
+// The code object is embedded into the shared library so that no file lookup happens at run time.
+__asm__(
+    ".section .rodata.rtq_hsaco,\"a\",@progbits\n"
+    ".balign 4096\n"
+    ".local rtq_hsaco_begin\n"
+    "rtq_hsaco_begin:\n"
+    ".incbin \"" RTQ_HSACO_PATH
+    "\"\n"
+    ".local rtq_hsaco_end\n"
+    "rtq_hsaco_end:\n"
+    ".byte 0\n"
+    ".previous\n");
+extern "C" const char rtq_hsaco_begin[];
+extern "C" const char rtq_hsaco_end[];
+
+namespace {
+
+thread_local std::string g_err;
+
+rtq_status fail(rtq_status st, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return st;
+}
+
+#define HIP_TRY(expr)                                                                              \
+  do {                                                                                             \
+    hipError_t e_ = (expr);                                                                        \
+    if (e_ != hipSuccess) return fail(RTQ_ERR_HIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_), \
+                                      __FILE__, __LINE__);                                         \
+  } while (0)
+
+#define RTQ_TRY(expr)              \
+  do {                             \
+    rtq_status s_ = (expr);        \
+    if (s_ != RTQ_OK) return s_;   \
+  } while (0)
+
+inline int64_t roundup(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+uint16_t f32_to_f16_bits(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+  if (ax < 0x38800000u) {
+    float af;
+    memcpy(&af, &ax, 4);
+    return (uint16_t)(sign | (uint32_t)__builtin_nearbyintf(af * 16777216.0f));
+  }
+  uint32_t e = (ax >> 23) - 112, mant = ax & 0x7fffffu, h = (e << 10) | (mant >> 13), rem = mant & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+  return (uint16_t)(sign | h);
+}
+
+float f16_bits_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  uint32_t bits;
+  if (e == 0) {
+    float v = (float)m * (1.0f / 16777216.0f);
+    memcpy(&bits, &v, 4);
+    bits |= sign;
+  } else if (e == 31) {
+    bits = sign | 0x7f800000u | (m << 13);
+  } else {
+    bits = sign | ((e + 112) << 23) | (m << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+enum Kid {
+  K_FILL,
+  K_QUANT_Q8_0,
+  K_LORA_DOWN,
+  K_FWD_Q4_0,
+  K_FWD_Q8_0,
+  K_FWD_Q4_0_ISUMS,
+  K_FWD_Q8_0_ISUMS,
+  K_DY_PREP,
+  K_LORA_G,
+  K_DX_Q4_0,
+  K_DX_Q8_0,
+  K_LORA_GRADS,
+  K_ROWS_Q4_0,
+  K_ROWS_Q8_0,
+  K_COUNT
+};
+const char* kKernelNames[K_COUNT] = {
+    "rtq_fill_zero", "rtq_quant_q8_0", "rtq_lora_down", "rtq_fwd_q4_0", "rtq_fwd_q8_0", "rtq_fwd_q4_0_isums",
+    "rtq_fwd_q8_0_isums", "rtq_dy_prep", "rtq_lora_g", "rtq_dx_q4_0", "rtq_dx_q8_0", "rtq_lora_grads",
+    "rtq_rows_q4_0", "rtq_rows_q8_0"};
+
+struct TimedLaunch {
+  int kid;
+  hipEvent_t a, b;
+};
+
+}  // namespace
+
+struct rtq_ctx {
+  int device = 0;
+  int cu_count = 256;
+  hipModule_t mod = nullptr;
+  hipFunction_t fn[K_COUNT] = {};
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  bool timing = false;
+  int timing_only = -1;  // -1: every kernel
+  std::vector<TimedLaunch> pending;
+  std::vector<hipEvent_t> free_events;
+  int64_t t_launches[K_COUNT] = {};
+  double t_ms[K_COUNT] = {};
+};
+
+struct rtq_weight {
+  rtq_ctx* ctx = nullptr;
+  int type = 0;
+  int64_t rows = 0, cols = 0;  // N, K
+  int64_t Np = 0, Kp = 0;
+  size_t gguf_bytes = 0;
+  void* dmem = nullptr;
+  void* wq = nullptr;
+  uint16_t* wd = nullptr;
+  void* wx = nullptr;
+};
+
+namespace {
+
+// ------------------------------------------------------------------ launching
+hipEvent_t get_event(rtq_ctx* c) {
+  if (!c->free_events.empty()) {
+    hipEvent_t e = c->free_events.back();
+    c->free_events.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+template <class Args>
+rtq_status launch(rtq_ctx* c, int kid, dim3 grid, dim3 block, hipStream_t s, const Args& args) {
+  if (grid.x == 0 || grid.y == 0 || grid.z == 0) return RTQ_OK;
+  if (grid.y > 65535 || grid.z > 65535)
+    return fail(RTQ_ERR_INVALID, "%s: grid (%u,%u,%u) out of range", kKernelNames[kid], grid.x, grid.y, grid.z);
+  Args copy = args;
+  void* params[] = {&copy};
+  hipEvent_t ea = nullptr, eb = nullptr;
+  const bool timed = c->timing && (c->timing_only < 0 || c->timing_only == kid);
+  if (timed) {
+    ea = get_event(c);
+    eb = get_event(c);
+    if (ea && eb) HIP_TRY(hipEventRecord(ea, s));
+  }
+  hipError_t e = hipModuleLaunchKernel(c->fn[kid], grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, s, params,
+                                       nullptr);
+  if (e != hipSuccess) return fail(RTQ_ERR_HIP, "launch %s: %s", kKernelNames[kid], hipGetErrorString(e));
+  if (timed && ea && eb) {
+    HIP_TRY(hipEventRecord(eb, s));
+    c->pending.push_back({kid, ea, eb});
+  }
+  return RTQ_OK;
+}
+
+// ------------------------------------------------------------------ workspace
+struct Arena {
+  char* base;
+  size_t cap, off;
+  template <class T>
+  T* take(size_t count) {
+    off = roundup((int64_t)off, 256);
+    T* p = reinterpret_cast<T*>(base + off);
+    off += count * sizeof(T);
+    return p;
+  }
+};
+
+// grows the context workspace to at least `bytes` (synchronises the device before freeing)
+rtq_status ensure_ws(rtq_ctx* c, size_t bytes) {
+  if (bytes <= c->ws_bytes) return RTQ_OK;
+  size_t want = std::max<size_t>(bytes + bytes / 4, 1 << 20);
+  if (c->ws) {
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipFree(c->ws));
+    c->ws = nullptr;
+    c->ws_bytes = 0;
+  }
+  HIP_TRY(hipMalloc(&c->ws, want));
+  c->ws_bytes = want;
+  return RTQ_OK;
+}
+
+bool is_q32(int type) { return type == RTQ_TYPE_Q4_0 || type == RTQ_TYPE_Q8_0; }
+bool supported(int type) { return is_q32(type); }
+
+int64_t block_elems(int type) { return is_q32(type) ? 32 : 256; }
+int64_t block_bytes(int type) {
+  switch (type) {
+    case RTQ_TYPE_Q4_0: return 18;
+    case RTQ_TYPE_Q8_0: return 34;
+    case RTQ_TYPE_Q4_K: return 144;
+    case RTQ_TYPE_Q6_K: return 210;
+  }
+  return 0;
+}
+
+// ------------------------------------------------------------------ per-call sizes
+struct FwdPlan {
+  int64_t T, Tp;
+  size_t xa_bytes, xd_floats, h_floats;
+};
+
+FwdPlan fwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
+  FwdPlan p;
+  p.T = t;
+  p.Tp = roundup(std::max<int64_t>(t, 1), RTQ_T_PAD);
+  p.xa_bytes = (size_t)p.Tp * w->Kp * 2;  // one f16 per element
+  p.xd_floats = (size_t)(w->Kp / 32) * p.Tp;
+  p.h_floats = (size_t)t * std::max<int64_t>(r, 0);
+  return p;
+}
+
+size_t fwd_ws_bytes(const FwdPlan& p) { return p.xa_bytes + p.xd_floats * 4 + p.h_floats * 4 + 4 * 256; }
+
+struct BwdPlan {
+  int64_t T, Tp;
+  size_t dy16_bytes, h_floats, g_floats;
+};
+
+BwdPlan bwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
+  BwdPlan p;
+  p.T = t;
+  p.Tp = roundup(std::max<int64_t>(t, 1), RTQ_T_PAD);
+  p.dy16_bytes = (size_t)p.Tp * w->Np * 2;
+  p.h_floats = (size_t)t * std::max<int64_t>(r, 0);
+  p.g_floats = p.h_floats;
+  return p;
+}
+
+size_t bwd_ws_bytes(const BwdPlan& p) { return p.dy16_bytes + (size_t)p.Tp * 4 + 2 * p.h_floats * 4 + 4 * 256; }
+
+// ------------------------------------------------------------------ enqueue: forward
+// y = x.W^T (+bias) (+ s h.B^T);  isums (debug) receives the per-block integer sums.
+rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int64_t t, float* y, const float* bias,
+                           const float* la, const float* lb, int64_t r, float s, int32_t* isums, Arena& ar,
+                           hipStream_t st) {
+  if (t <= 0) return RTQ_OK;
+  const bool lora = la && lb && r > 0;
+  FwdPlan p = fwd_plan(w, t, lora ? r : 0);
+  void* xa = ar.take<char>(p.xa_bytes);
+  float* xd = ar.take<float>(p.xd_floats);
+  float* h = lora ? ar.take<float>(p.h_floats) : nullptr;
+  if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
+
+  QuantArgs qa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xa, xd, nullptr};
+  const int64_t qthreads = p.Tp * (w->Kp / 32);
+  RTQ_TRY(launch(c, K_QUANT_Q8_0, dim3((unsigned)cdiv(qthreads, 256)), dim3(256), st, qa));
+  if (lora) {
+    LoraDownArgs ld{x, la, (int)t, (int)w->cols, (int)r, h};
+    RTQ_TRY(launch(c, K_LORA_DOWN, dim3((unsigned)cdiv(t, 4)), dim3(256), st, ld));
+  }
+  FwdArgs fa{};
+  fa.wq = w->wq;
+  fa.wd = w->wd;
+  fa.wx = w->wx;
+  fa.Np = (int)w->Np;
+  fa.Kp = (int)w->Kp;
+  fa.xa = xa;
+  fa.xd = xd;
+  fa.xb = nullptr;
+  fa.Tp = (int)p.Tp;
+  fa.T = (int)t;
+  fa.N = (int)w->rows;
+  fa.K = (int)w->cols;
+  fa.y = y;
+  fa.bias = bias;
+  fa.h = h;
+  fa.lb = lb;
+  fa.r = (int)r;
+  fa.s = s;
+  fa.isums = isums;
+  int kid;
+  if (w->type == RTQ_TYPE_Q4_0)
+    kid = isums ? K_FWD_Q4_0_ISUMS : K_FWD_Q4_0;
+  else
+    kid = isums ? K_FWD_Q8_0_ISUMS : K_FWD_Q8_0;
+  return launch(c, kid, dim3((unsigned)(w->Np / 64), (unsigned)(p.Tp / 64)), dim3(256), st, fa);
+}
+
+// ------------------------------------------------------------------ enqueue: backward
+// dx (+)= dy.W (+ g.A);  with LoRA also ga += g^T x, gb += (s dy)^T h.
+rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, int64_t t, float* dx, bool zero_dx,
+                            const float* x, const float* la, const float* lb, int64_t r, float s, float* ga,
+                            float* gb, Arena& ar, hipStream_t st) {
+  if (t <= 0) return RTQ_OK;
+  const bool lora = la && lb && r > 0;
+  BwdPlan p = bwd_plan(w, t, lora ? r : 0);
+  void* dy16 = ar.take<char>(p.dy16_bytes);
+  float* einv = ar.take<float>((size_t)p.Tp);
+  float* h = lora ? ar.take<float>(p.h_floats) : nullptr;
+  float* g = lora ? ar.take<float>(p.g_floats) : nullptr;
+  if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
+  const int N = (int)w->rows, K = (int)w->cols;
+
+  DyPrepArgs da{dy, (int)t, N, (int)p.Tp, (int)w->Np, dy16, einv, zero_dx ? dx : nullptr, K, g, (int)r};
+  RTQ_TRY(launch(c, K_DY_PREP, dim3((unsigned)p.Tp), dim3(256), st, da));
+  if (lora) {
+    LoraDownArgs ld{x, la, (int)t, K, (int)r, h};
+    RTQ_TRY(launch(c, K_LORA_DOWN, dim3((unsigned)cdiv(t, 4)), dim3(256), st, ld));
+    const int nps = 256;
+    LoraGArgs lg{dy, lb, (int)t, N, (int)r, s, nps, g};
+    RTQ_TRY(launch(c, K_LORA_G, dim3((unsigned)cdiv(t, 16), (unsigned)cdiv(N, nps), (unsigned)cdiv(r, 16)), dim3(64),
+                   st, lg));
+  }
+  // dx: grid (K chunks, token tiles, row splits), about 4 workgroups per CU
+  const int64_t base = (w->Kp / 128) * (p.Tp / 64);
+  const int64_t steps = w->Np / 32;
+  const int64_t target = 4LL * c->cu_count;
+  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(steps, cdiv(target, base)));
+  splits = std::min<int64_t>(splits, 65535);
+  const int64_t nps = cdiv(steps, splits) * 32;
+  splits = cdiv(w->Np, nps);
+  DxArgs xa{};
+  xa.wq = w->wq;
+  xa.wd = w->wd;
+  xa.wx = w->wx;
+  xa.Np = (int)w->Np;
+  xa.Kp = (int)w->Kp;
+  xa.dy16 = dy16;
+  xa.einv = einv;
+  xa.Tp = (int)p.Tp;
+  xa.T = (int)t;
+  xa.K = K;
+  xa.n_per_split = (int)nps;
+  xa.dx = dx;
+  xa.g = g;
+  xa.la = la;
+  xa.r = (int)r;
+  const int kid = w->type == RTQ_TYPE_Q4_0 ? K_DX_Q4_0 : K_DX_Q8_0;
+  RTQ_TRY(launch(c, kid, dim3((unsigned)(w->Kp / 128), (unsigned)(p.Tp / 64), (unsigned)splits), dim3(256), st, xa));
+  if (lora) {
+    const int64_t jt = cdiv(r, 16);
+    const int64_t gb_tiles = cdiv(N, 16) * jt;
+    const int64_t ga_tiles = jt * cdiv(K, 16);
+    LoraGradArgs lga{dy, h, g, x, (int)t, N, K, (int)r, s, gb, ga, (int)gb_tiles};
+    RTQ_TRY(launch(c, K_LORA_GRADS, dim3((unsigned)(gb_tiles + ga_tiles)), dim3(64), st, lga));
+  }
+  return RTQ_OK;
+}
+
+rtq_status check_weight(rtq_ctx* c, const rtq_weight* w) {
+  if (!c) return fail(RTQ_ERR_INVALID, "null context");
+  if (!w) return fail(RTQ_ERR_INVALID, "null weight");
+  if (w->ctx != c) return fail(RTQ_ERR_INVALID, "weight belongs to another context");
+  return RTQ_OK;
+}
+
+rtq_status check_lora(const rtq_lora* l, bool* on, int64_t* r, float* s) {
+  *on = false;
+  *r = 0;
+  *s = 0.0f;
+  if (!l || !l->enabled || l->rank <= 0) return RTQ_OK;
+  if (!l->a || !l->b) return fail(RTQ_ERR_INVALID, "lora enabled with null a/b");
+  if (l->rank > 4096) return fail(RTQ_ERR_INVALID, "lora rank %lld too large", (long long)l->rank);
+  *on = true;
+  *r = l->rank;
+  *s = l->alpha / (float)l->rank;  // Lora::scale, src/linear.rs:26-28
+  return RTQ_OK;
+}
+
+rtq_status check_t(int64_t t) {
+  if (t < 0) return fail(RTQ_ERR_INVALID, "negative token count");
+  if (t > (1LL << 24)) return fail(RTQ_ERR_INVALID, "token count %lld too large", (long long)t);
+  return RTQ_OK;
+}
+
+// ------------------------------------------------------------------ weight repack (host)
+// GGUF blocks -> fragment layout (see rtq_kargs.h).  Padding rows/blocks get scale 0 and
+// zero-valued codes.
+void repack_q32(int type, const uint8_t* src, int64_t N, int64_t K, int64_t Np, int64_t Kp, uint8_t* wq,
+                uint16_t* wd) {
+  const int64_t Kc = Kp / 128, nb = K / 32, nbp = Kp / 32, bb = block_bytes(type), rb = nb * bb;
+  for (int64_t n = 0; n < Np; n++) {
+    const int64_t rg = n / 16, li = n % 16;
+    for (int64_t b = 0; b < nbp; b++) {
+      const int64_t kc = b / 4, j = b % 4;
+      uint16_t d = 0;
+      uint8_t codes[32];
+      const bool real = n < N && b < nb;
+      if (type == RTQ_TYPE_Q4_0) {
+        if (real) {
+          const uint8_t* blk = src + n * rb + b * bb;
+          d = (uint16_t)(blk[0] | (blk[1] << 8));
+          memcpy(codes, blk + 2, 16);
+        } else {
+          memset(codes, 0x88, 16);
+        }
+        for (int g = 0; g < 4; g++)
+          memcpy(wq + ((rg * Kc + kc) * 64 + li + 16 * g) * 16 + j * 4, codes + 4 * g, 4);
+      } else {
+        if (real) {
+          const uint8_t* blk = src + n * rb + b * bb;
+          d = (uint16_t)(blk[0] | (blk[1] << 8));
+          memcpy(codes, blk + 2, 32);
+        } else {
+          memset(codes, 0, 32);
+        }
+        const int64_t part = j / 2, off = (j % 2) * 8;
+        for (int g = 0; g < 4; g++) {
+          uint8_t* dst = wq + (((rg * Kc + kc) * 2 + part) * 64 + li + 16 * g) * 16 + off;
+          memcpy(dst, codes + 4 * g, 4);
+          memcpy(dst + 4, codes + 16 + 4 * g, 4);
+        }
+      }
+      wd[((rg * Kc + kc) * 16 + li) * 4 + j] = d;
+    }
+  }
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+extern "C" {
+
+const char* rtq_version(void) { return "rtq 0.1 gfx950"; }
+const char* rtq_last_error(void) { return g_err.c_str(); }
+
+rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
+  if (!out) return fail(RTQ_ERR_INVALID, "null out");
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(RTQ_ERR_NO_DEVICE, "no HIP device visible");
+  if (device < 0 || device >= n) return fail(RTQ_ERR_INVALID, "device %d out of range (%d devices)", device, n);
+  HIP_TRY(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, device));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(RTQ_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
+  rtq_ctx* c = new rtq_ctx();
+  c->device = device;
+  c->cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+  hipError_t e = hipModuleLoadData(&c->mod, rtq_hsaco_begin);
+  if (e != hipSuccess) {
+    delete c;
+    return fail(RTQ_ERR_NO_DEVICE, "hipModuleLoadData: %s", hipGetErrorString(e));
+  }
+  for (int k = 0; k < K_COUNT; k++) {
+    e = hipModuleGetFunction(&c->fn[k], c->mod, kKernelNames[k]);
+    if (e != hipSuccess) {
+      (void)hipModuleUnload(c->mod);
+      delete c;
+      return fail(RTQ_ERR_NO_DEVICE, "kernel %s missing from code object: %s", kKernelNames[k], hipGetErrorString(e));
+    }
+  }
+  e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    (void)hipModuleUnload(c->mod);
+    delete c;
+    return fail(RTQ_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
+  }
+  *out = c;
+  return RTQ_OK;
+}
+
+void rtq_ctx_destroy(rtq_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  (void)hipDeviceSynchronize();
+  for (auto& p : c->pending) {
+    (void)hipEventDestroy(p.a);
+    (void)hipEventDestroy(p.b);
+  }
+  for (auto e : c->free_events) (void)hipEventDestroy(e);
+  if (c->ws) (void)hipFree(c->ws);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  if (c->mod) (void)hipModuleUnload(c->mod);
+  delete c;
+}
+
+void* rtq_ctx_stream(rtq_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+rtq_status rtq_ctx_reserve(rtq_ctx* c, int64_t max_t, int64_t max_rows, int64_t max_cols, int64_t max_rank) {
+  if (!c) return fail(RTQ_ERR_INVALID, "null context");
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  rtq_weight fake;
+  fake.rows = max_rows;
+  fake.cols = max_cols;
+  fake.Np = roundup(max_rows, RTQ_ROW_PAD);
+  fake.Kp = roundup(max_cols, RTQ_CHUNK_K);
+  size_t need = std::max(fwd_ws_bytes(fwd_plan(&fake, max_t, max_rank)), bwd_ws_bytes(bwd_plan(&fake, max_t, max_rank)));
+  return ensure_ws(c, need);
+}
+
+rtq_status rtq_ctx_set_timing(rtq_ctx* c, int enable, const char* only_kernel) {
+  if (!c) return fail(RTQ_ERR_INVALID, "null context");
+  std::lock_guard<std::mutex> lk(c->mu);
+  int only = -1;
+  if (only_kernel) {
+    for (int k = 0; k < K_COUNT; k++)
+      if (strcmp(only_kernel, kKernelNames[k]) == 0) only = k;
+    if (only < 0) return fail(RTQ_ERR_INVALID, "unknown kernel %s", only_kernel);
+  }
+  c->timing = enable != 0;
+  c->timing_only = only;
+  return RTQ_OK;
+}
+
+static void fold_timing(rtq_ctx* c) {
+  if (c->pending.empty()) return;
+  (void)hipSetDevice(c->device);
+  (void)hipDeviceSynchronize();
+  for (auto& p : c->pending) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+      c->t_launches[p.kid] += 1;
+      c->t_ms[p.kid] += ms;
+    }
+    c->free_events.push_back(p.a);
+    c->free_events.push_back(p.b);
+  }
+  c->pending.clear();
+}
+
+int rtq_ctx_timing_count(rtq_ctx* c) {
+  if (!c) return 0;
+  std::lock_guard<std::mutex> lk(c->mu);
+  fold_timing(c);
+  return K_COUNT;
+}
+
+rtq_status rtq_ctx_timing_get(rtq_ctx* c, int i, const char** name, int64_t* launches, double* total_ms) {
+  if (!c || i < 0 || i >= K_COUNT) return fail(RTQ_ERR_INVALID, "bad timing index");
+  std::lock_guard<std::mutex> lk(c->mu);
+  fold_timing(c);
+  if (name) *name = kKernelNames[i];
+  if (launches) *launches = c->t_launches[i];
+  if (total_ms) *total_ms = c->t_ms[i];
+  return RTQ_OK;
+}
+
+void rtq_ctx_timing_reset(rtq_ctx* c) {
+  if (!c) return;
+  std::lock_guard<std::mutex> lk(c->mu);
+  fold_timing(c);
+  for (int k = 0; k < K_COUNT; k++) {
+    c->t_launches[k] = 0;
+    c->t_ms[k] = 0.0;
+  }
+}
+
+rtq_status rtq_weight_create(rtq_ctx* c, int type, const void* blocks, size_t nbytes, int64_t rows, int64_t cols,
+                             rtq_weight** out) {
+  if (!c || !out) return fail(RTQ_ERR_INVALID, "null context/out");
+  *out = nullptr;
+  if (type != RTQ_TYPE_Q4_0 && type != RTQ_TYPE_Q8_0 && type != RTQ_TYPE_Q4_K && type != RTQ_TYPE_Q6_K)
+    return fail(RTQ_ERR_UNSUPPORTED, "ggml type %d is not supported", type);
+  if (!supported(type)) return fail(RTQ_ERR_UNSUPPORTED, "ggml type %d is not implemented yet", type);
+  if (rows <= 0 || cols <= 0) return fail(RTQ_ERR_INVALID, "empty weight %lldx%lld", (long long)rows, (long long)cols);
+  if (cols % block_elems(type))
+    return fail(RTQ_ERR_INVALID, "cols %lld not a multiple of the block size %lld", (long long)cols,
+                (long long)block_elems(type));
+  if (rows > (1LL << 30) || cols > (1LL << 24)) return fail(RTQ_ERR_INVALID, "weight too large");
+  const size_t expect = (size_t)rows * (size_t)(cols / block_elems(type) * block_bytes(type));
+  if (!blocks || nbytes != expect)
+    return fail(RTQ_ERR_INVALID, "weight bytes %zu != rows*row_bytes %zu", nbytes, expect);
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  rtq_weight* w = new rtq_weight();
+  w->ctx = c;
+  w->type = type;
+  w->rows = rows;
+  w->cols = cols;
+  w->Np = roundup(rows, RTQ_ROW_PAD);
+  w->Kp = roundup(cols, is_q32(type) ? RTQ_CHUNK_Q : RTQ_CHUNK_K);
+  w->gguf_bytes = expect;
+  const int64_t nbp = w->Kp / 32;
+  const size_t q_bytes = (size_t)w->Np * nbp * (type == RTQ_TYPE_Q4_0 ? 16 : 32);
+  const size_t d_bytes = (size_t)w->Np * nbp * 2;
+  const size_t q_off = 0, d_off = roundup((int64_t)q_bytes, 256);
+  const size_t total = d_off + roundup((int64_t)d_bytes, 256);
+  std::vector<uint8_t> host(total, 0);
+  repack_q32(type, (const uint8_t*)blocks, rows, cols, w->Np, w->Kp, host.data() + q_off,
+             reinterpret_cast<uint16_t*>(host.data() + d_off));
+  hipError_t e = hipMalloc(&w->dmem, total);
+  if (e != hipSuccess) {
+    delete w;
+    return fail(RTQ_ERR_HIP, "hipMalloc(%zu): %s", total, hipGetErrorString(e));
+  }
+  e = hipMemcpy(w->dmem, host.data(), total, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(w->dmem);
+    delete w;
+    return fail(RTQ_ERR_HIP, "upload: %s", hipGetErrorString(e));
+  }
+  w->wq = (char*)w->dmem + q_off;
+  w->wd = reinterpret_cast<uint16_t*>((char*)w->dmem + d_off);
+  *out = w;
+  return RTQ_OK;
+}
+
+void rtq_weight_destroy(rtq_weight* w) {
+  if (!w) return;
+  if (w->dmem) {
+    std::lock_guard<std::mutex> lk(w->ctx->mu);
+    (void)hipSetDevice(w->ctx->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(w->dmem);
+  }
+  delete w;
+}
+
+int64_t rtq_weight_out_dim(const rtq_weight* w) { return w ? w->rows : 0; }
+int64_t rtq_weight_in_dim(const rtq_weight* w) { return w ? w->cols : 0; }
+size_t rtq_weight_nbytes(const rtq_weight* w) { return w ? w->gguf_bytes : 0; }
+int rtq_weight_type(const rtq_weight* w) { return w ? w->type : -1; }
+
+// ------------------------------------------------------------------ device-pointer API
+rtq_status rtq_frozen_forward_d(rtq_ctx* c, const rtq_weight* w, const float* x, int64_t t, float* y, void* stream) {
+  return rtq_linear_forward_d(c, w, nullptr, nullptr, x, t, y, stream);
+}
+
+rtq_status rtq_linear_forward_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
+                                const float* x, int64_t t, float* y, void* stream) {
+  RTQ_TRY(check_weight(c, w));
+  RTQ_TRY(check_t(t));
+  bool on;
+  int64_t r;
+  float s;
+  RTQ_TRY(check_lora(lora, &on, &r, &s));
+  if (t > 0 && (!x || !y)) return fail(RTQ_ERR_INVALID, "null x/y");
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+  FwdPlan p = fwd_plan(w, t, on ? r : 0);
+  RTQ_TRY(ensure_ws(c, fwd_ws_bytes(p)));
+  Arena ar{(char*)c->ws, c->ws_bytes, 0};
+  return enqueue_forward(c, w, x, t, y, bias, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, nullptr, ar, st);
+}
+
+rtq_status rtq_frozen_backward_input_d(rtq_ctx* c, const rtq_weight* w, const float* dy, int64_t t, float* dx,
+                                       void* stream) {
+  RTQ_TRY(check_weight(c, w));
+  RTQ_TRY(check_t(t));
+  if (t > 0 && (!dy || !dx)) return fail(RTQ_ERR_INVALID, "null dy/dx");
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+  BwdPlan p = bwd_plan(w, t, 0);
+  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(p)));
+  Arena ar{(char*)c->ws, c->ws_bytes, 0};
+  return enqueue_backward(c, w, dy, t, dx, false, nullptr, nullptr, nullptr, 0, 0.0f, nullptr, nullptr, ar, st);
+}
+
+rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const float* x,
+                                 const float* dy, int64_t t, float* dx, float* ga, float* gb, void* stream) {
+  RTQ_TRY(check_weight(c, w));
+  RTQ_TRY(check_t(t));
+  bool on;
+  int64_t r;
+  float s;
+  RTQ_TRY(check_lora(lora, &on, &r, &s));
+  if (t > 0 && (!dy || !dx)) return fail(RTQ_ERR_INVALID, "null dy/dx");
+  if (on && t > 0 && (!x || !ga || !gb)) return fail(RTQ_ERR_INVALID, "lora backward needs x, ga and gb");
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+  BwdPlan p = bwd_plan(w, t, on ? r : 0);
+  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(p)));
+  Arena ar{(char*)c->ws, c->ws_bytes, 0};
+  return enqueue_backward(c, w, dy, t, dx, true, x, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, ga, gb,
+                          ar, st);
+}
+
+static rtq_status enqueue_rows(rtq_ctx* c, const rtq_weight* w, int64_t r0, int64_t count, float* out,
+                               hipStream_t st) {
+  RowArgs ra{w->wq, w->wd, w->wx, (int)w->Np, (int)w->Kp, (int)w->cols, (int)r0, (int)count, out};
+  const int64_t threads = count * (w->cols / 32);
+  return launch(c, w->type == RTQ_TYPE_Q4_0 ? K_ROWS_Q4_0 : K_ROWS_Q8_0, dim3((unsigned)cdiv(threads, 256)), dim3(256),
+                st, ra);
+}
+
+rtq_status rtq_frozen_rows_d(rtq_ctx* c, const rtq_weight* w, int64_t r0, int64_t count, float* out, void* stream) {
+  RTQ_TRY(check_weight(c, w));
+  if (r0 < 0 || count < 0 || r0 + count > w->rows) return fail(RTQ_ERR_INVALID, "rows out of range");
+  if (count == 0) return RTQ_OK;
+  if (!out) return fail(RTQ_ERR_INVALID, "null out");
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  return enqueue_rows(c, w, r0, count, out, stream ? (hipStream_t)stream : c->stream);
+}
+
+// ------------------------------------------------------------------ host-pointer API
+namespace {
+
+struct HostCall {
+  rtq_ctx* c;
+  std::unique_lock<std::mutex> lk;
+  explicit HostCall(rtq_ctx* ctx) : c(ctx), lk(ctx->mu) {}
+};
+
+static rtq_status h2d(void* d, const void* h, size_t bytes, hipStream_t st) {
+  if (bytes) HIP_TRY(hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, st));
+  return RTQ_OK;
+}
+static rtq_status d2h(void* h, const void* d, size_t bytes, hipStream_t st) {
+  if (bytes) HIP_TRY(hipMemcpyAsync(h, d, bytes, hipMemcpyDeviceToHost, st));
+  return RTQ_OK;
+}
+
+}  // namespace
+
+rtq_status rtq_linear_forward(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora, const float* x,
+                              int64_t t, float* y) {
+  RTQ_TRY(check_weight(c, w));
+  RTQ_TRY(check_t(t));
+  bool on;
+  int64_t r;
+  float s;
+  RTQ_TRY(check_lora(lora, &on, &r, &s));
+  if (t == 0) return RTQ_OK;
+  if (!x || !y) return fail(RTQ_ERR_INVALID, "null x/y");
+  HostCall hc(c);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = c->stream;
+  const int64_t N = w->rows, K = w->cols;
+  FwdPlan p = fwd_plan(w, t, on ? r : 0);
+  const size_t io = (size_t)(t * K + t * N + (bias ? N : 0) + (on ? r * K + N * r : 0)) * 4 + 6 * 256;
+  RTQ_TRY(ensure_ws(c, fwd_ws_bytes(p) + io));
+  Arena ar{(char*)c->ws, c->ws_bytes, 0};
+  float* xd = ar.take<float>((size_t)(t * K));
+  float* yd = ar.take<float>((size_t)(t * N));
+  float* bd = bias ? ar.take<float>((size_t)N) : nullptr;
+  float* ad = on ? ar.take<float>((size_t)(r * K)) : nullptr;
+  float* bld = on ? ar.take<float>((size_t)(N * r)) : nullptr;
+  RTQ_TRY(h2d(xd, x, (size_t)(t * K) * 4, st));
+  if (bd) RTQ_TRY(h2d(bd, bias, (size_t)N * 4, st));
+  if (on) {
+    RTQ_TRY(h2d(ad, lora->a, (size_t)(r * K) * 4, st));
+    RTQ_TRY(h2d(bld, lora->b, (size_t)(N * r) * 4, st));
+  }
+  RTQ_TRY(enqueue_forward(c, w, xd, t, yd, bd, ad, bld, on ? r : 0, s, nullptr, ar, st));
+  RTQ_TRY(d2h(y, yd, (size_t)(t * N) * 4, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return RTQ_OK;
+}
+
+rtq_status rtq_frozen_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int64_t t, float* y) {
+  return rtq_linear_forward(c, w, nullptr, nullptr, x, t, y);
+}
+
+static rtq_status backward_host(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const float* x, const float* dy,
+                                int64_t t, float* dx, float* ga, float* gb, bool linear) {
+  RTQ_TRY(check_weight(c, w));
+  RTQ_TRY(check_t(t));
+  bool on;
+  int64_t r;
+  float s;
+  RTQ_TRY(check_lora(linear ? lora : nullptr, &on, &r, &s));
+  if (t == 0) return RTQ_OK;
+  if (!dy || !dx) return fail(RTQ_ERR_INVALID, "null dy/dx");
+  if (on && (!x || !ga || !gb)) return fail(RTQ_ERR_INVALID, "lora backward needs x, ga and gb");
+  HostCall hc(c);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = c->stream;
+  const int64_t N = w->rows, K = w->cols;
+  BwdPlan p = bwd_plan(w, t, on ? r : 0);
+  const size_t io = (size_t)(t * N + t * K + (on ? t * K + 2 * r * K + 2 * N * r : 0)) * 4 + 8 * 256;
+  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(p) + io));
+  Arena ar{(char*)c->ws, c->ws_bytes, 0};
+  float* dyd = ar.take<float>((size_t)(t * N));
+  float* dxd = ar.take<float>((size_t)(t * K));
+  float *xd = nullptr, *ad = nullptr, *bld = nullptr, *gad = nullptr, *gbd = nullptr;
+  if (on) {
+    xd = ar.take<float>((size_t)(t * K));
+    ad = ar.take<float>((size_t)(r * K));
+    bld = ar.take<float>((size_t)(N * r));
+    gad = ar.take<float>((size_t)(r * K));
+    gbd = ar.take<float>((size_t)(N * r));
+  }
+  RTQ_TRY(h2d(dyd, dy, (size_t)(t * N) * 4, st));
+  if (!linear) RTQ_TRY(h2d(dxd, dx, (size_t)(t * K) * 4, st));  // FrozenMatmul accumulates into dx
+  if (on) {
+    RTQ_TRY(h2d(xd, x, (size_t)(t * K) * 4, st));
+    RTQ_TRY(h2d(ad, lora->a, (size_t)(r * K) * 4, st));
+    RTQ_TRY(h2d(bld, lora->b, (size_t)(N * r) * 4, st));
+    RTQ_TRY(h2d(gad, ga, (size_t)(r * K) * 4, st));
+    RTQ_TRY(h2d(gbd, gb, (size_t)(N * r) * 4, st));
+  }
+  RTQ_TRY(enqueue_backward(c, w, dyd, t, dxd, linear, xd, ad, bld, on ? r : 0, s, gad, gbd, ar, st));
+  RTQ_TRY(d2h(dx, dxd, (size_t)(t * K) * 4, st));
+  if (on) {
+    RTQ_TRY(d2h(ga, gad, (size_t)(r * K) * 4, st));
+    RTQ_TRY(d2h(gb, gbd, (size_t)(N * r) * 4, st));
+  }
+  HIP_TRY(hipStreamSynchronize(st));
+  return RTQ_OK;
+}
+
+rtq_status rtq_frozen_backward_input(rtq_ctx* c, const rtq_weight* w, const float* dy, int64_t t, float* dx) {
+  return backward_host(c, w, nullptr, nullptr, dy, t, dx, nullptr, nullptr, false);
+}
+
+rtq_status rtq_linear_backward(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const float* x, const float* dy,
+                               int64_t t, float* dx, float* ga, float* gb) {
+  return backward_host(c, w, lora, x, dy, t, dx, ga, gb, true);
+}
+
+rtq_status rtq_frozen_row(rtq_ctx* c, const rtq_weight* w, int64_t r, float* out) {
+  RTQ_TRY(check_weight(c, w));
+  if (r < 0 || r >= w->rows) return fail(RTQ_ERR_INVALID, "row %lld out of range", (long long)r);
+  if (!out) return fail(RTQ_ERR_INVALID, "null out");
+  HostCall hc(c);
+  HIP_TRY(hipSetDevice(c->device));
+  RTQ_TRY(ensure_ws(c, (size_t)w->cols * 4 + 256));
+  float* od = (float*)c->ws;
+  RTQ_TRY(enqueue_rows(c, w, r, 1, od, c->stream));
+  RTQ_TRY(d2h(out, od, (size_t)w->cols * 4, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return RTQ_OK;
+}
+
+// ------------------------------------------------------------------ parity / debug
+int64_t rtq_debug_isums_per_row(const rtq_weight* w) {
+  if (!w) return 0;
+  if (is_q32(w->type)) return w->cols / 32;
+  if (w->type == RTQ_TYPE_Q4_K) return 2 * (w->cols / 256);
+  return w->cols / 256;
+}
+
+rtq_status rtq_debug_quantize_acts(rtq_ctx* c, const rtq_weight* w, const float* x, int64_t t, void* out) {
+  RTQ_TRY(check_weight(c, w));
+  RTQ_TRY(check_t(t));
+  if (t == 0) return RTQ_OK;
+  if (!x || !out) return fail(RTQ_ERR_INVALID, "null x/out");
+  HostCall hc(c);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = c->stream;
+  const int64_t K = w->cols;
+  FwdPlan p = fwd_plan(w, t, 0);
+  RTQ_TRY(ensure_ws(c, fwd_ws_bytes(p) + (size_t)(t * K) * 4 + 256));
+  Arena ar{(char*)c->ws, c->ws_bytes, 0};
+  float* xdv = ar.take<float>((size_t)(t * K));
+  void* xa = ar.take<char>(p.xa_bytes);
+  float* xs = ar.take<float>(p.xd_floats);
+  RTQ_TRY(h2d(xdv, x, (size_t)(t * K) * 4, st));
+  QuantArgs qa{xdv, (int)t, (int)K, (int)p.Tp, (int)w->Kp, xa, xs, nullptr};
+  RTQ_TRY(launch(c, K_QUANT_Q8_0, dim3((unsigned)cdiv(p.Tp * (w->Kp / 32), 256)), dim3(256), st, qa));
+  std::vector<uint16_t> ha(p.xa_bytes / 2);
+  std::vector<float> hs(p.xd_floats);
+  RTQ_TRY(d2h(ha.data(), xa, p.xa_bytes, st));
+  RTQ_TRY(d2h(hs.data(), xs, p.xd_floats * 4, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  // re-pack into ggml block_q8_0 (fp16 d, 32 x int8)
+  const int64_t nb = K / 32, Kc = w->Kp / 128;
+  uint8_t* o = (uint8_t*)out;
+  for (int64_t ti = 0; ti < t; ti++)
+    for (int64_t b = 0; b < nb; b++) {
+      uint8_t* blk = o + (ti * nb + b) * 34;
+      const uint16_t d = f32_to_f16_bits(hs[(size_t)b * p.Tp + ti]);
+      blk[0] = (uint8_t)(d & 0xff);
+      blk[1] = (uint8_t)(d >> 8);
+      const int64_t kc = b / 4, j = b % 4, tg = ti / 16;
+      for (int g = 0; g < 4; g++) {
+        const uint16_t* f = &ha[(((tg * Kc + kc) * 4 + j) * 64 + (ti % 16) + 16 * g) * 8];
+        for (int s = 0; s < 8; s++) {
+          const int q = (int)f16_bits_to_f32(f[s]);
+          const int e = s < 4 ? 4 * g + s : 16 + 4 * g + (s - 4);
+          blk[2 + e] = (uint8_t)(int8_t)q;
+        }
+      }
+    }
+  return RTQ_OK;
+}
+
+rtq_status rtq_debug_block_isums(rtq_ctx* c, const rtq_weight* w, const float* x, int64_t t, int32_t* out) {
+  RTQ_TRY(check_weight(c, w));
+  RTQ_TRY(check_t(t));
+  if (t == 0) return RTQ_OK;
+  if (!x || !out) return fail(RTQ_ERR_INVALID, "null x/out");
+  HostCall hc(c);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = c->stream;
+  const int64_t N = w->rows, K = w->cols, m = rtq_debug_isums_per_row(w);
+  FwdPlan p = fwd_plan(w, t, 0);
+  const size_t isz = (size_t)(t * N * m) * 4;
+  RTQ_TRY(ensure_ws(c, fwd_ws_bytes(p) + (size_t)(t * K + t * N) * 4 + isz + 4 * 256));
+  Arena ar{(char*)c->ws, c->ws_bytes, 0};
+  float* xdv = ar.take<float>((size_t)(t * K));
+  float* yd = ar.take<float>((size_t)(t * N));
+  int32_t* id = ar.take<int32_t>((size_t)(t * N * m));
+  RTQ_TRY(h2d(xdv, x, (size_t)(t * K) * 4, st));
+  RTQ_TRY(enqueue_forward(c, w, xdv, t, yd, nullptr, nullptr, nullptr, 0, 0.0f, id, ar, st));
+  RTQ_TRY(d2h(out, id, isz, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return RTQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,224 @@
+"""Frozen quantised weights on the GPU — the ``FrozenMatmul`` plugin point.
+
+Mirrors the reference's contract (``src/frozen.rs:13-27``) and its GGUF implementation
+``RieFrozen`` (``src/rie.rs:50-129``): the frozen weight provides only the forward product
+``y = x . W^T`` (fresh output) and the input gradient ``dx += dy . W`` (accumulated), plus
+``row`` (dequantise one row) and ``nbytes``.  Arrays are row-major float32; like ``&[f32]`` /
+``Vec<f32>`` in the reference, inputs may be flat or 2-D and outputs are flat.
+
+``HipFrozen`` keeps the packed GGUF blocks on the device (uploaded once) and runs the gfx950
+kernels of librtq.so.  Shape errors raise ``AssertionError`` where the reference asserts;
+device failures raise ``RtqError``.
+"""
+from __future__ import annotations
+
+import abc
+import ctypes
+import weakref
+
+import numpy as np
+
+from . import _ffi
+
+
+class Context:
+    """One device, one stream, the loaded gfx950 code object (``rtq_ctx``).
+
+    Replaces the engine ThreadPool the reference threads through ``RieFrozen``
+    (``src/rie.rs:53,182``).
+    """
+
+    def __init__(self, device: int = 0):
+        L = _ffi.lib()
+        h = ctypes.c_void_p()
+        _ffi.check(L.rtq_ctx_create(device, ctypes.byref(h)), "rtq_ctx_create")
+        self._h = h
+        self.device = device
+        self._weights: weakref.WeakSet = weakref.WeakSet()
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        if self._h is None:
+            raise RuntimeError("context destroyed")
+        return self._h
+
+    @property
+    def stream(self) -> int:
+        return int(_ffi.lib().rtq_ctx_stream(self.handle) or 0)
+
+    def reserve(self, max_t: int, max_rows: int, max_cols: int, max_rank: int = 0) -> None:
+        _ffi.check(_ffi.lib().rtq_ctx_reserve(self.handle, max_t, max_rows, max_cols, max_rank), "rtq_ctx_reserve")
+
+    def set_timing(self, on: bool, only_kernel: str | None = None) -> None:
+        """HIP events around kernel launches (all kernels, or only ``only_kernel``)."""
+        _ffi.check(_ffi.lib().rtq_ctx_set_timing(self.handle, int(on), only_kernel.encode() if only_kernel else None),
+                   "rtq_ctx_set_timing")
+
+    def timing(self) -> dict[str, tuple[int, float]]:
+        """{kernel name: (launches, total ms)} for kernels launched since the last reset."""
+        L = _ffi.lib()
+        n = L.rtq_ctx_timing_count(self.handle)
+        out = {}
+        for i in range(n):
+            name = ctypes.c_char_p()
+            cnt = ctypes.c_int64()
+            ms = ctypes.c_double()
+            _ffi.check(L.rtq_ctx_timing_get(self.handle, i, ctypes.byref(name), ctypes.byref(cnt), ctypes.byref(ms)),
+                       "rtq_ctx_timing_get")
+            if cnt.value:
+                out[name.value.decode()] = (cnt.value, ms.value)
+        return out
+
+    def reset_timing(self) -> None:
+        _ffi.lib().rtq_ctx_timing_reset(self.handle)
+
+    def close(self) -> None:
+        """Destroys the weights still alive on this context, then the context itself."""
+        if self._h is not None:
+            for w in list(self._weights):
+                w.close()
+            _ffi.lib().rtq_ctx_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+_DEFAULT_CTX: Context | None = None
+
+
+def default_context() -> Context:
+    global _DEFAULT_CTX
+    if _DEFAULT_CTX is None:
+        _DEFAULT_CTX = Context(0)
+    return _DEFAULT_CTX
+
+
+def _f32(a, n: int, what: str) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    assert a.size == n, f"{what}: expected {n} elements, got {a.size}"
+    return a
+
+
+class FrozenMatmul(abc.ABC):
+    """A frozen ``[out x in]`` weight matrix (``trait FrozenMatmul``, src/frozen.rs:14-25)."""
+
+    @abc.abstractmethod
+    def out_dim(self) -> int: ...
+
+    @abc.abstractmethod
+    def in_dim(self) -> int: ...
+
+    @abc.abstractmethod
+    def forward(self, x, t: int) -> np.ndarray:
+        """``y[t x out] = x[t x in] . W^T``"""
+
+    @abc.abstractmethod
+    def backward_input(self, dy, t: int, dx: np.ndarray) -> None:
+        """``dx[t x in] += dy[t x out] . W`` (gradient to the input only; W is frozen)."""
+
+    @abc.abstractmethod
+    def row(self, r: int, out: np.ndarray) -> None:
+        """Dequantise one row into ``out``."""
+
+    @abc.abstractmethod
+    def nbytes(self) -> int: ...
+
+
+class HipFrozen(FrozenMatmul):
+    """GGUF-block weight on an MI355X (``RieFrozen::new``, src/rie.rs:58-60).
+
+    ``blocks`` are the weight's packed GGUF bytes (``Weight::data()``), ``rows`` = out,
+    ``cols`` = in.  Supported types: Q4_0 (2), Q8_0 (8).
+    """
+
+    def __init__(self, ggml_type: int, blocks, rows: int, cols: int, ctx: Context | None = None):
+        self.ctx = ctx or default_context()
+        b = np.ascontiguousarray(blocks, dtype=np.uint8)
+        h = ctypes.c_void_p()
+        _ffi.check(_ffi.lib().rtq_weight_create(self.ctx.handle, ggml_type, b.ctypes.data, b.nbytes, rows, cols,
+                                                ctypes.byref(h)), "rtq_weight_create")
+        self._h = h
+        self.ggml_type = ggml_type
+        self._rows, self._cols = rows, cols
+        self.ctx._weights.add(self)
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    def out_dim(self) -> int:
+        return self._rows
+
+    def in_dim(self) -> int:
+        return self._cols
+
+    def nbytes(self) -> int:
+        return int(_ffi.lib().rtq_weight_nbytes(self._h))
+
+    def forward(self, x, t: int) -> np.ndarray:
+        x = _f32(x, t * self._cols, "forward input")
+        y = np.empty(t * self._rows, dtype=np.float32)
+        _ffi.check(_ffi.lib().rtq_frozen_forward(self.ctx.handle, self._h, x.ctypes.data, t, y.ctypes.data),
+                   "rtq_frozen_forward")
+        return y
+
+    def backward_input(self, dy, t: int, dx: np.ndarray) -> None:
+        dy = _f32(dy, t * self._rows, "backward dy")
+        assert isinstance(dx, np.ndarray) and dx.dtype == np.float32 and dx.flags["C_CONTIGUOUS"], \
+            "dx must be a C-contiguous float32 array (accumulated in place)"
+        assert dx.size == t * self._cols, f"dx: expected {t * self._cols} elements, got {dx.size}"
+        _ffi.check(_ffi.lib().rtq_frozen_backward_input(self.ctx.handle, self._h, dy.ctypes.data, t, dx.ctypes.data),
+                   "rtq_frozen_backward_input")
+
+    def row(self, r: int, out: np.ndarray) -> None:
+        assert isinstance(out, np.ndarray) and out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
+        assert out.size == self._cols
+        _ffi.check(_ffi.lib().rtq_frozen_row(self.ctx.handle, self._h, r, out.ctypes.data), "rtq_frozen_row")
+
+    # ---- device-pointer variants (ints are device addresses; stream 0 = context stream)
+    def forward_d(self, x_ptr: int, t: int, y_ptr: int, stream: int = 0) -> None:
+        _ffi.check(_ffi.lib().rtq_frozen_forward_d(self.ctx.handle, self._h, x_ptr, t, y_ptr, stream or None),
+                   "rtq_frozen_forward_d")
+
+    def backward_input_d(self, dy_ptr: int, t: int, dx_ptr: int, stream: int = 0) -> None:
+        _ffi.check(_ffi.lib().rtq_frozen_backward_input_d(self.ctx.handle, self._h, dy_ptr, t, dx_ptr,
+                                                          stream or None), "rtq_frozen_backward_input_d")
+
+    def rows_d(self, r0: int, count: int, out_ptr: int, stream: int = 0) -> None:
+        _ffi.check(_ffi.lib().rtq_frozen_rows_d(self.ctx.handle, self._h, r0, count, out_ptr, stream or None),
+                   "rtq_frozen_rows_d")
+
+    # ---- parity hooks
+    def debug_quantize_acts(self, x, t: int) -> np.ndarray:
+        """The activation blocks (ggml layout) the GPU forward uses for ``x``."""
+        x = _f32(x, t * self._cols, "acts")
+        per = {2: 34 * (self._cols // 32), 8: 34 * (self._cols // 32)}.get(self.ggml_type,
+                                                                            292 * (self._cols // 256))
+        out = np.empty((t, per), dtype=np.uint8)
+        _ffi.check(_ffi.lib().rtq_debug_quantize_acts(self.ctx.handle, self._h, x.ctypes.data, t, out.ctypes.data),
+                   "rtq_debug_quantize_acts")
+        return out
+
+    def debug_block_isums(self, x, t: int) -> np.ndarray:
+        """Integer block sums computed by the GPU forward kernel: int32 [t, out, isums_per_row]."""
+        x = _f32(x, t * self._cols, "acts")
+        m = int(_ffi.lib().rtq_debug_isums_per_row(self._h))
+        out = np.empty((t, self._rows, m), dtype=np.int32)
+        _ffi.check(_ffi.lib().rtq_debug_block_isums(self.ctx.handle, self._h, x.ctypes.data, t, out.ctypes.data),
+                   "rtq_debug_block_isums")
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None:
+            _ffi.lib().rtq_weight_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

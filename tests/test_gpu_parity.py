@@ -1,0 +1,228 @@
+"""GPU parity: the gfx950 path through the C ABI against the CPU oracle on identical seeded inputs.
+
+Bars (from the hot-path contract):
+  * activation quantisation (Q8_0 blocks) and the integer block sums: bit-exact;
+  * row() dequantisation: bit-exact;
+  * f32 outputs and gradients: max |gpu - oracle| / max |oracle| <= 1e-3 per tensor (TOL);
+    the reference's own per-element check 1e-3 * max(|want|, 1) (tests/engine.rs:115) is also
+    applied to dx against the dense dequantised product.
+Inputs follow the benchmark recipe: W ~ N(0, 0.02) seed 1, X ~ N(0, 1) seed 2, dy ~ N(0, 1)
+seed 3, A ~ N(0, 1/1024) (std 1/32) seed 4, B ~ N(0, 0.01) seed 5, all from the reference Rng.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import rust_trainer_amd as rt
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+FORMATS = [O.Q4_0, O.Q8_0]
+
+
+def rel_err(got, want):
+    got = np.asarray(got, np.float64).reshape(-1)
+    want = np.asarray(want, np.float64).reshape(-1)
+    assert got.shape == want.shape
+    return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+def make(wtype, n, k, t, seed=1):
+    w = O.Rng(seed).vec_normal(n * k, 0.02).reshape(n, k)
+    blocks = O.quantize(wtype, w)
+    x = O.Rng(seed + 1).vec_normal(t * k, 1.0).reshape(t, k)
+    dy = O.Rng(seed + 2).vec_normal(t * n, 1.0).reshape(t, n)
+    return blocks, x, dy
+
+
+def lora(n, k, r):
+    A = O.Rng(4).vec_normal(r * k, 1.0 / 32.0).reshape(r, k)
+    B = O.Rng(5).vec_normal(n * r, 0.01).reshape(n, r)
+    return A, B
+
+
+def hip(ctx, wtype, blocks, n, k):
+    return rt.HipFrozen(wtype, blocks, n, k, ctx=ctx)
+
+
+# ---------------------------------------------------------------- bit-exact parts
+@pytest.mark.parametrize("wtype", FORMATS)
+def test_activation_quantisation_bit_exact(ctx, wtype):
+    n, k, t = 64, 1024, 37
+    blocks, x, _ = make(wtype, n, k, t)
+    # tie cases: a block whose amax is 127 has id = 1, so x = m + 0.5 must round away from zero
+    x[0, :32] = np.array([127.0, 2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 126.5] + [j - 11.5 for j in range(24)], np.float32)
+    x[1, 32:64] = 0.0  # all-zero block: d = 0, codes 0
+    x[2, :32] *= np.float32(1e-6)  # tiny scale: fp16 subnormal d
+    w = hip(ctx, wtype, blocks, n, k)
+    got = w.debug_quantize_acts(x, t)
+    want = O.quantize_acts(wtype, x)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("wtype", FORMATS)
+@pytest.mark.parametrize("n,k,t", [(80, 256, 20), (64, 96, 3), (128, 1024, 65)])
+def test_block_isums_bit_exact(ctx, wtype, n, k, t):
+    blocks, x, _ = make(wtype, n, k, t)
+    w = hip(ctx, wtype, blocks, n, k)
+    got = w.debug_block_isums(x, t)
+    want = O.block_isums(wtype, blocks, O.quantize_acts(wtype, x), k)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("wtype", FORMATS)
+def test_row_dequant_bit_exact(ctx, wtype):
+    n, k = 200, 384
+    blocks, _, _ = make(wtype, n, k, 1)
+    w = hip(ctx, wtype, blocks, n, k)
+    out = np.empty(k, np.float32)
+    for r in (0, 1, 15, 16, 63, 64, 127, 199):
+        w.row(r, out)
+        assert np.array_equal(out, O.frozen_row(wtype, blocks, n, k, r)), r
+
+
+# ---------------------------------------------------------------- FrozenMatmul
+SHAPES = [(64, 128, 1), (100, 96, 5), (256, 512, 37), (3072, 1024, 16), (3072, 1024, 256), (1024, 3072, 64)]
+
+
+@pytest.mark.parametrize("wtype", FORMATS)
+@pytest.mark.parametrize("n,k,t", SHAPES)
+def test_forward_matches_oracle(ctx, wtype, n, k, t):
+    blocks, x, _ = make(wtype, n, k, t)
+    w = hip(ctx, wtype, blocks, n, k)
+    y = w.forward(x, t)
+    assert y.shape == (t * n,)
+    want = O.frozen_forward(wtype, blocks, n, k, x, nthreads=8)
+    assert rel_err(y, want) <= TOL
+
+
+@pytest.mark.parametrize("wtype", FORMATS)
+@pytest.mark.parametrize("n,k,t", SHAPES)
+def test_backward_input_matches_oracle(ctx, wtype, n, k, t):
+    blocks, _, dy = make(wtype, n, k, t)
+    w = hip(ctx, wtype, blocks, n, k)
+    dx0 = O.Rng(7).vec_normal(t * k, 1.0)
+    dx = dx0.copy()
+    w.backward_input(dy, t, dx)  # accumulates
+    want = O.frozen_backward_input(wtype, blocks, n, k, dy, dx=np.zeros((t, k), np.float32), nthreads=8)
+    assert rel_err(dx - dx0, want) <= TOL
+    # tests/engine.rs:96-120: equals the dense dy . W built from row(), 1e-3 * max(|want|, 1)
+    W = np.stack([O.frozen_row(wtype, blocks, n, k, r) for r in range(n)]).astype(np.float64)
+    dense = dy.astype(np.float64) @ W
+    got = (dx - dx0).reshape(t, k)
+    assert (np.abs(got - dense) < 1e-3 * np.maximum(np.abs(dense), 1.0)).all()
+
+
+def test_empty_token_count(ctx):
+    blocks, _, _ = make(O.Q4_0, 64, 128, 1)
+    w = hip(ctx, O.Q4_0, blocks, 64, 128)
+    assert w.forward(np.zeros(0, np.float32), 0).size == 0
+    dx = np.zeros(0, np.float32)
+    w.backward_input(np.zeros(0, np.float32), 0, dx)
+
+
+def test_nbytes_and_dims(ctx):
+    blocks, _, _ = make(O.Q4_0, 3072, 1024, 1)
+    w = hip(ctx, O.Q4_0, blocks, 3072, 1024)
+    assert w.nbytes() == 3072 * 1024 // 32 * 18 == blocks.nbytes
+    assert (w.out_dim(), w.in_dim()) == (3072, 1024)
+
+
+def test_errors_are_status_codes(ctx):
+    blocks, _, _ = make(O.Q4_0, 64, 128, 1)
+    with pytest.raises(rt.RtqError) as e:
+        rt.HipFrozen(O.Q4_0, blocks[:, :-1], 64, 128, ctx=ctx)  # wrong byte count
+    assert e.value.status == 1
+    with pytest.raises(rt.RtqError) as e:
+        rt.HipFrozen(3, blocks, 64, 128, ctx=ctx)  # Q4_1: not a supported format
+    assert e.value.status == 2
+    w = hip(ctx, O.Q4_0, blocks, 64, 128)
+    with pytest.raises(rt.RtqError):
+        w.row(64, np.empty(128, np.float32))
+
+
+# ---------------------------------------------------------------- Linear + LoRA
+@pytest.mark.parametrize("wtype", FORMATS)
+@pytest.mark.parametrize("n,k,t,r", [(3072, 1024, 256, 16), (256, 512, 37, 2), (100, 96, 5, 16), (512, 256, 70, 64)])
+def test_linear_lora_matches_oracle(ctx, wtype, n, k, t, r):
+    alpha = 2.0 * r
+    blocks, x, dy = make(wtype, n, k, t)
+    A, B = lora(n, k, r)
+    bias = O.Rng(6).vec_normal(n, 0.1)
+    lin = rt.Linear("blk.0.ffn_gate", hip(ctx, wtype, blocks, n, k), bias=bias)
+    lin.lora = rt.Lora(r, alpha, A, B)
+    y = lin.forward(x, t)
+    want = O.linear_forward(wtype, blocks, n, k, x, bias=bias, A=A, B=B, alpha=alpha, nthreads=8)
+    assert rel_err(y, want) <= TOL
+    ga0 = O.Rng(8).vec_normal(r * k, 0.01)
+    gb0 = O.Rng(9).vec_normal(n * r, 0.01)
+    lin.lora.ga[...] = ga0
+    lin.lora.gb[...] = gb0
+    dx = lin.backward(x, dy, t)
+    wdx, wga, wgb = O.linear_backward(wtype, blocks, n, k, x, dy, A=A, B=B, alpha=alpha, nthreads=8)
+    assert rel_err(dx, wdx) <= TOL
+    assert rel_err(lin.lora.ga - ga0, wga) <= TOL
+    assert rel_err(lin.lora.gb - gb0, wgb) <= TOL
+
+
+def test_linear_disabled_adapter_and_no_bias(ctx):
+    n, k, t, r = 256, 256, 9, 4
+    blocks, x, dy = make(O.Q4_0, n, k, t)
+    A, B = lora(n, k, r)
+    lin = rt.Linear("blk.0.attn_q", hip(ctx, O.Q4_0, blocks, n, k))
+    lin.lora = rt.Lora(r, 8.0, A, B)
+    lin.lora_enabled = False
+    y = lin.forward(x, t)
+    assert rel_err(y, O.frozen_forward(O.Q4_0, blocks, n, k, x)) <= TOL
+    dx = lin.backward(x, dy, t)
+    assert rel_err(dx, O.frozen_backward_input(O.Q4_0, blocks, n, k, dy)) <= TOL
+    assert not lin.lora.ga.any() and not lin.lora.gb.any()
+
+
+# ---------------------------------------------------------------- device-pointer API
+def test_device_pointer_api_matches_host_api(ctx):
+    import torch
+
+    n, k, t, r = 3072, 1024, 256, 16
+    blocks, x, dy = make(O.Q4_0, n, k, t)
+    A, B = lora(n, k, r)
+    w = hip(ctx, O.Q4_0, blocks, n, k)
+    dev = torch.device("cuda", 0)
+    X = torch.from_numpy(x).to(dev)
+    DY = torch.from_numpy(dy).to(dev)
+    At, Bt = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+    Y = torch.empty(t, n, device=dev)
+    DX = torch.empty(t, k, device=dev)
+    GA = torch.zeros(r, k, device=dev)
+    GB = torch.zeros(n, r, device=dev)
+    from rust_trainer_amd import _ffi
+    import ctypes
+
+    lv = _ffi.RtqLora(r, 32.0, At.data_ptr(), Bt.data_ptr(), 1)
+    s = torch.cuda.current_stream().cuda_stream
+    _ffi.check(_ffi.lib().rtq_linear_forward_d(ctx.handle, w.handle, None, ctypes.byref(lv), X.data_ptr(), t,
+                                               Y.data_ptr(), s), "fwd_d")
+    _ffi.check(_ffi.lib().rtq_linear_backward_d(ctx.handle, w.handle, ctypes.byref(lv), X.data_ptr(), DY.data_ptr(), t,
+                                                DX.data_ptr(), GA.data_ptr(), GB.data_ptr(), s), "bwd_d")
+    torch.cuda.synchronize()
+    lin = rt.Linear("x", w)
+    lin.lora = rt.Lora(r, 32.0, A, B)
+    assert rel_err(Y.cpu().numpy(), lin.forward(x, t)) <= 1e-6
+    dx = lin.backward(x, dy, t)
+    assert rel_err(DX.cpu().numpy(), dx) <= 1e-5
+    assert rel_err(GA.cpu().numpy(), lin.lora.ga) <= 1e-5
+    assert rel_err(GB.cpu().numpy(), lin.lora.gb) <= 1e-5
+
+
+# ---------------------------------------------------------------- maximum size
+def test_lm_head_shape_t1(ctx):
+    # tied LM head of Qwen3-0.6B: 151936 x 1024, one token (decode-shaped GEMV)
+    n, k, t = 151936, 1024, 1
+    blocks, x, dy = make(O.Q4_0, n, k, t)
+    w = hip(ctx, O.Q4_0, blocks, n, k)
+    y = w.forward(x, t)
+    assert rel_err(y, O.frozen_forward(O.Q4_0, blocks, n, k, x, nthreads=16)) <= TOL
+    dx = np.zeros(t * k, np.float32)
+    w.backward_input(dy, t, dx)
+    assert rel_err(dx, O.frozen_backward_input(O.Q4_0, blocks, n, k, dy, nthreads=16)) <= TOL
