@@ -27,7 +27,7 @@ if ROOT not in sys.path:
 METRIC = "trained tokens/s fwd+bwd, Qwen3-0.6B Q4_0 LoRA r16; quant-matmul % roofline"
 N, K, T, R, ALPHA = 3072, 1024, 256, 16, 32.0
 HBM_PEAK_GBS = 8000.0
-F16_PEAK_TFLOPS = 2500.0  # dense f16 MFMA (the forward's integer block dots and dx run on it)
+F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16 MFMA (the forward's integer block dots and dx run on it)
 
 
 def kernel_work(name: str) -> tuple[float, float] | None:
@@ -37,17 +37,15 @@ def kernel_work(name: str) -> tuple[float, float] | None:
         acts = T * K + T * (K // 32) * 2  # int8 codes + fp16 scales
         return float(w_bytes + acts + T * N * 4 + N * R * 4 + T * R * 4), float(2 * T * N * K + 2 * T * N * R)
     if name.startswith("rtq_dx_"):
-        return float(w_bytes + T * N * 4 + T * K * 4 + R * K * 4 + T * R * 4), float(2 * T * N * K + 2 * T * R * K)
-    if name == "rtq_quant_q8_0":
-        return float(T * K * 4 + T * K + T * (K // 32) * 2), 0.0
-    if name == "rtq_dy_prep":
-        return float(T * N * 4 + T * N * 2 + T * K * 4), 0.0
-    if name == "rtq_lora_down":
-        return float(T * K * 4 + R * K * 4 + T * R * 4), float(2 * T * K * R)
-    if name == "rtq_lora_g":
-        return float(T * N * 4 + N * R * 4 + T * R * 4), float(2 * T * N * R)
-    if name == "rtq_lora_grads":
-        return float(T * N * 4 + T * K * 4 + 2 * T * R * 4 + 2 * (N * R + R * K) * 4), float(2 * T * R * (N + K))
+        return float(w_bytes + T * N * 4 + T * K * 4), float(2 * T * N * K)
+    if name == "rtq_act_prep_q8_0":  # quantise x, h = x.A^T
+        return float(T * K * 4 + T * K + T * (K // 32) * 4 + R * K * 4 + T * R * 4), float(2 * T * K * R)
+    if name == "rtq_lora_hg":  # h = x.A^T, g = s dy.B, clear dx
+        return float(T * K * 4 + T * N * 4 + (R * K + N * R) * 4 + 2 * T * R * 4 + T * K * 4), \
+            float(2 * T * R * (K + N))
+    if name == "rtq_lora_grads":  # dB, dA, dx += g.A
+        return float(T * N * 4 + T * K * 4 + 2 * T * R * 4 + 2 * (N * R + R * K) * 4 + 2 * T * K * 4), \
+            float(2 * T * R * (N + 2 * K))
     return None
 
 
@@ -199,7 +197,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 x q8_0 int block dots -> f32 (fwd); f16 (dx); f32 (LoRA)",
+        "dtype": "q4_0 x q8_0 int block dots -> f32 (fwd); bf16x3 (dx); f32 (LoRA)",
         "data": "synthetic",
         "config": {"workload": "configs[0]: Qwen3-0.6B gate_proj frozen linear, Q4_0 W 3072x1024, T=256, "
                                "LoRA r=16 alpha=32; Linear forward (y) + backward (dx, dA, dB)",

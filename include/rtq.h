@@ -12,8 +12,9 @@
  *   - forward OVERWRITES y; backward_input ACCUMULATES into dx (dx += dy . W);
  *     linear_backward returns a fresh dx (overwrites) and ACCUMULATES ga / gb;
  *   - errors are status codes (the reference asserts; a Rust wrapper panics on non-zero);
- *   - host-pointer entry points are synchronous; `_d` entry points take device pointers and a
- *     HIP stream (hipStream_t passed as void*, NULL = the context's own stream) and only enqueue.
+ *   - host-pointer entry points are synchronous (they run on the context's own stream); `_d` entry
+ *     points take device pointers and a HIP stream (hipStream_t passed as void*, NULL = the HIP
+ *     null stream, as torch's default stream is) and only enqueue.
  *     Calls on one context are serialised by a lock; `_d` calls that share a context must be
  *     issued on one stream (they share the context's device workspace).
  */

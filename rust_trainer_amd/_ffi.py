@@ -73,12 +73,23 @@ class RtqError(RuntimeError):
         self.status = status
 
 
+def _share_torch_hip_runtime() -> None:
+    """PyTorch-ROCm ships its own libamdhip64.so.7.  Loading it first makes librtq.so's dependency
+    on libamdhip64.so.7 resolve to that same runtime, so tensors and streams from torch and the
+    library's kernels live in one HIP runtime (two runtimes in one process do not share devices)."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def lib() -> ctypes.CDLL:
     """Loads librtq.so (raises if it has not been built)."""
     global _LIB
     if _LIB is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build()")
+        _share_torch_hip_runtime()
         L = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(L, name)

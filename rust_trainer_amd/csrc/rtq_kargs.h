@@ -4,121 +4,107 @@
 //
 // Device weight layout ("row-group / K-chunk" layout, same byte count as GGUF):
 //   rows are padded to Np = roundup(N, 64) and grouped by 16 (one MFMA tile edge); columns
-//   are padded to Kp = roundup(K, 128) for Q4_0 / Q8_0 (a chunk = 4 blocks of 32) and to
-//   roundup(K, 256) for Q4_K / Q6_K (a chunk = one 256-element super-block).  For every
+//   are padded to Kp = roundup(K, 128) for Q4_0 / Q8_0 (a chunk = 4 blocks of 32).  For every
 //   (row group rg, chunk kc) the quant codes of the 16 rows are stored so that lane l of a
 //   wave (row rg*16 + l%16, k-group g = l/16) reads its MFMA fragment with one coalesced
-//   16-byte load: lane l holds, for every 32-element group j of the chunk, the codes of
+//   16-byte load: lane l holds, for every 32-element block j of the chunk, the codes of
 //   elements {32j + 4g .. 32j + 4g + 3} and {32j + 16 + 4g .. 32j + 16 + 4g + 3}.  For Q4_0
 //   that is exactly bytes 4g..4g+3 of the GGUF block (low nibbles: the first four, high
-//   nibbles: the second four), so no nibble is moved across bytes.
+//   nibbles: the second four), so no nibble moves across bytes.
+//     Q4_0: qs  uint4 [Np/16][Kc][64]      (component j = block j's four bytes)
+//     Q8_0: qs  uint4 [Np/16][Kc][2][64]   (part p: blocks 2p, 2p+1; 8 bytes each: low word
+//                                           elements 4g..4g+3, high word 16+4g..16+4g+3)
+//     both: d   fp16  [Np/16][Kc][16][4]    (row-in-group, block)
 #pragma once
 #include <stdint.h>
 
-#define RTQ_ROW_PAD 64     // Np multiple
-#define RTQ_T_PAD 64       // Tp multiple (token tiles)
-#define RTQ_CHUNK_Q 128    // K chunk of Q4_0 / Q8_0
-#define RTQ_CHUNK_K 256    // K chunk of Q4_K / Q6_K
+#define RTQ_ROW_PAD 64    // Np multiple
+#define RTQ_CHUNK_Q 128   // K chunk of Q4_0 / Q8_0
 
-// ---------------------------------------------------------------- activation quantisation
-// x [T x K] f32 -> MFMA A-operand fragments of the integer codes (as f16, exact) and scales.
-//   xa: uint4 [Tp/16][Kp/32 blocks / 4 per chunk][4][64]  (one uint4 = 8 halves per lane)
+// ---------------------------------------------------------------- forward activation prep
+// One workgroup per 16 tokens.  x [T x K] f32 ->
+//   xq: Q8_0 codes as MFMA A fragments, exact f16: uint4 [Tp/16][Kp/128][4][64] (8 per lane per block)
 //   xd: f32 [Kp/32][Tp]  (value of the fp16 scale; 0 for padding)
-//   K-quant (Q8_K): xd is [Kp/256][Tp] (f32 d), xb: f16 bsums [Tp/16][Kp/256][64] (16 per
-//   super-block, 16-element groups, as MFMA A fragments of a K=16 product)
-struct QuantArgs {
+//   h:  x . A^T [T x r]  when A != null (LoRA down-projection, src/linear.rs:85)
+//   zero_y: rows of y cleared when the forward GEMM splits K (it then accumulates)
+struct ActArgs {
   const float* x;
   int T, K, Tp, Kp;
-  void* xa;
+  void* xq;
   float* xd;
-  void* xb;  // Q8_K only
-};
-
-// h[t][j] = sum_k x[t][k] * A[j][k]   (LoRA down-projection, src/linear.rs:85)
-struct LoraDownArgs {
-  const float* x;
   const float* A;
-  int T, K, r;
-  float* h;  // [T x r]
+  int r;
+  float* h;
+  float* zero_y;
+  int N;
 };
 
 // ---------------------------------------------------------------- forward GEMM
 struct FwdArgs {
   const void* wq;       // quant codes, device layout
-  const uint16_t* wd;   // fp16 scales, device layout (Q4_K: d,dmin pairs; Q6_K: d)
-  const void* wx;       // extra per-format data (Q4_K 6-bit scales/mins, Q6_K int8 scales)
+  const uint16_t* wd;   // fp16 scales, device layout
   int Np, Kp;
-  const void* xa;       // activation fragments
+  const void* xq;       // activation fragments (f16 integer codes)
   const float* xd;      // activation scales
-  const void* xb;       // activation bsums (Q8_K)
   int Tp, T, N, K;
+  int kc_per_split;     // K chunks per blockIdx.z (split-K accumulates with atomics)
   float* y;             // [T x N]
   const float* bias;    // [N] or null
   const float* h;       // [T x r] or null (LoRA disabled)
   const float* lb;      // LoRA B [N x r]
   int r;
   float s;              // alpha / r
-  int32_t* isums;       // debug: [T][N][isums_per_row] or null
+  int32_t* isums;       // debug: [T][N][K/32] or null
 };
 
 // ---------------------------------------------------------------- backward
-// dy [T x N] f32 -> f16 fragments scaled per token row by 2^e_t (exact power of two) for the
-// dx product; einv[t] = 2^-e_t.  Optionally zero-fills dx (Linear::backward returns a fresh dx)
-// and g (LoRA, accumulated with atomics afterwards).
-struct DyPrepArgs {
-  const float* dy;
-  int T, N, Tp, Np;
-  void* dy16;       // uint4 [Tp/16][Np/32][64]
-  float* einv;      // [Tp]
-  float* zero_dx;   // [T x K] or null
+// blockIdx.y == 0: h[t][j] = sum_k x[t][k] A[j][k]; blockIdx.y == 1: g[t][j] = sum_n (s dy[t][n]) B[n][j]
+// (src/linear.rs:106-111), one workgroup per 16 tokens; optionally clears dx first.
+struct HGArgs {
+  const float* x;
+  const float* A;
   int K;
-  float* zero_g;    // [T x r] or null
-  int r;
-};
-
-// g[t][j] += s * sum_n dy[t][n] * B[n][j]   (src/linear.rs:108-111), split over n
-struct LoraGArgs {
   const float* dy;
-  const float* lb;  // [N x r]
-  int T, N, r;
+  const float* B;
+  int N;
+  int T, r;
   float s;
-  int n_per_split;
-  float* g;         // [T x r], pre-zeroed
+  float* h;
+  float* g;
+  float* zero_dx;
 };
 
+// dx[t][k] += sum_n dy[t][n] W[n][k]: workgroup tile 64 tokens x 128 columns, rows of W split
+// over blockIdx.z (atomics when split), three bf16 MFMAs per product (hi/lo split of dy and W).
 struct DxArgs {
   const void* wq;
   const uint16_t* wd;
-  const void* wx;
   int Np, Kp;
-  const void* dy16;
-  const float* einv;
-  int Tp, T, K;
-  int n_per_split;  // rows of W per split (multiple of 32)
-  float* dx;        // [T x K], accumulated with atomics
-  const float* g;   // LoRA g [T x r] or null
-  const float* la;  // LoRA A [r x K]
-  int r;
+  const float* dy;
+  int T, N, K;
+  int n_per_split;      // rows of W per split (multiple of 32)
+  float* dx;            // [T x K]
 };
 
-// gb[n][j] += sum_t (s*dy[t][n]) * h[t][j];  ga[j][k] += sum_t g[t][j] * x[t][k]
+// gb[n][j] += sum_t (s*dy[t][n]) h[t][j];  ga[j][k] += sum_t g[t][j] x[t][k];  dx[t][k] += sum_j g[t][j] A[j][k]
 struct LoraGradArgs {
   const float* dy;
   const float* h;
   const float* g;
   const float* x;
+  const float* la;
   int T, N, K, r;
   float s;
   float* gb;  // [N x r]
   float* ga;  // [r x K]
-  int n_tiles_gb;  // blocks [0, n_tiles_gb) do gb, the rest do ga
+  float* dx;  // [T x K]
+  int n_gb, n_ga, n_dx;  // workgroups of each part, in this order
 };
 
 // rows [r0, r0+count) dequantised to f32 (bit-exact ggml dequant)
 struct RowArgs {
   const void* wq;
   const uint16_t* wd;
-  const void* wx;
   int Np, Kp, K;
   int r0, count;
   float* out;  // [count x K]

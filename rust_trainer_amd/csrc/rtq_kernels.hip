@@ -6,12 +6,15 @@
 // Arithmetic contract (reference: src/rie.rs:74-124, src/linear.rs:73-121):
 //  * activations are quantised to Q8_0 exactly as ggml's reference quantiser does;
 //  * each 32-element block dot is an exact integer sum.  The integer codes are fed to the
-//    f16 MFMA as exact small integers (|q8| <= 127, |q4| <= 8), every product is exact in the
-//    f32 accumulator and so is the 32-term sum (|isum| <= 32*127*127 < 2^24): the MFMA output
-//    *is* the integer block sum, with no i32->f32 conversion to pay;
+//    f16 MFMA as exact small integers (|q8| <= 127, |q4| <= 8): every product is exact in the
+//    f32 accumulator and so is the 32-term sum (|isum| <= 32*127*127 < 2^24), so the MFMA output
+//    is the integer block sum itself, with no i32->f32 conversion to pay in the epilogue;
 //  * block sums are scaled by d_w * d_x in f32 (the epilogue order is unpinned in the reference);
-//  * dx = dy . W runs on f16 MFMA: W dequantised in registers to f16 (one rounding of the exact
-//    product d*q) and dy scaled per token row by an exact power of two into f16 range.
+//  * dx = dy . W (no dy quantisation, straight-through as in the reference) runs on bf16 MFMA with
+//    both operands split into hi + lo bf16 parts (dy = dh + dl, W = wh + wl exactly for Q4_0):
+//    dh.wh + dl.wh + dh.wl leaves a relative error near 2^-16 per product, far inside the f32
+//    tolerance, and needs no range scaling (bf16 has the f32 exponent range);
+//  * the LoRA products run on f32 MFMA (exact f32 products, f32 accumulation).
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -19,36 +22,41 @@
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+// native integer vectors (HIP's u4v/u2v are union-wrapped structs whose copies become memcpy
+// and keep register arrays in scratch)
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
 
-enum { FMT_Q4_0 = 2, FMT_Q8_0 = 8, FMT_Q4_K = 12, FMT_Q6_K = 14 };
+enum { FMT_Q4_0 = 2, FMT_Q8_0 = 8 };
 
 __device__ __forceinline__ f4 mfma_f16(half8 a, half8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f4 mfma_bf16(bf8 a, bf8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ f4 mfma_f32(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-__device__ __forceinline__ half8 as_half8(uint4 v) { return __builtin_bit_cast(half8, v); }
-__device__ __forceinline__ uint32_t comp(const uint4& v, int j) {
+__device__ __forceinline__ uint32_t comp(const u4v& v, int j) {
   return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w));
 }
-__device__ __forceinline__ uint16_t hcomp(const uint2& v, int j) {
+__device__ __forceinline__ uint16_t hcomp(const u2v& v, int j) {
   const uint32_t w = (j < 2) ? v.x : v.y;
   return (uint16_t)((j & 1) ? (w >> 16) : (w & 0xffffu));
 }
 
-// four bytes b0..b3 (each < 256) -> two half2 words holding 1024 + b (exact f16 integers)
-__device__ __forceinline__ uint32_t bytes01_to_h2(uint32_t v) {
-  return (v & 0xffu) | ((v & 0xff00u) << 8) | 0x64006400u;
-}
-__device__ __forceinline__ uint32_t bytes23_to_h2(uint32_t v) {
-  return ((v >> 16) & 0xffu) | ((v >> 8) & 0xff0000u) | 0x64006400u;
-}
+// Bytes b0..b3 of v -> two half2 words {1024 + b0, 1024 + b1}, {1024 + b2, 1024 + b3} (exact f16
+// integers): v_perm_b32 interleaves the bytes with 0x64, the high byte of 1024.0 in f16.  The
+// selector picks bytes 0-3 from the second operand and 4-7 from the first.
+__device__ __forceinline__ uint32_t bytes01_to_h2(uint32_t v) { return __builtin_amdgcn_perm(0x64646464u, v, 0x04010400u); }
+__device__ __forceinline__ uint32_t bytes23_to_h2(uint32_t v) { return __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u); }
 __device__ __forceinline__ half2v sub_h2(uint32_t bits, _Float16 c) {
-  half2v h = __builtin_bit_cast(half2v, bits);
-  half2v cc = {c, c};
+  const half2v h = __builtin_bit_cast(half2v, bits);
+  const half2v cc = {c, c};
   return h - cc;  // exact: small integers
 }
 
@@ -57,9 +65,9 @@ __device__ __forceinline__ half2v sub_h2(uint32_t bits, _Float16 c) {
 __device__ __forceinline__ half8 q4_0_frag(uint32_t w) {
   const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
   const _Float16 c = (_Float16)1032.0f;
-  half2v a0 = sub_h2(bytes01_to_h2(lo), c), a1 = sub_h2(bytes23_to_h2(lo), c);
-  half2v a2 = sub_h2(bytes01_to_h2(hi), c), a3 = sub_h2(bytes23_to_h2(hi), c);
-  half8 r = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+  const half2v a0 = sub_h2(bytes01_to_h2(lo), c), a1 = sub_h2(bytes23_to_h2(lo), c);
+  const half2v a2 = sub_h2(bytes01_to_h2(hi), c), a3 = sub_h2(bytes23_to_h2(hi), c);
+  const half8 r = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
   return r;
 }
 
@@ -68,20 +76,21 @@ __device__ __forceinline__ half8 q8_frag(uint32_t lo, uint32_t hi) {
   lo ^= 0x80808080u;  // u = q + 128
   hi ^= 0x80808080u;
   const _Float16 c = (_Float16)1152.0f;
-  half2v a0 = sub_h2(bytes01_to_h2(lo), c), a1 = sub_h2(bytes23_to_h2(lo), c);
-  half2v a2 = sub_h2(bytes01_to_h2(hi), c), a3 = sub_h2(bytes23_to_h2(hi), c);
-  half8 r = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+  const half2v a0 = sub_h2(bytes01_to_h2(lo), c), a1 = sub_h2(bytes23_to_h2(lo), c);
+  const half2v a2 = sub_h2(bytes01_to_h2(hi), c), a3 = sub_h2(bytes23_to_h2(hi), c);
+  const half8 r = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
   return r;
+}
+
+// f32 -> bf16 hi + bf16 lo (hi = RNE(x), lo = RNE(x - hi); x - hi is exact in f32)
+__device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
+  hi = (__bf16)x;
+  lo = (__bf16)(x - (float)hi);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
   return v;
 }
 
@@ -90,420 +99,649 @@ extern "C" __global__ __launch_bounds__(256) void rtq_fill_zero(FillArgs a) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (int64_t)gridDim.x * 256) a.p[i] = 0.0f;
 }
 
-// ============================================================== activation quantisation (Q8_0)
-// One thread per (token, 32-element block).  ggml reference semantics:
-// d = amax/127, id = d ? 1/d : 0, q = roundf(x*id) (ties away from zero), stored scale fp16(d).
-extern "C" __global__ __launch_bounds__(256) void rtq_quant_q8_0(QuantArgs a) {
-  const int nb = a.Kp / 32;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)a.Tp * nb) return;
-  const int t = (int)(idx / nb), b = (int)(idx % nb);
-  const bool valid = t < a.T && b * 32 < a.K;
-  float v[32];
-  float amax = 0.0f;
-  if (valid) {
-    const float4* src = reinterpret_cast<const float4*>(a.x + (int64_t)t * a.K + b * 32);
+// grid-stride clear of rows [0, T) x [0, cols) by every thread of the grid
+__device__ __forceinline__ void clear_rows(float* p, int64_t n) {
+  const int64_t nthr = (int64_t)gridDim.x * gridDim.y * blockDim.x;
+  const int64_t id = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x;
+  for (int64_t i = id; i < n; i += nthr) p[i] = 0.0f;
+}
+
+// ============================================================== skinny f32 product
+// out16x16 tile (rows r0.., cols c0..) of  P[row][col] = sum_k S[row][k] * M(col, k), reduced
+// over k in [0, klen) by the NW waves of the workgroup (LDS reduction), f32 MFMA
+// 16x16x4.  M(col, k) = Bm[col*ldb + k] when b_rows (row-major over k), else Bm[k*ldb + col]
+// (column of a [klen x ncols] matrix).  Loads of four 16-k groups are issued before their
+// MFMAs.  Leaves the reduced tile in red[NW*256 + row*16 + col] for the caller.
+// Loads this lane's four consecutive k (kk .. kk+3) of S[row] and of M(col, .).  Indices are
+// clamped into the matrices and out-of-range values replaced by 0, so every load is issued
+// unconditionally (no divergent branches around memory instructions).
+__device__ __forceinline__ void load_group(const float* S, int nrows, int lds, const float* Bm, int ncols, int ldb,
+                                           bool b_rows, bool vec, int klen, int ke, int row, int col, int kk,
+                                           float av[4], float bv[4]) {
+  const uint32_t rowc = (uint32_t)min(row, nrows - 1), colc = (uint32_t)min(col, ncols - 1);
+  const bool rin = row < nrows && kk < ke, cin = col < ncols && kk < ke;
+  if (vec) {  // klen % 4 == 0, lds % 4 == 0, ldb % 4 == 0 (uniform)
+    const uint32_t kc = (uint32_t)min(kk, klen - 4);
+    const f4 q = *reinterpret_cast<const f4*>(S + (rowc * (uint32_t)lds + kc));
+    av[0] = q.x; av[1] = q.y; av[2] = q.z; av[3] = q.w;
+    if (b_rows) {
+      const f4 r = *reinterpret_cast<const f4*>(Bm + (colc * (uint32_t)ldb + kc));
+      bv[0] = r.x; bv[1] = r.y; bv[2] = r.z; bv[3] = r.w;
+    } else {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float4 q = src[i];
-      v[4 * i] = q.x;
-      v[4 * i + 1] = q.y;
-      v[4 * i + 2] = q.z;
-      v[4 * i + 3] = q.w;
+      for (int c = 0; c < 4; c++) bv[c] = Bm[(kc + c) * (uint32_t)ldb + colc];
     }
 #pragma unroll
-    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    for (int c = 0; c < 4; c++) {
+      av[c] = (rin && kk + c < klen) ? av[c] : 0.0f;
+      bv[c] = (cin && kk + c < klen) ? bv[c] : 0.0f;
+    }
   } else {
 #pragma unroll
-    for (int i = 0; i < 32; i++) v[i] = 0.0f;
-  }
-  const float d = __fdiv_rn(amax, 127.0f);
-  const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-  const _Float16 dh = (_Float16)d;
-  a.xd[(int64_t)b * a.Tp + t] = valid ? (float)dh : 0.0f;
-  _Float16 q[32];
-#pragma unroll
-  for (int i = 0; i < 32; i++) q[i] = (_Float16)roundf(__fmul_rn(v[i], id));
-  const int kc = b >> 2, j = b & 3, tg = t >> 4;
-  uint4* xa = reinterpret_cast<uint4*>(a.xa) + ((int64_t)(tg * (a.Kp / 128) + kc) * 4 + j) * 64;
-#pragma unroll
-  for (int g = 0; g < 4; g++) {
-    half8 f = {q[4 * g], q[4 * g + 1], q[4 * g + 2], q[4 * g + 3],
-               q[16 + 4 * g], q[17 + 4 * g], q[18 + 4 * g], q[19 + 4 * g]};
-    xa[(t & 15) + 16 * g] = __builtin_bit_cast(uint4, f);
-  }
-}
-
-// ============================================================== LoRA down-projection
-// h[t][j] = sum_k x[t][k] * A[j][k]  (src/linear.rs:85, matmul_nt).  One wave per token,
-// lanes stride over k, 16 adapter rows per pass, wave reduction per row.
-extern "C" __global__ __launch_bounds__(256) void rtq_lora_down(LoraDownArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= a.T) return;
-  const float* x = a.x + (int64_t)t * a.K;
-  for (int j0 = 0; j0 < a.r; j0 += 16) {
-    float acc[16];
-#pragma unroll
-    for (int j = 0; j < 16; j++) acc[j] = 0.0f;
-    for (int k = lane; k < a.K; k += 64) {
-      const float xv = x[k];
-#pragma unroll
-      for (int j = 0; j < 16; j++)
-        if (j0 + j < a.r) acc[j] = fmaf(xv, a.A[(int64_t)(j0 + j) * a.K + k], acc[j]);
-    }
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-      const float s = wave_sum(acc[j]);
-      if (lane == 0 && j0 + j < a.r) a.h[(int64_t)t * a.r + j0 + j] = s;
+    for (int c = 0; c < 4; c++) {
+      const uint32_t k = (uint32_t)min(kk + c, klen - 1);
+      const float x = S[rowc * (uint32_t)lds + k];
+      const float y = b_rows ? Bm[colc * (uint32_t)ldb + k] : Bm[k * (uint32_t)ldb + colc];
+      av[c] = (rin && kk + c < klen) ? x : 0.0f;
+      bv[c] = (cin && kk + c < klen) ? y : 0.0f;
     }
   }
 }
 
-// ============================================================== forward (Q4_0 / Q8_0)
-// Workgroup tile 64 tokens x 64 weight rows, 4 waves of 32 x 32 (2 x 2 MFMA tiles of 16x16).
-// Per 32-element block: one 16x16x32 f16 MFMA per tile gives the exact integer block sums,
-// then acc += isum * (d_w * d_x).  Weights and activations are read straight from their
-// fragment layouts (one 16-byte load per lane per fragment, fully coalesced).
+template <int NW>
+__device__ __forceinline__ void skinny_tile(const float* S, int nrows, int lds, const float* Bm, int ncols, int ldb,
+                                            bool b_rows, int klen, int r0, int c0, float sscale, float* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
+  const int per = ((klen + 15) / 16 + NW - 1) / NW * 16;  // k per wave, multiple of 16
+  const int kb = w * per, ke = min(kb + per, klen);
+  const int row = r0 + li, col = c0 + li;
+  const bool vec = (klen & 3) == 0 && (lds & 3) == 0 && (ldb & 3) == 0 && klen >= 4;
+  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  // two batches of four 16-k groups in flight: the loads of batch U + 2 are issued right after
+  // batch U's MFMAs (indices clamped, out-of-range values zeroed)
+  float av[2][4][4], bv[2][4][4];
+#define RTQ_SKINNY_LOAD(U, KB)                                                                           \
+  _Pragma("unroll") for (int u = 0; u < 4; u++)                                                          \
+      load_group(S, nrows, lds, Bm, ncols, ldb, b_rows, vec, klen, ke, row, col, (KB) + 16 * u + 4 * g,  \
+                 av[U][u], bv[U][u]);
+#define RTQ_SKINNY_MMA(U)                                                                                 \
+  _Pragma("unroll") for (int u = 0; u < 4; u++) _Pragma("unroll") for (int c = 0; c < 4; c++) acc =     \
+      mfma_f32(sscale == 1.0f ? av[U][u][c] : __fmul_rn(av[U][u][c], sscale), bv[U][u][c], acc);
+  RTQ_SKINNY_LOAD(0, kb)
+  RTQ_SKINNY_LOAD(1, kb + 64)
+  for (int k = kb; k < ke; k += 128) {
+    RTQ_SKINNY_MMA(0)
+    RTQ_SKINNY_LOAD(0, k + 128)
+    if (k + 64 < ke) {
+      RTQ_SKINNY_MMA(1)
+    }
+    RTQ_SKINNY_LOAD(1, k + 192)
+  }
+#undef RTQ_SKINNY_MMA
+#undef RTQ_SKINNY_LOAD
+  // lane holds rows 4g+i, column li
+#pragma unroll
+  for (int i = 0; i < 4; i++) red[w * 256 + (4 * g + i) * 16 + li] = acc[i];
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    float s = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ww++) s += red[ww * 256 + threadIdx.x];
+    red[threadIdx.x + NW * 256] = s;
+  }
+  __syncthreads();
+}
+
+// ============================================================== forward activation prep
+// ggml Q8_0 reference semantics: d = amax/127, id = d ? 1/d : 0, q = roundf(x*id) (ties away
+// from zero), stored scale fp16(d).  One workgroup per 16 tokens.
+extern "C" __global__ __launch_bounds__(512) void rtq_act_prep_q8_0(ActArgs a) {
+  __shared__ float red[9 * 256];
+  const int t0 = blockIdx.x * 16;
+  const int nbp = a.Kp / 32, Kc = a.Kp / 128;
+  for (int idx = threadIdx.x; idx < 16 * nbp; idx += 512) {
+    const int tl = idx / nbp, b = idx % nbp, t = t0 + tl;
+    const bool valid = t < a.T && b * 32 < a.K;
+    float v[32];
+    float amax = 0.0f;
+    if (valid) {
+      const f4* src = reinterpret_cast<const f4*>(a.x + (int64_t)t * a.K + b * 32);
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const f4 q = src[i];
+        v[4 * i] = q.x;
+        v[4 * i + 1] = q.y;
+        v[4 * i + 2] = q.z;
+        v[4 * i + 3] = q.w;
+      }
+#pragma unroll
+      for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; i++) v[i] = 0.0f;
+    }
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    a.xd[(int64_t)b * a.Tp + t] = valid ? (float)(_Float16)d : 0.0f;
+    _Float16 q[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) q[i] = (_Float16)roundf(__fmul_rn(v[i], id));  // exact small integers
+    const int kc = b >> 2, j = b & 3;
+    u4v* xq = reinterpret_cast<u4v*>(a.xq) + ((int64_t)((t >> 4) * Kc + kc) * 4 + j) * 64;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const half8 f = {q[4 * g], q[4 * g + 1], q[4 * g + 2], q[4 * g + 3],
+                       q[16 + 4 * g], q[17 + 4 * g], q[18 + 4 * g], q[19 + 4 * g]};
+      xq[(t & 15) + 16 * g] = __builtin_bit_cast(u4v, f);
+    }
+  }
+  if (a.zero_y) {
+    for (int tl = 0; tl < 16; tl++) {
+      const int t = t0 + tl;
+      if (t < a.T)
+        for (int n = threadIdx.x; n < a.N; n += 512) a.zero_y[(int64_t)t * a.N + n] = 0.0f;
+    }
+  }
+  if (a.A) {
+    for (int j0 = 0; j0 < a.r; j0 += 16) {
+      skinny_tile<8>(a.x, a.T, a.K, a.A, a.r, a.K, true, a.K, t0, j0, 1.0f, red);
+      if (threadIdx.x < 256) {
+        const int t = t0 + (threadIdx.x >> 4), j = j0 + (threadIdx.x & 15);
+        if (t < a.T && j < a.r) a.h[(int64_t)t * a.r + j] = red[8 * 256 + threadIdx.x];
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// ============================================================== forward GEMM (Q4_0 / Q8_0)
+// Workgroup: WT x 4 waves; wave (wt, wn) owns TS token tiles of 16 and one row group of 16.
+// Workgroup tile: (WT*TS*16) tokens x 64 weight rows.  Per 128-column chunk the workgroup stages
+// the activation fragments (int8 in memory, converted once to f16) and scales in LDS (double
+// buffered); each wave reads its weight fragments straight from global memory with one 16-byte
+// load per lane, one chunk ahead.  Per 32-element block: one 16x16x32 f16 MFMA per token tile
+// gives the exact integer block sums, then acc += isum * (d_w * d_x).
 template <int FMT>
 struct WChunk;
 
 template <>
 struct WChunk<FMT_Q4_0> {
-  uint4 q;
-  __device__ __forceinline__ void load(const FwdArgs& a, int rg, int kc, int Kc, int lane) {
-    q = reinterpret_cast<const uint4*>(a.wq)[(int64_t)(rg * Kc + kc) * 64 + lane];
+  static constexpr int QPC = 1;  // u4v per lane per chunk
+  u4v q;
+  u2v d;
+  __device__ __forceinline__ void load(const u4v* Q, uint32_t qo, const u2v* Dd, uint32_t dof) {
+    q = Q[qo];
+    d = Dd[dof];
   }
   __device__ __forceinline__ half8 frag(int j) const { return q4_0_frag(comp(q, j)); }
 };
 
 template <>
 struct WChunk<FMT_Q8_0> {
-  uint4 q[2];
-  __device__ __forceinline__ void load(const FwdArgs& a, int rg, int kc, int Kc, int lane) {
-    const uint4* p = reinterpret_cast<const uint4*>(a.wq) + (int64_t)(rg * Kc + kc) * 128;
-    q[0] = p[lane];
-    q[1] = p[64 + lane];
+  static constexpr int QPC = 2;
+  u4v q[2];
+  u2v d;
+  __device__ __forceinline__ void load(const u4v* Q, uint32_t qo, const u2v* Dd, uint32_t dof) {
+    q[0] = Q[qo];
+    q[1] = Q[qo + 64];
+    d = Dd[dof];
   }
   __device__ __forceinline__ half8 frag(int j) const {
-    const uint4& v = q[j >> 1];
+    const u4v& v = q[j >> 1];
     return (j & 1) ? q8_frag(v.z, v.w) : q8_frag(v.x, v.y);
   }
 };
 
-template <int FMT, bool DBG>
+template <int FMT, int WT, int WN, int TS, int D, bool DBG>
 __device__ __forceinline__ void fwd_q32(const FwdArgs& a) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int li = lane & 15, g = lane >> 4;
+  constexpr int TT = WT * TS;                    // token tiles per workgroup
+  constexpr int NTHR = 64 * WT * WN;             // threads per workgroup
+  constexpr int APT = TT * 256 / NTHR;           // activation u2v loads per thread per chunk
+  constexpr int XPT = (TT * 64 + NTHR - 1) / NTHR;  // scale loads per thread per chunk
+  static_assert((TT * 256) % NTHR == 0, "activation staging must divide evenly");
+  __shared__ u4v sA[2][TT][4][64];
+  __shared__ __attribute__((aligned(16))) float sX[2][4][TT * 16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
+  const int wt = w / WN, wn = w % WN;
   const int Kc = a.Kp / 128;
-  const int rg0 = (blockIdx.x * 64 + (w & 1) * 32) >> 4;
-  const int tg0 = (blockIdx.y * 64 + (w >> 1) * 32) >> 4;
+  const int rg = blockIdx.x * WN + wn;
+  const int tg0 = blockIdx.y * TT;
+  const int kc0 = blockIdx.z * a.kc_per_split;
+  const int kc1 = min(kc0 + a.kc_per_split, Kc);
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 acc[TS];
+#pragma unroll
+  for (int i = 0; i < TS; i++) acc[i] = zero;
+
+  // D-deep register ring: slot u holds the global data of chunk kc (kc - kc0 = u mod D); loads
+  // are issued unconditionally (chunk index clamped) so the wait for slot u only covers loads
+  // issued D chunks earlier.  Per-thread base pointers; a chunk adds a fixed stride.
+  const u4v* XA = reinterpret_cast<const u4v*>(a.xq);
+  const u4v* WQ = reinterpret_cast<const u4v*>(a.wq);
+  const u2v* WD = reinterpret_cast<const u2v*>(a.wd);
+  uint32_t xa_off[APT];
+#pragma unroll
+  for (int q = 0; q < APT; q++) {
+    const int idx = tid + NTHR * q, tsl = idx >> 8, rem = idx & 255;
+    xa_off[q] = ((uint32_t)(tg0 + tsl) * Kc * 4 + (rem >> 6)) * 64 + (rem & 63);
+  }
+  uint32_t xd_off[XPT];
+#pragma unroll
+  for (int q = 0; q < XPT; q++) {
+    const int e = min(tid + NTHR * q, TT * 64 - 1);
+    xd_off[q] = (uint32_t)(e / (TT * 16)) * a.Tp + tg0 * 16 + e % (TT * 16);
+  }
+  const uint32_t wq_off = (uint32_t)rg * Kc * WChunk<FMT>::QPC * 64 + lane;
+  const uint32_t wd_off = (uint32_t)rg * Kc * 16 + li;
+  u4v areg[D][APT];
+  float xreg[D][XPT];
+  WChunk<FMT> wr[D];
+#define RTQ_FWD_ISSUE(U, KC)                                                                          \
+  {                                                                                                   \
+    const int kcc = min((KC), kc1 - 1);                                                               \
+    _Pragma("unroll") for (int q = 0; q < APT; q++) areg[U][q] = XA[xa_off[q] + (uint32_t)kcc * 256];  \
+    _Pragma("unroll") for (int q = 0; q < XPT; q++) xreg[U][q] = a.xd[xd_off[q] + (uint32_t)kcc * 4 * a.Tp]; \
+    wr[U].load(WQ, wq_off + (uint32_t)kcc * WChunk<FMT>::QPC * 64, WD, wd_off + (uint32_t)kcc * 16);   \
+  }
+#define RTQ_FWD_BODY(U)                                                                                 \
+  {                                                                                                     \
+    const int kc = kb + (U);                                                                            \
+    if (kc < kc1) {                                                                                     \
+      const int buf = (kc - kc0) & 1;                                                                   \
+      _Pragma("unroll") for (int q = 0; q < APT; q++) {                                                 \
+        const int idx = tid + NTHR * q, tsl = idx >> 8, rem = idx & 255;                                \
+        sA[buf][tsl][rem >> 6][rem & 63] = areg[U][q];                                                  \
+      }                                                                                                 \
+      _Pragma("unroll") for (int q = 0; q < XPT; q++) {                                                 \
+        const int e = tid + NTHR * q;                                                                   \
+        if (e < TT * 64) sX[buf][e / (TT * 16)][e % (TT * 16)] = xreg[U][q];                            \
+      }                                                                                                 \
+      __syncthreads();                                                                                  \
+      RTQ_FWD_COMPUTE(wr[U], buf, kc)                                                                   \
+    }                                                                                                   \
+    RTQ_FWD_ISSUE(U, kc + D)                                                                            \
+  }
+#define RTQ_FWD_COMPUTE(WC, BUF, KC)                                                                   \
+  _Pragma("unroll") for (int j = 0; j < 4; j++) {                                                      \
+    const half8 bf = (WC).frag(j);                                                                     \
+    const float dw = h2f(hcomp((WC).d, j));                                                            \
+    _Pragma("unroll") for (int ts = 0; ts < TS; ts++) {                                                \
+      const int tt = wt * TS + ts;                                                                     \
+      const half8 af = __builtin_bit_cast(half8, sA[BUF][tt][j][lane]);                                \
+      const f4 xd = *reinterpret_cast<const f4*>(&sX[BUF][j][tt * 16 + 4 * g]);                        \
+      const f4 c = mfma_f16(af, bf, zero);                                                             \
+      if (DBG) {                                                                                       \
+        const int n = rg * 16 + li, b = (KC) * 4 + j, nb = a.K / 32;                                   \
+        _Pragma("unroll") for (int i = 0; i < 4; i++) {                                                \
+          const int t = (tg0 + tt) * 16 + 4 * g + i;                                                   \
+          if (t < a.T && n < a.N && b < nb) a.isums[((int64_t)t * a.N + n) * nb + b] = (int32_t)c[i]; \
+        }                                                                                              \
+      }                                                                                                \
+      _Pragma("unroll") for (int i = 0; i < 4; i++) acc[ts][i] = fmaf(c[i], dw * xd[i], acc[ts][i]);   \
+    }                                                                                                  \
+  }
+  static_assert(D == 4, "the pipeline below is written out for four slots");
+  if (kc0 < kc1) {
+    RTQ_FWD_ISSUE(0, kc0 + 0)
+    RTQ_FWD_ISSUE(1, kc0 + 1)
+    RTQ_FWD_ISSUE(2, kc0 + 2)
+    RTQ_FWD_ISSUE(3, kc0 + 3)
+    for (int kb = kc0; kb < kc1; kb += D) {
+      RTQ_FWD_BODY(0)
+      RTQ_FWD_BODY(1)
+      RTQ_FWD_BODY(2)
+      RTQ_FWD_BODY(3)
+    }
+  }
+#undef RTQ_FWD_BODY
+#undef RTQ_FWD_COMPUTE
+#undef RTQ_FWD_ISSUE
+
+  // epilogue: y = acc (+ bias) (+ s * h.B^T), in the order of src/linear.rs:76-90
+  const bool split = gridDim.z > 1;
+  const bool lead = blockIdx.z == 0;
+  const int n = rg * 16 + li;
+  const int nc = min(n, a.N - 1);
+#pragma unroll
+  for (int ts = 0; ts < TS; ts++) {
+    const int tt = wt * TS + ts;
+    f4 lacc = zero;
+    if (a.h && lead) {
+      const int trow = (tg0 + tt) * 16 + li;
+      const int trc = min(trow, a.T - 1);
+      for (int j0 = 0; j0 < a.r; j0 += 16) {
+        float hv[4], bv[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int j = j0 + 4 * u + g, jc = min(j, a.r - 1);
+          const float hx = a.h[(int64_t)trc * a.r + jc], bx = a.lb[(int64_t)nc * a.r + jc];
+          hv[u] = (trow < a.T && j < a.r) ? hx : 0.0f;
+          bv[u] = (n < a.N && j < a.r) ? bx : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) lacc = mfma_f32(hv[u], bv[u], lacc);
+      }
+    }
+    if (n < a.N) {
+      const float bias = (a.bias && lead) ? a.bias[n] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int t = (tg0 + tt) * 16 + 4 * g + i;
+        if (t < a.T) {
+          float v = acc[ts][i];
+          if (a.bias && lead) v = v + bias;
+          if (a.h && lead) v = v + a.s * lacc[i];
+          if (split)
+            atomicAdd(&a.y[(int64_t)t * a.N + n], v);
+          else
+            a.y[(int64_t)t * a.N + n] = v;
+        }
+      }
+    }
+  }
+}
+
+// wide: 4 waves (2 token x 2 row), tile 64 tokens x 32 rows;  skinny: 4 waves along rows, tile 16 x 64
+#define RTQ_FWD(NAME, FMT, WT, WN, TS, DBG)                                    \
+  extern "C" __global__ __launch_bounds__(64 * WT * WN) void NAME(FwdArgs a) { \
+    fwd_q32<FMT, WT, WN, TS, 4, DBG>(a);                                       \
+  }
+RTQ_FWD(rtq_fwd_q4_0_w, FMT_Q4_0, 2, 2, 2, false)
+RTQ_FWD(rtq_fwd_q4_0_s, FMT_Q4_0, 1, 4, 1, false)
+RTQ_FWD(rtq_fwd_q8_0_w, FMT_Q8_0, 2, 2, 2, false)
+RTQ_FWD(rtq_fwd_q8_0_s, FMT_Q8_0, 1, 4, 1, false)
+RTQ_FWD(rtq_fwd_q4_0_w_isums, FMT_Q4_0, 2, 2, 2, true)
+RTQ_FWD(rtq_fwd_q4_0_s_isums, FMT_Q4_0, 1, 4, 1, true)
+RTQ_FWD(rtq_fwd_q8_0_w_isums, FMT_Q8_0, 2, 2, 2, true)
+RTQ_FWD(rtq_fwd_q8_0_s_isums, FMT_Q8_0, 1, 4, 1, true)
+
+// ============================================================== backward: h and g (LoRA)
+extern "C" __global__ __launch_bounds__(512) void rtq_lora_hg(HGArgs a) {
+  __shared__ float red[9 * 256];
+  if (a.zero_dx) clear_rows(a.zero_dx, (int64_t)a.T * a.K);
+  const int t0 = blockIdx.x * 16;
+  const bool is_g = blockIdx.y == 1;
+  const float* S = is_g ? a.dy : a.x;
+  const float* Bm = is_g ? a.B : a.A;
+  const int klen = is_g ? a.N : a.K;
+  for (int j0 = 0; j0 < a.r; j0 += 16) {
+    skinny_tile<8>(S, a.T, klen, Bm, a.r, is_g ? a.r : a.K, !is_g, klen, t0, j0, is_g ? a.s : 1.0f, red);
+    if (threadIdx.x < 256) {
+      const int t = t0 + (threadIdx.x >> 4), j = j0 + (threadIdx.x & 15);
+      if (t < a.T && j < a.r) (is_g ? a.g : a.h)[(int64_t)t * a.r + j] = red[8 * 256 + threadIdx.x];
+    }
+    __syncthreads();
+  }
+}
+
+// ============================================================== dx = dy . W
+// Workgroup: 8 waves, tile 64 tokens x 128 columns (one K chunk); wave (wt, wk) owns 32 tokens x
+// 32 columns (2 x 2 MFMA tiles).  Rows of W are split over blockIdx.z.  Per 32-row step the
+// workgroup stages, double buffered in LDS:
+//   * dy[64 x 32] as bf16 hi/lo A fragments (each thread loads one float4, splits it once);
+//   * W[32 x 128] dequantised to f32 (d*q, exact), split into bf16 hi/lo and stored transposed
+//     ([k][n]) so a lane reads its B fragment (8 consecutive rows of one column) in 16 bytes.
+// Next step's global loads are issued before the current step's MFMAs.
+// dx W staging: thread (wave w, lane) owns rows 2p, 2p+1 (p = lane & 15) of the 32-row step,
+// k-group gg = lane >> 4, block jb = w & 3 and half hh = w >> 2 (hh 0: elements 4gg..4gg+3,
+// hh 1: 16+4gg..16+4gg+3 of the block).  Per row it loads the four codes it needs and the scale.
+template <int FMT>
+struct DxW;
+
+template <>
+struct DxW<FMT_Q4_0> {
+  uint32_t q[2];
+  uint16_t d[2];
+  __device__ __forceinline__ void load(const DxArgs& a, int rg, int kc, int Kc, int li0, int gg, int jb, int hh) {
+    const uint32_t* Q = reinterpret_cast<const uint32_t*>(a.wq);
+    const uint32_t base = (uint32_t)(rg * Kc + kc);
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      q[r] = Q[(base * 64 + li0 + r + 16 * gg) * 4 + jb];
+      d[r] = a.wd[(base * 16 + li0 + r) * 4 + jb];
+    }
+    (void)hh;
+  }
+  __device__ __forceinline__ void codes(int hh, float c[2][4]) const {
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+      for (int s = 0; s < 4; s++) c[r][s] = (float)((int)((q[r] >> (8 * s + 4 * hh)) & 0xf) - 8);
+  }
+};
+
+template <>
+struct DxW<FMT_Q8_0> {
+  uint32_t q[2];
+  uint16_t d[2];
+  __device__ __forceinline__ void load(const DxArgs& a, int rg, int kc, int Kc, int li0, int gg, int jb, int hh) {
+    const uint32_t* Q = reinterpret_cast<const uint32_t*>(a.wq);
+    const uint32_t base = (uint32_t)(rg * Kc + kc);
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      q[r] = Q[(((base * 2 + (jb >> 1)) * 64 + li0 + r + 16 * gg) * 2 + (jb & 1)) * 2 + hh];
+      d[r] = a.wd[(base * 16 + li0 + r) * 4 + jb];
+    }
+  }
+  __device__ __forceinline__ void codes(int hh, float c[2][4]) const {
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+      for (int s = 0; s < 4; s++) c[r][s] = (float)(int8_t)((q[r] >> (8 * s)) & 0xff);
+    (void)hh;
+  }
+};
+
+template <int FMT, int D>
+__device__ __forceinline__ void dx_q32(const DxArgs& a) {
+  __shared__ u4v sA[2][4][2][64];                                   // [buf][tile][hi/lo][lane]
+  __shared__ __attribute__((aligned(16))) __bf16 sW[2][2][128][40];   // [buf][hi/lo][k][n]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
+  const int wt = w >> 2, wk = w & 3;
+  const int kc = blockIdx.x, Kc = a.Kp / 128;
+  const int t0 = blockIdx.y * 64;
+  const int n0 = blockIdx.z * a.n_per_split;
+  const int n1 = min(n0 + a.n_per_split, a.Np);
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
   f4 acc[2][2];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
-#pragma unroll
-    for (int jn = 0; jn < 2; jn++) acc[i][jn] = zero;
+  for (int i = 0; i < 2; i++) acc[i][0] = acc[i][1] = zero;
 
-  const uint4* XA = reinterpret_cast<const uint4*>(a.xa);
-  for (int kc = 0; kc < Kc; ++kc) {
-    WChunk<FMT> wc[2];
-    uint2 wd[2];
+  // loader roles: dy: token tl = tid >> 3, float4 q4 = tid & 7;  W: see DxW
+  const int tl = tid >> 3, q4 = tid & 7;
+  const int trow = t0 + tl, trc = min(trow, a.T - 1);
+  const bool tin = trow < a.T;
+  const int wp = lane & 15, wgg = lane >> 4, jb = w & 3, hh = w >> 2;  // W staging roles
+  const int rgi = wp >> 3, li0 = (2 * wp) & 15;
+  const bool dy_vec = (a.N & 3) == 0;
+  // D-deep register ring of (dy float4, W codes + scale) per 32-row step; loads unconditional
+  // (row index clamped), so the wait for slot u covers only loads issued D steps earlier.
+  float dyr[D][4];
+  DxW<FMT> wr[D];
+#define RTQ_DX_ISSUE(U, N_)                                                                            \
+  {                                                                                                    \
+    const int ns = min((N_), n1 - 32);                                                                 \
+    const int nn = ns + 4 * q4;                                                                        \
+    if (dy_vec) {                                                                                      \
+      const f4 v = *reinterpret_cast<const f4*>(a.dy + (int64_t)trc * a.N + min(nn, a.N - 4)); \
+      dyr[U][0] = v.x; dyr[U][1] = v.y; dyr[U][2] = v.z; dyr[U][3] = v.w;                              \
+    } else {                                                                                           \
+      _Pragma("unroll") for (int c = 0; c < 4; c++) dyr[U][c] = a.dy[(int64_t)trc * a.N + min(nn + c, a.N - 1)]; \
+    }                                                                                                  \
+    _Pragma("unroll") for (int c = 0; c < 4; c++) dyr[U][c] = (tin && nn + c < a.N) ? dyr[U][c] : 0.0f; \
+    wr[U].load(a, (ns >> 4) + rgi, kc, Kc, li0, wgg, jb, hh);                                         \
+  }
+  auto stage_compute = [&](const float (&dyv)[4], const DxW<FMT>& wv, int buf) {
+    {  // stage dy: A fragment tile tl>>4, lane (tl&15) + 16*(q4>>1), slots 4*(q4&1) .. +3
+      __bf16 hi[4], lo[4];
 #pragma unroll
-    for (int ns = 0; ns < 2; ns++) {
-      wc[ns].load(a, rg0 + ns, kc, Kc, lane);
-      wd[ns] = reinterpret_cast<const uint2*>(a.wd)[(int64_t)(rg0 + ns) * Kc * 16 + kc * 16 + li];
+      for (int c = 0; c < 4; c++) split_bf16(dyv[c], hi[c], lo[c]);
+      u2v hv, lv;
+      hv.x = (uint32_t)__builtin_bit_cast(uint16_t, hi[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, hi[1]) << 16);
+      hv.y = (uint32_t)__builtin_bit_cast(uint16_t, hi[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, hi[3]) << 16);
+      lv.x = (uint32_t)__builtin_bit_cast(uint16_t, lo[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, lo[1]) << 16);
+      lv.y = (uint32_t)__builtin_bit_cast(uint16_t, lo[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, lo[3]) << 16);
+      const int fl = (tl & 15) + 16 * (q4 >> 1);
+      reinterpret_cast<u2v*>(&sA[buf][tl >> 4][0][fl])[q4 & 1] = hv;
+      reinterpret_cast<u2v*>(&sA[buf][tl >> 4][1][fl])[q4 & 1] = lv;
     }
-    uint4 xa[2][4];
-    f4 xd[2][4];
+    {  // stage W: rows 2p, 2p+1 packed into one 32-bit LDS word per column (hi and lo planes)
+      float c[2][4];
+      wv.codes(hh, c);
+      const float d0 = h2f(wv.d[0]), d1 = h2f(wv.d[1]);
+      const int kbase = 32 * jb + 16 * hh + 4 * wgg;
 #pragma unroll
-    for (int ts = 0; ts < 2; ts++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        xa[ts][j] = XA[((int64_t)((tg0 + ts) * Kc + kc) * 4 + j) * 64 + lane];
-        xd[ts][j] = *reinterpret_cast<const f4*>(a.xd + (int64_t)(kc * 4 + j) * a.Tp + (tg0 + ts) * 16 + 4 * g);
+      for (int e = 0; e < 4; e++) {
+        __bf16 h0, l0, h1, l1;
+        split_bf16(c[0][e] * d0, h0, l0);  // d * q is exact in f32
+        split_bf16(c[1][e] * d1, h1, l1);
+        const uint32_t hp = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        const uint32_t lp = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+        *reinterpret_cast<uint32_t*>(&sW[buf][0][kbase + e][2 * wp]) = hp;
+        *reinterpret_cast<uint32_t*>(&sW[buf][1][kbase + e][2 * wp]) = lp;
       }
+    }
+    __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int ts = 0; ts < 2; ts++) {
+      const bf8 ah = __builtin_bit_cast(bf8, sA[buf][wt * 2 + ts][0][lane]);
+      const bf8 al = __builtin_bit_cast(bf8, sA[buf][wt * 2 + ts][1][lane]);
 #pragma unroll
-      for (int ns = 0; ns < 2; ns++) {
-        const half8 bf = wc[ns].frag(j);
-        const float dw = h2f(hcomp(wd[ns], j));
-#pragma unroll
-        for (int ts = 0; ts < 2; ts++) {
-          const f4 c = mfma_f16(as_half8(xa[ts][j]), bf, zero);
-          if (DBG) {
-            const int n = (rg0 + ns) * 16 + li, b = kc * 4 + j, nb = a.K / 32;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-              const int t = (tg0 + ts) * 16 + 4 * g + i;
-              if (t < a.T && n < a.N && b < nb) a.isums[((int64_t)t * a.N + n) * nb + b] = (int32_t)c[i];
-            }
-          }
-#pragma unroll
-          for (int i = 0; i < 4; i++) acc[ts][ns][i] = fmaf(c[i], dw * xd[ts][j][i], acc[ts][ns][i]);
-        }
+      for (int ks = 0; ks < 2; ks++) {
+        const int kl = wk * 32 + ks * 16 + li;
+        const bf8 bh = *reinterpret_cast<const bf8*>(&sW[buf][0][kl][8 * g]);
+        const bf8 bl = *reinterpret_cast<const bf8*>(&sW[buf][1][kl][8 * g]);
+        acc[ts][ks] = mfma_bf16(ah, bh, acc[ts][ks]);
+        acc[ts][ks] = mfma_bf16(al, bh, acc[ts][ks]);
+        acc[ts][ks] = mfma_bf16(ah, bl, acc[ts][ks]);
       }
+    }
+  };
+#define RTQ_DX_BODY(U)                                     \
+  {                                                        \
+    const int n = nb + 32 * (U);                           \
+    if (n < n1) stage_compute(dyr[U], wr[U], ((n - n0) >> 5) & 1); \
+    RTQ_DX_ISSUE(U, n + 32 * D)                            \
+  }
+  static_assert(D == 3, "the pipeline below is written out for three slots");
+  if (n0 < n1) {
+    RTQ_DX_ISSUE(0, n0)
+    RTQ_DX_ISSUE(1, n0 + 32)
+    RTQ_DX_ISSUE(2, n0 + 64)
+    for (int nb = n0; nb < n1; nb += 32 * D) {
+      RTQ_DX_BODY(0)
+      RTQ_DX_BODY(1)
+      RTQ_DX_BODY(2)
     }
   }
-
-  // epilogue: y = acc (+ bias) (+ s * h.B^T), in the order of src/linear.rs:76-90
+#undef RTQ_DX_BODY
+#undef RTQ_DX_ISSUE
+  const bool split = gridDim.z > 1;
 #pragma unroll
   for (int ts = 0; ts < 2; ts++)
 #pragma unroll
-    for (int ns = 0; ns < 2; ns++) {
-      const int n = (rg0 + ns) * 16 + li;
-      f4 lacc = zero;
-      if (a.h) {
-        const int trow = (tg0 + ts) * 16 + li;
-        for (int j0 = 0; j0 < a.r; j0 += 4) {
-          const int j = j0 + g;
-          const float hv = (trow < a.T && j < a.r) ? a.h[(int64_t)trow * a.r + j] : 0.0f;
-          const float bv = (n < a.N && j < a.r) ? a.lb[(int64_t)n * a.r + j] : 0.0f;
-          lacc = mfma_f32(hv, bv, lacc);
-        }
-      }
-      if (n < a.N) {
-        const float bias = a.bias ? a.bias[n] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int t = (tg0 + ts) * 16 + 4 * g + i;
-          if (t < a.T) {
-            float v = acc[ts][ns][i];
-            if (a.bias) v = v + bias;
-            if (a.h) v = v + a.s * lacc[i];
-            a.y[(int64_t)t * a.N + n] = v;
-          }
-        }
-      }
-    }
-}
-
-extern "C" __global__ __launch_bounds__(256) void rtq_fwd_q4_0(FwdArgs a) { fwd_q32<FMT_Q4_0, false>(a); }
-extern "C" __global__ __launch_bounds__(256) void rtq_fwd_q8_0(FwdArgs a) { fwd_q32<FMT_Q8_0, false>(a); }
-extern "C" __global__ __launch_bounds__(256) void rtq_fwd_q4_0_isums(FwdArgs a) { fwd_q32<FMT_Q4_0, true>(a); }
-extern "C" __global__ __launch_bounds__(256) void rtq_fwd_q8_0_isums(FwdArgs a) { fwd_q32<FMT_Q8_0, true>(a); }
-
-// ============================================================== backward: dy preparation
-// One workgroup per (padded) token row: absmax -> exponent e with absmax*2^e in [2^14, 2^15),
-// f16 fragments of dy*2^e (exact scaling, one RNE rounding), einv = 2^-e.
-extern "C" __global__ __launch_bounds__(256) void rtq_dy_prep(DyPrepArgs a) {
-  __shared__ float red[4];
-  const int t = blockIdx.x, tid = threadIdx.x;
-  const bool valid = t < a.T;
-  if (valid && a.zero_dx)
-    for (int k = tid; k < a.K; k += 256) a.zero_dx[(int64_t)t * a.K + k] = 0.0f;
-  if (valid && a.zero_g)
-    for (int j = tid; j < a.r; j += 256) a.zero_g[(int64_t)t * a.r + j] = 0.0f;
-  const float* row = a.dy + (int64_t)t * a.N;
-  float m = 0.0f;
-  if (valid)
-    for (int n = tid; n < a.N; n += 256) m = fmaxf(m, fabsf(row[n]));
-  m = wave_max(m);
-  if ((tid & 63) == 0) red[tid >> 6] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  int e = 0;
-  if (m > 0.0f && m <= 3.4e38f) {
-    int ex;
-    frexpf(m, &ex);
-    e = 15 - ex;
-    e = e < -100 ? -100 : (e > 100 ? 100 : e);
-  }
-  const float sc = ldexpf(1.0f, e);
-  if (tid == 0) a.einv[t] = ldexpf(1.0f, -e);
-  const int ng = a.Np / 8;
-  uint4* out = reinterpret_cast<uint4*>(a.dy16) + (int64_t)(t >> 4) * (a.Np / 32) * 64;
-  for (int q = tid; q < ng; q += 256) {
-    const int n8 = q * 8;
-    _Float16 hv[8];
-#pragma unroll
-    for (int s = 0; s < 8; s++) {
-      const int n = n8 + s;
-      hv[s] = (_Float16)((valid && n < a.N) ? row[n] * sc : 0.0f);
-    }
-    half8 f = {hv[0], hv[1], hv[2], hv[3], hv[4], hv[5], hv[6], hv[7]};
-    const int nc = n8 >> 5, gg = (n8 & 31) >> 3;
-    out[nc * 64 + (t & 15) + 16 * gg] = __builtin_bit_cast(uint4, f);
-  }
-}
-
-// ============================================================== LoRA g = s * dy . B
-// One wave per (16 tokens, split of n, 16 adapter columns); f32 MFMA 16x16x4 over n; atomics.
-extern "C" __global__ __launch_bounds__(64) void rtq_lora_g(LoraGArgs a) {
-  const int lane = threadIdx.x, li = lane & 15, g = lane >> 4;
-  const int t0 = blockIdx.x * 16, j0 = blockIdx.z * 16;
-  const int n0 = blockIdx.y * a.n_per_split;
-  const int n1 = min(n0 + a.n_per_split, a.N);
-  const int trow = t0 + li, jcol = j0 + li;
-  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int n = n0; n < n1; n += 4) {
-    const int nn = n + g;
-    const float av = (trow < a.T && nn < n1) ? __fmul_rn(a.dy[(int64_t)trow * a.N + nn], a.s) : 0.0f;
-    const float bv = (jcol < a.r && nn < n1) ? a.lb[(int64_t)nn * a.r + jcol] : 0.0f;
-    acc = mfma_f32(av, bv, acc);
-  }
-  if (jcol < a.r)
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int t = t0 + 4 * g + i;
-      if (t < a.T) atomicAdd(&a.g[(int64_t)t * a.r + jcol], acc[i]);
-    }
-}
-
-// ============================================================== dx = dy . W (+ g . A)
-// Workgroup tile 64 tokens x 128 columns (one K chunk), rows of W split over blockIdx.z.
-// Per 32-row step the 32 x 128 weight slab is dequantised to f16 (d*q, one rounding) and
-// stored transposed in LDS ([k][n]) so each lane reads its B fragment (8 consecutive rows of
-// one column) with one 16-byte LDS read; dy fragments come straight from global memory.
-template <int FMT>
-__device__ __forceinline__ void dx_dequant_store(const DxArgs& a, _Float16 (*wt)[40], int rg, int kc, int Kc,
-                                                 int tid);
-
-template <>
-__device__ __forceinline__ void dx_dequant_store<FMT_Q4_0>(const DxArgs& a, _Float16 (*wt)[40], int rg0, int kc,
-                                                           int Kc, int tid) {
-  const int rgi = tid >> 7, ll = (tid & 127) >> 1, part = tid & 1;
-  const int rg = rg0 + rgi;
-  const uint2 q = reinterpret_cast<const uint2*>(a.wq)[((int64_t)(rg * Kc + kc) * 64 + ll) * 2 + part];
-  const uint32_t d2 = reinterpret_cast<const uint32_t*>(a.wd)[((int64_t)(rg * Kc + kc) * 16 + (ll & 15)) * 2 + part];
-  const int nl = rgi * 16 + (ll & 15), gg = ll >> 4;
-#pragma unroll
-  for (int jj = 0; jj < 2; jj++) {
-    const int j = 2 * part + jj;
-    const uint32_t w = jj ? q.y : q.x;
-    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(jj ? (d2 >> 16) : (d2 & 0xffffu)));
-    const half8 c = q4_0_frag(w);
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-      wt[32 * j + 4 * gg + s][nl] = c[s] * d;
-      wt[32 * j + 16 + 4 * gg + s][nl] = c[4 + s] * d;
-    }
-  }
-}
-
-template <>
-__device__ __forceinline__ void dx_dequant_store<FMT_Q8_0>(const DxArgs& a, _Float16 (*wt)[40], int rg0, int kc,
-                                                           int Kc, int tid) {
-  const int rgi = tid >> 7, ll = (tid & 127) >> 1, part = tid & 1;
-  const int rg = rg0 + rgi;
-  const uint4 q = reinterpret_cast<const uint4*>(a.wq)[(int64_t)(rg * Kc + kc) * 128 + part * 64 + ll];
-  const uint32_t d2 = reinterpret_cast<const uint32_t*>(a.wd)[((int64_t)(rg * Kc + kc) * 16 + (ll & 15)) * 2 + part];
-  const int nl = rgi * 16 + (ll & 15), gg = ll >> 4;
-#pragma unroll
-  for (int jj = 0; jj < 2; jj++) {
-    const int j = 2 * part + jj;
-    const half8 c = jj ? q8_frag(q.z, q.w) : q8_frag(q.x, q.y);
-    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(jj ? (d2 >> 16) : (d2 & 0xffffu)));
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-      wt[32 * j + 4 * gg + s][nl] = c[s] * d;
-      wt[32 * j + 16 + 4 * gg + s][nl] = c[4 + s] * d;
-    }
-  }
-}
-
-template <int FMT>
-__device__ __forceinline__ void dx_q32(const DxArgs& a) {
-  __shared__ __attribute__((aligned(16))) _Float16 wt[128][40];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
-  const int kc = blockIdx.x, Kc = a.Kp / 128;
-  const int tg0 = (blockIdx.y * 64 + (w >> 1) * 32) >> 4;
-  const int kw = (w & 1) * 64;
-  const int n0 = blockIdx.z * a.n_per_split;
-  const int n1 = min(n0 + a.n_per_split, a.Np);
-  const int Nc = a.Np / 32;
-  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f4 acc[2][4];
-#pragma unroll
-  for (int i = 0; i < 2; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = zero;
-  const uint4* DY = reinterpret_cast<const uint4*>(a.dy16);
-  for (int n = n0; n < n1; n += 32) {
-    __syncthreads();
-    dx_dequant_store<FMT>(a, wt, n >> 4, kc, Kc, tid);
-    __syncthreads();
-    uint4 af[2];
-#pragma unroll
-    for (int ts = 0; ts < 2; ts++) af[ts] = DY[((int64_t)(tg0 + ts) * Nc + (n >> 5)) * 64 + lane];
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++) {
-      const half8 bf = *reinterpret_cast<const half8*>(&wt[kw + ks * 16 + li][8 * g]);
-#pragma unroll
-      for (int ts = 0; ts < 2; ts++) acc[ts][ks] = mfma_f16(as_half8(af[ts]), bf, acc[ts][ks]);
-    }
-  }
-  const bool lora = a.g != nullptr && blockIdx.z == 0;
-#pragma unroll
-  for (int ts = 0; ts < 2; ts++)
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++) {
-      const int k = kc * 128 + kw + ks * 16 + li;
-      f4 lacc = zero;
-      if (lora) {
-        const int trow = (tg0 + ts) * 16 + li;
-        for (int j0 = 0; j0 < a.r; j0 += 4) {
-          const int j = j0 + g;
-          const float gv = (trow < a.T && j < a.r) ? a.g[(int64_t)trow * a.r + j] : 0.0f;
-          const float av = (k < a.K && j < a.r) ? a.la[(int64_t)j * a.K + k] : 0.0f;
-          lacc = mfma_f32(gv, av, lacc);
-        }
-      }
+    for (int ks = 0; ks < 2; ks++) {
+      const int k = kc * 128 + wk * 32 + ks * 16 + li;
       if (k < a.K)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int t = (tg0 + ts) * 16 + 4 * g + i;
+          const int t = t0 + wt * 32 + ts * 16 + 4 * g + i;
           if (t < a.T) {
-            float v = acc[ts][ks][i] * a.einv[t];
-            if (lora) v += lacc[i];
-            atomicAdd(&a.dx[(int64_t)t * a.K + k], v);
+            float* p = &a.dx[(int64_t)t * a.K + k];
+            if (split)
+              atomicAdd(p, acc[ts][ks][i]);
+            else
+              *p += acc[ts][ks][i];
           }
         }
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void rtq_dx_q4_0(DxArgs a) { dx_q32<FMT_Q4_0>(a); }
-extern "C" __global__ __launch_bounds__(256) void rtq_dx_q8_0(DxArgs a) { dx_q32<FMT_Q8_0>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dx_q4_0(DxArgs a) { dx_q32<FMT_Q4_0, 3>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dx_q8_0(DxArgs a) { dx_q32<FMT_Q8_0, 3>(a); }
 
-// ============================================================== LoRA gradients
+// ============================================================== LoRA gradients (+ dx += g.A)
 // gb[n][j] += sum_t (s*dy[t][n]) h[t][j]   (matmul_tn_acc, src/linear.rs:109)
 // ga[j][k] += sum_t g[t][j] x[t][k]        (matmul_tn_acc, src/linear.rs:113)
-// One wave per 16x16 output tile, f32 MFMA 16x16x4 over t; each tile has a single writer.
-extern "C" __global__ __launch_bounds__(64) void rtq_lora_grads(LoraGradArgs a) {
-  const int lane = threadIdx.x, li = lane & 15, g = lane >> 4;
+// dx[t][k] += sum_j g[t][j] A[j][k]        (src/linear.rs:115-118)
+// gb / ga: one 16x16 tile per workgroup, the 4 waves split t and reduce in LDS (single writer);
+// dx: four 16x16 tiles per workgroup, one per wave, K = r.
+extern "C" __global__ __launch_bounds__(1024) void rtq_lora_grads(LoraGradArgs a) {
+  __shared__ float red[16 * 256];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
   const int jt = (a.r + 15) / 16;
+  int b = blockIdx.x;
   f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  if ((int)blockIdx.x < a.n_tiles_gb) {
-    const int nt = blockIdx.x / jt, jtile = blockIdx.x % jt;
-    const int nrow = nt * 16 + li, jcol = jtile * 16 + li;
-    for (int t0 = 0; t0 < a.T; t0 += 4) {
-      const int t = t0 + g;
-      const float av = (nrow < a.N && t < a.T) ? __fmul_rn(a.dy[(int64_t)t * a.N + nrow], a.s) : 0.0f;
-      const float bv = (jcol < a.r && t < a.T) ? a.h[(int64_t)t * a.r + jcol] : 0.0f;
-      acc = mfma_f32(av, bv, acc);
-    }
-    if (jcol < a.r)
+  const int tper = ((a.T + 15) / 16 + 3) / 4 * 4;  // t per wave, multiple of 4
+  const int tb = w * tper, te = min(tb + tper, a.T);
+  if (b < a.n_gb + a.n_ga) {
+    const bool is_gb = b < a.n_gb;
+    if (!is_gb) b -= a.n_gb;
+    const int rt = b / jt, ct = b % jt;
+    // gb: rows n (tile rt), cols j (tile ct);  ga: rows j (tile ct), cols k (tile rt)
+    const int rrow = is_gb ? rt * 16 + li : ct * 16 + li;
+    const int ccol = is_gb ? ct * 16 + li : rt * 16 + li;
+    for (int t = tb; t < te; t += 16) {
+      float av[4], bv[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int n = nt * 16 + 4 * g + i;
-        if (n < a.N) a.gb[(int64_t)n * a.r + jcol] += acc[i];
+      for (int u = 0; u < 4; u++) {
+        const int tt = t + 4 * u + g, tc = min(tt, a.T - 1);
+        if (is_gb) {
+          const float x = a.dy[(int64_t)tc * a.N + min(rrow, a.N - 1)];
+          const float y = a.h[(int64_t)tc * a.r + min(ccol, a.r - 1)];
+          av[u] = (tt < te && rrow < a.N) ? __fmul_rn(x, a.s) : 0.0f;
+          bv[u] = (tt < te && ccol < a.r) ? y : 0.0f;
+        } else {
+          const float x = a.g[(int64_t)tc * a.r + min(rrow, a.r - 1)];
+          const float y = a.x[(int64_t)tc * a.K + min(ccol, a.K - 1)];
+          av[u] = (tt < te && rrow < a.r) ? x : 0.0f;
+          bv[u] = (tt < te && ccol < a.K) ? y : 0.0f;
+        }
       }
-  } else {
-    const int b = blockIdx.x - a.n_tiles_gb;
-    const int jtile = b % jt, kt = b / jt;
-    const int jrow = jtile * 16 + li, kcol = kt * 16 + li;
-    for (int t0 = 0; t0 < a.T; t0 += 4) {
-      const int t = t0 + g;
-      const float av = (jrow < a.r && t < a.T) ? a.g[(int64_t)t * a.r + jrow] : 0.0f;
-      const float bv = (kcol < a.K && t < a.T) ? a.x[(int64_t)t * a.K + kcol] : 0.0f;
-      acc = mfma_f32(av, bv, acc);
+#pragma unroll
+      for (int u = 0; u < 4; u++) acc = mfma_f32(av[u], bv[u], acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[w * 256 + (4 * g + i) * 16 + li] = acc[i];
+    __syncthreads();
+    if (threadIdx.x < 256) {
+      const int rl = threadIdx.x >> 4, cl = threadIdx.x & 15;
+      float s = 0.0f;
+#pragma unroll
+      for (int ww = 0; ww < 16; ww++) s += red[ww * 256 + threadIdx.x];
+      if (is_gb) {
+        const int n = rt * 16 + rl, j = ct * 16 + cl;
+        if (n < a.N && j < a.r) a.gb[(int64_t)n * a.r + j] += s;
+      } else {
+        const int j = ct * 16 + rl, k = rt * 16 + cl;
+        if (j < a.r && k < a.K) a.ga[(int64_t)j * a.K + k] += s;
+      }
+    }
+  } else if (a.dx) {
+    // dx tiles: tile index = (b - n_gb - n_ga) * 16 + w over (t-tiles x k-tiles)
+    const int tile = (b - a.n_gb - a.n_ga) * 16 + w;
+    const int ktiles = (a.K + 15) / 16;
+    const int tt = tile / ktiles, kt = tile % ktiles;
+    if (tt * 16 >= a.T) return;  // whole wave exits together; no barriers in this branch
+    const int trow = tt * 16 + li, kcol = kt * 16 + li;
+    for (int j0 = 0; j0 < a.r; j0 += 16) {
+      float gv[4], av[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int j = j0 + 4 * u + g, jc = min(j, a.r - 1);
+        const float x = a.g[(int64_t)min(trow, a.T - 1) * a.r + jc];
+        const float y = a.la[(int64_t)jc * a.K + min(kcol, a.K - 1)];
+        gv[u] = (trow < a.T && j < a.r) ? x : 0.0f;
+        av[u] = (kcol < a.K && j < a.r) ? y : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) acc = mfma_f32(gv[u], av[u], acc);
     }
     if (kcol < a.K)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const int j = jtile * 16 + 4 * g + i;
-        if (j < a.r) a.ga[(int64_t)j * a.K + kcol] += acc[i];
+        const int t = tt * 16 + 4 * g + i;
+        if (t < a.T) a.dx[(int64_t)t * a.K + kcol] += acc[i];
       }
   }
 }
@@ -516,7 +754,7 @@ extern "C" __global__ __launch_bounds__(256) void rtq_rows_q4_0(RowArgs a) {
   if (idx >= (int64_t)a.count * nb) return;
   const int rl = (int)(idx / nb), b = (int)(idx % nb);
   const int n = a.r0 + rl, rg = n >> 4, li = n & 15, kc = b >> 2, j = b & 3;
-  const uint4* q = reinterpret_cast<const uint4*>(a.wq) + (int64_t)(rg * Kc + kc) * 64;
+  const u4v* q = reinterpret_cast<const u4v*>(a.wq) + (int64_t)(rg * Kc + kc) * 64;
   const float d = h2f(a.wd[((int64_t)(rg * Kc + kc) * 16 + li) * 4 + j]);
   float* out = a.out + (int64_t)rl * a.K + b * 32;
 #pragma unroll
@@ -537,12 +775,12 @@ extern "C" __global__ __launch_bounds__(256) void rtq_rows_q8_0(RowArgs a) {
   if (idx >= (int64_t)a.count * nb) return;
   const int rl = (int)(idx / nb), b = (int)(idx % nb);
   const int n = a.r0 + rl, rg = n >> 4, li = n & 15, kc = b >> 2, j = b & 3;
-  const uint4* q = reinterpret_cast<const uint4*>(a.wq) + (int64_t)(rg * Kc + kc) * 128 + (j >> 1) * 64;
+  const u4v* q = reinterpret_cast<const u4v*>(a.wq) + (int64_t)(rg * Kc + kc) * 128 + (j >> 1) * 64;
   const float d = h2f(a.wd[((int64_t)(rg * Kc + kc) * 16 + li) * 4 + j]);
   float* out = a.out + (int64_t)rl * a.K + b * 32;
 #pragma unroll
   for (int gg = 0; gg < 4; gg++) {
-    const uint4 v = q[li + 16 * gg];
+    const u4v v = q[li + 16 * gg];
     const uint32_t lo = (j & 1) ? v.z : v.x, hi = (j & 1) ? v.w : v.y;
 #pragma unroll
     for (int s = 0; s < 4; s++) {

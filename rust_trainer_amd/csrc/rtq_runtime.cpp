@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -105,14 +106,16 @@ float f16_bits_to_f32(uint16_t h) {
 
 enum Kid {
   K_FILL,
-  K_QUANT_Q8_0,
-  K_LORA_DOWN,
-  K_FWD_Q4_0,
-  K_FWD_Q8_0,
-  K_FWD_Q4_0_ISUMS,
-  K_FWD_Q8_0_ISUMS,
-  K_DY_PREP,
-  K_LORA_G,
+  K_ACT_PREP,
+  K_FWD_Q4_0_W,
+  K_FWD_Q4_0_S,
+  K_FWD_Q8_0_W,
+  K_FWD_Q8_0_S,
+  K_FWD_Q4_0_W_ISUMS,
+  K_FWD_Q4_0_S_ISUMS,
+  K_FWD_Q8_0_W_ISUMS,
+  K_FWD_Q8_0_S_ISUMS,
+  K_LORA_HG,
   K_DX_Q4_0,
   K_DX_Q8_0,
   K_LORA_GRADS,
@@ -121,9 +124,10 @@ enum Kid {
   K_COUNT
 };
 const char* kKernelNames[K_COUNT] = {
-    "rtq_fill_zero", "rtq_quant_q8_0", "rtq_lora_down", "rtq_fwd_q4_0", "rtq_fwd_q8_0", "rtq_fwd_q4_0_isums",
-    "rtq_fwd_q8_0_isums", "rtq_dy_prep", "rtq_lora_g", "rtq_dx_q4_0", "rtq_dx_q8_0", "rtq_lora_grads",
-    "rtq_rows_q4_0", "rtq_rows_q8_0"};
+    "rtq_fill_zero",        "rtq_act_prep_q8_0",    "rtq_fwd_q4_0_w",       "rtq_fwd_q4_0_s",
+    "rtq_fwd_q8_0_w",       "rtq_fwd_q8_0_s",       "rtq_fwd_q4_0_w_isums", "rtq_fwd_q4_0_s_isums",
+    "rtq_fwd_q8_0_w_isums", "rtq_fwd_q8_0_s_isums", "rtq_lora_hg",          "rtq_dx_q4_0",
+    "rtq_dx_q8_0",          "rtq_lora_grads",       "rtq_rows_q4_0",        "rtq_rows_q8_0"};
 
 struct TimedLaunch {
   int kid;
@@ -145,6 +149,7 @@ struct rtq_ctx {
   int timing_only = -1;  // -1: every kernel
   std::vector<TimedLaunch> pending;
   std::vector<hipEvent_t> free_events;
+  int dx_splits = 0;  // 0: automatic; RTQ_DX_SPLITS overrides (tuning)
   int64_t t_launches[K_COUNT] = {};
   double t_ms[K_COUNT] = {};
 };
@@ -158,7 +163,6 @@ struct rtq_weight {
   void* dmem = nullptr;
   void* wq = nullptr;
   uint16_t* wd = nullptr;
-  void* wx = nullptr;
 };
 
 namespace {
@@ -197,6 +201,13 @@ rtq_status launch(rtq_ctx* c, int kid, dim3 grid, dim3 block, hipStream_t s, con
     c->pending.push_back({kid, ea, eb});
   }
   return RTQ_OK;
+}
+
+rtq_status fill_zero(rtq_ctx* c, float* p, int64_t n, hipStream_t s) {
+  if (n <= 0) return RTQ_OK;
+  FillArgs a{p, n};
+  const int64_t blocks = std::min<int64_t>(cdiv(n, 256), 2048);
+  return launch(c, K_FILL, dim3((unsigned)blocks), dim3(256), s, a);
 }
 
 // ------------------------------------------------------------------ workspace
@@ -242,39 +253,27 @@ int64_t block_bytes(int type) {
 }
 
 // ------------------------------------------------------------------ per-call sizes
+// Forward: tokens padded to 16 (skinny kernel, t <= 16) or 64 (wide kernel).
 struct FwdPlan {
   int64_t T, Tp;
-  size_t xa_bytes, xd_floats, h_floats;
+  bool skinny;
+  size_t xq_bytes, xd_floats, h_floats;
 };
 
 FwdPlan fwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
   FwdPlan p;
   p.T = t;
-  p.Tp = roundup(std::max<int64_t>(t, 1), RTQ_T_PAD);
-  p.xa_bytes = (size_t)p.Tp * w->Kp * 2;  // one f16 per element
+  p.skinny = t <= 16;
+  p.Tp = roundup(std::max<int64_t>(t, 1), p.skinny ? 16 : 64);
+  p.xq_bytes = (size_t)p.Tp * w->Kp * 2;  // one f16 per element
   p.xd_floats = (size_t)(w->Kp / 32) * p.Tp;
   p.h_floats = (size_t)t * std::max<int64_t>(r, 0);
   return p;
 }
 
-size_t fwd_ws_bytes(const FwdPlan& p) { return p.xa_bytes + p.xd_floats * 4 + p.h_floats * 4 + 4 * 256; }
+size_t fwd_ws_bytes(const FwdPlan& p) { return p.xq_bytes + p.xd_floats * 4 + p.h_floats * 4 + 4 * 256; }
 
-struct BwdPlan {
-  int64_t T, Tp;
-  size_t dy16_bytes, h_floats, g_floats;
-};
-
-BwdPlan bwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
-  BwdPlan p;
-  p.T = t;
-  p.Tp = roundup(std::max<int64_t>(t, 1), RTQ_T_PAD);
-  p.dy16_bytes = (size_t)p.Tp * w->Np * 2;
-  p.h_floats = (size_t)t * std::max<int64_t>(r, 0);
-  p.g_floats = p.h_floats;
-  return p;
-}
-
-size_t bwd_ws_bytes(const BwdPlan& p) { return p.dy16_bytes + (size_t)p.Tp * 4 + 2 * p.h_floats * 4 + 4 * 256; }
+size_t bwd_ws_bytes(int64_t t, int64_t r) { return (size_t)(2 * t * std::max<int64_t>(r, 0)) * 4 + 4 * 256; }
 
 // ------------------------------------------------------------------ enqueue: forward
 // y = x.W^T (+bias) (+ s h.B^T);  isums (debug) receives the per-block integer sums.
@@ -284,31 +283,39 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
   FwdPlan p = fwd_plan(w, t, lora ? r : 0);
-  void* xa = ar.take<char>(p.xa_bytes);
+  void* xq = ar.take<char>(p.xq_bytes);
   float* xd = ar.take<float>(p.xd_floats);
   float* h = lora ? ar.take<float>(p.h_floats) : nullptr;
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
-
-  QuantArgs qa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xa, xd, nullptr};
-  const int64_t qthreads = p.Tp * (w->Kp / 32);
-  RTQ_TRY(launch(c, K_QUANT_Q8_0, dim3((unsigned)cdiv(qthreads, 256)), dim3(256), st, qa));
-  if (lora) {
-    LoraDownArgs ld{x, la, (int)t, (int)w->cols, (int)r, h};
-    RTQ_TRY(launch(c, K_LORA_DOWN, dim3((unsigned)cdiv(t, 4)), dim3(256), st, ld));
+  const int64_t Kc = w->Kp / 128;
+  const int64_t rows_per_wg = p.skinny ? 64 : 32;
+  const int64_t tiles = (w->Np / rows_per_wg) * (p.Tp / (p.skinny ? 16 : 64));
+  // split K when the output alone gives too few workgroups (accumulate with atomics)
+  int64_t ks = 1;
+  if (!isums) {
+    if (p.skinny)
+      ks = std::min<int64_t>(Kc, std::max<int64_t>(1, cdiv(2 * c->cu_count, tiles)));
+    else if (tiles < c->cu_count / 2)
+      ks = std::min<int64_t>(std::min<int64_t>(Kc, 4), cdiv(c->cu_count, tiles));
   }
+  const int64_t kcps = cdiv(Kc, ks);
+  ks = cdiv(Kc, kcps);
+
+  ActArgs aa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xq, xd, lora ? la : nullptr, (int)r, h,
+             ks > 1 ? y : nullptr, (int)w->rows};
+  RTQ_TRY(launch(c, K_ACT_PREP, dim3((unsigned)(p.Tp / 16)), dim3(512), st, aa));
   FwdArgs fa{};
   fa.wq = w->wq;
   fa.wd = w->wd;
-  fa.wx = w->wx;
   fa.Np = (int)w->Np;
   fa.Kp = (int)w->Kp;
-  fa.xa = xa;
+  fa.xq = xq;
   fa.xd = xd;
-  fa.xb = nullptr;
   fa.Tp = (int)p.Tp;
   fa.T = (int)t;
   fa.N = (int)w->rows;
   fa.K = (int)w->cols;
+  fa.kc_per_split = (int)kcps;
   fa.y = y;
   fa.bias = bias;
   fa.h = h;
@@ -316,71 +323,50 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   fa.r = (int)r;
   fa.s = s;
   fa.isums = isums;
+  const bool q4 = w->type == RTQ_TYPE_Q4_0;
   int kid;
-  if (w->type == RTQ_TYPE_Q4_0)
-    kid = isums ? K_FWD_Q4_0_ISUMS : K_FWD_Q4_0;
+  if (p.skinny)
+    kid = isums ? (q4 ? K_FWD_Q4_0_S_ISUMS : K_FWD_Q8_0_S_ISUMS) : (q4 ? K_FWD_Q4_0_S : K_FWD_Q8_0_S);
   else
-    kid = isums ? K_FWD_Q8_0_ISUMS : K_FWD_Q8_0;
-  return launch(c, kid, dim3((unsigned)(w->Np / 64), (unsigned)(p.Tp / 64)), dim3(256), st, fa);
+    kid = isums ? (q4 ? K_FWD_Q4_0_W_ISUMS : K_FWD_Q8_0_W_ISUMS) : (q4 ? K_FWD_Q4_0_W : K_FWD_Q8_0_W);
+  return launch(c, kid, dim3((unsigned)(w->Np / rows_per_wg), (unsigned)(p.Tp / (p.skinny ? 16 : 64)), (unsigned)ks),
+                dim3(256), st, fa);
 }
 
 // ------------------------------------------------------------------ enqueue: backward
-// dx (+)= dy.W (+ g.A);  with LoRA also ga += g^T x, gb += (s dy)^T h.
+// dx (+)= dy.W;  with LoRA also dx += g.A, ga += g^T x, gb += (s dy)^T h  (g = s dy.B, h = x.A^T).
 rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, int64_t t, float* dx, bool zero_dx,
                             const float* x, const float* la, const float* lb, int64_t r, float s, float* ga,
                             float* gb, Arena& ar, hipStream_t st) {
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
-  BwdPlan p = bwd_plan(w, t, lora ? r : 0);
-  void* dy16 = ar.take<char>(p.dy16_bytes);
-  float* einv = ar.take<float>((size_t)p.Tp);
-  float* h = lora ? ar.take<float>(p.h_floats) : nullptr;
-  float* g = lora ? ar.take<float>(p.g_floats) : nullptr;
+  float* h = lora ? ar.take<float>((size_t)(t * r)) : nullptr;
+  float* g = lora ? ar.take<float>((size_t)(t * r)) : nullptr;
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   const int N = (int)w->rows, K = (int)w->cols;
-
-  DyPrepArgs da{dy, (int)t, N, (int)p.Tp, (int)w->Np, dy16, einv, zero_dx ? dx : nullptr, K, g, (int)r};
-  RTQ_TRY(launch(c, K_DY_PREP, dim3((unsigned)p.Tp), dim3(256), st, da));
   if (lora) {
-    LoraDownArgs ld{x, la, (int)t, K, (int)r, h};
-    RTQ_TRY(launch(c, K_LORA_DOWN, dim3((unsigned)cdiv(t, 4)), dim3(256), st, ld));
-    const int nps = 256;
-    LoraGArgs lg{dy, lb, (int)t, N, (int)r, s, nps, g};
-    RTQ_TRY(launch(c, K_LORA_G, dim3((unsigned)cdiv(t, 16), (unsigned)cdiv(N, nps), (unsigned)cdiv(r, 16)), dim3(64),
-                   st, lg));
+    HGArgs hg{x, la, K, dy, lb, N, (int)t, (int)r, s, h, g, zero_dx ? dx : nullptr};
+    RTQ_TRY(launch(c, K_LORA_HG, dim3((unsigned)cdiv(t, 16), 2), dim3(512), st, hg));
+  } else if (zero_dx) {
+    RTQ_TRY(fill_zero(c, dx, t * K, st));
   }
-  // dx: grid (K chunks, token tiles, row splits), about 4 workgroups per CU
-  const int64_t base = (w->Kp / 128) * (p.Tp / 64);
+  // dx: grid (K chunks, 64-token tiles, row splits), about two 8-wave workgroups per CU
+  const int64_t base = (w->Kp / 128) * cdiv(t, 64);
   const int64_t steps = w->Np / 32;
-  const int64_t target = 4LL * c->cu_count;
-  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(steps, cdiv(target, base)));
-  splits = std::min<int64_t>(splits, 65535);
+  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16), cdiv(2 * c->cu_count, base)));
+  if (c->dx_splits > 0) splits = std::min<int64_t>(steps, c->dx_splits);
   const int64_t nps = cdiv(steps, splits) * 32;
   splits = cdiv(w->Np, nps);
-  DxArgs xa{};
-  xa.wq = w->wq;
-  xa.wd = w->wd;
-  xa.wx = w->wx;
-  xa.Np = (int)w->Np;
-  xa.Kp = (int)w->Kp;
-  xa.dy16 = dy16;
-  xa.einv = einv;
-  xa.Tp = (int)p.Tp;
-  xa.T = (int)t;
-  xa.K = K;
-  xa.n_per_split = (int)nps;
-  xa.dx = dx;
-  xa.g = g;
-  xa.la = la;
-  xa.r = (int)r;
+  DxArgs xa{w->wq, w->wd, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)nps, dx};
   const int kid = w->type == RTQ_TYPE_Q4_0 ? K_DX_Q4_0 : K_DX_Q8_0;
-  RTQ_TRY(launch(c, kid, dim3((unsigned)(w->Kp / 128), (unsigned)(p.Tp / 64), (unsigned)splits), dim3(256), st, xa));
+  RTQ_TRY(launch(c, kid, dim3((unsigned)(w->Kp / 128), (unsigned)cdiv(t, 64), (unsigned)splits), dim3(512), st, xa));
   if (lora) {
     const int64_t jt = cdiv(r, 16);
-    const int64_t gb_tiles = cdiv(N, 16) * jt;
-    const int64_t ga_tiles = jt * cdiv(K, 16);
-    LoraGradArgs lga{dy, h, g, x, (int)t, N, K, (int)r, s, gb, ga, (int)gb_tiles};
-    RTQ_TRY(launch(c, K_LORA_GRADS, dim3((unsigned)(gb_tiles + ga_tiles)), dim3(64), st, lga));
+    LoraGradArgs lga{dy, h, g, x, la, (int)t, N, K, (int)r, s, gb, ga, dx, 0, 0, 0};
+    lga.n_gb = (int)(cdiv(N, 16) * jt);
+    lga.n_ga = (int)(cdiv(K, 16) * jt);
+    lga.n_dx = (int)cdiv(cdiv(t, 16) * cdiv(K, 16), 16);
+    RTQ_TRY(launch(c, K_LORA_GRADS, dim3((unsigned)(lga.n_gb + lga.n_ga + lga.n_dx)), dim3(1024), st, lga));
   }
   return RTQ_OK;
 }
@@ -476,6 +462,7 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   rtq_ctx* c = new rtq_ctx();
   c->device = device;
   c->cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+  if (const char* e = getenv("RTQ_DX_SPLITS")) c->dx_splits = atoi(e);
   hipError_t e = hipModuleLoadData(&c->mod, rtq_hsaco_begin);
   if (e != hipSuccess) {
     delete c;
@@ -524,8 +511,8 @@ rtq_status rtq_ctx_reserve(rtq_ctx* c, int64_t max_t, int64_t max_rows, int64_t 
   fake.rows = max_rows;
   fake.cols = max_cols;
   fake.Np = roundup(max_rows, RTQ_ROW_PAD);
-  fake.Kp = roundup(max_cols, RTQ_CHUNK_K);
-  size_t need = std::max(fwd_ws_bytes(fwd_plan(&fake, max_t, max_rank)), bwd_ws_bytes(bwd_plan(&fake, max_t, max_rank)));
+  fake.Kp = roundup(max_cols, RTQ_CHUNK_Q);
+  size_t need = std::max(fwd_ws_bytes(fwd_plan(&fake, max_t, max_rank)), bwd_ws_bytes(max_t, max_rank));
   return ensure_ws(c, need);
 }
 
@@ -609,7 +596,7 @@ rtq_status rtq_weight_create(rtq_ctx* c, int type, const void* blocks, size_t nb
   w->rows = rows;
   w->cols = cols;
   w->Np = roundup(rows, RTQ_ROW_PAD);
-  w->Kp = roundup(cols, is_q32(type) ? RTQ_CHUNK_Q : RTQ_CHUNK_K);
+  w->Kp = roundup(cols, RTQ_CHUNK_Q);
   w->gguf_bytes = expect;
   const int64_t nbp = w->Kp / 32;
   const size_t q_bytes = (size_t)w->Np * nbp * (type == RTQ_TYPE_Q4_0 ? 16 : 32);
@@ -668,7 +655,7 @@ rtq_status rtq_linear_forward_d(rtq_ctx* c, const rtq_weight* w, const float* bi
   if (t > 0 && (!x || !y)) return fail(RTQ_ERR_INVALID, "null x/y");
   std::lock_guard<std::mutex> lk(c->mu);
   HIP_TRY(hipSetDevice(c->device));
-  hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+  hipStream_t st = (hipStream_t)stream;  // NULL: the HIP null stream
   FwdPlan p = fwd_plan(w, t, on ? r : 0);
   RTQ_TRY(ensure_ws(c, fwd_ws_bytes(p)));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
@@ -682,9 +669,8 @@ rtq_status rtq_frozen_backward_input_d(rtq_ctx* c, const rtq_weight* w, const fl
   if (t > 0 && (!dy || !dx)) return fail(RTQ_ERR_INVALID, "null dy/dx");
   std::lock_guard<std::mutex> lk(c->mu);
   HIP_TRY(hipSetDevice(c->device));
-  hipStream_t st = stream ? (hipStream_t)stream : c->stream;
-  BwdPlan p = bwd_plan(w, t, 0);
-  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(p)));
+  hipStream_t st = (hipStream_t)stream;  // NULL: the HIP null stream
+  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, 0)));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   return enqueue_backward(c, w, dy, t, dx, false, nullptr, nullptr, nullptr, 0, 0.0f, nullptr, nullptr, ar, st);
 }
@@ -701,9 +687,8 @@ rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora
   if (on && t > 0 && (!x || !ga || !gb)) return fail(RTQ_ERR_INVALID, "lora backward needs x, ga and gb");
   std::lock_guard<std::mutex> lk(c->mu);
   HIP_TRY(hipSetDevice(c->device));
-  hipStream_t st = stream ? (hipStream_t)stream : c->stream;
-  BwdPlan p = bwd_plan(w, t, on ? r : 0);
-  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(p)));
+  hipStream_t st = (hipStream_t)stream;  // NULL: the HIP null stream
+  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, on ? r : 0)));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   return enqueue_backward(c, w, dy, t, dx, true, x, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, ga, gb,
                           ar, st);
@@ -711,7 +696,7 @@ rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora
 
 static rtq_status enqueue_rows(rtq_ctx* c, const rtq_weight* w, int64_t r0, int64_t count, float* out,
                                hipStream_t st) {
-  RowArgs ra{w->wq, w->wd, w->wx, (int)w->Np, (int)w->Kp, (int)w->cols, (int)r0, (int)count, out};
+  RowArgs ra{w->wq, w->wd, (int)w->Np, (int)w->Kp, (int)w->cols, (int)r0, (int)count, out};
   const int64_t threads = count * (w->cols / 32);
   return launch(c, w->type == RTQ_TYPE_Q4_0 ? K_ROWS_Q4_0 : K_ROWS_Q8_0, dim3((unsigned)cdiv(threads, 256)), dim3(256),
                 st, ra);
@@ -724,7 +709,7 @@ rtq_status rtq_frozen_rows_d(rtq_ctx* c, const rtq_weight* w, int64_t r0, int64_
   if (!out) return fail(RTQ_ERR_INVALID, "null out");
   std::lock_guard<std::mutex> lk(c->mu);
   HIP_TRY(hipSetDevice(c->device));
-  return enqueue_rows(c, w, r0, count, out, stream ? (hipStream_t)stream : c->stream);
+  return enqueue_rows(c, w, r0, count, out, (hipStream_t)stream);
 }
 
 // ------------------------------------------------------------------ host-pointer API
@@ -801,9 +786,8 @@ static rtq_status backward_host(rtq_ctx* c, const rtq_weight* w, const rtq_lora*
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t st = c->stream;
   const int64_t N = w->rows, K = w->cols;
-  BwdPlan p = bwd_plan(w, t, on ? r : 0);
   const size_t io = (size_t)(t * N + t * K + (on ? t * K + 2 * r * K + 2 * N * r : 0)) * 4 + 8 * 256;
-  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(p) + io));
+  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, on ? r : 0) + io));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   float* dyd = ar.take<float>((size_t)(t * N));
   float* dxd = ar.take<float>((size_t)(t * K));
@@ -878,14 +862,14 @@ rtq_status rtq_debug_quantize_acts(rtq_ctx* c, const rtq_weight* w, const float*
   RTQ_TRY(ensure_ws(c, fwd_ws_bytes(p) + (size_t)(t * K) * 4 + 256));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   float* xdv = ar.take<float>((size_t)(t * K));
-  void* xa = ar.take<char>(p.xa_bytes);
+  void* xq = ar.take<char>(p.xq_bytes);
   float* xs = ar.take<float>(p.xd_floats);
   RTQ_TRY(h2d(xdv, x, (size_t)(t * K) * 4, st));
-  QuantArgs qa{xdv, (int)t, (int)K, (int)p.Tp, (int)w->Kp, xa, xs, nullptr};
-  RTQ_TRY(launch(c, K_QUANT_Q8_0, dim3((unsigned)cdiv(p.Tp * (w->Kp / 32), 256)), dim3(256), st, qa));
-  std::vector<uint16_t> ha(p.xa_bytes / 2);
+  ActArgs aa{xdv, (int)t, (int)K, (int)p.Tp, (int)w->Kp, xq, xs, nullptr, 0, nullptr, nullptr, 0};
+  RTQ_TRY(launch(c, K_ACT_PREP, dim3((unsigned)(p.Tp / 16)), dim3(512), st, aa));
+  std::vector<uint8_t> hq(p.xq_bytes);
   std::vector<float> hs(p.xd_floats);
-  RTQ_TRY(d2h(ha.data(), xa, p.xa_bytes, st));
+  RTQ_TRY(d2h(hq.data(), xq, p.xq_bytes, st));
   RTQ_TRY(d2h(hs.data(), xs, p.xd_floats * 4, st));
   HIP_TRY(hipStreamSynchronize(st));
   // re-pack into ggml block_q8_0 (fp16 d, 32 x int8)
@@ -899,11 +883,12 @@ rtq_status rtq_debug_quantize_acts(rtq_ctx* c, const rtq_weight* w, const float*
       blk[1] = (uint8_t)(d >> 8);
       const int64_t kc = b / 4, j = b % 4, tg = ti / 16;
       for (int g = 0; g < 4; g++) {
-        const uint16_t* f = &ha[(((tg * Kc + kc) * 4 + j) * 64 + (ti % 16) + 16 * g) * 8];
+        const uint8_t* f = &hq[(((tg * Kc + kc) * 4 + j) * 64 + (ti % 16) + 16 * g) * 16];
         for (int s = 0; s < 8; s++) {
-          const int q = (int)f16_bits_to_f32(f[s]);
+          uint16_t hb;
+          memcpy(&hb, f + 2 * s, 2);
           const int e = s < 4 ? 4 * g + s : 16 + 4 * g + (s - 4);
-          blk[2 + e] = (uint8_t)(int8_t)q;
+          blk[2 + e] = (uint8_t)(int8_t)(int)f16_bits_to_f32(hb);
         }
       }
     }

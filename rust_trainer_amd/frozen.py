@@ -179,7 +179,7 @@ class HipFrozen(FrozenMatmul):
         assert out.size == self._cols
         _ffi.check(_ffi.lib().rtq_frozen_row(self.ctx.handle, self._h, r, out.ctypes.data), "rtq_frozen_row")
 
-    # ---- device-pointer variants (ints are device addresses; stream 0 = context stream)
+    # ---- device-pointer variants (ints are device addresses; stream 0 = the HIP null stream)
     def forward_d(self, x_ptr: int, t: int, y_ptr: int, stream: int = 0) -> None:
         _ffi.check(_ffi.lib().rtq_frozen_forward_d(self.ctx.handle, self._h, x_ptr, t, y_ptr, stream or None),
                    "rtq_frozen_forward_d")

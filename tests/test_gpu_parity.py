@@ -144,7 +144,8 @@ def test_errors_are_status_codes(ctx):
 
 # ---------------------------------------------------------------- Linear + LoRA
 @pytest.mark.parametrize("wtype", FORMATS)
-@pytest.mark.parametrize("n,k,t,r", [(3072, 1024, 256, 16), (256, 512, 37, 2), (100, 96, 5, 16), (512, 256, 70, 64)])
+@pytest.mark.parametrize("n,k,t,r", [(3072, 1024, 256, 16), (256, 512, 37, 2), (100, 96, 5, 16), (512, 256, 70, 64),
+                                     (512, 2048, 9, 16), (1024, 3072, 130, 8)])
 def test_linear_lora_matches_oracle(ctx, wtype, n, k, t, r):
     alpha = 2.0 * r
     blocks, x, dy = make(wtype, n, k, t)
