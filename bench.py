@@ -40,7 +40,7 @@ def kernel_work(name: str) -> tuple[float, float] | None:
         return float(w_bytes + T * N * 4 + T * K * 4), float(2 * T * N * K)
     if name == "rtq_act_prep_q8_0":  # quantise x, h = x.A^T
         return float(T * K * 4 + T * K + T * (K // 32) * 4 + R * K * 4 + T * R * 4), float(2 * T * K * R)
-    if name == "rtq_lora_hg":  # h = x.A^T, g = s dy.B, clear dx
+    if name == "rtq_bwd_prep":  # h = x.A^T, partial g = dy.B, clear dx
         return float(T * K * 4 + T * N * 4 + (R * K + N * R) * 4 + 2 * T * R * 4 + T * K * 4), \
             float(2 * T * R * (K + N))
     if name == "rtq_lora_grads":  # dB, dA, dx += g.A

@@ -27,6 +27,7 @@ HIPCC_FLAGS = [
     "-ffp-contract=off",          # fusions are written explicitly (fmaf); dequant rounds like the reference
     "-munsafe-fp-atomics",        # hardware f32 atomic add for split reductions
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",  # MFMA results in VGPRs: the epilogues read them with VALU
 ]
 
 

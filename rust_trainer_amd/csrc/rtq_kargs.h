@@ -7,26 +7,36 @@
 //   are padded to Kp = roundup(K, 128) for Q4_0 / Q8_0 (a chunk = 4 blocks of 32).  For every
 //   (row group rg, chunk kc) the quant codes of the 16 rows are stored so that lane l of a
 //   wave (row rg*16 + l%16, k-group g = l/16) reads its MFMA fragment with one coalesced
-//   16-byte load: lane l holds, for every 32-element block j of the chunk, the codes of
-//   elements {32j + 4g .. 32j + 4g + 3} and {32j + 16 + 4g .. 32j + 16 + 4g + 3}.  For Q4_0
-//   that is exactly bytes 4g..4g+3 of the GGUF block (low nibbles: the first four, high
-//   nibbles: the second four), so no nibble moves across bytes.
+//   load: lane l holds, for every 32-element block j of the chunk, the codes of elements
+//   {32j + 4g .. 32j + 4g + 3} and {32j + 16 + 4g .. 32j + 16 + 4g + 3}.  For Q4_0 that is
+//   exactly bytes 4g..4g+3 of the GGUF block (low nibbles: the first four, high nibbles: the
+//   second four), so no nibble moves across bytes.
 //     Q4_0: qs  uint4 [Np/16][Kc][64]      (component j = block j's four bytes)
 //     Q8_0: qs  uint4 [Np/16][Kc][2][64]   (part p: blocks 2p, 2p+1; 8 bytes each: low word
 //                                           elements 4g..4g+3, high word 16+4g..16+4g+3)
-//     both: d   fp16  [Np/16][Kc][16][4]    (row-in-group, block)
+//     both: d   fp16  [Np/16][Kc][2 h][4 q][2 j2][4 i]   scale of row 4q+i of the group, block
+//           2h+j2 of the chunk: the lane with k-group q reads the scales of rows 4q..4q+3 for
+//           a half chunk (two blocks) with one 16-byte load, which is the row set a lane holds
+//           in the output of an MFMA whose A operand is the weight.
 #pragma once
 #include <stdint.h>
 
 #define RTQ_ROW_PAD 64    // Np multiple
 #define RTQ_CHUNK_Q 128   // K chunk of Q4_0 / Q8_0
+#define RTQ_ACT_KQ 256    // columns per activation-prep workgroup (one LoRA-down partial each)
+
+// index of the fp16 scale of row li (0..15) of row group rg, block j (0..3) of chunk kc
+#define RTQ_WD_INDEX(rg, kc, Kc, li, j) \
+  (((((int64_t)(rg) * (Kc) + (kc)) * 2 + ((j) >> 1)) * 4 + ((li) >> 2)) * 8 + ((j) & 1) * 4 + ((li) & 3))
 
 // ---------------------------------------------------------------- forward activation prep
-// One workgroup per 16 tokens.  x [T x K] f32 ->
-//   xq: Q8_0 codes as MFMA A fragments, exact f16: uint4 [Tp/16][Kp/128][4][64] (8 per lane per block)
-//   xd: f32 [Kp/32][Tp]  (value of the fp16 scale; 0 for padding)
-//   h:  x . A^T [T x r]  when A != null (LoRA down-projection, src/linear.rs:85)
-//   zero_y: rows of y cleared when the forward GEMM splits K (it then accumulates)
+// Grid (Tp/16, nhp), nhp = Kp / RTQ_ACT_KQ rounded up to a multiple of 4; workgroup (x, y)
+// covers 16 tokens x columns [256y, 256y + 256).  x [T x K] f32 ->
+//   xq: Q8_0 codes as exact-f16 MFMA fragments: uint4 [Tp/16][Kp/128][4][64] (8 per lane per block)
+//   xd: f32 [Kp/128][Tp][4]  (value of the fp16 scale of block 4kc+j of token t; 0 for padding)
+//   hp: LoRA down-projection partials [T][r][nhp] (src/linear.rs:85): partial y sums the
+//       workgroup's columns; the forward GEMM sums them in order
+//   zero_y: rows of y cleared when the forward GEMM splits K across workgroups (atomics)
 struct ActArgs {
   const float* x;
   int T, K, Tp, Kp;
@@ -34,23 +44,25 @@ struct ActArgs {
   float* xd;
   const float* A;
   int r;
-  float* h;
+  float* hp;
   float* zero_y;
   int N;
 };
 
 // ---------------------------------------------------------------- forward GEMM
+// y[t][n] = sum_b d_w[n][b] d_x[t][b] isum_b(t, n)  (+ bias[n]) (+ s * sum_j h[t][j] B[n][j])
 struct FwdArgs {
   const void* wq;       // quant codes, device layout
   const uint16_t* wd;   // fp16 scales, device layout
   int Np, Kp;
   const void* xq;       // activation fragments (f16 integer codes)
-  const float* xd;      // activation scales
+  const float* xd;      // activation scales [Kp/128][Tp][4]
   int Tp, T, N, K;
-  int kc_per_split;     // K chunks per blockIdx.z (split-K accumulates with atomics)
+  int kc_per_split;     // K chunks per blockIdx.z (split-K across workgroups accumulates with atomics)
   float* y;             // [T x N]
   const float* bias;    // [N] or null
-  const float* h;       // [T x r] or null (LoRA disabled)
+  const float* hp;      // LoRA down-projection partials [T][r][nhp] or null (LoRA disabled)
+  int nhp;
   const float* lb;      // LoRA B [N x r]
   int r;
   float s;              // alpha / r
@@ -58,9 +70,8 @@ struct FwdArgs {
 };
 
 // ---------------------------------------------------------------- backward
-// blockIdx.y == 0: h[t][j] = sum_k x[t][k] A[j][k]; blockIdx.y == 1: g[t][j] = sum_n (s dy[t][n]) B[n][j]
-// (src/linear.rs:106-111), one workgroup per 16 tokens; optionally clears dx first.
-struct HGArgs {
+// rtq_bwd_prep: clears dx; h = x . A^T; partial g per RTQ_ACT_KQ rows of W (src/linear.rs:97-111)
+struct BwdPrepArgs {
   const float* x;
   const float* A;
   int K;
@@ -68,9 +79,10 @@ struct HGArgs {
   const float* B;
   int N;
   int T, r;
-  float s;
-  float* h;
-  float* g;
+  float* hp;     // [T][r][nhq] partials of x . A^T
+  int nhq;
+  float* gp;     // [T][r][ngq] partials of dy . B
+  int ngq;
   float* zero_dx;
 };
 
@@ -84,6 +96,13 @@ struct DxArgs {
   int T, N, K;
   int n_per_split;      // rows of W per split (multiple of 32)
   float* dx;            // [T x K]
+  // LoRA finalisation by the extra workgroups of the last grid row (when gp != null):
+  const float* hp;      // [T][r][nhq] partials from rtq_bwd_prep
+  const float* gp;      // [T][r][ngq]
+  int nhq, ngq, r;
+  float s;
+  float* h;             // [T x r] = sum of hp
+  float* g;             // [T x r] = s * sum of gp
 };
 
 // gb[n][j] += sum_t (s*dy[t][n]) h[t][j];  ga[j][k] += sum_t g[t][j] x[t][k];  dx[t][k] += sum_j g[t][j] A[j][k]

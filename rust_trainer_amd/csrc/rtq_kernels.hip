@@ -194,284 +194,425 @@ __device__ __forceinline__ void skinny_tile(const float* S, int nrows, int lds, 
 
 // ============================================================== forward activation prep
 // ggml Q8_0 reference semantics: d = amax/127, id = d ? 1/d : 0, q = roundf(x*id) (ties away
-// from zero), stored scale fp16(d).  One workgroup per 16 tokens.
-extern "C" __global__ __launch_bounds__(512) void rtq_act_prep_q8_0(ActArgs a) {
-  __shared__ float red[9 * 256];
-  const int t0 = blockIdx.x * 16;
-  const int nbp = a.Kp / 32, Kc = a.Kp / 128;
-  for (int idx = threadIdx.x; idx < 16 * nbp; idx += 512) {
-    const int tl = idx / nbp, b = idx % nbp, t = t0 + tl;
-    const bool valid = t < a.T && b * 32 < a.K;
-    float v[32];
-    float amax = 0.0f;
-    if (valid) {
-      const f4* src = reinterpret_cast<const f4*>(a.x + (int64_t)t * a.K + b * 32);
+// from zero), stored scale fp16(d).
+// Grid (Tp/16, nq [+1]): workgroup (x, y < nq) quantises 16 tokens x RTQ_ACT_KQ columns, 256
+// threads; thread (token tl = tid/16, segment sg = tid%16) owns 16 consecutive columns (half a
+// block), so every load instruction of a wave covers four contiguous 1 KB row segments.
+// With LoRA, workgroup (x, nq) computes h = x . A^T for its 16 tokens over all of K: per quarter
+// the x and A tiles go through LDS to f32 MFMAs, the next quarter's tiles are loaded into registers
+// while the current one is multiplied, and the four waves' column partials are summed in LDS.
+__device__ __forceinline__ void load_seg(const float* p, bool ok, float v[16]) {
+  if (ok) {
+    const f4* src = reinterpret_cast<const f4*>(p);
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const f4 q = src[i];
-        v[4 * i] = q.x;
-        v[4 * i + 1] = q.y;
-        v[4 * i + 2] = q.z;
-        v[4 * i + 3] = q.w;
-      }
-#pragma unroll
-      for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
-    } else {
-#pragma unroll
-      for (int i = 0; i < 32; i++) v[i] = 0.0f;
+    for (int i = 0; i < 4; i++) {
+      const f4 q = src[i];
+      v[4 * i] = q.x;
+      v[4 * i + 1] = q.y;
+      v[4 * i + 2] = q.z;
+      v[4 * i + 3] = q.w;
     }
-    const float d = __fdiv_rn(amax, 127.0f);
-    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-    a.xd[(int64_t)b * a.Tp + t] = valid ? (float)(_Float16)d : 0.0f;
-    _Float16 q[32];
+  } else {
 #pragma unroll
-    for (int i = 0; i < 32; i++) q[i] = (_Float16)roundf(__fmul_rn(v[i], id));  // exact small integers
-    const int kc = b >> 2, j = b & 3;
-    u4v* xq = reinterpret_cast<u4v*>(a.xq) + ((int64_t)((t >> 4) * Kc + kc) * 4 + j) * 64;
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-      const half8 f = {q[4 * g], q[4 * g + 1], q[4 * g + 2], q[4 * g + 3],
-                       q[16 + 4 * g], q[17 + 4 * g], q[18 + 4 * g], q[19 + 4 * g]};
-      xq[(t & 15) + 16 * g] = __builtin_bit_cast(u4v, f);
-    }
-  }
-  if (a.zero_y) {
-    for (int tl = 0; tl < 16; tl++) {
-      const int t = t0 + tl;
-      if (t < a.T)
-        for (int n = threadIdx.x; n < a.N; n += 512) a.zero_y[(int64_t)t * a.N + n] = 0.0f;
-    }
-  }
-  if (a.A) {
-    for (int j0 = 0; j0 < a.r; j0 += 16) {
-      skinny_tile<8>(a.x, a.T, a.K, a.A, a.r, a.K, true, a.K, t0, j0, 1.0f, red);
-      if (threadIdx.x < 256) {
-        const int t = t0 + (threadIdx.x >> 4), j = j0 + (threadIdx.x & 15);
-        if (t < a.T && j < a.r) a.h[(int64_t)t * a.r + j] = red[8 * 256 + threadIdx.x];
-      }
-      __syncthreads();
-    }
+    for (int i = 0; i < 16; i++) v[i] = 0.0f;
   }
 }
 
-// ============================================================== forward GEMM (Q4_0 / Q8_0)
-// Workgroup: WT x 4 waves; wave (wt, wn) owns TS token tiles of 16 and one row group of 16.
-// Workgroup tile: (WT*TS*16) tokens x 64 weight rows.  Per 128-column chunk the workgroup stages
-// the activation fragments (int8 in memory, converted once to f16) and scales in LDS (double
-// buffered); each wave reads its weight fragments straight from global memory with one 16-byte
-// load per lane, one chunk ahead.  Per 32-element block: one 16x16x32 f16 MFMA per token tile
-// gives the exact integer block sums, then acc += isum * (d_w * d_x).
-template <int FMT>
-struct WChunk;
-
-template <>
-struct WChunk<FMT_Q4_0> {
-  static constexpr int QPC = 1;  // u4v per lane per chunk
-  u4v q;
-  u2v d;
-  __device__ __forceinline__ void load(const u4v* Q, uint32_t qo, const u2v* Dd, uint32_t dof) {
-    q = Q[qo];
-    d = Dd[dof];
-  }
-  __device__ __forceinline__ half8 frag(int j) const { return q4_0_frag(comp(q, j)); }
-};
-
-template <>
-struct WChunk<FMT_Q8_0> {
-  static constexpr int QPC = 2;
-  u4v q[2];
-  u2v d;
-  __device__ __forceinline__ void load(const u4v* Q, uint32_t qo, const u2v* Dd, uint32_t dof) {
-    q[0] = Q[qo];
-    q[1] = Q[qo + 64];
-    d = Dd[dof];
-  }
-  __device__ __forceinline__ half8 frag(int j) const {
-    const u4v& v = q[j >> 1];
-    return (j & 1) ? q8_frag(v.z, v.w) : q8_frag(v.x, v.y);
-  }
-};
-
-template <int FMT, int WT, int WN, int TS, int D, bool DBG>
-__device__ __forceinline__ void fwd_q32(const FwdArgs& a) {
-  constexpr int TT = WT * TS;                    // token tiles per workgroup
-  constexpr int NTHR = 64 * WT * WN;             // threads per workgroup
-  constexpr int APT = TT * 256 / NTHR;           // activation u2v loads per thread per chunk
-  constexpr int XPT = (TT * 64 + NTHR - 1) / NTHR;  // scale loads per thread per chunk
-  static_assert((TT * 256) % NTHR == 0, "activation staging must divide evenly");
-  __shared__ u4v sA[2][TT][4][64];
-  __shared__ __attribute__((aligned(16))) float sX[2][4][TT * 16];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
-  const int wt = w / WN, wn = w % WN;
-  const int Kc = a.Kp / 128;
-  const int rg = blockIdx.x * WN + wn;
-  const int tg0 = blockIdx.y * TT;
-  const int kc0 = blockIdx.z * a.kc_per_split;
-  const int kc1 = min(kc0 + a.kc_per_split, Kc);
-  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f4 acc[TS];
+// One LoRA partial product over a 256-column slice, by one 256-thread workgroup (f32 MFMA):
+//   P[t][j] = sum over k in [k0, k0 + 256) of S[t][k] * M(j, k),  t in [t0, t0 + 16), j in [0, r)
+// with M(j, k) = M[j * ldm + k] (A rows: LoRA down, src/linear.rs:85) when !MT, or
+// M[k * ldm + j] (B columns: g = dy . B, src/linear.rs:111) when MT; S rows have length ks.
+// Written to out[(t * r + j) * pstride + pidx] (slice index fastest, so a consumer sums a token's
+// partials in slice order with a few wide loads).  Columns beyond kend count as zero.
+template <bool MT>
+__device__ __forceinline__ void lora_partial(const float* S, int T, int ks, const float* M, int ldm, int mrows, int r,
+                                             int k0, int kend, int t0, float* out, int pstride, int pidx, float* sx,
+                                             float* sm, float* red) {
+  constexpr int LDX = RTQ_ACT_KQ + 1, LDB = 17;
+  const int tid = threadIdx.x, tl = tid >> 4, sg = tid & 15, t = t0 + tl;
+  const int lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
+  {
+    float v[16];
+    const int kk = k0 + sg * 16;
+    load_seg(S + (int64_t)t * ks + kk, t < T && kk + 16 <= kend, v);
+    if (t < T && kk < kend && kk + 16 > kend) {  // ragged tail
 #pragma unroll
-  for (int i = 0; i < TS; i++) acc[i] = zero;
-
-  // D-deep register ring: slot u holds the global data of chunk kc (kc - kc0 = u mod D); loads
-  // are issued unconditionally (chunk index clamped) so the wait for slot u only covers loads
-  // issued D chunks earlier.  Per-thread base pointers; a chunk adds a fixed stride.
-  const u4v* XA = reinterpret_cast<const u4v*>(a.xq);
-  const u4v* WQ = reinterpret_cast<const u4v*>(a.wq);
-  const u2v* WD = reinterpret_cast<const u2v*>(a.wd);
-  uint32_t xa_off[APT];
-#pragma unroll
-  for (int q = 0; q < APT; q++) {
-    const int idx = tid + NTHR * q, tsl = idx >> 8, rem = idx & 255;
-    xa_off[q] = ((uint32_t)(tg0 + tsl) * Kc * 4 + (rem >> 6)) * 64 + (rem & 63);
-  }
-  uint32_t xd_off[XPT];
-#pragma unroll
-  for (int q = 0; q < XPT; q++) {
-    const int e = min(tid + NTHR * q, TT * 64 - 1);
-    xd_off[q] = (uint32_t)(e / (TT * 16)) * a.Tp + tg0 * 16 + e % (TT * 16);
-  }
-  const uint32_t wq_off = (uint32_t)rg * Kc * WChunk<FMT>::QPC * 64 + lane;
-  const uint32_t wd_off = (uint32_t)rg * Kc * 16 + li;
-  u4v areg[D][APT];
-  float xreg[D][XPT];
-  WChunk<FMT> wr[D];
-#define RTQ_FWD_ISSUE(U, KC)                                                                          \
-  {                                                                                                   \
-    const int kcc = min((KC), kc1 - 1);                                                               \
-    _Pragma("unroll") for (int q = 0; q < APT; q++) areg[U][q] = XA[xa_off[q] + (uint32_t)kcc * 256];  \
-    _Pragma("unroll") for (int q = 0; q < XPT; q++) xreg[U][q] = a.xd[xd_off[q] + (uint32_t)kcc * 4 * a.Tp]; \
-    wr[U].load(WQ, wq_off + (uint32_t)kcc * WChunk<FMT>::QPC * 64, WD, wd_off + (uint32_t)kcc * 16);   \
-  }
-#define RTQ_FWD_BODY(U)                                                                                 \
-  {                                                                                                     \
-    const int kc = kb + (U);                                                                            \
-    if (kc < kc1) {                                                                                     \
-      const int buf = (kc - kc0) & 1;                                                                   \
-      _Pragma("unroll") for (int q = 0; q < APT; q++) {                                                 \
-        const int idx = tid + NTHR * q, tsl = idx >> 8, rem = idx & 255;                                \
-        sA[buf][tsl][rem >> 6][rem & 63] = areg[U][q];                                                  \
-      }                                                                                                 \
-      _Pragma("unroll") for (int q = 0; q < XPT; q++) {                                                 \
-        const int e = tid + NTHR * q;                                                                   \
-        if (e < TT * 64) sX[buf][e / (TT * 16)][e % (TT * 16)] = xreg[U][q];                            \
-      }                                                                                                 \
-      __syncthreads();                                                                                  \
-      RTQ_FWD_COMPUTE(wr[U], buf, kc)                                                                   \
-    }                                                                                                   \
-    RTQ_FWD_ISSUE(U, kc + D)                                                                            \
-  }
-#define RTQ_FWD_COMPUTE(WC, BUF, KC)                                                                   \
-  _Pragma("unroll") for (int j = 0; j < 4; j++) {                                                      \
-    const half8 bf = (WC).frag(j);                                                                     \
-    const float dw = h2f(hcomp((WC).d, j));                                                            \
-    _Pragma("unroll") for (int ts = 0; ts < TS; ts++) {                                                \
-      const int tt = wt * TS + ts;                                                                     \
-      const half8 af = __builtin_bit_cast(half8, sA[BUF][tt][j][lane]);                                \
-      const f4 xd = *reinterpret_cast<const f4*>(&sX[BUF][j][tt * 16 + 4 * g]);                        \
-      const f4 c = mfma_f16(af, bf, zero);                                                             \
-      if (DBG) {                                                                                       \
-        const int n = rg * 16 + li, b = (KC) * 4 + j, nb = a.K / 32;                                   \
-        _Pragma("unroll") for (int i = 0; i < 4; i++) {                                                \
-          const int t = (tg0 + tt) * 16 + 4 * g + i;                                                   \
-          if (t < a.T && n < a.N && b < nb) a.isums[((int64_t)t * a.N + n) * nb + b] = (int32_t)c[i]; \
-        }                                                                                              \
-      }                                                                                                \
-      _Pragma("unroll") for (int i = 0; i < 4; i++) acc[ts][i] = fmaf(c[i], dw * xd[i], acc[ts][i]);   \
-    }                                                                                                  \
-  }
-  static_assert(D == 4, "the pipeline below is written out for four slots");
-  if (kc0 < kc1) {
-    RTQ_FWD_ISSUE(0, kc0 + 0)
-    RTQ_FWD_ISSUE(1, kc0 + 1)
-    RTQ_FWD_ISSUE(2, kc0 + 2)
-    RTQ_FWD_ISSUE(3, kc0 + 3)
-    for (int kb = kc0; kb < kc1; kb += D) {
-      RTQ_FWD_BODY(0)
-      RTQ_FWD_BODY(1)
-      RTQ_FWD_BODY(2)
-      RTQ_FWD_BODY(3)
+      for (int i = 0; i < 16; i++) v[i] = kk + i < kend ? S[(int64_t)t * ks + kk + i] : 0.0f;
     }
+#pragma unroll
+    for (int i = 0; i < 16; i++) sx[tl * LDX + sg * 16 + i] = v[i];
   }
-#undef RTQ_FWD_BODY
-#undef RTQ_FWD_COMPUTE
-#undef RTQ_FWD_ISSUE
-
-  // epilogue: y = acc (+ bias) (+ s * h.B^T), in the order of src/linear.rs:76-90
-  const bool split = gridDim.z > 1;
-  const bool lead = blockIdx.z == 0;
-  const int n = rg * 16 + li;
-  const int nc = min(n, a.N - 1);
+  for (int j0 = 0; j0 < r; j0 += 16) {
+    if (!MT) {  // A rows j0 .. j0+15, columns k0 .. k0+255: thread (row tl, segment sg)
+      float v[16];
+      const int jr = j0 + tl, kk = k0 + sg * 16;
+      load_seg(M + (int64_t)jr * ldm + kk, jr < r && kk + 16 <= kend, v);
+      if (jr < r && kk < kend && kk + 16 > kend) {
 #pragma unroll
-  for (int ts = 0; ts < TS; ts++) {
-    const int tt = wt * TS + ts;
-    f4 lacc = zero;
-    if (a.h && lead) {
-      const int trow = (tg0 + tt) * 16 + li;
-      const int trc = min(trow, a.T - 1);
-      for (int j0 = 0; j0 < a.r; j0 += 16) {
-        float hv[4], bv[4];
+        for (int i = 0; i < 16; i++) v[i] = kk + i < kend ? M[(int64_t)jr * ldm + kk + i] : 0.0f;
+      }
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const int j = j0 + 4 * u + g, jc = min(j, a.r - 1);
-          const float hx = a.h[(int64_t)trc * a.r + jc], bx = a.lb[(int64_t)nc * a.r + jc];
-          hv[u] = (trow < a.T && j < a.r) ? hx : 0.0f;
-          bv[u] = (n < a.N && j < a.r) ? bx : 0.0f;
-        }
+      for (int i = 0; i < 16; i++) sm[tl * LDX + sg * 16 + i] = v[i];
+    } else {  // B rows k0 .. k0+255 (16 ranks each): thread tid stages row k0 + tid
+      const int k = k0 + tid;
 #pragma unroll
-        for (int u = 0; u < 4; u++) lacc = mfma_f32(hv[u], bv[u], lacc);
+      for (int i = 0; i < 16; i++) {
+        const int j = j0 + i;
+        const float bv = M[(int64_t)min(k, mrows - 1) * ldm + min(j, r - 1)];
+        sm[tid * LDB + i] = (k < kend && j < r) ? bv : 0.0f;
       }
     }
-    if (n < a.N) {
-      const float bias = (a.bias && lead) ? a.bias[n] : 0.0f;
+    __syncthreads();
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int t = (tg0 + tt) * 16 + 4 * g + i;
-        if (t < a.T) {
-          float v = acc[ts][i];
-          if (a.bias && lead) v = v + bias;
-          if (a.h && lead) v = v + a.s * lacc[i];
-          if (split)
-            atomicAdd(&a.y[(int64_t)t * a.N + n], v);
-          else
-            a.y[(int64_t)t * a.N + n] = v;
-        }
-      }
+    for (int u = 0; u < 16; u++) {
+      const int kl = 64 * w + 4 * u + g;
+      acc = mfma_f32(sx[li * LDX + kl], MT ? sm[kl * LDB + li] : sm[li * LDX + kl], acc);
     }
-  }
-}
-
-// wide: 4 waves (2 token x 2 row), tile 64 tokens x 32 rows;  skinny: 4 waves along rows, tile 16 x 64
-#define RTQ_FWD(NAME, FMT, WT, WN, TS, DBG)                                    \
-  extern "C" __global__ __launch_bounds__(64 * WT * WN) void NAME(FwdArgs a) { \
-    fwd_q32<FMT, WT, WN, TS, 4, DBG>(a);                                       \
-  }
-RTQ_FWD(rtq_fwd_q4_0_w, FMT_Q4_0, 2, 2, 2, false)
-RTQ_FWD(rtq_fwd_q4_0_s, FMT_Q4_0, 1, 4, 1, false)
-RTQ_FWD(rtq_fwd_q8_0_w, FMT_Q8_0, 2, 2, 2, false)
-RTQ_FWD(rtq_fwd_q8_0_s, FMT_Q8_0, 1, 4, 1, false)
-RTQ_FWD(rtq_fwd_q4_0_w_isums, FMT_Q4_0, 2, 2, 2, true)
-RTQ_FWD(rtq_fwd_q4_0_s_isums, FMT_Q4_0, 1, 4, 1, true)
-RTQ_FWD(rtq_fwd_q8_0_w_isums, FMT_Q8_0, 2, 2, 2, true)
-RTQ_FWD(rtq_fwd_q8_0_s_isums, FMT_Q8_0, 1, 4, 1, true)
-
-// ============================================================== backward: h and g (LoRA)
-extern "C" __global__ __launch_bounds__(512) void rtq_lora_hg(HGArgs a) {
-  __shared__ float red[9 * 256];
-  if (a.zero_dx) clear_rows(a.zero_dx, (int64_t)a.T * a.K);
-  const int t0 = blockIdx.x * 16;
-  const bool is_g = blockIdx.y == 1;
-  const float* S = is_g ? a.dy : a.x;
-  const float* Bm = is_g ? a.B : a.A;
-  const int klen = is_g ? a.N : a.K;
-  for (int j0 = 0; j0 < a.r; j0 += 16) {
-    skinny_tile<8>(S, a.T, klen, Bm, a.r, is_g ? a.r : a.K, !is_g, klen, t0, j0, is_g ? a.s : 1.0f, red);
-    if (threadIdx.x < 256) {
-      const int t = t0 + (threadIdx.x >> 4), j = j0 + (threadIdx.x & 15);
-      if (t < a.T && j < a.r) (is_g ? a.g : a.h)[(int64_t)t * a.r + j] = red[8 * 256 + threadIdx.x];
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[w * 256 + (4 * g + i) * 16 + li] = acc[i];
+    __syncthreads();
+    {
+      const int tt = tid >> 4, jj = tid & 15, ty = t0 + tt, jo = j0 + jj;
+      const float ps = (red[tid] + red[256 + tid]) + (red[512 + tid] + red[768 + tid]);
+      if (ty < T && jo < r) out[((int64_t)ty * r + jo) * pstride + pidx] = ps;
     }
     __syncthreads();
   }
+}
+
+// sum of the np (multiple of 4) partials of element e, in slice order
+__device__ __forceinline__ float sum_partials(const float* p, int64_t e, int np) {
+  const f4* q = reinterpret_cast<const f4*>(p + e * np);
+  float s = 0.0f;
+  for (int i = 0; i < np / 4; i++) {
+    const f4 v = q[i];
+    s += ((v.x + v.y) + (v.z + v.w));
+  }
+  return s;
+}
+
+extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_0(ActArgs a) {
+  constexpr int KQ = RTQ_ACT_KQ, LDX = KQ + 1;
+  __shared__ float sx[16 * LDX];
+  __shared__ float sa[16 * LDX];
+  __shared__ float red[4 * 256];
+  const int tid = threadIdx.x, tl = tid >> 4, sg = tid & 15;
+  const int t0 = blockIdx.x * 16, t = t0 + tl;
+  const int Kc = a.Kp / 128;
+  const int k0 = blockIdx.y * KQ;
+  {
+    const int kk = k0 + sg * 16;  // first column of this thread's segment
+    float v[16];
+    load_seg(a.x + (int64_t)t * a.K + kk, t < a.T && kk < a.K, v);  // K % 32 == 0: all in or all out
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));  // the two halves of a block are adjacent lanes
+    if (kk < a.Kp) {
+      const float d = __fdiv_rn(amax, 127.0f);
+      const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+      const int b = kk >> 5, hf = sg & 1, kc = b >> 2, j = b & 3;
+      _Float16 q[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) q[i] = (_Float16)roundf(__fmul_rn(v[i], id));  // exact small integers
+      // this half block gives, for each k-group g, the four codes of one 8-element fragment half
+      u2v* xq = reinterpret_cast<u2v*>(a.xq) + ((((int64_t)(t >> 4) * Kc + kc) * 4 + j) * 64 + (t & 15)) * 2 + hf;
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const half2v lo = {q[4 * g], q[4 * g + 1]}, hi = {q[4 * g + 2], q[4 * g + 3]};
+        u2v w;
+        w.x = __builtin_bit_cast(uint32_t, lo);
+        w.y = __builtin_bit_cast(uint32_t, hi);
+        xq[g * 16 * 2] = w;
+      }
+      if (hf == 0) a.xd[((int64_t)kc * a.Tp + t) * 4 + j] = (t < a.T && kk < a.K) ? (float)(_Float16)d : 0.0f;
+    }
+  }
+  if (a.zero_y && blockIdx.y == 0) {
+    for (int tt = 0; tt < 16; tt++) {
+      const int ty = t0 + tt;
+      if (ty < a.T)
+        for (int n = tid; n < a.N; n += 256) a.zero_y[(int64_t)ty * a.N + n] = 0.0f;
+    }
+  }
+  if (a.A)  // uniform; quarters beyond K write zero partials
+    lora_partial<false>(a.x, a.T, a.K, a.A, a.K, a.r, a.r, k0, a.K, t0, a.hp, gridDim.y, blockIdx.y, sx, sa, red);
+}
+
+// ============================================================== forward GEMM (Q4_0 / Q8_0)
+// MFMA orientation: A operand = 16 weight rows x 32 columns, B operand = 32 columns x 16 tokens,
+// so output lane l holds token l%16 and weight rows 4(l/16)..4(l/16)+3: one activation scale per
+// lane and four consecutive outputs of a y row (one 16-byte store).
+// Workgroup = 4 waves sharing one output tile of TT*16 tokens x RG*16 rows; the waves split the
+// K range by half chunks (64 columns, two blocks; wave w takes half chunks w, w+4, ...), then
+// reduce their partial tiles through LDS.  Each wave keeps its operands in registers in a D-deep
+// ring: the loads of item i + D - 1 are issued before item i is computed, all unconditionally
+// (clamped indices), so the wait for item i covers only the loads issued D - 1 items earlier.
+// Per block: one 16x16x32 f16 MFMA per (token tile, row group) gives the exact integer block
+// sums, then acc += isum * (d_w * d_x).
+template <int FMT>
+struct WHalf;
+
+template <>
+struct WHalf<FMT_Q4_0> {
+  u2v q;  // blocks 2h, 2h+1 of the chunk: four code bytes each
+  u4v d;  // eight fp16 scales: [j2][i] = row 4g+i, block 2h+j2
+  __device__ __forceinline__ void load(const void* wq, const uint16_t* wd, int rg, int kc, int h, int Kc, int lane) {
+    q = reinterpret_cast<const u2v*>(wq)[(((uint32_t)rg * Kc + kc) * 64 + lane) * 2 + h];
+    d = reinterpret_cast<const u4v*>(wd)[(((uint32_t)rg * Kc + kc) * 2 + h) * 4 + (lane >> 4)];
+  }
+  __device__ __forceinline__ half8 frag(int j2) const { return q4_0_frag(j2 ? q.y : q.x); }
+};
+
+template <>
+struct WHalf<FMT_Q8_0> {
+  u4v q;  // part h: block 2h in (x, y), block 2h+1 in (z, w)
+  u4v d;
+  __device__ __forceinline__ void load(const void* wq, const uint16_t* wd, int rg, int kc, int h, int Kc, int lane) {
+    q = reinterpret_cast<const u4v*>(wq)[(((uint32_t)rg * Kc + kc) * 2 + h) * 64 + lane];
+    d = reinterpret_cast<const u4v*>(wd)[(((uint32_t)rg * Kc + kc) * 2 + h) * 4 + (lane >> 4)];
+  }
+  __device__ __forceinline__ half8 frag(int j2) const { return j2 ? q8_frag(q.z, q.w) : q8_frag(q.x, q.y); }
+};
+
+// scale i (0..3) of block j2 from the 16-byte scale vector: fp16 number 4*j2 + i
+__device__ __forceinline__ float wscale(const u4v& d, int j2, int i) {
+  const uint32_t w = comp(d, 2 * j2 + (i >> 1));
+  return h2f((uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu)));
+}
+
+template <int FMT, int TT, int RG>
+struct FwdSlot {
+  WHalf<FMT> w[RG];
+  u4v x[TT][2];  // activation fragments of blocks 2h, 2h+1
+  float xs[TT][2];
+};
+
+#define RTQ_LDS_RANK 64  // LoRA ranks up to this are staged in LDS by the forward GEMM
+
+template <int FMT, int TT, int RG, int D, bool DBG>
+__device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
+  __shared__ f4 red[4][TT * RG][64];
+  __shared__ float sh[TT * 16][RTQ_LDS_RANK + 1];  // LoRA down projection rows of this tile's tokens
+  __shared__ float sb[RG * 16][RTQ_LDS_RANK + 1];  // LoRA B rows of this tile
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
+  const int Kc = a.Kp / 128;
+  const int ngroups = a.Np / 16, ntt = a.Tp / 16;
+  const int rg0 = blockIdx.x * RG, tt0 = blockIdx.y * TT;
+  const int hc0 = blockIdx.z * a.kc_per_split * 2;
+  const int hc1 = min(hc0 + a.kc_per_split * 2, 2 * Kc);
+  const int nit = hc1 - hc0 > w ? (hc1 - hc0 - w + 3) / 4 : 0;  // half chunks of this wave
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 acc[TT][RG];
+#pragma unroll
+  for (int i = 0; i < TT; i++)
+#pragma unroll
+    for (int r = 0; r < RG; r++) acc[i][r] = zero;
+
+  const u4v* XQ = reinterpret_cast<const u4v*>(a.xq);
+  const float2* XD = reinterpret_cast<const float2*>(a.xd);
+  int rgc[RG], ttc[TT];
+#pragma unroll
+  for (int r = 0; r < RG; r++) rgc[r] = min(rg0 + r, ngroups - 1);
+#pragma unroll
+  for (int i = 0; i < TT; i++) ttc[i] = min(tt0 + i, ntt - 1);
+  FwdSlot<FMT, TT, RG> sl[D];
+  const bool lead = blockIdx.z == 0;
+  const bool lora = a.hp && lead;
+  const bool lora_lds = lora && a.r <= RTQ_LDS_RANK;
+
+  auto issue = [&](FwdSlot<FMT, TT, RG>& S, int it) {
+    const int hc = min(hc0 + w + 4 * min(it, max(nit - 1, 0)), 2 * Kc - 1);  // clamped: always a valid half chunk
+    const int kc = hc >> 1, h = hc & 1;
+#pragma unroll
+    for (int r = 0; r < RG; r++) S.w[r].load(a.wq, a.wd, rgc[r], kc, h, Kc, lane);
+#pragma unroll
+    for (int i = 0; i < TT; i++) {
+      const uint32_t base = (((uint32_t)ttc[i] * Kc + kc) * 4 + 2 * h) * 64 + lane;
+      S.x[i][0] = XQ[base];
+      S.x[i][1] = XQ[base + 64];
+      const float2 s2 = XD[((uint32_t)kc * a.Tp + ttc[i] * 16 + li) * 2 + h];
+      S.xs[i][0] = s2.x;
+      S.xs[i][1] = s2.y;
+    }
+  };
+  auto compute = [&](const FwdSlot<FMT, TT, RG>& S, int it) {
+    const int hc = hc0 + w + 4 * it;
+#pragma unroll
+    for (int j2 = 0; j2 < 2; j2++) {
+      half8 wf[RG];
+      float sc[RG][4];
+#pragma unroll
+      for (int r = 0; r < RG; r++) {
+        wf[r] = S.w[r].frag(j2);
+#pragma unroll
+        for (int i = 0; i < 4; i++) sc[r][i] = wscale(S.w[r].d, j2, i);
+      }
+#pragma unroll
+      for (int i = 0; i < TT; i++) {
+        const half8 xf = __builtin_bit_cast(half8, S.x[i][j2]);
+        const float xs = S.xs[i][j2];
+#pragma unroll
+        for (int r = 0; r < RG; r++) {
+          const f4 c = mfma_f16(wf[r], xf, zero);
+          if (DBG) {
+            const int t = (tt0 + i) * 16 + li, b = hc * 2 + j2, nb = a.K / 32;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              const int n = (rg0 + r) * 16 + 4 * g + e;
+              if (t < a.T && n < a.N && b < nb) a.isums[((int64_t)t * a.N + n) * nb + b] = (int32_t)c[e];
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < 4; e++) acc[i][r][e] = fmaf(c[e], sc[r][e] * xs, acc[i][r][e]);
+        }
+      }
+    }
+  };
+  // D-deep ring; item it lives in slot it % D
+#pragma unroll
+  for (int s = 0; s < D - 1; s++) issue(sl[s], s);
+  if (lora_lds) {
+    // stage h rows of this tile's tokens and B rows of its weight rows, 16 ranks at a time;
+    // the loads are issued after the ring prologue and overlap it
+    for (int j0 = 0; j0 < a.r; j0 += 16) {
+      constexpr int NH = TT * 16 * 16 / 256, NB = (RG * 16 * 16 + 255) / 256;
+      float hv[NH], bv[NB];
+#pragma unroll
+      for (int k = 0; k < NH; k++) {
+        const int e = threadIdx.x + 256 * k, tl = e >> 4, j = j0 + (e & 15);
+        hv[k] = sum_partials(a.hp, (int64_t)min(tt0 * 16 + tl, a.T - 1) * a.r + min(j, a.r - 1), a.nhp);
+      }
+#pragma unroll
+      for (int k = 0; k < NB; k++) {
+        const int e = min(threadIdx.x + 256 * k, RG * 256 - 1), nl = e >> 4, j = j0 + (e & 15);
+        bv[k] = a.lb[(int64_t)min(rg0 * 16 + nl, a.N - 1) * a.r + min(j, a.r - 1)];
+      }
+#pragma unroll
+      for (int k = 0; k < NH; k++) {
+        const int e = threadIdx.x + 256 * k;
+        sh[e >> 4][j0 + (e & 15)] = hv[k];
+      }
+#pragma unroll
+      for (int k = 0; k < NB; k++) {
+        const int e = threadIdx.x + 256 * k;
+        if (e < RG * 256) sb[e >> 4][j0 + (e & 15)] = bv[k];
+      }
+    }
+  }
+  for (int it0 = 0; it0 < nit; it0 += D) {
+#pragma unroll
+    for (int s = 0; s < D; s++) {
+      issue(sl[(s + D - 1) % D], it0 + s + D - 1);
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this item's math
+      if (it0 + s < nit) compute(sl[s], it0 + s);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- reduce the four waves' partial tiles: wave w finalises pairs p = w, w + 4, ...
+#pragma unroll
+  for (int i = 0; i < TT; i++)
+#pragma unroll
+    for (int r = 0; r < RG; r++) red[w][i * RG + r][lane] = acc[i][r];
+  __syncthreads();
+  const bool split = gridDim.z > 1;
+  for (int p = w; p < TT * RG; p += 4) {
+    const int i = p / RG, r = p % RG;
+    const f4 v0 = red[0][p][lane], v1 = red[1][p][lane], v2 = red[2][p][lane], v3 = red[3][p][lane];
+    f4 v;
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = (v0[e] + v1[e]) + (v2[e] + v3[e]);
+    const int t = (tt0 + i) * 16 + li;
+    const int nb0 = (rg0 + r) * 16;
+    const int n0 = nb0 + 4 * g;
+    if (nb0 >= a.N) continue;  // whole row group is padding (uniform over the wave)
+    // LoRA up: lacc[e] = sum_j B[n0+e][j] h[t][j]  (f32 MFMA, A operand = B rows, B operand = h rows)
+    f4 lacc = zero;
+    if (lora_lds) {
+      for (int j0 = 0; j0 < a.r; j0 += 4) {
+        const int j = j0 + g, jc = min(j, a.r - 1);
+        const float hv = sh[i * 16 + li][jc], bv = sb[r * 16 + li][jc];
+        lacc = mfma_f32((nb0 + li < a.N && j < a.r) ? bv : 0.0f, (t < a.T && j < a.r) ? hv : 0.0f, lacc);
+      }
+    } else if (lora) {  // rank above the LDS staging limit: straight from global memory
+      const int tc = min(t, a.T - 1);
+      const int nrow = min(nb0 + li, a.N - 1);
+      for (int j0 = 0; j0 < a.r; j0 += 4) {
+        const int j = j0 + g, jc = min(j, a.r - 1);
+        const float hv = sum_partials(a.hp, (int64_t)tc * a.r + jc, a.nhp);
+        const float bv = a.lb[(int64_t)nrow * a.r + jc];
+        lacc = mfma_f32((nb0 + li < a.N && j < a.r) ? bv : 0.0f, (t < a.T && j < a.r) ? hv : 0.0f, lacc);
+      }
+    }
+    if (t < a.T) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int n = n0 + e;
+        float o = v[e];
+        if (a.bias && lead) o = o + a.bias[min(n, a.N - 1)];
+        if (lora) o = o + a.s * lacc[e];
+        v[e] = o;
+      }
+      float* yr = a.y + (int64_t)t * a.N;
+      if (split) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (n0 + e < a.N) atomicAdd(&yr[n0 + e], v[e]);
+      } else if ((a.N & 3) == 0 && n0 + 3 < a.N) {
+        *reinterpret_cast<f4*>(yr + n0) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (n0 + e < a.N) yr[n0 + e] = v[e];
+      }
+    }
+  }
+}
+
+// wide: 4 token tiles x 3 row groups per workgroup (64 x 48 outputs), 2-deep ring;
+// skinny (T <= 16): 1 token tile x 4 row groups, 4-deep ring, split K across workgroups too.
+#define RTQ_FWD(NAME, FMT, TT, RG, D, DBG)                                   \
+  extern "C" __global__ __launch_bounds__(256) void NAME(FwdArgs a) {        \
+    fwd_tile<FMT, TT, RG, D, DBG>(a);                                        \
+  }
+RTQ_FWD(rtq_fwd_q4_0_w, FMT_Q4_0, 4, 3, 2, false)
+RTQ_FWD(rtq_fwd_q4_0_s, FMT_Q4_0, 1, 4, 4, false)
+RTQ_FWD(rtq_fwd_q8_0_w, FMT_Q8_0, 4, 3, 2, false)
+RTQ_FWD(rtq_fwd_q8_0_s, FMT_Q8_0, 1, 4, 4, false)
+RTQ_FWD(rtq_fwd_q4_0_w_isums, FMT_Q4_0, 4, 3, 2, true)
+RTQ_FWD(rtq_fwd_q4_0_s_isums, FMT_Q4_0, 1, 4, 4, true)
+RTQ_FWD(rtq_fwd_q8_0_w_isums, FMT_Q8_0, 4, 3, 2, true)
+RTQ_FWD(rtq_fwd_q8_0_s_isums, FMT_Q8_0, 1, 4, 4, true)
+
+// ============================================================== backward preparation
+// Grid (ceil(T/16), nhq + ngq), 256 threads (src/linear.rs:97-111); nhq, ngq multiples of 4:
+//   every workgroup: clears its share of dx (Linear::backward returns a fresh dx; the dx GEMM
+//                    then accumulates into it);
+//   y < nhq:         partial h over columns [256y, 256y + 256) of x . A^T -> hp[t][j][y]
+//   y = nhq + q:     partial g over rows [256q, 256q + 256) of W: dy . B   -> gp[t][j][q]
+// The dx kernel's extra workgroups sum the partials in slice order (h, and g scaled by s).
+extern "C" __global__ __launch_bounds__(256) void rtq_bwd_prep(BwdPrepArgs a) {
+  constexpr int KQ = RTQ_ACT_KQ, LDX = KQ + 1, LDB = 17;
+  static_assert(256 * LDB >= 16 * LDX, "the B slice reuses the A tile buffer");
+  __shared__ float sx[16 * LDX];
+  __shared__ float sm[256 * LDB];
+  __shared__ float red[4 * 256];
+  if (a.zero_dx) {
+    const int64_t n = (int64_t)a.T * a.K;
+    const int64_t nthr = (int64_t)gridDim.x * gridDim.y * 256;
+    for (int64_t i = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 256 + threadIdx.x; i < n; i += nthr)
+      a.zero_dx[i] = 0.0f;
+  }
+  if (!a.A) return;  // uniform
+  const int t0 = blockIdx.x * 16;
+  if ((int)blockIdx.y < a.nhq)
+    lora_partial<false>(a.x, a.T, a.K, a.A, a.K, a.r, a.r, blockIdx.y * KQ, a.K, t0, a.hp, a.nhq, blockIdx.y, sx, sm,
+                        red);
+  else
+    lora_partial<true>(a.dy, a.T, a.N, a.B, a.r, a.N, a.r, (blockIdx.y - a.nhq) * KQ, a.N, t0, a.gp, a.ngq,
+                       blockIdx.y - a.nhq, sx, sm, red);
 }
 
 // ============================================================== dx = dy . W
@@ -498,7 +639,7 @@ struct DxW<FMT_Q4_0> {
 #pragma unroll
     for (int r = 0; r < 2; r++) {
       q[r] = Q[(base * 64 + li0 + r + 16 * gg) * 4 + jb];
-      d[r] = a.wd[(base * 16 + li0 + r) * 4 + jb];
+      d[r] = a.wd[RTQ_WD_INDEX(rg, kc, Kc, li0 + r, jb)];
     }
     (void)hh;
   }
@@ -520,7 +661,7 @@ struct DxW<FMT_Q8_0> {
 #pragma unroll
     for (int r = 0; r < 2; r++) {
       q[r] = Q[(((base * 2 + (jb >> 1)) * 64 + li0 + r + 16 * gg) * 2 + (jb & 1)) * 2 + hh];
-      d[r] = a.wd[(base * 16 + li0 + r) * 4 + jb];
+      d[r] = a.wd[RTQ_WD_INDEX(rg, kc, Kc, li0 + r, jb)];
     }
   }
   __device__ __forceinline__ void codes(int hh, float c[2][4]) const {
@@ -534,6 +675,16 @@ struct DxW<FMT_Q8_0> {
 
 template <int FMT, int D>
 __device__ __forceinline__ void dx_q32(const DxArgs& a) {
+  if (a.gp && blockIdx.y == gridDim.y - 1) {
+    // h = sum of hp, g = s * sum of gp, both in slice order (src/linear.rs:106-111)
+    const int64_t n = (int64_t)a.T * a.r;
+    const int64_t nthr = (int64_t)gridDim.x * gridDim.z * blockDim.x;
+    for (int64_t e = ((int64_t)blockIdx.z * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += nthr) {
+      a.h[e] = sum_partials(a.hp, e, a.nhq);
+      a.g[e] = a.s * sum_partials(a.gp, e, a.ngq);
+    }
+    return;  // uniform over the workgroup, before any barrier
+  }
   __shared__ u4v sA[2][4][2][64];                                   // [buf][tile][hi/lo][lane]
   __shared__ __attribute__((aligned(16))) __bf16 sW[2][2][128][40];   // [buf][hi/lo][k][n]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
@@ -755,7 +906,7 @@ extern "C" __global__ __launch_bounds__(256) void rtq_rows_q4_0(RowArgs a) {
   const int rl = (int)(idx / nb), b = (int)(idx % nb);
   const int n = a.r0 + rl, rg = n >> 4, li = n & 15, kc = b >> 2, j = b & 3;
   const u4v* q = reinterpret_cast<const u4v*>(a.wq) + (int64_t)(rg * Kc + kc) * 64;
-  const float d = h2f(a.wd[((int64_t)(rg * Kc + kc) * 16 + li) * 4 + j]);
+  const float d = h2f(a.wd[RTQ_WD_INDEX(rg, kc, Kc, li, j)]);
   float* out = a.out + (int64_t)rl * a.K + b * 32;
 #pragma unroll
   for (int gg = 0; gg < 4; gg++) {
@@ -776,7 +927,7 @@ extern "C" __global__ __launch_bounds__(256) void rtq_rows_q8_0(RowArgs a) {
   const int rl = (int)(idx / nb), b = (int)(idx % nb);
   const int n = a.r0 + rl, rg = n >> 4, li = n & 15, kc = b >> 2, j = b & 3;
   const u4v* q = reinterpret_cast<const u4v*>(a.wq) + (int64_t)(rg * Kc + kc) * 128 + (j >> 1) * 64;
-  const float d = h2f(a.wd[((int64_t)(rg * Kc + kc) * 16 + li) * 4 + j]);
+  const float d = h2f(a.wd[RTQ_WD_INDEX(rg, kc, Kc, li, j)]);
   float* out = a.out + (int64_t)rl * a.K + b * 32;
 #pragma unroll
   for (int gg = 0; gg < 4; gg++) {

@@ -115,7 +115,7 @@ enum Kid {
   K_FWD_Q4_0_S_ISUMS,
   K_FWD_Q8_0_W_ISUMS,
   K_FWD_Q8_0_S_ISUMS,
-  K_LORA_HG,
+  K_BWD_PREP,
   K_DX_Q4_0,
   K_DX_Q8_0,
   K_LORA_GRADS,
@@ -126,7 +126,7 @@ enum Kid {
 const char* kKernelNames[K_COUNT] = {
     "rtq_fill_zero",        "rtq_act_prep_q8_0",    "rtq_fwd_q4_0_w",       "rtq_fwd_q4_0_s",
     "rtq_fwd_q8_0_w",       "rtq_fwd_q8_0_s",       "rtq_fwd_q4_0_w_isums", "rtq_fwd_q4_0_s_isums",
-    "rtq_fwd_q8_0_w_isums", "rtq_fwd_q8_0_s_isums", "rtq_lora_hg",          "rtq_dx_q4_0",
+    "rtq_fwd_q8_0_w_isums", "rtq_fwd_q8_0_s_isums", "rtq_bwd_prep",          "rtq_dx_q4_0",
     "rtq_dx_q8_0",          "rtq_lora_grads",       "rtq_rows_q4_0",        "rtq_rows_q8_0"};
 
 struct TimedLaunch {
@@ -145,6 +145,10 @@ struct rtq_ctx {
   std::mutex mu;
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  // arrival counters of the cross-workgroup reductions (all zero between calls: the workgroup
+  // that completes a reduction resets its counter)
+  unsigned* cnt = nullptr;
+  size_t cnt_cap = 0;
   bool timing = false;
   int timing_only = -1;  // -1: every kernel
   std::vector<TimedLaunch> pending;
@@ -203,13 +207,6 @@ rtq_status launch(rtq_ctx* c, int kid, dim3 grid, dim3 block, hipStream_t s, con
   return RTQ_OK;
 }
 
-rtq_status fill_zero(rtq_ctx* c, float* p, int64_t n, hipStream_t s) {
-  if (n <= 0) return RTQ_OK;
-  FillArgs a{p, n};
-  const int64_t blocks = std::min<int64_t>(cdiv(n, 256), 2048);
-  return launch(c, K_FILL, dim3((unsigned)blocks), dim3(256), s, a);
-}
-
 // ------------------------------------------------------------------ workspace
 struct Arena {
   char* base;
@@ -238,6 +235,22 @@ rtq_status ensure_ws(rtq_ctx* c, size_t bytes) {
   return RTQ_OK;
 }
 
+// Grows the counter array to n entries, zeroed in stream order before the kernels that use it.
+rtq_status ensure_cnt(rtq_ctx* c, size_t n, hipStream_t st) {
+  if (n <= c->cnt_cap) return RTQ_OK;
+  const size_t want = std::max<size_t>(n + n / 4, 4096);
+  if (c->cnt) {
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipFree(c->cnt));
+    c->cnt = nullptr;
+    c->cnt_cap = 0;
+  }
+  HIP_TRY(hipMalloc(&c->cnt, want * sizeof(unsigned)));
+  HIP_TRY(hipMemsetAsync(c->cnt, 0, want * sizeof(unsigned), st));
+  c->cnt_cap = want;
+  return RTQ_OK;
+}
+
 bool is_q32(int type) { return type == RTQ_TYPE_Q4_0 || type == RTQ_TYPE_Q8_0; }
 bool supported(int type) { return is_q32(type); }
 
@@ -254,26 +267,42 @@ int64_t block_bytes(int type) {
 
 // ------------------------------------------------------------------ per-call sizes
 // Forward: tokens padded to 16 (skinny kernel, t <= 16) or 64 (wide kernel).
+// The activation kernel writes one LoRA-down partial per RTQ_ACT_KQ columns (nhp of them).
 struct FwdPlan {
-  int64_t T, Tp;
+  int64_t T, Tp, nhp;
   bool skinny;
   size_t xq_bytes, xd_floats, h_floats;
 };
+
+constexpr int kFwdWideTT = 4, kFwdWideRG = 3;    // rtq_fwd_*_w: 64 tokens x 48 rows per workgroup
+constexpr int kFwdSkinnyRG = 4;                   // rtq_fwd_*_s: 16 tokens x 64 rows per workgroup
 
 FwdPlan fwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
   FwdPlan p;
   p.T = t;
   p.skinny = t <= 16;
-  p.Tp = roundup(std::max<int64_t>(t, 1), p.skinny ? 16 : 64);
+  p.Tp = roundup(std::max<int64_t>(t, 1), p.skinny ? 16 : 16 * kFwdWideTT);
+  p.nhp = roundup(cdiv(w->Kp, RTQ_ACT_KQ), 4);
   p.xq_bytes = (size_t)p.Tp * w->Kp * 2;  // one f16 per element
   p.xd_floats = (size_t)(w->Kp / 32) * p.Tp;
-  p.h_floats = (size_t)t * std::max<int64_t>(r, 0);
+  p.h_floats = (size_t)p.nhp * t * std::max<int64_t>(r, 0);
   return p;
+}
+
+// counters used by one call at most (token tiles of the activation kernel, plus backward tiles)
+size_t cnt_needed(int64_t t, int64_t rows, int64_t cols) {
+  return (size_t)(cdiv(std::max<int64_t>(t, 1), 16) + 64) * 2 + (size_t)(cdiv(cols, 64) * cdiv(t, 16));
 }
 
 size_t fwd_ws_bytes(const FwdPlan& p) { return p.xq_bytes + p.xd_floats * 4 + p.h_floats * 4 + 4 * 256; }
 
-size_t bwd_ws_bytes(int64_t t, int64_t r) { return (size_t)(2 * t * std::max<int64_t>(r, 0)) * 4 + 4 * 256; }
+// partial-product slices of the LoRA reductions over n columns (multiple of 4, see sum_partials)
+int64_t lora_slices(int64_t n) { return roundup(cdiv(std::max<int64_t>(n, 1), RTQ_ACT_KQ), 4); }
+
+// backward workspace: h, g [t x r] and their partials [t][r][slices]
+size_t bwd_ws_bytes(int64_t t, int64_t r, int64_t n, int64_t k) {
+  return (size_t)((2 + lora_slices(n) + lora_slices(k)) * t * std::max<int64_t>(r, 0)) * 4 + 4 * 256;
+}
 
 // ------------------------------------------------------------------ enqueue: forward
 // y = x.W^T (+bias) (+ s h.B^T);  isums (debug) receives the per-block integer sums.
@@ -285,25 +314,25 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   FwdPlan p = fwd_plan(w, t, lora ? r : 0);
   void* xq = ar.take<char>(p.xq_bytes);
   float* xd = ar.take<float>(p.xd_floats);
-  float* h = lora ? ar.take<float>(p.h_floats) : nullptr;
+  float* hp = lora ? ar.take<float>(p.h_floats) : nullptr;
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   const int64_t Kc = w->Kp / 128;
-  const int64_t rows_per_wg = p.skinny ? 64 : 32;
-  const int64_t tiles = (w->Np / rows_per_wg) * (p.Tp / (p.skinny ? 16 : 64));
-  // split K when the output alone gives too few workgroups (accumulate with atomics)
+  const int64_t rg_per_wg = p.skinny ? kFwdSkinnyRG : kFwdWideRG;
+  const int64_t gx = cdiv(w->Np / 16, rg_per_wg), gy = p.Tp / (p.skinny ? 16 : 16 * kFwdWideTT);
+  const int64_t tiles = gx * gy;
+  // split K across workgroups when the output alone gives too few of them (atomics into a
+  // zeroed y); every split keeps at least two chunks, i.e. one half chunk per wave
   int64_t ks = 1;
-  if (!isums) {
-    if (p.skinny)
-      ks = std::min<int64_t>(Kc, std::max<int64_t>(1, cdiv(2 * c->cu_count, tiles)));
-    else if (tiles < c->cu_count / 2)
-      ks = std::min<int64_t>(std::min<int64_t>(Kc, 4), cdiv(c->cu_count, tiles));
+  if (!isums && tiles < c->cu_count) {
+    const int64_t want = cdiv(p.skinny ? 2 * c->cu_count : c->cu_count, tiles);
+    ks = std::max<int64_t>(1, std::min<int64_t>(want, Kc / 2));
   }
   const int64_t kcps = cdiv(Kc, ks);
   ks = cdiv(Kc, kcps);
 
-  ActArgs aa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xq, xd, lora ? la : nullptr, (int)r, h,
+  ActArgs aa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xq, xd, lora ? la : nullptr, (int)r, hp,
              ks > 1 ? y : nullptr, (int)w->rows};
-  RTQ_TRY(launch(c, K_ACT_PREP, dim3((unsigned)(p.Tp / 16)), dim3(512), st, aa));
+  RTQ_TRY(launch(c, K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp), dim3(256), st, aa));
   FwdArgs fa{};
   fa.wq = w->wq;
   fa.wd = w->wd;
@@ -318,7 +347,8 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   fa.kc_per_split = (int)kcps;
   fa.y = y;
   fa.bias = bias;
-  fa.h = h;
+  fa.hp = hp;
+  fa.nhp = (int)p.nhp;
   fa.lb = lb;
   fa.r = (int)r;
   fa.s = s;
@@ -329,8 +359,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
     kid = isums ? (q4 ? K_FWD_Q4_0_S_ISUMS : K_FWD_Q8_0_S_ISUMS) : (q4 ? K_FWD_Q4_0_S : K_FWD_Q8_0_S);
   else
     kid = isums ? (q4 ? K_FWD_Q4_0_W_ISUMS : K_FWD_Q8_0_W_ISUMS) : (q4 ? K_FWD_Q4_0_W : K_FWD_Q8_0_W);
-  return launch(c, kid, dim3((unsigned)(w->Np / rows_per_wg), (unsigned)(p.Tp / (p.skinny ? 16 : 64)), (unsigned)ks),
-                dim3(256), st, fa);
+  return launch(c, kid, dim3((unsigned)gx, (unsigned)gy, (unsigned)ks), dim3(256), st, fa);
 }
 
 // ------------------------------------------------------------------ enqueue: backward
@@ -340,15 +369,17 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
                             float* gb, Arena& ar, hipStream_t st) {
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
+  const int N = (int)w->rows, K = (int)w->cols;
+  const int64_t nhq = lora_slices(K), ngq = lora_slices(N);
   float* h = lora ? ar.take<float>((size_t)(t * r)) : nullptr;
   float* g = lora ? ar.take<float>((size_t)(t * r)) : nullptr;
+  float* hp = lora ? ar.take<float>((size_t)(nhq * t * r)) : nullptr;
+  float* gp = lora ? ar.take<float>((size_t)(ngq * t * r)) : nullptr;
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
-  const int N = (int)w->rows, K = (int)w->cols;
-  if (lora) {
-    HGArgs hg{x, la, K, dy, lb, N, (int)t, (int)r, s, h, g, zero_dx ? dx : nullptr};
-    RTQ_TRY(launch(c, K_LORA_HG, dim3((unsigned)cdiv(t, 16), 2), dim3(512), st, hg));
-  } else if (zero_dx) {
-    RTQ_TRY(fill_zero(c, dx, t * K, st));
+  if (lora || zero_dx) {
+    BwdPrepArgs pa{x,  lora ? la : nullptr, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq,
+                   zero_dx ? dx : nullptr};
+    RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, 16), (unsigned)(lora ? nhq + ngq : 1)), dim3(256), st, pa));
   }
   // dx: grid (K chunks, 64-token tiles, row splits), about two 8-wave workgroups per CU
   const int64_t base = (w->Kp / 128) * cdiv(t, 64);
@@ -357,9 +388,11 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   if (c->dx_splits > 0) splits = std::min<int64_t>(steps, c->dx_splits);
   const int64_t nps = cdiv(steps, splits) * 32;
   splits = cdiv(w->Np, nps);
-  DxArgs xa{w->wq, w->wd, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)nps, dx};
+  DxArgs xa{w->wq, w->wd, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)nps, dx, hp, gp, (int)nhq, (int)ngq, (int)r,
+            s, h, g};
   const int kid = w->type == RTQ_TYPE_Q4_0 ? K_DX_Q4_0 : K_DX_Q8_0;
-  RTQ_TRY(launch(c, kid, dim3((unsigned)(w->Kp / 128), (unsigned)cdiv(t, 64), (unsigned)splits), dim3(512), st, xa));
+  RTQ_TRY(launch(c, kid, dim3((unsigned)(w->Kp / 128), (unsigned)(cdiv(t, 64) + (lora ? 1 : 0)), (unsigned)splits),
+                 dim3(512), st, xa));
   if (lora) {
     const int64_t jt = cdiv(r, 16);
     LoraGradArgs lga{dy, h, g, x, la, (int)t, N, K, (int)r, s, gb, ga, dx, 0, 0, 0};
@@ -435,7 +468,7 @@ void repack_q32(int type, const uint8_t* src, int64_t N, int64_t K, int64_t Np, 
           memcpy(dst + 4, codes + 16 + 4 * g, 4);
         }
       }
-      wd[((rg * Kc + kc) * 16 + li) * 4 + j] = d;
+      wd[RTQ_WD_INDEX(rg, kc, Kc, li, j)] = d;
     }
   }
 }
@@ -496,6 +529,7 @@ void rtq_ctx_destroy(rtq_ctx* c) {
   }
   for (auto e : c->free_events) (void)hipEventDestroy(e);
   if (c->ws) (void)hipFree(c->ws);
+  if (c->cnt) (void)hipFree(c->cnt);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   if (c->mod) (void)hipModuleUnload(c->mod);
   delete c;
@@ -512,8 +546,11 @@ rtq_status rtq_ctx_reserve(rtq_ctx* c, int64_t max_t, int64_t max_rows, int64_t 
   fake.cols = max_cols;
   fake.Np = roundup(max_rows, RTQ_ROW_PAD);
   fake.Kp = roundup(max_cols, RTQ_CHUNK_Q);
-  size_t need = std::max(fwd_ws_bytes(fwd_plan(&fake, max_t, max_rank)), bwd_ws_bytes(max_t, max_rank));
-  return ensure_ws(c, need);
+  size_t need = std::max(fwd_ws_bytes(fwd_plan(&fake, max_t, max_rank)), bwd_ws_bytes(max_t, max_rank, max_rows, max_cols));
+  RTQ_TRY(ensure_ws(c, need));
+  RTQ_TRY(ensure_cnt(c, cnt_needed(max_t, max_rows, max_cols), c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return RTQ_OK;
 }
 
 rtq_status rtq_ctx_set_timing(rtq_ctx* c, int enable, const char* only_kernel) {
@@ -670,7 +707,7 @@ rtq_status rtq_frozen_backward_input_d(rtq_ctx* c, const rtq_weight* w, const fl
   std::lock_guard<std::mutex> lk(c->mu);
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t st = (hipStream_t)stream;  // NULL: the HIP null stream
-  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, 0)));
+  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, 0, w->rows, w->cols)));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   return enqueue_backward(c, w, dy, t, dx, false, nullptr, nullptr, nullptr, 0, 0.0f, nullptr, nullptr, ar, st);
 }
@@ -688,7 +725,7 @@ rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora
   std::lock_guard<std::mutex> lk(c->mu);
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t st = (hipStream_t)stream;  // NULL: the HIP null stream
-  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, on ? r : 0)));
+  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, on ? r : 0, w->rows, w->cols)));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   return enqueue_backward(c, w, dy, t, dx, true, x, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, ga, gb,
                           ar, st);
@@ -787,7 +824,7 @@ static rtq_status backward_host(rtq_ctx* c, const rtq_weight* w, const rtq_lora*
   hipStream_t st = c->stream;
   const int64_t N = w->rows, K = w->cols;
   const size_t io = (size_t)(t * N + t * K + (on ? t * K + 2 * r * K + 2 * N * r : 0)) * 4 + 8 * 256;
-  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, on ? r : 0) + io));
+  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, on ? r : 0, w->rows, w->cols) + io));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   float* dyd = ar.take<float>((size_t)(t * N));
   float* dxd = ar.take<float>((size_t)(t * K));
@@ -866,7 +903,7 @@ rtq_status rtq_debug_quantize_acts(rtq_ctx* c, const rtq_weight* w, const float*
   float* xs = ar.take<float>(p.xd_floats);
   RTQ_TRY(h2d(xdv, x, (size_t)(t * K) * 4, st));
   ActArgs aa{xdv, (int)t, (int)K, (int)p.Tp, (int)w->Kp, xq, xs, nullptr, 0, nullptr, nullptr, 0};
-  RTQ_TRY(launch(c, K_ACT_PREP, dim3((unsigned)(p.Tp / 16)), dim3(512), st, aa));
+  RTQ_TRY(launch(c, K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp), dim3(256), st, aa));
   std::vector<uint8_t> hq(p.xq_bytes);
   std::vector<float> hs(p.xd_floats);
   RTQ_TRY(d2h(hq.data(), xq, p.xq_bytes, st));
@@ -878,7 +915,7 @@ rtq_status rtq_debug_quantize_acts(rtq_ctx* c, const rtq_weight* w, const float*
   for (int64_t ti = 0; ti < t; ti++)
     for (int64_t b = 0; b < nb; b++) {
       uint8_t* blk = o + (ti * nb + b) * 34;
-      const uint16_t d = f32_to_f16_bits(hs[(size_t)b * p.Tp + ti]);
+      const uint16_t d = f32_to_f16_bits(hs[((size_t)(b / 4) * p.Tp + ti) * 4 + b % 4]);  // [Kc][Tp][4]
       blk[0] = (uint8_t)(d & 0xff);
       blk[1] = (uint8_t)(d >> 8);
       const int64_t kc = b / 4, j = b % 4, tg = ti / 16;
