@@ -43,7 +43,7 @@ def kernel_work(name: str) -> tuple[float, float] | None:
     if name == "rtq_bwd_prep":  # h = x.A^T, partial g = dy.B, clear dx
         return float(T * K * 4 + T * N * 4 + (R * K + N * R) * 4 + 2 * T * R * 4 + T * K * 4), \
             float(2 * T * R * (K + N))
-    if name == "rtq_lora_grads":  # dB, dA, dx += g.A
+    if name == "rtq_bwd_finish":  # dB, dA, dx = sum of split partials + g.A
         return float(T * N * 4 + T * K * 4 + 2 * T * R * 4 + 2 * (N * R + R * K) * 4 + 2 * T * K * 4), \
             float(2 * T * R * (N + 2 * K))
     return None

@@ -70,7 +70,7 @@ struct FwdArgs {
 };
 
 // ---------------------------------------------------------------- backward
-// rtq_bwd_prep: clears dx; h = x . A^T; partial g per RTQ_ACT_KQ rows of W (src/linear.rs:97-111)
+// rtq_bwd_prep: partials of h = x . A^T and of dy . B per 256-column slice (src/linear.rs:106-111)
 struct BwdPrepArgs {
   const float* x;
   const float* A;
@@ -83,10 +83,9 @@ struct BwdPrepArgs {
   int nhq;
   float* gp;     // [T][r][ngq] partials of dy . B
   int ngq;
-  float* zero_dx;
 };
 
-// dx[t][k] += sum_n dy[t][n] W[n][k]: workgroup tile 64 tokens x 128 columns, rows of W split
+// part[z][t][k] = sum over rows n of split z of dy[t][n] W[n][k]: workgroup tile 64 tokens x 128 columns, rows of W split
 // over blockIdx.z (atomics when split), three bf16 MFMAs per product (hi/lo split of dy and W).
 struct DxArgs {
   const void* wq;
@@ -95,7 +94,7 @@ struct DxArgs {
   const float* dy;
   int T, N, K;
   int n_per_split;      // rows of W per split (multiple of 32)
-  float* dx;            // [T x K]
+  float* part;          // [splits][T][K] partial products
   // LoRA finalisation by the extra workgroups of the last grid row (when gp != null):
   const float* hp;      // [T][r][nhq] partials from rtq_bwd_prep
   const float* gp;      // [T][r][ngq]
@@ -105,11 +104,12 @@ struct DxArgs {
   float* g;             // [T x r] = s * sum of gp
 };
 
-// gb[n][j] += sum_t (s*dy[t][n]) h[t][j];  ga[j][k] += sum_t g[t][j] x[t][k];  dx[t][k] += sum_j g[t][j] A[j][k]
+// dx[t][k] = [dx +] sum_s part[s][t][k] [+ sum_j g[t][j] A[j][k]];
+// gb[n][j] += sum_t (s*dy[t][n]) h[t][j];  ga[j][k] += sum_t g[t][j] x[t][k]
 struct LoraGradArgs {
   const float* dy;
   const float* h;
-  const float* g;
+  const float* g;       // null: no LoRA
   const float* x;
   const float* la;
   int T, N, K, r;
@@ -118,6 +118,9 @@ struct LoraGradArgs {
   float* ga;  // [r x K]
   float* dx;  // [T x K]
   int n_gb, n_ga, n_dx;  // workgroups of each part, in this order
+  const float* part;     // [nsplit][T][K] from the dx kernel
+  int nsplit;
+  int accumulate;        // 1: dx += (FrozenMatmul::backward_input); 0: dx = (Linear::backward)
 };
 
 // rows [r0, r0+count) dequantised to f32 (bit-exact ggml dequant)

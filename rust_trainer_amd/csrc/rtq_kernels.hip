@@ -587,11 +587,9 @@ RTQ_FWD(rtq_fwd_q8_0_w_isums, FMT_Q8_0, 4, 3, 2, true)
 RTQ_FWD(rtq_fwd_q8_0_s_isums, FMT_Q8_0, 1, 4, 4, true)
 
 // ============================================================== backward preparation
-// Grid (ceil(T/16), nhq + ngq), 256 threads (src/linear.rs:97-111); nhq, ngq multiples of 4:
-//   every workgroup: clears its share of dx (Linear::backward returns a fresh dx; the dx GEMM
-//                    then accumulates into it);
-//   y < nhq:         partial h over columns [256y, 256y + 256) of x . A^T -> hp[t][j][y]
-//   y = nhq + q:     partial g over rows [256q, 256q + 256) of W: dy . B   -> gp[t][j][q]
+// Grid (ceil(T/16), nhq + ngq), 256 threads (src/linear.rs:106-111); nhq, ngq multiples of 4:
+//   y < nhq:     partial h over columns [256y, 256y + 256) of x . A^T -> hp[t][j][y]
+//   y = nhq + q: partial g over rows [256q, 256q + 256) of W: dy . B   -> gp[t][j][q]
 // The dx kernel's extra workgroups sum the partials in slice order (h, and g scaled by s).
 extern "C" __global__ __launch_bounds__(256) void rtq_bwd_prep(BwdPrepArgs a) {
   constexpr int KQ = RTQ_ACT_KQ, LDX = KQ + 1, LDB = 17;
@@ -599,13 +597,6 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_prep(BwdPrepArgs a) {
   __shared__ float sx[16 * LDX];
   __shared__ float sm[256 * LDB];
   __shared__ float red[4 * 256];
-  if (a.zero_dx) {
-    const int64_t n = (int64_t)a.T * a.K;
-    const int64_t nthr = (int64_t)gridDim.x * gridDim.y * 256;
-    for (int64_t i = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 256 + threadIdx.x; i < n; i += nthr)
-      a.zero_dx[i] = 0.0f;
-  }
-  if (!a.A) return;  // uniform
   const int t0 = blockIdx.x * 16;
   if ((int)blockIdx.y < a.nhq)
     lora_partial<false>(a.x, a.T, a.K, a.A, a.K, a.r, a.r, blockIdx.y * KQ, a.K, t0, a.hp, a.nhq, blockIdx.y, sx, sm,
@@ -617,64 +608,36 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_prep(BwdPrepArgs a) {
 
 // ============================================================== dx = dy . W
 // Workgroup: 8 waves, tile 64 tokens x 128 columns (one K chunk); wave (wt, wk) owns 32 tokens x
-// 32 columns (2 x 2 MFMA tiles).  Rows of W are split over blockIdx.z.  Per 32-row step the
-// workgroup stages, double buffered in LDS:
-//   * dy[64 x 32] as bf16 hi/lo A fragments (each thread loads one float4, splits it once);
-//   * W[32 x 128] dequantised to f32 (d*q, exact), split into bf16 hi/lo and stored transposed
-//     ([k][n]) so a lane reads its B fragment (8 consecutive rows of one column) in 16 bytes.
-// Next step's global loads are issued before the current step's MFMAs.
-// dx W staging: thread (wave w, lane) owns rows 2p, 2p+1 (p = lane & 15) of the 32-row step,
-// k-group gg = lane >> 4, block jb = w & 3 and half hh = w >> 2 (hh 0: elements 4gg..4gg+3,
-// hh 1: 16+4gg..16+4gg+3 of the block).  Per row it loads the four codes it needs and the scale.
+// 32 columns (2 x 2 MFMA tiles).  Rows of W are split over blockIdx.z; each split writes its own
+// partial tile part[z][t][k] (plain stores; rtq_bwd_finish sums the splits in order).  Per
+// 32-row step the workgroup stages, double buffered in LDS:
+//   * dy[64 x 32] as bf16 hi/lo A fragments: each thread loads one float4 and splits it;
+//   * W[32 x 128] dequantised (d*q: at most 15 significant bits, exact in f32), split exactly into
+//     bf16 hi + lo by truncation, stored transposed ([k][n]) so a lane reads its B fragment
+//     (8 consecutive rows of one column) in 16 bytes.
+// Three bf16 MFMAs per product (dh.wh + dl.wh + dh.wl): the missing dl.wl term and the
+// truncation of dl leave a relative error near 2^-16 per product.
+// Global loads go through buffer descriptors: a per-thread 32-bit offset plus a per-step scalar
+// offset, with out-of-range reads (tokens >= T) returning zero.  A 4-deep register ring keeps
+// the loads of step s + 3 in flight while step s is staged and multiplied.
+// W staging: thread -> half hh = tid/256 (hh 0: elements 4gg..4gg+3 of the block, hh 1:
+// 16+4gg..16+4gg+3), row group rgl, rows 2p, 2p+1, k-group gg and block jb, ordered so the code
+// words a wave loads lie in one 512-byte span; the two rows' scales are adjacent (one load).
+// The converted pair of rows goes to LDS as one 32-bit word per column.  Within a column the
+// 8-row groups are XOR-swizzled by the block index so the four blocks' writes use different banks.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 template <int FMT>
-struct DxW;
-
-template <>
-struct DxW<FMT_Q4_0> {
-  uint32_t q[2];
-  uint16_t d[2];
-  __device__ __forceinline__ void load(const DxArgs& a, int rg, int kc, int Kc, int li0, int gg, int jb, int hh) {
-    const uint32_t* Q = reinterpret_cast<const uint32_t*>(a.wq);
-    const uint32_t base = (uint32_t)(rg * Kc + kc);
-#pragma unroll
-    for (int r = 0; r < 2; r++) {
-      q[r] = Q[(base * 64 + li0 + r + 16 * gg) * 4 + jb];
-      d[r] = a.wd[RTQ_WD_INDEX(rg, kc, Kc, li0 + r, jb)];
-    }
-    (void)hh;
-  }
-  __device__ __forceinline__ void codes(int hh, float c[2][4]) const {
-#pragma unroll
-    for (int r = 0; r < 2; r++)
-#pragma unroll
-      for (int s = 0; s < 4; s++) c[r][s] = (float)((int)((q[r] >> (8 * s + 4 * hh)) & 0xf) - 8);
-  }
+struct DxSlot {
+  f4 dy;
+  uint32_t q[2];  // the four codes this thread converts, of rows 2p and 2p+1
+  uint32_t d;     // fp16 scales of rows 2p (low half) and 2p+1 (high half)
 };
 
-template <>
-struct DxW<FMT_Q8_0> {
-  uint32_t q[2];
-  uint16_t d[2];
-  __device__ __forceinline__ void load(const DxArgs& a, int rg, int kc, int Kc, int li0, int gg, int jb, int hh) {
-    const uint32_t* Q = reinterpret_cast<const uint32_t*>(a.wq);
-    const uint32_t base = (uint32_t)(rg * Kc + kc);
-#pragma unroll
-    for (int r = 0; r < 2; r++) {
-      q[r] = Q[(((base * 2 + (jb >> 1)) * 64 + li0 + r + 16 * gg) * 2 + (jb & 1)) * 2 + hh];
-      d[r] = a.wd[RTQ_WD_INDEX(rg, kc, Kc, li0 + r, jb)];
-    }
-  }
-  __device__ __forceinline__ void codes(int hh, float c[2][4]) const {
-#pragma unroll
-    for (int r = 0; r < 2; r++)
-#pragma unroll
-      for (int s = 0; s < 4; s++) c[r][s] = (float)(int8_t)((q[r] >> (8 * s)) & 0xff);
-    (void)hh;
-  }
-};
-
-template <int FMT, int D>
-__device__ __forceinline__ void dx_q32(const DxArgs& a) {
+template <int FMT>
+__device__ __forceinline__ void dx_tile(const DxArgs& a) {
   if (a.gp && blockIdx.y == gridDim.y - 1) {
     // h = sum of hp, g = s * sum of gp, both in slice order (src/linear.rs:106-111)
     const int64_t n = (int64_t)a.T * a.r;
@@ -685,6 +648,7 @@ __device__ __forceinline__ void dx_q32(const DxArgs& a) {
     }
     return;  // uniform over the workgroup, before any barrier
   }
+  constexpr int D = 4;
   __shared__ u4v sA[2][4][2][64];                                   // [buf][tile][hi/lo][lane]
   __shared__ __attribute__((aligned(16))) __bf16 sW[2][2][128][40];   // [buf][hi/lo][k][n]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
@@ -692,64 +656,102 @@ __device__ __forceinline__ void dx_q32(const DxArgs& a) {
   const int kc = blockIdx.x, Kc = a.Kp / 128;
   const int t0 = blockIdx.y * 64;
   const int n0 = blockIdx.z * a.n_per_split;
-  const int n1 = min(n0 + a.n_per_split, a.Np);
+  const int nsteps = (min(n0 + a.n_per_split, a.Np) - n0) / 32;
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
   f4 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; i++) acc[i][0] = acc[i][1] = zero;
 
-  // loader roles: dy: token tl = tid >> 3, float4 q4 = tid & 7;  W: see DxW
+  // dy loader: token tl = tid >> 3, float4 q4 = tid & 7 (columns ns + 4 q4 .. +3 of the step)
   const int tl = tid >> 3, q4 = tid & 7;
-  const int trow = t0 + tl, trc = min(trow, a.T - 1);
-  const bool tin = trow < a.T;
-  const int wp = lane & 15, wgg = lane >> 4, jb = w & 3, hh = w >> 2;  // W staging roles
-  const int rgi = wp >> 3, li0 = (2 * wp) & 15;
+  const __amdgpu_buffer_rsrc_t rdy = make_rsrc(a.dy, (uint32_t)a.T * a.N * 4u);
+  const uint32_t dy_off = ((uint32_t)(t0 + tl) * a.N + 4 * q4) * 4u;
   const bool dy_vec = (a.N & 3) == 0;
-  // D-deep register ring of (dy float4, W codes + scale) per 32-row step; loads unconditional
-  // (row index clamped), so the wait for slot u covers only loads issued D steps earlier.
-  float dyr[D][4];
-  DxW<FMT> wr[D];
-#define RTQ_DX_ISSUE(U, N_)                                                                            \
-  {                                                                                                    \
-    const int ns = min((N_), n1 - 32);                                                                 \
-    const int nn = ns + 4 * q4;                                                                        \
-    if (dy_vec) {                                                                                      \
-      const f4 v = *reinterpret_cast<const f4*>(a.dy + (int64_t)trc * a.N + min(nn, a.N - 4)); \
-      dyr[U][0] = v.x; dyr[U][1] = v.y; dyr[U][2] = v.z; dyr[U][3] = v.w;                              \
-    } else {                                                                                           \
-      _Pragma("unroll") for (int c = 0; c < 4; c++) dyr[U][c] = a.dy[(int64_t)trc * a.N + min(nn + c, a.N - 1)]; \
-    }                                                                                                  \
-    _Pragma("unroll") for (int c = 0; c < 4; c++) dyr[U][c] = (tin && nn + c < a.N) ? dyr[U][c] : 0.0f; \
-    wr[U].load(a, (ns >> 4) + rgi, kc, Kc, li0, wgg, jb, hh);                                         \
-  }
-  auto stage_compute = [&](const float (&dyv)[4], const DxW<FMT>& wv, int buf) {
-    {  // stage dy: A fragment tile tl>>4, lane (tl&15) + 16*(q4>>1), slots 4*(q4&1) .. +3
-      __bf16 hi[4], lo[4];
+  // W loader (see above)
+  const int hh = tid >> 8, rgl = (tid >> 7) & 1, qp = (tid >> 2) & 31, jb = tid & 3;
+  const int wp = qp & 7, wgg = qp >> 3;   // rows 2wp, 2wp+1 of row group rgl; k-group wgg
+  const int li0 = 2 * wp, FL0 = 16 * wgg + li0;
+  const int nloc = rgl * 16 + li0;         // first of the two rows within the step
+  const uint32_t wq_bytes = (uint32_t)(a.Np / 16) * Kc * 64 * 16 * (FMT == FMT_Q8_0 ? 2 : 1);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.wq, wq_bytes);
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.wd, (uint32_t)(a.Np / 16) * Kc * 128);
+  uint32_t q_off[2];
 #pragma unroll
-      for (int c = 0; c < 4; c++) split_bf16(dyv[c], hi[c], lo[c]);
+  for (int r = 0; r < 2; r++) {
+    if (FMT == FMT_Q4_0)
+      q_off[r] = ((((uint32_t)rgl * Kc + kc) * 64 + FL0 + r) * 4 + jb) * 4u;
+    else
+      q_off[r] = ((((((uint32_t)rgl * Kc + kc) * 2 + (jb >> 1)) * 64 + FL0 + r) * 2 + (jb & 1)) * 2 + hh) * 4u;
+  }
+  const uint32_t d_off = (uint32_t)RTQ_WD_INDEX(rgl, kc, Kc, li0, jb) * 2u;  // rows li0, li0+1 adjacent
+  const uint32_t q_rg = (uint32_t)Kc * 64 * 16 * (FMT == FMT_Q8_0 ? 2 : 1);  // bytes per row group
+  const uint32_t d_rg = (uint32_t)Kc * 128;
+
+  DxSlot<FMT> sl[D];
+  auto issue = [&](DxSlot<FMT>& S, int step) {
+    const int ns = n0 + 32 * min(step, max(nsteps - 1, 0));  // clamped: always a real step
+    const uint32_t srg = (uint32_t)(ns >> 4);
+    if (dy_vec) {
+      S.dy = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rdy, dy_off, (uint32_t)ns * 4u, 0));
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        S.dy[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rdy, dy_off + 4u * c, (uint32_t)ns * 4u, 0));
+    }
+    if (ns + 32 > a.N) {  // ragged tail of N: columns >= N hold the next row's values
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        if (ns + 4 * q4 + c >= a.N) S.dy[c] = 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) S.q[r] = __builtin_amdgcn_raw_buffer_load_b32(rq, q_off[r], srg * q_rg, 0);
+    S.d = __builtin_amdgcn_raw_buffer_load_b32(rd, d_off, srg * d_rg, 0);
+  };
+  auto stage_compute = [&](const DxSlot<FMT>& S, int buf) {
+    {  // dy: A fragment tile tl>>4, lane (tl&15) + 16*(q4>>1), slots 4*(q4&1) .. +3
+      // bit view of the whole vector: masking bit_casts of single float4 lanes is miscompiled
+      // by this compiler (every lane gets lane 0's mask)
+      const u4v vb = __builtin_bit_cast(u4v, S.dy);
+      uint32_t lb[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) lb[c] = __builtin_bit_cast(uint32_t, S.dy[c] - __builtin_bit_cast(float, vb[c] & 0xffff0000u));
       u2v hv, lv;
-      hv.x = (uint32_t)__builtin_bit_cast(uint16_t, hi[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, hi[1]) << 16);
-      hv.y = (uint32_t)__builtin_bit_cast(uint16_t, hi[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, hi[3]) << 16);
-      lv.x = (uint32_t)__builtin_bit_cast(uint16_t, lo[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, lo[1]) << 16);
-      lv.y = (uint32_t)__builtin_bit_cast(uint16_t, lo[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, lo[3]) << 16);
+      hv.x = __builtin_amdgcn_perm(vb[1], vb[0], 0x07060302u);  // high halves: bf16 by truncation
+      hv.y = __builtin_amdgcn_perm(vb[3], vb[2], 0x07060302u);
+      lv.x = __builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u);
+      lv.y = __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u);
       const int fl = (tl & 15) + 16 * (q4 >> 1);
       reinterpret_cast<u2v*>(&sA[buf][tl >> 4][0][fl])[q4 & 1] = hv;
       reinterpret_cast<u2v*>(&sA[buf][tl >> 4][1][fl])[q4 & 1] = lv;
     }
-    {  // stage W: rows 2p, 2p+1 packed into one 32-bit LDS word per column (hi and lo planes)
-      float c[2][4];
-      wv.codes(hh, c);
-      const float d0 = h2f(wv.d[0]), d1 = h2f(wv.d[1]);
-      const int kbase = 32 * jb + 16 * hh + 4 * wgg;
+    {  // W: rows 2p, 2p+1 -> bf16 hi / lo planes, one 32-bit word (both rows) per column
+      uint32_t vb[2][4], lb[2][4];
+#pragma unroll
+      for (int r = 0; r < 2; r++) {
+        const float d = h2f((uint16_t)(r ? (S.d >> 16) : (S.d & 0xffffu)));
+        // unsigned byte codes u and offset o with value (u - o) * d: Q4_0 nibble - 8, Q8_0 (q ^ 0x80) - 128
+        uint32_t u;
+        float m;
+        if (FMT == FMT_Q4_0) {
+          u = (hh ? (S.q[r] >> 4) : S.q[r]) & 0x0f0f0f0fu;
+          m = -8.0f * d;
+        } else {
+          u = S.q[r] ^ 0x80808080u;
+          m = -128.0f * d;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float v = fmaf((float)((u >> (8 * e)) & 0xffu), d, m);  // exact: <= 15 significant bits
+          vb[r][e] = __builtin_bit_cast(uint32_t, v);
+          lb[r][e] = __builtin_bit_cast(uint32_t, v - __builtin_bit_cast(float, vb[r][e] & 0xffff0000u));
+        }
+      }
+      const int kb = 32 * jb + 16 * hh + 4 * wgg;
+      const int ns = nloc ^ (8 * jb);  // swizzled row (pair start stays even)
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        __bf16 h0, l0, h1, l1;
-        split_bf16(c[0][e] * d0, h0, l0);  // d * q is exact in f32
-        split_bf16(c[1][e] * d1, h1, l1);
-        const uint32_t hp = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-        const uint32_t lp = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-        *reinterpret_cast<uint32_t*>(&sW[buf][0][kbase + e][2 * wp]) = hp;
-        *reinterpret_cast<uint32_t*>(&sW[buf][1][kbase + e][2 * wp]) = lp;
+        *reinterpret_cast<uint32_t*>(&sW[buf][0][kb + e][ns]) = __builtin_amdgcn_perm(vb[1][e], vb[0][e], 0x07060302u);
+        *reinterpret_cast<uint32_t*>(&sW[buf][1][kb + e][ns]) = __builtin_amdgcn_perm(lb[1][e], lb[0][e], 0x07060302u);
       }
     }
     __syncthreads();
@@ -759,35 +761,28 @@ __device__ __forceinline__ void dx_q32(const DxArgs& a) {
       const bf8 al = __builtin_bit_cast(bf8, sA[buf][wt * 2 + ts][1][lane]);
 #pragma unroll
       for (int ks = 0; ks < 2; ks++) {
-        const int kl = wk * 32 + ks * 16 + li;
-        const bf8 bh = *reinterpret_cast<const bf8*>(&sW[buf][0][kl][8 * g]);
-        const bf8 bl = *reinterpret_cast<const bf8*>(&sW[buf][1][kl][8 * g]);
+        const int kl = wk * 32 + ks * 16 + li;  // column kl lies in block wk: rows swizzled by 8 wk
+        const bf8 bh = *reinterpret_cast<const bf8*>(&sW[buf][0][kl][8 * (g ^ wk)]);
+        const bf8 bl = *reinterpret_cast<const bf8*>(&sW[buf][1][kl][8 * (g ^ wk)]);
         acc[ts][ks] = mfma_bf16(ah, bh, acc[ts][ks]);
         acc[ts][ks] = mfma_bf16(al, bh, acc[ts][ks]);
         acc[ts][ks] = mfma_bf16(ah, bl, acc[ts][ks]);
       }
     }
   };
-#define RTQ_DX_BODY(U)                                     \
-  {                                                        \
-    const int n = nb + 32 * (U);                           \
-    if (n < n1) stage_compute(dyr[U], wr[U], ((n - n0) >> 5) & 1); \
-    RTQ_DX_ISSUE(U, n + 32 * D)                            \
-  }
-  static_assert(D == 3, "the pipeline below is written out for three slots");
-  if (n0 < n1) {
-    RTQ_DX_ISSUE(0, n0)
-    RTQ_DX_ISSUE(1, n0 + 32)
-    RTQ_DX_ISSUE(2, n0 + 64)
-    for (int nb = n0; nb < n1; nb += 32 * D) {
-      RTQ_DX_BODY(0)
-      RTQ_DX_BODY(1)
-      RTQ_DX_BODY(2)
+#pragma unroll
+  for (int s0 = 0; s0 < D - 1; s0++) issue(sl[s0], s0);
+  for (int st0 = 0; st0 < nsteps; st0 += D) {
+#pragma unroll
+    for (int s0 = 0; s0 < D; s0++) {
+      issue(sl[(s0 + D - 1) % D], st0 + s0 + D - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (st0 + s0 < nsteps) stage_compute(sl[s0], (st0 + s0) & 1);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
-#undef RTQ_DX_BODY
-#undef RTQ_DX_ISSUE
-  const bool split = gridDim.z > 1;
+  // partial tile of this split (rows t >= T and columns k >= K are dropped)
+  float* out = a.part + (int64_t)blockIdx.z * a.T * a.K;
 #pragma unroll
   for (int ts = 0; ts < 2; ts++)
 #pragma unroll
@@ -797,33 +792,30 @@ __device__ __forceinline__ void dx_q32(const DxArgs& a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const int t = t0 + wt * 32 + ts * 16 + 4 * g + i;
-          if (t < a.T) {
-            float* p = &a.dx[(int64_t)t * a.K + k];
-            if (split)
-              atomicAdd(p, acc[ts][ks][i]);
-            else
-              *p += acc[ts][ks][i];
-          }
+          if (t < a.T) out[(int64_t)t * a.K + k] = acc[ts][ks][i];
         }
     }
 }
 
-extern "C" __global__ __launch_bounds__(512) void rtq_dx_q4_0(DxArgs a) { dx_q32<FMT_Q4_0, 3>(a); }
-extern "C" __global__ __launch_bounds__(512) void rtq_dx_q8_0(DxArgs a) { dx_q32<FMT_Q8_0, 3>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dx_q4_0(DxArgs a) { dx_tile<FMT_Q4_0>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dx_q8_0(DxArgs a) { dx_tile<FMT_Q8_0>(a); }
 
-// ============================================================== LoRA gradients (+ dx += g.A)
+// ============================================================== backward finish
+// dx[t][k] = [dx[t][k] +] sum over splits s (in order) of part[s][t][k] [+ sum_j g[t][j] A[j][k]]
+//   (FrozenMatmul::backward_input accumulates, src/frozen.rs:19-20; Linear::backward returns
+//    w.backward_input(dy) + g.A, src/linear.rs:100-101,115-118)
 // gb[n][j] += sum_t (s*dy[t][n]) h[t][j]   (matmul_tn_acc, src/linear.rs:109)
 // ga[j][k] += sum_t g[t][j] x[t][k]        (matmul_tn_acc, src/linear.rs:113)
-// dx[t][k] += sum_j g[t][j] A[j][k]        (src/linear.rs:115-118)
 // gb / ga: one 16x16 tile per workgroup, the 4 waves split t and reduce in LDS (single writer);
-// dx: four 16x16 tiles per workgroup, one per wave, K = r.
-extern "C" __global__ __launch_bounds__(1024) void rtq_lora_grads(LoraGradArgs a) {
-  __shared__ float red[16 * 256];
+// dx: four 16x16 tiles per workgroup, one per wave.
+extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a) {
+  constexpr int NW = 4;
+  __shared__ float red[NW * 256];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
   const int jt = (a.r + 15) / 16;
   int b = blockIdx.x;
   f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  const int tper = ((a.T + 15) / 16 + 3) / 4 * 4;  // t per wave, multiple of 4
+  const int tper = (a.T + NW * 16 - 1) / (NW * 16) * 16;  // t per wave, multiple of 16
   const int tb = w * tper, te = min(tb + tper, a.T);
   if (b < a.n_gb + a.n_ga) {
     const bool is_gb = b < a.n_gb;
@@ -855,11 +847,11 @@ extern "C" __global__ __launch_bounds__(1024) void rtq_lora_grads(LoraGradArgs a
 #pragma unroll
     for (int i = 0; i < 4; i++) red[w * 256 + (4 * g + i) * 16 + li] = acc[i];
     __syncthreads();
-    if (threadIdx.x < 256) {
+    {
       const int rl = threadIdx.x >> 4, cl = threadIdx.x & 15;
       float s = 0.0f;
 #pragma unroll
-      for (int ww = 0; ww < 16; ww++) s += red[ww * 256 + threadIdx.x];
+      for (int ww = 0; ww < NW; ww++) s += red[ww * 256 + threadIdx.x];
       if (is_gb) {
         const int n = rt * 16 + rl, j = ct * 16 + cl;
         if (n < a.N && j < a.r) a.gb[(int64_t)n * a.r + j] += s;
@@ -868,32 +860,57 @@ extern "C" __global__ __launch_bounds__(1024) void rtq_lora_grads(LoraGradArgs a
         if (j < a.r && k < a.K) a.ga[(int64_t)j * a.K + k] += s;
       }
     }
-  } else if (a.dx) {
-    // dx tiles: tile index = (b - n_gb - n_ga) * 16 + w over (t-tiles x k-tiles)
-    const int tile = (b - a.n_gb - a.n_ga) * 16 + w;
+  } else {
+    // dx tiles: tile index = (b - n_gb - n_ga) * NW + w over (t-tiles x k-tiles)
+    const int tile = (b - a.n_gb - a.n_ga) * NW + w;
     const int ktiles = (a.K + 15) / 16;
     const int tt = tile / ktiles, kt = tile % ktiles;
     if (tt * 16 >= a.T) return;  // whole wave exits together; no barriers in this branch
     const int trow = tt * 16 + li, kcol = kt * 16 + li;
-    for (int j0 = 0; j0 < a.r; j0 += 16) {
-      float gv[4], av[4];
+    if (a.g) {
+      for (int j0 = 0; j0 < a.r; j0 += 16) {
+        float gv[4], av[4];
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const int j = j0 + 4 * u + g, jc = min(j, a.r - 1);
-        const float x = a.g[(int64_t)min(trow, a.T - 1) * a.r + jc];
-        const float y = a.la[(int64_t)jc * a.K + min(kcol, a.K - 1)];
-        gv[u] = (trow < a.T && j < a.r) ? x : 0.0f;
-        av[u] = (kcol < a.K && j < a.r) ? y : 0.0f;
+        for (int u = 0; u < 4; u++) {
+          const int j = j0 + 4 * u + g, jc = min(j, a.r - 1);
+          const float x = a.g[(int64_t)min(trow, a.T - 1) * a.r + jc];
+          const float y = a.la[(int64_t)jc * a.K + min(kcol, a.K - 1)];
+          gv[u] = (trow < a.T && j < a.r) ? x : 0.0f;
+          av[u] = (kcol < a.K && j < a.r) ? y : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc = mfma_f32(gv[u], av[u], acc);
       }
-#pragma unroll
-      for (int u = 0; u < 4; u++) acc = mfma_f32(gv[u], av[u], acc);
     }
-    if (kcol < a.K)
+    if (kcol < a.K) {
+      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      const int64_t tk = (int64_t)a.T * a.K;
+      for (int s0 = 0; s0 < a.nsplit; s0 += 4) {
+        float v[4][4];
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int t = min(tt * 16 + 4 * g + i, a.T - 1);
+            const float x = a.part[(int64_t)min(s0 + q, a.nsplit - 1) * tk + (int64_t)t * a.K + kcol];
+            v[q][i] = s0 + q < a.nsplit ? x : 0.0f;
+          }
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) ps[i] += v[q][i];
+      }
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int t = tt * 16 + 4 * g + i;
-        if (t < a.T) a.dx[(int64_t)t * a.K + kcol] += acc[i];
+        if (t < a.T) {
+          float* p = &a.dx[(int64_t)t * a.K + kcol];
+          float o = a.accumulate ? *p + ps[i] : ps[i];
+          if (a.g) o += acc[i];
+          *p = o;
+        }
       }
+    }
   }
 }
 

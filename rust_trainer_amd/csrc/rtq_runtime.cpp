@@ -118,7 +118,7 @@ enum Kid {
   K_BWD_PREP,
   K_DX_Q4_0,
   K_DX_Q8_0,
-  K_LORA_GRADS,
+  K_BWD_FINISH,
   K_ROWS_Q4_0,
   K_ROWS_Q8_0,
   K_COUNT
@@ -127,7 +127,7 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_fill_zero",        "rtq_act_prep_q8_0",    "rtq_fwd_q4_0_w",       "rtq_fwd_q4_0_s",
     "rtq_fwd_q8_0_w",       "rtq_fwd_q8_0_s",       "rtq_fwd_q4_0_w_isums", "rtq_fwd_q4_0_s_isums",
     "rtq_fwd_q8_0_w_isums", "rtq_fwd_q8_0_s_isums", "rtq_bwd_prep",          "rtq_dx_q4_0",
-    "rtq_dx_q8_0",          "rtq_lora_grads",       "rtq_rows_q4_0",        "rtq_rows_q8_0"};
+    "rtq_dx_q8_0",          "rtq_bwd_finish",       "rtq_rows_q4_0",        "rtq_rows_q8_0"};
 
 struct TimedLaunch {
   int kid;
@@ -145,10 +145,6 @@ struct rtq_ctx {
   std::mutex mu;
   void* ws = nullptr;
   size_t ws_bytes = 0;
-  // arrival counters of the cross-workgroup reductions (all zero between calls: the workgroup
-  // that completes a reduction resets its counter)
-  unsigned* cnt = nullptr;
-  size_t cnt_cap = 0;
   bool timing = false;
   int timing_only = -1;  // -1: every kernel
   std::vector<TimedLaunch> pending;
@@ -235,22 +231,6 @@ rtq_status ensure_ws(rtq_ctx* c, size_t bytes) {
   return RTQ_OK;
 }
 
-// Grows the counter array to n entries, zeroed in stream order before the kernels that use it.
-rtq_status ensure_cnt(rtq_ctx* c, size_t n, hipStream_t st) {
-  if (n <= c->cnt_cap) return RTQ_OK;
-  const size_t want = std::max<size_t>(n + n / 4, 4096);
-  if (c->cnt) {
-    HIP_TRY(hipDeviceSynchronize());
-    HIP_TRY(hipFree(c->cnt));
-    c->cnt = nullptr;
-    c->cnt_cap = 0;
-  }
-  HIP_TRY(hipMalloc(&c->cnt, want * sizeof(unsigned)));
-  HIP_TRY(hipMemsetAsync(c->cnt, 0, want * sizeof(unsigned), st));
-  c->cnt_cap = want;
-  return RTQ_OK;
-}
-
 bool is_q32(int type) { return type == RTQ_TYPE_Q4_0 || type == RTQ_TYPE_Q8_0; }
 bool supported(int type) { return is_q32(type); }
 
@@ -289,19 +269,12 @@ FwdPlan fwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
   return p;
 }
 
-// counters used by one call at most (token tiles of the activation kernel, plus backward tiles)
-size_t cnt_needed(int64_t t, int64_t rows, int64_t cols) {
-  return (size_t)(cdiv(std::max<int64_t>(t, 1), 16) + 64) * 2 + (size_t)(cdiv(cols, 64) * cdiv(t, 16));
-}
-
 size_t fwd_ws_bytes(const FwdPlan& p) { return p.xq_bytes + p.xd_floats * 4 + p.h_floats * 4 + 4 * 256; }
 
-// partial-product slices of the LoRA reductions over n columns (multiple of 4, see sum_partials)
-int64_t lora_slices(int64_t n) { return roundup(cdiv(std::max<int64_t>(n, 1), RTQ_ACT_KQ), 4); }
-
-// backward workspace: h, g [t x r] and their partials [t][r][slices]
+// backward workspace: h, g [t x r], their slice partials [t][r][slices], dx partials [<= 16][t][k]
 size_t bwd_ws_bytes(int64_t t, int64_t r, int64_t n, int64_t k) {
-  return (size_t)((2 + lora_slices(n) + lora_slices(k)) * t * std::max<int64_t>(r, 0)) * 4 + 4 * 256;
+  const int64_t sl = roundup(cdiv(std::max<int64_t>(n, 1), RTQ_ACT_KQ), 4) + roundup(cdiv(std::max<int64_t>(k, 1), RTQ_ACT_KQ), 4);
+  return (size_t)((2 + sl) * t * std::max<int64_t>(r, 0)) * 4 + (size_t)16 * t * k * 4 + 6 * 256;
 }
 
 // ------------------------------------------------------------------ enqueue: forward
@@ -363,45 +336,59 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
 }
 
 // ------------------------------------------------------------------ enqueue: backward
-// dx (+)= dy.W;  with LoRA also dx += g.A, ga += g^T x, gb += (s dy)^T h  (g = s dy.B, h = x.A^T).
-rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, int64_t t, float* dx, bool zero_dx,
+// dx split plan: grid (K chunks, 64-token tiles, row splits), about two 8-wave workgroups per CU
+struct DxPlan {
+  int64_t splits, nps;
+};
+DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
+  const int64_t base = (w->Kp / 128) * cdiv(t, 64);
+  const int64_t steps = w->Np / 32;
+  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16), cdiv(2 * c->cu_count, base)));
+  if (c->dx_splits > 0) splits = std::min<int64_t>(steps, c->dx_splits);
+  DxPlan p;
+  p.nps = cdiv(steps, splits) * 32;
+  p.splits = cdiv(w->Np, p.nps);
+  return p;
+}
+
+// partial-product slices of the LoRA reductions over n columns (multiple of 4, see sum_partials)
+int64_t lora_slices(int64_t n) { return roundup(cdiv(std::max<int64_t>(n, 1), RTQ_ACT_KQ), 4); }
+
+// dx (+)= dy.W (accumulate: FrozenMatmul::backward_input; otherwise dx is overwritten, as
+// Linear::backward returns a fresh dx); with LoRA also dx += g.A, ga += g^T x, gb += (s dy)^T h
+// (g = s dy.B, h = x.A^T).  Kernels: [rtq_bwd_prep: slice partials of h, g] -> rtq_dx_* (per-split
+// partials of dx; its last grid row sums the h, g partials) -> rtq_bwd_finish.
+rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, int64_t t, float* dx, bool accumulate,
                             const float* x, const float* la, const float* lb, int64_t r, float s, float* ga,
                             float* gb, Arena& ar, hipStream_t st) {
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
   const int N = (int)w->rows, K = (int)w->cols;
+  if ((uint64_t)t * (uint64_t)N * 4u >= (1ull << 31))
+    return fail(RTQ_ERR_INVALID, "dy of %lld x %d floats exceeds the 2 GiB buffer-offset range", (long long)t, N);
+  const DxPlan dp = dx_plan(c, w, t);
   const int64_t nhq = lora_slices(K), ngq = lora_slices(N);
   float* h = lora ? ar.take<float>((size_t)(t * r)) : nullptr;
   float* g = lora ? ar.take<float>((size_t)(t * r)) : nullptr;
   float* hp = lora ? ar.take<float>((size_t)(nhq * t * r)) : nullptr;
   float* gp = lora ? ar.take<float>((size_t)(ngq * t * r)) : nullptr;
+  float* part = ar.take<float>((size_t)(dp.splits * t * K));
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
-  if (lora || zero_dx) {
-    BwdPrepArgs pa{x,  lora ? la : nullptr, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq,
-                   zero_dx ? dx : nullptr};
-    RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, 16), (unsigned)(lora ? nhq + ngq : 1)), dim3(256), st, pa));
-  }
-  // dx: grid (K chunks, 64-token tiles, row splits), about two 8-wave workgroups per CU
-  const int64_t base = (w->Kp / 128) * cdiv(t, 64);
-  const int64_t steps = w->Np / 32;
-  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16), cdiv(2 * c->cu_count, base)));
-  if (c->dx_splits > 0) splits = std::min<int64_t>(steps, c->dx_splits);
-  const int64_t nps = cdiv(steps, splits) * 32;
-  splits = cdiv(w->Np, nps);
-  DxArgs xa{w->wq, w->wd, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)nps, dx, hp, gp, (int)nhq, (int)ngq, (int)r,
-            s, h, g};
-  const int kid = w->type == RTQ_TYPE_Q4_0 ? K_DX_Q4_0 : K_DX_Q8_0;
-  RTQ_TRY(launch(c, kid, dim3((unsigned)(w->Kp / 128), (unsigned)(cdiv(t, 64) + (lora ? 1 : 0)), (unsigned)splits),
-                 dim3(512), st, xa));
   if (lora) {
-    const int64_t jt = cdiv(r, 16);
-    LoraGradArgs lga{dy, h, g, x, la, (int)t, N, K, (int)r, s, gb, ga, dx, 0, 0, 0};
-    lga.n_gb = (int)(cdiv(N, 16) * jt);
-    lga.n_ga = (int)(cdiv(K, 16) * jt);
-    lga.n_dx = (int)cdiv(cdiv(t, 16) * cdiv(K, 16), 16);
-    RTQ_TRY(launch(c, K_LORA_GRADS, dim3((unsigned)(lga.n_gb + lga.n_ga + lga.n_dx)), dim3(1024), st, lga));
+    BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq};
+    RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, 16), (unsigned)(nhq + ngq)), dim3(256), st, pa));
   }
-  return RTQ_OK;
+  DxArgs xa{w->wq, w->wd, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, part,
+            lora ? hp : nullptr, lora ? gp : nullptr, (int)nhq, (int)ngq, (int)r, s, h, g};
+  const int kid = w->type == RTQ_TYPE_Q4_0 ? K_DX_Q4_0 : K_DX_Q8_0;
+  RTQ_TRY(launch(c, kid, dim3((unsigned)(w->Kp / 128), (unsigned)(cdiv(t, 64) + (lora ? 1 : 0)), (unsigned)dp.splits),
+                 dim3(512), st, xa));
+  const int64_t jt = cdiv(r, 16);
+  LoraGradArgs fa{dy, h, g, x, la, (int)t, N, K, (int)r, s, gb, ga, dx, 0, 0, 0, part, (int)dp.splits, accumulate ? 1 : 0};
+  fa.n_gb = lora ? (int)(cdiv(N, 16) * jt) : 0;
+  fa.n_ga = lora ? (int)(cdiv(K, 16) * jt) : 0;
+  fa.n_dx = (int)cdiv(cdiv(t, 16) * cdiv(K, 16), 4);  // four 16x16 tiles per 256-thread workgroup
+  return launch(c, K_BWD_FINISH, dim3((unsigned)(fa.n_gb + fa.n_ga + fa.n_dx)), dim3(256), st, fa);
 }
 
 rtq_status check_weight(rtq_ctx* c, const rtq_weight* w) {
@@ -509,10 +496,9 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
       return fail(RTQ_ERR_NO_DEVICE, "kernel %s missing from code object: %s", kKernelNames[k], hipGetErrorString(e));
     }
   }
-  e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);  // default priority
   if (e != hipSuccess) {
-    (void)hipModuleUnload(c->mod);
-    delete c;
+    rtq_ctx_destroy(c);
     return fail(RTQ_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
   }
   *out = c;
@@ -529,7 +515,6 @@ void rtq_ctx_destroy(rtq_ctx* c) {
   }
   for (auto e : c->free_events) (void)hipEventDestroy(e);
   if (c->ws) (void)hipFree(c->ws);
-  if (c->cnt) (void)hipFree(c->cnt);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   if (c->mod) (void)hipModuleUnload(c->mod);
   delete c;
@@ -548,8 +533,6 @@ rtq_status rtq_ctx_reserve(rtq_ctx* c, int64_t max_t, int64_t max_rows, int64_t 
   fake.Kp = roundup(max_cols, RTQ_CHUNK_Q);
   size_t need = std::max(fwd_ws_bytes(fwd_plan(&fake, max_t, max_rank)), bwd_ws_bytes(max_t, max_rank, max_rows, max_cols));
   RTQ_TRY(ensure_ws(c, need));
-  RTQ_TRY(ensure_cnt(c, cnt_needed(max_t, max_rows, max_cols), c->stream));
-  HIP_TRY(hipStreamSynchronize(c->stream));
   return RTQ_OK;
 }
 
@@ -709,7 +692,7 @@ rtq_status rtq_frozen_backward_input_d(rtq_ctx* c, const rtq_weight* w, const fl
   hipStream_t st = (hipStream_t)stream;  // NULL: the HIP null stream
   RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, 0, w->rows, w->cols)));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
-  return enqueue_backward(c, w, dy, t, dx, false, nullptr, nullptr, nullptr, 0, 0.0f, nullptr, nullptr, ar, st);
+  return enqueue_backward(c, w, dy, t, dx, true, nullptr, nullptr, nullptr, 0, 0.0f, nullptr, nullptr, ar, st);
 }
 
 rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const float* x,
@@ -727,7 +710,7 @@ rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora
   hipStream_t st = (hipStream_t)stream;  // NULL: the HIP null stream
   RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, on ? r : 0, w->rows, w->cols)));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
-  return enqueue_backward(c, w, dy, t, dx, true, x, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, ga, gb,
+  return enqueue_backward(c, w, dy, t, dx, false, x, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, ga, gb,
                           ar, st);
 }
 
@@ -845,7 +828,7 @@ static rtq_status backward_host(rtq_ctx* c, const rtq_weight* w, const rtq_lora*
     RTQ_TRY(h2d(gad, ga, (size_t)(r * K) * 4, st));
     RTQ_TRY(h2d(gbd, gb, (size_t)(N * r) * 4, st));
   }
-  RTQ_TRY(enqueue_backward(c, w, dyd, t, dxd, linear, xd, ad, bld, on ? r : 0, s, gad, gbd, ar, st));
+  RTQ_TRY(enqueue_backward(c, w, dyd, t, dxd, !linear, xd, ad, bld, on ? r : 0, s, gad, gbd, ar, st));
   RTQ_TRY(d2h(dx, dxd, (size_t)(t * K) * 4, st));
   if (on) {
     RTQ_TRY(d2h(ga, gad, (size_t)(r * K) * 4, st));
