@@ -7,9 +7,15 @@ hot path over the batch: Linear forward (y) and Linear backward (dx, dA, dB), de
 inputs, through the C ABI's device-pointer entry points on torch's current stream.  Operand sets
 rotate over >256 MB so neither L2 nor the Infinity Cache holds a step's inputs.
 
-Prints one JSON line: metric/value (tokens/s = T / step time), per-kernel average durations from
-HIP events recorded by the library on the launch stream, the roofline of the dominant kernel, and
-the CPU oracle's time on the host cores (cpu_baseline, bounded sample).
+The timed region is one replay of a HIP graph (torch.cuda.CUDAGraph over the library's device-pointer
+calls on one stream) of exactly K steps, with no events inside, so the GPU runs the kernels back to
+back.  Per-kernel durations come from an eager pass of the same steps with HIP events recorded by the
+library around each launch on the launch stream; these intervals include the dispatch of the kernel
+packet and so read a few microseconds longer than the kernel-trace durations of rocprofv3.
+
+Prints one JSON line: metric/value (tokens/s = T / step time), per-kernel average durations, the
+roofline of the dominant kernel, and the CPU oracle's time on the host cores (cpu_baseline,
+bounded sample).
 """
 from __future__ import annotations
 
@@ -148,9 +154,11 @@ def main() -> int:
         sets.append(s)
     torch.cuda.synchronize()
     L = _ffi.lib()
-    stream = torch.cuda.current_stream().cuda_stream
+    # all work goes to one side stream, captured into HIP graphs (torch.cuda.CUDAGraph): the step's
+    # five kernels are launched back to back by the GPU, without host launch gaps
+    side = torch.cuda.Stream()
 
-    def step(i: int) -> None:
+    def step(i: int, stream: int) -> None:
         s = sets[i % len(sets)]
         lp = ctypes.byref(s["lora"])
         _ffi.check(L.rtq_linear_forward_d(ctx.handle, s["w"].handle, None, lp, s["x"].data_ptr(), T,
@@ -159,31 +167,49 @@ def main() -> int:
                                            s["dx"].data_ptr(), s["ga"].data_ptr(), s["gb"].data_ptr(), stream),
                    "backward")
 
-    for i in range(args.warmup):
-        step(i)
+    def capture(nsteps: int) -> "torch.cuda.CUDAGraph":
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            st = torch.cuda.current_stream().cuda_stream
+            for i in range(nsteps):
+                step(i, st)
+        return g
+
+    with torch.cuda.stream(side):
+        st = torch.cuda.current_stream().cuda_stream
+        for i in range(args.warmup):
+            step(i, st)
     torch.cuda.synchronize()
 
-    # per-kernel breakdown: HIP events around every launch (separate pass, not the timed one)
+    # per-kernel durations: HIP events recorded by the library around every launch, on the launch
+    # stream, in an eager pass (event records are not captured into graphs); then the dominant
+    # kernel alone, with events around its launches only
+    def eager(nsteps: int) -> None:
+        with torch.cuda.stream(side):
+            st = torch.cuda.current_stream().cuda_stream
+            for i in range(nsteps):
+                step(i, st)
+        torch.cuda.synchronize()
+
     ctx.set_timing(True)
     ctx.reset_timing()
-    for i in range(args.steps):
-        step(i)
-    torch.cuda.synchronize()
+    eager(args.steps)
     per = {name: (cnt, ms) for name, (cnt, ms) in ctx.timing().items()}
-    ctx.set_timing(False)
     dominant = max(per, key=lambda k: per[k][1])
-
-    # timed region: events only around the dominant kernel
     ctx.set_timing(True, dominant)
     ctx.reset_timing()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    eager(args.steps)
     dom_cnt, dom_ms = ctx.timing()[dominant]
     ctx.set_timing(False)
+
+    # timed region: exactly K steps, one graph replay, no events inside
+    g = capture(args.steps)
+    g.replay()  # warm replay
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
 
     result = {
@@ -197,13 +223,15 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 x q8_0 int block dots -> f32 (fwd); bf16x3 (dx); f32 (LoRA)",
+        "dtype": "int8 x int4 block dots -> f32 (forward); bf16x3 -> f32 (dx); f32 (LoRA)",
         "data": "synthetic",
         "config": {"workload": "configs[0]: Qwen3-0.6B gate_proj frozen linear, Q4_0 W 3072x1024, T=256, "
                                "LoRA r=16 alpha=32; Linear forward (y) + backward (dx, dA, dB)",
                    "rows": N, "cols": K, "tokens": T, "rank": R, "operand_sets": args.sets},
         "roofline": roofline(dominant, dom_ms / dom_cnt),
-        "kernels_avg_us": {k: round(ms * 1e3 / c, 3) for k, (c, ms) in sorted(per.items())},
+        "kernels": {k: {"avg_us": round(ms * 1e3 / c, 3),
+                        "frac": roofline(k, ms / c)["frac"] if kernel_work(k) else None}
+                    for k, (c, ms) in sorted(per.items())},
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline((blocks, X, DY, A, B), args.cpu_seconds)

@@ -55,7 +55,7 @@ def build_runtime(hsaco: str) -> str:
     out = os.path.join(PKG, "librtq.so")
     tmp = out + ".tmp"
     cxx = shutil.which("g++") or "g++"
-    _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",
+    _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter", "-Wno-attributes",
           "-D__HIP_PLATFORM_AMD__", f'-DRTQ_HSACO_PATH="{hsaco}"',
           "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"), "-I", CSRC,
           os.path.join(CSRC, "rtq_runtime.cpp"), "-o", tmp,

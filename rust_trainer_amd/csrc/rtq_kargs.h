@@ -94,6 +94,7 @@ struct DxArgs {
   const float* dy;
   int T, N, K;
   int n_per_split;      // rows of W per split (multiple of 32)
+  int nsplit;           // splits: grid = Kc * ceil(T/64) * nsplit workgroups (+ LoRA finalisers)
   float* part;          // [splits][T][K] partial products
   // LoRA finalisation by the extra workgroups of the last grid row (when gp != null):
   const float* hp;      // [T][r][nhq] partials from rtq_bwd_prep

@@ -638,11 +638,18 @@ struct DxSlot {
 
 template <int FMT>
 __device__ __forceinline__ void dx_tile(const DxArgs& a) {
-  if (a.gp && blockIdx.y == gridDim.y - 1) {
+  // Flat grid, XCD-aware: consecutive workgroup ids go to the 8 XCDs in turn, so id % 8 selects
+  // a group of row splits and all (token tile, K chunk) workgroups of a split run on one XCD,
+  // whose L2 then fetches that split's dy slice and W rows once.  The last n_fin workgroups
+  // finalise h and g (LoRA).
+  const int Kc = a.Kp / 128, ntt = (a.T + 63) / 64;
+  const int nmain = Kc * ntt * a.nsplit;
+  const int id = blockIdx.x;
+  if (id >= nmain) {
     // h = sum of hp, g = s * sum of gp, both in slice order (src/linear.rs:106-111)
     const int64_t n = (int64_t)a.T * a.r;
-    const int64_t nthr = (int64_t)gridDim.x * gridDim.z * blockDim.x;
-    for (int64_t e = ((int64_t)blockIdx.z * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += nthr) {
+    const int64_t nthr = (int64_t)(gridDim.x - nmain) * blockDim.x;
+    for (int64_t e = (int64_t)(id - nmain) * blockDim.x + threadIdx.x; e < n; e += nthr) {
       a.h[e] = sum_partials(a.hp, e, a.nhq);
       a.g[e] = a.s * sum_partials(a.gp, e, a.ngq);
     }
@@ -653,9 +660,21 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   __shared__ __attribute__((aligned(16))) __bf16 sW[2][2][128][40];   // [buf][hi/lo][k][n]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
   const int wt = w >> 2, wk = w & 3;
-  const int kc = blockIdx.x, Kc = a.Kp / 128;
-  const int t0 = blockIdx.y * 64;
-  const int n0 = blockIdx.z * a.n_per_split;
+  // id -> (split, token tile, K chunk).  With nsplit a multiple of 8, split = id % 8 + 8 * group
+  // keeps all workgroups of a split on one XCD; otherwise splits are taken in order.
+  const int per = ntt * Kc;  // workgroups per split
+  int sp, within;
+  if ((a.nsplit & 7) == 0) {
+    const int grp = id / (8 * per), rem = id % (8 * per);
+    sp = grp * 8 + rem % 8;
+    within = rem / 8;
+  } else {
+    sp = id / per;
+    within = id % per;
+  }
+  const int kc = within % Kc;
+  const int t0 = (within / Kc) * 64;
+  const int n0 = sp * a.n_per_split;
   const int nsteps = (min(n0 + a.n_per_split, a.Np) - n0) / 32;
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
   f4 acc[2][2];
@@ -781,33 +800,28 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  // partial tile of this split (rows t >= T and columns k >= K are dropped)
-  float* out = a.part + (int64_t)blockIdx.z * a.T * a.K;
+  // partial tile of this split in fragment order: part[sp][tile][wave][lane][16], tile = token
+  // tile * Kc + K chunk; element ts*8 + ks*4 + i is row t0 + 32wt + 16ts + 4g + i, column
+  // 128kc + 32wk + 16ks + li.  Four 16-byte stores per lane, contiguous per wave.
+  f4* out = reinterpret_cast<f4*>(a.part) +
+            ((((int64_t)sp * ntt + (t0 >> 6)) * Kc + kc) * 8 + w) * 256 + lane * 4;
 #pragma unroll
   for (int ts = 0; ts < 2; ts++)
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-      const int k = kc * 128 + wk * 32 + ks * 16 + li;
-      if (k < a.K)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int t = t0 + wt * 32 + ts * 16 + 4 * g + i;
-          if (t < a.T) out[(int64_t)t * a.K + k] = acc[ts][ks][i];
-        }
-    }
+    for (int ks = 0; ks < 2; ks++) out[ts * 2 + ks] = acc[ts][ks];
 }
 
 extern "C" __global__ __launch_bounds__(512) void rtq_dx_q4_0(DxArgs a) { dx_tile<FMT_Q4_0>(a); }
 extern "C" __global__ __launch_bounds__(512) void rtq_dx_q8_0(DxArgs a) { dx_tile<FMT_Q8_0>(a); }
 
 // ============================================================== backward finish
-// dx[t][k] = [dx[t][k] +] sum over splits s (in order) of part[s][t][k] [+ sum_j g[t][j] A[j][k]]
+// dx[t][k] = [dx[t][k] +] sum over splits s (in order) of the partials [+ sum_j g[t][j] A[j][k]]
 //   (FrozenMatmul::backward_input accumulates, src/frozen.rs:19-20; Linear::backward returns
 //    w.backward_input(dy) + g.A, src/linear.rs:100-101,115-118)
 // gb[n][j] += sum_t (s*dy[t][n]) h[t][j]   (matmul_tn_acc, src/linear.rs:109)
 // ga[j][k] += sum_t g[t][j] x[t][k]        (matmul_tn_acc, src/linear.rs:113)
 // gb / ga: one 16x16 tile per workgroup, the 4 waves split t and reduce in LDS (single writer);
-// dx: four 16x16 tiles per workgroup, one per wave.
+// dx: one wave per 32 x 32 fragment of the dx kernel's tiles (the dx kernel's partial layout).
 extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a) {
   constexpr int NW = 4;
   __shared__ float red[NW * 256];
@@ -861,56 +875,63 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a)
       }
     }
   } else {
-    // dx tiles: tile index = (b - n_gb - n_ga) * NW + w over (t-tiles x k-tiles)
-    const int tile = (b - a.n_gb - a.n_ga) * NW + w;
-    const int ktiles = (a.K + 15) / 16;
-    const int tt = tile / ktiles, kt = tile % ktiles;
-    if (tt * 16 >= a.T) return;  // whole wave exits together; no barriers in this branch
-    const int trow = tt * 16 + li, kcol = kt * 16 + li;
-    if (a.g) {
-      for (int j0 = 0; j0 < a.r; j0 += 16) {
-        float gv[4], av[4];
+    // dx fragment f = (b - n_gb - n_ga) * NW + w: dx tile f / 8 (token tile * Kc + K chunk),
+    // dx wave f % 8 = (wt, wk); lane element ts*8 + ks*4 + i <-> row t0 + 32wt + 16ts + 4g + i,
+    // column 128kc + 32wk + 16ks + li (the MFMA output layout of both kernels)
+    const int Kc = (a.K + 127) / 128, ntt = (a.T + 63) / 64;
+    const int f = (b - a.n_gb - a.n_ga) * NW + w;
+    if (f >= ntt * Kc * 8) return;  // whole wave exits together; no barriers in this branch
+    const int tile = f >> 3, dw = f & 7, wt = dw >> 2, wk = dw & 3;
+    const int t0 = (tile / Kc) * 64 + wt * 32, k0 = (tile % Kc) * 128 + wk * 32;
+    const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    f4 ps[2][2] = {{zero, zero}, {zero, zero}};
+    const f4* pp = reinterpret_cast<const f4*>(a.part) + (int64_t)f * 256 + lane * 4;
+    const int64_t sstride = (int64_t)ntt * Kc * 8 * 256;  // f4 per split
+    for (int s0 = 0; s0 < a.nsplit; s0 += 2) {  // two splits' fragments in flight, summed in order
+      f4 v[2][4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const int j = j0 + 4 * u + g, jc = min(j, a.r - 1);
-          const float x = a.g[(int64_t)min(trow, a.T - 1) * a.r + jc];
-          const float y = a.la[(int64_t)jc * a.K + min(kcol, a.K - 1)];
-          gv[u] = (trow < a.T && j < a.r) ? x : 0.0f;
-          av[u] = (kcol < a.K && j < a.r) ? y : 0.0f;
-        }
+      for (int q = 0; q < 2; q++)
 #pragma unroll
-        for (int u = 0; u < 4; u++) acc = mfma_f32(gv[u], av[u], acc);
-      }
+        for (int e = 0; e < 4; e++) v[q][e] = pp[(int64_t)min(s0 + q, a.nsplit - 1) * sstride + e];
+#pragma unroll
+      for (int q = 0; q < 2; q++)
+        if (s0 + q < a.nsplit)
+#pragma unroll
+          for (int e = 0; e < 4; e++) ps[e >> 1][e & 1] += v[q][e];
     }
-    if (kcol < a.K) {
-      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      const int64_t tk = (int64_t)a.T * a.K;
-      for (int s0 = 0; s0 < a.nsplit; s0 += 4) {
-        float v[4][4];
 #pragma unroll
-        for (int q = 0; q < 4; q++)
+    for (int ts = 0; ts < 2; ts++)
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) {
+        const int trow = t0 + ts * 16 + li, kcol = k0 + ks * 16 + li;
+        f4 ga = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (a.g) {
+          for (int j0 = 0; j0 < a.r; j0 += 16) {
+            float gv[4], av[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+              const int j = j0 + 4 * u + g, jc = min(j, a.r - 1);
+              const float x = a.g[(int64_t)min(trow, a.T - 1) * a.r + jc];
+              const float y = a.la[(int64_t)jc * a.K + min(kcol, a.K - 1)];
+              gv[u] = (trow < a.T && j < a.r) ? x : 0.0f;
+              av[u] = (kcol < a.K && j < a.r) ? y : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) ga = mfma_f32(gv[u], av[u], ga);
+          }
+        }
+        if (kcol < a.K)
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            const int t = min(tt * 16 + 4 * g + i, a.T - 1);
-            const float x = a.part[(int64_t)min(s0 + q, a.nsplit - 1) * tk + (int64_t)t * a.K + kcol];
-            v[q][i] = s0 + q < a.nsplit ? x : 0.0f;
+            const int t = t0 + ts * 16 + 4 * g + i;
+            if (t < a.T) {
+              float* p = &a.dx[(int64_t)t * a.K + kcol];
+              float o = a.accumulate ? *p + ps[ts][ks][i] : ps[ts][ks][i];
+              if (a.g) o += ga[i];
+              *p = o;
+            }
           }
-#pragma unroll
-        for (int q = 0; q < 4; q++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) ps[i] += v[q][i];
       }
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int t = tt * 16 + 4 * g + i;
-        if (t < a.T) {
-          float* p = &a.dx[(int64_t)t * a.K + kcol];
-          float o = a.accumulate ? *p + ps[i] : ps[i];
-          if (a.g) o += acc[i];
-          *p = o;
-        }
-      }
-    }
   }
 }
 

@@ -274,7 +274,8 @@ size_t fwd_ws_bytes(const FwdPlan& p) { return p.xq_bytes + p.xd_floats * 4 + p.
 // backward workspace: h, g [t x r], their slice partials [t][r][slices], dx partials [<= 16][t][k]
 size_t bwd_ws_bytes(int64_t t, int64_t r, int64_t n, int64_t k) {
   const int64_t sl = roundup(cdiv(std::max<int64_t>(n, 1), RTQ_ACT_KQ), 4) + roundup(cdiv(std::max<int64_t>(k, 1), RTQ_ACT_KQ), 4);
-  return (size_t)((2 + sl) * t * std::max<int64_t>(r, 0)) * 4 + (size_t)16 * t * k * 4 + 6 * 256;
+  return (size_t)((2 + sl) * t * std::max<int64_t>(r, 0)) * 4 + (size_t)16 * roundup(t, 64) * roundup(k, 128) * 4 +
+         6 * 256;
 }
 
 // ------------------------------------------------------------------ enqueue: forward
@@ -336,14 +337,15 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
 }
 
 // ------------------------------------------------------------------ enqueue: backward
-// dx split plan: grid (K chunks, 64-token tiles, row splits), about two 8-wave workgroups per CU
+// dx split plan: K chunks x 64-token tiles x row splits, about one 8-wave workgroup per CU (more
+// splits add partial-sum traffic: each split writes and the finish kernel reads T x K floats)
 struct DxPlan {
   int64_t splits, nps;
 };
 DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
   const int64_t base = (w->Kp / 128) * cdiv(t, 64);
   const int64_t steps = w->Np / 32;
-  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16), cdiv(2 * c->cu_count, base)));
+  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16), cdiv(c->cu_count, base)));
   if (c->dx_splits > 0) splits = std::min<int64_t>(steps, c->dx_splits);
   DxPlan p;
   p.nps = cdiv(steps, splits) * 32;
@@ -372,22 +374,23 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   float* g = lora ? ar.take<float>((size_t)(t * r)) : nullptr;
   float* hp = lora ? ar.take<float>((size_t)(nhq * t * r)) : nullptr;
   float* gp = lora ? ar.take<float>((size_t)(ngq * t * r)) : nullptr;
-  float* part = ar.take<float>((size_t)(dp.splits * t * K));
+  float* part = ar.take<float>((size_t)(dp.splits * roundup(t, 64) * w->Kp));  // fragment-order partials
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   if (lora) {
     BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq};
     RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, 16), (unsigned)(nhq + ngq)), dim3(256), st, pa));
   }
-  DxArgs xa{w->wq, w->wd, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, part,
+  DxArgs xa{w->wq, w->wd, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, (int)dp.splits, part,
             lora ? hp : nullptr, lora ? gp : nullptr, (int)nhq, (int)ngq, (int)r, s, h, g};
   const int kid = w->type == RTQ_TYPE_Q4_0 ? K_DX_Q4_0 : K_DX_Q8_0;
-  RTQ_TRY(launch(c, kid, dim3((unsigned)(w->Kp / 128), (unsigned)(cdiv(t, 64) + (lora ? 1 : 0)), (unsigned)dp.splits),
-                 dim3(512), st, xa));
+  const int64_t nmain = (w->Kp / 128) * cdiv(t, 64) * dp.splits;
+  const int64_t nfin = lora ? std::min<int64_t>(64, cdiv(t * r, 512)) : 0;  // LoRA finalisers
+  RTQ_TRY(launch(c, kid, dim3((unsigned)(nmain + nfin)), dim3(512), st, xa));
   const int64_t jt = cdiv(r, 16);
   LoraGradArgs fa{dy, h, g, x, la, (int)t, N, K, (int)r, s, gb, ga, dx, 0, 0, 0, part, (int)dp.splits, accumulate ? 1 : 0};
   fa.n_gb = lora ? (int)(cdiv(N, 16) * jt) : 0;
   fa.n_ga = lora ? (int)(cdiv(K, 16) * jt) : 0;
-  fa.n_dx = (int)cdiv(cdiv(t, 16) * cdiv(K, 16), 4);  // four 16x16 tiles per 256-thread workgroup
+  fa.n_dx = (int)cdiv((w->Kp / 128) * cdiv(t, 64) * 8, 4);  // one wave per dx fragment, four per workgroup
   return launch(c, K_BWD_FINISH, dim3((unsigned)(fa.n_gb + fa.n_ga + fa.n_dx)), dim3(256), st, fa);
 }
 
