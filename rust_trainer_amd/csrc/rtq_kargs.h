@@ -18,12 +18,27 @@
 //           2h+j2 of the chunk: the lane with k-group q reads the scales of rows 4q..4q+3 for
 //           a half chunk (two blocks) with one 16-byte load, which is the row set a lane holds
 //           in the output of an MFMA whose A operand is the weight.
+//   K-quants (256-element super-blocks, Kp = K) are transcoded at upload into the same code
+//   layouts, with their 6-bit sub-block scales kept as integers:
+//     Q4_K: qs as Q4_0, unsigned 4-bit codes u (value d*sc*u - dmin*m);
+//     Q6_K: qs as Q8_0, signed codes q in [-32, 31] (value d*sc*q, sc per 16 elements);
+//     wd (uint16) [Np/16][Kc][2 h][16 li][2 j2] (RTQ_WK_INDEX): block 2h+j2 of row li, low byte sc
+//           (Q6_K: sc of elements 0..15), high byte m (Q6_K: sc of elements 16..31, int8).  The
+//           lane that builds row li's MFMA fragment for a half chunk reads one 32-bit word;
+//     wsb (uint32) [Np/16][Kp/256][16 li] (RTQ_WSB_INDEX): fp16 d (low) and fp16 dmin (high; 0
+//           for Q6_K) of the super-block; the lane with k-group q reads rows 4q..4q+3 at once.
 #pragma once
 #include <stdint.h>
 
 #define RTQ_ROW_PAD 64    // Np multiple
 #define RTQ_CHUNK_Q 128   // K chunk of Q4_0 / Q8_0
 #define RTQ_ACT_KQ 256    // columns per activation-prep workgroup (one LoRA-down partial each)
+
+// index of the K-quant sub-block scale word of row li of row group rg, block j of chunk kc
+#define RTQ_WK_INDEX(rg, kc, Kc, li, j) \
+  (((((int64_t)(rg) * (Kc) + (kc)) * 2 + ((j) >> 1)) * 16 + (li)) * 2 + ((j) & 1))
+// index of the K-quant super-block scale pair of row li of row group rg, super-block sb
+#define RTQ_WSB_INDEX(rg, sb, Ksb, li) (((int64_t)(rg) * (Ksb) + (sb)) * 16 + (li))
 
 // index of the fp16 scale of row li (0..15) of row group rg, block j (0..3) of chunk kc
 #define RTQ_WD_INDEX(rg, kc, Kc, li, j) \
@@ -37,6 +52,8 @@
 //   hp: LoRA down-projection partials [T][r][nhp] (src/linear.rs:85): partial y sums the
 //       workgroup's columns; the forward GEMM sums them in order
 //   zero_y: rows of y cleared when the forward GEMM splits K across workgroups (atomics)
+// rtq_act_prep_q8_k (K-quant weights): Q8_K per 256-column super-block (one workgroup's
+// columns), same xq layout; xd holds the super-block's f32 d for each of its 32-element blocks.
 struct ActArgs {
   const float* x;
   int T, K, Tp, Kp;
@@ -51,12 +68,14 @@ struct ActArgs {
 
 // ---------------------------------------------------------------- forward GEMM
 // y[t][n] = sum_b d_w[n][b] d_x[t][b] isum_b(t, n)  (+ bias[n]) (+ s * sum_j h[t][j] B[n][j])
+// K-quants: sum over super-blocks of (d d_x) S1 - (dmin d_x) S2 (Q4_K) or (d d_x) S (Q6_K)
 struct FwdArgs {
   const void* wq;       // quant codes, device layout
-  const uint16_t* wd;   // fp16 scales, device layout
+  const uint16_t* wd;   // fp16 scales (K-quants: sub-block scale words), device layout
   int Np, Kp;
   const void* xq;       // activation fragments (f16 integer codes)
   const float* xd;      // activation scales [Kp/128][Tp][4]
+  const uint32_t* wsb;  // K-quant super-block scales (RTQ_WSB_INDEX)
   int Tp, T, N, K;
   int kc_per_split;     // K chunks per blockIdx.z (split-K across workgroups accumulates with atomics)
   float* y;             // [T x N]
@@ -66,7 +85,8 @@ struct FwdArgs {
   const float* lb;      // LoRA B [N x r]
   int r;
   float s;              // alpha / r
-  int32_t* isums;       // debug: [T][N][K/32] or null
+  int32_t* isums;       // debug: [T][N][K/32] (Q4_0, Q8_0), [T][N][K/256][2] (Q4_K: S1, S2),
+                        // [T][N][K/256] (Q6_K: S), or null
 };
 
 // ---------------------------------------------------------------- backward
@@ -90,6 +110,7 @@ struct BwdPrepArgs {
 struct DxArgs {
   const void* wq;
   const uint16_t* wd;
+  const uint32_t* wsb;  // K-quant super-block scales (RTQ_WSB_INDEX)
   int Np, Kp;
   const float* dy;
   int T, N, K;
@@ -128,6 +149,7 @@ struct LoraGradArgs {
 struct RowArgs {
   const void* wq;
   const uint16_t* wd;
+  const uint32_t* wsb;
   int Np, Kp, K;
   int r0, count;
   float* out;  // [count x K]

@@ -29,7 +29,10 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u2v __attribute__((ext_vector_type(2)));
 
-enum { FMT_Q4_0 = 2, FMT_Q8_0 = 8 };
+enum { FMT_Q4_0 = 2, FMT_Q8_0 = 8, FMT_Q4_K = 12, FMT_Q6_K = 14 };
+__host__ __device__ constexpr bool is_kquant(int fmt) { return fmt == FMT_Q4_K || fmt == FMT_Q6_K; }
+// formats whose device codes are bytes (Q8_0 layout); the others hold nibbles (Q4_0 layout)
+__host__ __device__ constexpr bool byte_codes(int fmt) { return fmt == FMT_Q8_0 || fmt == FMT_Q6_K; }
 
 __device__ __forceinline__ f4 mfma_f16(half8 a, half8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -60,11 +63,12 @@ __device__ __forceinline__ half2v sub_h2(uint32_t bits, _Float16 c) {
   return h - cc;  // exact: small integers
 }
 
-// Q4_0 fragment: bytes 4g..4g+3 of the block -> codes (nibble - 8) of elements
+// Q4_0 fragment: bytes 4g..4g+3 of the block -> codes (nibble - OFF) of elements
 // {4g..4g+3} (low nibbles) then {16+4g..16+4g+3} (high nibbles), as exact f16.
+template <int OFF = 8>
 __device__ __forceinline__ half8 q4_0_frag(uint32_t w) {
   const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-  const _Float16 c = (_Float16)1032.0f;
+  const _Float16 c = (_Float16)(1024.0f + OFF);
   const half2v a0 = sub_h2(bytes01_to_h2(lo), c), a1 = sub_h2(bytes23_to_h2(lo), c);
   const half2v a2 = sub_h2(bytes01_to_h2(hi), c), a3 = sub_h2(bytes23_to_h2(hi), c);
   const half8 r = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
@@ -195,6 +199,9 @@ __device__ __forceinline__ void skinny_tile(const float* S, int nrows, int lds, 
 // ============================================================== forward activation prep
 // ggml Q8_0 reference semantics: d = amax/127, id = d ? 1/d : 0, q = roundf(x*id) (ties away
 // from zero), stored scale fp16(d).
+// ggml Q8_K reference semantics (K-quant weights, one 256-column super-block per token and
+// workgroup): max = the signed element of largest |x| (the first one on ties), iscale = -127/max,
+// q = min(127, nearest-even(iscale*x)), d = 1/iscale (f32); all zero: d = 0, q = 0.
 // Grid (Tp/16, nq [+1]): workgroup (x, y < nq) quantises 16 tokens x RTQ_ACT_KQ columns, 256
 // threads; thread (token tl = tid/16, segment sg = tid%16) owns 16 consecutive columns (half a
 // block), so every load instruction of a wave covers four contiguous 1 KB row segments.
@@ -292,7 +299,8 @@ __device__ __forceinline__ float sum_partials(const float* p, int64_t e, int np)
   return s;
 }
 
-extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_0(ActArgs a) {
+template <bool QK>
+__device__ __forceinline__ void act_prep(const ActArgs& a) {
   constexpr int KQ = RTQ_ACT_KQ, LDX = KQ + 1;
   __shared__ float sx[16 * LDX];
   __shared__ float sa[16 * LDX];
@@ -305,17 +313,50 @@ extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_0(ActArgs a) {
     const int kk = k0 + sg * 16;  // first column of this thread's segment
     float v[16];
     load_seg(a.x + (int64_t)t * a.K + kk, t < a.T && kk < a.K, v);  // K % 32 == 0: all in or all out
-    float amax = 0.0f;
+    _Float16 q[16];  // codes: exact small integers
+    float dstore;    // the block scale as the dot products use it
+    if (!QK) {
+      float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1));  // the two halves of a block are adjacent lanes
-    if (kk < a.Kp) {
+      for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
+      amax = fmaxf(amax, __shfl_xor(amax, 1));  // the two halves of a block are adjacent lanes
       const float d = __fdiv_rn(amax, 127.0f);
       const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-      const int b = kk >> 5, hf = sg & 1, kc = b >> 2, j = b & 3;
-      _Float16 q[16];
 #pragma unroll
-      for (int i = 0; i < 16; i++) q[i] = (_Float16)roundf(__fmul_rn(v[i], id));  // exact small integers
+      for (int i = 0; i < 16; i++) q[i] = (_Float16)roundf(__fmul_rn(v[i], id));
+      dstore = (float)(_Float16)d;
+    } else {
+      // first element of largest |x| in this segment, then over the token's 16 adjacent lanes
+      // (larger |x| wins, equal |x|: the lower column)
+      float best = 0.0f, bmax = 0.0f;
+      int bi = 0;
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float ax = fabsf(v[i]);
+        if (ax > best) {
+          best = ax;
+          bmax = v[i];
+          bi = i;
+        }
+      }
+      bi += sg * 16;
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) {
+        const float ob = __shfl_xor(best, m), om = __shfl_xor(bmax, m);
+        const int oi = __shfl_xor(bi, m);
+        if (ob > best || (ob == best && oi < bi)) {
+          best = ob;
+          bmax = om;
+          bi = oi;
+        }
+      }
+      const float iscale = best != 0.0f ? __fdiv_rn(-127.0f, bmax) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; i++) q[i] = (_Float16)fminf(127.0f, rintf(__fmul_rn(iscale, v[i])));
+      dstore = best != 0.0f ? __fdiv_rn(1.0f, iscale) : 0.0f;
+    }
+    if (kk < a.Kp) {
+      const int b = kk >> 5, hf = sg & 1, kc = b >> 2, j = b & 3;
       // this half block gives, for each k-group g, the four codes of one 8-element fragment half
       u2v* xq = reinterpret_cast<u2v*>(a.xq) + ((((int64_t)(t >> 4) * Kc + kc) * 4 + j) * 64 + (t & 15)) * 2 + hf;
 #pragma unroll
@@ -326,7 +367,7 @@ extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_0(ActArgs a) {
         w.y = __builtin_bit_cast(uint32_t, hi);
         xq[g * 16 * 2] = w;
       }
-      if (hf == 0) a.xd[((int64_t)kc * a.Tp + t) * 4 + j] = (t < a.T && kk < a.K) ? (float)(_Float16)d : 0.0f;
+      if (hf == 0) a.xd[((int64_t)kc * a.Tp + t) * 4 + j] = (t < a.T && kk < a.K) ? dstore : 0.0f;
     }
   }
   if (a.zero_y && blockIdx.y == 0) {
@@ -340,6 +381,9 @@ extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_0(ActArgs a) {
     lora_partial<false>(a.x, a.T, a.K, a.A, a.K, a.r, a.r, k0, a.K, t0, a.hp, gridDim.y, blockIdx.y, sx, sa, red);
 }
 
+extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_0(ActArgs a) { act_prep<false>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_k(ActArgs a) { act_prep<true>(a); }
+
 // ============================================================== forward GEMM (Q4_0 / Q8_0)
 // MFMA orientation: A operand = 16 weight rows x 32 columns, B operand = 32 columns x 16 tokens,
 // so output lane l holds token l%16 and weight rows 4(l/16)..4(l/16)+3: one activation scale per
@@ -351,6 +395,15 @@ extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_0(ActArgs a) {
 // (clamped indices), so the wait for item i covers only the loads issued D - 1 items earlier.
 // Per block: one 16x16x32 f16 MFMA per (token tile, row group) gives the exact integer block
 // sums, then acc += isum * (d_w * d_x).
+// K-quants: the 6-bit sub-block scales are folded into the weight fragments, so the MFMA
+// accumulators sum whole super-blocks exactly (every partial is an integer below 2^24), and the
+// f32 epilogue runs once per super-block with the super-block's (d, dmin) and d_x:
+//   Q4_K: S1 = sum_j sc_j isum_j (fragment sc_j * u <= 945) and S2 = sum_j m_j bsum_j (fragment
+//         m_j: the MFMA sums the activation codes); y += (d d_x) S1 - (dmin d_x) S2;
+//   Q6_K: sc = 16 sh + sl (sh in [-8, 7], sl in [0, 15]) so that sh*q and sl*q stay exact f16
+//         integers; S = 16 S_hi + S_lo (one rounding, as the integer S converted to f32);
+//         y += (d d_x) S.
+// Wave w takes super-blocks w, w+4, ... (four half chunks each) instead of half chunks w, w+4.
 template <int FMT>
 struct WHalf;
 
@@ -358,7 +411,8 @@ template <>
 struct WHalf<FMT_Q4_0> {
   u2v q;  // blocks 2h, 2h+1 of the chunk: four code bytes each
   u4v d;  // eight fp16 scales: [j2][i] = row 4g+i, block 2h+j2
-  __device__ __forceinline__ void load(const void* wq, const uint16_t* wd, int rg, int kc, int h, int Kc, int lane) {
+  __device__ __forceinline__ void load(const void* wq, const uint16_t* wd, const uint32_t*, int rg, int kc, int h,
+                                       int Kc, int lane) {
     q = reinterpret_cast<const u2v*>(wq)[(((uint32_t)rg * Kc + kc) * 64 + lane) * 2 + h];
     d = reinterpret_cast<const u4v*>(wd)[(((uint32_t)rg * Kc + kc) * 2 + h) * 4 + (lane >> 4)];
   }
@@ -369,11 +423,63 @@ template <>
 struct WHalf<FMT_Q8_0> {
   u4v q;  // part h: block 2h in (x, y), block 2h+1 in (z, w)
   u4v d;
-  __device__ __forceinline__ void load(const void* wq, const uint16_t* wd, int rg, int kc, int h, int Kc, int lane) {
+  __device__ __forceinline__ void load(const void* wq, const uint16_t* wd, const uint32_t*, int rg, int kc, int h,
+                                       int Kc, int lane) {
     q = reinterpret_cast<const u4v*>(wq)[(((uint32_t)rg * Kc + kc) * 2 + h) * 64 + lane];
     d = reinterpret_cast<const u4v*>(wd)[(((uint32_t)rg * Kc + kc) * 2 + h) * 4 + (lane >> 4)];
   }
   __device__ __forceinline__ half8 frag(int j2) const { return j2 ? q8_frag(q.z, q.w) : q8_frag(q.x, q.y); }
+};
+
+// sub-block scale word (row lane % 16, blocks 2h, 2h+1) and super-block scales (rows 4g..4g+3)
+__device__ __forceinline__ void load_kscales(const uint16_t* wd, const uint32_t* wsb, int rg, int kc, int h, int Kc,
+                                             int lane, uint32_t& k, u4v& e) {
+  k = reinterpret_cast<const uint32_t*>(wd)[(((uint32_t)rg * Kc + kc) * 2 + h) * 16 + (lane & 15)];
+  e = reinterpret_cast<const u4v*>(wsb)[((uint32_t)rg * (Kc >> 1) + (kc >> 1)) * 4 + (lane >> 4)];
+}
+
+template <>
+struct WHalf<FMT_Q4_K> {
+  u2v q;       // unsigned codes, Q4_0 layout
+  uint32_t k;  // (sc | m << 8) of block 2h (low half) and 2h+1 (high half), row lane % 16
+  u4v e;       // (d | dmin << 16) of rows 4g..4g+3
+  __device__ __forceinline__ void load(const void* wq, const uint16_t* wd, const uint32_t* wsb, int rg, int kc, int h,
+                                       int Kc, int lane) {
+    q = reinterpret_cast<const u2v*>(wq)[(((uint32_t)rg * Kc + kc) * 64 + lane) * 2 + h];
+    load_kscales(wd, wsb, rg, kc, h, Kc, lane, k, e);
+  }
+  // f1 = sc * u (exact, <= 945), f2 = m (every element)
+  __device__ __forceinline__ void frags(int j2, half8& f1, half8& f2) const {
+    const uint32_t wv = j2 ? (k >> 16) : k;
+    const _Float16 sc = (_Float16)(float)(wv & 0x3fu), m = (_Float16)(float)((wv >> 8) & 0x3fu);
+    f1 = q4_0_frag<0>(j2 ? q.y : q.x) * sc;
+    const half8 mm = {m, m, m, m, m, m, m, m};
+    f2 = mm;
+  }
+};
+
+template <>
+struct WHalf<FMT_Q6_K> {
+  u4v q;       // int8 codes, Q8_0 layout
+  uint32_t k;  // (sc0 | sc1 << 8) of block 2h (low half) and 2h+1 (high half), row lane % 16
+  u4v e;       // (d | 0 << 16) of rows 4g..4g+3
+  __device__ __forceinline__ void load(const void* wq, const uint16_t* wd, const uint32_t* wsb, int rg, int kc, int h,
+                                       int Kc, int lane) {
+    q = reinterpret_cast<const u4v*>(wq)[(((uint32_t)rg * Kc + kc) * 2 + h) * 64 + lane];
+    load_kscales(wd, wsb, rg, kc, h, Kc, lane, k, e);
+  }
+  // f1 = sh * q, f2 = sl * q with sc = 16 sh + sl per 16-element sub-block (elements 0..3 of the
+  // fragment lie in the block's first sub-block, 4..7 in its second)
+  __device__ __forceinline__ void frags(int j2, half8& f1, half8& f2) const {
+    const uint32_t wv = j2 ? (k >> 16) : k;
+    const int s0 = (int)(int8_t)(wv & 0xffu), s1 = (int)(int8_t)((wv >> 8) & 0xffu);
+    const _Float16 h0 = (_Float16)(float)(s0 >> 4), h1 = (_Float16)(float)(s1 >> 4);
+    const _Float16 l0 = (_Float16)(float)(s0 & 15), l1 = (_Float16)(float)(s1 & 15);
+    const half8 qf = j2 ? q8_frag(q.z, q.w) : q8_frag(q.x, q.y);
+    const half8 sh = {h0, h0, h0, h0, h1, h1, h1, h1}, sl = {l0, l0, l0, l0, l1, l1, l1, l1};
+    f1 = qf * sh;
+    f2 = qf * sl;
+  }
 };
 
 // scale i (0..3) of block j2 from the 16-byte scale vector: fp16 number 4*j2 + i
@@ -393,6 +499,7 @@ struct FwdSlot {
 
 template <int FMT, int TT, int RG, int D, bool DBG>
 __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
+  constexpr bool KQ = is_kquant(FMT);
   __shared__ f4 red[4][TT * RG][64];
   __shared__ float sh[TT * 16][RTQ_LDS_RANK + 1];  // LoRA down projection rows of this tile's tokens
   __shared__ float sb[RG * 16][RTQ_LDS_RANK + 1];  // LoRA B rows of this tile
@@ -402,13 +509,28 @@ __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
   const int rg0 = blockIdx.x * RG, tt0 = blockIdx.y * TT;
   const int hc0 = blockIdx.z * a.kc_per_split * 2;
   const int hc1 = min(hc0 + a.kc_per_split * 2, 2 * Kc);
-  const int nit = hc1 - hc0 > w ? (hc1 - hc0 - w + 3) / 4 : 0;  // half chunks of this wave
+  // items (half chunks) of this wave; K-quant splits hold whole super-blocks (four half chunks)
+  int nit;
+  if (KQ) {
+    const int nsb = (hc1 - hc0) >> 2;
+    nit = nsb > w ? (nsb - w + 3) / 4 * 4 : 0;
+  } else {
+    nit = hc1 - hc0 > w ? (hc1 - hc0 - w + 3) / 4 : 0;
+  }
+  auto item_hc = [&](int it) { return KQ ? hc0 + 4 * (w + 4 * (it >> 2)) + (it & 3) : hc0 + w + 4 * it; };
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
   f4 acc[TT][RG];
+  f4 s1[KQ ? TT : 1][KQ ? RG : 1], s2[KQ ? TT : 1][KQ ? RG : 1];  // K-quant super-block sums
 #pragma unroll
   for (int i = 0; i < TT; i++)
 #pragma unroll
     for (int r = 0; r < RG; r++) acc[i][r] = zero;
+  if (KQ) {
+#pragma unroll
+    for (int i = 0; i < (KQ ? TT : 1); i++)
+#pragma unroll
+      for (int r = 0; r < (KQ ? RG : 1); r++) s1[i][r] = s2[i][r] = zero;
+  }
 
   const u4v* XQ = reinterpret_cast<const u4v*>(a.xq);
   const float2* XD = reinterpret_cast<const float2*>(a.xd);
@@ -423,10 +545,10 @@ __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
   const bool lora_lds = lora && a.r <= RTQ_LDS_RANK;
 
   auto issue = [&](FwdSlot<FMT, TT, RG>& S, int it) {
-    const int hc = min(hc0 + w + 4 * min(it, max(nit - 1, 0)), 2 * Kc - 1);  // clamped: always a valid half chunk
+    const int hc = min(item_hc(min(it, max(nit - 1, 0))), 2 * Kc - 1);  // clamped: always a valid half chunk
     const int kc = hc >> 1, h = hc & 1;
 #pragma unroll
-    for (int r = 0; r < RG; r++) S.w[r].load(a.wq, a.wd, rgc[r], kc, h, Kc, lane);
+    for (int r = 0; r < RG; r++) S.w[r].load(a.wq, a.wd, a.wsb, rgc[r], kc, h, Kc, lane);
 #pragma unroll
     for (int i = 0; i < TT; i++) {
       const uint32_t base = (((uint32_t)ttc[i] * Kc + kc) * 4 + 2 * h) * 64 + lane;
@@ -438,34 +560,86 @@ __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
     }
   };
   auto compute = [&](const FwdSlot<FMT, TT, RG>& S, int it) {
-    const int hc = hc0 + w + 4 * it;
+    const int hc = item_hc(it);
+    if constexpr (KQ) {
 #pragma unroll
-    for (int j2 = 0; j2 < 2; j2++) {
-      half8 wf[RG];
-      float sc[RG][4];
+      for (int j2 = 0; j2 < 2; j2++) {
+        half8 f1[RG], f2[RG];
 #pragma unroll
-      for (int r = 0; r < RG; r++) {
-        wf[r] = S.w[r].frag(j2);
+        for (int r = 0; r < RG; r++) S.w[r].frags(j2, f1[r], f2[r]);
 #pragma unroll
-        for (int i = 0; i < 4; i++) sc[r][i] = wscale(S.w[r].d, j2, i);
+        for (int i = 0; i < TT; i++) {
+          const half8 xf = __builtin_bit_cast(half8, S.x[i][j2]);
+#pragma unroll
+          for (int r = 0; r < RG; r++) {
+            s1[i][r] = mfma_f16(f1[r], xf, s1[i][r]);
+            s2[i][r] = mfma_f16(f2[r], xf, s2[i][r]);
+          }
+        }
       }
+      if ((it & 3) == 3) {  // last half chunk of the super-block: f32 epilogue, then restart the sums
+        const int sb = hc >> 2, nsb = a.K / 256;
 #pragma unroll
-      for (int i = 0; i < TT; i++) {
-        const half8 xf = __builtin_bit_cast(half8, S.x[i][j2]);
-        const float xs = S.xs[i][j2];
+        for (int i = 0; i < TT; i++) {
+          const float xs = S.xs[i][0];  // the super-block's Q8_K d of token li
 #pragma unroll
-        for (int r = 0; r < RG; r++) {
-          const f4 c = mfma_f16(wf[r], xf, zero);
-          if (DBG) {
-            const int t = (tt0 + i) * 16 + li, b = hc * 2 + j2, nb = a.K / 32;
+          for (int r = 0; r < RG; r++) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-              const int n = (rg0 + r) * 16 + 4 * g + e;
-              if (t < a.T && n < a.N && b < nb) a.isums[((int64_t)t * a.N + n) * nb + b] = (int32_t)c[e];
+              const uint32_t ev = comp(S.w[r].e, e);
+              const float dd = h2f((uint16_t)(ev & 0xffffu)) * xs;
+              if (FMT == FMT_Q4_K) {
+                const float dm = h2f((uint16_t)(ev >> 16)) * xs;
+                acc[i][r][e] = fmaf(dd, s1[i][r][e], fmaf(-dm, s2[i][r][e], acc[i][r][e]));
+              } else {
+                acc[i][r][e] = fmaf(dd, fmaf(16.0f, s1[i][r][e], s2[i][r][e]), acc[i][r][e]);
+              }
+              if (DBG) {
+                const int t = (tt0 + i) * 16 + li, n = (rg0 + r) * 16 + 4 * g + e;
+                if (t < a.T && n < a.N && sb < nsb) {
+                  if (FMT == FMT_Q4_K) {
+                    a.isums[(((int64_t)t * a.N + n) * nsb + sb) * 2] = (int32_t)s1[i][r][e];
+                    a.isums[(((int64_t)t * a.N + n) * nsb + sb) * 2 + 1] = (int32_t)s2[i][r][e];
+                  } else {
+                    a.isums[((int64_t)t * a.N + n) * nsb + sb] = 16 * (int32_t)s1[i][r][e] + (int32_t)s2[i][r][e];
+                  }
+                }
+              }
             }
+            s1[i][r] = zero;
+            s2[i][r] = zero;
           }
+        }
+      }
+    } else {
 #pragma unroll
-          for (int e = 0; e < 4; e++) acc[i][r][e] = fmaf(c[e], sc[r][e] * xs, acc[i][r][e]);
+      for (int j2 = 0; j2 < 2; j2++) {
+        half8 wf[RG];
+        float sc[RG][4];
+#pragma unroll
+        for (int r = 0; r < RG; r++) {
+          wf[r] = S.w[r].frag(j2);
+#pragma unroll
+          for (int i = 0; i < 4; i++) sc[r][i] = wscale(S.w[r].d, j2, i);
+        }
+#pragma unroll
+        for (int i = 0; i < TT; i++) {
+          const half8 xf = __builtin_bit_cast(half8, S.x[i][j2]);
+          const float xs = S.xs[i][j2];
+#pragma unroll
+          for (int r = 0; r < RG; r++) {
+            const f4 c = mfma_f16(wf[r], xf, zero);
+            if (DBG) {
+              const int t = (tt0 + i) * 16 + li, b = hc * 2 + j2, nb = a.K / 32;
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                const int n = (rg0 + r) * 16 + 4 * g + e;
+                if (t < a.T && n < a.N && b < nb) a.isums[((int64_t)t * a.N + n) * nb + b] = (int32_t)c[e];
+              }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[i][r][e] = fmaf(c[e], sc[r][e] * xs, acc[i][r][e]);
+          }
         }
       }
     }
@@ -585,6 +759,14 @@ RTQ_FWD(rtq_fwd_q4_0_w_isums, FMT_Q4_0, 4, 3, 2, true)
 RTQ_FWD(rtq_fwd_q4_0_s_isums, FMT_Q4_0, 1, 4, 4, true)
 RTQ_FWD(rtq_fwd_q8_0_w_isums, FMT_Q8_0, 4, 3, 2, true)
 RTQ_FWD(rtq_fwd_q8_0_s_isums, FMT_Q8_0, 1, 4, 4, true)
+RTQ_FWD(rtq_fwd_q4_k_w, FMT_Q4_K, 4, 2, 2, false)
+RTQ_FWD(rtq_fwd_q4_k_s, FMT_Q4_K, 1, 4, 4, false)
+RTQ_FWD(rtq_fwd_q6_k_w, FMT_Q6_K, 4, 2, 2, false)
+RTQ_FWD(rtq_fwd_q6_k_s, FMT_Q6_K, 1, 4, 4, false)
+RTQ_FWD(rtq_fwd_q4_k_w_isums, FMT_Q4_K, 4, 2, 2, true)
+RTQ_FWD(rtq_fwd_q4_k_s_isums, FMT_Q4_K, 1, 4, 4, true)
+RTQ_FWD(rtq_fwd_q6_k_w_isums, FMT_Q6_K, 4, 2, 2, true)
+RTQ_FWD(rtq_fwd_q6_k_s_isums, FMT_Q6_K, 1, 4, 4, true)
 
 // ============================================================== backward preparation
 // Grid (ceil(T/16), nhq + ngq), 256 threads (src/linear.rs:106-111); nhq, ngq multiples of 4:
@@ -612,9 +794,10 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_prep(BwdPrepArgs a) {
 // partial tile part[z][t][k] (plain stores; rtq_bwd_finish sums the splits in order).  Per
 // 32-row step the workgroup stages, double buffered in LDS:
 //   * dy[64 x 32] as bf16 hi/lo A fragments: each thread loads one float4 and splits it;
-//   * W[32 x 128] dequantised (d*q: at most 15 significant bits, exact in f32), split exactly into
-//     bf16 hi + lo by truncation, stored transposed ([k][n]) so a lane reads its B fragment
-//     (8 consecutive rows of one column) in 16 bytes.
+//   * W[32 x 128] dequantised (Q4_0, Q8_0: d*q, at most 15 significant bits; Q6_K: (d*sc)*q, at
+//     most 23; Q4_K: (d*sc)*u - dmin*m rounded once, as ggml's dequantisation), split into bf16
+//     hi + lo by truncation (exact for Q4_0 / Q8_0), stored transposed ([k][n]) so a lane reads
+//     its B fragment (8 consecutive rows of one column) in 16 bytes.
 // Three bf16 MFMAs per product (dh.wh + dl.wh + dh.wl): the missing dl.wl term and the
 // truncation of dl leave a relative error near 2^-16 per product.
 // Global loads go through buffer descriptors: a per-thread 32-bit offset plus a per-step scalar
@@ -635,6 +818,15 @@ struct DxSlot {
   uint32_t q[2];  // the four codes this thread converts, of rows 2p and 2p+1
   uint32_t d;     // fp16 scales of rows 2p (low half) and 2p+1 (high half)
 };
+template <>
+struct DxSlot<FMT_Q4_K> {
+  f4 dy;
+  uint32_t q[2];
+  u2v k;  // sub-block scale words of rows 2p, 2p+1 (blocks 2h, 2h+1 of the chunk)
+  u2v e;  // super-block (d, dmin) of rows 2p, 2p+1
+};
+template <>
+struct DxSlot<FMT_Q6_K> : DxSlot<FMT_Q4_K> {};
 
 template <int FMT>
 __device__ __forceinline__ void dx_tile(const DxArgs& a) {
@@ -691,20 +883,26 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   const int wp = qp & 7, wgg = qp >> 3;   // rows 2wp, 2wp+1 of row group rgl; k-group wgg
   const int li0 = 2 * wp, FL0 = 16 * wgg + li0;
   const int nloc = rgl * 16 + li0;         // first of the two rows within the step
-  const uint32_t wq_bytes = (uint32_t)(a.Np / 16) * Kc * 64 * 16 * (FMT == FMT_Q8_0 ? 2 : 1);
+  constexpr bool KQ = is_kquant(FMT), B8 = byte_codes(FMT);
+  const uint32_t wq_bytes = (uint32_t)(a.Np / 16) * Kc * 64 * 16 * (B8 ? 2 : 1);
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.wq, wq_bytes);
   const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.wd, (uint32_t)(a.Np / 16) * Kc * 128);
+  const __amdgpu_buffer_rsrc_t re = make_rsrc(a.wsb, KQ ? (uint32_t)(a.Np / 16) * Kc * 32 : 0u);
   uint32_t q_off[2];
 #pragma unroll
   for (int r = 0; r < 2; r++) {
-    if (FMT == FMT_Q4_0)
+    if (!B8)
       q_off[r] = ((((uint32_t)rgl * Kc + kc) * 64 + FL0 + r) * 4 + jb) * 4u;
     else
       q_off[r] = ((((((uint32_t)rgl * Kc + kc) * 2 + (jb >> 1)) * 64 + FL0 + r) * 2 + (jb & 1)) * 2 + hh) * 4u;
   }
-  const uint32_t d_off = (uint32_t)RTQ_WD_INDEX(rgl, kc, Kc, li0, jb) * 2u;  // rows li0, li0+1 adjacent
-  const uint32_t q_rg = (uint32_t)Kc * 64 * 16 * (FMT == FMT_Q8_0 ? 2 : 1);  // bytes per row group
-  const uint32_t d_rg = (uint32_t)Kc * 128;
+  // scales of rows li0, li0+1: adjacent fp16 (Q4_0, Q8_0); for K-quants the two rows' sub-block
+  // words (one 8-byte load) and super-block pairs (one 8-byte load)
+  const uint32_t d_off = KQ ? (uint32_t)RTQ_WK_INDEX(rgl, kc, Kc, li0, jb & 2) * 2u
+                            : (uint32_t)RTQ_WD_INDEX(rgl, kc, Kc, li0, jb) * 2u;
+  const uint32_t e_off = (uint32_t)RTQ_WSB_INDEX(rgl, kc >> 1, Kc >> 1, li0) * 4u;
+  const uint32_t q_rg = (uint32_t)Kc * 64 * 16 * (B8 ? 2 : 1);  // bytes per row group
+  const uint32_t d_rg = (uint32_t)Kc * 128, e_rg = (uint32_t)Kc * 32;
 
   DxSlot<FMT> sl[D];
   auto issue = [&](DxSlot<FMT>& S, int step) {
@@ -724,7 +922,12 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
     }
 #pragma unroll
     for (int r = 0; r < 2; r++) S.q[r] = __builtin_amdgcn_raw_buffer_load_b32(rq, q_off[r], srg * q_rg, 0);
-    S.d = __builtin_amdgcn_raw_buffer_load_b32(rd, d_off, srg * d_rg, 0);
+    if constexpr (KQ) {
+      S.k = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(rd, d_off, srg * d_rg, 0));
+      S.e = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(re, e_off, srg * e_rg, 0));
+    } else {
+      S.d = __builtin_amdgcn_raw_buffer_load_b32(rd, d_off, srg * d_rg, 0);
+    }
   };
   auto stage_compute = [&](const DxSlot<FMT>& S, int buf) {
     {  // dy: A fragment tile tl>>4, lane (tl&15) + 16*(q4>>1), slots 4*(q4&1) .. +3
@@ -747,20 +950,29 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
       uint32_t vb[2][4], lb[2][4];
 #pragma unroll
       for (int r = 0; r < 2; r++) {
-        const float d = h2f((uint16_t)(r ? (S.d >> 16) : (S.d & 0xffffu)));
-        // unsigned byte codes u and offset o with value (u - o) * d: Q4_0 nibble - 8, Q8_0 (q ^ 0x80) - 128
-        uint32_t u;
-        float m;
-        if (FMT == FMT_Q4_0) {
-          u = (hh ? (S.q[r] >> 4) : S.q[r]) & 0x0f0f0f0fu;
-          m = -8.0f * d;
+        // unsigned byte codes u with value u * d + m:
+        //   Q4_0 (nibble - 8) d;  Q8_0 ((q ^ 0x80) - 128) d;  Q4_K (d sc) u - dmin m;
+        //   Q6_K ((q ^ 0x80) - 128) (d sc), sc of the 16-element half hh
+        float d, m;
+        if constexpr (KQ) {
+          const uint32_t kw = (r ? S.k.y : S.k.x) >> (16 * (jb & 1)), ev = r ? S.e.y : S.e.x;
+          const float dsb = h2f((uint16_t)(ev & 0xffffu));
+          if (FMT == FMT_Q4_K) {
+            d = dsb * (float)(kw & 0x3fu);                         // exact products
+            m = -(h2f((uint16_t)(ev >> 16)) * (float)((kw >> 8) & 0x3fu));
+          } else {
+            d = dsb * (float)(int)(int8_t)((kw >> (8 * hh)) & 0xffu);
+            m = -128.0f * d;
+          }
         } else {
-          u = S.q[r] ^ 0x80808080u;
-          m = -128.0f * d;
+          d = h2f((uint16_t)(r ? (S.d >> 16) : (S.d & 0xffffu)));
+          m = (FMT == FMT_Q4_0 ? -8.0f : -128.0f) * d;
         }
+        const uint32_t u = B8 ? S.q[r] ^ 0x80808080u : (hh ? (S.q[r] >> 4) : S.q[r]) & 0x0f0f0f0fu;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          const float v = fmaf((float)((u >> (8 * e)) & 0xffu), d, m);  // exact: <= 15 significant bits
+          // the dequantised value, rounded once (exact for Q4_0, Q8_0 and Q6_K)
+          const float v = fmaf((float)((u >> (8 * e)) & 0xffu), d, m);
           vb[r][e] = __builtin_bit_cast(uint32_t, v);
           lb[r][e] = __builtin_bit_cast(uint32_t, v - __builtin_bit_cast(float, vb[r][e] & 0xffff0000u));
         }
@@ -813,6 +1025,8 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
 
 extern "C" __global__ __launch_bounds__(512) void rtq_dx_q4_0(DxArgs a) { dx_tile<FMT_Q4_0>(a); }
 extern "C" __global__ __launch_bounds__(512) void rtq_dx_q8_0(DxArgs a) { dx_tile<FMT_Q8_0>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dx_q4_k(DxArgs a) { dx_tile<FMT_Q4_K>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dx_q6_k(DxArgs a) { dx_tile<FMT_Q6_K>(a); }
 
 // ============================================================== backward finish
 // dx[t][k] = [dx[t][k] +] sum over splits s (in order) of the partials [+ sum_j g[t][j] A[j][k]]
@@ -978,3 +1192,51 @@ extern "C" __global__ __launch_bounds__(256) void rtq_rows_q8_0(RowArgs a) {
     }
   }
 }
+
+// K-quants, one thread per (row, 32-element block), bit-exact with ggml's dequantisation:
+//   Q4_K: (d*sc)*u - dmin*m (two roundings at most: the products are exact);
+//   Q6_K: (d*sc)*q, sc of each 16-element half (exact product, then one rounding).
+template <int FMT>
+__device__ __forceinline__ void rows_kquant(const RowArgs& a) {
+  const int nb = a.K / 32, Kc = a.Kp / 128;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)a.count * nb) return;
+  const int rl = (int)(idx / nb), b = (int)(idx % nb);
+  const int n = a.r0 + rl, rg = n >> 4, li = n & 15, kc = b >> 2, j = b & 3;
+  const uint32_t kw = a.wd[RTQ_WK_INDEX(rg, kc, Kc, li, j)];
+  const uint32_t ev = a.wsb[RTQ_WSB_INDEX(rg, kc >> 1, Kc >> 1, li)];
+  const float dsb = h2f((uint16_t)(ev & 0xffffu));
+  float* out = a.out + (int64_t)rl * a.K + b * 32;
+  if (FMT == FMT_Q4_K) {
+    const float sc = __fmul_rn(dsb, (float)(kw & 0x3fu));
+    const float mn = __fmul_rn(h2f((uint16_t)(ev >> 16)), (float)((kw >> 8) & 0x3fu));
+    const u4v* q = reinterpret_cast<const u4v*>(a.wq) + (int64_t)(rg * Kc + kc) * 64;
+#pragma unroll
+    for (int gg = 0; gg < 4; gg++) {
+      const uint32_t w = comp(q[li + 16 * gg], j);
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        const uint32_t byte = (w >> (8 * s)) & 0xffu;
+        out[4 * gg + s] = __fsub_rn(__fmul_rn(sc, (float)(byte & 0xfu)), mn);
+        out[16 + 4 * gg + s] = __fsub_rn(__fmul_rn(sc, (float)(byte >> 4)), mn);
+      }
+    }
+  } else {
+    const float s0 = __fmul_rn(dsb, (float)(int)(int8_t)(kw & 0xffu));
+    const float s1 = __fmul_rn(dsb, (float)(int)(int8_t)((kw >> 8) & 0xffu));
+    const u4v* q = reinterpret_cast<const u4v*>(a.wq) + (int64_t)(rg * Kc + kc) * 128 + (j >> 1) * 64;
+#pragma unroll
+    for (int gg = 0; gg < 4; gg++) {
+      const u4v v = q[li + 16 * gg];
+      const uint32_t lo = (j & 1) ? v.z : v.x, hi = (j & 1) ? v.w : v.y;
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        out[4 * gg + s] = __fmul_rn(s0, (float)(int8_t)((lo >> (8 * s)) & 0xffu));
+        out[16 + 4 * gg + s] = __fmul_rn(s1, (float)(int8_t)((hi >> (8 * s)) & 0xffu));
+      }
+    }
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void rtq_rows_q4_k(RowArgs a) { rows_kquant<FMT_Q4_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_rows_q6_k(RowArgs a) { rows_kquant<FMT_Q6_K>(a); }

@@ -104,30 +104,33 @@ float f16_bits_to_f32(uint16_t h) {
   return f;
 }
 
+// format index of the per-format kernel tables: Q4_0, Q8_0, Q4_K, Q6_K
+enum { F_Q4_0, F_Q8_0, F_Q4_K, F_Q6_K, F_COUNT };
+
 enum Kid {
   K_FILL,
-  K_ACT_PREP,
-  K_FWD_Q4_0_W,
-  K_FWD_Q4_0_S,
-  K_FWD_Q8_0_W,
-  K_FWD_Q8_0_S,
-  K_FWD_Q4_0_W_ISUMS,
-  K_FWD_Q4_0_S_ISUMS,
-  K_FWD_Q8_0_W_ISUMS,
-  K_FWD_Q8_0_S_ISUMS,
-  K_BWD_PREP,
-  K_DX_Q4_0,
-  K_DX_Q8_0,
-  K_BWD_FINISH,
-  K_ROWS_Q4_0,
-  K_ROWS_Q8_0,
-  K_COUNT
+  K_ACT_PREP,    // Q8_0 activations (Q4_0, Q8_0 weights)
+  K_ACT_PREP_K,  // Q8_K activations (Q4_K, Q6_K weights)
+  K_FWD_W,       // + format: wide forward GEMM
+  K_FWD_S = K_FWD_W + F_COUNT,            // skinny (t <= 16)
+  K_FWD_W_ISUMS = K_FWD_S + F_COUNT,      // debug variants writing the integer sums
+  K_FWD_S_ISUMS = K_FWD_W_ISUMS + F_COUNT,
+  K_BWD_PREP = K_FWD_S_ISUMS + F_COUNT,
+  K_DX,          // + format
+  K_BWD_FINISH = K_DX + F_COUNT,
+  K_ROWS,        // + format
+  K_COUNT = K_ROWS + F_COUNT
 };
 const char* kKernelNames[K_COUNT] = {
-    "rtq_fill_zero",        "rtq_act_prep_q8_0",    "rtq_fwd_q4_0_w",       "rtq_fwd_q4_0_s",
-    "rtq_fwd_q8_0_w",       "rtq_fwd_q8_0_s",       "rtq_fwd_q4_0_w_isums", "rtq_fwd_q4_0_s_isums",
-    "rtq_fwd_q8_0_w_isums", "rtq_fwd_q8_0_s_isums", "rtq_bwd_prep",          "rtq_dx_q4_0",
-    "rtq_dx_q8_0",          "rtq_bwd_finish",       "rtq_rows_q4_0",        "rtq_rows_q8_0"};
+    "rtq_fill_zero",        "rtq_act_prep_q8_0",    "rtq_act_prep_q8_k",
+    "rtq_fwd_q4_0_w",       "rtq_fwd_q8_0_w",       "rtq_fwd_q4_k_w",       "rtq_fwd_q6_k_w",
+    "rtq_fwd_q4_0_s",       "rtq_fwd_q8_0_s",       "rtq_fwd_q4_k_s",       "rtq_fwd_q6_k_s",
+    "rtq_fwd_q4_0_w_isums", "rtq_fwd_q8_0_w_isums", "rtq_fwd_q4_k_w_isums", "rtq_fwd_q6_k_w_isums",
+    "rtq_fwd_q4_0_s_isums", "rtq_fwd_q8_0_s_isums", "rtq_fwd_q4_k_s_isums", "rtq_fwd_q6_k_s_isums",
+    "rtq_bwd_prep",
+    "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
+    "rtq_bwd_finish",
+    "rtq_rows_q4_0",        "rtq_rows_q8_0",        "rtq_rows_q4_k",        "rtq_rows_q6_k"};
 
 struct TimedLaunch {
   int kid;
@@ -163,6 +166,7 @@ struct rtq_weight {
   void* dmem = nullptr;
   void* wq = nullptr;
   uint16_t* wd = nullptr;
+  uint32_t* wsb = nullptr;  // K-quant super-block scales, else null
 };
 
 namespace {
@@ -232,7 +236,18 @@ rtq_status ensure_ws(rtq_ctx* c, size_t bytes) {
 }
 
 bool is_q32(int type) { return type == RTQ_TYPE_Q4_0 || type == RTQ_TYPE_Q8_0; }
-bool supported(int type) { return is_q32(type); }
+bool is_kquant(int type) { return type == RTQ_TYPE_Q4_K || type == RTQ_TYPE_Q6_K; }
+bool supported(int type) { return is_q32(type) || is_kquant(type); }
+int fmt_index(int type) {
+  switch (type) {
+    case RTQ_TYPE_Q4_0: return F_Q4_0;
+    case RTQ_TYPE_Q8_0: return F_Q8_0;
+    case RTQ_TYPE_Q4_K: return F_Q4_K;
+    default: return F_Q6_K;
+  }
+}
+// device codes are bytes (Q8_0 layout) for Q8_0 and Q6_K, nibbles (Q4_0 layout) otherwise
+bool byte_codes(int type) { return type == RTQ_TYPE_Q8_0 || type == RTQ_TYPE_Q6_K; }
 
 int64_t block_elems(int type) { return is_q32(type) ? 32 : 256; }
 int64_t block_bytes(int type) {
@@ -254,8 +269,9 @@ struct FwdPlan {
   size_t xq_bytes, xd_floats, h_floats;
 };
 
-constexpr int kFwdWideTT = 4, kFwdWideRG = 3;    // rtq_fwd_*_w: 64 tokens x 48 rows per workgroup
-constexpr int kFwdSkinnyRG = 4;                   // rtq_fwd_*_s: 16 tokens x 64 rows per workgroup
+constexpr int kFwdWideTT = 4;     // rtq_fwd_*_w: 64 tokens x (16 * wide_rg) rows per workgroup
+constexpr int kFwdSkinnyRG = 4;   // rtq_fwd_*_s: 16 tokens x 64 rows per workgroup
+int wide_rg(int type) { return is_kquant(type) ? 2 : 3; }
 
 FwdPlan fwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
   FwdPlan p;
@@ -291,25 +307,29 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   float* hp = lora ? ar.take<float>(p.h_floats) : nullptr;
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   const int64_t Kc = w->Kp / 128;
-  const int64_t rg_per_wg = p.skinny ? kFwdSkinnyRG : kFwdWideRG;
+  const bool kq = is_kquant(w->type);
+  const int64_t rg_per_wg = p.skinny ? kFwdSkinnyRG : wide_rg(w->type);
   const int64_t gx = cdiv(w->Np / 16, rg_per_wg), gy = p.Tp / (p.skinny ? 16 : 16 * kFwdWideTT);
   const int64_t tiles = gx * gy;
   // split K across workgroups when the output alone gives too few of them (atomics into a
-  // zeroed y); every split keeps at least two chunks, i.e. one half chunk per wave
+  // zeroed y); every split keeps at least one half chunk per wave (K-quants: one super-block of
+  // two chunks per wave, and splits on super-block boundaries)
   int64_t ks = 1;
   if (!isums && tiles < c->cu_count) {
     const int64_t want = cdiv(p.skinny ? 2 * c->cu_count : c->cu_count, tiles);
-    ks = std::max<int64_t>(1, std::min<int64_t>(want, Kc / 2));
+    ks = std::max<int64_t>(1, std::min<int64_t>(want, Kc / (kq ? 8 : 2)));
   }
-  const int64_t kcps = cdiv(Kc, ks);
+  int64_t kcps = cdiv(Kc, ks);
+  if (kq) kcps = roundup(kcps, 2);
   ks = cdiv(Kc, kcps);
 
   ActArgs aa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xq, xd, lora ? la : nullptr, (int)r, hp,
              ks > 1 ? y : nullptr, (int)w->rows};
-  RTQ_TRY(launch(c, K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp), dim3(256), st, aa));
+  RTQ_TRY(launch(c, kq ? K_ACT_PREP_K : K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp), dim3(256), st, aa));
   FwdArgs fa{};
   fa.wq = w->wq;
   fa.wd = w->wd;
+  fa.wsb = w->wsb;
   fa.Np = (int)w->Np;
   fa.Kp = (int)w->Kp;
   fa.xq = xq;
@@ -327,12 +347,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   fa.r = (int)r;
   fa.s = s;
   fa.isums = isums;
-  const bool q4 = w->type == RTQ_TYPE_Q4_0;
-  int kid;
-  if (p.skinny)
-    kid = isums ? (q4 ? K_FWD_Q4_0_S_ISUMS : K_FWD_Q8_0_S_ISUMS) : (q4 ? K_FWD_Q4_0_S : K_FWD_Q8_0_S);
-  else
-    kid = isums ? (q4 ? K_FWD_Q4_0_W_ISUMS : K_FWD_Q8_0_W_ISUMS) : (q4 ? K_FWD_Q4_0_W : K_FWD_Q8_0_W);
+  const int kid = (p.skinny ? (isums ? K_FWD_S_ISUMS : K_FWD_S) : (isums ? K_FWD_W_ISUMS : K_FWD_W)) + fmt_index(w->type);
   return launch(c, kid, dim3((unsigned)gx, (unsigned)gy, (unsigned)ks), dim3(256), st, fa);
 }
 
@@ -380,9 +395,9 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
     BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq};
     RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, 16), (unsigned)(nhq + ngq)), dim3(256), st, pa));
   }
-  DxArgs xa{w->wq, w->wd, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, (int)dp.splits, part,
+  DxArgs xa{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, (int)dp.splits, part,
             lora ? hp : nullptr, lora ? gp : nullptr, (int)nhq, (int)ngq, (int)r, s, h, g};
-  const int kid = w->type == RTQ_TYPE_Q4_0 ? K_DX_Q4_0 : K_DX_Q8_0;
+  const int kid = K_DX + fmt_index(w->type);
   const int64_t nmain = (w->Kp / 128) * cdiv(t, 64) * dp.splits;
   const int64_t nfin = lora ? std::min<int64_t>(64, cdiv(t * r, 512)) : 0;  // LoRA finalisers
   RTQ_TRY(launch(c, kid, dim3((unsigned)(nmain + nfin)), dim3(512), st, xa));
@@ -423,42 +438,95 @@ rtq_status check_t(int64_t t) {
 // ------------------------------------------------------------------ weight repack (host)
 // GGUF blocks -> fragment layout (see rtq_kargs.h).  Padding rows/blocks get scale 0 and
 // zero-valued codes.
+
+// Places the codes of block j of chunk kc, row li of row group rg.  Nibble layouts take 16 bytes
+// (element e in the low nibble of byte e, element e + 16 in its high nibble), byte layouts 32.
+void place_codes(bool bytes, const uint8_t* codes, int64_t rg, int64_t kc, int64_t li, int64_t j, int64_t Kc,
+                 uint8_t* wq) {
+  if (!bytes) {
+    for (int g = 0; g < 4; g++) memcpy(wq + ((rg * Kc + kc) * 64 + li + 16 * g) * 16 + j * 4, codes + 4 * g, 4);
+    return;
+  }
+  const int64_t part = j / 2, off = (j % 2) * 8;
+  for (int g = 0; g < 4; g++) {
+    uint8_t* dst = wq + (((rg * Kc + kc) * 2 + part) * 64 + li + 16 * g) * 16 + off;
+    memcpy(dst, codes + 4 * g, 4);
+    memcpy(dst + 4, codes + 16 + 4 * g, 4);
+  }
+}
+
+inline uint16_t le16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
 void repack_q32(int type, const uint8_t* src, int64_t N, int64_t K, int64_t Np, int64_t Kp, uint8_t* wq,
                 uint16_t* wd) {
   const int64_t Kc = Kp / 128, nb = K / 32, nbp = Kp / 32, bb = block_bytes(type), rb = nb * bb;
+  const bool q4 = type == RTQ_TYPE_Q4_0;
   for (int64_t n = 0; n < Np; n++) {
     const int64_t rg = n / 16, li = n % 16;
     for (int64_t b = 0; b < nbp; b++) {
       const int64_t kc = b / 4, j = b % 4;
       uint16_t d = 0;
       uint8_t codes[32];
-      const bool real = n < N && b < nb;
-      if (type == RTQ_TYPE_Q4_0) {
-        if (real) {
-          const uint8_t* blk = src + n * rb + b * bb;
-          d = (uint16_t)(blk[0] | (blk[1] << 8));
-          memcpy(codes, blk + 2, 16);
-        } else {
-          memset(codes, 0x88, 16);
-        }
-        for (int g = 0; g < 4; g++)
-          memcpy(wq + ((rg * Kc + kc) * 64 + li + 16 * g) * 16 + j * 4, codes + 4 * g, 4);
+      if (n < N && b < nb) {
+        const uint8_t* blk = src + n * rb + b * bb;
+        d = le16(blk);
+        memcpy(codes, blk + 2, q4 ? 16 : 32);
       } else {
-        if (real) {
-          const uint8_t* blk = src + n * rb + b * bb;
-          d = (uint16_t)(blk[0] | (blk[1] << 8));
-          memcpy(codes, blk + 2, 32);
-        } else {
-          memset(codes, 0, 32);
-        }
-        const int64_t part = j / 2, off = (j % 2) * 8;
-        for (int g = 0; g < 4; g++) {
-          uint8_t* dst = wq + (((rg * Kc + kc) * 2 + part) * 64 + li + 16 * g) * 16 + off;
-          memcpy(dst, codes + 4 * g, 4);
-          memcpy(dst + 4, codes + 16 + 4 * g, 4);
-        }
+        memset(codes, q4 ? 0x88 : 0, 32);  // code value 0
       }
+      place_codes(!q4, codes, rg, kc, li, j, Kc, wq);
       wd[RTQ_WD_INDEX(rg, kc, Kc, li, j)] = d;
+    }
+  }
+}
+
+// GGUF Q4_K / Q6_K super-blocks (ggml layouts) -> the Q4_0 / Q8_0 code layouts, the integer
+// sub-block scales (wd) and the fp16 super-block scales (wsb), see rtq_kargs.h.
+//   Q4_K (144 B): fp16 d, fp16 dmin, 12 bytes of 6-bit (sc, m) for 8 sub-blocks, 128 bytes of
+//     nibbles: sub-block 2c takes the low nibbles of bytes 32c..32c+31, sub-block 2c+1 the high;
+//     sub-block j < 4: sc = s[j] & 63, m = s[j+4] & 63; j >= 4: the low / high nibble of s[j+4]
+//     with the top two bits of s[j-4] (sc) / s[j] (m) above them.
+//   Q6_K (210 B): ql[128], qh[64], int8 sc[16], fp16 d; element 128h + 32m + l has the low four
+//     bits of ql[64h + l + 32(m & 1)] (low nibble for m < 2, else high) and the two bits
+//     (qh[32h + l] >> 2m) & 3 above them, minus 32; sc[e / 16] scales element e.
+void repack_kquant(int type, const uint8_t* src, int64_t N, int64_t K, int64_t Np, int64_t Kp, uint8_t* wq,
+                   uint16_t* wd, uint32_t* wsb) {
+  const int64_t Kc = Kp / 128, Ksb = Kp / 256, nsb = K / 256, bb = block_bytes(type), rb = nsb * bb;
+  const bool q4k = type == RTQ_TYPE_Q4_K;
+  for (int64_t n = 0; n < Np; n++) {
+    const int64_t rg = n / 16, li = n % 16;
+    for (int64_t sb = 0; sb < Ksb; sb++) {
+      const uint8_t* blk = (n < N && sb < nsb) ? src + n * rb + sb * bb : nullptr;
+      uint32_t dd = 0;
+      if (blk) dd = q4k ? (uint32_t)le16(blk) | ((uint32_t)le16(blk + 2) << 16) : (uint32_t)le16(blk + 208);
+      wsb[RTQ_WSB_INDEX(rg, sb, Ksb, li)] = dd;
+      for (int jj = 0; jj < 8; jj++) {
+        const int64_t b = sb * 8 + jj, kc = b / 4, j = b % 4;
+        uint8_t codes[32] = {};
+        uint16_t word = 0;
+        if (blk && q4k) {
+          const uint8_t* sc = blk + 4;
+          const int s6 = jj < 4 ? sc[jj] & 63 : (sc[jj + 4] & 0xF) | ((sc[jj - 4] >> 6) << 4);
+          const int m6 = jj < 4 ? sc[jj + 4] & 63 : (sc[jj + 4] >> 4) | ((sc[jj] >> 6) << 4);
+          word = (uint16_t)(s6 | (m6 << 8));
+          const uint8_t* qs = blk + 16 + 32 * (jj / 2);
+          const int sh = (jj & 1) ? 4 : 0;
+          for (int e = 0; e < 16; e++)
+            codes[e] = (uint8_t)(((qs[e] >> sh) & 0xF) | (((qs[e + 16] >> sh) & 0xF) << 4));
+        } else if (blk) {
+          const int h = jj / 4, m = jj % 4;
+          const uint8_t* ql = blk + 64 * h + 32 * (m & 1);
+          const uint8_t* qh = blk + 128 + 32 * h;
+          for (int l = 0; l < 32; l++) {
+            const int lo = (m < 2) ? (ql[l] & 0xF) : (ql[l] >> 4);
+            const int hi = (qh[l] >> (2 * m)) & 3;
+            codes[l] = (uint8_t)(int8_t)((lo | (hi << 4)) - 32);
+          }
+          word = (uint16_t)(blk[192 + 2 * jj] | (blk[193 + 2 * jj] << 8));
+        }
+        place_codes(!q4k, codes, rg, kc, li, j, Kc, wq);
+        wd[RTQ_WK_INDEX(rg, kc, Kc, li, j)] = word;
+      }
     }
   }
 }
@@ -622,13 +690,22 @@ rtq_status rtq_weight_create(rtq_ctx* c, int type, const void* blocks, size_t nb
   w->Kp = roundup(cols, RTQ_CHUNK_Q);
   w->gguf_bytes = expect;
   const int64_t nbp = w->Kp / 32;
-  const size_t q_bytes = (size_t)w->Np * nbp * (type == RTQ_TYPE_Q4_0 ? 16 : 32);
+  const size_t q_bytes = (size_t)w->Np * nbp * (byte_codes(type) ? 32 : 16);
   const size_t d_bytes = (size_t)w->Np * nbp * 2;
-  const size_t q_off = 0, d_off = roundup((int64_t)q_bytes, 256);
-  const size_t total = d_off + roundup((int64_t)d_bytes, 256);
+  const size_t e_bytes = is_kquant(type) ? (size_t)w->Np * (w->Kp / 256) * 4 : 0;
+  const size_t q_off = 0, d_off = roundup((int64_t)q_bytes, 256), e_off = d_off + roundup((int64_t)d_bytes, 256);
+  const size_t total = e_off + roundup((int64_t)e_bytes, 256);
+  if (q_bytes >= (1ull << 31)) {  // the kernels address codes with 32-bit buffer offsets
+    delete w;
+    return fail(RTQ_ERR_INVALID, "weight %lldx%lld: %zu code bytes exceed 2 GiB", (long long)rows, (long long)cols, q_bytes);
+  }
   std::vector<uint8_t> host(total, 0);
-  repack_q32(type, (const uint8_t*)blocks, rows, cols, w->Np, w->Kp, host.data() + q_off,
-             reinterpret_cast<uint16_t*>(host.data() + d_off));
+  if (is_kquant(type))
+    repack_kquant(type, (const uint8_t*)blocks, rows, cols, w->Np, w->Kp, host.data() + q_off,
+                  reinterpret_cast<uint16_t*>(host.data() + d_off), reinterpret_cast<uint32_t*>(host.data() + e_off));
+  else
+    repack_q32(type, (const uint8_t*)blocks, rows, cols, w->Np, w->Kp, host.data() + q_off,
+               reinterpret_cast<uint16_t*>(host.data() + d_off));
   hipError_t e = hipMalloc(&w->dmem, total);
   if (e != hipSuccess) {
     delete w;
@@ -642,6 +719,7 @@ rtq_status rtq_weight_create(rtq_ctx* c, int type, const void* blocks, size_t nb
   }
   w->wq = (char*)w->dmem + q_off;
   w->wd = reinterpret_cast<uint16_t*>((char*)w->dmem + d_off);
+  w->wsb = is_kquant(type) ? reinterpret_cast<uint32_t*>((char*)w->dmem + e_off) : nullptr;
   *out = w;
   return RTQ_OK;
 }
@@ -719,10 +797,9 @@ rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora
 
 static rtq_status enqueue_rows(rtq_ctx* c, const rtq_weight* w, int64_t r0, int64_t count, float* out,
                                hipStream_t st) {
-  RowArgs ra{w->wq, w->wd, (int)w->Np, (int)w->Kp, (int)w->cols, (int)r0, (int)count, out};
+  RowArgs ra{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, (int)w->cols, (int)r0, (int)count, out};
   const int64_t threads = count * (w->cols / 32);
-  return launch(c, w->type == RTQ_TYPE_Q4_0 ? K_ROWS_Q4_0 : K_ROWS_Q8_0, dim3((unsigned)cdiv(threads, 256)), dim3(256),
-                st, ra);
+  return launch(c, K_ROWS + fmt_index(w->type), dim3((unsigned)cdiv(threads, 256)), dim3(256), st, ra);
 }
 
 rtq_status rtq_frozen_rows_d(rtq_ctx* c, const rtq_weight* w, int64_t r0, int64_t count, float* out, void* stream) {
@@ -888,31 +965,51 @@ rtq_status rtq_debug_quantize_acts(rtq_ctx* c, const rtq_weight* w, const float*
   void* xq = ar.take<char>(p.xq_bytes);
   float* xs = ar.take<float>(p.xd_floats);
   RTQ_TRY(h2d(xdv, x, (size_t)(t * K) * 4, st));
+  const bool kq = is_kquant(w->type);
   ActArgs aa{xdv, (int)t, (int)K, (int)p.Tp, (int)w->Kp, xq, xs, nullptr, 0, nullptr, nullptr, 0};
-  RTQ_TRY(launch(c, K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp), dim3(256), st, aa));
+  RTQ_TRY(launch(c, kq ? K_ACT_PREP_K : K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp), dim3(256), st, aa));
   std::vector<uint8_t> hq(p.xq_bytes);
   std::vector<float> hs(p.xd_floats);
   RTQ_TRY(d2h(hq.data(), xq, p.xq_bytes, st));
   RTQ_TRY(d2h(hs.data(), xs, p.xd_floats * 4, st));
   HIP_TRY(hipStreamSynchronize(st));
-  // re-pack into ggml block_q8_0 (fp16 d, 32 x int8)
+  // codes of block b of token ti from the fragment layout
   const int64_t nb = K / 32, Kc = w->Kp / 128;
+  auto codes = [&](int64_t ti, int64_t b, int8_t* q) {
+    const int64_t kc = b / 4, j = b % 4, tg = ti / 16;
+    for (int g = 0; g < 4; g++) {
+      const uint8_t* f = &hq[(((tg * Kc + kc) * 4 + j) * 64 + (ti % 16) + 16 * g) * 16];
+      for (int s = 0; s < 8; s++) {
+        uint16_t hb;
+        memcpy(&hb, f + 2 * s, 2);
+        q[s < 4 ? 4 * g + s : 16 + 4 * g + (s - 4)] = (int8_t)(int)f16_bits_to_f32(hb);
+      }
+    }
+  };
   uint8_t* o = (uint8_t*)out;
+  if (!kq) {  // ggml block_q8_0: fp16 d, 32 x int8
+    for (int64_t ti = 0; ti < t; ti++)
+      for (int64_t b = 0; b < nb; b++) {
+        uint8_t* blk = o + (ti * nb + b) * 34;
+        const uint16_t d = f32_to_f16_bits(hs[((size_t)(b / 4) * p.Tp + ti) * 4 + b % 4]);  // [Kc][Tp][4]
+        blk[0] = (uint8_t)(d & 0xff);
+        blk[1] = (uint8_t)(d >> 8);
+        codes(ti, b, (int8_t*)blk + 2);
+      }
+    return RTQ_OK;
+  }
+  // ggml block_q8_K: f32 d, 256 x int8, 16 x int16 sums of 16 codes
+  const int64_t nsb = K / 256;
   for (int64_t ti = 0; ti < t; ti++)
-    for (int64_t b = 0; b < nb; b++) {
-      uint8_t* blk = o + (ti * nb + b) * 34;
-      const uint16_t d = f32_to_f16_bits(hs[((size_t)(b / 4) * p.Tp + ti) * 4 + b % 4]);  // [Kc][Tp][4]
-      blk[0] = (uint8_t)(d & 0xff);
-      blk[1] = (uint8_t)(d >> 8);
-      const int64_t kc = b / 4, j = b % 4, tg = ti / 16;
-      for (int g = 0; g < 4; g++) {
-        const uint8_t* f = &hq[(((tg * Kc + kc) * 4 + j) * 64 + (ti % 16) + 16 * g) * 16];
-        for (int s = 0; s < 8; s++) {
-          uint16_t hb;
-          memcpy(&hb, f + 2 * s, 2);
-          const int e = s < 4 ? 4 * g + s : 16 + 4 * g + (s - 4);
-          blk[2 + e] = (uint8_t)(int8_t)(int)f16_bits_to_f32(hb);
-        }
+    for (int64_t sb = 0; sb < nsb; sb++) {
+      uint8_t* blk = o + (ti * nsb + sb) * 292;
+      memcpy(blk, &hs[((size_t)(2 * sb) * p.Tp + ti) * 4], 4);
+      int8_t* q = (int8_t*)blk + 4;
+      for (int jj = 0; jj < 8; jj++) codes(ti, sb * 8 + jj, q + 32 * jj);
+      for (int g = 0; g < 16; g++) {
+        int16_t bs = 0;
+        for (int l = 0; l < 16; l++) bs = (int16_t)(bs + q[16 * g + l]);
+        memcpy(blk + 260 + 2 * g, &bs, 2);
       }
     }
   return RTQ_OK;

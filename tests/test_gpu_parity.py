@@ -1,7 +1,7 @@
 """GPU parity: the gfx950 path through the C ABI against the CPU oracle on identical seeded inputs.
 
 Bars (from the hot-path contract):
-  * activation quantisation (Q8_0 blocks) and the integer block sums: bit-exact;
+  * activation quantisation (Q8_0 / Q8_K blocks) and the integer block sums: bit-exact;
   * row() dequantisation: bit-exact;
   * f32 outputs and gradients: max |gpu - oracle| / max |oracle| <= 1e-3 per tensor (TOL);
     the reference's own per-element check 1e-3 * max(|want|, 1) (tests/engine.rs:115) is also
@@ -18,7 +18,13 @@ import rust_trainer_amd as rt
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3
-FORMATS = [O.Q4_0, O.Q8_0]
+FORMATS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q6_K]
+BLOCK = {O.Q4_0: 32, O.Q8_0: 32, O.Q4_K: 256, O.Q6_K: 256}
+
+
+def cases(shapes, formats=FORMATS):
+    """(format, *shape) for every shape whose K is a whole number of the format's blocks."""
+    return [(f, *sh) for f in formats for sh in shapes if sh[1] % BLOCK[f] == 0]
 
 
 def rel_err(got, want):
@@ -47,7 +53,7 @@ def hip(ctx, wtype, blocks, n, k):
 
 
 # ---------------------------------------------------------------- bit-exact parts
-@pytest.mark.parametrize("wtype", FORMATS)
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
 def test_activation_quantisation_bit_exact(ctx, wtype):
     n, k, t = 64, 1024, 37
     blocks, x, _ = make(wtype, n, k, t)
@@ -61,8 +67,29 @@ def test_activation_quantisation_bit_exact(ctx, wtype):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("wtype", FORMATS)
-@pytest.mark.parametrize("n,k,t", [(80, 256, 20), (64, 96, 3), (128, 1024, 65)])
+@pytest.mark.parametrize("wtype", [O.Q4_K, O.Q6_K])
+def test_activation_quantisation_q8_k_bit_exact(ctx, wtype):
+    n, k, t = 64, 1024, 21
+    blocks, x, _ = make(wtype, n, k, t)
+    # first element of largest |x| wins, across the 16-column segments of a super-block too
+    x[0, :256] *= np.float32(0.01)
+    x[0, 40], x[0, 200] = -7.0, 7.0
+    x[1, 256:512] *= np.float32(0.01)
+    x[1, 300], x[1, 301] = 5.0, -5.0
+    x[2, 512:768] *= np.float32(0.01)
+    x[2, 520], x[2, 515] = -3.0, 3.0  # lower column, later segment order does not matter
+    # max = -127: iscale = 1, so x = m + 0.5 rounds to even
+    x[3, :8] = np.array([-127.0, 2.5, -2.5, 0.5, -0.5, 1.5, 126.5, -126.5], np.float32)
+    x[3, 8:256] = np.float32(0.25)
+    x[4, 768:1024] = 0.0  # all-zero super-block: d = 0, codes 0
+    x[5, :256] *= np.float32(1e-6)
+    w = hip(ctx, wtype, blocks, n, k)
+    got = w.debug_quantize_acts(x, t)
+    want = O.quantize_acts(wtype, x)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("wtype,n,k,t", cases([(80, 256, 20), (64, 96, 3), (128, 1024, 65), (48, 512, 3)]))
 def test_block_isums_bit_exact(ctx, wtype, n, k, t):
     blocks, x, _ = make(wtype, n, k, t)
     w = hip(ctx, wtype, blocks, n, k)
@@ -73,7 +100,7 @@ def test_block_isums_bit_exact(ctx, wtype, n, k, t):
 
 @pytest.mark.parametrize("wtype", FORMATS)
 def test_row_dequant_bit_exact(ctx, wtype):
-    n, k = 200, 384
+    n, k = 200, 384 if BLOCK[wtype] == 32 else 512
     blocks, _, _ = make(wtype, n, k, 1)
     w = hip(ctx, wtype, blocks, n, k)
     out = np.empty(k, np.float32)
@@ -83,11 +110,11 @@ def test_row_dequant_bit_exact(ctx, wtype):
 
 
 # ---------------------------------------------------------------- FrozenMatmul
-SHAPES = [(64, 128, 1), (100, 96, 5), (256, 512, 37), (3072, 1024, 16), (3072, 1024, 256), (1024, 3072, 64)]
+SHAPES = [(64, 128, 1), (100, 96, 5), (256, 512, 37), (3072, 1024, 16), (3072, 1024, 256), (1024, 3072, 64),
+          (2048, 1024, 1), (1024, 1024, 16), (80, 2048, 130)]
 
 
-@pytest.mark.parametrize("wtype", FORMATS)
-@pytest.mark.parametrize("n,k,t", SHAPES)
+@pytest.mark.parametrize("wtype,n,k,t", cases(SHAPES))
 def test_forward_matches_oracle(ctx, wtype, n, k, t):
     blocks, x, _ = make(wtype, n, k, t)
     w = hip(ctx, wtype, blocks, n, k)
@@ -97,8 +124,7 @@ def test_forward_matches_oracle(ctx, wtype, n, k, t):
     assert rel_err(y, want) <= TOL
 
 
-@pytest.mark.parametrize("wtype", FORMATS)
-@pytest.mark.parametrize("n,k,t", SHAPES)
+@pytest.mark.parametrize("wtype,n,k,t", cases(SHAPES))
 def test_backward_input_matches_oracle(ctx, wtype, n, k, t):
     blocks, _, dy = make(wtype, n, k, t)
     w = hip(ctx, wtype, blocks, n, k)
@@ -143,9 +169,8 @@ def test_errors_are_status_codes(ctx):
 
 
 # ---------------------------------------------------------------- Linear + LoRA
-@pytest.mark.parametrize("wtype", FORMATS)
-@pytest.mark.parametrize("n,k,t,r", [(3072, 1024, 256, 16), (256, 512, 37, 2), (100, 96, 5, 16), (512, 256, 70, 64),
-                                     (512, 2048, 9, 16), (1024, 3072, 130, 8)])
+@pytest.mark.parametrize("wtype,n,k,t,r", cases([(3072, 1024, 256, 16), (256, 512, 37, 2), (100, 96, 5, 16),
+                                                 (512, 256, 70, 64), (512, 2048, 9, 16), (1024, 3072, 130, 8)]))
 def test_linear_lora_matches_oracle(ctx, wtype, n, k, t, r):
     alpha = 2.0 * r
     blocks, x, dy = make(wtype, n, k, t)
@@ -217,13 +242,14 @@ def test_device_pointer_api_matches_host_api(ctx):
 
 
 # ---------------------------------------------------------------- maximum size
-def test_lm_head_shape_t1(ctx):
+@pytest.mark.parametrize("wtype", FORMATS)
+def test_lm_head_shape_t1(ctx, wtype):
     # tied LM head of Qwen3-0.6B: 151936 x 1024, one token (decode-shaped GEMV)
     n, k, t = 151936, 1024, 1
-    blocks, x, dy = make(O.Q4_0, n, k, t)
-    w = hip(ctx, O.Q4_0, blocks, n, k)
+    blocks, x, dy = make(wtype, n, k, t)
+    w = hip(ctx, wtype, blocks, n, k)
     y = w.forward(x, t)
-    assert rel_err(y, O.frozen_forward(O.Q4_0, blocks, n, k, x, nthreads=16)) <= TOL
+    assert rel_err(y, O.frozen_forward(wtype, blocks, n, k, x, nthreads=16)) <= TOL
     dx = np.zeros(t * k, np.float32)
     w.backward_input(dy, t, dx)
-    assert rel_err(dx, O.frozen_backward_input(O.Q4_0, blocks, n, k, dy, nthreads=16)) <= TOL
+    assert rel_err(dx, O.frozen_backward_input(wtype, blocks, n, k, dy, nthreads=16)) <= TOL
