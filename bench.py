@@ -16,6 +16,14 @@ packet and so read a few microseconds longer than the kernel-trace durations of 
 Prints one JSON line: metric/value (tokens/s = T / step time), per-kernel average durations, the
 roofline of the dominant kernel, and the CPU oracle's time on the host cores (cpu_baseline,
 bounded sample).
+
+``--sweep`` measures BASELINE configs[1] instead: Q8_0, Q4_K, Q6_K (and Q4_0) at the Qwen3-0.6B
+shapes q_proj 2048x1024, k/v_proj 1024x1024, down_proj 1024x3072 and the tied LM head 151936x1024,
+T in {1, 16, 256, 2048}, LoRA r=16 except on the LM head.  Per case it times a graph of calls
+(Linear forward; Linear backward, or FrozenMatmul::backward_input for the LM head) rotating over
+operand sets of at least 512 MB in total, and prints one JSON line with the per-call time and the
+call's roofline fraction (algorithmic bytes and flops, each operand touched once).  ``--case
+FMT:SHAPE:T`` runs one of those cases (for a kernel trace of it).
 """
 from __future__ import annotations
 
@@ -88,6 +96,126 @@ def measured_traffic(name: str):
     return None
 
 
+# ---------------------------------------------------------------- configs[1] sweep
+SWEEP_SHAPES = {"q_proj": (2048, 1024), "kv_proj": (1024, 1024), "down_proj": (1024, 3072), "lm_head": (151936, 1024)}
+SWEEP_TYPES = {"Q8_0": 8, "Q4_K": 12, "Q6_K": 14, "Q4_0": 2}
+SWEEP_T = (1, 16, 256, 2048)
+BLOCK = {2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
+
+
+def call_work(wtype: int, n: int, k: int, t: int, r: int, backward: bool) -> tuple[float, float]:
+    """(algorithmic bytes, flops) of one Linear call, each operand touched once."""
+    be, bb = BLOCK[wtype]
+    wb = n * k // be * bb
+    if not backward:  # y = x W^T + s (x A^T) B^T
+        return float(wb + t * k * 4 + t * n * 4 + r * (k + n) * 4), float(2 * t * n * k + 2 * t * r * (k + n))
+    # dx = dy W (+ g A), g = s dy B, h = x A^T, dA += g^T x, dB += (s dy)^T h
+    lora_bytes = (t * k * 4 + 2 * (r * k + n * r) * 4 + (r * k + n * r) * 4) if r else 0
+    return float(wb + t * n * 4 + t * k * 4 + lora_bytes), float(2 * t * n * k + (6 * t * r * k + 4 * t * n * r if r else 0))
+
+
+def call_roofline(bytes_: float, flops: float, sec: float) -> dict:
+    t_hbm, t_mfma = bytes_ / (HBM_PEAK_GBS * 1e9), flops / (F16_PEAK_TFLOPS * 1e12)
+    if t_hbm >= t_mfma:
+        return {"bound": "hbm", "achieved": round(bytes_ / sec / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(t_hbm / sec, 4)}
+    return {"bound": "mfma", "achieved": round(flops / sec / 1e12, 2), "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(t_mfma / sec, 4)}
+
+
+def sweep(cases: list[tuple[str, str, int]], calls_min: int) -> None:
+    import torch
+
+    import rust_trainer_amd as rt
+    from rust_trainer_amd import _ffi, synth
+
+    dev = torch.device("cuda", 0)
+    L = _ffi.lib()
+    ctx = rt.Context(0)
+    side = torch.cuda.Stream()
+    weights_cache: dict = {}
+    for fmt, shape, t in cases:
+        wtype = SWEEP_TYPES[fmt]
+        n, k = SWEEP_SHAPES[shape]
+        r = 0 if shape == "lm_head" else R
+        key = (fmt, shape)
+        # N(0, 0.02) weights, N(0, 1) activations and gradients from torch's generators (seeded):
+        # the reference Rng's stream is not needed for timing, and is slow at the LM head's sizes
+        if key not in weights_cache:
+            weights_cache.clear()
+            gen = torch.Generator().manual_seed(1)
+            w = (torch.randn(n, k, generator=gen) * 0.02).numpy()
+            weights_cache[key] = synth.QUANTIZERS[wtype](w)
+            del w
+        blocks = weights_cache[key]
+        gd = torch.Generator(device=dev).manual_seed(2)
+        x = torch.randn(t, k, device=dev, generator=gd)
+        dy = torch.randn(t, n, device=dev, generator=gd)
+        A = torch.randn(max(r, 1), k, device=dev, generator=gd) / 32.0
+        B = torch.randn(n, max(r, 1), device=dev, generator=gd) * 0.01
+        set_bytes = blocks.nbytes + 4 * (2 * t * k + 2 * t * n)
+        nsets = int(min(1024, max(2, -(-512 * 2**20 // set_bytes))))
+        sets = []
+        for _ in range(nsets):
+            sset = {"w": rt.HipFrozen(wtype, blocks, n, k, ctx=ctx), "x": x.clone(), "dy": dy.clone(),
+                    "y": torch.empty(t, n, device=dev), "dx": torch.zeros(t, k, device=dev),
+                    "a": A.clone(), "b": B.clone(), "ga": torch.zeros(max(r, 1), k, device=dev),
+                    "gb": torch.zeros(n, max(r, 1), device=dev)}
+            sset["lora"] = _ffi.RtqLora(r, 2.0 * r, sset["a"].data_ptr(), sset["b"].data_ptr(), 1) if r else None
+            sets.append(sset)
+        ctx.reserve(t, n, k, r)
+        torch.cuda.synchronize()
+
+        def fwd(i: int, st: int) -> None:
+            ss = sets[i % nsets]
+            lp = ctypes.byref(ss["lora"]) if r else None
+            _ffi.check(L.rtq_linear_forward_d(ctx.handle, ss["w"].handle, None, lp, ss["x"].data_ptr(), t,
+                                              ss["y"].data_ptr(), st), "forward")
+
+        def bwd(i: int, st: int) -> None:
+            ss = sets[i % nsets]
+            if r:
+                _ffi.check(L.rtq_linear_backward_d(ctx.handle, ss["w"].handle, ctypes.byref(ss["lora"]),
+                                                   ss["x"].data_ptr(), ss["dy"].data_ptr(), t, ss["dx"].data_ptr(),
+                                                   ss["ga"].data_ptr(), ss["gb"].data_ptr(), st), "backward")
+            else:
+                _ffi.check(L.rtq_frozen_backward_input_d(ctx.handle, ss["w"].handle, ss["dy"].data_ptr(), t,
+                                                         ss["dx"].data_ptr(), st), "backward_input")
+
+        ncalls = max(calls_min, nsets)
+        out = {"sweep": "configs[1]", "format": fmt, "shape": shape, "rows": n, "cols": k, "tokens": t,
+               "lora_rank": r, "operand_sets": nsets, "calls": ncalls}
+        for name, fn in (("forward", fwd), ("backward", bwd)):
+            with torch.cuda.stream(side):
+                st = torch.cuda.current_stream().cuda_stream
+                for i in range(min(ncalls, 2 * nsets)):
+                    fn(i, st)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                st = torch.cuda.current_stream().cuda_stream
+                for i in range(ncalls):
+                    fn(i, st)
+            g.replay()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            g.replay()
+            torch.cuda.synchronize()
+            sec = (time.perf_counter() - t0) / ncalls
+            bytes_, flops = call_work(wtype, n, k, t, r, name == "backward")
+            out[name] = {"us_per_call": round(sec * 1e6, 3), "tokens_per_s": round(t / sec, 1),
+                         "gflops": round(flops / sec / 1e9, 1), "algorithmic_bytes": int(bytes_),
+                         "roofline": call_roofline(bytes_, flops, sec)}
+            del g
+        print(json.dumps(out), flush=True)
+        for sset in sets:
+            sset["w"].close()
+        del sets, x, dy, A, B
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    ctx.close()
+
+
 def cpu_baseline(inputs, seconds: float) -> dict:
     """The CPU oracle (C restatement of the reference algorithm) on the host cores, bounded sample."""
     import numpy as np
@@ -118,12 +246,23 @@ def main() -> int:
     ap.add_argument("--sets", type=int, default=40, help="rotating operand sets (~10 MB each)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sweep", action="store_true", help="configs[1] sweep: one JSON line per case")
+    ap.add_argument("--case", default=None, help="one sweep case FMT:SHAPE:T, e.g. Q4_K:lm_head:1")
+    ap.add_argument("--calls", type=int, default=50, help="sweep: calls per timed graph (at least the sets)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build runs the hot path on one GPU only; --gpus {args.gpus} "
               f"(WORLD_SIZE={world}) is not supported (the multi-GPU sharding is design-only)", file=sys.stderr)
         return 2
+    if args.sweep or args.case:
+        if args.case:
+            fmt, shape, t = args.case.split(":")
+            cases = [(fmt, shape, int(t))]
+        else:
+            cases = [(f, s, t) for f in ("Q8_0", "Q4_K", "Q6_K", "Q4_0") for s in SWEEP_SHAPES for t in SWEEP_T]
+        sweep(cases, args.calls)
+        return 0
 
     import numpy as np
     import torch

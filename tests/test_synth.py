@@ -17,10 +17,13 @@ def test_rng_streams_match(seed):
     assert np.abs(n1 - n2).max() <= 2e-6 * 0.02 * 8  # last-ulp libm differences only
 
 
-@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0, O.Q4_K, O.Q6_K])
 def test_quantisers_bit_identical(wtype):
-    w = O.Rng(1).vec_normal(37 * 256, 0.02).reshape(37, 256)
+    w = O.Rng(1).vec_normal(37 * 512, 0.02).reshape(37, 512)
     w[0, :32] = 0.0
     w[1, :32] = np.float32(1e-7)
     w[2, :32] = np.array([127.0, 2.5, -2.5, 0.5, -0.5] + [0.0] * 27, np.float32)
+    w[3, :256] = 0.0  # an all-zero super-block
+    w[4, :256] = np.abs(w[4, :256])  # no negative values: min 0
+    w[5, 256:] = -np.abs(w[5, 256:])  # no positive values
     assert np.array_equal(synth.QUANTIZERS[wtype](w), O.quantize(wtype, w))
