@@ -105,8 +105,9 @@ struct BwdPrepArgs {
   int ngq;
 };
 
-// part[z][t][k] = sum over rows n of split z of dy[t][n] W[n][k]: workgroup tile 64 tokens x 128 columns, rows of W split
-// over blockIdx.z (atomics when split), three bf16 MFMAs per product (hi/lo split of dy and W).
+// part[z][t][k] = sum over rows n of split z of dy[t][n] W[n][k], three bf16 MFMAs per product (hi/lo split of dy
+// and W).  rtq_dx_*: workgroup tile 64 tokens x 128 columns, partials in MFMA fragment order;
+// rtq_dx16_* (T <= 16): tile 16 tokens x 128 columns, partials row-major [nsplit][T][K].
 struct DxArgs {
   const void* wq;
   const uint16_t* wd;
@@ -140,9 +141,10 @@ struct LoraGradArgs {
   float* ga;  // [r x K]
   float* dx;  // [T x K]
   int n_gb, n_ga, n_dx;  // workgroups of each part, in this order
-  const float* part;     // [nsplit][T][K] from the dx kernel
+  const float* part;     // split partials from the dx kernel
   int nsplit;
   int accumulate;        // 1: dx += (FrozenMatmul::backward_input); 0: dx = (Linear::backward)
+  int part_rows;         // 1: partials row-major [nsplit][T][K] (rtq_dx16_*); 0: fragment order (rtq_dx_*)
 };
 
 // rows [r0, r0+count) dequantised to f32 (bit-exact ggml dequant)

@@ -828,6 +828,40 @@ struct DxSlot<FMT_Q4_K> {
 template <>
 struct DxSlot<FMT_Q6_K> : DxSlot<FMT_Q4_K> {};
 
+// h = sum of hp, g = s * sum of gp, both in slice order (src/linear.rs:106-111), by the nfin
+// finaliser workgroups of a dx grid (rel: this workgroup's index among them)
+__device__ __forceinline__ void dx_lora_sums(const DxArgs& a, int rel, int nfin) {
+  const int64_t n = (int64_t)a.T * a.r;
+  const int64_t nthr = (int64_t)nfin * blockDim.x;
+  for (int64_t e = (int64_t)rel * blockDim.x + threadIdx.x; e < n; e += nthr) {
+    a.h[e] = sum_partials(a.hp, e, a.nhq);
+    a.g[e] = a.s * sum_partials(a.gp, e, a.ngq);
+  }
+}
+
+// dequantisation of the unsigned byte codes of one row, value fmaf(u, d, m):
+//   Q4_0 (nibble - 8) d;  Q8_0 ((q ^ 0x80) - 128) d;  Q4_K (d sc) u - dmin m;
+//   Q6_K ((q ^ 0x80) - 128) (d sc), sc of the 16-element half hh
+// d16: fp16 scale (Q4_0, Q8_0); kw: the row's sub-block scale words of the half chunk (blocks 2h,
+// 2h+1), ev: its super-block (d, dmin) (K-quants)
+template <int FMT>
+__device__ __forceinline__ void dq_params(uint32_t d16, uint32_t kw, uint32_t ev, int jb, int hh, float& d, float& m) {
+  if constexpr (is_kquant(FMT)) {
+    kw >>= 16 * (jb & 1);
+    const float dsb = h2f((uint16_t)(ev & 0xffffu));
+    if (FMT == FMT_Q4_K) {
+      d = dsb * (float)(kw & 0x3fu);  // exact products
+      m = -(h2f((uint16_t)(ev >> 16)) * (float)((kw >> 8) & 0x3fu));
+    } else {
+      d = dsb * (float)(int)(int8_t)((kw >> (8 * hh)) & 0xffu);
+      m = -128.0f * d;
+    }
+  } else {
+    d = h2f((uint16_t)d16);
+    m = (FMT == FMT_Q4_0 ? -8.0f : -128.0f) * d;
+  }
+}
+
 template <int FMT>
 __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   // Flat grid, XCD-aware: consecutive workgroup ids go to the 8 XCDs in turn, so id % 8 selects
@@ -838,13 +872,7 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   const int nmain = Kc * ntt * a.nsplit;
   const int id = blockIdx.x;
   if (id >= nmain) {
-    // h = sum of hp, g = s * sum of gp, both in slice order (src/linear.rs:106-111)
-    const int64_t n = (int64_t)a.T * a.r;
-    const int64_t nthr = (int64_t)(gridDim.x - nmain) * blockDim.x;
-    for (int64_t e = (int64_t)(id - nmain) * blockDim.x + threadIdx.x; e < n; e += nthr) {
-      a.h[e] = sum_partials(a.hp, e, a.nhq);
-      a.g[e] = a.s * sum_partials(a.gp, e, a.ngq);
-    }
+    dx_lora_sums(a, id - nmain, gridDim.x - nmain);
     return;  // uniform over the workgroup, before any barrier
   }
   constexpr int D = 4;
@@ -950,24 +978,11 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
       uint32_t vb[2][4], lb[2][4];
 #pragma unroll
       for (int r = 0; r < 2; r++) {
-        // unsigned byte codes u with value u * d + m:
-        //   Q4_0 (nibble - 8) d;  Q8_0 ((q ^ 0x80) - 128) d;  Q4_K (d sc) u - dmin m;
-        //   Q6_K ((q ^ 0x80) - 128) (d sc), sc of the 16-element half hh
         float d, m;
-        if constexpr (KQ) {
-          const uint32_t kw = (r ? S.k.y : S.k.x) >> (16 * (jb & 1)), ev = r ? S.e.y : S.e.x;
-          const float dsb = h2f((uint16_t)(ev & 0xffffu));
-          if (FMT == FMT_Q4_K) {
-            d = dsb * (float)(kw & 0x3fu);                         // exact products
-            m = -(h2f((uint16_t)(ev >> 16)) * (float)((kw >> 8) & 0x3fu));
-          } else {
-            d = dsb * (float)(int)(int8_t)((kw >> (8 * hh)) & 0xffu);
-            m = -128.0f * d;
-          }
-        } else {
-          d = h2f((uint16_t)(r ? (S.d >> 16) : (S.d & 0xffffu)));
-          m = (FMT == FMT_Q4_0 ? -8.0f : -128.0f) * d;
-        }
+        if constexpr (KQ)
+          dq_params<FMT>(0u, r ? S.k.y : S.k.x, r ? S.e.y : S.e.x, jb, hh, d, m);
+        else
+          dq_params<FMT>(r ? (S.d >> 16) : (S.d & 0xffffu), 0u, 0u, jb, hh, d, m);
         const uint32_t u = B8 ? S.q[r] ^ 0x80808080u : (hh ? (S.q[r] >> 4) : S.q[r]) & 0x0f0f0f0fu;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
@@ -1022,6 +1037,183 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) out[ts * 2 + ks] = acc[ts][ks];
 }
+
+// ============================================================== dx = dy . W for T <= 16
+// Same arithmetic as dx_tile with one 16-token tile: workgroup of 4 waves, tile 16 tokens x 128
+// columns (wave w: the 32 columns of block w), 32 rows per step, many row splits (a GEMV-shaped
+// product needs them to fill the GPU).  Each thread stages both halves of its W words, and the
+// partials are written row-major for the real tokens only: part[split][t][k].
+template <int FMT>
+struct Dx16Slot {
+  float2 dy;          // rows 2p, 2p+1 of the step, token tid / 16
+  uint32_t q[2][2];   // [row][half] code words (nibble formats: both halves in q[r][0])
+  uint32_t d;         // fp16 scales of the two rows (Q4_0, Q8_0)
+  u2v k, e;           // sub-block and super-block scales of the two rows (K-quants)
+};
+
+template <int FMT>
+__device__ __forceinline__ void dx16_tile(const DxArgs& a) {
+  const int Kc = a.Kp / 128;
+  const int nmain = Kc * a.nsplit;
+  const int id = blockIdx.x;
+  if (id >= nmain) {
+    dx_lora_sums(a, id - nmain, gridDim.x - nmain);
+    return;  // uniform over the workgroup, before any barrier
+  }
+  constexpr bool KQ = is_kquant(FMT), B8 = byte_codes(FMT);
+  constexpr int D = 4;
+  __shared__ u4v sA[2][2][64];                                       // [buf][hi/lo][lane]
+  __shared__ __attribute__((aligned(16))) __bf16 sW[2][2][128][40];  // [buf][hi/lo][k][n]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
+  // id -> (split, K chunk), XCD-aware as in dx_tile
+  int sp, kc;
+  if ((a.nsplit & 7) == 0) {
+    const int grp = id / (8 * Kc), rem = id % (8 * Kc);
+    sp = grp * 8 + rem % 8;
+    kc = rem / 8;
+  } else {
+    sp = id / Kc;
+    kc = id % Kc;
+  }
+  const int n0 = sp * a.n_per_split;
+  const int nsteps = (min(n0 + a.n_per_split, a.Np) - n0) / 32;
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 acc[2] = {zero, zero};
+
+  // dy loader: token tl = tid >> 4, rows 2pp, 2pp+1 of the step (tokens >= T read zero)
+  const int tl = tid >> 4, pp = tid & 15;
+  const __amdgpu_buffer_rsrc_t rdy = make_rsrc(a.dy, (uint32_t)a.T * a.N * 4u);
+  const uint32_t dy_off = ((uint32_t)tl * a.N + 2 * pp) * 4u;
+  const bool dy_vec = (a.N & 1) == 0;
+  // W loader: row group rgl, rows 2wp, 2wp+1, k-group wgg, block jb (both halves)
+  const int rgl = tid >> 7, qp = (tid >> 2) & 31, jb = tid & 3;
+  const int wp = qp & 7, wgg = qp >> 3;
+  const int li0 = 2 * wp, FL0 = 16 * wgg + li0;
+  const int nloc = rgl * 16 + li0;
+  const uint32_t wq_bytes = (uint32_t)(a.Np / 16) * Kc * 64 * 16 * (B8 ? 2 : 1);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.wq, wq_bytes);
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.wd, (uint32_t)(a.Np / 16) * Kc * 128);
+  const __amdgpu_buffer_rsrc_t re = make_rsrc(a.wsb, KQ ? (uint32_t)(a.Np / 16) * Kc * 32 : 0u);
+  uint32_t q_off[2];
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    if (!B8)
+      q_off[r] = ((((uint32_t)rgl * Kc + kc) * 64 + FL0 + r) * 4 + jb) * 4u;
+    else
+      q_off[r] = (((((uint32_t)rgl * Kc + kc) * 2 + (jb >> 1)) * 64 + FL0 + r) * 2 + (jb & 1)) * 8u;
+  }
+  const uint32_t d_off = KQ ? (uint32_t)RTQ_WK_INDEX(rgl, kc, Kc, li0, jb & 2) * 2u
+                            : (uint32_t)RTQ_WD_INDEX(rgl, kc, Kc, li0, jb) * 2u;
+  const uint32_t e_off = (uint32_t)RTQ_WSB_INDEX(rgl, kc >> 1, Kc >> 1, li0) * 4u;
+  const uint32_t q_rg = (uint32_t)Kc * 64 * 16 * (B8 ? 2 : 1);
+  const uint32_t d_rg = (uint32_t)Kc * 128, e_rg = (uint32_t)Kc * 32;
+
+  Dx16Slot<FMT> sl[D];
+  auto issue = [&](Dx16Slot<FMT>& S, int step) {
+    const int ns = n0 + 32 * min(step, max(nsteps - 1, 0));  // clamped: always a real step
+    const uint32_t srg = (uint32_t)(ns >> 4);
+    if (dy_vec) {
+      S.dy = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rdy, dy_off, (uint32_t)ns * 4u, 0));
+    } else {
+      S.dy.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rdy, dy_off, (uint32_t)ns * 4u, 0));
+      S.dy.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rdy, dy_off + 4u, (uint32_t)ns * 4u, 0));
+    }
+    if (ns + 32 > a.N) {  // ragged tail of N: columns >= N hold the next token's values
+      if (ns + 2 * pp >= a.N) S.dy.x = 0.0f;
+      if (ns + 2 * pp + 1 >= a.N) S.dy.y = 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      if (B8) {
+        const u2v v = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(rq, q_off[r], srg * q_rg, 0));
+        S.q[r][0] = v.x;
+        S.q[r][1] = v.y;
+      } else {
+        S.q[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rq, q_off[r], srg * q_rg, 0);
+      }
+    }
+    if constexpr (KQ) {
+      S.k = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(rd, d_off, srg * d_rg, 0));
+      S.e = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(re, e_off, srg * e_rg, 0));
+    } else {
+      S.d = __builtin_amdgcn_raw_buffer_load_b32(rd, d_off, srg * d_rg, 0);
+    }
+  };
+  auto stage_compute = [&](const Dx16Slot<FMT>& S, int buf) {
+    {  // dy: A fragment lane tl + 16 (pp >> 2), bf16 slots 2 (pp & 3), +1 (whole-vector bit view)
+      const u2v vb = __builtin_bit_cast(u2v, S.dy);
+      const uint32_t l0 = __builtin_bit_cast(uint32_t, S.dy.x - __builtin_bit_cast(float, vb.x & 0xffff0000u));
+      const uint32_t l1 = __builtin_bit_cast(uint32_t, S.dy.y - __builtin_bit_cast(float, vb.y & 0xffff0000u));
+      const int fl = tl + 16 * (pp >> 2);
+      reinterpret_cast<uint32_t*>(&sA[buf][0][fl])[pp & 3] = __builtin_amdgcn_perm(vb.y, vb.x, 0x07060302u);
+      reinterpret_cast<uint32_t*>(&sA[buf][1][fl])[pp & 3] = __builtin_amdgcn_perm(l1, l0, 0x07060302u);
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {  // W: rows li0, li0+1, half hh
+      uint32_t vb[2][4], lb[2][4];
+#pragma unroll
+      for (int r = 0; r < 2; r++) {
+        float d, m;
+        if constexpr (KQ)
+          dq_params<FMT>(0u, r ? S.k.y : S.k.x, r ? S.e.y : S.e.x, jb, hh, d, m);
+        else
+          dq_params<FMT>(r ? (S.d >> 16) : (S.d & 0xffffu), 0u, 0u, jb, hh, d, m);
+        const uint32_t u = B8 ? S.q[r][hh] ^ 0x80808080u : (hh ? (S.q[r][0] >> 4) : S.q[r][0]) & 0x0f0f0f0fu;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float v = fmaf((float)((u >> (8 * e)) & 0xffu), d, m);
+          vb[r][e] = __builtin_bit_cast(uint32_t, v);
+          lb[r][e] = __builtin_bit_cast(uint32_t, v - __builtin_bit_cast(float, vb[r][e] & 0xffff0000u));
+        }
+      }
+      const int kb = 32 * jb + 16 * hh + 4 * wgg;
+      const int nsw = nloc ^ (8 * jb);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        *reinterpret_cast<uint32_t*>(&sW[buf][0][kb + e][nsw]) = __builtin_amdgcn_perm(vb[1][e], vb[0][e], 0x07060302u);
+        *reinterpret_cast<uint32_t*>(&sW[buf][1][kb + e][nsw]) = __builtin_amdgcn_perm(lb[1][e], lb[0][e], 0x07060302u);
+      }
+    }
+    __syncthreads();
+    const bf8 ah = __builtin_bit_cast(bf8, sA[buf][0][lane]);
+    const bf8 al = __builtin_bit_cast(bf8, sA[buf][1][lane]);
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      const int kl = w * 32 + ks * 16 + li;  // column kl lies in block w: rows swizzled by 8 w
+      const bf8 bh = *reinterpret_cast<const bf8*>(&sW[buf][0][kl][8 * (g ^ w)]);
+      const bf8 bl = *reinterpret_cast<const bf8*>(&sW[buf][1][kl][8 * (g ^ w)]);
+      acc[ks] = mfma_bf16(ah, bh, acc[ks]);
+      acc[ks] = mfma_bf16(al, bh, acc[ks]);
+      acc[ks] = mfma_bf16(ah, bl, acc[ks]);
+    }
+  };
+#pragma unroll
+  for (int s0 = 0; s0 < D - 1; s0++) issue(sl[s0], s0);
+  for (int st0 = 0; st0 < nsteps; st0 += D) {
+#pragma unroll
+    for (int s0 = 0; s0 < D; s0++) {
+      issue(sl[(s0 + D - 1) % D], st0 + s0 + D - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (st0 + s0 < nsteps) stage_compute(sl[s0], (st0 + s0) & 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // lane holds tokens 4g .. 4g+3 of column 128 kc + 32 w + 16 ks + li
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+    const int col = kc * 128 + w * 32 + ks * 16 + li;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int t = 4 * g + e;
+      if (t < a.T && col < a.K) a.part[((int64_t)sp * a.T + t) * a.K + col] = acc[ks][e];
+    }
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q4_0(DxArgs a) { dx16_tile<FMT_Q4_0>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q8_0(DxArgs a) { dx16_tile<FMT_Q8_0>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q4_k(DxArgs a) { dx16_tile<FMT_Q4_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q6_k(DxArgs a) { dx16_tile<FMT_Q6_K>(a); }
 
 extern "C" __global__ __launch_bounds__(512) void rtq_dx_q4_0(DxArgs a) { dx_tile<FMT_Q4_0>(a); }
 extern "C" __global__ __launch_bounds__(512) void rtq_dx_q8_0(DxArgs a) { dx_tile<FMT_Q8_0>(a); }
@@ -1087,6 +1279,45 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a)
         const int j = ct * 16 + rl, k = rt * 16 + cl;
         if (j < a.r && k < a.K) a.ga[(int64_t)j * a.K + k] += s;
       }
+    }
+  } else if (a.part_rows) {
+    // dx from row-major partials: wave per (token t, 64 columns); lane (k4 = li, split subset g)
+    // sums splits g, g+4, ... of four columns, the subsets are combined by shuffles (fixed order)
+    const int nseg = (a.K + 63) / 64;
+    const int f = (b - a.n_gb - a.n_ga) * NW + w;
+    if (f >= a.T * nseg) return;  // whole wave exits together; no barriers in this branch
+    const int t = f / nseg, k0 = (f % nseg) * 64 + 4 * li;
+    const bool kin = k0 < a.K;  // K % 32 == 0: four columns in or out together
+    f4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+    const f4* pp = reinterpret_cast<const f4*>(a.part + (int64_t)t * a.K + min(k0, a.K - 4));
+    const int64_t sstride = (int64_t)a.T * a.K / 4;  // f4 per split
+    for (int s0 = g; s0 < a.nsplit; s0 += 16) {  // up to four loads in flight, summed in order
+      f4 v[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) v[q] = pp[(int64_t)min(s0 + 4 * q, a.nsplit - 1) * sstride];
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        if (s0 + 4 * q < a.nsplit) sum += v[q];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      sum[e] += __shfl_xor(sum[e], 16);
+      sum[e] += __shfl_xor(sum[e], 32);
+    }
+    if (g == 0 && kin) {
+      if (a.g) {  // + g[t] . A[:, k0 .. k0+3]  (src/linear.rs:115-118)
+        f4 ga = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < a.r; j++) {
+          const float gv = a.g[(int64_t)t * a.r + j];
+          const float* av = a.la + (int64_t)j * a.K + k0;  // caller's A: no alignment assumed
+#pragma unroll
+          for (int e = 0; e < 4; e++) ga[e] = fmaf(gv, av[e], ga[e]);
+        }
+        sum += ga;
+      }
+      float* p = a.dx + (int64_t)t * a.K + k0;
+#pragma unroll
+      for (int e = 0; e < 4; e++) p[e] = a.accumulate ? p[e] + sum[e] : sum[e];
     }
   } else {
     // dx fragment f = (b - n_gb - n_ga) * NW + w: dx tile f / 8 (token tile * Kc + K chunk),

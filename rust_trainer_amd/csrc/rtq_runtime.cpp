@@ -117,7 +117,8 @@ enum Kid {
   K_FWD_S_ISUMS = K_FWD_W_ISUMS + F_COUNT,
   K_BWD_PREP = K_FWD_S_ISUMS + F_COUNT,
   K_DX,          // + format
-  K_BWD_FINISH = K_DX + F_COUNT,
+  K_DX16 = K_DX + F_COUNT,  // + format: t <= 16
+  K_BWD_FINISH = K_DX16 + F_COUNT,
   K_ROWS,        // + format
   K_COUNT = K_ROWS + F_COUNT
 };
@@ -129,6 +130,7 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_fwd_q4_0_s_isums", "rtq_fwd_q8_0_s_isums", "rtq_fwd_q4_k_s_isums", "rtq_fwd_q6_k_s_isums",
     "rtq_bwd_prep",
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
+    "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
     "rtq_bwd_finish",
     "rtq_rows_q4_0",        "rtq_rows_q8_0",        "rtq_rows_q4_k",        "rtq_rows_q6_k"};
 
@@ -287,12 +289,6 @@ FwdPlan fwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
 
 size_t fwd_ws_bytes(const FwdPlan& p) { return p.xq_bytes + p.xd_floats * 4 + p.h_floats * 4 + 4 * 256; }
 
-// backward workspace: h, g [t x r], their slice partials [t][r][slices], dx partials [<= 16][t][k]
-size_t bwd_ws_bytes(int64_t t, int64_t r, int64_t n, int64_t k) {
-  const int64_t sl = roundup(cdiv(std::max<int64_t>(n, 1), RTQ_ACT_KQ), 4) + roundup(cdiv(std::max<int64_t>(k, 1), RTQ_ACT_KQ), 4);
-  return (size_t)((2 + sl) * t * std::max<int64_t>(r, 0)) * 4 + (size_t)16 * roundup(t, 64) * roundup(k, 128) * 4 +
-         6 * 256;
-}
 
 // ------------------------------------------------------------------ enqueue: forward
 // y = x.W^T (+bias) (+ s h.B^T);  isums (debug) receives the per-block integer sums.
@@ -352,20 +348,40 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
 }
 
 // ------------------------------------------------------------------ enqueue: backward
-// dx split plan: K chunks x 64-token tiles x row splits, about one 8-wave workgroup per CU (more
-// splits add partial-sum traffic: each split writes and the finish kernel reads T x K floats)
+// dx split plan.
+//   t > 16 (rtq_dx_*): K chunks x 64-token tiles x row splits, about one 8-wave workgroup per CU
+//     (more splits add partial-sum traffic: each split writes and the finish kernel reads a
+//     64-token-padded T x K block);
+//   t <= 16 (rtq_dx16_*): K chunks x row splits, about three 4-wave workgroups per CU with at least
+//     four 32-row steps each (partials are T x K floats per split).
 struct DxPlan {
   int64_t splits, nps;
+  bool tok16;
+  size_t part_floats;
 };
 DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
-  const int64_t base = (w->Kp / 128) * cdiv(t, 64);
-  const int64_t steps = w->Np / 32;
-  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16), cdiv(c->cu_count, base)));
-  if (c->dx_splits > 0) splits = std::min<int64_t>(steps, c->dx_splits);
   DxPlan p;
+  p.tok16 = t <= 16;
+  const int64_t Kc = w->Kp / 128, steps = w->Np / 32;
+  int64_t splits;
+  if (p.tok16)
+    splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(std::max<int64_t>(steps / 4, 1), 256),
+                                                    cdiv(3 * c->cu_count, Kc)));
+  else
+    splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16), cdiv(c->cu_count, Kc * cdiv(t, 64))));
+  if (c->dx_splits > 0) splits = std::min<int64_t>(steps, c->dx_splits);
   p.nps = cdiv(steps, splits) * 32;
   p.splits = cdiv(w->Np, p.nps);
+  p.part_floats = p.tok16 ? (size_t)(p.splits * t * w->cols) : (size_t)(p.splits * roundup(t, 64) * w->Kp);
   return p;
+}
+
+// backward workspace: h, g [t x r], their slice partials [t][r][slices], dx split partials
+size_t bwd_ws_bytes(const rtq_ctx* c, const rtq_weight* w, int64_t t, int64_t r) {
+  const int64_t n = w->rows, k = w->cols;
+  const int64_t sl = roundup(cdiv(std::max<int64_t>(n, 1), RTQ_ACT_KQ), 4) + roundup(cdiv(std::max<int64_t>(k, 1), RTQ_ACT_KQ), 4);
+  return (size_t)((2 + sl) * t * std::max<int64_t>(r, 0)) * 4 + dx_plan(c, w, std::max<int64_t>(t, 1)).part_floats * 4 +
+         6 * 256;
 }
 
 // partial-product slices of the LoRA reductions over n columns (multiple of 4, see sum_partials)
@@ -389,7 +405,7 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   float* g = lora ? ar.take<float>((size_t)(t * r)) : nullptr;
   float* hp = lora ? ar.take<float>((size_t)(nhq * t * r)) : nullptr;
   float* gp = lora ? ar.take<float>((size_t)(ngq * t * r)) : nullptr;
-  float* part = ar.take<float>((size_t)(dp.splits * roundup(t, 64) * w->Kp));  // fragment-order partials
+  float* part = ar.take<float>(dp.part_floats);
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   if (lora) {
     BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq};
@@ -397,15 +413,17 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   }
   DxArgs xa{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, (int)dp.splits, part,
             lora ? hp : nullptr, lora ? gp : nullptr, (int)nhq, (int)ngq, (int)r, s, h, g};
-  const int kid = K_DX + fmt_index(w->type);
-  const int64_t nmain = (w->Kp / 128) * cdiv(t, 64) * dp.splits;
+  const int kid = (dp.tok16 ? K_DX16 : K_DX) + fmt_index(w->type);
+  const int64_t nmain = (w->Kp / 128) * (dp.tok16 ? 1 : cdiv(t, 64)) * dp.splits;
   const int64_t nfin = lora ? std::min<int64_t>(64, cdiv(t * r, 512)) : 0;  // LoRA finalisers
-  RTQ_TRY(launch(c, kid, dim3((unsigned)(nmain + nfin)), dim3(512), st, xa));
+  RTQ_TRY(launch(c, kid, dim3((unsigned)(nmain + nfin)), dim3(dp.tok16 ? 256 : 512), st, xa));
   const int64_t jt = cdiv(r, 16);
-  LoraGradArgs fa{dy, h, g, x, la, (int)t, N, K, (int)r, s, gb, ga, dx, 0, 0, 0, part, (int)dp.splits, accumulate ? 1 : 0};
+  LoraGradArgs fa{dy, h, g, x, la, (int)t, N, K, (int)r, s, gb, ga, dx, 0, 0, 0, part, (int)dp.splits, accumulate ? 1 : 0,
+                  dp.tok16 ? 1 : 0};
   fa.n_gb = lora ? (int)(cdiv(N, 16) * jt) : 0;
   fa.n_ga = lora ? (int)(cdiv(K, 16) * jt) : 0;
-  fa.n_dx = (int)cdiv((w->Kp / 128) * cdiv(t, 64) * 8, 4);  // one wave per dx fragment, four per workgroup
+  // one wave per dx fragment (or per token and 64 columns), four per workgroup
+  fa.n_dx = dp.tok16 ? (int)cdiv(t * cdiv(K, 64), 4) : (int)cdiv((w->Kp / 128) * cdiv(t, 64) * 8, 4);
   return launch(c, K_BWD_FINISH, dim3((unsigned)(fa.n_gb + fa.n_ga + fa.n_dx)), dim3(256), st, fa);
 }
 
@@ -602,7 +620,10 @@ rtq_status rtq_ctx_reserve(rtq_ctx* c, int64_t max_t, int64_t max_rows, int64_t 
   fake.cols = max_cols;
   fake.Np = roundup(max_rows, RTQ_ROW_PAD);
   fake.Kp = roundup(max_cols, RTQ_CHUNK_Q);
-  size_t need = std::max(fwd_ws_bytes(fwd_plan(&fake, max_t, max_rank)), bwd_ws_bytes(max_t, max_rank, max_rows, max_cols));
+  fake.type = RTQ_TYPE_Q4_0;
+  size_t need = fwd_ws_bytes(fwd_plan(&fake, max_t, max_rank));
+  for (int64_t t : {std::min<int64_t>(max_t, 16), max_t})  // both dx paths
+    need = std::max(need, bwd_ws_bytes(c, &fake, t, max_rank));
   RTQ_TRY(ensure_ws(c, need));
   return RTQ_OK;
 }
@@ -771,7 +792,7 @@ rtq_status rtq_frozen_backward_input_d(rtq_ctx* c, const rtq_weight* w, const fl
   std::lock_guard<std::mutex> lk(c->mu);
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t st = (hipStream_t)stream;  // NULL: the HIP null stream
-  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, 0, w->rows, w->cols)));
+  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(c, w, t, 0)));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   return enqueue_backward(c, w, dy, t, dx, true, nullptr, nullptr, nullptr, 0, 0.0f, nullptr, nullptr, ar, st);
 }
@@ -789,7 +810,7 @@ rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora
   std::lock_guard<std::mutex> lk(c->mu);
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t st = (hipStream_t)stream;  // NULL: the HIP null stream
-  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, on ? r : 0, w->rows, w->cols)));
+  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(c, w, t, on ? r : 0)));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   return enqueue_backward(c, w, dy, t, dx, false, x, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, ga, gb,
                           ar, st);
@@ -887,7 +908,7 @@ static rtq_status backward_host(rtq_ctx* c, const rtq_weight* w, const rtq_lora*
   hipStream_t st = c->stream;
   const int64_t N = w->rows, K = w->cols;
   const size_t io = (size_t)(t * N + t * K + (on ? t * K + 2 * r * K + 2 * N * r : 0)) * 4 + 8 * 256;
-  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(t, on ? r : 0, w->rows, w->cols) + io));
+  RTQ_TRY(ensure_ws(c, bwd_ws_bytes(c, w, t, on ? r : 0) + io));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   float* dyd = ar.take<float>((size_t)(t * N));
   float* dxd = ar.take<float>((size_t)(t * K));
