@@ -17,14 +17,16 @@
 //     both: d   fp16  [Np/16][Kc][2 h][4 q][2 j2][4 i]   scale of row 4q+i of the group, block
 //           2h+j2 of the chunk: the lane with k-group q reads the scales of rows 4q..4q+3 for
 //           a half chunk (two blocks) with one 16-byte load, which is the row set a lane holds
-//           in the output of an MFMA whose A operand is the weight.
+//           in the output of an MFMA whose A operand is the weight;
+//           wdr fp16 [Np/16][Kc][16 li][4 j] (RTQ_WR_INDEX): the same scales row by row, for the
+//           GEMV kernel, whose lanes hold one weight row each (8 bytes per lane and chunk).
 //   K-quants (256-element super-blocks, Kp = K) are transcoded at upload into the same code
 //   layouts, with their 6-bit sub-block scales kept as integers:
 //     Q4_K: qs as Q4_0, unsigned 4-bit codes u (value d*sc*u - dmin*m);
 //     Q6_K: qs as Q8_0, signed codes q in [-32, 31] (value d*sc*q, sc per 16 elements);
-//     wd (uint16) [Np/16][Kc][2 h][16 li][2 j2] (RTQ_WK_INDEX): block 2h+j2 of row li, low byte sc
-//           (Q6_K: sc of elements 0..15), high byte m (Q6_K: sc of elements 16..31, int8).  The
-//           lane that builds row li's MFMA fragment for a half chunk reads one 32-bit word;
+//     wd (uint16) [Np/16][Kc][16 li][4 j] (RTQ_WR_INDEX): block j of row li, low byte sc (Q6_K: sc
+//           of elements 0..15), high byte m (Q6_K: sc of elements 16..31, int8).  The lane that
+//           builds row li's MFMA fragment reads one 32-bit word per half chunk;
 //     wsb (uint32) [Np/16][Kp/256][16 li] (RTQ_WSB_INDEX): fp16 d (low) and fp16 dmin (high; 0
 //           for Q6_K) of the super-block; the lane with k-group q reads rows 4q..4q+3 at once.
 #pragma once
@@ -33,10 +35,11 @@
 #define RTQ_ROW_PAD 64    // Np multiple
 #define RTQ_CHUNK_Q 128   // K chunk of Q4_0 / Q8_0
 #define RTQ_ACT_KQ 256    // columns per activation-prep workgroup (one LoRA-down partial each)
+#define RTQ_LDS_RANK 64   // LoRA ranks up to this are staged in LDS by the forward kernels
 
-// index of the K-quant sub-block scale word of row li of row group rg, block j of chunk kc
-#define RTQ_WK_INDEX(rg, kc, Kc, li, j) \
-  (((((int64_t)(rg) * (Kc) + (kc)) * 2 + ((j) >> 1)) * 16 + (li)) * 2 + ((j) & 1))
+// index of the row-major scale (K-quants: sub-block scale word) of row li of row group rg, block j
+// of chunk kc
+#define RTQ_WR_INDEX(rg, kc, Kc, li, j) ((((int64_t)(rg) * (Kc) + (kc)) * 16 + (li)) * 4 + (j))
 // index of the K-quant super-block scale pair of row li of row group rg, super-block sb
 #define RTQ_WSB_INDEX(rg, sb, Ksb, li) (((int64_t)(rg) * (Ksb) + (sb)) * 16 + (li))
 
@@ -54,11 +57,15 @@
 //   zero_y: rows of y cleared when the forward GEMM splits K across workgroups (atomics)
 // rtq_act_prep_q8_k (K-quant weights): Q8_K per 256-column super-block (one workgroup's
 // columns), same xq layout; xd holds the super-block's f32 d for each of its 32-element blocks.
+// xg (GEMV, Tp = 16): [Kp/32][2][16]: the block's scale per token, then -gbias * (sum of the
+// block's codes) per token (the accumulator seed that removes the GEMV's code bias).
 struct ActArgs {
   const float* x;
   int T, K, Tp, Kp;
   void* xq;
   float* xd;
+  float* xg;
+  float gbias;
   const float* A;
   int r;
   float* hp;
@@ -72,6 +79,8 @@ struct ActArgs {
 struct FwdArgs {
   const void* wq;       // quant codes, device layout
   const uint16_t* wd;   // fp16 scales (K-quants: sub-block scale words), device layout
+  const uint16_t* wdr;  // row-major scales (RTQ_WR_INDEX; the K-quants' wd itself)
+  const float* xg;      // GEMV activation scales and seeds [Kp/32][2][16]
   int Np, Kp;
   const void* xq;       // activation fragments (f16 integer codes)
   const float* xd;      // activation scales [Kp/128][Tp][4]

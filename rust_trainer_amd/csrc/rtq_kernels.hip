@@ -355,6 +355,12 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
       for (int i = 0; i < 16; i++) q[i] = (_Float16)fminf(127.0f, rintf(__fmul_rn(iscale, v[i])));
       dstore = best != 0.0f ? __fdiv_rn(1.0f, iscale) : 0.0f;
     }
+    float csum = 0.0f;  // sum of the block's codes (exact integer), for the GEMV's seed
+    if (a.xg) {         // uniform
+#pragma unroll
+      for (int i = 0; i < 16; i++) csum += (float)q[i];
+      csum += __shfl_xor(csum, 1);
+    }
     if (kk < a.Kp) {
       const int b = kk >> 5, hf = sg & 1, kc = b >> 2, j = b & 3;
       // this half block gives, for each k-group g, the four codes of one 8-element fragment half
@@ -367,7 +373,12 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
         w.y = __builtin_bit_cast(uint32_t, hi);
         xq[g * 16 * 2] = w;
       }
-      if (hf == 0) a.xd[((int64_t)kc * a.Tp + t) * 4 + j] = (t < a.T && kk < a.K) ? dstore : 0.0f;
+      const bool real = t < a.T && kk < a.K;
+      if (hf == 0) a.xd[((int64_t)kc * a.Tp + t) * 4 + j] = real ? dstore : 0.0f;
+      if (a.xg && hf == 0) {  // Tp == 16: t is the token within the tile
+        a.xg[(int64_t)(b * 2) * 16 + t] = real ? dstore : 0.0f;
+        a.xg[(int64_t)(b * 2 + 1) * 16 + t] = real ? -a.gbias * csum : 0.0f;
+      }
     }
   }
   if (a.zero_y && blockIdx.y == 0) {
@@ -434,7 +445,7 @@ struct WHalf<FMT_Q8_0> {
 // sub-block scale word (row lane % 16, blocks 2h, 2h+1) and super-block scales (rows 4g..4g+3)
 __device__ __forceinline__ void load_kscales(const uint16_t* wd, const uint32_t* wsb, int rg, int kc, int h, int Kc,
                                              int lane, uint32_t& k, u4v& e) {
-  k = reinterpret_cast<const uint32_t*>(wd)[(((uint32_t)rg * Kc + kc) * 2 + h) * 16 + (lane & 15)];
+  k = reinterpret_cast<const uint32_t*>(wd)[(((uint32_t)rg * Kc + kc) * 16 + (lane & 15)) * 2 + h];
   e = reinterpret_cast<const u4v*>(wsb)[((uint32_t)rg * (Kc >> 1) + (kc >> 1)) * 4 + (lane >> 4)];
 }
 
@@ -495,7 +506,6 @@ struct FwdSlot {
   float xs[TT][2];
 };
 
-#define RTQ_LDS_RANK 64  // LoRA ranks up to this are staged in LDS by the forward GEMM
 
 template <int FMT, int TT, int RG, int D, bool DBG>
 __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
@@ -768,6 +778,235 @@ RTQ_FWD(rtq_fwd_q4_k_s_isums, FMT_Q4_K, 1, 4, 4, true)
 RTQ_FWD(rtq_fwd_q6_k_w_isums, FMT_Q6_K, 4, 2, 2, true)
 RTQ_FWD(rtq_fwd_q6_k_s_isums, FMT_Q6_K, 1, 4, 4, true)
 
+// ============================================================== forward GEMV (T <= 16)
+// MFMA orientation transposed against fwd_tile: A operand = the 16 token slots x 32 columns of the
+// activation fragments, B operand = 32 columns x 16 weight rows, so output lane l holds weight row
+// l % 16 for tokens 4(l/16) .. 4(l/16)+3: one weight scale per lane and block.
+// Q4_0 / Q8_0 weight fragments keep the f16 code bias (1024 + u, u the unsigned code): the MFMA
+// accumulator is seeded with -(1024 + offset) * (sum of the token's codes in the block), computed by
+// the activation prep, so the MFMA output is still the exact integer block sum (every partial is
+// an integer below 2^24) and the fragment costs no subtraction.  K-quants use fwd_tile's scaled
+// fragments and super-block sums.
+// Workgroup = 4 waves, each owning RG row groups over the workgroup's whole K range (the runtime
+// takes this kernel when the row tiles alone give a workgroup per CU: an LM head).  The activation
+// fragments and the per-token block scales and seeds of the workgroup's K range are staged in LDS
+// once; the weight items (one chunk of RG row groups) stream through a D-deep register ring.
+// blockIdx.y splits K across workgroups in whole chunks (whole super-blocks for K-quants),
+// accumulating with atomics into a y the activation prep cleared.
+__device__ __forceinline__ half8 h8_from_words(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const u4v v = {a, b, c, d};
+  return __builtin_bit_cast(half8, v);
+}
+// nibbles of bytes 4g..4g+3 -> 1024 + nibble (low nibbles, then high nibbles)
+__device__ __forceinline__ half8 nib_frag_biased(uint32_t w) {
+  const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+  return h8_from_words(bytes01_to_h2(lo), bytes23_to_h2(lo), bytes01_to_h2(hi), bytes23_to_h2(hi));
+}
+// int8 codes -> 1024 + (q + 128)
+__device__ __forceinline__ half8 byte_frag_biased(uint32_t lo, uint32_t hi) {
+  lo ^= 0x80808080u;
+  hi ^= 0x80808080u;
+  return h8_from_words(bytes01_to_h2(lo), bytes23_to_h2(lo), bytes01_to_h2(hi), bytes23_to_h2(hi));
+}
+
+template <int FMT>
+struct GRow {                          // one row group, one chunk; lane = (row li, k-group g)
+  u4v q[byte_codes(FMT) ? 2 : 1];      // codes: nibble layout (component j = block j) or byte layout (part p)
+  u2v d;                               // row li, blocks 0..3: fp16 scales / K-quant sub-block words
+  uint32_t e;                          // row li: K-quant super-block (d, dmin)
+};
+
+template <int FMT, int RG>
+struct GSlot {
+  GRow<FMT> w[RG];
+};
+
+template <int FMT, int RG, int D>
+__device__ __forceinline__ void gemv_tile(const FwdArgs& a) {
+  constexpr bool KQ = is_kquant(FMT), B8 = byte_codes(FMT);
+  extern __shared__ __attribute__((aligned(16))) char gsm[];
+  __shared__ float sh[16][RTQ_LDS_RANK + 1];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
+  const int Kc = a.Kp / 128, ngroups = a.Np / 16;
+  // this workgroup's chunk range [kcb, kce)
+  const int kcb = blockIdx.y * a.kc_per_split, kce = min(kcb + a.kc_per_split, Kc), kcnt = kce - kcb;
+  u4v* sX = reinterpret_cast<u4v*>(gsm);                             // [kcnt * 4][64]
+  float* sG = reinterpret_cast<float*>(gsm + (size_t)kcnt * 4 * 64 * 16);  // [kcnt * 4][2][16]
+  // this wave's rows, over chunks [c0, c0 + nit)
+  const int rg0 = (blockIdx.x * 4 + w) * RG;
+  const int c0 = kcb, nit = kcnt;
+  int rgc[RG];
+#pragma unroll
+  for (int r = 0; r < RG; r++) rgc[r] = min(rg0 + r, ngroups - 1);
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 acc[RG], s1[KQ ? RG : 1], s2[KQ ? RG : 1];
+#pragma unroll
+  for (int r = 0; r < RG; r++) acc[r] = zero;
+  if (KQ) {
+#pragma unroll
+    for (int r = 0; r < (KQ ? RG : 1); r++) s1[r] = s2[r] = zero;
+  }
+  const bool lead = blockIdx.y == 0;
+  const bool lora = a.hp && lead;
+
+  auto issue = [&](GSlot<FMT, RG>& S, int it) {
+    const int kc = min(c0 + min(it, max(nit - 1, 0)), Kc - 1);  // clamped: always a valid chunk
+#pragma unroll
+    for (int r = 0; r < RG; r++) {
+      const uint32_t base = (uint32_t)rgc[r] * Kc + kc;
+      if (B8) {
+        S.w[r].q[0] = reinterpret_cast<const u4v*>(a.wq)[(base * 2) * 64 + lane];
+        S.w[r].q[B8 ? 1 : 0] = reinterpret_cast<const u4v*>(a.wq)[(base * 2 + 1) * 64 + lane];
+      } else {
+        S.w[r].q[0] = reinterpret_cast<const u4v*>(a.wq)[base * 64 + lane];
+      }
+      S.w[r].d = reinterpret_cast<const u2v*>(a.wdr)[base * 16 + li];
+      if (KQ) S.w[r].e = a.wsb[((uint32_t)rgc[r] * (Kc >> 1) + (kc >> 1)) * 16 + li];
+    }
+  };
+  GSlot<FMT, RG> sl[D];
+#pragma unroll
+  for (int s = 0; s < D - 1; s++) issue(sl[s], s);
+
+  // stage the activation fragments and token scales / seeds of chunks [kcb, kce)
+  {
+    const u4v* XQ = reinterpret_cast<const u4v*>(a.xq);
+    const int nx = kcnt * 4 * 64;
+    for (int i = threadIdx.x; i < nx; i += 256) sX[i] = XQ[(size_t)kcb * 4 * 64 + i];
+    const u4v* XG = reinterpret_cast<const u4v*>(a.xg);
+    const int ng = kcnt * 4 * 2 * 4;
+    for (int i = threadIdx.x; i < ng; i += 256) reinterpret_cast<u4v*>(sG)[i] = XG[(size_t)kcb * 4 * 2 * 4 + i];
+    if (lora)  // the runtime takes this kernel for ranks up to RTQ_LDS_RANK only
+      for (int e = threadIdx.x; e < 16 * a.r; e += 256) {
+        const int t = e / a.r, j = e % a.r;
+        sh[t][j] = t < a.T ? sum_partials(a.hp, (int64_t)t * a.r + j, a.nhp) : 0.0f;
+      }
+  }
+  __syncthreads();
+
+  auto compute = [&](const GSlot<FMT, RG>& S, int it) {
+    const int kc = c0 + it, kl = kc - kcb;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const half8 xf = __builtin_bit_cast(half8, sX[(kl * 4 + j) * 64 + lane]);
+      if constexpr (!KQ) {
+        const f4 dxv = *reinterpret_cast<const f4*>(&sG[((kl * 4 + j) * 2) * 16 + 4 * g]);
+        const f4 seed = *reinterpret_cast<const f4*>(&sG[((kl * 4 + j) * 2 + 1) * 16 + 4 * g]);
+#pragma unroll
+        for (int r = 0; r < RG; r++) {
+          half8 wf;
+          if (B8) {
+            const u4v& qq = S.w[r].q[j >> 1];
+            wf = (j & 1) ? byte_frag_biased(qq.z, qq.w) : byte_frag_biased(qq.x, qq.y);
+          } else {
+            wf = nib_frag_biased(comp(S.w[r].q[0], j));
+          }
+          const f4 c = mfma_f16(xf, wf, seed);
+          const float dw = h2f(hcomp(S.w[r].d, j));
+#pragma unroll
+          for (int e = 0; e < 4; e++) acc[r][e] = fmaf(c[e], dw * dxv[e], acc[r][e]);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < RG; r++) {
+          const uint32_t wv = hcomp(S.w[r].d, j);
+          half8 f1, f2;
+          if (FMT == FMT_Q4_K) {
+            const _Float16 sc = (_Float16)(float)(wv & 0x3fu), m = (_Float16)(float)((wv >> 8) & 0x3fu);
+            f1 = q4_0_frag<0>(comp(S.w[r].q[0], j)) * sc;
+            const half8 mm = {m, m, m, m, m, m, m, m};
+            f2 = mm;
+          } else {
+            const int sa = (int)(int8_t)(wv & 0xffu), sb = (int)(int8_t)((wv >> 8) & 0xffu);
+            const _Float16 h0 = (_Float16)(float)(sa >> 4), h1 = (_Float16)(float)(sb >> 4);
+            const _Float16 l0 = (_Float16)(float)(sa & 15), l1 = (_Float16)(float)(sb & 15);
+            const u4v& qq = S.w[r].q[j >> 1];
+            const half8 qf = (j & 1) ? q8_frag(qq.z, qq.w) : q8_frag(qq.x, qq.y);
+            const half8 sh8 = {h0, h0, h0, h0, h1, h1, h1, h1}, sl8 = {l0, l0, l0, l0, l1, l1, l1, l1};
+            f1 = qf * sh8;
+            f2 = qf * sl8;
+          }
+          s1[r] = mfma_f16(xf, f1, s1[r]);
+          s2[r] = mfma_f16(xf, f2, s2[r]);
+        }
+      }
+    }
+    if constexpr (KQ) {
+      if (kc & 1) {  // last chunk of the super-block
+        const f4 dxv = *reinterpret_cast<const f4*>(&sG[((kl * 4) * 2) * 16 + 4 * g]);  // the super-block's d_x
+#pragma unroll
+        for (int r = 0; r < RG; r++) {
+          const uint32_t ev = S.w[r].e;
+          const float dsb = h2f((uint16_t)(ev & 0xffffu));
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            if (FMT == FMT_Q4_K) {
+              const float dm = h2f((uint16_t)(ev >> 16)) * dxv[e];
+              acc[r][e] = fmaf(dsb * dxv[e], s1[r][e], fmaf(-dm, s2[r][e], acc[r][e]));
+            } else {
+              acc[r][e] = fmaf(dsb * dxv[e], fmaf(16.0f, s1[r][e], s2[r][e]), acc[r][e]);
+            }
+          }
+          s1[r] = zero;
+          s2[r] = zero;
+        }
+      }
+    }
+  };
+  for (int it0 = 0; it0 < nit; it0 += D) {
+#pragma unroll
+    for (int s = 0; s < D; s++) {
+      issue(sl[(s + D - 1) % D], it0 + s + D - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (it0 + s < nit) compute(sl[s], it0 + s);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  const bool split = gridDim.y > 1;
+#pragma unroll
+  for (int r = 0; r < RG; r++) {
+    const int n = (rg0 + r) * 16 + li;
+    if (rg0 + r >= ngroups || n >= a.N) continue;
+    float lo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (lora) {  // LoRA up: sum_j B[n][j] h[t][j] (src/linear.rs:86); rank <= RTQ_LDS_RANK here
+      for (int j0 = 0; j0 < a.r; j0 += 16) {
+        float bv[16];  // sixteen independent loads of B's row n in flight
+#pragma unroll
+        for (int q = 0; q < 16; q++) bv[q] = a.lb[(int64_t)n * a.r + min(j0 + q, a.r - 1)];
+#pragma unroll
+        for (int q = 0; q < 16; q++)
+          if (j0 + q < a.r)
+#pragma unroll
+            for (int e = 0; e < 4; e++) lo[e] = fmaf(bv[q], sh[4 * g + e][j0 + q], lo[e]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int t = 4 * g + e;
+      if (t >= a.T) continue;
+      float o = acc[r][e];
+      if (a.bias && lead) o = o + a.bias[n];
+      if (lora) o = o + a.s * lo[e];
+      float* yp = a.y + (int64_t)t * a.N + n;
+      if (split)
+        atomicAdd(yp, o);
+      else
+        *yp = o;
+    }
+  }
+}
+
+// Q4 layouts: 4 row groups per wave; byte layouts: 2; 4-deep ring.
+#define RTQ_GEMV(NAME, FMT, RG, D)                                         \
+  extern "C" __global__ __launch_bounds__(256) void NAME(FwdArgs a) {      \
+    gemv_tile<FMT, RG, D>(a);                                              \
+  }
+RTQ_GEMV(rtq_gemv_q4_0, FMT_Q4_0, 4, 4)
+RTQ_GEMV(rtq_gemv_q8_0, FMT_Q8_0, 2, 4)
+RTQ_GEMV(rtq_gemv_q4_k, FMT_Q4_K, 4, 4)
+RTQ_GEMV(rtq_gemv_q6_k, FMT_Q6_K, 2, 4)
+
 // ============================================================== backward preparation
 // Grid (ceil(T/16), nhq + ngq), 256 threads (src/linear.rs:106-111); nhq, ngq multiples of 4:
 //   y < nhq:     partial h over columns [256y, 256y + 256) of x . A^T -> hp[t][j][y]
@@ -822,7 +1061,7 @@ template <>
 struct DxSlot<FMT_Q4_K> {
   f4 dy;
   uint32_t q[2];
-  u2v k;  // sub-block scale words of rows 2p, 2p+1 (blocks 2h, 2h+1 of the chunk)
+  u4v k;  // sub-block scale words of rows 2p (x: blocks 0, 1; y: 2, 3) and 2p+1 (z, w)
   u2v e;  // super-block (d, dmin) of rows 2p, 2p+1
 };
 template <>
@@ -842,8 +1081,8 @@ __device__ __forceinline__ void dx_lora_sums(const DxArgs& a, int rel, int nfin)
 // dequantisation of the unsigned byte codes of one row, value fmaf(u, d, m):
 //   Q4_0 (nibble - 8) d;  Q8_0 ((q ^ 0x80) - 128) d;  Q4_K (d sc) u - dmin m;
 //   Q6_K ((q ^ 0x80) - 128) (d sc), sc of the 16-element half hh
-// d16: fp16 scale (Q4_0, Q8_0); kw: the row's sub-block scale words of the half chunk (blocks 2h,
-// 2h+1), ev: its super-block (d, dmin) (K-quants)
+// d16: fp16 scale (Q4_0, Q8_0); kw: the row's sub-block scale words of blocks 2h, 2h+1 of the chunk
+// (h = jb / 2), ev: its super-block (d, dmin) (K-quants)
 template <int FMT>
 __device__ __forceinline__ void dq_params(uint32_t d16, uint32_t kw, uint32_t ev, int jb, int hh, float& d, float& m) {
   if constexpr (is_kquant(FMT)) {
@@ -925,8 +1164,8 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
       q_off[r] = ((((((uint32_t)rgl * Kc + kc) * 2 + (jb >> 1)) * 64 + FL0 + r) * 2 + (jb & 1)) * 2 + hh) * 4u;
   }
   // scales of rows li0, li0+1: adjacent fp16 (Q4_0, Q8_0); for K-quants the two rows' sub-block
-  // words (one 8-byte load) and super-block pairs (one 8-byte load)
-  const uint32_t d_off = KQ ? (uint32_t)RTQ_WK_INDEX(rgl, kc, Kc, li0, jb & 2) * 2u
+  // words (one 16-byte load) and super-block pairs (one 8-byte load)
+  const uint32_t d_off = KQ ? (uint32_t)RTQ_WR_INDEX(rgl, kc, Kc, li0, 0) * 2u
                             : (uint32_t)RTQ_WD_INDEX(rgl, kc, Kc, li0, jb) * 2u;
   const uint32_t e_off = (uint32_t)RTQ_WSB_INDEX(rgl, kc >> 1, Kc >> 1, li0) * 4u;
   const uint32_t q_rg = (uint32_t)Kc * 64 * 16 * (B8 ? 2 : 1);  // bytes per row group
@@ -951,7 +1190,7 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
 #pragma unroll
     for (int r = 0; r < 2; r++) S.q[r] = __builtin_amdgcn_raw_buffer_load_b32(rq, q_off[r], srg * q_rg, 0);
     if constexpr (KQ) {
-      S.k = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(rd, d_off, srg * d_rg, 0));
+      S.k = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rd, d_off, srg * d_rg, 0));
       S.e = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(re, e_off, srg * e_rg, 0));
     } else {
       S.d = __builtin_amdgcn_raw_buffer_load_b32(rd, d_off, srg * d_rg, 0);
@@ -980,7 +1219,7 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
       for (int r = 0; r < 2; r++) {
         float d, m;
         if constexpr (KQ)
-          dq_params<FMT>(0u, r ? S.k.y : S.k.x, r ? S.e.y : S.e.x, jb, hh, d, m);
+          dq_params<FMT>(0u, comp(S.k, 2 * r + (jb >> 1)), r ? S.e.y : S.e.x, jb, hh, d, m);
         else
           dq_params<FMT>(r ? (S.d >> 16) : (S.d & 0xffffu), 0u, 0u, jb, hh, d, m);
         const uint32_t u = B8 ? S.q[r] ^ 0x80808080u : (hh ? (S.q[r] >> 4) : S.q[r]) & 0x0f0f0f0fu;
@@ -1048,7 +1287,8 @@ struct Dx16Slot {
   float2 dy;          // rows 2p, 2p+1 of the step, token tid / 16
   uint32_t q[2][2];   // [row][half] code words (nibble formats: both halves in q[r][0])
   uint32_t d;         // fp16 scales of the two rows (Q4_0, Q8_0)
-  u2v k, e;           // sub-block and super-block scales of the two rows (K-quants)
+  u4v k;              // sub-block scale words of the two rows (K-quants, as DxSlot)
+  u2v e;              // super-block scales of the two rows (K-quants)
 };
 
 template <int FMT>
@@ -1102,7 +1342,7 @@ __device__ __forceinline__ void dx16_tile(const DxArgs& a) {
     else
       q_off[r] = (((((uint32_t)rgl * Kc + kc) * 2 + (jb >> 1)) * 64 + FL0 + r) * 2 + (jb & 1)) * 8u;
   }
-  const uint32_t d_off = KQ ? (uint32_t)RTQ_WK_INDEX(rgl, kc, Kc, li0, jb & 2) * 2u
+  const uint32_t d_off = KQ ? (uint32_t)RTQ_WR_INDEX(rgl, kc, Kc, li0, 0) * 2u
                             : (uint32_t)RTQ_WD_INDEX(rgl, kc, Kc, li0, jb) * 2u;
   const uint32_t e_off = (uint32_t)RTQ_WSB_INDEX(rgl, kc >> 1, Kc >> 1, li0) * 4u;
   const uint32_t q_rg = (uint32_t)Kc * 64 * 16 * (B8 ? 2 : 1);
@@ -1133,7 +1373,7 @@ __device__ __forceinline__ void dx16_tile(const DxArgs& a) {
       }
     }
     if constexpr (KQ) {
-      S.k = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(rd, d_off, srg * d_rg, 0));
+      S.k = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rd, d_off, srg * d_rg, 0));
       S.e = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(re, e_off, srg * e_rg, 0));
     } else {
       S.d = __builtin_amdgcn_raw_buffer_load_b32(rd, d_off, srg * d_rg, 0);
@@ -1155,7 +1395,7 @@ __device__ __forceinline__ void dx16_tile(const DxArgs& a) {
       for (int r = 0; r < 2; r++) {
         float d, m;
         if constexpr (KQ)
-          dq_params<FMT>(0u, r ? S.k.y : S.k.x, r ? S.e.y : S.e.x, jb, hh, d, m);
+          dq_params<FMT>(0u, comp(S.k, 2 * r + (jb >> 1)), r ? S.e.y : S.e.x, jb, hh, d, m);
         else
           dq_params<FMT>(r ? (S.d >> 16) : (S.d & 0xffffu), 0u, 0u, jb, hh, d, m);
         const uint32_t u = B8 ? S.q[r][hh] ^ 0x80808080u : (hh ? (S.q[r][0] >> 4) : S.q[r][0]) & 0x0f0f0f0fu;
@@ -1434,7 +1674,7 @@ __device__ __forceinline__ void rows_kquant(const RowArgs& a) {
   if (idx >= (int64_t)a.count * nb) return;
   const int rl = (int)(idx / nb), b = (int)(idx % nb);
   const int n = a.r0 + rl, rg = n >> 4, li = n & 15, kc = b >> 2, j = b & 3;
-  const uint32_t kw = a.wd[RTQ_WK_INDEX(rg, kc, Kc, li, j)];
+  const uint32_t kw = a.wd[RTQ_WR_INDEX(rg, kc, Kc, li, j)];
   const uint32_t ev = a.wsb[RTQ_WSB_INDEX(rg, kc >> 1, Kc >> 1, li)];
   const float dsb = h2f((uint16_t)(ev & 0xffffu));
   float* out = a.out + (int64_t)rl * a.K + b * 32;

@@ -115,7 +115,8 @@ enum Kid {
   K_FWD_S = K_FWD_W + F_COUNT,            // skinny (t <= 16)
   K_FWD_W_ISUMS = K_FWD_S + F_COUNT,      // debug variants writing the integer sums
   K_FWD_S_ISUMS = K_FWD_W_ISUMS + F_COUNT,
-  K_BWD_PREP = K_FWD_S_ISUMS + F_COUNT,
+  K_GEMV = K_FWD_S_ISUMS + F_COUNT,       // + format: t <= 16, large N
+  K_BWD_PREP = K_GEMV + F_COUNT,
   K_DX,          // + format
   K_DX16 = K_DX + F_COUNT,  // + format: t <= 16
   K_BWD_FINISH = K_DX16 + F_COUNT,
@@ -128,6 +129,7 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_fwd_q4_0_s",       "rtq_fwd_q8_0_s",       "rtq_fwd_q4_k_s",       "rtq_fwd_q6_k_s",
     "rtq_fwd_q4_0_w_isums", "rtq_fwd_q8_0_w_isums", "rtq_fwd_q4_k_w_isums", "rtq_fwd_q6_k_w_isums",
     "rtq_fwd_q4_0_s_isums", "rtq_fwd_q8_0_s_isums", "rtq_fwd_q4_k_s_isums", "rtq_fwd_q6_k_s_isums",
+    "rtq_gemv_q4_0",        "rtq_gemv_q8_0",        "rtq_gemv_q4_k",        "rtq_gemv_q6_k",
     "rtq_bwd_prep",
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
@@ -168,6 +170,7 @@ struct rtq_weight {
   void* dmem = nullptr;
   void* wq = nullptr;
   uint16_t* wd = nullptr;
+  uint16_t* wdr = nullptr;  // row-major scales for the GEMV (the K-quants' wd itself)
   uint32_t* wsb = nullptr;  // K-quant super-block scales, else null
 };
 
@@ -186,7 +189,7 @@ hipEvent_t get_event(rtq_ctx* c) {
 }
 
 template <class Args>
-rtq_status launch(rtq_ctx* c, int kid, dim3 grid, dim3 block, hipStream_t s, const Args& args) {
+rtq_status launch(rtq_ctx* c, int kid, dim3 grid, dim3 block, hipStream_t s, const Args& args, unsigned shmem = 0) {
   if (grid.x == 0 || grid.y == 0 || grid.z == 0) return RTQ_OK;
   if (grid.y > 65535 || grid.z > 65535)
     return fail(RTQ_ERR_INVALID, "%s: grid (%u,%u,%u) out of range", kKernelNames[kid], grid.x, grid.y, grid.z);
@@ -199,8 +202,8 @@ rtq_status launch(rtq_ctx* c, int kid, dim3 grid, dim3 block, hipStream_t s, con
     eb = get_event(c);
     if (ea && eb) HIP_TRY(hipEventRecord(ea, s));
   }
-  hipError_t e = hipModuleLaunchKernel(c->fn[kid], grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, s, params,
-                                       nullptr);
+  hipError_t e = hipModuleLaunchKernel(c->fn[kid], grid.x, grid.y, grid.z, block.x, block.y, block.z, shmem, s,
+                                       params, nullptr);
   if (e != hipSuccess) return fail(RTQ_ERR_HIP, "launch %s: %s", kKernelNames[kid], hipGetErrorString(e));
   if (timed && ea && eb) {
     HIP_TRY(hipEventRecord(eb, s));
@@ -268,26 +271,52 @@ int64_t block_bytes(int type) {
 struct FwdPlan {
   int64_t T, Tp, nhp;
   bool skinny;
-  size_t xq_bytes, xd_floats, h_floats;
+  bool gemv;  // t <= 16 through rtq_gemv_* (see gemv_plan)
+  size_t xq_bytes, xd_floats, xg_floats, h_floats;
 };
 
 constexpr int kFwdWideTT = 4;     // rtq_fwd_*_w: 64 tokens x (16 * wide_rg) rows per workgroup
 constexpr int kFwdSkinnyRG = 4;   // rtq_fwd_*_s: 16 tokens x 64 rows per workgroup
 int wide_rg(int type) { return is_kquant(type) ? 2 : 3; }
+int gemv_rg(int type) { return byte_codes(type) ? 2 : 4; }
+constexpr int64_t kGemvChunkLds = 4 * 64 * 16 + 4 * 2 * 16 * 4;  // LDS bytes per staged chunk
+constexpr int64_t kGemvMaxChunks = 26;                          // <= 117 KB of staged activations
+
+// GEMV grid: (row tiles of 4 waves x RG row groups, K splits); K is split across workgroups
+// (atomics) until there are about two workgroups per CU and the staged chunks fit LDS, in whole
+// chunks (two for K-quants)
+struct GemvPlan {
+  int64_t gx, gy, kcps;
+};
+GemvPlan gemv_plan(const rtq_ctx* c, const rtq_weight* w) {
+  GemvPlan g;
+  const int64_t Kc = w->Kp / 128, ngroups = w->Np / 16, rg = gemv_rg(w->type), unit = is_kquant(w->type) ? 2 : 1;
+  g.gx = cdiv(ngroups, 4 * rg);
+  int64_t ks = 1;
+  if (g.gx < 2 * c->cu_count) ks = std::max<int64_t>(1, std::min<int64_t>(cdiv(2 * c->cu_count, g.gx), Kc / unit));
+  ks = std::max(ks, cdiv(Kc, kGemvMaxChunks));
+  g.kcps = roundup(cdiv(Kc, ks), unit);
+  g.gy = cdiv(Kc, g.kcps);
+  return g;
+}
 
 FwdPlan fwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
   FwdPlan p;
   p.T = t;
   p.skinny = t <= 16;
+  p.gemv = p.skinny && r <= RTQ_LDS_RANK;
   p.Tp = roundup(std::max<int64_t>(t, 1), p.skinny ? 16 : 16 * kFwdWideTT);
   p.nhp = roundup(cdiv(w->Kp, RTQ_ACT_KQ), 4);
   p.xq_bytes = (size_t)p.Tp * w->Kp * 2;  // one f16 per element
   p.xd_floats = (size_t)(w->Kp / 32) * p.Tp;
+  p.xg_floats = p.gemv ? (size_t)(w->Kp / 32) * 2 * 16 : 0;
   p.h_floats = (size_t)p.nhp * t * std::max<int64_t>(r, 0);
   return p;
 }
 
-size_t fwd_ws_bytes(const FwdPlan& p) { return p.xq_bytes + p.xd_floats * 4 + p.h_floats * 4 + 4 * 256; }
+size_t fwd_ws_bytes(const FwdPlan& p) {
+  return p.xq_bytes + p.xd_floats * 4 + p.xg_floats * 4 + p.h_floats * 4 + 5 * 256;
+}
 
 
 // ------------------------------------------------------------------ enqueue: forward
@@ -298,10 +327,47 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
   FwdPlan p = fwd_plan(w, t, lora ? r : 0);
+  // the debug sums come from the skinny / wide kernels; the GEMV pays off once its row tiles alone
+  // give a workgroup per CU (an LM head), below that the skinny kernel's K split wins
+  if (isums || cdiv(w->Np / 16, 4 * gemv_rg(w->type)) < c->cu_count) p.gemv = false;
   void* xq = ar.take<char>(p.xq_bytes);
   float* xd = ar.take<float>(p.xd_floats);
+  float* xg = p.gemv ? ar.take<float>(p.xg_floats) : nullptr;
   float* hp = lora ? ar.take<float>(p.h_floats) : nullptr;
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
+  if (p.gemv) {
+    const GemvPlan gp = gemv_plan(c, w);
+    const float gbias = w->type == RTQ_TYPE_Q4_0 ? 1032.0f : (w->type == RTQ_TYPE_Q8_0 ? 1152.0f : 0.0f);
+    ActArgs aa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xq, xd, xg, gbias, lora ? la : nullptr, (int)r, hp,
+               gp.gy > 1 ? y : nullptr, (int)w->rows};
+    RTQ_TRY(launch(c, is_kquant(w->type) ? K_ACT_PREP_K : K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp),
+                   dim3(256), st, aa));
+    FwdArgs fa{};
+    fa.wq = w->wq;
+    fa.wd = w->wd;
+    fa.wdr = w->wdr;
+    fa.xg = xg;
+    fa.wsb = w->wsb;
+    fa.Np = (int)w->Np;
+    fa.Kp = (int)w->Kp;
+    fa.xq = xq;
+    fa.xd = xd;
+    fa.Tp = (int)p.Tp;
+    fa.T = (int)t;
+    fa.N = (int)w->rows;
+    fa.K = (int)w->cols;
+    fa.kc_per_split = (int)gp.kcps;
+    fa.y = y;
+    fa.bias = bias;
+    fa.hp = hp;
+    fa.nhp = (int)p.nhp;
+    fa.lb = lb;
+    fa.r = (int)r;
+    fa.s = s;
+    const int kid = K_GEMV + fmt_index(w->type);
+    return launch(c, kid, dim3((unsigned)gp.gx, (unsigned)gp.gy), dim3(256), st, fa,
+                  (unsigned)(gp.kcps * kGemvChunkLds));
+  }
   const int64_t Kc = w->Kp / 128;
   const bool kq = is_kquant(w->type);
   const int64_t rg_per_wg = p.skinny ? kFwdSkinnyRG : wide_rg(w->type);
@@ -319,7 +385,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   if (kq) kcps = roundup(kcps, 2);
   ks = cdiv(Kc, kcps);
 
-  ActArgs aa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xq, xd, lora ? la : nullptr, (int)r, hp,
+  ActArgs aa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xq, xd, nullptr, 0.0f, lora ? la : nullptr, (int)r, hp,
              ks > 1 ? y : nullptr, (int)w->rows};
   RTQ_TRY(launch(c, kq ? K_ACT_PREP_K : K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp), dim3(256), st, aa));
   FwdArgs fa{};
@@ -476,7 +542,7 @@ void place_codes(bool bytes, const uint8_t* codes, int64_t rg, int64_t kc, int64
 inline uint16_t le16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
 void repack_q32(int type, const uint8_t* src, int64_t N, int64_t K, int64_t Np, int64_t Kp, uint8_t* wq,
-                uint16_t* wd) {
+                uint16_t* wd, uint16_t* wdr) {
   const int64_t Kc = Kp / 128, nb = K / 32, nbp = Kp / 32, bb = block_bytes(type), rb = nb * bb;
   const bool q4 = type == RTQ_TYPE_Q4_0;
   for (int64_t n = 0; n < Np; n++) {
@@ -494,6 +560,7 @@ void repack_q32(int type, const uint8_t* src, int64_t N, int64_t K, int64_t Np, 
       }
       place_codes(!q4, codes, rg, kc, li, j, Kc, wq);
       wd[RTQ_WD_INDEX(rg, kc, Kc, li, j)] = d;
+      wdr[RTQ_WR_INDEX(rg, kc, Kc, li, j)] = d;
     }
   }
 }
@@ -543,7 +610,7 @@ void repack_kquant(int type, const uint8_t* src, int64_t N, int64_t K, int64_t N
           word = (uint16_t)(blk[192 + 2 * jj] | (blk[193 + 2 * jj] << 8));
         }
         place_codes(!q4k, codes, rg, kc, li, j, Kc, wq);
-        wd[RTQ_WK_INDEX(rg, kc, Kc, li, j)] = word;
+        wd[RTQ_WR_INDEX(rg, kc, Kc, li, j)] = word;
       }
     }
   }
@@ -714,8 +781,10 @@ rtq_status rtq_weight_create(rtq_ctx* c, int type, const void* blocks, size_t nb
   const size_t q_bytes = (size_t)w->Np * nbp * (byte_codes(type) ? 32 : 16);
   const size_t d_bytes = (size_t)w->Np * nbp * 2;
   const size_t e_bytes = is_kquant(type) ? (size_t)w->Np * (w->Kp / 256) * 4 : 0;
+  const size_t r_bytes = is_kquant(type) ? 0 : d_bytes;  // row-major copy of the fp16 scales
   const size_t q_off = 0, d_off = roundup((int64_t)q_bytes, 256), e_off = d_off + roundup((int64_t)d_bytes, 256);
-  const size_t total = e_off + roundup((int64_t)e_bytes, 256);
+  const size_t r_off = e_off + roundup((int64_t)e_bytes, 256);
+  const size_t total = r_off + roundup((int64_t)r_bytes, 256);
   if (q_bytes >= (1ull << 31)) {  // the kernels address codes with 32-bit buffer offsets
     delete w;
     return fail(RTQ_ERR_INVALID, "weight %lldx%lld: %zu code bytes exceed 2 GiB", (long long)rows, (long long)cols, q_bytes);
@@ -726,7 +795,7 @@ rtq_status rtq_weight_create(rtq_ctx* c, int type, const void* blocks, size_t nb
                   reinterpret_cast<uint16_t*>(host.data() + d_off), reinterpret_cast<uint32_t*>(host.data() + e_off));
   else
     repack_q32(type, (const uint8_t*)blocks, rows, cols, w->Np, w->Kp, host.data() + q_off,
-               reinterpret_cast<uint16_t*>(host.data() + d_off));
+               reinterpret_cast<uint16_t*>(host.data() + d_off), reinterpret_cast<uint16_t*>(host.data() + r_off));
   hipError_t e = hipMalloc(&w->dmem, total);
   if (e != hipSuccess) {
     delete w;
@@ -741,6 +810,7 @@ rtq_status rtq_weight_create(rtq_ctx* c, int type, const void* blocks, size_t nb
   w->wq = (char*)w->dmem + q_off;
   w->wd = reinterpret_cast<uint16_t*>((char*)w->dmem + d_off);
   w->wsb = is_kquant(type) ? reinterpret_cast<uint32_t*>((char*)w->dmem + e_off) : nullptr;
+  w->wdr = is_kquant(type) ? w->wd : reinterpret_cast<uint16_t*>((char*)w->dmem + r_off);
   *out = w;
   return RTQ_OK;
 }
@@ -987,7 +1057,7 @@ rtq_status rtq_debug_quantize_acts(rtq_ctx* c, const rtq_weight* w, const float*
   float* xs = ar.take<float>(p.xd_floats);
   RTQ_TRY(h2d(xdv, x, (size_t)(t * K) * 4, st));
   const bool kq = is_kquant(w->type);
-  ActArgs aa{xdv, (int)t, (int)K, (int)p.Tp, (int)w->Kp, xq, xs, nullptr, 0, nullptr, nullptr, 0};
+  ActArgs aa{xdv, (int)t, (int)K, (int)p.Tp, (int)w->Kp, xq, xs, nullptr, 0.0f, nullptr, 0, nullptr, nullptr, 0};
   RTQ_TRY(launch(c, kq ? K_ACT_PREP_K : K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp), dim3(256), st, aa));
   std::vector<uint8_t> hq(p.xq_bytes);
   std::vector<float> hs(p.xd_floats);

@@ -192,6 +192,28 @@ def test_linear_lora_matches_oracle(ctx, wtype, n, k, t, r):
     assert rel_err(lin.lora.gb - gb0, wgb) <= TOL
 
 
+@pytest.mark.parametrize("wtype", FORMATS)
+@pytest.mark.parametrize("t", [1, 7, 16])
+def test_linear_lora_large_n(ctx, wtype, t):
+    # N = 65536 takes the T <= 16 GEMV kernel with K split across workgroups (atomics), plus the
+    # LoRA up-projection and bias in its epilogue
+    n, k, r = 65536, 1024, 16
+    alpha = 32.0
+    blocks, x, dy = make(wtype, n, k, t)
+    A, B = lora(n, k, r)
+    bias = O.Rng(6).vec_normal(n, 0.1)
+    lin = rt.Linear("blk.0.ffn_up", hip(ctx, wtype, blocks, n, k), bias=bias)
+    lin.lora = rt.Lora(r, alpha, A, B)
+    y = lin.forward(x, t)
+    want = O.linear_forward(wtype, blocks, n, k, x, bias=bias, A=A, B=B, alpha=alpha, nthreads=8)
+    assert rel_err(y, want) <= TOL
+    dx = lin.backward(x, dy, t)
+    wdx, wga, wgb = O.linear_backward(wtype, blocks, n, k, x, dy, A=A, B=B, alpha=alpha, nthreads=8)
+    assert rel_err(dx, wdx) <= TOL
+    assert rel_err(lin.lora.ga, wga) <= TOL
+    assert rel_err(lin.lora.gb, wgb) <= TOL
+
+
 def test_linear_disabled_adapter_and_no_bias(ctx):
     n, k, t, r = 256, 256, 9, 4
     blocks, x, dy = make(O.Q4_0, n, k, t)
