@@ -24,6 +24,12 @@ T in {1, 16, 256, 2048}, LoRA r=16 except on the LM head.  Per case it times a g
 operand sets of at least 512 MB in total, and prints one JSON line with the per-call time and the
 call's roofline fraction (algorithmic bytes and flops, each operand touched once).  ``--case
 FMT:SHAPE:T`` runs one of those cases (for a kernel trace of it).
+
+``--traffic`` runs 24 eager config-1 steps and then three 64 MiB device copies, for two
+``rocprofv3 --pmc`` passes (FETCH_SIZE, then WRITE_SIZE); ``--traffic-report FETCH_DIR WRITE_DIR``
+turns the two passes into HBM bytes per launch of each library kernel (each counter scaled so that
+the copies read and write 64 MiB), writes ``profiles/traffic_<kernel>_config1.json`` (read by the
+default run for ``roofline.traffic``) and prints a table.
 """
 from __future__ import annotations
 
@@ -54,9 +60,8 @@ def kernel_work(name: str) -> tuple[float, float] | None:
         return float(w_bytes + T * N * 4 + T * K * 4), float(2 * T * N * K)
     if name == "rtq_act_prep_q8_0":  # quantise x, h = x.A^T
         return float(T * K * 4 + T * K + T * (K // 32) * 4 + R * K * 4 + T * R * 4), float(2 * T * K * R)
-    if name == "rtq_bwd_prep":  # h = x.A^T, partial g = dy.B, clear dx
-        return float(T * K * 4 + T * N * 4 + (R * K + N * R) * 4 + 2 * T * R * 4 + T * K * 4), \
-            float(2 * T * R * (K + N))
+    if name == "rtq_bwd_prep":  # partials of h = x.A^T and g = dy.B
+        return float(T * K * 4 + T * N * 4 + (R * K + N * R) * 4 + 2 * T * R * 4), float(2 * T * R * (K + N))
     if name == "rtq_bwd_finish":  # dB, dA, dx = sum of split partials + g.A
         return float(T * N * 4 + T * K * 4 + 2 * T * R * 4 + 2 * (N * R + R * K) * 4 + 2 * T * K * 4), \
             float(2 * T * R * (N + 2 * K))
@@ -216,6 +221,96 @@ def sweep(cases: list[tuple[str, str, int]], calls_min: int) -> None:
     ctx.close()
 
 
+# ---------------------------------------------------------------- HBM traffic (rocprofv3 --pmc)
+COPY_MIB = 64
+
+
+def traffic_run() -> None:
+    import torch
+
+    import rust_trainer_amd as rt
+    from rust_trainer_amd import _ffi, synth
+
+    dev = torch.device("cuda", 0)
+    ctx = rt.Context(0)
+    ctx.reserve(T, N, K, R)
+    L = _ffi.lib()
+    blocks = synth.quantize_q4_0(synth.Rng(1).vec_normal(N * K, 0.02).reshape(N, K))
+    sets = []
+    for _ in range(8):
+        s = {"w": rt.HipFrozen(rt.TYPE_Q4_0, blocks, N, K, ctx=ctx), "x": torch.randn(T, K, device=dev),
+             "dy": torch.randn(T, N, device=dev), "y": torch.empty(T, N, device=dev), "dx": torch.empty(T, K, device=dev),
+             "a": torch.randn(R, K, device=dev) / 32.0, "b": torch.randn(N, R, device=dev) * 0.01,
+             "ga": torch.zeros(R, K, device=dev), "gb": torch.zeros(N, R, device=dev)}
+        s["lora"] = _ffi.RtqLora(R, ALPHA, s["a"].data_ptr(), s["b"].data_ptr(), 1)
+        sets.append(s)
+    st = torch.cuda.current_stream().cuda_stream
+    for i in range(24):
+        s = sets[i % len(sets)]
+        lp = ctypes.byref(s["lora"])
+        _ffi.check(L.rtq_linear_forward_d(ctx.handle, s["w"].handle, None, lp, s["x"].data_ptr(), T, s["y"].data_ptr(),
+                                          st), "forward")
+        _ffi.check(L.rtq_linear_backward_d(ctx.handle, s["w"].handle, lp, s["x"].data_ptr(), s["dy"].data_ptr(), T,
+                                           s["dx"].data_ptr(), s["ga"].data_ptr(), s["gb"].data_ptr(), st), "backward")
+    torch.cuda.synchronize()
+    src = torch.empty(COPY_MIB * 2**20 // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for s in sets:
+        s["w"].close()
+    ctx.close()
+    print("traffic run done", flush=True)
+
+
+def traffic_report(fetch_dir: str, write_dir: str) -> None:
+    """Counter CSVs of the two --pmc passes -> profiles/traffic_<kernel>_config1.json and a table."""
+    import csv
+    import glob
+
+    def read(d: str, counter: str) -> tuple[dict, float]:
+        per: dict = {}
+        copies = []
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] != counter:
+                    continue
+                v, name = float(r["Counter_Value"]), r["Kernel_Name"]
+                dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
+                if name.startswith("rtq_"):
+                    per.setdefault(name, []).append((v, dur))
+                elif "copy" in name.lower():
+                    copies.append(v)
+        copies.sort()
+        return per, (sum(copies[-3:]) / len(copies[-3:]) if copies else 0.0)
+
+    fetch, fcopy = read(fetch_dir, "FETCH_SIZE")
+    write, wcopy = read(write_dir, "WRITE_SIZE")
+    ff = COPY_MIB * 1024 / fcopy if fcopy else None  # KiB the copy moves / KiB the counter reads
+    wf = COPY_MIB * 1024 / wcopy if wcopy else None
+    rows = []
+    for name in sorted(set(fetch) & set(write)):
+        fk = sum(v for v, _ in fetch[name]) / len(fetch[name])
+        wk = sum(v for v, _ in write[name]) / len(write[name])
+        total = (fk * ff + wk * wf) * 1024 if ff and wf else None
+        algo = kernel_work(name)
+        out = {"kernel": name, "workload": "configs[0] (Q4_0 3072x1024, T=256, LoRA r=16)",
+               "fetch_kib_raw": round(fk, 1), "write_kib_raw": round(wk, 1),
+               "fetch_scale": round(ff, 4) if ff else None, "write_scale": round(wf, 4) if wf else None,
+               "bytes_per_launch": round(total) if total else None,
+               "algorithmic_bytes": int(algo[0]) if algo else None, "launches": len(fetch[name])}
+        json.dump(out, open(os.path.join(ROOT, "profiles", f"traffic_{name}_config1.json"), "w"), indent=1)
+        rows.append(out)
+    print(f"calibration: {COPY_MIB} MiB copies read {fcopy:.0f} KiB (FETCH_SIZE) and write {wcopy:.0f} KiB "
+          f"(WRITE_SIZE) -> scales {ff:.4f} / {wf:.4f}")
+    print("| kernel | launches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes/launch (scaled) | algorithmic bytes |")
+    print("|---|---|---|---|---|---|")
+    for o in rows:
+        print(f"| {o['kernel']} | {o['launches']} | {o['fetch_kib_raw']} | {o['write_kib_raw']} | "
+              f"{o['bytes_per_launch']} | {o['algorithmic_bytes']} |")
+
+
 def cpu_baseline(inputs, seconds: float) -> dict:
     """The CPU oracle (C restatement of the reference algorithm) on the host cores, bounded sample."""
     import numpy as np
@@ -249,12 +344,20 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="configs[1] sweep: one JSON line per case")
     ap.add_argument("--case", default=None, help="one sweep case FMT:SHAPE:T, e.g. Q4_K:lm_head:1")
     ap.add_argument("--calls", type=int, default=50, help="sweep: calls per timed graph (at least the sets)")
+    ap.add_argument("--traffic", action="store_true", help="config-1 steps + calibration copies for --pmc passes")
+    ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
+    if args.traffic_report:
+        traffic_report(*args.traffic_report)
+        return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build runs the hot path on one GPU only; --gpus {args.gpus} "
               f"(WORLD_SIZE={world}) is not supported (the multi-GPU sharding is design-only)", file=sys.stderr)
         return 2
+    if args.traffic:
+        traffic_run()
+        return 0
     if args.sweep or args.case:
         if args.case:
             fmt, shape, t = args.case.split(":")

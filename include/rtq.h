@@ -30,7 +30,7 @@ extern "C" {
 typedef int rtq_status;
 #define RTQ_OK 0
 #define RTQ_ERR_INVALID 1     /* bad argument / shape mismatch (reference: assert!) */
-#define RTQ_ERR_UNSUPPORTED 2 /* weight type not implemented on the GPU path */
+#define RTQ_ERR_UNSUPPORTED 2 /* ggml type other than Q4_0, Q8_0, Q4_K, Q6_K */
 #define RTQ_ERR_HIP 3         /* HIP runtime error (message in rtq_last_error) */
 #define RTQ_ERR_NO_DEVICE 4   /* no usable gfx950 device / code object failed to load */
 
