@@ -507,9 +507,10 @@ struct FwdSlot {
 };
 
 
-template <int FMT, int TT, int RG, int D, bool DBG>
+template <int FMT, int TT, int RG, int D, bool DBG, int NW = 4>
 __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
   constexpr bool KQ = is_kquant(FMT);
+  static_assert(NW == 4 || (NW == 8 && !KQ), "K-quant tiles split K over four waves");
   __shared__ f4 red[4][TT * RG][64];
   __shared__ float sh[TT * 16][RTQ_LDS_RANK + 1];  // LoRA down projection rows of this tile's tokens
   __shared__ float sb[RG * 16][RTQ_LDS_RANK + 1];  // LoRA B rows of this tile
@@ -525,9 +526,9 @@ __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
     const int nsb = (hc1 - hc0) >> 2;
     nit = nsb > w ? (nsb - w + 3) / 4 * 4 : 0;
   } else {
-    nit = hc1 - hc0 > w ? (hc1 - hc0 - w + 3) / 4 : 0;
+    nit = hc1 - hc0 > w ? (hc1 - hc0 - w + NW - 1) / NW : 0;
   }
-  auto item_hc = [&](int it) { return KQ ? hc0 + 4 * (w + 4 * (it >> 2)) + (it & 3) : hc0 + w + 4 * it; };
+  auto item_hc = [&](int it) { return KQ ? hc0 + 4 * (w + 4 * (it >> 2)) + (it & 3) : hc0 + w + NW * it; };
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
   f4 acc[TT][RG];
   f4 s1[KQ ? TT : 1][KQ ? RG : 1], s2[KQ ? TT : 1][KQ ? RG : 1];  // K-quant super-block sums
@@ -657,9 +658,9 @@ __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
   // D-deep ring; item it lives in slot it % D
 #pragma unroll
   for (int s = 0; s < D - 1; s++) issue(sl[s], s);
-  if (lora_lds) {
-    // stage h rows of this tile's tokens and B rows of its weight rows, 16 ranks at a time;
-    // the loads are issued after the ring prologue and overlap it
+  if (lora_lds && threadIdx.x < 256) {
+    // stage h rows of this tile's tokens and B rows of its weight rows, 16 ranks at a time, by the
+    // first four waves; the loads are issued after the ring prologue and overlap it
     for (int j0 = 0; j0 < a.r; j0 += 16) {
       constexpr int NH = TT * 16 * 16 / 256, NB = (RG * 16 * 16 + 255) / 256;
       float hv[NH], bv[NB];
@@ -695,14 +696,33 @@ __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
     }
   }
 
-  // ---- reduce the four waves' partial tiles: wave w finalises pairs p = w, w + 4, ...
+  // ---- reduce the waves' partial tiles (eight waves: w + 4 into w first), then wave w < 4
+  // finalises pairs p = w, w + 4, ...
+  if (NW == 8) {
+    if (w >= 4) {
 #pragma unroll
-  for (int i = 0; i < TT; i++)
+      for (int i = 0; i < TT; i++)
 #pragma unroll
-    for (int r = 0; r < RG; r++) red[w][i * RG + r][lane] = acc[i][r];
+        for (int r = 0; r < RG; r++) red[w - 4][i * RG + r][lane] = acc[i][r];
+    }
+    __syncthreads();
+    if (w < 4) {
+#pragma unroll
+      for (int i = 0; i < TT; i++)
+#pragma unroll
+        for (int r = 0; r < RG; r++) acc[i][r] += red[w][i * RG + r][lane];
+    }
+    __syncthreads();
+  }
+  if (w < 4) {
+#pragma unroll
+    for (int i = 0; i < TT; i++)
+#pragma unroll
+      for (int r = 0; r < RG; r++) red[w][i * RG + r][lane] = acc[i][r];
+  }
   __syncthreads();
   const bool split = gridDim.z > 1;
-  for (int p = w; p < TT * RG; p += 4) {
+  for (int p = w; p < (w < 4 ? TT * RG : 0); p += 4) {
     const int i = p / RG, r = p % RG;
     const f4 v0 = red[0][p][lane], v1 = red[1][p][lane], v2 = red[2][p][lane], v3 = red[3][p][lane];
     f4 v;
@@ -762,6 +782,13 @@ __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
     fwd_tile<FMT, TT, RG, D, DBG>(a);                                        \
   }
 RTQ_FWD(rtq_fwd_q4_0_w, FMT_Q4_0, 4, 3, 2, false)
+// eight waves splitting K (two per SIMD), Q4_0 / Q8_0
+#define RTQ_FWD8(NAME, FMT, TT, RG, D)                                       \
+  extern "C" __global__ __launch_bounds__(512) void NAME(FwdArgs a) {        \
+    fwd_tile<FMT, TT, RG, D, false, 8>(a);                                   \
+  }
+RTQ_FWD8(rtq_fwd_q4_0_w8, FMT_Q4_0, 4, 3, 2)
+RTQ_FWD8(rtq_fwd_q8_0_w8, FMT_Q8_0, 4, 3, 2)
 RTQ_FWD(rtq_fwd_q4_0_s, FMT_Q4_0, 1, 4, 4, false)
 RTQ_FWD(rtq_fwd_q8_0_w, FMT_Q8_0, 4, 3, 2, false)
 RTQ_FWD(rtq_fwd_q8_0_s, FMT_Q8_0, 1, 4, 4, false)

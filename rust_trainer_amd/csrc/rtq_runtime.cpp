@@ -116,7 +116,9 @@ enum Kid {
   K_FWD_W_ISUMS = K_FWD_S + F_COUNT,      // debug variants writing the integer sums
   K_FWD_S_ISUMS = K_FWD_W_ISUMS + F_COUNT,
   K_GEMV = K_FWD_S_ISUMS + F_COUNT,       // + format: t <= 16, large N
-  K_BWD_PREP = K_GEMV + F_COUNT,
+  K_FWD_Q4_0_W8 = K_GEMV + F_COUNT,       // wide forward with eight waves splitting K
+  K_FWD_Q8_0_W8,
+  K_BWD_PREP,
   K_DX,          // + format
   K_DX16 = K_DX + F_COUNT,  // + format: t <= 16
   K_BWD_FINISH = K_DX16 + F_COUNT,
@@ -130,6 +132,7 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_fwd_q4_0_w_isums", "rtq_fwd_q8_0_w_isums", "rtq_fwd_q4_k_w_isums", "rtq_fwd_q6_k_w_isums",
     "rtq_fwd_q4_0_s_isums", "rtq_fwd_q8_0_s_isums", "rtq_fwd_q4_k_s_isums", "rtq_fwd_q6_k_s_isums",
     "rtq_gemv_q4_0",        "rtq_gemv_q8_0",        "rtq_gemv_q4_k",        "rtq_gemv_q6_k",
+    "rtq_fwd_q4_0_w8",      "rtq_fwd_q8_0_w8",
     "rtq_bwd_prep",
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
@@ -157,6 +160,7 @@ struct rtq_ctx {
   std::vector<TimedLaunch> pending;
   std::vector<hipEvent_t> free_events;
   int dx_splits = 0;  // 0: automatic; RTQ_DX_SPLITS overrides (tuning)
+  int fwd_waves = 8;  // waves splitting K in the wide Q4_0 / Q8_0 forward (RTQ_FWD_WAVES: 4 or 8)
   int64_t t_launches[K_COUNT] = {};
   double t_ms[K_COUNT] = {};
 };
@@ -411,8 +415,13 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   fa.r = (int)r;
   fa.s = s;
   fa.isums = isums;
-  const int kid = (p.skinny ? (isums ? K_FWD_S_ISUMS : K_FWD_S) : (isums ? K_FWD_W_ISUMS : K_FWD_W)) + fmt_index(w->type);
-  return launch(c, kid, dim3((unsigned)gx, (unsigned)gy, (unsigned)ks), dim3(256), st, fa);
+  int kid = (p.skinny ? (isums ? K_FWD_S_ISUMS : K_FWD_S) : (isums ? K_FWD_W_ISUMS : K_FWD_W)) + fmt_index(w->type);
+  int threads = 256;
+  if (!p.skinny && !isums && !kq && c->fwd_waves == 8) {
+    kid = w->type == RTQ_TYPE_Q4_0 ? K_FWD_Q4_0_W8 : K_FWD_Q8_0_W8;
+    threads = 512;
+  }
+  return launch(c, kid, dim3((unsigned)gx, (unsigned)gy, (unsigned)ks), dim3(threads), st, fa);
 }
 
 // ------------------------------------------------------------------ enqueue: backward
@@ -641,6 +650,7 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   c->device = device;
   c->cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   if (const char* e = getenv("RTQ_DX_SPLITS")) c->dx_splits = atoi(e);
+  if (const char* e = getenv("RTQ_FWD_WAVES")) c->fwd_waves = atoi(e) == 4 ? 4 : 8;
   hipError_t e = hipModuleLoadData(&c->mod, rtq_hsaco_begin);
   if (e != hipSuccess) {
     delete c;
