@@ -56,7 +56,7 @@ def kernel_work(name: str) -> tuple[float, float] | None:
     if name.startswith("rtq_fwd_"):
         acts = T * K + T * (K // 32) * 2  # int8 codes + fp16 scales
         return float(w_bytes + acts + T * N * 4 + N * R * 4 + T * R * 4), float(2 * T * N * K + 2 * T * N * R)
-    if name.startswith("rtq_dx_"):
+    if name.startswith("rtq_dx"):  # rtq_dx_*, rtq_dx2_*, rtq_dx16_*
         return float(w_bytes + T * N * 4 + T * K * 4), float(2 * T * N * K)
     if name == "rtq_act_prep_q8_0":  # quantise x, h = x.A^T
         return float(T * K * 4 + T * K + T * (K // 32) * 4 + R * K * 4 + T * R * 4), float(2 * T * K * R)
@@ -68,8 +68,10 @@ def kernel_work(name: str) -> tuple[float, float] | None:
     return None
 
 
-def roofline(name: str, avg_ms: float) -> dict:
+def roofline(name: str, avg_ms: float) -> dict | None:
     work = kernel_work(name)
+    if work is None:
+        return None
     bytes_, flops = work
     ai = flops / bytes_ if bytes_ else 0.0
     ridge = F16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
