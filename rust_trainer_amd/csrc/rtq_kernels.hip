@@ -1223,7 +1223,7 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
       S.d = __builtin_amdgcn_raw_buffer_load_b32(rd, d_off, srg * d_rg, 0);
     }
   };
-  auto stage_compute = [&](const DxSlot<FMT>& S, int buf) {
+  auto stage = [&](const DxSlot<FMT>& S, int buf) {
     {  // dy: A fragment tile tl>>4, lane (tl&15) + 16*(q4>>1), slots 4*(q4&1) .. +3
       // bit view of the whole vector: masking bit_casts of single float4 lanes is miscompiled
       // by this compiler (every lane gets lane 0's mask)
@@ -1266,42 +1266,66 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
         *reinterpret_cast<uint32_t*>(&sW[buf][1][kb + e][ns]) = __builtin_amdgcn_perm(lb[1][e], lb[0][e], 0x07060302u);
       }
     }
-    __syncthreads();
+  };
+  // the wave's operand fragments of one step: A (dy) hi / lo of its two token tiles, B (W) hi / lo
+  // of its two column tiles
+  struct Frags {
+    bf8 a[2][2], b[2][2];
+  };
+  auto load_frags = [&](int buf, Frags& F) {
 #pragma unroll
     for (int ts = 0; ts < 2; ts++) {
-      const bf8 ah = __builtin_bit_cast(bf8, sA[buf][wt * 2 + ts][0][lane]);
-      const bf8 al = __builtin_bit_cast(bf8, sA[buf][wt * 2 + ts][1][lane]);
+      F.a[ts][0] = __builtin_bit_cast(bf8, sA[buf][wt * 2 + ts][0][lane]);
+      F.a[ts][1] = __builtin_bit_cast(bf8, sA[buf][wt * 2 + ts][1][lane]);
+    }
 #pragma unroll
-      for (int ks = 0; ks < 2; ks++) {
-        const int kl = wk * 32 + ks * 16 + li;  // column kl lies in block wk: rows swizzled by 8 wk
-        const bf8 bh = *reinterpret_cast<const bf8*>(&sW[buf][0][kl][8 * (g ^ wk)]);
-        const bf8 bl = *reinterpret_cast<const bf8*>(&sW[buf][1][kl][8 * (g ^ wk)]);
-        acc[ts][ks] = mfma_bf16(ah, bh, acc[ts][ks]);
-        acc[ts][ks] = mfma_bf16(al, bh, acc[ts][ks]);
-        acc[ts][ks] = mfma_bf16(ah, bl, acc[ts][ks]);
-      }
+    for (int ks = 0; ks < 2; ks++) {
+      const int kl = wk * 32 + ks * 16 + li;  // column kl lies in block wk: rows swizzled by 8 wk
+      F.b[ks][0] = *reinterpret_cast<const bf8*>(&sW[buf][0][kl][8 * (g ^ wk)]);
+      F.b[ks][1] = *reinterpret_cast<const bf8*>(&sW[buf][1][kl][8 * (g ^ wk)]);
     }
   };
+  auto compute = [&](const Frags& F) {
+#pragma unroll
+    for (int ts = 0; ts < 2; ts++)
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) {
+        acc[ts][ks] = mfma_bf16(F.a[ts][0], F.b[ks][0], acc[ts][ks]);
+        acc[ts][ks] = mfma_bf16(F.a[ts][1], F.b[ks][0], acc[ts][ks]);
+        acc[ts][ks] = mfma_bf16(F.a[ts][0], F.b[ks][1], acc[ts][ks]);
+      }
+  };
+  // Step s: one barrier (buffer s & 1 is staged by all waves, buffer (s + 1) & 1 is free: every
+  // wave has finished step s - 1's reads), then step s's fragments are read from LDS, step s + 1 is
+  // staged while those reads complete (LDS operations complete in order: reads issued first), and
+  // step s's MFMAs run under the staging's tail.  Loads run D - 1 steps ahead of the MFMAs.
 #pragma unroll
   for (int s0 = 0; s0 < D - 1; s0++) issue(sl[s0], s0);
+  if (nsteps > 0) stage(sl[0], 0);
   for (int st0 = 0; st0 < nsteps; st0 += D) {
 #pragma unroll
     for (int s0 = 0; s0 < D; s0++) {
-      issue(sl[(s0 + D - 1) % D], st0 + s0 + D - 1);
+      const int step = st0 + s0;
+      issue(sl[(s0 + D - 1) % D], step + D - 1);
       __builtin_amdgcn_sched_barrier(0);
-      if (st0 + s0 < nsteps) stage_compute(sl[s0], (st0 + s0) & 1);
+      __syncthreads();
+      Frags F;
+      if (step < nsteps) load_frags(step & 1, F);
+      if (step + 1 < nsteps) stage(sl[(s0 + 1) % D], (step + 1) & 1);
+      if (step < nsteps) compute(F);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  // partial tile of this split in fragment order: part[sp][tile][wave][lane][16], tile = token
-  // tile * Kc + K chunk; element ts*8 + ks*4 + i is row t0 + 32wt + 16ts + 4g + i, column
-  // 128kc + 32wk + 16ks + li.  Four 16-byte stores per lane, contiguous per wave.
+  // partial tile of this split in fragment order: part[sp][tile][wave][q][lane] (float4 each),
+  // tile = token tile * Kc + K chunk, q = 2 ts + ks; its element i is row t0 + 32wt + 16ts + 4g + i,
+  // column 128kc + 32wk + 16ks + li.  Each of the four 16-byte stores of a wave writes 1 KB
+  // contiguously.
   f4* out = reinterpret_cast<f4*>(a.part) +
-            ((((int64_t)sp * ntt + (t0 >> 6)) * Kc + kc) * 8 + w) * 256 + lane * 4;
+            ((((int64_t)sp * ntt + (t0 >> 6)) * Kc + kc) * 8 + w) * 256 + lane;
 #pragma unroll
   for (int ts = 0; ts < 2; ts++)
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) out[ts * 2 + ks] = acc[ts][ks];
+    for (int ks = 0; ks < 2; ks++) out[(ts * 2 + ks) * 64] = acc[ts][ks];
 }
 
 // ============================================================== dx = dy . W for T <= 16
@@ -1597,14 +1621,14 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a)
     const int t0 = (tile / Kc) * 64 + wt * 32, k0 = (tile % Kc) * 128 + wk * 32;
     const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     f4 ps[2][2] = {{zero, zero}, {zero, zero}};
-    const f4* pp = reinterpret_cast<const f4*>(a.part) + (int64_t)f * 256 + lane * 4;
+    const f4* pp = reinterpret_cast<const f4*>(a.part) + (int64_t)f * 256 + lane;
     const int64_t sstride = (int64_t)ntt * Kc * 8 * 256;  // f4 per split
     for (int s0 = 0; s0 < a.nsplit; s0 += 2) {  // two splits' fragments in flight, summed in order
       f4 v[2][4];
 #pragma unroll
       for (int q = 0; q < 2; q++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[q][e] = pp[(int64_t)min(s0 + q, a.nsplit - 1) * sstride + e];
+        for (int e = 0; e < 4; e++) v[q][e] = pp[(int64_t)min(s0 + q, a.nsplit - 1) * sstride + e * 64];
 #pragma unroll
       for (int q = 0; q < 2; q++)
         if (s0 + q < a.nsplit)
