@@ -1518,7 +1518,7 @@ extern "C" __global__ __launch_bounds__(512) void rtq_dx_q6_k(DxArgs a) { dx_til
 // gb[n][j] += sum_t (s*dy[t][n]) h[t][j]   (matmul_tn_acc, src/linear.rs:109)
 // ga[j][k] += sum_t g[t][j] x[t][k]        (matmul_tn_acc, src/linear.rs:113)
 // gb / ga: one 16x16 tile per workgroup, the 4 waves split t and reduce in LDS (single writer);
-// dx: one wave per 32 x 32 fragment of the dx kernel's tiles (the dx kernel's partial layout).
+// dx: one wave per 16 x 16 quarter of a dx-kernel fragment (the dx kernel's partial layout).
 extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a) {
   constexpr int NW = 4;
   __shared__ float red[NW * 256];
@@ -1535,25 +1535,30 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a)
     // gb: rows n (tile rt), cols j (tile ct);  ga: rows j (tile ct), cols k (tile rt)
     const int rrow = is_gb ? rt * 16 + li : ct * 16 + li;
     const int ccol = is_gb ? ct * 16 + li : rt * 16 + li;
-    for (int t = tb; t < te; t += 16) {
-      float av[4], bv[4];
+    // 64 tokens per pass: the loads of all four 16-token groups are issued before their MFMAs
+    for (int t64 = tb; t64 < te; t64 += 64) {
+      float av[4][4], bv[4][4];
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const int tt = t + 4 * u + g, tc = min(tt, a.T - 1);
-        if (is_gb) {
-          const float x = a.dy[(int64_t)tc * a.N + min(rrow, a.N - 1)];
-          const float y = a.h[(int64_t)tc * a.r + min(ccol, a.r - 1)];
-          av[u] = (tt < te && rrow < a.N) ? __fmul_rn(x, a.s) : 0.0f;
-          bv[u] = (tt < te && ccol < a.r) ? y : 0.0f;
-        } else {
-          const float x = a.g[(int64_t)tc * a.r + min(rrow, a.r - 1)];
-          const float y = a.x[(int64_t)tc * a.K + min(ccol, a.K - 1)];
-          av[u] = (tt < te && rrow < a.r) ? x : 0.0f;
-          bv[u] = (tt < te && ccol < a.K) ? y : 0.0f;
+      for (int v = 0; v < 4; v++)
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int tt = t64 + 16 * v + 4 * u + g, tc = min(tt, a.T - 1);
+          if (is_gb) {
+            const float x = a.dy[(int64_t)tc * a.N + min(rrow, a.N - 1)];
+            const float y = a.h[(int64_t)tc * a.r + min(ccol, a.r - 1)];
+            av[v][u] = (tt < te && rrow < a.N) ? __fmul_rn(x, a.s) : 0.0f;
+            bv[v][u] = (tt < te && ccol < a.r) ? y : 0.0f;
+          } else {
+            const float x = a.g[(int64_t)tc * a.r + min(rrow, a.r - 1)];
+            const float y = a.x[(int64_t)tc * a.K + min(ccol, a.K - 1)];
+            av[v][u] = (tt < te && rrow < a.r) ? x : 0.0f;
+            bv[v][u] = (tt < te && ccol < a.K) ? y : 0.0f;
+          }
         }
-      }
 #pragma unroll
-      for (int u = 0; u < 4; u++) acc = mfma_f32(av[u], bv[u], acc);
+      for (int v = 0; v < 4; v++)
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc = mfma_f32(av[v][u], bv[v][u], acc);
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) red[w * 256 + (4 * g + i) * 16 + li] = acc[i];
@@ -1611,62 +1616,53 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a)
       for (int e = 0; e < 4; e++) p[e] = a.accumulate ? p[e] + sum[e] : sum[e];
     }
   } else {
-    // dx fragment f = (b - n_gb - n_ga) * NW + w: dx tile f / 8 (token tile * Kc + K chunk),
-    // dx wave f % 8 = (wt, wk); lane element ts*8 + ks*4 + i <-> row t0 + 32wt + 16ts + 4g + i,
-    // column 128kc + 32wk + 16ks + li (the MFMA output layout of both kernels)
+    // dx quarter fq = (b - n_gb - n_ga) * NW + w: fragment f = fq / 4 of the dx kernel's partials
+    // (tile f / 8 = token tile * Kc + K chunk, its wave f % 8 = (wt, wk)), quarter q = fq % 4 =
+    // (ts, ks); lane element i <-> row t0 + 32wt + 16ts + 4g + i, column 128kc + 32wk + 16ks + li
+    // (the MFMA output layout of both kernels).  All splits' loads are issued at once.
     const int Kc = (a.K + 127) / 128, ntt = (a.T + 63) / 64;
-    const int f = (b - a.n_gb - a.n_ga) * NW + w;
-    if (f >= ntt * Kc * 8) return;  // whole wave exits together; no barriers in this branch
+    const int fq = (b - a.n_gb - a.n_ga) * NW + w;
+    if (fq >= ntt * Kc * 8 * 4) return;  // whole wave exits together; no barriers in this branch
+    const int f = fq >> 2, q = fq & 3, ts = q >> 1, ks = q & 1;
     const int tile = f >> 3, dw = f & 7, wt = dw >> 2, wk = dw & 3;
-    const int t0 = (tile / Kc) * 64 + wt * 32, k0 = (tile % Kc) * 128 + wk * 32;
-    const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    f4 ps[2][2] = {{zero, zero}, {zero, zero}};
-    const f4* pp = reinterpret_cast<const f4*>(a.part) + (int64_t)f * 256 + lane;
+    const int t0 = (tile / Kc) * 64 + wt * 32 + ts * 16, k0 = (tile % Kc) * 128 + wk * 32 + ks * 16;
+    const f4* pp = reinterpret_cast<const f4*>(a.part) + (int64_t)f * 256 + q * 64 + lane;
     const int64_t sstride = (int64_t)ntt * Kc * 8 * 256;  // f4 per split
-    for (int s0 = 0; s0 < a.nsplit; s0 += 2) {  // two splits' fragments in flight, summed in order
-      f4 v[2][4];
+    constexpr int MAXS = 16;                              // the runtime keeps nsplit <= 16 here
+    f4 v[MAXS];
 #pragma unroll
-      for (int q = 0; q < 2; q++)
+    for (int sp = 0; sp < MAXS; sp++) v[sp] = pp[(int64_t)min(sp, a.nsplit - 1) * sstride];
+    f4 ps = v[0];
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[q][e] = pp[(int64_t)min(s0 + q, a.nsplit - 1) * sstride + e * 64];
+    for (int sp = 1; sp < MAXS; sp++)
+      if (sp < a.nsplit) ps += v[sp];  // split order
+    const int trow = t0 + li, kcol = k0 + li;
+    f4 ga = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.g) {  // + g . A for this 16 x 16 tile (f32 MFMA; lane: token 4g + i, column li)
+      for (int j0 = 0; j0 < a.r; j0 += 16) {
+        float gv[4], av[4];
 #pragma unroll
-      for (int q = 0; q < 2; q++)
-        if (s0 + q < a.nsplit)
-#pragma unroll
-          for (int e = 0; e < 4; e++) ps[e >> 1][e & 1] += v[q][e];
-    }
-#pragma unroll
-    for (int ts = 0; ts < 2; ts++)
-#pragma unroll
-      for (int ks = 0; ks < 2; ks++) {
-        const int trow = t0 + ts * 16 + li, kcol = k0 + ks * 16 + li;
-        f4 ga = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (a.g) {
-          for (int j0 = 0; j0 < a.r; j0 += 16) {
-            float gv[4], av[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-              const int j = j0 + 4 * u + g, jc = min(j, a.r - 1);
-              const float x = a.g[(int64_t)min(trow, a.T - 1) * a.r + jc];
-              const float y = a.la[(int64_t)jc * a.K + min(kcol, a.K - 1)];
-              gv[u] = (trow < a.T && j < a.r) ? x : 0.0f;
-              av[u] = (kcol < a.K && j < a.r) ? y : 0.0f;
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++) ga = mfma_f32(gv[u], av[u], ga);
-          }
+        for (int u = 0; u < 4; u++) {
+          const int j = j0 + 4 * u + g, jc = min(j, a.r - 1);
+          const float x = a.g[(int64_t)min(trow, a.T - 1) * a.r + jc];
+          const float y = a.la[(int64_t)jc * a.K + min(kcol, a.K - 1)];
+          gv[u] = (trow < a.T && j < a.r) ? x : 0.0f;
+          av[u] = (kcol < a.K && j < a.r) ? y : 0.0f;
         }
-        if (kcol < a.K)
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const int t = t0 + ts * 16 + 4 * g + i;
-            if (t < a.T) {
-              float* p = &a.dx[(int64_t)t * a.K + kcol];
-              float o = a.accumulate ? *p + ps[ts][ks][i] : ps[ts][ks][i];
-              if (a.g) o += ga[i];
-              *p = o;
-            }
-          }
+        for (int u = 0; u < 4; u++) ga = mfma_f32(gv[u], av[u], ga);
+      }
+    }
+    if (kcol < a.K)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int t = t0 + 4 * g + i;
+        if (t < a.T) {
+          float* p = &a.dx[(int64_t)t * a.K + kcol];
+          float o = a.accumulate ? *p + ps[i] : ps[i];
+          if (a.g) o += ga[i];
+          *p = o;
+        }
       }
   }
 }

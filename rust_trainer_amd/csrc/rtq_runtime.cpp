@@ -446,7 +446,7 @@ DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
                                                     cdiv(3 * c->cu_count, Kc)));
   else
     splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16), cdiv(c->cu_count, Kc * cdiv(t, 64))));
-  if (c->dx_splits > 0) splits = std::min<int64_t>(steps, c->dx_splits);
+  if (c->dx_splits > 0) splits = std::min<int64_t>(std::min<int64_t>(steps, p.tok16 ? 256 : 16), c->dx_splits);
   p.nps = cdiv(steps, splits) * 32;
   p.splits = cdiv(w->Np, p.nps);
   p.part_floats = p.tok16 ? (size_t)(p.splits * t * w->cols) : (size_t)(p.splits * roundup(t, 64) * w->Kp);
@@ -499,8 +499,8 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
                   dp.tok16 ? 1 : 0};
   fa.n_gb = lora ? (int)(cdiv(N, 16) * jt) : 0;
   fa.n_ga = lora ? (int)(cdiv(K, 16) * jt) : 0;
-  // one wave per dx fragment (or per token and 64 columns), four per workgroup
-  fa.n_dx = dp.tok16 ? (int)cdiv(t * cdiv(K, 64), 4) : (int)cdiv((w->Kp / 128) * cdiv(t, 64) * 8, 4);
+  // one wave per quarter of a dx fragment (or per token and 64 columns), four per workgroup
+  fa.n_dx = dp.tok16 ? (int)cdiv(t * cdiv(K, 64), 4) : (int)((w->Kp / 128) * cdiv(t, 64) * 8);
   return launch(c, K_BWD_FINISH, dim3((unsigned)(fa.n_gb + fa.n_ga + fa.n_dx)), dim3(256), st, fa);
 }
 
