@@ -1302,19 +1302,34 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
 #pragma unroll
   for (int s0 = 0; s0 < D - 1; s0++) issue(sl[s0], s0);
   if (nsteps > 0) stage(sl[0], 0);
-  for (int st0 = 0; st0 < nsteps; st0 += D) {
+  // one step of the loop; `full`: a step of a complete group of D (no guards, one basic block, so
+  // the scheduler can interleave the MFMAs with the staging arithmetic; staging past the last step
+  // only writes the unused buffer)
+  auto step_body = [&](int s0, int step, bool full) {
+    issue(sl[(s0 + D - 1) % D], step + D - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    Frags F;
+    if (full || step < nsteps) load_frags(step & 1, F);
+    if (full || step + 1 < nsteps) stage(sl[(s0 + 1) % D], (step + 1) & 1);
+    if (full || step < nsteps) compute(F);
+    if (full) {
 #pragma unroll
-    for (int s0 = 0; s0 < D; s0++) {
-      const int step = st0 + s0;
-      issue(sl[(s0 + D - 1) % D], step + D - 1);
-      __builtin_amdgcn_sched_barrier(0);
-      __syncthreads();
-      Frags F;
-      if (step < nsteps) load_frags(step & 1, F);
-      if (step + 1 < nsteps) stage(sl[(s0 + 1) % D], (step + 1) & 1);
-      if (step < nsteps) compute(F);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int m = 0; m < 12; m++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+      }
     }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  const int nfull = nsteps / D * D;
+  for (int st0 = 0; st0 < nfull; st0 += D) {
+#pragma unroll
+    for (int s0 = 0; s0 < D; s0++) step_body(s0, st0 + s0, true);
+  }
+  if (nfull < nsteps) {
+#pragma unroll
+    for (int s0 = 0; s0 < D; s0++) step_body(s0, nfull + s0, false);
   }
   // partial tile of this split in fragment order: part[sp][tile][wave][q][lane] (float4 each),
   // tile = token tile * Kc + K chunk, q = 2 ts + ks; its element i is row t0 + 32wt + 16ts + 4g + i,
