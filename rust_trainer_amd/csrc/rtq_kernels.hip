@@ -24,6 +24,8 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 // native integer vectors (HIP's u4v/u2v are union-wrapped structs whose copies become memcpy
 // and keep register arrays in scratch)
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
@@ -804,6 +806,269 @@ RTQ_FWD(rtq_fwd_q4_k_w_isums, FMT_Q4_K, 4, 2, 2, true)
 RTQ_FWD(rtq_fwd_q4_k_s_isums, FMT_Q4_K, 1, 4, 4, true)
 RTQ_FWD(rtq_fwd_q6_k_w_isums, FMT_Q6_K, 4, 2, 2, true)
 RTQ_FWD(rtq_fwd_q6_k_s_isums, FMT_Q6_K, 1, 4, 4, true)
+
+// ============================================================== forward GEMM, large grids (Q4_0 / Q8_0)
+// For outputs of at least a workgroup per CU in 128 x 128 tiles.  Workgroup = 4 waves, tile 128
+// weight rows (8 row groups) x 128 tokens (8 token tiles); wave w computes row groups
+// 4(w & 1) .. +3 x token tiles 4(w >> 1) .. +3 (16 MFMA tiles), so every operand fragment serves
+// two waves and four tiles per wave.  Per half chunk (64 columns, two blocks) the workgroup's
+// operands - weight codes and scales, activation codes and scales - are copied global -> LDS by
+// direct-to-LDS loads (no VGPR staging) into a 3-stage ring: while stage s is computed, the loads
+// of stages s + 1 and s + 2 are in flight.  One barrier per stage; the wait before it names the
+// loads of stage s only (the raw s_barrier keeps the compiler from draining every load there).
+// The 1D grid deals the tiles, ordered token block by token block, to the eight XCDs in
+// contiguous ranges: the workgroups running on one XCD share one token block's activations in
+// that XCD's L2 while they stream weight rows.  Arithmetic as fwd_tile: exact integer block sums
+// from the f16 MFMA, acc += isum * (d_w * d_x).
+#define RTQ_LDSP(p) ((__attribute__((address_space(3))) void*)(p))
+
+template <int FMT>
+struct MmStage {  // one half chunk in LDS, in 16-byte units
+  static constexpr int XQ = 0;                                       // [tt 8][j2 2][lane 64] codes
+  static constexpr int WQ = 8 * 2 * 64;                              // [rg 8][lane 64] Q4_0 8 B, Q8_0 16 B
+  static constexpr int WD = WQ + (FMT == FMT_Q4_0 ? 8 * 64 / 2 : 8 * 64);  // [rg 8][row 16] fp16 scale pairs
+  static constexpr int XD = WD + 8 * 4;                              // [t 128] two activation scales
+  static constexpr int SIZE = XD + 128 / 2;
+  static constexpr int NWQ = FMT == FMT_Q4_0 ? 16 : 8;               // loads of weight codes
+  static constexpr int LOADS = 16 + NWQ + 2 + 4;                     // wave-wide loads per stage
+  static constexpr int RING = 3;
+};
+
+template <int FMT>
+__device__ __forceinline__ void mm_tile(const FwdArgs& a) {
+  using St = MmStage<FMT>;
+  extern __shared__ u4v mm_lds[];
+  const int lane = threadIdx.x & 63, li = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wr = w & 1, wt = w >> 1;
+  const int Kc = a.Kp / 128, nhc = a.Kp / 64;
+  const int ngroups = a.Np / 16, ntt = a.Tp / 16;
+  // XCD-aware tile order: workgroup id -> (XCD id % 8, slot id / 8) -> a contiguous tile range per XCD
+  const int nrb = (ngroups + 7) / 8, ntiles = nrb * (ntt / 8);
+  const int id = blockIdx.x, xcd = id & 7, per = ntiles >> 3, rem = ntiles & 7;
+  const int q = xcd * per + min(xcd, rem) + (id >> 3);
+  const int rg0 = (q % nrb) * 8, tt0 = (q / nrb) * 8;
+
+  // Operands reach LDS by buffer loads with the LDS destination (4 or 16 bytes per lane; gfx950
+  // has no 8-byte form, so 8-byte items - Q4_0 half-chunk codes, scale pairs - go as pairs of
+  // words).  Every lane's byte offset for half chunk 0 is computed once; a half chunk adds a
+  // wave-uniform offset (kc * A + h * B per operand) in an SGPR.  The buffer ranges are the arrays'
+  // sizes, so a load past an array's end reads zeros instead of faulting.
+  const uint32_t nb_x = (uint32_t)a.Tp * a.Kp * 2, nb_xd = (uint32_t)Kc * a.Tp * 16;
+  const uint32_t nb_w = (uint32_t)a.Np * a.Kp / (FMT == FMT_Q4_0 ? 2 : 1), nb_wd = (uint32_t)a.Np * a.Kp / 16;
+  const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.xq), (short)0, nb_x, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_xd = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.xd), (short)0, nb_xd, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_w = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.wq), (short)0, nb_w, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_wd = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.wdr), (short)0, nb_wd, 0x00020000);
+  constexpr int NSLOT = (St::LOADS + 3) / 4;
+  uint32_t voff[NSLOT];
+#pragma unroll
+  for (int k = 0; k < NSLOT; k++) {
+    const int i = w + 4 * k;
+    uint32_t v = 0;
+    if (i < 16) {  // activation fragments: token tile i / 2, block 2h + i % 2
+      const uint32_t ttg = (uint32_t)min(tt0 + (i >> 1), ntt - 1);
+      v = ((ttg * Kc * 4 + (i & 1)) * 64 + lane) * 16;
+    } else if (i < 16 + St::NWQ) {  // weight codes
+      if (FMT == FMT_Q4_0) {  // row group (i - 16) / 2, words 64 m .. 64 m + 63 of its 128
+        const int wi = ((i - 16) & 1) * 64 + lane;
+        const uint32_t rgg = (uint32_t)min(rg0 + ((i - 16) >> 1), ngroups - 1);
+        v = ((rgg * Kc * 64 + (wi >> 1)) * 4 + (wi & 1)) * 4;
+      } else {
+        const uint32_t rgg = (uint32_t)min(rg0 + i - 16, ngroups - 1);
+        v = (rgg * Kc * 2 * 64 + lane) * 16;
+      }
+    } else if (i < 16 + St::NWQ + 2) {  // weight scale pairs: word wi -> row wi % 16 of row group wi / 16
+      const int wi = (i - 16 - St::NWQ) * 64 + lane;
+      const uint32_t rgg = (uint32_t)min(rg0 + (wi >> 4), ngroups - 1);
+      v = ((rgg * Kc * 16 + (wi & 15)) * 2) * 4;
+    } else {  // activation scales of blocks 2h, 2h+1: word wi -> token wi / 2
+      const int wi = (i - 18 - St::NWQ) * 64 + lane;
+      const uint32_t tok = (uint32_t)min(tt0 * 16 + (wi >> 1), a.Tp - 1);
+      v = (tok * 4 + (wi & 1)) * 4;
+    }
+    voff[k] = v;
+  }
+  auto issue = [&](int st, int hc) {
+    u4v* S = mm_lds + st * St::SIZE;
+    const uint32_t kc = hc >> 1, h = hc & 1;
+#pragma unroll
+    for (int k = 0; k < NSLOT; k++) {
+      const int i = w + 4 * k;  // wave-uniform
+      if (i < 16) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, RTQ_LDSP(S + St::XQ + i * 64), 16, voff[k], hc * 2048u, 0, 0);
+      } else if (i < 16 + St::NWQ) {
+        if (FMT == FMT_Q4_0)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + ((i - 16) >> 1) * 32 + ((i - 16) & 1) * 16), 4,
+                                                   voff[k], kc * 1024u + h * 8u, 0, 0);
+        else
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + (i - 16) * 64), 16, voff[k], hc * 1024u, 0, 0);
+      } else if (i < 16 + St::NWQ + 2) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_wd, RTQ_LDSP(S + St::WD + (i - 16 - St::NWQ) * 16), 4, voff[k],
+                                                 kc * 128u + h * 4u, 0, 0);
+      } else if (i < St::LOADS) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_xd, RTQ_LDSP(S + St::XD + (i - 18 - St::NWQ) * 16), 4, voff[k],
+                                                 kc * (uint32_t)a.Tp * 16u + h * 8u, 0, 0);
+      }
+    }
+  };
+
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  const f16v zero16 = {};
+  f4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[i][r] = zero;
+
+  // Per block and token tile, one 4-block f16 MFMA (16x16x4, k slot 0 only) forms the scale
+  // products d_w[row] * d_x[token] of the wave's four row groups - exact in f32, fp16 times fp16 -
+  // in the layout of the block-sum tiles, so the epilogue is one FMA per output element.
+  auto compute = [&](int st) {
+    const u4v* S = mm_lds + st * St::SIZE;
+    // every LDS read of the stage first (fragments of both blocks), then the math
+    u4v xr[2][4];
+#pragma unroll
+    for (int j2 = 0; j2 < 2; j2++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) xr[j2][i] = S[St::XQ + ((wt * 4 + i) * 2 + j2) * 64 + lane];
+    u4v wq[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int rl = wr * 4 + r;
+      if (FMT == FMT_Q4_0) {
+        const u2v q2 = reinterpret_cast<const u2v*>(S + St::WQ)[rl * 64 + lane];
+        wq[r] = u4v{q2.x, q2.y, 0u, 0u};
+      } else {
+        wq[r] = S[St::WQ + rl * 64 + lane];
+      }
+    }
+    const uint32_t dwp = reinterpret_cast<const uint32_t*>(S + St::WD)[(wr * 4 + g) * 16 + li];  // row group g, row li
+    float2 xs[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) xs[i] = reinterpret_cast<const float2*>(S + St::XD)[(wt * 4 + i) * 16 + li];
+#pragma unroll
+    for (int j2 = 0; j2 < 2; j2++) {
+      half8 wf[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        if (FMT == FMT_Q4_0)
+          wf[r] = q4_0_frag(j2 ? wq[r].y : wq[r].x);
+        else
+          wf[r] = j2 ? q8_frag(wq[r].z, wq[r].w) : q8_frag(wq[r].x, wq[r].y);
+      }
+      const u2v dwa = {j2 ? (dwp >> 16) : (dwp & 0xffffu), 0u};
+      const half4 sa = __builtin_bit_cast(half4, dwa);
+      // software pipeline over the token tiles: the MFMAs of tile i + 1 are issued before the
+      // FMAs that consume tile i
+      f16v sc[2];
+      f4 c[2][4];
+      auto products = [&](int i, int b) {
+        const half4 sb = {(_Float16)(j2 ? xs[i].y : xs[i].x), (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f16(sa, sb, zero16, 0, 0, 0);
+        const half8 xf = __builtin_bit_cast(half8, xr[j2][i]);
+#pragma unroll
+        for (int r = 0; r < 4; r++) c[b][r] = mfma_f16(wf[r], xf, zero);
+      };
+      products(0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        if (i + 1 < 4) products(i + 1, (i + 1) & 1);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) acc[i][r][e] = fmaf(c[i & 1][r][e], sc[i & 1][4 * r + e], acc[i][r][e]);
+      }
+    }
+  };
+
+  // 3-stage ring over half chunks; each wave issues at least LOADS / 4 (rounded down) loads per
+  // stage, so "at most that many outstanding" at the top of step s means stage s has landed
+  issue(0, 0);
+  if (nhc > 1) issue(1, 1);
+  for (int hc = 0; hc < nhc; hc++) {
+    if (hc + 1 < nhc)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (St::LOADS / 4));  // vmcnt <= loads of stage s + 1
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (hc + 2 < nhc) issue((hc + 2) % St::RING, hc + 2);
+    compute(hc % St::RING);
+  }
+
+  // ---- epilogue: bias, LoRA up-projection (h and B rows staged in LDS over the ring), y
+  const bool lora = a.hp != nullptr;
+  const bool lora_lds = lora && a.r <= RTQ_LDS_RANK;
+  float(*sh)[RTQ_LDS_RANK + 1] = reinterpret_cast<float(*)[RTQ_LDS_RANK + 1]>(mm_lds);
+  float(*sb)[RTQ_LDS_RANK + 1] = sh + 128;
+  if (lora_lds) {
+    __builtin_amdgcn_s_barrier();  // every wave is past its last read of the ring
+    asm volatile("" ::: "memory");
+    for (int j0 = 0; j0 < a.r; j0 += 16) {
+      float hv[8], bv[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const int e = threadIdx.x + 256 * k, tl = e >> 4, j = j0 + (e & 15);
+        hv[k] = sum_partials(a.hp, (int64_t)min(tt0 * 16 + tl, a.T - 1) * a.r + min(j, a.r - 1), a.nhp);
+        bv[k] = a.lb[(int64_t)min(rg0 * 16 + tl, a.N - 1) * a.r + min(j, a.r - 1)];
+      }
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const int e = threadIdx.x + 256 * k;
+        sh[e >> 4][j0 + (e & 15)] = hv[k];
+        sb[e >> 4][j0 + (e & 15)] = bv[k];
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int tl = (wt * 4 + i) * 16 + li, t = tt0 * 16 + tl;
+      const int rl = (wr * 4 + r) * 16, nb0 = rg0 * 16 + rl, n0 = nb0 + 4 * g;
+      if (nb0 >= a.N) continue;  // whole row group is padding (uniform over the wave)
+      f4 lacc = zero;
+      if (lora_lds) {
+        for (int j0 = 0; j0 < a.r; j0 += 4) {
+          const int j = j0 + g, jc = min(j, a.r - 1);
+          const float hv = sh[tl][jc], bv = sb[rl + li][jc];
+          lacc = mfma_f32((nb0 + li < a.N && j < a.r) ? bv : 0.0f, (t < a.T && j < a.r) ? hv : 0.0f, lacc);
+        }
+      } else if (lora) {  // rank above the LDS staging limit: straight from global memory
+        const int tc = min(t, a.T - 1), nrow = min(nb0 + li, a.N - 1);
+        for (int j0 = 0; j0 < a.r; j0 += 4) {
+          const int j = j0 + g, jc = min(j, a.r - 1);
+          const float hv = sum_partials(a.hp, (int64_t)tc * a.r + jc, a.nhp);
+          const float bv = a.lb[(int64_t)nrow * a.r + jc];
+          lacc = mfma_f32((nb0 + li < a.N && j < a.r) ? bv : 0.0f, (t < a.T && j < a.r) ? hv : 0.0f, lacc);
+        }
+      }
+      if (t < a.T) {
+        f4 v = acc[i][r];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          float o = v[e];
+          if (a.bias) o = o + a.bias[min(n0 + e, a.N - 1)];
+          if (lora) o = o + a.s * lacc[e];
+          v[e] = o;
+        }
+        float* yr = a.y + (int64_t)t * a.N;
+        if ((a.N & 3) == 0 && n0 + 3 < a.N) {
+          *reinterpret_cast<f4*>(yr + n0) = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (n0 + e < a.N) yr[n0 + e] = v[e];
+        }
+      }
+    }
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void rtq_mm_q4_0(FwdArgs a) { mm_tile<FMT_Q4_0>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_mm_q8_0(FwdArgs a) { mm_tile<FMT_Q8_0>(a); }
 
 // ============================================================== forward GEMV (T <= 16)
 // MFMA orientation transposed against fwd_tile: A operand = the 16 token slots x 32 columns of the

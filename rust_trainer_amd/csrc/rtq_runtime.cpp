@@ -118,6 +118,8 @@ enum Kid {
   K_GEMV = K_FWD_S_ISUMS + F_COUNT,       // + format: t <= 16, large N
   K_FWD_Q4_0_W8 = K_GEMV + F_COUNT,       // wide forward with eight waves splitting K
   K_FWD_Q8_0_W8,
+  K_MM_Q4_0,     // large-grid forward (128 x 128 tiles, LDS ring)
+  K_MM_Q8_0,
   K_BWD_PREP,
   K_DX,          // + format
   K_DX16 = K_DX + F_COUNT,  // + format: t <= 16
@@ -132,7 +134,7 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_fwd_q4_0_w_isums", "rtq_fwd_q8_0_w_isums", "rtq_fwd_q4_k_w_isums", "rtq_fwd_q6_k_w_isums",
     "rtq_fwd_q4_0_s_isums", "rtq_fwd_q8_0_s_isums", "rtq_fwd_q4_k_s_isums", "rtq_fwd_q6_k_s_isums",
     "rtq_gemv_q4_0",        "rtq_gemv_q8_0",        "rtq_gemv_q4_k",        "rtq_gemv_q6_k",
-    "rtq_fwd_q4_0_w8",      "rtq_fwd_q8_0_w8",
+    "rtq_fwd_q4_0_w8",      "rtq_fwd_q8_0_w8",      "rtq_mm_q4_0",          "rtq_mm_q8_0",
     "rtq_bwd_prep",
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
@@ -161,6 +163,7 @@ struct rtq_ctx {
   std::vector<hipEvent_t> free_events;
   int dx_splits = 0;  // 0: automatic; RTQ_DX_SPLITS overrides (tuning)
   int fwd_waves = 8;  // waves splitting K in the wide Q4_0 / Q8_0 forward (RTQ_FWD_WAVES: 4 or 8)
+  int fwd_mm = -1;    // large-grid forward: -1 automatic, 0 never, 1 whenever the format allows (RTQ_FWD_MM)
   int64_t t_launches[K_COUNT] = {};
   double t_ms[K_COUNT] = {};
 };
@@ -282,6 +285,13 @@ struct FwdPlan {
 };
 
 constexpr int kFwdWideTT = 4;     // rtq_fwd_*_w: 64 tokens x (16 * wide_rg) rows per workgroup
+constexpr int kMmTile = 128;      // rtq_mm_*: 128 rows x 128 tokens per workgroup
+// rtq_mm_* dynamic LDS: a 3-stage ring of half-chunk operands (codes, scales), reused after the
+// K loop for the LoRA h and B rows of the tile (128 rows each, RTQ_LDS_RANK + 1 floats)
+unsigned mm_lds_bytes(int type) {
+  const unsigned stage = 16u * (8 * 2 * 64 + (type == RTQ_TYPE_Q4_0 ? 8 * 64 / 2 : 8 * 64) + 8 * 4 + 128 / 2);
+  return std::max(3 * stage, 2u * 128u * (RTQ_LDS_RANK + 1) * 4u);
+}
 constexpr int kFwdSkinnyRG = 4;   // rtq_fwd_*_s: 16 tokens x 64 rows per workgroup
 int wide_rg(int type) { return is_kquant(type) ? 2 : 3; }
 int gemv_rg(int type) { return byte_codes(type) ? 2 : 4; }
@@ -311,7 +321,9 @@ FwdPlan fwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
   p.T = t;
   p.skinny = t <= 16;
   p.gemv = p.skinny && r <= RTQ_LDS_RANK;
-  p.Tp = roundup(std::max<int64_t>(t, 1), p.skinny ? 16 : 16 * kFwdWideTT);
+  // wide: 128-token padding, the token block of rtq_mm_* (rtq_fwd_*_w covers the first
+  // cdiv(t, 64) token tiles of it)
+  p.Tp = roundup(std::max<int64_t>(t, 1), p.skinny ? 16 : kMmTile);
   p.nhp = roundup(cdiv(w->Kp, RTQ_ACT_KQ), 4);
   p.xq_bytes = (size_t)p.Tp * w->Kp * 2;  // one f16 per element
   p.xd_floats = (size_t)(w->Kp / 32) * p.Tp;
@@ -377,13 +389,17 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   const int64_t Kc = w->Kp / 128;
   const bool kq = is_kquant(w->type);
   const int64_t rg_per_wg = p.skinny ? kFwdSkinnyRG : wide_rg(w->type);
-  const int64_t gx = cdiv(w->Np / 16, rg_per_wg), gy = p.Tp / (p.skinny ? 16 : 16 * kFwdWideTT);
+  const int64_t gx = cdiv(w->Np / 16, rg_per_wg), gy = p.skinny ? p.Tp / 16 : cdiv(t, 16 * kFwdWideTT);
+  // the large-grid kernel once its 128 x 128 tiles alone give a workgroup per CU
+  const int64_t mm_tiles = cdiv(w->Np / 16, 8) * (p.Tp / kMmTile);
+  const bool mm = !p.skinny && !isums && !is_kquant(w->type) &&
+                  (c->fwd_mm == 1 || (c->fwd_mm < 0 && mm_tiles >= c->cu_count));
   const int64_t tiles = gx * gy;
   // split K across workgroups when the output alone gives too few of them (atomics into a
   // zeroed y); every split keeps at least one half chunk per wave (K-quants: one super-block of
   // two chunks per wave, and splits on super-block boundaries)
   int64_t ks = 1;
-  if (!isums && tiles < c->cu_count) {
+  if (!isums && !mm && tiles < c->cu_count) {
     const int64_t want = cdiv(p.skinny ? 2 * c->cu_count : c->cu_count, tiles);
     ks = std::max<int64_t>(1, std::min<int64_t>(want, Kc / (kq ? 8 : 2)));
   }
@@ -397,6 +413,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   FwdArgs fa{};
   fa.wq = w->wq;
   fa.wd = w->wd;
+  fa.wdr = w->wdr;  // rtq_mm_* reads the row-major scales
   fa.wsb = w->wsb;
   fa.Np = (int)w->Np;
   fa.Kp = (int)w->Kp;
@@ -415,6 +432,11 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   fa.r = (int)r;
   fa.s = s;
   fa.isums = isums;
+  if (mm && (!fa.wq || !fa.wdr || !fa.xq || !fa.xd || !fa.y))
+    return fail(RTQ_ERR_INVALID, "internal: rtq_mm_* operand missing");
+  if (mm)
+    return launch(c, w->type == RTQ_TYPE_Q4_0 ? K_MM_Q4_0 : K_MM_Q8_0, dim3((unsigned)mm_tiles), dim3(256), st, fa,
+                  mm_lds_bytes(w->type));
   int kid = (p.skinny ? (isums ? K_FWD_S_ISUMS : K_FWD_S) : (isums ? K_FWD_W_ISUMS : K_FWD_W)) + fmt_index(w->type);
   int threads = 256;
   if (!p.skinny && !isums && !kq && c->fwd_waves == 8) {
@@ -651,6 +673,7 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   c->cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   if (const char* e = getenv("RTQ_DX_SPLITS")) c->dx_splits = atoi(e);
   if (const char* e = getenv("RTQ_FWD_WAVES")) c->fwd_waves = atoi(e) == 4 ? 4 : 8;
+  if (const char* e = getenv("RTQ_FWD_MM")) c->fwd_mm = atoi(e) ? 1 : 0;
   hipError_t e = hipModuleLoadData(&c->mod, rtq_hsaco_begin);
   if (e != hipSuccess) {
     delete c;

@@ -275,3 +275,53 @@ def test_lm_head_shape_t1(ctx, wtype):
     dx = np.zeros(t * k, np.float32)
     w.backward_input(dy, t, dx)
     assert rel_err(dx, O.frozen_backward_input(wtype, blocks, n, k, dy, nthreads=16)) <= TOL
+
+
+# ---------------------------------------------------------------- large-grid forward (rtq_mm_*)
+@pytest.fixture(scope="module")
+def ctx_mm():
+    """A context that sends every wide Q4_0 / Q8_0 forward through the 128 x 128-tile kernel
+    (RTQ_FWD_MM=1), so small shapes cover its padding and epilogue cases."""
+    import os
+
+    old = os.environ.get("RTQ_FWD_MM")
+    os.environ["RTQ_FWD_MM"] = "1"
+    try:
+        c = rt.Context(0)
+    finally:
+        if old is None:
+            del os.environ["RTQ_FWD_MM"]
+        else:
+            os.environ["RTQ_FWD_MM"] = old
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
+@pytest.mark.parametrize("n,k,t,r", [(200, 256, 130, 16), (320, 512, 256, 0), (1000, 1024, 300, 80), (130, 128, 129, 16),
+                                     (64, 128, 17, 4)])
+def test_linear_forward_mm_matches_oracle(ctx_mm, wtype, n, k, t, r):
+    # partial row groups and row blocks (N = 130, 200), N % 4 != 0 (scalar stores), token padding
+    # inside a 128-token block, no LoRA, LoRA rank above the LDS staging limit (80)
+    blocks, x, _ = make(wtype, n, k, t)
+    bias = O.Rng(6).vec_normal(n, 0.1)
+    lin = rt.Linear("blk.0.attn_q", hip(ctx_mm, wtype, blocks, n, k), bias=bias)
+    kw = {}
+    if r:
+        A, B = lora(n, k, r)
+        lin.lora = rt.Lora(r, 2.0 * r, A, B)
+        kw = dict(A=A, B=B, alpha=2.0 * r)
+    y = lin.forward(x, t)
+    want = O.linear_forward(wtype, blocks, n, k, x, bias=bias, nthreads=8, **kw)
+    assert rel_err(y, want) <= TOL
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
+def test_forward_mm_selected_by_grid_size(ctx, wtype):
+    # 4096 rows x 1024 tokens: 32 x 8 tiles of 128 x 128, a workgroup per CU, so the default
+    # context picks rtq_mm_* by itself
+    n, k, t = 4096, 256, 1024
+    blocks, x, _ = make(wtype, n, k, t)
+    w = hip(ctx, wtype, blocks, n, k)
+    y = w.forward(x, t)
+    assert rel_err(y, O.frozen_forward(wtype, blocks, n, k, x, nthreads=8)) <= TOL
