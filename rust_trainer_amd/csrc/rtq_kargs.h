@@ -71,6 +71,7 @@ struct ActArgs {
   float* hp;
   float* zero_y;
   int N;
+  uint16_t* xdh;  // or null: the fp16 bits of xd, same layout (rtq_mm_*'s scale MFMA operand)
 };
 
 // ---------------------------------------------------------------- forward GEMM
@@ -96,6 +97,7 @@ struct FwdArgs {
   float s;              // alpha / r
   int32_t* isums;       // debug: [T][N][K/32] (Q4_0, Q8_0), [T][N][K/256][2] (Q4_K: S1, S2),
                         // [T][N][K/256] (Q6_K: S), or null
+  const uint16_t* xdh;  // fp16 activation scales, layout of xd (rtq_mm_*)
 };
 
 // ---------------------------------------------------------------- backward

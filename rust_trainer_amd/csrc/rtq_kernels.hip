@@ -377,6 +377,8 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
       }
       const bool real = t < a.T && kk < a.K;
       if (hf == 0) a.xd[((int64_t)kc * a.Tp + t) * 4 + j] = real ? dstore : 0.0f;
+      if (a.xdh && hf == 0)  // Q8_0: dstore is an fp16 value
+        a.xdh[((int64_t)kc * a.Tp + t) * 4 + j] = real ? __builtin_bit_cast(uint16_t, (_Float16)dstore) : (uint16_t)0;
       if (a.xg && hf == 0) {  // Tp == 16: t is the token within the tile
         a.xg[(int64_t)(b * 2) * 16 + t] = real ? dstore : 0.0f;
         a.xg[(int64_t)(b * 2 + 1) * 16 + t] = real ? -a.gbias * csum : 0.0f;
@@ -827,10 +829,10 @@ struct MmStage {  // one half chunk in LDS, in 16-byte units
   static constexpr int XQ = 0;                                       // [tt 8][j2 2][lane 64] codes
   static constexpr int WQ = 8 * 2 * 64;                              // [rg 8][lane 64] Q4_0 8 B, Q8_0 16 B
   static constexpr int WD = WQ + (FMT == FMT_Q4_0 ? 8 * 64 / 2 : 8 * 64);  // [rg 8][row 16] fp16 scale pairs
-  static constexpr int XD = WD + 8 * 4;                              // [t 128] two activation scales
-  static constexpr int SIZE = XD + 128 / 2;
+  static constexpr int XD = WD + 8 * 4;                              // [t 128] fp16 activation scale pairs
+  static constexpr int SIZE = XD + 128 / 4;
   static constexpr int NWQ = FMT == FMT_Q4_0 ? 16 : 8;               // loads of weight codes
-  static constexpr int LOADS = 16 + NWQ + 2 + 4;                     // wave-wide loads per stage
+  static constexpr int LOADS = 16 + NWQ + 2 + 2;                     // wave-wide loads per stage
   static constexpr int RING = 3;
 };
 
@@ -854,10 +856,10 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
   // words).  Every lane's byte offset for half chunk 0 is computed once; a half chunk adds a
   // wave-uniform offset (kc * A + h * B per operand) in an SGPR.  The buffer ranges are the arrays'
   // sizes, so a load past an array's end reads zeros instead of faulting.
-  const uint32_t nb_x = (uint32_t)a.Tp * a.Kp * 2, nb_xd = (uint32_t)Kc * a.Tp * 16;
+  const uint32_t nb_x = (uint32_t)a.Tp * a.Kp * 2, nb_xd = (uint32_t)Kc * a.Tp * 8;
   const uint32_t nb_w = (uint32_t)a.Np * a.Kp / (FMT == FMT_Q4_0 ? 2 : 1), nb_wd = (uint32_t)a.Np * a.Kp / 16;
   const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.xq), (short)0, nb_x, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rs_xd = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.xd), (short)0, nb_xd, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_xd = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.xdh), (short)0, nb_xd, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs_w = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.wq), (short)0, nb_w, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs_wd = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.wdr), (short)0, nb_wd, 0x00020000);
   constexpr int NSLOT = (St::LOADS + 3) / 4;
@@ -882,10 +884,10 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
       const int wi = (i - 16 - St::NWQ) * 64 + lane;
       const uint32_t rgg = (uint32_t)min(rg0 + (wi >> 4), ngroups - 1);
       v = ((rgg * Kc * 16 + (wi & 15)) * 2) * 4;
-    } else {  // activation scales of blocks 2h, 2h+1: word wi -> token wi / 2
+    } else {  // fp16 activation scales of blocks 2h, 2h+1: word wi -> token wi
       const int wi = (i - 18 - St::NWQ) * 64 + lane;
-      const uint32_t tok = (uint32_t)min(tt0 * 16 + (wi >> 1), a.Tp - 1);
-      v = (tok * 4 + (wi & 1)) * 4;
+      const uint32_t tok = (uint32_t)min(tt0 * 16 + wi, a.Tp - 1);
+      v = tok * 8;
     }
     voff[k] = v;
   }
@@ -908,7 +910,7 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
                                                  kc * 128u + h * 4u, 0, 0);
       } else if (i < St::LOADS) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_xd, RTQ_LDSP(S + St::XD + (i - 18 - St::NWQ) * 16), 4, voff[k],
-                                                 kc * (uint32_t)a.Tp * 16u + h * 8u, 0, 0);
+                                                 kc * (uint32_t)a.Tp * 8u + h * 4u, 0, 0);
       }
     }
   };
@@ -944,9 +946,9 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
       }
     }
     const uint32_t dwp = reinterpret_cast<const uint32_t*>(S + St::WD)[(wr * 4 + g) * 16 + li];  // row group g, row li
-    float2 xs[4];
+    uint32_t xs[4];  // fp16 activation scales of blocks 2h (low half), 2h+1 (high half), token li
 #pragma unroll
-    for (int i = 0; i < 4; i++) xs[i] = reinterpret_cast<const float2*>(S + St::XD)[(wt * 4 + i) * 16 + li];
+    for (int i = 0; i < 4; i++) xs[i] = reinterpret_cast<const uint32_t*>(S + St::XD)[(wt * 4 + i) * 16 + li];
 #pragma unroll
     for (int j2 = 0; j2 < 2; j2++) {
       half8 wf[4];
@@ -964,7 +966,8 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
       f16v sc[2];
       f4 c[2][4];
       auto products = [&](int i, int b) {
-        const half4 sb = {(_Float16)(j2 ? xs[i].y : xs[i].x), (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+        const u2v xsa = {j2 ? (xs[i] >> 16) : (xs[i] & 0xffffu), 0u};
+        const half4 sb = __builtin_bit_cast(half4, xsa);
         sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f16(sa, sb, zero16, 0, 0, 0);
         const half8 xf = __builtin_bit_cast(half8, xr[j2][i]);
 #pragma unroll
@@ -983,18 +986,25 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
   };
 
   // 3-stage ring over half chunks; each wave issues at least LOADS / 4 (rounded down) loads per
-  // stage, so "at most that many outstanding" at the top of step s means stage s has landed
+  // stage, so "at most that many outstanding" at the top of step s means stage s has landed.  The
+  // loop is unrolled by the ring size so that every stage's LDS offsets are immediates.
   issue(0, 0);
   if (nhc > 1) issue(1, 1);
-  for (int hc = 0; hc < nhc; hc++) {
-    if (hc + 1 < nhc)
-      __builtin_amdgcn_s_waitcnt(0x0F70 | (St::LOADS / 4));  // vmcnt <= loads of stage s + 1
-    else
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    if (hc + 2 < nhc) issue((hc + 2) % St::RING, hc + 2);
-    compute(hc % St::RING);
+  for (int hc0 = 0; hc0 < nhc; hc0 += St::RING) {
+#pragma unroll
+    for (int u = 0; u < St::RING; u++) {
+      const int hc = hc0 + u;
+      if (hc < nhc) {
+        if (hc + 1 < nhc)
+          __builtin_amdgcn_s_waitcnt(0x0F70 | (St::LOADS / 4));  // vmcnt <= loads of stage s + 1
+        else
+          __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (hc + 2 < nhc) issue((u + 2) % St::RING, hc + 2);
+        compute(u);
+      }
+    }
   }
 
   // ---- epilogue: bias, LoRA up-projection (h and B rows staged in LDS over the ring), y

@@ -281,7 +281,7 @@ struct FwdPlan {
   int64_t T, Tp, nhp;
   bool skinny;
   bool gemv;  // t <= 16 through rtq_gemv_* (see gemv_plan)
-  size_t xq_bytes, xd_floats, xg_floats, h_floats;
+  size_t xq_bytes, xd_floats, xg_floats, h_floats, xdh_bytes;
 };
 
 constexpr int kFwdWideTT = 4;     // rtq_fwd_*_w: 64 tokens x (16 * wide_rg) rows per workgroup
@@ -289,7 +289,7 @@ constexpr int kMmTile = 128;      // rtq_mm_*: 128 rows x 128 tokens per workgro
 // rtq_mm_* dynamic LDS: a 3-stage ring of half-chunk operands (codes, scales), reused after the
 // K loop for the LoRA h and B rows of the tile (128 rows each, RTQ_LDS_RANK + 1 floats)
 unsigned mm_lds_bytes(int type) {
-  const unsigned stage = 16u * (8 * 2 * 64 + (type == RTQ_TYPE_Q4_0 ? 8 * 64 / 2 : 8 * 64) + 8 * 4 + 128 / 2);
+  const unsigned stage = 16u * (8 * 2 * 64 + (type == RTQ_TYPE_Q4_0 ? 8 * 64 / 2 : 8 * 64) + 8 * 4 + 128 / 4);
   return std::max(3 * stage, 2u * 128u * (RTQ_LDS_RANK + 1) * 4u);
 }
 constexpr int kFwdSkinnyRG = 4;   // rtq_fwd_*_s: 16 tokens x 64 rows per workgroup
@@ -327,13 +327,14 @@ FwdPlan fwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
   p.nhp = roundup(cdiv(w->Kp, RTQ_ACT_KQ), 4);
   p.xq_bytes = (size_t)p.Tp * w->Kp * 2;  // one f16 per element
   p.xd_floats = (size_t)(w->Kp / 32) * p.Tp;
+  p.xdh_bytes = p.skinny ? 0 : p.xd_floats * 2;  // fp16 copy for rtq_mm_*
   p.xg_floats = p.gemv ? (size_t)(w->Kp / 32) * 2 * 16 : 0;
   p.h_floats = (size_t)p.nhp * t * std::max<int64_t>(r, 0);
   return p;
 }
 
 size_t fwd_ws_bytes(const FwdPlan& p) {
-  return p.xq_bytes + p.xd_floats * 4 + p.xg_floats * 4 + p.h_floats * 4 + 5 * 256;
+  return p.xq_bytes + p.xd_floats * 4 + p.xg_floats * 4 + p.h_floats * 4 + p.xdh_bytes + 6 * 256;
 }
 
 
@@ -407,8 +408,10 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   if (kq) kcps = roundup(kcps, 2);
   ks = cdiv(Kc, kcps);
 
+  uint16_t* xdh = mm ? ar.take<uint16_t>(p.xdh_bytes / 2) : nullptr;
+  if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   ActArgs aa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xq, xd, nullptr, 0.0f, lora ? la : nullptr, (int)r, hp,
-             ks > 1 ? y : nullptr, (int)w->rows};
+             ks > 1 ? y : nullptr, (int)w->rows, xdh};
   RTQ_TRY(launch(c, kq ? K_ACT_PREP_K : K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp), dim3(256), st, aa));
   FwdArgs fa{};
   fa.wq = w->wq;
@@ -432,7 +435,8 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   fa.r = (int)r;
   fa.s = s;
   fa.isums = isums;
-  if (mm && (!fa.wq || !fa.wdr || !fa.xq || !fa.xd || !fa.y))
+  fa.xdh = xdh;
+  if (mm && (!fa.wq || !fa.wdr || !fa.xq || !fa.xdh || !fa.y))
     return fail(RTQ_ERR_INVALID, "internal: rtq_mm_* operand missing");
   if (mm)
     return launch(c, w->type == RTQ_TYPE_Q4_0 ? K_MM_Q4_0 : K_MM_Q8_0, dim3((unsigned)mm_tiles), dim3(256), st, fa,
