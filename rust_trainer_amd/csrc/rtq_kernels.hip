@@ -811,17 +811,18 @@ RTQ_FWD(rtq_fwd_q6_k_s_isums, FMT_Q6_K, 1, 4, 4, true)
 
 // ============================================================== forward GEMM, large grids (Q4_0 / Q8_0)
 // For outputs of at least a workgroup per CU in 128 x 128 tiles.  Workgroup = 4 waves, tile 128
-// weight rows (8 row groups) x 128 tokens (8 token tiles); wave w computes row groups
-// 4(w & 1) .. +3 x token tiles 4(w >> 1) .. +3 (16 MFMA tiles), so every operand fragment serves
-// two waves and four tiles per wave.  Per half chunk (64 columns, two blocks) the workgroup's
-// operands - weight codes and scales, activation codes and scales - are copied global -> LDS by
-// direct-to-LDS loads (no VGPR staging) into a 3-stage ring: while stage s is computed, the loads
-// of stages s + 1 and s + 2 are in flight.  One barrier per stage; the wait before it names the
-// loads of stage s only (the raw s_barrier keeps the compiler from draining every load there).
-// The 1D grid deals the tiles, ordered token block by token block, to the eight XCDs in
-// contiguous ranges: the workgroups running on one XCD share one token block's activations in
-// that XCD's L2 while they stream weight rows.  Arithmetic as fwd_tile: exact integer block sums
-// from the f16 MFMA, acc += isum * (d_w * d_x).
+// weight rows (8 row groups) x 128 tokens (8 token tiles); wave w computes row groups 2w, 2w+1 x
+// all 8 token tiles (16 MFMA tiles): a weight fragment is unpacked once per 8 token tiles, the
+// activation fragments are shared by the four waves through LDS.  Per half chunk (64 columns,
+// two blocks) the workgroup's operands - weight codes and scales, activation codes and scales -
+// are copied global -> LDS by buffer loads with an LDS destination (no VGPR staging) into a
+// 3-stage ring: while stage s is computed, the loads of stages s + 1 and s + 2 are in flight.  One
+// barrier per stage; the wait before it names the loads of stage s only (the raw s_barrier keeps
+// the compiler from draining every load there).  The 1D grid deals the tiles, ordered token block
+// by token block, to the eight XCDs in contiguous ranges: the workgroups running on one XCD share
+// one token block's activations in that XCD's L2 while they stream weight rows.  Arithmetic as
+// fwd_tile: exact integer block sums from the f16 MFMA, acc += isum * (d_w * d_x), with the scale
+// products formed by a 4-block f16 MFMA in the layout of the block-sum tiles.
 #define RTQ_LDSP(p) ((__attribute__((address_space(3))) void*)(p))
 
 template <int FMT>
@@ -842,7 +843,6 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
   extern __shared__ u4v mm_lds[];
   const int lane = threadIdx.x & 63, li = lane & 15, g = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wr = w & 1, wt = w >> 1;
   const int Kc = a.Kp / 128, nhc = a.Kp / 64;
   const int ngroups = a.Np / 16, ntt = a.Tp / 16;
   // XCD-aware tile order: workgroup id -> (XCD id % 8, slot id / 8) -> a contiguous tile range per XCD
@@ -917,71 +917,62 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
 
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
   const f16v zero16 = {};
-  f4 acc[4][4];
+  f4 acc[8][2];  // [token tile][row group]
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < 8; i++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) acc[i][r] = zero;
+    for (int r = 0; r < 2; r++) acc[i][r] = zero;
 
-  // Per block and token tile, one 4-block f16 MFMA (16x16x4, k slot 0 only) forms the scale
-  // products d_w[row] * d_x[token] of the wave's four row groups - exact in f32, fp16 times fp16 -
-  // in the layout of the block-sum tiles, so the epilogue is one FMA per output element.
+  // Per token tile, one 4-block f16 MFMA (16x16x4, k slot 0 only) forms the scale products
+  // d_w[row] * d_x[token] of block b = (row group r, block j2) = (b >> 1, b & 1) - exact in f32,
+  // fp16 times fp16 - in the layout of the block-sum tiles, so the epilogue is one FMA per output
+  // element and block.
   auto compute = [&](int st) {
     const u4v* S = mm_lds + st * St::SIZE;
-    // every LDS read of the stage first (fragments of both blocks), then the math
-    u4v xr[2][4];
+    half8 wf[2][2];  // [row group][block]
 #pragma unroll
-    for (int j2 = 0; j2 < 2; j2++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) xr[j2][i] = S[St::XQ + ((wt * 4 + i) * 2 + j2) * 64 + lane];
-    u4v wq[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int rl = wr * 4 + r;
+    for (int r = 0; r < 2; r++) {
+      const int rl = 2 * w + r;
       if (FMT == FMT_Q4_0) {
         const u2v q2 = reinterpret_cast<const u2v*>(S + St::WQ)[rl * 64 + lane];
-        wq[r] = u4v{q2.x, q2.y, 0u, 0u};
+        wf[r][0] = q4_0_frag(q2.x);
+        wf[r][1] = q4_0_frag(q2.y);
       } else {
-        wq[r] = S[St::WQ + rl * 64 + lane];
+        const u4v qv = S[St::WQ + rl * 64 + lane];
+        wf[r][0] = q8_frag(qv.x, qv.y);
+        wf[r][1] = q8_frag(qv.z, qv.w);
       }
     }
-    const uint32_t dwp = reinterpret_cast<const uint32_t*>(S + St::WD)[(wr * 4 + g) * 16 + li];  // row group g, row li
-    uint32_t xs[4];  // fp16 activation scales of blocks 2h (low half), 2h+1 (high half), token li
+    // scale MFMA operands: lane group g = 2 r + j2 holds row li of row group 2w + r, block j2
+    const uint32_t dwp = reinterpret_cast<const uint32_t*>(S + St::WD)[(2 * w + (g >> 1)) * 16 + li];
+    const u2v dwa = {(g & 1) ? (dwp >> 16) : (dwp & 0xffffu), 0u};
+    const half4 sa = __builtin_bit_cast(half4, dwa);
+    f16v sc[2];
+    f4 c[2][2][2];  // [pipeline slot][row group][block]
+    auto products = [&](int i, int b) {
+      const uint32_t xsv = reinterpret_cast<const uint32_t*>(S + St::XD)[i * 16 + li];
+      const u2v xsa = {(g & 1) ? (xsv >> 16) : (xsv & 0xffffu), 0u};
+      sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f16(sa, __builtin_bit_cast(half4, xsa), zero16, 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; i++) xs[i] = reinterpret_cast<const uint32_t*>(S + St::XD)[(wt * 4 + i) * 16 + li];
+      for (int j2 = 0; j2 < 2; j2++) {
+        const half8 xf = __builtin_bit_cast(half8, S[St::XQ + (i * 2 + j2) * 64 + lane]);
 #pragma unroll
-    for (int j2 = 0; j2 < 2; j2++) {
-      half8 wf[4];
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        if (FMT == FMT_Q4_0)
-          wf[r] = q4_0_frag(j2 ? wq[r].y : wq[r].x);
-        else
-          wf[r] = j2 ? q8_frag(wq[r].z, wq[r].w) : q8_frag(wq[r].x, wq[r].y);
+        for (int r = 0; r < 2; r++) c[b][r][j2] = mfma_f16(wf[r][j2], xf, zero);
       }
-      const u2v dwa = {j2 ? (dwp >> 16) : (dwp & 0xffffu), 0u};
-      const half4 sa = __builtin_bit_cast(half4, dwa);
-      // software pipeline over the token tiles: the MFMAs of tile i + 1 are issued before the
-      // FMAs that consume tile i
-      f16v sc[2];
-      f4 c[2][4];
-      auto products = [&](int i, int b) {
-        const u2v xsa = {j2 ? (xs[i] >> 16) : (xs[i] & 0xffffu), 0u};
-        const half4 sb = __builtin_bit_cast(half4, xsa);
-        sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f16(sa, sb, zero16, 0, 0, 0);
-        const half8 xf = __builtin_bit_cast(half8, xr[j2][i]);
+    };
+    // software pipeline over the token tiles: the MFMAs of tile i + 1 are issued before the FMAs
+    // that consume tile i
+    products(0, 0);
 #pragma unroll
-        for (int r = 0; r < 4; r++) c[b][r] = mfma_f16(wf[r], xf, zero);
-      };
-      products(0, 0);
+    for (int i = 0; i < 8; i++) {
+      if (i + 1 < 8) products(i + 1, (i + 1) & 1);
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        if (i + 1 < 4) products(i + 1, (i + 1) & 1);
+      for (int r = 0; r < 2; r++)
 #pragma unroll
-        for (int r = 0; r < 4; r++)
+        for (int j2 = 0; j2 < 2; j2++)
 #pragma unroll
-          for (int e = 0; e < 4; e++) acc[i][r][e] = fmaf(c[i & 1][r][e], sc[i & 1][4 * r + e], acc[i][r][e]);
-      }
+          for (int e = 0; e < 4; e++)
+            acc[i][r][e] = fmaf(c[i & 1][r][j2][e], sc[i & 1][4 * (2 * r + j2) + e], acc[i][r][e]);
     }
   };
 
@@ -1033,11 +1024,11 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
     __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
+  for (int i = 0; i < 8; i++) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int tl = (wt * 4 + i) * 16 + li, t = tt0 * 16 + tl;
-      const int rl = (wr * 4 + r) * 16, nb0 = rg0 * 16 + rl, n0 = nb0 + 4 * g;
+    for (int r = 0; r < 2; r++) {
+      const int tl = i * 16 + li, t = tt0 * 16 + tl;
+      const int rl = (2 * w + r) * 16, nb0 = rg0 * 16 + rl, n0 = nb0 + 4 * g;
       if (nb0 >= a.N) continue;  // whole row group is padding (uniform over the wave)
       f4 lacc = zero;
       if (lora_lds) {

@@ -325,3 +325,22 @@ def test_forward_mm_selected_by_grid_size(ctx, wtype):
     w = hip(ctx, wtype, blocks, n, k)
     y = w.forward(x, t)
     assert rel_err(y, O.frozen_forward(wtype, blocks, n, k, x, nthreads=8)) <= TOL
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
+@pytest.mark.parametrize("r", [0, 16, 80])
+def test_forward_mm_many_tiles(ctx, wtype, r):
+    # 64 row blocks x 10 token blocks = 640 workgroups, more than two per CU; LoRA staged in LDS
+    # (r = 16) or read from global memory (r = 80); T = 1250 pads the last token block
+    n, k, t = 8192, 256, 1250
+    blocks, x, _ = make(wtype, n, k, t)
+    bias = O.Rng(6).vec_normal(n, 0.1)
+    lin = rt.Linear("blk.0.ffn_up", hip(ctx, wtype, blocks, n, k), bias=bias)
+    kw = {}
+    if r:
+        A, B = lora(n, k, r)
+        lin.lora = rt.Lora(r, 2.0 * r, A, B)
+        kw = dict(A=A, B=B, alpha=2.0 * r)
+    y = lin.forward(x, t)
+    want = O.linear_forward(wtype, blocks, n, k, x, bias=bias, nthreads=8, **kw)
+    assert rel_err(y, want) <= TOL
