@@ -1344,21 +1344,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
 
-template <int FMT>
+template <int FMT, int NQ = 1>
 struct DxSlot {
-  f4 dy;
+  f4 dy[NQ];
   uint32_t q[2];  // the four codes this thread converts, of rows 2p and 2p+1
   uint32_t d;     // fp16 scales of rows 2p (low half) and 2p+1 (high half)
 };
-template <>
-struct DxSlot<FMT_Q4_K> {
-  f4 dy;
+template <int NQ>
+struct DxSlot<FMT_Q4_K, NQ> {
+  f4 dy[NQ];
   uint32_t q[2];
   u4v k;  // sub-block scale words of rows 2p (x: blocks 0, 1; y: 2, 3) and 2p+1 (z, w)
   u2v e;  // super-block (d, dmin) of rows 2p, 2p+1
 };
-template <>
-struct DxSlot<FMT_Q6_K> : DxSlot<FMT_Q4_K> {};
+template <int NQ>
+struct DxSlot<FMT_Q6_K, NQ> : DxSlot<FMT_Q4_K, NQ> {};
 
 // h = sum of hp, g = s * sum of gp, both in slice order (src/linear.rs:106-111), by the nfin
 // finaliser workgroups of a dx grid (rel: this workgroup's index among them)
@@ -1394,27 +1394,33 @@ __device__ __forceinline__ void dq_params(uint32_t d16, uint32_t kw, uint32_t ev
   }
 }
 
-template <int FMT>
+// TW: tokens per workgroup.  64: wave (wt, wk) = (w / 4, w % 4) owns 32 tokens x 32 columns
+// (2 x 2 MFMA tiles).  256 (large T): wave (wt, wk) = (w / 2, w % 2) owns 64 tokens x 64 columns
+// (4 x 4 tiles), so each dequantised weight element feeds four times the MFMAs; the partials keep
+// the 64-token fragment order of the TW = 64 kernel.
+template <int FMT, int TW>
 __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   // Flat grid, XCD-aware: consecutive workgroup ids go to the 8 XCDs in turn, so id % 8 selects
   // a group of row splits and all (token tile, K chunk) workgroups of a split run on one XCD,
   // whose L2 then fetches that split's dy slice and W rows once.  The last n_fin workgroups
   // finalise h and g (LoRA).
-  const int Kc = a.Kp / 128, ntt = (a.T + 63) / 64;
-  const int nmain = Kc * ntt * a.nsplit;
+  constexpr int TS = TW == 64 ? 2 : 4, KS = TS;  // MFMA tiles per wave in tokens and in columns
+  constexpr int NQ = TW / 64;                     // float4 of dy staged per thread and step
+  const int Kc = a.Kp / 128, ntt = (a.T + 63) / 64, nwt = (a.T + TW - 1) / TW;
+  const int nmain = Kc * nwt * a.nsplit;
   const int id = blockIdx.x;
   if (id >= nmain) {
     dx_lora_sums(a, id - nmain, gridDim.x - nmain);
     return;  // uniform over the workgroup, before any barrier
   }
-  constexpr int D = 4;
-  __shared__ u4v sA[2][4][2][64];                                   // [buf][tile][hi/lo][lane]
+  constexpr int D = TW == 64 ? 4 : 3;
+  __shared__ u4v sA[2][TW / 16][2][64];                             // [buf][tile][hi/lo][lane]
   __shared__ __attribute__((aligned(16))) __bf16 sW[2][2][128][40];   // [buf][hi/lo][k][n]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
-  const int wt = w >> 2, wk = w & 3;
+  const int wt = TW == 64 ? w >> 2 : w >> 1, wk = TW == 64 ? w & 3 : w & 1;
   // id -> (split, token tile, K chunk).  With nsplit a multiple of 8, split = id % 8 + 8 * group
   // keeps all workgroups of a split on one XCD; otherwise splits are taken in order.
-  const int per = ntt * Kc;  // workgroups per split
+  const int per = nwt * Kc;  // workgroups per split
   int sp, within;
   if ((a.nsplit & 7) == 0) {
     const int grp = id / (8 * per), rem = id % (8 * per);
@@ -1425,15 +1431,18 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
     within = id % per;
   }
   const int kc = within % Kc;
-  const int t0 = (within / Kc) * 64;
+  const int t0 = (within / Kc) * TW;
   const int n0 = sp * a.n_per_split;
   const int nsteps = (min(n0 + a.n_per_split, a.Np) - n0) / 32;
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f4 acc[2][2];
+  f4 acc[TS][KS];
 #pragma unroll
-  for (int i = 0; i < 2; i++) acc[i][0] = acc[i][1] = zero;
+  for (int i = 0; i < TS; i++)
+#pragma unroll
+    for (int j = 0; j < KS; j++) acc[i][j] = zero;
 
-  // dy loader: token tl = tid >> 3, float4 q4 = tid & 7 (columns ns + 4 q4 .. +3 of the step)
+  // dy loader: tokens tl + 64 m (m < NQ) with tl = tid >> 3, float4 q4 = tid & 7 (columns
+  // ns + 4 q4 .. +3 of the step)
   const int tl = tid >> 3, q4 = tid & 7;
   const __amdgpu_buffer_rsrc_t rdy = make_rsrc(a.dy, (uint32_t)a.T * a.N * 4u);
   const uint32_t dy_off = ((uint32_t)(t0 + tl) * a.N + 4 * q4) * 4u;
@@ -1464,21 +1473,25 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   const uint32_t q_rg = (uint32_t)Kc * 64 * 16 * (B8 ? 2 : 1);  // bytes per row group
   const uint32_t d_rg = (uint32_t)Kc * 128, e_rg = (uint32_t)Kc * 32;
 
-  DxSlot<FMT> sl[D];
-  auto issue = [&](DxSlot<FMT>& S, int step) {
+  DxSlot<FMT, NQ> sl[D];
+  auto issue = [&](DxSlot<FMT, NQ>& S, int step) {
     const int ns = n0 + 32 * min(step, max(nsteps - 1, 0));  // clamped: always a real step
     const uint32_t srg = (uint32_t)(ns >> 4);
-    if (dy_vec) {
-      S.dy = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rdy, dy_off, (uint32_t)ns * 4u, 0));
-    } else {
 #pragma unroll
-      for (int c = 0; c < 4; c++)
-        S.dy[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rdy, dy_off + 4u * c, (uint32_t)ns * 4u, 0));
-    }
-    if (ns + 32 > a.N) {  // ragged tail of N: columns >= N hold the next row's values
+    for (int m = 0; m < NQ; m++) {
+      const uint32_t mo = dy_off + (uint32_t)(64 * m) * a.N * 4u;
+      if (dy_vec) {
+        S.dy[m] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rdy, mo, (uint32_t)ns * 4u, 0));
+      } else {
 #pragma unroll
-      for (int c = 0; c < 4; c++)
-        if (ns + 4 * q4 + c >= a.N) S.dy[c] = 0.0f;
+        for (int c = 0; c < 4; c++)
+          S.dy[m][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rdy, mo + 4u * c, (uint32_t)ns * 4u, 0));
+      }
+      if (ns + 32 > a.N) {  // ragged tail of N: columns >= N hold the next row's values
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          if (ns + 4 * q4 + c >= a.N) S.dy[m][c] = 0.0f;
+      }
     }
 #pragma unroll
     for (int r = 0; r < 2; r++) S.q[r] = __builtin_amdgcn_raw_buffer_load_b32(rq, q_off[r], srg * q_rg, 0);
@@ -1489,22 +1502,23 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
       S.d = __builtin_amdgcn_raw_buffer_load_b32(rd, d_off, srg * d_rg, 0);
     }
   };
-  auto stage = [&](const DxSlot<FMT>& S, int buf) {
-    {  // dy: A fragment tile tl>>4, lane (tl&15) + 16*(q4>>1), slots 4*(q4&1) .. +3
+  auto stage = [&](const DxSlot<FMT, NQ>& S, int buf) {
+#pragma unroll
+    for (int m = 0; m < NQ; m++) {  // dy: A fragment tile (tl>>4) + 4m, lane (tl&15) + 16*(q4>>1), slots 4*(q4&1) ..
       // bit view of the whole vector: masking bit_casts of single float4 lanes is miscompiled
       // by this compiler (every lane gets lane 0's mask)
-      const u4v vb = __builtin_bit_cast(u4v, S.dy);
+      const u4v vb = __builtin_bit_cast(u4v, S.dy[m]);
       uint32_t lb[4];
 #pragma unroll
-      for (int c = 0; c < 4; c++) lb[c] = __builtin_bit_cast(uint32_t, S.dy[c] - __builtin_bit_cast(float, vb[c] & 0xffff0000u));
+      for (int c = 0; c < 4; c++) lb[c] = __builtin_bit_cast(uint32_t, S.dy[m][c] - __builtin_bit_cast(float, vb[c] & 0xffff0000u));
       u2v hv, lv;
       hv.x = __builtin_amdgcn_perm(vb[1], vb[0], 0x07060302u);  // high halves: bf16 by truncation
       hv.y = __builtin_amdgcn_perm(vb[3], vb[2], 0x07060302u);
       lv.x = __builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u);
       lv.y = __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u);
       const int fl = (tl & 15) + 16 * (q4 >> 1);
-      reinterpret_cast<u2v*>(&sA[buf][tl >> 4][0][fl])[q4 & 1] = hv;
-      reinterpret_cast<u2v*>(&sA[buf][tl >> 4][1][fl])[q4 & 1] = lv;
+      reinterpret_cast<u2v*>(&sA[buf][(tl >> 4) + 4 * m][0][fl])[q4 & 1] = hv;
+      reinterpret_cast<u2v*>(&sA[buf][(tl >> 4) + 4 * m][1][fl])[q4 & 1] = lv;
     }
     {  // W: rows 2p, 2p+1 -> bf16 hi / lo planes, one 32-bit word (both rows) per column
       uint32_t vb[2][4], lb[2][4];
@@ -1536,26 +1550,27 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   // the wave's operand fragments of one step: A (dy) hi / lo of its two token tiles, B (W) hi / lo
   // of its two column tiles
   struct Frags {
-    bf8 a[2][2], b[2][2];
+    bf8 a[TS][2], b[KS][2];
   };
   auto load_frags = [&](int buf, Frags& F) {
 #pragma unroll
-    for (int ts = 0; ts < 2; ts++) {
-      F.a[ts][0] = __builtin_bit_cast(bf8, sA[buf][wt * 2 + ts][0][lane]);
-      F.a[ts][1] = __builtin_bit_cast(bf8, sA[buf][wt * 2 + ts][1][lane]);
+    for (int ts = 0; ts < TS; ts++) {
+      F.a[ts][0] = __builtin_bit_cast(bf8, sA[buf][wt * TS + ts][0][lane]);
+      F.a[ts][1] = __builtin_bit_cast(bf8, sA[buf][wt * TS + ts][1][lane]);
     }
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-      const int kl = wk * 32 + ks * 16 + li;  // column kl lies in block wk: rows swizzled by 8 wk
-      F.b[ks][0] = *reinterpret_cast<const bf8*>(&sW[buf][0][kl][8 * (g ^ wk)]);
-      F.b[ks][1] = *reinterpret_cast<const bf8*>(&sW[buf][1][kl][8 * (g ^ wk)]);
+    for (int ks = 0; ks < KS; ks++) {
+      // column kl lies in block kl / 32, whose rows are swizzled by 8 (kl / 32)
+      const int kl = wk * 16 * KS + ks * 16 + li, jbk = (wk * 16 * KS + ks * 16) >> 5;
+      F.b[ks][0] = *reinterpret_cast<const bf8*>(&sW[buf][0][kl][8 * (g ^ jbk)]);
+      F.b[ks][1] = *reinterpret_cast<const bf8*>(&sW[buf][1][kl][8 * (g ^ jbk)]);
     }
   };
   auto compute = [&](const Frags& F) {
 #pragma unroll
-    for (int ts = 0; ts < 2; ts++)
+    for (int ts = 0; ts < TS; ts++)
 #pragma unroll
-      for (int ks = 0; ks < 2; ks++) {
+      for (int ks = 0; ks < KS; ks++) {
         acc[ts][ks] = mfma_bf16(F.a[ts][0], F.b[ks][0], acc[ts][ks]);
         acc[ts][ks] = mfma_bf16(F.a[ts][1], F.b[ks][0], acc[ts][ks]);
         acc[ts][ks] = mfma_bf16(F.a[ts][0], F.b[ks][1], acc[ts][ks]);
@@ -1581,9 +1596,9 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
     if (full || step < nsteps) compute(F);
     if (full) {
 #pragma unroll
-      for (int m = 0; m < 12; m++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+      for (int m = 0; m < 3 * TS * KS; m++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, TW == 64 ? 4 : 2, 0);  // VALU
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1598,15 +1613,28 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
     for (int s0 = 0; s0 < D; s0++) step_body(s0, nfull + s0, false);
   }
   // partial tile of this split in fragment order: part[sp][tile][wave][q][lane] (float4 each),
-  // tile = token tile * Kc + K chunk, q = 2 ts + ks; its element i is row t0 + 32wt + 16ts + 4g + i,
-  // column 128kc + 32wk + 16ks + li.  Each of the four 16-byte stores of a wave writes 1 KB
-  // contiguously.
-  f4* out = reinterpret_cast<f4*>(a.part) +
-            ((((int64_t)sp * ntt + (t0 >> 6)) * Kc + kc) * 8 + w) * 256 + lane;
+  // tile = 64-token tile * Kc + K chunk, wave = 4 wt' + wk', q = 2 ts' + ks' in the TW = 64 layout:
+  // element i is row 64 tile + 32wt' + 16ts' + 4g + i, column 128kc + 32wk' + 16ks' + li.  Each
+  // 16-byte store of a wave writes 1 KB contiguously.
+  if (TW == 64) {
+    f4* out = reinterpret_cast<f4*>(a.part) + ((((int64_t)sp * ntt + (t0 >> 6)) * Kc + kc) * 8 + w) * 256 + lane;
 #pragma unroll
-  for (int ts = 0; ts < 2; ts++)
+    for (int ts = 0; ts < 2; ts++)
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) out[(ts * 2 + ks) * 64] = acc[ts][ks];
+      for (int ks = 0; ks < 2; ks++) out[(ts * 2 + ks) * 64] = acc[ts][ks];
+  } else {
+    const int tt64 = (t0 >> 6) + wt;  // this wave's 64 tokens form one 64-token tile
+    if (tt64 < ntt) {
+      f4* out = reinterpret_cast<f4*>(a.part) + (((int64_t)sp * ntt + tt64) * Kc + kc) * 8 * 256 + lane;
+#pragma unroll
+      for (int ts = 0; ts < 4; ts++)
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+          const int wo = (ts >> 1) * 4 + 2 * wk + (ks >> 1), qo = (ts & 1) * 2 + (ks & 1);
+          out[(wo * 4 + qo) * 64] = acc[ts][ks];
+        }
+    }
+  }
 }
 
 // ============================================================== dx = dy . W for T <= 16
@@ -1787,10 +1815,14 @@ extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q8_0(DxArgs a) { dx16
 extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q4_k(DxArgs a) { dx16_tile<FMT_Q4_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q6_k(DxArgs a) { dx16_tile<FMT_Q6_K>(a); }
 
-extern "C" __global__ __launch_bounds__(512) void rtq_dx_q4_0(DxArgs a) { dx_tile<FMT_Q4_0>(a); }
-extern "C" __global__ __launch_bounds__(512) void rtq_dx_q8_0(DxArgs a) { dx_tile<FMT_Q8_0>(a); }
-extern "C" __global__ __launch_bounds__(512) void rtq_dx_q4_k(DxArgs a) { dx_tile<FMT_Q4_K>(a); }
-extern "C" __global__ __launch_bounds__(512) void rtq_dx_q6_k(DxArgs a) { dx_tile<FMT_Q6_K>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dx_q4_0(DxArgs a) { dx_tile<FMT_Q4_0, 64>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dx_q8_0(DxArgs a) { dx_tile<FMT_Q8_0, 64>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dx_q4_k(DxArgs a) { dx_tile<FMT_Q4_K, 64>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dx_q6_k(DxArgs a) { dx_tile<FMT_Q6_K, 64>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dxw_q4_0(DxArgs a) { dx_tile<FMT_Q4_0, 256>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dxw_q8_0(DxArgs a) { dx_tile<FMT_Q8_0, 256>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dxw_q4_k(DxArgs a) { dx_tile<FMT_Q4_K, 256>(a); }
+extern "C" __global__ __launch_bounds__(512) void rtq_dxw_q6_k(DxArgs a) { dx_tile<FMT_Q6_K, 256>(a); }
 
 // ============================================================== backward finish
 // dx[t][k] = [dx[t][k] +] sum over splits s (in order) of the partials [+ sum_j g[t][j] A[j][k]]

@@ -123,7 +123,8 @@ enum Kid {
   K_BWD_PREP,
   K_DX,          // + format
   K_DX16 = K_DX + F_COUNT,  // + format: t <= 16
-  K_BWD_FINISH = K_DX16 + F_COUNT,
+  K_DXW = K_DX16 + F_COUNT,  // + format: large t, 256-token tiles
+  K_BWD_FINISH = K_DXW + F_COUNT,
   K_ROWS,        // + format
   K_COUNT = K_ROWS + F_COUNT
 };
@@ -138,6 +139,7 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_bwd_prep",
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
+    "rtq_dxw_q4_0",         "rtq_dxw_q8_0",         "rtq_dxw_q4_k",         "rtq_dxw_q6_k",
     "rtq_bwd_finish",
     "rtq_rows_q4_0",        "rtq_rows_q8_0",        "rtq_rows_q4_k",        "rtq_rows_q6_k"};
 
@@ -162,6 +164,7 @@ struct rtq_ctx {
   std::vector<TimedLaunch> pending;
   std::vector<hipEvent_t> free_events;
   int dx_splits = 0;  // 0: automatic; RTQ_DX_SPLITS overrides (tuning)
+  int dx_wide = -1;   // 256-token dx tiles: -1 automatic, 0 never, 1 for every t > 16 (RTQ_DX_WIDE)
   int fwd_waves = 8;  // waves splitting K in the wide Q4_0 / Q8_0 forward (RTQ_FWD_WAVES: 4 or 8)
   int fwd_mm = -1;    // large-grid forward: -1 automatic, 0 never, 1 whenever the format allows (RTQ_FWD_MM)
   int64_t t_launches[K_COUNT] = {};
@@ -456,22 +459,27 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
 //     (more splits add partial-sum traffic: each split writes and the finish kernel reads a
 //     64-token-padded T x K block);
 //   t <= 16 (rtq_dx16_*): K chunks x row splits, about three 4-wave workgroups per CU with at least
-//     four 32-row steps each (partials are T x K floats per split).
+//     four 32-row steps each (partials are T x K floats per split);
+//   t >= kDxWideT (rtq_dxw_*): as the first, with 256-token tiles.
+constexpr int64_t kDxWideT = 1024;
 struct DxPlan {
   int64_t splits, nps;
   bool tok16;
+  bool wide;  // rtq_dxw_*: 256-token tiles (each dequantised weight element feeds 4x the MFMAs)
   size_t part_floats;
 };
 DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
   DxPlan p;
   p.tok16 = t <= 16;
+  p.wide = !p.tok16 && (c->dx_wide == 1 || (c->dx_wide < 0 && t >= kDxWideT));
   const int64_t Kc = w->Kp / 128, steps = w->Np / 32;
   int64_t splits;
   if (p.tok16)
     splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(std::max<int64_t>(steps / 4, 1), 256),
                                                     cdiv(3 * c->cu_count, Kc)));
   else
-    splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16), cdiv(c->cu_count, Kc * cdiv(t, 64))));
+    splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16),
+                                                    cdiv(c->cu_count, Kc * cdiv(t, p.wide ? 256 : 64))));
   if (c->dx_splits > 0) splits = std::min<int64_t>(std::min<int64_t>(steps, p.tok16 ? 256 : 16), c->dx_splits);
   p.nps = cdiv(steps, splits) * 32;
   p.splits = cdiv(w->Np, p.nps);
@@ -516,8 +524,8 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   }
   DxArgs xa{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, (int)dp.splits, part,
             lora ? hp : nullptr, lora ? gp : nullptr, (int)nhq, (int)ngq, (int)r, s, h, g};
-  const int kid = (dp.tok16 ? K_DX16 : K_DX) + fmt_index(w->type);
-  const int64_t nmain = (w->Kp / 128) * (dp.tok16 ? 1 : cdiv(t, 64)) * dp.splits;
+  const int kid = (dp.tok16 ? K_DX16 : (dp.wide ? K_DXW : K_DX)) + fmt_index(w->type);
+  const int64_t nmain = (w->Kp / 128) * (dp.tok16 ? 1 : cdiv(t, dp.wide ? 256 : 64)) * dp.splits;
   const int64_t nfin = lora ? std::min<int64_t>(64, cdiv(t * r, 512)) : 0;  // LoRA finalisers
   RTQ_TRY(launch(c, kid, dim3((unsigned)(nmain + nfin)), dim3(dp.tok16 ? 256 : 512), st, xa));
   const int64_t jt = cdiv(r, 16);
@@ -676,6 +684,7 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   c->device = device;
   c->cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   if (const char* e = getenv("RTQ_DX_SPLITS")) c->dx_splits = atoi(e);
+  if (const char* e = getenv("RTQ_DX_WIDE")) c->dx_wide = atoi(e) ? 1 : 0;
   if (const char* e = getenv("RTQ_FWD_WAVES")) c->fwd_waves = atoi(e) == 4 ? 4 : 8;
   if (const char* e = getenv("RTQ_FWD_MM")) c->fwd_mm = atoi(e) ? 1 : 0;
   hipError_t e = hipModuleLoadData(&c->mod, rtq_hsaco_begin);

@@ -344,3 +344,64 @@ def test_forward_mm_many_tiles(ctx, wtype, r):
     y = lin.forward(x, t)
     want = O.linear_forward(wtype, blocks, n, k, x, bias=bias, nthreads=8, **kw)
     assert rel_err(y, want) <= TOL
+
+
+# ---------------------------------------------------------------- dx with 256-token tiles (rtq_dxw_*)
+@pytest.fixture(scope="module")
+def ctx_dxw():
+    """A context that sends every t > 16 dx through the 256-token-tile kernel (RTQ_DX_WIDE=1), so
+    small shapes cover its token padding and partial-layout mapping."""
+    import os
+
+    old = os.environ.get("RTQ_DX_WIDE")
+    os.environ["RTQ_DX_WIDE"] = "1"
+    try:
+        c = rt.Context(0)
+    finally:
+        if old is None:
+            del os.environ["RTQ_DX_WIDE"]
+        else:
+            os.environ["RTQ_DX_WIDE"] = old
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("wtype,n,k,t", cases([(256, 512, 37), (100, 256, 300), (80, 2048, 130), (3072, 1024, 256),
+                                               (1024, 3072, 64)]))
+def test_backward_input_dxw_matches_oracle(ctx_dxw, wtype, n, k, t):
+    blocks, _, dy = make(wtype, n, k, t)
+    w = hip(ctx_dxw, wtype, blocks, n, k)
+    dx0 = O.Rng(7).vec_normal(t * k, 1.0)
+    dx = dx0.copy()
+    w.backward_input(dy, t, dx)
+    want = O.frozen_backward_input(wtype, blocks, n, k, dy, dx=np.zeros((t, k), np.float32), nthreads=8)
+    assert rel_err(dx - dx0, want) <= TOL
+    W = np.stack([O.frozen_row(wtype, blocks, n, k, r) for r in range(n)]).astype(np.float64)
+    dense = dy.astype(np.float64) @ W
+    got = (dx - dx0).reshape(t, k)
+    assert (np.abs(got - dense) < 1e-3 * np.maximum(np.abs(dense), 1.0)).all()
+
+
+@pytest.mark.parametrize("wtype", FORMATS)
+def test_linear_backward_dxw_lora(ctx_dxw, wtype):
+    n, k, t, r = 512, 1024 if BLOCK[wtype] == 256 else 768, 300, 16
+    blocks, x, dy = make(wtype, n, k, t)
+    A, B = lora(n, k, r)
+    lin = rt.Linear("blk.0.attn_v", hip(ctx_dxw, wtype, blocks, n, k))
+    lin.lora = rt.Lora(r, 32.0, A, B)
+    dx = lin.backward(x, dy, t)
+    wdx, wga, wgb = O.linear_backward(wtype, blocks, n, k, x, dy, A=A, B=B, alpha=32.0, nthreads=8)
+    assert rel_err(dx, wdx) <= TOL
+    assert rel_err(lin.lora.ga, wga) <= TOL
+    assert rel_err(lin.lora.gb, wgb) <= TOL
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q6_K])
+def test_backward_input_dxw_selected_by_t(ctx, wtype):
+    # t >= 1024 takes the 256-token tiles in the default context
+    n, k, t = 1024, 1024, 1100
+    blocks, _, dy = make(wtype, n, k, t)
+    w = hip(ctx, wtype, blocks, n, k)
+    dx = np.zeros(t * k, np.float32)
+    w.backward_input(dy, t, dx)
+    assert rel_err(dx, O.frozen_backward_input(wtype, blocks, n, k, dy, nthreads=8)) <= TOL
