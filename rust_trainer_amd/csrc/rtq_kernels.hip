@@ -1407,7 +1407,8 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   constexpr int TS = TW == 64 ? 2 : 4, KS = TS;  // MFMA tiles per wave in tokens and in columns
   constexpr int NQ = TW / 64;                     // float4 of dy staged per thread and step
   const int Kc = a.Kp / 128, ntt = (a.T + 63) / 64, nwt = (a.T + TW - 1) / TW;
-  const int nmain = Kc * nwt * a.nsplit;
+  const int nunit = a.nsplit * nwt;  // (token group, row split) units of Kc workgroups each
+  const int nmain = (nunit + 7) / 8 * 8 * Kc;
   const int id = blockIdx.x;
   if (id >= nmain) {
     dx_lora_sums(a, id - nmain, gridDim.x - nmain);
@@ -1418,20 +1419,13 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   __shared__ __attribute__((aligned(16))) __bf16 sW[2][2][128][40];   // [buf][hi/lo][k][n]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
   const int wt = TW == 64 ? w >> 2 : w >> 1, wk = TW == 64 ? w & 3 : w & 1;
-  // id -> (split, token tile, K chunk).  With nsplit a multiple of 8, split = id % 8 + 8 * group
-  // keeps all workgroups of a split on one XCD; otherwise splits are taken in order.
-  const int per = nwt * Kc;  // workgroups per split
-  int sp, within;
-  if ((a.nsplit & 7) == 0) {
-    const int grp = id / (8 * per), rem = id % (8 * per);
-    sp = grp * 8 + rem % 8;
-    within = rem / 8;
-  } else {
-    sp = id / per;
-    within = id % per;
-  }
-  const int kc = within % Kc;
-  const int t0 = (within / Kc) * TW;
+  // id -> (XCD id % 8, slot id / 8) -> K chunk slot % Kc of unit u = (slot / Kc) * 8 + XCD: the Kc
+  // workgroups of a unit run back to back on one XCD and share its dy rows in that L2; unit
+  // u = token group * nsplit + split, so an XCD's concurrent units also share weight rows
+  const int kc = (id >> 3) % Kc, u = (id >> 3) / Kc * 8 + (id & 7);
+  if (u >= nunit) return;  // padding of the unit count to a multiple of 8 (uniform, before any barrier)
+  const int sp = u % a.nsplit;
+  const int t0 = (u / a.nsplit) * TW;
   const int n0 = sp * a.n_per_split;
   const int nsteps = (min(n0 + a.n_per_split, a.Np) - n0) / 32;
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};

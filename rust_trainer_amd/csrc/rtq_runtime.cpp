@@ -525,7 +525,9 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   DxArgs xa{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, (int)dp.splits, part,
             lora ? hp : nullptr, lora ? gp : nullptr, (int)nhq, (int)ngq, (int)r, s, h, g};
   const int kid = (dp.tok16 ? K_DX16 : (dp.wide ? K_DXW : K_DX)) + fmt_index(w->type);
-  const int64_t nmain = (w->Kp / 128) * (dp.tok16 ? 1 : cdiv(t, dp.wide ? 256 : 64)) * dp.splits;
+  // t > 16: (token group, split) units of K-chunk workgroups, padded to a multiple of 8 (XCD order)
+  const int64_t nmain = dp.tok16 ? (w->Kp / 128) * dp.splits
+                                 : roundup(cdiv(t, dp.wide ? 256 : 64) * dp.splits, 8) * (w->Kp / 128);
   const int64_t nfin = lora ? std::min<int64_t>(64, cdiv(t * r, 512)) : 0;  // LoRA finalisers
   RTQ_TRY(launch(c, kid, dim3((unsigned)(nmain + nfin)), dim3(dp.tok16 ? 256 : 512), st, xa));
   const int64_t jt = cdiv(r, 16);
