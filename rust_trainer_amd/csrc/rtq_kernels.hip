@@ -1935,14 +1935,17 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a)
     const int t0 = (tile / Kc) * 64 + wt * 32 + ts * 16, k0 = (tile % Kc) * 128 + wk * 32 + ks * 16;
     const f4* pp = reinterpret_cast<const f4*>(a.part) + (int64_t)f * 256 + q * 64 + lane;
     const int64_t sstride = (int64_t)ntt * Kc * 8 * 256;  // f4 per split
-    constexpr int MAXS = 16;                              // the runtime keeps nsplit <= 16 here
-    f4 v[MAXS];
+    constexpr int MAXS = 16;  // partials loaded at once; more splits are summed 16 at a time
+    f4 ps = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c0 = 0; c0 < a.nsplit; c0 += MAXS) {
+      f4 v[MAXS];
 #pragma unroll
-    for (int sp = 0; sp < MAXS; sp++) v[sp] = pp[(int64_t)min(sp, a.nsplit - 1) * sstride];
-    f4 ps = v[0];
+      for (int sp = 0; sp < MAXS; sp++) v[sp] = pp[(int64_t)min(c0 + sp, a.nsplit - 1) * sstride];
+      if (c0 == 0) ps = v[0];
 #pragma unroll
-    for (int sp = 1; sp < MAXS; sp++)
-      if (sp < a.nsplit) ps += v[sp];  // split order
+      for (int sp = 0; sp < MAXS; sp++)
+        if ((c0 > 0 || sp > 0) && c0 + sp < a.nsplit) ps += v[sp];  // split order
+    }
     const int trow = t0 + li, kcol = k0 + li;
     f4 ga = {0.0f, 0.0f, 0.0f, 0.0f};
     if (a.g) {  // + g . A for this 16 x 16 tile (f32 MFMA; lane: token 4g + i, column li)

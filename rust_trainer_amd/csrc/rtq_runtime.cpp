@@ -460,8 +460,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
 //     64-token-padded T x K block);
 //   t <= 16 (rtq_dx16_*): K chunks x row splits, about three 4-wave workgroups per CU with at least
 //     four 32-row steps each (partials are T x K floats per split);
-//   t >= kDxWideT (rtq_dxw_*): as the first, with 256-token tiles.
-constexpr int64_t kDxWideT = 1024;
+//   rtq_dxw_*: as the first, with 256-token tiles, where that grid fills the CUs (see dx_plan).
 struct DxPlan {
   int64_t splits, nps;
   bool tok16;
@@ -471,16 +470,25 @@ struct DxPlan {
 DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
   DxPlan p;
   p.tok16 = t <= 16;
-  p.wide = !p.tok16 && (c->dx_wide == 1 || (c->dx_wide < 0 && t >= kDxWideT));
   const int64_t Kc = w->Kp / 128, steps = w->Np / 32;
+  // 256-token tiles when their grid fills whole rounds of the CUs (at least 85%) with at least 16
+  // row steps per workgroup; the split count rounds to the nearest whole grid (up to 32 splits)
+  const int64_t per_split = Kc * cdiv(t, 256);
+  const int64_t wsplits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(32, steps),
+                                                                  (c->cu_count + per_split / 2) / per_split));
+  const int64_t wgrid = roundup(cdiv(t, 256) * wsplits, 8) * Kc;
+  const bool wide_fits = 100 * wgrid >= 85 * cdiv(wgrid, c->cu_count) * c->cu_count && steps / wsplits >= 16;
+  p.wide = !p.tok16 && (c->dx_wide == 1 || (c->dx_wide < 0 && wide_fits));
   int64_t splits;
   if (p.tok16)
     splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(std::max<int64_t>(steps / 4, 1), 256),
                                                     cdiv(3 * c->cu_count, Kc)));
+  else if (p.wide)
+    splits = wsplits;
   else
-    splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16),
-                                                    cdiv(c->cu_count, Kc * cdiv(t, p.wide ? 256 : 64))));
-  if (c->dx_splits > 0) splits = std::min<int64_t>(std::min<int64_t>(steps, p.tok16 ? 256 : 16), c->dx_splits);
+    splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16), cdiv(c->cu_count, Kc * cdiv(t, 64))));
+  if (c->dx_splits > 0)
+    splits = std::min<int64_t>(std::min<int64_t>(steps, p.tok16 ? 256 : (p.wide ? 64 : 16)), c->dx_splits);
   p.nps = cdiv(steps, splits) * 32;
   p.splits = cdiv(w->Np, p.nps);
   p.part_floats = p.tok16 ? (size_t)(p.splits * t * w->cols) : (size_t)(p.splits * roundup(t, 64) * w->Kp);

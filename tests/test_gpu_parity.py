@@ -397,9 +397,10 @@ def test_linear_backward_dxw_lora(ctx_dxw, wtype):
 
 
 @pytest.mark.parametrize("wtype", [O.Q4_0, O.Q6_K])
-def test_backward_input_dxw_selected_by_t(ctx, wtype):
-    # t >= 1024 takes the 256-token tiles in the default context
-    n, k, t = 1024, 1024, 1100
+def test_backward_input_dxw_selected_by_grid(ctx, wtype):
+    # 4 token groups x 8 K chunks x 8 row splits of 16 steps: the default context picks the
+    # 256-token tiles by itself
+    n, k, t = 4096, 1024, 1000
     blocks, _, dy = make(wtype, n, k, t)
     w = hip(ctx, wtype, blocks, n, k)
     dx = np.zeros(t * k, np.float32)
