@@ -1824,10 +1824,11 @@ extern "C" __global__ __launch_bounds__(512) void rtq_dxw_q6_k(DxArgs a) { dx_ti
 //    w.backward_input(dy) + g.A, src/linear.rs:100-101,115-118)
 // gb[n][j] += sum_t (s*dy[t][n]) h[t][j]   (matmul_tn_acc, src/linear.rs:109)
 // ga[j][k] += sum_t g[t][j] x[t][k]        (matmul_tn_acc, src/linear.rs:113)
-// gb / ga: one 16x16 tile per workgroup, the 4 waves split t and reduce in LDS (single writer);
-// dx: one wave per 16 x 16 quarter of a dx-kernel fragment (the dx kernel's partial layout).
-extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a) {
-  constexpr int NW = 4;
+// gb / ga: one 16x16 tile per workgroup, the NW waves split t and reduce in LDS (single writer,
+// fixed order); dx: one wave per 16 x 16 quarter of a dx-kernel fragment (the dx kernel's partial
+// layout).  NW = 4, or 16 for long token ranges (four times the loads in flight per tile).
+template <int NW>
+__device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
   __shared__ float red[NW * 256];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
   const int jt = (a.r + 15) / 16;
@@ -1870,7 +1871,7 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a)
 #pragma unroll
     for (int i = 0; i < 4; i++) red[w * 256 + (4 * g + i) * 16 + li] = acc[i];
     __syncthreads();
-    {
+    if (threadIdx.x < 256) {
       const int rl = threadIdx.x >> 4, cl = threadIdx.x & 15;
       float s = 0.0f;
 #pragma unroll
@@ -1976,6 +1977,9 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a)
       }
   }
 }
+
+extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a) { bwd_finish<4>(a); }
+extern "C" __global__ __launch_bounds__(1024) void rtq_bwd_finish16(LoraGradArgs a) { bwd_finish<16>(a); }
 
 // ============================================================== row dequant (FrozenMatmul::row)
 // One thread per (row, 32-element block); bit-exact ggml dequant: (q - 8) * d, q * d.

@@ -125,6 +125,7 @@ enum Kid {
   K_DX16 = K_DX + F_COUNT,  // + format: t <= 16
   K_DXW = K_DX16 + F_COUNT,  // + format: large t, 256-token tiles
   K_BWD_FINISH = K_DXW + F_COUNT,
+  K_BWD_FINISH16,  // 16 waves per workgroup: long token reductions of dA / dB
   K_ROWS,        // + format
   K_COUNT = K_ROWS + F_COUNT
 };
@@ -140,7 +141,7 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
     "rtq_dxw_q4_0",         "rtq_dxw_q8_0",         "rtq_dxw_q4_k",         "rtq_dxw_q6_k",
-    "rtq_bwd_finish",
+    "rtq_bwd_finish",       "rtq_bwd_finish16",
     "rtq_rows_q4_0",        "rtq_rows_q8_0",        "rtq_rows_q4_k",        "rtq_rows_q6_k"};
 
 struct TimedLaunch {
@@ -543,9 +544,12 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
                   dp.tok16 ? 1 : 0};
   fa.n_gb = lora ? (int)(cdiv(N, 16) * jt) : 0;
   fa.n_ga = lora ? (int)(cdiv(K, 16) * jt) : 0;
-  // one wave per quarter of a dx fragment (or per token and 64 columns), four per workgroup
-  fa.n_dx = dp.tok16 ? (int)cdiv(t * cdiv(K, 64), 4) : (int)((w->Kp / 128) * cdiv(t, 64) * 8);
-  return launch(c, K_BWD_FINISH, dim3((unsigned)(fa.n_gb + fa.n_ga + fa.n_dx)), dim3(256), st, fa);
+  // one wave per quarter of a dx fragment (or per token and 64 columns), nw per workgroup; 16 waves
+  // per workgroup when the dA / dB tiles reduce over many tokens
+  const int nw = lora && t >= 512 ? 16 : 4;
+  fa.n_dx = dp.tok16 ? (int)cdiv(t * cdiv(K, 64), nw) : (int)cdiv((w->Kp / 128) * cdiv(t, 64) * 32, nw);
+  return launch(c, nw == 16 ? K_BWD_FINISH16 : K_BWD_FINISH, dim3((unsigned)(fa.n_gb + fa.n_ga + fa.n_dx)),
+                dim3(64 * nw), st, fa);
 }
 
 rtq_status check_weight(rtq_ctx* c, const rtq_weight* w) {

@@ -406,3 +406,24 @@ def test_backward_input_dxw_selected_by_grid(ctx, wtype):
     dx = np.zeros(t * k, np.float32)
     w.backward_input(dy, t, dx)
     assert rel_err(dx, O.frozen_backward_input(wtype, blocks, n, k, dy, nthreads=8)) <= TOL
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q6_K])
+@pytest.mark.parametrize("t", [512, 700])
+def test_linear_backward_long_token_range(ctx, wtype, t):
+    # t >= 512 with LoRA: the 16-wave finish reduces dA / dB over the tokens (t = 700: ragged
+    # last wave range)
+    n, k, r = 640, 1024, 16
+    blocks, x, dy = make(wtype, n, k, t)
+    A, B = lora(n, k, r)
+    lin = rt.Linear("blk.0.ffn_down", hip(ctx, wtype, blocks, n, k))
+    lin.lora = rt.Lora(r, 32.0, A, B)
+    ga0 = O.Rng(8).vec_normal(r * k, 0.01)
+    gb0 = O.Rng(9).vec_normal(n * r, 0.01)
+    lin.lora.ga[...] = ga0
+    lin.lora.gb[...] = gb0
+    dx = lin.backward(x, dy, t)
+    wdx, wga, wgb = O.linear_backward(wtype, blocks, n, k, x, dy, A=A, B=B, alpha=32.0, nthreads=8)
+    assert rel_err(dx, wdx) <= TOL
+    assert rel_err(lin.lora.ga - ga0, wga) <= TOL
+    assert rel_err(lin.lora.gb - gb0, wgb) <= TOL
