@@ -30,7 +30,7 @@ extern "C" {
 typedef int rtq_status;
 #define RTQ_OK 0
 #define RTQ_ERR_INVALID 1     /* bad argument / shape mismatch (reference: assert!) */
-#define RTQ_ERR_UNSUPPORTED 2 /* ggml type other than Q4_0, Q8_0, Q4_K, Q6_K */
+#define RTQ_ERR_UNSUPPORTED 2 /* weight type other than Q4_0, Q8_0, Q4_K, Q6_K, F32, TQ8_0 */
 #define RTQ_ERR_HIP 3         /* HIP runtime error (message in rtq_last_error) */
 #define RTQ_ERR_NO_DEVICE 4   /* no usable gfx950 device / code object failed to load */
 
@@ -39,6 +39,13 @@ typedef int rtq_status;
 #define RTQ_TYPE_Q8_0 8
 #define RTQ_TYPE_Q4_K 12
 #define RTQ_TYPE_Q6_K 14
+/* The trainer-native FrozenWeight storage (src/frozen.rs:33-45, HF / random-init models):
+ *   F32:   row-major f32 [rows x cols] (ggml id 0);
+ *   TQ8_0: not a ggml type - FrozenWeight::Q8_0, an f32 scale per 32 elements: the scales
+ *          [rows x cols/32] (f32) followed by the codes [rows x cols] (i8), cols % 32 == 0.
+ * Their forward takes f32 activations (no activation quantisation) and runs as f32 GEMMs. */
+#define RTQ_TYPE_F32 0
+#define RTQ_TYPE_TQ8_0 264
 
 typedef struct rtq_ctx rtq_ctx;
 typedef struct rtq_weight rtq_weight;

@@ -24,7 +24,11 @@ import os
 import numpy as np
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K = 0, 1, 2, 8, 12, 14, 15
-TYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_K: "Q8_K"}
+# not a ggml type: the trainer-native FrozenWeight::Q8_0 (src/frozen.rs:38-45), f32 scale per 32
+# elements, packed as scales [n][k/32] (f32) then codes [n][k] (i8)
+TQ8_0 = 264
+TYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_K: "Q8_K",
+              TQ8_0: "TQ8_0"}
 BLOCK_ELEMS = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256}
 BLOCK_BYTES = {F32: 4, F16: 2, Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210, Q8_K: 292}
 
@@ -55,6 +59,7 @@ def lib() -> ctypes.CDLL:
             "or_fp16_to_fp32": (_f, [ctypes.c_uint16]),
             "or_row_bytes": (_i64, [_i, _i64]),
             "or_quantize": (_i, [_i, _p, _i64, _p]),
+            "or_tq8_quantize": (_i, [_p, _i64, _i64, _p]),
             "or_dequant_row": (_i, [_i, _p, _i64, _p]),
             "or_act_type_for": (_i, [_i]),
             "or_quantize_acts_q8_0": (None, [_p, _i64, _p]),
@@ -139,9 +144,14 @@ def row_bytes(wtype: int, k: int) -> int:
 
 
 def quantize(wtype: int, w: np.ndarray) -> np.ndarray:
-    """Quantise an [n x k] f32 matrix row-major into GGUF blocks (uint8 [n, row_bytes])."""
+    """Quantise an [n x k] f32 matrix row-major into GGUF blocks (uint8 [n, row_bytes]); TQ8_0: the
+    trainer-native packing (flat uint8: scales then codes, src/frozen.rs:53-73)."""
     w = _f32(w)
     n, k = w.shape
+    if wtype == TQ8_0:
+        out = np.empty(n * (k // 32) * 4 + n * k, dtype=np.uint8)
+        _check(lib().or_tq8_quantize(_ptr(w), n, k, _ptr(out)), "tq8_quantize")
+        return out
     out = np.empty((n, row_bytes(wtype, k)), dtype=np.uint8)
     _check(lib().or_quantize(wtype, _ptr(w), w.size, _ptr(out)), "quantize")
     return out

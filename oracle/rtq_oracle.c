@@ -574,9 +574,61 @@ void or_matmul_tn_acc(float* out, const float* a, const float* b, int64_t k, int
   }
 }
 
+/* ------------------------------------------------------------------ trainer-native Q8_0
+ * FrozenWeight::Q8_0 (src/frozen.rs:38-45): per 32-element block an f32 scale d = amax / 127 and
+ * codes round(x / d) (Rust f32::round: halves away from zero, as C roundf), clamped to +-127
+ * (src/frozen.rs:53-73).  Packed here as scales [n][k/32] then codes [n][k].  The forward is
+ * q8_dot (src/frozen.rs:80-93: per block an f32 sum of q * x, then acc += d * s), the input
+ * gradient q8_axpy per token and row (src/frozen.rs:96-108,156-166: a = g * d, blocks with
+ * a == 0 skipped, y += a * q), row() is q8_axpy(1) into zeros (src/frozen.rs:172-176). */
+int or_tq8_quantize(const float* w, int64_t n, int64_t k, void* out) {
+  if (k % QK) return -2;
+  const int64_t nb = k / QK;
+  float* sc = (float*)out;
+  int8_t* qs = (int8_t*)((uint8_t*)out + (size_t)(n * nb) * 4);
+  for (int64_t b = 0; b < n * nb; b++) {
+    const float* blk = w + b * QK;
+    float amax = 0.0f;
+    for (int i = 0; i < QK; i++) amax = fmaxf(amax, fabsf(blk[i]));
+    const float d = amax / 127.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    sc[b] = d;
+    for (int i = 0; i < QK; i++) {
+      float q = roundf(blk[i] * id);
+      q = q < -127.0f ? -127.0f : (q > 127.0f ? 127.0f : q);
+      qs[b * QK + i] = (int8_t)q;
+    }
+  }
+  return 0;
+}
+
+static float tq8_dot(const float* sc, const int8_t* qs, const float* x, int64_t k) {
+  float acc = 0.0f;
+  for (int64_t b = 0; b < k / QK; b++) {
+    float s = 0.0f;
+    for (int i = 0; i < QK; i++) s += (float)qs[b * QK + i] * x[b * QK + i];
+    acc += sc[b] * s;
+  }
+  return acc;
+}
+
+static void tq8_axpy(float alpha, const float* sc, const int8_t* qs, float* y, int64_t k) {
+  for (int64_t b = 0; b < k / QK; b++) {
+    const float a = alpha * sc[b];
+    if (a == 0.0f) continue;
+    for (int i = 0; i < QK; i++) y[b * QK + i] += a * (float)qs[b * QK + i];
+  }
+}
+
+static void tq8_views(const void* w, int64_t n, int64_t k, const float** sc, const int8_t** qs) {
+  *sc = (const float*)w;
+  *qs = (const int8_t*)((const uint8_t*)w + (size_t)(n * (k / QK)) * 4);
+}
+
 /* ------------------------------------------------------------------ FrozenMatmul */
 static int supported_weight(int t) {
-  return t == OR_F32 || t == OR_F16 || t == OR_Q4_0 || t == OR_Q8_0 || t == OR_Q4_K || t == OR_Q6_K;
+  return t == OR_F32 || t == OR_F16 || t == OR_Q4_0 || t == OR_Q8_0 || t == OR_Q4_K || t == OR_Q6_K ||
+         t == OR_TQ8_0;
 }
 
 /* activation rows quantised once per call (QuantActs::prepare) */
@@ -638,6 +690,16 @@ static float row_dot(int wtype, const uint8_t* wrow, const uint8_t* arow, int64_
 int or_frozen_forward(int wtype, const void* w, int64_t n, int64_t k, const float* x, int64_t t, float* y,
                       int nthreads) {
   if (!supported_weight(wtype)) return -1;
+  if (wtype == OR_TQ8_0) { /* src/frozen.rs:121-136 */
+    if (k % QK) return -2;
+    const float* sc;
+    const int8_t* qs;
+    tq8_views(w, n, k, &sc, &qs);
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t i = 0; i < t; i++)
+      for (int64_t o = 0; o < n; o++) y[i * n + o] = tq8_dot(sc + o * (k / QK), qs + o * k, x + i * k, k);
+    return 0;
+  }
   const int64_t wrb = or_row_bytes(wtype, k);
   if (wrb < 0) return -2;
   const uint8_t* W = (const uint8_t*)w;
@@ -673,6 +735,23 @@ int or_frozen_forward(int wtype, const void* w, int64_t n, int64_t k, const floa
 int or_frozen_forward_f64(int wtype, const void* w, int64_t n, int64_t k, const float* x, int64_t t,
                           double* y) {
   if (!supported_weight(wtype)) return -1;
+  if (wtype == OR_TQ8_0) { /* the same products, every sum in f64 */
+    if (k % QK) return -2;
+    const float* sc;
+    const int8_t* qs;
+    tq8_views(w, n, k, &sc, &qs);
+    for (int64_t i = 0; i < t; i++)
+      for (int64_t o = 0; o < n; o++) {
+        double acc = 0;
+        for (int64_t b = 0; b < k / QK; b++) {
+          double s = 0;
+          for (int j = 0; j < QK; j++) s += (double)qs[o * k + b * QK + j] * (double)x[i * k + b * QK + j];
+          acc += (double)sc[o * (k / QK) + b] * s;
+        }
+        y[i * n + o] = acc;
+      }
+    return 0;
+  }
   const int64_t wrb = or_row_bytes(wtype, k);
   if (wrb < 0) return -2;
   const uint8_t* W = (const uint8_t*)w;
@@ -734,6 +813,19 @@ int or_frozen_forward_f64(int wtype, const void* w, int64_t n, int64_t k, const 
 int or_frozen_backward_input(int wtype, const void* w, int64_t n, int64_t k, const float* dy, int64_t t,
                              float* dx, int nthreads) {
   if (!supported_weight(wtype)) return -1;
+  if (wtype == OR_TQ8_0) { /* src/frozen.rs:155-166: per token, rows in order */
+    if (k % QK) return -2;
+    const float* sc;
+    const int8_t* qs;
+    tq8_views(w, n, k, &sc, &qs);
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t i = 0; i < t; i++)
+      for (int64_t o = 0; o < n; o++) {
+        const float g = dy[i * n + o];
+        if (g != 0.0f) tq8_axpy(g, sc + o * (k / QK), qs + o * k, dx + i * k, k);
+      }
+    return 0;
+  }
   const int64_t wrb = or_row_bytes(wtype, k);
   if (wrb < 0) return -2;
   const uint8_t* W = (const uint8_t*)w;
@@ -768,6 +860,15 @@ int or_frozen_backward_input(int wtype, const void* w, int64_t n, int64_t k, con
 }
 
 int or_frozen_row(int wtype, const void* w, int64_t n, int64_t k, int64_t r, float* out) {
+  if (wtype == OR_TQ8_0) {
+    if (k % QK || r < 0 || r >= n) return -2;
+    const float* sc;
+    const int8_t* qs;
+    tq8_views(w, n, k, &sc, &qs);
+    memset(out, 0, (size_t)k * 4);
+    tq8_axpy(1.0f, sc + r * (k / QK), qs + r * k, out, k);
+    return 0;
+  }
   const int64_t wrb = or_row_bytes(wtype, k);
   if (wrb < 0 || r < 0 || r >= n) return -2;
   return or_dequant_row(wtype, (const uint8_t*)w + r * wrb, k, out);

@@ -34,8 +34,14 @@ enum {
   OR_Q8_0 = 8,
   OR_Q4_K = 12,
   OR_Q6_K = 14,
-  OR_Q8_K = 15
+  OR_Q8_K = 15,
+  /* not a ggml type: the trainer-native FrozenWeight::Q8_0 (src/frozen.rs:38-45), f32 scale per 32
+     elements; packed as the scales [n][k/32] (f32) followed by the codes [n][k] (i8) */
+  OR_TQ8_0 = 264
 };
+
+/* ---- trainer-native FrozenWeight::Q8_0 (src/frozen.rs:53-73 quantiser, :80-108 dot / axpy) ---- */
+int or_tq8_quantize(const float* w, int64_t n, int64_t k, void* out);
 
 /* ---- Rng: src/tensor.rs:155-199 ---- */
 uint64_t or_rng_seed(uint64_t seed);

@@ -15,6 +15,8 @@ RTQ_OK = 0
 STATUS_NAMES = {0: "OK", 1: "ERR_INVALID", 2: "ERR_UNSUPPORTED", 3: "ERR_HIP", 4: "ERR_NO_DEVICE"}
 
 TYPE_Q4_0, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 2, 8, 12, 14
+# trainer-native FrozenWeight storage (src/frozen.rs:33-45): f32, and Q8_0 with f32 block scales
+TYPE_F32, TYPE_TQ8_0 = 0, 264
 
 # every symbol include/rtq.h declares, with (restype, argtypes)
 _p = ctypes.c_void_p

@@ -59,7 +59,7 @@ def build_runtime(hsaco: str) -> str:
           "-D__HIP_PLATFORM_AMD__", f'-DRTQ_HSACO_PATH="{hsaco}"',
           "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"), "-I", CSRC,
           os.path.join(CSRC, "rtq_runtime.cpp"), "-o", tmp,
-          "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"])
+          "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-lrocblas", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"])
     os.replace(tmp, out)
     return out
 

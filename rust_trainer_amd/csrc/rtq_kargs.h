@@ -74,6 +74,20 @@ struct ActArgs {
   uint16_t* xdh;  // or null: the fp16 bits of xd, same layout (rtq_mm_*'s scale MFMA operand)
 };
 
+// ---------------------------------------------------------------- trainer-native weights
+// FrozenWeight::{F32, Q8_0} (src/frozen.rs:33-45): f32 [N][K], or f32 scales [N][K/32] then i8
+// codes [N][K] (TQ8_0).  Their products are plain f32 GEMMs (rocBLAS); these kernels dequantise
+// (out = 0 + d * q, row() of src/frozen.rs:172-176), copy rows and add the bias.
+struct DenseArgs {
+  const float* w;    // F32 weight, or null
+  const float* sc;   // TQ8_0 scales, or null
+  const int8_t* qs;  // TQ8_0 codes
+  int64_t N, K;
+  int64_t r0, count;  // rows [r0, r0 + count) (dequant / row copy); bias: count = T
+  float* out;         // [count][K]; bias: y [T][N]
+  const float* bias;
+};
+
 // ---------------------------------------------------------------- forward GEMM
 // y[t][n] = sum_b d_w[n][b] d_x[t][b] isum_b(t, n)  (+ bias[n]) (+ s * sum_j h[t][j] B[n][j])
 // K-quants: sum over super-blocks of (d d_x) S1 - (dmin d_x) S2 (Q4_K) or (d d_x) S (Q6_K)

@@ -1981,6 +1981,28 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
 extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a) { bwd_finish<4>(a); }
 extern "C" __global__ __launch_bounds__(1024) void rtq_bwd_finish16(LoraGradArgs a) { bwd_finish<16>(a); }
 
+// ============================================================== trainer-native weights
+// rows [r0, r0 + count) of an F32 (copy) or TQ8_0 weight (0 + d * q: q8_axpy(1) into zeros,
+// src/frozen.rs:172-176, bit-exact) into out [count][K]; the same kernel dequantises a whole TQ8_0
+// weight for the f32 GEMMs
+extern "C" __global__ __launch_bounds__(256) void rtq_dense_rows(DenseArgs a) {
+  const int64_t n = a.count * a.K;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = a.r0 + i / a.K, k = i % a.K;
+    if (a.w)
+      a.out[i] = a.w[r * a.K + k];
+    else
+      a.out[i] = 0.0f + a.sc[r * (a.K / 32) + k / 32] * (float)a.qs[r * a.K + k];
+  }
+}
+
+// y[t][n] += bias[n] (src/linear.rs:77-83), t < count
+extern "C" __global__ __launch_bounds__(256) void rtq_dense_bias(DenseArgs a) {
+  const int64_t n = a.count * a.N;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    a.out[i] = a.out[i] + a.bias[i % a.N];
+}
+
 // ============================================================== row dequant (FrozenMatmul::row)
 // One thread per (row, 32-element block); bit-exact ggml dequant: (q - 8) * d, q * d.
 extern "C" __global__ __launch_bounds__(256) void rtq_rows_q4_0(RowArgs a) {

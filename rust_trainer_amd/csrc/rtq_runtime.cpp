@@ -10,6 +10,7 @@
 #include "rtq.h"
 
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <cstdarg>
@@ -126,6 +127,8 @@ enum Kid {
   K_DXW = K_DX16 + F_COUNT,  // + format: large t, 256-token tiles
   K_BWD_FINISH = K_DXW + F_COUNT,
   K_BWD_FINISH16,  // 16 waves per workgroup: long token reductions of dA / dB
+  K_DENSE_ROWS,    // trainer-native weights: rows / dequantisation, bias
+  K_DENSE_BIAS,
   K_ROWS,        // + format
   K_COUNT = K_ROWS + F_COUNT
 };
@@ -141,7 +144,7 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
     "rtq_dxw_q4_0",         "rtq_dxw_q8_0",         "rtq_dxw_q4_k",         "rtq_dxw_q6_k",
-    "rtq_bwd_finish",       "rtq_bwd_finish16",
+    "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_dense_rows",       "rtq_dense_bias",
     "rtq_rows_q4_0",        "rtq_rows_q8_0",        "rtq_rows_q4_k",        "rtq_rows_q6_k"};
 
 struct TimedLaunch {
@@ -168,6 +171,7 @@ struct rtq_ctx {
   int dx_wide = -1;   // 256-token dx tiles: -1 automatic, 0 never, 1 for every t > 16 (RTQ_DX_WIDE)
   int fwd_waves = 8;  // waves splitting K in the wide Q4_0 / Q8_0 forward (RTQ_FWD_WAVES: 4 or 8)
   int fwd_mm = -1;    // large-grid forward: -1 automatic, 0 never, 1 whenever the format allows (RTQ_FWD_MM)
+  rocblas_handle blas = nullptr;  // created on the first trainer-native (f32 GEMM) weight
   int64_t t_launches[K_COUNT] = {};
   double t_ms[K_COUNT] = {};
 };
@@ -183,6 +187,7 @@ struct rtq_weight {
   uint16_t* wd = nullptr;
   uint16_t* wdr = nullptr;  // row-major scales for the GEMV (the K-quants' wd itself)
   uint32_t* wsb = nullptr;  // K-quant super-block scales, else null
+  const float* wsc = nullptr;  // TQ8_0: f32 block scales (wq: the i8 codes; F32: wq is the weight)
 };
 
 namespace {
@@ -255,7 +260,9 @@ rtq_status ensure_ws(rtq_ctx* c, size_t bytes) {
 
 bool is_q32(int type) { return type == RTQ_TYPE_Q4_0 || type == RTQ_TYPE_Q8_0; }
 bool is_kquant(int type) { return type == RTQ_TYPE_Q4_K || type == RTQ_TYPE_Q6_K; }
-bool supported(int type) { return is_q32(type) || is_kquant(type); }
+// trainer-native FrozenWeight storage: f32 products through rocBLAS
+bool is_dense(int type) { return type == RTQ_TYPE_F32 || type == RTQ_TYPE_TQ8_0; }
+bool supported(int type) { return is_q32(type) || is_kquant(type) || is_dense(type); }
 int fmt_index(int type) {
   switch (type) {
     case RTQ_TYPE_Q4_0: return F_Q4_0;
@@ -267,9 +274,11 @@ int fmt_index(int type) {
 // device codes are bytes (Q8_0 layout) for Q8_0 and Q6_K, nibbles (Q4_0 layout) otherwise
 bool byte_codes(int type) { return type == RTQ_TYPE_Q8_0 || type == RTQ_TYPE_Q6_K; }
 
-int64_t block_elems(int type) { return is_q32(type) ? 32 : 256; }
+int64_t block_elems(int type) { return type == RTQ_TYPE_F32 ? 1 : (is_q32(type) || type == RTQ_TYPE_TQ8_0 ? 32 : 256); }
 int64_t block_bytes(int type) {
   switch (type) {
+    case RTQ_TYPE_F32: return 4;
+    case RTQ_TYPE_TQ8_0: return 36;  // f32 scale + 32 codes (stored as two arrays)
     case RTQ_TYPE_Q4_0: return 18;
     case RTQ_TYPE_Q8_0: return 34;
     case RTQ_TYPE_Q4_K: return 144;
@@ -286,6 +295,7 @@ struct FwdPlan {
   bool skinny;
   bool gemv;  // t <= 16 through rtq_gemv_* (see gemv_plan)
   size_t xq_bytes, xd_floats, xg_floats, h_floats, xdh_bytes;
+  size_t dense_bytes;  // trainer-native weights: dequantised TQ8_0 copy + h
 };
 
 constexpr int kFwdWideTT = 4;     // rtq_fwd_*_w: 64 tokens x (16 * wide_rg) rows per workgroup
@@ -321,8 +331,13 @@ GemvPlan gemv_plan(const rtq_ctx* c, const rtq_weight* w) {
 }
 
 FwdPlan fwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
-  FwdPlan p;
+  FwdPlan p{};
   p.T = t;
+  if (is_dense(w->type)) {
+    p.dense_bytes = (w->type == RTQ_TYPE_TQ8_0 ? (size_t)(w->rows * w->cols) * 4 : 0) +
+                    (size_t)(t * std::max<int64_t>(r, 0)) * 4 + 2 * 256;
+    return p;
+  }
   p.skinny = t <= 16;
   p.gemv = p.skinny && r <= RTQ_LDS_RANK;
   // wide: 128-token padding, the token block of rtq_mm_* (rtq_fwd_*_w covers the first
@@ -338,7 +353,94 @@ FwdPlan fwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
 }
 
 size_t fwd_ws_bytes(const FwdPlan& p) {
-  return p.xq_bytes + p.xd_floats * 4 + p.xg_floats * 4 + p.h_floats * 4 + p.xdh_bytes + 6 * 256;
+  return p.xq_bytes + p.xd_floats * 4 + p.xg_floats * 4 + p.h_floats * 4 + p.xdh_bytes + p.dense_bytes + 6 * 256;
+}
+
+// ------------------------------------------------------------------ trainer-native weights
+// FrozenWeight::{F32, Q8_0} (src/frozen.rs:33-187) and the Linear LoRA math around them as f32
+// GEMMs (rocBLAS, column-major: a row-major product C = op(A) op(B) is the column-major
+// C^T = op(B)^T op(A)^T).  TQ8_0 is dequantised per call into the workspace first.
+rtq_status blas_handle(rtq_ctx* c, hipStream_t st, rocblas_handle* h) {
+  if (!c->blas && rocblas_create_handle(&c->blas) != rocblas_status_success) {
+    c->blas = nullptr;
+    return fail(RTQ_ERR_HIP, "rocblas_create_handle failed");
+  }
+  if (rocblas_set_stream(c->blas, st) != rocblas_status_success) return fail(RTQ_ERR_HIP, "rocblas_set_stream failed");
+  *h = c->blas;
+  return RTQ_OK;
+}
+
+// row-major C[M x N] = alpha op(A) op(B) + beta C; lda / ldb / ldc: row lengths as stored
+rtq_status rm_sgemm(rocblas_handle h, bool ta, bool tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
+                    int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc) {
+  if (M == 0 || N == 0) return RTQ_OK;
+  const rocblas_status e =
+      rocblas_sgemm(h, tb ? rocblas_operation_transpose : rocblas_operation_none,
+                    ta ? rocblas_operation_transpose : rocblas_operation_none, (rocblas_int)N, (rocblas_int)M,
+                    (rocblas_int)K, &alpha, B, (rocblas_int)ldb, A, (rocblas_int)lda, &beta, C, (rocblas_int)ldc);
+  if (e != rocblas_status_success) return fail(RTQ_ERR_HIP, "rocblas_sgemm: %s", rocblas_status_to_string(e));
+  return RTQ_OK;
+}
+
+// the weight as f32 [N][K]: F32 in place, TQ8_0 dequantised into the arena
+rtq_status dense_weight(rtq_ctx* c, const rtq_weight* w, Arena& ar, hipStream_t st, const float** W) {
+  if (w->type == RTQ_TYPE_F32) {
+    *W = reinterpret_cast<const float*>(w->wq);
+    return RTQ_OK;
+  }
+  float* out = ar.take<float>((size_t)(w->rows * w->cols));
+  if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
+  DenseArgs da{nullptr, w->wsc, reinterpret_cast<const int8_t*>(w->wq), w->rows, w->cols, 0, w->rows, out, nullptr};
+  RTQ_TRY(launch(c, K_DENSE_ROWS, dim3((unsigned)std::min<int64_t>(cdiv(w->rows * w->cols, 256), 8192)), dim3(256), st, da));
+  *W = out;
+  return RTQ_OK;
+}
+
+// y = x W^T (src/frozen.rs:121-122); + bias; + s (x A^T) B^T (src/linear.rs:73-93)
+rtq_status enqueue_forward_dense(rtq_ctx* c, const rtq_weight* w, const float* x, int64_t t, float* y,
+                                 const float* bias, const float* la, const float* lb, int64_t r, float s, Arena& ar,
+                                 hipStream_t st) {
+  const int64_t N = w->rows, K = w->cols;
+  const float* W;
+  RTQ_TRY(dense_weight(c, w, ar, st, &W));
+  rocblas_handle h;
+  RTQ_TRY(blas_handle(c, st, &h));
+  RTQ_TRY(rm_sgemm(h, false, true, t, N, K, 1.0f, x, K, W, K, 0.0f, y, N));
+  if (bias) {
+    DenseArgs da{nullptr, nullptr, nullptr, N, K, 0, t, y, bias};
+    RTQ_TRY(launch(c, K_DENSE_BIAS, dim3((unsigned)std::min<int64_t>(cdiv(t * N, 256), 8192)), dim3(256), st, da));
+  }
+  if (la && lb && r > 0) {
+    float* hh = ar.take<float>((size_t)(t * r));
+    if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
+    RTQ_TRY(rm_sgemm(h, false, true, t, r, K, 1.0f, x, K, la, K, 0.0f, hh, r));  // h = x A^T
+    RTQ_TRY(rm_sgemm(h, false, true, t, N, r, s, hh, r, lb, r, 1.0f, y, N));     // y += s h B^T
+  }
+  return RTQ_OK;
+}
+
+// dx (+)= dy W (src/frozen.rs:139-167); with LoRA (src/linear.rs:97-121): h = x A^T,
+// gb += (s dy)^T h, g = (s dy) B, ga += g^T x, dx += g A
+rtq_status enqueue_backward_dense(rtq_ctx* c, const rtq_weight* w, const float* dy, int64_t t, float* dx,
+                                  bool accumulate, const float* x, const float* la, const float* lb, int64_t r,
+                                  float s, float* ga, float* gb, Arena& ar, hipStream_t st) {
+  const int64_t N = w->rows, K = w->cols;
+  const float* W;
+  RTQ_TRY(dense_weight(c, w, ar, st, &W));
+  rocblas_handle h;
+  RTQ_TRY(blas_handle(c, st, &h));
+  RTQ_TRY(rm_sgemm(h, false, false, t, K, N, 1.0f, dy, N, W, K, accumulate ? 1.0f : 0.0f, dx, K));
+  if (la && lb && r > 0) {
+    float* hh = ar.take<float>((size_t)(t * r));
+    float* g = ar.take<float>((size_t)(t * r));
+    if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
+    RTQ_TRY(rm_sgemm(h, false, true, t, r, K, 1.0f, x, K, la, K, 0.0f, hh, r));   // h = x A^T
+    RTQ_TRY(rm_sgemm(h, true, false, N, r, t, s, dy, N, hh, r, 1.0f, gb, r));     // gb += s dy^T h
+    RTQ_TRY(rm_sgemm(h, false, false, t, r, N, s, dy, N, lb, r, 0.0f, g, r));     // g = s dy B
+    RTQ_TRY(rm_sgemm(h, true, false, r, K, t, 1.0f, g, r, x, K, 1.0f, ga, K));    // ga += g^T x
+    RTQ_TRY(rm_sgemm(h, false, false, t, K, r, 1.0f, g, r, la, K, 1.0f, dx, K));  // dx += g A
+  }
+  return RTQ_OK;
 }
 
 
@@ -349,6 +451,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
                            hipStream_t st) {
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
+  if (is_dense(w->type)) return enqueue_forward_dense(c, w, x, t, y, bias, la, lb, lora ? r : 0, s, ar, st);
   FwdPlan p = fwd_plan(w, t, lora ? r : 0);
   // the debug sums come from the skinny / wide kernels; the GEMV pays off once its row tiles alone
   // give a workgroup per CU (an LM head), below that the skinny kernel's K split wins
@@ -499,6 +602,9 @@ DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
 // backward workspace: h, g [t x r], their slice partials [t][r][slices], dx split partials
 size_t bwd_ws_bytes(const rtq_ctx* c, const rtq_weight* w, int64_t t, int64_t r) {
   const int64_t n = w->rows, k = w->cols;
+  if (is_dense(w->type))
+    return (w->type == RTQ_TYPE_TQ8_0 ? (size_t)(n * k) * 4 : 0) + (size_t)(2 * t * std::max<int64_t>(r, 0)) * 4 +
+           3 * 256;
   const int64_t sl = roundup(cdiv(std::max<int64_t>(n, 1), RTQ_ACT_KQ), 4) + roundup(cdiv(std::max<int64_t>(k, 1), RTQ_ACT_KQ), 4);
   return (size_t)((2 + sl) * t * std::max<int64_t>(r, 0)) * 4 + dx_plan(c, w, std::max<int64_t>(t, 1)).part_floats * 4 +
          6 * 256;
@@ -516,6 +622,8 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
                             float* gb, Arena& ar, hipStream_t st) {
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
+  if (is_dense(w->type))
+    return enqueue_backward_dense(c, w, dy, t, dx, accumulate, x, la, lb, lora ? r : 0, s, ga, gb, ar, st);
   const int N = (int)w->rows, K = (int)w->cols;
   if ((uint64_t)t * (uint64_t)N * 4u >= (1ull << 31))
     return fail(RTQ_ERR_INVALID, "dy of %lld x %d floats exceeds the 2 GiB buffer-offset range", (long long)t, N);
@@ -733,6 +841,7 @@ void rtq_ctx_destroy(rtq_ctx* c) {
   }
   for (auto e : c->free_events) (void)hipEventDestroy(e);
   if (c->ws) (void)hipFree(c->ws);
+  if (c->blas) (void)rocblas_destroy_handle(c->blas);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   if (c->mod) (void)hipModuleUnload(c->mod);
   delete c;
@@ -837,6 +946,31 @@ rtq_status rtq_weight_create(rtq_ctx* c, int type, const void* blocks, size_t nb
   w->Np = roundup(rows, RTQ_ROW_PAD);
   w->Kp = roundup(cols, RTQ_CHUNK_Q);
   w->gguf_bytes = expect;
+  if (is_dense(type)) {  // trainer-native storage, uploaded as it is
+    if ((uint64_t)rows * (uint64_t)cols * 4u >= (1ull << 31) * 2u) {
+      delete w;
+      return fail(RTQ_ERR_INVALID, "weight %lldx%lld too large for the f32 GEMM path", (long long)rows, (long long)cols);
+    }
+    hipError_t e = hipMalloc(&w->dmem, expect);
+    if (e != hipSuccess) {
+      delete w;
+      return fail(RTQ_ERR_HIP, "hipMalloc(%zu): %s", expect, hipGetErrorString(e));
+    }
+    e = hipMemcpy(w->dmem, blocks, expect, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(w->dmem);
+      delete w;
+      return fail(RTQ_ERR_HIP, "upload: %s", hipGetErrorString(e));
+    }
+    if (type == RTQ_TYPE_TQ8_0) {
+      w->wsc = reinterpret_cast<const float*>(w->dmem);
+      w->wq = (char*)w->dmem + (size_t)rows * (cols / 32) * 4;
+    } else {
+      w->wq = w->dmem;
+    }
+    *out = w;
+    return RTQ_OK;
+  }
   const int64_t nbp = w->Kp / 32;
   const size_t q_bytes = (size_t)w->Np * nbp * (byte_codes(type) ? 32 : 16);
   const size_t d_bytes = (size_t)w->Np * nbp * 2;
@@ -948,6 +1082,11 @@ rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora
 
 static rtq_status enqueue_rows(rtq_ctx* c, const rtq_weight* w, int64_t r0, int64_t count, float* out,
                                hipStream_t st) {
+  if (is_dense(w->type)) {  // F32: copy; TQ8_0: 0 + d * q (src/frozen.rs:169-177)
+    DenseArgs da{w->type == RTQ_TYPE_F32 ? reinterpret_cast<const float*>(w->wq) : nullptr, w->wsc,
+                 reinterpret_cast<const int8_t*>(w->wq), w->rows, w->cols, r0, count, out, nullptr};
+    return launch(c, K_DENSE_ROWS, dim3((unsigned)std::min<int64_t>(cdiv(count * w->cols, 256), 8192)), dim3(256), st, da);
+  }
   RowArgs ra{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, (int)w->cols, (int)r0, (int)count, out};
   const int64_t threads = count * (w->cols / 32);
   return launch(c, K_ROWS + fmt_index(w->type), dim3((unsigned)cdiv(threads, 256)), dim3(256), st, ra);
@@ -1094,7 +1233,7 @@ rtq_status rtq_frozen_row(rtq_ctx* c, const rtq_weight* w, int64_t r, float* out
 
 // ------------------------------------------------------------------ parity / debug
 int64_t rtq_debug_isums_per_row(const rtq_weight* w) {
-  if (!w) return 0;
+  if (!w || is_dense(w->type)) return 0;
   if (is_q32(w->type)) return w->cols / 32;
   if (w->type == RTQ_TYPE_Q4_K) return 2 * (w->cols / 256);
   return w->cols / 256;
@@ -1103,6 +1242,7 @@ int64_t rtq_debug_isums_per_row(const rtq_weight* w) {
 rtq_status rtq_debug_quantize_acts(rtq_ctx* c, const rtq_weight* w, const float* x, int64_t t, void* out) {
   RTQ_TRY(check_weight(c, w));
   RTQ_TRY(check_t(t));
+  if (is_dense(w->type)) return fail(RTQ_ERR_UNSUPPORTED, "trainer-native weights take f32 activations");
   if (t == 0) return RTQ_OK;
   if (!x || !out) return fail(RTQ_ERR_INVALID, "null x/out");
   HostCall hc(c);
@@ -1169,6 +1309,7 @@ rtq_status rtq_debug_quantize_acts(rtq_ctx* c, const rtq_weight* w, const float*
 rtq_status rtq_debug_block_isums(rtq_ctx* c, const rtq_weight* w, const float* x, int64_t t, int32_t* out) {
   RTQ_TRY(check_weight(c, w));
   RTQ_TRY(check_t(t));
+  if (is_dense(w->type)) return fail(RTQ_ERR_UNSUPPORTED, "trainer-native weights have no integer block sums");
   if (t == 0) return RTQ_OK;
   if (!x || !out) return fail(RTQ_ERR_INVALID, "null x/out");
   HostCall hc(c);

@@ -128,16 +128,55 @@ class FrozenMatmul(abc.ABC):
     def nbytes(self) -> int: ...
 
 
-class HipFrozen(FrozenMatmul):
-    """GGUF-block weight on an MI355X (``RieFrozen::new``, src/rie.rs:58-60).
+def pack_trainer_q8_0(w, out: int, inp: int) -> np.ndarray:
+    """FrozenWeight::q8_0's quantiser (src/frozen.rs:53-73) into the TYPE_TQ8_0 packing: per
+    32-element block d = amax / 127 (f32), q = round(x / d) with halves away from zero (Rust
+    f32::round), clamped to +-127; the scales [out x inp/32] (f32) then the codes (i8), as bytes."""
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(out, inp)
+    assert inp % 32 == 0, "TQ8_0 needs whole 32-element blocks"
+    blk = w.reshape(-1, 32)
+    amax = np.abs(blk).max(axis=1)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    inv = np.zeros_like(d)
+    nz = d > 0
+    inv[nz] = np.float32(1.0) / d[nz]
+    v = blk * inv[:, None]                       # f32 products, as x * id in the reference
+    tr = np.trunc(v)
+    q = tr + np.where(np.abs(v - tr) >= np.float32(0.5), np.sign(v), np.float32(0.0))  # exact half-away rounding
+    q = np.clip(q, -127.0, 127.0).astype(np.int8)
+    return np.concatenate([d.view(np.uint8), q.reshape(-1).view(np.uint8)])
 
-    ``blocks`` are the weight's packed GGUF bytes (``Weight::data()``), ``rows`` = out,
-    ``cols`` = in.  Supported types: Q4_0 (2), Q8_0 (8).
+
+class HipFrozen(FrozenMatmul):
+    """Frozen weight on an MI355X (``RieFrozen::new``, src/rie.rs:58-60; ``FrozenWeight``,
+    src/frozen.rs:33-75).
+
+    ``blocks`` are the weight's packed bytes: GGUF blocks (``Weight::data()``) for Q4_0 (2), Q8_0 (8),
+    Q4_K (12), Q6_K (14); a float32 [rows x cols] array for F32 (0); the ``pack_trainer_q8_0``
+    bytes for the trainer-native Q8_0 with f32 scales (TYPE_TQ8_0).  ``rows`` = out, ``cols`` = in.
     """
+
+    @classmethod
+    def f32(cls, w, out: int, inp: int, ctx: Context | None = None) -> "HipFrozen":
+        """``FrozenWeight::f32`` (src/frozen.rs:48-51)."""
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        assert w.size == out * inp, "weight shape mismatch"
+        return cls(_ffi.TYPE_F32, w, out, inp, ctx=ctx)
+
+    @classmethod
+    def q8_0(cls, w, out: int, inp: int, ctx: Context | None = None) -> "HipFrozen":
+        """``FrozenWeight::q8_0`` (src/frozen.rs:53-73): quantised when ``inp`` is a multiple of 32,
+        else kept f32."""
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        assert w.size == out * inp
+        if inp % 32:
+            return cls.f32(w, out, inp, ctx=ctx)
+        return cls(_ffi.TYPE_TQ8_0, pack_trainer_q8_0(w, out, inp), out, inp, ctx=ctx)
 
     def __init__(self, ggml_type: int, blocks, rows: int, cols: int, ctx: Context | None = None):
         self.ctx = ctx or default_context()
-        b = np.ascontiguousarray(blocks, dtype=np.uint8)
+        arr = np.ascontiguousarray(blocks)
+        b = arr.view(np.uint8).reshape(-1) if arr.dtype != np.uint8 else arr  # bytes as they are
         h = ctypes.c_void_p()
         _ffi.check(_ffi.lib().rtq_weight_create(self.ctx.handle, ggml_type, b.ctypes.data, b.nbytes, rows, cols,
                                                 ctypes.byref(h)), "rtq_weight_create")

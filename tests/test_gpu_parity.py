@@ -427,3 +427,62 @@ def test_linear_backward_long_token_range(ctx, wtype, t):
     assert rel_err(dx, wdx) <= TOL
     assert rel_err(lin.lora.ga - ga0, wga) <= TOL
     assert rel_err(lin.lora.gb - gb0, wgb) <= TOL
+
+
+# ---------------------------------------------------------------- trainer-native FrozenWeight (F32, Q8_0 f32-scale)
+def _trainer_weight(ctx, kind, n, k):
+    w = O.Rng(1).vec_normal(n * k, 0.02).reshape(n, k)
+    if kind == "f32":
+        return rt.HipFrozen.f32(w, n, k, ctx=ctx), O.F32, w.astype(np.float32).view(np.uint8)
+    return rt.HipFrozen.q8_0(w, n, k, ctx=ctx), O.TQ8_0, O.quantize(O.TQ8_0, w)
+
+
+@pytest.mark.parametrize("kind", ["f32", "tq8"])
+@pytest.mark.parametrize("n,k,t", [(64, 128, 1), (200, 256, 37), (3072, 1024, 256)])
+def test_trainer_native_frozen_matches_oracle(ctx, kind, n, k, t):
+    hw, otype, ob = _trainer_weight(ctx, kind, n, k)
+    assert hw.nbytes() == (n * k * 4 if kind == "f32" else n * (k // 32) * 4 + n * k)  # src/frozen.rs:180-185
+    x = O.Rng(2).vec_normal(t * k, 1.0).reshape(t, k)
+    dy = O.Rng(3).vec_normal(t * n, 1.0).reshape(t, n)
+    assert rel_err(hw.forward(x, t), O.frozen_forward(otype, ob, n, k, x, nthreads=8)) <= TOL
+    dx0 = O.Rng(7).vec_normal(t * k, 1.0)
+    dx = dx0.copy()
+    hw.backward_input(dy, t, dx)  # accumulates
+    want = O.frozen_backward_input(otype, ob, n, k, dy, nthreads=8)
+    assert rel_err(dx - dx0, want) <= TOL
+    out = np.empty(k, np.float32)
+    for r in (0, n // 2, n - 1):  # row(): copy / 0 + d * q, bit-exact
+        hw.row(r, out)
+        assert np.array_equal(out, O.frozen_row(otype, ob, n, k, r)), r
+
+
+@pytest.mark.parametrize("kind", ["f32", "tq8"])
+def test_trainer_native_linear_lora_matches_oracle(ctx, kind):
+    n, k, t, r = 512, 256, 70, 16
+    hw, otype, ob = _trainer_weight(ctx, kind, n, k)
+    _, x, dy = make(O.Q4_0, n, k, t)
+    A, B = lora(n, k, r)
+    bias = O.Rng(6).vec_normal(n, 0.1)
+    lin = rt.Linear("blk.0.attn_o", hw, bias=bias)
+    lin.lora = rt.Lora(r, 2.0 * r, A, B)
+    y = lin.forward(x, t)
+    assert rel_err(y, O.linear_forward(otype, ob, n, k, x, bias=bias, A=A, B=B, alpha=2.0 * r, nthreads=8)) <= TOL
+    ga0 = O.Rng(8).vec_normal(r * k, 0.01)
+    gb0 = O.Rng(9).vec_normal(n * r, 0.01)
+    lin.lora.ga[...] = ga0
+    lin.lora.gb[...] = gb0
+    dx = lin.backward(x, dy, t)
+    wdx, wga, wgb = O.linear_backward(otype, ob, n, k, x, dy, A=A, B=B, alpha=2.0 * r, nthreads=8)
+    assert rel_err(dx, wdx) <= TOL
+    assert rel_err(lin.lora.ga - ga0, wga) <= TOL
+    assert rel_err(lin.lora.gb - gb0, wgb) <= TOL
+
+
+def test_trainer_q8_0_falls_back_to_f32(ctx):
+    # FrozenWeight::q8_0 keeps f32 when the row length is not a whole number of blocks
+    # (src/frozen.rs:55-57)
+    w = O.Rng(1).vec_normal(8 * 40, 0.02).reshape(8, 40)
+    hw = rt.HipFrozen.q8_0(w, 8, 40, ctx=ctx)
+    assert hw.ggml_type == rt.TYPE_F32 and hw.nbytes() == 8 * 40 * 4
+    x = O.Rng(2).vec_normal(3 * 40, 1.0).reshape(3, 40)
+    assert rel_err(hw.forward(x, 3), x.astype(np.float64) @ w.T.astype(np.float64)) <= 1e-5

@@ -348,3 +348,50 @@ def test_lora_grads_finite_differences():
 def test_oracle_rejects_bad_shapes():
     with pytest.raises(ValueError):
         O.frozen_forward(O.Q4_0, np.zeros((2, 18), np.uint8), 2, 48, np.zeros((1, 48), np.float32))
+
+
+# ---------------------------------------------------------------- trainer-native FrozenWeight (src/frozen.rs)
+def _tq8_views(b, n, k):
+    sc = b[: n * (k // 32) * 4].view(np.float32).reshape(n, k // 32)
+    qs = b[n * (k // 32) * 4:].view(np.int8).reshape(n, k)
+    return sc, qs
+
+
+def test_tq8_quantiser_known_answers():
+    # src/frozen.rs:59-70: d = amax / 127, q = round(x / d) with halves away from zero; amax 127
+    # gives d = 1, so x = m + 0.5 must round away from zero
+    w = np.zeros((3, 32), np.float32)
+    w[0, :8] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.49, -126.5, 3.0]
+    w[2, :] = np.float32(1e-30) * np.arange(32, dtype=np.float32)  # tiny but non-zero
+    sc, qs = _tq8_views(O.quantize(O.TQ8_0, w), 3, 32)
+    assert sc[0, 0] == 1.0 and list(qs[0, :8]) == [127, 3, -3, 1, -1, 1, -127, 3]
+    assert sc[1, 0] == 0.0 and not qs[1].any()  # all-zero block: d = 0, id = 0, codes 0
+    assert qs[2, 31] == 127 and sc[2, 0] == np.float32(np.float32(31e-30) / np.float32(127.0))
+
+
+def test_tq8_round_trip_bound():
+    n, k = 40, 256
+    w = O.Rng(11).vec_normal(n * k, 0.02).reshape(n, k)
+    sc, qs = _tq8_views(O.quantize(O.TQ8_0, w), n, k)
+    deq = (qs.astype(np.float64).reshape(n, k // 32, 32) * sc[:, :, None]).reshape(n, k)
+    assert (np.abs(deq - w) <= sc.repeat(32, axis=1) * 0.5 * (1 + 1e-6)).all()
+
+
+def test_tq8_forward_backward_row_match_dense_products():
+    # q8_dot / q8_axpy / row (src/frozen.rs:80-108,113-177) against float64 products of the
+    # dequantised matrix, and the adjoint identity <dy, x W^T> = <dy W, x> (src/frozen.rs:218-227)
+    n, k, t = 48, 128, 5
+    w = O.Rng(1).vec_normal(n * k, 0.02).reshape(n, k)
+    b = O.quantize(O.TQ8_0, w)
+    sc, qs = _tq8_views(b, n, k)
+    W = (qs.astype(np.float64).reshape(n, k // 32, 32) * sc[:, :, None]).reshape(n, k)
+    x = O.Rng(2).vec_normal(t * k, 1.0).reshape(t, k)
+    dy = O.Rng(3).vec_normal(t * n, 1.0).reshape(t, n)
+    y = O.frozen_forward(O.TQ8_0, b, n, k, x)
+    assert np.abs(y - x.astype(np.float64) @ W.T).max() <= 1e-5 * np.abs(x @ W.T).max()
+    assert np.allclose(O.frozen_forward_f64(O.TQ8_0, b, n, k, x), x.astype(np.float64) @ W.T, rtol=1e-12, atol=1e-12)
+    dx = O.frozen_backward_input(O.TQ8_0, b, n, k, dy)
+    assert np.abs(dx - dy.astype(np.float64) @ W).max() <= 1e-5 * np.abs(dy @ W).max()
+    assert abs(float((dy * y).sum()) - float((dx * x).sum())) <= 1e-4 * float(np.abs(dy * y).sum())
+    for r in (0, 17, n - 1):
+        assert np.array_equal(O.frozen_row(O.TQ8_0, b, n, k, r), (np.float32(0) + sc[r].repeat(32) * qs[r].astype(np.float32)))

@@ -27,3 +27,15 @@ def test_quantisers_bit_identical(wtype):
     w[4, :256] = np.abs(w[4, :256])  # no negative values: min 0
     w[5, 256:] = -np.abs(w[5, 256:])  # no positive values
     assert np.array_equal(synth.QUANTIZERS[wtype](w), O.quantize(wtype, w))
+
+
+def test_trainer_q8_0_packing_matches_oracle():
+    # the product's FrozenWeight::q8_0 quantiser (rust_trainer_amd.pack_trainer_q8_0) against the
+    # oracle's, bit for bit, including halves (x / d = m + 0.5) and all-zero blocks
+    import rust_trainer_amd as rt
+
+    for seed, (n, k) in enumerate([(64, 128), (33, 256), (5, 32)]):
+        w = O.Rng(seed + 1).vec_normal(n * k, 0.02).reshape(n, k)
+        w[0, :6] = [1.0, 0.5 / 127, -0.5 / 127, 1.5 / 127, -2.5 / 127, 0.0]
+        w[1, :32] = 0.0
+        assert np.array_equal(rt.pack_trainer_q8_0(w, n, k), O.quantize(O.TQ8_0, w))
