@@ -30,6 +30,10 @@ FMT:SHAPE:T`` runs one of those cases (for a kernel trace of it).
 turns the two passes into HBM bytes per launch of each library kernel (each counter scaled so that
 the copies read and write 64 MiB), writes ``profiles/traffic_<kernel>_config1.json`` (read by the
 default run for ``roofline.traffic``) and prints a table.
+
+``--gguf-load PRESET[:WTYPE]`` builds a synthetic GGUF model (``SyntheticSpec``), writes it to a
+temporary file, maps and parses it and uploads every frozen tensor to the GPU, and prints one JSON
+line with the load throughput (frozen-tensor bytes over map + parse + upload time).
 """
 from __future__ import annotations
 
@@ -335,6 +339,61 @@ def cpu_baseline(inputs, seconds: float) -> dict:
                       f"C restatement of RieFrozen/Linear (oracle/rtq_oracle.c, -O3 AVX2, OpenMP)"}
 
 
+def gguf_load(arg: str) -> None:
+    """Load throughput of a synthetic GGUF model: write the file, map and parse it, upload every
+    frozen tensor (the loader's ``fz``, src/rie.rs:183, :218-231) with rtq_weight_from_gguf."""
+    import tempfile
+
+    import torch
+
+    import rust_trainer_amd as rt
+    from rust_trainer_amd import gguf as G
+
+    preset, _, wt = arg.partition(":")
+    spec = G.SyntheticSpec.preset(preset, G.GGML_NAMES[wt or "Q4_0"])
+    assert spec is not None, f"unknown preset {preset}; one of {list(G.SyntheticSpec.PRESETS)}"
+    t0 = time.perf_counter()
+    w = spec.writer()
+    build_s = time.perf_counter() - t0
+    print(f"[gguf-load] built {preset} in {build_s:.1f} s", file=sys.stderr, flush=True)
+    ctx = rt.Context(0)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "model.gguf")
+        t0 = time.perf_counter()
+        w.write(path)
+        write_s = time.perf_counter() - t0
+        w.close()
+        size = os.path.getsize(path)
+        t0 = time.perf_counter()
+        g = G.GgufFile.open(path)
+        open_s = time.perf_counter() - t0
+        frozen = [t for t in g.tensors() if not t.name.endswith("norm.weight")]
+        per_type: dict = {}
+        weights = []
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for t in frozen:
+            weights.append(rt.HipFrozen.from_gguf(g, t.name, ctx=ctx))
+            per_type[t.ty] = per_type.get(t.ty, 0) + t.nbytes
+        torch.cuda.synchronize()
+        upload_s = time.perf_counter() - t0
+        fbytes = sum(t.nbytes for t in frozen)
+        for x in weights:
+            x.close()
+        g.close()
+    ctx.close()
+    print(json.dumps({
+        "metric": "GGUF load: frozen-tensor bytes uploaded per second (map + parse + repack + host-to-device)",
+        "value": round(fbytes / (open_s + upload_s) / 1e9, 3), "unit": "GB/s", "higher_is_better": True,
+        "n_gpus": 1, "data": "synthetic",
+        "config": {"workload": f"SyntheticSpec::preset({preset}, {wt or 'Q4_0'}) (configs[2] shapes for qwen3-0.6b)",
+                   "file_bytes": size, "frozen_tensors": len(frozen), "frozen_bytes": fbytes,
+                   "bytes_by_type": {str(k): v for k, v in per_type.items()}},
+        "open_ms": round(open_s * 1e3, 3), "upload_ms": round(upload_s * 1e3, 1),
+        "write_GBps": round(size / write_s / 1e9, 3), "build_s": round(build_s, 1),
+    }), flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -348,6 +407,8 @@ def main() -> int:
     ap.add_argument("--calls", type=int, default=50, help="sweep: calls per timed graph (at least the sets)")
     ap.add_argument("--traffic", action="store_true", help="config-1 steps + calibration copies for --pmc passes")
     ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
+    ap.add_argument("--gguf-load", default=None, metavar="PRESET[:WTYPE]",
+                    help="GGUF load throughput of a synthetic model, e.g. qwen3-0.6b:Q4_0")
     args = ap.parse_args()
     if args.traffic_report:
         traffic_report(*args.traffic_report)
@@ -359,6 +420,9 @@ def main() -> int:
         return 2
     if args.traffic:
         traffic_run()
+        return 0
+    if args.gguf_load:
+        gguf_load(args.gguf_load)
         return 0
     if args.sweep or args.case:
         if args.case:

@@ -125,6 +125,54 @@ int64_t rtq_debug_isums_per_row(const rtq_weight* w);
  * (Q4_0/Q8_0: one per 32-block; Q4_K: (S1, S2) per super-block; Q6_K: S per super-block). */
 rtq_status rtq_debug_block_isums(rtq_ctx* ctx, const rtq_weight* w, const float* x, int64_t t, int32_t* out);
 
+/* ---- GGUF v3 container (rie_core::gguf::{GgufFile, GgufWriter}) ----
+ * Reader: GgufFile::open (src/rie.rs:159, :370) maps the file; GgufFile::from_bytes
+ * (tests/engine.rs:27-31, examples/bench_train.rs:28-32, tests/agentd.rs:14) borrows the caller's bytes, which must
+ * outlive the handle.  Every length and offset is checked against the image (RTQ_ERR_INVALID with
+ * a message otherwise).  Strings and tensor data point into the image; they are valid until close.
+ * Value types: u8 0, i8 1, u16 2, i16 3, u32 4, i32 5, f32 6, bool 7, string 8, array 9, u64 10,
+ * i64 11, f64 12.  Tensor dims ne[0] = row length (columns), ne[1..] = rows (n_rows/row_len). */
+typedef struct rtq_gguf rtq_gguf;
+typedef struct rtq_gguf_writer rtq_gguf_writer;
+rtq_status rtq_gguf_open(const char* path, rtq_gguf** out);
+rtq_status rtq_gguf_from_bytes(const void* data, size_t nbytes, rtq_gguf** out);
+void rtq_gguf_close(rtq_gguf* g);
+uint32_t rtq_gguf_version(const rtq_gguf* g);
+int64_t rtq_gguf_kv_count(const rtq_gguf* g);
+int64_t rtq_gguf_find_kv(const rtq_gguf* g, const char* key); /* -1 if absent */
+/* key i: type, array element type (-1 unless an array), count (array length / string bytes / 1),
+ * data (the value; arrays of strings: the first u64-length-prefixed element) */
+rtq_status rtq_gguf_kv(const rtq_gguf* g, int64_t i, const char** key, int* type, int* elem_type, uint64_t* count,
+                       const void** data);
+/* GgufFile::get_str (src/rie.rs:371-374): not NUL-terminated, length in *len */
+rtq_status rtq_gguf_get_str(const rtq_gguf* g, const char* key, const char** s, uint64_t* len);
+/* GgufFile::get_f32 / get_u32 (src/rie.rs:379): any numeric or bool value, widened to double */
+rtq_status rtq_gguf_get_f64(const rtq_gguf* g, const char* key, double* v);
+int64_t rtq_gguf_tensor_count(const rtq_gguf* g);
+int64_t rtq_gguf_find_tensor(const rtq_gguf* g, const char* name); /* GgufFile::tensor; -1 if absent */
+/* GgufFile::tensor + tensor_data (src/rie.rs:381-384): nbytes is 0 for a ggml type of unknown size */
+rtq_status rtq_gguf_tensor(const rtq_gguf* g, int64_t i, const char** name, int* type, int* n_dims, int64_t ne[4],
+                           const void** data, size_t* nbytes);
+/* Uploads a GGUF tensor as a frozen weight (the loader's `fz(ggml type, bytes, rows, cols)`,
+ * src/rie.rs:183-190): rows = ne[1]*ne[2]*ne[3], cols = ne[0]. */
+rtq_status rtq_weight_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, const char* name, rtq_weight** out);
+
+/* Writer (GgufWriter::new / kv / tensor / to_bytes, src/rie.rs:349-363).  Tensors are laid out in
+ * insertion order at general.alignment (default 32; set it as a u32 key before writing). */
+rtq_status rtq_gguf_writer_create(rtq_gguf_writer** out);
+void rtq_gguf_writer_destroy(rtq_gguf_writer* w);
+/* scalar: count 1, data -> the value; string (8): count bytes at data; array (9): count elements of
+ * elem_type at data (an array of strings: data is const char* const*, NUL-terminated strings) */
+rtq_status rtq_gguf_writer_kv(rtq_gguf_writer* w, const char* key, int type, int elem_type, uint64_t count,
+                              const void* data);
+/* nbytes must be the ggml size of ne[0]*...*ne[n_dims-1] elements of type */
+rtq_status rtq_gguf_writer_tensor(rtq_gguf_writer* w, const char* name, int type, int n_dims, const int64_t* ne,
+                                  const void* data, size_t nbytes);
+/* the image (to_bytes), owned by the writer until its next call or destroy */
+rtq_status rtq_gguf_writer_bytes(rtq_gguf_writer* w, const void** data, size_t* nbytes);
+/* the image written to path.tmp, then renamed to path (src/rie.rs:359-362) */
+rtq_status rtq_gguf_writer_write(rtq_gguf_writer* w, const char* path);
+
 #ifdef __cplusplus
 }
 #endif

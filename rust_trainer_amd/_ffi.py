@@ -64,6 +64,28 @@ SIGNATURES = {
     "rtq_debug_quantize_acts": (_i, [_p, _p, _p, _i64, _p]),
     "rtq_debug_isums_per_row": (_i64, [_p]),
     "rtq_debug_block_isums": (_i, [_p, _p, _p, _i64, _p]),
+    # GGUF v3 container
+    "rtq_gguf_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_p)]),
+    "rtq_gguf_from_bytes": (_i, [_p, _sz, ctypes.POINTER(_p)]),
+    "rtq_gguf_close": (None, [_p]),
+    "rtq_gguf_version": (ctypes.c_uint32, [_p]),
+    "rtq_gguf_kv_count": (_i64, [_p]),
+    "rtq_gguf_find_kv": (_i64, [_p, ctypes.c_char_p]),
+    "rtq_gguf_kv": (_i, [_p, _i64, ctypes.POINTER(_p), ctypes.POINTER(_i), ctypes.POINTER(_i),
+                         ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(_p)]),
+    "rtq_gguf_get_str": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(_p), ctypes.POINTER(ctypes.c_uint64)]),
+    "rtq_gguf_get_f64": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+    "rtq_gguf_tensor_count": (_i64, [_p]),
+    "rtq_gguf_find_tensor": (_i64, [_p, ctypes.c_char_p]),
+    "rtq_gguf_tensor": (_i, [_p, _i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i), ctypes.POINTER(_i),
+                             ctypes.POINTER(_i64), ctypes.POINTER(_p), ctypes.POINTER(_sz)]),
+    "rtq_weight_from_gguf": (_i, [_p, _p, ctypes.c_char_p, ctypes.POINTER(_p)]),
+    "rtq_gguf_writer_create": (_i, [ctypes.POINTER(_p)]),
+    "rtq_gguf_writer_destroy": (None, [_p]),
+    "rtq_gguf_writer_kv": (_i, [_p, ctypes.c_char_p, _i, _i, ctypes.c_uint64, _p]),
+    "rtq_gguf_writer_tensor": (_i, [_p, ctypes.c_char_p, _i, _i, ctypes.POINTER(_i64), _p, _sz]),
+    "rtq_gguf_writer_bytes": (_i, [_p, ctypes.POINTER(_p), ctypes.POINTER(_sz)]),
+    "rtq_gguf_writer_write": (_i, [_p, ctypes.c_char_p]),
 }
 
 _LIB = None

@@ -465,7 +465,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
     const GemvPlan gp = gemv_plan(c, w);
     const float gbias = w->type == RTQ_TYPE_Q4_0 ? 1032.0f : (w->type == RTQ_TYPE_Q8_0 ? 1152.0f : 0.0f);
     ActArgs aa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xq, xd, xg, gbias, lora ? la : nullptr, (int)r, hp,
-               gp.gy > 1 ? y : nullptr, (int)w->rows};
+               gp.gy > 1 ? y : nullptr, (int)w->rows, nullptr};
     RTQ_TRY(launch(c, is_kquant(w->type) ? K_ACT_PREP_K : K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp),
                    dim3(256), st, aa));
     FwdArgs fa{};
@@ -784,6 +784,17 @@ void repack_kquant(int type, const uint8_t* src, int64_t N, int64_t K, int64_t N
 }
 
 }  // namespace
+
+// error reporting shared with the other translation units of the library (rtq_gguf.cpp)
+rtq_status rtq_fail(rtq_status st, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return st;
+}
 
 // ====================================================================== C ABI
 extern "C" {
@@ -1257,7 +1268,7 @@ rtq_status rtq_debug_quantize_acts(rtq_ctx* c, const rtq_weight* w, const float*
   float* xs = ar.take<float>(p.xd_floats);
   RTQ_TRY(h2d(xdv, x, (size_t)(t * K) * 4, st));
   const bool kq = is_kquant(w->type);
-  ActArgs aa{xdv, (int)t, (int)K, (int)p.Tp, (int)w->Kp, xq, xs, nullptr, 0.0f, nullptr, 0, nullptr, nullptr, 0};
+  ActArgs aa{xdv, (int)t, (int)K, (int)p.Tp, (int)w->Kp, xq, xs, nullptr, 0.0f, nullptr, 0, nullptr, nullptr, 0, nullptr};
   RTQ_TRY(launch(c, kq ? K_ACT_PREP_K : K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp), dim3(256), st, aa));
   std::vector<uint8_t> hq(p.xq_bytes);
   std::vector<float> hs(p.xd_floats);

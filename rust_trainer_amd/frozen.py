@@ -173,6 +173,20 @@ class HipFrozen(FrozenMatmul):
             return cls.f32(w, out, inp, ctx=ctx)
         return cls(_ffi.TYPE_TQ8_0, pack_trainer_q8_0(w, out, inp), out, inp, ctx=ctx)
 
+    @classmethod
+    def from_gguf(cls, file, name: str, ctx: Context | None = None) -> "HipFrozen":
+        """Uploads GGUF tensor ``name`` of an open ``gguf.GgufFile`` straight from the mapped
+        image (the loader's ``fz(&l.wq)``, src/rie.rs:183, :218-231)."""
+        t = file.tensor(name)
+        assert t is not None, f"no tensor {name}"
+        self = cls.__new__(cls)
+        self.ctx = ctx or default_context()
+        h = ctypes.c_void_p()
+        _ffi.check(_ffi.lib().rtq_weight_from_gguf(self.ctx.handle, file.handle, name.encode(), ctypes.byref(h)),
+                   "rtq_weight_from_gguf")
+        self._adopt(h, t.ty, t.n_rows(), t.row_len())
+        return self
+
     def __init__(self, ggml_type: int, blocks, rows: int, cols: int, ctx: Context | None = None):
         self.ctx = ctx or default_context()
         arr = np.ascontiguousarray(blocks)
@@ -180,6 +194,9 @@ class HipFrozen(FrozenMatmul):
         h = ctypes.c_void_p()
         _ffi.check(_ffi.lib().rtq_weight_create(self.ctx.handle, ggml_type, b.ctypes.data, b.nbytes, rows, cols,
                                                 ctypes.byref(h)), "rtq_weight_create")
+        self._adopt(h, ggml_type, rows, cols)
+
+    def _adopt(self, h: ctypes.c_void_p, ggml_type: int, rows: int, cols: int) -> None:
         self._h = h
         self.ggml_type = ggml_type
         self._rows, self._cols = rows, cols
