@@ -31,6 +31,10 @@ turns the two passes into HBM bytes per launch of each library kernel (each coun
 the copies read and write 64 MiB), writes ``profiles/traffic_<kernel>_config1.json`` (read by the
 default run for ``roofline.traffic``) and prints a table.
 
+``--head`` measures the LM head + cross-entropy of configs[2] (``Model::head``: tied Q4_0 head
+151936 x 1024, 512 positions, loss on the last 256) through ``rtq_lm_head_d``, one JSON line with
+the per-call time, per-kernel times, the softmax kernels' HBM fraction and the CPU oracle's rate.
+
 ``--gguf-load PRESET[:WTYPE]`` builds a synthetic GGUF model (``SyntheticSpec``), writes it to a
 temporary file, maps and parses it and uploads every frozen tensor to the GPU, and prints one JSON
 line with the load throughput (frozen-tensor bytes over map + parse + upload time).
@@ -339,6 +343,110 @@ def cpu_baseline(inputs, seconds: float) -> dict:
                       f"C restatement of RieFrozen/Linear (oracle/rtq_oracle.c, -O3 AVX2, OpenMP)"}
 
 
+# ---------------------------------------------------------------- LM head + cross-entropy
+HEAD_V, HEAD_D, HEAD_T, HEAD_N = 151936, 1024, 512, 256
+
+
+def head_bench(steps: int, warmup: int, cpu_seconds: float, no_cpu: bool) -> None:
+    """Model::head of configs[2]: Qwen3-0.6B tied LM head (Q4_0 151936 x 1024), 512 positions,
+    cross-entropy on the last 256 (answer_targets), weights 1/256; one call = final RMSNorm +
+    logits + log-softmax + dlogits + lm_head backward_input + RMSNorm backward (rtq_lm_head_d)."""
+    import numpy as np
+    import torch
+
+    import rust_trainer_amd as rt
+    from rust_trainer_amd import _ffi, synth
+
+    V, D, T_, N_ = HEAD_V, HEAD_D, HEAD_T, HEAD_N
+    blocks = synth.quantize_q4_0(synth.Rng(1).vec_normal(V * D, 0.02).reshape(V, D))
+    X = synth.Rng(2).vec_normal(T_ * D, 1.0).reshape(T_, D)
+    tokens = (synth.Rng(3).next_u64(T_) % np.uint64(V)).astype(np.int32)
+    targets = rt.answer_targets(tokens, T_ - N_)
+    pos = np.array([tg.pos for tg in targets], np.int32)
+    tok = np.array([tg.token for tg in targets], np.int32)
+    wts = np.full(N_, 1.0 / N_, np.float32)
+    norm = np.ones(D, np.float32)
+    dev = torch.device("cuda", 0)
+    ctx = rt.Context(0)
+    f = rt.HipFrozen(rt.TYPE_Q4_0, blocks, V, D, ctx=ctx)
+    xd, nd = torch.from_numpy(X).to(dev), torch.from_numpy(norm).to(dev)
+    pd, kd, wd = (torch.from_numpy(a).to(dev) for a in (pos, tok, wts))
+    lp = torch.empty(N_, device=dev)
+    hit = torch.empty(N_, dtype=torch.int32, device=dev)
+    dx = torch.empty(T_, D, device=dev)
+    L = _ffi.lib()
+    side = torch.cuda.Stream()
+
+    def call(st: int) -> None:
+        _ffi.check(L.rtq_lm_head_d(ctx.handle, f.handle, nd.data_ptr(), 1e-6, 0.0, xd.data_ptr(), T_, pd.data_ptr(),
+                                   kd.data_ptr(), wd.data_ptr(), N_, lp.data_ptr(), hit.data_ptr(), dx.data_ptr(),
+                                   st), "rtq_lm_head_d")
+
+    def eager(k: int) -> None:
+        with torch.cuda.stream(side):
+            st = torch.cuda.current_stream().cuda_stream
+            for _ in range(k):
+                call(st)
+        torch.cuda.synchronize()
+
+    eager(warmup)
+    ctx.set_timing(True)
+    ctx.reset_timing()
+    eager(steps)
+    per = ctx.timing()
+    ctx.set_timing(False)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        st = torch.cuda.current_stream().cuda_stream
+        for _ in range(steps):
+            call(st)
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    logits_bytes = N_ * V * 4
+    ce = [k for k in per if k.startswith("rtq_head_") and k != "rtq_head_norm" and k != "rtq_head_norm_bwd"]
+    ce_ms = sum(per[k][1] / per[k][0] for k in ce)
+    ce_bytes = 4 * logits_bytes  # max, sum and grad read the logits, grad writes dlogits over them
+    wbytes = V * D // 32 * 18
+    bytes_, flops = 2 * wbytes + (T_ * D + 2 * N_ * D) * 4 + T_ * D * 4, 4.0 * N_ * V * D
+    result = {
+        "metric": "LM head + cross-entropy fwd+bwd (Model::head), targets/s", "value": round(N_ / (ms * 1e-3), 1),
+        "unit": "targets/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "data": "synthetic",
+        "dtype": "int8 x int4 block dots -> f32 (logits); f32 / f64 softmax; bf16x3 -> f32 (dlogits . W)",
+        "config": {"workload": "configs[2] head: tied LM head Q4_0 151936x1024, 512 positions, loss on the "
+                               "last 256 (answer_targets), weights 1/256",
+                   "vocab": V, "hidden": D, "positions": T_, "targets": N_},
+        "call_roofline": call_roofline(bytes_, flops, ms * 1e-3),
+        "softmax_roofline": {"bound": "hbm", "achieved": round(ce_bytes / (ce_ms * 1e-3) / 1e9, 1),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(ce_bytes / (ce_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "kernels": ce, "algorithmic_bytes": ce_bytes},
+        "kernels": {k: {"avg_us": round(m * 1e3 / c, 3), "launches": c} for k, (c, m) in sorted(per.items())},
+    }
+    if not no_cpu:
+        import oracle as O
+
+        threads = max(1, min(16, os.cpu_count() or 1))
+        n_s, calls, t0 = 16, 0, time.perf_counter()
+        while True:
+            O.lm_head(O.Q4_0, blocks, V, D, norm, X, pos[:n_s], tok[:n_s], wts[:n_s], nthreads=threads)
+            calls += 1
+            el = time.perf_counter() - t0
+            if el >= cpu_seconds:
+                break
+        result["cpu_baseline"] = {"value": round(n_s * calls / el, 1), "unit": "targets/s", "cores": threads,
+                                  "kind": "port",
+                                  "sample": f"{calls} calls of Model::head on {n_s} targets in {el:.1f} s "
+                                            f"(oracle/rtq_oracle.c or_lm_head, -O3 AVX2, OpenMP)"}
+    f.close()
+    ctx.close()
+    print(json.dumps(result), flush=True)
+
+
 def gguf_load(arg: str) -> None:
     """Load throughput of a synthetic GGUF model: write the file, map and parse it, upload every
     frozen tensor (the loader's ``fz``, src/rie.rs:183, :218-231) with rtq_weight_from_gguf."""
@@ -407,6 +515,7 @@ def main() -> int:
     ap.add_argument("--calls", type=int, default=50, help="sweep: calls per timed graph (at least the sets)")
     ap.add_argument("--traffic", action="store_true", help="config-1 steps + calibration copies for --pmc passes")
     ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
+    ap.add_argument("--head", action="store_true", help="configs[2] LM head + cross-entropy (Model::head)")
     ap.add_argument("--gguf-load", default=None, metavar="PRESET[:WTYPE]",
                     help="GGUF load throughput of a synthetic model, e.g. qwen3-0.6b:Q4_0")
     args = ap.parse_args()
@@ -423,6 +532,9 @@ def main() -> int:
         return 0
     if args.gguf_load:
         gguf_load(args.gguf_load)
+        return 0
+    if args.head:
+        head_bench(args.steps, args.warmup, args.cpu_seconds, args.no_cpu)
         return 0
     if args.sweep or args.case:
         if args.case:

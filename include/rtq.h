@@ -116,6 +116,28 @@ rtq_status rtq_linear_forward_d(rtq_ctx* ctx, const rtq_weight* w, const float* 
 rtq_status rtq_linear_backward_d(rtq_ctx* ctx, const rtq_weight* w, const rtq_lora* lora, const float* x,
                                  const float* dy, int64_t t, float* dx, float* ga, float* gb, void* stream);
 
+/* ---- embedding gather and LM head + cross-entropy ---- */
+/* embed_tokens (src/model.rs:446-454): out[i x in] = row(ids[i]).  Host version: ids out of range are
+ * rejected (the reference asserts, :450); device version: such rows come out NaN, nothing is read. */
+rtq_status rtq_frozen_gather(rtq_ctx* ctx, const rtq_weight* w, const int32_t* ids, int64_t count, float* out);
+rtq_status rtq_frozen_gather_d(rtq_ctx* ctx, const rtq_weight* w, const int32_t* ids, int64_t count, float* out,
+                               void* stream);
+/* Model::head (src/model.rs:561-609) for n targets (pos[i] < t, tok[i] < vocab = lm_head rows):
+ * ns = rmsnorm(x[pos], norm_w, eps, offset) (src/ops.rs:14-36), logits = lm_head.forward(ns),
+ * softmax_row with an f64 normaliser (src/ops.rs:238-247), logp[i] = logit[tok] - lse, a hit when
+ * the target's logit is >= every logit.  With weights (else NULL, and dx unused): for
+ * L = -sum weights[i] logp[i], dx[t x d] = dL/dx, OVERWRITTEN (zero outside target rows;
+ * targets sharing a position add in target order).  All targets are processed in one pass (the
+ * reference's 64-target chunks bound its memory; here the workspace holds n x vocab logits).
+ * Host version: *hits = number of hits, targets out of range rejected.  Device version: hit[i]
+ * per target (0 / 1); a target out of range reads nothing and gets logp NaN, hit 0, no gradient. */
+rtq_status rtq_lm_head(rtq_ctx* ctx, const rtq_weight* lm_head, const float* norm_w, float eps, float offset,
+                       const float* x, int64_t t, const int32_t* pos, const int32_t* tok, const float* weights,
+                       int64_t n, float* logp, int64_t* hits, float* dx);
+rtq_status rtq_lm_head_d(rtq_ctx* ctx, const rtq_weight* lm_head, const float* norm_w, float eps, float offset,
+                         const float* x, int64_t t, const int32_t* pos, const int32_t* tok, const float* weights,
+                         int64_t n, float* logp, int32_t* hit, float* dx, void* stream);
+
 /* ---- parity / debug (host pointers, synchronous) ---- */
 /* The activation blocks the GPU forward actually uses for x, in ggml layout (block_q8_0: 34 B per
  * 32 elements for Q4_0/Q8_0 weights; block_q8_K: 292 B per 256 for Q4_K/Q6_K), t * act_row_bytes. */

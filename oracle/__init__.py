@@ -76,6 +76,7 @@ def lib() -> ctypes.CDLL:
             "or_matmul_tn_acc": (None, [_p, _p, _p, _i64, _i64, _i64, _i]),
             "or_linear_forward": (_i, [_i, _p, _i64, _i64, _p, _i64, _f, _p, _p, _i, _p, _i64, _p, _i]),
             "or_linear_backward": (_i, [_i, _p, _i64, _i64, _i64, _f, _p, _p, _i, _p, _p, _i64, _p, _p, _p, _i]),
+            "or_lm_head": (_i, [_i, _p, _i64, _i64, _p, _f, _f, _p, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -286,3 +287,19 @@ def linear_backward(wtype, wblocks, n, k, x, dy, A=None, B=None, alpha=0.0, ga=N
                                     int(lora_enabled), _ptr(x), _ptr(dy), t, _ptr(dx), _ptr(ga), _ptr(gb), nthreads),
            "linear_backward")
     return dx, ga, gb
+
+
+def lm_head(wtype, wblocks, V, d, norm, x, pos, tok, wts=None, eps=1e-6, off=0.0, chunk=64, nthreads=1):
+    """Model::head (src/model.rs:561-609): returns (logp [n], hits, dx [t x d] or None)."""
+    x = _f32(x).reshape(-1, d)
+    t = x.shape[0]
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    tok = np.ascontiguousarray(tok, dtype=np.int32)
+    n = pos.size
+    logp = np.empty(n, np.float32)
+    hits = ctypes.c_int64()
+    dx = np.empty((t, d), np.float32) if wts is not None else None
+    _check(lib().or_lm_head(wtype, _ptr(np.ascontiguousarray(wblocks)), V, d, _ptr(_f32(norm)), eps, off, _ptr(x), t,
+                            _ptr(pos), _ptr(tok), _ptr(None if wts is None else _f32(wts)), n, chunk, _ptr(logp),
+                            ctypes.byref(hits), _ptr(dx), nthreads), "lm_head")
+    return logp, hits.value, dx

@@ -922,3 +922,91 @@ int or_linear_backward(int wtype, const void* w, int64_t n, int64_t k, int64_t r
   }
   return 0;
 }
+
+/* ---- LM head + cross-entropy: Model::head (src/model.rs:561-609) ---- */
+
+/* rmsnorm (src/ops.rs:14-36, fused_scale = false): y = (x * ir) * (w + off), ir = 1 / sqrt(dot(x, x) / d + eps) */
+static void head_rmsnorm(const float* x, const float* w, int64_t d, float eps, float off, float* y, float* inv) {
+  const float ms = or_dot(x, x, d) / (float)d;
+  const float ir = 1.0f / sqrtf(ms + eps);
+  *inv = ir;
+  for (int64_t i = 0; i < d; i++) y[i] = x[i] * ir * (w[i] + off);
+}
+
+/* softmax_row (src/ops.rs:238-247): p = exp(v - max) in f32, normaliser summed in f64, p *= (f32)(1/s);
+ * returns lse = max + (f32)ln(s) */
+static float head_softmax_row(const float* row, int64_t v, float* p) {
+  float m = -INFINITY;
+  for (int64_t j = 0; j < v; j++) m = fmaxf(m, row[j]);
+  double s = 0.0;
+  for (int64_t j = 0; j < v; j++) {
+    p[j] = expf(row[j] - m);
+    s += (double)p[j];
+  }
+  const float inv = (float)(1.0 / s);
+  for (int64_t j = 0; j < v; j++) p[j] *= inv;
+  return m + (float)log(s);
+}
+
+int or_lm_head(int wtype, const void* w, int64_t V, int64_t d, const float* norm, float eps, float off,
+               const float* x, int64_t t, const int32_t* pos, const int32_t* tok, const float* wts, int64_t n,
+               int64_t chunk, float* logp, int64_t* hits, float* dx, int nthreads) {
+  if (chunk < 1) chunk = 1;
+  for (int64_t i = 0; i < n; i++)
+    if (pos[i] < 0 || pos[i] >= t || tok[i] < 0 || tok[i] >= V) return -1; /* src/model.rs:575 assert */
+  if (wts && dx) memset(dx, 0, (size_t)(t * d) * 4);
+  int64_t nh = 0;
+  float* xs = (float*)malloc((size_t)(chunk * d) * 4);
+  float* ns = (float*)malloc((size_t)(chunk * d) * 4);
+  float* inv = (float*)malloc((size_t)chunk * 4);
+  float* logits = (float*)malloc((size_t)(chunk * V) * 4);
+  float* p = (float*)malloc((size_t)V * 4);
+  float* dns = (float*)malloc((size_t)(chunk * d) * 4);
+  float* g = (float*)malloc((size_t)d * 4);
+  int rc = 0;
+  for (int64_t c0 = 0; c0 < n && !rc; c0 += chunk) {
+    const int64_t m = n - c0 < chunk ? n - c0 : chunk;
+    for (int64_t i = 0; i < m; i++) {
+      memcpy(xs + i * d, x + (int64_t)pos[c0 + i] * d, (size_t)d * 4);
+      head_rmsnorm(xs + i * d, norm, d, eps, off, ns + i * d, inv + i);
+    }
+    rc = or_frozen_forward(wtype, w, V, d, ns, m, logits, nthreads);
+    if (rc) break;
+    for (int64_t i = 0; i < m; i++) {
+      float* row = logits + i * V;
+      const float lse = head_softmax_row(row, V, p);
+      const float tl = row[tok[c0 + i]];
+      logp[c0 + i] = tl - lse;
+      int all = 1;
+      for (int64_t j = 0; j < V && all; j++) all = row[j] <= tl;
+      nh += all;
+      if (wts) { /* d(-w logp)/dlogits = w (softmax - onehot), written over the logits */
+        const float wi = wts[c0 + i];
+        for (int64_t j = 0; j < V; j++) row[j] = wi * p[j];
+        row[tok[c0 + i]] -= wi;
+      }
+    }
+    if (wts && dx) {
+      memset(dns, 0, (size_t)(m * d) * 4);
+      rc = or_frozen_backward_input(wtype, w, V, d, logits, m, dns, nthreads);
+      if (rc) break;
+      for (int64_t i = 0; i < m; i++) { /* rmsnorm_backward (src/ops.rs:39-56), then dx[pos] += dxs */
+        const float* xr = xs + i * d;
+        const float ir = inv[i];
+        for (int64_t k = 0; k < d; k++) g[k] = dns[i * d + k] * (norm[k] + off);
+        const float cc = or_dot(g, xr, d) * ir * ir * ir / (float)d;
+        float* o = dx + (int64_t)pos[c0 + i] * d;
+        for (int64_t k = 0; k < d; k++) o[k] += g[k] * ir - xr[k] * cc;
+      }
+    }
+  }
+  if (hits) *hits = nh;
+  free(xs);
+  free(ns);
+  free(inv);
+  free(logits);
+  free(p);
+  free(dns);
+  free(g);
+  return rc;
+}

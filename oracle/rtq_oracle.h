@@ -13,6 +13,7 @@
  *   src/linear.rs:73-121    Linear::forward / Linear::backward (LoRA order)
  *   src/tensor.rs:24-120    dot / axpy / matmul_nt / matmul_nn / matmul_tn_acc
  *   src/tensor.rs:155-199   Rng (SplitMix64 + Box-Muller)
+ *   src/model.rs:561-609    Model::head (final RMSNorm, LM head, log-softmax, dlogits, RMSNorm backward)
  *   ggml block formats Q4_0, Q8_0, Q4_K, Q6_K and activation blocks Q8_0 / Q8_K; rie-core
  *   (git dependency pinned at f3be365b41f929cc81ee08afaa994d02bbeee2f5, Cargo.lock:529-540,
  *   absent from the container) follows ggml's public block semantics for these formats.
@@ -106,6 +107,16 @@ int or_linear_backward(int wtype, const void* w, int64_t n, int64_t k, int64_t r
                        const float* A, const float* B, int lora_enabled, const float* x, const float* dy,
                        int64_t t, float* dx, float* ga, float* gb, int nthreads);
 
+/* ---- LM head + cross-entropy: Model::head (src/model.rs:561-609) ----
+ * For targets i (positions pos[i] into x [t x d], tokens tok[i] < V), in chunks of `chunk` targets:
+ * RMSNorm of the target rows (src/ops.rs:14-36), logits = lm_head.forward, softmax_row with an f64
+ * normaliser (src/ops.rs:238-247); logp[i] = logit[tok] - lse; *hits = number of targets whose
+ * logit is >= every logit.  With wts: dlogits = wts[i] (softmax - onehot), dns = lm_head
+ * backward_input, dx (overwritten, [t x d]) += rmsnorm_backward (src/ops.rs:39-56) at pos[i].
+ * Returns -1 on a target out of range (the reference asserts). */
+int or_lm_head(int wtype, const void* w, int64_t V, int64_t d, const float* norm, float eps, float off,
+               const float* x, int64_t t, const int32_t* pos, const int32_t* tok, const float* wts, int64_t n,
+               int64_t chunk, float* logp, int64_t* hits, float* dx, int nthreads);
 #ifdef __cplusplus
 }
 #endif

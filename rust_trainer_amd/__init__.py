@@ -9,8 +9,9 @@ This package is the host-side mirror of the reference's plugin interface (``Froz
 from ._ffi import RtqError, TYPE_F32, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, TYPE_TQ8_0, lib  # noqa: F401
 from .frozen import Context, FrozenMatmul, HipFrozen, default_context, pack_trainer_q8_0  # noqa: F401
 from .gguf import GgufFile, GgufWriter, SyntheticSpec, Value  # noqa: F401
+from .head import Target, answer_targets, embed_tokens, head  # noqa: F401
 from .linear import Linear, Lora  # noqa: F401
 
 __all__ = ["Context", "FrozenMatmul", "HipFrozen", "Linear", "Lora", "RtqError", "default_context", "lib",
            "TYPE_Q4_0", "TYPE_Q8_0", "TYPE_Q4_K", "TYPE_Q6_K", "TYPE_F32", "TYPE_TQ8_0", "pack_trainer_q8_0",
-           "GgufFile", "GgufWriter", "SyntheticSpec", "Value"]
+           "GgufFile", "GgufWriter", "SyntheticSpec", "Value", "Target", "answer_targets", "embed_tokens", "head"]

@@ -64,6 +64,10 @@ SIGNATURES = {
     "rtq_debug_quantize_acts": (_i, [_p, _p, _p, _i64, _p]),
     "rtq_debug_isums_per_row": (_i64, [_p]),
     "rtq_debug_block_isums": (_i, [_p, _p, _p, _i64, _p]),
+    "rtq_frozen_gather": (_i, [_p, _p, _p, _i64, _p]),
+    "rtq_frozen_gather_d": (_i, [_p, _p, _p, _i64, _p, _p]),
+    "rtq_lm_head": (_i, [_p, _p, _p, _f, _f, _p, _i64, _p, _p, _p, _i64, _p, ctypes.POINTER(_i64), _p]),
+    "rtq_lm_head_d": (_i, [_p, _p, _p, _f, _f, _p, _i64, _p, _p, _p, _i64, _p, _p, _p, _p]),
     # GGUF v3 container
     "rtq_gguf_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_p)]),
     "rtq_gguf_from_bytes": (_i, [_p, _sz, ctypes.POINTER(_p)]),

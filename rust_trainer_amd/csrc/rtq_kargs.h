@@ -86,6 +86,7 @@ struct DenseArgs {
   int64_t r0, count;  // rows [r0, r0 + count) (dequant / row copy); bias: count = T
   float* out;         // [count][K]; bias: y [T][N]
   const float* bias;
+  const int32_t* idx;  // or null: out row i is weight row idx[i] (embedding gather), else r0 + i
 };
 
 // ---------------------------------------------------------------- forward GEMM
@@ -179,10 +180,36 @@ struct RowArgs {
   const uint32_t* wsb;
   int Np, Kp, K;
   int r0, count;
-  float* out;  // [count x K]
+  float* out;          // [count x K]
+  const int32_t* idx;  // or null: row i of out is weight row idx[i] (embedding gather), else r0 + i
+  int rows;            // weight rows (bound of idx)
 };
 
 struct FillArgs {
   float* p;
   int64_t n;
+};
+
+// ---------------------------------------------------------------- LM head + cross-entropy
+// Model::head (src/model.rs:561-609): final RMSNorm of the target rows, log-softmax with an f64
+// normaliser (softmax_row, src/ops.rs:238-247), dlogits = w (softmax - onehot), and the RMSNorm
+// backward (src/ops.rs:39-56) of dlogits . W, added into dx at the target positions.
+struct HeadArgs {
+  const float* x;      // [t x d] final hidden states
+  const int32_t* pos;  // [n] target positions
+  const int32_t* tok;  // [n] target tokens
+  const float* wts;    // [n] loss weights, or null (log-probs only)
+  const float* norm;   // [d] final norm weight
+  float eps, off;
+  int t, d, n, V;
+  int G, L;            // vocabulary slices per row (grid x of the softmax kernels) and slice length
+  float* ns;           // [n x d] normalised target rows (the lm_head input)
+  float* inv;          // [n] 1 / rms
+  float* logits;       // [n x V] logits; overwritten by dlogits when wts
+  float* pmax;         // [n x G] slice maxima
+  double* psum;        // [n x G] slice sums of exp(v - max)
+  float* logp;         // [n]
+  int32_t* hit;        // [n] 1 if the target's logit is >= every logit of its row
+  const float* dns;    // [n x d] dlogits . W (lm_head backward_input)
+  float* dx;           // [t x d] dL/dx (rows without a target are cleared separately)
 };

@@ -1988,7 +1988,15 @@ extern "C" __global__ __launch_bounds__(1024) void rtq_bwd_finish16(LoraGradArgs
 extern "C" __global__ __launch_bounds__(256) void rtq_dense_rows(DenseArgs a) {
   const int64_t n = a.count * a.K;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int64_t r = a.r0 + i / a.K, k = i % a.K;
+    const int64_t k = i % a.K;
+    int64_t r = a.r0 + i / a.K;
+    if (a.idx) {
+      r = a.idx[i / a.K];
+      if (r < 0 || r >= a.N) {  // out-of-range id: NaN row, nothing read
+        a.out[i] = __builtin_nanf("");
+        continue;
+      }
+    }
     if (a.w)
       a.out[i] = a.w[r * a.K + k];
     else
@@ -2004,13 +2012,28 @@ extern "C" __global__ __launch_bounds__(256) void rtq_dense_bias(DenseArgs a) {
 }
 
 // ============================================================== row dequant (FrozenMatmul::row)
+// embedding gather: weight row of out row rl; an id outside [0, rows) gives a NaN block, nothing read
+__device__ __forceinline__ bool gather_row(const RowArgs& a, int rl, int b, int* n) {
+  const int r = a.idx[rl];
+  if (r >= 0 && r < a.rows) {
+    *n = r;
+    return true;
+  }
+  float* out = a.out + (int64_t)rl * a.K + b * 32;
+#pragma unroll
+  for (int e = 0; e < 32; e++) out[e] = __builtin_nanf("");
+  return false;
+}
+
 // One thread per (row, 32-element block); bit-exact ggml dequant: (q - 8) * d, q * d.
 extern "C" __global__ __launch_bounds__(256) void rtq_rows_q4_0(RowArgs a) {
   const int nb = a.K / 32, Kc = a.Kp / 128;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)a.count * nb) return;
   const int rl = (int)(idx / nb), b = (int)(idx % nb);
-  const int n = a.r0 + rl, rg = n >> 4, li = n & 15, kc = b >> 2, j = b & 3;
+  int n = a.r0 + rl;
+  if (a.idx && !gather_row(a, rl, b, &n)) return;
+  const int rg = n >> 4, li = n & 15, kc = b >> 2, j = b & 3;
   const u4v* q = reinterpret_cast<const u4v*>(a.wq) + (int64_t)(rg * Kc + kc) * 64;
   const float d = h2f(a.wd[RTQ_WD_INDEX(rg, kc, Kc, li, j)]);
   float* out = a.out + (int64_t)rl * a.K + b * 32;
@@ -2031,7 +2054,9 @@ extern "C" __global__ __launch_bounds__(256) void rtq_rows_q8_0(RowArgs a) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)a.count * nb) return;
   const int rl = (int)(idx / nb), b = (int)(idx % nb);
-  const int n = a.r0 + rl, rg = n >> 4, li = n & 15, kc = b >> 2, j = b & 3;
+  int n = a.r0 + rl;
+  if (a.idx && !gather_row(a, rl, b, &n)) return;
+  const int rg = n >> 4, li = n & 15, kc = b >> 2, j = b & 3;
   const u4v* q = reinterpret_cast<const u4v*>(a.wq) + (int64_t)(rg * Kc + kc) * 128 + (j >> 1) * 64;
   const float d = h2f(a.wd[RTQ_WD_INDEX(rg, kc, Kc, li, j)]);
   float* out = a.out + (int64_t)rl * a.K + b * 32;
@@ -2056,7 +2081,9 @@ __device__ __forceinline__ void rows_kquant(const RowArgs& a) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)a.count * nb) return;
   const int rl = (int)(idx / nb), b = (int)(idx % nb);
-  const int n = a.r0 + rl, rg = n >> 4, li = n & 15, kc = b >> 2, j = b & 3;
+  int n = a.r0 + rl;
+  if (a.idx && !gather_row(a, rl, b, &n)) return;
+  const int rg = n >> 4, li = n & 15, kc = b >> 2, j = b & 3;
   const uint32_t kw = a.wd[RTQ_WR_INDEX(rg, kc, Kc, li, j)];
   const uint32_t ev = a.wsb[RTQ_WSB_INDEX(rg, kc >> 1, Kc >> 1, li)];
   const float dsb = h2f((uint16_t)(ev & 0xffffu));
@@ -2094,3 +2121,180 @@ __device__ __forceinline__ void rows_kquant(const RowArgs& a) {
 
 extern "C" __global__ __launch_bounds__(256) void rtq_rows_q4_k(RowArgs a) { rows_kquant<FMT_Q4_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_rows_q6_k(RowArgs a) { rows_kquant<FMT_Q6_K>(a); }
+
+// ============================================================== LM head + cross-entropy
+// Model::head (src/model.rs:561-609) for all targets at once: rtq_head_norm (gather + RMSNorm),
+// the lm_head forward (the kernels above), rtq_head_max / _sum / _grad over G vocabulary slices per
+// row (softmax_row, src/ops.rs:238-247: p = exp(v - max) in f32, normaliser summed in f64, the
+// gradient w (p / s - onehot) written over the logits), the lm_head backward_input, and
+// rtq_head_norm_bwd (rmsnorm_backward, src/ops.rs:39-56, added into dx at the target positions).
+// A target outside [0, t) x [0, V) reads nothing: its normalised row is 0, logp NaN, gradient 0.
+
+__device__ __forceinline__ bool head_target_ok(const HeadArgs& a, int i) {
+  const int p = a.pos[i], k = a.tok[i];
+  return p >= 0 && p < a.t && k >= 0 && k < a.V;
+}
+
+// sum over the 256 threads of a workgroup; every thread gets the same value
+template <class T>
+__device__ __forceinline__ T block_sum256(T v, T* red) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  __syncthreads();  // red may still be read from a previous call
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__device__ __forceinline__ float block_max256(float v, float* red) {
+  v = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// calls f(j, logit) for every element j of slice g of row i (float4 loads when rows are 16 B aligned)
+template <class F>
+__device__ __forceinline__ void head_slice(const HeadArgs& a, const float* row, int j0, int j1, F&& f) {
+  if ((a.V & 3) == 0) {
+    const f4* r4 = reinterpret_cast<const f4*>(row);
+    for (int q = j0 / 4 + (int)threadIdx.x; q < j1 / 4; q += 256) {
+      const f4 v = r4[q];
+      f(4 * q, v[0]);
+      f(4 * q + 1, v[1]);
+      f(4 * q + 2, v[2]);
+      f(4 * q + 3, v[3]);
+    }
+  } else {
+    for (int j = j0 + (int)threadIdx.x; j < j1; j += 256) f(j, row[j]);
+  }
+}
+
+// grid n: ns[i] = (x[pos[i]] * ir) * (norm + off), ir = 1 / sqrt(dot(x, x) / d + eps)
+extern "C" __global__ __launch_bounds__(256) void rtq_head_norm(HeadArgs a) {
+  __shared__ float red[4];
+  const int i = blockIdx.x;
+  float* out = a.ns + (int64_t)i * a.d;
+  if (!head_target_ok(a, i)) {
+    for (int k = threadIdx.x; k < a.d; k += 256) out[k] = 0.0f;
+    if (threadIdx.x == 0) a.inv[i] = 0.0f;
+    return;
+  }
+  const float* xr = a.x + (int64_t)a.pos[i] * a.d;
+  float s = 0.0f;
+  for (int k = threadIdx.x; k < a.d; k += 256) s = s + xr[k] * xr[k];
+  s = block_sum256(s, red);
+  const float ir = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(s, (float)a.d) + a.eps));
+  for (int k = threadIdx.x; k < a.d; k += 256) out[k] = (xr[k] * ir) * (a.norm[k] + a.off);
+  if (threadIdx.x == 0) a.inv[i] = ir;
+}
+
+// grid (G, n): maximum of slice g of row i
+extern "C" __global__ __launch_bounds__(256) void rtq_head_max(HeadArgs a) {
+  __shared__ float red[4];
+  const int g = blockIdx.x, i = blockIdx.y;
+  const float* row = a.logits + (int64_t)i * a.V;
+  const int j0 = g * a.L, j1 = min(a.V, j0 + a.L);
+  float m = -__builtin_inff();
+  head_slice(a, row, j0, j1, [&](int, float v) { m = fmaxf(m, v); });
+  m = block_max256(m, red);
+  if (threadIdx.x == 0) a.pmax[(int64_t)i * a.G + g] = m;
+}
+
+__device__ __forceinline__ float head_row_max(const HeadArgs& a, int i) {
+  float m = -__builtin_inff();
+  for (int q = 0; q < a.G; q++) m = fmaxf(m, a.pmax[(int64_t)i * a.G + q]);
+  return m;
+}
+
+// grid (G, n): sum over slice g of row i of exp(v - max), each term rounded to f32, summed in f64
+extern "C" __global__ __launch_bounds__(256) void rtq_head_sum(HeadArgs a) {
+  __shared__ double red[4];
+  const int g = blockIdx.x, i = blockIdx.y;
+  const float* row = a.logits + (int64_t)i * a.V;
+  const int j0 = g * a.L, j1 = min(a.V, j0 + a.L);
+  const float m = head_row_max(a, i);
+  double s = 0.0;
+  head_slice(a, row, j0, j1, [&](int, float v) { s += (double)expf(v - m); });
+  s = block_sum256(s, red);
+  if (threadIdx.x == 0) a.psum[(int64_t)i * a.G + g] = s;
+}
+
+// grid (G, n): log-prob and hit of target i (by the slice holding its token), then, with weights,
+// dlogits = w * (exp(v - max) * (f32)(1 / s)), minus w at the token, over the slice
+extern "C" __global__ __launch_bounds__(256) void rtq_head_grad(HeadArgs a) {
+  const int g = blockIdx.x, i = blockIdx.y;
+  float* row = a.logits + (int64_t)i * a.V;
+  const int j0 = g * a.L, j1 = min(a.V, j0 + a.L);
+  const float m = head_row_max(a, i);
+  double s = 0.0;
+  for (int q = 0; q < a.G; q++) s += a.psum[(int64_t)i * a.G + q];
+  const float inv = (float)(1.0 / s);
+  const float lse = m + (float)log(s);
+  const bool ok = head_target_ok(a, i);
+  const int tk = ok ? a.tok[i] : -1;
+  if (threadIdx.x == 0) {
+    if (ok && tk >= j0 && tk < j1) {
+      const float tl = row[tk];
+      a.logp[i] = tl - lse;
+      a.hit[i] = tl >= m ? 1 : 0;
+    } else if (!ok && g == 0) {
+      a.logp[i] = __builtin_nanf("");
+      a.hit[i] = 0;
+    }
+  }
+  if (!a.wts) return;
+  __syncthreads();  // the target's logit is read before its slice is overwritten
+  const float wi = ok ? a.wts[i] : 0.0f;
+  if ((a.V & 3) == 0) {
+    f4* r4 = reinterpret_cast<f4*>(row);
+    for (int q = j0 / 4 + (int)threadIdx.x; q < j1 / 4; q += 256) {
+      f4 v = r4[q];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        float dl = ok ? wi * (expf(v[e] - m) * inv) : 0.0f;
+        if (4 * q + e == tk) dl = dl - wi;
+        v[e] = dl;
+      }
+      r4[q] = v;
+    }
+  } else {
+    for (int j = j0 + (int)threadIdx.x; j < j1; j += 256) {
+      float dl = ok ? wi * (expf(row[j] - m) * inv) : 0.0f;
+      if (j == tk) dl = dl - wi;
+      row[j] = dl;
+    }
+  }
+}
+
+// grid n: the first target at each position writes that dx row: 0 + the rmsnorm_backward of every
+// target at the position, in target order (dx[pos] += dxs, src/model.rs:600-604)
+extern "C" __global__ __launch_bounds__(256) void rtq_head_norm_bwd(HeadArgs a) {
+  __shared__ float red[4];
+  const int i = blockIdx.x;
+  if (!head_target_ok(a, i)) return;
+  const int p = a.pos[i];
+  int earlier = 0;
+  for (int j = threadIdx.x; j < i; j += 256) earlier |= (a.pos[j] == p && head_target_ok(a, j)) ? 1 : 0;
+  if (__syncthreads_or(earlier)) return;
+  // later targets at the same position (rare): then walk them in order, else only target i
+  int later = 0;
+  for (int j = i + 1 + (int)threadIdx.x; j < a.n; j += 256) later |= (a.pos[j] == p && head_target_ok(a, j)) ? 1 : 0;
+  const int jend = __syncthreads_or(later) ? a.n : i + 1;
+  const float* xr = a.x + (int64_t)p * a.d;
+  float* o = a.dx + (int64_t)p * a.d;
+  for (int j = i; j < jend; j++) {
+    if (a.pos[j] != p || !head_target_ok(a, j)) continue;
+    const float ir = a.inv[j];
+    const float* dr = a.dns + (int64_t)j * a.d;
+    float s = 0.0f;
+    for (int k = threadIdx.x; k < a.d; k += 256) s = s + (dr[k] * (a.norm[k] + a.off)) * xr[k];
+    s = block_sum256(s, red);
+    const float c = __fdiv_rn(((s * ir) * ir) * ir, (float)a.d);
+    for (int k = threadIdx.x; k < a.d; k += 256) {
+      const float gk = dr[k] * (a.norm[k] + a.off);
+      o[k] = (j == i ? 0.0f : o[k]) + (gk * ir - xr[k] * c);
+    }
+  }
+}

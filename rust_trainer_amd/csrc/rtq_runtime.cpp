@@ -129,6 +129,11 @@ enum Kid {
   K_BWD_FINISH16,  // 16 waves per workgroup: long token reductions of dA / dB
   K_DENSE_ROWS,    // trainer-native weights: rows / dequantisation, bias
   K_DENSE_BIAS,
+  K_HEAD_NORM,   // LM head + cross-entropy (Model::head)
+  K_HEAD_MAX,
+  K_HEAD_SUM,
+  K_HEAD_GRAD,
+  K_HEAD_NORM_BWD,
   K_ROWS,        // + format
   K_COUNT = K_ROWS + F_COUNT
 };
@@ -145,6 +150,8 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
     "rtq_dxw_q4_0",         "rtq_dxw_q8_0",         "rtq_dxw_q4_k",         "rtq_dxw_q6_k",
     "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_dense_rows",       "rtq_dense_bias",
+    "rtq_head_norm",        "rtq_head_max",         "rtq_head_sum",         "rtq_head_grad",
+    "rtq_head_norm_bwd",
     "rtq_rows_q4_0",        "rtq_rows_q8_0",        "rtq_rows_q4_k",        "rtq_rows_q6_k"};
 
 struct TimedLaunch {
@@ -390,7 +397,7 @@ rtq_status dense_weight(rtq_ctx* c, const rtq_weight* w, Arena& ar, hipStream_t 
   }
   float* out = ar.take<float>((size_t)(w->rows * w->cols));
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
-  DenseArgs da{nullptr, w->wsc, reinterpret_cast<const int8_t*>(w->wq), w->rows, w->cols, 0, w->rows, out, nullptr};
+  DenseArgs da{nullptr, w->wsc, reinterpret_cast<const int8_t*>(w->wq), w->rows, w->cols, 0, w->rows, out, nullptr, nullptr};
   RTQ_TRY(launch(c, K_DENSE_ROWS, dim3((unsigned)std::min<int64_t>(cdiv(w->rows * w->cols, 256), 8192)), dim3(256), st, da));
   *W = out;
   return RTQ_OK;
@@ -407,7 +414,7 @@ rtq_status enqueue_forward_dense(rtq_ctx* c, const rtq_weight* w, const float* x
   RTQ_TRY(blas_handle(c, st, &h));
   RTQ_TRY(rm_sgemm(h, false, true, t, N, K, 1.0f, x, K, W, K, 0.0f, y, N));
   if (bias) {
-    DenseArgs da{nullptr, nullptr, nullptr, N, K, 0, t, y, bias};
+    DenseArgs da{nullptr, nullptr, nullptr, N, K, 0, t, y, bias, nullptr};
     RTQ_TRY(launch(c, K_DENSE_BIAS, dim3((unsigned)std::min<int64_t>(cdiv(t * N, 256), 8192)), dim3(256), st, da));
   }
   if (la && lb && r > 0) {
@@ -1092,13 +1099,14 @@ rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora
 }
 
 static rtq_status enqueue_rows(rtq_ctx* c, const rtq_weight* w, int64_t r0, int64_t count, float* out,
-                               hipStream_t st) {
+                               hipStream_t st, const int32_t* idx = nullptr) {
   if (is_dense(w->type)) {  // F32: copy; TQ8_0: 0 + d * q (src/frozen.rs:169-177)
     DenseArgs da{w->type == RTQ_TYPE_F32 ? reinterpret_cast<const float*>(w->wq) : nullptr, w->wsc,
-                 reinterpret_cast<const int8_t*>(w->wq), w->rows, w->cols, r0, count, out, nullptr};
+                 reinterpret_cast<const int8_t*>(w->wq), w->rows, w->cols, r0, count, out, nullptr, idx};
     return launch(c, K_DENSE_ROWS, dim3((unsigned)std::min<int64_t>(cdiv(count * w->cols, 256), 8192)), dim3(256), st, da);
   }
-  RowArgs ra{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, (int)w->cols, (int)r0, (int)count, out};
+  RowArgs ra{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, (int)w->cols, (int)r0, (int)count, out, idx,
+             (int)w->rows};
   const int64_t threads = count * (w->cols / 32);
   return launch(c, K_ROWS + fmt_index(w->type), dim3((unsigned)cdiv(threads, 256)), dim3(256), st, ra);
 }
@@ -1111,6 +1119,100 @@ rtq_status rtq_frozen_rows_d(rtq_ctx* c, const rtq_weight* w, int64_t r0, int64_
   std::lock_guard<std::mutex> lk(c->mu);
   HIP_TRY(hipSetDevice(c->device));
   return enqueue_rows(c, w, r0, count, out, (hipStream_t)stream);
+}
+
+rtq_status rtq_frozen_gather_d(rtq_ctx* c, const rtq_weight* w, const int32_t* ids, int64_t count, float* out,
+                               void* stream) {
+  RTQ_TRY(check_weight(c, w));
+  if (count < 0 || count > (1LL << 24)) return fail(RTQ_ERR_INVALID, "gather count %lld out of range", (long long)count);
+  if (count == 0) return RTQ_OK;
+  if (!ids || !out) return fail(RTQ_ERR_INVALID, "null ids/out");
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  return enqueue_rows(c, w, 0, count, out, (hipStream_t)stream, ids);
+}
+
+// ------------------------------------------------------------------ LM head + cross-entropy
+namespace {
+
+struct HeadPlan {
+  int G, L;
+  size_t bytes;  // workspace: head buffers + the larger of the lm_head forward / backward workspaces
+};
+
+HeadPlan head_plan(const rtq_ctx* c, const rtq_weight* w, int64_t n, bool grad) {
+  const int64_t V = w->rows, d = w->cols;
+  // enough (slice, row) workgroups to fill the chip four times, slices of at least 4096 logits
+  int64_t G = std::min<int64_t>(std::max<int64_t>(cdiv(4 * c->cu_count, n), 1), std::max<int64_t>(V / 4096, 1));
+  G = std::min<int64_t>(G, 64);
+  const int64_t L = roundup(cdiv(V, G), 4);
+  G = cdiv(V, L);
+  size_t b = (size_t)(n * d) * 4 * 2 + (size_t)n * 4 + (size_t)(n * V) * 4 + (size_t)(n * G) * 12 + 8 * 256;
+  size_t sub = fwd_ws_bytes(fwd_plan(w, n, 0));
+  if (grad) sub = std::max(sub, bwd_ws_bytes(c, w, n, 0));
+  return HeadPlan{(int)G, (int)L, b + sub};
+}
+
+rtq_status enqueue_head(rtq_ctx* c, const rtq_weight* w, const float* norm, float eps, float off, const float* x,
+                        int64_t t, const int32_t* pos, const int32_t* tok, const float* wts, int64_t n, float* logp,
+                        int32_t* hit, float* dx, const HeadPlan& hp, Arena& ar, hipStream_t st) {
+  const int64_t V = w->rows, d = w->cols;
+  float* ns = ar.take<float>((size_t)(n * d));
+  float* inv = ar.take<float>((size_t)n);
+  float* logits = ar.take<float>((size_t)(n * V));
+  float* pmax = ar.take<float>((size_t)(n * hp.G));
+  double* psum = ar.take<double>((size_t)(n * hp.G));
+  float* dns = wts ? ar.take<float>((size_t)(n * d)) : nullptr;
+  if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
+  HeadArgs ha{x,   pos,   tok,    wts,  norm,      eps,  off,    (int)t, (int)d, (int)n, (int)V, hp.G, hp.L,
+              ns,  inv,   logits, pmax, psum,      logp, hit,    dns,    dx};
+  RTQ_TRY(launch(c, K_HEAD_NORM, dim3((unsigned)n), dim3(256), st, ha));
+  Arena fa = ar;
+  RTQ_TRY(enqueue_forward(c, w, ns, n, logits, nullptr, nullptr, nullptr, 0, 0.0f, nullptr, fa, st));
+  const dim3 sg((unsigned)hp.G, (unsigned)n);
+  RTQ_TRY(launch(c, K_HEAD_MAX, sg, dim3(256), st, ha));
+  RTQ_TRY(launch(c, K_HEAD_SUM, sg, dim3(256), st, ha));
+  RTQ_TRY(launch(c, K_HEAD_GRAD, sg, dim3(256), st, ha));
+  if (!wts) return RTQ_OK;
+  Arena ba = ar;
+  RTQ_TRY(enqueue_backward(c, w, logits, n, dns, false, nullptr, nullptr, nullptr, 0, 0.0f, nullptr, nullptr, ba, st));
+  FillArgs fz{dx, t * d};
+  RTQ_TRY(launch(c, K_FILL, dim3((unsigned)std::min<int64_t>(cdiv(t * d, 256), 4096)), dim3(256), st, fz));
+  return launch(c, K_HEAD_NORM_BWD, dim3((unsigned)n), dim3(256), st, ha);
+}
+
+rtq_status check_head(rtq_ctx* c, const rtq_weight* w, const float* norm, const float* x, int64_t t, const int32_t* pos,
+                      const int32_t* tok, const float* wts, int64_t n, const float* logp, const float* dx) {
+  RTQ_TRY(check_weight(c, w));
+  RTQ_TRY(check_t(t));
+  if (n < 0 || n > 65535) return fail(RTQ_ERR_INVALID, "target count %lld out of range [0, 65535]", (long long)n);
+  if (n > 0 && (!norm || !x || !pos || !tok || !logp)) return fail(RTQ_ERR_INVALID, "null norm/x/pos/tok/logp");
+  if (n > 0 && wts && !dx) return fail(RTQ_ERR_INVALID, "weights given without dx");
+  if ((double)n * (double)w->rows > 4e9) return fail(RTQ_ERR_INVALID, "n x vocab logits too large");
+  return RTQ_OK;
+}
+
+}  // namespace
+
+rtq_status rtq_lm_head_d(rtq_ctx* c, const rtq_weight* w, const float* norm, float eps, float offset, const float* x,
+                         int64_t t, const int32_t* pos, const int32_t* tok, const float* weights, int64_t n,
+                         float* logp, int32_t* hit, float* dx, void* stream) {
+  RTQ_TRY(check_head(c, w, norm, x, t, pos, tok, weights, n, logp, dx));
+  if (n > 0 && !hit) return fail(RTQ_ERR_INVALID, "null hit");
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = (hipStream_t)stream;
+  if (n == 0) {
+    if (weights && dx && t > 0) {
+      FillArgs fz{dx, t * w->cols};
+      return launch(c, K_FILL, dim3((unsigned)std::min<int64_t>(cdiv(t * w->cols, 256), 4096)), dim3(256), st, fz);
+    }
+    return RTQ_OK;
+  }
+  const HeadPlan hp = head_plan(c, w, n, weights != nullptr);
+  RTQ_TRY(ensure_ws(c, hp.bytes));
+  Arena ar{(char*)c->ws, c->ws_bytes, 0};
+  return enqueue_head(c, w, norm, eps, offset, x, t, pos, tok, weights, n, logp, hit, dx, hp, ar, st);
 }
 
 // ------------------------------------------------------------------ host-pointer API
@@ -1239,6 +1341,78 @@ rtq_status rtq_frozen_row(rtq_ctx* c, const rtq_weight* w, int64_t r, float* out
   RTQ_TRY(enqueue_rows(c, w, r, 1, od, c->stream));
   RTQ_TRY(d2h(out, od, (size_t)w->cols * 4, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
+  return RTQ_OK;
+}
+
+/* embed_tokens (src/model.rs:446-454): out[i] = row(ids[i]) */
+rtq_status rtq_frozen_gather(rtq_ctx* c, const rtq_weight* w, const int32_t* ids, int64_t count, float* out) {
+  RTQ_TRY(check_weight(c, w));
+  if (count < 0 || count > (1LL << 24)) return fail(RTQ_ERR_INVALID, "gather count %lld out of range", (long long)count);
+  if (count == 0) return RTQ_OK;
+  if (!ids || !out) return fail(RTQ_ERR_INVALID, "null ids/out");
+  for (int64_t i = 0; i < count; i++)
+    if (ids[i] < 0 || ids[i] >= w->rows)
+      return fail(RTQ_ERR_INVALID, "token %d out of vocab (%lld rows)", ids[i], (long long)w->rows);
+  HostCall hc(c);
+  HIP_TRY(hipSetDevice(c->device));
+  const size_t ob = (size_t)(count * w->cols) * 4;
+  RTQ_TRY(ensure_ws(c, ob + (size_t)count * 4 + 512));
+  Arena ar{(char*)c->ws, c->ws_bytes, 0};
+  float* od = ar.take<float>((size_t)(count * w->cols));
+  int32_t* idd = ar.take<int32_t>((size_t)count);
+  RTQ_TRY(h2d(idd, ids, (size_t)count * 4, c->stream));
+  RTQ_TRY(enqueue_rows(c, w, 0, count, od, c->stream, idd));
+  RTQ_TRY(d2h(out, od, ob, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return RTQ_OK;
+}
+
+/* Model::head (src/model.rs:561-609) with host arrays; targets out of range are rejected (the
+ * reference asserts, :575) */
+rtq_status rtq_lm_head(rtq_ctx* c, const rtq_weight* w, const float* norm, float eps, float offset, const float* x,
+                       int64_t t, const int32_t* pos, const int32_t* tok, const float* weights, int64_t n, float* logp,
+                       int64_t* hits, float* dx) {
+  RTQ_TRY(check_head(c, w, norm, x, t, pos, tok, weights, n, logp, dx));
+  for (int64_t i = 0; i < n; i++)
+    if (pos[i] < 0 || pos[i] >= t || tok[i] < 0 || tok[i] >= w->rows)
+      return fail(RTQ_ERR_INVALID, "target %lld (pos %d, token %d) out of range", (long long)i, pos[i], tok[i]);
+  const int64_t d = w->cols;
+  if (hits) *hits = 0;
+  if (n == 0) {
+    if (weights && dx) memset(dx, 0, (size_t)(t * d) * 4);
+    return RTQ_OK;
+  }
+  HostCall hc(c);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = c->stream;
+  const HeadPlan hp = head_plan(c, w, n, weights != nullptr);
+  const size_t io = (size_t)(t * d + d + n * 5 + (weights ? t * d : 0)) * 4 + 8 * 256;
+  RTQ_TRY(ensure_ws(c, hp.bytes + io));
+  Arena ar{(char*)c->ws, c->ws_bytes, 0};
+  float* xd = ar.take<float>((size_t)(t * d));
+  float* nd = ar.take<float>((size_t)d);
+  int32_t* pd = ar.take<int32_t>((size_t)n);
+  int32_t* kd = ar.take<int32_t>((size_t)n);
+  float* wd = weights ? ar.take<float>((size_t)n) : nullptr;
+  float* ld = ar.take<float>((size_t)n);
+  int32_t* hd = ar.take<int32_t>((size_t)n);
+  float* dxd = weights ? ar.take<float>((size_t)(t * d)) : nullptr;
+  RTQ_TRY(h2d(xd, x, (size_t)(t * d) * 4, st));
+  RTQ_TRY(h2d(nd, norm, (size_t)d * 4, st));
+  RTQ_TRY(h2d(pd, pos, (size_t)n * 4, st));
+  RTQ_TRY(h2d(kd, tok, (size_t)n * 4, st));
+  if (wd) RTQ_TRY(h2d(wd, weights, (size_t)n * 4, st));
+  RTQ_TRY(enqueue_head(c, w, nd, eps, offset, xd, t, pd, kd, wd, n, ld, hd, dxd, hp, ar, st));
+  std::vector<int32_t> hv((size_t)n);
+  RTQ_TRY(d2h(logp, ld, (size_t)n * 4, st));
+  RTQ_TRY(d2h(hv.data(), hd, (size_t)n * 4, st));
+  if (dxd) RTQ_TRY(d2h(dx, dxd, (size_t)(t * d) * 4, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (hits) {
+    int64_t s = 0;
+    for (int32_t h : hv) s += h;
+    *hits = s;
+  }
   return RTQ_OK;
 }
 

@@ -395,3 +395,88 @@ def test_tq8_forward_backward_row_match_dense_products():
     assert abs(float((dy * y).sum()) - float((dx * x).sum())) <= 1e-4 * float(np.abs(dy * y).sum())
     for r in (0, 17, n - 1):
         assert np.array_equal(O.frozen_row(O.TQ8_0, b, n, k, r), (np.float32(0) + sc[r].repeat(32) * qs[r].astype(np.float32)))
+
+
+# ---------------------------------------------------------------- LM head + cross-entropy
+def _head_case(wtype, V, d, t, seed=1):
+    w = O.Rng(seed).vec_normal(V * d, 0.3).reshape(V, d)
+    blocks = O.quantize(wtype, w) if wtype != O.F32 else w.astype(np.float32).view(np.uint8).reshape(V, -1)
+    x = O.Rng(seed + 1).vec_normal(t * d, 1.0).reshape(t, d)
+    norm = (1.0 + O.Rng(seed + 2).vec_normal(d, 0.1)).astype(np.float32)
+    return blocks, x, norm
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0, O.Q6_K])
+def test_lm_head_closed_forms_f64(wtype):
+    """Model::head (src/model.rs:561-609) against f64 closed forms over the same operands: the
+    log-softmax of the oracle's logits, the argmax hits, and dx = rmsnorm_backward(dequant(W)^T
+    w (softmax - onehot)) scattered to the target positions (repeated positions add)."""
+    V, d, t = 700, 256, 11
+    blocks, x, norm = _head_case(wtype, V, d, t)
+    pos = np.array([0, 4, 10, 4, 7, 2, 9], np.int32)
+    tok = np.array([3, 699, 0, 17, 350, 5, 698], np.int32)
+    wts = np.array([1.0, 0.5, 2.0, 1.0, 0.25, 1.5, 1.0], np.float32)
+    eps, off = 1e-6, 0.0
+    logp, hits, dx = O.lm_head(wtype, blocks, V, d, norm, x, pos, tok, wts, eps=eps, off=off, chunk=3)
+    # f64 restatement
+    xs = x[pos].astype(np.float64)
+    ir = 1.0 / np.sqrt((xs * xs).sum(1) / d + eps)
+    ns = (xs * ir[:, None] * (norm.astype(np.float64) + off)).astype(np.float32)
+    logits = O.frozen_forward(wtype, blocks, V, d, ns).astype(np.float64)
+    m = logits.max(1, keepdims=True)
+    lse = (m + np.log(np.exp(logits - m).sum(1, keepdims=True)))[:, 0]
+    want = logits[np.arange(pos.size), tok] - lse
+    np.testing.assert_allclose(logp, want, rtol=0, atol=2e-5 * np.abs(want).max())
+    assert hits == int((logits.argmax(1) == tok).sum())
+    p = np.exp(logits - lse[:, None])
+    dl = wts[:, None].astype(np.float64) * p
+    dl[np.arange(pos.size), tok] -= wts
+    Wd = O.dequantize(wtype, blocks, d).astype(np.float64).reshape(V, d)
+    dns = dl @ Wd
+    g = dns * (norm.astype(np.float64) + off)
+    c = (g * xs).sum(1) * ir ** 3 / d
+    dxs = g * ir[:, None] - xs * c[:, None]
+    want_dx = np.zeros((t, d))
+    for i, p_ in enumerate(pos):
+        want_dx[p_] += dxs[i]
+    assert np.abs(dx - want_dx).max() <= 1e-4 * np.abs(want_dx).max()
+    assert not dx[[1, 3, 5, 6, 8]].any()  # rows without targets stay zero
+    # without weights: log-probs only, same values
+    lp2, h2, dx2 = O.lm_head(wtype, blocks, V, d, norm, x, pos, tok, None, eps=eps, off=off, chunk=64)
+    np.testing.assert_array_equal(lp2, logp)
+    assert h2 == hits and dx2 is None
+
+
+def test_lm_head_gradient_finite_differences():
+    """dL/dx of L = -sum w_i logp_i by central differences in x (F32 head: no activation
+    quantisation, so L is smooth), norm offset 1 as in the zero-centred norm."""
+    V, d, t = 60, 32, 4
+    blocks, x, norm = _head_case(O.F32, V, d, t, seed=7)
+    x = x.astype(np.float64)
+    pos = np.array([1, 3, 0], np.int32)
+    tok = np.array([2, 59, 30], np.int32)
+    wts = np.array([1.0, 0.5, 2.0], np.float32)
+    eps, off = 1e-5, 1.0
+
+    def loss(xx):
+        lp, _, _ = O.lm_head(O.F32, blocks, V, d, norm, xx.astype(np.float32), pos, tok, None, eps=eps, off=off)
+        return -float((wts.astype(np.float64) * lp).sum())
+
+    _, _, dx = O.lm_head(O.F32, blocks, V, d, norm, x.astype(np.float32), pos, tok, wts, eps=eps, off=off)
+    h = 1e-2
+    rng = np.random.default_rng(0)
+    for _ in range(12):
+        r, k = int(rng.choice(pos)), int(rng.integers(0, d))
+        xp, xm = x.copy(), x.copy()
+        xp[r, k] += h
+        xm[r, k] -= h
+        fd = (loss(xp) - loss(xm)) / (2 * h)
+        assert abs(fd - dx[r, k]) <= 2e-2 * max(1.0, abs(fd)), (r, k, fd, dx[r, k])
+
+
+def test_lm_head_rejects_out_of_range_targets():
+    blocks, x, norm = _head_case(O.Q8_0, 64, 32, 3)
+    with pytest.raises(Exception):
+        O.lm_head(O.Q8_0, blocks, 64, 32, norm, x, [3], [0])
+    with pytest.raises(Exception):
+        O.lm_head(O.Q8_0, blocks, 64, 32, norm, x, [0], [64])
