@@ -41,6 +41,26 @@ _f = ctypes.c_float
 _i = ctypes.c_int
 
 
+class OrLinear(ctypes.Structure):
+    _fields_ = [("wtype", ctypes.c_int), ("w", ctypes.c_void_p), ("out", ctypes.c_int64), ("in_", ctypes.c_int64),
+                ("bias", ctypes.c_void_p), ("rank", ctypes.c_int64), ("alpha", ctypes.c_float),
+                ("A", ctypes.c_void_p), ("B", ctypes.c_void_p), ("ga", ctypes.c_void_p), ("gb", ctypes.c_void_p)]
+
+
+class OrLayer(ctypes.Structure):
+    _fields_ = [("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p), ("q_norm", ctypes.c_void_p),
+                ("k_norm", ctypes.c_void_p)] + [(n, OrLinear) for n in ("q", "k", "v", "o", "gate", "up", "down")]
+
+
+class OrModel(ctypes.Structure):
+    _fields_ = [("n_layer", ctypes.c_int), ("d", ctypes.c_int64), ("n_head", ctypes.c_int64),
+                ("n_kv", ctypes.c_int64), ("hd", ctypes.c_int64), ("rot", ctypes.c_int64), ("n_ff", ctypes.c_int64),
+                ("eps", ctypes.c_float), ("off", ctypes.c_float), ("theta", ctypes.c_float),
+                ("freq_scale", ctypes.c_float), ("neox", ctypes.c_int), ("kv_f16", ctypes.c_int),
+                ("embed", OrLinear), ("lm_head", OrLinear), ("out_norm", ctypes.c_void_p),
+                ("layers", ctypes.POINTER(OrLayer))]
+
+
 def lib() -> ctypes.CDLL:
     global _LIB
     if _LIB is None:
@@ -77,6 +97,10 @@ def lib() -> ctypes.CDLL:
             "or_linear_forward": (_i, [_i, _p, _i64, _i64, _p, _i64, _f, _p, _p, _i, _p, _i64, _p, _i]),
             "or_linear_backward": (_i, [_i, _p, _i64, _i64, _i64, _f, _p, _p, _i, _p, _p, _i64, _p, _p, _p, _i]),
             "or_lm_head": (_i, [_i, _p, _i64, _i64, _p, _f, _f, _p, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _i]),
+            "or_round_f16": (_f, [_f]),
+            "or_rope_table": (None, [_i64, _i64, _f, _f, _p, _p]),
+            "or_model_forward_backward": (_i, [ctypes.POINTER(OrModel), _p, _i64, _p, _p, _p, _i64, _p,
+                                               ctypes.POINTER(_i64), _i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -303,3 +327,74 @@ def lm_head(wtype, wblocks, V, d, norm, x, pos, tok, wts=None, eps=1e-6, off=0.0
                             _ptr(pos), _ptr(tok), _ptr(None if wts is None else _f32(wts)), n, chunk, _ptr(logp),
                             ctypes.byref(hits), _ptr(dx), nthreads), "lm_head")
     return logp, hits.value, dx
+
+
+def round_f16(x: float) -> float:
+    return float(lib().or_round_f16(x))
+
+
+def rope_table(t: int, rot: int, theta: float, freq_scale: float = 1.0):
+    cos_ = np.empty((t, rot // 2), np.float32)
+    sin_ = np.empty((t, rot // 2), np.float32)
+    lib().or_rope_table(t, rot, theta, freq_scale, _ptr(cos_), _ptr(sin_))
+    return cos_, sin_
+
+
+LINEARS = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+def model_forward_backward(m: dict, tokens, pos, tok, wts=None, nthreads=1):
+    """Model::forward_backward (src/model.rs:615-687) of a model described by ``m``:
+    scalars n_layer, d, n_head, n_kv, hd, rot, n_ff, eps, off, theta, freq_scale, neox, kv_f16;
+    ``embed`` / ``lm_head`` = (wtype, blocks, out, in); ``out_norm``; ``layers`` = list of dicts with
+    attn_norm, ffn_norm, q_norm, k_norm (or None) and per linear name a dict wtype, blocks, out, in,
+    optional bias, A [r x in], B [out x r], alpha.  Returns (logp, hits, grads) with grads[l][name] =
+    (ga, gb) accumulated from zero."""
+    keep = []
+
+    def arr(a, dt=np.float32):
+        if a is None:
+            return None
+        a = np.ascontiguousarray(a, dtype=dt)
+        keep.append(a)
+        return a.ctypes.data
+
+    def lin(d_, grads=None):
+        A, B = d_.get("A"), d_.get("B")
+        r = 0 if A is None else int(np.asarray(A).shape[0])
+        ga = gb = None
+        if r:
+            ga = np.zeros((r, d_["in"]), np.float32)
+            gb = np.zeros((d_["out"], r), np.float32)
+            keep.extend([ga, gb])
+            if grads is not None:
+                grads.append((ga, gb))
+        elif grads is not None:
+            grads.append(None)
+        blocks = np.ascontiguousarray(d_["blocks"])
+        keep.append(blocks)
+        return OrLinear(d_["wtype"], blocks.ctypes.data, d_["out"], d_["in"], arr(d_.get("bias")), r,
+                        float(d_.get("alpha", 0.0)), arr(A), arr(B), None if ga is None else ga.ctypes.data,
+                        None if gb is None else gb.ctypes.data)
+
+    L = (OrLayer * m["n_layer"])()
+    grads = []
+    for i, ld in enumerate(m["layers"]):
+        gl = []
+        L[i] = OrLayer(arr(ld["attn_norm"]), arr(ld["ffn_norm"]), arr(ld.get("q_norm")), arr(ld.get("k_norm")),
+                       *[lin(ld[n], gl) for n in LINEARS])
+        grads.append(dict(zip(LINEARS, gl)))
+    e, h = m["embed"], m["lm_head"]
+    M = OrModel(m["n_layer"], m["d"], m["n_head"], m["n_kv"], m["hd"], m["rot"], m["n_ff"], m["eps"], m["off"],
+                m["theta"], m["freq_scale"], int(m["neox"]), int(m["kv_f16"]),
+                lin(dict(wtype=e[0], blocks=e[1], out=e[2], **{"in": e[3]})),
+                lin(dict(wtype=h[0], blocks=h[1], out=h[2], **{"in": h[3]})), arr(m["out_norm"]), L)
+    tokens = np.ascontiguousarray(tokens, np.int32)
+    pos = np.ascontiguousarray(pos, np.int32)
+    tok = np.ascontiguousarray(tok, np.int32)
+    logp = np.empty(pos.size, np.float32)
+    hits = ctypes.c_int64()
+    _check(lib().or_model_forward_backward(ctypes.byref(M), _ptr(tokens), tokens.size, _ptr(pos), _ptr(tok),
+                                           arr(wts), pos.size, _ptr(logp), ctypes.byref(hits), nthreads),
+           "model_forward_backward")
+    return logp, hits.value, grads

@@ -117,6 +117,48 @@ int or_linear_backward(int wtype, const void* w, int64_t n, int64_t k, int64_t r
 int or_lm_head(int wtype, const void* w, int64_t V, int64_t d, const float* norm, float eps, float off,
                const float* x, int64_t t, const int32_t* pos, const int32_t* tok, const float* wts, int64_t n,
                int64_t chunk, float* logp, int64_t* hits, float* dx, int nthreads);
+/* ---- model-level training step (rtq_oracle_model.c) ----
+ * src/model.rs:644-687 forward_backward_layout over src/model.rs:165-197 Block,
+ * src/attention.rs:162-367 Attention, src/model.rs:113-134 Mlp. */
+typedef struct {
+  int wtype;
+  const void* w; /* frozen weight (GGUF blocks, or f32 for OR_F32) */
+  int64_t out, in;
+  const float* bias; /* [out] or NULL */
+  int64_t rank;      /* 0: no adapter */
+  float alpha;
+  const float* A; /* [rank x in] */
+  const float* B; /* [out x rank] */
+  float* ga;      /* accumulated gradients, [rank x in] / [out x rank] */
+  float* gb;
+} or_linear;
+
+typedef struct {
+  const float *attn_norm, *ffn_norm; /* [d] */
+  const float *q_norm, *k_norm;      /* [head_dim], or NULL without QK-norm */
+  or_linear q, k, v, o, gate, up, down;
+} or_layer;
+
+typedef struct {
+  int n_layer;
+  int64_t d, n_head, n_kv, hd, rot, n_ff;
+  float eps, off, theta, freq_scale;
+  int neox, kv_f16;
+  or_linear embed, lm_head; /* the same weight twice when tied; no adapters on either */
+  const float* out_norm;
+  const or_layer* layers;
+} or_model;
+
+/* round_f16 (src/attention.rs:34-51) */
+float or_round_f16(float x);
+/* Rope tables for positions 0..t-1 (src/ops.rs:141-167): cos / sin [t x rot/2] */
+void or_rope_table(int64_t t, int64_t rot, float theta, float freq_scale, float* cos_, float* sin_);
+/* Model::forward_backward (src/model.rs:615-687) on one sequence: logp[n] per target; with wts,
+ * the adapters' ga / gb accumulate dL/dA, dL/dB of L = -sum wts[i] logp[i].  Returns -1 on bad
+ * shapes or tokens. */
+int or_model_forward_backward(const or_model* m, const int32_t* tokens, int64_t t, const int32_t* pos,
+                              const int32_t* tok, const float* wts, int64_t n, float* logp, int64_t* hits,
+                              int nthreads);
 #ifdef __cplusplus
 }
 #endif
