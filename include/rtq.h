@@ -49,6 +49,7 @@ typedef int rtq_status;
 
 typedef struct rtq_ctx rtq_ctx;
 typedef struct rtq_weight rtq_weight;
+typedef struct rtq_gguf rtq_gguf; /* GGUF v3 image (reader, below) */
 
 /* LoRA adapter view (src/linear.rs:8-16): a is [rank x in], b is [out x rank], scale = alpha/rank.
  * enabled = 0 bypasses the adapter (Linear::lora_enabled, src/linear.rs:45). */
@@ -138,6 +139,46 @@ rtq_status rtq_lm_head_d(rtq_ctx* ctx, const rtq_weight* lm_head, const float* n
                          const float* x, int64_t t, const int32_t* pos, const int32_t* tok, const float* weights,
                          int64_t n, float* logp, int32_t* hit, float* dx, void* stream);
 
+/* ---- device-resident training step (Model::forward_backward over the frozen linears) ----
+ * A GGUF Qwen / Llama decoder (load_gguf_from, src/rie.rs:164-260) with every frozen tensor, norm
+ * and adapter in device memory.  One call runs embed_tokens, the blocks (RMSNorm, q/k/v, QK-norm,
+ * RoPE, f16 K/V, causal GQA attention, o, SwiGLU MLP: src/model.rs:165-197, src/attention.rs:
+ * 162-367, src/model.rs:113-134), Model::head and the blocks' backward in reverse
+ * (src/model.rs:644-687), accumulating the adapters' gradients on the device.  Every block's
+ * activations are kept for its backward instead of being recomputed (the same values). */
+typedef struct rtq_model rtq_model;
+typedef struct rtq_model_config {
+  int64_t n_layer, n_embd, n_head, n_head_kv, head_dim, rope_dim, n_ff, n_vocab;
+  float rms_eps, norm_offset, rope_base, rope_freq_scale;
+  int rope_neox, qk_norm, kv_f16, tied;
+} rtq_model_config;
+/* hyper-parameters from `<arch>.*` keys, tensors blk.{i}.{attn_q,attn_k,attn_v,attn_output,
+ * ffn_gate,ffn_up,ffn_down}.weight (+ optional q/k/v .bias), norms F32; tied when output.weight is
+ * absent; post-norm layers are rejected (src/rie.rs:204-206) */
+rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out);
+void rtq_model_destroy(rtq_model* m);
+rtq_status rtq_model_get_config(const rtq_model* m, rtq_model_config* out);
+/* Model::attach_lora (src/model.rs:406-419): target_mask bit i adapts linear i of (q, k, v, o, gate,
+ * up, down) in every block; A ~ U(-1/sqrt(in), 1/sqrt(in)) drawn from Rng(seed) in block order, B = 0
+ * (Lora::new, src/linear.rs:21-25); *n_params = adapter parameters */
+rtq_status rtq_model_attach_lora(rtq_model* m, int64_t rank, float alpha, uint32_t target_mask, uint64_t seed,
+                                 int64_t* n_params);
+int64_t rtq_model_lora_count(const rtq_model* m); /* adapted linears, in (block, q..down) order */
+rtq_status rtq_model_lora_info(const rtq_model* m, int64_t i, int* layer, int* which, int64_t* rank, int64_t* in,
+                               int64_t* out, float* alpha);
+/* host copies of adapter i's a [rank x in], b [out x rank], ga, gb (any may be NULL) */
+rtq_status rtq_model_lora_get(rtq_model* m, int64_t i, float* a, float* b, float* ga, float* gb);
+rtq_status rtq_model_lora_set(rtq_model* m, int64_t i, const float* a, const float* b);
+/* device pointers of adapter i (an optimiser on the device updates a / b in place) */
+rtq_status rtq_model_lora_device(rtq_model* m, int64_t i, float** a, float** b, float** ga, float** gb);
+rtq_status rtq_model_zero_grad(rtq_model* m); /* Model::zero_grad (src/model.rs:436) */
+/* Model::forward_backward (src/model.rs:615-687) on one sequence (host arrays): tokens [t], targets
+ * (pos[i], tok[i]) with loss weights [n]; logp [n] and *hits out.  weights NULL: log-probs only
+ * (Model::score, no backward).  Synchronous on the context's stream. */
+rtq_status rtq_model_forward_backward(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* pos,
+                                      const int32_t* tok, const float* weights, int64_t n, float* logp,
+                                      int64_t* hits);
+
 /* ---- parity / debug (host pointers, synchronous) ---- */
 /* The activation blocks the GPU forward actually uses for x, in ggml layout (block_q8_0: 34 B per
  * 32 elements for Q4_0/Q8_0 weights; block_q8_K: 292 B per 256 for Q4_K/Q6_K), t * act_row_bytes. */
@@ -154,7 +195,6 @@ rtq_status rtq_debug_block_isums(rtq_ctx* ctx, const rtq_weight* w, const float*
  * a message otherwise).  Strings and tensor data point into the image; they are valid until close.
  * Value types: u8 0, i8 1, u16 2, i16 3, u32 4, i32 5, f32 6, bool 7, string 8, array 9, u64 10,
  * i64 11, f64 12.  Tensor dims ne[0] = row length (columns), ne[1..] = rows (n_rows/row_len). */
-typedef struct rtq_gguf rtq_gguf;
 typedef struct rtq_gguf_writer rtq_gguf_writer;
 rtq_status rtq_gguf_open(const char* path, rtq_gguf** out);
 rtq_status rtq_gguf_from_bytes(const void* data, size_t nbytes, rtq_gguf** out);

@@ -11,7 +11,8 @@ from .frozen import Context, FrozenMatmul, HipFrozen, default_context, pack_trai
 from .gguf import GgufFile, GgufWriter, SyntheticSpec, Value  # noqa: F401
 from .head import Target, answer_targets, embed_tokens, head  # noqa: F401
 from .linear import Linear, Lora  # noqa: F401
+from .model import GpuModel  # noqa: F401
 
 __all__ = ["Context", "FrozenMatmul", "HipFrozen", "Linear", "Lora", "RtqError", "default_context", "lib",
            "TYPE_Q4_0", "TYPE_Q8_0", "TYPE_Q4_K", "TYPE_Q6_K", "TYPE_F32", "TYPE_TQ8_0", "pack_trainer_q8_0",
-           "GgufFile", "GgufWriter", "SyntheticSpec", "Value", "Target", "answer_targets", "embed_tokens", "head"]
+           "GgufFile", "GgufWriter", "SyntheticSpec", "Value", "Target", "answer_targets", "embed_tokens", "head", "GpuModel"]

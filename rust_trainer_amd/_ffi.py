@@ -33,6 +33,13 @@ class RtqLora(ctypes.Structure):
 
 _LP = ctypes.POINTER(RtqLora)
 
+
+class RtqModelConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int64) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "rope_dim",
+                                              "n_ff", "n_vocab")] + \
+               [(n, ctypes.c_float) for n in ("rms_eps", "norm_offset", "rope_base", "rope_freq_scale")] + \
+               [(n, ctypes.c_int) for n in ("rope_neox", "qk_norm", "kv_f16", "tied")]
+
 SIGNATURES = {
     "rtq_version": (ctypes.c_char_p, []),
     "rtq_last_error": (ctypes.c_char_p, []),
@@ -68,6 +75,20 @@ SIGNATURES = {
     "rtq_frozen_gather_d": (_i, [_p, _p, _p, _i64, _p, _p]),
     "rtq_lm_head": (_i, [_p, _p, _p, _f, _f, _p, _i64, _p, _p, _p, _i64, _p, ctypes.POINTER(_i64), _p]),
     "rtq_lm_head_d": (_i, [_p, _p, _p, _f, _f, _p, _i64, _p, _p, _p, _i64, _p, _p, _p, _p]),
+    # device-resident training step
+    "rtq_model_from_gguf": (_i, [_p, _p, ctypes.POINTER(_p)]),
+    "rtq_model_destroy": (None, [_p]),
+    "rtq_model_get_config": (_i, [_p, _p]),
+    "rtq_model_attach_lora": (_i, [_p, _i64, _f, ctypes.c_uint32, ctypes.c_uint64, ctypes.POINTER(_i64)]),
+    "rtq_model_lora_count": (_i64, [_p]),
+    "rtq_model_lora_info": (_i, [_p, _i64, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i64),
+                                 ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_f)]),
+    "rtq_model_lora_get": (_i, [_p, _i64, _p, _p, _p, _p]),
+    "rtq_model_lora_set": (_i, [_p, _i64, _p, _p]),
+    "rtq_model_lora_device": (_i, [_p, _i64, ctypes.POINTER(_p), ctypes.POINTER(_p), ctypes.POINTER(_p),
+                                   ctypes.POINTER(_p)]),
+    "rtq_model_zero_grad": (_i, [_p]),
+    "rtq_model_forward_backward": (_i, [_p, _p, _i64, _p, _p, _p, _i64, _p, ctypes.POINTER(_i64)]),
     # GGUF v3 container
     "rtq_gguf_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_p)]),
     "rtq_gguf_from_bytes": (_i, [_p, _sz, ctypes.POINTER(_p)]),

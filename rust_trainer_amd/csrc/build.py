@@ -1,7 +1,7 @@
 """Build recipe for librtq.so (the C-ABI library) and the CPU oracle.
 
 1. ``rtq_kernels.hip`` -> gfx950 code object (``hipcc --genco``), into ``rust_trainer_amd/_build/``;
-2. ``rtq_runtime.cpp`` + ``rtq_gguf.cpp`` -> ``rust_trainer_amd/librtq.so`` (g++ against the HIP runtime), with the
+2. ``rtq_runtime.cpp`` + ``rtq_gguf.cpp`` + ``rtq_model.cpp`` -> ``rust_trainer_amd/librtq.so`` (g++ against the HIP runtime), with the
    code object embedded (``.incbin``) and loaded at run time with ``hipModuleLoadData``;
 3. ``oracle/`` -> ``oracle/liboracle.so`` (test infrastructure, plain gcc).
 
@@ -58,7 +58,8 @@ def build_runtime(hsaco: str) -> str:
     _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter", "-Wno-attributes",
           "-D__HIP_PLATFORM_AMD__", f'-DRTQ_HSACO_PATH="{hsaco}"',
           "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"), "-I", CSRC,
-          os.path.join(CSRC, "rtq_runtime.cpp"), os.path.join(CSRC, "rtq_gguf.cpp"), "-o", tmp,
+          os.path.join(CSRC, "rtq_runtime.cpp"), os.path.join(CSRC, "rtq_gguf.cpp"),
+          os.path.join(CSRC, "rtq_model.cpp"), "-o", tmp,
           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-lrocblas", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"])
     os.replace(tmp, out)
     return out

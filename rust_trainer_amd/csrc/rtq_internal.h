@@ -1,0 +1,30 @@
+// rtq_internal.h — declarations shared by the translation units of librtq.so (not part of the
+// C ABI): error reporting and kernel launches by the model-level step (rtq_model.cpp).
+#ifndef RTQ_INTERNAL_H
+#define RTQ_INTERNAL_H
+#include <hip/hip_runtime.h>
+
+#include "rtq.h"
+
+// kernels of the decoder block (rtq_model_kernels.hip), in this order after the matmul kernels
+enum RtqModelKernel {
+  KM_RMSNORM,
+  KM_RMSNORM_BWD,
+  KM_QK_PREP,
+  KM_QK_BWD,
+  KM_GEMM,
+  KM_SOFTMAX,
+  KM_SOFTMAX_BWD,
+  KM_GROUP_SUM,
+  KM_SWIGLU,
+  KM_SWIGLU_BWD,
+  KM_ADD,
+  KM_COUNT
+};
+
+// sets the thread-local message of rtq_last_error and returns st
+rtq_status rtq_fail(rtq_status st, const char* fmt, ...);
+// launches decoder kernel km with one by-value argument struct at args (timed like every launch)
+rtq_status rtq_model_launch(rtq_ctx* c, int km, dim3 grid, dim3 block, hipStream_t s, const void* args);
+int rtq_ctx_device_id(const rtq_ctx* c);
+#endif

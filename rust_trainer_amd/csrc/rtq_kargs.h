@@ -213,3 +213,93 @@ struct HeadArgs {
   const float* dns;    // [n x d] dlogits . W (lm_head backward_input)
   float* dx;           // [t x d] dL/dx (rows without a target are cleared separately)
 };
+
+// ---------------------------------------------------------------- model-level step
+// The decoder block around the frozen linears (src/model.rs:165-197, src/attention.rs:162-367,
+// src/model.rs:113-134, src/ops.rs:14-56, :118-196), all tensors row-major f32 on the device.
+struct MNormArgs {
+  const float* a;    // [rows x d] input (the residual stream)
+  const float* b;    // or null: the input is a + b, written to h
+  float* h;          // [rows x d] a + b (when b), else unused
+  const float* w;    // [d] norm weight
+  float* y;          // [rows x d]
+  float* inv;        // [rows] 1 / rms
+  int rows, d;
+  float eps, off;
+  int fused;         // 1: x * (ir * (w + off)) (QK-norm order), 0: (x * ir) * (w + off)
+};
+
+struct MNormBwdArgs {
+  const float* x;    // [rows x d] the norm's input
+  const float* w;
+  const float* inv;
+  const float* dy;   // [rows x d] gradient of the norm's output
+  const float* res;  // or null: out = res + dx_norm (the residual branch's gradient)
+  float* out;        // [rows x d]
+  int rows, d;
+  float off;
+};
+
+// per (token, head) row of width hd: QK-norm, RoPE, f16 rounding of K and V
+struct MQkArgs {
+  const float* q_raw;  // [t x nh x hd]
+  const float* k_raw;  // [t x nkv x hd]
+  const float* v_raw;  // [t x nkv x hd]
+  const float* q_norm; // [hd] or null
+  const float* k_norm;
+  const float* cos_;   // [t x rot/2]
+  const float* sin_;
+  float* q;            // outputs, same layouts
+  float* k;
+  float* v;
+  float* q_inv;        // [t x nh]
+  float* k_inv;        // [t x nkv]
+  // backward: gradients in (dq [t x nh x hd], dk), out (dq_raw, dk_raw); dv passes through
+  const float* dq;
+  const float* dk;
+  float* dq_raw;
+  float* dk_raw;
+  int t, nh, nkv, hd, rot, neox, kv_f16;
+  float eps, off;
+};
+
+// C(b, m, n) (+)= sum_k A(b, m, k) * B(b, k, n), A(b, m, k) = A[(b / divA) * sAb + m * sAm + k * sAk]
+// (rounded product a_scale * A first when a_scale != 1), likewise B and C.
+// causal 0: full; 1: only tiles touching n <= m (others skipped); 2: k < min(K, m0 + 64) (A zero
+// above the diagonal); 3: k >= m0 (A(b, m, k) zero for k < m).
+struct MGemmArgs {
+  const float* A;
+  const float* B;
+  float* C;
+  int M, N, K;
+  int64_t sAb, sAm, sAk, sBb, sBk, sBn, sCb, sCm, sCn;
+  int divA, divB;
+  float a_scale;
+  int causal, accumulate;
+};
+
+// attention rows (h, i) of S / P / dP [nh x t x t]
+struct MSoftArgs {
+  float* s;          // forward: scores in, probabilities out (0 for j > i)
+  const float* p;    // backward: probabilities
+  float* dp;         // backward: dP in, dS = P (dP - sum P dP) scale out (0 for j > i)
+  int t, nh;
+  float scale;
+};
+
+struct MGroupArgs {
+  const float* dkh;  // [nh x t x hd] per-head gradients
+  const float* dvh;
+  float* dk;         // [t x nkv x hd]: sum of the group's heads, in head order
+  float* dv;
+  int t, nh, nkv, hd;
+};
+
+struct MEltArgs {
+  const float* a;
+  const float* b;
+  const float* c;
+  float* y;
+  float* z;
+  int64_t n;
+};

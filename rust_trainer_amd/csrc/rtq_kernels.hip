@@ -2298,3 +2298,6 @@ extern "C" __global__ __launch_bounds__(256) void rtq_head_norm_bwd(HeadArgs a) 
     }
   }
 }
+
+// ============================================================== decoder block (model-level step)
+#include "rtq_model_kernels.hip"

@@ -1,0 +1,596 @@
+// rtq_model.cpp — the device-resident training step over the frozen linears (rtq_model_* in
+// include/rtq.h): a GGUF Qwen / Llama decoder loaded into HBM, LoRA adapters on its projections,
+// and Model::forward_backward (src/model.rs:615-687) with every activation kept on the device.
+//
+// Reference structure restated (files under the reference repository):
+//   load_gguf_from        src/rie.rs:164-260 (tensor names, tied head, kv_f16, QK-norm detection)
+//   Model::attach_lora    src/model.rs:406-419, Lora::new src/linear.rs:21-25 (A ~ U(+-1/sqrt(in)), B = 0)
+//   forward_backward      src/model.rs:644-687 (embed, blocks, head, blocks in reverse)
+//   Block / Attention / Mlp src/model.rs:165-197, src/attention.rs:162-367, src/model.rs:113-134
+// The reference recomputes each block's forward in the backward (checkpointing) to save memory;
+// the recomputation reproduces the same values, so here every block's activations are simply kept
+// (config-3 shapes: 60 MB per layer).
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "rtq_internal.h"
+#include "rtq_kargs.h"
+
+namespace {
+
+enum { LQ, LK, LV, LO, LGATE, LUP, LDOWN, NLIN };
+const char* const kLinName[NLIN] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
+
+#define M_TRY(expr)              \
+  do {                           \
+    rtq_status s_ = (expr);      \
+    if (s_ != RTQ_OK) return s_; \
+  } while (0)
+#define M_HIP(expr)                                                                                     \
+  do {                                                                                                  \
+    hipError_t e_ = (expr);                                                                             \
+    if (e_ != hipSuccess) return rtq_fail(RTQ_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_));         \
+  } while (0)
+
+struct Lin {
+  rtq_weight* w = nullptr;
+  const float* bias = nullptr;  // device, or null
+  int64_t out = 0, in = 0;
+  int64_t rank = 0;  // 0: no adapter
+  float alpha = 0.0f;
+  float *A = nullptr, *B = nullptr, *ga = nullptr, *gb = nullptr;
+};
+
+struct Layer {
+  const float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+  Lin lin[NLIN];
+};
+
+// activations of one block, kept for its backward
+struct Cache {
+  float *n1, *inv1, *q_raw, *k_raw, *v_raw, *q, *k, *v, *q_inv, *k_inv, *P, *o, *h, *n2, *inv2, *g, *u, *hm;
+};
+
+// SplitMix64 + uniform of the reference Rng (src/tensor.rs:155-180)
+struct Rng {
+  uint64_t s;
+  explicit Rng(uint64_t seed) : s(seed ^ 0x9E3779B97F4A7C15ULL) {}
+  uint64_t next() {
+    s += 0x9E3779B97F4A7C15ULL;
+    uint64_t z = s;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+  }
+  float uniform() { return (float)(next() >> 40) / (float)(1u << 24); }
+  float uniform_sym(float bound) { return (uniform() * 2.0f - 1.0f) * bound; }
+};
+
+}  // namespace
+
+struct rtq_model {
+  rtq_ctx* ctx = nullptr;
+  rtq_model_config cfg{};
+  rtq_weight* embed = nullptr;
+  rtq_weight* head = nullptr;  // == embed when tied
+  const float* out_norm = nullptr;
+  std::vector<Layer> layers;
+  std::vector<void*> owned;  // device allocations of weights, norms, biases and adapters
+  std::vector<rtq_weight*> weights;
+  // step buffers, sized for t_cap tokens and n_cap targets
+  int64_t t_cap = 0, n_cap = 0;
+  void* step_mem = nullptr;
+  float *X = nullptr, *cos_ = nullptr, *sin_ = nullptr;
+  std::vector<Cache> cache;
+  float *dY, *dX, *mo, *f, *dhm, *dg, *du, *dn2, *dxu, *dh, *d_o, *dP, *dq, *dkh, *dvh, *dk, *dv, *dq_raw, *dk_raw,
+      *dn1, *dxk, *dxv;
+  int32_t *tok_d = nullptr, *pos_d = nullptr, *tgt_d = nullptr, *hit_d = nullptr;
+  float *wts_d = nullptr, *logp_d = nullptr;
+  int64_t rope_t = -1;  // t of the uploaded RoPE tables
+};
+
+namespace {
+
+rtq_status dev_alloc(rtq_model* m, size_t bytes, void** out) {
+  M_HIP(hipMalloc(out, bytes ? bytes : 4));
+  m->owned.push_back(*out);
+  return RTQ_OK;
+}
+
+rtq_status upload_vec(rtq_model* m, const rtq_gguf* g, const std::string& name, int64_t n, const float** out,
+                      bool required) {
+  *out = nullptr;
+  const int64_t i = rtq_gguf_find_tensor(g, name.c_str());
+  if (i < 0) return required ? rtq_fail(RTQ_ERR_INVALID, "GGUF: missing tensor %s", name.c_str()) : RTQ_OK;
+  int type = 0, nd = 0;
+  int64_t ne[4];
+  const void* data = nullptr;
+  size_t nbytes = 0;
+  M_TRY(rtq_gguf_tensor(g, i, nullptr, &type, &nd, ne, &data, &nbytes));
+  if (type != RTQ_TYPE_F32 || nbytes != (size_t)n * 4)
+    return rtq_fail(RTQ_ERR_UNSUPPORTED, "GGUF: %s must be F32 with %lld elements", name.c_str(), (long long)n);
+  void* d;
+  M_TRY(dev_alloc(m, nbytes, &d));
+  M_HIP(hipMemcpy(d, data, nbytes, hipMemcpyHostToDevice));
+  *out = (const float*)d;
+  return RTQ_OK;
+}
+
+double kv_num(const rtq_gguf* g, const std::string& key, double dflt) {
+  double v = 0.0;
+  return rtq_gguf_get_f64(g, key.c_str(), &v) == RTQ_OK ? v : dflt;
+}
+
+rtq_status load_weight(rtq_model* m, const rtq_gguf* g, const std::string& name, int64_t out, int64_t in,
+                       rtq_weight** w) {
+  M_TRY(rtq_weight_from_gguf(m->ctx, g, name.c_str(), w));
+  m->weights.push_back(*w);
+  if (rtq_weight_out_dim(*w) != out || rtq_weight_in_dim(*w) != in)
+    return rtq_fail(RTQ_ERR_INVALID, "GGUF: %s is %lldx%lld, expected %lldx%lld", name.c_str(),
+                    (long long)rtq_weight_out_dim(*w), (long long)rtq_weight_in_dim(*w), (long long)out, (long long)in);
+  return RTQ_OK;
+}
+
+hipStream_t stream_of(rtq_model* m) { return (hipStream_t)rtq_ctx_stream(m->ctx); }
+
+// ---------------------------------------------------------------- launches
+rtq_status k_norm(rtq_model* m, const float* a, const float* b, float* h, const float* w, float* y, float* inv,
+                  int64_t rows, int64_t d, int fused) {
+  MNormArgs na{a, b, h, w, y, inv, (int)rows, (int)d, m->cfg.rms_eps, m->cfg.norm_offset, fused};
+  return rtq_model_launch(m->ctx, KM_RMSNORM, dim3((unsigned)rows), dim3(256), stream_of(m), &na);
+}
+
+rtq_status k_norm_bwd(rtq_model* m, const float* x, const float* w, const float* inv, const float* dy, const float* res,
+                      float* out, int64_t rows, int64_t d) {
+  MNormBwdArgs na{x, w, inv, dy, res, out, (int)rows, (int)d, m->cfg.norm_offset};
+  return rtq_model_launch(m->ctx, KM_RMSNORM_BWD, dim3((unsigned)rows), dim3(256), stream_of(m), &na);
+}
+
+rtq_status k_elt(rtq_model* m, int km, const float* a, const float* b, const float* c, float* y, float* z, int64_t n) {
+  MEltArgs ea{a, b, c, y, z, n};
+  const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 4096);
+  return rtq_model_launch(m->ctx, km, dim3(grid), dim3(256), stream_of(m), &ea);
+}
+
+struct Op {  // one GEMM operand: base, batch stride and divisor, row / column strides
+  const float* p;
+  int64_t sb, s0, s1;
+  int div;
+};
+
+// C(b, m, n) (+)= sum_k A(b, m, k) B(b, k, n) for b < batch
+rtq_status k_gemm(rtq_model* m, int64_t M, int64_t N, int64_t K, int64_t batch, Op A, Op B, float* C, int64_t sCb,
+                  int64_t sCm, int64_t sCn, float a_scale, int causal, int acc) {
+  MGemmArgs ga{A.p,   B.p,   C,     (int)M, (int)N, (int)K, A.sb,  A.s0,     A.s1, B.sb, B.s0,
+               B.s1,  sCb,   sCm,   sCn,    A.div,  B.div,  a_scale, causal, acc};
+  return rtq_model_launch(m->ctx, KM_GEMM, dim3((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64), (unsigned)batch),
+                          dim3(256), stream_of(m), &ga);
+}
+
+rtq_lora lora_view(const Lin& l) { return rtq_lora{l.rank, l.alpha, l.A, l.B, l.rank > 0 ? 1 : 0}; }
+
+rtq_status lin_fwd(rtq_model* m, const Lin& l, const float* x, int64_t t, float* y) {
+  const rtq_lora lv = lora_view(l);
+  return rtq_linear_forward_d(m->ctx, l.w, l.bias, l.rank > 0 ? &lv : nullptr, x, t, y, stream_of(m));
+}
+
+rtq_status lin_bwd(rtq_model* m, const Lin& l, const float* x, const float* dy, int64_t t, float* dx) {
+  const rtq_lora lv = lora_view(l);
+  return rtq_linear_backward_d(m->ctx, l.w, l.rank > 0 ? &lv : nullptr, x, dy, t, dx, l.ga, l.gb, stream_of(m));
+}
+
+// ---------------------------------------------------------------- step buffers
+rtq_status ensure_step(rtq_model* m, int64_t t, int64_t n) {
+  if (t <= m->t_cap && n <= m->n_cap) return RTQ_OK;
+  const rtq_model_config& c = m->cfg;
+  const int64_t T = std::max(t, m->t_cap), N = std::max<int64_t>(std::max(n, m->n_cap), 1);
+  const int64_t d = c.n_embd, qd = c.n_head * c.head_dim, kd = c.n_head_kv * c.head_dim, ff = c.n_ff;
+  const int64_t half = c.rope_dim / 2, L = c.n_layer;
+  const int64_t att = c.n_head * T * T, hdh = c.n_head * T * c.head_dim;
+  std::vector<std::pair<float**, int64_t>> f;  // (pointer, floats)
+  f.push_back({&m->X, (L + 1) * T * d});
+  f.push_back({&m->cos_, T * half + 1});
+  f.push_back({&m->sin_, T * half + 1});
+  m->cache.assign((size_t)L, Cache{});
+  for (auto& k : m->cache) {
+    for (auto pr : std::initializer_list<std::pair<float**, int64_t>>{
+             {&k.n1, T * d},   {&k.inv1, T},     {&k.q_raw, T * qd}, {&k.k_raw, T * kd}, {&k.v_raw, T * kd},
+             {&k.q, T * qd},   {&k.k, T * kd},   {&k.v, T * kd},     {&k.q_inv, T * c.n_head},
+             {&k.k_inv, T * c.n_head_kv},        {&k.P, att},        {&k.o, T * qd},     {&k.h, T * d},
+             {&k.n2, T * d},   {&k.inv2, T},     {&k.g, T * ff},     {&k.u, T * ff},     {&k.hm, T * ff}})
+      f.push_back(pr);
+  }
+  for (auto pr : std::initializer_list<std::pair<float**, int64_t>>{
+           {&m->dY, T * d},   {&m->dX, T * d},    {&m->mo, T * d},   {&m->f, T * d},      {&m->dhm, T * ff},
+           {&m->dg, T * ff},  {&m->du, T * ff},   {&m->dn2, T * d},  {&m->dxu, T * d},    {&m->dh, T * d},
+           {&m->d_o, T * qd}, {&m->dP, att},      {&m->dq, T * qd},  {&m->dkh, hdh},      {&m->dvh, hdh},
+           {&m->dk, T * kd},  {&m->dv, T * kd},   {&m->dq_raw, T * qd}, {&m->dk_raw, T * kd}, {&m->dn1, T * d},
+           {&m->dxk, T * d},  {&m->dxv, T * d},   {&m->wts_d, N},    {&m->logp_d, N}})
+    f.push_back(pr);
+  size_t bytes = 0;
+  for (auto& pr : f) bytes += ((size_t)pr.second * 4 + 255) / 256 * 256;
+  const size_t ibytes = ((size_t)T * 4 + 255) / 256 * 256 + 3 * (((size_t)N * 4 + 255) / 256 * 256);
+  if (m->step_mem) {
+    M_HIP(hipStreamSynchronize(stream_of(m)));
+    M_HIP(hipFree(m->step_mem));
+    m->step_mem = nullptr;
+  }
+  m->t_cap = m->n_cap = 0;
+  M_HIP(hipMalloc(&m->step_mem, bytes + ibytes));
+  char* p = (char*)m->step_mem;
+  for (auto& pr : f) {
+    *pr.first = (float*)p;
+    p += ((size_t)pr.second * 4 + 255) / 256 * 256;
+  }
+  m->tok_d = (int32_t*)p;
+  p += ((size_t)T * 4 + 255) / 256 * 256;
+  for (int32_t** q : {&m->pos_d, &m->tgt_d, &m->hit_d}) {
+    *q = (int32_t*)p;
+    p += ((size_t)N * 4 + 255) / 256 * 256;
+  }
+  m->t_cap = T;
+  m->n_cap = N;
+  m->rope_t = -1;
+  return RTQ_OK;
+}
+
+// RoPE tables for positions 0..t-1 (Rope::with, src/ops.rs:136-167), computed in f32 on the host
+rtq_status ensure_rope(rtq_model* m, int64_t t) {
+  if (m->rope_t == t) return RTQ_OK;
+  const rtq_model_config& c = m->cfg;
+  const int64_t half = c.rope_dim / 2;
+  std::vector<float> cs((size_t)(t * half)), sn((size_t)(t * half));
+  for (int64_t i = 0; i < half; i++) {
+    const float fr = powf(c.rope_base, -2.0f * (float)i / (float)c.rope_dim) * c.rope_freq_scale;
+    for (int64_t p = 0; p < t; p++) {
+      const float a = (float)p * fr;
+      cs[(size_t)(p * half + i)] = cosf(a);
+      sn[(size_t)(p * half + i)] = sinf(a);
+    }
+  }
+  M_HIP(hipMemcpyAsync(m->cos_, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, stream_of(m)));
+  M_HIP(hipMemcpyAsync(m->sin_, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, stream_of(m)));
+  M_HIP(hipStreamSynchronize(stream_of(m)));  // the host tables go out of scope
+  m->rope_t = t;
+  return RTQ_OK;
+}
+
+// ---------------------------------------------------------------- one block
+MQkArgs qk_args(rtq_model* m, const Layer& L, Cache& k, int64_t t) {
+  const rtq_model_config& c = m->cfg;
+  return MQkArgs{k.q_raw,   k.k_raw,   k.v_raw,   L.q_norm, L.k_norm, m->cos_,        m->sin_,
+                 k.q,       k.k,       k.v,       k.q_inv,  k.k_inv,  m->dq,          m->dk,
+                 m->dq_raw, m->dk_raw, (int)t,    (int)c.n_head,      (int)c.n_head_kv, (int)c.head_dim,
+                 (int)c.rope_dim,      c.rope_neox, c.kv_f16,         c.rms_eps,        c.norm_offset};
+}
+
+rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* y) {
+  const rtq_model_config& c = m->cfg;
+  const Layer& L = m->layers[(size_t)l];
+  Cache& k = m->cache[(size_t)l];
+  const int64_t d = c.n_embd, nh = c.n_head, nkv = c.n_head_kv, hd = c.head_dim, grp = nh / nkv;
+  const int64_t qd = nh * hd, kd = nkv * hd;
+  M_TRY(k_norm(m, x, nullptr, nullptr, L.attn_norm, k.n1, k.inv1, t, d, 0));
+  M_TRY(lin_fwd(m, L.lin[LQ], k.n1, t, k.q_raw));
+  M_TRY(lin_fwd(m, L.lin[LK], k.n1, t, k.k_raw));
+  M_TRY(lin_fwd(m, L.lin[LV], k.n1, t, k.v_raw));
+  const MQkArgs qa = qk_args(m, L, k, t);
+  M_TRY(rtq_model_launch(m->ctx, KM_QK_PREP, dim3((unsigned)((t * (nh + 2 * nkv) + 3) / 4)), dim3(256), stream_of(m),
+                         &qa));
+  const float scale = 1.0f / sqrtf((float)hd);
+  // S = (q scale) K^T per head (causal), softmax in place, O = P V
+  M_TRY(k_gemm(m, t, t, hd, nh, Op{k.q, hd, qd, 1, 1}, Op{k.k, hd, 1, kd, (int)grp}, k.P, t * t, t, 1, scale, 1, 0));
+  MSoftArgs sa{k.P, nullptr, nullptr, (int)t, (int)nh, scale};
+  M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX, dim3((unsigned)t, (unsigned)nh), dim3(256), stream_of(m), &sa));
+  M_TRY(k_gemm(m, t, hd, t, nh, Op{k.P, t * t, t, 1, 1}, Op{k.v, hd, kd, 1, (int)grp}, k.o, hd, qd, 1, 1.0f, 2, 0));
+  M_TRY(lin_fwd(m, L.lin[LO], k.o, t, m->mo));
+  M_TRY(k_norm(m, x, m->mo, k.h, L.ffn_norm, k.n2, k.inv2, t, d, 0));  // h = x + attn, n2 = rmsnorm(h)
+  M_TRY(lin_fwd(m, L.lin[LGATE], k.n2, t, k.g));
+  M_TRY(lin_fwd(m, L.lin[LUP], k.n2, t, k.u));
+  M_TRY(k_elt(m, KM_SWIGLU, k.g, k.u, nullptr, k.hm, nullptr, t * c.n_ff));
+  M_TRY(lin_fwd(m, L.lin[LDOWN], k.hm, t, m->f));
+  return k_elt(m, KM_ADD, k.h, m->f, nullptr, y, nullptr, t * d);  // y = h + mlp
+}
+
+rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const float* dy, float* dx) {
+  const rtq_model_config& c = m->cfg;
+  const Layer& L = m->layers[(size_t)l];
+  Cache& k = m->cache[(size_t)l];
+  const int64_t d = c.n_embd, nh = c.n_head, nkv = c.n_head_kv, hd = c.head_dim, grp = nh / nkv;
+  const int64_t qd = nh * hd, kd = nkv * hd;
+  const float scale = 1.0f / sqrtf((float)hd);
+  // Mlp::backward (src/model.rs:120-133)
+  M_TRY(lin_bwd(m, L.lin[LDOWN], k.hm, dy, t, m->dhm));
+  M_TRY(k_elt(m, KM_SWIGLU_BWD, k.g, k.u, m->dhm, m->dg, m->du, t * c.n_ff));
+  M_TRY(lin_bwd(m, L.lin[LGATE], k.n2, m->dg, t, m->dn2));
+  M_TRY(lin_bwd(m, L.lin[LUP], k.n2, m->du, t, m->dxu));
+  M_TRY(k_elt(m, KM_ADD, m->dn2, m->dxu, nullptr, m->dn2, nullptr, t * d));
+  M_TRY(k_norm_bwd(m, k.h, L.ffn_norm, k.inv2, m->dn2, dy, m->dh, t, d));  // dh = dy + rmsnorm_backward
+  // Attention::backward (src/attention.rs:243-355)
+  M_TRY(lin_bwd(m, L.lin[LO], k.o, m->dh, t, m->d_o));
+  M_TRY(k_gemm(m, t, t, hd, nh, Op{m->d_o, hd, qd, 1, 1}, Op{k.v, hd, 1, kd, (int)grp}, m->dP, t * t, t, 1, 1.0f, 1,
+               0));  // dP = dO V^T
+  MSoftArgs sa{nullptr, k.P, m->dP, (int)t, (int)nh, scale};
+  M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX_BWD, dim3((unsigned)t, (unsigned)nh), dim3(256), stream_of(m), &sa));
+  M_TRY(k_gemm(m, t, hd, t, nh, Op{k.P, t * t, 1, t, 1}, Op{m->d_o, hd, qd, 1, 1}, m->dvh, t * hd, hd, 1, 1.0f, 3,
+               0));  // dV_h = P^T dO
+  M_TRY(k_gemm(m, t, hd, t, nh, Op{m->dP, t * t, t, 1, 1}, Op{k.k, hd, kd, 1, (int)grp}, m->dq, hd, qd, 1, 1.0f, 2,
+               0));  // dQ = dS K
+  M_TRY(k_gemm(m, t, hd, t, nh, Op{m->dP, t * t, 1, t, 1}, Op{k.q, hd, qd, 1, 1}, m->dkh, t * hd, hd, 1, 1.0f, 3,
+               0));  // dK_h = dS^T Q
+  MGroupArgs gsa{m->dkh, m->dvh, m->dk, m->dv, (int)t, (int)nh, (int)nkv, (int)hd};
+  M_TRY(rtq_model_launch(m->ctx, KM_GROUP_SUM, dim3((unsigned)std::min<int64_t>((t * kd + 255) / 256, 4096)),
+                         dim3(256), stream_of(m), &gsa));
+  const MQkArgs qa = qk_args(m, L, k, t);
+  M_TRY(rtq_model_launch(m->ctx, KM_QK_BWD, dim3((unsigned)((t * (nh + nkv) + 3) / 4)), dim3(256), stream_of(m), &qa));
+  M_TRY(lin_bwd(m, L.lin[LQ], k.n1, m->dq_raw, t, m->dn1));
+  M_TRY(lin_bwd(m, L.lin[LK], k.n1, m->dk_raw, t, m->dxk));
+  M_TRY(lin_bwd(m, L.lin[LV], k.n1, m->dv, t, m->dxv));
+  M_TRY(k_elt(m, KM_ADD, m->dn1, m->dxk, m->dxv, m->dn1, nullptr, t * d));  // dq + (dk + dv)
+  return k_norm_bwd(m, x, L.attn_norm, k.inv1, m->dn1, m->dh, dx, t, d);    // dx = dh + rmsnorm_backward
+}
+
+}  // namespace
+
+extern "C" {
+
+rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out) {
+  if (!ctx || !g || !out) return rtq_fail(RTQ_ERR_INVALID, "null ctx/gguf/out");
+  *out = nullptr;
+  const char* arch_p = nullptr;
+  uint64_t arch_n = 0;
+  M_TRY(rtq_gguf_get_str(g, "general.architecture", &arch_p, &arch_n));
+  const std::string arch(arch_p, arch_n);
+  rtq_model* m = new rtq_model();
+  m->ctx = ctx;
+  rtq_model_config& c = m->cfg;
+  c.n_layer = (int64_t)kv_num(g, arch + ".block_count", 0);
+  c.n_embd = (int64_t)kv_num(g, arch + ".embedding_length", 0);
+  c.n_head = (int64_t)kv_num(g, arch + ".attention.head_count", 0);
+  c.n_head_kv = (int64_t)kv_num(g, arch + ".attention.head_count_kv", (double)c.n_head);
+  c.head_dim = (int64_t)kv_num(g, arch + ".attention.key_length", c.n_head ? (double)(c.n_embd / c.n_head) : 0);
+  c.rope_dim = (int64_t)kv_num(g, arch + ".rope.dimension_count", (double)c.head_dim);
+  c.n_ff = (int64_t)kv_num(g, arch + ".feed_forward_length", 0);
+  c.rms_eps = (float)kv_num(g, arch + ".attention.layer_norm_rms_epsilon", 1e-6);
+  c.rope_base = (float)kv_num(g, arch + ".rope.freq_base", 10000.0);
+  c.rope_freq_scale = 1.0f;
+  c.norm_offset = 0.0f;
+  c.rope_neox = arch != "llama";  // Qwen GGUFs rotate NEOX pairs, Llama GGUFs adjacent pairs
+  c.kv_f16 = 1;                   // the loader's AttnConfig { kv_f16: true } (src/rie.rs:201)
+  const int64_t te = rtq_gguf_find_tensor(g, "token_embd.weight");
+  rtq_status st = RTQ_OK;
+  auto fail_out = [&](rtq_status s) {
+    rtq_model_destroy(m);
+    return s;
+  };
+  if (te < 0) return fail_out(rtq_fail(RTQ_ERR_INVALID, "GGUF: missing token_embd.weight"));
+  {
+    int64_t ne[4];
+    int nd = 0;
+    if ((st = rtq_gguf_tensor(g, te, nullptr, nullptr, &nd, ne, nullptr, nullptr)) != RTQ_OK) return fail_out(st);
+    c.n_vocab = nd >= 2 ? ne[1] : 0;
+  }
+  if (c.n_layer <= 0 || c.n_embd <= 0 || c.n_head <= 0 || c.n_head_kv <= 0 || c.n_head % c.n_head_kv ||
+      c.head_dim <= 0 || c.head_dim > 512 || c.rope_dim <= 0 || c.rope_dim > c.head_dim || c.rope_dim % 2 ||
+      c.n_ff <= 0 || c.n_vocab <= 0)
+    return fail_out(rtq_fail(RTQ_ERR_UNSUPPORTED, "GGUF %s: unsupported or missing model hyper-parameters",
+                             arch.c_str()));
+  c.qk_norm = rtq_gguf_find_tensor(g, "blk.0.attn_q_norm.weight") >= 0;
+  c.tied = rtq_gguf_find_tensor(g, "output.weight") < 0;
+  const int64_t d = c.n_embd, qd = c.n_head * c.head_dim, kd = c.n_head_kv * c.head_dim;
+  if ((st = load_weight(m, g, "token_embd.weight", c.n_vocab, d, &m->embed)) != RTQ_OK) return fail_out(st);
+  if (c.tied) {
+    m->head = m->embed;
+  } else if ((st = load_weight(m, g, "output.weight", c.n_vocab, d, &m->head)) != RTQ_OK) {
+    return fail_out(st);
+  }
+  if ((st = upload_vec(m, g, "output_norm.weight", d, &m->out_norm, true)) != RTQ_OK) return fail_out(st);
+  m->layers.resize((size_t)c.n_layer);
+  const int64_t outs[NLIN] = {qd, kd, kd, d, c.n_ff, c.n_ff, d}, ins[NLIN] = {d, d, d, qd, d, d, c.n_ff};
+  for (int64_t l = 0; l < c.n_layer; l++) {
+    Layer& L = m->layers[(size_t)l];
+    const std::string p = "blk." + std::to_string(l) + ".";
+    if (rtq_gguf_find_tensor(g, (p + "post_attention_norm.weight").c_str()) >= 0 ||
+        rtq_gguf_find_tensor(g, (p + "post_ffw_norm.weight").c_str()) >= 0)
+      return fail_out(rtq_fail(RTQ_ERR_UNSUPPORTED, "post-norm layers are not supported"));  // src/rie.rs:204-206
+    if ((st = upload_vec(m, g, p + "attn_norm.weight", d, &L.attn_norm, true)) != RTQ_OK ||
+        (st = upload_vec(m, g, p + "ffn_norm.weight", d, &L.ffn_norm, true)) != RTQ_OK ||
+        (st = upload_vec(m, g, p + "attn_q_norm.weight", c.head_dim, &L.q_norm, c.qk_norm)) != RTQ_OK ||
+        (st = upload_vec(m, g, p + "attn_k_norm.weight", c.head_dim, &L.k_norm, c.qk_norm)) != RTQ_OK)
+      return fail_out(st);
+    for (int i = 0; i < NLIN; i++) {
+      Lin& ln = L.lin[i];
+      ln.out = outs[i];
+      ln.in = ins[i];
+      if ((st = load_weight(m, g, p + kLinName[i] + ".weight", ln.out, ln.in, &ln.w)) != RTQ_OK) return fail_out(st);
+      if (i <= LV && (st = upload_vec(m, g, p + kLinName[i] + ".bias", ln.out, &ln.bias, false)) != RTQ_OK)
+        return fail_out(st);
+    }
+  }
+  *out = m;
+  return RTQ_OK;
+}
+
+void rtq_model_destroy(rtq_model* m) {
+  if (!m) return;
+  (void)hipSetDevice(rtq_ctx_device_id(m->ctx));
+  (void)hipStreamSynchronize(stream_of(m));
+  for (rtq_weight* w : m->weights) rtq_weight_destroy(w);
+  for (void* p : m->owned) (void)hipFree(p);
+  if (m->step_mem) (void)hipFree(m->step_mem);
+  delete m;
+}
+
+rtq_status rtq_model_get_config(const rtq_model* m, rtq_model_config* out) {
+  if (!m || !out) return rtq_fail(RTQ_ERR_INVALID, "null model/out");
+  *out = m->cfg;
+  return RTQ_OK;
+}
+
+rtq_status rtq_model_attach_lora(rtq_model* m, int64_t rank, float alpha, uint32_t target_mask, uint64_t seed,
+                                 int64_t* n_params) {
+  if (!m || rank <= 0 || rank > 4096) return rtq_fail(RTQ_ERR_INVALID, "bad model/rank");
+  M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
+  Rng rng(seed);
+  int64_t n = 0;
+  for (Layer& L : m->layers)
+    for (int i = 0; i < NLIN; i++) {
+      if (!(target_mask >> i & 1u)) continue;
+      Lin& ln = L.lin[i];
+      const float bound = 1.0f / sqrtf((float)ln.in);
+      std::vector<float> a((size_t)(rank * ln.in));
+      for (float& v : a) v = rng.uniform_sym(bound);
+      void *A, *B, *ga, *gb;
+      M_TRY(dev_alloc(m, a.size() * 4, &A));
+      M_TRY(dev_alloc(m, (size_t)(ln.out * rank) * 4, &B));
+      M_TRY(dev_alloc(m, a.size() * 4, &ga));
+      M_TRY(dev_alloc(m, (size_t)(ln.out * rank) * 4, &gb));
+      M_HIP(hipMemcpy(A, a.data(), a.size() * 4, hipMemcpyHostToDevice));
+      M_HIP(hipMemset(B, 0, (size_t)(ln.out * rank) * 4));
+      M_HIP(hipMemset(ga, 0, a.size() * 4));
+      M_HIP(hipMemset(gb, 0, (size_t)(ln.out * rank) * 4));
+      ln.rank = rank;
+      ln.alpha = alpha;
+      ln.A = (float*)A;
+      ln.B = (float*)B;
+      ln.ga = (float*)ga;
+      ln.gb = (float*)gb;
+      n += rank * (ln.in + ln.out);
+    }
+  if (n_params) *n_params = n;
+  return RTQ_OK;
+}
+
+int64_t rtq_model_lora_count(const rtq_model* m) {
+  int64_t n = 0;
+  if (m)
+    for (const Layer& L : m->layers)
+      for (const Lin& ln : L.lin) n += ln.rank > 0;
+  return n;
+}
+
+namespace {
+Lin* lora_at(rtq_model* m, int64_t i, int* layer, int* which) {
+  if (!m || i < 0) return nullptr;
+  for (size_t l = 0; l < m->layers.size(); l++)
+    for (int k = 0; k < NLIN; k++)
+      if (m->layers[l].lin[k].rank > 0 && i-- == 0) {
+        if (layer) *layer = (int)l;
+        if (which) *which = k;
+        return &m->layers[l].lin[k];
+      }
+  return nullptr;
+}
+}  // namespace
+
+rtq_status rtq_model_lora_info(const rtq_model* m, int64_t i, int* layer, int* which, int64_t* rank, int64_t* in,
+                               int64_t* out, float* alpha) {
+  Lin* ln = lora_at(const_cast<rtq_model*>(m), i, layer, which);
+  if (!ln) return rtq_fail(RTQ_ERR_INVALID, "adapter %lld out of range", (long long)i);
+  if (rank) *rank = ln->rank;
+  if (in) *in = ln->in;
+  if (out) *out = ln->out;
+  if (alpha) *alpha = ln->alpha;
+  return RTQ_OK;
+}
+
+rtq_status rtq_model_lora_device(rtq_model* m, int64_t i, float** a, float** b, float** ga, float** gb) {
+  Lin* ln = lora_at(m, i, nullptr, nullptr);
+  if (!ln) return rtq_fail(RTQ_ERR_INVALID, "adapter %lld out of range", (long long)i);
+  if (a) *a = ln->A;
+  if (b) *b = ln->B;
+  if (ga) *ga = ln->ga;
+  if (gb) *gb = ln->gb;
+  return RTQ_OK;
+}
+
+rtq_status rtq_model_lora_get(rtq_model* m, int64_t i, float* a, float* b, float* ga, float* gb) {
+  Lin* ln = lora_at(m, i, nullptr, nullptr);
+  if (!ln) return rtq_fail(RTQ_ERR_INVALID, "adapter %lld out of range", (long long)i);
+  M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
+  M_HIP(hipStreamSynchronize(stream_of(m)));
+  const size_t na = (size_t)(ln->rank * ln->in) * 4, nb = (size_t)(ln->out * ln->rank) * 4;
+  if (a) M_HIP(hipMemcpy(a, ln->A, na, hipMemcpyDeviceToHost));
+  if (b) M_HIP(hipMemcpy(b, ln->B, nb, hipMemcpyDeviceToHost));
+  if (ga) M_HIP(hipMemcpy(ga, ln->ga, na, hipMemcpyDeviceToHost));
+  if (gb) M_HIP(hipMemcpy(gb, ln->gb, nb, hipMemcpyDeviceToHost));
+  return RTQ_OK;
+}
+
+rtq_status rtq_model_lora_set(rtq_model* m, int64_t i, const float* a, const float* b) {
+  Lin* ln = lora_at(m, i, nullptr, nullptr);
+  if (!ln) return rtq_fail(RTQ_ERR_INVALID, "adapter %lld out of range", (long long)i);
+  M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
+  M_HIP(hipStreamSynchronize(stream_of(m)));
+  if (a) M_HIP(hipMemcpy(ln->A, a, (size_t)(ln->rank * ln->in) * 4, hipMemcpyHostToDevice));
+  if (b) M_HIP(hipMemcpy(ln->B, b, (size_t)(ln->out * ln->rank) * 4, hipMemcpyHostToDevice));
+  return RTQ_OK;
+}
+
+rtq_status rtq_model_zero_grad(rtq_model* m) {
+  if (!m) return rtq_fail(RTQ_ERR_INVALID, "null model");
+  M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
+  for (Layer& L : m->layers)
+    for (Lin& ln : L.lin)
+      if (ln.rank > 0) {
+        M_HIP(hipMemsetAsync(ln.ga, 0, (size_t)(ln.rank * ln.in) * 4, stream_of(m)));
+        M_HIP(hipMemsetAsync(ln.gb, 0, (size_t)(ln.out * ln.rank) * 4, stream_of(m)));
+      }
+  M_HIP(hipStreamSynchronize(stream_of(m)));
+  return RTQ_OK;
+}
+
+rtq_status rtq_model_forward_backward(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* pos,
+                                      const int32_t* tok, const float* weights, int64_t n, float* logp,
+                                      int64_t* hits) {
+  if (!m || !tokens || t <= 0 || n < 0 || (n > 0 && (!pos || !tok || !logp)))
+    return rtq_fail(RTQ_ERR_INVALID, "null model/tokens/targets or empty sequence");
+  const rtq_model_config& c = m->cfg;
+  if (t > 65535) return rtq_fail(RTQ_ERR_INVALID, "sequence of %lld tokens too long", (long long)t);
+  for (int64_t i = 0; i < t; i++)
+    if (tokens[i] < 0 || tokens[i] >= c.n_vocab)
+      return rtq_fail(RTQ_ERR_INVALID, "token %d out of vocab", tokens[i]);  // src/model.rs:450
+  for (int64_t i = 0; i < n; i++)
+    if (pos[i] < 0 || pos[i] >= t || tok[i] < 0 || tok[i] >= c.n_vocab)
+      return rtq_fail(RTQ_ERR_INVALID, "target %lld out of range", (long long)i);  // src/model.rs:575
+  M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
+  M_TRY(ensure_step(m, t, n));
+  M_TRY(ensure_rope(m, t));
+  hipStream_t st = stream_of(m);
+  const int64_t d = c.n_embd;
+  M_HIP(hipMemcpyAsync(m->tok_d, tokens, (size_t)t * 4, hipMemcpyHostToDevice, st));
+  if (n > 0) {
+    M_HIP(hipMemcpyAsync(m->pos_d, pos, (size_t)n * 4, hipMemcpyHostToDevice, st));
+    M_HIP(hipMemcpyAsync(m->tgt_d, tok, (size_t)n * 4, hipMemcpyHostToDevice, st));
+    if (weights) M_HIP(hipMemcpyAsync(m->wts_d, weights, (size_t)n * 4, hipMemcpyHostToDevice, st));
+  }
+  M_TRY(rtq_frozen_gather_d(m->ctx, m->embed, m->tok_d, t, m->X, st));  // embed_tokens
+  for (int64_t l = 0; l < c.n_layer; l++) M_TRY(block_forward(m, (int)l, t, m->X + l * t * d, m->X + (l + 1) * t * d));
+  if (n > 0) {
+    M_TRY(rtq_lm_head_d(m->ctx, m->head, m->out_norm, c.rms_eps, c.norm_offset, m->X + c.n_layer * t * d, t,
+                        m->pos_d, m->tgt_d, weights ? m->wts_d : nullptr, n, m->logp_d, m->hit_d,
+                        weights ? m->dY : nullptr, st));
+    if (weights)
+      for (int64_t l = c.n_layer - 1; l >= 0; l--) {
+        M_TRY(block_backward(m, (int)l, t, m->X + l * t * d, m->dY, m->dX));
+        std::swap(m->dY, m->dX);
+      }
+    std::vector<int32_t> hv((size_t)n);
+    M_HIP(hipMemcpyAsync(logp, m->logp_d, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+    M_HIP(hipMemcpyAsync(hv.data(), m->hit_d, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+    M_HIP(hipStreamSynchronize(st));
+    if (hits) {
+      int64_t s = 0;
+      for (int32_t h : hv) s += h;
+      *hits = s;
+    }
+  } else {
+    M_HIP(hipStreamSynchronize(st));
+    if (hits) *hits = 0;
+  }
+  return RTQ_OK;
+}
+
+}  // extern "C"

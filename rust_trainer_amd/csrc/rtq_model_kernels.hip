@@ -1,0 +1,303 @@
+// rtq_model_kernels.hip — the decoder block around the frozen linears, for the device-resident
+// training step (rtq_model_* in include/rtq.h).  Included by rtq_kernels.hip (one code object).
+//
+// Reference operations restated (files under the reference repository):
+//   rmsnorm_ordered / rmsnorm_backward     src/ops.rs:14-56
+//   Rope::apply (NEOX / normal pairs)       src/ops.rs:178-196
+//   round_f16                               src/attention.rs:34-51
+//   Attention forward / backward            src/attention.rs:162-367 (causal GQA, probabilities kept)
+//   Mlp (SwiGLU), sigmoid / silu / grad     src/model.rs:113-134, src/tensor.rs:123-143
+// Arithmetic follows the reference's f32 operation order element by element; reductions (norm
+// sums, softmax sums, dot products) are tree-ordered.
+
+// ------------------------------------------------------------------ helpers
+__device__ __forceinline__ float m_round_f16(float x) {
+  const uint32_t b = __float_as_uint(x);
+  const uint32_t sign = b & 0x80000000u, abs_ = b & 0x7fffffffu;
+  if (abs_ >= 0x7f800000u) return x;
+  const int e = (int)(abs_ >> 23) - 127;
+  if (e > 15) return __uint_as_float(sign | 0x7f800000u);
+  const int q_exp = e < -14 ? -24 : e - 10;
+  const float q = __uint_as_float((uint32_t)(q_exp + 127) << 23);
+  const float r = __fmul_rn(rintf(__fdiv_rn(__uint_as_float(abs_), q)), q);
+  return __uint_as_float(sign | __float_as_uint(r));
+}
+
+__device__ __forceinline__ float m_sigmoid(float x) {
+  if (x >= 0.0f) return __fdiv_rn(1.0f, 1.0f + expf(-x));
+  const float e = expf(x);
+  return __fdiv_rn(e, 1.0f + e);
+}
+__device__ __forceinline__ float m_silu(float x) { return __fdiv_rn(x, 1.0f + expf(-x)); }
+__device__ __forceinline__ float m_silu_grad(float x) {
+  const float s = m_sigmoid(x);
+  return s * (1.0f + x * (1.0f - s));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+// ------------------------------------------------------------------ RMSNorm
+// grid rows, 256 threads: y = rmsnorm(a (+ b)); with b, h = a + b is written too
+extern "C" __global__ __launch_bounds__(256) void rtq_m_rmsnorm(MNormArgs a) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  const float* ar = a.a + (int64_t)r * a.d;
+  const float* br = a.b ? a.b + (int64_t)r * a.d : nullptr;
+  float* hr = a.b ? a.h + (int64_t)r * a.d : nullptr;
+  float s = 0.0f;
+  for (int k = threadIdx.x; k < a.d; k += 256) {
+    float x = ar[k];
+    if (br) {
+      x = x + br[k];
+      hr[k] = x;
+    }
+    s = s + x * x;
+  }
+  s = block_sum256(s, red);
+  const float ir = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(s, (float)a.d) + a.eps));
+  const float* xr = br ? hr : ar;
+  float* yr = a.y + (int64_t)r * a.d;
+  for (int k = threadIdx.x; k < a.d; k += 256) {
+    const float x = xr[k], wo = a.w[k] + a.off;
+    yr[k] = a.fused ? x * (ir * wo) : (x * ir) * wo;
+  }
+  if (threadIdx.x == 0) a.inv[r] = ir;
+}
+
+// grid rows, 256 threads: out = (res +) rmsnorm_backward(x, w, inv, dy)
+extern "C" __global__ __launch_bounds__(256) void rtq_m_rmsnorm_bwd(MNormBwdArgs a) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  const float* xr = a.x + (int64_t)r * a.d;
+  const float* dr = a.dy + (int64_t)r * a.d;
+  float s = 0.0f;
+  for (int k = threadIdx.x; k < a.d; k += 256) s = s + (dr[k] * (a.w[k] + a.off)) * xr[k];
+  s = block_sum256(s, red);
+  const float ir = a.inv[r];
+  const float c = __fdiv_rn(((s * ir) * ir) * ir, (float)a.d);
+  float* o = a.out + (int64_t)r * a.d;
+  const float* rr = a.res ? a.res + (int64_t)r * a.d : nullptr;
+  for (int k = threadIdx.x; k < a.d; k += 256) {
+    const float g = dr[k] * (a.w[k] + a.off);
+    const float v = g * ir - xr[k] * c;
+    o[k] = rr ? rr[k] + v : v;
+  }
+}
+
+// ------------------------------------------------------------------ QK-norm + RoPE + f16 K/V
+// One wave per (token, head) row of width hd (hd <= 512): rows [0, t nh) are q, then t nkv k rows,
+// then t nkv v rows.  LDS holds the normalised row so the RoPE pairs can be read across lanes.
+// rotates the row src into dst (sgn -1: the inverse rotation), rounding to f16 when rnd
+__device__ __forceinline__ void m_rope_row(const MQkArgs& a, const float* src, float* dst, int p, float sgn, bool rnd) {
+  const int half = a.rot / 2, lane = threadIdx.x & 63;
+  const float* cr = a.cos_ + (int64_t)p * half;
+  const float* sr = a.sin_ + (int64_t)p * half;
+  for (int i = lane; i < half; i += 64) {
+    const float c = cr[i], s = sgn * sr[i];
+    const int ia = a.neox ? i : 2 * i, ib = a.neox ? i + half : 2 * i + 1;
+    const float x1 = src[ia], x2 = src[ib];
+    const float y1 = x1 * c - x2 * s, y2 = x2 * c + x1 * s;
+    dst[ia] = rnd ? m_round_f16(y1) : y1;
+    dst[ib] = rnd ? m_round_f16(y2) : y2;
+  }
+  for (int e = a.rot + lane; e < a.hd; e += 64) dst[e] = rnd ? m_round_f16(src[e]) : src[e];
+}
+
+extern "C" __global__ __launch_bounds__(256) void rtq_m_qk_prep(MQkArgs a) {
+  __shared__ float buf[4][512];
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wv;
+  const int64_t nq = (int64_t)a.t * a.nh, nk = (int64_t)a.t * a.nkv;
+  if (row >= nq + 2 * nk) return;
+  float* sb = buf[wv];
+  if (row >= nq + nk) {  // v: f16 rounding only
+    const int64_t o = (row - nq - nk) * a.hd;
+    for (int e = lane; e < a.hd; e += 64) a.v[o + e] = a.kv_f16 ? m_round_f16(a.v_raw[o + e]) : a.v_raw[o + e];
+    return;
+  }
+  const bool isq = row < nq;
+  const int64_t r = isq ? row : row - nq;
+  const int heads = isq ? a.nh : a.nkv;
+  const int p = (int)(r / heads);
+  const float* x = (isq ? a.q_raw : a.k_raw) + r * a.hd;
+  const float* w = isq ? a.q_norm : a.k_norm;
+  if (w) {
+    float s = 0.0f;
+    for (int e = lane; e < a.hd; e += 64) s = s + x[e] * x[e];
+    s = wave_sum(s);
+    const float ir = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(s, (float)a.hd) + a.eps));
+    for (int e = lane; e < a.hd; e += 64) sb[e] = x[e] * (ir * (w[e] + a.off));
+    if (lane == 0) (isq ? a.q_inv : a.k_inv)[r] = ir;
+  } else {
+    for (int e = lane; e < a.hd; e += 64) sb[e] = x[e];
+  }
+  __builtin_amdgcn_wave_barrier();
+  m_rope_row(a, sb, (isq ? a.q : a.k) + r * a.hd, p, 1.0f, !isq && a.kv_f16);
+}
+
+// backward: dq_raw / dk_raw = rmsnorm_backward(inverse RoPE of dq / dk); rows [0, t nh) q, then k
+extern "C" __global__ __launch_bounds__(256) void rtq_m_qk_bwd(MQkArgs a) {
+  __shared__ float buf[4][512];
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wv;
+  const int64_t nq = (int64_t)a.t * a.nh, nk = (int64_t)a.t * a.nkv;
+  if (row >= nq + nk) return;
+  const bool isq = row < nq;
+  const int64_t r = isq ? row : row - nq;
+  const int heads = isq ? a.nh : a.nkv;
+  const int p = (int)(r / heads);
+  float* sb = buf[wv];
+  m_rope_row(a, (isq ? a.dq : a.dk) + r * a.hd, sb, p, -1.0f, false);
+  __builtin_amdgcn_wave_barrier();
+  float* out = (isq ? a.dq_raw : a.dk_raw) + r * a.hd;
+  const float* w = isq ? a.q_norm : a.k_norm;
+  if (!w) {
+    for (int e = lane; e < a.hd; e += 64) out[e] = sb[e];
+    return;
+  }
+  const float* x = (isq ? a.q_raw : a.k_raw) + r * a.hd;
+  const float ir = (isq ? a.q_inv : a.k_inv)[r];
+  float s = 0.0f;
+  for (int e = lane; e < a.hd; e += 64) s = s + (sb[e] * (w[e] + a.off)) * x[e];
+  s = wave_sum(s);
+  const float c = __fdiv_rn(((s * ir) * ir) * ir, (float)a.hd);
+  for (int e = lane; e < a.hd; e += 64) {
+    const float g = sb[e] * (w[e] + a.off);
+    out[e] = g * ir - x[e] * c;
+  }
+}
+
+// ------------------------------------------------------------------ batched f32 GEMM
+// 64 x 64 output tile per 256-thread workgroup, 16-deep k slices through LDS; thread (ty, tx) owns
+// rows m0 + ty + 16 i and columns n0 + tx + 16 j.  Operands are read with their own strides, the
+// unit-stride index fastest across lanes.
+extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm(MGemmArgs a) {
+  constexpr int BM = 64, BN = 64, BK = 16;
+  __shared__ float As[BK][BM + 4];
+  __shared__ float Bs[BK][BN + 4];
+  const int b = blockIdx.z, m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  if (a.causal == 1 && n0 > m0 + BM - 1) return;  // every element has n > m
+  const float* A = a.A + (int64_t)(b / a.divA) * a.sAb;
+  const float* B = a.B + (int64_t)(b / a.divB) * a.sBb;
+  int k0 = 0, k1 = a.K;
+  if (a.causal == 2) k1 = min(a.K, m0 + BM);
+  if (a.causal == 3) k0 = (m0 / BK) * BK;
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const bool a_kfast = a.sAk == 1, b_nfast = a.sBn == 1;
+  float acc[4][4] = {};
+  for (int kk = k0; kk < k1; kk += BK) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int e = threadIdx.x + 256 * i;
+      const int am = a_kfast ? e / BK : e % BM, ak = a_kfast ? e % BK : e / BM;
+      const int gm = m0 + am, gk = kk + ak;
+      float v = (gm < a.M && gk < k1) ? A[(int64_t)gm * a.sAm + (int64_t)gk * a.sAk] : 0.0f;
+      if (a.a_scale != 1.0f) v = v * a.a_scale;
+      As[ak][am] = v;
+      const int bn = b_nfast ? e % BN : e / BK, bk = b_nfast ? e / BN : e % BK;
+      const int gn = n0 + bn, gk2 = kk + bk;
+      Bs[bk][bn] = (gn < a.N && gk2 < k1) ? B[(int64_t)gk2 * a.sBk + (int64_t)gn * a.sBn] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < BK; k++) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) av[i] = As[k][ty + 16 * i];
+#pragma unroll
+      for (int j = 0; j < 4; j++) bv[j] = Bs[k][tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = acc[i][j] + av[i] * bv[j];
+    }
+    __syncthreads();
+  }
+  float* C = a.C + (int64_t)b * a.sCb;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int m = m0 + ty + 16 * i;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int n = n0 + tx + 16 * j;
+      if (n >= a.N) continue;
+      float* c = C + (int64_t)m * a.sCm + (int64_t)n * a.sCn;
+      *c = a.accumulate ? *c + acc[i][j] : acc[i][j];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ attention softmax
+// grid (t, nh): row i of head h over j <= i: p = exp(s - max) / sum (0 for j > i)
+extern "C" __global__ __launch_bounds__(256) void rtq_m_softmax(MSoftArgs a) {
+  __shared__ float red[4];
+  const int i = blockIdx.x, h = blockIdx.y;
+  float* row = a.s + ((int64_t)h * a.t + i) * a.t;
+  float m = -__builtin_inff();
+  for (int j = threadIdx.x; j <= i; j += 256) m = fmaxf(m, row[j]);
+  m = block_max256(m, red);
+  float s = 0.0f;
+  for (int j = threadIdx.x; j <= i; j += 256) s = s + expf(row[j] - m);
+  s = block_sum256(s, red);
+  const float inv = __fdiv_rn(1.0f, s);
+  for (int j = threadIdx.x; j < a.t; j += 256) row[j] = j <= i ? expf(row[j] - m) * inv : 0.0f;
+}
+
+// grid (t, nh): dS = (P (dP - sum_j P dP)) scale over j <= i, 0 beyond, written over dP
+extern "C" __global__ __launch_bounds__(256) void rtq_m_softmax_bwd(MSoftArgs a) {
+  __shared__ float red[4];
+  const int i = blockIdx.x, h = blockIdx.y;
+  const float* p = a.p + ((int64_t)h * a.t + i) * a.t;
+  float* dp = a.dp + ((int64_t)h * a.t + i) * a.t;
+  float s = 0.0f;
+  for (int j = threadIdx.x; j <= i; j += 256) s = s + p[j] * dp[j];
+  s = block_sum256(s, red);
+  for (int j = threadIdx.x; j < a.t; j += 256) dp[j] = j <= i ? (p[j] * (dp[j] - s)) * a.scale : 0.0f;
+}
+
+// dk / dv [t x nkv x hd] = sum over the group's heads (head order) of dkh / dvh [nh x t x hd]
+extern "C" __global__ __launch_bounds__(256) void rtq_m_group_sum(MGroupArgs a) {
+  const int64_t n = (int64_t)a.t * a.nkv * a.hd;
+  const int grp = a.nh / a.nkv;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < n; idx += (int64_t)gridDim.x * 256) {
+    const int e = (int)(idx % a.hd);
+    const int64_t ig = idx / a.hd;
+    const int g = (int)(ig % a.nkv);
+    const int64_t i = ig / a.nkv;
+    float sk = 0.0f, sv = 0.0f;
+    for (int h = g * grp; h < (g + 1) * grp; h++) {
+      const int64_t o = ((int64_t)h * a.t + i) * a.hd + e;
+      sk = sk + a.dkh[o];
+      sv = sv + a.dvh[o];
+    }
+    a.dk[idx] = sk;
+    a.dv[idx] = sv;
+  }
+}
+
+// ------------------------------------------------------------------ elementwise
+// SwiGLU forward: y = silu(a) * b
+extern "C" __global__ __launch_bounds__(256) void rtq_m_swiglu(MEltArgs a) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (int64_t)gridDim.x * 256)
+    a.y[i] = m_silu(a.a[i]) * a.b[i];
+}
+
+// SwiGLU backward: dg = (dh u) silu'(g) -> y, du = dh silu(g) -> z  (a = g, b = u, c = dh)
+extern "C" __global__ __launch_bounds__(256) void rtq_m_swiglu_bwd(MEltArgs a) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (int64_t)gridDim.x * 256) {
+    const float g = a.a[i], u = a.b[i], dh = a.c[i];
+    a.y[i] = (dh * u) * m_silu_grad(g);
+    a.z[i] = dh * m_silu(g);
+  }
+}
+
+// y = a + b, or a + (b + c) when c is given
+extern "C" __global__ __launch_bounds__(256) void rtq_m_add(MEltArgs a) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (int64_t)gridDim.x * 256)
+    a.y[i] = a.c ? a.a[i] + (a.b[i] + a.c[i]) : a.a[i] + a.b[i];
+}

@@ -21,6 +21,7 @@
 #include <string>
 #include <vector>
 
+#include "rtq_internal.h"
 #include "rtq_kargs.h"
 
 #ifndef RTQ_HSACO_PATH
@@ -135,7 +136,8 @@ enum Kid {
   K_HEAD_GRAD,
   K_HEAD_NORM_BWD,
   K_ROWS,        // + format
-  K_COUNT = K_ROWS + F_COUNT
+  K_MODEL = K_ROWS + F_COUNT,  // + RtqModelKernel: the decoder block (rtq_model.cpp)
+  K_COUNT = K_MODEL + KM_COUNT
 };
 const char* kKernelNames[K_COUNT] = {
     "rtq_fill_zero",        "rtq_act_prep_q8_0",    "rtq_act_prep_q8_k",
@@ -152,7 +154,10 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_dense_rows",       "rtq_dense_bias",
     "rtq_head_norm",        "rtq_head_max",         "rtq_head_sum",         "rtq_head_grad",
     "rtq_head_norm_bwd",
-    "rtq_rows_q4_0",        "rtq_rows_q8_0",        "rtq_rows_q4_k",        "rtq_rows_q6_k"};
+    "rtq_rows_q4_0",        "rtq_rows_q8_0",        "rtq_rows_q4_k",        "rtq_rows_q6_k",
+    "rtq_m_rmsnorm",        "rtq_m_rmsnorm_bwd",    "rtq_m_qk_prep",        "rtq_m_qk_bwd",
+    "rtq_m_gemm",           "rtq_m_softmax",        "rtq_m_softmax_bwd",    "rtq_m_group_sum",
+    "rtq_m_swiglu",         "rtq_m_swiglu_bwd",     "rtq_m_add"};
 
 struct TimedLaunch {
   int kid;
@@ -213,13 +218,11 @@ hipEvent_t get_event(rtq_ctx* c) {
   return e;
 }
 
-template <class Args>
-rtq_status launch(rtq_ctx* c, int kid, dim3 grid, dim3 block, hipStream_t s, const Args& args, unsigned shmem = 0) {
+rtq_status launch_raw(rtq_ctx* c, int kid, dim3 grid, dim3 block, hipStream_t s, void* argp, unsigned shmem) {
   if (grid.x == 0 || grid.y == 0 || grid.z == 0) return RTQ_OK;
   if (grid.y > 65535 || grid.z > 65535)
     return fail(RTQ_ERR_INVALID, "%s: grid (%u,%u,%u) out of range", kKernelNames[kid], grid.x, grid.y, grid.z);
-  Args copy = args;
-  void* params[] = {&copy};
+  void* params[] = {argp};
   hipEvent_t ea = nullptr, eb = nullptr;
   const bool timed = c->timing && (c->timing_only < 0 || c->timing_only == kid);
   if (timed) {
@@ -235,6 +238,12 @@ rtq_status launch(rtq_ctx* c, int kid, dim3 grid, dim3 block, hipStream_t s, con
     c->pending.push_back({kid, ea, eb});
   }
   return RTQ_OK;
+}
+
+template <class Args>
+rtq_status launch(rtq_ctx* c, int kid, dim3 grid, dim3 block, hipStream_t s, const Args& args, unsigned shmem = 0) {
+  Args copy = args;
+  return launch_raw(c, kid, grid, block, s, &copy, shmem);
 }
 
 // ------------------------------------------------------------------ workspace
@@ -792,7 +801,14 @@ void repack_kquant(int type, const uint8_t* src, int64_t N, int64_t K, int64_t N
 
 }  // namespace
 
-// error reporting shared with the other translation units of the library (rtq_gguf.cpp)
+rtq_status rtq_model_launch(rtq_ctx* c, int km, dim3 grid, dim3 block, hipStream_t s, const void* args) {
+  if (km < 0 || km >= KM_COUNT) return fail(RTQ_ERR_INVALID, "bad decoder kernel id %d", km);
+  return launch_raw(c, K_MODEL + km, grid, block, s, const_cast<void*>(args), 0);
+}
+
+int rtq_ctx_device_id(const rtq_ctx* c) { return c ? c->device : -1; }
+
+// error reporting shared with the other translation units of the library (rtq_gguf.cpp, rtq_model.cpp)
 rtq_status rtq_fail(rtq_status st, const char* fmt, ...) {
   char buf[512];
   va_list ap;
