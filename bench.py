@@ -447,6 +447,127 @@ def head_bench(steps: int, warmup: int, cpu_seconds: float, no_cpu: bool) -> Non
     print(json.dumps(result), flush=True)
 
 
+# ---------------------------------------------------------------- full training step
+STEP_T, STEP_N, STEP_R, STEP_ALPHA = 512, 256, 16, 32.0
+
+
+def model_flops(cfg: dict, t: int, n: int) -> tuple[float, dict]:
+    """Flops of one training step (forward + backward, activations kept): per block 2 t (params) for
+    each linear pass (forward, dx), the LoRA products, attention's causal products; the head's
+    forward and dx on the n target rows."""
+    d, nh, nkv, hd, ff, L, V = (cfg[k] for k in ("n_embd", "n_head", "n_head_kv", "head_dim", "n_ff", "n_layer",
+                                                  "n_vocab"))
+    lin = d * nh * hd + 2 * d * nkv * hd + nh * hd * d + 3 * d * ff
+    r = STEP_R
+    lora_dims = [(d, nh * hd), (d, nkv * hd), (d, nkv * hd), (nh * hd, d), (d, ff), (d, ff), (ff, d)]
+    lora = sum(2 * t * r * (k + n_) + 2 * t * r * (3 * k + 2 * n_) for k, n_ in lora_dims)
+    att_fwd = 2 * 2 * nh * (t * (t + 1) / 2) * hd  # S and O over the causal half
+    att_bwd = 4 * 2 * nh * (t * (t + 1) / 2) * hd  # dP, dV, dQ, dK
+    per_block = 2 * t * lin * 2 + lora + att_fwd + att_bwd
+    head = 2 * n * V * d * 2
+    parts = {"linears_fwd_dx": 4.0 * t * lin * L, "lora": float(lora * L), "attention": (att_fwd + att_bwd) * L,
+             "head": float(head)}
+    return per_block * L + head, parts
+
+
+def model_bench(steps: int, warmup: int, cpu_seconds: float, no_cpu: bool) -> dict:
+    """Qwen3-0.6B-shaped synthetic Q4_0 GGUF, LoRA r=16 alpha=32 on q,k,v,o,gate,up,down,
+    512 uniform-random tokens, cross-entropy on the last 256 (answer_targets, weights 1/256); one
+    step = zero_grad + Model::forward_backward (rtq_model_forward_backward)."""
+    import numpy as np
+    import torch
+
+    import rust_trainer_amd as rt
+    from rust_trainer_amd import gguf as G, synth
+
+    t0 = time.perf_counter()
+    spec = G.SyntheticSpec.preset("qwen3-0.6b", G.GGML_Q4_0)
+    image = spec.build()
+    print(f"[model] built the synthetic GGUF in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    g = G.GgufFile.from_bytes(image)
+    ctx = rt.Context(0)
+    model = rt.GpuModel.from_gguf(g, ctx=ctx)
+    n_params = model.attach_lora(STEP_R, STEP_ALPHA, seed=1)
+    cfg = model.config
+    tokens = (synth.Rng(7).next_u64(STEP_T) % np.uint64(cfg["n_vocab"])).astype(np.int32)
+    targets = rt.answer_targets(tokens, STEP_T - STEP_N)
+    wts = np.full(len(targets), 1.0 / len(targets), np.float32)
+
+    def step() -> np.ndarray:
+        model.zero_grad()
+        return model.forward_backward(tokens, targets, wts)[0]
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ctx.set_timing(True)
+    ctx.reset_timing()
+    step()
+    per = ctx.timing()
+    ctx.set_timing(False)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        lp = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    flops, parts = model_flops(cfg, STEP_T, len(targets))
+    total_k = sum(m for _, m in per.values())
+    result = {
+        "value": round(STEP_T / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 3),
+        "mean_loss": float(-lp.mean()),
+        "config": {"workload": "configs[2]: Qwen3-0.6B-shaped synthetic Q4_0 GGUF (28 layers, hidden 1024, FFN "
+                               "3072, 16/8 heads of 128, QK-norm, NEOX RoPE 1e6, vocab 151936 tied), LoRA r=16 "
+                               "alpha=32 on q,k,v,o,gate,up,down, 512 random tokens, loss on the last 256",
+                   "tokens": STEP_T, "targets": len(targets), "rank": STEP_R, "lora_params": n_params},
+        "step_flops": flops, "step_flops_parts": parts,
+        "step_roofline": {"bound": "mfma", "achieved": round(flops / (ms * 1e-3) / 1e12, 2), "peak": F16_PEAK_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(flops / (ms * 1e-3) / 1e12 / F16_PEAK_TFLOPS, 4)},
+        "kernels": {k: {"launches": c, "total_us": round(m * 1e3, 1), "share": round(m / total_k, 4)}
+                    for k, (c, m) in sorted(per.items(), key=lambda kv: -kv[1][1])},
+    }
+    if not no_cpu:
+        result["cpu_baseline"] = model_cpu_baseline(spec, cpu_seconds)
+    model.close()
+    ctx.close()
+    return result
+
+
+def model_cpu_baseline(spec, seconds: float) -> dict:
+    """The oracle's training step (C restatement of Model::forward_backward) on the host cores, on a
+    bounded sample: the same model cut to 2 of its 28 blocks (same shapes, same head), timed, and
+    scaled to 28 blocks by timing the head alone (step = head + 14 x (2-block step - head))."""
+    import numpy as np
+
+    import oracle as O
+    from rust_trainer_amd import gguf as G, synth
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from model_cases import adapters, oracle_model
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    small = G.SyntheticSpec.preset("qwen3-0.6b", G.GGML_Q4_0)
+    small.n_layer = 2
+    g = G.GgufFile.from_bytes(small.build())
+    lora = adapters(g, STEP_R, STEP_ALPHA)
+    m = oracle_model(g, lora, STEP_ALPHA)
+    tokens = (synth.Rng(7).next_u64(STEP_T) % np.uint64(small.n_vocab)).astype(np.int32)
+    pos = np.arange(STEP_T - STEP_N - 1, STEP_T - 1, dtype=np.int32)
+    tok = tokens[STEP_T - STEP_N:].copy()
+    wts = np.full(STEP_N, 1.0 / STEP_N, np.float32)
+    t0 = time.perf_counter()
+    O.model_forward_backward(m, tokens, pos, tok, wts, nthreads=threads)
+    two = time.perf_counter() - t0
+    e = m["embed"]
+    x = np.zeros((STEP_T, small.n_embd), np.float32)
+    t0 = time.perf_counter()
+    O.lm_head(e[0], e[1], e[2], e[3], m["out_norm"], x, pos, tok, wts, nthreads=threads)
+    head = time.perf_counter() - t0
+    step = head + (28 / 2) * (two - head)
+    return {"value": round(STEP_T / step, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle step on 2 of 28 blocks ({two:.1f} s) and the head alone ({head:.1f} s), scaled to "
+                      f"28 blocks: {step:.1f} s per 512-token step (oracle/rtq_oracle*.c, -O3 AVX2, OpenMP)"}
+
+
 def gguf_load(arg: str) -> None:
     """Load throughput of a synthetic GGUF model: write the file, map and parse it, upload every
     frozen tensor (the loader's ``fz``, src/rie.rs:183, :218-231) with rtq_weight_from_gguf."""
@@ -516,6 +637,7 @@ def main() -> int:
     ap.add_argument("--traffic", action="store_true", help="config-1 steps + calibration copies for --pmc passes")
     ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--head", action="store_true", help="configs[2] LM head + cross-entropy (Model::head)")
+    ap.add_argument("--model", action="store_true", help="configs[2] full training step (Model::forward_backward)")
     ap.add_argument("--gguf-load", default=None, metavar="PRESET[:WTYPE]",
                     help="GGUF load throughput of a synthetic model, e.g. qwen3-0.6b:Q4_0")
     args = ap.parse_args()
@@ -535,6 +657,9 @@ def main() -> int:
         return 0
     if args.head:
         head_bench(args.steps, args.warmup, args.cpu_seconds, args.no_cpu)
+        return 0
+    if args.model:
+        print(json.dumps(model_bench(args.steps, args.warmup, args.cpu_seconds, args.no_cpu)), flush=True)
         return 0
     if args.sweep or args.case:
         if args.case:

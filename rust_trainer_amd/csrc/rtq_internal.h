@@ -19,6 +19,7 @@ enum RtqModelKernel {
   KM_SWIGLU,
   KM_SWIGLU_BWD,
   KM_ADD,
+  KM_GEMM32,
   KM_COUNT
 };
 

@@ -165,8 +165,12 @@ rtq_status k_gemm(rtq_model* m, int64_t M, int64_t N, int64_t K, int64_t batch, 
                   int64_t sCm, int64_t sCn, float a_scale, int causal, int acc) {
   MGemmArgs ga{A.p,   B.p,   C,     (int)M, (int)N, (int)K, A.sb,  A.s0,     A.s1, B.sb, B.s0,
                B.s1,  sCb,   sCm,   sCn,    A.div,  B.div,  a_scale, causal, acc};
-  return rtq_model_launch(m->ctx, KM_GEMM, dim3((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64), (unsigned)batch),
-                          dim3(256), stream_of(m), &ga);
+  // 64-row tiles when the grid fills the chip twice over, else 32-row tiles (twice the workgroups)
+  const int64_t tiles64 = (N + 63) / 64 * ((M + 63) / 64) * batch / (causal == 1 ? 2 : 1);
+  const int bm = tiles64 >= 2 * 256 ? 64 : 32;
+  return rtq_model_launch(m->ctx, bm == 64 ? KM_GEMM : KM_GEMM32,
+                          dim3((unsigned)((N + 63) / 64), (unsigned)((M + bm - 1) / bm), (unsigned)batch), dim3(256),
+                          stream_of(m), &ga);
 }
 
 rtq_lora lora_view(const Lin& l) { return rtq_lora{l.rank, l.alpha, l.A, l.B, l.rank > 0 ? 1 : 0}; }

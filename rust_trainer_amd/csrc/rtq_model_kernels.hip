@@ -172,11 +172,45 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_qk_bwd(MQkArgs a) {
 }
 
 // ------------------------------------------------------------------ batched f32 GEMM
-// 64 x 64 output tile per 256-thread workgroup, 16-deep k slices through LDS; thread (ty, tx) owns
-// rows m0 + ty + 16 i and columns n0 + tx + 16 j.  Operands are read with their own strides, the
-// unit-stride index fastest across lanes.
-extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm(MGemmArgs a) {
-  constexpr int BM = 64, BN = 64, BK = 16;
+// BM x 64 output tile per 256-thread workgroup on f32 MFMA (16x16x4: exact f32 products, f32
+// accumulation); wave w owns rows (w / 2) BM / 2 .. and columns (w % 2) 32 .. as (BM / 32) x 2
+// MFMA tiles.  32-deep k slabs go through LDS; the next slab's operands are loaded into registers
+// while the current one feeds the MFMAs.  Operands are read with their own strides, the
+// unit-stride index fastest across lanes.  BM = 32 doubles the grid of the thin products
+// (N = head_dim) so that each CU holds two workgroups.
+template <int BM>
+struct MGemmSlab {
+  static constexpr int BN = 64, BK = 32, NA = BM * BK / 256, NB = BN * BK / 256;
+  float a[NA], b[NB];
+};
+
+template <int BM>
+__device__ __forceinline__ void m_gemm_load(const MGemmArgs& a, const float* A, const float* B, int m0, int n0, int kk,
+                                            int k1, MGemmSlab<BM>& r) {
+  using S = MGemmSlab<BM>;
+  const bool a_kfast = a.sAk == 1, b_nfast = a.sBn == 1;
+#pragma unroll
+  for (int i = 0; i < S::NA; i++) {
+    const int e = threadIdx.x + 256 * i;
+    const int am = a_kfast ? e / S::BK : e % BM, ak = a_kfast ? e % S::BK : e / BM;
+    const int gm = m0 + am, gk = kk + ak;
+    float v = (gm < a.M && gk < k1) ? A[(int64_t)gm * a.sAm + (int64_t)gk * a.sAk] : 0.0f;
+    if (a.a_scale != 1.0f) v = v * a.a_scale;
+    r.a[i] = v;
+  }
+#pragma unroll
+  for (int i = 0; i < S::NB; i++) {
+    const int e = threadIdx.x + 256 * i;
+    const int bn = b_nfast ? e % S::BN : e / S::BK, bk = b_nfast ? e / S::BN : e % S::BK;
+    const int gn = n0 + bn, gk = kk + bk;
+    r.b[i] = (gn < a.N && gk < k1) ? B[(int64_t)gk * a.sBk + (int64_t)gn * a.sBn] : 0.0f;
+  }
+}
+
+template <int BM>
+__device__ __forceinline__ void m_gemm(const MGemmArgs& a) {
+  using S = MGemmSlab<BM>;
+  constexpr int BN = S::BN, BK = S::BK, TM = BM / 32;  // MFMA row tiles per wave
   __shared__ float As[BK][BM + 4];
   __shared__ float Bs[BK][BN + 4];
   const int b = blockIdx.z, m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
@@ -186,51 +220,62 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm(MGemmArgs a) {
   int k0 = 0, k1 = a.K;
   if (a.causal == 2) k1 = min(a.K, m0 + BM);
   if (a.causal == 3) k0 = (m0 / BK) * BK;
-  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
   const bool a_kfast = a.sAk == 1, b_nfast = a.sBn == 1;
-  float acc[4][4] = {};
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
+  const int wm = (w >> 1) * (BM / 2), wn = (w & 1) * 32;
+  f4 acc[TM][2];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  S r;
+  if (k0 < k1) m_gemm_load<BM>(a, A, B, m0, n0, k0, k1, r);
   for (int kk = k0; kk < k1; kk += BK) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < S::NA; i++) {
       const int e = threadIdx.x + 256 * i;
-      const int am = a_kfast ? e / BK : e % BM, ak = a_kfast ? e % BK : e / BM;
-      const int gm = m0 + am, gk = kk + ak;
-      float v = (gm < a.M && gk < k1) ? A[(int64_t)gm * a.sAm + (int64_t)gk * a.sAk] : 0.0f;
-      if (a.a_scale != 1.0f) v = v * a.a_scale;
-      As[ak][am] = v;
-      const int bn = b_nfast ? e % BN : e / BK, bk = b_nfast ? e / BN : e % BK;
-      const int gn = n0 + bn, gk2 = kk + bk;
-      Bs[bk][bn] = (gn < a.N && gk2 < k1) ? B[(int64_t)gk2 * a.sBk + (int64_t)gn * a.sBn] : 0.0f;
+      As[a_kfast ? e % BK : e / BM][a_kfast ? e / BK : e % BM] = r.a[i];
+    }
+#pragma unroll
+    for (int i = 0; i < S::NB; i++) {
+      const int e = threadIdx.x + 256 * i;
+      Bs[b_nfast ? e / BN : e % BK][b_nfast ? e % BN : e / BK] = r.b[i];
     }
     __syncthreads();
+    if (kk + BK < k1) m_gemm_load<BM>(a, A, B, m0, n0, kk + BK, k1, r);
 #pragma unroll
-    for (int k = 0; k < BK; k++) {
-      float av[4], bv[4];
+    for (int k4 = 0; k4 < BK; k4 += 4) {
+      float av[TM], bv[2];
 #pragma unroll
-      for (int i = 0; i < 4; i++) av[i] = As[k][ty + 16 * i];
+      for (int i = 0; i < TM; i++) av[i] = As[k4 + g][wm + 16 * i + li];
 #pragma unroll
-      for (int j = 0; j < 4; j++) bv[j] = Bs[k][tx + 16 * j];
+      for (int j = 0; j < 2; j++) bv[j] = Bs[k4 + g][wn + 16 * j + li];
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = acc[i][j] + av[i] * bv[j];
+        for (int j = 0; j < 2; j++) acc[i][j] = mfma_f32(av[i], bv[j], acc[i][j]);
     }
     __syncthreads();
   }
   float* C = a.C + (int64_t)b * a.sCb;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int m = m0 + ty + 16 * i;
-    if (m >= a.M) continue;
+  for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int n = n0 + tx + 16 * j;
-      if (n >= a.N) continue;
-      float* c = C + (int64_t)m * a.sCm + (int64_t)n * a.sCn;
-      *c = a.accumulate ? *c + acc[i][j] : acc[i][j];
+    for (int e = 0; e < 4; e++) {
+      const int m = m0 + wm + 16 * i + 4 * g + e;
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int n = n0 + wn + 16 * j + li;
+        if (n >= a.N) continue;
+        float* c = C + (int64_t)m * a.sCm + (int64_t)n * a.sCn;
+        *c = a.accumulate ? *c + acc[i][j][e] : acc[i][j][e];
+      }
     }
-  }
 }
+
+extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm(MGemmArgs a) { m_gemm<64>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32(MGemmArgs a) { m_gemm<32>(a); }
 
 // ------------------------------------------------------------------ attention softmax
 // grid (t, nh): row i of head h over j <= i: p = exp(s - max) / sum (0 for j > i)
