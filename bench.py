@@ -1,21 +1,28 @@
 """Benchmark of the frozen quantised-matmul hot path on one MI355X.
 
-Workload: one Qwen3-0.6B gate_proj frozen linear, Q4_0 W 3072x1024
-(N(0, 0.02), ggml reference quantiser), X 256x1024 and dy 256x3072 ~ N(0, 1), LoRA r=16 alpha=32
-(A ~ N(0, 1/1024), B ~ N(0, 0.01)); seeds 1..5 of the reference Rng.  One step = one pass of the
-hot path over the batch: Linear forward (y) and Linear backward (dx, dA, dB), device-resident
-inputs, through the C ABI's device-pointer entry points on torch's current stream.  Operand sets
-rotate over >256 MB so neither L2 nor the Infinity Cache holds a step's inputs.
+Default workload (the configuration the metric names): one LoRA training
+step of a Qwen3-0.6B-shaped synthetic Q4_0 GGUF model (28 layers, hidden 1024, FFN 3072, 16 / 8
+heads of 128, QK-norm, NEOX RoPE, vocabulary 151936 tied; random N(0, 0.02) weights, norms 1) with
+LoRA r=16 alpha=32 on q, k, v, o, gate, up, down, on 512 uniform-random token ids with cross-entropy
+on the last 256 positions.  One step = zero_grad + Model::forward_backward through
+rtq_model_forward_backward: 196 frozen-linear calls fused into 112 (q | k | v, gate | up), the
+attention and norms around them, the LM head + cross-entropy, and the backward of all of it, every
+tensor resident in HBM.  ``value`` = 512 tokens / step time (the reference's tok/s definition,
+examples/bench_train.rs:57-61); the K timed steps run back to back between two synchronisations.
+``roofline`` is that of the dominant quantised-matmul kernel of the step (its algorithmic bytes and
+flops over its event-timed total; see ``step_roofline``), ``cpu_baseline`` the oracle's step on 16
+host threads (bounded sample, scaled: see ``model_cpu_baseline``).
 
-The timed region is one replay of a HIP graph (torch.cuda.CUDAGraph over the library's device-pointer
-calls on one stream) of exactly K steps, with no events inside, so the GPU runs the kernels back to
-back.  Per-kernel durations come from an eager pass of the same steps with HIP events recorded by the
+``--linear`` measures configs[0] instead: one Qwen3-0.6B gate_proj frozen linear, Q4_0 W 3072x1024
+(N(0, 0.02), ggml reference quantiser), X 256x1024 and dy 256x3072 ~ N(0, 1), LoRA r=16 alpha=32
+(A ~ N(0, 1/1024), B ~ N(0, 0.01)); seeds 1..5 of the reference Rng.  One step = Linear forward (y)
+and Linear backward (dx, dA, dB), device-resident inputs, through the C ABI's device-pointer entry
+points on torch's current stream.  Operand sets rotate over >256 MB so neither L2 nor the Infinity
+Cache holds a step's inputs.  The timed region is one replay of a HIP graph (torch.cuda.CUDAGraph
+over the library's device-pointer calls on one stream) of exactly K steps, with no events inside.
+Per-kernel durations come from an eager pass of the same steps with HIP events recorded by the
 library around each launch on the launch stream; these intervals include the dispatch of the kernel
 packet and so read a few microseconds longer than the kernel-trace durations of rocprofv3.
-
-Prints one JSON line: metric/value (tokens/s = T / step time), per-kernel average durations, the
-roofline of the dominant kernel, and the CPU oracle's time on the host cores (cpu_baseline,
-bounded sample).
 
 ``--sweep`` measures BASELINE configs[1] instead: Q8_0, Q4_K, Q6_K (and Q4_0) at the Qwen3-0.6B
 shapes q_proj 2048x1024, k/v_proj 1024x1024, down_proj 1024x3072 and the tied LM head 151936x1024,
@@ -29,7 +36,9 @@ FMT:SHAPE:T`` runs one of those cases (for a kernel trace of it).
 ``rocprofv3 --pmc`` passes (FETCH_SIZE, then WRITE_SIZE); ``--traffic-report FETCH_DIR WRITE_DIR``
 turns the two passes into HBM bytes per launch of each library kernel (each counter scaled so that
 the copies read and write 64 MiB), writes ``profiles/traffic_<kernel>_config1.json`` (read by the
-default run for ``roofline.traffic``) and prints a table.
+``--linear`` run for ``roofline.traffic``) and prints a table.  ``--traffic-step`` does the same for
+two configs[2] training steps; ``--traffic-report F W --traffic-step`` writes
+``profiles/traffic_<kernel>_config3.json`` for the block-linear kernels (read by the default run).
 
 ``--head`` measures the LM head + cross-entropy of configs[2] (``Model::head``: tied Q4_0 head
 151936 x 1024, 512 positions, loss on the last 256) through ``rtq_lm_head_d``, one JSON line with
@@ -274,8 +283,50 @@ def traffic_run() -> None:
     print("traffic run done", flush=True)
 
 
-def traffic_report(fetch_dir: str, write_dir: str) -> None:
-    """Counter CSVs of the two --pmc passes -> profiles/traffic_<kernel>_config1.json and a table."""
+def traffic_run_step() -> None:
+    """Two configs[2] training steps, then the three 64 MiB calibration copies (for --pmc passes)."""
+    import numpy as np
+    import torch
+
+    import rust_trainer_amd as rt
+    from rust_trainer_amd import gguf as G, synth
+
+    g = G.GgufFile.from_bytes(G.SyntheticSpec.preset("qwen3-0.6b", G.GGML_Q4_0).build())
+    ctx = rt.Context(0)
+    model = rt.GpuModel.from_gguf(g, ctx=ctx)
+    model.attach_lora(STEP_R, STEP_ALPHA, seed=1)
+    tokens = (synth.Rng(7).next_u64(STEP_T) % np.uint64(model.config["n_vocab"])).astype(np.int32)
+    targets = rt.answer_targets(tokens, STEP_T - STEP_N)
+    wts = np.full(len(targets), 1.0 / len(targets), np.float32)
+    for _ in range(2):
+        model.zero_grad()
+        model.forward_backward(tokens, targets, wts)
+    src = torch.empty(COPY_MIB * 2**20 // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    model.close()
+    ctx.close()
+    print("traffic step run done", flush=True)
+
+
+def step_kernel_work(name: str) -> tuple[float, float] | None:
+    """Average algorithmic (bytes, flops) per launch of a block-linear kernel of the configs[2] step."""
+    cfg = {"n_embd": 1024, "n_head": 16, "n_head_kv": 8, "head_dim": 128, "n_ff": 3072}
+    calls = step_layer_calls(cfg, STEP_T)
+    if name.startswith("rtq_fwd_"):
+        w = [call_work(2, n, k, STEP_T, r, False) for n, k, r in calls]
+    elif name.startswith("rtq_dx_"):
+        w = [(float(n * k // 32 * 18 + STEP_T * (n + k) * 4), float(2 * STEP_T * n * k)) for n, k, _ in calls]
+    else:
+        return None
+    return sum(b for b, _ in w) / len(w), sum(f for _, f in w) / len(w)
+
+
+def traffic_report(fetch_dir: str, write_dir: str, step: bool = False) -> None:
+    """Counter CSVs of the two --pmc passes -> profiles/traffic_<kernel>_config1.json (config3 for
+    the training step) and a table."""
     import csv
     import glob
 
@@ -304,13 +355,17 @@ def traffic_report(fetch_dir: str, write_dir: str) -> None:
         fk = sum(v for v, _ in fetch[name]) / len(fetch[name])
         wk = sum(v for v, _ in write[name]) / len(write[name])
         total = (fk * ff + wk * wf) * 1024 if ff and wf else None
-        algo = kernel_work(name)
-        out = {"kernel": name, "workload": "configs[0] (Q4_0 3072x1024, T=256, LoRA r=16)",
+        algo = step_kernel_work(name) if step else kernel_work(name)
+        out = {"kernel": name, "workload": "configs[2] training step (average launch of the block linears)" if step
+               else "configs[0] (Q4_0 3072x1024, T=256, LoRA r=16)",
                "fetch_kib_raw": round(fk, 1), "write_kib_raw": round(wk, 1),
                "fetch_scale": round(ff, 4) if ff else None, "write_scale": round(wf, 4) if wf else None,
                "bytes_per_launch": round(total) if total else None,
                "algorithmic_bytes": int(algo[0]) if algo else None, "launches": len(fetch[name])}
-        json.dump(out, open(os.path.join(ROOT, "profiles", f"traffic_{name}_config1.json"), "w"), indent=1)
+        if step and algo is None:
+            continue
+        tag = "config3" if step else "config1"
+        json.dump(out, open(os.path.join(ROOT, "profiles", f"traffic_{name}_{tag}.json"), "w"), indent=1)
         rows.append(out)
     print(f"calibration: {COPY_MIB} MiB copies read {fcopy:.0f} KiB (FETCH_SIZE) and write {wcopy:.0f} KiB "
           f"(WRITE_SIZE) -> scales {ff:.4f} / {wf:.4f}")
@@ -532,6 +587,71 @@ def model_bench(steps: int, warmup: int, cpu_seconds: float, no_cpu: bool) -> di
     return result
 
 
+def step_layer_calls(cfg: dict, t: int) -> list[tuple[int, int, int]]:
+    """(rows, cols, adapter rank) of the frozen linear calls of one block: q | k | v, o, gate | up,
+    down (the fused groups of rtq_model_*)."""
+    d, nh, nkv, hd, ff = (cfg[k] for k in ("n_embd", "n_head", "n_head_kv", "head_dim", "n_ff"))
+    return [(nh * hd + 2 * nkv * hd, d, 3 * STEP_R), (d, nh * hd, STEP_R), (2 * ff, d, 2 * STEP_R), (d, ff, STEP_R)]
+
+
+def step_roofline(cfg: dict, kernels: dict) -> dict | None:
+    """Roofline of the dominant quantised-matmul kernel of the step: the algorithmic bytes and flops
+    of the block linears it ran (forward: W + x + y + adapter, 2 T N K + LoRA; dx: W + dy + dx,
+    2 T N K) over its total time in the step."""
+    qmm = {k: v for k, v in kernels.items() if k.startswith(("rtq_fwd_", "rtq_mm_", "rtq_gemv_", "rtq_dx"))}
+    if not qmm:
+        return None
+    name = max(qmm, key=lambda k: qmm[k]["total_us"])
+    calls = step_layer_calls(cfg, STEP_T) * cfg["n_layer"]
+    if qmm[name]["launches"] != len(calls):
+        return None  # the kernel also served other shapes: no per-call attribution
+    backward = name.startswith("rtq_dx")
+    bytes_ = flops = 0.0
+    for n, k, r in calls:
+        b, f = call_work(2, n, k, STEP_T, 0 if backward else r, False)
+        if backward:  # dx = dy . W: W + dy + dx
+            b, f = float(n * k // 32 * 18 + STEP_T * n * 4 + STEP_T * k * 4), float(2 * STEP_T * n * k)
+        bytes_ += b
+        flops += f
+    sec = qmm[name]["total_us"] * 1e-6
+    out = call_roofline(bytes_, flops, sec)
+    out.update({"kernel": name, "launches": len(calls), "avg_us": round(qmm[name]["total_us"] / len(calls), 3),
+                "algorithmic_bytes": int(bytes_ / len(calls)), "flops": int(flops / len(calls)),
+                "traffic": measured_traffic_step(name)})
+    return out
+
+
+def measured_traffic_step(name: str):
+    p = os.path.join(ROOT, "profiles", f"traffic_{name}_config3.json")
+    if os.path.exists(p):
+        try:
+            return json.load(open(p)).get("bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def step_line(args) -> dict:
+    """The contract line: configs[2]'s full training step."""
+    r = model_bench(args.steps, args.warmup, args.cpu_seconds, args.no_cpu)
+    cfg = {"n_embd": 1024, "n_head": 16, "n_head_kv": 8, "head_dim": 128, "n_ff": 3072, "n_layer": 28}
+    line = {
+        "metric": METRIC, "value": r["value"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": r["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 x int4 block dots -> f32 (frozen forward); bf16x3 -> f32 (frozen dx); f32 (LoRA, norms, "
+                 "attention on f32 MFMA)",
+        "data": "synthetic",
+        "config": r["config"],
+        "roofline": step_roofline(cfg, r["kernels"]),
+        "step_roofline": r["step_roofline"],
+        "kernels": r["kernels"],
+    }
+    if "cpu_baseline" in r:
+        line["cpu_baseline"] = r["cpu_baseline"]
+    return line
+
+
 def model_cpu_baseline(spec, seconds: float) -> dict:
     """The oracle's training step (C restatement of Model::forward_backward) on the host cores, on a
     bounded sample: the same model cut to 2 of its 28 blocks (same shapes, same head), timed, and
@@ -626,8 +746,8 @@ def gguf_load(arg: str) -> None:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 20; --linear 200)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 3; --linear 20)")
     ap.add_argument("--sets", type=int, default=40, help="rotating operand sets (~10 MB each)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -636,13 +756,21 @@ def main() -> int:
     ap.add_argument("--calls", type=int, default=50, help="sweep: calls per timed graph (at least the sets)")
     ap.add_argument("--traffic", action="store_true", help="config-1 steps + calibration copies for --pmc passes")
     ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
+    ap.add_argument("--traffic-step", action="store_true",
+                    help="configs[2] steps + calibration copies for --pmc passes (with --traffic-report: the step)")
     ap.add_argument("--head", action="store_true", help="configs[2] LM head + cross-entropy (Model::head)")
-    ap.add_argument("--model", action="store_true", help="configs[2] full training step (Model::forward_backward)")
+    ap.add_argument("--model", action="store_true", help="configs[2] step details only (no contract fields)")
+    ap.add_argument("--linear", action="store_true", help="configs[0]: one frozen linear, forward + backward")
     ap.add_argument("--gguf-load", default=None, metavar="PRESET[:WTYPE]",
                     help="GGUF load throughput of a synthetic model, e.g. qwen3-0.6b:Q4_0")
     args = ap.parse_args()
+    linear_mode = args.linear or args.traffic or args.sweep or bool(args.case) or args.head
+    if args.steps is None:
+        args.steps = 200 if linear_mode else 20
+    if args.warmup is None:
+        args.warmup = 20 if linear_mode else 3
     if args.traffic_report:
-        traffic_report(*args.traffic_report)
+        traffic_report(*args.traffic_report, step=args.traffic_step)
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -652,6 +780,9 @@ def main() -> int:
     if args.traffic:
         traffic_run()
         return 0
+    if args.traffic_step:
+        traffic_run_step()
+        return 0
     if args.gguf_load:
         gguf_load(args.gguf_load)
         return 0
@@ -660,6 +791,9 @@ def main() -> int:
         return 0
     if args.model:
         print(json.dumps(model_bench(args.steps, args.warmup, args.cpu_seconds, args.no_cpu)), flush=True)
+        return 0
+    if not args.linear and not args.sweep and not args.case:
+        print(json.dumps(step_line(args)), flush=True)
         return 0
     if args.sweep or args.case:
         if args.case:
