@@ -169,8 +169,10 @@ rtq_status rtq_model_lora_info(const rtq_model* m, int64_t i, int* layer, int* w
 /* host copies of adapter i's a [rank x in], b [out x rank], ga, gb (any may be NULL) */
 rtq_status rtq_model_lora_get(rtq_model* m, int64_t i, float* a, float* b, float* ga, float* gb);
 rtq_status rtq_model_lora_set(rtq_model* m, int64_t i, const float* a, const float* b);
-/* device pointers of adapter i (an optimiser on the device updates a / b in place) */
-rtq_status rtq_model_lora_device(rtq_model* m, int64_t i, float** a, float** b, float** ga, float** gb);
+/* device pointers of adapter i (an optimiser on the device updates a / b in place): a, ga are
+ * [rank x in] contiguous; b, gb are [out x rank] blocks with row stride *ldb floats (adapters of
+ * linears that run fused share one matrix) */
+rtq_status rtq_model_lora_device(rtq_model* m, int64_t i, float** a, float** b, float** ga, float** gb, int64_t* ldb);
 rtq_status rtq_model_zero_grad(rtq_model* m); /* Model::zero_grad (src/model.rs:436) */
 /* Model::forward_backward (src/model.rs:615-687) on one sequence (host arrays): tokens [t], targets
  * (pos[i], tok[i]) with loss weights [n]; logp [n] and *hits out.  weights NULL: log-probs only

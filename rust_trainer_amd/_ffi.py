@@ -86,7 +86,7 @@ SIGNATURES = {
     "rtq_model_lora_get": (_i, [_p, _i64, _p, _p, _p, _p]),
     "rtq_model_lora_set": (_i, [_p, _i64, _p, _p]),
     "rtq_model_lora_device": (_i, [_p, _i64, ctypes.POINTER(_p), ctypes.POINTER(_p), ctypes.POINTER(_p),
-                                   ctypes.POINTER(_p)]),
+                                   ctypes.POINTER(_p), ctypes.POINTER(_i64)]),
     "rtq_model_zero_grad": (_i, [_p]),
     "rtq_model_forward_backward": (_i, [_p, _p, _i64, _p, _p, _p, _i64, _p, ctypes.POINTER(_i64)]),
     # GGUF v3 container

@@ -20,6 +20,7 @@ enum RtqModelKernel {
   KM_SWIGLU_BWD,
   KM_ADD,
   KM_GEMM32,
+  KM_LORA_MASK,
   KM_COUNT
 };
 

@@ -261,6 +261,7 @@ struct MQkArgs {
   float* dk_raw;
   int t, nh, nkv, hd, rot, neox, kv_f16;
   float eps, off;
+  int64_t ldq, ldk, ldv;  // per-token row strides of q_raw / dq_raw, k_raw / dk_raw, v_raw (fused q|k|v rows)
 };
 
 // C(b, m, n) (+)= sum_k A(b, m, k) * B(b, k, n), A(b, m, k) = A[(b / divA) * sAb + m * sAm + k * sAk]
@@ -291,15 +292,26 @@ struct MGroupArgs {
   const float* dkh;  // [nh x t x hd] per-head gradients
   const float* dvh;
   float* dk;         // [t x nkv x hd]: sum of the group's heads, in head order
-  float* dv;
+  float* dv;         // token i's row at dv + i * ldv
   int t, nh, nkv, hd;
+  int64_t ldv;
 };
 
+// elementwise over rows x cols: a, b at row stride lda, c at ldc, y, z at ldy
 struct MEltArgs {
   const float* a;
   const float* b;
   const float* c;
   float* y;
   float* z;
-  int64_t n;
+  int64_t n, cols, lda, ldc, ldy;
+};
+
+// clears the off-block entries of a fused adapter's gb [rows x rank]: row range m (row0[m], rows[m])
+// keeps columns [col0[m], col0[m] + r[m]) only
+struct MMaskArgs {
+  float* gb;
+  int64_t rows, rank;
+  int nm;
+  int64_t row0[3], nrow[3], col0[3], r[3];
 };

@@ -10,6 +10,12 @@
 // The reference recomputes each block's forward in the backward (checkpointing) to save memory;
 // the recomputation reproduces the same values, so here every block's activations are simply kept
 // (config-3 shapes: 60 MB per layer).
+//
+// Linears that read the same input and share a ggml type run as one frozen weight: q | k | v
+// (rows concatenated) and gate | up.  Their adapters become one LoRA of rank (members x r) whose B
+// is block-diagonal (zeros elsewhere) and whose alpha is scaled alike, so alpha / rank and every
+// output are unchanged; the gradients of the structurally zero B entries are cleared after each
+// backward.  Each member adapter stays addressable (rtq_model_lora_*), its B as a strided block.
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -34,23 +40,36 @@ const char* const kLinName[NLIN] = {"attn_q", "attn_k", "attn_v", "attn_output",
     if (e_ != hipSuccess) return rtq_fail(RTQ_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_));         \
   } while (0)
 
-struct Lin {
+// one member linear of a group: its rows of the fused weight and its adapter block
+struct Member {
+  int lin = 0;
+  int64_t row0 = 0, rows = 0;
+  int64_t col0 = 0, r = 0;  // adapter block: A rows / B columns [col0, col0 + r); r = 0: not adapted
+};
+
+// one frozen weight run by one linear call: a single linear, or q | k | v / gate | up fused
+struct Group {
   rtq_weight* w = nullptr;
-  const float* bias = nullptr;  // device, or null
-  int64_t out = 0, in = 0;
-  int64_t rank = 0;  // 0: no adapter
+  const float* bias = nullptr;  // device [rows], or null
+  int64_t rows = 0, in = 0;
+  int nm = 0;
+  Member mem[3];
+  int64_t rank = 0;  // fused adapter rank (sum of the members' r); 0: no adapter
   float alpha = 0.0f;
-  float *A = nullptr, *B = nullptr, *ga = nullptr, *gb = nullptr;
+  float *A = nullptr, *B = nullptr, *ga = nullptr, *gb = nullptr;  // [rank x in], [rows x rank]
 };
 
 struct Layer {
   const float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
-  Lin lin[NLIN];
+  std::vector<Group> groups;
+  int gi[NLIN], mi[NLIN];  // group and member of each linear
+  bool qkv_fused = false, gu_fused = false;
 };
 
-// activations of one block, kept for its backward
+// activations of one block, kept for its backward.  qkv holds q | k | v per token when fused (row
+// stride qd + 2 kd), else q [t x qd], then k, then v; gu likewise gate | up.
 struct Cache {
-  float *n1, *inv1, *q_raw, *k_raw, *v_raw, *q, *k, *v, *q_inv, *k_inv, *P, *o, *h, *n2, *inv2, *g, *u, *hm;
+  float *n1, *inv1, *qkv, *q, *k, *v, *q_inv, *k_inv, *P, *o, *h, *n2, *inv2, *gu, *hm;
 };
 
 // SplitMix64 + uniform of the reference Rng (src/tensor.rs:155-180)
@@ -84,8 +103,7 @@ struct rtq_model {
   void* step_mem = nullptr;
   float *X = nullptr, *cos_ = nullptr, *sin_ = nullptr;
   std::vector<Cache> cache;
-  float *dY, *dX, *mo, *f, *dhm, *dg, *du, *dn2, *dxu, *dh, *d_o, *dP, *dq, *dkh, *dvh, *dk, *dv, *dq_raw, *dk_raw,
-      *dn1, *dxk, *dxv;
+  float *dY, *dX, *mo, *f, *dhm, *dgu, *dn2, *dxu, *dh, *d_o, *dP, *dq, *dkh, *dvh, *dk, *dqkv, *dn1, *dxk, *dxv;
   int32_t *tok_d = nullptr, *pos_d = nullptr, *tgt_d = nullptr, *hit_d = nullptr;
   float *wts_d = nullptr, *logp_d = nullptr;
   int64_t rope_t = -1;  // t of the uploaded RoPE tables
@@ -148,10 +166,16 @@ rtq_status k_norm_bwd(rtq_model* m, const float* x, const float* w, const float*
   return rtq_model_launch(m->ctx, KM_RMSNORM_BWD, dim3((unsigned)rows), dim3(256), stream_of(m), &na);
 }
 
-rtq_status k_elt(rtq_model* m, int km, const float* a, const float* b, const float* c, float* y, float* z, int64_t n) {
-  MEltArgs ea{a, b, c, y, z, n};
-  const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 4096);
+// elementwise over rows x cols (a, b at row stride lda, c at ldc, y, z at ldy)
+rtq_status k_elt2(rtq_model* m, int km, const float* a, const float* b, const float* c, float* y, float* z,
+                  int64_t rows, int64_t cols, int64_t lda, int64_t ldc, int64_t ldy) {
+  MEltArgs ea{a, b, c, y, z, rows * cols, cols, lda, ldc, ldy};
+  const unsigned grid = (unsigned)std::min<int64_t>((rows * cols + 255) / 256, 4096);
   return rtq_model_launch(m->ctx, km, dim3(grid), dim3(256), stream_of(m), &ea);
+}
+
+rtq_status k_elt(rtq_model* m, int km, const float* a, const float* b, const float* c, float* y, float* z, int64_t n) {
+  return k_elt2(m, km, a, b, c, y, z, 1, n, n, n, n);
 }
 
 struct Op {  // one GEMM operand: base, batch stride and divisor, row / column strides
@@ -173,16 +197,26 @@ rtq_status k_gemm(rtq_model* m, int64_t M, int64_t N, int64_t K, int64_t batch, 
                           stream_of(m), &ga);
 }
 
-rtq_lora lora_view(const Lin& l) { return rtq_lora{l.rank, l.alpha, l.A, l.B, l.rank > 0 ? 1 : 0}; }
+rtq_lora lora_view(const Group& l) { return rtq_lora{l.rank, l.alpha, l.A, l.B, l.rank > 0 ? 1 : 0}; }
 
-rtq_status lin_fwd(rtq_model* m, const Lin& l, const float* x, int64_t t, float* y) {
+rtq_status lin_fwd(rtq_model* m, const Group& l, const float* x, int64_t t, float* y) {
   const rtq_lora lv = lora_view(l);
   return rtq_linear_forward_d(m->ctx, l.w, l.bias, l.rank > 0 ? &lv : nullptr, x, t, y, stream_of(m));
 }
 
-rtq_status lin_bwd(rtq_model* m, const Lin& l, const float* x, const float* dy, int64_t t, float* dx) {
+rtq_status lin_bwd(rtq_model* m, const Group& l, const float* x, const float* dy, int64_t t, float* dx) {
   const rtq_lora lv = lora_view(l);
-  return rtq_linear_backward_d(m->ctx, l.w, l.rank > 0 ? &lv : nullptr, x, dy, t, dx, l.ga, l.gb, stream_of(m));
+  M_TRY(rtq_linear_backward_d(m->ctx, l.w, l.rank > 0 ? &lv : nullptr, x, dy, t, dx, l.ga, l.gb, stream_of(m)));
+  if (l.rank == 0 || l.nm < 2) return RTQ_OK;
+  MMaskArgs ma{l.gb, l.rows, l.rank, l.nm, {}, {}, {}, {}};
+  for (int i = 0; i < l.nm; i++) {
+    ma.row0[i] = l.mem[i].row0;
+    ma.nrow[i] = l.mem[i].rows;
+    ma.col0[i] = l.mem[i].col0;
+    ma.r[i] = l.mem[i].r;
+  }
+  return rtq_model_launch(m->ctx, KM_LORA_MASK, dim3((unsigned)std::min<int64_t>((l.rows * l.rank + 255) / 256, 4096)),
+                          dim3(256), stream_of(m), &ma);
 }
 
 // ---------------------------------------------------------------- step buffers
@@ -200,17 +234,17 @@ rtq_status ensure_step(rtq_model* m, int64_t t, int64_t n) {
   m->cache.assign((size_t)L, Cache{});
   for (auto& k : m->cache) {
     for (auto pr : std::initializer_list<std::pair<float**, int64_t>>{
-             {&k.n1, T * d},   {&k.inv1, T},     {&k.q_raw, T * qd}, {&k.k_raw, T * kd}, {&k.v_raw, T * kd},
+             {&k.n1, T * d},   {&k.inv1, T},     {&k.qkv, T * (qd + 2 * kd)},
              {&k.q, T * qd},   {&k.k, T * kd},   {&k.v, T * kd},     {&k.q_inv, T * c.n_head},
              {&k.k_inv, T * c.n_head_kv},        {&k.P, att},        {&k.o, T * qd},     {&k.h, T * d},
-             {&k.n2, T * d},   {&k.inv2, T},     {&k.g, T * ff},     {&k.u, T * ff},     {&k.hm, T * ff}})
+             {&k.n2, T * d},   {&k.inv2, T},     {&k.gu, T * 2 * ff}, {&k.hm, T * ff}})
       f.push_back(pr);
   }
   for (auto pr : std::initializer_list<std::pair<float**, int64_t>>{
            {&m->dY, T * d},   {&m->dX, T * d},    {&m->mo, T * d},   {&m->f, T * d},      {&m->dhm, T * ff},
-           {&m->dg, T * ff},  {&m->du, T * ff},   {&m->dn2, T * d},  {&m->dxu, T * d},    {&m->dh, T * d},
+           {&m->dgu, T * 2 * ff},                 {&m->dn2, T * d},  {&m->dxu, T * d},    {&m->dh, T * d},
            {&m->d_o, T * qd}, {&m->dP, att},      {&m->dq, T * qd},  {&m->dkh, hdh},      {&m->dvh, hdh},
-           {&m->dk, T * kd},  {&m->dv, T * kd},   {&m->dq_raw, T * qd}, {&m->dk_raw, T * kd}, {&m->dn1, T * d},
+           {&m->dk, T * kd},  {&m->dqkv, T * (qd + 2 * kd)},     {&m->dn1, T * d},
            {&m->dxk, T * d},  {&m->dxv, T * d},   {&m->wts_d, N},    {&m->logp_d, N}})
     f.push_back(pr);
   size_t bytes = 0;
@@ -262,12 +296,34 @@ rtq_status ensure_rope(rtq_model* m, int64_t t) {
 }
 
 // ---------------------------------------------------------------- one block
+// q, k, v raw rows in a cache's qkv buffer (or the gradient buffer of the same layout)
+struct QkvView {
+  float *q, *k, *v;
+  int64_t ldq, ldk, ldv;
+};
+
+QkvView qkv_view(const rtq_model* m, const Layer& L, float* base, int64_t t) {
+  const rtq_model_config& c = m->cfg;
+  const int64_t qd = c.n_head * c.head_dim, kd = c.n_head_kv * c.head_dim;
+  if (L.qkv_fused) return QkvView{base, base + qd, base + qd + kd, qd + 2 * kd, qd + 2 * kd, qd + 2 * kd};
+  return QkvView{base, base + t * qd, base + t * (qd + kd), qd, kd, kd};
+}
+
 MQkArgs qk_args(rtq_model* m, const Layer& L, Cache& k, int64_t t) {
   const rtq_model_config& c = m->cfg;
-  return MQkArgs{k.q_raw,   k.k_raw,   k.v_raw,   L.q_norm, L.k_norm, m->cos_,        m->sin_,
-                 k.q,       k.k,       k.v,       k.q_inv,  k.k_inv,  m->dq,          m->dk,
-                 m->dq_raw, m->dk_raw, (int)t,    (int)c.n_head,      (int)c.n_head_kv, (int)c.head_dim,
-                 (int)c.rope_dim,      c.rope_neox, c.kv_f16,         c.rms_eps,        c.norm_offset};
+  const QkvView x = qkv_view(m, L, k.qkv, t), dx = qkv_view(m, L, m->dqkv, t);
+  return MQkArgs{x.q,   x.k,   x.v,   L.q_norm, L.k_norm, m->cos_,          m->sin_,          k.q,
+                 k.k,   k.v,   k.q_inv, k.k_inv, m->dq,     m->dk,            dx.q,             dx.k,
+                 (int)t, (int)c.n_head, (int)c.n_head_kv, (int)c.head_dim, (int)c.rope_dim, c.rope_neox,
+                 c.kv_f16, c.rms_eps, c.norm_offset, x.ldq, x.ldk, x.ldv};
+}
+
+// gate | u views of a cache's gu buffer (or the gradient buffer of the same layout)
+void gu_view(const rtq_model* m, const Layer& L, float* base, int64_t t, float** g, float** u, int64_t* ld) {
+  const int64_t ff = m->cfg.n_ff;
+  *g = base;
+  *u = L.gu_fused ? base + ff : base + t * ff;
+  *ld = L.gu_fused ? 2 * ff : ff;
 }
 
 rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* y) {
@@ -277,9 +333,14 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* 
   const int64_t d = c.n_embd, nh = c.n_head, nkv = c.n_head_kv, hd = c.head_dim, grp = nh / nkv;
   const int64_t qd = nh * hd, kd = nkv * hd;
   M_TRY(k_norm(m, x, nullptr, nullptr, L.attn_norm, k.n1, k.inv1, t, d, 0));
-  M_TRY(lin_fwd(m, L.lin[LQ], k.n1, t, k.q_raw));
-  M_TRY(lin_fwd(m, L.lin[LK], k.n1, t, k.k_raw));
-  M_TRY(lin_fwd(m, L.lin[LV], k.n1, t, k.v_raw));
+  const QkvView qv = qkv_view(m, L, k.qkv, t);
+  if (L.qkv_fused) {
+    M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LQ]], k.n1, t, k.qkv));
+  } else {
+    M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LQ]], k.n1, t, qv.q));
+    M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LK]], k.n1, t, qv.k));
+    M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LV]], k.n1, t, qv.v));
+  }
   const MQkArgs qa = qk_args(m, L, k, t);
   M_TRY(rtq_model_launch(m->ctx, KM_QK_PREP, dim3((unsigned)((t * (nh + 2 * nkv) + 3) / 4)), dim3(256), stream_of(m),
                          &qa));
@@ -289,12 +350,19 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* 
   MSoftArgs sa{k.P, nullptr, nullptr, (int)t, (int)nh, scale};
   M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX, dim3((unsigned)t, (unsigned)nh), dim3(256), stream_of(m), &sa));
   M_TRY(k_gemm(m, t, hd, t, nh, Op{k.P, t * t, t, 1, 1}, Op{k.v, hd, kd, 1, (int)grp}, k.o, hd, qd, 1, 1.0f, 2, 0));
-  M_TRY(lin_fwd(m, L.lin[LO], k.o, t, m->mo));
+  M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LO]], k.o, t, m->mo));
   M_TRY(k_norm(m, x, m->mo, k.h, L.ffn_norm, k.n2, k.inv2, t, d, 0));  // h = x + attn, n2 = rmsnorm(h)
-  M_TRY(lin_fwd(m, L.lin[LGATE], k.n2, t, k.g));
-  M_TRY(lin_fwd(m, L.lin[LUP], k.n2, t, k.u));
-  M_TRY(k_elt(m, KM_SWIGLU, k.g, k.u, nullptr, k.hm, nullptr, t * c.n_ff));
-  M_TRY(lin_fwd(m, L.lin[LDOWN], k.hm, t, m->f));
+  float *g, *u;
+  int64_t ldg;
+  gu_view(m, L, k.gu, t, &g, &u, &ldg);
+  if (L.gu_fused) {
+    M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LGATE]], k.n2, t, k.gu));
+  } else {
+    M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LGATE]], k.n2, t, g));
+    M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LUP]], k.n2, t, u));
+  }
+  M_TRY(k_elt2(m, KM_SWIGLU, g, u, nullptr, k.hm, nullptr, t, c.n_ff, ldg, c.n_ff, c.n_ff));
+  M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LDOWN]], k.hm, t, m->f));
   return k_elt(m, KM_ADD, k.h, m->f, nullptr, y, nullptr, t * d);  // y = h + mlp
 }
 
@@ -306,14 +374,22 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
   const int64_t qd = nh * hd, kd = nkv * hd;
   const float scale = 1.0f / sqrtf((float)hd);
   // Mlp::backward (src/model.rs:120-133)
-  M_TRY(lin_bwd(m, L.lin[LDOWN], k.hm, dy, t, m->dhm));
-  M_TRY(k_elt(m, KM_SWIGLU_BWD, k.g, k.u, m->dhm, m->dg, m->du, t * c.n_ff));
-  M_TRY(lin_bwd(m, L.lin[LGATE], k.n2, m->dg, t, m->dn2));
-  M_TRY(lin_bwd(m, L.lin[LUP], k.n2, m->du, t, m->dxu));
-  M_TRY(k_elt(m, KM_ADD, m->dn2, m->dxu, nullptr, m->dn2, nullptr, t * d));
+  M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LDOWN]], k.hm, dy, t, m->dhm));
+  float *g, *u, *dg, *du;
+  int64_t ldg;
+  gu_view(m, L, k.gu, t, &g, &u, &ldg);
+  gu_view(m, L, m->dgu, t, &dg, &du, &ldg);
+  M_TRY(k_elt2(m, KM_SWIGLU_BWD, g, u, m->dhm, dg, du, t, c.n_ff, ldg, c.n_ff, ldg));
+  if (L.gu_fused) {
+    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LGATE]], k.n2, m->dgu, t, m->dn2));  // dgate.Wg + dup.Wu in one pass
+  } else {
+    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LGATE]], k.n2, dg, t, m->dn2));
+    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LUP]], k.n2, du, t, m->dxu));
+    M_TRY(k_elt(m, KM_ADD, m->dn2, m->dxu, nullptr, m->dn2, nullptr, t * d));
+  }
   M_TRY(k_norm_bwd(m, k.h, L.ffn_norm, k.inv2, m->dn2, dy, m->dh, t, d));  // dh = dy + rmsnorm_backward
   // Attention::backward (src/attention.rs:243-355)
-  M_TRY(lin_bwd(m, L.lin[LO], k.o, m->dh, t, m->d_o));
+  M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LO]], k.o, m->dh, t, m->d_o));
   M_TRY(k_gemm(m, t, t, hd, nh, Op{m->d_o, hd, qd, 1, 1}, Op{k.v, hd, 1, kd, (int)grp}, m->dP, t * t, t, 1, 1.0f, 1,
                0));  // dP = dO V^T
   MSoftArgs sa{nullptr, k.P, m->dP, (int)t, (int)nh, scale};
@@ -324,16 +400,104 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
                0));  // dQ = dS K
   M_TRY(k_gemm(m, t, hd, t, nh, Op{m->dP, t * t, 1, t, 1}, Op{k.q, hd, qd, 1, 1}, m->dkh, t * hd, hd, 1, 1.0f, 3,
                0));  // dK_h = dS^T Q
-  MGroupArgs gsa{m->dkh, m->dvh, m->dk, m->dv, (int)t, (int)nh, (int)nkv, (int)hd};
+  const QkvView dv = qkv_view(m, L, m->dqkv, t);
+  MGroupArgs gsa{m->dkh, m->dvh, m->dk, dv.v, (int)t, (int)nh, (int)nkv, (int)hd, dv.ldv};
   M_TRY(rtq_model_launch(m->ctx, KM_GROUP_SUM, dim3((unsigned)std::min<int64_t>((t * kd + 255) / 256, 4096)),
                          dim3(256), stream_of(m), &gsa));
   const MQkArgs qa = qk_args(m, L, k, t);
   M_TRY(rtq_model_launch(m->ctx, KM_QK_BWD, dim3((unsigned)((t * (nh + nkv) + 3) / 4)), dim3(256), stream_of(m), &qa));
-  M_TRY(lin_bwd(m, L.lin[LQ], k.n1, m->dq_raw, t, m->dn1));
-  M_TRY(lin_bwd(m, L.lin[LK], k.n1, m->dk_raw, t, m->dxk));
-  M_TRY(lin_bwd(m, L.lin[LV], k.n1, m->dv, t, m->dxv));
-  M_TRY(k_elt(m, KM_ADD, m->dn1, m->dxk, m->dxv, m->dn1, nullptr, t * d));  // dq + (dk + dv)
-  return k_norm_bwd(m, x, L.attn_norm, k.inv1, m->dn1, m->dh, dx, t, d);    // dx = dh + rmsnorm_backward
+  if (L.qkv_fused) {
+    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LQ]], k.n1, m->dqkv, t, m->dn1));  // dq.Wq + dk.Wk + dv.Wv in one pass
+  } else {
+    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LQ]], k.n1, dv.q, t, m->dn1));
+    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LK]], k.n1, dv.k, t, m->dxk));
+    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LV]], k.n1, dv.v, t, m->dxv));
+    M_TRY(k_elt(m, KM_ADD, m->dn1, m->dxk, m->dxv, m->dn1, nullptr, t * d));  // dq + (dk + dv)
+  }
+  return k_norm_bwd(m, x, L.attn_norm, k.inv1, m->dn1, m->dh, dx, t, d);  // dx = dh + rmsnorm_backward
+}
+
+// the ggml type, packed bytes and shape of a GGUF tensor
+rtq_status tensor_bytes(const rtq_gguf* g, const std::string& name, int* type, const uint8_t** data, size_t* nbytes) {
+  const int64_t i = rtq_gguf_find_tensor(g, name.c_str());
+  if (i < 0) return rtq_fail(RTQ_ERR_INVALID, "GGUF: missing tensor %s", name.c_str());
+  const void* d = nullptr;
+  M_TRY(rtq_gguf_tensor(g, i, nullptr, type, nullptr, nullptr, &d, nbytes));
+  *data = (const uint8_t*)d;
+  return RTQ_OK;
+}
+
+// the layer's linears as groups: q | k | v and gate | up fused when their ggml types agree
+rtq_status load_groups(rtq_model* m, const rtq_gguf* g, const std::string& p, Layer& L, const int64_t* outs,
+                       const int64_t* ins) {
+  const int sets[4][3] = {{LQ, LK, LV}, {LO, -1, -1}, {LGATE, LUP, -1}, {LDOWN, -1, -1}};
+  for (const auto& set : sets) {
+    int n = 0, type0 = -1;
+    bool same = true;
+    for (int j = 0; j < 3 && set[j] >= 0; j++, n++) {
+      int type = 0;
+      const uint8_t* d;
+      size_t nb;
+      M_TRY(tensor_bytes(g, p + kLinName[set[j]] + ".weight", &type, &d, &nb));
+      same = same && (j == 0 || type == type0);
+      type0 = j == 0 ? type : type0;
+    }
+    const int parts = same ? 1 : n;  // one fused group, or one group per linear
+    for (int q = 0; q < parts; q++) {
+      Group G;
+      const int first = same ? 0 : q, last = same ? n : q + 1;
+      std::vector<uint8_t> bytes;
+      std::vector<float> bias;
+      bool any_bias = false;
+      int type = 0;
+      for (int j = first; j < last; j++) {
+        const int li = set[j];
+        const uint8_t* d;
+        size_t nb;
+        M_TRY(tensor_bytes(g, p + kLinName[li] + ".weight", &type, &d, &nb));
+        Member& mb = G.mem[G.nm++];
+        mb.lin = li;
+        mb.row0 = G.rows;
+        mb.rows = outs[li];
+        G.rows += outs[li];
+        G.in = ins[li];
+        L.gi[li] = (int)L.groups.size();
+        L.mi[li] = G.nm - 1;
+        if (last - first == 1) {  // a lone linear uploads straight from the image
+          M_TRY(load_weight(m, g, p + kLinName[li] + ".weight", outs[li], ins[li], &G.w));
+        } else {
+          bytes.insert(bytes.end(), d, d + nb);
+        }
+        const int64_t bi = li <= LV ? rtq_gguf_find_tensor(g, (p + kLinName[li] + ".bias").c_str()) : -1;
+        std::vector<float> b((size_t)outs[li], 0.0f);
+        if (bi >= 0) {
+          const void* bd;
+          size_t bn;
+          int bt = 0;
+          M_TRY(rtq_gguf_tensor(g, bi, nullptr, &bt, nullptr, nullptr, &bd, &bn));
+          if (bt != RTQ_TYPE_F32 || bn != (size_t)outs[li] * 4)
+            return rtq_fail(RTQ_ERR_UNSUPPORTED, "GGUF: %s.bias must be F32", (p + kLinName[li]).c_str());
+          memcpy(b.data(), bd, bn);
+          any_bias = true;
+        }
+        bias.insert(bias.end(), b.begin(), b.end());
+      }
+      if (!G.w) {
+        M_TRY(rtq_weight_create(m->ctx, type, bytes.data(), bytes.size(), G.rows, G.in, &G.w));
+        m->weights.push_back(G.w);
+      }
+      if (any_bias) {  // absent biases are zeros: y + 0 = y
+        void* bd;
+        M_TRY(dev_alloc(m, bias.size() * 4, &bd));
+        M_HIP(hipMemcpy(bd, bias.data(), bias.size() * 4, hipMemcpyHostToDevice));
+        G.bias = (const float*)bd;
+      }
+      L.groups.push_back(G);
+    }
+    if (set[0] == LQ) L.qkv_fused = same;
+    if (set[0] == LGATE) L.gu_fused = same;
+  }
+  return RTQ_OK;
 }
 
 }  // namespace
@@ -404,14 +568,7 @@ rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out)
         (st = upload_vec(m, g, p + "attn_q_norm.weight", c.head_dim, &L.q_norm, c.qk_norm)) != RTQ_OK ||
         (st = upload_vec(m, g, p + "attn_k_norm.weight", c.head_dim, &L.k_norm, c.qk_norm)) != RTQ_OK)
       return fail_out(st);
-    for (int i = 0; i < NLIN; i++) {
-      Lin& ln = L.lin[i];
-      ln.out = outs[i];
-      ln.in = ins[i];
-      if ((st = load_weight(m, g, p + kLinName[i] + ".weight", ln.out, ln.in, &ln.w)) != RTQ_OK) return fail_out(st);
-      if (i <= LV && (st = upload_vec(m, g, p + kLinName[i] + ".bias", ln.out, &ln.bias, false)) != RTQ_OK)
-        return fail_out(st);
-    }
+    if ((st = load_groups(m, g, p, L, outs, ins)) != RTQ_OK) return fail_out(st);
   }
   *out = m;
   return RTQ_OK;
@@ -437,32 +594,53 @@ rtq_status rtq_model_attach_lora(rtq_model* m, int64_t rank, float alpha, uint32
                                  int64_t* n_params) {
   if (!m || rank <= 0 || rank > 4096) return rtq_fail(RTQ_ERR_INVALID, "bad model/rank");
   M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
+  M_HIP(hipStreamSynchronize(stream_of(m)));
   Rng rng(seed);
   int64_t n = 0;
-  for (Layer& L : m->layers)
-    for (int i = 0; i < NLIN; i++) {
-      if (!(target_mask >> i & 1u)) continue;
-      Lin& ln = L.lin[i];
-      const float bound = 1.0f / sqrtf((float)ln.in);
-      std::vector<float> a((size_t)(rank * ln.in));
-      for (float& v : a) v = rng.uniform_sym(bound);
-      void *A, *B, *ga, *gb;
-      M_TRY(dev_alloc(m, a.size() * 4, &A));
-      M_TRY(dev_alloc(m, (size_t)(ln.out * rank) * 4, &B));
-      M_TRY(dev_alloc(m, a.size() * 4, &ga));
-      M_TRY(dev_alloc(m, (size_t)(ln.out * rank) * 4, &gb));
-      M_HIP(hipMemcpy(A, a.data(), a.size() * 4, hipMemcpyHostToDevice));
-      M_HIP(hipMemset(B, 0, (size_t)(ln.out * rank) * 4));
-      M_HIP(hipMemset(ga, 0, a.size() * 4));
-      M_HIP(hipMemset(gb, 0, (size_t)(ln.out * rank) * 4));
-      ln.rank = rank;
-      ln.alpha = alpha;
-      ln.A = (float*)A;
-      ln.B = (float*)B;
-      ln.ga = (float*)ga;
-      ln.gb = (float*)gb;
-      n += rank * (ln.in + ln.out);
+  for (Layer& L : m->layers) {
+    // block layout of each group's adapter: members in linear order, r columns each if targeted
+    std::vector<std::vector<float>> ahost(L.groups.size());
+    for (Group& G : L.groups) {
+      G.rank = 0;
+      for (int j = 0; j < G.nm; j++) {
+        Member& mb = G.mem[j];
+        mb.col0 = G.rank;
+        mb.r = (target_mask >> mb.lin & 1u) ? rank : 0;
+        G.rank += mb.r;
+      }
     }
+    for (int i = 0; i < NLIN; i++) {  // A drawn linear by linear, in the reference's order
+      if (!(target_mask >> i & 1u)) continue;
+      Group& G = L.groups[(size_t)L.gi[i]];
+      std::vector<float>& a = ahost[(size_t)L.gi[i]];
+      a.resize((size_t)(G.rank * G.in), 0.0f);
+      const Member& mb = G.mem[L.mi[i]];
+      const float bound = 1.0f / sqrtf((float)G.in);
+      for (int64_t e = 0; e < rank * G.in; e++) a[(size_t)(mb.col0 * G.in + e)] = rng.uniform_sym(bound);
+      n += rank * (G.in + mb.rows);
+    }
+    for (size_t gi = 0; gi < L.groups.size(); gi++) {
+      Group& G = L.groups[gi];
+      if (G.rank == 0) continue;
+      const size_t na = (size_t)(G.rank * G.in) * 4, nb = (size_t)(G.rows * G.rank) * 4;
+      void *A, *B, *ga, *gb;
+      M_TRY(dev_alloc(m, na, &A));
+      M_TRY(dev_alloc(m, nb, &B));
+      M_TRY(dev_alloc(m, na, &ga));
+      M_TRY(dev_alloc(m, nb, &gb));
+      M_HIP(hipMemcpy(A, ahost[gi].data(), na, hipMemcpyHostToDevice));
+      M_HIP(hipMemset(B, 0, nb));
+      M_HIP(hipMemset(ga, 0, na));
+      M_HIP(hipMemset(gb, 0, nb));
+      int members = 0;
+      for (int j = 0; j < G.nm; j++) members += G.mem[j].r > 0;
+      G.alpha = alpha * (float)members;  // alpha / rank unchanged
+      G.A = (float*)A;
+      G.B = (float*)B;
+      G.ga = (float*)ga;
+      G.gb = (float*)gb;
+    }
+  }
   if (n_params) *n_params = n;
   return RTQ_OK;
 }
@@ -471,65 +649,83 @@ int64_t rtq_model_lora_count(const rtq_model* m) {
   int64_t n = 0;
   if (m)
     for (const Layer& L : m->layers)
-      for (const Lin& ln : L.lin) n += ln.rank > 0;
+      for (const Group& G : L.groups)
+        for (int j = 0; j < G.nm; j++) n += G.mem[j].r > 0;
   return n;
 }
 
 namespace {
-Lin* lora_at(rtq_model* m, int64_t i, int* layer, int* which) {
-  if (!m || i < 0) return nullptr;
-  for (size_t l = 0; l < m->layers.size(); l++)
-    for (int k = 0; k < NLIN; k++)
-      if (m->layers[l].lin[k].rank > 0 && i-- == 0) {
+// adapter i in (block, linear) order: its group and member
+bool lora_at(const rtq_model* m, int64_t i, int* layer, int* which, const Group** grp, const Member** mem) {
+  if (!m || i < 0) return false;
+  for (size_t l = 0; l < m->layers.size(); l++) {
+    const Layer& L = m->layers[l];
+    for (int k = 0; k < NLIN; k++) {
+      const Group& G = L.groups[(size_t)L.gi[k]];
+      const Member& mb = G.mem[L.mi[k]];
+      if (mb.r > 0 && i-- == 0) {
         if (layer) *layer = (int)l;
         if (which) *which = k;
-        return &m->layers[l].lin[k];
+        *grp = &G;
+        *mem = &mb;
+        return true;
       }
-  return nullptr;
+    }
+  }
+  return false;
 }
 }  // namespace
 
 rtq_status rtq_model_lora_info(const rtq_model* m, int64_t i, int* layer, int* which, int64_t* rank, int64_t* in,
                                int64_t* out, float* alpha) {
-  Lin* ln = lora_at(const_cast<rtq_model*>(m), i, layer, which);
-  if (!ln) return rtq_fail(RTQ_ERR_INVALID, "adapter %lld out of range", (long long)i);
-  if (rank) *rank = ln->rank;
-  if (in) *in = ln->in;
-  if (out) *out = ln->out;
-  if (alpha) *alpha = ln->alpha;
+  const Group* G;
+  const Member* mb;
+  if (!lora_at(m, i, layer, which, &G, &mb)) return rtq_fail(RTQ_ERR_INVALID, "adapter %lld out of range", (long long)i);
+  if (rank) *rank = mb->r;
+  if (in) *in = G->in;
+  if (out) *out = mb->rows;
+  if (alpha) *alpha = G->alpha * (float)mb->r / (float)G->rank;
   return RTQ_OK;
 }
 
-rtq_status rtq_model_lora_device(rtq_model* m, int64_t i, float** a, float** b, float** ga, float** gb) {
-  Lin* ln = lora_at(m, i, nullptr, nullptr);
-  if (!ln) return rtq_fail(RTQ_ERR_INVALID, "adapter %lld out of range", (long long)i);
-  if (a) *a = ln->A;
-  if (b) *b = ln->B;
-  if (ga) *ga = ln->ga;
-  if (gb) *gb = ln->gb;
+rtq_status rtq_model_lora_device(rtq_model* m, int64_t i, float** a, float** b, float** ga, float** gb, int64_t* ldb) {
+  const Group* G;
+  const Member* mb;
+  if (!lora_at(m, i, nullptr, nullptr, &G, &mb)) return rtq_fail(RTQ_ERR_INVALID, "adapter %lld out of range", (long long)i);
+  const int64_t ao = mb->col0 * G->in, bo = mb->row0 * G->rank + mb->col0;
+  if (a) *a = G->A + ao;
+  if (b) *b = G->B + bo;
+  if (ga) *ga = G->ga + ao;
+  if (gb) *gb = G->gb + bo;
+  if (ldb) *ldb = G->rank;
   return RTQ_OK;
 }
 
 rtq_status rtq_model_lora_get(rtq_model* m, int64_t i, float* a, float* b, float* ga, float* gb) {
-  Lin* ln = lora_at(m, i, nullptr, nullptr);
-  if (!ln) return rtq_fail(RTQ_ERR_INVALID, "adapter %lld out of range", (long long)i);
+  const Group* G;
+  const Member* mb;
+  if (!lora_at(m, i, nullptr, nullptr, &G, &mb)) return rtq_fail(RTQ_ERR_INVALID, "adapter %lld out of range", (long long)i);
   M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
   M_HIP(hipStreamSynchronize(stream_of(m)));
-  const size_t na = (size_t)(ln->rank * ln->in) * 4, nb = (size_t)(ln->out * ln->rank) * 4;
-  if (a) M_HIP(hipMemcpy(a, ln->A, na, hipMemcpyDeviceToHost));
-  if (b) M_HIP(hipMemcpy(b, ln->B, nb, hipMemcpyDeviceToHost));
-  if (ga) M_HIP(hipMemcpy(ga, ln->ga, na, hipMemcpyDeviceToHost));
-  if (gb) M_HIP(hipMemcpy(gb, ln->gb, nb, hipMemcpyDeviceToHost));
+  const int64_t ao = mb->col0 * G->in, bo = mb->row0 * G->rank + mb->col0;
+  const size_t na = (size_t)(mb->r * G->in) * 4, w = (size_t)mb->r * 4, ld = (size_t)G->rank * 4;
+  if (a) M_HIP(hipMemcpy(a, G->A + ao, na, hipMemcpyDeviceToHost));
+  if (ga) M_HIP(hipMemcpy(ga, G->ga + ao, na, hipMemcpyDeviceToHost));
+  if (b) M_HIP(hipMemcpy2D(b, w, G->B + bo, ld, w, (size_t)mb->rows, hipMemcpyDeviceToHost));
+  if (gb) M_HIP(hipMemcpy2D(gb, w, G->gb + bo, ld, w, (size_t)mb->rows, hipMemcpyDeviceToHost));
   return RTQ_OK;
 }
 
 rtq_status rtq_model_lora_set(rtq_model* m, int64_t i, const float* a, const float* b) {
-  Lin* ln = lora_at(m, i, nullptr, nullptr);
-  if (!ln) return rtq_fail(RTQ_ERR_INVALID, "adapter %lld out of range", (long long)i);
+  const Group* G;
+  const Member* mb;
+  if (!lora_at(m, i, nullptr, nullptr, &G, &mb)) return rtq_fail(RTQ_ERR_INVALID, "adapter %lld out of range", (long long)i);
   M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
   M_HIP(hipStreamSynchronize(stream_of(m)));
-  if (a) M_HIP(hipMemcpy(ln->A, a, (size_t)(ln->rank * ln->in) * 4, hipMemcpyHostToDevice));
-  if (b) M_HIP(hipMemcpy(ln->B, b, (size_t)(ln->out * ln->rank) * 4, hipMemcpyHostToDevice));
+  const int64_t ao = mb->col0 * G->in, bo = mb->row0 * G->rank + mb->col0;
+  const size_t w = (size_t)mb->r * 4, ld = (size_t)G->rank * 4;
+  if (a) M_HIP(hipMemcpy(G->A + ao, a, (size_t)(mb->r * G->in) * 4, hipMemcpyHostToDevice));
+  if (b) M_HIP(hipMemcpy2D(G->B + bo, ld, b, w, w, (size_t)mb->rows, hipMemcpyHostToDevice));
   return RTQ_OK;
 }
 
@@ -537,10 +733,10 @@ rtq_status rtq_model_zero_grad(rtq_model* m) {
   if (!m) return rtq_fail(RTQ_ERR_INVALID, "null model");
   M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
   for (Layer& L : m->layers)
-    for (Lin& ln : L.lin)
-      if (ln.rank > 0) {
-        M_HIP(hipMemsetAsync(ln.ga, 0, (size_t)(ln.rank * ln.in) * 4, stream_of(m)));
-        M_HIP(hipMemsetAsync(ln.gb, 0, (size_t)(ln.out * ln.rank) * 4, stream_of(m)));
+    for (Group& G : L.groups)
+      if (G.rank > 0) {
+        M_HIP(hipMemsetAsync(G.ga, 0, (size_t)(G.rank * G.in) * 4, stream_of(m)));
+        M_HIP(hipMemsetAsync(G.gb, 0, (size_t)(G.rows * G.rank) * 4, stream_of(m)));
       }
   M_HIP(hipStreamSynchronize(stream_of(m)));
   return RTQ_OK;

@@ -115,15 +115,16 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_qk_prep(MQkArgs a) {
   if (row >= nq + 2 * nk) return;
   float* sb = buf[wv];
   if (row >= nq + nk) {  // v: f16 rounding only
-    const int64_t o = (row - nq - nk) * a.hd;
-    for (int e = lane; e < a.hd; e += 64) a.v[o + e] = a.kv_f16 ? m_round_f16(a.v_raw[o + e]) : a.v_raw[o + e];
+    const int64_t rv = row - nq - nk, o = rv * a.hd;
+    const float* vr = a.v_raw + (rv / a.nkv) * a.ldv + (rv % a.nkv) * a.hd;
+    for (int e = lane; e < a.hd; e += 64) a.v[o + e] = a.kv_f16 ? m_round_f16(vr[e]) : vr[e];
     return;
   }
   const bool isq = row < nq;
   const int64_t r = isq ? row : row - nq;
   const int heads = isq ? a.nh : a.nkv;
   const int p = (int)(r / heads);
-  const float* x = (isq ? a.q_raw : a.k_raw) + r * a.hd;
+  const float* x = (isq ? a.q_raw + p * a.ldq : a.k_raw + p * a.ldk) + (r % heads) * a.hd;
   const float* w = isq ? a.q_norm : a.k_norm;
   if (w) {
     float s = 0.0f;
@@ -153,13 +154,14 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_qk_bwd(MQkArgs a) {
   float* sb = buf[wv];
   m_rope_row(a, (isq ? a.dq : a.dk) + r * a.hd, sb, p, -1.0f, false);
   __builtin_amdgcn_wave_barrier();
-  float* out = (isq ? a.dq_raw : a.dk_raw) + r * a.hd;
+  const int64_t roff = (isq ? p * a.ldq : p * a.ldk) + (r % heads) * a.hd;
+  float* out = (isq ? a.dq_raw : a.dk_raw) + roff;
   const float* w = isq ? a.q_norm : a.k_norm;
   if (!w) {
     for (int e = lane; e < a.hd; e += 64) out[e] = sb[e];
     return;
   }
-  const float* x = (isq ? a.q_raw : a.k_raw) + r * a.hd;
+  const float* x = (isq ? a.q_raw : a.k_raw) + roff;
   const float ir = (isq ? a.q_inv : a.k_inv)[r];
   float s = 0.0f;
   for (int e = lane; e < a.hd; e += 64) s = s + (sb[e] * (w[e] + a.off)) * x[e];
@@ -321,28 +323,49 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_group_sum(MGroupArgs a) 
       sv = sv + a.dvh[o];
     }
     a.dk[idx] = sk;
-    a.dv[idx] = sv;
+    a.dv[i * a.ldv + (int64_t)g * a.hd + e] = sv;
   }
 }
 
 // ------------------------------------------------------------------ elementwise
+#define M_ELT_LOOP                                                                                       \
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (int64_t)gridDim.x * 256) { \
+    const int64_t rr = i / a.cols, cc = i % a.cols, ia = rr * a.lda + cc, ic = rr * a.ldc + cc,          \
+                  iy = rr * a.ldy + cc;
 // SwiGLU forward: y = silu(a) * b
 extern "C" __global__ __launch_bounds__(256) void rtq_m_swiglu(MEltArgs a) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (int64_t)gridDim.x * 256)
-    a.y[i] = m_silu(a.a[i]) * a.b[i];
+  M_ELT_LOOP
+    (void)ic;
+    a.y[iy] = m_silu(a.a[ia]) * a.b[ia];
+  }
 }
 
 // SwiGLU backward: dg = (dh u) silu'(g) -> y, du = dh silu(g) -> z  (a = g, b = u, c = dh)
 extern "C" __global__ __launch_bounds__(256) void rtq_m_swiglu_bwd(MEltArgs a) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (int64_t)gridDim.x * 256) {
-    const float g = a.a[i], u = a.b[i], dh = a.c[i];
-    a.y[i] = (dh * u) * m_silu_grad(g);
-    a.z[i] = dh * m_silu(g);
+  M_ELT_LOOP
+    const float g = a.a[ia], u = a.b[ia], dh = a.c[ic];
+    a.y[iy] = (dh * u) * m_silu_grad(g);
+    a.z[iy] = dh * m_silu(g);
   }
 }
 
 // y = a + b, or a + (b + c) when c is given
 extern "C" __global__ __launch_bounds__(256) void rtq_m_add(MEltArgs a) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (int64_t)gridDim.x * 256)
-    a.y[i] = a.c ? a.a[i] + (a.b[i] + a.c[i]) : a.a[i] + a.b[i];
+  M_ELT_LOOP
+    a.y[iy] = a.c ? a.a[ia] + (a.b[ia] + a.c[ic]) : a.a[ia] + a.b[ia];
+  }
+}
+#undef M_ELT_LOOP
+
+// off-block entries of a fused adapter's gb are cleared (they are gradients of B entries that are
+// structurally zero)
+extern "C" __global__ __launch_bounds__(256) void rtq_m_lora_mask(MMaskArgs a) {
+  const int64_t n = a.rows * a.rank;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / a.rank, col = i % a.rank;
+    bool keep = false;
+    for (int m = 0; m < a.nm; m++)
+      if (row >= a.row0[m] && row < a.row0[m] + a.nrow[m]) keep = col >= a.col0[m] && col < a.col0[m] + a.r[m];
+    if (!keep) a.gb[i] = 0.0f;
+  }
 }

@@ -157,7 +157,8 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_rows_q4_0",        "rtq_rows_q8_0",        "rtq_rows_q4_k",        "rtq_rows_q6_k",
     "rtq_m_rmsnorm",        "rtq_m_rmsnorm_bwd",    "rtq_m_qk_prep",        "rtq_m_qk_bwd",
     "rtq_m_gemm",           "rtq_m_softmax",        "rtq_m_softmax_bwd",    "rtq_m_group_sum",
-    "rtq_m_swiglu",         "rtq_m_swiglu_bwd",     "rtq_m_add",            "rtq_m_gemm32"};
+    "rtq_m_swiglu",         "rtq_m_swiglu_bwd",     "rtq_m_add",            "rtq_m_gemm32",
+    "rtq_m_lora_mask"};
 
 struct TimedLaunch {
   int kid;

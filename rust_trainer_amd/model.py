@@ -93,12 +93,14 @@ class GpuModel:
         _ffi.check(_ffi.lib().rtq_model_lora_set(self._h, i, None if av is None else av.ctypes.data,
                                                  None if bv is None else bv.ctypes.data), "rtq_model_lora_set")
 
-    def lora_device(self, i: int) -> tuple[int, int, int, int]:
-        """Device addresses of adapter i's (a, b, ga, gb)."""
+    def lora_device(self, i: int) -> tuple[int, int, int, int, int]:
+        """Device addresses of adapter i's (a, b, ga, gb) and the row stride of b / gb in floats
+        (the adapters of fused linears share one B matrix)."""
         ps = [ctypes.c_void_p() for _ in range(4)]
-        _ffi.check(_ffi.lib().rtq_model_lora_device(self._h, i, *[ctypes.byref(p) for p in ps]),
+        ld = ctypes.c_int64()
+        _ffi.check(_ffi.lib().rtq_model_lora_device(self._h, i, *[ctypes.byref(p) for p in ps], ctypes.byref(ld)),
                    "rtq_model_lora_device")
-        return tuple(int(p.value or 0) for p in ps)
+        return tuple(int(p.value or 0) for p in ps) + (ld.value,)
 
     def zero_grad(self) -> None:
         _ffi.check(_ffi.lib().rtq_model_zero_grad(self._h), "rtq_model_zero_grad")
