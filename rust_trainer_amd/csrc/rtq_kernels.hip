@@ -810,9 +810,10 @@ RTQ_FWD(rtq_fwd_q6_k_w_isums, FMT_Q6_K, 4, 2, 2, true)
 RTQ_FWD(rtq_fwd_q6_k_s_isums, FMT_Q6_K, 1, 4, 4, true)
 
 // ============================================================== forward GEMM, large grids (Q4_0 / Q8_0)
-// For outputs of at least a workgroup per CU in 128 x 128 tiles.  Workgroup = 4 waves, tile 128
-// weight rows (8 row groups) x 128 tokens (8 token tiles); wave w computes row groups 2w, 2w+1 x
-// all 8 token tiles (16 MFMA tiles): a weight fragment is unpacked once per 8 token tiles, the
+// For outputs of at least a workgroup per CU in 128 x 128 tiles (128 x 64: rtq_mm64_*).  Workgroup
+// = 4 waves, tile 128 weight rows (8 row groups) x 16 TTN tokens (TTN = 8 or 4 token tiles); wave w
+// computes row groups 2w, 2w+1 x all TTN token tiles: a weight fragment is unpacked once per TTN
+// token tiles, the
 // activation fragments are shared by the four waves through LDS.  Per half chunk (64 columns,
 // two blocks) the workgroup's operands - weight codes and scales, activation codes and scales -
 // are copied global -> LDS by buffer loads with an LDS destination (no VGPR staging) into a
@@ -825,31 +826,33 @@ RTQ_FWD(rtq_fwd_q6_k_s_isums, FMT_Q6_K, 1, 4, 4, true)
 // products formed by a 4-block f16 MFMA in the layout of the block-sum tiles.
 #define RTQ_LDSP(p) ((__attribute__((address_space(3))) void*)(p))
 
-template <int FMT>
-struct MmStage {  // one half chunk in LDS, in 16-byte units
-  static constexpr int XQ = 0;                                       // [tt 8][j2 2][lane 64] codes
-  static constexpr int WQ = 8 * 2 * 64;                              // [rg 8][lane 64] Q4_0 8 B, Q8_0 16 B
+template <int FMT, int TTN>
+struct MmStage {  // one half chunk in LDS, in 16-byte units; TTN token tiles of 16 per workgroup
+  static constexpr int XQ = 0;                                       // [tt TTN][j2 2][lane 64] codes
+  static constexpr int WQ = TTN * 2 * 64;                            // [rg 8][lane 64] Q4_0 8 B, Q8_0 16 B
   static constexpr int WD = WQ + (FMT == FMT_Q4_0 ? 8 * 64 / 2 : 8 * 64);  // [rg 8][row 16] fp16 scale pairs
-  static constexpr int XD = WD + 8 * 4;                              // [t 128] fp16 activation scale pairs
-  static constexpr int SIZE = XD + 128 / 4;
+  static constexpr int XD = WD + 8 * 4;                              // [t 16 TTN] fp16 activation scale pairs
+  static constexpr int SIZE = XD + 16 * TTN / 4;
+  static constexpr int NX = 2 * TTN;                                 // loads of activation fragments
   static constexpr int NWQ = FMT == FMT_Q4_0 ? 16 : 8;               // loads of weight codes
-  static constexpr int LOADS = 16 + NWQ + 2 + 2;                     // wave-wide loads per stage
+  static constexpr int NXD = TTN / 4;                                // loads of activation scales
+  static constexpr int LOADS = NX + NWQ + 2 + NXD;                   // wave-wide loads per stage
   static constexpr int RING = 3;
 };
 
-template <int FMT>
+template <int FMT, int TTN>
 __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
-  using St = MmStage<FMT>;
+  using St = MmStage<FMT, TTN>;
   extern __shared__ u4v mm_lds[];
   const int lane = threadIdx.x & 63, li = lane & 15, g = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int Kc = a.Kp / 128, nhc = a.Kp / 64;
   const int ngroups = a.Np / 16, ntt = a.Tp / 16;
   // XCD-aware tile order: workgroup id -> (XCD id % 8, slot id / 8) -> a contiguous tile range per XCD
-  const int nrb = (ngroups + 7) / 8, ntiles = nrb * (ntt / 8);
+  const int nrb = (ngroups + 7) / 8, ntiles = nrb * (ntt / TTN);
   const int id = blockIdx.x, xcd = id & 7, per = ntiles >> 3, rem = ntiles & 7;
   const int q = xcd * per + min(xcd, rem) + (id >> 3);
-  const int rg0 = (q % nrb) * 8, tt0 = (q / nrb) * 8;
+  const int rg0 = (q % nrb) * 8, tt0 = (q / nrb) * TTN;
 
   // Operands reach LDS by buffer loads with the LDS destination (4 or 16 bytes per lane; gfx950
   // has no 8-byte form, so 8-byte items - Q4_0 half-chunk codes, scale pairs - go as pairs of
@@ -868,24 +871,25 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
   for (int k = 0; k < NSLOT; k++) {
     const int i = w + 4 * k;
     uint32_t v = 0;
-    if (i < 16) {  // activation fragments: token tile i / 2, block 2h + i % 2
+    if (i < St::NX) {  // activation fragments: token tile i / 2, block 2h + i % 2
       const uint32_t ttg = (uint32_t)min(tt0 + (i >> 1), ntt - 1);
       v = ((ttg * Kc * 4 + (i & 1)) * 64 + lane) * 16;
-    } else if (i < 16 + St::NWQ) {  // weight codes
-      if (FMT == FMT_Q4_0) {  // row group (i - 16) / 2, words 64 m .. 64 m + 63 of its 128
-        const int wi = ((i - 16) & 1) * 64 + lane;
-        const uint32_t rgg = (uint32_t)min(rg0 + ((i - 16) >> 1), ngroups - 1);
+    } else if (i < St::NX + St::NWQ) {  // weight codes
+      const int iw = i - St::NX;
+      if (FMT == FMT_Q4_0) {  // row group iw / 2, words 64 m .. 64 m + 63 of its 128
+        const int wi = (iw & 1) * 64 + lane;
+        const uint32_t rgg = (uint32_t)min(rg0 + (iw >> 1), ngroups - 1);
         v = ((rgg * Kc * 64 + (wi >> 1)) * 4 + (wi & 1)) * 4;
       } else {
-        const uint32_t rgg = (uint32_t)min(rg0 + i - 16, ngroups - 1);
+        const uint32_t rgg = (uint32_t)min(rg0 + iw, ngroups - 1);
         v = (rgg * Kc * 2 * 64 + lane) * 16;
       }
-    } else if (i < 16 + St::NWQ + 2) {  // weight scale pairs: word wi -> row wi % 16 of row group wi / 16
-      const int wi = (i - 16 - St::NWQ) * 64 + lane;
+    } else if (i < St::NX + St::NWQ + 2) {  // weight scale pairs: word wi -> row wi % 16 of row group wi / 16
+      const int wi = (i - St::NX - St::NWQ) * 64 + lane;
       const uint32_t rgg = (uint32_t)min(rg0 + (wi >> 4), ngroups - 1);
       v = ((rgg * Kc * 16 + (wi & 15)) * 2) * 4;
     } else {  // fp16 activation scales of blocks 2h, 2h+1: word wi -> token wi
-      const int wi = (i - 18 - St::NWQ) * 64 + lane;
+      const int wi = (i - St::NX - St::NWQ - 2) * 64 + lane;
       const uint32_t tok = (uint32_t)min(tt0 * 16 + wi, a.Tp - 1);
       v = tok * 8;
     }
@@ -897,29 +901,30 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
 #pragma unroll
     for (int k = 0; k < NSLOT; k++) {
       const int i = w + 4 * k;  // wave-uniform
-      if (i < 16) {
+      if (i < St::NX) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, RTQ_LDSP(S + St::XQ + i * 64), 16, voff[k], hc * 2048u, 0, 0);
-      } else if (i < 16 + St::NWQ) {
+      } else if (i < St::NX + St::NWQ) {
+        const int iw = i - St::NX;
         if (FMT == FMT_Q4_0)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + ((i - 16) >> 1) * 32 + ((i - 16) & 1) * 16), 4,
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + (iw >> 1) * 32 + (iw & 1) * 16), 4,
                                                    voff[k], kc * 1024u + h * 8u, 0, 0);
         else
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + (i - 16) * 64), 16, voff[k], hc * 1024u, 0, 0);
-      } else if (i < 16 + St::NWQ + 2) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_wd, RTQ_LDSP(S + St::WD + (i - 16 - St::NWQ) * 16), 4, voff[k],
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + iw * 64), 16, voff[k], hc * 1024u, 0, 0);
+      } else if (i < St::NX + St::NWQ + 2) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_wd, RTQ_LDSP(S + St::WD + (i - St::NX - St::NWQ) * 16), 4, voff[k],
                                                  kc * 128u + h * 4u, 0, 0);
       } else if (i < St::LOADS) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_xd, RTQ_LDSP(S + St::XD + (i - 18 - St::NWQ) * 16), 4, voff[k],
-                                                 kc * (uint32_t)a.Tp * 8u + h * 4u, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_xd, RTQ_LDSP(S + St::XD + (i - St::NX - St::NWQ - 2) * 16), 4,
+                                                 voff[k], kc * (uint32_t)a.Tp * 8u + h * 4u, 0, 0);
       }
     }
   };
 
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
   const f16v zero16 = {};
-  f4 acc[8][2];  // [token tile][row group]
+  f4 acc[TTN][2];  // [token tile][row group]
 #pragma unroll
-  for (int i = 0; i < 8; i++)
+  for (int i = 0; i < TTN; i++)
 #pragma unroll
     for (int r = 0; r < 2; r++) acc[i][r] = zero;
 
@@ -964,8 +969,8 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
     // that consume tile i
     products(0, 0);
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      if (i + 1 < 8) products(i + 1, (i + 1) & 1);
+    for (int i = 0; i < TTN; i++) {
+      if (i + 1 < TTN) products(i + 1, (i + 1) & 1);
 #pragma unroll
       for (int r = 0; r < 2; r++)
 #pragma unroll
@@ -1009,22 +1014,23 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
     for (int j0 = 0; j0 < a.r; j0 += 16) {
       float hv[8], bv[8];
 #pragma unroll
-      for (int k = 0; k < 8; k++) {
+      for (int k = 0; k < 8; k++) {  // rows e / 16: 16 TTN token rows of h, 128 weight rows of B
         const int e = threadIdx.x + 256 * k, tl = e >> 4, j = j0 + (e & 15);
-        hv[k] = sum_partials(a.hp, (int64_t)min(tt0 * 16 + tl, a.T - 1) * a.r + min(j, a.r - 1), a.nhp);
+        hv[k] = tl < 16 * TTN ? sum_partials(a.hp, (int64_t)min(tt0 * 16 + tl, a.T - 1) * a.r + min(j, a.r - 1), a.nhp)
+                              : 0.0f;
         bv[k] = a.lb[(int64_t)min(rg0 * 16 + tl, a.N - 1) * a.r + min(j, a.r - 1)];
       }
 #pragma unroll
       for (int k = 0; k < 8; k++) {
         const int e = threadIdx.x + 256 * k;
-        sh[e >> 4][j0 + (e & 15)] = hv[k];
+        if ((e >> 4) < 16 * TTN) sh[e >> 4][j0 + (e & 15)] = hv[k];
         sb[e >> 4][j0 + (e & 15)] = bv[k];
       }
     }
     __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
+  for (int i = 0; i < TTN; i++) {
 #pragma unroll
     for (int r = 0; r < 2; r++) {
       const int tl = i * 16 + li, t = tt0 * 16 + tl;
@@ -1068,8 +1074,11 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
   }
 }
 
-extern "C" __global__ __launch_bounds__(256) void rtq_mm_q4_0(FwdArgs a) { mm_tile<FMT_Q4_0>(a); }
-extern "C" __global__ __launch_bounds__(256) void rtq_mm_q8_0(FwdArgs a) { mm_tile<FMT_Q8_0>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_mm_q4_0(FwdArgs a) { mm_tile<FMT_Q4_0, 8>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_mm_q8_0(FwdArgs a) { mm_tile<FMT_Q8_0, 8>(a); }
+// 128 rows x 64 tokens: twice the grid, for outputs whose 128 x 128 tiles would leave CUs idle
+extern "C" __global__ __launch_bounds__(256) void rtq_mm64_q4_0(FwdArgs a) { mm_tile<FMT_Q4_0, 4>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_mm64_q8_0(FwdArgs a) { mm_tile<FMT_Q8_0, 4>(a); }
 
 // ============================================================== forward GEMV (T <= 16)
 // MFMA orientation transposed against fwd_tile: A operand = the 16 token slots x 32 columns of the

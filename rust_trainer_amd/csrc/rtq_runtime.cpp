@@ -122,6 +122,8 @@ enum Kid {
   K_FWD_Q8_0_W8,
   K_MM_Q4_0,     // large-grid forward (128 x 128 tiles, LDS ring)
   K_MM_Q8_0,
+  K_MM64_Q4_0,   // the same with 128 x 64 tiles
+  K_MM64_Q8_0,
   K_BWD_PREP,
   K_DX,          // + format
   K_DX16 = K_DX + F_COUNT,  // + format: t <= 16
@@ -147,6 +149,7 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_fwd_q4_0_s_isums", "rtq_fwd_q8_0_s_isums", "rtq_fwd_q4_k_s_isums", "rtq_fwd_q6_k_s_isums",
     "rtq_gemv_q4_0",        "rtq_gemv_q8_0",        "rtq_gemv_q4_k",        "rtq_gemv_q6_k",
     "rtq_fwd_q4_0_w8",      "rtq_fwd_q8_0_w8",      "rtq_mm_q4_0",          "rtq_mm_q8_0",
+    "rtq_mm64_q4_0",        "rtq_mm64_q8_0",
     "rtq_bwd_prep",
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
@@ -183,7 +186,8 @@ struct rtq_ctx {
   int dx_splits = 0;  // 0: automatic; RTQ_DX_SPLITS overrides (tuning)
   int dx_wide = -1;   // 256-token dx tiles: -1 automatic, 0 never, 1 for every t > 16 (RTQ_DX_WIDE)
   int fwd_waves = 8;  // waves splitting K in the wide Q4_0 / Q8_0 forward (RTQ_FWD_WAVES: 4 or 8)
-  int fwd_mm = -1;    // large-grid forward: -1 automatic, 0 never, 1 whenever the format allows (RTQ_FWD_MM)
+  int fwd_mm = -1;    // large-grid forward: -1 automatic, 0 never, 1 / 2 the 128- / 64-token tiles whenever
+                      // the format allows (RTQ_FWD_MM)
   rocblas_handle blas = nullptr;  // created on the first trainer-native (f32 GEMM) weight
   int64_t t_launches[K_COUNT] = {};
   double t_ms[K_COUNT] = {};
@@ -319,8 +323,9 @@ constexpr int kFwdWideTT = 4;     // rtq_fwd_*_w: 64 tokens x (16 * wide_rg) row
 constexpr int kMmTile = 128;      // rtq_mm_*: 128 rows x 128 tokens per workgroup
 // rtq_mm_* dynamic LDS: a 3-stage ring of half-chunk operands (codes, scales), reused after the
 // K loop for the LoRA h and B rows of the tile (128 rows each, RTQ_LDS_RANK + 1 floats)
-unsigned mm_lds_bytes(int type) {
-  const unsigned stage = 16u * (8 * 2 * 64 + (type == RTQ_TYPE_Q4_0 ? 8 * 64 / 2 : 8 * 64) + 8 * 4 + 128 / 4);
+unsigned mm_lds_bytes(int type, int ttn) {  // ttn: token tiles of 16 per workgroup (8 or 4)
+  const unsigned stage =
+      16u * (ttn * 2 * 64 + (type == RTQ_TYPE_Q4_0 ? 8 * 64 / 2 : 8 * 64) + 8 * 4 + 16 * ttn / 4);
   return std::max(3 * stage, 2u * 128u * (RTQ_LDS_RANK + 1) * 4u);
 }
 constexpr int kFwdSkinnyRG = 4;   // rtq_fwd_*_s: 16 tokens x 64 rows per workgroup
@@ -515,10 +520,18 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   const bool kq = is_kquant(w->type);
   const int64_t rg_per_wg = p.skinny ? kFwdSkinnyRG : wide_rg(w->type);
   const int64_t gx = cdiv(w->Np / 16, rg_per_wg), gy = p.skinny ? p.Tp / 16 : cdiv(t, 16 * kFwdWideTT);
-  // the large-grid kernel once its 128 x 128 tiles alone give a workgroup per CU
-  const int64_t mm_tiles = cdiv(w->Np / 16, 8) * (p.Tp / kMmTile);
-  const bool mm = !p.skinny && !isums && !is_kquant(w->type) &&
-                  (c->fwd_mm == 1 || (c->fwd_mm < 0 && mm_tiles >= c->cu_count));
+  // the large-grid kernel once its 128 x 128 tiles alone give a workgroup per CU, else its
+  // 128 x 64 tiles if those do
+  const int64_t mm_rows = cdiv(w->Np / 16, 8);
+  const int64_t mm128 = mm_rows * (p.Tp / kMmTile), mm64 = mm_rows * (p.Tp / 64);
+  int mm_ttn = 0;  // token tiles per workgroup of the chosen rtq_mm kernel, 0: none
+  if (!p.skinny && !isums && !is_kquant(w->type)) {
+    if (c->fwd_mm == 1) mm_ttn = 8;
+    else if (c->fwd_mm == 2) mm_ttn = 4;
+    else if (c->fwd_mm < 0) mm_ttn = mm128 >= c->cu_count ? 8 : (mm64 >= c->cu_count ? 4 : 0);
+  }
+  const bool mm = mm_ttn > 0;
+  const int64_t mm_tiles = mm_ttn == 8 ? mm128 : mm64;
   const int64_t tiles = gx * gy;
   // split K across workgroups when the output alone gives too few of them (atomics into a
   // zeroed y); every split keeps at least one half chunk per wave (K-quants: one super-block of
@@ -563,8 +576,8 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   if (mm && (!fa.wq || !fa.wdr || !fa.xq || !fa.xdh || !fa.y))
     return fail(RTQ_ERR_INVALID, "internal: rtq_mm_* operand missing");
   if (mm)
-    return launch(c, w->type == RTQ_TYPE_Q4_0 ? K_MM_Q4_0 : K_MM_Q8_0, dim3((unsigned)mm_tiles), dim3(256), st, fa,
-                  mm_lds_bytes(w->type));
+    return launch(c, (mm_ttn == 8 ? K_MM_Q4_0 : K_MM64_Q4_0) + (w->type == RTQ_TYPE_Q4_0 ? 0 : 1),
+                  dim3((unsigned)mm_tiles), dim3(256), st, fa, mm_lds_bytes(w->type, mm_ttn));
   int kid = (p.skinny ? (isums ? K_FWD_S_ISUMS : K_FWD_S) : (isums ? K_FWD_W_ISUMS : K_FWD_W)) + fmt_index(w->type);
   int threads = 256;
   if (!p.skinny && !isums && !kq && c->fwd_waves == 8) {
@@ -843,7 +856,7 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   if (const char* e = getenv("RTQ_DX_SPLITS")) c->dx_splits = atoi(e);
   if (const char* e = getenv("RTQ_DX_WIDE")) c->dx_wide = atoi(e) ? 1 : 0;
   if (const char* e = getenv("RTQ_FWD_WAVES")) c->fwd_waves = atoi(e) == 4 ? 4 : 8;
-  if (const char* e = getenv("RTQ_FWD_MM")) c->fwd_mm = atoi(e) ? 1 : 0;
+  if (const char* e = getenv("RTQ_FWD_MM")) c->fwd_mm = std::min(std::max(atoi(e), 0), 2);
   hipError_t e = hipModuleLoadData(&c->mod, rtq_hsaco_begin);
   if (e != hipSuccess) {
     delete c;

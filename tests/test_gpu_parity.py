@@ -278,14 +278,15 @@ def test_lm_head_shape_t1(ctx, wtype):
 
 
 # ---------------------------------------------------------------- large-grid forward (rtq_mm_*)
-@pytest.fixture(scope="module")
-def ctx_mm():
+@pytest.fixture(scope="module", params=["1", "2"], ids=["mm128", "mm64"])
+def ctx_mm(request):
     """A context that sends every wide Q4_0 / Q8_0 forward through the 128 x 128-tile kernel
-    (RTQ_FWD_MM=1), so small shapes cover its padding and epilogue cases."""
+    (RTQ_FWD_MM=1) or its 128 x 64-tile variant (RTQ_FWD_MM=2), so small shapes cover their
+    padding and epilogue cases."""
     import os
 
     old = os.environ.get("RTQ_FWD_MM")
-    os.environ["RTQ_FWD_MM"] = "1"
+    os.environ["RTQ_FWD_MM"] = request.param
     try:
         c = rt.Context(0)
     finally:
@@ -325,6 +326,29 @@ def test_forward_mm_selected_by_grid_size(ctx, wtype):
     w = hip(ctx, wtype, blocks, n, k)
     y = w.forward(x, t)
     assert rel_err(y, O.frozen_forward(wtype, blocks, n, k, x, nthreads=8)) <= TOL
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
+@pytest.mark.parametrize("r", [0, 48])
+def test_forward_mm64_selected_by_grid_size(ctx, wtype, r):
+    # the fused q|k|v shape of the configs[2] step: 4096 rows x 512 tokens is 128 tiles of 128 x
+    # 128 (half the CUs) but 256 of 128 x 64, so the default context picks rtq_mm64_*
+    n, k, t = 4096, 1024, 512
+    blocks, x, _ = make(wtype, n, k, t)
+    lin = rt.Linear("blk.0.attn_qkv", hip(ctx, wtype, blocks, n, k))
+    kw = {}
+    if r:
+        A, B = lora(n, k, r)
+        lin.lora = rt.Lora(r, 2.0 * r, A, B)
+        kw = dict(A=A, B=B, alpha=2.0 * r)
+    ctx.set_timing(True)
+    ctx.reset_timing()
+    y = lin.forward(x, t)
+    ran = ctx.timing()
+    ctx.set_timing(False)
+    assert any(name.startswith("rtq_mm64_") for name in ran), ran
+    want = O.linear_forward(wtype, blocks, n, k, x, nthreads=16, **kw)
+    assert rel_err(y, want) <= TOL
 
 
 @pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
