@@ -176,13 +176,15 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_qk_bwd(MQkArgs a) {
 // ------------------------------------------------------------------ batched f32 GEMM
 // BM x 64 output tile per 256-thread workgroup on f32 MFMA (16x16x4: exact f32 products, f32
 // accumulation); wave w owns rows (w / 2) BM / 2 .. and columns (w % 2) 32 .. as (BM / 32) x 2
-// MFMA tiles.  32-deep k slabs go through LDS; the next slab's operands are loaded into registers
-// while the current one feeds the MFMAs.  Operands are read with their own strides, the
+// MFMA tiles.  k slabs (see MGemmSlab) go through LDS; the next slab's operands are loaded into
+// registers while the current one feeds the MFMAs.  Operands are read with their own strides, the
 // unit-stride index fastest across lanes.  BM = 32 doubles the grid of the thin products
 // (N = head_dim) so that each CU holds two workgroups.
 template <int BM>
 struct MGemmSlab {
-  static constexpr int BN = 64, BK = 32, NA = BM * BK / 256, NB = BN * BK / 256;
+  // 32-row tiles serve the long-K products (O, dV, dQ, dK: K = t): 64-deep slabs, whose MFMAs
+  // outlast the next slab's load latency; 64-row tiles the K = head_dim ones: 32-deep slabs
+  static constexpr int BN = 64, BK = BM == 32 ? 64 : 32, NA = BM * BK / 256, NB = BN * BK / 256;
   float a[NA], b[NB];
 };
 
