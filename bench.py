@@ -314,13 +314,13 @@ def traffic_run_step() -> None:
 def step_kernel_work(name: str) -> tuple[float, float] | None:
     """Average algorithmic (bytes, flops) per launch of a block-linear kernel of the configs[2] step."""
     cfg = {"n_embd": 1024, "n_head": 16, "n_head_kv": 8, "head_dim": 128, "n_ff": 3072}
-    calls = step_layer_calls(cfg, STEP_T)
-    if name.startswith("rtq_fwd_"):
-        w = [call_work(2, n, k, STEP_T, r, False) for n, k, r in calls]
-    elif name.startswith("rtq_dx_"):
+    calls, backward = step_calls_for(name, cfg)
+    if calls is None:
+        return None
+    if backward:
         w = [(float(n * k // 32 * 18 + STEP_T * (n + k) * 4), float(2 * STEP_T * n * k)) for n, k, _ in calls]
     else:
-        return None
+        w = [call_work(2, n, k, STEP_T, r, False) for n, k, r in calls]
     return sum(b for b, _ in w) / len(w), sum(f for _, f in w) / len(w)
 
 
@@ -356,7 +356,7 @@ def traffic_report(fetch_dir: str, write_dir: str, step: bool = False) -> None:
         wk = sum(v for v, _ in write[name]) / len(write[name])
         total = (fk * ff + wk * wf) * 1024 if ff and wf else None
         algo = step_kernel_work(name) if step else kernel_work(name)
-        out = {"kernel": name, "workload": "configs[2] training step (average launch of the block linears)" if step
+        out = {"kernel": name, "workload": "configs[2] training step (average launch over the block linears it serves)" if step
                else "configs[0] (Q4_0 3072x1024, T=256, LoRA r=16)",
                "fetch_kib_raw": round(fk, 1), "write_kib_raw": round(wk, 1),
                "fetch_scale": round(ff, 4) if ff else None, "write_scale": round(wf, 4) if wf else None,
@@ -594,6 +594,20 @@ def step_layer_calls(cfg: dict, t: int) -> list[tuple[int, int, int]]:
     return [(nh * hd + 2 * nkv * hd, d, 3 * STEP_R), (d, nh * hd, STEP_R), (2 * ff, d, 2 * STEP_R), (d, ff, STEP_R)]
 
 
+def step_calls_for(name: str, cfg: dict):
+    """(calls, backward) of the block linears a kernel serves in the step, by the runtime's choice at
+    T = 512: rtq_mm64_* the wide fused forwards (q | k | v, gate | up), rtq_fwd_*_w8 the others (o,
+    down), rtq_dx_* every input gradient."""
+    qkv, o, gu, down = step_layer_calls(cfg, STEP_T)
+    if name.startswith("rtq_dx_"):
+        return [qkv, o, gu, down], True
+    if name.startswith("rtq_mm64_"):
+        return [qkv, gu], False
+    if name.startswith("rtq_fwd_"):
+        return [o, down], False
+    return None, False
+
+
 def step_roofline(cfg: dict, kernels: dict) -> dict | None:
     """Roofline of the dominant quantised-matmul kernel of the step: the algorithmic bytes and flops
     of the block linears it ran (forward: W + x + y + adapter, 2 T N K + LoRA; dx: W + dy + dx,
@@ -602,10 +616,12 @@ def step_roofline(cfg: dict, kernels: dict) -> dict | None:
     if not qmm:
         return None
     name = max(qmm, key=lambda k: qmm[k]["total_us"])
-    calls = step_layer_calls(cfg, STEP_T) * cfg["n_layer"]
+    per_layer, backward = step_calls_for(name, cfg)
+    if per_layer is None:
+        return None
+    calls = per_layer * cfg["n_layer"]
     if qmm[name]["launches"] != len(calls):
         return None  # the kernel also served other shapes: no per-call attribution
-    backward = name.startswith("rtq_dx")
     bytes_ = flops = 0.0
     for n, k, r in calls:
         b, f = call_work(2, n, k, STEP_T, 0 if backward else r, False)
