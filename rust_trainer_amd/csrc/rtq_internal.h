@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include "rtq.h"
+#include "rtq_kargs.h"
 
 // kernels of the decoder block (rtq_model_kernels.hip), in this order after the matmul kernels
 enum RtqModelKernel {
@@ -29,4 +30,10 @@ rtq_status rtq_fail(rtq_status st, const char* fmt, ...);
 // launches decoder kernel km with one by-value argument struct at args (timed like every launch)
 rtq_status rtq_model_launch(rtq_ctx* c, int km, dim3 grid, dim3 block, hipStream_t s, const void* args);
 int rtq_ctx_device_id(const rtq_ctx* c);
+// rtq_linear_backward_d for a block-diagonal adapter over row-concatenated weights: gb and
+// g = s dy.B only inside rb's blocks (gb outside them is left untouched).  Quantised weights only;
+// a dense weight computes every pair (the caller clears gb outside the blocks).
+rtq_status rtq_linear_backward_blocks_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const RankBlocks* rb,
+                                        const float* x, const float* dy, int64_t t, float* dx, float* ga, float* gb,
+                                        void* stream);
 #endif

@@ -117,6 +117,14 @@ struct FwdArgs {
 
 // ---------------------------------------------------------------- backward
 // rtq_bwd_prep: partials of h = x . A^T and of dy . B per 256-column slice (src/linear.rs:106-111)
+// Block-diagonal adapter of row-concatenated weights (a fused q|k|v or gate|up projection):
+// member m owns weight rows [row0[m], row0[m] + nrow[m]) and ranks [col0[m], col0[m] + r[m]) (r 0:
+// not adapted); only those (row, rank) pairs of B and gb exist.  nm = 0: one plain adapter.
+struct RankBlocks {
+  int nm;
+  int row0[3], nrow[3], col0[3], r[3];
+};
+
 struct BwdPrepArgs {
   const float* x;
   const float* A;
@@ -129,6 +137,7 @@ struct BwdPrepArgs {
   int nhq;
   float* gp;     // [T][r][ngq] partials of dy . B
   int ngq;
+  RankBlocks rb;  // g = dy . B restricted to each member's rows
 };
 
 // part[z][t][k] = sum over rows n of split z of dy[t][n] W[n][k], three bf16 MFMAs per product (hi/lo split of dy
@@ -171,6 +180,8 @@ struct LoraGradArgs {
   int nsplit;
   int accumulate;        // 1: dx += (FrozenMatmul::backward_input); 0: dx = (Linear::backward)
   int part_rows;         // 1: partials row-major [nsplit][T][K] (rtq_dx16_*); 0: fragment order (rtq_dx_*)
+  RankBlocks rb;         // gb written only inside the members' blocks
+  int gb_cpt;            // > 0: n_gb = row tiles x gb_cpt rank tiles counted from each row tile's member's col0
 };
 
 // rows [r0, r0+count) dequantised to f32 (bit-exact ggml dequant)

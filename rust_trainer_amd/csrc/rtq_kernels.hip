@@ -227,16 +227,34 @@ __device__ __forceinline__ void load_seg(const float* p, bool ok, float v[16]) {
   }
 }
 
+// (row n, rank j) lies in a member's block of a block-diagonal adapter (always, for a plain one)
+__device__ __forceinline__ bool rb_keep(const RankBlocks& b, int n, int j) {
+  if (b.nm == 0) return true;
+  bool keep = false;
+  for (int m = 0; m < b.nm; m++)
+    if (n >= b.row0[m] && n < b.row0[m] + b.nrow[m]) keep = j >= b.col0[m] && j < b.col0[m] + b.r[m];
+  return keep;
+}
+// some (row, rank) pair of [n0, n1) x [j0, j1) lies in a member's block
+__device__ __forceinline__ bool rb_any(const RankBlocks& b, int n0, int n1, int j0, int j1) {
+  if (b.nm == 0) return true;
+  for (int m = 0; m < b.nm; m++)
+    if (max(n0, b.row0[m]) < min(n1, b.row0[m] + b.nrow[m]) && max(j0, b.col0[m]) < min(j1, b.col0[m] + b.r[m]))
+      return true;
+  return false;
+}
+
 // One LoRA partial product over a 256-column slice, by one 256-thread workgroup (f32 MFMA):
 //   P[t][j] = sum over k in [k0, k0 + 256) of S[t][k] * M(j, k),  t in [t0, t0 + 16), j in [0, r)
 // with M(j, k) = M[j * ldm + k] (A rows: LoRA down, src/linear.rs:85) when !MT, or
 // M[k * ldm + j] (B columns: g = dy . B, src/linear.rs:111) when MT; S rows have length ks.
 // Written to out[(t * r + j) * pstride + pidx] (slice index fastest, so a consumer sums a token's
-// partials in slice order with a few wide loads).  Columns beyond kend count as zero.
+// partials in slice order with a few wide loads).  Columns beyond kend count as zero.  With MT, B
+// entries outside rb's blocks count as zero, and rank tiles with none inside are written as zeros.
 template <bool MT>
 __device__ __forceinline__ void lora_partial(const float* S, int T, int ks, const float* M, int ldm, int mrows, int r,
                                              int k0, int kend, int t0, float* out, int pstride, int pidx, float* sx,
-                                             float* sm, float* red) {
+                                             float* sm, float* red, const RankBlocks* rb = nullptr) {
   constexpr int LDX = RTQ_ACT_KQ + 1, LDB = 17;
   const int tid = threadIdx.x, tl = tid >> 4, sg = tid & 15, t = t0 + tl;
   const int lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
@@ -252,6 +270,11 @@ __device__ __forceinline__ void lora_partial(const float* S, int T, int ks, cons
     for (int i = 0; i < 16; i++) sx[tl * LDX + sg * 16 + i] = v[i];
   }
   for (int j0 = 0; j0 < r; j0 += 16) {
+    if (MT && !rb_any(*rb, k0, min(k0 + RTQ_ACT_KQ, kend), j0, min(j0 + 16, r))) {  // uniform over the workgroup
+      const int tt = tid >> 4, jj = tid & 15, ty = t0 + tt, jo = j0 + jj;
+      if (ty < T && jo < r) out[((int64_t)ty * r + jo) * pstride + pidx] = 0.0f;
+      continue;
+    }
     if (!MT) {  // A rows j0 .. j0+15, columns k0 .. k0+255: thread (row tl, segment sg)
       float v[16];
       const int jr = j0 + tl, kk = k0 + sg * 16;
@@ -268,7 +291,7 @@ __device__ __forceinline__ void lora_partial(const float* S, int T, int ks, cons
       for (int i = 0; i < 16; i++) {
         const int j = j0 + i;
         const float bv = M[(int64_t)min(k, mrows - 1) * ldm + min(j, r - 1)];
-        sm[tid * LDB + i] = (k < kend && j < r) ? bv : 0.0f;
+        sm[tid * LDB + i] = (k < kend && j < r && rb_keep(*rb, k, j)) ? bv : 0.0f;
       }
     }
     __syncthreads();
@@ -1326,7 +1349,7 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_prep(BwdPrepArgs a) {
                         red);
   else
     lora_partial<true>(a.dy, a.T, a.N, a.B, a.r, a.N, a.r, (blockIdx.y - a.nhq) * KQ, a.N, t0, a.gp, a.ngq,
-                       blockIdx.y - a.nhq, sx, sm, red);
+                       blockIdx.y - a.nhq, sx, sm, red, &a.rb);
 }
 
 // ============================================================== dx = dy . W
@@ -1848,7 +1871,17 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
   if (b < a.n_gb + a.n_ga) {
     const bool is_gb = b < a.n_gb;
     if (!is_gb) b -= a.n_gb;
-    const int rt = b / jt, ct = b % jt;
+    int rt = b / jt, ct = b % jt;
+    if (is_gb) {  // block-diagonal adapter: only tiles that meet a member's block (uniform exit)
+      if (a.gb_cpt > 0) {  // rank tiles counted from the col0 of the row tile's member
+        rt = b / a.gb_cpt;
+        int m = 0;
+        for (int i = 1; i < a.rb.nm; i++)
+          if (rt * 16 >= a.rb.row0[i]) m = i;
+        ct = (a.rb.nm ? a.rb.col0[m] / 16 : 0) + b % a.gb_cpt;
+      }
+      if (ct >= jt || !rb_any(a.rb, rt * 16, min(rt * 16 + 16, a.N), ct * 16, min(ct * 16 + 16, a.r))) return;
+    }
     // gb: rows n (tile rt), cols j (tile ct);  ga: rows j (tile ct), cols k (tile rt)
     const int rrow = is_gb ? rt * 16 + li : ct * 16 + li;
     const int ccol = is_gb ? ct * 16 + li : rt * 16 + li;
@@ -1887,7 +1920,7 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
       for (int ww = 0; ww < NW; ww++) s += red[ww * 256 + threadIdx.x];
       if (is_gb) {
         const int n = rt * 16 + rl, j = ct * 16 + cl;
-        if (n < a.N && j < a.r) a.gb[(int64_t)n * a.r + j] += s;
+        if (n < a.N && j < a.r && rb_keep(a.rb, n, j)) a.gb[(int64_t)n * a.r + j] += s;
       } else {
         const int j = ct * 16 + rl, k = rt * 16 + cl;
         if (j < a.r && k < a.K) a.ga[(int64_t)j * a.K + k] += s;

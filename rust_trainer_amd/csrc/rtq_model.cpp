@@ -204,10 +204,27 @@ rtq_status lin_fwd(rtq_model* m, const Group& l, const float* x, int64_t t, floa
   return rtq_linear_forward_d(m->ctx, l.w, l.bias, l.rank > 0 ? &lv : nullptr, x, t, y, stream_of(m));
 }
 
+// a fused group's adapter is block-diagonal (each member's rows see only its own ranks): the
+// quantised backward computes gb and g = s dy.B inside the blocks only; the dense (rocBLAS) one
+// computes every pair and the off-block gb entries are cleared after it
 rtq_status lin_bwd(rtq_model* m, const Group& l, const float* x, const float* dy, int64_t t, float* dx) {
   const rtq_lora lv = lora_view(l);
-  M_TRY(rtq_linear_backward_d(m->ctx, l.w, l.rank > 0 ? &lv : nullptr, x, dy, t, dx, l.ga, l.gb, stream_of(m)));
+  const int wt = rtq_weight_type(l.w);
+  const bool dense = wt == RTQ_TYPE_F32 || wt == RTQ_TYPE_TQ8_0;
+  if (l.rank == 0 || l.nm < 2 || dense)
+    M_TRY(rtq_linear_backward_d(m->ctx, l.w, l.rank > 0 ? &lv : nullptr, x, dy, t, dx, l.ga, l.gb, stream_of(m)));
   if (l.rank == 0 || l.nm < 2) return RTQ_OK;
+  if (!dense) {
+    RankBlocks rb{};
+    rb.nm = l.nm;
+    for (int i = 0; i < l.nm; i++) {
+      rb.row0[i] = (int)l.mem[i].row0;
+      rb.nrow[i] = (int)l.mem[i].rows;
+      rb.col0[i] = (int)l.mem[i].col0;
+      rb.r[i] = (int)l.mem[i].r;
+    }
+    return rtq_linear_backward_blocks_d(m->ctx, l.w, &lv, &rb, x, dy, t, dx, l.ga, l.gb, stream_of(m));
+  }
   MMaskArgs ma{l.gb, l.rows, l.rank, l.nm, {}, {}, {}, {}};
   for (int i = 0; i < l.nm; i++) {
     ma.row0[i] = l.mem[i].row0;

@@ -649,7 +649,7 @@ int64_t lora_slices(int64_t n) { return roundup(cdiv(std::max<int64_t>(n, 1), RT
 // partials of dx; its last grid row sums the h, g partials) -> rtq_bwd_finish.
 rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, int64_t t, float* dx, bool accumulate,
                             const float* x, const float* la, const float* lb, int64_t r, float s, float* ga,
-                            float* gb, Arena& ar, hipStream_t st) {
+                            float* gb, Arena& ar, hipStream_t st, const RankBlocks* rb = nullptr) {
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
   if (is_dense(w->type))
@@ -666,7 +666,8 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   float* part = ar.take<float>(dp.part_floats);
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   if (lora) {
-    BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq};
+    BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq, RankBlocks{}};
+    if (rb) pa.rb = *rb;
     RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, 16), (unsigned)(nhq + ngq)), dim3(256), st, pa));
   }
   DxArgs xa{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, (int)dp.splits, part,
@@ -679,8 +680,21 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   RTQ_TRY(launch(c, kid, dim3((unsigned)(nmain + nfin)), dim3(dp.tok16 ? 256 : 512), st, xa));
   const int64_t jt = cdiv(r, 16);
   LoraGradArgs fa{dy, h, g, x, la, (int)t, N, K, (int)r, s, gb, ga, dx, 0, 0, 0, part, (int)dp.splits, accumulate ? 1 : 0,
-                  dp.tok16 ? 1 : 0};
-  fa.n_gb = lora ? (int)(cdiv(N, 16) * jt) : 0;
+                  dp.tok16 ? 1 : 0, RankBlocks{}, 0};
+  // block-diagonal adapter with members on 16-row boundaries: per row tile only the rank tiles of
+  // its member's block (gb_cpt of them at most)
+  fa.gb_cpt = 0;
+  if (rb && rb->nm > 0) {
+    fa.rb = *rb;
+    bool aligned = true;
+    int cpt = 0;
+    for (int m = 0; m < rb->nm; m++) {
+      aligned = aligned && rb->row0[m] % 16 == 0;
+      if (rb->r[m] > 0) cpt = std::max(cpt, (rb->col0[m] + rb->r[m] - 1) / 16 - rb->col0[m] / 16 + 1);
+    }
+    if (aligned) fa.gb_cpt = std::max(cpt, 1);
+  }
+  fa.n_gb = lora ? (int)(cdiv(N, 16) * (fa.gb_cpt > 0 ? fa.gb_cpt : jt)) : 0;
   fa.n_ga = lora ? (int)(cdiv(K, 16) * jt) : 0;
   // one wave per quarter of a dx fragment (or per token and 64 columns), nw per workgroup; 16 waves
   // per workgroup when the dA / dB tiles reduce over many tokens
@@ -1109,8 +1123,9 @@ rtq_status rtq_frozen_backward_input_d(rtq_ctx* c, const rtq_weight* w, const fl
   return enqueue_backward(c, w, dy, t, dx, true, nullptr, nullptr, nullptr, 0, 0.0f, nullptr, nullptr, ar, st);
 }
 
-rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const float* x,
-                                 const float* dy, int64_t t, float* dx, float* ga, float* gb, void* stream) {
+static rtq_status linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const float* x,
+                                    const float* dy, int64_t t, float* dx, float* ga, float* gb, void* stream,
+                                    const RankBlocks* rb) {
   RTQ_TRY(check_weight(c, w));
   RTQ_TRY(check_t(t));
   bool on;
@@ -1125,7 +1140,12 @@ rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora
   RTQ_TRY(ensure_ws(c, bwd_ws_bytes(c, w, t, on ? r : 0)));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   return enqueue_backward(c, w, dy, t, dx, false, x, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, ga, gb,
-                          ar, st);
+                          ar, st, rb);
+}
+
+rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const float* x,
+                                 const float* dy, int64_t t, float* dx, float* ga, float* gb, void* stream) {
+  return linear_backward_d(c, w, lora, x, dy, t, dx, ga, gb, stream, nullptr);
 }
 
 static rtq_status enqueue_rows(rtq_ctx* c, const rtq_weight* w, int64_t r0, int64_t count, float* out,
@@ -1546,3 +1566,18 @@ rtq_status rtq_debug_block_isums(rtq_ctx* c, const rtq_weight* w, const float* x
 }
 
 }  // extern "C"
+
+// internal (rtq_internal.h): C++ linkage, not exported as part of the C ABI
+rtq_status rtq_linear_backward_blocks_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const RankBlocks* rb,
+                                        const float* x, const float* dy, int64_t t, float* dx, float* ga, float* gb,
+                                        void* stream) {
+  RTQ_TRY(check_weight(c, w));
+  if (rb && (rb->nm < 0 || rb->nm > 3)) return fail(RTQ_ERR_INVALID, "internal: %d adapter blocks", rb->nm);
+  if (rb && lora && lora->enabled && lora->rank > 0) {
+    for (int m = 0; m < rb->nm; m++)
+      if (rb->row0[m] < 0 || rb->nrow[m] < 0 || (int64_t)rb->row0[m] + rb->nrow[m] > w->rows || rb->col0[m] < 0 ||
+          rb->r[m] < 0 || (int64_t)rb->col0[m] + rb->r[m] > lora->rank)
+        return fail(RTQ_ERR_INVALID, "internal: adapter block %d outside the weight or rank", m);
+  }
+  return linear_backward_d(c, w, lora, x, dy, t, dx, ga, gb, stream, rb);
+}

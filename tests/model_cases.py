@@ -52,7 +52,7 @@ def oracle_model(g: G.GgufFile, lora=None, alpha=0.0, kv_f16=True):
                   q_norm=vec(p + "attn_q_norm.weight"), k_norm=vec(p + "attn_k_norm.weight"))
         for name, gname in GGUF_NAMES.items():
             ld[name] = W(p + gname + ".weight")
-            if lora is not None:
+            if lora is not None and (li, name) in lora:  # linears missing from lora are not adapted
                 A, B = lora[(li, name)]
                 ld[name].update(A=A, B=B, alpha=alpha)
         layers.append(ld)
