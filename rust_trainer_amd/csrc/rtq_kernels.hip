@@ -1885,30 +1885,34 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
     // gb: rows n (tile rt), cols j (tile ct);  ga: rows j (tile ct), cols k (tile rt)
     const int rrow = is_gb ? rt * 16 + li : ct * 16 + li;
     const int ccol = is_gb ? ct * 16 + li : rt * 16 + li;
-    // 64 tokens per pass: the loads of all four 16-token groups are issued before their MFMAs
+    // up to 64 tokens per pass: the loads of its 16-token groups (nv, wave-uniform; none past the
+    // wave's range) are issued before their MFMAs
     for (int t64 = tb; t64 < te; t64 += 64) {
+      const int nv = min(4, (te - t64 + 15) / 16);
       float av[4][4], bv[4][4];
 #pragma unroll
       for (int v = 0; v < 4; v++)
+        if (v < nv)
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const int tt = t64 + 16 * v + 4 * u + g, tc = min(tt, a.T - 1);
-          if (is_gb) {
-            const float x = a.dy[(int64_t)tc * a.N + min(rrow, a.N - 1)];
-            const float y = a.h[(int64_t)tc * a.r + min(ccol, a.r - 1)];
-            av[v][u] = (tt < te && rrow < a.N) ? __fmul_rn(x, a.s) : 0.0f;
-            bv[v][u] = (tt < te && ccol < a.r) ? y : 0.0f;
-          } else {
-            const float x = a.g[(int64_t)tc * a.r + min(rrow, a.r - 1)];
-            const float y = a.x[(int64_t)tc * a.K + min(ccol, a.K - 1)];
-            av[v][u] = (tt < te && rrow < a.r) ? x : 0.0f;
-            bv[v][u] = (tt < te && ccol < a.K) ? y : 0.0f;
+          for (int u = 0; u < 4; u++) {
+            const int tt = t64 + 16 * v + 4 * u + g, tc = min(tt, a.T - 1);
+            if (is_gb) {
+              const float x = a.dy[(int64_t)tc * a.N + min(rrow, a.N - 1)];
+              const float y = a.h[(int64_t)tc * a.r + min(ccol, a.r - 1)];
+              av[v][u] = (tt < te && rrow < a.N) ? __fmul_rn(x, a.s) : 0.0f;
+              bv[v][u] = (tt < te && ccol < a.r) ? y : 0.0f;
+            } else {
+              const float x = a.g[(int64_t)tc * a.r + min(rrow, a.r - 1)];
+              const float y = a.x[(int64_t)tc * a.K + min(ccol, a.K - 1)];
+              av[v][u] = (tt < te && rrow < a.r) ? x : 0.0f;
+              bv[v][u] = (tt < te && ccol < a.K) ? y : 0.0f;
+            }
           }
-        }
 #pragma unroll
       for (int v = 0; v < 4; v++)
+        if (v < nv)
 #pragma unroll
-        for (int u = 0; u < 4; u++) acc = mfma_f32(av[v][u], bv[v][u], acc);
+          for (int u = 0; u < 4; u++) acc = mfma_f32(av[v][u], bv[v][u], acc);
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) red[w * 256 + (4 * g + i) * 16 + li] = acc[i];
