@@ -22,6 +22,7 @@ enum RtqModelKernel {
   KM_ADD,
   KM_GEMM32,
   KM_LORA_MASK,
+  KM_GEMM32G,
   KM_COUNT
 };
 

@@ -290,6 +290,14 @@ struct MGemmArgs {
   int causal, accumulate;
 };
 
+// up to three independent products in one launch of the 32-row-tile kernel: flat workgroup ids
+// [start[i], start[i + 1]) belong to product i (column tiles fastest, then row tiles, then batch)
+struct MGemmGroupArgs {
+  MGemmArgs p[3];
+  int np;
+  int start[4];
+};
+
 // attention rows (h, i) of S / P / dP [nh x t x t]
 struct MSoftArgs {
   float* s;          // forward: scores in, probabilities out (0 for j > i)

@@ -197,6 +197,31 @@ rtq_status k_gemm(rtq_model* m, int64_t M, int64_t N, int64_t K, int64_t batch, 
                           stream_of(m), &ga);
 }
 
+// independent products C_i (+)= A_i B_i (M_i x N_i x K_i, batch_i) in one launch of 32-row tiles
+struct GemmJob {
+  int64_t M, N, K, batch;
+  Op A, B;
+  float* C;
+  int64_t sCb, sCm, sCn;
+  float a_scale;
+  int causal, acc;
+};
+rtq_status k_gemm_group(rtq_model* m, const GemmJob* jobs, int n) {
+  if (n < 1 || n > 3) return rtq_fail(RTQ_ERR_INVALID, "internal: %d grouped products", n);
+  MGemmGroupArgs g{};
+  g.np = n;
+  int64_t total = 0;
+  for (int i = 0; i < n; i++) {
+    const GemmJob& j = jobs[i];
+    g.p[i] = MGemmArgs{j.A.p, j.B.p, j.C, (int)j.M, (int)j.N, (int)j.K, j.A.sb, j.A.s0, j.A.s1, j.B.sb, j.B.s0,
+                       j.B.s1, j.sCb, j.sCm, j.sCn, j.A.div, j.B.div, j.a_scale, j.causal, j.acc};
+    g.start[i] = (int)total;
+    total += (j.N + 63) / 64 * ((j.M + 31) / 32) * j.batch;
+  }
+  for (int i = n; i < 4; i++) g.start[i] = (int)total;
+  return rtq_model_launch(m->ctx, KM_GEMM32G, dim3((unsigned)total), dim3(256), stream_of(m), &g);
+}
+
 rtq_lora lora_view(const Group& l) { return rtq_lora{l.rank, l.alpha, l.A, l.B, l.rank > 0 ? 1 : 0}; }
 
 rtq_status lin_fwd(rtq_model* m, const Group& l, const float* x, int64_t t, float* y) {
@@ -411,12 +436,12 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
                0));  // dP = dO V^T
   MSoftArgs sa{nullptr, k.P, m->dP, (int)t, (int)nh, scale};
   M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX_BWD, dim3((unsigned)t, (unsigned)nh), dim3(256), stream_of(m), &sa));
-  M_TRY(k_gemm(m, t, hd, t, nh, Op{k.P, t * t, 1, t, 1}, Op{m->d_o, hd, qd, 1, 1}, m->dvh, t * hd, hd, 1, 1.0f, 3,
-               0));  // dV_h = P^T dO
-  M_TRY(k_gemm(m, t, hd, t, nh, Op{m->dP, t * t, t, 1, 1}, Op{k.k, hd, kd, 1, (int)grp}, m->dq, hd, qd, 1, 1.0f, 2,
-               0));  // dQ = dS K
-  M_TRY(k_gemm(m, t, hd, t, nh, Op{m->dP, t * t, 1, t, 1}, Op{k.q, hd, qd, 1, 1}, m->dkh, t * hd, hd, 1, 1.0f, 3,
-               0));  // dK_h = dS^T Q
+  // dV_h = P^T dO, dQ = dS K, dK_h = dS^T Q: independent, one launch
+  const GemmJob jobs[3] = {
+      {t, hd, t, nh, Op{k.P, t * t, 1, t, 1}, Op{m->d_o, hd, qd, 1, 1}, m->dvh, t * hd, hd, 1, 1.0f, 3, 0},
+      {t, hd, t, nh, Op{m->dP, t * t, t, 1, 1}, Op{k.k, hd, kd, 1, (int)grp}, m->dq, hd, qd, 1, 1.0f, 2, 0},
+      {t, hd, t, nh, Op{m->dP, t * t, 1, t, 1}, Op{k.q, hd, qd, 1, 1}, m->dkh, t * hd, hd, 1, 1.0f, 3, 0}};
+  M_TRY(k_gemm_group(m, jobs, 3));
   const QkvView dv = qkv_view(m, L, m->dqkv, t);
   MGroupArgs gsa{m->dkh, m->dvh, m->dk, dv.v, (int)t, (int)nh, (int)nkv, (int)hd, dv.ldv};
   M_TRY(rtq_model_launch(m->ctx, KM_GROUP_SUM, dim3((unsigned)std::min<int64_t>((t * kd + 255) / 256, 4096)),

@@ -174,57 +174,101 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_qk_bwd(MQkArgs a) {
 }
 
 // ------------------------------------------------------------------ batched f32 GEMM
-// BM x 64 output tile per 256-thread workgroup on f32 MFMA (16x16x4: exact f32 products, f32
-// accumulation); wave w owns rows (w / 2) BM / 2 .. and columns (w % 2) 32 .. as (BM / 32) x 2
-// MFMA tiles.  k slabs (see MGemmSlab) go through LDS; the next slab's operands are loaded into
-// registers while the current one feeds the MFMAs.  Operands are read with their own strides, the
-// unit-stride index fastest across lanes.  BM = 32 doubles the grid of the thin products
-// (N = head_dim) so that each CU holds two workgroups.
+// C(b) (+)= A(b) B(b) on f32 MFMA (16x16x4: exact f32 products, f32 accumulation), a BM x 64 output
+// tile per 256-thread workgroup, k slabs of BK through LDS.  MFMA q of a 16-deep k group takes
+// k = 16 kb + 4 g + q in k slot g of A and of B alike.  An operand whose global unit-stride index is
+// k (mode 1) sits in LDS as [row][k] and a lane reads its 4 k with one 16-byte read; one whose
+// unit-stride index is the row (mode 2) sits as [k][row] and is read by 4 single reads.  Both are
+// loaded and stored as 16-byte vectors along the unit-stride index (when the other strides, the
+// extent and the base allow); otherwise single floats in the mode-1 arrangement (mode 0).  The next
+// slab is loaded into registers while the current one feeds the MFMAs.
+// Waves 2 x 2: BM = 64, 32 x 32 each (2 x 2 MFMA tiles); BM = 32, 16 x 32 (1 x 2).
 template <int BM>
-struct MGemmSlab {
-  // 32-row tiles serve the long-K products (O, dV, dQ, dK: K = t): 64-deep slabs, whose MFMAs
-  // outlast the next slab's load latency; 64-row tiles the K = head_dim ones: 32-deep slabs
-  static constexpr int BN = 64, BK = BM == 32 ? 64 : 32, NA = BM * BK / 256, NB = BN * BK / 256;
-  float a[NA], b[NB];
+struct MGemmCfg {
+  // 32-row tiles serve the long-K products (O, dV, dQ, dK: K = t): 64-deep slabs; 64-row tiles the
+  // K = head_dim ones: 32-deep slabs
+  static constexpr int BN = 64, BK = BM == 32 ? 64 : 32;
+  static constexpr int NA = BM * BK / 1024, NB = BN * BK / 1024;  // float4 per thread and slab
+  static constexpr int TM = BM / 32;                              // 16-row MFMA tiles per wave
 };
+// LDS floats of an R x BK operand in either layout: [R][BK + 4] or [BK][R + 4]
+template <int R, int BK>
+constexpr int m_opnd_lds() { return R * (BK + 4) > BK * (R + 4) ? R * (BK + 4) : BK * (R + 4); }
 
-template <int BM>
-__device__ __forceinline__ void m_gemm_load(const MGemmArgs& a, const float* A, const float* B, int m0, int n0, int kk,
-                                            int k1, MGemmSlab<BM>& r) {
-  using S = MGemmSlab<BM>;
-  const bool a_kfast = a.sAk == 1, b_nfast = a.sBn == 1;
+// load mode of an operand whose element (r, k) is P[r * sr + k * sk] (P already offset to its batch)
+__device__ __forceinline__ int m_opnd_mode(const float* P, int64_t sr, int64_t sk, int64_t sb, int nrows, int K) {
+  const bool al = (reinterpret_cast<uintptr_t>(P) & 15u) == 0 && sb % 4 == 0;
+  if (al && sk == 1 && sr % 4 == 0 && K % 4 == 0) return 1;
+  if (al && sr == 1 && sk % 4 == 0 && nrows % 4 == 0) return 2;
+  return 0;
+}
+
+// NV float4 of an R x BK operand tile: rows [r0, r0 + R), k in [kk, kk + BK); rows >= nrows and
+// k >= k1 read as zero (mode 1 / 2: a vector is inside or outside as a whole, k1 and nrows being
+// multiples of 4 there)
+template <int R, int BK, int NV>
+__device__ __forceinline__ void m_opnd_load(const float* P, int64_t sr, int64_t sk, int nrows, int r0, int kk, int k1,
+                                            int mode, float scale, f4 (&v)[NV]) {
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int i = 0; i < S::NA; i++) {
+  for (int i = 0; i < NV; i++) {
     const int e = threadIdx.x + 256 * i;
-    const int am = a_kfast ? e / S::BK : e % BM, ak = a_kfast ? e % S::BK : e / BM;
-    const int gm = m0 + am, gk = kk + ak;
-    float v = (gm < a.M && gk < k1) ? A[(int64_t)gm * a.sAm + (int64_t)gk * a.sAk] : 0.0f;
-    if (a.a_scale != 1.0f) v = v * a.a_scale;
-    r.a[i] = v;
-  }
+    if (mode == 2) {
+      const int gr = r0 + (e % (R / 4)) * 4, gk = kk + e / (R / 4);
+      v[i] = (gr < nrows && gk < k1) ? *reinterpret_cast<const f4*>(P + (int64_t)gk * sk + gr) : zero;
+    } else {
+      const int gr = r0 + e / (BK / 4), gk = kk + (e % (BK / 4)) * 4;
+      if (mode == 1) {
+        v[i] = (gr < nrows && gk < k1) ? *reinterpret_cast<const f4*>(P + (int64_t)gr * sr + gk) : zero;
+      } else {
 #pragma unroll
-  for (int i = 0; i < S::NB; i++) {
-    const int e = threadIdx.x + 256 * i;
-    const int bn = b_nfast ? e % S::BN : e / S::BK, bk = b_nfast ? e / S::BN : e % S::BK;
-    const int gn = n0 + bn, gk = kk + bk;
-    r.b[i] = (gn < a.N && gk < k1) ? B[(int64_t)gk * a.sBk + (int64_t)gn * a.sBn] : 0.0f;
+        for (int q = 0; q < 4; q++)
+          v[i][q] = (gr < nrows && gk + q < k1) ? P[(int64_t)gr * sr + (int64_t)(gk + q) * sk] : 0.0f;
+      }
+    }
+    if (scale != 1.0f)
+#pragma unroll
+      for (int q = 0; q < 4; q++) v[i][q] = v[i][q] * scale;
   }
 }
 
+template <int R, int BK, int NV>
+__device__ __forceinline__ void m_opnd_store(float* S, int mode, const f4 (&v)[NV]) {
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int e = threadIdx.x + 256 * i;
+    if (mode == 2)
+      *reinterpret_cast<f4*>(S + (e / (R / 4)) * (R + 4) + (e % (R / 4)) * 4) = v[i];
+    else
+      *reinterpret_cast<f4*>(S + (e / (BK / 4)) * (BK + 4) + (e % (BK / 4)) * 4) = v[i];
+  }
+}
+
+// k = 16 kb + 4 g + q (q = 0..3) of LDS row r (mode 1 / 0 layout) or column r (mode 2)
+template <int R, int BK>
+__device__ __forceinline__ f4 m_opnd_frag(const float* S, int mode, int r, int kb, int g) {
+  if (mode == 2) {
+    const float* p = S + (16 * kb + 4 * g) * (R + 4) + r;
+    return f4{p[0], p[R + 4], p[2 * (R + 4)], p[3 * (R + 4)]};
+  }
+  return *reinterpret_cast<const f4*>(S + r * (BK + 4) + 16 * kb + 4 * g);
+}
+
 template <int BM>
-__device__ __forceinline__ void m_gemm(const MGemmArgs& a) {
-  using S = MGemmSlab<BM>;
-  constexpr int BN = S::BN, BK = S::BK, TM = BM / 32;  // MFMA row tiles per wave
-  __shared__ float As[BK][BM + 4];
-  __shared__ float Bs[BK][BN + 4];
-  const int b = blockIdx.z, m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+__device__ __forceinline__ void m_gemm(const MGemmArgs& a, int bx, int by, int bz) {
+  using Cf = MGemmCfg<BM>;
+  constexpr int BN = Cf::BN, BK = Cf::BK, TM = Cf::TM;
+  __shared__ __attribute__((aligned(16))) float As[m_opnd_lds<BM, BK>()];
+  __shared__ __attribute__((aligned(16))) float Bs[m_opnd_lds<BN, BK>()];
+  const int b = bz, m0 = by * BM, n0 = bx * BN;
   if (a.causal == 1 && n0 > m0 + BM - 1) return;  // every element has n > m
   const float* A = a.A + (int64_t)(b / a.divA) * a.sAb;
   const float* B = a.B + (int64_t)(b / a.divB) * a.sBb;
   int k0 = 0, k1 = a.K;
   if (a.causal == 2) k1 = min(a.K, m0 + BM);
   if (a.causal == 3) k0 = (m0 / BK) * BK;
-  const bool a_kfast = a.sAk == 1, b_nfast = a.sBn == 1;
+  const int amode = m_opnd_mode(A, a.sAm, a.sAk, a.sAb, a.M, a.K);
+  const int bmode = m_opnd_mode(B, a.sBn, a.sBk, a.sBb, a.N, a.K);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
   const int wm = (w >> 1) * (BM / 2), wn = (w & 1) * 32;
   f4 acc[TM][2];
@@ -232,32 +276,32 @@ __device__ __forceinline__ void m_gemm(const MGemmArgs& a) {
   for (int i = 0; i < TM; i++)
 #pragma unroll
     for (int j = 0; j < 2; j++) acc[i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  S r;
-  if (k0 < k1) m_gemm_load<BM>(a, A, B, m0, n0, k0, k1, r);
+  f4 ra[Cf::NA], rb[Cf::NB];
+  if (k0 < k1) {
+    m_opnd_load<BM, BK>(A, a.sAm, a.sAk, a.M, m0, k0, k1, amode, a.a_scale, ra);
+    m_opnd_load<BN, BK>(B, a.sBn, a.sBk, a.N, n0, k0, k1, bmode, 1.0f, rb);
+  }
   for (int kk = k0; kk < k1; kk += BK) {
-#pragma unroll
-    for (int i = 0; i < S::NA; i++) {
-      const int e = threadIdx.x + 256 * i;
-      As[a_kfast ? e % BK : e / BM][a_kfast ? e / BK : e % BM] = r.a[i];
-    }
-#pragma unroll
-    for (int i = 0; i < S::NB; i++) {
-      const int e = threadIdx.x + 256 * i;
-      Bs[b_nfast ? e / BN : e % BK][b_nfast ? e % BN : e / BK] = r.b[i];
-    }
+    m_opnd_store<BM, BK>(As, amode, ra);
+    m_opnd_store<BN, BK>(Bs, bmode, rb);
     __syncthreads();
-    if (kk + BK < k1) m_gemm_load<BM>(a, A, B, m0, n0, kk + BK, k1, r);
+    if (kk + BK < k1) {
+      m_opnd_load<BM, BK>(A, a.sAm, a.sAk, a.M, m0, kk + BK, k1, amode, a.a_scale, ra);
+      m_opnd_load<BN, BK>(B, a.sBn, a.sBk, a.N, n0, kk + BK, k1, bmode, 1.0f, rb);
+    }
 #pragma unroll
-    for (int k4 = 0; k4 < BK; k4 += 4) {
-      float av[TM], bv[2];
+    for (int kb = 0; kb < BK / 16; kb++) {
+      f4 af[TM], bf[2];
 #pragma unroll
-      for (int i = 0; i < TM; i++) av[i] = As[k4 + g][wm + 16 * i + li];
+      for (int i = 0; i < TM; i++) af[i] = m_opnd_frag<BM, BK>(As, amode, wm + 16 * i + li, kb, g);
 #pragma unroll
-      for (int j = 0; j < 2; j++) bv[j] = Bs[k4 + g][wn + 16 * j + li];
+      for (int j = 0; j < 2; j++) bf[j] = m_opnd_frag<BN, BK>(Bs, bmode, wn + 16 * j + li, kb, g);
 #pragma unroll
-      for (int i = 0; i < TM; i++)
+      for (int q = 0; q < 4; q++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = mfma_f32(av[i], bv[j], acc[i][j]);
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int j = 0; j < 2; j++) acc[i][j] = mfma_f32(af[i][q], bf[j][q], acc[i][j]);
     }
     __syncthreads();
   }
@@ -278,8 +322,30 @@ __device__ __forceinline__ void m_gemm(const MGemmArgs& a) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm(MGemmArgs a) { m_gemm<64>(a); }
-extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32(MGemmArgs a) { m_gemm<32>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm(MGemmArgs a) {
+  m_gemm<64>(a, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32(MGemmArgs a) {
+  m_gemm<32>(a, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// grouped products (MGemmGroupArgs): one flat grid, so the products' workgroups share the CUs.  Row
+// tiles are ordered longest first (causal 2: the last rows reduce over the most k; causal 3: the
+// first rows)
+__device__ __forceinline__ void m_gemm32_member(const MGemmArgs& a, int l) {
+  const int nx = (a.N + 63) / 64, ny = (a.M + 31) / 32;
+  const int bx = l % nx, yy = (l / nx) % ny, bz = l / (nx * ny);
+  m_gemm<32>(a, bx, a.causal == 2 ? ny - 1 - yy : yy, bz);
+}
+extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32g(MGemmGroupArgs g) {
+  const int id = blockIdx.x;
+  if (id < g.start[1])
+    m_gemm32_member(g.p[0], id);
+  else if (g.np > 1 && id < g.start[2])
+    m_gemm32_member(g.p[1], id - g.start[1]);
+  else if (g.np > 2 && id < g.start[3])
+    m_gemm32_member(g.p[2], id - g.start[2]);
+}
 
 // ------------------------------------------------------------------ attention softmax
 // grid (t, nh): row i of head h over j <= i: p = exp(s - max) / sum (0 for j > i)

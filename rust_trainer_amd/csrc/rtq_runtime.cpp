@@ -161,7 +161,7 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_m_rmsnorm",        "rtq_m_rmsnorm_bwd",    "rtq_m_qk_prep",        "rtq_m_qk_bwd",
     "rtq_m_gemm",           "rtq_m_softmax",        "rtq_m_softmax_bwd",    "rtq_m_group_sum",
     "rtq_m_swiglu",         "rtq_m_swiglu_bwd",     "rtq_m_add",            "rtq_m_gemm32",
-    "rtq_m_lora_mask"};
+    "rtq_m_lora_mask",      "rtq_m_gemm32g"};
 
 struct TimedLaunch {
   int kid;
