@@ -288,6 +288,7 @@ struct MGemmArgs {
   int divA, divB;
   float a_scale;
   int causal, accumulate;
+  int batch;
 };
 
 // up to three independent products in one launch of the 32-row-tile kernel: flat workgroup ids

@@ -187,13 +187,13 @@ struct Op {  // one GEMM operand: base, batch stride and divisor, row / column s
 // C(b, m, n) (+)= sum_k A(b, m, k) B(b, k, n) for b < batch
 rtq_status k_gemm(rtq_model* m, int64_t M, int64_t N, int64_t K, int64_t batch, Op A, Op B, float* C, int64_t sCb,
                   int64_t sCm, int64_t sCn, float a_scale, int causal, int acc) {
-  MGemmArgs ga{A.p,   B.p,   C,     (int)M, (int)N, (int)K, A.sb,  A.s0,     A.s1, B.sb, B.s0,
-               B.s1,  sCb,   sCm,   sCn,    A.div,  B.div,  a_scale, causal, acc};
+  MGemmArgs ga{A.p, B.p, C, (int)M, (int)N, (int)K, A.sb, A.s0, A.s1, B.sb, B.s0, B.s1, sCb, sCm, sCn, A.div, B.div,
+               a_scale, causal, acc, (int)batch};
   // 64-row tiles when the grid fills the chip twice over, else 32-row tiles (twice the workgroups)
   const int64_t tiles64 = (N + 63) / 64 * ((M + 63) / 64) * batch / (causal == 1 ? 2 : 1);
   const int bm = tiles64 >= 2 * 256 ? 64 : 32;
-  return rtq_model_launch(m->ctx, bm == 64 ? KM_GEMM : KM_GEMM32,
-                          dim3((unsigned)((N + 63) / 64), (unsigned)((M + bm - 1) / bm), (unsigned)batch), dim3(256),
+  const int64_t tiles = (N + 63) / 64 * ((M + bm - 1) / bm) * batch;  // flat, XCD-aware (8 x ceil(tiles / 8))
+  return rtq_model_launch(m->ctx, bm == 64 ? KM_GEMM : KM_GEMM32, dim3((unsigned)((tiles + 7) / 8 * 8)), dim3(256),
                           stream_of(m), &ga);
 }
 
@@ -214,12 +214,12 @@ rtq_status k_gemm_group(rtq_model* m, const GemmJob* jobs, int n) {
   for (int i = 0; i < n; i++) {
     const GemmJob& j = jobs[i];
     g.p[i] = MGemmArgs{j.A.p, j.B.p, j.C, (int)j.M, (int)j.N, (int)j.K, j.A.sb, j.A.s0, j.A.s1, j.B.sb, j.B.s0,
-                       j.B.s1, j.sCb, j.sCm, j.sCn, j.A.div, j.B.div, j.a_scale, j.causal, j.acc};
+                       j.B.s1, j.sCb, j.sCm, j.sCn, j.A.div, j.B.div, j.a_scale, j.causal, j.acc, (int)j.batch};
     g.start[i] = (int)total;
     total += (j.N + 63) / 64 * ((j.M + 31) / 32) * j.batch;
   }
   for (int i = n; i < 4; i++) g.start[i] = (int)total;
-  return rtq_model_launch(m->ctx, KM_GEMM32G, dim3((unsigned)total), dim3(256), stream_of(m), &g);
+  return rtq_model_launch(m->ctx, KM_GEMM32G, dim3((unsigned)((total + 7) / 8 * 8)), dim3(256), stream_of(m), &g);
 }
 
 rtq_lora lora_view(const Group& l) { return rtq_lora{l.rank, l.alpha, l.A, l.B, l.rank > 0 ? 1 : 0}; }

@@ -322,23 +322,35 @@ __device__ __forceinline__ void m_gemm(const MGemmArgs& a, int bx, int by, int b
     }
 }
 
+// Flat grids of 8 * ceil(n / 8) workgroups, XCD-aware: workgroup id goes to XCD id % 8, so the
+// tile index l = (id % 8) * ceil(n / 8) + id / 8 gives each XCD a contiguous range of tiles (column
+// tiles fastest, then row tiles, then batch): the tiles of one head share an XCD and its L2.  Row
+// tiles run longest first (causal 2: the last rows reduce over the most k; causal 3: the first).
+__device__ __forceinline__ int m_xcd_tile(int n) {
+  const int per = (n + 7) / 8, id = blockIdx.x;
+  const int l = (id & 7) * per + (id >> 3);
+  return l < n ? l : -1;
+}
+template <int BM>
+__device__ __forceinline__ void m_gemm_tile(const MGemmArgs& a, int l) {
+  const int nx = (a.N + 63) / 64, ny = (a.M + BM - 1) / BM;
+  const int bx = l % nx, yy = (l / nx) % ny, bz = l / (nx * ny);
+  m_gemm<BM>(a, bx, a.causal == 2 ? ny - 1 - yy : yy, bz);
+}
 extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm(MGemmArgs a) {
-  m_gemm<64>(a, blockIdx.x, blockIdx.y, blockIdx.z);
+  const int l = m_xcd_tile((a.N + 63) / 64 * ((a.M + 63) / 64) * a.batch);
+  if (l >= 0) m_gemm_tile<64>(a, l);
 }
 extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32(MGemmArgs a) {
-  m_gemm<32>(a, blockIdx.x, blockIdx.y, blockIdx.z);
+  const int l = m_xcd_tile((a.N + 63) / 64 * ((a.M + 31) / 32) * a.batch);
+  if (l >= 0) m_gemm_tile<32>(a, l);
 }
 
-// grouped products (MGemmGroupArgs): one flat grid, so the products' workgroups share the CUs.  Row
-// tiles are ordered longest first (causal 2: the last rows reduce over the most k; causal 3: the
-// first rows)
-__device__ __forceinline__ void m_gemm32_member(const MGemmArgs& a, int l) {
-  const int nx = (a.N + 63) / 64, ny = (a.M + 31) / 32;
-  const int bx = l % nx, yy = (l / nx) % ny, bz = l / (nx * ny);
-  m_gemm<32>(a, bx, a.causal == 2 ? ny - 1 - yy : yy, bz);
-}
+// grouped products (MGemmGroupArgs) in one flat grid, so the products' workgroups share the CUs
+__device__ __forceinline__ void m_gemm32_member(const MGemmArgs& a, int l) { m_gemm_tile<32>(a, l); }
 extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32g(MGemmGroupArgs g) {
-  const int id = blockIdx.x;
+  const int id = m_xcd_tile(g.start[g.np]);
+  if (id < 0) return;
   if (id < g.start[1])
     m_gemm32_member(g.p[0], id);
   else if (g.np > 1 && id < g.start[2])
