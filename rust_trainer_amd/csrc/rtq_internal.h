@@ -31,10 +31,18 @@ rtq_status rtq_fail(rtq_status st, const char* fmt, ...);
 // launches decoder kernel km with one by-value argument struct at args (timed like every launch)
 rtq_status rtq_model_launch(rtq_ctx* c, int km, dim3 grid, dim3 block, hipStream_t s, const void* args);
 int rtq_ctx_device_id(const rtq_ctx* c);
-// rtq_linear_backward_d for a block-diagonal adapter over row-concatenated weights: gb and
-// g = s dy.B only inside rb's blocks (gb outside them is left untouched).  Quantised weights only;
-// a dense weight computes every pair (the caller clears gb outside the blocks).
+// floats of the LoRA-down partials a forward of t tokens at rank r can keep for the backward of the
+// same x (0: not kept for this weight - dense, or slicings that differ)
+int64_t rtq_lora_partial_floats(const rtq_weight* w, int64_t t, int64_t r);
+// rtq_linear_forward_d that also leaves the LoRA-down partials in hp_keep (null or too small a
+// weight: as rtq_linear_forward_d)
+rtq_status rtq_linear_forward_keep_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
+                                     const float* x, int64_t t, float* y, float* hp_keep, void* stream);
+// rtq_linear_backward_d for a block-diagonal adapter over row-concatenated weights (rb; null: a
+// plain adapter): gb and g = s dy.B only inside rb's blocks (gb outside them is left untouched).
+// Quantised weights only; a dense weight computes every pair (the caller clears gb outside the
+// blocks).  hp_have: the partials a rtq_linear_forward_keep_d of the same x left (or null).
 rtq_status rtq_linear_backward_blocks_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const RankBlocks* rb,
                                         const float* x, const float* dy, int64_t t, float* dx, float* ga, float* gb,
-                                        void* stream);
+                                        const float* hp_have, void* stream);
 #endif

@@ -138,6 +138,7 @@ struct BwdPrepArgs {
   float* gp;     // [T][r][ngq] partials of dy . B
   int ngq;
   RankBlocks rb;  // g = dy . B restricted to each member's rows
+  int y0;         // grid row offset: nhq when the h partials are already there (only g is computed)
 };
 
 // part[z][t][k] = sum over rows n of split z of dy[t][n] W[n][k], three bf16 MFMAs per product (hi/lo split of dy

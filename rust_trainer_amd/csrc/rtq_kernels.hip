@@ -1343,13 +1343,12 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_prep(BwdPrepArgs a) {
   __shared__ float sx[16 * LDX];
   __shared__ float sm[256 * LDB];
   __shared__ float red[4 * 256];
-  const int t0 = blockIdx.x * 16;
-  if ((int)blockIdx.y < a.nhq)
-    lora_partial<false>(a.x, a.T, a.K, a.A, a.K, a.r, a.r, blockIdx.y * KQ, a.K, t0, a.hp, a.nhq, blockIdx.y, sx, sm,
-                        red);
+  const int t0 = blockIdx.x * 16, y = (int)blockIdx.y + a.y0;
+  if (y < a.nhq)
+    lora_partial<false>(a.x, a.T, a.K, a.A, a.K, a.r, a.r, y * KQ, a.K, t0, a.hp, a.nhq, y, sx, sm, red);
   else
-    lora_partial<true>(a.dy, a.T, a.N, a.B, a.r, a.N, a.r, (blockIdx.y - a.nhq) * KQ, a.N, t0, a.gp, a.ngq,
-                       blockIdx.y - a.nhq, sx, sm, red, &a.rb);
+    lora_partial<true>(a.dy, a.T, a.N, a.B, a.r, a.N, a.r, (y - a.nhq) * KQ, a.N, t0, a.gp, a.ngq, y - a.nhq, sx, sm,
+                       red, &a.rb);
 }
 
 // ============================================================== dx = dy . W

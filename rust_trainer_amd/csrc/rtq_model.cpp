@@ -57,6 +57,7 @@ struct Group {
   int64_t rank = 0;  // fused adapter rank (sum of the members' r); 0: no adapter
   float alpha = 0.0f;
   float *A = nullptr, *B = nullptr, *ga = nullptr, *gb = nullptr;  // [rank x in], [rows x rank]
+  float* hpk = nullptr;  // the forward's LoRA-down partials of this step, reused by the backward (or null)
 };
 
 struct Layer {
@@ -101,6 +102,8 @@ struct rtq_model {
   // step buffers, sized for t_cap tokens and n_cap targets
   int64_t t_cap = 0, n_cap = 0;
   void* step_mem = nullptr;
+  void* hpk_mem = nullptr;  // every group's kept LoRA-down partials
+  size_t hpk_cap = 0;
   float *X = nullptr, *cos_ = nullptr, *sin_ = nullptr;
   std::vector<Cache> cache;
   float *dY, *dX, *mo, *f, *dhm, *dgu, *dn2, *dxu, *dh, *d_o, *dP, *dq, *dkh, *dvh, *dk, *dqkv, *dn1, *dxk, *dxv;
@@ -226,7 +229,7 @@ rtq_lora lora_view(const Group& l) { return rtq_lora{l.rank, l.alpha, l.A, l.B, 
 
 rtq_status lin_fwd(rtq_model* m, const Group& l, const float* x, int64_t t, float* y) {
   const rtq_lora lv = lora_view(l);
-  return rtq_linear_forward_d(m->ctx, l.w, l.bias, l.rank > 0 ? &lv : nullptr, x, t, y, stream_of(m));
+  return rtq_linear_forward_keep_d(m->ctx, l.w, l.bias, l.rank > 0 ? &lv : nullptr, x, t, y, l.hpk, stream_of(m));
 }
 
 // a fused group's adapter is block-diagonal (each member's rows see only its own ranks): the
@@ -236,9 +239,11 @@ rtq_status lin_bwd(rtq_model* m, const Group& l, const float* x, const float* dy
   const rtq_lora lv = lora_view(l);
   const int wt = rtq_weight_type(l.w);
   const bool dense = wt == RTQ_TYPE_F32 || wt == RTQ_TYPE_TQ8_0;
-  if (l.rank == 0 || l.nm < 2 || dense)
+  if (l.rank == 0 || dense)
     M_TRY(rtq_linear_backward_d(m->ctx, l.w, l.rank > 0 ? &lv : nullptr, x, dy, t, dx, l.ga, l.gb, stream_of(m)));
-  if (l.rank == 0 || l.nm < 2) return RTQ_OK;
+  if (l.rank == 0 || (dense && l.nm < 2)) return RTQ_OK;
+  if (!dense && l.nm < 2)
+    return rtq_linear_backward_blocks_d(m->ctx, l.w, &lv, nullptr, x, dy, t, dx, l.ga, l.gb, l.hpk, stream_of(m));
   if (!dense) {
     RankBlocks rb{};
     rb.nm = l.nm;
@@ -248,7 +253,7 @@ rtq_status lin_bwd(rtq_model* m, const Group& l, const float* x, const float* dy
       rb.col0[i] = (int)l.mem[i].col0;
       rb.r[i] = (int)l.mem[i].r;
     }
-    return rtq_linear_backward_blocks_d(m->ctx, l.w, &lv, &rb, x, dy, t, dx, l.ga, l.gb, stream_of(m));
+    return rtq_linear_backward_blocks_d(m->ctx, l.w, &lv, &rb, x, dy, t, dx, l.ga, l.gb, l.hpk, stream_of(m));
   }
   MMaskArgs ma{l.gb, l.rows, l.rank, l.nm, {}, {}, {}, {}};
   for (int i = 0; i < l.nm; i++) {
@@ -262,6 +267,32 @@ rtq_status lin_bwd(rtq_model* m, const Group& l, const float* x, const float* dy
 }
 
 // ---------------------------------------------------------------- step buffers
+// one buffer for every adapted group's kept LoRA-down partials at t tokens (rank and t may change
+// between steps: sized and assigned per step)
+rtq_status ensure_hpk(rtq_model* m, int64_t t) {
+  size_t need = 0;
+  for (auto& L : m->layers)
+    for (auto& G : L.groups) need += ((size_t)rtq_lora_partial_floats(G.w, t, G.rank) * 4 + 255) / 256 * 256;
+  if (need > m->hpk_cap) {
+    if (m->hpk_mem) {
+      M_HIP(hipStreamSynchronize(stream_of(m)));
+      M_HIP(hipFree(m->hpk_mem));
+      m->hpk_mem = nullptr;
+      m->hpk_cap = 0;
+    }
+    M_HIP(hipMalloc(&m->hpk_mem, need));
+    m->hpk_cap = need;
+  }
+  char* p = (char*)m->hpk_mem;
+  for (auto& L : m->layers)
+    for (auto& G : L.groups) {
+      const size_t f = (size_t)rtq_lora_partial_floats(G.w, t, G.rank);
+      G.hpk = f ? (float*)p : nullptr;
+      p += (f * 4 + 255) / 256 * 256;
+    }
+  return RTQ_OK;
+}
+
 rtq_status ensure_step(rtq_model* m, int64_t t, int64_t n) {
   if (t <= m->t_cap && n <= m->n_cap) return RTQ_OK;
   const rtq_model_config& c = m->cfg;
@@ -623,6 +654,7 @@ void rtq_model_destroy(rtq_model* m) {
   for (rtq_weight* w : m->weights) rtq_weight_destroy(w);
   for (void* p : m->owned) (void)hipFree(p);
   if (m->step_mem) (void)hipFree(m->step_mem);
+  if (m->hpk_mem) (void)hipFree(m->hpk_mem);
   delete m;
 }
 
@@ -799,6 +831,7 @@ rtq_status rtq_model_forward_backward(rtq_model* m, const int32_t* tokens, int64
       return rtq_fail(RTQ_ERR_INVALID, "target %lld out of range", (long long)i);  // src/model.rs:575
   M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
   M_TRY(ensure_step(m, t, n));
+  M_TRY(ensure_hpk(m, t));
   M_TRY(ensure_rope(m, t));
   hipStream_t st = stream_of(m);
   const int64_t d = c.n_embd;

@@ -468,9 +468,11 @@ rtq_status enqueue_backward_dense(rtq_ctx* c, const rtq_weight* w, const float* 
 
 // ------------------------------------------------------------------ enqueue: forward
 // y = x.W^T (+bias) (+ s h.B^T);  isums (debug) receives the per-block integer sums.
+// hp_keep (optional, nhp * t * r floats): the LoRA-down partials go there instead of the workspace,
+// for a later enqueue_backward of the same x to reuse
 rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int64_t t, float* y, const float* bias,
                            const float* la, const float* lb, int64_t r, float s, int32_t* isums, Arena& ar,
-                           hipStream_t st) {
+                           hipStream_t st, float* hp_keep = nullptr) {
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
   if (is_dense(w->type)) return enqueue_forward_dense(c, w, x, t, y, bias, la, lb, lora ? r : 0, s, ar, st);
@@ -481,7 +483,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   void* xq = ar.take<char>(p.xq_bytes);
   float* xd = ar.take<float>(p.xd_floats);
   float* xg = p.gemv ? ar.take<float>(p.xg_floats) : nullptr;
-  float* hp = lora ? ar.take<float>(p.h_floats) : nullptr;
+  float* hp = lora ? (hp_keep ? hp_keep : ar.take<float>(p.h_floats)) : nullptr;
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   if (p.gemv) {
     const GemvPlan gp = gemv_plan(c, w);
@@ -649,7 +651,8 @@ int64_t lora_slices(int64_t n) { return roundup(cdiv(std::max<int64_t>(n, 1), RT
 // partials of dx; its last grid row sums the h, g partials) -> rtq_bwd_finish.
 rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, int64_t t, float* dx, bool accumulate,
                             const float* x, const float* la, const float* lb, int64_t r, float s, float* ga,
-                            float* gb, Arena& ar, hipStream_t st, const RankBlocks* rb = nullptr) {
+                            float* gb, Arena& ar, hipStream_t st, const RankBlocks* rb = nullptr,
+                            const float* hp_have = nullptr) {
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
   if (is_dense(w->type))
@@ -661,14 +664,17 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   const int64_t nhq = lora_slices(K), ngq = lora_slices(N);
   float* h = lora ? ar.take<float>((size_t)(t * r)) : nullptr;
   float* g = lora ? ar.take<float>((size_t)(t * r)) : nullptr;
-  float* hp = lora ? ar.take<float>((size_t)(nhq * t * r)) : nullptr;
+  // hp_have: the forward's LoRA-down partials of this x (same slices), so only g is computed here
+  const bool have_h = lora && hp_have != nullptr;
+  float* hp = lora ? (have_h ? const_cast<float*>(hp_have) : ar.take<float>((size_t)(nhq * t * r))) : nullptr;
   float* gp = lora ? ar.take<float>((size_t)(ngq * t * r)) : nullptr;
   float* part = ar.take<float>(dp.part_floats);
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   if (lora) {
-    BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq, RankBlocks{}};
+    BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq, RankBlocks{}, have_h ? (int)nhq : 0};
     if (rb) pa.rb = *rb;
-    RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, 16), (unsigned)(nhq + ngq)), dim3(256), st, pa));
+    RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, 16), (unsigned)(have_h ? ngq : nhq + ngq)), dim3(256), st,
+                   pa));
   }
   DxArgs xa{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, (int)dp.splits, part,
             lora ? hp : nullptr, lora ? gp : nullptr, (int)nhq, (int)ngq, (int)r, s, h, g};
@@ -1125,7 +1131,7 @@ rtq_status rtq_frozen_backward_input_d(rtq_ctx* c, const rtq_weight* w, const fl
 
 static rtq_status linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const float* x,
                                     const float* dy, int64_t t, float* dx, float* ga, float* gb, void* stream,
-                                    const RankBlocks* rb) {
+                                    const RankBlocks* rb, const float* hp_have = nullptr) {
   RTQ_TRY(check_weight(c, w));
   RTQ_TRY(check_t(t));
   bool on;
@@ -1140,7 +1146,7 @@ static rtq_status linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_l
   RTQ_TRY(ensure_ws(c, bwd_ws_bytes(c, w, t, on ? r : 0)));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   return enqueue_backward(c, w, dy, t, dx, false, x, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, ga, gb,
-                          ar, st, rb);
+                          ar, st, rb, hp_have);
 }
 
 rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const float* x,
@@ -1568,9 +1574,35 @@ rtq_status rtq_debug_block_isums(rtq_ctx* c, const rtq_weight* w, const float* x
 }  // extern "C"
 
 // internal (rtq_internal.h): C++ linkage, not exported as part of the C ABI
+int64_t rtq_lora_partial_floats(const rtq_weight* w, int64_t t, int64_t r) {
+  if (!w || is_dense(w->type) || t <= 0 || r <= 0) return 0;
+  const int64_t nhp = roundup(cdiv(w->Kp, RTQ_ACT_KQ), 4);
+  return nhp == lora_slices(w->cols) ? nhp * t * r : 0;  // the forward's and the backward's slicing agree
+}
+
+rtq_status rtq_linear_forward_keep_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
+                                     const float* x, int64_t t, float* y, float* hp_keep, void* stream) {
+  RTQ_TRY(check_weight(c, w));
+  RTQ_TRY(check_t(t));
+  bool on;
+  int64_t r;
+  float s;
+  RTQ_TRY(check_lora(lora, &on, &r, &s));
+  if (t > 0 && (!x || !y)) return fail(RTQ_ERR_INVALID, "null x/y");
+  if (hp_keep && rtq_lora_partial_floats(w, t, on ? r : 0) == 0) hp_keep = nullptr;
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = (hipStream_t)stream;
+  FwdPlan p = fwd_plan(w, t, on ? r : 0);
+  RTQ_TRY(ensure_ws(c, fwd_ws_bytes(p)));
+  Arena ar{(char*)c->ws, c->ws_bytes, 0};
+  return enqueue_forward(c, w, x, t, y, bias, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, nullptr, ar, st,
+                         hp_keep);
+}
+
 rtq_status rtq_linear_backward_blocks_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const RankBlocks* rb,
                                         const float* x, const float* dy, int64_t t, float* dx, float* ga, float* gb,
-                                        void* stream) {
+                                        const float* hp_have, void* stream) {
   RTQ_TRY(check_weight(c, w));
   if (rb && (rb->nm < 0 || rb->nm > 3)) return fail(RTQ_ERR_INVALID, "internal: %d adapter blocks", rb->nm);
   if (rb && lora && lora->enabled && lora->rank > 0) {
@@ -1579,5 +1611,6 @@ rtq_status rtq_linear_backward_blocks_d(rtq_ctx* c, const rtq_weight* w, const r
           rb->r[m] < 0 || (int64_t)rb->col0[m] + rb->r[m] > lora->rank)
         return fail(RTQ_ERR_INVALID, "internal: adapter block %d outside the weight or rank", m);
   }
-  return linear_backward_d(c, w, lora, x, dy, t, dx, ga, gb, stream, rb);
+  if (hp_have && rtq_lora_partial_floats(w, t, lora && lora->enabled ? lora->rank : 0) == 0) hp_have = nullptr;
+  return linear_backward_d(c, w, lora, x, dy, t, dx, ga, gb, stream, rb, hp_have);
 }
