@@ -102,6 +102,8 @@ struct rtq_model {
   // step buffers, sized for t_cap tokens and n_cap targets
   int64_t t_cap = 0, n_cap = 0;
   void* step_mem = nullptr;
+  void* grads = nullptr;  // every adapter's dA and dB (attach_lora), grad_bytes long
+  size_t grad_bytes = 0;
   void* hpk_mem = nullptr;  // every group's kept LoRA-down partials
   size_t hpk_cap = 0;
   float *X = nullptr, *cos_ = nullptr, *sin_ = nullptr;
@@ -671,9 +673,10 @@ rtq_status rtq_model_attach_lora(rtq_model* m, int64_t rank, float alpha, uint32
   M_HIP(hipStreamSynchronize(stream_of(m)));
   Rng rng(seed);
   int64_t n = 0;
-  for (Layer& L : m->layers) {
-    // block layout of each group's adapter: members in linear order, r columns each if targeted
-    std::vector<std::vector<float>> ahost(L.groups.size());
+  // block layout of each group's adapter: members in linear order, r columns each if targeted;
+  // every adapter's dA and dB in one allocation, so zero_grad is one fill
+  size_t gbytes = 0;
+  for (Layer& L : m->layers)
     for (Group& G : L.groups) {
       G.rank = 0;
       for (int j = 0; j < G.nm; j++) {
@@ -682,7 +685,16 @@ rtq_status rtq_model_attach_lora(rtq_model* m, int64_t rank, float alpha, uint32
         mb.r = (target_mask >> mb.lin & 1u) ? rank : 0;
         G.rank += mb.r;
       }
+      gbytes += ((size_t)(G.rank * G.in) * 4 + 255) / 256 * 256 + ((size_t)(G.rows * G.rank) * 4 + 255) / 256 * 256;
     }
+  void* gmem = nullptr;
+  M_TRY(dev_alloc(m, gbytes, &gmem));
+  M_HIP(hipMemset(gmem, 0, gbytes));
+  m->grads = gmem;
+  m->grad_bytes = gbytes;
+  char* gp = (char*)gmem;
+  for (Layer& L : m->layers) {
+    std::vector<std::vector<float>> ahost(L.groups.size());
     for (int i = 0; i < NLIN; i++) {  // A drawn linear by linear, in the reference's order
       if (!(target_mask >> i & 1u)) continue;
       Group& G = L.groups[(size_t)L.gi[i]];
@@ -697,15 +709,15 @@ rtq_status rtq_model_attach_lora(rtq_model* m, int64_t rank, float alpha, uint32
       Group& G = L.groups[gi];
       if (G.rank == 0) continue;
       const size_t na = (size_t)(G.rank * G.in) * 4, nb = (size_t)(G.rows * G.rank) * 4;
-      void *A, *B, *ga, *gb;
+      void *A, *B;
       M_TRY(dev_alloc(m, na, &A));
       M_TRY(dev_alloc(m, nb, &B));
-      M_TRY(dev_alloc(m, na, &ga));
-      M_TRY(dev_alloc(m, nb, &gb));
+      void* ga = gp;
+      gp += (na + 255) / 256 * 256;
+      void* gb = gp;
+      gp += (nb + 255) / 256 * 256;
       M_HIP(hipMemcpy(A, ahost[gi].data(), na, hipMemcpyHostToDevice));
       M_HIP(hipMemset(B, 0, nb));
-      M_HIP(hipMemset(ga, 0, na));
-      M_HIP(hipMemset(gb, 0, nb));
       int members = 0;
       for (int j = 0; j < G.nm; j++) members += G.mem[j].r > 0;
       G.alpha = alpha * (float)members;  // alpha / rank unchanged
@@ -806,12 +818,7 @@ rtq_status rtq_model_lora_set(rtq_model* m, int64_t i, const float* a, const flo
 rtq_status rtq_model_zero_grad(rtq_model* m) {
   if (!m) return rtq_fail(RTQ_ERR_INVALID, "null model");
   M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
-  for (Layer& L : m->layers)
-    for (Group& G : L.groups)
-      if (G.rank > 0) {
-        M_HIP(hipMemsetAsync(G.ga, 0, (size_t)(G.rank * G.in) * 4, stream_of(m)));
-        M_HIP(hipMemsetAsync(G.gb, 0, (size_t)(G.rows * G.rank) * 4, stream_of(m)));
-      }
+  if (m->grads) M_HIP(hipMemsetAsync(m->grads, 0, m->grad_bytes, stream_of(m)));  // every adapter's dA, dB
   M_HIP(hipStreamSynchronize(stream_of(m)));
   return RTQ_OK;
 }
