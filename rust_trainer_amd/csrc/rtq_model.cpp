@@ -423,7 +423,8 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* 
   // S = (q scale) K^T per head (causal), softmax in place, O = P V
   M_TRY(k_gemm(m, t, t, hd, nh, Op{k.q, hd, qd, 1, 1}, Op{k.k, hd, 1, kd, (int)grp}, k.P, t * t, t, 1, scale, 1, 0));
   MSoftArgs sa{k.P, nullptr, nullptr, (int)t, (int)nh, scale};
-  M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX, dim3((unsigned)t, (unsigned)nh), dim3(256), stream_of(m), &sa));
+  M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX, dim3((unsigned)((t + 3) / 4), (unsigned)nh), dim3(256), stream_of(m),
+                         &sa));
   M_TRY(k_gemm(m, t, hd, t, nh, Op{k.P, t * t, t, 1, 1}, Op{k.v, hd, kd, 1, (int)grp}, k.o, hd, qd, 1, 1.0f, 2, 0));
   M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LO]], k.o, t, m->mo));
   M_TRY(k_norm(m, x, m->mo, k.h, L.ffn_norm, k.n2, k.inv2, t, d, 0));  // h = x + attn, n2 = rmsnorm(h)
@@ -468,7 +469,8 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
   M_TRY(k_gemm(m, t, t, hd, nh, Op{m->d_o, hd, qd, 1, 1}, Op{k.v, hd, 1, kd, (int)grp}, m->dP, t * t, t, 1, 1.0f, 1,
                0));  // dP = dO V^T
   MSoftArgs sa{nullptr, k.P, m->dP, (int)t, (int)nh, scale};
-  M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX_BWD, dim3((unsigned)t, (unsigned)nh), dim3(256), stream_of(m), &sa));
+  M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX_BWD, dim3((unsigned)((t + 3) / 4), (unsigned)nh), dim3(256),
+                         stream_of(m), &sa));
   // dV_h = P^T dO, dQ = dS K, dK_h = dS^T Q: independent, one launch
   const GemmJob jobs[3] = {
       {t, hd, t, nh, Op{k.P, t * t, 1, t, 1}, Op{m->d_o, hd, qd, 1, 1}, m->dvh, t * hd, hd, 1, 1.0f, 3, 0},

@@ -360,31 +360,33 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32g(MGemmGroupArgs g
 }
 
 // ------------------------------------------------------------------ attention softmax
-// grid (t, nh): row i of head h over j <= i: p = exp(s - max) / sum (0 for j > i)
+// grid (ceil(t / 4), nh), 256 threads: one wave per row i of head h (wave reductions, no barriers),
+// over j <= i: p = exp(s - max) / sum (0 for j > i)
 extern "C" __global__ __launch_bounds__(256) void rtq_m_softmax(MSoftArgs a) {
-  __shared__ float red[4];
-  const int i = blockIdx.x, h = blockIdx.y;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6), h = blockIdx.y, lane = threadIdx.x & 63;
+  if (i >= a.t) return;  // whole wave
   float* row = a.s + ((int64_t)h * a.t + i) * a.t;
   float m = -__builtin_inff();
-  for (int j = threadIdx.x; j <= i; j += 256) m = fmaxf(m, row[j]);
-  m = block_max256(m, red);
+  for (int j = lane; j <= i; j += 64) m = fmaxf(m, row[j]);
+  m = wave_max(m);
   float s = 0.0f;
-  for (int j = threadIdx.x; j <= i; j += 256) s = s + expf(row[j] - m);
-  s = block_sum256(s, red);
+  for (int j = lane; j <= i; j += 64) s = s + expf(row[j] - m);
+  s = wave_sum(s);
   const float inv = __fdiv_rn(1.0f, s);
-  for (int j = threadIdx.x; j < a.t; j += 256) row[j] = j <= i ? expf(row[j] - m) * inv : 0.0f;
+  for (int j = lane; j < a.t; j += 64) row[j] = j <= i ? expf(row[j] - m) * inv : 0.0f;
 }
 
-// grid (t, nh): dS = (P (dP - sum_j P dP)) scale over j <= i, 0 beyond, written over dP
+// grid (ceil(t / 4), nh), one wave per row: dS = (P (dP - sum_j P dP)) scale over j <= i, 0 beyond,
+// written over dP
 extern "C" __global__ __launch_bounds__(256) void rtq_m_softmax_bwd(MSoftArgs a) {
-  __shared__ float red[4];
-  const int i = blockIdx.x, h = blockIdx.y;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6), h = blockIdx.y, lane = threadIdx.x & 63;
+  if (i >= a.t) return;
   const float* p = a.p + ((int64_t)h * a.t + i) * a.t;
   float* dp = a.dp + ((int64_t)h * a.t + i) * a.t;
   float s = 0.0f;
-  for (int j = threadIdx.x; j <= i; j += 256) s = s + p[j] * dp[j];
-  s = block_sum256(s, red);
-  for (int j = threadIdx.x; j < a.t; j += 256) dp[j] = j <= i ? (p[j] * (dp[j] - s)) * a.scale : 0.0f;
+  for (int j = lane; j <= i; j += 64) s = s + p[j] * dp[j];
+  s = wave_sum(s);
+  for (int j = lane; j < a.t; j += 64) dp[j] = j <= i ? (p[j] * (dp[j] - s)) * a.scale : 0.0f;
 }
 
 // dk / dv [t x nkv x hd] = sum over the group's heads (head order) of dkh / dvh [nh x t x hd]
