@@ -1466,9 +1466,10 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
 #pragma unroll
     for (int j = 0; j < KS; j++) acc[i][j] = zero;
 
-  // dy loader: tokens tl + 64 m (m < NQ) with tl = tid >> 3, float4 q4 = tid & 7 (columns
-  // ns + 4 q4 .. +3 of the step)
-  const int tl = tid >> 3, q4 = tid & 7;
+  // dy loader: tokens tl + 64 m (m < NQ), float4 q4 (columns ns + 4 q4 .. +3 of the step); wave w
+  // covers tokens 16 (w % 4) .. +15 and float4 columns 4 (w / 4) .. +3, so its 64 lanes write the
+  // bf16 halves of 32 consecutive A-fragment lanes (512 contiguous bytes: no LDS bank conflicts)
+  const int tl = 16 * ((tid >> 6) & 3) + (tid & 15), q4 = 4 * (tid >> 8) + ((tid >> 4) & 3);
   const __amdgpu_buffer_rsrc_t rdy = make_rsrc(a.dy, (uint32_t)a.T * a.N * 4u);
   const uint32_t dy_off = ((uint32_t)(t0 + tl) * a.N + 4 * q4) * 4u;
   const bool dy_vec = (a.N & 3) == 0;
