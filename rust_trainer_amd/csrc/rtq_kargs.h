@@ -139,6 +139,7 @@ struct BwdPrepArgs {
   int ngq;
   RankBlocks rb;  // g = dy . B restricted to each member's rows
   int y0;         // grid row offset: nhq when the h partials are already there (only g is computed)
+  int gtok;       // tokens per g-partial workgroup: 64 (a wave per 16 tokens) or 16 (a wave per 64 rows)
 };
 
 // part[z][t][k] = sum over rows n of split z of dy[t][n] W[n][k], three bf16 MFMAs per product (hi/lo split of dy

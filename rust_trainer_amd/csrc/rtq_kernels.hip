@@ -244,18 +244,15 @@ __device__ __forceinline__ bool rb_any(const RankBlocks& b, int n0, int n1, int 
   return false;
 }
 
-// One LoRA partial product over a 256-column slice, by one 256-thread workgroup (f32 MFMA):
-//   P[t][j] = sum over k in [k0, k0 + 256) of S[t][k] * M(j, k),  t in [t0, t0 + 16), j in [0, r)
-// with M(j, k) = M[j * ldm + k] (A rows: LoRA down, src/linear.rs:85) when !MT, or
-// M[k * ldm + j] (B columns: g = dy . B, src/linear.rs:111) when MT; S rows have length ks.
-// Written to out[(t * r + j) * pstride + pidx] (slice index fastest, so a consumer sums a token's
-// partials in slice order with a few wide loads).  Columns beyond kend count as zero.  With MT, B
-// entries outside rb's blocks count as zero, and rank tiles with none inside are written as zeros.
-template <bool MT>
-__device__ __forceinline__ void lora_partial(const float* S, int T, int ks, const float* M, int ldm, int mrows, int r,
-                                             int k0, int kend, int t0, float* out, int pstride, int pidx, float* sx,
-                                             float* sm, float* red, const RankBlocks* rb = nullptr) {
-  constexpr int LDX = RTQ_ACT_KQ + 1, LDB = 17;
+// LoRA-down partial product over a 256-column slice, by one 256-thread workgroup (f32 MFMA):
+//   P[t][j] = sum over k in [k0, k0 + 256) of S[t][k] * M[j * ldm + k],  t in [t0, t0 + 16), j < r
+// (h = x . A^T, src/linear.rs:85,106).  Written to out[(t * r + j) * pstride + pidx] (slice index
+// fastest, so a consumer sums a token's partials in slice order with a few wide loads).  Columns
+// beyond kend count as zero.
+__device__ __forceinline__ void lora_partial(const float* S, int T, int ks, const float* M, int ldm, int r, int k0,
+                                             int kend, int t0, float* out, int pstride, int pidx, float* sx,
+                                             float* sm, float* red) {
+  constexpr int LDX = RTQ_ACT_KQ + 1;
   const int tid = threadIdx.x, tl = tid >> 4, sg = tid & 15, t = t0 + tl;
   const int lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
   {
@@ -270,12 +267,7 @@ __device__ __forceinline__ void lora_partial(const float* S, int T, int ks, cons
     for (int i = 0; i < 16; i++) sx[tl * LDX + sg * 16 + i] = v[i];
   }
   for (int j0 = 0; j0 < r; j0 += 16) {
-    if (MT && !rb_any(*rb, k0, min(k0 + RTQ_ACT_KQ, kend), j0, min(j0 + 16, r))) {  // uniform over the workgroup
-      const int tt = tid >> 4, jj = tid & 15, ty = t0 + tt, jo = j0 + jj;
-      if (ty < T && jo < r) out[((int64_t)ty * r + jo) * pstride + pidx] = 0.0f;
-      continue;
-    }
-    if (!MT) {  // A rows j0 .. j0+15, columns k0 .. k0+255: thread (row tl, segment sg)
+    {  // A rows j0 .. j0+15, columns k0 .. k0+255: thread (row tl, segment sg)
       float v[16];
       const int jr = j0 + tl, kk = k0 + sg * 16;
       load_seg(M + (int64_t)jr * ldm + kk, jr < r && kk + 16 <= kend, v);
@@ -285,21 +277,13 @@ __device__ __forceinline__ void lora_partial(const float* S, int T, int ks, cons
       }
 #pragma unroll
       for (int i = 0; i < 16; i++) sm[tl * LDX + sg * 16 + i] = v[i];
-    } else {  // B rows k0 .. k0+255 (16 ranks each): thread tid stages row k0 + tid
-      const int k = k0 + tid;
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const int j = j0 + i;
-        const float bv = M[(int64_t)min(k, mrows - 1) * ldm + min(j, r - 1)];
-        sm[tid * LDB + i] = (k < kend && j < r && rb_keep(*rb, k, j)) ? bv : 0.0f;
-      }
     }
     __syncthreads();
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int u = 0; u < 16; u++) {
       const int kl = 64 * w + 4 * u + g;
-      acc = mfma_f32(sx[li * LDX + kl], MT ? sm[kl * LDB + li] : sm[li * LDX + kl], acc);
+      acc = mfma_f32(sx[li * LDX + kl], sm[li * LDX + kl], acc);
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) red[w * 256 + (4 * g + i) * 16 + li] = acc[i];
@@ -310,6 +294,88 @@ __device__ __forceinline__ void lora_partial(const float* S, int T, int ks, cons
       if (ty < T && jo < r) out[((int64_t)ty * r + jo) * pstride + pidx] = ps;
     }
     __syncthreads();
+  }
+}
+
+// LoRA-up input-gradient partial over one 256-row slice q of B (g = dy . B, src/linear.rs:111),
+// for TW tokens t0 .. t0+TW-1, by one 256-thread workgroup (f32 MFMA):
+//   gp[(t * r + j) * ngq + q] = sum over n in [256q, 256q + 256) of dy[t][n] * B[n][j]
+// B entries outside rb's blocks count as zero; rank tiles with none inside are written as zeros.
+// B's slice (256 rows x 16 ranks) is staged in LDS once per rank tile and shared by the waves;
+// LDS row n of the slice sits at 16n + 16 (n / 64), so the four lane groups of one MFMA step read
+// four different 16-bank spans.  Each wave holds its dy rows in registers in MFMA operand order:
+//   TW = 64: wave w owns tokens t0 + 16w .. +15 and all 256 rows; lane (token li, group g) loads
+//            rows 64g .. 64g+63 of the slice (256 contiguous bytes), step u contracts row 64g + u;
+//            no cross-wave reduction;
+//   TW = 16: wave w owns rows 64w .. 64w+63 of the 16 tokens; lane (li, g) loads rows
+//            64w + 16g .. +15, step u contracts row 64w + 16g + u; the four waves' sums are added
+//            in LDS in wave order (for grids too small to fill the chip with 64-token workgroups).
+template <int TW>
+__device__ __forceinline__ void lora_up_partial(const BwdPrepArgs& a, int t0, int q, float* sb, float* red) {
+  constexpr int KQ = RTQ_ACT_KQ, NU = TW == 64 ? 64 : 16;
+  static_assert(KQ == 256, "one slice row per thread, four 64-row lane groups");
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
+  const int k0 = q * KQ, tw = TW == 64 ? t0 + 16 * w : t0, t = tw + li;
+  const int kl0 = TW == 64 ? 64 * g : 64 * w + 16 * g, kb = k0 + kl0;  // first slice row of this lane
+  float v[NU];
+  {
+    const float* row = a.dy + (int64_t)min(t, a.T - 1) * a.N;
+    if (t < a.T && kb + NU <= a.N) {
+      const f4* s4 = reinterpret_cast<const f4*>(row + kb);
+#pragma unroll
+      for (int i = 0; i < NU / 4; i++) {
+        const f4 e = s4[i];
+        v[4 * i] = e.x;
+        v[4 * i + 1] = e.y;
+        v[4 * i + 2] = e.z;
+        v[4 * i + 3] = e.w;
+      }
+    } else {  // tokens past T, ragged N
+#pragma unroll
+      for (int u = 0; u < NU; u++) v[u] = (t < a.T && kb + u < a.N) ? row[min(kb + u, a.N - 1)] : 0.0f;
+    }
+  }
+  const bool tok_ok = tw < a.T;  // wave-uniform
+  for (int j0 = 0; j0 < a.r; j0 += 16) {
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool any = rb_any(a.rb, k0, min(k0 + KQ, a.N), j0, min(j0 + 16, a.r));  // uniform over the workgroup
+    if (any) {
+      {
+        const int k = k0 + tid;
+        const float* brow = a.B + (int64_t)min(k, a.N - 1) * a.r;
+        float* dst = sb + 16 * tid + 16 * (tid >> 6);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const int j = j0 + i;
+          const float bv = brow[min(j, a.r - 1)];
+          dst[i] = (k < a.N && j < a.r && rb_keep(a.rb, k, j)) ? bv : 0.0f;
+        }
+      }
+      __syncthreads();
+      if (tok_ok) {
+        const float* sg = sb + 16 * kl0 + 16 * (kl0 >> 6) + li;
+#pragma unroll
+        for (int u = 0; u < NU; u++) acc = mfma_f32(v[u], sg[16 * u], acc);
+      }
+      if (TW == 16) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) red[w * 256 + (4 * g + i) * 16 + li] = acc[i];
+      }
+      __syncthreads();  // red is complete; sb may be restaged (red is rewritten only after the next staging barrier)
+    }
+    if (TW == 64) {  // lane (rank li, token group g) holds tokens tw + 4g + i
+      const int j = j0 + li;
+      if (j < a.r)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int tt = tw + 4 * g + i;
+          if (tt < a.T) a.gp[((int64_t)tt * a.r + j) * a.ngq + q] = acc[i];
+        }
+    } else {  // thread (token tid / 16, rank tid % 16)
+      const int tt = t0 + (tid >> 4), j = j0 + (tid & 15);
+      const float ps = any ? (red[tid] + red[256 + tid]) + (red[512 + tid] + red[768 + tid]) : 0.0f;
+      if (tt < a.T && j < a.r) a.gp[((int64_t)tt * a.r + j) * a.ngq + q] = ps;
+    }
   }
 }
 
@@ -416,7 +482,7 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
     }
   }
   if (a.A)  // uniform; quarters beyond K write zero partials
-    lora_partial<false>(a.x, a.T, a.K, a.A, a.K, a.r, a.r, k0, a.K, t0, a.hp, gridDim.y, blockIdx.y, sx, sa, red);
+    lora_partial(a.x, a.T, a.K, a.A, a.K, a.r, k0, a.K, t0, a.hp, gridDim.y, blockIdx.y, sx, sa, red);
 }
 
 extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_0(ActArgs a) { act_prep<false>(a); }
@@ -1337,18 +1403,25 @@ RTQ_GEMV(rtq_gemv_q6_k, FMT_Q6_K, 2, 4)
 //   y < nhq:     partial h over columns [256y, 256y + 256) of x . A^T -> hp[t][j][y]
 //   y = nhq + q: partial g over rows [256q, 256q + 256) of W: dy . B   -> gp[t][j][q]
 // The dx kernel's extra workgroups sum the partials in slice order (h, and g scaled by s).
+// Grid (ceil(T / 16), [nhq +] ngq): rows y < nhq of the grid compute h partials for 16 tokens each,
+// the others g partials for gtok tokens each (workgroups x >= ceil(T / gtok) of those rows exit).
 extern "C" __global__ __launch_bounds__(256) void rtq_bwd_prep(BwdPrepArgs a) {
-  constexpr int KQ = RTQ_ACT_KQ, LDX = KQ + 1, LDB = 17;
-  static_assert(256 * LDB >= 16 * LDX, "the B slice reuses the A tile buffer");
+  constexpr int KQ = RTQ_ACT_KQ, LDX = KQ + 1;
+  constexpr int SM = 16 * KQ + 64 > 16 * LDX ? 16 * KQ + 64 : 16 * LDX;  // A tile, or B slice (padded rows)
   __shared__ float sx[16 * LDX];
-  __shared__ float sm[256 * LDB];
+  __shared__ float sm[SM];
   __shared__ float red[4 * 256];
-  const int t0 = blockIdx.x * 16, y = (int)blockIdx.y + a.y0;
-  if (y < a.nhq)
-    lora_partial<false>(a.x, a.T, a.K, a.A, a.K, a.r, a.r, y * KQ, a.K, t0, a.hp, a.nhq, y, sx, sm, red);
-  else
-    lora_partial<true>(a.dy, a.T, a.N, a.B, a.r, a.N, a.r, (y - a.nhq) * KQ, a.N, t0, a.gp, a.ngq, y - a.nhq, sx, sm,
-                       red, &a.rb);
+  const int y = (int)blockIdx.y + a.y0;
+  if (y < a.nhq) {
+    lora_partial(a.x, a.T, a.K, a.A, a.K, a.r, y * KQ, a.K, blockIdx.x * 16, a.hp, a.nhq, y, sx, sm, red);
+  } else {
+    const int t0 = blockIdx.x * a.gtok;
+    if (t0 >= a.T) return;  // whole workgroup
+    if (a.gtok == 64)
+      lora_up_partial<64>(a, t0, y - a.nhq, sm, red);
+    else
+      lora_up_partial<16>(a, t0, y - a.nhq, sm, red);
+  }
 }
 
 // ============================================================== dx = dy . W

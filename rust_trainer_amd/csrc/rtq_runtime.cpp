@@ -671,10 +671,14 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   float* part = ar.take<float>(dp.part_floats);
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   if (lora) {
-    BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq, RankBlocks{}, have_h ? (int)nhq : 0};
+    // h partials: 16 tokens per workgroup; g partials: 64, or 16 where 64-token workgroups would
+    // leave more than half of the CUs without one
+    const int gtok = cdiv(t, 64) * ngq * 2 >= c->cu_count ? 64 : 16;
+    BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq, RankBlocks{},
+                   have_h ? (int)nhq : 0, gtok};
     if (rb) pa.rb = *rb;
-    RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, 16), (unsigned)(have_h ? ngq : nhq + ngq)), dim3(256), st,
-                   pa));
+    RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, have_h ? gtok : 16), (unsigned)(have_h ? ngq : nhq + ngq)),
+                   dim3(256), st, pa));
   }
   DxArgs xa{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, (int)dp.splits, part,
             lora ? hp : nullptr, lora ? gp : nullptr, (int)nhq, (int)ngq, (int)r, s, h, g};
