@@ -135,7 +135,7 @@ struct BwdPrepArgs {
   int T, r;
   float* hp;     // [T][r][nhq] partials of x . A^T
   int nhq;
-  float* gp;     // [T][r][ngq] partials of dy . B
+  float* gp;     // [ngq][T][r] partials of dy . B
   int ngq;
   RankBlocks rb;  // g = dy . B restricted to each member's rows
   int y0;         // grid row offset: nhq when the h partials are already there (only g is computed)
@@ -157,7 +157,7 @@ struct DxArgs {
   float* part;          // [splits][T][K] partial products
   // LoRA finalisation by the extra workgroups of the last grid row (when gp != null):
   const float* hp;      // [T][r][nhq] partials from rtq_bwd_prep
-  const float* gp;      // [T][r][ngq]
+  const float* gp;      // [ngq][T][r]
   int nhq, ngq, r;
   float s;
   float* h;             // [T x r] = sum of hp
@@ -183,7 +183,6 @@ struct LoraGradArgs {
   int accumulate;        // 1: dx += (FrozenMatmul::backward_input); 0: dx = (Linear::backward)
   int part_rows;         // 1: partials row-major [nsplit][T][K] (rtq_dx16_*); 0: fragment order (rtq_dx_*)
   RankBlocks rb;         // gb written only inside the members' blocks
-  int gb_cpt;            // > 0: n_gb = row tiles x gb_cpt rank tiles counted from each row tile's member's col0
 };
 
 // rows [r0, r0+count) dequantised to f32 (bit-exact ggml dequant)

@@ -228,20 +228,24 @@ __device__ __forceinline__ void load_seg(const float* p, bool ok, float v[16]) {
 }
 
 // (row n, rank j) lies in a member's block of a block-diagonal adapter (always, for a plain one)
+// (member loops unrolled over the fixed capacity: constant indices keep the struct out of scratch)
 __device__ __forceinline__ bool rb_keep(const RankBlocks& b, int n, int j) {
   if (b.nm == 0) return true;
   bool keep = false;
-  for (int m = 0; m < b.nm; m++)
-    if (n >= b.row0[m] && n < b.row0[m] + b.nrow[m]) keep = j >= b.col0[m] && j < b.col0[m] + b.r[m];
+#pragma unroll
+  for (int m = 0; m < 3; m++)
+    if (m < b.nm && n >= b.row0[m] && n < b.row0[m] + b.nrow[m]) keep = j >= b.col0[m] && j < b.col0[m] + b.r[m];
   return keep;
 }
 // some (row, rank) pair of [n0, n1) x [j0, j1) lies in a member's block
 __device__ __forceinline__ bool rb_any(const RankBlocks& b, int n0, int n1, int j0, int j1) {
   if (b.nm == 0) return true;
-  for (int m = 0; m < b.nm; m++)
-    if (max(n0, b.row0[m]) < min(n1, b.row0[m] + b.nrow[m]) && max(j0, b.col0[m]) < min(j1, b.col0[m] + b.r[m]))
-      return true;
-  return false;
+  bool any = false;
+#pragma unroll
+  for (int m = 0; m < 3; m++)
+    any = any || (m < b.nm && max(n0, b.row0[m]) < min(n1, b.row0[m] + b.nrow[m]) &&
+                  max(j0, b.col0[m]) < min(j1, b.col0[m] + b.r[m]));
+  return any;
 }
 
 // LoRA-down partial product over a 256-column slice, by one 256-thread workgroup (f32 MFMA):
@@ -299,7 +303,8 @@ __device__ __forceinline__ void lora_partial(const float* S, int T, int ks, cons
 
 // LoRA-up input-gradient partial over one 256-row slice q of B (g = dy . B, src/linear.rs:111),
 // for TW tokens t0 .. t0+TW-1, by one 256-thread workgroup (f32 MFMA):
-//   gp[(t * r + j) * ngq + q] = sum over n in [256q, 256q + 256) of dy[t][n] * B[n][j]
+//   gp[(q * T + t) * r + j] = sum over n in [256q, 256q + 256) of dy[t][n] * B[n][j]
+// (slice-major, so each store instruction writes whole rank rows of consecutive tokens)
 // B entries outside rb's blocks count as zero; rank tiles with none inside are written as zeros.
 // B's slice (256 rows x 16 ranks) is staged in LDS once per rank tile and shared by the waves;
 // LDS row n of the slice sits at 16n + 16 (n / 64), so the four lane groups of one MFMA step read
@@ -369,12 +374,12 @@ __device__ __forceinline__ void lora_up_partial(const BwdPrepArgs& a, int t0, in
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const int tt = tw + 4 * g + i;
-          if (tt < a.T) a.gp[((int64_t)tt * a.r + j) * a.ngq + q] = acc[i];
+          if (tt < a.T) a.gp[((int64_t)q * a.T + tt) * a.r + j] = acc[i];
         }
     } else {  // thread (token tid / 16, rank tid % 16)
       const int tt = t0 + (tid >> 4), j = j0 + (tid & 15);
       const float ps = any ? (red[tid] + red[256 + tid]) + (red[512 + tid] + red[768 + tid]) : 0.0f;
-      if (tt < a.T && j < a.r) a.gp[((int64_t)tt * a.r + j) * a.ngq + q] = ps;
+      if (tt < a.T && j < a.r) a.gp[((int64_t)q * a.T + tt) * a.r + j] = ps;
     }
   }
 }
@@ -386,6 +391,16 @@ __device__ __forceinline__ float sum_partials(const float* p, int64_t e, int np)
   for (int i = 0; i < np / 4; i++) {
     const f4 v = q[i];
     s += ((v.x + v.y) + (v.z + v.w));
+  }
+  return s;
+}
+
+// the same sum over slice-major partials p[i * stride + e] (same association as sum_partials)
+__device__ __forceinline__ float sum_slices(const float* p, int64_t e, int np, int64_t stride) {
+  float s = 0.0f;
+  for (int i = 0; i < np; i += 4) {
+    const float* q = p + (int64_t)i * stride + e;
+    s += ((q[0] + q[stride]) + (q[2 * stride] + q[3 * stride]));
   }
   return s;
 }
@@ -1471,7 +1486,7 @@ __device__ __forceinline__ void dx_lora_sums(const DxArgs& a, int rel, int nfin)
   const int64_t nthr = (int64_t)nfin * blockDim.x;
   for (int64_t e = (int64_t)rel * blockDim.x + threadIdx.x; e < n; e += nthr) {
     a.h[e] = sum_partials(a.hp, e, a.nhq);
-    a.g[e] = a.s * sum_partials(a.gp, e, a.ngq);
+    a.g[e] = a.s * sum_slices(a.gp, e, a.ngq, n);
   }
 }
 
@@ -1929,80 +1944,100 @@ extern "C" __global__ __launch_bounds__(512) void rtq_dxw_q6_k(DxArgs a) { dx_ti
 //    w.backward_input(dy) + g.A, src/linear.rs:100-101,115-118)
 // gb[n][j] += sum_t (s*dy[t][n]) h[t][j]   (matmul_tn_acc, src/linear.rs:109)
 // ga[j][k] += sum_t g[t][j] x[t][k]        (matmul_tn_acc, src/linear.rs:113)
-// gb / ga: one 16x16 tile per workgroup, the NW waves split t and reduce in LDS (single writer,
-// fixed order); dx: one wave per 16 x 16 quarter of a dx-kernel fragment (the dx kernel's partial
-// layout).  NW = 4, or 16 for long token ranges (four times the loads in flight per tile).
+// gb / ga: one 64 x 16 tile (64 rows m of X = s.dy or x, 16 ranks j) per workgroup; the NW waves
+// split the tokens and contract 4 tokens per step with four f32 MFMAs (MFMA e takes rows
+// m0 + 4i + e, so a lane's four X values are one 16-byte load of a token row); their tiles are
+// added in LDS in wave order (single writer, fixed order).  GB: tile b of gb (X = dy, H = h),
+// otherwise of ga (X = x, H = g).
+template <int NW, bool GB>
+__device__ __forceinline__ void lora_grad_tile(const LoraGradArgs& a, int b, float* red) {
+  constexpr int LDR = 17;  // LDS row stride of a wave's 64 x 16 tile (the four lane groups on different banks)
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
+  const int jt = (a.r + 15) / 16, m0 = (b / jt) * 64, j0 = (b % jt) * 16;
+  const int M = GB ? a.N : a.K;
+  // block-diagonal adapter: only tiles that meet a member's block (uniform exit)
+  if (GB && !rb_any(a.rb, m0, min(m0 + 64, a.N), j0, min(j0 + 16, a.r))) return;
+  const float* X = GB ? a.dy : a.x;  // [T x M]
+  const float* H = GB ? a.h : a.g;   // [T x r]
+  const int tper = (a.T + NW * 16 - 1) / (NW * 16) * 16;  // tokens per wave, multiple of 16
+  const int tb = w * tper, te = min(tb + tper, a.T);
+  const int mc = m0 + 4 * li, jc = j0 + li;
+  const bool vec = (M & 3) == 0;  // 16-byte aligned rows (always for x: K % 32 == 0)
+  f4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
+  for (int t32 = tb; t32 < te; t32 += 32) {  // 32 tokens: all loads, then up to 32 MFMAs
+    const int nv = min(2, (te - t32 + 15) / 16);  // 16-token groups with tokens (wave-uniform)
+    f4 xv[2][4];
+    float hv[2][4];
+#pragma unroll
+    for (int v = 0; v < 2; v++)
+      if (v < nv)
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int t = t32 + 16 * v + 4 * u + g, tc = min(t, a.T - 1);
+          const bool tin = t < te;
+          const float* xr = X + (int64_t)tc * M;
+          if (vec) {
+            const f4 x4 = *reinterpret_cast<const f4*>(xr + min(mc, M - 4));
+            xv[v][u] = (tin && mc < M) ? x4 : f4{0.0f, 0.0f, 0.0f, 0.0f};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) xv[v][u][e] = (tin && mc + e < M) ? xr[min(mc + e, M - 1)] : 0.0f;
+          }
+          const float hh = H[(int64_t)tc * a.r + min(jc, a.r - 1)];
+          hv[v][u] = (tin && jc < a.r) ? hh : 0.0f;
+        }
+#pragma unroll
+    for (int v = 0; v < 2; v++)
+      if (v < nv)
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          f4 x4 = xv[v][u];
+          if (GB) x4 = f4{__fmul_rn(x4.x, a.s), __fmul_rn(x4.y, a.s), __fmul_rn(x4.z, a.s), __fmul_rn(x4.w, a.s)};
+          acc0 = mfma_f32(x4.x, hv[v][u], acc0);  // s.dy (src/linear.rs:108) for gb; x for ga
+          acc1 = mfma_f32(x4.y, hv[v][u], acc1);
+          acc2 = mfma_f32(x4.z, hv[v][u], acc2);
+          acc3 = mfma_f32(x4.w, hv[v][u], acc3);
+        }
+  }
+  // lane (rank li, group g): element i of acc<e> is row m0 + 4 (4g + i) + e
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float* rr = red + w * 64 * LDR + (16 * g + 4 * i) * LDR + li;
+    rr[0] = acc0[i];
+    rr[LDR] = acc1[i];
+    rr[2 * LDR] = acc2[i];
+    rr[3 * LDR] = acc3[i];
+  }
+  __syncthreads();
+  for (int o = threadIdx.x; o < 1024; o += NW * 64) {
+    // gb: consecutive threads take consecutive ranks of a row; ga: consecutive columns of a rank
+    const int mr = GB ? o >> 4 : o & 63, jr = GB ? o & 15 : o >> 6;
+    float sum = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ww++) sum += red[ww * 64 * LDR + mr * LDR + jr];
+    const int m = m0 + mr, j = j0 + jr;
+    if (m < M && j < a.r) {
+      if (GB) {
+        if (rb_keep(a.rb, m, j)) a.gb[(int64_t)m * a.r + j] += sum;
+      } else {
+        a.ga[(int64_t)j * a.K + m] += sum;
+      }
+    }
+  }
+}
+
+// One grid, three kinds of workgroups: gb tiles, ga tiles (lora_grad_tile), then dx: one wave per
+// 16 x 16 quarter of a dx-kernel fragment (the dx kernel's partial layout) or per token and 64
+// columns (row-major partials).  NW = 4, or 16 for long token ranges.
 template <int NW>
 __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
-  __shared__ float red[NW * 256];
+  __shared__ float red[NW * 64 * 17];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
-  const int jt = (a.r + 15) / 16;
-  int b = blockIdx.x;
-  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  const int tper = (a.T + NW * 16 - 1) / (NW * 16) * 16;  // t per wave, multiple of 16
-  const int tb = w * tper, te = min(tb + tper, a.T);
-  if (b < a.n_gb + a.n_ga) {
-    const bool is_gb = b < a.n_gb;
-    if (!is_gb) b -= a.n_gb;
-    int rt = b / jt, ct = b % jt;
-    if (is_gb) {  // block-diagonal adapter: only tiles that meet a member's block (uniform exit)
-      if (a.gb_cpt > 0) {  // rank tiles counted from the col0 of the row tile's member
-        rt = b / a.gb_cpt;
-        int m = 0;
-        for (int i = 1; i < a.rb.nm; i++)
-          if (rt * 16 >= a.rb.row0[i]) m = i;
-        ct = (a.rb.nm ? a.rb.col0[m] / 16 : 0) + b % a.gb_cpt;
-      }
-      if (ct >= jt || !rb_any(a.rb, rt * 16, min(rt * 16 + 16, a.N), ct * 16, min(ct * 16 + 16, a.r))) return;
-    }
-    // gb: rows n (tile rt), cols j (tile ct);  ga: rows j (tile ct), cols k (tile rt)
-    const int rrow = is_gb ? rt * 16 + li : ct * 16 + li;
-    const int ccol = is_gb ? ct * 16 + li : rt * 16 + li;
-    // up to 64 tokens per pass: the loads of its 16-token groups (nv, wave-uniform; none past the
-    // wave's range) are issued before their MFMAs
-    for (int t64 = tb; t64 < te; t64 += 64) {
-      const int nv = min(4, (te - t64 + 15) / 16);
-      float av[4][4], bv[4][4];
-#pragma unroll
-      for (int v = 0; v < 4; v++)
-        if (v < nv)
-#pragma unroll
-          for (int u = 0; u < 4; u++) {
-            const int tt = t64 + 16 * v + 4 * u + g, tc = min(tt, a.T - 1);
-            if (is_gb) {
-              const float x = a.dy[(int64_t)tc * a.N + min(rrow, a.N - 1)];
-              const float y = a.h[(int64_t)tc * a.r + min(ccol, a.r - 1)];
-              av[v][u] = (tt < te && rrow < a.N) ? __fmul_rn(x, a.s) : 0.0f;
-              bv[v][u] = (tt < te && ccol < a.r) ? y : 0.0f;
-            } else {
-              const float x = a.g[(int64_t)tc * a.r + min(rrow, a.r - 1)];
-              const float y = a.x[(int64_t)tc * a.K + min(ccol, a.K - 1)];
-              av[v][u] = (tt < te && rrow < a.r) ? x : 0.0f;
-              bv[v][u] = (tt < te && ccol < a.K) ? y : 0.0f;
-            }
-          }
-#pragma unroll
-      for (int v = 0; v < 4; v++)
-        if (v < nv)
-#pragma unroll
-          for (int u = 0; u < 4; u++) acc = mfma_f32(av[v][u], bv[v][u], acc);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) red[w * 256 + (4 * g + i) * 16 + li] = acc[i];
-    __syncthreads();
-    if (threadIdx.x < 256) {
-      const int rl = threadIdx.x >> 4, cl = threadIdx.x & 15;
-      float s = 0.0f;
-#pragma unroll
-      for (int ww = 0; ww < NW; ww++) s += red[ww * 256 + threadIdx.x];
-      if (is_gb) {
-        const int n = rt * 16 + rl, j = ct * 16 + cl;
-        if (n < a.N && j < a.r && rb_keep(a.rb, n, j)) a.gb[(int64_t)n * a.r + j] += s;
-      } else {
-        const int j = ct * 16 + rl, k = rt * 16 + cl;
-        if (j < a.r && k < a.K) a.ga[(int64_t)j * a.K + k] += s;
-      }
-    }
+  const int b = blockIdx.x;
+  if (b < a.n_gb) {
+    lora_grad_tile<NW, true>(a, b, red);
+  } else if (b < a.n_gb + a.n_ga) {
+    lora_grad_tile<NW, false>(a, b - a.n_gb, red);
   } else if (a.part_rows) {
     // dx from row-major partials: wave per (token t, 64 columns); lane (k4 = li, split subset g)
     // sums splits g, g+4, ... of four columns, the subsets are combined by shuffles (fixed order)

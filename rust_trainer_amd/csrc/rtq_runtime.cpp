@@ -690,25 +690,13 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   RTQ_TRY(launch(c, kid, dim3((unsigned)(nmain + nfin)), dim3(dp.tok16 ? 256 : 512), st, xa));
   const int64_t jt = cdiv(r, 16);
   LoraGradArgs fa{dy, h, g, x, la, (int)t, N, K, (int)r, s, gb, ga, dx, 0, 0, 0, part, (int)dp.splits, accumulate ? 1 : 0,
-                  dp.tok16 ? 1 : 0, RankBlocks{}, 0};
-  // block-diagonal adapter with members on 16-row boundaries: per row tile only the rank tiles of
-  // its member's block (gb_cpt of them at most)
-  fa.gb_cpt = 0;
-  if (rb && rb->nm > 0) {
-    fa.rb = *rb;
-    bool aligned = true;
-    int cpt = 0;
-    for (int m = 0; m < rb->nm; m++) {
-      aligned = aligned && rb->row0[m] % 16 == 0;
-      if (rb->r[m] > 0) cpt = std::max(cpt, (rb->col0[m] + rb->r[m] - 1) / 16 - rb->col0[m] / 16 + 1);
-    }
-    if (aligned) fa.gb_cpt = std::max(cpt, 1);
-  }
-  fa.n_gb = lora ? (int)(cdiv(N, 16) * (fa.gb_cpt > 0 ? fa.gb_cpt : jt)) : 0;
-  fa.n_ga = lora ? (int)(cdiv(K, 16) * jt) : 0;
-  // one wave per quarter of a dx fragment (or per token and 64 columns), nw per workgroup; 16 waves
-  // per workgroup when the dA / dB tiles reduce over many tokens
-  const int nw = lora && t >= 512 ? 16 : 4;
+                  dp.tok16 ? 1 : 0, RankBlocks{}};
+  if (rb) fa.rb = *rb;  // block-diagonal adapter: dB tiles outside every member's block exit at once
+  // dB / dA: one workgroup per 64-row x 16-rank tile; dx: one wave per quarter of a dx fragment (or
+  // per token and 64 columns); nw waves per workgroup, 16 when the dA / dB tiles reduce over many tokens
+  fa.n_gb = lora ? (int)(cdiv(N, 64) * jt) : 0;
+  fa.n_ga = lora ? (int)(cdiv(K, 64) * jt) : 0;
+  const int nw = lora && t >= 256 ? 16 : 4;
   fa.n_dx = dp.tok16 ? (int)cdiv(t * cdiv(K, 64), nw) : (int)cdiv((w->Kp / 128) * cdiv(t, 64) * 32, nw);
   return launch(c, nw == 16 ? K_BWD_FINISH16 : K_BWD_FINISH, dim3((unsigned)(fa.n_gb + fa.n_ga + fa.n_dx)),
                 dim3(64 * nw), st, fa);
