@@ -120,6 +120,8 @@ enum Kid {
   K_GEMV = K_FWD_S_ISUMS + F_COUNT,       // + format: t <= 16, large N
   K_FWD_Q4_0_W8 = K_GEMV + F_COUNT,       // wide forward with eight waves splitting K
   K_FWD_Q8_0_W8,
+  K_FWD_Q4_0_W8R2,  // the same with 32-row tiles
+  K_FWD_Q8_0_W8R2,
   K_MM_Q4_0,     // large-grid forward (128 x 128 tiles, LDS ring)
   K_MM_Q8_0,
   K_MM64_Q4_0,   // the same with 128 x 64 tiles
@@ -148,7 +150,8 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_fwd_q4_0_w_isums", "rtq_fwd_q8_0_w_isums", "rtq_fwd_q4_k_w_isums", "rtq_fwd_q6_k_w_isums",
     "rtq_fwd_q4_0_s_isums", "rtq_fwd_q8_0_s_isums", "rtq_fwd_q4_k_s_isums", "rtq_fwd_q6_k_s_isums",
     "rtq_gemv_q4_0",        "rtq_gemv_q8_0",        "rtq_gemv_q4_k",        "rtq_gemv_q6_k",
-    "rtq_fwd_q4_0_w8",      "rtq_fwd_q8_0_w8",      "rtq_mm_q4_0",          "rtq_mm_q8_0",
+    "rtq_fwd_q4_0_w8",      "rtq_fwd_q8_0_w8",      "rtq_fwd_q4_0_w8r2",    "rtq_fwd_q8_0_w8r2",
+    "rtq_mm_q4_0",          "rtq_mm_q8_0",
     "rtq_mm64_q4_0",        "rtq_mm64_q8_0",
     "rtq_bwd_prep",
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
@@ -186,6 +189,7 @@ struct rtq_ctx {
   int dx_splits = 0;  // 0: automatic; RTQ_DX_SPLITS overrides (tuning)
   int dx_wide = -1;   // 256-token dx tiles: -1 automatic, 0 never, 1 for every t > 16 (RTQ_DX_WIDE)
   int fwd_waves = 8;  // waves splitting K in the wide Q4_0 / Q8_0 forward (RTQ_FWD_WAVES: 4 or 8)
+  int fwd_rg = -1;    // row groups of 16 per eight-wave forward tile: -1 automatic, 2 or 3 (RTQ_FWD_RG)
   int fwd_mm = -1;    // large-grid forward: -1 automatic, 0 never, 1 / 2 the 128- / 64-token tiles whenever
                       // the format allows (RTQ_FWD_MM)
   rocblas_handle blas = nullptr;  // created on the first trainer-native (f32 GEMM) weight
@@ -520,8 +524,14 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   }
   const int64_t Kc = w->Kp / 128;
   const bool kq = is_kquant(w->type);
-  const int64_t rg_per_wg = p.skinny ? kFwdSkinnyRG : wide_rg(w->type);
-  const int64_t gx = cdiv(w->Np / 16, rg_per_wg), gy = p.skinny ? p.Tp / 16 : cdiv(t, 16 * kFwdWideTT);
+  const bool w8 = !p.skinny && !isums && !kq && c->fwd_waves == 8;  // rtq_fwd_*_w8[r2]
+  const int64_t gy = p.skinny ? p.Tp / 16 : cdiv(t, 16 * kFwdWideTT);
+  // the eight-wave forward with 32-row tiles where 48-row tiles would leave CUs without a workgroup
+  // and 32-row tiles would not (RTQ_FWD_RG: 2 or 3 forces one)
+  const bool rg2 = w8 && (c->fwd_rg == 2 || (c->fwd_rg < 0 && cdiv(w->Np / 16, 3) * gy < c->cu_count &&
+                                                cdiv(w->Np / 16, 2) * gy >= c->cu_count));
+  const int64_t rg_per_wg = p.skinny ? kFwdSkinnyRG : (rg2 ? 2 : wide_rg(w->type));
+  const int64_t gx = cdiv(w->Np / 16, rg_per_wg);
   // the large-grid kernel once its 128 x 128 tiles alone give a workgroup per CU, else its
   // 128 x 64 tiles if those do
   const int64_t mm_rows = cdiv(w->Np / 16, 8);
@@ -582,8 +592,8 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
                   dim3((unsigned)mm_tiles), dim3(256), st, fa, mm_lds_bytes(w->type, mm_ttn));
   int kid = (p.skinny ? (isums ? K_FWD_S_ISUMS : K_FWD_S) : (isums ? K_FWD_W_ISUMS : K_FWD_W)) + fmt_index(w->type);
   int threads = 256;
-  if (!p.skinny && !isums && !kq && c->fwd_waves == 8) {
-    kid = w->type == RTQ_TYPE_Q4_0 ? K_FWD_Q4_0_W8 : K_FWD_Q8_0_W8;
+  if (w8) {
+    kid = (rg2 ? K_FWD_Q4_0_W8R2 : K_FWD_Q4_0_W8) + (w->type == RTQ_TYPE_Q4_0 ? 0 : 1);
     threads = 512;
   }
   return launch(c, kid, dim3((unsigned)gx, (unsigned)gy, (unsigned)ks), dim3(threads), st, fa);
@@ -869,6 +879,7 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   if (const char* e = getenv("RTQ_DX_WIDE")) c->dx_wide = atoi(e) ? 1 : 0;
   if (const char* e = getenv("RTQ_FWD_WAVES")) c->fwd_waves = atoi(e) == 4 ? 4 : 8;
   if (const char* e = getenv("RTQ_FWD_MM")) c->fwd_mm = std::min(std::max(atoi(e), 0), 2);
+  if (const char* e = getenv("RTQ_FWD_RG")) c->fwd_rg = atoi(e) == 2 ? 2 : 3;
   hipError_t e = hipModuleLoadData(&c->mod, rtq_hsaco_begin);
   if (e != hipSuccess) {
     delete c;
