@@ -151,11 +151,20 @@ typedef struct rtq_model_config {
   int64_t n_layer, n_embd, n_head, n_head_kv, head_dim, rope_dim, n_ff, n_vocab;
   float rms_eps, norm_offset, rope_base, rope_freq_scale;
   int rope_neox, qk_norm, kv_f16, tied;
+  int64_t n_rope_factors; /* length of rope_freqs.weight (0: none) */
 } rtq_model_config;
 /* hyper-parameters from `<arch>.*` keys, tensors blk.{i}.{attn_q,attn_k,attn_v,attn_output,
  * ffn_gate,ffn_up,ffn_down}.weight (+ optional q/k/v .bias), norms F32; tied when output.weight is
- * absent; post-norm layers are rejected (src/rie.rs:204-206) */
+ * absent.  Refused with RTQ_ERR_UNSUPPORTED as the reference's loader refuses them: architectures
+ * other than llama / qwen2 / qwen3 (trainable_arch, src/rie.rs:153-155), embedding / residual /
+ * logit scales other than 1, softcaps, a sliding window, an attention scale other than
+ * 1/sqrt(head_dim) (src/rie.rs:173-183), mixture-of-experts FFNs (:211-216), post-norm layers
+ * (:204-206), and RoPE scaling other than none / linear.  Linear RoPE scaling
+ * (<arch>.rope.scaling.factor) and rope_freqs.weight (per-frequency divisors) are applied as
+ * Rope::at_positions does (src/ops.rs:141-158). */
 rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out);
+/* the hyper-parameters and refusals of rtq_model_from_gguf alone, without a device */
+rtq_status rtq_model_config_from_gguf(const rtq_gguf* g, rtq_model_config* out);
 void rtq_model_destroy(rtq_model* m);
 rtq_status rtq_model_get_config(const rtq_model* m, rtq_model_config* out);
 /* Model::attach_lora (src/model.rs:406-419): target_mask bit i adapts linear i of (q, k, v, o, gate,
@@ -180,6 +189,27 @@ rtq_status rtq_model_zero_grad(rtq_model* m); /* Model::zero_grad (src/model.rs:
 rtq_status rtq_model_forward_backward(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* pos,
                                       const int32_t* tok, const float* weights, int64_t n, float* logp,
                                       int64_t* hits);
+/* Model::forward_backward_packed (src/model.rs:634-642) on a packed batch (Packed / pack,
+ * src/model.rs:234-290): positions [t] (RoPE, Model::rope_for :461-481) and segments [t] of every
+ * token; token i may attend to token j <= i when segments[j] is 0 (the shared prompt) or equals
+ * segments[i] (Rope::allowed, src/ops.rs:160-167).  Targets index the packed tokens. */
+rtq_status rtq_model_forward_backward_packed(rtq_model* m, const int32_t* tokens, int64_t t,
+                                             const int32_t* positions, const int32_t* segments, const int32_t* pos,
+                                             const int32_t* tok, const float* weights, int64_t n, float* logp,
+                                             int64_t* hits);
+/* Model::checkpointing (src/model.rs:299-300; the loader's default true, src/rie.rs:254): 1 keeps
+ * only each block's input and recomputes its forward in the backward (src/model.rs:663-665,
+ * 678-680); 0 keeps every block's activations; -1 (default) keeps them when they take at most half
+ * of the device memory free at the step, else recomputes.  The results are the same. */
+rtq_status rtq_model_set_checkpointing(rtq_model* m, int mode);
+int rtq_model_checkpointing(const rtq_model* m); /* 1 when the last step recomputed */
+/* parity / debug: while layer >= 0 (-1: off), each step copies that block's tensors in the forward
+ * (x, n1, inv1, q_raw, k_raw, v_raw, q, k, v, q_inv, k_inv, P [nh x t x t], o, h, n2, inv2, gate,
+ * up, hm, y) and its backward (dy, dhm, dgate, dup, dn2, dh, d_o, dS, dq, dk, dv, dq_raw, dk_raw,
+ * dn1, dx), row-major per token; rtq_model_debug_tensor copies one to the host (nfloats must match;
+ * out NULL: only checks that the tensor exists and holds at most nfloats). */
+rtq_status rtq_model_debug_capture(rtq_model* m, int64_t layer);
+rtq_status rtq_model_debug_tensor(rtq_model* m, const char* name, float* out, int64_t nfloats);
 
 /* ---- parity / debug (host pointers, synchronous) ---- */
 /* The activation blocks the GPU forward actually uses for x, in ggml layout (block_q8_0: 34 B per

@@ -58,7 +58,7 @@ class OrModel(ctypes.Structure):
                 ("eps", ctypes.c_float), ("off", ctypes.c_float), ("theta", ctypes.c_float),
                 ("freq_scale", ctypes.c_float), ("neox", ctypes.c_int), ("kv_f16", ctypes.c_int),
                 ("embed", OrLinear), ("lm_head", OrLinear), ("out_norm", ctypes.c_void_p),
-                ("layers", ctypes.POINTER(OrLayer))]
+                ("layers", ctypes.POINTER(OrLayer)), ("rope_factors", ctypes.c_void_p), ("n_factors", ctypes.c_int64)]
 
 
 def lib() -> ctypes.CDLL:
@@ -101,6 +101,19 @@ def lib() -> ctypes.CDLL:
             "or_rope_table": (None, [_i64, _i64, _f, _f, _p, _p]),
             "or_model_forward_backward": (_i, [ctypes.POINTER(OrModel), _p, _i64, _p, _p, _p, _i64, _p,
                                                ctypes.POINTER(_i64), _i]),
+            "or_model_forward_backward_layout": (_i, [ctypes.POINTER(OrModel), _p, _i64, _p, _p, _p, _p, _p, _i64,
+                                                      _p, ctypes.POINTER(_i64), _i]),
+            "or_rope_table_at": (None, [_p, _i64, _i64, _f, _f, _p, _i64, _p, _p]),
+            "or_allowed": (_i, [_p, _i64, _i64]),
+            "or_rmsnorm": (None, [_p, _p, _i64, _i64, _f, _f, _i, _p, _p]),
+            "or_rmsnorm_backward": (None, [_p, _p, _p, _p, _i64, _i64, _f, _p]),
+            "or_qk_prep": (None, [ctypes.POINTER(OrModel), _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p]),
+            "or_qk_backward": (None, [ctypes.POINTER(OrModel), _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p,
+                                      _p]),
+            "or_attention_forward": (None, [ctypes.POINTER(OrModel), _p, _p, _p, _i64, _p, _p, _p, _i]),
+            "or_attention_backward": (None, [ctypes.POINTER(OrModel), _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _i]),
+            "or_swiglu": (None, [_p, _p, _i64, _p]),
+            "or_swiglu_backward": (None, [_p, _p, _p, _i64, _p, _p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -333,24 +346,31 @@ def round_f16(x: float) -> float:
     return float(lib().or_round_f16(x))
 
 
-def rope_table(t: int, rot: int, theta: float, freq_scale: float = 1.0):
+def rope_table(t: int, rot: int, theta: float, freq_scale: float = 1.0, positions=None, factors=None):
+    """Rope::at_positions (src/ops.rs:141-167): cos / sin [t x rot/2] for positions (default 0..t-1)."""
     cos_ = np.empty((t, rot // 2), np.float32)
     sin_ = np.empty((t, rot // 2), np.float32)
-    lib().or_rope_table(t, rot, theta, freq_scale, _ptr(cos_), _ptr(sin_))
+    if positions is None and factors is None:
+        lib().or_rope_table(t, rot, theta, freq_scale, _ptr(cos_), _ptr(sin_))
+        return cos_, sin_
+    pos = None if positions is None else np.ascontiguousarray(positions, np.int32)
+    fac = None if factors is None else _f32(factors)
+    lib().or_rope_table_at(_ptr(pos), t, rot, theta, freq_scale, _ptr(fac), 0 if fac is None else fac.size,
+                           _ptr(cos_), _ptr(sin_))
     return cos_, sin_
+
+
+def allowed(seg, i: int, j: int) -> bool:
+    """Rope::allowed (src/ops.rs:160-167)"""
+    s = None if seg is None else np.ascontiguousarray(seg, np.int32)
+    return bool(lib().or_allowed(_ptr(s), i, j))
 
 
 LINEARS = ("q", "k", "v", "o", "gate", "up", "down")
 
 
-def model_forward_backward(m: dict, tokens, pos, tok, wts=None, nthreads=1):
-    """Model::forward_backward (src/model.rs:615-687) of a model described by ``m``:
-    scalars n_layer, d, n_head, n_kv, hd, rot, n_ff, eps, off, theta, freq_scale, neox, kv_f16;
-    ``embed`` / ``lm_head`` = (wtype, blocks, out, in); ``out_norm``; ``layers`` = list of dicts with
-    attn_norm, ffn_norm, q_norm, k_norm (or None) and per linear name a dict wtype, blocks, out, in,
-    optional bias, A [r x in], B [out x r], alpha.  Returns (logp, hits, grads) with grads[l][name] =
-    (ga, gb) accumulated from zero."""
-    keep = []
+def _model_struct(m: dict, keep: list, grads: list | None = None):
+    """(OrModel, per-layer grads) for the dict description of model_forward_backward"""
 
     def arr(a, dt=np.float32):
         if a is None:
@@ -359,7 +379,7 @@ def model_forward_backward(m: dict, tokens, pos, tok, wts=None, nthreads=1):
         keep.append(a)
         return a.ctypes.data
 
-    def lin(d_, grads=None):
+    def lin(d_, gl=None):
         A, B = d_.get("A"), d_.get("B")
         r = 0 if A is None else int(np.asarray(A).shape[0])
         ga = gb = None
@@ -367,34 +387,132 @@ def model_forward_backward(m: dict, tokens, pos, tok, wts=None, nthreads=1):
             ga = np.zeros((r, d_["in"]), np.float32)
             gb = np.zeros((d_["out"], r), np.float32)
             keep.extend([ga, gb])
-            if grads is not None:
-                grads.append((ga, gb))
-        elif grads is not None:
-            grads.append(None)
+            if gl is not None:
+                gl.append((ga, gb))
+        elif gl is not None:
+            gl.append(None)
         blocks = np.ascontiguousarray(d_["blocks"])
         keep.append(blocks)
         return OrLinear(d_["wtype"], blocks.ctypes.data, d_["out"], d_["in"], arr(d_.get("bias")), r,
                         float(d_.get("alpha", 0.0)), arr(A), arr(B), None if ga is None else ga.ctypes.data,
                         None if gb is None else gb.ctypes.data)
 
-    L = (OrLayer * m["n_layer"])()
-    grads = []
-    for i, ld in enumerate(m["layers"]):
+    n_layer = m["n_layer"]
+    L = (OrLayer * max(n_layer, 1))()
+    keep.append(L)
+    for i, ld in enumerate(m["layers"][:n_layer]):
         gl = []
         L[i] = OrLayer(arr(ld["attn_norm"]), arr(ld["ffn_norm"]), arr(ld.get("q_norm")), arr(ld.get("k_norm")),
                        *[lin(ld[n], gl) for n in LINEARS])
-        grads.append(dict(zip(LINEARS, gl)))
+        if grads is not None:
+            grads.append(dict(zip(LINEARS, gl)))
     e, h = m["embed"], m["lm_head"]
-    M = OrModel(m["n_layer"], m["d"], m["n_head"], m["n_kv"], m["hd"], m["rot"], m["n_ff"], m["eps"], m["off"],
+    fac = m.get("rope_factors")
+    M = OrModel(n_layer, m["d"], m["n_head"], m["n_kv"], m["hd"], m["rot"], m["n_ff"], m["eps"], m["off"],
                 m["theta"], m["freq_scale"], int(m["neox"]), int(m["kv_f16"]),
                 lin(dict(wtype=e[0], blocks=e[1], out=e[2], **{"in": e[3]})),
-                lin(dict(wtype=h[0], blocks=h[1], out=h[2], **{"in": h[3]})), arr(m["out_norm"]), L)
+                lin(dict(wtype=h[0], blocks=h[1], out=h[2], **{"in": h[3]})), arr(m["out_norm"]), L,
+                arr(fac), 0 if fac is None else int(np.asarray(fac).size))
+    return M
+
+
+def model_forward_backward(m: dict, tokens, pos, tok, wts=None, nthreads=1, positions=None, segments=None):
+    """Model::forward_backward (src/model.rs:615-687) of a model described by ``m``:
+    scalars n_layer, d, n_head, n_kv, hd, rot, n_ff, eps, off, theta, freq_scale, neox, kv_f16
+    (optional rope_factors); ``embed`` / ``lm_head`` = (wtype, blocks, out, in); ``out_norm``;
+    ``layers`` = list of dicts with attn_norm, ffn_norm, q_norm, k_norm (or None) and per linear name
+    a dict wtype, blocks, out, in, optional bias, A [r x in], B [out x r], alpha.  ``positions`` /
+    ``segments`` (both [t]) give a packed layout (Model::forward_backward_packed, :634-642).
+    Returns (logp, hits, grads) with grads[l][name] = (ga, gb) accumulated from zero."""
+    keep: list = []
+    grads: list = []
+    M = _model_struct(m, keep, grads)
     tokens = np.ascontiguousarray(tokens, np.int32)
     pos = np.ascontiguousarray(pos, np.int32)
     tok = np.ascontiguousarray(tok, np.int32)
+    ps = None if positions is None else np.ascontiguousarray(positions, np.int32)
+    sg = None if segments is None else np.ascontiguousarray(segments, np.int32)
+    w = None if wts is None else _f32(wts)
     logp = np.empty(pos.size, np.float32)
     hits = ctypes.c_int64()
-    _check(lib().or_model_forward_backward(ctypes.byref(M), _ptr(tokens), tokens.size, _ptr(pos), _ptr(tok),
-                                           arr(wts), pos.size, _ptr(logp), ctypes.byref(hits), nthreads),
-           "model_forward_backward")
+    _check(lib().or_model_forward_backward_layout(ctypes.byref(M), _ptr(tokens), tokens.size, _ptr(ps), _ptr(sg),
+                                                  _ptr(pos), _ptr(tok), _ptr(w), pos.size, _ptr(logp),
+                                                  ctypes.byref(hits), nthreads), "model_forward_backward")
     return logp, hits.value, grads
+
+
+class BlockOps:
+    """The operations of one decoder block (src/model.rs:165-197, src/attention.rs:162-367,
+    src/model.rs:113-134) as separate calls on host arrays, for checking a device step op by op on
+    the device's own inputs.  ``m`` is the dict description of model_forward_backward."""
+
+    def __init__(self, m: dict):
+        self._keep: list = []
+        self.m = m
+        self.M = _model_struct(dict(m, n_layer=0, layers=[]), self._keep)
+
+    def rmsnorm(self, x, w, fused=False):
+        x = _f32(x)
+        rows, d = x.shape
+        y, inv = np.empty_like(x), np.empty(rows, np.float32)
+        lib().or_rmsnorm(_ptr(x), _ptr(_f32(w)), rows, d, self.m["eps"], self.m["off"], int(fused), _ptr(y), _ptr(inv))
+        return y, inv
+
+    def rmsnorm_backward(self, x, w, inv, dy):
+        x, dy = _f32(x), _f32(dy)
+        dx = np.empty_like(x)
+        lib().or_rmsnorm_backward(_ptr(x), _ptr(_f32(w)), _ptr(_f32(inv)), _ptr(dy), x.shape[0], x.shape[1],
+                                  self.m["off"], _ptr(dx))
+        return dx
+
+    def qk_prep(self, q_norm, k_norm, cos_, sin_, q_raw, k_raw, v_raw):
+        m, t = self.m, q_raw.shape[0]
+        q_raw, k_raw, v_raw = _f32(q_raw), _f32(k_raw), _f32(v_raw)
+        q, k, v = np.empty_like(q_raw), np.empty_like(k_raw), np.empty_like(v_raw)
+        qi, ki = np.empty(t * m["n_head"], np.float32), np.empty(t * m["n_kv"], np.float32)
+        qn = None if q_norm is None else _f32(q_norm)
+        kn = None if k_norm is None else _f32(k_norm)
+        lib().or_qk_prep(ctypes.byref(self.M), _ptr(qn), _ptr(kn), _ptr(_f32(cos_)), _ptr(_f32(sin_)), _ptr(q_raw),
+                         _ptr(k_raw), _ptr(v_raw), t, _ptr(q), _ptr(k), _ptr(v), _ptr(qi), _ptr(ki))
+        return q, k, v, qi, ki
+
+    def qk_backward(self, q_norm, k_norm, cos_, sin_, q_raw, k_raw, q_inv, k_inv, dq, dk):
+        t = q_raw.shape[0]
+        dq_raw, dk_raw = np.empty_like(_f32(q_raw)), np.empty_like(_f32(k_raw))
+        qn = None if q_norm is None else _f32(q_norm)
+        kn = None if k_norm is None else _f32(k_norm)
+        args = [_f32(a) for a in (cos_, sin_, q_raw, k_raw, q_inv, k_inv, dq, dk)]
+        lib().or_qk_backward(ctypes.byref(self.M), _ptr(qn), _ptr(kn), *[_ptr(a) for a in args], t, _ptr(dq_raw),
+                             _ptr(dk_raw))
+        return dq_raw, dk_raw
+
+    def attention(self, q, k, v, seg=None, nthreads=16):
+        m, t = self.m, q.shape[0]
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        probs = np.empty((m["n_head"], t, t), np.float32)
+        o = np.empty((t, m["n_head"] * m["hd"]), np.float32)
+        sg = None if seg is None else np.ascontiguousarray(seg, np.int32)
+        lib().or_attention_forward(ctypes.byref(self.M), _ptr(q), _ptr(k), _ptr(v), t, _ptr(sg), _ptr(probs), _ptr(o),
+                                   nthreads)
+        return probs, o
+
+    def attention_backward(self, q, k, v, probs, d_o, seg=None, nthreads=16):
+        t = q.shape[0]
+        q, k, v, probs, d_o = (_f32(a) for a in (q, k, v, probs, d_o))
+        dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+        sg = None if seg is None else np.ascontiguousarray(seg, np.int32)
+        lib().or_attention_backward(ctypes.byref(self.M), _ptr(q), _ptr(k), _ptr(v), _ptr(probs), _ptr(d_o), t,
+                                    _ptr(sg), _ptr(dq), _ptr(dk), _ptr(dv), nthreads)
+        return dq, dk, dv
+
+    def swiglu(self, g, u):
+        g, u = _f32(g), _f32(u)
+        hm = np.empty_like(g)
+        lib().or_swiglu(_ptr(g), _ptr(u), g.size, _ptr(hm))
+        return hm
+
+    def swiglu_backward(self, g, u, dhm):
+        g, u, dhm = _f32(g), _f32(u), _f32(dhm)
+        dg, du = np.empty_like(g), np.empty_like(g)
+        lib().or_swiglu_backward(_ptr(g), _ptr(u), _ptr(dhm), g.size, _ptr(dg), _ptr(du))
+        return dg, du

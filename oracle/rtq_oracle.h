@@ -147,18 +147,63 @@ typedef struct {
   or_linear embed, lm_head; /* the same weight twice when tied; no adapters on either */
   const float* out_norm;
   const or_layer* layers;
+  const float* rope_factors; /* per-frequency divisors (rope_freqs.weight), or NULL */
+  int64_t n_factors;
 } or_model;
 
 /* round_f16 (src/attention.rs:34-51) */
 float or_round_f16(float x);
 /* Rope tables for positions 0..t-1 (src/ops.rs:141-167): cos / sin [t x rot/2] */
 void or_rope_table(int64_t t, int64_t rot, float theta, float freq_scale, float* cos_, float* sin_);
+/* Rope::at_positions (src/ops.rs:141-167): tables for tokens at positions[p] (NULL: p), with the
+ * inverse frequency of pair i divided by factors[i] where i < n_factors and factors[i] != 0 */
+void or_rope_table_at(const int32_t* positions, int64_t t, int64_t rot, float theta, float freq_scale,
+                      const float* factors, int64_t n_factors, float* cos_, float* sin_);
+/* Rope::allowed (src/ops.rs:160-167): causal, and within the segment layout (seg NULL: plain) */
+int or_allowed(const int32_t* seg, int64_t i, int64_t j);
+
+/* ---- the block's operations (teacher-forced parity of a device step, op by op) ---- */
+/* rmsnorm_ordered (src/ops.rs:14-36): y, inv [rows]; fused selects x * (inv * w) over (x * inv) * w */
+void or_rmsnorm(const float* x, const float* w, int64_t rows, int64_t d, float eps, float off, int fused, float* y,
+                float* inv);
+/* rmsnorm_backward (src/ops.rs:39-56): dx overwritten */
+void or_rmsnorm_backward(const float* x, const float* w, const float* inv, const float* dy, int64_t rows, int64_t d,
+                         float off, float* dx);
+/* Attention::forward from the raw projections to the rotated heads (src/attention.rs:169-185):
+ * QK-norm (q_norm / k_norm may be NULL), RoPE, f16 rounding of k and v when m->kv_f16.
+ * q_raw [t x nh x hd], k_raw / v_raw [t x nkv x hd]; q_inv [t nh], k_inv [t nkv] (unused without norms) */
+void or_qk_prep(const or_model* m, const float* q_norm, const float* k_norm, const float* cos_, const float* sin_,
+                const float* q_raw, const float* k_raw, const float* v_raw, int64_t t, float* q, float* k, float* v,
+                float* q_inv, float* k_inv);
+/* the backward of or_qk_prep for q and k (src/attention.rs:322-333): inverse RoPE, then the QK-norm
+ * backward; dq / dk are not modified */
+void or_qk_backward(const or_model* m, const float* q_norm, const float* k_norm, const float* cos_, const float* sin_,
+                    const float* q_raw, const float* k_raw, const float* q_inv, const float* k_inv, const float* dq,
+                    const float* dk, int64_t t, float* dq_raw, float* dk_raw);
+/* causal GQA attention over the allowed pairs (src/attention.rs:187-235): probs [nh x t x t] (zero
+ * where not allowed), o [t x nh x hd] */
+void or_attention_forward(const or_model* m, const float* q, const float* k, const float* v, int64_t t,
+                          const int32_t* seg, float* probs, float* o, int nthreads);
+/* its backward (src/attention.rs:262-320): dq [t x nh x hd], dk / dv [t x nkv x hd], overwritten */
+void or_attention_backward(const or_model* m, const float* q, const float* k, const float* v, const float* probs,
+                           const float* d_o, int64_t t, const int32_t* seg, float* dq, float* dk, float* dv,
+                           int nthreads);
+/* SwiGLU (src/model.rs:114-119, :123-128): hm = silu(g) u; dg = dhm u silu'(g), du = dhm silu(g) */
+void or_swiglu(const float* g, const float* u, int64_t n, float* hm);
+void or_swiglu_backward(const float* g, const float* u, const float* dhm, int64_t n, float* dg, float* du);
+
 /* Model::forward_backward (src/model.rs:615-687) on one sequence: logp[n] per target; with wts,
  * the adapters' ga / gb accumulate dL/dA, dL/dB of L = -sum wts[i] logp[i].  Returns -1 on bad
  * shapes or tokens. */
 int or_model_forward_backward(const or_model* m, const int32_t* tokens, int64_t t, const int32_t* pos,
                               const int32_t* tok, const float* wts, int64_t n, float* logp, int64_t* hits,
                               int nthreads);
+/* forward_backward_layout (src/model.rs:644-687) with a packed layout (Model::forward_backward_packed,
+ * :634-642): positions [t] of each token (RoPE) and segments [t] (may-attend rule); either NULL
+ * for the plain sequence. */
+int or_model_forward_backward_layout(const or_model* m, const int32_t* tokens, int64_t t, const int32_t* positions,
+                                     const int32_t* segments, const int32_t* pos, const int32_t* tok,
+                                     const float* wts, int64_t n, float* logp, int64_t* hits, int nthreads);
 #ifdef __cplusplus
 }
 #endif

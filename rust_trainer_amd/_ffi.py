@@ -38,7 +38,8 @@ class RtqModelConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "rope_dim",
                                               "n_ff", "n_vocab")] + \
                [(n, ctypes.c_float) for n in ("rms_eps", "norm_offset", "rope_base", "rope_freq_scale")] + \
-               [(n, ctypes.c_int) for n in ("rope_neox", "qk_norm", "kv_f16", "tied")]
+               [(n, ctypes.c_int) for n in ("rope_neox", "qk_norm", "kv_f16", "tied")] + \
+               [("n_rope_factors", ctypes.c_int64)]
 
 SIGNATURES = {
     "rtq_version": (ctypes.c_char_p, []),
@@ -77,6 +78,7 @@ SIGNATURES = {
     "rtq_lm_head_d": (_i, [_p, _p, _p, _f, _f, _p, _i64, _p, _p, _p, _i64, _p, _p, _p, _p]),
     # device-resident training step
     "rtq_model_from_gguf": (_i, [_p, _p, ctypes.POINTER(_p)]),
+    "rtq_model_config_from_gguf": (_i, [_p, _p]),
     "rtq_model_destroy": (None, [_p]),
     "rtq_model_get_config": (_i, [_p, _p]),
     "rtq_model_attach_lora": (_i, [_p, _i64, _f, ctypes.c_uint32, ctypes.c_uint64, ctypes.POINTER(_i64)]),
@@ -89,6 +91,11 @@ SIGNATURES = {
                                    ctypes.POINTER(_p), ctypes.POINTER(_i64)]),
     "rtq_model_zero_grad": (_i, [_p]),
     "rtq_model_forward_backward": (_i, [_p, _p, _i64, _p, _p, _p, _i64, _p, ctypes.POINTER(_i64)]),
+    "rtq_model_forward_backward_packed": (_i, [_p, _p, _i64, _p, _p, _p, _p, _p, _i64, _p, ctypes.POINTER(_i64)]),
+    "rtq_model_set_checkpointing": (_i, [_p, _i]),
+    "rtq_model_checkpointing": (_i, [_p]),
+    "rtq_model_debug_capture": (_i, [_p, _i64]),
+    "rtq_model_debug_tensor": (_i, [_p, ctypes.c_char_p, _p, _i64]),
     # GGUF v3 container
     "rtq_gguf_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_p)]),
     "rtq_gguf_from_bytes": (_i, [_p, _sz, ctypes.POINTER(_p)]),

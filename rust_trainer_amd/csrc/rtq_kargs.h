@@ -280,6 +280,10 @@ struct MQkArgs {
 // (rounded product a_scale * A first when a_scale != 1), likewise B and C.
 // causal 0: full; 1: only tiles touching n <= m (others skipped); 2: k < min(K, m0 + 64) (A zero
 // above the diagonal); 3: k >= m0 (A(b, m, k) zero for k < m).
+// live (or null): attention layout of a packed batch, one byte per 64 x 64 block of (query i, key
+// j) pairs, nonzero when some pair of the block may attend; nlb blocks per side.  The causal mode
+// names the roles: 1 (m, n) = (i, j), 2 (m, k) = (i, j), 3 (m, k) = (j, i).  Dead output tiles are
+// skipped (not written), dead k slabs are not read.
 struct MGemmArgs {
   const float* A;
   const float* B;
@@ -290,6 +294,8 @@ struct MGemmArgs {
   float a_scale;
   int causal, accumulate;
   int batch;
+  const uint8_t* live;
+  int nlb;
 };
 
 // up to three independent products in one launch of the 32-row-tile kernel: flat workgroup ids
@@ -307,6 +313,12 @@ struct MSoftArgs {
   float* dp;         // backward: dP in, dS = P (dP - sum P dP) scale out (0 for j > i)
   int t, nh;
   float scale;
+  // packed layout (or null): segment of each token (j may be seen by i when seg[j] == 0 or
+  // seg[j] == seg[i]) and the 64 x 64 block liveness map of MGemmArgs; only live blocks are read
+  // and written (0 where a pair may not attend)
+  const int32_t* seg;
+  const uint8_t* live;
+  int nlb;
 };
 
 struct MGroupArgs {

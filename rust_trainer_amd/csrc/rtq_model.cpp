@@ -7,15 +7,22 @@
 //   Model::attach_lora    src/model.rs:406-419, Lora::new src/linear.rs:21-25 (A ~ U(+-1/sqrt(in)), B = 0)
 //   forward_backward      src/model.rs:644-687 (embed, blocks, head, blocks in reverse)
 //   Block / Attention / Mlp src/model.rs:165-197, src/attention.rs:162-367, src/model.rs:113-134
-// The reference recomputes each block's forward in the backward (checkpointing) to save memory;
-// the recomputation reproduces the same values, so here every block's activations are simply kept
-// (config-3 shapes: 60 MB per layer).
+// The reference recomputes each block's forward in the backward (checkpointing, src/model.rs:
+// 663-665, 678-680) to save memory; the recomputation reproduces the same values.  Here the step
+// keeps every block's activations when they fit (config-3 shapes: 60 MB per layer) and recomputes
+// otherwise, or as rtq_model_set_checkpointing forces.
+//
+// Packed batches (Model::forward_backward_packed, src/model.rs:634-642): RoPE tables at the given
+// token positions and the segment may-attend rule (Rope::allowed, src/ops.rs:160-167), applied as a
+// 64 x 64 block liveness map (the attention products skip dead tiles and k slabs) plus the
+// element rule in the softmax kernels.
 //
 // Linears that read the same input and share a ggml type run as one frozen weight: q | k | v
 // (rows concatenated) and gate | up.  Their adapters become one LoRA of rank (members x r) whose B
 // is block-diagonal (zeros elsewhere) and whose alpha is scaled alike, so alpha / rank and every
 // output are unchanged; the gradients of the structurally zero B entries are cleared after each
 // backward.  Each member adapter stays addressable (rtq_model_lora_*), its B as a strided block.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -108,6 +115,19 @@ struct rtq_model {
   size_t hpk_cap = 0;
   float *X = nullptr, *cos_ = nullptr, *sin_ = nullptr;
   std::vector<Cache> cache;
+  int64_t cache_cap = 0;      // Cache sets allocated (n_layer when keeping, 1 when recomputing)
+  int ckpt_mode = -1;         // -1 automatic, 0 keep activations, 1 recompute (rtq_model_set_checkpointing)
+  bool ckpt = false;          // this step recomputes each block's forward in the backward
+  std::vector<float> rope_factors;  // rope_freqs.weight (per-frequency divisors), or empty
+  // packed layout of the current step (null / 0: a plain causal sequence)
+  int32_t* seg_d = nullptr;
+  uint8_t* live_d = nullptr;
+  int64_t nlb = 0;
+  bool packed = false;
+  bool rope_plain = false;  // the uploaded RoPE tables are for positions 0..rope_t-1
+  // rtq_model_debug_capture: one layer's tensors copied during the step
+  int64_t dbg_layer = -1;
+  std::vector<std::pair<std::string, std::pair<float*, int64_t>>> dbg;
   float *dY, *dX, *mo, *f, *dhm, *dgu, *dn2, *dxu, *dh, *d_o, *dP, *dq, *dkh, *dvh, *dk, *dqkv, *dn1, *dxk, *dxv;
   int32_t *tok_d = nullptr, *pos_d = nullptr, *tgt_d = nullptr, *hit_d = nullptr;
   float *wts_d = nullptr, *logp_d = nullptr;
@@ -120,6 +140,16 @@ rtq_status dev_alloc(rtq_model* m, size_t bytes, void** out) {
   M_HIP(hipMalloc(out, bytes ? bytes : 4));
   m->owned.push_back(*out);
   return RTQ_OK;
+}
+
+void dev_free(rtq_model* m, void* p) {
+  if (!p) return;
+  for (size_t i = 0; i < m->owned.size(); i++)
+    if (m->owned[i] == p) {
+      m->owned.erase(m->owned.begin() + (ptrdiff_t)i);
+      (void)hipFree(p);
+      return;
+    }
 }
 
 rtq_status upload_vec(rtq_model* m, const rtq_gguf* g, const std::string& name, int64_t n, const float** out,
@@ -190,10 +220,11 @@ struct Op {  // one GEMM operand: base, batch stride and divisor, row / column s
 };
 
 // C(b, m, n) (+)= sum_k A(b, m, k) B(b, k, n) for b < batch
+// attention products of the step take the packed layout's liveness map (null for a plain sequence)
 rtq_status k_gemm(rtq_model* m, int64_t M, int64_t N, int64_t K, int64_t batch, Op A, Op B, float* C, int64_t sCb,
                   int64_t sCm, int64_t sCn, float a_scale, int causal, int acc) {
   MGemmArgs ga{A.p, B.p, C, (int)M, (int)N, (int)K, A.sb, A.s0, A.s1, B.sb, B.s0, B.s1, sCb, sCm, sCn, A.div, B.div,
-               a_scale, causal, acc, (int)batch};
+               a_scale, causal, acc, (int)batch, causal && m->packed ? m->live_d : nullptr, (int)m->nlb};
   // 64-row tiles when the grid fills the chip twice over, else 32-row tiles (twice the workgroups)
   const int64_t tiles64 = (N + 63) / 64 * ((M + 63) / 64) * batch / (causal == 1 ? 2 : 1);
   const int bm = tiles64 >= 2 * 256 ? 64 : 32;
@@ -219,7 +250,8 @@ rtq_status k_gemm_group(rtq_model* m, const GemmJob* jobs, int n) {
   for (int i = 0; i < n; i++) {
     const GemmJob& j = jobs[i];
     g.p[i] = MGemmArgs{j.A.p, j.B.p, j.C, (int)j.M, (int)j.N, (int)j.K, j.A.sb, j.A.s0, j.A.s1, j.B.sb, j.B.s0,
-                       j.B.s1, j.sCb, j.sCm, j.sCn, j.A.div, j.B.div, j.a_scale, j.causal, j.acc, (int)j.batch};
+                       j.B.s1, j.sCb, j.sCm, j.sCn, j.A.div, j.B.div, j.a_scale, j.causal, j.acc, (int)j.batch,
+                       j.causal && m->packed ? m->live_d : nullptr, (int)m->nlb};
     g.start[i] = (int)total;
     total += (j.N + 63) / 64 * ((j.M + 31) / 32) * j.batch;
   }
@@ -295,70 +327,97 @@ rtq_status ensure_hpk(rtq_model* m, int64_t t) {
   return RTQ_OK;
 }
 
-rtq_status ensure_step(rtq_model* m, int64_t t, int64_t n) {
-  if (t <= m->t_cap && n <= m->n_cap) return RTQ_OK;
-  const rtq_model_config& c = m->cfg;
-  const int64_t T = std::max(t, m->t_cap), N = std::max<int64_t>(std::max(n, m->n_cap), 1);
+// Assigns every step buffer of `dst` for T tokens, N targets and `caches` sets of block activations
+// (n_layer when keeping them, 1 when recomputing) from `base` (0: only counts) and returns the
+// bytes.  Each buffer starts on a 256-byte boundary.
+size_t step_layout(rtq_model* dst, int64_t T, int64_t N, int64_t caches, uintptr_t base) {
+  const rtq_model_config& c = dst->cfg;
   const int64_t d = c.n_embd, qd = c.n_head * c.head_dim, kd = c.n_head_kv * c.head_dim, ff = c.n_ff;
   const int64_t half = c.rope_dim / 2, L = c.n_layer;
-  const int64_t att = c.n_head * T * T, hdh = c.n_head * T * c.head_dim;
-  std::vector<std::pair<float**, int64_t>> f;  // (pointer, floats)
-  f.push_back({&m->X, (L + 1) * T * d});
-  f.push_back({&m->cos_, T * half + 1});
-  f.push_back({&m->sin_, T * half + 1});
-  m->cache.assign((size_t)L, Cache{});
-  for (auto& k : m->cache) {
-    for (auto pr : std::initializer_list<std::pair<float**, int64_t>>{
-             {&k.n1, T * d},   {&k.inv1, T},     {&k.qkv, T * (qd + 2 * kd)},
-             {&k.q, T * qd},   {&k.k, T * kd},   {&k.v, T * kd},     {&k.q_inv, T * c.n_head},
-             {&k.k_inv, T * c.n_head_kv},        {&k.P, att},        {&k.o, T * qd},     {&k.h, T * d},
-             {&k.n2, T * d},   {&k.inv2, T},     {&k.gu, T * 2 * ff}, {&k.hm, T * ff}})
-      f.push_back(pr);
+  const int64_t att = c.n_head * T * T, hdh = c.n_head * T * c.head_dim, nlb = (T + 63) / 64;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const uintptr_t p = base + off;
+    off += (bytes + 255) / 256 * 256;
+    return p;
+  };
+  auto fl = [&](float** p, int64_t floats) { *p = reinterpret_cast<float*>(take((size_t)floats * 4)); };
+  fl(&dst->X, (L + 1) * T * d);
+  fl(&dst->cos_, T * half + 1);
+  fl(&dst->sin_, T * half + 1);
+  dst->cache.assign((size_t)caches, Cache{});
+  for (Cache& k : dst->cache) {
+    fl(&k.n1, T * d), fl(&k.inv1, T), fl(&k.qkv, T * (qd + 2 * kd)), fl(&k.q, T * qd), fl(&k.k, T * kd);
+    fl(&k.v, T * kd), fl(&k.q_inv, T * c.n_head), fl(&k.k_inv, T * c.n_head_kv), fl(&k.P, att), fl(&k.o, T * qd);
+    fl(&k.h, T * d), fl(&k.n2, T * d), fl(&k.inv2, T), fl(&k.gu, T * 2 * ff), fl(&k.hm, T * ff);
   }
-  for (auto pr : std::initializer_list<std::pair<float**, int64_t>>{
-           {&m->dY, T * d},   {&m->dX, T * d},    {&m->mo, T * d},   {&m->f, T * d},      {&m->dhm, T * ff},
-           {&m->dgu, T * 2 * ff},                 {&m->dn2, T * d},  {&m->dxu, T * d},    {&m->dh, T * d},
-           {&m->d_o, T * qd}, {&m->dP, att},      {&m->dq, T * qd},  {&m->dkh, hdh},      {&m->dvh, hdh},
-           {&m->dk, T * kd},  {&m->dqkv, T * (qd + 2 * kd)},     {&m->dn1, T * d},
-           {&m->dxk, T * d},  {&m->dxv, T * d},   {&m->wts_d, N},    {&m->logp_d, N}})
-    f.push_back(pr);
-  size_t bytes = 0;
-  for (auto& pr : f) bytes += ((size_t)pr.second * 4 + 255) / 256 * 256;
-  const size_t ibytes = ((size_t)T * 4 + 255) / 256 * 256 + 3 * (((size_t)N * 4 + 255) / 256 * 256);
+  fl(&dst->dY, T * d), fl(&dst->dX, T * d), fl(&dst->mo, T * d), fl(&dst->f, T * d), fl(&dst->dhm, T * ff);
+  fl(&dst->dgu, T * 2 * ff), fl(&dst->dn2, T * d), fl(&dst->dxu, T * d), fl(&dst->dh, T * d), fl(&dst->d_o, T * qd);
+  fl(&dst->dP, att), fl(&dst->dq, T * qd), fl(&dst->dkh, hdh), fl(&dst->dvh, hdh), fl(&dst->dk, T * kd);
+  fl(&dst->dqkv, T * (qd + 2 * kd)), fl(&dst->dn1, T * d), fl(&dst->dxk, T * d), fl(&dst->dxv, T * d);
+  fl(&dst->wts_d, N), fl(&dst->logp_d, N);
+  dst->tok_d = reinterpret_cast<int32_t*>(take((size_t)T * 4));
+  dst->seg_d = reinterpret_cast<int32_t*>(take((size_t)T * 4));
+  dst->live_d = reinterpret_cast<uint8_t*>(take((size_t)(nlb * nlb)));
+  for (int32_t** q : {&dst->pos_d, &dst->tgt_d, &dst->hit_d}) *q = reinterpret_cast<int32_t*>(take((size_t)N * 4));
+  return off;
+}
+
+// whether a step of t tokens recomputes block activations: as forced, or (automatic) when keeping
+// every layer's activations would take more than half of the device memory free now
+rtq_status choose_ckpt(rtq_model* m, int64_t t, int64_t n) {
+  if (m->ckpt_mode >= 0) {
+    m->ckpt = m->ckpt_mode == 1;
+    return RTQ_OK;
+  }
+  if (m->cfg.n_layer <= 1) {
+    m->ckpt = false;
+    return RTQ_OK;
+  }
+  const int64_t T = std::max(t, m->t_cap), N = std::max<int64_t>(std::max(n, m->n_cap), 1);
+  rtq_model probe;
+  probe.cfg = m->cfg;
+  const size_t keep = step_layout(&probe, T, N, m->cfg.n_layer, 0);
+  size_t free_b = 0, total_b = 0;
+  M_HIP(hipMemGetInfo(&free_b, &total_b));
+  const size_t held = m->step_mem ? step_layout(&probe, m->t_cap, std::max<int64_t>(m->n_cap, 1), m->cache_cap, 0) : 0;
+  m->ckpt = keep > (free_b + held) / 2;
+  return RTQ_OK;
+}
+
+rtq_status ensure_step(rtq_model* m, int64_t t, int64_t n) {
+  const int64_t caches = m->ckpt ? 1 : m->cfg.n_layer;
+  if (t <= m->t_cap && n <= m->n_cap && caches == m->cache_cap) return RTQ_OK;
+  const int64_t T = std::max(t, m->t_cap), N = std::max<int64_t>(std::max(n, m->n_cap), 1);
   if (m->step_mem) {
     M_HIP(hipStreamSynchronize(stream_of(m)));
     M_HIP(hipFree(m->step_mem));
     m->step_mem = nullptr;
   }
-  m->t_cap = m->n_cap = 0;
-  M_HIP(hipMalloc(&m->step_mem, bytes + ibytes));
-  char* p = (char*)m->step_mem;
-  for (auto& pr : f) {
-    *pr.first = (float*)p;
-    p += ((size_t)pr.second * 4 + 255) / 256 * 256;
-  }
-  m->tok_d = (int32_t*)p;
-  p += ((size_t)T * 4 + 255) / 256 * 256;
-  for (int32_t** q : {&m->pos_d, &m->tgt_d, &m->hit_d}) {
-    *q = (int32_t*)p;
-    p += ((size_t)N * 4 + 255) / 256 * 256;
-  }
+  m->t_cap = m->n_cap = m->cache_cap = 0;
+  const size_t bytes = step_layout(m, T, N, caches, 0);
+  M_HIP(hipMalloc(&m->step_mem, bytes));
+  step_layout(m, T, N, caches, reinterpret_cast<uintptr_t>(m->step_mem));
   m->t_cap = T;
   m->n_cap = N;
+  m->cache_cap = caches;
   m->rope_t = -1;
   return RTQ_OK;
 }
 
-// RoPE tables for positions 0..t-1 (Rope::with, src/ops.rs:136-167), computed in f32 on the host
-rtq_status ensure_rope(rtq_model* m, int64_t t) {
-  if (m->rope_t == t) return RTQ_OK;
+// RoPE tables for the tokens' positions (Rope::at_positions, src/ops.rs:141-167; positions null:
+// 0..t-1), computed in f32 on the host: inverse frequencies base^(-2i / rot) * freq_scale, divided
+// by rope_freqs.weight's factor where that is non-zero
+rtq_status ensure_rope(rtq_model* m, int64_t t, const int32_t* positions) {
+  if (!positions && m->rope_plain && m->rope_t == t) return RTQ_OK;
   const rtq_model_config& c = m->cfg;
   const int64_t half = c.rope_dim / 2;
   std::vector<float> cs((size_t)(t * half)), sn((size_t)(t * half));
   for (int64_t i = 0; i < half; i++) {
-    const float fr = powf(c.rope_base, -2.0f * (float)i / (float)c.rope_dim) * c.rope_freq_scale;
+    float fr = powf(c.rope_base, -2.0f * (float)i / (float)c.rope_dim) * c.rope_freq_scale;
+    if (i < (int64_t)m->rope_factors.size() && m->rope_factors[(size_t)i] != 0.0f) fr /= m->rope_factors[(size_t)i];
     for (int64_t p = 0; p < t; p++) {
-      const float a = (float)p * fr;
+      const float a = (float)(positions ? positions[p] : p) * fr;
       cs[(size_t)(p * half + i)] = cosf(a);
       sn[(size_t)(p * half + i)] = sinf(a);
     }
@@ -367,6 +426,50 @@ rtq_status ensure_rope(rtq_model* m, int64_t t) {
   M_HIP(hipMemcpyAsync(m->sin_, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, stream_of(m)));
   M_HIP(hipStreamSynchronize(stream_of(m)));  // the host tables go out of scope
   m->rope_t = t;
+  m->rope_plain = positions == nullptr;
+  return RTQ_OK;
+}
+
+// the packed layout's segments and 64 x 64 block liveness map (a block of (query, key) pairs is
+// live when some pair may attend: the diagonal blocks always, an earlier key block when it holds a
+// shared-prompt token or a segment that the query block holds too)
+rtq_status upload_layout(rtq_model* m, const int32_t* seg, int64_t t) {
+  if (!seg) {
+    m->packed = false;
+    m->nlb = 0;
+    return RTQ_OK;
+  }
+  const int64_t nlb = (t + 63) / 64;
+  std::vector<std::vector<int32_t>> segs((size_t)nlb);
+  std::vector<uint8_t> has0((size_t)nlb, 0), live((size_t)(nlb * nlb), 0);
+  for (int64_t b = 0; b < nlb; b++) {
+    std::vector<int32_t>& v = segs[(size_t)b];
+    for (int64_t j = b * 64; j < std::min(t, b * 64 + 64); j++) {
+      if (seg[j] == 0) has0[(size_t)b] = 1;
+      else v.push_back(seg[j]);
+    }
+    std::sort(v.begin(), v.end());
+    v.erase(std::unique(v.begin(), v.end()), v.end());
+  }
+  for (int64_t a = 0; a < nlb; a++)
+    for (int64_t b = 0; b <= a; b++) {
+      bool lv = a == b || has0[(size_t)b];
+      if (!lv) {
+        const auto &x = segs[(size_t)a], &y = segs[(size_t)b];
+        size_t i = 0, j = 0;
+        while (!lv && i < x.size() && j < y.size()) {
+          if (x[i] == y[j]) lv = true;
+          else if (x[i] < y[j]) i++;
+          else j++;
+        }
+      }
+      live[(size_t)(a * nlb + b)] = lv ? 1 : 0;
+    }
+  M_HIP(hipMemcpyAsync(m->seg_d, seg, (size_t)t * 4, hipMemcpyHostToDevice, stream_of(m)));
+  M_HIP(hipMemcpyAsync(m->live_d, live.data(), live.size(), hipMemcpyHostToDevice, stream_of(m)));
+  M_HIP(hipStreamSynchronize(stream_of(m)));
+  m->packed = true;
+  m->nlb = nlb;
   return RTQ_OK;
 }
 
@@ -404,7 +507,7 @@ void gu_view(const rtq_model* m, const Layer& L, float* base, int64_t t, float**
 rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* y) {
   const rtq_model_config& c = m->cfg;
   const Layer& L = m->layers[(size_t)l];
-  Cache& k = m->cache[(size_t)l];
+  Cache& k = m->cache[m->ckpt ? 0 : (size_t)l];
   const int64_t d = c.n_embd, nh = c.n_head, nkv = c.n_head_kv, hd = c.head_dim, grp = nh / nkv;
   const int64_t qd = nh * hd, kd = nkv * hd;
   M_TRY(k_norm(m, x, nullptr, nullptr, L.attn_norm, k.n1, k.inv1, t, d, 0));
@@ -422,7 +525,8 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* 
   const float scale = 1.0f / sqrtf((float)hd);
   // S = (q scale) K^T per head (causal), softmax in place, O = P V
   M_TRY(k_gemm(m, t, t, hd, nh, Op{k.q, hd, qd, 1, 1}, Op{k.k, hd, 1, kd, (int)grp}, k.P, t * t, t, 1, scale, 1, 0));
-  MSoftArgs sa{k.P, nullptr, nullptr, (int)t, (int)nh, scale};
+  MSoftArgs sa{k.P, nullptr, nullptr, (int)t, (int)nh, scale, m->packed ? m->seg_d : nullptr,
+               m->packed ? m->live_d : nullptr, (int)m->nlb};
   M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX, dim3((unsigned)((t + 3) / 4), (unsigned)nh), dim3(256), stream_of(m),
                          &sa));
   M_TRY(k_gemm(m, t, hd, t, nh, Op{k.P, t * t, t, 1, 1}, Op{k.v, hd, kd, 1, (int)grp}, k.o, hd, qd, 1, 1.0f, 2, 0));
@@ -445,7 +549,7 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* 
 rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const float* dy, float* dx) {
   const rtq_model_config& c = m->cfg;
   const Layer& L = m->layers[(size_t)l];
-  Cache& k = m->cache[(size_t)l];
+  Cache& k = m->cache[m->ckpt ? 0 : (size_t)l];
   const int64_t d = c.n_embd, nh = c.n_head, nkv = c.n_head_kv, hd = c.head_dim, grp = nh / nkv;
   const int64_t qd = nh * hd, kd = nkv * hd;
   const float scale = 1.0f / sqrtf((float)hd);
@@ -468,7 +572,8 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
   M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LO]], k.o, m->dh, t, m->d_o));
   M_TRY(k_gemm(m, t, t, hd, nh, Op{m->d_o, hd, qd, 1, 1}, Op{k.v, hd, 1, kd, (int)grp}, m->dP, t * t, t, 1, 1.0f, 1,
                0));  // dP = dO V^T
-  MSoftArgs sa{nullptr, k.P, m->dP, (int)t, (int)nh, scale};
+  MSoftArgs sa{nullptr, k.P, m->dP, (int)t, (int)nh, scale, m->packed ? m->seg_d : nullptr,
+               m->packed ? m->live_d : nullptr, (int)m->nlb};
   M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX_BWD, dim3((unsigned)((t + 3) / 4), (unsigned)nh), dim3(256),
                          stream_of(m), &sa));
   // dV_h = P^T dO, dQ = dS K, dK_h = dS^T Q: independent, one launch
@@ -492,6 +597,92 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
     M_TRY(k_elt(m, KM_ADD, m->dn1, m->dxk, m->dxv, m->dn1, nullptr, t * d));  // dq + (dk + dv)
   }
   return k_norm_bwd(m, x, L.attn_norm, k.inv1, m->dn1, m->dh, dx, t, d);  // dx = dh + rmsnorm_backward
+}
+
+// ---------------------------------------------------------------- debug capture
+// rtq_model_debug_capture: copies of one layer's tensors taken during the step, in plain row-major
+// layouts (per token: q_raw [qd], k_raw / v_raw [kd], gate / up [ff], ...)
+rtq_status dbg_put(rtq_model* m, const char* name, const float* src, int64_t rows, int64_t cols, int64_t ld) {
+  float* dst = nullptr;
+  for (auto& e : m->dbg)
+    if (e.first == name) {
+      if (e.second.second != rows * cols) {
+        dev_free(m, e.second.first);
+        e.second.first = nullptr;
+      }
+      dst = e.second.first;
+      if (!dst) {
+        void* p;
+        M_TRY(dev_alloc(m, (size_t)(rows * cols) * 4, &p));
+        e.second = {(float*)p, rows * cols};
+        dst = (float*)p;
+      }
+    }
+  if (!dst) {
+    void* p;
+    M_TRY(dev_alloc(m, (size_t)(rows * cols) * 4, &p));
+    m->dbg.push_back({name, {(float*)p, rows * cols}});
+    dst = (float*)p;
+  }
+  M_HIP(hipMemcpy2DAsync(dst, (size_t)cols * 4, src, (size_t)ld * 4, (size_t)cols * 4, (size_t)rows,
+                         hipMemcpyDeviceToDevice, stream_of(m)));
+  return RTQ_OK;
+}
+
+rtq_status dbg_forward(rtq_model* m, int l, int64_t t, const float* x, const float* y) {
+  const rtq_model_config& c = m->cfg;
+  const Layer& L = m->layers[(size_t)l];
+  Cache& k = m->cache[m->ckpt ? 0 : (size_t)l];
+  const int64_t d = c.n_embd, qd = c.n_head * c.head_dim, kd = c.n_head_kv * c.head_dim, ff = c.n_ff;
+  const QkvView qv = qkv_view(m, L, k.qkv, t);
+  float *g, *u;
+  int64_t ldg;
+  gu_view(m, L, k.gu, t, &g, &u, &ldg);
+  M_TRY(dbg_put(m, "x", x, t, d, d));
+  M_TRY(dbg_put(m, "n1", k.n1, t, d, d));
+  M_TRY(dbg_put(m, "inv1", k.inv1, 1, t, t));
+  M_TRY(dbg_put(m, "q_raw", qv.q, t, qd, qv.ldq));
+  M_TRY(dbg_put(m, "k_raw", qv.k, t, kd, qv.ldk));
+  M_TRY(dbg_put(m, "v_raw", qv.v, t, kd, qv.ldv));
+  M_TRY(dbg_put(m, "q", k.q, t, qd, qd));
+  M_TRY(dbg_put(m, "k", k.k, t, kd, kd));
+  M_TRY(dbg_put(m, "v", k.v, t, kd, kd));
+  M_TRY(dbg_put(m, "q_inv", k.q_inv, 1, t * c.n_head, t * c.n_head));
+  M_TRY(dbg_put(m, "k_inv", k.k_inv, 1, t * c.n_head_kv, t * c.n_head_kv));
+  M_TRY(dbg_put(m, "P", k.P, c.n_head * t, t, t));
+  M_TRY(dbg_put(m, "o", k.o, t, qd, qd));
+  M_TRY(dbg_put(m, "h", k.h, t, d, d));
+  M_TRY(dbg_put(m, "n2", k.n2, t, d, d));
+  M_TRY(dbg_put(m, "inv2", k.inv2, 1, t, t));
+  M_TRY(dbg_put(m, "gate", g, t, ff, ldg));
+  M_TRY(dbg_put(m, "up", u, t, ff, ldg));
+  M_TRY(dbg_put(m, "hm", k.hm, t, ff, ff));
+  return dbg_put(m, "y", y, t, d, d);
+}
+
+rtq_status dbg_backward(rtq_model* m, int l, int64_t t, const float* dy, const float* dx) {
+  const rtq_model_config& c = m->cfg;
+  const Layer& L = m->layers[(size_t)l];
+  const int64_t d = c.n_embd, qd = c.n_head * c.head_dim, kd = c.n_head_kv * c.head_dim, ff = c.n_ff;
+  const QkvView dv = qkv_view(m, L, m->dqkv, t);
+  float *dg, *du;
+  int64_t ldg;
+  gu_view(m, L, m->dgu, t, &dg, &du, &ldg);
+  M_TRY(dbg_put(m, "dy", dy, t, d, d));
+  M_TRY(dbg_put(m, "dhm", m->dhm, t, ff, ff));
+  M_TRY(dbg_put(m, "dgate", dg, t, ff, ldg));
+  M_TRY(dbg_put(m, "dup", du, t, ff, ldg));
+  M_TRY(dbg_put(m, "dn2", m->dn2, t, d, d));
+  M_TRY(dbg_put(m, "dh", m->dh, t, d, d));
+  M_TRY(dbg_put(m, "d_o", m->d_o, t, qd, qd));
+  M_TRY(dbg_put(m, "dS", m->dP, c.n_head * t, t, t));
+  M_TRY(dbg_put(m, "dq", m->dq, t, qd, qd));
+  M_TRY(dbg_put(m, "dk", m->dk, t, kd, kd));
+  M_TRY(dbg_put(m, "dv", dv.v, t, kd, dv.ldv));
+  M_TRY(dbg_put(m, "dq_raw", dv.q, t, qd, dv.ldq));
+  M_TRY(dbg_put(m, "dk_raw", dv.k, t, kd, dv.ldk));
+  M_TRY(dbg_put(m, "dn1", m->dn1, t, d, d));
+  return dbg_put(m, "dx", dx, t, d, d);
 }
 
 // the ggml type, packed bytes and shape of a GGUF tensor
@@ -581,16 +772,22 @@ rtq_status load_groups(rtq_model* m, const rtq_gguf* g, const std::string& p, La
 
 extern "C" {
 
-rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out) {
-  if (!ctx || !g || !out) return rtq_fail(RTQ_ERR_INVALID, "null ctx/gguf/out");
-  *out = nullptr;
+}  // extern "C"
+
+namespace {
+// hyper-parameters and the loader's refusals (load_gguf_from, src/rie.rs:164-260), no device work;
+// factors: rope_freqs.weight (or null)
+rtq_status parse_config(const rtq_gguf* g, rtq_model_config* out, std::vector<float>* factors) {
   const char* arch_p = nullptr;
   uint64_t arch_n = 0;
   M_TRY(rtq_gguf_get_str(g, "general.architecture", &arch_p, &arch_n));
   const std::string arch(arch_p, arch_n);
-  rtq_model* m = new rtq_model();
-  m->ctx = ctx;
-  rtq_model_config& c = m->cfg;
+  // trainable_arch (src/rie.rs:153-155, :170-172): the decoders whose forward the step reproduces
+  // (Mistral GGUFs declare "llama")
+  if (arch != "llama" && arch != "qwen2" && arch != "qwen3")
+    return rtq_fail(RTQ_ERR_UNSUPPORTED,
+                    "architecture '%s' is not trainable yet (supported: llama, mistral, qwen2, qwen3)", arch.c_str());
+  rtq_model_config c{};
   c.n_layer = (int64_t)kv_num(g, arch + ".block_count", 0);
   c.n_embd = (int64_t)kv_num(g, arch + ".embedding_length", 0);
   c.n_head = (int64_t)kv_num(g, arch + ".attention.head_count", 0);
@@ -602,28 +799,100 @@ rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out)
   c.rope_base = (float)kv_num(g, arch + ".rope.freq_base", 10000.0);
   c.rope_freq_scale = 1.0f;
   c.norm_offset = 0.0f;
+  // the loader's "plain" model check (src/rie.rs:173-183: embedding / residual / logit scale 1, no
+  // softcaps, no sliding window, attention scale 1/sqrt(head_dim)) and its dense-FFN check
+  // (:211-216), on the GGUF keys that carry those settings
+  auto kv_is = [&](const char* key, double plain) {
+    double v = 0.0;
+    return rtq_gguf_get_f64(g, (arch + key).c_str(), &v) != RTQ_OK || v == plain;
+  };
+  if (!kv_is(".expert_count", 0.0))
+    return rtq_fail(RTQ_ERR_UNSUPPORTED, "mixture-of-experts feed-forward blocks are not trainable yet "
+                                         "(dense models only)");
+  if (!kv_is(".embedding_scale", 1.0) || !kv_is(".residual_scale", 1.0) || !kv_is(".logit_scale", 1.0) ||
+      !kv_is(".attn_logit_softcapping", 0.0) || !kv_is(".final_logit_softcapping", 0.0) ||
+      !kv_is(".attention.sliding_window", 0.0))
+    return rtq_fail(RTQ_ERR_UNSUPPORTED, "%s: unsupported scaling/softcap/sliding-window settings", arch.c_str());
+  // RoPE frequency scaling (rope_freq_scale, src/rie.rs:229; Rope::at_positions src/ops.rs:141-158):
+  // linear scaling divides every frequency by the factor; other scaling types are refused
+  {
+    const char* ty = nullptr;
+    uint64_t tn = 0;
+    std::string type = "none";
+    if (rtq_gguf_get_str(g, (arch + ".rope.scaling.type").c_str(), &ty, &tn) == RTQ_OK) type.assign(ty, tn);
+    const double factor = kv_num(g, arch + ".rope.scaling.factor", 0.0);
+    const double legacy = kv_num(g, arch + ".rope.scale_linear", 0.0);
+    if (type == "linear" && factor > 0.0) c.rope_freq_scale = (float)(1.0 / factor);
+    else if (type == "none" && legacy > 0.0) c.rope_freq_scale = (float)(1.0 / legacy);
+    else if (type != "none" && !(type == "linear" && factor == 0.0))
+      return rtq_fail(RTQ_ERR_UNSUPPORTED, "%s: RoPE scaling '%s' is not supported", arch.c_str(), type.c_str());
+  }
   c.rope_neox = arch != "llama";  // Qwen GGUFs rotate NEOX pairs, Llama GGUFs adjacent pairs
   c.kv_f16 = 1;                   // the loader's AttnConfig { kv_f16: true } (src/rie.rs:201)
   const int64_t te = rtq_gguf_find_tensor(g, "token_embd.weight");
-  rtq_status st = RTQ_OK;
-  auto fail_out = [&](rtq_status s) {
-    rtq_model_destroy(m);
-    return s;
-  };
-  if (te < 0) return fail_out(rtq_fail(RTQ_ERR_INVALID, "GGUF: missing token_embd.weight"));
+  if (te < 0) return rtq_fail(RTQ_ERR_INVALID, "GGUF: missing token_embd.weight");
   {
     int64_t ne[4];
     int nd = 0;
-    if ((st = rtq_gguf_tensor(g, te, nullptr, nullptr, &nd, ne, nullptr, nullptr)) != RTQ_OK) return fail_out(st);
+    M_TRY(rtq_gguf_tensor(g, te, nullptr, nullptr, &nd, ne, nullptr, nullptr));
     c.n_vocab = nd >= 2 ? ne[1] : 0;
   }
   if (c.n_layer <= 0 || c.n_embd <= 0 || c.n_head <= 0 || c.n_head_kv <= 0 || c.n_head % c.n_head_kv ||
       c.head_dim <= 0 || c.head_dim > 512 || c.rope_dim <= 0 || c.rope_dim > c.head_dim || c.rope_dim % 2 ||
       c.n_ff <= 0 || c.n_vocab <= 0)
-    return fail_out(rtq_fail(RTQ_ERR_UNSUPPORTED, "GGUF %s: unsupported or missing model hyper-parameters",
-                             arch.c_str()));
+    return rtq_fail(RTQ_ERR_UNSUPPORTED, "GGUF %s: unsupported or missing model hyper-parameters", arch.c_str());
+  if (!kv_is(".attention.scale", 1.0) &&
+      std::fabs(kv_num(g, arch + ".attention.scale", 0.0) - 1.0 / std::sqrt((double)c.head_dim)) >= 1e-6)
+    return rtq_fail(RTQ_ERR_UNSUPPORTED, "%s: unsupported scaling/softcap/sliding-window settings", arch.c_str());
+  // Llama-3.1-style per-frequency divisors (rope_freqs.weight, Model::rope_factors src/model.rs:477;
+  // applied in Rope::at_positions src/ops.rs:151-156)
+  if (const int64_t rf = rtq_gguf_find_tensor(g, "rope_freqs.weight"); rf >= 0) {
+    int type = 0;
+    const void* data = nullptr;
+    size_t nbytes = 0;
+    M_TRY(rtq_gguf_tensor(g, rf, nullptr, &type, nullptr, nullptr, &data, &nbytes));
+    if (type != RTQ_TYPE_F32 || nbytes % 4 || nbytes / 4 > (size_t)c.rope_dim / 2)
+      return rtq_fail(RTQ_ERR_UNSUPPORTED, "GGUF: rope_freqs.weight must be F32 with at most %lld elements",
+                      (long long)(c.rope_dim / 2));
+    c.n_rope_factors = (int64_t)(nbytes / 4);
+    if (factors) factors->assign((const float*)data, (const float*)data + nbytes / 4);
+  }
   c.qk_norm = rtq_gguf_find_tensor(g, "blk.0.attn_q_norm.weight") >= 0;
   c.tied = rtq_gguf_find_tensor(g, "output.weight") < 0;
+  for (int64_t l = 0; l < c.n_layer; l++) {  // src/rie.rs:204-206
+    const std::string p = "blk." + std::to_string(l) + ".";
+    if (rtq_gguf_find_tensor(g, (p + "post_attention_norm.weight").c_str()) >= 0 ||
+        rtq_gguf_find_tensor(g, (p + "post_ffw_norm.weight").c_str()) >= 0)
+      return rtq_fail(RTQ_ERR_UNSUPPORTED, "post-norm layers are not supported");
+  }
+  *out = c;
+  return RTQ_OK;
+}
+}  // namespace
+
+extern "C" {
+
+rtq_status rtq_model_config_from_gguf(const rtq_gguf* g, rtq_model_config* out) {
+  if (!g || !out) return rtq_fail(RTQ_ERR_INVALID, "null gguf/out");
+  return parse_config(g, out, nullptr);
+}
+
+rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out) {
+  if (!ctx || !g || !out) return rtq_fail(RTQ_ERR_INVALID, "null ctx/gguf/out");
+  *out = nullptr;
+  rtq_model_config cfg{};
+  std::vector<float> factors;
+  M_TRY(parse_config(g, &cfg, &factors));
+  rtq_model* m = new rtq_model();
+  m->ctx = ctx;
+  m->cfg = cfg;
+  m->rope_factors = factors;
+  const rtq_model_config& c = m->cfg;
+  rtq_status st = RTQ_OK;
+  auto fail_out = [&](rtq_status s) {
+    rtq_model_destroy(m);
+    return s;
+  };
   const int64_t d = c.n_embd, qd = c.n_head * c.head_dim, kd = c.n_head_kv * c.head_dim;
   if ((st = load_weight(m, g, "token_embd.weight", c.n_vocab, d, &m->embed)) != RTQ_OK) return fail_out(st);
   if (c.tied) {
@@ -637,9 +906,6 @@ rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out)
   for (int64_t l = 0; l < c.n_layer; l++) {
     Layer& L = m->layers[(size_t)l];
     const std::string p = "blk." + std::to_string(l) + ".";
-    if (rtq_gguf_find_tensor(g, (p + "post_attention_norm.weight").c_str()) >= 0 ||
-        rtq_gguf_find_tensor(g, (p + "post_ffw_norm.weight").c_str()) >= 0)
-      return fail_out(rtq_fail(RTQ_ERR_UNSUPPORTED, "post-norm layers are not supported"));  // src/rie.rs:204-206
     if ((st = upload_vec(m, g, p + "attn_norm.weight", d, &L.attn_norm, true)) != RTQ_OK ||
         (st = upload_vec(m, g, p + "ffn_norm.weight", d, &L.ffn_norm, true)) != RTQ_OK ||
         (st = upload_vec(m, g, p + "attn_q_norm.weight", c.head_dim, &L.q_norm, c.qk_norm)) != RTQ_OK ||
@@ -673,62 +939,101 @@ rtq_status rtq_model_attach_lora(rtq_model* m, int64_t rank, float alpha, uint32
   if (!m || rank <= 0 || rank > 4096) return rtq_fail(RTQ_ERR_INVALID, "bad model/rank");
   M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
   M_HIP(hipStreamSynchronize(stream_of(m)));
+  // the new block layout of each group's adapter (members in linear order, r columns each if
+  // targeted), computed before anything changes; every adapter's dA and dB in one allocation, so
+  // zero_grad is one fill
+  struct Plan {
+    int64_t rank = 0, col0[3] = {}, r[3] = {};
+    void *A = nullptr, *B = nullptr;
+  };
+  std::vector<std::vector<Plan>> plan(m->layers.size());
+  size_t gbytes = 0;
+  for (size_t l = 0; l < m->layers.size(); l++)
+    for (const Group& G : m->layers[l].groups) {
+      Plan p;
+      for (int j = 0; j < G.nm; j++) {
+        p.col0[j] = p.rank;
+        p.r[j] = (target_mask >> G.mem[j].lin & 1u) ? rank : 0;
+        p.rank += p.r[j];
+      }
+      gbytes += ((size_t)(p.rank * G.in) * 4 + 255) / 256 * 256 + ((size_t)(G.rows * p.rank) * 4 + 255) / 256 * 256;
+      plan[l].push_back(p);
+    }
+  // allocate everything first: a failure leaves the previous adapters as they were
+  std::vector<void*> fresh;
+  auto undo = [&](rtq_status st) {
+    for (void* p : fresh) dev_free(m, p);
+    return st;
+  };
+  void* gmem = nullptr;
+  rtq_status st = dev_alloc(m, gbytes, &gmem);
+  if (st != RTQ_OK) return undo(st);
+  fresh.push_back(gmem);
+  for (size_t l = 0; l < m->layers.size(); l++)
+    for (size_t gi = 0; gi < m->layers[l].groups.size(); gi++) {
+      Plan& p = plan[l][gi];
+      const Group& G = m->layers[l].groups[gi];
+      if (p.rank == 0) continue;
+      if ((st = dev_alloc(m, (size_t)(p.rank * G.in) * 4, &p.A)) != RTQ_OK) return undo(st);
+      fresh.push_back(p.A);
+      if ((st = dev_alloc(m, (size_t)(G.rows * p.rank) * 4, &p.B)) != RTQ_OK) return undo(st);
+      fresh.push_back(p.B);
+    }
+  if (hipMemset(gmem, 0, gbytes) != hipSuccess) return undo(rtq_fail(RTQ_ERR_HIP, "hipMemset of adapter gradients"));
+  // A ~ U(+-1/sqrt(in)) drawn linear by linear in the reference's order (Lora::new, src/linear.rs:21-25), B = 0
   Rng rng(seed);
   int64_t n = 0;
-  // block layout of each group's adapter: members in linear order, r columns each if targeted;
-  // every adapter's dA and dB in one allocation, so zero_grad is one fill
-  size_t gbytes = 0;
-  for (Layer& L : m->layers)
-    for (Group& G : L.groups) {
-      G.rank = 0;
-      for (int j = 0; j < G.nm; j++) {
-        Member& mb = G.mem[j];
-        mb.col0 = G.rank;
-        mb.r = (target_mask >> mb.lin & 1u) ? rank : 0;
-        G.rank += mb.r;
-      }
-      gbytes += ((size_t)(G.rank * G.in) * 4 + 255) / 256 * 256 + ((size_t)(G.rows * G.rank) * 4 + 255) / 256 * 256;
-    }
-  void* gmem = nullptr;
-  M_TRY(dev_alloc(m, gbytes, &gmem));
-  M_HIP(hipMemset(gmem, 0, gbytes));
-  m->grads = gmem;
-  m->grad_bytes = gbytes;
-  char* gp = (char*)gmem;
-  for (Layer& L : m->layers) {
+  for (size_t l = 0; l < m->layers.size(); l++) {
+    Layer& L = m->layers[l];
     std::vector<std::vector<float>> ahost(L.groups.size());
-    for (int i = 0; i < NLIN; i++) {  // A drawn linear by linear, in the reference's order
+    for (int i = 0; i < NLIN; i++) {
       if (!(target_mask >> i & 1u)) continue;
-      Group& G = L.groups[(size_t)L.gi[i]];
+      const Group& G = L.groups[(size_t)L.gi[i]];
+      const Plan& p = plan[l][(size_t)L.gi[i]];
       std::vector<float>& a = ahost[(size_t)L.gi[i]];
-      a.resize((size_t)(G.rank * G.in), 0.0f);
-      const Member& mb = G.mem[L.mi[i]];
+      a.resize((size_t)(p.rank * G.in), 0.0f);
       const float bound = 1.0f / sqrtf((float)G.in);
-      for (int64_t e = 0; e < rank * G.in; e++) a[(size_t)(mb.col0 * G.in + e)] = rng.uniform_sym(bound);
-      n += rank * (G.in + mb.rows);
+      for (int64_t e = 0; e < rank * G.in; e++) a[(size_t)(p.col0[L.mi[i]] * G.in + e)] = rng.uniform_sym(bound);
+      n += rank * (G.in + G.mem[L.mi[i]].rows);
     }
     for (size_t gi = 0; gi < L.groups.size(); gi++) {
-      Group& G = L.groups[gi];
-      if (G.rank == 0) continue;
-      const size_t na = (size_t)(G.rank * G.in) * 4, nb = (size_t)(G.rows * G.rank) * 4;
-      void *A, *B;
-      M_TRY(dev_alloc(m, na, &A));
-      M_TRY(dev_alloc(m, nb, &B));
-      void* ga = gp;
-      gp += (na + 255) / 256 * 256;
-      void* gb = gp;
-      gp += (nb + 255) / 256 * 256;
-      M_HIP(hipMemcpy(A, ahost[gi].data(), na, hipMemcpyHostToDevice));
-      M_HIP(hipMemset(B, 0, nb));
-      int members = 0;
-      for (int j = 0; j < G.nm; j++) members += G.mem[j].r > 0;
-      G.alpha = alpha * (float)members;  // alpha / rank unchanged
-      G.A = (float*)A;
-      G.B = (float*)B;
-      G.ga = (float*)ga;
-      G.gb = (float*)gb;
+      const Plan& p = plan[l][gi];
+      const Group& G = L.groups[gi];
+      if (p.rank == 0) continue;
+      if (hipMemcpy(p.A, ahost[gi].data(), (size_t)(p.rank * G.in) * 4, hipMemcpyHostToDevice) != hipSuccess ||
+          hipMemset(p.B, 0, (size_t)(G.rows * p.rank) * 4) != hipSuccess)
+        return undo(rtq_fail(RTQ_ERR_HIP, "adapter upload failed"));
     }
   }
+  // commit: the previous adapters' memory is released, the new layout takes their place
+  dev_free(m, m->grads);
+  char* gp = (char*)gmem;
+  for (size_t l = 0; l < m->layers.size(); l++)
+    for (size_t gi = 0; gi < m->layers[l].groups.size(); gi++) {
+      Group& G = m->layers[l].groups[gi];
+      const Plan& p = plan[l][gi];
+      dev_free(m, G.A);
+      dev_free(m, G.B);
+      G.rank = p.rank;
+      int members = 0;
+      for (int j = 0; j < G.nm; j++) {
+        G.mem[j].col0 = p.col0[j];
+        G.mem[j].r = p.r[j];
+        members += p.r[j] > 0;
+      }
+      G.alpha = alpha * (float)members;  // alpha / rank unchanged
+      G.A = (float*)p.A;
+      G.B = (float*)p.B;
+      G.ga = G.gb = nullptr;
+      if (p.rank == 0) continue;
+      const size_t na = (size_t)(p.rank * G.in) * 4, nb = (size_t)(G.rows * p.rank) * 4;
+      G.ga = (float*)gp;
+      gp += (na + 255) / 256 * 256;
+      G.gb = (float*)gp;
+      gp += (nb + 255) / 256 * 256;
+    }
+  m->grads = gmem;
+  m->grad_bytes = gbytes;
   if (n_params) *n_params = n;
   return RTQ_OK;
 }
@@ -825,9 +1130,13 @@ rtq_status rtq_model_zero_grad(rtq_model* m) {
   return RTQ_OK;
 }
 
-rtq_status rtq_model_forward_backward(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* pos,
-                                      const int32_t* tok, const float* weights, int64_t n, float* logp,
-                                      int64_t* hits) {
+}  // extern "C"
+
+namespace {
+// forward_backward_layout (src/model.rs:644-687): embed, blocks (activations kept, or only the
+// block inputs when recomputing), head, blocks in reverse (recomputing each block's forward first)
+rtq_status step(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* positions, const int32_t* segments,
+                const int32_t* pos, const int32_t* tok, const float* weights, int64_t n, float* logp, int64_t* hits) {
   if (!m || !tokens || t <= 0 || n < 0 || (n > 0 && (!pos || !tok || !logp)))
     return rtq_fail(RTQ_ERR_INVALID, "null model/tokens/targets or empty sequence");
   const rtq_model_config& c = m->cfg;
@@ -838,10 +1147,18 @@ rtq_status rtq_model_forward_backward(rtq_model* m, const int32_t* tokens, int64
   for (int64_t i = 0; i < n; i++)
     if (pos[i] < 0 || pos[i] >= t || tok[i] < 0 || tok[i] >= c.n_vocab)
       return rtq_fail(RTQ_ERR_INVALID, "target %lld out of range", (long long)i);  // src/model.rs:575
+  if (positions)
+    for (int64_t i = 0; i < t; i++)
+      if (positions[i] < 0) return rtq_fail(RTQ_ERR_INVALID, "position %lld is negative", (long long)i);
+  if (segments)
+    for (int64_t i = 0; i < t; i++)
+      if (segments[i] < 0) return rtq_fail(RTQ_ERR_INVALID, "segment %lld is negative", (long long)i);
   M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
+  M_TRY(choose_ckpt(m, t, n));
   M_TRY(ensure_step(m, t, n));
   M_TRY(ensure_hpk(m, t));
-  M_TRY(ensure_rope(m, t));
+  M_TRY(ensure_rope(m, t, positions));
+  M_TRY(upload_layout(m, segments, t));
   hipStream_t st = stream_of(m);
   const int64_t d = c.n_embd;
   M_HIP(hipMemcpyAsync(m->tok_d, tokens, (size_t)t * 4, hipMemcpyHostToDevice, st));
@@ -851,14 +1168,21 @@ rtq_status rtq_model_forward_backward(rtq_model* m, const int32_t* tokens, int64
     if (weights) M_HIP(hipMemcpyAsync(m->wts_d, weights, (size_t)n * 4, hipMemcpyHostToDevice, st));
   }
   M_TRY(rtq_frozen_gather_d(m->ctx, m->embed, m->tok_d, t, m->X, st));  // embed_tokens
-  for (int64_t l = 0; l < c.n_layer; l++) M_TRY(block_forward(m, (int)l, t, m->X + l * t * d, m->X + (l + 1) * t * d));
+  for (int64_t l = 0; l < c.n_layer; l++) {
+    float *x = m->X + l * t * d, *y = m->X + (l + 1) * t * d;
+    M_TRY(block_forward(m, (int)l, t, x, y));
+    if (l == m->dbg_layer) M_TRY(dbg_forward(m, (int)l, t, x, y));
+  }
   if (n > 0) {
     M_TRY(rtq_lm_head_d(m->ctx, m->head, m->out_norm, c.rms_eps, c.norm_offset, m->X + c.n_layer * t * d, t,
                         m->pos_d, m->tgt_d, weights ? m->wts_d : nullptr, n, m->logp_d, m->hit_d,
                         weights ? m->dY : nullptr, st));
     if (weights)
       for (int64_t l = c.n_layer - 1; l >= 0; l--) {
-        M_TRY(block_backward(m, (int)l, t, m->X + l * t * d, m->dY, m->dX));
+        const float* x = m->X + l * t * d;
+        if (m->ckpt) M_TRY(block_forward(m, (int)l, t, x, m->f));  // recompute (output unused: f is scratch)
+        M_TRY(block_backward(m, (int)l, t, x, m->dY, m->dX));
+        if (l == m->dbg_layer) M_TRY(dbg_backward(m, (int)l, t, m->dY, m->dX));
         std::swap(m->dY, m->dX);
       }
     std::vector<int32_t> hv((size_t)n);
@@ -875,6 +1199,55 @@ rtq_status rtq_model_forward_backward(rtq_model* m, const int32_t* tokens, int64
     if (hits) *hits = 0;
   }
   return RTQ_OK;
+}
+}  // namespace
+
+extern "C" {
+
+rtq_status rtq_model_forward_backward(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* pos,
+                                      const int32_t* tok, const float* weights, int64_t n, float* logp,
+                                      int64_t* hits) {
+  return step(m, tokens, t, nullptr, nullptr, pos, tok, weights, n, logp, hits);
+}
+
+rtq_status rtq_model_forward_backward_packed(rtq_model* m, const int32_t* tokens, int64_t t,
+                                             const int32_t* positions, const int32_t* segments, const int32_t* pos,
+                                             const int32_t* tok, const float* weights, int64_t n, float* logp,
+                                             int64_t* hits) {
+  if (!positions || !segments) return rtq_fail(RTQ_ERR_INVALID, "packed step needs positions and segments");
+  return step(m, tokens, t, positions, segments, pos, tok, weights, n, logp, hits);
+}
+
+rtq_status rtq_model_set_checkpointing(rtq_model* m, int mode) {
+  if (!m || mode < -1 || mode > 1) return rtq_fail(RTQ_ERR_INVALID, "bad model/checkpointing mode %d", mode);
+  m->ckpt_mode = mode;
+  return RTQ_OK;
+}
+
+int rtq_model_checkpointing(const rtq_model* m) { return m ? (m->ckpt ? 1 : 0) : -1; }
+
+rtq_status rtq_model_debug_capture(rtq_model* m, int64_t layer) {
+  if (!m || layer < -1 || layer >= m->cfg.n_layer) return rtq_fail(RTQ_ERR_INVALID, "bad model/layer");
+  m->dbg_layer = layer;
+  return RTQ_OK;
+}
+
+rtq_status rtq_model_debug_tensor(rtq_model* m, const char* name, float* out, int64_t nfloats) {
+  if (!m || !name) return rtq_fail(RTQ_ERR_INVALID, "null model/name");
+  for (auto& e : m->dbg)
+    if (e.first == name) {
+      if (!out) return e.second.second > nfloats ? rtq_fail(RTQ_ERR_INVALID, "%s has %lld floats", name,
+                                                            (long long)e.second.second)
+                                                 : RTQ_OK;
+      if (nfloats != e.second.second)
+        return rtq_fail(RTQ_ERR_INVALID, "%s has %lld floats, not %lld", name, (long long)e.second.second,
+                        (long long)nfloats);
+      M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
+      M_HIP(hipStreamSynchronize(stream_of(m)));
+      M_HIP(hipMemcpy(out, e.second.first, (size_t)nfloats * 4, hipMemcpyDeviceToHost));
+      return RTQ_OK;
+    }
+  return rtq_fail(RTQ_ERR_INVALID, "no captured tensor %s", name);
 }
 
 }  // extern "C"

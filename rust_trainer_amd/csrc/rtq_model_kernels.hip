@@ -262,11 +262,22 @@ __device__ __forceinline__ void m_gemm(const MGemmArgs& a, int bx, int by, int b
   __shared__ __attribute__((aligned(16))) float Bs[m_opnd_lds<BN, BK>()];
   const int b = bz, m0 = by * BM, n0 = bx * BN;
   if (a.causal == 1 && n0 > m0 + BM - 1) return;  // every element has n > m
+  if (a.causal == 1 && a.live && !a.live[(m0 >> 6) * a.nlb + (n0 >> 6)]) return;  // no pair may attend
   const float* A = a.A + (int64_t)(b / a.divA) * a.sAb;
   const float* B = a.B + (int64_t)(b / a.divB) * a.sBb;
   int k0 = 0, k1 = a.K;
   if (a.causal == 2) k1 = min(a.K, m0 + BM);
   if (a.causal == 3) k0 = (m0 / BK) * BK;
+  // packed layouts: k slabs (BK <= 64, inside one 64-block) of no live block are skipped
+  const uint8_t* lrow = (a.live && a.causal >= 2) ? a.live + (a.causal == 2 ? (int64_t)(m0 >> 6) * a.nlb : (m0 >> 6))
+                                                  : nullptr;
+  const int lstep = a.causal == 2 ? 1 : a.nlb;
+  auto next_live = [&](int kk) {
+    if (lrow)
+      while (kk < k1 && !lrow[(kk >> 6) * lstep]) kk += BK;
+    return kk;
+  };
+  k0 = next_live(k0);
   const int amode = m_opnd_mode(A, a.sAm, a.sAk, a.sAb, a.M, a.K);
   const int bmode = m_opnd_mode(B, a.sBn, a.sBk, a.sBb, a.N, a.K);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
@@ -281,13 +292,14 @@ __device__ __forceinline__ void m_gemm(const MGemmArgs& a, int bx, int by, int b
     m_opnd_load<BM, BK>(A, a.sAm, a.sAk, a.M, m0, k0, k1, amode, a.a_scale, ra);
     m_opnd_load<BN, BK>(B, a.sBn, a.sBk, a.N, n0, k0, k1, bmode, 1.0f, rb);
   }
-  for (int kk = k0; kk < k1; kk += BK) {
+  for (int kk = k0; kk < k1;) {
     m_opnd_store<BM, BK>(As, amode, ra);
     m_opnd_store<BN, BK>(Bs, bmode, rb);
     __syncthreads();
-    if (kk + BK < k1) {
-      m_opnd_load<BM, BK>(A, a.sAm, a.sAk, a.M, m0, kk + BK, k1, amode, a.a_scale, ra);
-      m_opnd_load<BN, BK>(B, a.sBn, a.sBk, a.N, n0, kk + BK, k1, bmode, 1.0f, rb);
+    const int kn = next_live(kk + BK);
+    if (kn < k1) {
+      m_opnd_load<BM, BK>(A, a.sAm, a.sAk, a.M, m0, kn, k1, amode, a.a_scale, ra);
+      m_opnd_load<BN, BK>(B, a.sBn, a.sBk, a.N, n0, kn, k1, bmode, 1.0f, rb);
     }
 #pragma unroll
     for (int kb = 0; kb < BK / 16; kb++) {
@@ -304,6 +316,7 @@ __device__ __forceinline__ void m_gemm(const MGemmArgs& a, int bx, int by, int b
           for (int j = 0; j < 2; j++) acc[i][j] = mfma_f32(af[i][q], bf[j][q], acc[i][j]);
     }
     __syncthreads();
+    kk = kn;
   }
   float* C = a.C + (int64_t)b * a.sCb;
 #pragma unroll
@@ -361,12 +374,42 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32g(MGemmGroupArgs g
 
 // ------------------------------------------------------------------ attention softmax
 // grid (ceil(t / 4), nh), 256 threads: one wave per row i of head h (wave reductions, no barriers),
-// over j <= i: p = exp(s - max) / sum (0 for j > i)
+// over j <= i: p = exp(s - max) / sum (0 for j > i).  Packed layouts (a.live): only the row's live
+// 64-blocks are visited, one element per lane, and only pairs that may attend enter the max and the
+// sum (their p is 0).
+__device__ __forceinline__ bool m_may_attend(const MSoftArgs& a, int si, int i, int j) {
+  return j <= i && j < a.t && (a.seg[j] == 0 || a.seg[j] == si);
+}
+
 extern "C" __global__ __launch_bounds__(256) void rtq_m_softmax(MSoftArgs a) {
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6), h = blockIdx.y, lane = threadIdx.x & 63;
   if (i >= a.t) return;  // whole wave
   float* row = a.s + ((int64_t)h * a.t + i) * a.t;
   float m = -__builtin_inff();
+  if (a.live) {
+    const uint8_t* lr = a.live + (int64_t)(i >> 6) * a.nlb;
+    const int si = a.seg[i];
+    for (int jb = 0; jb <= (i >> 6); jb++) {
+      if (!lr[jb]) continue;
+      const int j = jb * 64 + lane;
+      if (m_may_attend(a, si, i, j)) m = fmaxf(m, row[j]);
+    }
+    m = wave_max(m);
+    float s = 0.0f;
+    for (int jb = 0; jb <= (i >> 6); jb++) {
+      if (!lr[jb]) continue;
+      const int j = jb * 64 + lane;
+      if (m_may_attend(a, si, i, j)) s = s + expf(row[j] - m);
+    }
+    s = wave_sum(s);
+    const float inv = __fdiv_rn(1.0f, s);
+    for (int jb = 0; jb < a.nlb; jb++) {
+      if (!lr[jb]) continue;
+      const int j = jb * 64 + lane;
+      if (j < a.t) row[j] = m_may_attend(a, si, i, j) ? expf(row[j] - m) * inv : 0.0f;
+    }
+    return;
+  }
   for (int j = lane; j <= i; j += 64) m = fmaxf(m, row[j]);
   m = wave_max(m);
   float s = 0.0f;
@@ -377,13 +420,29 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_softmax(MSoftArgs a) {
 }
 
 // grid (ceil(t / 4), nh), one wave per row: dS = (P (dP - sum_j P dP)) scale over j <= i, 0 beyond,
-// written over dP
+// written over dP (packed layouts: over the row's live blocks, 0 where a pair may not attend)
 extern "C" __global__ __launch_bounds__(256) void rtq_m_softmax_bwd(MSoftArgs a) {
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6), h = blockIdx.y, lane = threadIdx.x & 63;
   if (i >= a.t) return;
   const float* p = a.p + ((int64_t)h * a.t + i) * a.t;
   float* dp = a.dp + ((int64_t)h * a.t + i) * a.t;
   float s = 0.0f;
+  if (a.live) {
+    const uint8_t* lr = a.live + (int64_t)(i >> 6) * a.nlb;
+    const int si = a.seg[i];
+    for (int jb = 0; jb <= (i >> 6); jb++) {
+      if (!lr[jb]) continue;
+      const int j = jb * 64 + lane;
+      if (m_may_attend(a, si, i, j)) s = s + p[j] * dp[j];
+    }
+    s = wave_sum(s);
+    for (int jb = 0; jb < a.nlb; jb++) {
+      if (!lr[jb]) continue;
+      const int j = jb * 64 + lane;
+      if (j < a.t) dp[j] = m_may_attend(a, si, i, j) ? (p[j] * (dp[j] - s)) * a.scale : 0.0f;
+    }
+    return;
+  }
   for (int j = lane; j <= i; j += 64) s = s + p[j] * dp[j];
   s = wave_sum(s);
   for (int j = lane; j < a.t; j += 64) dp[j] = j <= i ? (p[j] * (dp[j] - s)) * a.scale : 0.0f;

@@ -20,6 +20,14 @@ GGUF_LINEARS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up
 DEFAULT_TARGETS = LINEARS  # src/model.rs:321-322 (the DeltaNet projections do not occur in GGUF models)
 
 
+def model_config(file) -> dict:
+    """The hyper-parameters ``GpuModel.from_gguf`` would load from ``file`` (an open
+    ``gguf.GgufFile``), with the same refusals (``RtqError``), without a device."""
+    c = _ffi.RtqModelConfig()
+    _ffi.check(_ffi.lib().rtq_model_config_from_gguf(file.handle, ctypes.byref(c)), "rtq_model_config_from_gguf")
+    return {n: getattr(c, n) for n, _ in c._fields_}
+
+
 def _target_mask(targets) -> int:
     mask = 0
     for t in targets:
@@ -120,7 +128,53 @@ class GpuModel:
                                                          tok.ctypes.data, None if w is None else w.ctypes.data,
                                                          pos.size, logp.ctypes.data, ctypes.byref(hits)),
                    "rtq_model_forward_backward")
+        self._stepped = True
         return logp, int(hits.value)
+
+    def forward_backward_packed(self, packed, targets, weights=None) -> tuple[np.ndarray, int]:
+        """``Model::forward_backward_packed`` (src/model.rs:634-642) over a ``packing.Packed`` batch:
+        RoPE at each token's own position, attention within the segment layout; ``targets`` index
+        ``packed.tokens`` (``Packed.map_targets``)."""
+        toks = np.ascontiguousarray(packed.tokens, dtype=np.int32).reshape(-1)
+        ps = np.ascontiguousarray(packed.positions, dtype=np.int32).reshape(-1)
+        sg = np.ascontiguousarray(packed.segments, dtype=np.int32).reshape(-1)
+        assert ps.size == toks.size and sg.size == toks.size, "one position and segment per token"
+        pos = np.array([t.pos for t in targets], dtype=np.int32)
+        tok = np.array([t.token for t in targets], dtype=np.int32)
+        w = None if weights is None else np.ascontiguousarray(weights, dtype=np.float32)
+        if w is not None:
+            assert w.size == pos.size, "one weight per target"
+        logp = np.empty(pos.size, dtype=np.float32)
+        hits = ctypes.c_int64()
+        _ffi.check(_ffi.lib().rtq_model_forward_backward_packed(
+            self._h, toks.ctypes.data, toks.size, ps.ctypes.data, sg.ctypes.data, pos.ctypes.data, tok.ctypes.data,
+            None if w is None else w.ctypes.data, pos.size, logp.ctypes.data, ctypes.byref(hits)),
+            "rtq_model_forward_backward_packed")
+        self._stepped = True
+        return logp, int(hits.value)
+
+    @property
+    def checkpointing(self):
+        """``Model::checkpointing``: True recomputes each block's forward in the backward, False keeps
+        every block's activations, None (default) decides per step by memory.  Reading it gives the
+        last step's choice (None before any step)."""
+        v = int(_ffi.lib().rtq_model_checkpointing(self._h))
+        return None if not getattr(self, "_stepped", False) else bool(v)
+
+    @checkpointing.setter
+    def checkpointing(self, on) -> None:
+        mode = -1 if on is None else (1 if on else 0)
+        _ffi.check(_ffi.lib().rtq_model_set_checkpointing(self._h, mode), "rtq_model_set_checkpointing")
+
+    def debug_capture(self, layer: int) -> None:
+        """Copy block ``layer``'s tensors during each step (-1: off); read them with ``debug_tensor``."""
+        _ffi.check(_ffi.lib().rtq_model_debug_capture(self._h, layer), "rtq_model_debug_capture")
+
+    def debug_tensor(self, name: str, shape) -> np.ndarray:
+        out = np.empty(shape, np.float32)
+        _ffi.check(_ffi.lib().rtq_model_debug_tensor(self._h, name.encode(), out.ctypes.data, out.size),
+                   "rtq_model_debug_tensor")
+        return out
 
     def score(self, tokens, targets) -> tuple[np.ndarray, int]:
         """``Model::score`` (src/model.rs:553-557): log-probs and hits, no backward."""
