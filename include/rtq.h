@@ -117,6 +117,17 @@ rtq_status rtq_linear_forward_d(rtq_ctx* ctx, const rtq_weight* w, const float* 
 rtq_status rtq_linear_backward_d(rtq_ctx* ctx, const rtq_weight* w, const rtq_lora* lora, const float* x,
                                  const float* dy, int64_t t, float* dx, float* ga, float* gb, void* stream);
 
+/* rtq_linear_forward_d that allocates nothing.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Its workspace is a 64 MiB device array of the library, one per GPU, held
+ * from the first context on that GPU until the process ends; a call whose workspace would exceed it
+ * fails with RTQ_ERR_INVALID before launching anything (config 1, 256 tokens over 3072 x 1024, needs
+ * 0.8 MiB; 2048 tokens over K = 4096 about 19 MiB).  Every call on one GPU shares that array, so
+ * calls that overlap on one GPU (other streams, other contexts, other threads) race; calls on one
+ * stream do not.  GGUF block weights only (F32 / TQ8_0: RTQ_ERR_UNSUPPORTED). */
+rtq_status rtq_linear_forward_noalloc_d(rtq_ctx* ctx, const rtq_weight* w, const float* bias, const rtq_lora* lora,
+                                        const float* x, int64_t t, float* y, void* stream);
+
 /* ---- embedding gather and LM head + cross-entropy ---- */
 /* embed_tokens (src/model.rs:446-454): out[i x in] = row(ids[i]).  Host version: ids out of range are
  * rejected (the reference asserts, :450); device version: such rows come out NaN, nothing is read. */

@@ -77,6 +77,7 @@ SIGNATURES = {
     "rtq_lm_head": (_i, [_p, _p, _p, _f, _f, _p, _i64, _p, _p, _p, _i64, _p, ctypes.POINTER(_i64), _p]),
     "rtq_lm_head_d": (_i, [_p, _p, _p, _f, _f, _p, _i64, _p, _p, _p, _i64, _p, _p, _p, _p]),
     # device-resident training step
+    "rtq_linear_forward_noalloc_d": (_i, [_p, _p, _p, _LP, _p, _i64, _p, _p]),
     "rtq_model_from_gguf": (_i, [_p, _p, ctypes.POINTER(_p)]),
     "rtq_model_config_from_gguf": (_i, [_p, _p]),
     "rtq_model_destroy": (None, [_p]),

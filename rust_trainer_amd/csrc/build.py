@@ -2,7 +2,8 @@
 
 1. ``rtq_kernels.hip`` -> gfx950 code object (``hipcc --genco``), into ``rust_trainer_amd/_build/``;
 2. ``rtq_runtime.cpp`` + ``rtq_gguf.cpp`` + ``rtq_model.cpp`` -> ``rust_trainer_amd/librtq.so`` (g++ against the HIP runtime), with the
-   code object embedded (``.incbin``) and loaded at run time with ``hipModuleLoadData``;
+   code object embedded (``.incbin``) and loaded at run time with ``hipModuleLoadData``, plus
+   ``rtq_noalloc.hip`` compiled by hipcc (its device array is registered with the HIP runtime);
 3. ``oracle/`` -> ``oracle/liboracle.so`` (test infrastructure, plain gcc).
 
 Everything is built in-tree so the shared objects travel with the repository snapshot.
@@ -51,7 +52,19 @@ def build_kernels() -> str:
     return out
 
 
-def build_runtime(hsaco: str) -> str:
+def build_noalloc() -> str:
+    """rtq_noalloc.hip (host + gfx950 device code: the no-allocation entry point's scratch array)
+    -> an object linked into librtq.so"""
+    os.makedirs(BUILD, exist_ok=True)
+    out = os.path.join(BUILD, "rtq_noalloc.o")
+    tmp = out + ".tmp.o"
+    _run([os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, "-fPIC", "-c", "-I", os.path.join(ROOT, "include"),
+          "-I", CSRC, os.path.join(CSRC, "rtq_noalloc.hip"), "-o", tmp])
+    os.replace(tmp, out)
+    return out
+
+
+def build_runtime(hsaco: str, noalloc_obj: str) -> str:
     out = os.path.join(PKG, "librtq.so")
     tmp = out + ".tmp"
     cxx = shutil.which("g++") or "g++"
@@ -59,7 +72,7 @@ def build_runtime(hsaco: str) -> str:
           "-D__HIP_PLATFORM_AMD__", f'-DRTQ_HSACO_PATH="{hsaco}"',
           "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"), "-I", CSRC,
           os.path.join(CSRC, "rtq_runtime.cpp"), os.path.join(CSRC, "rtq_gguf.cpp"),
-          os.path.join(CSRC, "rtq_model.cpp"), "-o", tmp,
+          os.path.join(CSRC, "rtq_model.cpp"), noalloc_obj, "-o", tmp,
           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-lrocblas", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"])
     os.replace(tmp, out)
     return out
@@ -71,7 +84,7 @@ def build_oracle() -> None:
 
 def build() -> None:
     hsaco = build_kernels()
-    build_runtime(hsaco)
+    build_runtime(hsaco, build_noalloc())
     build_oracle()
 
 

@@ -45,4 +45,11 @@ rtq_status rtq_linear_forward_keep_d(rtq_ctx* c, const rtq_weight* w, const floa
 rtq_status rtq_linear_backward_blocks_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const RankBlocks* rb,
                                         const float* x, const float* dy, int64_t t, float* dx, float* ga, float* gb,
                                         const float* hp_have, void* stream);
+// rtq_noalloc.hip: resolves the no-allocation scratch array's address on `device` (current)
+rtq_status rtq_scratch_setup(int device);
+// rtq_linear_forward_d with the caller's workspace ws (ws_bytes) instead of the context's: never
+// allocates; a forward needing more than ws_bytes fails with RTQ_ERR_INVALID before any launch.
+// Trainer-native weights (F32, TQ8_0) are refused (RTQ_ERR_UNSUPPORTED).
+rtq_status rtq_linear_forward_ws_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
+                                   const float* x, int64_t t, float* y, void* stream, void* ws, size_t ws_bytes);
 #endif

@@ -893,6 +893,11 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
       return fail(RTQ_ERR_NO_DEVICE, "kernel %s missing from code object: %s", kKernelNames[k], hipGetErrorString(e));
     }
   }
+  if (const rtq_status st = rtq_scratch_setup(device); st != RTQ_OK) {  // rtq_linear_forward_noalloc_d's array
+    (void)hipModuleUnload(c->mod);
+    delete c;
+    return st;
+  }
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);  // default priority
   if (e != hipSuccess) {
     rtq_ctx_destroy(c);
@@ -1601,6 +1606,28 @@ rtq_status rtq_linear_forward_keep_d(rtq_ctx* c, const rtq_weight* w, const floa
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   return enqueue_forward(c, w, x, t, y, bias, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, nullptr, ar, st,
                          hp_keep);
+}
+
+rtq_status rtq_linear_forward_ws_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
+                                   const float* x, int64_t t, float* y, void* stream, void* ws, size_t ws_bytes) {
+  RTQ_TRY(check_weight(c, w));
+  RTQ_TRY(check_t(t));
+  bool on;
+  int64_t r;
+  float s;
+  RTQ_TRY(check_lora(lora, &on, &r, &s));
+  if (t > 0 && (!x || !y)) return fail(RTQ_ERR_INVALID, "null x/y");
+  if (is_dense(w->type))
+    return fail(RTQ_ERR_UNSUPPORTED, "the no-allocation forward serves GGUF block weights (Q4_0, Q8_0, Q4_K, Q6_K)");
+  const size_t need = fwd_ws_bytes(fwd_plan(w, t, on ? r : 0));
+  if (need > ws_bytes)
+    return fail(RTQ_ERR_INVALID, "forward of %lld tokens over %lldx%lld needs %zu bytes of scratch; the maximum is %zu",
+                (long long)t, (long long)w->rows, (long long)w->cols, need, ws_bytes);
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  Arena ar{(char*)ws, ws_bytes, 0};
+  return enqueue_forward(c, w, x, t, y, bias, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, nullptr, ar,
+                         (hipStream_t)stream);
 }
 
 rtq_status rtq_linear_backward_blocks_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const RankBlocks* rb,
