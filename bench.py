@@ -44,6 +44,12 @@ two configs[2] training steps; ``--traffic-report F W --traffic-step`` writes
 151936 x 1024, 512 positions, loss on the last 256) through ``rtq_lm_head_d``, one JSON line with
 the per-call time, per-kernel times, the softmax kernels' HBM fraction and the CPU oracle's rate.
 
+``--config 3`` / ``--config 4`` measure BASELINE configs[3] (Qwen3-4B-shaped Q4_K/Q6_K model, a
+packed batch of 8 x 1024 tokens sharing a 200-token prefix) and configs[4] (Llama-3-8B-shaped Q8_0
+model, 2048 tokens, LoRA r=64, activations recomputed): one JSON line each with tokens/s, the
+per-kernel breakdown and the dominant quantised-matmul kernel's roofline (work recorded by the
+runtime per launch).  Their weights are drawn from numpy's PCG64 in parallel worker processes.
+
 ``--gguf-load PRESET[:WTYPE]`` builds a synthetic GGUF model (``SyntheticSpec``), writes it to a
 temporary file, maps and parses it and uploads every frozen tensor to the GPU, and prints one JSON
 line with the load throughput (frozen-tensor bytes over map + parse + upload time).
@@ -668,6 +674,137 @@ def step_line(args) -> dict:
     return line
 
 
+# ---------------------------------------------------------------- configs[3] and configs[4]
+def config_workload(idx: int):
+    """(spec, description, build_batch) of BASELINE.json configs[3] / configs[4]; build_batch(model)
+    returns (one step's callable, sequence tokens per step, extra config fields)."""
+    import numpy as np
+
+    import rust_trainer_amd as rt
+    from rust_trainer_amd import gguf as G, synth
+    from rust_trainer_amd.packing import answer_targets, pack
+
+    if idx == 3:
+        spec = G.SyntheticSpec.preset("qwen3-4b", G.GGML_Q4_K)
+        desc = ("configs[3]: Qwen3-4B-shaped synthetic GGUF (36 layers, hidden 2560, FFN 9728, 32/8 heads of 128, "
+                "QK-norm, NEOX RoPE 1e6, vocab 151936 tied), Q4_K attention/gate/up, Q6_K down and embedding/output, "
+                "LoRA r=16 alpha=32 on every projection; 8 sequences x 1024 random tokens sharing a 200-token prefix, "
+                "packed (shared prompt computed once, 6792 tokens), answer-token loss on the final 300 positions of "
+                "each sequence")
+        rank, alpha = 16, 32.0
+
+        def batch(model):
+            V = model.config["n_vocab"]
+            r = synth.Rng(11).next_u64(200 + 8 * 824) % np.uint64(V)
+            prefix = [int(v) for v in r[:200]]
+            seqs = [prefix + [int(v) for v in r[200 + 824 * k: 200 + 824 * (k + 1)]] for k in range(8)]
+            p = pack(seqs)
+            targets = []
+            for k, sq in enumerate(seqs):
+                targets += p.map_targets(k, answer_targets(sq, 1024 - 300))
+            wts = np.full(len(targets), 1.0 / len(targets), np.float32)
+
+            def step():
+                model.zero_grad()
+                return model.forward_backward_packed(p, targets, wts)[0]
+
+            return step, 8 * 1024, {"packed_tokens": len(p.tokens), "sequences": 8, "targets": len(targets),
+                                    "rank": rank}
+    elif idx == 4:
+        spec = G.SyntheticSpec.preset("llama3-8b", G.GGML_Q8_0)
+        desc = ("configs[4]: Llama-3-8B-shaped synthetic GGUF (32 layers, hidden 4096, FFN 14336, 32/8 heads of 128, "
+                "adjacent-pair RoPE 5e5, vocab 128256 untied), every linear Q8_0, LoRA r=64 alpha=128 on every "
+                "projection; 2048 random tokens, activations recomputed in the backward (checkpointing), loss on "
+                "the last 1024 positions")
+        rank, alpha = 64, 128.0
+
+        def batch(model):
+            V = model.config["n_vocab"]
+            tokens = (synth.Rng(7).next_u64(2048) % np.uint64(V)).astype(np.int32)
+            targets = rt.answer_targets(tokens, 2048 - 1024)
+            wts = np.full(len(targets), 1.0 / len(targets), np.float32)
+            model.checkpointing = True
+
+            def step():
+                model.zero_grad()
+                return model.forward_backward(tokens, targets, wts)[0]
+
+            return step, 2048, {"tokens": 2048, "targets": len(targets), "rank": rank, "checkpointing": True}
+    else:
+        raise SystemExit(f"--config {idx}: use 3 or 4 (configs[0] is --linear, configs[1] --sweep, configs[2] the "
+                         f"default line)")
+    spec.fast = True
+    return spec, desc, rank, alpha, batch
+
+
+def config_bench(idx: int, steps: int, warmup: int) -> dict:
+    """One JSON line for configs[3] / configs[4]: tokens/s of the whole training step (sequence
+    tokens / step time), per-kernel event times, the dominant quantised-matmul kernel's roofline from
+    the algorithmic work the runtime records per launch."""
+    import numpy as np
+    import torch
+
+    import rust_trainer_amd as rt
+    from rust_trainer_amd import gguf as G
+
+    spec, desc, rank, alpha, batch = config_workload(idx)
+    t0 = time.perf_counter()
+    workers = max(1, min(16, os.cpu_count() or 1))
+    image = spec.build(workers=workers)
+    print(f"[config {idx}] built the synthetic GGUF ({len(image) / 1e9:.2f} GB) in {time.perf_counter() - t0:.1f} s "
+          f"with {workers} workers", file=sys.stderr, flush=True)
+    g = G.GgufFile.from_bytes(image)
+    ctx = rt.Context(0)
+    t0 = time.perf_counter()
+    model = rt.GpuModel.from_gguf(g, ctx=ctx)
+    print(f"[config {idx}] loaded in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    n_params = model.attach_lora(rank, alpha, seed=1)
+    step, seq_tokens, extra = batch(model)
+    for i in range(warmup):
+        step()
+        print(f"[config {idx}] warmup step {i + 1} done", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    ctx.set_timing(True)
+    ctx.reset_timing()
+    step()
+    per = ctx.timing()
+    work = ctx.timing_work()
+    ctx.set_timing(False)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        lp = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    total_k = sum(m for _, m in per.values())
+    qmm = {k: v for k, v in per.items() if k in work}
+    dom = max(qmm, key=lambda k: qmm[k][1]) if qmm else None
+    roof = None
+    if dom:
+        cnt, kms = per[dom]
+        fl, by = work[dom]
+        roof = call_roofline(by / cnt, fl / cnt, kms * 1e-3 / cnt)
+        roof.update({"kernel": dom, "launches": cnt, "avg_us": round(kms * 1e3 / cnt, 3),
+                     "algorithmic_bytes": int(by / cnt), "flops": int(fl / cnt), "traffic": None,
+                     "timing": "HIP events on the launch stream (a few us above kernel-trace durations)"})
+    linear_fl = sum(f for f, _ in work.values())
+    linear_ms = sum(per[k][1] for k in work)
+    return {
+        "metric": f"trained tokens/s fwd+bwd, BASELINE configs[{idx}]", "value": round(seq_tokens / (ms * 1e-3), 1),
+        "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 x int4/int6/int8 block dots -> f32 (frozen forward); bf16x3 -> f32 (frozen dx); f32 (LoRA, "
+                 "norms, attention on f32 MFMA)",
+        "data": "synthetic (weights N(0, 0.02) from numpy PCG64, quantised with the synthetic encoders)",
+        "config": dict({"workload": desc, "lora_params": n_params}, **extra),
+        "mean_loss": float(-lp.mean()),
+        "roofline": roof,
+        "frozen_linear_kernels": {"tflops_achieved": round(linear_fl / (linear_ms * 1e-3) / 1e12, 2),
+                                  "share_of_kernel_time": round(linear_ms / total_k, 4)},
+        "kernels": {k: {"launches": c, "total_us": round(m * 1e3, 1), "share": round(m / total_k, 4)}
+                    for k, (c, m) in sorted(per.items(), key=lambda kv: -kv[1][1])[:24]},
+    }
+
+
 def model_cpu_baseline(spec, seconds: float) -> dict:
     """The oracle's training step (C restatement of Model::forward_backward) on the host cores, on a
     bounded sample: the same model cut to 2 of its 28 blocks (same shapes, same head), timed, and
@@ -777,14 +914,18 @@ def main() -> int:
     ap.add_argument("--head", action="store_true", help="configs[2] LM head + cross-entropy (Model::head)")
     ap.add_argument("--model", action="store_true", help="configs[2] step details only (no contract fields)")
     ap.add_argument("--linear", action="store_true", help="configs[0]: one frozen linear, forward + backward")
+    ap.add_argument("--config", type=int, default=None, metavar="I",
+                    help="BASELINE.json configs[I] for I = 3 (Qwen3-4B packed) or 4 (Llama-3-8B, recomputed): one "
+                         "JSON line (configs[0] is --linear, configs[1] --sweep, configs[2] the default line)")
     ap.add_argument("--gguf-load", default=None, metavar="PRESET[:WTYPE]",
                     help="GGUF load throughput of a synthetic model, e.g. qwen3-0.6b:Q4_0")
     args = ap.parse_args()
     linear_mode = args.linear or args.traffic or args.sweep or bool(args.case) or args.head
+    big = args.config in (3, 4)
     if args.steps is None:
-        args.steps = 200 if linear_mode else 20
+        args.steps = 200 if linear_mode else (3 if big else 20)
     if args.warmup is None:
-        args.warmup = 20 if linear_mode else 3
+        args.warmup = 20 if linear_mode else (1 if big else 3)
     if args.traffic_report:
         traffic_report(*args.traffic_report, step=args.traffic_step)
         return 0
@@ -801,6 +942,12 @@ def main() -> int:
         return 0
     if args.gguf_load:
         gguf_load(args.gguf_load)
+        return 0
+    if args.config is not None:
+        if args.config == 2:
+            print(json.dumps(step_line(args)), flush=True)
+        else:
+            print(json.dumps(config_bench(args.config, args.steps, args.warmup)), flush=True)
         return 0
     if args.head:
         head_bench(args.steps, args.warmup, args.cpu_seconds, args.no_cpu)

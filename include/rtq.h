@@ -77,6 +77,10 @@ rtq_status rtq_ctx_set_timing(rtq_ctx* ctx, int enable, const char* only_kernel)
 /* Synchronises, folds the recorded events into per-kernel totals, returns the number of kernels seen. */
 int rtq_ctx_timing_count(rtq_ctx* ctx);
 rtq_status rtq_ctx_timing_get(rtq_ctx* ctx, int i, const char** name, int64_t* launches, double* total_ms);
+/* the algorithmic work of kernel i's timed launches (frozen-linear GEMM / GEMV and dx kernels; 0
+ * for others): flops 2 T N K (+ the LoRA products in the forward) and bytes = GGUF weight bytes +
+ * f32 inputs and outputs (+ A, B), each operand counted once */
+rtq_status rtq_ctx_timing_work(rtq_ctx* ctx, int i, double* flops, double* bytes);
 void rtq_ctx_timing_reset(rtq_ctx* ctx);
 
 /* ---- weights (RieFrozen::new, src/rie.rs:58-60; Weight::data() bytes, src/rie.rs:186) ---- */

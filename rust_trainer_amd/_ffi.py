@@ -52,6 +52,7 @@ SIGNATURES = {
     "rtq_ctx_timing_count": (_i, [_p]),
     "rtq_ctx_timing_get": (_i, [_p, _i, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i64),
                                 ctypes.POINTER(ctypes.c_double)]),
+    "rtq_ctx_timing_work": (_i, [_p, _i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "rtq_ctx_timing_reset": (None, [_p]),
     "rtq_weight_create": (_i, [_p, _i, _p, _sz, _i64, _i64, ctypes.POINTER(_p)]),
     "rtq_weight_destroy": (None, [_p]),

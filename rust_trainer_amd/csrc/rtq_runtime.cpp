@@ -169,6 +169,7 @@ const char* kKernelNames[K_COUNT] = {
 struct TimedLaunch {
   int kid;
   hipEvent_t a, b;
+  double flops, bytes;  // algorithmic work of the launch (0 for kernels without a work model)
 };
 
 }  // namespace
@@ -195,6 +196,9 @@ struct rtq_ctx {
   rocblas_handle blas = nullptr;  // created on the first trainer-native (f32 GEMM) weight
   int64_t t_launches[K_COUNT] = {};
   double t_ms[K_COUNT] = {};
+  double t_flops[K_COUNT] = {}, t_bytes[K_COUNT] = {};
+  // algorithmic work of the next launch (set_work), attached to its timing record
+  double next_flops = 0.0, next_bytes = 0.0;
 };
 
 struct rtq_weight {
@@ -244,8 +248,9 @@ rtq_status launch_raw(rtq_ctx* c, int kid, dim3 grid, dim3 block, hipStream_t s,
   if (e != hipSuccess) return fail(RTQ_ERR_HIP, "launch %s: %s", kKernelNames[kid], hipGetErrorString(e));
   if (timed && ea && eb) {
     HIP_TRY(hipEventRecord(eb, s));
-    c->pending.push_back({kid, ea, eb});
+    c->pending.push_back({kid, ea, eb, c->next_flops, c->next_bytes});
   }
+  c->next_flops = c->next_bytes = 0.0;
   return RTQ_OK;
 }
 
@@ -254,6 +259,11 @@ rtq_status launch(rtq_ctx* c, int kid, dim3 grid, dim3 block, hipStream_t s, con
   Args copy = args;
   return launch_raw(c, kid, grid, block, s, &copy, shmem);
 }
+
+// the algorithmic work of a frozen-linear call (each operand touched once), recorded with the next
+// launch's timing: forward = packed W + x + y + A, B (f32) and 2 T N K + the LoRA products; dx =
+// packed W + dy + dx and 2 T N K
+void set_work(rtq_ctx* c, const rtq_weight* w, int64_t t, int64_t r, bool backward);
 
 // ------------------------------------------------------------------ workspace
 struct Arena {
@@ -519,6 +529,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
     fa.r = (int)r;
     fa.s = s;
     const int kid = K_GEMV + fmt_index(w->type);
+    set_work(c, w, t, lora ? r : 0, false);
     return launch(c, kid, dim3((unsigned)gp.gx, (unsigned)gp.gy), dim3(256), st, fa,
                   (unsigned)(gp.kcps * kGemvChunkLds));
   }
@@ -587,6 +598,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   fa.xdh = xdh;
   if (mm && (!fa.wq || !fa.wdr || !fa.xq || !fa.xdh || !fa.y))
     return fail(RTQ_ERR_INVALID, "internal: rtq_mm_* operand missing");
+  set_work(c, w, t, lora ? r : 0, false);
   if (mm)
     return launch(c, (mm_ttn == 8 ? K_MM_Q4_0 : K_MM64_Q4_0) + (w->type == RTQ_TYPE_Q4_0 ? 0 : 1),
                   dim3((unsigned)mm_tiles), dim3(256), st, fa, mm_lds_bytes(w->type, mm_ttn));
@@ -693,6 +705,7 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   DxArgs xa{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, (int)dp.splits, part,
             lora ? hp : nullptr, lora ? gp : nullptr, (int)nhq, (int)ngq, (int)r, s, h, g};
   const int kid = (dp.tok16 ? K_DX16 : (dp.wide ? K_DXW : K_DX)) + fmt_index(w->type);
+  set_work(c, w, t, 0, true);
   // t > 16: (token group, split) units of K-chunk workgroups, padded to a multiple of 8 (XCD order)
   const int64_t nmain = dp.tok16 ? (w->Kp / 128) * dp.splits
                                  : roundup(cdiv(t, dp.wide ? 256 : 64) * dp.splits, 8) * (w->Kp / 128);
@@ -710,6 +723,18 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   fa.n_dx = dp.tok16 ? (int)cdiv(t * cdiv(K, 64), nw) : (int)cdiv((w->Kp / 128) * cdiv(t, 64) * 32, nw);
   return launch(c, nw == 16 ? K_BWD_FINISH16 : K_BWD_FINISH, dim3((unsigned)(fa.n_gb + fa.n_ga + fa.n_dx)),
                 dim3(64 * nw), st, fa);
+}
+
+void set_work(rtq_ctx* c, const rtq_weight* w, int64_t t, int64_t r, bool backward) {
+  const double N = (double)w->rows, K = (double)w->cols, T = (double)t, R = (double)std::max<int64_t>(r, 0);
+  const double wb = (double)w->gguf_bytes;
+  if (backward) {
+    c->next_flops = 2.0 * T * N * K;
+    c->next_bytes = wb + 4.0 * T * (N + K);
+  } else {
+    c->next_flops = 2.0 * T * N * K + 2.0 * T * R * (K + N);
+    c->next_bytes = wb + 4.0 * T * (N + K) + 4.0 * R * (K + N);
+  }
 }
 
 rtq_status check_weight(rtq_ctx* c, const rtq_weight* w) {
@@ -965,6 +990,8 @@ static void fold_timing(rtq_ctx* c) {
     if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
       c->t_launches[p.kid] += 1;
       c->t_ms[p.kid] += ms;
+      c->t_flops[p.kid] += p.flops;
+      c->t_bytes[p.kid] += p.bytes;
     }
     c->free_events.push_back(p.a);
     c->free_events.push_back(p.b);
@@ -989,6 +1016,15 @@ rtq_status rtq_ctx_timing_get(rtq_ctx* c, int i, const char** name, int64_t* lau
   return RTQ_OK;
 }
 
+rtq_status rtq_ctx_timing_work(rtq_ctx* c, int i, double* flops, double* bytes) {
+  if (!c || i < 0 || i >= K_COUNT) return fail(RTQ_ERR_INVALID, "bad timing index");
+  std::lock_guard<std::mutex> lk(c->mu);
+  fold_timing(c);
+  if (flops) *flops = c->t_flops[i];
+  if (bytes) *bytes = c->t_bytes[i];
+  return RTQ_OK;
+}
+
 void rtq_ctx_timing_reset(rtq_ctx* c) {
   if (!c) return;
   std::lock_guard<std::mutex> lk(c->mu);
@@ -996,6 +1032,7 @@ void rtq_ctx_timing_reset(rtq_ctx* c) {
   for (int k = 0; k < K_COUNT; k++) {
     c->t_launches[k] = 0;
     c->t_ms[k] = 0.0;
+    c->t_flops[k] = c->t_bytes[k] = 0.0;
   }
 }
 

@@ -69,6 +69,23 @@ class Context:
                 out[name.value.decode()] = (cnt.value, ms.value)
         return out
 
+    def timing_work(self) -> dict[str, tuple[float, float]]:
+        """{kernel name: (flops, bytes)}: the algorithmic work of the timed launches (frozen-linear
+        kernels; see rtq_ctx_timing_work)."""
+        L = _ffi.lib()
+        out = {}
+        for i in range(L.rtq_ctx_timing_count(self.handle)):
+            name = ctypes.c_char_p()
+            cnt = ctypes.c_int64()
+            ms = ctypes.c_double()
+            fl, by = ctypes.c_double(), ctypes.c_double()
+            _ffi.check(L.rtq_ctx_timing_get(self.handle, i, ctypes.byref(name), ctypes.byref(cnt), ctypes.byref(ms)),
+                       "rtq_ctx_timing_get")
+            _ffi.check(L.rtq_ctx_timing_work(self.handle, i, ctypes.byref(fl), ctypes.byref(by)), "rtq_ctx_timing_work")
+            if cnt.value and fl.value:
+                out[name.value.decode()] = (fl.value, by.value)
+        return out
+
     def reset_timing(self) -> None:
         _ffi.lib().rtq_ctx_timing_reset(self.handle)
 

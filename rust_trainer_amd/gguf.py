@@ -295,7 +295,10 @@ class GgufWriter:
         data, n = ctypes.c_void_p(), ctypes.c_size_t()
         _ffi.check(_ffi.lib().rtq_gguf_writer_bytes(self._h, ctypes.byref(data), ctypes.byref(n)),
                    "rtq_gguf_writer_bytes")
-        return ctypes.string_at(data.value, n.value)
+        if not n.value:
+            return b""
+        # through a ctypes array (string_at takes a C int size: images over 2 GiB)
+        return bytes((ctypes.c_char * n.value).from_address(data.value))
 
     def write(self, path: str | os.PathLike) -> None:
         _ffi.check(_ffi.lib().rtq_gguf_writer_write(self._h, os.fsencode(path)), "rtq_gguf_writer_write")
@@ -330,6 +333,9 @@ class SyntheticSpec:
     rms_eps: float = 1e-6
     std: float = 0.02
     tensor_types: dict = dataclasses.field(default_factory=dict)
+    # weights from numpy's PCG64 (N(0, std) per tensor, seeded as above) instead of the reference's
+    # SplitMix64 stream: 6x faster to draw, for the multi-billion-parameter benchmark models
+    fast: bool = False
 
     # name -> (arch, layers, hidden, heads, kv heads, head dim, ff, vocab, tied, rope base, per-role types)
     PRESETS = {
@@ -390,7 +396,27 @@ class SyntheticSpec:
         n = int(np.prod(dims, dtype=np.int64))
         if name.endswith("norm.weight"):
             return np.ones(n, dtype=np.float32).view(np.uint8)
-        w = Rng(self.seed * 1_000_003 + index).vec_normal(n, self.std).reshape(-1, dims[0])
+        if self.fast:
+            return np.concatenate([self._fast_rows(index, ggml_type, dims, r0, r1)
+                                   for r0, r1 in self._fast_chunks(dims)])
+        else:
+            w = Rng(self.seed * 1_000_003 + index).vec_normal(n, self.std).reshape(-1, dims[0])
+        if ggml_type == GGML_F32:
+            return w.view(np.uint8).reshape(-1)
+        return QUANTIZERS[ggml_type](w).reshape(-1)
+
+    FAST_CHUNK = 1 << 24  # elements per independently seeded row chunk of a fast tensor
+
+    def _fast_chunks(self, dims) -> list[tuple[int, int]]:
+        rows = int(np.prod(dims[1:], dtype=np.int64)) if len(dims) > 1 else 1
+        step = max(1, self.FAST_CHUNK // int(dims[0]))
+        return [(r, min(rows, r + step)) for r in range(0, rows, step)]
+
+    def _fast_rows(self, index: int, ggml_type: int, dims, r0: int, r1: int) -> np.ndarray:
+        """rows [r0, r1) of a fast tensor: N(0, std) from PCG64 seeded by (tensor, first row)"""
+        rng = np.random.default_rng([self.seed * 1_000_003 + index, r0])
+        w = (rng.standard_normal((r1 - r0) * int(dims[0]), dtype=np.float32) * np.float32(self.std))
+        w = w.reshape(r1 - r0, int(dims[0]))
         if ggml_type == GGML_F32:
             return w.view(np.uint8).reshape(-1)
         return QUANTIZERS[ggml_type](w).reshape(-1)
@@ -413,17 +439,36 @@ class SyntheticSpec:
                 (f"{a}.rope.freq_base", Value.F32(self.rope_base)),
                 (f"{a}.vocab_size", Value.U32(self.n_vocab))]
 
-    def writer(self) -> GgufWriter:
+    def writer(self, workers: int = 1) -> GgufWriter:
+        """The image's writer; ``workers`` > 1 draws and quantises the tensors in that many forked
+        processes (the bytes are the same)."""
         w = GgufWriter()
         for k, v in self.metadata():
             w.kv(k, v)
-        for i, (name, ty, dims) in enumerate(self.plan()):
-            w.tensor(name, dims, ty, self.tensor_values(i, name, ty, dims))
+        plan = self.plan()
+        if workers > 1 and len(plan) > 1:
+            import concurrent.futures as cf
+            import multiprocessing as mp
+
+            with cf.ProcessPoolExecutor(max_workers=workers, mp_context=mp.get_context("fork")) as ex:
+                if self.fast:  # row chunks, so one large tensor keeps every worker busy
+                    futs = [[ex.submit(self._fast_rows, i, ty, dims, r0, r1) for r0, r1 in self._fast_chunks(dims)]
+                            if not name.endswith("norm.weight") else [ex.submit(self.tensor_values, i, name, ty, dims)]
+                            for i, (name, ty, dims) in enumerate(plan)]
+                    for (name, ty, dims), fs in zip(plan, futs):
+                        w.tensor(name, dims, ty, np.concatenate([f.result() for f in fs]))
+                else:
+                    futs = [ex.submit(self.tensor_values, i, name, ty, dims) for i, (name, ty, dims) in enumerate(plan)]
+                    for (name, ty, dims), f in zip(plan, futs):
+                        w.tensor(name, dims, ty, f.result())
+        else:
+            for i, (name, ty, dims) in enumerate(plan):
+                w.tensor(name, dims, ty, self.tensor_values(i, name, ty, dims))
         return w
 
-    def build(self) -> bytes:
+    def build(self, workers: int = 1) -> bytes:
         """The whole GGUF image (``SyntheticSpec::build``)."""
-        w = self.writer()
+        w = self.writer(workers)
         try:
             return w.to_bytes()
         finally:

@@ -74,7 +74,10 @@ def packed_batch(V, prompt_len, extras, seed):
     return seqs
 
 
-@pytest.mark.parametrize("wtype", [O.F32, O.Q4_0, O.Q4_K])
+MIXED = "Q4_K/Q6_K"  # configs[3]'s mix: Q4_K attention / gate / up, Q6_K down and output
+
+
+@pytest.mark.parametrize("wtype", [O.F32, O.Q4_0, MIXED])
 def test_packed_batch_equals_separate_examples(ctx, wtype):
     """F32 weights: the reference's 1e-5 bars (tests/gradcheck.rs:325-336).  Quantised weights: the
     first example, whose tokens sit at the same indices in both layouts, gives bit-identical
@@ -85,7 +88,11 @@ def test_packed_batch_equals_separate_examples(ctx, wtype):
     the oracle's).  The reference's own 1e-4 bar (tests/engine.rs:325) holds on its CPU because each
     attention row is summed in the same order either way (the oracle's packed and separate runs are
     bit-identical); here the bound is 2e-2 on log-probs and 5e-3 on gradients."""
-    spec = tiny_spec(wtype, n_layer=2, n_vocab=500)
+    if wtype == MIXED:
+        spec = tiny_spec(O.Q4_K, n_layer=2, n_vocab=500, tied=False,
+                         tensor_types={"ffn_down": O.Q6_K, "output": O.Q6_K, "token_embd": O.Q6_K})
+    else:
+        spec = tiny_spec(wtype, n_layer=2, n_vocab=500)
     g = G.GgufFile.from_bytes(spec.build())
     model, _ = model_with(ctx, g, 3, 6.0)
     # three examples sharing a 70-token prompt (more than one 64-token block), one answer starting
