@@ -128,7 +128,7 @@ rtq_status rtq_linear_backward_d(rtq_ctx* ctx, const rtq_weight* w, const rtq_lo
  * fails with RTQ_ERR_INVALID before launching anything (config 1, 256 tokens over 3072 x 1024, needs
  * 0.8 MiB; 2048 tokens over K = 4096 about 19 MiB).  Every call on one GPU shares that array, so
  * calls that overlap on one GPU (other streams, other contexts, other threads) race; calls on one
- * stream do not.  GGUF block weights only (F32 / TQ8_0: RTQ_ERR_UNSUPPORTED). */
+ * stream do not. */
 rtq_status rtq_linear_forward_noalloc_d(rtq_ctx* ctx, const rtq_weight* w, const float* bias, const rtq_lora* lora,
                                         const float* x, int64_t t, float* y, void* stream);
 

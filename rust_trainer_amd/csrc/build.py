@@ -73,7 +73,7 @@ def build_runtime(hsaco: str, noalloc_obj: str) -> str:
           "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"), "-I", CSRC,
           os.path.join(CSRC, "rtq_runtime.cpp"), os.path.join(CSRC, "rtq_gguf.cpp"),
           os.path.join(CSRC, "rtq_model.cpp"), noalloc_obj, "-o", tmp,
-          "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-lrocblas", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"])
+          "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"])
     os.replace(tmp, out)
     return out
 

@@ -23,6 +23,8 @@ enum RtqModelKernel {
   KM_GEMM32,
   KM_LORA_MASK,
   KM_GEMM32G,
+  KM_GEMM_Q8,
+  KM_GEMM32_Q8,
   KM_COUNT
 };
 
@@ -49,7 +51,6 @@ rtq_status rtq_linear_backward_blocks_d(rtq_ctx* c, const rtq_weight* w, const r
 rtq_status rtq_scratch_setup(int device);
 // rtq_linear_forward_d with the caller's workspace ws (ws_bytes) instead of the context's: never
 // allocates; a forward needing more than ws_bytes fails with RTQ_ERR_INVALID before any launch.
-// Trainer-native weights (F32, TQ8_0) are refused (RTQ_ERR_UNSUPPORTED).
 rtq_status rtq_linear_forward_ws_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
                                    const float* x, int64_t t, float* y, void* stream, void* ws, size_t ws_bytes);
 #endif

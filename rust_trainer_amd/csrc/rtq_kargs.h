@@ -76,8 +76,9 @@ struct ActArgs {
 
 // ---------------------------------------------------------------- trainer-native weights
 // FrozenWeight::{F32, Q8_0} (src/frozen.rs:33-45): f32 [N][K], or f32 scales [N][K/32] then i8
-// codes [N][K] (TQ8_0).  Their products are plain f32 GEMMs (rocBLAS); these kernels dequantise
-// (out = 0 + d * q, row() of src/frozen.rs:172-176), copy rows and add the bias.
+// codes [N][K] (TQ8_0).  Their products run on the f32 MFMA GEMM (rtq_m_gemm*, the TQ8_0 codes
+// decoded in its operand loads); these kernels dequantise rows (out = 0 + d * q, row() of
+// src/frozen.rs:172-176), copy rows and add the bias.
 struct DenseArgs {
   const float* w;    // F32 weight, or null
   const float* sc;   // TQ8_0 scales, or null
@@ -296,6 +297,9 @@ struct MGemmArgs {
   int batch;
   const uint8_t* live;
   int nlb;
+  // rtq_m_gemm*_q8: B holds int8 codes (element (k, n) at ((const int8_t*)B)[k * sBk + n * sBn]) with
+  // an f32 scale per 32 consecutive codes, Bsc[code index / 32] (FrozenWeight::Q8_0, src/frozen.rs:38-45)
+  const float* Bsc;
 };
 
 // up to three independent products in one launch of the 32-row-tile kernel: flat workgroup ids

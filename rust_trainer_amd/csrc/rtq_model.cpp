@@ -224,7 +224,7 @@ struct Op {  // one GEMM operand: base, batch stride and divisor, row / column s
 rtq_status k_gemm(rtq_model* m, int64_t M, int64_t N, int64_t K, int64_t batch, Op A, Op B, float* C, int64_t sCb,
                   int64_t sCm, int64_t sCn, float a_scale, int causal, int acc) {
   MGemmArgs ga{A.p, B.p, C, (int)M, (int)N, (int)K, A.sb, A.s0, A.s1, B.sb, B.s0, B.s1, sCb, sCm, sCn, A.div, B.div,
-               a_scale, causal, acc, (int)batch, causal && m->packed ? m->live_d : nullptr, (int)m->nlb};
+               a_scale, causal, acc, (int)batch, causal && m->packed ? m->live_d : nullptr, (int)m->nlb, nullptr};
   // 64-row tiles when the grid fills the chip twice over, else 32-row tiles (twice the workgroups)
   const int64_t tiles64 = (N + 63) / 64 * ((M + 63) / 64) * batch / (causal == 1 ? 2 : 1);
   const int bm = tiles64 >= 2 * 256 ? 64 : 32;
@@ -251,7 +251,7 @@ rtq_status k_gemm_group(rtq_model* m, const GemmJob* jobs, int n) {
     const GemmJob& j = jobs[i];
     g.p[i] = MGemmArgs{j.A.p, j.B.p, j.C, (int)j.M, (int)j.N, (int)j.K, j.A.sb, j.A.s0, j.A.s1, j.B.sb, j.B.s0,
                        j.B.s1, j.sCb, j.sCm, j.sCn, j.A.div, j.B.div, j.a_scale, j.causal, j.acc, (int)j.batch,
-                       j.causal && m->packed ? m->live_d : nullptr, (int)m->nlb};
+                       j.causal && m->packed ? m->live_d : nullptr, (int)m->nlb, nullptr};
     g.start[i] = (int)total;
     total += (j.N + 63) / 64 * ((j.M + 31) / 32) * j.batch;
   }
@@ -267,7 +267,7 @@ rtq_status lin_fwd(rtq_model* m, const Group& l, const float* x, int64_t t, floa
 }
 
 // a fused group's adapter is block-diagonal (each member's rows see only its own ranks): the
-// quantised backward computes gb and g = s dy.B inside the blocks only; the dense (rocBLAS) one
+// quantised backward computes gb and g = s dy.B inside the blocks only; the dense (f32 GEMM) one
 // computes every pair and the off-block gb entries are cleared after it
 rtq_status lin_bwd(rtq_model* m, const Group& l, const float* x, const float* dy, int64_t t, float* dx) {
   const rtq_lora lv = lora_view(l);

@@ -232,6 +232,45 @@ __device__ __forceinline__ void m_opnd_load(const float* P, int64_t sr, int64_t 
   }
 }
 
+// the same for a TQ8_0 operand: element (r, k) = Sc[e / 32] * Q[e], e = r * sr + k * sk (four
+// consecutive codes of a vector share one 32-code scale block: e is a multiple of 4 there)
+__device__ __forceinline__ int m_q8_mode(const int8_t* Q, int64_t sr, int64_t sk, int nrows, int K) {
+  const bool al = (reinterpret_cast<uintptr_t>(Q) & 3u) == 0;
+  if (al && sk == 1 && sr % 4 == 0 && K % 4 == 0) return 1;
+  if (al && sr == 1 && sk % 4 == 0 && nrows % 4 == 0) return 2;
+  return 0;
+}
+__device__ __forceinline__ f4 m_q8_vec(const int8_t* Q, const float* Sc, int64_t e) {
+  const uint32_t u = *reinterpret_cast<const uint32_t*>(Q + e);
+  const float d = Sc[e >> 5];
+  return f4{d * (float)(int8_t)(u & 0xffu), d * (float)(int8_t)((u >> 8) & 0xffu), d * (float)(int8_t)((u >> 16) & 0xffu),
+            d * (float)(int8_t)(u >> 24)};
+}
+template <int R, int BK, int NV>
+__device__ __forceinline__ void m_opnd_load_q8(const int8_t* Q, const float* Sc, int64_t sr, int64_t sk, int nrows,
+                                               int r0, int kk, int k1, int mode, f4 (&v)[NV]) {
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int e = threadIdx.x + 256 * i;
+    if (mode == 2) {
+      const int gr = r0 + (e % (R / 4)) * 4, gk = kk + e / (R / 4);
+      v[i] = (gr < nrows && gk < k1) ? m_q8_vec(Q, Sc, (int64_t)gk * sk + gr) : zero;
+    } else {
+      const int gr = r0 + e / (BK / 4), gk = kk + (e % (BK / 4)) * 4;
+      if (mode == 1) {
+        v[i] = (gr < nrows && gk < k1) ? m_q8_vec(Q, Sc, (int64_t)gr * sr + gk) : zero;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int64_t ix = (int64_t)gr * sr + (int64_t)(gk + q) * sk;
+          v[i][q] = (gr < nrows && gk + q < k1) ? Sc[ix >> 5] * (float)Q[ix] : 0.0f;
+        }
+      }
+    }
+  }
+}
+
 template <int R, int BK, int NV>
 __device__ __forceinline__ void m_opnd_store(float* S, int mode, const f4 (&v)[NV]) {
 #pragma unroll
@@ -254,7 +293,7 @@ __device__ __forceinline__ f4 m_opnd_frag(const float* S, int mode, int r, int k
   return *reinterpret_cast<const f4*>(S + r * (BK + 4) + 16 * kb + 4 * g);
 }
 
-template <int BM>
+template <int BM, bool BQ = false>
 __device__ __forceinline__ void m_gemm(const MGemmArgs& a, int bx, int by, int bz) {
   using Cf = MGemmCfg<BM>;
   constexpr int BN = Cf::BN, BK = Cf::BK, TM = Cf::TM;
@@ -279,7 +318,14 @@ __device__ __forceinline__ void m_gemm(const MGemmArgs& a, int bx, int by, int b
   };
   k0 = next_live(k0);
   const int amode = m_opnd_mode(A, a.sAm, a.sAk, a.sAb, a.M, a.K);
-  const int bmode = m_opnd_mode(B, a.sBn, a.sBk, a.sBb, a.N, a.K);
+  const int8_t* Bq = reinterpret_cast<const int8_t*>(a.B);  // BQ: the codes (batch 1)
+  const int bmode = BQ ? m_q8_mode(Bq, a.sBn, a.sBk, a.N, a.K) : m_opnd_mode(B, a.sBn, a.sBk, a.sBb, a.N, a.K);
+  auto load_b = [&](int kk, f4 (&v)[Cf::NB]) {
+    if constexpr (BQ)
+      m_opnd_load_q8<BN, BK>(Bq, a.Bsc, a.sBn, a.sBk, a.N, n0, kk, k1, bmode, v);
+    else
+      m_opnd_load<BN, BK>(B, a.sBn, a.sBk, a.N, n0, kk, k1, bmode, 1.0f, v);
+  };
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
   const int wm = (w >> 1) * (BM / 2), wn = (w & 1) * 32;
   f4 acc[TM][2];
@@ -290,7 +336,7 @@ __device__ __forceinline__ void m_gemm(const MGemmArgs& a, int bx, int by, int b
   f4 ra[Cf::NA], rb[Cf::NB];
   if (k0 < k1) {
     m_opnd_load<BM, BK>(A, a.sAm, a.sAk, a.M, m0, k0, k1, amode, a.a_scale, ra);
-    m_opnd_load<BN, BK>(B, a.sBn, a.sBk, a.N, n0, k0, k1, bmode, 1.0f, rb);
+    load_b(k0, rb);
   }
   for (int kk = k0; kk < k1;) {
     m_opnd_store<BM, BK>(As, amode, ra);
@@ -299,7 +345,7 @@ __device__ __forceinline__ void m_gemm(const MGemmArgs& a, int bx, int by, int b
     const int kn = next_live(kk + BK);
     if (kn < k1) {
       m_opnd_load<BM, BK>(A, a.sAm, a.sAk, a.M, m0, kn, k1, amode, a.a_scale, ra);
-      m_opnd_load<BN, BK>(B, a.sBn, a.sBk, a.N, n0, kn, k1, bmode, 1.0f, rb);
+      load_b(kn, rb);
     }
 #pragma unroll
     for (int kb = 0; kb < BK / 16; kb++) {
@@ -344,11 +390,11 @@ __device__ __forceinline__ int m_xcd_tile(int n) {
   const int l = (id & 7) * per + (id >> 3);
   return l < n ? l : -1;
 }
-template <int BM>
+template <int BM, bool BQ = false>
 __device__ __forceinline__ void m_gemm_tile(const MGemmArgs& a, int l) {
   const int nx = (a.N + 63) / 64, ny = (a.M + BM - 1) / BM;
   const int bx = l % nx, yy = (l / nx) % ny, bz = l / (nx * ny);
-  m_gemm<BM>(a, bx, a.causal == 2 ? ny - 1 - yy : yy, bz);
+  m_gemm<BM, BQ>(a, bx, a.causal == 2 ? ny - 1 - yy : yy, bz);
 }
 extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm(MGemmArgs a) {
   const int l = m_xcd_tile((a.N + 63) / 64 * ((a.M + 63) / 64) * a.batch);
@@ -357,6 +403,15 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm(MGemmArgs a) {
 extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32(MGemmArgs a) {
   const int l = m_xcd_tile((a.N + 63) / 64 * ((a.M + 31) / 32) * a.batch);
   if (l >= 0) m_gemm_tile<32>(a, l);
+}
+// B a TQ8_0 weight (the trainer-native FrozenWeight::Q8_0 products of the runtime)
+extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm_q8(MGemmArgs a) {
+  const int l = m_xcd_tile((a.N + 63) / 64 * ((a.M + 63) / 64) * a.batch);
+  if (l >= 0) m_gemm_tile<64, true>(a, l);
+}
+extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32_q8(MGemmArgs a) {
+  const int l = m_xcd_tile((a.N + 63) / 64 * ((a.M + 31) / 32) * a.batch);
+  if (l >= 0) m_gemm_tile<32, true>(a, l);
 }
 
 // grouped products (MGemmGroupArgs) in one flat grid, so the products' workgroups share the CUs

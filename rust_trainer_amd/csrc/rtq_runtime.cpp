@@ -10,7 +10,6 @@
 #include "rtq.h"
 
 #include <hip/hip_runtime.h>
-#include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <cstdarg>
@@ -164,7 +163,7 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_m_rmsnorm",        "rtq_m_rmsnorm_bwd",    "rtq_m_qk_prep",        "rtq_m_qk_bwd",
     "rtq_m_gemm",           "rtq_m_softmax",        "rtq_m_softmax_bwd",    "rtq_m_group_sum",
     "rtq_m_swiglu",         "rtq_m_swiglu_bwd",     "rtq_m_add",            "rtq_m_gemm32",
-    "rtq_m_lora_mask",      "rtq_m_gemm32g"};
+    "rtq_m_lora_mask",      "rtq_m_gemm32g",        "rtq_m_gemm_q8",        "rtq_m_gemm32_q8"};
 
 struct TimedLaunch {
   int kid;
@@ -193,7 +192,6 @@ struct rtq_ctx {
   int fwd_rg = -1;    // row groups of 16 per eight-wave forward tile: -1 automatic, 2 or 3 (RTQ_FWD_RG)
   int fwd_mm = -1;    // large-grid forward: -1 automatic, 0 never, 1 / 2 the 128- / 64-token tiles whenever
                       // the format allows (RTQ_FWD_MM)
-  rocblas_handle blas = nullptr;  // created on the first trainer-native (f32 GEMM) weight
   int64_t t_launches[K_COUNT] = {};
   double t_ms[K_COUNT] = {};
   double t_flops[K_COUNT] = {}, t_bytes[K_COUNT] = {};
@@ -295,7 +293,7 @@ rtq_status ensure_ws(rtq_ctx* c, size_t bytes) {
 
 bool is_q32(int type) { return type == RTQ_TYPE_Q4_0 || type == RTQ_TYPE_Q8_0; }
 bool is_kquant(int type) { return type == RTQ_TYPE_Q4_K || type == RTQ_TYPE_Q6_K; }
-// trainer-native FrozenWeight storage: f32 products through rocBLAS
+// trainer-native FrozenWeight storage: f32 products on the f32 MFMA GEMM
 bool is_dense(int type) { return type == RTQ_TYPE_F32 || type == RTQ_TYPE_TQ8_0; }
 bool supported(int type) { return is_q32(type) || is_kquant(type) || is_dense(type); }
 int fmt_index(int type) {
@@ -330,7 +328,7 @@ struct FwdPlan {
   bool skinny;
   bool gemv;  // t <= 16 through rtq_gemv_* (see gemv_plan)
   size_t xq_bytes, xd_floats, xg_floats, h_floats, xdh_bytes;
-  size_t dense_bytes;  // trainer-native weights: dequantised TQ8_0 copy + h
+  size_t dense_bytes;  // trainer-native weights: h
 };
 
 constexpr int kFwdWideTT = 4;     // rtq_fwd_*_w: 64 tokens x (16 * wide_rg) rows per workgroup
@@ -370,8 +368,7 @@ FwdPlan fwd_plan(const rtq_weight* w, int64_t t, int64_t r) {
   FwdPlan p{};
   p.T = t;
   if (is_dense(w->type)) {
-    p.dense_bytes = (w->type == RTQ_TYPE_TQ8_0 ? (size_t)(w->rows * w->cols) * 4 : 0) +
-                    (size_t)(t * std::max<int64_t>(r, 0)) * 4 + 2 * 256;
+    p.dense_bytes = (size_t)(t * std::max<int64_t>(r, 0)) * 4 + 2 * 256;
     return p;
   }
   p.skinny = t <= 16;
@@ -394,54 +391,54 @@ size_t fwd_ws_bytes(const FwdPlan& p) {
 
 // ------------------------------------------------------------------ trainer-native weights
 // FrozenWeight::{F32, Q8_0} (src/frozen.rs:33-187) and the Linear LoRA math around them as f32
-// GEMMs (rocBLAS, column-major: a row-major product C = op(A) op(B) is the column-major
-// C^T = op(B)^T op(A)^T).  TQ8_0 is dequantised per call into the workspace first.
-rtq_status blas_handle(rtq_ctx* c, hipStream_t st, rocblas_handle* h) {
-  if (!c->blas && rocblas_create_handle(&c->blas) != rocblas_status_success) {
-    c->blas = nullptr;
-    return fail(RTQ_ERR_HIP, "rocblas_create_handle failed");
-  }
-  if (rocblas_set_stream(c->blas, st) != rocblas_status_success) return fail(RTQ_ERR_HIP, "rocblas_set_stream failed");
-  *h = c->blas;
-  return RTQ_OK;
+// products on the f32 MFMA GEMM of the decoder kernels (rtq_m_gemm*: exact f32 products, f32
+// accumulation).  A TQ8_0 weight is read as codes plus one f32 scale per 32 and decoded in the
+// GEMM's operand loads: no dequantised copy of the weight is materialised.
+
+// C(m, n) (+)= sum_k A(m, k) B(k, n), A(m, k) = a_scale * A[m * sAm + k * sAk] (the product rounded
+// first), B(k, n) = W[k * sBk + n * sBn] for f32 W, or the TQ8_0 weight w's decoded element at that
+// index; C at row stride ldc.  64-row tiles when they fill the chip twice over, else 32-row tiles.
+rtq_status dense_gemm(rtq_ctx* c, hipStream_t st, int64_t M, int64_t N, int64_t K, const float* A, int64_t sAm,
+                      int64_t sAk, float a_scale, const float* B, const rtq_weight* q8, int64_t sBk, int64_t sBn,
+                      float* C, int64_t ldc, bool acc) {
+  if (M <= 0 || N <= 0) return RTQ_OK;
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return fail(RTQ_ERR_INVALID, "f32 product too large");
+  MGemmArgs ga{};
+  ga.A = A;
+  ga.B = q8 ? reinterpret_cast<const float*>(q8->wq) : B;
+  ga.Bsc = q8 ? q8->wsc : nullptr;
+  ga.C = C;
+  ga.M = (int)M;
+  ga.N = (int)N;
+  ga.K = (int)K;
+  ga.sAm = sAm;
+  ga.sAk = sAk;
+  ga.sBk = sBk;
+  ga.sBn = sBn;
+  ga.sCm = ldc;
+  ga.sCn = 1;
+  ga.divA = ga.divB = 1;
+  ga.a_scale = a_scale;
+  ga.accumulate = acc ? 1 : 0;
+  ga.batch = 1;
+  const int64_t tiles64 = cdiv(N, 64) * cdiv(M, 64);
+  const int bm = tiles64 >= 2 * c->cu_count ? 64 : 32;
+  const int64_t tiles = cdiv(N, 64) * cdiv(M, bm);
+  if (tiles > INT32_MAX - 8) return fail(RTQ_ERR_INVALID, "f32 product too large");
+  const int km = q8 ? (bm == 64 ? KM_GEMM_Q8 : KM_GEMM32_Q8) : (bm == 64 ? KM_GEMM : KM_GEMM32);
+  return launch(c, K_MODEL + km, dim3((unsigned)roundup(tiles, 8)), dim3(256), st, ga);
 }
 
-// row-major C[M x N] = alpha op(A) op(B) + beta C; lda / ldb / ldc: row lengths as stored
-rtq_status rm_sgemm(rocblas_handle h, bool ta, bool tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
-                    int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc) {
-  if (M == 0 || N == 0) return RTQ_OK;
-  const rocblas_status e =
-      rocblas_sgemm(h, tb ? rocblas_operation_transpose : rocblas_operation_none,
-                    ta ? rocblas_operation_transpose : rocblas_operation_none, (rocblas_int)N, (rocblas_int)M,
-                    (rocblas_int)K, &alpha, B, (rocblas_int)ldb, A, (rocblas_int)lda, &beta, C, (rocblas_int)ldc);
-  if (e != rocblas_status_success) return fail(RTQ_ERR_HIP, "rocblas_sgemm: %s", rocblas_status_to_string(e));
-  return RTQ_OK;
-}
-
-// the weight as f32 [N][K]: F32 in place, TQ8_0 dequantised into the arena
-rtq_status dense_weight(rtq_ctx* c, const rtq_weight* w, Arena& ar, hipStream_t st, const float** W) {
-  if (w->type == RTQ_TYPE_F32) {
-    *W = reinterpret_cast<const float*>(w->wq);
-    return RTQ_OK;
-  }
-  float* out = ar.take<float>((size_t)(w->rows * w->cols));
-  if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
-  DenseArgs da{nullptr, w->wsc, reinterpret_cast<const int8_t*>(w->wq), w->rows, w->cols, 0, w->rows, out, nullptr, nullptr};
-  RTQ_TRY(launch(c, K_DENSE_ROWS, dim3((unsigned)std::min<int64_t>(cdiv(w->rows * w->cols, 256), 8192)), dim3(256), st, da));
-  *W = out;
-  return RTQ_OK;
-}
+// the weight as a B operand of y = x W^T (B(k, n) = W[n][k]) or dx = dy W (B(k, n) = W[k][n])
+const float* dense_b(const rtq_weight* w) { return w->type == RTQ_TYPE_F32 ? reinterpret_cast<const float*>(w->wq) : nullptr; }
+const rtq_weight* dense_q8(const rtq_weight* w) { return w->type == RTQ_TYPE_TQ8_0 ? w : nullptr; }
 
 // y = x W^T (src/frozen.rs:121-122); + bias; + s (x A^T) B^T (src/linear.rs:73-93)
 rtq_status enqueue_forward_dense(rtq_ctx* c, const rtq_weight* w, const float* x, int64_t t, float* y,
                                  const float* bias, const float* la, const float* lb, int64_t r, float s, Arena& ar,
                                  hipStream_t st) {
   const int64_t N = w->rows, K = w->cols;
-  const float* W;
-  RTQ_TRY(dense_weight(c, w, ar, st, &W));
-  rocblas_handle h;
-  RTQ_TRY(blas_handle(c, st, &h));
-  RTQ_TRY(rm_sgemm(h, false, true, t, N, K, 1.0f, x, K, W, K, 0.0f, y, N));
+  RTQ_TRY(dense_gemm(c, st, t, N, K, x, K, 1, 1.0f, dense_b(w), dense_q8(w), 1, K, y, N, false));
   if (bias) {
     DenseArgs da{nullptr, nullptr, nullptr, N, K, 0, t, y, bias, nullptr};
     RTQ_TRY(launch(c, K_DENSE_BIAS, dim3((unsigned)std::min<int64_t>(cdiv(t * N, 256), 8192)), dim3(256), st, da));
@@ -449,8 +446,8 @@ rtq_status enqueue_forward_dense(rtq_ctx* c, const rtq_weight* w, const float* x
   if (la && lb && r > 0) {
     float* hh = ar.take<float>((size_t)(t * r));
     if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
-    RTQ_TRY(rm_sgemm(h, false, true, t, r, K, 1.0f, x, K, la, K, 0.0f, hh, r));  // h = x A^T
-    RTQ_TRY(rm_sgemm(h, false, true, t, N, r, s, hh, r, lb, r, 1.0f, y, N));     // y += s h B^T
+    RTQ_TRY(dense_gemm(c, st, t, r, K, x, K, 1, 1.0f, la, nullptr, 1, K, hh, r, false));  // h = x A^T
+    RTQ_TRY(dense_gemm(c, st, t, N, r, hh, r, 1, s, lb, nullptr, 1, r, y, N, true));     // y += (s h) B^T
   }
   return RTQ_OK;
 }
@@ -461,24 +458,19 @@ rtq_status enqueue_backward_dense(rtq_ctx* c, const rtq_weight* w, const float* 
                                   bool accumulate, const float* x, const float* la, const float* lb, int64_t r,
                                   float s, float* ga, float* gb, Arena& ar, hipStream_t st) {
   const int64_t N = w->rows, K = w->cols;
-  const float* W;
-  RTQ_TRY(dense_weight(c, w, ar, st, &W));
-  rocblas_handle h;
-  RTQ_TRY(blas_handle(c, st, &h));
-  RTQ_TRY(rm_sgemm(h, false, false, t, K, N, 1.0f, dy, N, W, K, accumulate ? 1.0f : 0.0f, dx, K));
+  RTQ_TRY(dense_gemm(c, st, t, K, N, dy, N, 1, 1.0f, dense_b(w), dense_q8(w), K, 1, dx, K, accumulate));
   if (la && lb && r > 0) {
     float* hh = ar.take<float>((size_t)(t * r));
     float* g = ar.take<float>((size_t)(t * r));
     if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
-    RTQ_TRY(rm_sgemm(h, false, true, t, r, K, 1.0f, x, K, la, K, 0.0f, hh, r));   // h = x A^T
-    RTQ_TRY(rm_sgemm(h, true, false, N, r, t, s, dy, N, hh, r, 1.0f, gb, r));     // gb += s dy^T h
-    RTQ_TRY(rm_sgemm(h, false, false, t, r, N, s, dy, N, lb, r, 0.0f, g, r));     // g = s dy B
-    RTQ_TRY(rm_sgemm(h, true, false, r, K, t, 1.0f, g, r, x, K, 1.0f, ga, K));    // ga += g^T x
-    RTQ_TRY(rm_sgemm(h, false, false, t, K, r, 1.0f, g, r, la, K, 1.0f, dx, K));  // dx += g A
+    RTQ_TRY(dense_gemm(c, st, t, r, K, x, K, 1, 1.0f, la, nullptr, 1, K, hh, r, false));  // h = x A^T
+    RTQ_TRY(dense_gemm(c, st, N, r, t, dy, 1, N, s, hh, nullptr, r, 1, gb, r, true));     // gb += (s dy)^T h
+    RTQ_TRY(dense_gemm(c, st, t, r, N, dy, N, 1, s, lb, nullptr, r, 1, g, r, false));     // g = (s dy) B
+    RTQ_TRY(dense_gemm(c, st, r, K, t, g, 1, r, 1.0f, x, nullptr, K, 1, ga, K, true));    // ga += g^T x
+    RTQ_TRY(dense_gemm(c, st, t, K, r, g, r, 1, 1.0f, la, nullptr, K, 1, dx, K, true));   // dx += g A
   }
   return RTQ_OK;
 }
-
 
 // ------------------------------------------------------------------ enqueue: forward
 // y = x.W^T (+bias) (+ s h.B^T);  isums (debug) receives the per-block integer sums.
@@ -656,9 +648,7 @@ DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
 // backward workspace: h, g [t x r], their slice partials [t][r][slices], dx split partials
 size_t bwd_ws_bytes(const rtq_ctx* c, const rtq_weight* w, int64_t t, int64_t r) {
   const int64_t n = w->rows, k = w->cols;
-  if (is_dense(w->type))
-    return (w->type == RTQ_TYPE_TQ8_0 ? (size_t)(n * k) * 4 : 0) + (size_t)(2 * t * std::max<int64_t>(r, 0)) * 4 +
-           3 * 256;
+  if (is_dense(w->type)) return (size_t)(2 * t * std::max<int64_t>(r, 0)) * 4 + 3 * 256;
   const int64_t sl = roundup(cdiv(std::max<int64_t>(n, 1), RTQ_ACT_KQ), 4) + roundup(cdiv(std::max<int64_t>(k, 1), RTQ_ACT_KQ), 4);
   return (size_t)((2 + sl) * t * std::max<int64_t>(r, 0)) * 4 + dx_plan(c, w, std::max<int64_t>(t, 1)).part_floats * 4 +
          6 * 256;
@@ -942,7 +932,6 @@ void rtq_ctx_destroy(rtq_ctx* c) {
   }
   for (auto e : c->free_events) (void)hipEventDestroy(e);
   if (c->ws) (void)hipFree(c->ws);
-  if (c->blas) (void)rocblas_destroy_handle(c->blas);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   if (c->mod) (void)hipModuleUnload(c->mod);
   delete c;
@@ -1654,8 +1643,6 @@ rtq_status rtq_linear_forward_ws_d(rtq_ctx* c, const rtq_weight* w, const float*
   float s;
   RTQ_TRY(check_lora(lora, &on, &r, &s));
   if (t > 0 && (!x || !y)) return fail(RTQ_ERR_INVALID, "null x/y");
-  if (is_dense(w->type))
-    return fail(RTQ_ERR_UNSUPPORTED, "the no-allocation forward serves GGUF block weights (Q4_0, Q8_0, Q4_K, Q6_K)");
   const size_t need = fwd_ws_bytes(fwd_plan(w, t, on ? r : 0));
   if (need > ws_bytes)
     return fail(RTQ_ERR_INVALID, "forward of %lld tokens over %lldx%lld needs %zu bytes of scratch; the maximum is %zu",

@@ -520,7 +520,7 @@ def _trainer_weight(ctx, kind, n, k):
 
 
 @pytest.mark.parametrize("kind", ["f32", "tq8"])
-@pytest.mark.parametrize("n,k,t", [(64, 128, 1), (200, 256, 37), (3072, 1024, 256)])
+@pytest.mark.parametrize("n,k,t", [(64, 128, 1), (200, 256, 37), (37, 96, 5), (3072, 1024, 256), (1000, 2048, 600)])
 def test_trainer_native_frozen_matches_oracle(ctx, kind, n, k, t):
     hw, otype, ob = _trainer_weight(ctx, kind, n, k)
     assert hw.nbytes() == (n * k * 4 if kind == "f32" else n * (k // 32) * 4 + n * k)  # src/frozen.rs:180-185

@@ -7,7 +7,7 @@ library's file-scope device array) against rtq_linear_forward_d on the same inpu
   every output equals the allocating entry point's within 1e-5 (the kernels are the same);
 * the device's free memory does not move across the no-allocation calls;
 * a forward whose workspace exceeds the array is refused before any launch, naming the maximum;
-  trainer-native (F32) weights are refused.
+* trainer-native (F32, TQ8_0) weights allocate nothing either and give the allocating path's output.
 """
 import ctypes
 
@@ -91,7 +91,21 @@ def test_noalloc_forward_refuses_what_it_cannot_serve():
     assert rc == 1 and b"maximum" in _ffi.lib().rtq_last_error()
     torch.cuda.synchronize()
     assert bool((y == 5.0).all()), "a refused call wrote its output"
-    wf = rt.HipFrozen(O.F32, np.zeros((n, 256), np.float32), n, 256, ctx=ctx)
-    rc = _ffi.lib().rtq_linear_forward_noalloc_d(ctx.handle, wf.handle, None, None, x.data_ptr(), 4, y.data_ptr(), None)
-    assert rc == 2
+    # trainer-native weights run on the f32 GEMM and allocate nothing either: same output as the
+    # allocating entry point
+    stream = torch.cuda.current_stream().cuda_stream
+    for wf in (rt.HipFrozen.f32(O.Rng(5).vec_normal(96 * 256, 0.02), 96, 256, ctx=ctx),
+               rt.HipFrozen.q8_0(O.Rng(6).vec_normal(96 * 256, 0.02), 96, 256, ctx=ctx)):
+        xs = torch.from_numpy(O.Rng(7).vec_normal(9 * 256, 1.0).reshape(9, 256)).to(dev)
+        y1, y2 = torch.empty(9, 96, device=dev), torch.empty(9, 96, device=dev)
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info(0)[0]
+        _ffi.check(_ffi.lib().rtq_linear_forward_noalloc_d(ctx.handle, wf.handle, None, None, xs.data_ptr(), 9,
+                                                           y1.data_ptr(), stream), "rtq_linear_forward_noalloc_d")
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info(0)[0] == free0
+        _ffi.check(_ffi.lib().rtq_linear_forward_d(ctx.handle, wf.handle, None, None, xs.data_ptr(), 9, y2.data_ptr(),
+                                                   stream), "rtq_linear_forward_d")
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2)
     ctx.close()
