@@ -277,6 +277,64 @@ def test_lm_head_shape_t1(ctx, wtype):
     assert rel_err(dx, O.frozen_backward_input(wtype, blocks, n, k, dy, nthreads=16)) <= TOL
 
 
+# ---------------------------------------------------------------- configs[1] sweep points
+def _dense_dx_check(wtype, blocks, n, k, dy, got):
+    """tests/engine.rs:96-120: dx equals the dense dy . W of the dequantised rows, per element
+    within 1e-3 * max(|want|, 1)"""
+    W = O.dequantize(wtype, blocks, k).reshape(n, k).astype(np.float64)
+    dense = dy.astype(np.float64) @ W
+    bad = np.abs(got.reshape(dense.shape) - dense) >= 1e-3 * np.maximum(np.abs(dense), 1.0)
+    assert not bad.any(), f"{int(bad.sum())} dx elements off"
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("shape", ["q_proj", "kv_proj", "down_proj"])
+def test_config1_sweep_t2048_matches_oracle(ctx, wtype, shape):
+    """configs[1] at T = 2048 (Linear forward with LoRA r = 16, Linear backward: dx, dA, dB)"""
+    import time
+
+    n, k = {"q_proj": (2048, 1024), "kv_proj": (1024, 1024), "down_proj": (1024, 3072)}[shape]
+    t, r = 2048, 16
+    blocks, x, dy = make(wtype, n, k, t)
+    A, B = lora(n, k, r)
+    lin = rt.Linear(shape, hip(ctx, wtype, blocks, n, k))
+    lin.lora = rt.Lora(r, 32.0, A, B)
+    y = lin.forward(x, t)
+    dx = lin.backward(x, dy, t)
+    t0 = time.perf_counter()
+    wy = O.linear_forward(wtype, blocks, n, k, x, A=A, B=B, alpha=32.0, nthreads=16)
+    wdx, wga, wgb = O.linear_backward(wtype, blocks, n, k, x, dy, A=A, B=B, alpha=32.0, nthreads=16)
+    print(f"oracle (16 threads): {time.perf_counter() - t0:.1f} s")
+    errs = rel_err(y, wy), rel_err(dx, wdx), rel_err(lin.lora.ga, wga), rel_err(lin.lora.gb, wgb)
+    print("y, dx, dA, dB rel err", " ".join(f"{e:.1e}" for e in errs))
+    assert max(errs) <= TOL
+    # the frozen part alone against the dense product (FrozenMatmul::backward_input)
+    dxf = np.zeros(t * k, np.float32)
+    lin.w.backward_input(dy, t, dxf)
+    _dense_dx_check(wtype, blocks, n, k, dy, dxf)
+
+
+@pytest.mark.parametrize("wtype,t", [(O.Q4_0, 16), (O.Q8_0, 16), (O.Q4_K, 16), (O.Q6_K, 16), (O.Q4_K, 256)])
+def test_config1_lm_head_matches_oracle(ctx, wtype, t):
+    """configs[1]'s tied LM head 151936 x 1024 (no adapter) at T = 16 in every format and T = 256
+    (Q4_K): forward and FrozenMatmul::backward_input against the oracle and, per element, against
+    the dense product"""
+    import time
+
+    n, k = 151936, 1024
+    blocks, x, dy = make(wtype, n, k, t)
+    w = hip(ctx, wtype, blocks, n, k)
+    y = w.forward(x, t)
+    dx = np.zeros(t * k, np.float32)
+    w.backward_input(dy, t, dx)
+    t0 = time.perf_counter()
+    wy = O.frozen_forward(wtype, blocks, n, k, x, nthreads=16)
+    wdx = O.frozen_backward_input(wtype, blocks, n, k, dy, nthreads=16)
+    print(f"oracle (16 threads): {time.perf_counter() - t0:.1f} s; y {rel_err(y, wy):.1e} dx {rel_err(dx, wdx):.1e}")
+    assert rel_err(y, wy) <= TOL and rel_err(dx, wdx) <= TOL
+    _dense_dx_check(wtype, blocks, n, k, dy, dx)
+
+
 # ---------------------------------------------------------------- large-grid forward (rtq_mm_*)
 @pytest.fixture(scope="module", params=["1", "2"], ids=["mm128", "mm64"])
 def ctx_mm(request):
