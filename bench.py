@@ -543,7 +543,7 @@ def model_bench(steps: int, warmup: int, cpu_seconds: float, no_cpu: bool) -> di
 
     t0 = time.perf_counter()
     spec = G.SyntheticSpec.preset("qwen3-0.6b", G.GGML_Q4_0)
-    image = spec.build()
+    image = spec.build(workers=max(1, min(16, os.cpu_count() or 1)))
     print(f"[model] built the synthetic GGUF in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
     g = G.GgufFile.from_bytes(image)
     ctx = rt.Context(0)

@@ -218,6 +218,12 @@ rtq_status rtq_model_forward_backward_packed(rtq_model* m, const int32_t* tokens
  * of the device memory free at the step, else recomputes.  The results are the same. */
 rtq_status rtq_model_set_checkpointing(rtq_model* m, int mode);
 int rtq_model_checkpointing(const rtq_model* m); /* 1 when the last step recomputed */
+/* Attention kernels of the step (the results agree within f32 rounding): 1 the fused kernels
+ * (online softmax, no probability matrix; head_dim 64 or 128 only), 0 the probability-matrix path
+ * (S, softmax, P V and their backward as separate launches, P [heads x t x t] kept per layer), -1
+ * (default) fused for packed batches and sequences of 4096 tokens or more. */
+rtq_status rtq_model_set_attention(rtq_model* m, int mode);
+int rtq_model_attention_fused(const rtq_model* m); /* 1 when the last step used the fused kernels */
 /* parity / debug: while layer >= 0 (-1: off), each step copies that block's tensors in the forward
  * (x, n1, inv1, q_raw, k_raw, v_raw, q, k, v, q_inv, k_inv, P [nh x t x t], o, h, n2, inv2, gate,
  * up, hm, y) and its backward (dy, dhm, dgate, dup, dn2, dh, d_o, dS, dq, dk, dv, dq_raw, dk_raw,

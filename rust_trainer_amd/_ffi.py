@@ -96,6 +96,8 @@ SIGNATURES = {
     "rtq_model_forward_backward_packed": (_i, [_p, _p, _i64, _p, _p, _p, _p, _p, _i64, _p, ctypes.POINTER(_i64)]),
     "rtq_model_set_checkpointing": (_i, [_p, _i]),
     "rtq_model_checkpointing": (_i, [_p]),
+    "rtq_model_set_attention": (_i, [_p, _i]),
+    "rtq_model_attention_fused": (_i, [_p]),
     "rtq_model_debug_capture": (_i, [_p, _i64]),
     "rtq_model_debug_tensor": (_i, [_p, ctypes.c_char_p, _p, _i64]),
     # GGUF v3 container

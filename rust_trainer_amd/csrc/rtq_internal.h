@@ -25,6 +25,16 @@ enum RtqModelKernel {
   KM_GEMM32G,
   KM_GEMM_Q8,
   KM_GEMM32_Q8,
+  KM_ATTN_FWD64,
+  KM_ATTN_FWD128,
+  KM_ATTN_DQ64,
+  KM_ATTN_DQ128,
+  KM_ATTN_DKV64,
+  KM_ATTN_DKV128,
+  KM_ATTN_MERGE_FWD,
+  KM_ATTN_MERGE_DQ,
+  KM_ATTN_MERGE_DKV,
+  KM_ATTN_BWD_D,
   KM_COUNT
 };
 

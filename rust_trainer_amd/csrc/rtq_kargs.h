@@ -325,6 +325,42 @@ struct MSoftArgs {
   int nlb;
 };
 
+// ---------------------------------------------------------------- fused attention
+// One work item = one wave: (head, 16-row block of queries, range of 64-key tiles) for the
+// forward and dQ passes; (KV head, 16-key block, range of (group head, 64-query tile) pairs
+// p = head_in_group * ceil(t / 64) + tile) for the dK / dV pass.  slot >= 0: the item covers part
+// of its block's range and writes a partial to part[slot] (merged by rtq_m_attn_merge in slot
+// order); slot < 0: it covers the whole range and writes the result.
+struct MAttnItem {
+  int head, blk, b0, b1, slot, pad0, pad1, pad2;
+};
+// one block whose items wrote partials to slots [s0, s0 + n)
+struct MAttnMerge {
+  int head, blk, s0, n;
+};
+struct MAttnArgs {
+  const float* q;   // [t][nh][hd] (rotated, row stride ldq)
+  const float* k;   // [t][nkv][hd] (ldk)
+  const float* v;   // [t][nkv][hd] (ldv)
+  float* o;         // forward output [t][nh][hd] (ldq)
+  float* lse;       // [nh][t]: log-sum-exp of each query row's scaled scores (forward out, backward in)
+  const float* dO;  // backward: gradient of o [t][nh][hd] (ldq)
+  float* D;         // backward: [nh][t], sum_e dO * o per query row
+  float* dq;        // [t][nh][hd] (ldq)
+  float* dk;        // [t][nkv][hd] (ldk)
+  float* dv;        // rows at ld_dv
+  float* part;      // partial slots
+  const MAttnItem* items;
+  const MAttnMerge* merges;
+  int n_items, n_merges;
+  const int32_t* seg;  // packed layout (or null): segment per token
+  const uint8_t* live; // and the 64 x 64 block liveness map (nlb blocks per side)
+  int nlb;
+  int t, nh, nkv, hd;
+  int64_t ldq, ldk, ldv, ld_dv;
+  float scale;
+};
+
 struct MGroupArgs {
   const float* dkh;  // [nh x t x hd] per-head gradients
   const float* dvh;

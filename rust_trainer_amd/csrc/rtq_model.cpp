@@ -24,6 +24,7 @@
 // backward.  Each member adapter stays addressable (rtq_model_lora_*), its B as a strided block.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -78,6 +79,7 @@ struct Layer {
 // stride qd + 2 kd), else q [t x qd], then k, then v; gu likewise gate | up.
 struct Cache {
   float *n1, *inv1, *qkv, *q, *k, *v, *q_inv, *k_inv, *P, *o, *h, *n2, *inv2, *gu, *hm;
+  float* lse;  // fused attention: log-sum-exp per (head, query) [nh x t] (P is then not kept)
 };
 
 // SplitMix64 + uniform of the reference Rng (src/tensor.rs:155-180)
@@ -125,6 +127,25 @@ struct rtq_model {
   int64_t nlb = 0;
   bool packed = false;
   bool rope_plain = false;  // the uploaded RoPE tables are for positions 0..rope_t-1
+  // fused attention (head_dim 64 or 128): work tables of the current layout, partial slots.
+  // attn_mode -1 (default): fused for packed layouts and sequences of 4096 tokens or more (where
+  // the probability matrix's t^2 memory and masked work dominate; below that the matrix path's
+  // larger GEMM tiles win on f32 MFMA), the probability-matrix path otherwise; 0 / 1 force one
+  // (rtq_model_set_attention).  attn_fused: this step's choice.
+  bool attn_hd_ok = false;
+  int attn_mode = -1;
+  bool attn_fused = false;
+  int64_t layout_fused = -1;  // attn_fused the step buffers were laid out for
+  float* attn_D = nullptr;  // [nh x t] dO . o per query row
+  void* attn_mem = nullptr;
+  size_t attn_cap = 0;
+  MAttnItem *it_fwd = nullptr, *it_kv = nullptr;
+  MAttnMerge *mg_fwd = nullptr, *mg_kv = nullptr;
+  int n_fwd = 0, n_kv = 0, n_mfwd = 0, n_mkv = 0;
+  float* attn_part = nullptr;
+  int64_t attn_t = -1;
+  bool attn_packed = false;
+  std::vector<int32_t> attn_seg;  // the segments the tables were built for
   // rtq_model_debug_capture: one layer's tensors copied during the step
   int64_t dbg_layer = -1;
   std::vector<std::pair<std::string, std::pair<float*, int64_t>>> dbg;
@@ -334,7 +355,10 @@ size_t step_layout(rtq_model* dst, int64_t T, int64_t N, int64_t caches, uintptr
   const rtq_model_config& c = dst->cfg;
   const int64_t d = c.n_embd, qd = c.n_head * c.head_dim, kd = c.n_head_kv * c.head_dim, ff = c.n_ff;
   const int64_t half = c.rope_dim / 2, L = c.n_layer;
-  const int64_t att = c.n_head * T * T, hdh = c.n_head * T * c.head_dim, nlb = (T + 63) / 64;
+  // the unfused attention keeps P [nh x t x t] per layer and needs dP and per-head dk, dv; the
+  // fused kernels keep only each row's log-sum-exp
+  const bool fz = dst->attn_fused;
+  const int64_t att = fz ? 1 : c.n_head * T * T, hdh = fz ? 1 : c.n_head * T * c.head_dim, nlb = (T + 63) / 64;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     const uintptr_t p = base + off;
@@ -350,7 +374,9 @@ size_t step_layout(rtq_model* dst, int64_t T, int64_t N, int64_t caches, uintptr
     fl(&k.n1, T * d), fl(&k.inv1, T), fl(&k.qkv, T * (qd + 2 * kd)), fl(&k.q, T * qd), fl(&k.k, T * kd);
     fl(&k.v, T * kd), fl(&k.q_inv, T * c.n_head), fl(&k.k_inv, T * c.n_head_kv), fl(&k.P, att), fl(&k.o, T * qd);
     fl(&k.h, T * d), fl(&k.n2, T * d), fl(&k.inv2, T), fl(&k.gu, T * 2 * ff), fl(&k.hm, T * ff);
+    fl(&k.lse, fz ? c.n_head * T : 1);
   }
+  fl(&dst->attn_D, fz ? c.n_head * T : 1);
   fl(&dst->dY, T * d), fl(&dst->dX, T * d), fl(&dst->mo, T * d), fl(&dst->f, T * d), fl(&dst->dhm, T * ff);
   fl(&dst->dgu, T * 2 * ff), fl(&dst->dn2, T * d), fl(&dst->dxu, T * d), fl(&dst->dh, T * d), fl(&dst->d_o, T * qd);
   fl(&dst->dP, att), fl(&dst->dq, T * qd), fl(&dst->dkh, hdh), fl(&dst->dvh, hdh), fl(&dst->dk, T * kd);
@@ -377,6 +403,7 @@ rtq_status choose_ckpt(rtq_model* m, int64_t t, int64_t n) {
   const int64_t T = std::max(t, m->t_cap), N = std::max<int64_t>(std::max(n, m->n_cap), 1);
   rtq_model probe;
   probe.cfg = m->cfg;
+  probe.attn_fused = m->attn_fused;
   const size_t keep = step_layout(&probe, T, N, m->cfg.n_layer, 0);
   size_t free_b = 0, total_b = 0;
   M_HIP(hipMemGetInfo(&free_b, &total_b));
@@ -387,7 +414,8 @@ rtq_status choose_ckpt(rtq_model* m, int64_t t, int64_t n) {
 
 rtq_status ensure_step(rtq_model* m, int64_t t, int64_t n) {
   const int64_t caches = m->ckpt ? 1 : m->cfg.n_layer;
-  if (t <= m->t_cap && n <= m->n_cap && caches == m->cache_cap) return RTQ_OK;
+  if (t <= m->t_cap && n <= m->n_cap && caches == m->cache_cap && m->layout_fused == (int64_t)m->attn_fused)
+    return RTQ_OK;
   const int64_t T = std::max(t, m->t_cap), N = std::max<int64_t>(std::max(n, m->n_cap), 1);
   if (m->step_mem) {
     M_HIP(hipStreamSynchronize(stream_of(m)));
@@ -401,6 +429,7 @@ rtq_status ensure_step(rtq_model* m, int64_t t, int64_t n) {
   m->t_cap = T;
   m->n_cap = N;
   m->cache_cap = caches;
+  m->layout_fused = m->attn_fused;
   m->rope_t = -1;
   return RTQ_OK;
 }
@@ -473,6 +502,139 @@ rtq_status upload_layout(rtq_model* m, const int32_t* seg, int64_t t) {
   return RTQ_OK;
 }
 
+// work tables of the fused attention for t tokens and the current layout (segments or null):
+// forward / dq items (head, 16-row query block, range of its live 64-key tiles) and dk / dv items
+// (KV head, 16-key block, range of its live (group head, 64-query tile) pairs), each block's list
+// cut into chunks of at most `chunk` live tiles so that there are about three items per SIMD; blocks
+// cut into several items get partial slots and a merge entry.  Rebuilt when t or the layout changes.
+rtq_status ensure_attn_plan(rtq_model* m, int64_t t, const int32_t* seg) {
+  const bool packed = seg != nullptr;
+  if (m->attn_t == t && m->attn_packed == packed &&
+      (!packed || std::equal(m->attn_seg.begin(), m->attn_seg.end(), seg)))
+    return RTQ_OK;
+  const rtq_model_config& c = m->cfg;
+  const int nh = (int)c.n_head, nkv = (int)c.n_head_kv, grp = nh / nkv;
+  const int64_t nqb = (t + 15) / 16, nkt = (t + 63) / 64, nlb = (t + 63) / 64;
+  // the block liveness of the layout (as upload_layout derives it)
+  std::vector<uint8_t> live;
+  if (packed) {
+    live.assign((size_t)(nlb * nlb), 0);
+    M_HIP(hipMemcpy(live.data(), m->live_d, live.size(), hipMemcpyDeviceToHost));
+  }
+  auto lv = [&](int64_t qb64, int64_t kb64) { return kb64 <= qb64 && (!packed || live[(size_t)(qb64 * nlb + kb64)]); };
+  std::vector<std::vector<int>> fl((size_t)nqb), kl((size_t)nqb);
+  int64_t fu = 0, ku = 0;
+  for (int64_t qb = 0; qb < nqb; qb++) {  // 16-row query block qb: key tiles up to its last row
+    const int64_t last = std::min(t - 1, qb * 16 + 15) / 64;
+    for (int64_t kt = 0; kt <= last; kt++)
+      if (lv(qb * 16 / 64, kt)) fl[(size_t)qb].push_back((int)kt);
+    fu += (int64_t)fl[(size_t)qb].size() * nh;
+  }
+  for (int64_t kb = 0; kb < nqb; kb++) {  // 16-key block kb: (group head, query tile) pairs at or after it
+    for (int hr = 0; hr < grp; hr++)
+      for (int64_t qt = kb * 16 / 64; qt < nkt; qt++)
+        if (lv(qt, kb * 16 / 64)) kl[(size_t)kb].push_back((int)(hr * nkt + qt));
+    ku += (int64_t)kl[(size_t)kb].size() * nkv;
+  }
+  const int64_t target = 3 * 4 * (int64_t)256;  // about three waves per SIMD
+  const int64_t cf = std::max<int64_t>(1, (fu + target - 1) / target), ck = std::max<int64_t>(1, (ku + target - 1) / target);
+  std::vector<MAttnItem> itf, itk;
+  std::vector<MAttnMerge> mf, mk;
+  int slots_f = 0, slots_k = 0;
+  auto cut = [](const std::vector<int>& L, int64_t chunk, int head, int blk, int& slots, std::vector<MAttnItem>& items,
+                std::vector<MAttnMerge>& merges) {
+    const int n = (int)((L.size() + chunk - 1) / chunk);
+    if (n == 0) return;
+    const int s0 = n > 1 ? slots : -1;
+    for (int i = 0; i < n; i++) {
+      const int a0 = L[(size_t)(i * chunk)], a1 = L[std::min(L.size(), (size_t)((i + 1) * chunk)) - 1] + 1;
+      items.push_back(MAttnItem{head, blk, a0, a1, n > 1 ? s0 + i : -1, 0, 0, 0});
+    }
+    if (n > 1) {
+      merges.push_back(MAttnMerge{head, blk, s0, n});
+      slots += n;
+    }
+  };
+  for (int h = 0; h < nh; h++)
+    for (int64_t qb = 0; qb < nqb; qb++) cut(fl[(size_t)qb], cf, h, (int)qb, slots_f, itf, mf);
+  for (int g = 0; g < nkv; g++)
+    for (int64_t kb = 0; kb < nqb; kb++) cut(kl[(size_t)kb], ck, g, (int)kb, slots_k, itk, mk);
+  const auto al = [](size_t b) { return (b + 255) / 256 * 256; };
+  const size_t slots = (size_t)std::max(slots_f, slots_k);
+  const size_t bytes = al(itf.size() * sizeof(MAttnItem)) + al(itk.size() * sizeof(MAttnItem)) +
+                       al(mf.size() * sizeof(MAttnMerge)) + al(mk.size() * sizeof(MAttnMerge)) +
+                       al(std::max<size_t>(slots, 1) * 32 * (size_t)c.head_dim * 4);
+  M_HIP(hipStreamSynchronize(stream_of(m)));
+  if (bytes > m->attn_cap) {
+    if (m->attn_mem) M_HIP(hipFree(m->attn_mem));
+    m->attn_mem = nullptr;
+    m->attn_cap = 0;
+    M_HIP(hipMalloc(&m->attn_mem, bytes));
+    m->attn_cap = bytes;
+  }
+  char* p = (char*)m->attn_mem;
+  m->it_fwd = (MAttnItem*)p;
+  p += al(itf.size() * sizeof(MAttnItem));
+  m->it_kv = (MAttnItem*)p;
+  p += al(itk.size() * sizeof(MAttnItem));
+  m->mg_fwd = (MAttnMerge*)p;
+  p += al(mf.size() * sizeof(MAttnMerge));
+  m->mg_kv = (MAttnMerge*)p;
+  p += al(mk.size() * sizeof(MAttnMerge));
+  m->attn_part = (float*)p;
+  M_HIP(hipMemcpy(m->it_fwd, itf.data(), itf.size() * sizeof(MAttnItem), hipMemcpyHostToDevice));
+  M_HIP(hipMemcpy(m->it_kv, itk.data(), itk.size() * sizeof(MAttnItem), hipMemcpyHostToDevice));
+  M_HIP(hipMemcpy(m->mg_fwd, mf.data(), mf.size() * sizeof(MAttnMerge), hipMemcpyHostToDevice));
+  M_HIP(hipMemcpy(m->mg_kv, mk.data(), mk.size() * sizeof(MAttnMerge), hipMemcpyHostToDevice));
+  m->n_fwd = (int)itf.size();
+  m->n_kv = (int)itk.size();
+  m->n_mfwd = (int)mf.size();
+  m->n_mkv = (int)mk.size();
+  m->attn_t = t;
+  m->attn_packed = packed;
+  m->attn_seg.assign(seg ? seg : seg, seg ? seg + t : seg);
+  return RTQ_OK;
+}
+
+MAttnArgs attn_args(rtq_model* m, Cache& k, int64_t t) {
+  const rtq_model_config& c = m->cfg;
+  MAttnArgs a{};
+  a.q = k.q;
+  a.k = k.k;
+  a.v = k.v;
+  a.o = k.o;
+  a.lse = k.lse;
+  a.D = m->attn_D;
+  a.part = m->attn_part;
+  a.seg = m->packed ? m->seg_d : nullptr;
+  a.live = m->packed ? m->live_d : nullptr;
+  a.nlb = (int)m->nlb;
+  a.t = (int)t;
+  a.nh = (int)c.n_head;
+  a.nkv = (int)c.n_head_kv;
+  a.hd = (int)c.head_dim;
+  a.ldq = c.n_head * c.head_dim;
+  a.ldk = a.ldv = c.n_head_kv * c.head_dim;
+  a.scale = 1.0f / sqrtf((float)c.head_dim);
+  return a;
+}
+
+// launches an item pass (one wave per item, four per workgroup)
+rtq_status attn_launch(rtq_model* m, int km, MAttnArgs a, const MAttnItem* items, int n) {
+  if (n <= 0) return RTQ_OK;
+  a.items = items;
+  a.n_items = n;
+  return rtq_model_launch(m->ctx, km, dim3((unsigned)((n + 3) / 4)), dim3(256), stream_of(m), &a);
+}
+// one thread per element of each merged block (16 x hd, or 2 x 16 x hd for dk and dv)
+rtq_status attn_merge(rtq_model* m, int km, MAttnArgs a, const MAttnMerge* mg, int n) {
+  if (n <= 0) return RTQ_OK;
+  a.merges = mg;
+  a.n_merges = n;
+  const int64_t nel = (km == KM_ATTN_MERGE_DKV ? 32 : 16) * (int64_t)a.hd;
+  return rtq_model_launch(m->ctx, km, dim3((unsigned)(n * ((nel + 255) / 256))), dim3(256), stream_of(m), &a);
+}
+
 // ---------------------------------------------------------------- one block
 // q, k, v raw rows in a cache's qkv buffer (or the gradient buffer of the same layout)
 struct QkvView {
@@ -523,6 +685,11 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* 
   M_TRY(rtq_model_launch(m->ctx, KM_QK_PREP, dim3((unsigned)((t * (nh + 2 * nkv) + 3) / 4)), dim3(256), stream_of(m),
                          &qa));
   const float scale = 1.0f / sqrtf((float)hd);
+  if (m->attn_fused) {  // fused: o and each row's log-sum-exp, no probability matrix
+    const MAttnArgs aa = attn_args(m, k, t);
+    M_TRY(attn_launch(m, hd == 64 ? KM_ATTN_FWD64 : KM_ATTN_FWD128, aa, m->it_fwd, m->n_fwd));
+    M_TRY(attn_merge(m, KM_ATTN_MERGE_FWD, aa, m->mg_fwd, m->n_mfwd));
+  } else {
   // S = (q scale) K^T per head (causal), softmax in place, O = P V
   M_TRY(k_gemm(m, t, t, hd, nh, Op{k.q, hd, qd, 1, 1}, Op{k.k, hd, 1, kd, (int)grp}, k.P, t * t, t, 1, scale, 1, 0));
   MSoftArgs sa{k.P, nullptr, nullptr, (int)t, (int)nh, scale, m->packed ? m->seg_d : nullptr,
@@ -530,6 +697,7 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* 
   M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX, dim3((unsigned)((t + 3) / 4), (unsigned)nh), dim3(256), stream_of(m),
                          &sa));
   M_TRY(k_gemm(m, t, hd, t, nh, Op{k.P, t * t, t, 1, 1}, Op{k.v, hd, kd, 1, (int)grp}, k.o, hd, qd, 1, 1.0f, 2, 0));
+  }
   M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LO]], k.o, t, m->mo));
   M_TRY(k_norm(m, x, m->mo, k.h, L.ffn_norm, k.n2, k.inv2, t, d, 0));  // h = x + attn, n2 = rmsnorm(h)
   float *g, *u;
@@ -570,6 +738,20 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
   M_TRY(k_norm_bwd(m, k.h, L.ffn_norm, k.inv2, m->dn2, dy, m->dh, t, d));  // dh = dy + rmsnorm_backward
   // Attention::backward (src/attention.rs:243-355)
   M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LO]], k.o, m->dh, t, m->d_o));
+  const QkvView dv = qkv_view(m, L, m->dqkv, t);
+  if (m->attn_fused) {  // D = dO . o; dq over key tiles; dk, dv over (group head, query tile) pairs
+    MAttnArgs aa = attn_args(m, k, t);
+    aa.dO = m->d_o;
+    aa.dq = m->dq;
+    aa.dk = m->dk;
+    aa.dv = dv.v;
+    aa.ld_dv = dv.ldv;
+    M_TRY(rtq_model_launch(m->ctx, KM_ATTN_BWD_D, dim3((unsigned)((t * nh + 3) / 4)), dim3(256), stream_of(m), &aa));
+    M_TRY(attn_launch(m, hd == 64 ? KM_ATTN_DQ64 : KM_ATTN_DQ128, aa, m->it_fwd, m->n_fwd));
+    M_TRY(attn_merge(m, KM_ATTN_MERGE_DQ, aa, m->mg_fwd, m->n_mfwd));
+    M_TRY(attn_launch(m, hd == 64 ? KM_ATTN_DKV64 : KM_ATTN_DKV128, aa, m->it_kv, m->n_kv));
+    M_TRY(attn_merge(m, KM_ATTN_MERGE_DKV, aa, m->mg_kv, m->n_mkv));
+  } else {
   M_TRY(k_gemm(m, t, t, hd, nh, Op{m->d_o, hd, qd, 1, 1}, Op{k.v, hd, 1, kd, (int)grp}, m->dP, t * t, t, 1, 1.0f, 1,
                0));  // dP = dO V^T
   MSoftArgs sa{nullptr, k.P, m->dP, (int)t, (int)nh, scale, m->packed ? m->seg_d : nullptr,
@@ -582,10 +764,10 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
       {t, hd, t, nh, Op{m->dP, t * t, t, 1, 1}, Op{k.k, hd, kd, 1, (int)grp}, m->dq, hd, qd, 1, 1.0f, 2, 0},
       {t, hd, t, nh, Op{m->dP, t * t, 1, t, 1}, Op{k.q, hd, qd, 1, 1}, m->dkh, t * hd, hd, 1, 1.0f, 3, 0}};
   M_TRY(k_gemm_group(m, jobs, 3));
-  const QkvView dv = qkv_view(m, L, m->dqkv, t);
   MGroupArgs gsa{m->dkh, m->dvh, m->dk, dv.v, (int)t, (int)nh, (int)nkv, (int)hd, dv.ldv};
   M_TRY(rtq_model_launch(m->ctx, KM_GROUP_SUM, dim3((unsigned)std::min<int64_t>((t * kd + 255) / 256, 4096)),
                          dim3(256), stream_of(m), &gsa));
+  }
   const MQkArgs qa = qk_args(m, L, k, t);
   M_TRY(rtq_model_launch(m->ctx, KM_QK_BWD, dim3((unsigned)((t * (nh + nkv) + 3) / 4)), dim3(256), stream_of(m), &qa));
   if (L.qkv_fused) {
@@ -649,7 +831,8 @@ rtq_status dbg_forward(rtq_model* m, int l, int64_t t, const float* x, const flo
   M_TRY(dbg_put(m, "v", k.v, t, kd, kd));
   M_TRY(dbg_put(m, "q_inv", k.q_inv, 1, t * c.n_head, t * c.n_head));
   M_TRY(dbg_put(m, "k_inv", k.k_inv, 1, t * c.n_head_kv, t * c.n_head_kv));
-  M_TRY(dbg_put(m, "P", k.P, c.n_head * t, t, t));
+  if (m->attn_fused) M_TRY(dbg_put(m, "lse", k.lse, c.n_head, t, t));
+  else M_TRY(dbg_put(m, "P", k.P, c.n_head * t, t, t));
   M_TRY(dbg_put(m, "o", k.o, t, qd, qd));
   M_TRY(dbg_put(m, "h", k.h, t, d, d));
   M_TRY(dbg_put(m, "n2", k.n2, t, d, d));
@@ -675,7 +858,7 @@ rtq_status dbg_backward(rtq_model* m, int l, int64_t t, const float* dy, const f
   M_TRY(dbg_put(m, "dn2", m->dn2, t, d, d));
   M_TRY(dbg_put(m, "dh", m->dh, t, d, d));
   M_TRY(dbg_put(m, "d_o", m->d_o, t, qd, qd));
-  M_TRY(dbg_put(m, "dS", m->dP, c.n_head * t, t, t));
+  if (!m->attn_fused) M_TRY(dbg_put(m, "dS", m->dP, c.n_head * t, t, t));
   M_TRY(dbg_put(m, "dq", m->dq, t, qd, qd));
   M_TRY(dbg_put(m, "dk", m->dk, t, kd, kd));
   M_TRY(dbg_put(m, "dv", dv.v, t, kd, dv.ldv));
@@ -887,6 +1070,7 @@ rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out)
   m->ctx = ctx;
   m->cfg = cfg;
   m->rope_factors = factors;
+  m->attn_hd_ok = cfg.head_dim == 64 || cfg.head_dim == 128;  // the fused attention kernels' head sizes
   const rtq_model_config& c = m->cfg;
   rtq_status st = RTQ_OK;
   auto fail_out = [&](rtq_status s) {
@@ -925,6 +1109,7 @@ void rtq_model_destroy(rtq_model* m) {
   for (void* p : m->owned) (void)hipFree(p);
   if (m->step_mem) (void)hipFree(m->step_mem);
   if (m->hpk_mem) (void)hipFree(m->hpk_mem);
+  if (m->attn_mem) (void)hipFree(m->attn_mem);
   delete m;
 }
 
@@ -1154,11 +1339,13 @@ rtq_status step(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* p
     for (int64_t i = 0; i < t; i++)
       if (segments[i] < 0) return rtq_fail(RTQ_ERR_INVALID, "segment %lld is negative", (long long)i);
   M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
+  m->attn_fused = m->attn_hd_ok && (m->attn_mode == 1 || (m->attn_mode < 0 && (segments || t >= 4096)));
   M_TRY(choose_ckpt(m, t, n));
   M_TRY(ensure_step(m, t, n));
   M_TRY(ensure_hpk(m, t));
   M_TRY(ensure_rope(m, t, positions));
   M_TRY(upload_layout(m, segments, t));
+  if (m->attn_fused) M_TRY(ensure_attn_plan(m, t, segments));
   hipStream_t st = stream_of(m);
   const int64_t d = c.n_embd;
   M_HIP(hipMemcpyAsync(m->tok_d, tokens, (size_t)t * 4, hipMemcpyHostToDevice, st));
@@ -1225,6 +1412,14 @@ rtq_status rtq_model_set_checkpointing(rtq_model* m, int mode) {
 }
 
 int rtq_model_checkpointing(const rtq_model* m) { return m ? (m->ckpt ? 1 : 0) : -1; }
+
+rtq_status rtq_model_set_attention(rtq_model* m, int mode) {
+  if (!m || mode < -1 || mode > 1) return rtq_fail(RTQ_ERR_INVALID, "bad model/attention mode %d", mode);
+  m->attn_mode = mode;
+  return RTQ_OK;
+}
+
+int rtq_model_attention_fused(const rtq_model* m) { return m ? (m->attn_fused ? 1 : 0) : -1; }
 
 rtq_status rtq_model_debug_capture(rtq_model* m, int64_t layer) {
   if (!m || layer < -1 || layer >= m->cfg.n_layer) return rtq_fail(RTQ_ERR_INVALID, "bad model/layer");

@@ -565,3 +565,5 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_lora_mask(MMaskArgs a) {
     if (!keep) a.gb[i] = 0.0f;
   }
 }
+
+#include "rtq_attn.hip"

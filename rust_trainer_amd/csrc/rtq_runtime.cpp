@@ -163,7 +163,10 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_m_rmsnorm",        "rtq_m_rmsnorm_bwd",    "rtq_m_qk_prep",        "rtq_m_qk_bwd",
     "rtq_m_gemm",           "rtq_m_softmax",        "rtq_m_softmax_bwd",    "rtq_m_group_sum",
     "rtq_m_swiglu",         "rtq_m_swiglu_bwd",     "rtq_m_add",            "rtq_m_gemm32",
-    "rtq_m_lora_mask",      "rtq_m_gemm32g",        "rtq_m_gemm_q8",        "rtq_m_gemm32_q8"};
+    "rtq_m_lora_mask",      "rtq_m_gemm32g",        "rtq_m_gemm_q8",        "rtq_m_gemm32_q8",
+    "rtq_m_attn_fwd64",     "rtq_m_attn_fwd128",    "rtq_m_attn_dq64",      "rtq_m_attn_dq128",
+    "rtq_m_attn_dkv64",     "rtq_m_attn_dkv128",    "rtq_m_attn_merge_fwd", "rtq_m_attn_merge_dq",
+    "rtq_m_attn_merge_dkv", "rtq_m_attn_bwd_d"};
 
 struct TimedLaunch {
   int kid;

@@ -166,6 +166,19 @@ class GpuModel:
         mode = -1 if on is None else (1 if on else 0)
         _ffi.check(_ffi.lib().rtq_model_set_checkpointing(self._h, mode), "rtq_model_set_checkpointing")
 
+    @property
+    def fused_attention(self):
+        """Attention kernels: True the fused kernels (no probability matrix; head_dim 64 / 128),
+        False the probability-matrix path, None (default) chosen per step (fused for packed batches
+        and 4096+ tokens).  Reading it gives the last step's choice (None before any step)."""
+        v = int(_ffi.lib().rtq_model_attention_fused(self._h))
+        return None if not getattr(self, "_stepped", False) else bool(v)
+
+    @fused_attention.setter
+    def fused_attention(self, on) -> None:
+        mode = -1 if on is None else (1 if on else 0)
+        _ffi.check(_ffi.lib().rtq_model_set_attention(self._h, mode), "rtq_model_set_attention")
+
     def debug_capture(self, layer: int) -> None:
         """Copy block ``layer``'s tensors during each step (-1: off); read them with ``debug_tensor``."""
         _ffi.check(_ffi.lib().rtq_model_debug_capture(self._h, layer), "rtq_model_debug_capture")

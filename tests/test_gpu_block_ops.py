@@ -76,11 +76,16 @@ def check_block(ctx, g, model, m, layer, t, seg, lora_map, report):
     d, nh, nkv, hd, ff = c["n_embd"], c["n_head"], c["n_head_kv"], c["head_dim"], c["n_ff"]
     qd, kd = nh * hd, nkv * hd
     shapes = dict(x=(t, d), n1=(t, d), inv1=(t,), q_raw=(t, qd), k_raw=(t, kd), v_raw=(t, kd), q=(t, qd), k=(t, kd),
-                  v=(t, kd), q_inv=(t * nh,), k_inv=(t * nkv,), P=(nh, t, t), o=(t, qd), h=(t, d), n2=(t, d),
+                  v=(t, kd), q_inv=(t * nh,), k_inv=(t * nkv,), o=(t, qd), h=(t, d), n2=(t, d),
                   inv2=(t,), gate=(t, ff), up=(t, ff), hm=(t, ff), y=(t, d), dy=(t, d), dhm=(t, ff), dgate=(t, ff),
                   dup=(t, ff), dn2=(t, d), dh=(t, d), d_o=(t, qd), dq=(t, qd), dk=(t, kd), dv=(t, kd),
                   dq_raw=(t, qd), dk_raw=(t, kd), dn1=(t, d), dx=(t, d))
     T = {n: model.debug_tensor(n, s) for n, s in shapes.items()}
+    fused = model.fused_attention  # fused attention: each row's log-sum-exp is kept instead of P
+    if fused:
+        T["lse"] = model.debug_tensor("lse", (nh, t))
+    else:
+        T["P"] = model.debug_tensor("P", (nh, t, t))
     L = m["layers"][layer]
     ops = O.BlockOps(m)
     errs = {}
@@ -102,7 +107,17 @@ def check_block(ctx, g, model, m, layer, t, seg, lora_map, report):
     if seg is not None:
         s = np.asarray(seg)
         allowed &= (s[None, :] == 0) | (s[None, :] == s[:, None])
-    errs["P"] = rel(T["P"], P, np.broadcast_to(allowed, P.shape))
+    if fused:
+        # the device's probabilities p = exp((q scale) . k - lse) from its own q, k and lse (f64)
+        qs = (T["q"].reshape(t, nh, hd) * np.float32(1.0 / np.sqrt(hd))).astype(np.float64)
+        kk = T["k"].reshape(t, nkv, hd).astype(np.float64)
+        P_dev = np.zeros((nh, t, t), np.float32)
+        for hh in range(nh):
+            sc_ = qs[:, hh, :] @ kk[:, hh // (nh // nkv), :].T
+            P_dev[hh] = np.where(allowed, np.exp(sc_ - T["lse"][hh][:, None]), 0.0)
+    else:
+        P_dev = np.where(np.broadcast_to(allowed, T["P"].shape), T["P"], 0.0).astype(np.float32)
+    errs["P"] = rel(P_dev, P, np.broadcast_to(allowed, P.shape))
     errs["o"] = rel(T["o"], o)
     codes_exact(ctx, wt["o"], T["o"], t)
     errs["h"] = rel(T["h"], T["x"] + lin_fwd(L, "o", T["o"], t))
@@ -125,9 +140,8 @@ def check_block(ctx, g, model, m, layer, t, seg, lora_map, report):
     errs["dh"] = rel(T["dh"], T["dy"] + ops.rmsnorm_backward(T["h"], L["ffn_norm"], T["inv2"], T["dn2"]))
     d_o, *grads["o"] = lin_bwd(L, "o", T["o"], T["dh"], t)
     errs["d_o"] = rel(T["d_o"], d_o)
-    # the device leaves blocks of a packed layout where no pair may attend unwritten: only the
-    # allowed entries are its probabilities
-    P_dev = np.where(np.broadcast_to(allowed, T["P"].shape), T["P"], 0.0).astype(np.float32)
+    # (the unfused device path leaves blocks of a packed layout where no pair may attend unwritten:
+    # only the allowed entries are its probabilities)
     dq, dk, dv = ops.attention_backward(T["q"], T["k"], T["v"], P_dev, T["d_o"], seg)
     errs["dq"], errs["dk"], errs["dv"] = rel(T["dq"], dq), rel(T["dk"], dk), rel(T["dv"], dv)
     dq_raw, dk_raw = ops.qk_backward(L["q_norm"], L["k_norm"], cos_, sin_, T["q_raw"], T["k_raw"], T["q_inv"],
@@ -185,6 +199,22 @@ def test_config2_block_ops_match_oracle(ctx, wtype):
         model.forward_backward(toks, [rt.Target(int(p), int(k)) for p, k in zip(pos, tok)], wts)
         print(f"layer {layer} (recompute: {model.checkpointing})")
         check_block(ctx, g, model, m, layer, t, None, {}, {})
+    model.close()
+
+
+def test_config2_block_ops_fused_attention_match_oracle(ctx):
+    """the configs[2] block with the fused attention kernels forced (the default picks them for
+    packed batches and 4096+ tokens only)"""
+    spec = tiny_spec(O.Q4_K, **CONFIG2_BLOCK)
+    g, model, m = build(ctx, spec, 16, 32.0, ALL)
+    model.fused_attention = True
+    t, n = 512, 256
+    toks, pos, tok = sequence(spec.n_vocab, t, n, 9)
+    model.debug_capture(1)
+    model.zero_grad()
+    model.forward_backward(toks, [rt.Target(int(p), int(k)) for p, k in zip(pos, tok)], np.full(n, 1.0 / n, np.float32))
+    assert model.fused_attention is True
+    check_block(ctx, g, model, m, 1, t, None, {}, {})
     model.close()
 
 
@@ -248,10 +278,12 @@ def test_config3_block_ops_packed_match_oracle(ctx):
     model.close()
 
 
-def test_config4_block_ops_match_oracle_recomputed(ctx):
+@pytest.mark.parametrize("fused", [None, True])
+def test_config4_block_ops_match_oracle_recomputed(ctx, fused):
     spec = tiny_spec(O.Q8_0, n_layer=2, arch="llama", tied=False, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128,
                      rope_dim=128, n_ff=14336, n_vocab=4096, rope_base=5e5)
     g, model, m = build(ctx, spec, 64, 128.0, ALL)
+    model.fused_attention = fused
     t, n = 2048, 1024
     toks, pos, tok = sequence(spec.n_vocab, t, n, 17)
     model.checkpointing = True

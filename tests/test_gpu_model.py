@@ -33,9 +33,10 @@ def rel_err(got, want):
     return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
 
 
-def run_both(ctx, spec, rank=4, alpha=8.0, t=40, n=16, seed=5, weights=True):
+def run_both(ctx, spec, rank=4, alpha=8.0, t=40, n=16, seed=5, weights=True, fused=None):
     g = G.GgufFile.from_bytes(spec.build())
     model = rt.GpuModel.from_gguf(g, ctx=ctx)
+    model.fused_attention = fused
     model.attach_lora(rank, alpha, seed=1)
     lora = adapters(g, rank, alpha)
     for i in range(model.lora_count()):
@@ -90,11 +91,14 @@ def noise_floor(g, lora, alpha, toks, pos, tok, wts, seeds=4):
     return fl, fg
 
 
-@pytest.mark.parametrize("t", [40, 37])
-def test_model_step_f32_weights_matches_oracle(ctx, t):
+@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("t", [40, 37, 150])
+def test_model_step_f32_weights_matches_oracle(ctx, t, fused):
     """F32 weights: no activation quantisation, so the step is smooth and the 1e-3 bar holds
-    (t = 37: attention rows of odd length, so the attention products take single-float loads)"""
-    model, logp, hits, lp_o, hits_o, grads = run_both(ctx, tiny_spec(O.F32, n_layer=2), t=t)
+    (t = 37: attention rows of odd length, so the attention products take single-float loads;
+    t = 150: several key tiles), with either attention path"""
+    model, logp, hits, lp_o, hits_o, grads = run_both(ctx, tiny_spec(O.F32, n_layer=2), t=t, fused=fused)
+    assert model.fused_attention is fused
     assert rel_err(logp, lp_o) <= TOL and hits == hits_o
     assert grad_err(model, grads) <= TOL
     model.close()

@@ -37,11 +37,12 @@ def all_grads(model):
     return [np.concatenate([ga.ravel(), gb.ravel()]) for ga, gb in (model.lora(i)[2:] for i in range(model.lora_count()))]
 
 
-@pytest.mark.parametrize("wtype", [O.F32, O.Q4_0, O.Q6_K])
-def test_checkpointing_changes_nothing(ctx, wtype):
+@pytest.mark.parametrize("wtype,fused", [(O.F32, False), (O.Q4_0, False), (O.Q6_K, False), (O.Q4_0, True)])
+def test_checkpointing_changes_nothing(ctx, wtype, fused):
     spec = tiny_spec(wtype, n_layer=3)
     g = G.GgufFile.from_bytes(spec.build())
     model, _ = model_with(ctx, g, 4, 8.0)
+    model.fused_attention = fused
     toks, pos, tok = sequence(spec.n_vocab, 48, 20, 3)
     targets = [rt.Target(int(p), int(k)) for p, k in zip(pos, tok)]
     wts = np.full(20, 0.05, np.float32)
@@ -77,9 +78,11 @@ def packed_batch(V, prompt_len, extras, seed):
 MIXED = "Q4_K/Q6_K"  # configs[3]'s mix: Q4_K attention / gate / up, Q6_K down and output
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("wtype", [O.F32, O.Q4_0, MIXED])
-def test_packed_batch_equals_separate_examples(ctx, wtype):
-    """F32 weights: the reference's 1e-5 bars (tests/gradcheck.rs:325-336).  Quantised weights: the
+def test_packed_batch_equals_separate_examples(ctx, wtype, fused):
+    """Both sides on the same attention kernels (either path).  F32 weights: the reference's 1e-5
+    bars (tests/gradcheck.rs:325-336).  Quantised weights: the
     first example, whose tokens sit at the same indices in both layouts, gives bit-identical
     log-probs; the others attend over keys at shifted indices, so the device's attention sums group
     their terms differently (wave-tree and MFMA k-group order), and a one-ulp difference can move a
@@ -95,6 +98,7 @@ def test_packed_batch_equals_separate_examples(ctx, wtype):
         spec = tiny_spec(wtype, n_layer=2, n_vocab=500)
     g = G.GgufFile.from_bytes(spec.build())
     model, _ = model_with(ctx, g, 3, 6.0)
+    model.fused_attention = fused  # the same attention kernels for the packed batch and the examples
     # three examples sharing a 70-token prompt (more than one 64-token block), one answer starting
     # inside the shared part (tests/gradcheck.rs:289-295)
     seqs = packed_batch(spec.n_vocab, 70, [(50, 72), (90, 71), (30, 69)], 44)
@@ -127,10 +131,12 @@ def test_packed_batch_equals_separate_examples(ctx, wtype):
     model.close()
 
 
-def test_packed_step_matches_oracle(ctx):
+@pytest.mark.parametrize("fused", [True, False])
+def test_packed_step_matches_oracle(ctx, fused):
     spec = tiny_spec(O.F32, n_layer=2, n_vocab=400)
     g = G.GgufFile.from_bytes(spec.build())
     model, lora = model_with(ctx, g, 4, 8.0)
+    model.fused_attention = fused
     seqs = packed_batch(spec.n_vocab, 40, [(30, 41), (55, 38), (12, 45), (70, 60)], 9)
     p = pack([s for s, _ in seqs])
     targets = []
