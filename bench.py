@@ -128,6 +128,11 @@ def measured_traffic(name: str):
 
 # ---------------------------------------------------------------- configs[1] sweep
 SWEEP_SHAPES = {"q_proj": (2048, 1024), "kv_proj": (1024, 1024), "down_proj": (1024, 3072), "lm_head": (151936, 1024)}
+# the merged projections of the configs[3] / configs[4] blocks (q|k|v and gate|up are one launch in the
+# step), for --case runs only: (rows, cols, LoRA rank)
+BLOCK_SHAPES = {"llama_qkv": (6144, 4096, 64), "llama_o": (4096, 4096, 64), "llama_gate_up": (28672, 4096, 64),
+                "llama_down": (4096, 14336, 64), "llama_head": (128256, 4096, 0), "qwen4b_qkv": (6144, 2560, 16),
+                "qwen4b_gate_up": (19456, 2560, 16), "qwen4b_down": (2560, 9728, 16)}
 SWEEP_TYPES = {"Q8_0": 8, "Q4_K": 12, "Q6_K": 14, "Q4_0": 2}
 SWEEP_T = (1, 16, 256, 2048)
 BLOCK = {2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
@@ -166,8 +171,11 @@ def sweep(cases: list[tuple[str, str, int]], calls_min: int) -> None:
     weights_cache: dict = {}
     for fmt, shape, t in cases:
         wtype = SWEEP_TYPES[fmt]
-        n, k = SWEEP_SHAPES[shape]
-        r = 0 if shape == "lm_head" else R
+        if shape in BLOCK_SHAPES:
+            n, k, r = BLOCK_SHAPES[shape]
+        else:
+            n, k = SWEEP_SHAPES[shape]
+            r = 0 if shape == "lm_head" else R
         key = (fmt, shape)
         # N(0, 0.02) weights, N(0, 1) activations and gradients from torch's generators (seeded):
         # the reference Rng's stream is not needed for timing, and is slow at the LM head's sizes
@@ -213,7 +221,7 @@ def sweep(cases: list[tuple[str, str, int]], calls_min: int) -> None:
                                                          ss["dx"].data_ptr(), st), "backward_input")
 
         ncalls = max(calls_min, nsets)
-        out = {"sweep": "configs[1]", "format": fmt, "shape": shape, "rows": n, "cols": k, "tokens": t,
+        out = {"sweep": "configs[1]" if shape in SWEEP_SHAPES else "block", "format": fmt, "shape": shape, "rows": n, "cols": k, "tokens": t,
                "lora_rank": r, "operand_sets": nsets, "calls": ncalls}
         for name, fn in (("forward", fwd), ("backward", bwd)):
             with torch.cuda.stream(side):

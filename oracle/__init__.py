@@ -91,6 +91,7 @@ def lib() -> ctypes.CDLL:
             "or_frozen_backward_input": (_i, [_i, _p, _i64, _i64, _p, _i64, _p, _i]),
             "or_frozen_row": (_i, [_i, _p, _i64, _i64, _i64, _p]),
             "or_dot": (_f, [_p, _p, _i64]),
+            "or_pin_threads": (_i, [_i]),
             "or_matmul_nt": (None, [_p, _p, _i64, _i64, _i64, _p, _i]),
             "or_matmul_nn": (None, [_p, _p, _i64, _i64, _i64, _p, _i]),
             "or_matmul_tn_acc": (None, [_p, _p, _p, _i64, _i64, _i64, _i]),
@@ -340,6 +341,24 @@ def lm_head(wtype, wblocks, V, d, norm, x, pos, tok, wts=None, eps=1e-6, off=0.0
                             _ptr(pos), _ptr(tok), _ptr(None if wts is None else _f32(wts)), n, chunk, _ptr(logp),
                             ctypes.byref(hits), _ptr(dx), nthreads), "lm_head")
     return logp, hits.value, dx
+
+
+def pin_threads(n: int) -> int:
+    """Pins an OpenMP team of ``n`` (and the pool threads later teams reuse) to the process's allowed
+    CPUs, one each, for timed runs; returns the number of allowed CPUs (-1: affinity unavailable)."""
+    return lib().or_pin_threads(n)
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the timed baselines' records."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def round_f16(x: float) -> float:

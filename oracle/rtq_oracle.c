@@ -22,10 +22,12 @@
  *   Linear                  f64 closed forms of src/linear.rs:84-118 and finite differences.
  * Parity against rie-core itself is unpinned: rie-core is not in this container.
  */
+#define _GNU_SOURCE
 #include "rtq_oracle.h"
 
 #include <math.h>
 #include <omp.h>
+#include <sched.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -540,6 +542,28 @@ static inline void axpy(float alpha, const float* x, float* y, int64_t n) {
 }
 
 static int nthr(int n) { return n > 0 ? n : 1; }
+
+/* Timing support (not part of the restated algorithm): pins the threads of an OpenMP team of n -
+   the calling thread and the pool threads that every later team of at most n reuses - one each to
+   the CPUs of the process's affinity mask, in order, so timed runs do not migrate.  Returns the
+   number of CPUs in the mask, or -1 if the mask cannot be read or set. */
+int or_pin_threads(int n) {
+  cpu_set_t allowed;
+  if (sched_getaffinity(0, sizeof allowed, &allowed) != 0) return -1;
+  int cpus[CPU_SETSIZE], ncpu = 0;
+  for (int c = 0; c < CPU_SETSIZE; c++)
+    if (CPU_ISSET(c, &allowed)) cpus[ncpu++] = c;
+  if (ncpu == 0) return -1;
+  int failed = 0;
+#pragma omp parallel num_threads(nthr(n)) reduction(+ : failed)
+  {
+    cpu_set_t one;
+    CPU_ZERO(&one);
+    CPU_SET(cpus[omp_get_thread_num() % ncpu], &one);
+    failed += sched_setaffinity(0, sizeof one, &one) != 0;
+  }
+  return failed ? -1 : ncpu;
+}
 
 /* out[m x n] = a[m x k] . b^T, b [n x k]  (src/tensor.rs:61-79) */
 void or_matmul_nt(const float* a, const float* b, int64_t m, int64_t k, int64_t n, float* out, int nthreads) {

@@ -92,6 +92,7 @@ int or_frozen_row(int wtype, const void* w, int64_t n, int64_t k, int64_t r, flo
 
 /* ---- dense primitives (src/tensor.rs:24-120) ---- */
 float or_dot(const float* a, const float* b, int64_t n);
+int or_pin_threads(int n); /* timing support: pin an OpenMP team of n to the allowed CPUs */
 void or_matmul_nt(const float* a, const float* b, int64_t m, int64_t k, int64_t n, float* out, int nthreads);
 void or_matmul_nn(const float* a, const float* b, int64_t m, int64_t k, int64_t n, float* out, int nthreads);
 void or_matmul_tn_acc(float* out, const float* a, const float* b, int64_t k, int64_t m, int64_t n,

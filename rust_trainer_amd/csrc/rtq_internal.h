@@ -47,9 +47,11 @@ int rtq_ctx_device_id(const rtq_ctx* c);
 // same x (0: not kept for this weight - dense, or slicings that differ)
 int64_t rtq_lora_partial_floats(const rtq_weight* w, int64_t t, int64_t r);
 // rtq_linear_forward_d that also leaves the LoRA-down partials in hp_keep (null or too small a
-// weight: as rtq_linear_forward_d)
+// weight: as rtq_linear_forward_d); rb (or null): the adapter's block-diagonal structure, so each
+// row's up-projection reads its own member's ranks only (B is zero elsewhere)
 rtq_status rtq_linear_forward_keep_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
-                                     const float* x, int64_t t, float* y, float* hp_keep, void* stream);
+                                     const RankBlocks* rb, const float* x, int64_t t, float* y, float* hp_keep,
+                                     void* stream);
 // rtq_linear_backward_d for a block-diagonal adapter over row-concatenated weights (rb; null: a
 // plain adapter): gb and g = s dy.B only inside rb's blocks (gb outside them is left untouched).
 // Quantised weights only; a dense weight computes every pair (the caller clears gb outside the

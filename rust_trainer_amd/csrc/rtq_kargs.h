@@ -93,6 +93,14 @@ struct DenseArgs {
 // ---------------------------------------------------------------- forward GEMM
 // y[t][n] = sum_b d_w[n][b] d_x[t][b] isum_b(t, n)  (+ bias[n]) (+ s * sum_j h[t][j] B[n][j])
 // K-quants: sum over super-blocks of (d d_x) S1 - (dmin d_x) S2 (Q4_K) or (d d_x) S (Q6_K)
+// Block-diagonal adapter of row-concatenated weights (a fused q|k|v or gate|up projection):
+// member m owns weight rows [row0[m], row0[m] + nrow[m]) and ranks [col0[m], col0[m] + r[m]) (r 0:
+// not adapted); only those (row, rank) pairs of B and gb exist.  nm = 0: one plain adapter.
+struct RankBlocks {
+  int nm;
+  int row0[3], nrow[3], col0[3], r[3];
+};
+
 struct FwdArgs {
   const void* wq;       // quant codes, device layout
   const uint16_t* wd;   // fp16 scales (K-quants: sub-block scale words), device layout
@@ -114,18 +122,11 @@ struct FwdArgs {
   int32_t* isums;       // debug: [T][N][K/32] (Q4_0, Q8_0), [T][N][K/256][2] (Q4_K: S1, S2),
                         // [T][N][K/256] (Q6_K: S), or null
   const uint16_t* xdh;  // fp16 activation scales, layout of xd (rtq_mm_*)
+  RankBlocks rb;        // LoRA B's block structure: a row's up-projection reads its member's ranks only
 };
 
 // ---------------------------------------------------------------- backward
 // rtq_bwd_prep: partials of h = x . A^T and of dy . B per 256-column slice (src/linear.rs:106-111)
-// Block-diagonal adapter of row-concatenated weights (a fused q|k|v or gate|up projection):
-// member m owns weight rows [row0[m], row0[m] + nrow[m]) and ranks [col0[m], col0[m] + r[m]) (r 0:
-// not adapted); only those (row, rank) pairs of B and gb exist.  nm = 0: one plain adapter.
-struct RankBlocks {
-  int nm;
-  int row0[3], nrow[3], col0[3], r[3];
-};
-
 struct BwdPrepArgs {
   const float* x;
   const float* A;

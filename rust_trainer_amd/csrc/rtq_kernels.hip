@@ -248,6 +248,25 @@ __device__ __forceinline__ bool rb_any(const RankBlocks& b, int n0, int n1, int 
   return any;
 }
 
+// ranks [lo, hi) that the LoRA up-projection of rows [n0, n1) reads: the span of their members'
+// rank windows (every rank of a plain adapter; empty when no member row is adapted)
+__device__ __forceinline__ void rb_span(const RankBlocks& b, int r, int n0, int n1, int& lo, int& hi) {
+  if (b.nm == 0) {
+    lo = 0;
+    hi = r;
+    return;
+  }
+  lo = r;
+  hi = 0;
+#pragma unroll
+  for (int m = 0; m < 3; m++)
+    if (m < b.nm && b.r[m] > 0 && max(n0, b.row0[m]) < min(n1, b.row0[m] + b.nrow[m])) {
+      lo = min(lo, b.col0[m]);
+      hi = max(hi, b.col0[m] + b.r[m]);
+    }
+  hi = max(hi, lo);
+}
+
 // LoRA-down partial product over a 256-column slice, by one 256-thread workgroup (f32 MFMA):
 //   P[t][j] = sum over k in [k0, k0 + 256) of S[t][k] * M[j * ldm + k],  t in [t0, t0 + 16), j < r
 // (h = x . A^T, src/linear.rs:85,106).  Written to out[(t * r + j) * pstride + pidx] (slice index
@@ -661,7 +680,11 @@ __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
   FwdSlot<FMT, TT, RG> sl[D];
   const bool lead = blockIdx.z == 0;
   const bool lora = a.hp && lead;
-  const bool lora_lds = lora && a.r <= RTQ_LDS_RANK;
+  // the up-projection of row group rg reads the ranks of its member of a block-diagonal adapter
+  // only (the other B entries are zeros); the tile's rank span is staged in LDS when it fits
+  int span0 = 0, span1 = 0;
+  if (lora) rb_span(a.rb, a.r, rg0 * 16, min((rg0 + RG) * 16, a.N), span0, span1);
+  const bool lora_lds = lora && span1 - span0 <= RTQ_LDS_RANK;
 
   auto issue = [&](FwdSlot<FMT, TT, RG>& S, int it) {
     const int hc = min(item_hc(min(it, max(nit - 1, 0))), 2 * Kc - 1);  // clamped: always a valid half chunk
@@ -769,7 +792,7 @@ __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
   if (lora_lds && threadIdx.x < 256) {
     // stage h rows of this tile's tokens and B rows of its weight rows, 16 ranks at a time, by the
     // first four waves; the loads are issued after the ring prologue and overlap it
-    for (int j0 = 0; j0 < a.r; j0 += 16) {
+    for (int j0 = span0; j0 < span1; j0 += 16) {  // staged rank j at column j - span0
       constexpr int NH = TT * 16 * 16 / 256, NB = (RG * 16 * 16 + 255) / 256;
       float hv[NH], bv[NB];
 #pragma unroll
@@ -785,12 +808,12 @@ __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
 #pragma unroll
       for (int k = 0; k < NH; k++) {
         const int e = threadIdx.x + 256 * k;
-        sh[e >> 4][j0 + (e & 15)] = hv[k];
+        sh[e >> 4][j0 - span0 + (e & 15)] = hv[k];
       }
 #pragma unroll
       for (int k = 0; k < NB; k++) {
         const int e = threadIdx.x + 256 * k;
-        if (e < RG * 256) sb[e >> 4][j0 + (e & 15)] = bv[k];
+        if (e < RG * 256) sb[e >> 4][j0 - span0 + (e & 15)] = bv[k];
       }
     }
   }
@@ -842,20 +865,22 @@ __device__ __forceinline__ void fwd_tile(const FwdArgs& a) {
     if (nb0 >= a.N) continue;  // whole row group is padding (uniform over the wave)
     // LoRA up: lacc[e] = sum_j B[n0+e][j] h[t][j]  (f32 MFMA, A operand = B rows, B operand = h rows)
     f4 lacc = zero;
+    int lo = 0, hi = 0;  // this row group's ranks
+    if (lora) rb_span(a.rb, a.r, nb0, nb0 + 16, lo, hi);
     if (lora_lds) {
-      for (int j0 = 0; j0 < a.r; j0 += 4) {
-        const int j = j0 + g, jc = min(j, a.r - 1);
+      for (int j0 = lo; j0 < hi; j0 += 4) {
+        const int j = j0 + g, jc = min(j, hi - 1) - span0;
         const float hv = sh[i * 16 + li][jc], bv = sb[r * 16 + li][jc];
-        lacc = mfma_f32((nb0 + li < a.N && j < a.r) ? bv : 0.0f, (t < a.T && j < a.r) ? hv : 0.0f, lacc);
+        lacc = mfma_f32((nb0 + li < a.N && j < hi) ? bv : 0.0f, (t < a.T && j < hi) ? hv : 0.0f, lacc);
       }
-    } else if (lora) {  // rank above the LDS staging limit: straight from global memory
+    } else if (lora) {  // rank span above the LDS staging limit: straight from global memory
       const int tc = min(t, a.T - 1);
       const int nrow = min(nb0 + li, a.N - 1);
-      for (int j0 = 0; j0 < a.r; j0 += 4) {
-        const int j = j0 + g, jc = min(j, a.r - 1);
+      for (int j0 = lo; j0 < hi; j0 += 4) {
+        const int j = j0 + g, jc = min(j, hi - 1);
         const float hv = sum_partials(a.hp, (int64_t)tc * a.r + jc, a.nhp);
         const float bv = a.lb[(int64_t)nrow * a.r + jc];
-        lacc = mfma_f32((nb0 + li < a.N && j < a.r) ? bv : 0.0f, (t < a.T && j < a.r) ? hv : 0.0f, lacc);
+        lacc = mfma_f32((nb0 + li < a.N && j < hi) ? bv : 0.0f, (t < a.T && j < hi) ? hv : 0.0f, lacc);
       }
     }
     if (t < a.T) {
@@ -1110,62 +1135,75 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
     }
   }
 
-  // ---- epilogue: bias, LoRA up-projection (h and B rows staged in LDS over the ring), y
+  // ---- epilogue: bias, LoRA up-projection, y.  The up-projection reads, per row group, only the
+  // ranks of its member of a block-diagonal adapter (the other B entries are zeros); h and B rows of
+  // the tile's rank span are staged in LDS over the ring, RTQ_LDS_RANK ranks at a time.
   const bool lora = a.hp != nullptr;
-  const bool lora_lds = lora && a.r <= RTQ_LDS_RANK;
   float(*sh)[RTQ_LDS_RANK + 1] = reinterpret_cast<float(*)[RTQ_LDS_RANK + 1]>(mm_lds);
   float(*sb)[RTQ_LDS_RANK + 1] = sh + 128;
-  if (lora_lds) {
-    __builtin_amdgcn_s_barrier();  // every wave is past its last read of the ring
+  int span0 = 0, span1 = 0;  // ranks read by the tile's rows (workgroup-uniform)
+  int win0[2] = {0, 0}, win1[2] = {0, 0};  // ranks read by row group 2w + r (wave-uniform)
+  if (lora) {
+    rb_span(a.rb, a.r, rg0 * 16, min(rg0 * 16 + 128, a.N), span0, span1);
+#pragma unroll
+    for (int r = 0; r < 2; r++) rb_span(a.rb, a.r, (rg0 + 2 * w + r) * 16, (rg0 + 2 * w + r) * 16 + 16, win0[r], win1[r]);
+  }
+  f4 lacc[TTN][2];
+#pragma unroll
+  for (int i = 0; i < TTN; i++)
+#pragma unroll
+    for (int r = 0; r < 2; r++) lacc[i][r] = zero;
+  for (int c0 = span0; c0 < span1; c0 += RTQ_LDS_RANK) {
+    const int c1 = min(c0 + RTQ_LDS_RANK, span1);
+    __builtin_amdgcn_s_barrier();  // every wave is past its last read of the ring / previous chunk
     asm volatile("" ::: "memory");
-    for (int j0 = 0; j0 < a.r; j0 += 16) {
+    for (int j0 = c0; j0 < c1; j0 += 16) {
       float hv[8], bv[8];
 #pragma unroll
       for (int k = 0; k < 8; k++) {  // rows e / 16: 16 TTN token rows of h, 128 weight rows of B
-        const int e = threadIdx.x + 256 * k, tl = e >> 4, j = j0 + (e & 15);
-        hv[k] = tl < 16 * TTN ? sum_partials(a.hp, (int64_t)min(tt0 * 16 + tl, a.T - 1) * a.r + min(j, a.r - 1), a.nhp)
-                              : 0.0f;
-        bv[k] = a.lb[(int64_t)min(rg0 * 16 + tl, a.N - 1) * a.r + min(j, a.r - 1)];
+        const int e = threadIdx.x + 256 * k, tl = e >> 4, j = min(j0 + (e & 15), a.r - 1);
+        hv[k] = tl < 16 * TTN ? sum_partials(a.hp, (int64_t)min(tt0 * 16 + tl, a.T - 1) * a.r + j, a.nhp) : 0.0f;
+        bv[k] = a.lb[(int64_t)min(rg0 * 16 + tl, a.N - 1) * a.r + j];
       }
 #pragma unroll
       for (int k = 0; k < 8; k++) {
-        const int e = threadIdx.x + 256 * k;
-        if ((e >> 4) < 16 * TTN) sh[e >> 4][j0 + (e & 15)] = hv[k];
-        sb[e >> 4][j0 + (e & 15)] = bv[k];
+        const int e = threadIdx.x + 256 * k, jl = j0 - c0 + (e & 15);
+        if ((e >> 4) < 16 * TTN) sh[e >> 4][jl] = hv[k];
+        sb[e >> 4][jl] = bv[k];
       }
     }
     __syncthreads();
+    // lacc[e] += sum_j B[n0+e][j] h[t][j] over this chunk's part of the row group's window (f32
+    // MFMA, A operand = B rows, B operand = h rows; lane group g takes rank j0 + g)
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int lo = max(win0[r], c0), hi = min(win1[r], c1);
+      const int nb0 = (rg0 + 2 * w + r) * 16, rl = (2 * w + r) * 16;
+      for (int j0 = lo; j0 < hi; j0 += 4) {
+        const int j = j0 + g, jl = min(j, hi - 1) - c0;
+        const float bv = (nb0 + li < a.N && j < hi) ? sb[rl + li][jl] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TTN; i++) {
+          const float hv = (tt0 * 16 + i * 16 + li < a.T && j < hi) ? sh[i * 16 + li][jl] : 0.0f;
+          lacc[i][r] = mfma_f32(bv, hv, lacc[i][r]);
+        }
+      }
+    }
   }
 #pragma unroll
   for (int i = 0; i < TTN; i++) {
 #pragma unroll
     for (int r = 0; r < 2; r++) {
-      const int tl = i * 16 + li, t = tt0 * 16 + tl;
-      const int rl = (2 * w + r) * 16, nb0 = rg0 * 16 + rl, n0 = nb0 + 4 * g;
+      const int t = tt0 * 16 + i * 16 + li;
+      const int nb0 = (rg0 + 2 * w + r) * 16, n0 = nb0 + 4 * g;
       if (nb0 >= a.N) continue;  // whole row group is padding (uniform over the wave)
-      f4 lacc = zero;
-      if (lora_lds) {
-        for (int j0 = 0; j0 < a.r; j0 += 4) {
-          const int j = j0 + g, jc = min(j, a.r - 1);
-          const float hv = sh[tl][jc], bv = sb[rl + li][jc];
-          lacc = mfma_f32((nb0 + li < a.N && j < a.r) ? bv : 0.0f, (t < a.T && j < a.r) ? hv : 0.0f, lacc);
-        }
-      } else if (lora) {  // rank above the LDS staging limit: straight from global memory
-        const int tc = min(t, a.T - 1), nrow = min(nb0 + li, a.N - 1);
-        for (int j0 = 0; j0 < a.r; j0 += 4) {
-          const int j = j0 + g, jc = min(j, a.r - 1);
-          const float hv = sum_partials(a.hp, (int64_t)tc * a.r + jc, a.nhp);
-          const float bv = a.lb[(int64_t)nrow * a.r + jc];
-          lacc = mfma_f32((nb0 + li < a.N && j < a.r) ? bv : 0.0f, (t < a.T && j < a.r) ? hv : 0.0f, lacc);
-        }
-      }
       if (t < a.T) {
         f4 v = acc[i][r];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           float o = v[e];
           if (a.bias) o = o + a.bias[min(n0 + e, a.N - 1)];
-          if (lora) o = o + a.s * lacc[e];
+          if (lora) o = o + a.s * lacc[i][r][e];
           v[e] = o;
         }
         float* yr = a.y + (int64_t)t * a.N;

@@ -282,9 +282,25 @@ rtq_status k_gemm_group(rtq_model* m, const GemmJob* jobs, int n) {
 
 rtq_lora lora_view(const Group& l) { return rtq_lora{l.rank, l.alpha, l.A, l.B, l.rank > 0 ? 1 : 0}; }
 
+// a fused group's members as rank blocks (nm 0: one plain adapter)
+RankBlocks rank_blocks(const Group& l) {
+  RankBlocks rb{};
+  if (l.nm < 2) return rb;
+  rb.nm = l.nm;
+  for (int i = 0; i < l.nm; i++) {
+    rb.row0[i] = (int)l.mem[i].row0;
+    rb.nrow[i] = (int)l.mem[i].rows;
+    rb.col0[i] = (int)l.mem[i].col0;
+    rb.r[i] = (int)l.mem[i].r;
+  }
+  return rb;
+}
+
 rtq_status lin_fwd(rtq_model* m, const Group& l, const float* x, int64_t t, float* y) {
   const rtq_lora lv = lora_view(l);
-  return rtq_linear_forward_keep_d(m->ctx, l.w, l.bias, l.rank > 0 ? &lv : nullptr, x, t, y, l.hpk, stream_of(m));
+  const RankBlocks rb = rank_blocks(l);
+  return rtq_linear_forward_keep_d(m->ctx, l.w, l.bias, l.rank > 0 ? &lv : nullptr, &rb, x, t, y, l.hpk,
+                                   stream_of(m));
 }
 
 // a fused group's adapter is block-diagonal (each member's rows see only its own ranks): the
@@ -300,14 +316,7 @@ rtq_status lin_bwd(rtq_model* m, const Group& l, const float* x, const float* dy
   if (!dense && l.nm < 2)
     return rtq_linear_backward_blocks_d(m->ctx, l.w, &lv, nullptr, x, dy, t, dx, l.ga, l.gb, l.hpk, stream_of(m));
   if (!dense) {
-    RankBlocks rb{};
-    rb.nm = l.nm;
-    for (int i = 0; i < l.nm; i++) {
-      rb.row0[i] = (int)l.mem[i].row0;
-      rb.nrow[i] = (int)l.mem[i].rows;
-      rb.col0[i] = (int)l.mem[i].col0;
-      rb.r[i] = (int)l.mem[i].r;
-    }
+    const RankBlocks rb = rank_blocks(l);
     return rtq_linear_backward_blocks_d(m->ctx, l.w, &lv, &rb, x, dy, t, dx, l.ga, l.gb, l.hpk, stream_of(m));
   }
   MMaskArgs ma{l.gb, l.rows, l.rank, l.nm, {}, {}, {}, {}};

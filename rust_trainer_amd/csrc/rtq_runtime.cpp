@@ -481,9 +481,10 @@ rtq_status enqueue_backward_dense(rtq_ctx* c, const rtq_weight* w, const float* 
 // for a later enqueue_backward of the same x to reuse
 rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int64_t t, float* y, const float* bias,
                            const float* la, const float* lb, int64_t r, float s, int32_t* isums, Arena& ar,
-                           hipStream_t st, float* hp_keep = nullptr) {
+                           hipStream_t st, float* hp_keep = nullptr, const RankBlocks* rb = nullptr) {
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
+  const RankBlocks rbv = lora && rb ? *rb : RankBlocks{};
   if (is_dense(w->type)) return enqueue_forward_dense(c, w, x, t, y, bias, la, lb, lora ? r : 0, s, ar, st);
   FwdPlan p = fwd_plan(w, t, lora ? r : 0);
   // the debug sums come from the skinny / wide kernels; the GEMV pays off once its row tiles alone
@@ -523,6 +524,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
     fa.lb = lb;
     fa.r = (int)r;
     fa.s = s;
+    fa.rb = rbv;
     const int kid = K_GEMV + fmt_index(w->type);
     set_work(c, w, t, lora ? r : 0, false);
     return launch(c, kid, dim3((unsigned)gp.gx, (unsigned)gp.gy), dim3(256), st, fa,
@@ -589,6 +591,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   fa.lb = lb;
   fa.r = (int)r;
   fa.s = s;
+  fa.rb = rbv;
   fa.isums = isums;
   fa.xdh = xdh;
   if (mm && (!fa.wq || !fa.wdr || !fa.xq || !fa.xdh || !fa.y))
@@ -1617,10 +1620,24 @@ int64_t rtq_lora_partial_floats(const rtq_weight* w, int64_t t, int64_t r) {
   return nhp == lora_slices(w->cols) ? nhp * t * r : 0;  // the forward's and the backward's slicing agree
 }
 
+// a block-diagonal adapter's blocks lie inside the weight's rows and the adapter's ranks
+rtq_status check_blocks(const rtq_weight* w, const rtq_lora* lora, const RankBlocks* rb) {
+  if (rb && (rb->nm < 0 || rb->nm > 3)) return fail(RTQ_ERR_INVALID, "internal: %d adapter blocks", rb->nm);
+  if (rb && lora && lora->enabled && lora->rank > 0) {
+    for (int m = 0; m < rb->nm; m++)
+      if (rb->row0[m] < 0 || rb->nrow[m] < 0 || (int64_t)rb->row0[m] + rb->nrow[m] > w->rows || rb->col0[m] < 0 ||
+          rb->r[m] < 0 || (int64_t)rb->col0[m] + rb->r[m] > lora->rank)
+        return fail(RTQ_ERR_INVALID, "internal: adapter block %d outside the weight or rank", m);
+  }
+  return RTQ_OK;
+}
+
 rtq_status rtq_linear_forward_keep_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
-                                     const float* x, int64_t t, float* y, float* hp_keep, void* stream) {
+                                     const RankBlocks* rb, const float* x, int64_t t, float* y, float* hp_keep,
+                                     void* stream) {
   RTQ_TRY(check_weight(c, w));
   RTQ_TRY(check_t(t));
+  RTQ_TRY(check_blocks(w, lora, rb));
   bool on;
   int64_t r;
   float s;
@@ -1634,7 +1651,7 @@ rtq_status rtq_linear_forward_keep_d(rtq_ctx* c, const rtq_weight* w, const floa
   RTQ_TRY(ensure_ws(c, fwd_ws_bytes(p)));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   return enqueue_forward(c, w, x, t, y, bias, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, nullptr, ar, st,
-                         hp_keep);
+                         hp_keep, rb);
 }
 
 rtq_status rtq_linear_forward_ws_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
@@ -1661,13 +1678,7 @@ rtq_status rtq_linear_backward_blocks_d(rtq_ctx* c, const rtq_weight* w, const r
                                         const float* x, const float* dy, int64_t t, float* dx, float* ga, float* gb,
                                         const float* hp_have, void* stream) {
   RTQ_TRY(check_weight(c, w));
-  if (rb && (rb->nm < 0 || rb->nm > 3)) return fail(RTQ_ERR_INVALID, "internal: %d adapter blocks", rb->nm);
-  if (rb && lora && lora->enabled && lora->rank > 0) {
-    for (int m = 0; m < rb->nm; m++)
-      if (rb->row0[m] < 0 || rb->nrow[m] < 0 || (int64_t)rb->row0[m] + rb->nrow[m] > w->rows || rb->col0[m] < 0 ||
-          rb->r[m] < 0 || (int64_t)rb->col0[m] + rb->r[m] > lora->rank)
-        return fail(RTQ_ERR_INVALID, "internal: adapter block %d outside the weight or rank", m);
-  }
+  RTQ_TRY(check_blocks(w, lora, rb));
   if (hp_have && rtq_lora_partial_floats(w, t, lora && lora->enabled ? lora->rank : 0) == 0) hp_have = nullptr;
   return linear_backward_d(c, w, lora, x, dy, t, dx, ga, gb, stream, rb, hp_have);
 }
