@@ -10,8 +10,9 @@ attention and norms around them, the LM head + cross-entropy, and the backward o
 tensor resident in HBM.  ``value`` = 512 tokens / step time (the reference's tok/s definition,
 examples/bench_train.rs:57-61); the K timed steps run back to back between two synchronisations.
 ``roofline`` is that of the dominant quantised-matmul kernel of the step (its algorithmic bytes and
-flops over its event-timed total; see ``step_roofline``), ``cpu_baseline`` the oracle's step on 16
-host threads (bounded sample, scaled: see ``model_cpu_baseline``).
+flops over its event-timed total; see ``step_roofline``), ``cpu_baseline`` the oracle's whole step
+(all 28 blocks) on the host cores, threads pinned, median of 3 after a warm-up (see
+``model_cpu_baseline``).
 
 ``--linear`` measures configs[0] instead: one Qwen3-0.6B gate_proj frozen linear, Q4_0 W 3072x1024
 (N(0, 0.02), ggml reference quantiser), X 256x1024 and dy 256x3072 ~ N(0, 1), LoRA r=16 alpha=32
@@ -35,10 +36,10 @@ FMT:SHAPE:T`` runs one of those cases (for a kernel trace of it).
 ``--traffic`` runs 24 eager config-1 steps and then three 64 MiB device copies, for two
 ``rocprofv3 --pmc`` passes (FETCH_SIZE, then WRITE_SIZE); ``--traffic-report FETCH_DIR WRITE_DIR``
 turns the two passes into HBM bytes per launch of each library kernel (each counter scaled so that
-the copies read and write 64 MiB), writes ``profiles/traffic_<kernel>_config1.json`` (read by the
+the copies read and write 64 MiB), writes ``profiles/traffic_<kernel>_configs0.json`` (read by the
 ``--linear`` run for ``roofline.traffic``) and prints a table.  ``--traffic-step`` does the same for
 two configs[2] training steps; ``--traffic-report F W --traffic-step`` writes
-``profiles/traffic_<kernel>_config3.json`` for the block-linear kernels (read by the default run).
+``profiles/traffic_<kernel>_configs2.json`` for the block-linear kernels (read by the default run).
 
 ``--head`` measures the LM head + cross-entropy of configs[2] (``Model::head``: tied Q4_0 head
 151936 x 1024, 512 positions, loss on the last 256) through ``rtq_lm_head_d``, one JSON line with
@@ -117,7 +118,7 @@ def roofline(name: str, avg_ms: float) -> dict | None:
 
 def measured_traffic(name: str):
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary, if any."""
-    p = os.path.join(ROOT, "profiles", f"traffic_{name}_config1.json")
+    p = os.path.join(ROOT, "profiles", f"traffic_{name}_configs0.json")
     if os.path.exists(p):
         try:
             return json.load(open(p)).get("bytes_per_launch")
@@ -339,7 +340,7 @@ def step_kernel_work(name: str) -> tuple[float, float] | None:
 
 
 def traffic_report(fetch_dir: str, write_dir: str, step: bool = False) -> None:
-    """Counter CSVs of the two --pmc passes -> profiles/traffic_<kernel>_config1.json (config3 for
+    """Counter CSVs of the two --pmc passes -> profiles/traffic_<kernel>_configs0.json (configs2 for
     the training step) and a table."""
     import csv
     import glob
@@ -378,7 +379,7 @@ def traffic_report(fetch_dir: str, write_dir: str, step: bool = False) -> None:
                "algorithmic_bytes": int(algo[0]) if algo else None, "launches": len(fetch[name])}
         if step and algo is None:
             continue
-        tag = "config3" if step else "config1"
+        tag = "configs2" if step else "configs0"
         json.dump(out, open(os.path.join(ROOT, "profiles", f"traffic_{name}_{tag}.json"), "w"), indent=1)
         rows.append(out)
     print(f"calibration: {COPY_MIB} MiB copies read {fcopy:.0f} KiB (FETCH_SIZE) and write {wcopy:.0f} KiB "
@@ -390,26 +391,222 @@ def traffic_report(fetch_dir: str, write_dir: str, step: bool = False) -> None:
               f"{o['bytes_per_launch']} | {o['algorithmic_bytes']} |")
 
 
+SQ_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES SQ_ACTIVE_INST_VALU SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS "
+               "SQ_LDS_BANK_CONFLICT SQ_WAIT_INST_LDS SQ_WAVE_CYCLES GRBM_GUI_ACTIVE")
+SIMD_NUM, CU_NUM = 1024, 256
+
+
+def counters_report(sq_dir: str, fetch_dir: str | None, write_dir: str | None, title: str, out_md: str) -> None:
+    """Per-kernel summary of one rocprofv3 --pmc pass of SQ_COUNTERS (and, if given, the FETCH_SIZE /
+    WRITE_SIZE passes with the copy calibration of --traffic-report) -> a markdown table in
+    profiles/<out_md>, kernels ordered by their share of the profiled run's kernel time.
+    MFMA busy % = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs); VALU busy % =
+    SQ_ACTIVE_INST_VALU / (GRBM_GUI_ACTIVE per XCD x 256 CUs); LDS bank-conflict % = conflict cycles /
+    (GRBM_GUI_ACTIVE per XCD x 256 CUs) (the formulas of rocprofiler-sdk's MfmaUtil, VALUBusy and
+    LDSBankConflict; GRBM_GUI_ACTIVE in the CSV is the sum over the 8 XCDs)."""
+    import csv
+    import glob
+
+    def per_kernel(d: str) -> dict:
+        agg: dict = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                name = r["Kernel_Name"]
+                k = agg.setdefault(name, {"disp": {}, "sum": {}, "each": []})
+                k["disp"][r["Dispatch_Id"]] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
+                k["sum"][r["Counter_Name"]] = k["sum"].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+                k["each"].append(float(r["Counter_Value"]))
+        return agg
+
+    sq = per_kernel(sq_dir)
+    fetch = per_kernel(fetch_dir) if fetch_dir else {}
+    write = per_kernel(write_dir) if write_dir else {}
+
+    def copy_scale(agg: dict) -> float | None:  # the three largest copy dispatches are the calibration copies
+        vals = sorted(x for n, v in agg.items() if "copy" in n.lower() for x in v["each"])
+        return COPY_MIB * 1024 / (sum(vals[-3:]) / len(vals[-3:])) if vals else None
+
+    fs, ws = copy_scale(fetch), copy_scale(write)
+    total_us = sum(sum(v["disp"].values()) for n, v in sq.items() if n.startswith("rtq_"))
+    rows = []
+    for name, v in sq.items():
+        if not name.startswith("rtq_"):
+            continue
+        n = len(v["disp"])
+        c = {k: x / n for k, x in v["sum"].items()}
+        gui = c.get("GRBM_GUI_ACTIVE", 0.0) / 8.0
+        row = {"kernel": name, "dispatches": n, "avg_us": sum(v["disp"].values()) / n,
+               "share": sum(v["disp"].values()) / total_us if total_us else 0.0,
+               "mfma_busy": 100.0 * c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (gui * SIMD_NUM) if gui else None,
+               "valu_busy": 100.0 * c.get("SQ_ACTIVE_INST_VALU", 0.0) / (gui * CU_NUM) if gui else None,
+               "lds_conflict": 100.0 * c.get("SQ_LDS_BANK_CONFLICT", 0.0) / (gui * CU_NUM) if gui else None,
+               "valu": c.get("SQ_INSTS_VALU"), "mfma": c.get("SQ_INSTS_MFMA"), "lds": c.get("SQ_INSTS_LDS"),
+               "wait_lds": c.get("SQ_WAIT_INST_LDS")}
+        if name in fetch and fs:
+            row["fetch_mb"] = fetch[name]["sum"]["FETCH_SIZE"] / len(fetch[name]["disp"]) * fs * 1024 / 1e6
+        if name in write and ws:
+            row["write_mb"] = write[name]["sum"]["WRITE_SIZE"] / len(write[name]["disp"]) * ws * 1024 / 1e6
+        rows.append(row)
+    rows.sort(key=lambda r: -r["share"])
+
+    def f(x, fmt):
+        return "-" if x is None else format(x, fmt)
+
+    lines = [f"# {title}", "",
+             "| kernel | dispatches | avg us (under counters) | share | MFMA busy % | VALU busy % | LDS bank-conflict % | "
+             "VALU insts | MFMA insts | LDS insts | HBM read MB | HBM write MB |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for r in rows:
+        lines.append(f"| {r['kernel']} | {r['dispatches']} | {r['avg_us']:.1f} | {r['share']:.3f} | {f(r['mfma_busy'], '.1f')} | "
+                     f"{f(r['valu_busy'], '.1f')} | {f(r['lds_conflict'], '.1f')} | {f(r['valu'], '.0f')} | "
+                     f"{f(r['mfma'], '.0f')} | {f(r['lds'], '.0f')} | {f(r.get('fetch_mb'), '.2f')} | "
+                     f"{f(r.get('write_mb'), '.2f')} |")
+    if fs and ws:
+        lines += ["", f"HBM bytes: FETCH_SIZE x {fs:.4f} and WRITE_SIZE x {ws:.4f} (the {COPY_MIB} MiB calibration copies' "
+                  "counter readings against the bytes they move)."]
+    text = "\n".join(lines) + "\n"
+    path = os.path.join(ROOT, "profiles", out_md)
+    head = ""
+    if os.path.exists(path):  # keep a hand-written preamble (commands) above the generated table
+        old = open(path).read()
+        cut = old.find("<!-- generated -->")
+        head = old[:cut] if cut >= 0 else ""
+    open(path, "w").write((head or "") + "<!-- generated -->\n" + text)
+    print(text)
+
+
+# ---------------------------------------------------------------- MFMA instruction-mix probes
+PROBES = (("rtq_probe_f16", "f16 16x16x32 + 4 FMA / lane", 8, 256),
+          ("rtq_probe_i8", "i8 32x32x32 + 16 cvt + 16 FMA / lane", 2, 1024),
+          ("rtq_probe_i8x64", "i8 16x16x64 (half K zero) + 4 cvt + 4 FMA / lane", 8, 256),
+          ("rtq_probe_f16_mfma", "f16 16x16x32 alone", 8, 256),
+          ("rtq_probe_i8_mfma", "i8 32x32x32 alone", 2, 1024),
+          ("rtq_probe_i8x64_mfma", "i8 16x16x64 alone", 8, 256))
+
+
+def hip_runtime() -> ctypes.CDLL:
+    """The HIP runtime torch loaded (the same one librtq.so uses), for the module API."""
+    import torch
+
+    torch.cuda.init()
+    for line in open("/proc/self/maps"):
+        if "libamdhip64.so" in line:
+            return ctypes.CDLL(line.split()[-1])
+    raise RuntimeError("libamdhip64 is not loaded")
+
+
+def mfma_mix(iters: int) -> None:
+    """--mfma-mix: the rtq_probe.hip probes (the forward's block dot in its f16 and int8 MFMA forms,
+    with and without the per-block scale epilogue), 2048 workgroups of 4 waves each, timed with HIP
+    events; one JSON line per probe with its rate in output-blocks (32-column block dots of one
+    output element) and the equivalent int8 dot TOPS (64 ops per output-block)."""
+    import torch
+
+    path = os.path.join(ROOT, "rust_trainer_amd", "_build", "rtq_probe.hsaco")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built: run __graft_entry__.build()")
+    hip = hip_runtime()
+    mod = ctypes.c_void_p()
+    if hip.hipModuleLoad(ctypes.byref(mod), path.encode()) != 0:
+        raise RuntimeError("hipModuleLoad failed")
+
+    class ProbeArgs(ctypes.Structure):
+        _fields_ = [("inp", ctypes.c_void_p), ("out", ctypes.c_void_p), ("iters", ctypes.c_int)]
+
+    seeds = torch.randint(-127, 128, (4096,), dtype=torch.int32, device="cuda")
+    grid, block = 2048, 256
+    out = torch.empty(grid * block, device="cuda")
+    st = torch.cuda.current_stream()
+    hip.hipModuleLaunchKernel.argtypes = [ctypes.c_void_p] + [ctypes.c_uint] * 6 + \
+        [ctypes.c_uint, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)]
+    for name, desc, tiles, tile_out in PROBES:
+        fn = ctypes.c_void_p()
+        if hip.hipModuleGetFunction(ctypes.byref(fn), mod, name.encode()) != 0:
+            raise RuntimeError(f"no kernel {name}")
+        args = ProbeArgs(seeds.data_ptr(), out.data_ptr(), iters)
+        params = (ctypes.c_void_p * 1)(ctypes.cast(ctypes.pointer(args), ctypes.c_void_p))
+
+        def launch():
+            rc = hip.hipModuleLaunchKernel(fn, grid, 1, 1, block, 1, 1, 0, ctypes.c_void_p(st.cuda_stream), params, None)
+            if rc != 0:
+                raise RuntimeError(f"launch of {name} failed ({rc})")
+
+        launch()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(5):
+            launch()
+        e1.record(st)
+        torch.cuda.synchronize()
+        sec = e0.elapsed_time(e1) * 1e-3 / 5
+        blocks = grid * (block // 64) * iters * tiles * tile_out
+        print(json.dumps({"probe": name, "form": desc, "us": round(sec * 1e6, 1),
+                          "output_blocks_per_s": round(blocks / sec / 1e12, 3) * 1e12,
+                          "dot_tops": round(blocks * 64 / sec / 1e12, 1)}), flush=True)
+    hip.hipModuleUnload(mod)
+
+
+def host_threads() -> int:
+    """Host threads the CPU baselines use: the CPUs of this process's affinity mask, at most 16 (one
+    GPU's share of the GPU box's host cores, whatever the machine's total)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def timed_runs(fn, warmup: int, runs: int, threads: int) -> list[float]:
+    """Seconds of each of ``runs`` calls of fn after ``warmup`` untimed ones, with an OpenMP team of
+    ``threads`` pinned one per CPU (the calling thread's affinity is restored afterwards)."""
+    import oracle as O
+
+    saved = os.sched_getaffinity(0)
+    try:
+        O.pin_threads(threads)
+        for _ in range(warmup):
+            fn()
+        out = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            out.append(time.perf_counter() - t0)
+        return out
+    finally:
+        os.sched_setaffinity(0, saved)
+
+
 def cpu_baseline(inputs, seconds: float) -> dict:
-    """The CPU oracle (C restatement of the reference algorithm) on the host cores, bounded sample."""
-    import numpy as np
+    """configs[0] on the host cores: the oracle's Linear forward + backward (C restatement of
+    RieFrozen / Linear, AVX2 + FMA, OpenMP), threads pinned, 2 warm-up calls then the median of 10,
+    at nproc (at most 16), 4 and 1 threads.  ``seconds`` is unused (the sample is fixed)."""
+    import statistics
 
     import oracle as O
 
     blocks, x, dy, A, B = inputs
-    threads = max(1, min(16, os.cpu_count() or 1))
-    steps, t0 = 0, time.perf_counter()
-    while True:
+
+    def step():
         O.linear_forward(O.Q4_0, blocks, N, K, x, A=A, B=B, alpha=ALPHA, nthreads=threads)
         O.linear_backward(O.Q4_0, blocks, N, K, x, dy, A=A, B=B, alpha=ALPHA, nthreads=threads)
-        steps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or steps >= 1000:
-            break
-    del np
-    return {"value": round(T * steps / el, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{steps} config-1 steps (Linear forward + backward, T={T}) in {el:.1f} s; "
-                      f"C restatement of RieFrozen/Linear (oracle/rtq_oracle.c, -O3 AVX2, OpenMP)"}
+
+    fb, ff = call_work(2, N, K, T, R, False)
+    bb, bf = call_work(2, N, K, T, R, True)
+    nproc = host_threads()
+    by = {}
+    for threads in sorted({nproc, 4, 1}, reverse=True):
+        ts = timed_runs(step, 2, 10, threads)
+        med = statistics.median(ts)
+        by[str(threads)] = {"tokens_per_s": round(T / med, 1), "median_ms": round(med * 1e3, 3),
+                            "gflops": round((ff + bf) / med / 1e9, 2), "gb_per_s": round((fb + bb) / med / 1e9, 3),
+                            "runs_ms": [round(t * 1e3, 3) for t in ts]}
+    return {"value": by[str(nproc)]["tokens_per_s"], "unit": "tokens/s", "cores": nproc, "kind": "port",
+            "cpu_model": O.cpu_model(), "by_threads": by,
+            "method": "threads pinned one per CPU (sched_setaffinity), AVX2 + FMA build (-march=x86-64-v3), "
+                      "2 warm-up calls then the median of 10",
+            "sample": f"configs[0] whole: Linear forward + backward (y, dx, dA, dB), Q4_0 {N}x{K}, T={T}, "
+                      f"LoRA r={R}; C restatement of RieFrozen/Linear (oracle/rtq_oracle.c, -O3, OpenMP)"}
 
 
 # ---------------------------------------------------------------- LM head + cross-entropy
@@ -595,7 +792,7 @@ def model_bench(steps: int, warmup: int, cpu_seconds: float, no_cpu: bool) -> di
                     for k, (c, m) in sorted(per.items(), key=lambda kv: -kv[1][1])},
     }
     if not no_cpu:
-        result["cpu_baseline"] = model_cpu_baseline(spec, cpu_seconds)
+        result["cpu_baseline"] = model_cpu_baseline(spec, g, cpu_seconds)
     model.close()
     ctx.close()
     return result
@@ -652,7 +849,7 @@ def step_roofline(cfg: dict, kernels: dict) -> dict | None:
 
 
 def measured_traffic_step(name: str):
-    p = os.path.join(ROOT, "profiles", f"traffic_{name}_config3.json")
+    p = os.path.join(ROOT, "profiles", f"traffic_{name}_configs2.json")
     if os.path.exists(p):
         try:
             return json.load(open(p)).get("bytes_per_launch")
@@ -813,10 +1010,13 @@ def config_bench(idx: int, steps: int, warmup: int) -> dict:
     }
 
 
-def model_cpu_baseline(spec, seconds: float) -> dict:
-    """The oracle's training step (C restatement of Model::forward_backward) on the host cores, on a
-    bounded sample: the same model cut to 2 of its 28 blocks (same shapes, same head), timed, and
-    scaled to 28 blocks by timing the head alone (step = head + 14 x (2-block step - head))."""
+def model_cpu_baseline(spec, g, seconds: float) -> dict:
+    """configs[2]'s training step on the host cores: the oracle's Model::forward_backward (C
+    restatement, AVX2 + FMA, OpenMP) over the whole 28-block model, threads pinned at nproc (at most
+    16), one warm-up step of a 2-block cut of the same model (same shapes: thread pool, first-touch
+    pages), then the median of 3 full steps.  ``seconds`` is unused (the sample is fixed)."""
+    import statistics
+
     import numpy as np
 
     import oracle as O
@@ -825,28 +1025,32 @@ def model_cpu_baseline(spec, seconds: float) -> dict:
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from model_cases import adapters, oracle_model
 
-    threads = max(1, min(16, os.cpu_count() or 1))
-    small = G.SyntheticSpec.preset("qwen3-0.6b", G.GGML_Q4_0)
-    small.n_layer = 2
-    g = G.GgufFile.from_bytes(small.build())
-    lora = adapters(g, STEP_R, STEP_ALPHA)
-    m = oracle_model(g, lora, STEP_ALPHA)
-    tokens = (synth.Rng(7).next_u64(STEP_T) % np.uint64(small.n_vocab)).astype(np.int32)
+    threads = host_threads()
+    tokens = (synth.Rng(7).next_u64(STEP_T) % np.uint64(spec.n_vocab)).astype(np.int32)
     pos = np.arange(STEP_T - STEP_N - 1, STEP_T - 1, dtype=np.int32)
     tok = tokens[STEP_T - STEP_N:].copy()
     wts = np.full(STEP_N, 1.0 / STEP_N, np.float32)
-    t0 = time.perf_counter()
-    O.model_forward_backward(m, tokens, pos, tok, wts, nthreads=threads)
-    two = time.perf_counter() - t0
-    e = m["embed"]
-    x = np.zeros((STEP_T, small.n_embd), np.float32)
-    t0 = time.perf_counter()
-    O.lm_head(e[0], e[1], e[2], e[3], m["out_norm"], x, pos, tok, wts, nthreads=threads)
-    head = time.perf_counter() - t0
-    step = head + (28 / 2) * (two - head)
-    return {"value": round(STEP_T / step, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"oracle step on 2 of 28 blocks ({two:.1f} s) and the head alone ({head:.1f} s), scaled to "
-                      f"28 blocks: {step:.1f} s per 512-token step (oracle/rtq_oracle*.c, -O3 AVX2, OpenMP)"}
+
+    def model_of(n_layer: int):
+        sp = G.SyntheticSpec.preset("qwen3-0.6b", G.GGML_Q4_0)
+        sp.n_layer = n_layer
+        g = G.GgufFile.from_bytes(sp.build(workers=threads))
+        return oracle_model(g, adapters(g, STEP_R, STEP_ALPHA), STEP_ALPHA), g
+
+    small, gs = model_of(2)
+    timed_runs(lambda: O.model_forward_backward(small, tokens, pos, tok, wts, nthreads=threads), 1, 0, threads)
+    del small, gs
+    full = oracle_model(g, adapters(g, STEP_R, STEP_ALPHA), STEP_ALPHA)  # the GPU step's own GGUF image
+    ts = timed_runs(lambda: O.model_forward_backward(full, tokens, pos, tok, wts, nthreads=threads), 0, 3, threads)
+    med = statistics.median(ts)
+    return {"value": round(STEP_T / med, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_model": O.cpu_model(),
+            "method": "threads pinned one per CPU (sched_setaffinity), AVX2 + FMA build (-march=x86-64-v3), one "
+                      "warm-up step of a 2-block cut of the model, then the median of 3 full steps",
+            "runs_s": [round(t, 2) for t in ts],
+            "sample": f"configs[2] whole: the oracle's Model::forward_backward over all {spec.n_layer} blocks and the "
+                      f"head, {STEP_T} tokens, loss on the last {STEP_N}, LoRA r={STEP_R} on every projection "
+                      f"(oracle/rtq_oracle*.c, -O3, OpenMP): {med:.1f} s per step"}
 
 
 def gguf_load(arg: str) -> None:
@@ -917,6 +1121,10 @@ def main() -> int:
     ap.add_argument("--calls", type=int, default=50, help="sweep: calls per timed graph (at least the sets)")
     ap.add_argument("--traffic", action="store_true", help="config-1 steps + calibration copies for --pmc passes")
     ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
+    ap.add_argument("--counters-report", nargs=4, metavar=("SQ_DIR", "FETCH_DIR", "WRITE_DIR", "OUT_MD"),
+                    help="per-kernel counter table (SQ pass + traffic passes) -> profiles/OUT_MD")
+    ap.add_argument("--mfma-mix", type=int, default=None, metavar="ITERS",
+                    help="instruction-mix probes of the forward's block dot (f16 vs int8 MFMA), ITERS loop trips")
     ap.add_argument("--traffic-step", action="store_true",
                     help="configs[2] steps + calibration copies for --pmc passes (with --traffic-report: the step)")
     ap.add_argument("--head", action="store_true", help="configs[2] LM head + cross-entropy (Model::head)")
@@ -934,6 +1142,15 @@ def main() -> int:
         args.steps = 200 if linear_mode else (3 if big else 20)
     if args.warmup is None:
         args.warmup = 20 if linear_mode else (1 if big else 3)
+    if args.mfma_mix:
+        mfma_mix(args.mfma_mix)
+        return 0
+    if args.counters_report:
+        sq_d, f_d, w_d, out_md = args.counters_report
+        title = ("configs[2] training step: counters per kernel" if args.traffic_step
+                 else "configs[0] Linear forward + backward: counters per kernel")
+        counters_report(sq_d, f_d, w_d, title, out_md)
+        return 0
     if args.traffic_report:
         traffic_report(*args.traffic_report, step=args.traffic_step)
         return 0

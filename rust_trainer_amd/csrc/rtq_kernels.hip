@@ -1455,12 +1455,14 @@ RTQ_GEMV(rtq_gemv_q4_k, FMT_Q4_K, 4, 4)
 RTQ_GEMV(rtq_gemv_q6_k, FMT_Q6_K, 2, 4)
 
 // ============================================================== backward preparation
-// Grid (ceil(T/16), nhq + ngq), 256 threads (src/linear.rs:106-111); nhq, ngq multiples of 4:
-//   y < nhq:     partial h over columns [256y, 256y + 256) of x . A^T -> hp[t][j][y]
-//   y = nhq + q: partial g over rows [256q, 256q + 256) of W: dy . B   -> gp[t][j][q]
+// LoRA partial products of src/linear.rs:106-111, 256 threads per workgroup, grid
+// (ceil(T / 16), nhq + ngq) offset by y0 (nhq 0: the forward kept the h partials):
+//   grid row y < nhq:     h partial over columns [256y, 256y + 256) of x . A^T for the 16 tokens
+//                         16x .. 16x + 15 -> hp[(t * r + j) * nhq + y] (slice index fastest);
+//   grid row y = nhq + q: g partial over rows [256q, 256q + 256) of dy . B for the gtok (64 or 16)
+//                         tokens gtok x .. -> gp[(q * T + t) * r + j] (slice-major); workgroups
+//                         with gtok x >= T exit.
 // The dx kernel's extra workgroups sum the partials in slice order (h, and g scaled by s).
-// Grid (ceil(T / 16), [nhq +] ngq): rows y < nhq of the grid compute h partials for 16 tokens each,
-// the others g partials for gtok tokens each (workgroups x >= ceil(T / gtok) of those rows exit).
 extern "C" __global__ __launch_bounds__(256) void rtq_bwd_prep(BwdPrepArgs a) {
   constexpr int KQ = RTQ_ACT_KQ, LDX = KQ + 1;
   constexpr int SM = 16 * KQ + 64 > 16 * LDX ? 16 * KQ + 64 : 16 * LDX;  // A tile, or B slice (padded rows)
