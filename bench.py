@@ -479,6 +479,9 @@ def counters_report(sq_dir: str, fetch_dir: str | None, write_dir: str | None, t
 PROBES = (("rtq_probe_f16", "f16 16x16x32 + 4 FMA / lane", 8, 256),
           ("rtq_probe_i8", "i8 32x32x32 + 16 cvt + 16 FMA / lane", 2, 1024),
           ("rtq_probe_i8x64", "i8 16x16x64 (half K zero) + 4 cvt + 4 FMA / lane", 8, 256),
+          ("rtq_probe_f16s", "f16 16x16x32 + 4 FMA / lane, scale products by one 16x16x4 f16 MFMA per 4 tile-blocks", 8, 256),
+          ("rtq_probe_i8m", "i8 32x32x32 + 16 cvt + 16 FMA / lane, scale products by a 32x32x8 f16 MFMA", 2, 1024),
+          ("rtq_probe_i8v", "i8 32x32x32 + 16 cvt + 16 FMA / lane, scale products by 16 VALU multiplies", 2, 1024),
           ("rtq_probe_f16_mfma", "f16 16x16x32 alone", 8, 256),
           ("rtq_probe_i8_mfma", "i8 32x32x32 alone", 2, 1024),
           ("rtq_probe_i8x64_mfma", "i8 16x16x64 alone", 8, 256))
@@ -497,12 +500,12 @@ def hip_runtime() -> ctypes.CDLL:
 
 def mfma_mix(iters: int) -> None:
     """--mfma-mix: the rtq_probe.hip probes (the forward's block dot in its f16 and int8 MFMA forms,
-    with and without the per-block scale epilogue), 2048 workgroups of 4 waves each, timed with HIP
+    with and without the per-block scale epilogue and the scale products), 2048 workgroups of 4 waves each, timed with HIP
     events; one JSON line per probe with its rate in output-blocks (32-column block dots of one
     output element) and the equivalent int8 dot TOPS (64 ops per output-block)."""
     import torch
 
-    path = os.path.join(ROOT, "rust_trainer_amd", "_build", "rtq_probe.hsaco")
+    path = os.path.join(ROOT, "rust_trainer_amd", "rtq_probe.hsaco")
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is not built: run __graft_entry__.build()")
     hip = hip_runtime()

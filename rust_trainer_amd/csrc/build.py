@@ -4,7 +4,7 @@
 2. ``rtq_runtime.cpp`` + ``rtq_gguf.cpp`` + ``rtq_model.cpp`` -> ``rust_trainer_amd/librtq.so`` (g++ against the HIP runtime), with the
    code object embedded (``.incbin``) and loaded at run time with ``hipModuleLoadData``, plus
    ``rtq_noalloc.hip`` compiled by hipcc (its device array is registered with the HIP runtime);
-3. ``rtq_probe.hip`` -> ``rust_trainer_amd/_build/rtq_probe.hsaco`` (instruction-mix probes for
+3. ``rtq_probe.hip`` -> ``rust_trainer_amd/rtq_probe.hsaco`` (instruction-mix probes for
    ``bench.py --mfma-mix``; not part of the library);
 4. ``oracle/`` -> ``oracle/liboracle.so`` (test infrastructure, plain gcc).
 
@@ -55,9 +55,9 @@ def build_kernels() -> str:
 
 
 def build_probe() -> str:
-    """rtq_probe.hip -> its own gfx950 code object (bench.py --mfma-mix loads it; not in librtq.so)"""
-    os.makedirs(BUILD, exist_ok=True)
-    out = os.path.join(BUILD, "rtq_probe.hsaco")
+    """rtq_probe.hip -> its own gfx950 code object beside librtq.so (bench.py --mfma-mix loads it;
+    not part of the library)"""
+    out = os.path.join(PKG, "rtq_probe.hsaco")
     tmp = out + ".tmp"
     _run([os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, "--genco", "--no-gpu-bundle-output",
           os.path.join(CSRC, "rtq_probe.hip"), "-o", tmp])
