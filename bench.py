@@ -129,9 +129,10 @@ def measured_traffic(name: str):
 
 # ---------------------------------------------------------------- configs[1] sweep
 SWEEP_SHAPES = {"q_proj": (2048, 1024), "kv_proj": (1024, 1024), "down_proj": (1024, 3072), "lm_head": (151936, 1024)}
-# the merged projections of the configs[3] / configs[4] blocks (q|k|v and gate|up are one launch in the
-# step), for --case runs only: (rows, cols, LoRA rank)
-BLOCK_SHAPES = {"llama_qkv": (6144, 4096, 64), "llama_o": (4096, 4096, 64), "llama_gate_up": (28672, 4096, 64),
+# the merged projections of the configs[2] / configs[3] / configs[4] blocks (q|k|v and gate|up are one
+# launch in the step; one plain adapter here), for --case runs only: (rows, cols, LoRA rank)
+BLOCK_SHAPES = {"qwen06_qkv": (4096, 1024, 16), "qwen06_gate_up": (6144, 1024, 16), "qwen06_o": (1024, 2048, 16),
+                "qwen06_down": (1024, 3072, 16), "llama_qkv": (6144, 4096, 64), "llama_o": (4096, 4096, 64), "llama_gate_up": (28672, 4096, 64),
                 "llama_down": (4096, 14336, 64), "llama_head": (128256, 4096, 0), "qwen4b_qkv": (6144, 2560, 16),
                 "qwen4b_gate_up": (19456, 2560, 16), "qwen4b_down": (2560, 9728, 16)}
 SWEEP_TYPES = {"Q8_0": 8, "Q4_K": 12, "Q6_K": 14, "Q4_0": 2}

@@ -980,11 +980,28 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int Kc = a.Kp / 128, nhc = a.Kp / 64;
   const int ngroups = a.Np / 16, ntt = a.Tp / 16;
-  // XCD-aware tile order: workgroup id -> (XCD id % 8, slot id / 8) -> a contiguous tile range per XCD
-  const int nrb = (ngroups + 7) / 8, ntiles = nrb * (ntt / TTN);
+  // XCD-aware tile order: workgroup id -> (XCD id % 8, slot id / 8) -> a contiguous range of the
+  // tile order per XCD.  The order takes the row blocks in groups of MM_GR: within a group token
+  // block by token block, the group's row blocks of one token block consecutive.  The ~64
+  // workgroups an XCD runs at once then cover MM_GR row blocks x 64 / MM_GR token blocks, whose
+  // weight rows and activation columns they share in that XCD's L2 (row blocks fastest over all
+  // token blocks would re-read every weight row from HBM once per token block).
+  constexpr int MM_GR = 8;
+  const int nrb = (ngroups + 7) / 8, ntb = ntt / TTN, ntiles = nrb * ntb;
   const int id = blockIdx.x, xcd = id & 7, per = ntiles >> 3, rem = ntiles & 7;
   const int q = xcd * per + min(xcd, rem) + (id >> 3);
-  const int rg0 = (q % nrb) * 8, tt0 = (q / nrb) * TTN;
+  const int gfull = nrb / MM_GR, q0 = gfull * MM_GR * ntb;
+  int rb, tb;
+  if (q < q0) {
+    const int in = q % (MM_GR * ntb);
+    rb = (q / (MM_GR * ntb)) * MM_GR + in % MM_GR;
+    tb = in / MM_GR;
+  } else {  // the last, partial group of nrb % MM_GR row blocks
+    const int gr = nrb - gfull * MM_GR, in = q - q0;
+    rb = gfull * MM_GR + in % gr;
+    tb = in / gr;
+  }
+  const int rg0 = rb * 8, tt0 = tb * TTN;
 
   // Operands reach LDS by buffer loads with the LDS destination (4 or 16 bytes per lane; gfx950
   // has no 8-byte form, so 8-byte items - Q4_0 half-chunk codes, scale pairs - go as pairs of
@@ -997,59 +1014,58 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
   const __amdgpu_buffer_rsrc_t rs_xd = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.xdh), (short)0, nb_xd, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs_w = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.wq), (short)0, nb_w, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs_wd = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.wdr), (short)0, nb_wd, 0x00020000);
-  constexpr int NSLOT = (St::LOADS + 3) / 4;
-  uint32_t voff[NSLOT];
+  // Every wave issues the same kinds of loads (no per-wave branching in the loop): KX activation
+  // fragments (i = w + 4k), KW weight-code loads (iw = w + 4k), and one scale load: waves 0, 1 a
+  // weight scale-pair word row, waves 2 .. 1 + NXD the activation scales (NXD is 1 or 2).
+  constexpr int KX = St::NX / 4, KW = St::NWQ / 4;
+  static_assert(St::NX % 4 == 0 && St::NWQ % 4 == 0 && St::NXD <= 2, "load split over four waves");
+  uint32_t vx[KX], vw[KW], ve = 0;
 #pragma unroll
-  for (int k = 0; k < NSLOT; k++) {
+  for (int k = 0; k < KX; k++) {  // activation fragments: token tile i / 2, block 2h + i % 2
     const int i = w + 4 * k;
-    uint32_t v = 0;
-    if (i < St::NX) {  // activation fragments: token tile i / 2, block 2h + i % 2
-      const uint32_t ttg = (uint32_t)min(tt0 + (i >> 1), ntt - 1);
-      v = ((ttg * Kc * 4 + (i & 1)) * 64 + lane) * 16;
-    } else if (i < St::NX + St::NWQ) {  // weight codes
-      const int iw = i - St::NX;
-      if (FMT == FMT_Q4_0) {  // row group iw / 2, words 64 m .. 64 m + 63 of its 128
-        const int wi = (iw & 1) * 64 + lane;
-        const uint32_t rgg = (uint32_t)min(rg0 + (iw >> 1), ngroups - 1);
-        v = ((rgg * Kc * 64 + (wi >> 1)) * 4 + (wi & 1)) * 4;
-      } else {
-        const uint32_t rgg = (uint32_t)min(rg0 + iw, ngroups - 1);
-        v = (rgg * Kc * 2 * 64 + lane) * 16;
-      }
-    } else if (i < St::NX + St::NWQ + 2) {  // weight scale pairs: word wi -> row wi % 16 of row group wi / 16
-      const int wi = (i - St::NX - St::NWQ) * 64 + lane;
-      const uint32_t rgg = (uint32_t)min(rg0 + (wi >> 4), ngroups - 1);
-      v = ((rgg * Kc * 16 + (wi & 15)) * 2) * 4;
-    } else {  // fp16 activation scales of blocks 2h, 2h+1: word wi -> token wi
-      const int wi = (i - St::NX - St::NWQ - 2) * 64 + lane;
-      const uint32_t tok = (uint32_t)min(tt0 * 16 + wi, a.Tp - 1);
-      v = tok * 8;
+    const uint32_t ttg = (uint32_t)min(tt0 + (i >> 1), ntt - 1);
+    vx[k] = ((ttg * Kc * 4 + (i & 1)) * 64 + lane) * 16;
+  }
+#pragma unroll
+  for (int k = 0; k < KW; k++) {  // weight codes
+    const int iw = w + 4 * k;
+    if (FMT == FMT_Q4_0) {  // row group iw / 2, words 64 m .. 64 m + 63 of its 128
+      const int wi = (iw & 1) * 64 + lane;
+      const uint32_t rgg = (uint32_t)min(rg0 + (iw >> 1), ngroups - 1);
+      vw[k] = ((rgg * Kc * 64 + (wi >> 1)) * 4 + (wi & 1)) * 4;
+    } else {
+      const uint32_t rgg = (uint32_t)min(rg0 + iw, ngroups - 1);
+      vw[k] = (rgg * Kc * 2 * 64 + lane) * 16;
     }
-    voff[k] = v;
+  }
+  if (w < 2) {  // weight scale pairs: word wi -> row wi % 16 of row group wi / 16
+    const int wi = w * 64 + lane;
+    const uint32_t rgg = (uint32_t)min(rg0 + (wi >> 4), ngroups - 1);
+    ve = ((rgg * Kc * 16 + (wi & 15)) * 2) * 4;
+  } else if (w - 2 < St::NXD) {  // fp16 activation scales of blocks 2h, 2h+1: word wi -> token wi
+    const int wi = (w - 2) * 64 + lane;
+    ve = (uint32_t)min(tt0 * 16 + wi, a.Tp - 1) * 8;
   }
   auto issue = [&](int st, int hc) {
     u4v* S = mm_lds + st * St::SIZE;
     const uint32_t kc = hc >> 1, h = hc & 1;
 #pragma unroll
-    for (int k = 0; k < NSLOT; k++) {
-      const int i = w + 4 * k;  // wave-uniform
-      if (i < St::NX) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, RTQ_LDSP(S + St::XQ + i * 64), 16, voff[k], hc * 2048u, 0, 0);
-      } else if (i < St::NX + St::NWQ) {
-        const int iw = i - St::NX;
-        if (FMT == FMT_Q4_0)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + (iw >> 1) * 32 + (iw & 1) * 16), 4,
-                                                   voff[k], kc * 1024u + h * 8u, 0, 0);
-        else
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + iw * 64), 16, voff[k], hc * 1024u, 0, 0);
-      } else if (i < St::NX + St::NWQ + 2) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_wd, RTQ_LDSP(S + St::WD + (i - St::NX - St::NWQ) * 16), 4, voff[k],
-                                                 kc * 128u + h * 4u, 0, 0);
-      } else if (i < St::LOADS) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_xd, RTQ_LDSP(S + St::XD + (i - St::NX - St::NWQ - 2) * 16), 4,
-                                                 voff[k], kc * (uint32_t)a.Tp * 8u + h * 4u, 0, 0);
-      }
+    for (int k = 0; k < KX; k++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, RTQ_LDSP(S + St::XQ + (w + 4 * k) * 64), 16, vx[k], hc * 2048u, 0, 0);
+#pragma unroll
+    for (int k = 0; k < KW; k++) {
+      const int iw = w + 4 * k;
+      if (FMT == FMT_Q4_0)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + (iw >> 1) * 32 + (iw & 1) * 16), 4, vw[k],
+                                                 kc * 1024u + h * 8u, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + iw * 64), 16, vw[k], hc * 1024u, 0, 0);
     }
+    if (w < 2)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_wd, RTQ_LDSP(S + St::WD + w * 16), 4, ve, kc * 128u + h * 4u, 0, 0);
+    else if (w - 2 < St::NXD)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_xd, RTQ_LDSP(S + St::XD + (w - 2) * 16), 4, ve,
+                                               kc * (uint32_t)a.Tp * 8u + h * 4u, 0, 0);
   };
 
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1113,9 +1129,10 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
     }
   };
 
-  // 3-stage ring over half chunks; each wave issues at least LOADS / 4 (rounded down) loads per
-  // stage, so "at most that many outstanding" at the top of step s means stage s has landed.  The
-  // loop is unrolled by the ring size so that every stage's LDS offsets are immediates.
+  // 3-stage ring over half chunks; each wave issues at least MINL loads per stage, so "at most
+  // that many outstanding" at the top of step s means stage s has landed.  The loop is unrolled by
+  // the ring size so that every stage's LDS offsets are immediates.
+  constexpr int MINL = KX + KW + (St::NXD >= 2 ? 1 : 0);
   issue(0, 0);
   if (nhc > 1) issue(1, 1);
   for (int hc0 = 0; hc0 < nhc; hc0 += St::RING) {
@@ -1124,7 +1141,7 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
       const int hc = hc0 + u;
       if (hc < nhc) {
         if (hc + 1 < nhc)
-          __builtin_amdgcn_s_waitcnt(0x0F70 | (St::LOADS / 4));  // vmcnt <= loads of stage s + 1
+          __builtin_amdgcn_s_waitcnt(0x0F70 | MINL);  // vmcnt <= loads of stage s + 1
         else
           __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __builtin_amdgcn_s_barrier();
