@@ -758,6 +758,8 @@ def model_bench(steps: int, warmup: int, cpu_seconds: float, no_cpu: bool) -> di
     ctx = rt.Context(0)
     model = rt.GpuModel.from_gguf(g, ctx=ctx)
     n_params = model.attach_lora(STEP_R, STEP_ALPHA, seed=1)
+    if ATTENTION_MODE is not None:  # --attention: force the fused or the unfused kernels
+        model.fused_attention = ATTENTION_MODE
     cfg = model.config
     tokens = (synth.Rng(7).next_u64(STEP_T) % np.uint64(cfg["n_vocab"])).astype(np.int32)
     targets = rt.answer_targets(tokens, STEP_T - STEP_N)
@@ -883,6 +885,9 @@ def step_line(args) -> dict:
     return line
 
 
+ATTENTION_MODE = None  # bench.py --attention fused|unfused (None: the library's choice)
+
+
 # ---------------------------------------------------------------- configs[3] and configs[4]
 def config_workload(idx: int):
     """(spec, description, build_batch) of BASELINE.json configs[3] / configs[4]; build_batch(model)
@@ -968,6 +973,8 @@ def config_bench(idx: int, steps: int, warmup: int) -> dict:
     model = rt.GpuModel.from_gguf(g, ctx=ctx)
     print(f"[config {idx}] loaded in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
     n_params = model.attach_lora(rank, alpha, seed=1)
+    if ATTENTION_MODE is not None:
+        model.fused_attention = ATTENTION_MODE
     step, seq_tokens, extra = batch(model)
     for i in range(warmup):
         step()
@@ -1127,6 +1134,8 @@ def main() -> int:
     ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--counters-report", nargs=4, metavar=("SQ_DIR", "FETCH_DIR", "WRITE_DIR", "OUT_MD"),
                     help="per-kernel counter table (SQ pass + traffic passes) -> profiles/OUT_MD")
+    ap.add_argument("--attention", choices=("fused", "unfused"), default=None,
+                    help="training-step benches: force the fused or the unfused attention kernels")
     ap.add_argument("--mfma-mix", type=int, default=None, metavar="ITERS",
                     help="instruction-mix probes of the forward's block dot (f16 vs int8 MFMA), ITERS loop trips")
     ap.add_argument("--traffic-step", action="store_true",
@@ -1146,6 +1155,9 @@ def main() -> int:
         args.steps = 200 if linear_mode else (3 if big else 20)
     if args.warmup is None:
         args.warmup = 20 if linear_mode else (1 if big else 3)
+    global ATTENTION_MODE
+    if args.attention:
+        ATTENTION_MODE = args.attention == "fused"
     if args.mfma_mix:
         mfma_mix(args.mfma_mix)
         return 0

@@ -35,6 +35,11 @@ enum RtqModelKernel {
   KM_ATTN_MERGE_DQ,
   KM_ATTN_MERGE_DKV,
   KM_ATTN_BWD_D,
+  KM_GEMM_BF,
+  KM_GEMM32_BF,
+  KM_GEMM32G_BF,
+  KM_GEMM_HF,
+  KM_GEMM32_HF,
   KM_COUNT
 };
 

@@ -135,6 +135,9 @@ struct rtq_model {
   bool attn_hd_ok = false;
   int attn_mode = -1;
   bool attn_fused = false;
+  // the probability-matrix path's products on split-bf16 MFMA (rtq_m_gemm*_bf); RTQ_ATTN_F32=1 at
+  // load time keeps them on f32 MFMA (rtq_m_gemm*), for comparison
+  bool attn_f32 = false;
   int64_t layout_fused = -1;  // attn_fused the step buffers were laid out for
   float* attn_D = nullptr;  // [nh x t] dO . o per query row
   void* attn_mem = nullptr;
@@ -242,16 +245,21 @@ struct Op {  // one GEMM operand: base, batch stride and divisor, row / column s
 
 // C(b, m, n) (+)= sum_k A(b, m, k) B(b, k, n) for b < batch
 // attention products of the step take the packed layout's liveness map (null for a plain sequence)
+// split: the 16-bit MFMA form of the product (rtq_m_gemm*_hf for the forward's, rtq_m_gemm*_bf for
+// the backward's), unless attn_f32 keeps every product on f32 MFMA
+enum GemmSplit { SPLIT_HF, SPLIT_BF };
 rtq_status k_gemm(rtq_model* m, int64_t M, int64_t N, int64_t K, int64_t batch, Op A, Op B, float* C, int64_t sCb,
-                  int64_t sCm, int64_t sCn, float a_scale, int causal, int acc) {
+                  int64_t sCm, int64_t sCn, float a_scale, int causal, int acc, GemmSplit split) {
   MGemmArgs ga{A.p, B.p, C, (int)M, (int)N, (int)K, A.sb, A.s0, A.s1, B.sb, B.s0, B.s1, sCb, sCm, sCn, A.div, B.div,
                a_scale, causal, acc, (int)batch, causal && m->packed ? m->live_d : nullptr, (int)m->nlb, nullptr};
   // 64-row tiles when the grid fills the chip twice over, else 32-row tiles (twice the workgroups)
   const int64_t tiles64 = (N + 63) / 64 * ((M + 63) / 64) * batch / (causal == 1 ? 2 : 1);
   const int bm = tiles64 >= 2 * 256 ? 64 : 32;
   const int64_t tiles = (N + 63) / 64 * ((M + bm - 1) / bm) * batch;  // flat, XCD-aware (8 x ceil(tiles / 8))
-  return rtq_model_launch(m->ctx, bm == 64 ? KM_GEMM : KM_GEMM32, dim3((unsigned)((tiles + 7) / 8 * 8)), dim3(256),
-                          stream_of(m), &ga);
+  const int kid = m->attn_f32          ? (bm == 64 ? KM_GEMM : KM_GEMM32)
+                  : split == SPLIT_HF ? (bm == 64 ? KM_GEMM_HF : KM_GEMM32_HF)
+                                      : (bm == 64 ? KM_GEMM_BF : KM_GEMM32_BF);
+  return rtq_model_launch(m->ctx, kid, dim3((unsigned)((tiles + 7) / 8 * 8)), dim3(256), stream_of(m), &ga);
 }
 
 // independent products C_i (+)= A_i B_i (M_i x N_i x K_i, batch_i) in one launch of 32-row tiles
@@ -277,7 +285,8 @@ rtq_status k_gemm_group(rtq_model* m, const GemmJob* jobs, int n) {
     total += (j.N + 63) / 64 * ((j.M + 31) / 32) * j.batch;
   }
   for (int i = n; i < 4; i++) g.start[i] = (int)total;
-  return rtq_model_launch(m->ctx, KM_GEMM32G, dim3((unsigned)((total + 7) / 8 * 8)), dim3(256), stream_of(m), &g);
+  return rtq_model_launch(m->ctx, m->attn_f32 ? KM_GEMM32G : KM_GEMM32G_BF, dim3((unsigned)((total + 7) / 8 * 8)),
+                          dim3(256), stream_of(m), &g);
 }
 
 rtq_lora lora_view(const Group& l) { return rtq_lora{l.rank, l.alpha, l.A, l.B, l.rank > 0 ? 1 : 0}; }
@@ -700,12 +709,14 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* 
     M_TRY(attn_merge(m, KM_ATTN_MERGE_FWD, aa, m->mg_fwd, m->n_mfwd));
   } else {
   // S = (q scale) K^T per head (causal), softmax in place, O = P V
-  M_TRY(k_gemm(m, t, t, hd, nh, Op{k.q, hd, qd, 1, 1}, Op{k.k, hd, 1, kd, (int)grp}, k.P, t * t, t, 1, scale, 1, 0));
+  M_TRY(k_gemm(m, t, t, hd, nh, Op{k.q, hd, qd, 1, 1}, Op{k.k, hd, 1, kd, (int)grp}, k.P, t * t, t, 1, scale, 1, 0,
+               SPLIT_HF));
   MSoftArgs sa{k.P, nullptr, nullptr, (int)t, (int)nh, scale, m->packed ? m->seg_d : nullptr,
                m->packed ? m->live_d : nullptr, (int)m->nlb};
   M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX, dim3((unsigned)((t + 3) / 4), (unsigned)nh), dim3(256), stream_of(m),
                          &sa));
-  M_TRY(k_gemm(m, t, hd, t, nh, Op{k.P, t * t, t, 1, 1}, Op{k.v, hd, kd, 1, (int)grp}, k.o, hd, qd, 1, 1.0f, 2, 0));
+  M_TRY(k_gemm(m, t, hd, t, nh, Op{k.P, t * t, t, 1, 1}, Op{k.v, hd, kd, 1, (int)grp}, k.o, hd, qd, 1, 1.0f, 2, 0,
+               SPLIT_HF));
   }
   M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LO]], k.o, t, m->mo));
   M_TRY(k_norm(m, x, m->mo, k.h, L.ffn_norm, k.n2, k.inv2, t, d, 0));  // h = x + attn, n2 = rmsnorm(h)
@@ -762,7 +773,7 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
     M_TRY(attn_merge(m, KM_ATTN_MERGE_DKV, aa, m->mg_kv, m->n_mkv));
   } else {
   M_TRY(k_gemm(m, t, t, hd, nh, Op{m->d_o, hd, qd, 1, 1}, Op{k.v, hd, 1, kd, (int)grp}, m->dP, t * t, t, 1, 1.0f, 1,
-               0));  // dP = dO V^T
+               0, SPLIT_BF));  // dP = dO V^T
   MSoftArgs sa{nullptr, k.P, m->dP, (int)t, (int)nh, scale, m->packed ? m->seg_d : nullptr,
                m->packed ? m->live_d : nullptr, (int)m->nlb};
   M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX_BWD, dim3((unsigned)((t + 3) / 4), (unsigned)nh), dim3(256),
@@ -1076,6 +1087,7 @@ rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out)
   std::vector<float> factors;
   M_TRY(parse_config(g, &cfg, &factors));
   rtq_model* m = new rtq_model();
+  if (const char* e = getenv("RTQ_ATTN_F32")) m->attn_f32 = atoi(e) != 0;
   m->ctx = ctx;
   m->cfg = cfg;
   m->rope_factors = factors;

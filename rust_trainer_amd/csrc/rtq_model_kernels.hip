@@ -427,6 +427,249 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32g(MGemmGroupArgs g
     m_gemm32_member(g.p[2], id - g.start[2]);
 }
 
+// ------------------------------------------------------------------ batched split-16-bit GEMM
+// The attention products of m_gemm on 16-bit MFMA (16x16x32): each f32 operand element x is split
+// as it is staged into a high and a low 16-bit part, and acc += Ah Bh + Al Bh + Ah Bl (f32
+// accumulation).  HF (the forward's S = q k^T and o = p v): f16 parts rounded to nearest, hi =
+// f16(x), lo = f16(x - hi), 22 significant bits, so the dropped Al Bl term leaves a relative error
+// near 2^-22 per product (k and v, stored as f16 values, split exactly), close enough to f32 that
+// the activations the next quantised linear sees keep their Q8 codes; the operands there are
+// bounded (q scaled, probabilities, f16 k and v).  BF (the backward's products of score and output
+// gradients, whose magnitudes can lie below f16's range): bf16 parts by truncation, a relative
+// error near 2^-16 per product.  Same tiles, grids, load modes, causal ranges and liveness skipping
+// as m_gemm; LDS holds each operand as hi and lo planes [row][k] (k unit stride, rows padded to
+// BK + 8 elements), so a lane's fragment (row li, k = 32 c + 8 g .. + 7) is one 16-byte read per
+// plane (the padding puts the 16 rows of one lane group on distinct banks).  Mode-2 operands
+// (unit stride along rows) are transposed as they are written (2-byte stores).
+template <int R, int BK>
+constexpr int m_bf_ld() { return BK + 8; }
+
+// hi / lo bf16 halves of four floats (bit view of the whole vector: single-lane masks of a float4
+// bit_cast are miscompiled by this compiler)
+__device__ __forceinline__ void m_split4(const f4 v, u2v& hi, u2v& lo) {
+  const u4v vb = __builtin_bit_cast(u4v, v);
+  uint32_t lb[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) lb[c] = __builtin_bit_cast(uint32_t, v[c] - __builtin_bit_cast(float, vb[c] & 0xffff0000u));
+  hi.x = __builtin_amdgcn_perm(vb[1], vb[0], 0x07060302u);
+  hi.y = __builtin_amdgcn_perm(vb[3], vb[2], 0x07060302u);
+  lo.x = __builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u);
+  lo.y = __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u);
+}
+
+// the same split into f16 parts rounded to nearest
+__device__ __forceinline__ void m_split4_f16(const f4 v, u2v& hi, u2v& lo) {
+  uint32_t hb[4], lb[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const _Float16 h = (_Float16)v[c];
+    hb[c] = __builtin_bit_cast(uint16_t, h);
+    lb[c] = __builtin_bit_cast(uint16_t, (_Float16)(v[c] - (float)h));
+  }
+  hi.x = hb[0] | (hb[1] << 16);
+  hi.y = hb[2] | (hb[3] << 16);
+  lo.x = lb[0] | (lb[1] << 16);
+  lo.y = lb[2] | (lb[3] << 16);
+}
+
+// NV float4 of an R x BK operand tile for m_gemm_bf: modes 0 / 1 as m_opnd_load; mode 2 (unit stride
+// along rows) gives each thread one group of four rows at NV consecutive k (thread tid: rows
+// 4 (tid % (R / 4)) .., k = NV (tid / (R / 4)) ..), so the store can write them transposed as
+// runs along k
+template <int R, int BK, int NV>
+__device__ __forceinline__ void m_bf_load(const float* P, int64_t sr, int64_t sk, int nrows, int r0, int kk, int k1,
+                                          int mode, float scale, f4 (&v)[NV]) {
+  static_assert(NV * 1024 == R * BK, "every element of the tile once");
+  if (mode != 2) {
+    m_opnd_load<R, BK>(P, sr, sk, nrows, r0, kk, k1, mode, scale, v);
+    return;
+  }
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int gr = r0 + (threadIdx.x % (R / 4)) * 4, kb = kk + (threadIdx.x / (R / 4)) * NV;
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int gk = kb + i;
+    v[i] = (gr < nrows && gk < k1) ? *reinterpret_cast<const f4*>(P + (int64_t)gk * sk + gr) : zero;
+    if (scale != 1.0f)
+#pragma unroll
+      for (int q = 0; q < 4; q++) v[i][q] = v[i][q] * scale;
+  }
+}
+
+template <int R, int BK, bool HF, int NV>
+__device__ __forceinline__ void m_bf_store(uint16_t* Sh, uint16_t* Sl, int mode, const f4 (&v)[NV]) {
+  constexpr int LD = m_bf_ld<R, BK>();
+  u2v hi[NV], lo[NV];
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    if (HF)
+      m_split4_f16(v[i], hi[i], lo[i]);
+    else
+      m_split4(v[i], hi[i], lo[i]);
+  }
+  if (mode == 2) {  // rows r .. r + 3 at k .. k + NV - 1: per row, NV consecutive elements
+    static_assert(NV == 2 || NV == 4, "runs of 2 or 4 along k");
+    const int r = (threadIdx.x % (R / 4)) * 4, k = (threadIdx.x / (R / 4)) * NV;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      // element q of each of the NV vectors: bf16 half (q & 1) of word q >> 1
+      uint32_t eh[NV], el[NV];
+#pragma unroll
+      for (int i = 0; i < NV; i++) {
+        const uint32_t wh = (q >> 1) ? hi[i].y : hi[i].x, wl = (q >> 1) ? lo[i].y : lo[i].x;
+        eh[i] = (q & 1) ? (wh >> 16) : (wh & 0xffffu);
+        el[i] = (q & 1) ? (wl >> 16) : (wl & 0xffffu);
+      }
+      if constexpr (NV == 4) {
+        *reinterpret_cast<u2v*>(Sh + (r + q) * LD + k) = u2v{eh[0] | (eh[1] << 16), eh[2] | (eh[3] << 16)};
+        *reinterpret_cast<u2v*>(Sl + (r + q) * LD + k) = u2v{el[0] | (el[1] << 16), el[2] | (el[3] << 16)};
+      } else {
+        *reinterpret_cast<uint32_t*>(Sh + (r + q) * LD + k) = eh[0] | (eh[1] << 16);
+        *reinterpret_cast<uint32_t*>(Sl + (r + q) * LD + k) = el[0] | (el[1] << 16);
+      }
+    }
+  } else {  // row r, columns k .. k + 3
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int e = threadIdx.x + 256 * i;
+      const int r = e / (BK / 4), k = (e % (BK / 4)) * 4;
+      *reinterpret_cast<u2v*>(Sh + r * LD + k) = hi[i];
+      *reinterpret_cast<u2v*>(Sl + r * LD + k) = lo[i];
+    }
+  }
+}
+
+template <int BM, bool HF>
+__device__ __forceinline__ void m_gemm_bf(const MGemmArgs& a, int bx, int by, int bz) {
+  using Cf = MGemmCfg<BM>;
+  constexpr int BN = Cf::BN, BK = Cf::BK, TM = Cf::TM;
+  constexpr int LDA = m_bf_ld<BM, BK>(), LDB = m_bf_ld<BN, BK>();
+  static_assert(BK % 32 == 0, "k slabs of whole 32-deep MFMA steps");
+  __shared__ __attribute__((aligned(16))) uint16_t Ah[BM * LDA], Al[BM * LDA];
+  __shared__ __attribute__((aligned(16))) uint16_t Bh[BN * LDB], Bl[BN * LDB];
+  const int b = bz, m0 = by * BM, n0 = bx * BN;
+  if (a.causal == 1 && n0 > m0 + BM - 1) return;  // every element has n > m
+  if (a.causal == 1 && a.live && !a.live[(m0 >> 6) * a.nlb + (n0 >> 6)]) return;  // no pair may attend
+  const float* A = a.A + (int64_t)(b / a.divA) * a.sAb;
+  const float* B = a.B + (int64_t)(b / a.divB) * a.sBb;
+  int k0 = 0, k1 = a.K;
+  if (a.causal == 2) k1 = min(a.K, m0 + BM);
+  if (a.causal == 3) k0 = (m0 / BK) * BK;
+  const uint8_t* lrow = (a.live && a.causal >= 2) ? a.live + (a.causal == 2 ? (int64_t)(m0 >> 6) * a.nlb : (m0 >> 6))
+                                                  : nullptr;
+  const int lstep = a.causal == 2 ? 1 : a.nlb;
+  auto next_live = [&](int kk) {
+    if (lrow)
+      while (kk < k1 && !lrow[(kk >> 6) * lstep]) kk += BK;
+    return kk;
+  };
+  k0 = next_live(k0);
+  const int amode = m_opnd_mode(A, a.sAm, a.sAk, a.sAb, a.M, a.K);
+  const int bmode = m_opnd_mode(B, a.sBn, a.sBk, a.sBb, a.N, a.K);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
+  const int wm = (w >> 1) * (BM / 2), wn = (w & 1) * 32;
+  f4 acc[TM][2];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  f4 ra[Cf::NA], rb[Cf::NB];
+  if (k0 < k1) {
+    m_bf_load<BM, BK>(A, a.sAm, a.sAk, a.M, m0, k0, k1, amode, a.a_scale, ra);
+    m_bf_load<BN, BK>(B, a.sBn, a.sBk, a.N, n0, k0, k1, bmode, 1.0f, rb);
+  }
+  for (int kk = k0; kk < k1;) {
+    m_bf_store<BM, BK, HF>(Ah, Al, amode, ra);
+    m_bf_store<BN, BK, HF>(Bh, Bl, bmode, rb);
+    __syncthreads();
+    const int kn = next_live(kk + BK);
+    if (kn < k1) {
+      m_bf_load<BM, BK>(A, a.sAm, a.sAk, a.M, m0, kn, k1, amode, a.a_scale, ra);
+      m_bf_load<BN, BK>(B, a.sBn, a.sBk, a.N, n0, kn, k1, bmode, 1.0f, rb);
+    }
+#pragma unroll
+    for (int kc = 0; kc < BK / 32; kc++) {
+      bf8 ah[TM], al[TM], bh[2], bl[2];
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const int o = (wm + 16 * i + li) * LDA + 32 * kc + 8 * g;
+        ah[i] = *reinterpret_cast<const bf8*>(Ah + o);
+        al[i] = *reinterpret_cast<const bf8*>(Al + o);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int o = (wn + 16 * j + li) * LDB + 32 * kc + 8 * g;
+        bh[j] = *reinterpret_cast<const bf8*>(Bh + o);
+        bl[j] = *reinterpret_cast<const bf8*>(Bl + o);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          if (HF) {
+            acc[i][j] = mfma_f16(__builtin_bit_cast(half8, ah[i]), __builtin_bit_cast(half8, bh[j]), acc[i][j]);
+            acc[i][j] = mfma_f16(__builtin_bit_cast(half8, al[i]), __builtin_bit_cast(half8, bh[j]), acc[i][j]);
+            acc[i][j] = mfma_f16(__builtin_bit_cast(half8, ah[i]), __builtin_bit_cast(half8, bl[j]), acc[i][j]);
+          } else {
+            acc[i][j] = mfma_bf16(ah[i], bh[j], acc[i][j]);
+            acc[i][j] = mfma_bf16(al[i], bh[j], acc[i][j]);
+            acc[i][j] = mfma_bf16(ah[i], bl[j], acc[i][j]);
+          }
+        }
+    }
+    __syncthreads();
+    kk = kn;
+  }
+  float* C = a.C + (int64_t)b * a.sCb;
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int m = m0 + wm + 16 * i + 4 * g + e;
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int n = n0 + wn + 16 * j + li;
+        if (n >= a.N) continue;
+        float* c = C + (int64_t)m * a.sCm + (int64_t)n * a.sCn;
+        *c = a.accumulate ? *c + acc[i][j][e] : acc[i][j][e];
+      }
+    }
+}
+
+template <int BM, bool HF>
+__device__ __forceinline__ void m_gemm_bf_tile(const MGemmArgs& a, int l) {
+  const int nx = (a.N + 63) / 64, ny = (a.M + BM - 1) / BM;
+  const int bx = l % nx, yy = (l / nx) % ny, bz = l / (nx * ny);
+  m_gemm_bf<BM, HF>(a, bx, a.causal == 2 ? ny - 1 - yy : yy, bz);
+}
+extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm_bf(MGemmArgs a) {
+  const int l = m_xcd_tile((a.N + 63) / 64 * ((a.M + 63) / 64) * a.batch);
+  if (l >= 0) m_gemm_bf_tile<64, false>(a, l);
+}
+extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32_bf(MGemmArgs a) {
+  const int l = m_xcd_tile((a.N + 63) / 64 * ((a.M + 31) / 32) * a.batch);
+  if (l >= 0) m_gemm_bf_tile<32, false>(a, l);
+}
+extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm_hf(MGemmArgs a) {
+  const int l = m_xcd_tile((a.N + 63) / 64 * ((a.M + 63) / 64) * a.batch);
+  if (l >= 0) m_gemm_bf_tile<64, true>(a, l);
+}
+extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32_hf(MGemmArgs a) {
+  const int l = m_xcd_tile((a.N + 63) / 64 * ((a.M + 31) / 32) * a.batch);
+  if (l >= 0) m_gemm_bf_tile<32, true>(a, l);
+}
+extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32g_bf(MGemmGroupArgs g) {
+  const int id = m_xcd_tile(g.start[g.np]);
+  if (id < 0) return;
+  if (id < g.start[1])
+    m_gemm_bf_tile<32, false>(g.p[0], id);
+  else if (g.np > 1 && id < g.start[2])
+    m_gemm_bf_tile<32, false>(g.p[1], id - g.start[1]);
+  else if (g.np > 2 && id < g.start[3])
+    m_gemm_bf_tile<32, false>(g.p[2], id - g.start[2]);
+}
+
 // ------------------------------------------------------------------ attention softmax
 // grid (ceil(t / 4), nh), 256 threads: one wave per row i of head h (wave reductions, no barriers),
 // over j <= i: p = exp(s - max) / sum (0 for j > i).  Packed layouts (a.live): only the row's live

@@ -166,7 +166,8 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_m_lora_mask",      "rtq_m_gemm32g",        "rtq_m_gemm_q8",        "rtq_m_gemm32_q8",
     "rtq_m_attn_fwd64",     "rtq_m_attn_fwd128",    "rtq_m_attn_dq64",      "rtq_m_attn_dq128",
     "rtq_m_attn_dkv64",     "rtq_m_attn_dkv128",    "rtq_m_attn_merge_fwd", "rtq_m_attn_merge_dq",
-    "rtq_m_attn_merge_dkv", "rtq_m_attn_bwd_d"};
+    "rtq_m_attn_merge_dkv", "rtq_m_attn_bwd_d",     "rtq_m_gemm_bf",        "rtq_m_gemm32_bf",
+    "rtq_m_gemm32g_bf",     "rtq_m_gemm_hf",        "rtq_m_gemm32_hf"};
 
 struct TimedLaunch {
   int kid;
