@@ -1,0 +1,703 @@
+// rtq_fa.hip — fused causal GQA attention of the training step on 16-bit MFMA with LDS-shared
+// tiles (Attention::forward / backward, src/attention.rs:187-235, :262-320); the probabilities are
+// never stored.  Included by rtq_model_kernels.hip after rtq_attn.hip (whose masks, row helpers and
+// merge kernels it shares).
+//
+// Work: a workgroup of four waves takes one item (MAttnItem) of 64 rows - 64 queries of one head
+// (forward, dq) or 64 keys of one KV head (dk / dv) - wave w owning rows 16 w .. 16 w + 15, over
+// the item's range of 64-wide tiles of the other side; each tile is staged in LDS once and shared
+// by the four waves, the next tile's loads in registers while the current one is multiplied.
+// Arithmetic, per product (acc is f32, the MFMA 16x16x32 output layout lane = column li, rows
+// 4 g .. 4 g + 3):
+//   forward S = (q scale) k^T, o = p v, and the backward's recomputed S: f16 MFMA; the stored k and
+//     v are f16 values (kv_f16), staged exactly as one f16 plane; q scale and p are split into f16
+//     hi = f16(x) and lo = f16(x - hi) (22 significant bits): acc += xh y + xl y;
+//   backward dP = dO v^T, dq = dS k, dk = dS^T q, dv = p^T dO: bf16 MFMA, both operands split into
+//     bf16 hi / lo by truncation (f16 k and v split exactly), acc += xh yh + xl yh + xh yl (a
+//     relative error near 2^-16 per product; gradients may lie below f16's range).
+// The scores are taken in base 2: q is scaled by scale log2(e), so p = 2^(s2 - m2) with the hardware
+// exp2 (v_exp_f32); the stored lse stays natural (m2 ln 2 + log l) and the backward recomputes
+// p = 2^(s2 - lse log2(e)).  Masks, online softmax (running max m2 and sum l per query row,
+// rescaled by 2^(m_old - m_new)), D = dO . o, ds = (p (dp - D)) scale and the partial-slot merges
+// follow rtq_attn.hip (whose forward merge reads base-2 maxima); the mask works on segments held
+// in registers (the keys' per tile, the rows' per item).  An item covering part of its block's
+// range writes its four 16-row sub-blocks to slots slot + w n (n = items of the block, in
+// it.pad0), so each sub-block's partials are contiguous for rtq_m_attn_merge_*.
+
+constexpr int kFaPad = 8;  // 16-bit elements of row padding: a lane group's 16 rows on distinct banks
+constexpr float kLog2e = 1.44269504088896340736f, kLn2 = 0.693147180559945309417f;
+
+// two floats -> packed f16 pair, rounded toward zero (one v_cvt_pkrtz; exact for f16 values)
+__device__ __forceinline__ uint32_t fa_pk(float x, float y) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, y));
+}
+__device__ __forceinline__ float fa_lo16(uint32_t p) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(p & 0xffffu)); }
+__device__ __forceinline__ float fa_hi16(uint32_t p) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(p >> 16)); }
+// two floats -> f16 hi / lo pairs: hi = f16(x) toward zero, lo = f16(x - hi) (x - hi is exact in
+// f32), 22 significant bits of x
+__device__ __forceinline__ void fa_split_pair(float x, float y, uint32_t& hi, uint32_t& lo) {
+  hi = fa_pk(x, y);
+  lo = fa_pk(x - fa_lo16(hi), y - fa_hi16(hi));
+}
+__device__ __forceinline__ void fa_split_f16(const f4 v, u2v& hi, u2v& lo) {
+  uint32_t h0, l0, h1, l1;
+  fa_split_pair(v[0], v[1], h0, l0);
+  fa_split_pair(v[2], v[3], h1, l1);
+  hi = u2v{h0, h1};
+  lo = u2v{l0, l1};
+}
+// four floats -> f16 (exact for f16 values), packed
+__device__ __forceinline__ u2v fa_f16(const f4 v) { return u2v{fa_pk(v[0], v[1]), fa_pk(v[2], v[3])}; }
+// one float -> bf16 hi / lo bits (truncation)
+__device__ __forceinline__ void fa_split_bf(float x, uint32_t& hi, uint32_t& lo) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, x);
+  hi = b >> 16;
+  lo = __builtin_bit_cast(uint32_t, x - __builtin_bit_cast(float, b & 0xffff0000u)) >> 16;
+}
+__device__ __forceinline__ half8 fa_h8(const uint16_t* p) { return *reinterpret_cast<const half8*>(p); }
+__device__ __forceinline__ bf8 fa_b8(const uint16_t* p) { return *reinterpret_cast<const bf8*>(p); }
+
+// ---- tile staging: 64 rows x HD of X (rows r0 + i, stride ld, clamped to t - 1), 256 threads
+// natural layout [row][d]: thread -> row tid / 4, columns (tid % 4) HD / 4 .. (NF float4)
+template <int HD>
+struct FaNat {
+  static constexpr int NF = HD / 16;
+  f4 v[NF];
+  __device__ __forceinline__ void load(const float* X, int64_t ld, int r0, int t) {
+    const float* p = X + (int64_t)min(r0 + (int)(threadIdx.x >> 2), t - 1) * ld + (threadIdx.x & 3) * (HD / 4);
+#pragma unroll
+    for (int i = 0; i < NF; i++) v[i] = *reinterpret_cast<const f4*>(p + 4 * i);
+  }
+};
+// transposed layout [d][row]: thread -> rows KPT kg .. (kg = tid / (HD / 4)), columns 4 (tid % (HD / 4)) ..
+template <int HD>
+struct FaTr {
+  static constexpr int KPT = HD / 16;  // rows per thread: 8 (HD 128) or 4 (HD 64)
+  f4 v[KPT];
+  __device__ __forceinline__ void load(const float* X, int64_t ld, int r0, int t) {
+    const int kg = threadIdx.x / (HD / 4), d4 = threadIdx.x % (HD / 4);
+#pragma unroll
+    for (int i = 0; i < KPT; i++)
+      v[i] = *reinterpret_cast<const f4*>(X + (int64_t)min(r0 + kg * KPT + i, t - 1) * ld + 4 * d4);
+  }
+};
+// stores: f16 one plane (exact values), natural
+template <int HD, int LD>
+__device__ __forceinline__ void fa_store_nat_f16(const FaNat<HD>& s, uint16_t* P) {
+  uint16_t* p = P + (threadIdx.x >> 2) * LD + (threadIdx.x & 3) * (HD / 4);
+#pragma unroll
+  for (int i = 0; i < FaNat<HD>::NF; i++) *reinterpret_cast<u2v*>(p + 4 * i) = fa_f16(s.v[i]);
+}
+// f16 hi / lo planes, natural, values times mul
+template <int HD, int LD>
+__device__ __forceinline__ void fa_store_nat_f16x2(const FaNat<HD>& s, float mul, uint16_t* Ph, uint16_t* Pl) {
+  const int o = (threadIdx.x >> 2) * LD + (threadIdx.x & 3) * (HD / 4);
+#pragma unroll
+  for (int i = 0; i < FaNat<HD>::NF; i++) {
+    u2v hi, lo;
+    fa_split_f16(mul == 1.0f ? s.v[i] : s.v[i] * mul, hi, lo);
+    *reinterpret_cast<u2v*>(Ph + o + 4 * i) = hi;
+    *reinterpret_cast<u2v*>(Pl + o + 4 * i) = lo;
+  }
+}
+// bf16 hi / lo planes, natural
+template <int HD, int LD>
+__device__ __forceinline__ void fa_store_nat_bf(const FaNat<HD>& s, uint16_t* Ph, uint16_t* Pl) {
+  const int o = (threadIdx.x >> 2) * LD + (threadIdx.x & 3) * (HD / 4);
+#pragma unroll
+  for (int i = 0; i < FaNat<HD>::NF; i++) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) fa_split_bf(s.v[i][c], h[c], l[c]);
+    *reinterpret_cast<u2v*>(Ph + o + 4 * i) = u2v{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    *reinterpret_cast<u2v*>(Pl + o + 4 * i) = u2v{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+  }
+}
+// transposed stores [d][row] (row stride LD): f16 one plane, or bf16 hi / lo planes
+template <int HD, int LD>
+__device__ __forceinline__ void fa_store_tr_f16(const FaTr<HD>& s, uint16_t* P) {
+  constexpr int KPT = FaTr<HD>::KPT;
+  const int kg = threadIdx.x / (HD / 4), d4 = threadIdx.x % (HD / 4);
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    uint16_t* p = P + (4 * d4 + c) * LD + kg * KPT;
+    if constexpr (KPT == 8)
+      *reinterpret_cast<u4v*>(p) = u4v{fa_pk(s.v[0][c], s.v[1][c]), fa_pk(s.v[2][c], s.v[3][c]),
+                                       fa_pk(s.v[4][c], s.v[5][c]), fa_pk(s.v[6][c], s.v[7][c])};
+    else
+      *reinterpret_cast<u2v*>(p) = u2v{fa_pk(s.v[0][c], s.v[1][c]), fa_pk(s.v[2][c], s.v[3][c])};
+  }
+}
+template <int HD, int LD>
+__device__ __forceinline__ void fa_store_tr_bf(const FaTr<HD>& s, uint16_t* Ph, uint16_t* Pl) {
+  constexpr int KPT = FaTr<HD>::KPT;
+  const int kg = threadIdx.x / (HD / 4), d4 = threadIdx.x % (HD / 4);
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    uint32_t h[KPT], l[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; i++) fa_split_bf(s.v[i][c], h[i], l[i]);
+    const int o = (4 * d4 + c) * LD + kg * KPT;
+    if constexpr (KPT == 8) {
+      *reinterpret_cast<u4v*>(Ph + o) = u4v{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+      *reinterpret_cast<u4v*>(Pl + o) = u4v{l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16)};
+    } else {
+      *reinterpret_cast<u2v*>(Ph + o) = u2v{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+      *reinterpret_cast<u2v*>(Pl + o) = u2v{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+    }
+  }
+}
+
+// a 16 x 64 tile in MFMA output order (tv[j][i]: row 4 g + i, column 16 j + li) -> two 16-bit planes
+// [row][col] (stride 64 + kFaPad) of the wave: f16 hi / lo (HF) or bf16 hi / lo
+template <bool HF>
+__device__ __forceinline__ void fa_put_tile(const float (&tv)[4][4], uint16_t* Th, uint16_t* Tl) {
+  constexpr int LD = 64 + kFaPad;
+  const int lane = threadIdx.x & 63, li = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; i += 2)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      uint32_t h, l;  // rows 4 g + i (low halves) and 4 g + i + 1 (high halves)
+      if (HF) {
+        fa_split_pair(tv[j][i], tv[j][i + 1], h, l);
+      } else {
+        uint32_t h0, l0, h1, l1;
+        fa_split_bf(tv[j][i], h0, l0);
+        fa_split_bf(tv[j][i + 1], h1, l1);
+        h = h0 | (h1 << 16);
+        l = l0 | (l1 << 16);
+      }
+      Th[(4 * g + i) * LD + 16 * j + li] = (uint16_t)(h & 0xffffu);
+      Tl[(4 * g + i) * LD + 16 * j + li] = (uint16_t)(l & 0xffffu);
+      Th[(4 * g + i + 1) * LD + 16 * j + li] = (uint16_t)(h >> 16);
+      Tl[(4 * g + i + 1) * LD + 16 * j + li] = (uint16_t)(l >> 16);
+    }
+}
+
+// may query i (segment si) attend to key j (segment sj)?  (attn_ok with both segments in registers:
+// no load under the condition)
+__device__ __forceinline__ bool fa_ok(int i, int j, int si, int sj, int t) { return j <= i && i < t && (sj == 0 || sj == si); }
+
+// the next live 64-wide tile of rows r0 (64-block qb) at or after kt, below b1
+__device__ __forceinline__ int fa_next_live(const MAttnArgs& a, int qb, int kt, int b1) {
+  while (kt < b1 && !attn_tile_live(a, qb, kt)) kt++;
+  return kt;
+}
+
+// ------------------------------------------------------------------ forward
+template <int HD>
+struct FaFwdLds {
+  static constexpr int LDK = HD + kFaPad, LDV = 64 + kFaPad;
+  uint16_t k[64 * LDK];    // K tile [key][d], f16
+  uint16_t vt[HD * LDV];   // V tile [d][key], f16
+  uint16_t ph[4][16 * LDV], pl[4][16 * LDV];  // per wave: p [row][key], f16 hi / lo
+};
+
+template <int HD>
+__device__ __forceinline__ void fa_fwd(const MAttnArgs& a, const MAttnItem& it, FaFwdLds<HD>& L) {
+  constexpr int NC = HD / 16, NK = HD / 32, LDK = FaFwdLds<HD>::LDK, LDV = FaFwdLds<HD>::LDV;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
+  const int h = it.head, kvh = h / (a.nh / a.nkv), qb = it.blk, r0 = qb * 64 + 16 * w;
+  // q rows of the wave times scale log2(e) (scores in base 2: p = 2^(s2 - m2)), f16 hi / lo
+  // operand fragments
+  const float qs2 = a.scale * kLog2e;
+  half8 qh[NK], ql[NK];
+  {
+    const float* qr = a.q + (int64_t)min(r0 + li, a.t - 1) * a.ldq + (int64_t)h * HD + 8 * g;
+#pragma unroll
+    for (int c = 0; c < NK; c++) {
+      u2v h0, l0, h1, l1;
+      fa_split_f16(*reinterpret_cast<const f4*>(qr + 32 * c) * qs2, h0, l0);
+      fa_split_f16(*reinterpret_cast<const f4*>(qr + 32 * c + 4) * qs2, h1, l1);
+      qh[c] = __builtin_bit_cast(half8, u4v{h0.x, h0.y, h1.x, h1.y});
+      ql[c] = __builtin_bit_cast(half8, u4v{l0.x, l0.y, l1.x, l1.y});
+    }
+  }
+  int si[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) si[i] = attn_seg(a, r0 + 4 * g + i);
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 oacc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; c++) oacc[c] = zero;
+  float mr[4], lr[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    mr[i] = -__builtin_inff();
+    lr[i] = 0.0f;
+  }
+  const float* kb = a.k + (int64_t)kvh * HD;
+  const float* vb = a.v + (int64_t)kvh * HD;
+  FaNat<HD> kn;
+  FaTr<HD> vn;
+  int kt = fa_next_live(a, qb, it.b0, it.b1);
+  if (kt < it.b1) {
+    kn.load(kb, a.ldk, kt * 64, a.t);
+    vn.load(vb, a.ldv, kt * 64, a.t);
+  }
+  while (kt < it.b1) {  // kt is workgroup-uniform: every wave runs the same barriers
+    const int k0 = kt * 64;
+    fa_store_nat_f16<HD, LDK>(kn, L.k);
+    fa_store_tr_f16<HD, LDV>(vn, L.vt);
+    __syncthreads();
+    const int kt2 = fa_next_live(a, qb, kt + 1, it.b1);
+    if (kt2 < it.b1) {
+      kn.load(kb, a.ldk, kt2 * 64, a.t);
+      vn.load(vb, a.ldv, kt2 * 64, a.t);
+    }
+    f4 s[4] = {zero, zero, zero, zero};
+#pragma unroll
+    for (int c = 0; c < NK; c++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const half8 kf = fa_h8(L.k + (16 * j + li) * LDK + 32 * c + 8 * g);
+        s[j] = mfma_f16(qh[c], kf, s[j]);
+        s[j] = mfma_f16(ql[c], kf, s[j]);
+      }
+    float p[4][4];
+    int sk[4];  // segments of the lane's keys
+#pragma unroll
+    for (int j = 0; j < 4; j++) sk[j] = attn_seg(a, k0 + 16 * j + li);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = r0 + 4 * g + i;
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        p[j][i] = fa_ok(row, k0 + 16 * j + li, si[i], sk[j], a.t) ? s[j][i] : -__builtin_inff();
+        mx = fmaxf(mx, p[j][i]);
+      }
+      mx = group16_max(mx);
+      const float mn = fmaxf(mr[i], mx);
+      const bool none = mn == -__builtin_inff();  // no key of the row so far
+      const float corr = mr[i] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mr[i] - mn);
+      float ls = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        p[j][i] = none ? 0.0f : __builtin_amdgcn_exp2f(p[j][i] - mn);  // 2^-inf = 0 for masked keys
+        ls = ls + p[j][i];
+      }
+      ls = group16_sum(ls);
+      lr[i] = lr[i] * corr + ls;
+      mr[i] = mn;
+#pragma unroll
+      for (int c = 0; c < NC; c++) oacc[c][i] = oacc[c][i] * corr;
+    }
+    fa_put_tile<true>(p, L.ph[w], L.pl[w]);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const half8 ph = fa_h8(L.ph[w] + li * LDV + 32 * c + 8 * g);
+      const half8 pl = fa_h8(L.pl[w] + li * LDV + 32 * c + 8 * g);
+#pragma unroll
+      for (int cc = 0; cc < NC; cc++) {
+        const half8 vf = fa_h8(L.vt + (16 * cc + li) * LDV + 32 * c + 8 * g);
+        oacc[cc] = mfma_f16(ph, vf, oacc[cc]);
+        oacc[cc] = mfma_f16(pl, vf, oacc[cc]);
+      }
+    }
+    __syncthreads();  // every wave is done with this tile's K, V (and its own p) before the next store
+    kt = kt2;
+  }
+  if (it.slot < 0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = r0 + 4 * g + i;
+      if (row >= a.t) continue;
+      float* orow = a.o + (int64_t)row * a.ldq + (int64_t)h * HD + li;
+#pragma unroll
+      for (int c = 0; c < NC; c++) orow[16 * c] = __fdiv_rn(oacc[c][i], lr[i]);
+      if (li == 0) a.lse[(int64_t)h * a.t + row] = mr[i] * kLn2 + logf(lr[i]);  // natural log-sum-exp
+    }
+  } else {  // partials: o, m (base 2), l
+    float* pp = a.part + (int64_t)(it.slot + w * it.pad0) * (32 * HD);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+      for (int c = 0; c < NC; c++) pp[(4 * g + i) * HD + 16 * c + li] = oacc[c][i];
+      if (li == 0) {
+        pp[16 * HD + 4 * g + i] = mr[i];
+        pp[16 * HD + 16 + 4 * g + i] = lr[i];
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ dq
+template <int HD>
+struct FaDqLds {
+  static constexpr int LDK = HD + kFaPad, LDT = 64 + kFaPad;
+  uint16_t k[64 * LDK];                  // K [key][d], f16 (S)
+  uint16_t vh[64 * LDK], vl[64 * LDK];   // V [key][d], bf16 hi / lo (dP = dO V^T)
+  uint16_t kth[HD * LDT], ktl[HD * LDT]; // K [d][key], bf16 hi / lo (dq = dS K)
+  uint16_t sh[4][16 * LDT], sl[4][16 * LDT];  // per wave: dS [row][key], bf16 hi / lo
+};
+
+template <int HD>
+__device__ __forceinline__ void fa_dq(const MAttnArgs& a, const MAttnItem& it, FaDqLds<HD>& L) {
+  constexpr int NC = HD / 16, NK = HD / 32, LDK = FaDqLds<HD>::LDK, LDT = FaDqLds<HD>::LDT;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
+  const int h = it.head, kvh = h / (a.nh / a.nkv), qb = it.blk, r0 = qb * 64 + 16 * w;
+  const float qs2 = a.scale * kLog2e;  // scores in base 2, as the forward
+  half8 qh[NK], ql[NK];
+  bf8 dh[NK], dl[NK];
+  {
+    const int rc = min(r0 + li, a.t - 1);
+    const float* qr = a.q + (int64_t)rc * a.ldq + (int64_t)h * HD + 8 * g;
+    const float* dr = a.dO + (int64_t)rc * a.ldq + (int64_t)h * HD + 8 * g;
+#pragma unroll
+    for (int c = 0; c < NK; c++) {
+      u2v h0, l0, h1, l1;
+      fa_split_f16(*reinterpret_cast<const f4*>(qr + 32 * c) * qs2, h0, l0);
+      fa_split_f16(*reinterpret_cast<const f4*>(qr + 32 * c + 4) * qs2, h1, l1);
+      qh[c] = __builtin_bit_cast(half8, u4v{h0.x, h0.y, h1.x, h1.y});
+      ql[c] = __builtin_bit_cast(half8, u4v{l0.x, l0.y, l1.x, l1.y});
+      uint32_t eh[8], el[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) fa_split_bf(dr[32 * c + e], eh[e], el[e]);
+      dh[c] = __builtin_bit_cast(bf8, u4v{eh[0] | (eh[1] << 16), eh[2] | (eh[3] << 16), eh[4] | (eh[5] << 16), eh[6] | (eh[7] << 16)});
+      dl[c] = __builtin_bit_cast(bf8, u4v{el[0] | (el[1] << 16), el[2] | (el[3] << 16), el[4] | (el[5] << 16), el[6] | (el[7] << 16)});
+    }
+  }
+  int si[4];
+  float lq[4], Dq[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int row = min(r0 + 4 * g + i, a.t - 1);
+    si[i] = attn_seg(a, row);
+    lq[i] = a.lse[(int64_t)h * a.t + row] * kLog2e;
+    Dq[i] = a.D[(int64_t)h * a.t + row];
+  }
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 acc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; c++) acc[c] = zero;
+  const float* kb = a.k + (int64_t)kvh * HD;
+  const float* vb = a.v + (int64_t)kvh * HD;
+  FaNat<HD> kn, vn;
+  FaTr<HD> kt_;
+  int kt = fa_next_live(a, qb, it.b0, it.b1);
+  if (kt < it.b1) {
+    kn.load(kb, a.ldk, kt * 64, a.t);
+    vn.load(vb, a.ldv, kt * 64, a.t);
+    kt_.load(kb, a.ldk, kt * 64, a.t);
+  }
+  while (kt < it.b1) {
+    const int k0 = kt * 64;
+    fa_store_nat_f16<HD, LDK>(kn, L.k);
+    fa_store_nat_bf<HD, LDK>(vn, L.vh, L.vl);
+    fa_store_tr_bf<HD, LDT>(kt_, L.kth, L.ktl);
+    __syncthreads();
+    const int kt2 = fa_next_live(a, qb, kt + 1, it.b1);
+    if (kt2 < it.b1) {
+      kn.load(kb, a.ldk, kt2 * 64, a.t);
+      vn.load(vb, a.ldv, kt2 * 64, a.t);
+      kt_.load(kb, a.ldk, kt2 * 64, a.t);
+    }
+    f4 s[4] = {zero, zero, zero, zero}, dp[4] = {zero, zero, zero, zero};
+#pragma unroll
+    for (int c = 0; c < NK; c++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int o = (16 * j + li) * LDK + 32 * c + 8 * g;
+        const half8 kf = fa_h8(L.k + o);
+        s[j] = mfma_f16(qh[c], kf, s[j]);
+        s[j] = mfma_f16(ql[c], kf, s[j]);
+        const bf8 vh = fa_b8(L.vh + o), vl = fa_b8(L.vl + o);
+        dp[j] = mfma_bf16(dh[c], vh, dp[j]);
+        dp[j] = mfma_bf16(dl[c], vh, dp[j]);
+        dp[j] = mfma_bf16(dh[c], vl, dp[j]);
+      }
+    float ds[4][4];
+    int sk[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) sk[j] = attn_seg(a, k0 + 16 * j + li);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const bool ok = fa_ok(r0 + 4 * g + i, k0 + 16 * j + li, si[i], sk[j], a.t);
+        const float p = __builtin_amdgcn_exp2f(s[j][i] - lq[i]);
+        ds[j][i] = ok ? (p * (dp[j][i] - Dq[i])) * a.scale : 0.0f;
+      }
+    fa_put_tile<false>(ds, L.sh[w], L.sl[w]);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const bf8 sh = fa_b8(L.sh[w] + li * LDT + 32 * c + 8 * g);
+      const bf8 sl = fa_b8(L.sl[w] + li * LDT + 32 * c + 8 * g);
+#pragma unroll
+      for (int cc = 0; cc < NC; cc++) {
+        const int o = (16 * cc + li) * LDT + 32 * c + 8 * g;
+        const bf8 kh = fa_b8(L.kth + o), kl = fa_b8(L.ktl + o);
+        acc[cc] = mfma_bf16(sh, kh, acc[cc]);
+        acc[cc] = mfma_bf16(sl, kh, acc[cc]);
+        acc[cc] = mfma_bf16(sh, kl, acc[cc]);
+      }
+    }
+    __syncthreads();
+    kt = kt2;
+  }
+  if (it.slot < 0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = r0 + 4 * g + i;
+      if (row >= a.t) continue;
+      float* q = a.dq + (int64_t)row * a.ldq + (int64_t)h * HD + li;
+#pragma unroll
+      for (int c = 0; c < NC; c++) q[16 * c] = acc[c][i];
+    }
+  } else {
+    float* pp = a.part + (int64_t)(it.slot + w * it.pad0) * (32 * HD);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int c = 0; c < NC; c++) pp[(4 * g + i) * HD + 16 * c + li] = acc[c][i];
+  }
+}
+
+// ------------------------------------------------------------------ dk, dv
+// Item: 64 keys (it.blk) of KV head it.head over (group head, 64-query tile) pairs [b0, b1); each
+// pair is taken as two 32-query halves, staged as q scale (f16 hi / lo, [q][d], for S^T = k q^T),
+// q (bf16 hi / lo, [d][q], for dk += dS^T q), dO (bf16 hi / lo, [q][d] for dP^T = v dO^T and [d][q]
+// for dv += p^T dO).
+template <int HD>
+struct FaKvLds {
+  static constexpr int LDN = HD + kFaPad, LDT = 32 + kFaPad, LDP = 32 + kFaPad;
+  uint16_t qsh[32 * LDN], qsl[32 * LDN];    // q scale [q][d], f16 hi / lo
+  uint16_t qth[HD * LDT], qtl[HD * LDT];    // q [d][q], bf16 hi / lo
+  uint16_t dsh_[32 * LDN], dsl_[32 * LDN];  // dO [q][d], bf16 hi / lo
+  uint16_t dth[HD * LDT], dtl[HD * LDT];    // dO [d][q], bf16 hi / lo
+  uint16_t ph[4][16 * LDP], pl[4][16 * LDP], sh[4][16 * LDP], sl[4][16 * LDP];  // per wave: p^T, dS^T [key][q]
+};
+// 32 rows x HD staging (natural: thread -> row tid / 8, columns (tid % 8) HD / 8 ..; transposed:
+// thread -> rows KPT kg .., columns 4 (tid % (HD / 4)) .., KPT = HD / 32)
+template <int HD>
+struct FaNat32 {
+  static constexpr int NF = HD / 32;
+  f4 v[NF];
+  __device__ __forceinline__ void load(const float* X, int64_t ld, int r0, int t) {
+    const float* p = X + (int64_t)min(r0 + (int)(threadIdx.x >> 3), t - 1) * ld + (threadIdx.x & 7) * (HD / 8);
+#pragma unroll
+    for (int i = 0; i < NF; i++) v[i] = *reinterpret_cast<const f4*>(p + 4 * i);
+  }
+};
+template <int HD>
+struct FaTr32 {
+  static constexpr int KPT = HD / 32;  // 4 (HD 128) or 2 (HD 64)
+  f4 v[KPT];
+  __device__ __forceinline__ void load(const float* X, int64_t ld, int r0, int t) {
+    const int kg = threadIdx.x / (HD / 4), d4 = threadIdx.x % (HD / 4);
+#pragma unroll
+    for (int i = 0; i < KPT; i++)
+      v[i] = *reinterpret_cast<const f4*>(X + (int64_t)min(r0 + kg * KPT + i, t - 1) * ld + 4 * d4);
+  }
+};
+template <int HD, int LD>
+__device__ __forceinline__ void fa_store32_nat(const FaNat32<HD>& s, bool f16, float mul, uint16_t* Ph, uint16_t* Pl) {
+  const int o = (threadIdx.x >> 3) * LD + (threadIdx.x & 7) * (HD / 8);
+#pragma unroll
+  for (int i = 0; i < FaNat32<HD>::NF; i++) {
+    u2v hi, lo;
+    if (f16) {
+      fa_split_f16(mul == 1.0f ? s.v[i] : s.v[i] * mul, hi, lo);
+    } else {
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) fa_split_bf(s.v[i][c], h[c], l[c]);
+      hi = u2v{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+      lo = u2v{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+    }
+    *reinterpret_cast<u2v*>(Ph + o + 4 * i) = hi;
+    *reinterpret_cast<u2v*>(Pl + o + 4 * i) = lo;
+  }
+}
+template <int HD, int LD>
+__device__ __forceinline__ void fa_store32_tr_bf(const FaTr32<HD>& s, uint16_t* Ph, uint16_t* Pl) {
+  constexpr int KPT = FaTr32<HD>::KPT;
+  const int kg = threadIdx.x / (HD / 4), d4 = threadIdx.x % (HD / 4);
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    uint32_t h[KPT], l[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; i++) fa_split_bf(s.v[i][c], h[i], l[i]);
+    const int o = (4 * d4 + c) * LD + kg * KPT;
+    if constexpr (KPT == 4) {
+      *reinterpret_cast<u2v*>(Ph + o) = u2v{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+      *reinterpret_cast<u2v*>(Pl + o) = u2v{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+    } else {
+      *reinterpret_cast<uint32_t*>(Ph + o) = h[0] | (h[1] << 16);
+      *reinterpret_cast<uint32_t*>(Pl + o) = l[0] | (l[1] << 16);
+    }
+  }
+}
+// a 16 x 32 tile in MFMA output order (tv[j][i]: row 4 g + i, column 16 j + li, j < 2) -> bf16 hi / lo
+// planes [row][col] (stride 32 + kFaPad)
+__device__ __forceinline__ void fa_put_tile32(const float (&tv)[2][4], uint16_t* Th, uint16_t* Tl) {
+  constexpr int LD = 32 + kFaPad;
+  const int lane = threadIdx.x & 63, li = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      uint32_t h, l;
+      fa_split_bf(tv[j][i], h, l);
+      Th[(4 * g + i) * LD + 16 * j + li] = (uint16_t)h;
+      Tl[(4 * g + i) * LD + 16 * j + li] = (uint16_t)l;
+    }
+}
+
+template <int HD>
+__device__ __forceinline__ void fa_dkv(const MAttnArgs& a, const MAttnItem& it, FaKvLds<HD>& L) {
+  constexpr int NC = HD / 16, NK = HD / 32;
+  constexpr int LDN = FaKvLds<HD>::LDN, LDT = FaKvLds<HD>::LDT, LDP = FaKvLds<HD>::LDP;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
+  const int kvh = it.head, grp = a.nh / a.nkv, kbk = it.blk, c0 = kbk * 64 + 16 * w, nqt = (a.t + 63) / 64;
+  // the wave's 16 keys: k (f16, exact) and v (bf16 hi / lo) operand fragments
+  half8 kf[NK];
+  bf8 vh[NK], vl[NK];
+  {
+    const int kc = min(c0 + li, a.t - 1);
+    const float* kr = a.k + (int64_t)kc * a.ldk + (int64_t)kvh * HD + 8 * g;
+    const float* vr = a.v + (int64_t)kc * a.ldv + (int64_t)kvh * HD + 8 * g;
+#pragma unroll
+    for (int c = 0; c < NK; c++) {
+      const u2v k0 = fa_f16(*reinterpret_cast<const f4*>(kr + 32 * c));
+      const u2v k1 = fa_f16(*reinterpret_cast<const f4*>(kr + 32 * c + 4));
+      kf[c] = __builtin_bit_cast(half8, u4v{k0.x, k0.y, k1.x, k1.y});
+      uint32_t eh[8], el[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) fa_split_bf(vr[32 * c + e], eh[e], el[e]);
+      vh[c] = __builtin_bit_cast(bf8, u4v{eh[0] | (eh[1] << 16), eh[2] | (eh[3] << 16), eh[4] | (eh[5] << 16), eh[6] | (eh[7] << 16)});
+      vl[c] = __builtin_bit_cast(bf8, u4v{el[0] | (el[1] << 16), el[2] | (el[3] << 16), el[4] | (el[5] << 16), el[6] | (el[7] << 16)});
+    }
+  }
+  int skey[4];  // segments of the lane's keys c0 + 4 g + i
+#pragma unroll
+  for (int i = 0; i < 4; i++) skey[i] = attn_seg(a, c0 + 4 * g + i);
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 dk[NC], dv[NC];
+#pragma unroll
+  for (int c = 0; c < NC; c++) dk[c] = dv[c] = zero;
+  // (pair, half) steps: pair pr = (group head, 64-query tile), half hf = 32-query half
+  auto live_pair = [&](int pr) {
+    const int qt = pr % nqt;
+    return qt * 64 + 63 >= kbk * 64 && attn_tile_live(a, qt, kbk);
+  };
+  auto next_step = [&](int st) {  // step st = 2 pr + hf; the next live one at or after st
+    while (st < 2 * it.b1 && !live_pair(st >> 1)) st = ((st >> 1) + 1) * 2;
+    return st;
+  };
+  FaNat32<HD> qn, dn;
+  FaTr32<HD> qtn, dtn;
+  auto load_step = [&](int st) {
+    const int pr = st >> 1, h = kvh * grp + pr / nqt, q0 = (pr % nqt) * 64 + 32 * (st & 1);
+    const float* qh = a.q + (int64_t)h * HD;
+    const float* dh = a.dO + (int64_t)h * HD;
+    qn.load(qh, a.ldq, q0, a.t);
+    dn.load(dh, a.ldq, q0, a.t);
+    qtn.load(qh, a.ldq, q0, a.t);
+    dtn.load(dh, a.ldq, q0, a.t);
+  };
+  int st = next_step(2 * it.b0);
+  if (st < 2 * it.b1) load_step(st);
+  while (st < 2 * it.b1) {  // workgroup-uniform
+    const int pr = st >> 1, h = kvh * grp + pr / nqt, q0 = (pr % nqt) * 64 + 32 * (st & 1);
+    fa_store32_nat<HD, LDN>(qn, true, a.scale * kLog2e, L.qsh, L.qsl);  // scores in base 2
+    fa_store32_tr_bf<HD, LDT>(qtn, L.qth, L.qtl);
+    fa_store32_nat<HD, LDN>(dn, false, 1.0f, L.dsh_, L.dsl_);
+    fa_store32_tr_bf<HD, LDT>(dtn, L.dth, L.dtl);
+    __syncthreads();
+    const int st2 = next_step(st + 1);
+    if (st2 < 2 * it.b1) load_step(st2);
+    // S^T = k (q scale)^T and dP^T = v dO^T: 16 keys x 32 queries
+    f4 s[2] = {zero, zero}, dp[2] = {zero, zero};
+#pragma unroll
+    for (int c = 0; c < NK; c++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int o = (16 * j + li) * LDN + 32 * c + 8 * g;
+        const half8 qhf = fa_h8(L.qsh + o), qlf = fa_h8(L.qsl + o);
+        s[j] = mfma_f16(kf[c], qhf, s[j]);
+        s[j] = mfma_f16(kf[c], qlf, s[j]);
+        const bf8 dhf = fa_b8(L.dsh_ + o), dlf = fa_b8(L.dsl_ + o);
+        dp[j] = mfma_bf16(vh[c], dhf, dp[j]);
+        dp[j] = mfma_bf16(vl[c], dhf, dp[j]);
+        dp[j] = mfma_bf16(vh[c], dlf, dp[j]);
+      }
+    float pt[2][4], dst[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int qr = q0 + 16 * j + li, qc = min(qr, a.t - 1);
+      const float lq = a.lse[(int64_t)h * a.t + qc] * kLog2e, Dq = a.D[(int64_t)h * a.t + qc];
+      const int sq = attn_seg(a, qc);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const bool ok = fa_ok(qr, c0 + 4 * g + i, sq, skey[i], a.t);
+        const float p = ok ? __builtin_amdgcn_exp2f(s[j][i] - lq) : 0.0f;
+        pt[j][i] = p;
+        dst[j][i] = ok ? (p * (dp[j][i] - Dq)) * a.scale : 0.0f;
+      }
+    }
+    fa_put_tile32(pt, L.ph[w], L.pl[w]);
+    fa_put_tile32(dst, L.sh[w], L.sl[w]);
+    __builtin_amdgcn_wave_barrier();
+    {  // dV += P^T dO, dK += dS^T q over the 32 queries (one 32-deep step)
+      const bf8 phf = fa_b8(L.ph[w] + li * LDP + 8 * g), plf = fa_b8(L.pl[w] + li * LDP + 8 * g);
+      const bf8 shf = fa_b8(L.sh[w] + li * LDP + 8 * g), slf = fa_b8(L.sl[w] + li * LDP + 8 * g);
+#pragma unroll
+      for (int cc = 0; cc < NC; cc++) {
+        const int o = (16 * cc + li) * LDT + 8 * g;
+        const bf8 doh = fa_b8(L.dth + o), dol = fa_b8(L.dtl + o);
+        dv[cc] = mfma_bf16(phf, doh, dv[cc]);
+        dv[cc] = mfma_bf16(plf, doh, dv[cc]);
+        dv[cc] = mfma_bf16(phf, dol, dv[cc]);
+        const bf8 qh2 = fa_b8(L.qth + o), ql2 = fa_b8(L.qtl + o);
+        dk[cc] = mfma_bf16(shf, qh2, dk[cc]);
+        dk[cc] = mfma_bf16(slf, qh2, dk[cc]);
+        dk[cc] = mfma_bf16(shf, ql2, dk[cc]);
+      }
+    }
+    __syncthreads();
+    st = st2;
+  }
+  if (it.slot < 0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int key = c0 + 4 * g + i;
+      if (key >= a.t) continue;
+      float* kr = a.dk + (int64_t)key * a.ldk + (int64_t)kvh * HD + li;
+      float* vr = a.dv + (int64_t)key * a.ld_dv + (int64_t)kvh * HD + li;
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        kr[16 * c] = dk[c][i];
+        vr[16 * c] = dv[c][i];
+      }
+    }
+  } else {
+    float* pp = a.part + (int64_t)(it.slot + w * it.pad0) * (32 * HD);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        pp[(4 * g + i) * HD + 16 * c + li] = dk[c][i];
+        pp[16 * HD + (4 * g + i) * HD + 16 * c + li] = dv[c][i];
+      }
+  }
+}
+
+// ------------------------------------------------------------------ entry points: one workgroup per item
+#define RTQ_FA_KERNEL(NAME, FN, LDS, HD)                                      \
+  extern "C" __global__ __launch_bounds__(256) void NAME(MAttnArgs a) {       \
+    __shared__ __attribute__((aligned(16))) LDS<HD> L;                        \
+    if ((int)blockIdx.x >= a.n_items) return; /* whole workgroup */           \
+    FN<HD>(a, a.items[blockIdx.x], L);                                        \
+  }
+RTQ_FA_KERNEL(rtq_m_fa_fwd64, fa_fwd, FaFwdLds, 64)
+RTQ_FA_KERNEL(rtq_m_fa_fwd128, fa_fwd, FaFwdLds, 128)
+RTQ_FA_KERNEL(rtq_m_fa_dq64, fa_dq, FaDqLds, 64)
+RTQ_FA_KERNEL(rtq_m_fa_dq128, fa_dq, FaDqLds, 128)
+RTQ_FA_KERNEL(rtq_m_fa_dkv64, fa_dkv, FaKvLds, 64)
+RTQ_FA_KERNEL(rtq_m_fa_dkv128, fa_dkv, FaKvLds, 128)
+#undef RTQ_FA_KERNEL

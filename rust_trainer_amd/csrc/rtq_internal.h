@@ -25,12 +25,6 @@ enum RtqModelKernel {
   KM_GEMM32G,
   KM_GEMM_Q8,
   KM_GEMM32_Q8,
-  KM_ATTN_FWD64,
-  KM_ATTN_FWD128,
-  KM_ATTN_DQ64,
-  KM_ATTN_DQ128,
-  KM_ATTN_DKV64,
-  KM_ATTN_DKV128,
   KM_ATTN_MERGE_FWD,
   KM_ATTN_MERGE_DQ,
   KM_ATTN_MERGE_DKV,
@@ -40,6 +34,12 @@ enum RtqModelKernel {
   KM_GEMM32G_BF,
   KM_GEMM_HF,
   KM_GEMM32_HF,
+  KM_FA_FWD64,
+  KM_FA_FWD128,
+  KM_FA_DQ64,
+  KM_FA_DQ128,
+  KM_FA_DKV64,
+  KM_FA_DKV128,
   KM_COUNT
 };
 
@@ -48,6 +48,7 @@ rtq_status rtq_fail(rtq_status st, const char* fmt, ...);
 // launches decoder kernel km with one by-value argument struct at args (timed like every launch)
 rtq_status rtq_model_launch(rtq_ctx* c, int km, dim3 grid, dim3 block, hipStream_t s, const void* args);
 int rtq_ctx_device_id(const rtq_ctx* c);
+int rtq_ctx_cu_count(const rtq_ctx* c);
 // floats of the LoRA-down partials a forward of t tokens at rank r can keep for the backward of the
 // same x (0: not kept for this weight - dense, or slicings that differ)
 int64_t rtq_lora_partial_floats(const rtq_weight* w, int64_t t, int64_t r);

@@ -128,15 +128,14 @@ struct rtq_model {
   bool packed = false;
   bool rope_plain = false;  // the uploaded RoPE tables are for positions 0..rope_t-1
   // fused attention (head_dim 64 or 128): work tables of the current layout, partial slots.
-  // attn_mode -1 (default): fused for packed layouts and sequences of 4096 tokens or more (where
-  // the probability matrix's t^2 memory and masked work dominate; below that the matrix path's
-  // larger GEMM tiles win on f32 MFMA), the probability-matrix path otherwise; 0 / 1 force one
-  // (rtq_model_set_attention).  attn_fused: this step's choice.
+  // attn_mode -1 (default): fused for packed layouts and sequences of 2048 tokens or more (below
+  // that, at 512 tokens, the probability-matrix path's larger product tiles and fewer merges win);
+  // 0 / 1 force one (rtq_model_set_attention).  attn_fused: this step's choice.
   bool attn_hd_ok = false;
   int attn_mode = -1;
   bool attn_fused = false;
-  // the probability-matrix path's products on split-bf16 MFMA (rtq_m_gemm*_bf); RTQ_ATTN_F32=1 at
-  // load time keeps them on f32 MFMA (rtq_m_gemm*), for comparison
+  // the probability-matrix path's products on split 16-bit MFMA (rtq_m_gemm*_hf forward, *_bf
+  // backward); RTQ_ATTN_F32=1 at load time keeps them on f32 MFMA (rtq_m_gemm*), for comparison
   bool attn_f32 = false;
   int64_t layout_fused = -1;  // attn_fused the step buffers were laid out for
   float* attn_D = nullptr;  // [nh x t] dO . o per query row
@@ -532,7 +531,7 @@ rtq_status ensure_attn_plan(rtq_model* m, int64_t t, const int32_t* seg) {
     return RTQ_OK;
   const rtq_model_config& c = m->cfg;
   const int nh = (int)c.n_head, nkv = (int)c.n_head_kv, grp = nh / nkv;
-  const int64_t nqb = (t + 15) / 16, nkt = (t + 63) / 64, nlb = (t + 63) / 64;
+  const int64_t nkt = (t + 63) / 64, nlb = (t + 63) / 64;
   // the block liveness of the layout (as upload_layout derives it)
   std::vector<uint8_t> live;
   if (packed) {
@@ -540,43 +539,48 @@ rtq_status ensure_attn_plan(rtq_model* m, int64_t t, const int32_t* seg) {
     M_HIP(hipMemcpy(live.data(), m->live_d, live.size(), hipMemcpyDeviceToHost));
   }
   auto lv = [&](int64_t qb64, int64_t kb64) { return kb64 <= qb64 && (!packed || live[(size_t)(qb64 * nlb + kb64)]); };
-  std::vector<std::vector<int>> fl((size_t)nqb), kl((size_t)nqb);
+  // items of 64 rows (one workgroup of four waves each): a query block's live key tiles (forward,
+  // dq), a key block's live (group head, query tile) pairs (dk, dv)
+  std::vector<std::vector<int>> fl((size_t)nlb), kl((size_t)nlb);
   int64_t fu = 0, ku = 0;
-  for (int64_t qb = 0; qb < nqb; qb++) {  // 16-row query block qb: key tiles up to its last row
-    const int64_t last = std::min(t - 1, qb * 16 + 15) / 64;
-    for (int64_t kt = 0; kt <= last; kt++)
-      if (lv(qb * 16 / 64, kt)) fl[(size_t)qb].push_back((int)kt);
+  for (int64_t qb = 0; qb < nlb; qb++) {
+    for (int64_t kt = 0; kt <= qb; kt++)
+      if (lv(qb, kt)) fl[(size_t)qb].push_back((int)kt);
     fu += (int64_t)fl[(size_t)qb].size() * nh;
   }
-  for (int64_t kb = 0; kb < nqb; kb++) {  // 16-key block kb: (group head, query tile) pairs at or after it
+  for (int64_t kb = 0; kb < nlb; kb++) {
     for (int hr = 0; hr < grp; hr++)
-      for (int64_t qt = kb * 16 / 64; qt < nkt; qt++)
-        if (lv(qt, kb * 16 / 64)) kl[(size_t)kb].push_back((int)(hr * nkt + qt));
+      for (int64_t qt = kb; qt < nkt; qt++)
+        if (lv(qt, kb)) kl[(size_t)kb].push_back((int)(hr * nkt + qt));
     ku += (int64_t)kl[(size_t)kb].size() * nkv;
   }
-  const int64_t target = 3 * 4 * (int64_t)256;  // about three waves per SIMD
+  // about two workgroups per CU: longer ranges are cut into pieces whose partials are merged
+  const int64_t target = 2 * (int64_t)rtq_ctx_cu_count(m->ctx);
   const int64_t cf = std::max<int64_t>(1, (fu + target - 1) / target), ck = std::max<int64_t>(1, (ku + target - 1) / target);
   std::vector<MAttnItem> itf, itk;
   std::vector<MAttnMerge> mf, mk;
   int slots_f = 0, slots_k = 0;
-  auto cut = [](const std::vector<int>& L, int64_t chunk, int head, int blk, int& slots, std::vector<MAttnItem>& items,
-                std::vector<MAttnMerge>& merges) {
+  // a block cut into n > 1 pieces takes 4 n slots: 16-row sub-block w of piece i writes slot
+  // s0 + i + w n, so each sub-block's n partials are contiguous (one merge per sub-block)
+  auto cut = [t](const std::vector<int>& L, int64_t chunk, int head, int blk, int& slots, std::vector<MAttnItem>& items,
+                 std::vector<MAttnMerge>& merges) {
     const int n = (int)((L.size() + chunk - 1) / chunk);
     if (n == 0) return;
     const int s0 = n > 1 ? slots : -1;
     for (int i = 0; i < n; i++) {
       const int a0 = L[(size_t)(i * chunk)], a1 = L[std::min(L.size(), (size_t)((i + 1) * chunk)) - 1] + 1;
-      items.push_back(MAttnItem{head, blk, a0, a1, n > 1 ? s0 + i : -1, 0, 0, 0});
+      items.push_back(MAttnItem{head, blk, a0, a1, n > 1 ? s0 + i : -1, n, 0, 0});
     }
     if (n > 1) {
-      merges.push_back(MAttnMerge{head, blk, s0, n});
-      slots += n;
+      for (int w = 0; w < 4; w++)
+        if ((int64_t)(4 * blk + w) * 16 < t) merges.push_back(MAttnMerge{head, 4 * blk + w, s0 + w * n, n});
+      slots += 4 * n;
     }
   };
   for (int h = 0; h < nh; h++)
-    for (int64_t qb = 0; qb < nqb; qb++) cut(fl[(size_t)qb], cf, h, (int)qb, slots_f, itf, mf);
+    for (int64_t qb = 0; qb < nlb; qb++) cut(fl[(size_t)qb], cf, h, (int)qb, slots_f, itf, mf);
   for (int g = 0; g < nkv; g++)
-    for (int64_t kb = 0; kb < nqb; kb++) cut(kl[(size_t)kb], ck, g, (int)kb, slots_k, itk, mk);
+    for (int64_t kb = 0; kb < nlb; kb++) cut(kl[(size_t)kb], ck, g, (int)kb, slots_k, itk, mk);
   const auto al = [](size_t b) { return (b + 255) / 256 * 256; };
   const size_t slots = (size_t)std::max(slots_f, slots_k);
   const size_t bytes = al(itf.size() * sizeof(MAttnItem)) + al(itk.size() * sizeof(MAttnItem)) +
@@ -638,11 +642,12 @@ MAttnArgs attn_args(rtq_model* m, Cache& k, int64_t t) {
 }
 
 // launches an item pass (one wave per item, four per workgroup)
+// one workgroup (four waves) per item
 rtq_status attn_launch(rtq_model* m, int km, MAttnArgs a, const MAttnItem* items, int n) {
   if (n <= 0) return RTQ_OK;
   a.items = items;
   a.n_items = n;
-  return rtq_model_launch(m->ctx, km, dim3((unsigned)((n + 3) / 4)), dim3(256), stream_of(m), &a);
+  return rtq_model_launch(m->ctx, km, dim3((unsigned)n), dim3(256), stream_of(m), &a);
 }
 // one thread per element of each merged block (16 x hd, or 2 x 16 x hd for dk and dv)
 rtq_status attn_merge(rtq_model* m, int km, MAttnArgs a, const MAttnMerge* mg, int n) {
@@ -705,7 +710,7 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* 
   const float scale = 1.0f / sqrtf((float)hd);
   if (m->attn_fused) {  // fused: o and each row's log-sum-exp, no probability matrix
     const MAttnArgs aa = attn_args(m, k, t);
-    M_TRY(attn_launch(m, hd == 64 ? KM_ATTN_FWD64 : KM_ATTN_FWD128, aa, m->it_fwd, m->n_fwd));
+    M_TRY(attn_launch(m, hd == 64 ? KM_FA_FWD64 : KM_FA_FWD128, aa, m->it_fwd, m->n_fwd));
     M_TRY(attn_merge(m, KM_ATTN_MERGE_FWD, aa, m->mg_fwd, m->n_mfwd));
   } else {
   // S = (q scale) K^T per head (causal), softmax in place, O = P V
@@ -767,9 +772,9 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
     aa.dv = dv.v;
     aa.ld_dv = dv.ldv;
     M_TRY(rtq_model_launch(m->ctx, KM_ATTN_BWD_D, dim3((unsigned)((t * nh + 3) / 4)), dim3(256), stream_of(m), &aa));
-    M_TRY(attn_launch(m, hd == 64 ? KM_ATTN_DQ64 : KM_ATTN_DQ128, aa, m->it_fwd, m->n_fwd));
+    M_TRY(attn_launch(m, hd == 64 ? KM_FA_DQ64 : KM_FA_DQ128, aa, m->it_fwd, m->n_fwd));
     M_TRY(attn_merge(m, KM_ATTN_MERGE_DQ, aa, m->mg_fwd, m->n_mfwd));
-    M_TRY(attn_launch(m, hd == 64 ? KM_ATTN_DKV64 : KM_ATTN_DKV128, aa, m->it_kv, m->n_kv));
+    M_TRY(attn_launch(m, hd == 64 ? KM_FA_DKV64 : KM_FA_DKV128, aa, m->it_kv, m->n_kv));
     M_TRY(attn_merge(m, KM_ATTN_MERGE_DKV, aa, m->mg_kv, m->n_mkv));
   } else {
   M_TRY(k_gemm(m, t, t, hd, nh, Op{m->d_o, hd, qd, 1, 1}, Op{k.v, hd, 1, kd, (int)grp}, m->dP, t * t, t, 1, 1.0f, 1,
@@ -1360,7 +1365,7 @@ rtq_status step(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* p
     for (int64_t i = 0; i < t; i++)
       if (segments[i] < 0) return rtq_fail(RTQ_ERR_INVALID, "segment %lld is negative", (long long)i);
   M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
-  m->attn_fused = m->attn_hd_ok && (m->attn_mode == 1 || (m->attn_mode < 0 && (segments || t >= 4096)));
+  m->attn_fused = m->attn_hd_ok && (m->attn_mode == 1 || (m->attn_mode < 0 && (segments || t >= 2048)));
   M_TRY(choose_ckpt(m, t, n));
   M_TRY(ensure_step(m, t, n));
   M_TRY(ensure_hpk(m, t));

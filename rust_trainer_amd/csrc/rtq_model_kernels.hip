@@ -810,3 +810,4 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_lora_mask(MMaskArgs a) {
 }
 
 #include "rtq_attn.hip"
+#include "rtq_fa.hip"

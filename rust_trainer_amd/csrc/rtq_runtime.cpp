@@ -142,7 +142,7 @@ enum Kid {
   K_MODEL = K_ROWS + F_COUNT,  // + RtqModelKernel: the decoder block (rtq_model.cpp)
   K_COUNT = K_MODEL + KM_COUNT
 };
-const char* kKernelNames[K_COUNT] = {
+constexpr const char* kKernelNames[] = {
     "rtq_fill_zero",        "rtq_act_prep_q8_0",    "rtq_act_prep_q8_k",
     "rtq_fwd_q4_0_w",       "rtq_fwd_q8_0_w",       "rtq_fwd_q4_k_w",       "rtq_fwd_q6_k_w",
     "rtq_fwd_q4_0_s",       "rtq_fwd_q8_0_s",       "rtq_fwd_q4_k_s",       "rtq_fwd_q6_k_s",
@@ -164,10 +164,12 @@ const char* kKernelNames[K_COUNT] = {
     "rtq_m_gemm",           "rtq_m_softmax",        "rtq_m_softmax_bwd",    "rtq_m_group_sum",
     "rtq_m_swiglu",         "rtq_m_swiglu_bwd",     "rtq_m_add",            "rtq_m_gemm32",
     "rtq_m_lora_mask",      "rtq_m_gemm32g",        "rtq_m_gemm_q8",        "rtq_m_gemm32_q8",
-    "rtq_m_attn_fwd64",     "rtq_m_attn_fwd128",    "rtq_m_attn_dq64",      "rtq_m_attn_dq128",
-    "rtq_m_attn_dkv64",     "rtq_m_attn_dkv128",    "rtq_m_attn_merge_fwd", "rtq_m_attn_merge_dq",
+    "rtq_m_attn_merge_fwd", "rtq_m_attn_merge_dq",
     "rtq_m_attn_merge_dkv", "rtq_m_attn_bwd_d",     "rtq_m_gemm_bf",        "rtq_m_gemm32_bf",
-    "rtq_m_gemm32g_bf",     "rtq_m_gemm_hf",        "rtq_m_gemm32_hf"};
+    "rtq_m_gemm32g_bf",     "rtq_m_gemm_hf",        "rtq_m_gemm32_hf",      "rtq_m_fa_fwd64",
+    "rtq_m_fa_fwd128",      "rtq_m_fa_dq64",        "rtq_m_fa_dq128",       "rtq_m_fa_dkv64",
+    "rtq_m_fa_dkv128"};
+static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT, "one name per kernel id, in id order");
 
 struct TimedLaunch {
   int kid;
@@ -865,6 +867,7 @@ rtq_status rtq_model_launch(rtq_ctx* c, int km, dim3 grid, dim3 block, hipStream
 }
 
 int rtq_ctx_device_id(const rtq_ctx* c) { return c ? c->device : -1; }
+int rtq_ctx_cu_count(const rtq_ctx* c) { return c ? (int)c->cu_count : 256; }
 
 // error reporting shared with the other translation units of the library (rtq_gguf.cpp, rtq_model.cpp)
 rtq_status rtq_fail(rtq_status st, const char* fmt, ...) {

@@ -218,6 +218,25 @@ def test_config2_block_ops_fused_attention_match_oracle(ctx):
     model.close()
 
 
+@pytest.mark.parametrize("t", [45, 333])
+def test_fused_attention_head_dim_64_match_oracle(ctx, t):
+    """the fused attention kernels at head_dim 64 (the other width they are built for), four query
+    heads per KV head, ragged lengths (a partial last 64-row block)"""
+    spec = tiny_spec(O.Q8_0, n_layer=1, n_embd=512, n_head=8, n_head_kv=2, head_dim=64, rope_dim=64, n_ff=768,
+                     n_vocab=500)
+    g, model, m = build(ctx, spec, 8, 16.0, ALL)
+    model.fused_attention = True
+    n = min(t - 1, 120)
+    toks, pos, tok = sequence(spec.n_vocab, t, n, 5)
+    model.debug_capture(0)
+    model.zero_grad()
+    model.forward_backward(toks, [rt.Target(int(p), int(k)) for p, k in zip(pos, tok)],
+                           np.linspace(0.5, 1.5, n).astype(np.float32))
+    assert model.fused_attention is True
+    check_block(ctx, g, model, m, 0, t, None, {}, {})
+    model.close()
+
+
 @pytest.mark.parametrize("t", [16, 700])
 @pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
 def test_odd_fused_groups_block_ops_match_oracle(ctx, wtype, t):
@@ -278,7 +297,7 @@ def test_config3_block_ops_packed_match_oracle(ctx):
     model.close()
 
 
-@pytest.mark.parametrize("fused", [None, True])
+@pytest.mark.parametrize("fused", [False, None])  # None: the default, fused at 2048 tokens
 def test_config4_block_ops_match_oracle_recomputed(ctx, fused):
     spec = tiny_spec(O.Q8_0, n_layer=2, arch="llama", tied=False, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128,
                      rope_dim=128, n_ff=14336, n_vocab=4096, rope_base=5e5)
