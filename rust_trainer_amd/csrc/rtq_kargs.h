@@ -187,6 +187,15 @@ struct LoraGradArgs {
   RankBlocks rb;         // gb written only inside the members' blocks
 };
 
+// dA / dB of up to RTQ_LORA_JOBS linears in one launch (rtq_lora_grads[16]): workgroups
+// [start[j], start[j + 1]) are job j's gb tiles (its n_gb) then its ga tiles (n_ga) of 64 rows
+#define RTQ_LORA_JOBS 8
+struct LoraGradBatch {
+  int njobs;
+  int start[RTQ_LORA_JOBS + 1];
+  LoraGradArgs job[RTQ_LORA_JOBS];
+};
+
 // rows [r0, r0+count) dequantised to f32 (bit-exact ggml dequant)
 struct RowArgs {
   const void* wq;

@@ -2004,29 +2004,59 @@ extern "C" __global__ __launch_bounds__(512) void rtq_dxw_q6_k(DxArgs a) { dx_ti
 //    w.backward_input(dy) + g.A, src/linear.rs:100-101,115-118)
 // gb[n][j] += sum_t (s*dy[t][n]) h[t][j]   (matmul_tn_acc, src/linear.rs:109)
 // ga[j][k] += sum_t g[t][j] x[t][k]        (matmul_tn_acc, src/linear.rs:113)
-// gb / ga: one 64 x 16 tile (64 rows m of X = s.dy or x, 16 ranks j) per workgroup; the NW waves
-// split the tokens and contract 4 tokens per step with four f32 MFMAs (MFMA e takes rows
-// m0 + 4i + e, so a lane's four X values are one 16-byte load of a token row); their tiles are
-// added in LDS in wave order (single writer, fixed order).  GB: tile b of gb (X = dy, H = h),
-// otherwise of ga (X = x, H = g).
-template <int NW, bool GB>
+// gb / ga: one R x 16 tile (R = 16 E rows m of X = s.dy or x, 16 ranks j) per workgroup: E = 4, or
+// E = 1 where 64-row tiles would leave most CUs without a workgroup.  The NW waves split the tokens
+// and contract 4 tokens per step with E f32 MFMAs (MFMA e takes rows m0 + E rho + e, rho the MFMA's
+// row, so a lane's E values of a token row are one load); their tiles are added in LDS in wave order
+// (single writer, fixed order).  The accumulated outputs are read at the start, so that load's
+// latency overlaps the contraction.  GB: tile b of gb (X = dy, H = h), otherwise of ga (X = x, H = g).
+template <int E>
+struct FloatVec;
+template <>
+struct FloatVec<1> {
+  using T = float;
+};
+template <>
+struct FloatVec<4> {
+  using T = f4;
+};
+template <int NW, int E, bool GB>
 __device__ __forceinline__ void lora_grad_tile(const LoraGradArgs& a, int b, float* red) {
-  constexpr int LDR = 17;  // LDS row stride of a wave's 64 x 16 tile (the four lane groups on different banks)
+  constexpr int LDR = 17;  // LDS row stride of a wave's R x 16 tile (the four lane groups on different banks)
+  constexpr int R = 16 * E, NO = (R * 16 + NW * 64 - 1) / (NW * 64);  // outputs per thread
+  using V = typename FloatVec<E>::T;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
-  const int jt = (a.r + 15) / 16, m0 = (b / jt) * 64, j0 = (b % jt) * 16;
+  const int jt = (a.r + 15) / 16, m0 = (b / jt) * R, j0 = (b % jt) * 16;
   const int M = GB ? a.N : a.K;
   // block-diagonal adapter: only tiles that meet a member's block (uniform exit)
-  if (GB && !rb_any(a.rb, m0, min(m0 + 64, a.N), j0, min(j0 + 16, a.r))) return;
+  if (GB && !rb_any(a.rb, m0, min(m0 + R, a.N), j0, min(j0 + 16, a.r))) return;
+  // output o of this thread: gb: consecutive threads take consecutive ranks of a row; ga: consecutive
+  // columns of a rank
+  auto out_at = [&](int o, int& m, int& j) {
+    m = m0 + (GB ? o >> 4 : o % R);
+    j = j0 + (GB ? o & 15 : o / R);
+  };
+  float prev[NO];
+#pragma unroll
+  for (int q = 0; q < NO; q++) {
+    const int o = threadIdx.x + q * NW * 64;
+    int m, j;
+    out_at(o, m, j);
+    prev[q] = 0.0f;
+    if (o < R * 16 && m < M && j < a.r) prev[q] = GB ? a.gb[(int64_t)m * a.r + j] : a.ga[(int64_t)j * a.K + m];
+  }
   const float* X = GB ? a.dy : a.x;  // [T x M]
   const float* H = GB ? a.h : a.g;   // [T x r]
   const int tper = (a.T + NW * 16 - 1) / (NW * 16) * 16;  // tokens per wave, multiple of 16
   const int tb = w * tper, te = min(tb + tper, a.T);
-  const int mc = m0 + 4 * li, jc = j0 + li;
-  const bool vec = (M & 3) == 0;  // 16-byte aligned rows (always for x: K % 32 == 0)
-  f4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
-  for (int t32 = tb; t32 < te; t32 += 32) {  // 32 tokens: all loads, then up to 32 MFMAs
+  const int mc = m0 + E * li, jc = j0 + li;
+  const bool vec = (M % E) == 0;  // E-aligned rows (always for x: K % 32 == 0)
+  f4 acc[E];
+#pragma unroll
+  for (int e = 0; e < E; e++) acc[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int t32 = tb; t32 < te; t32 += 32) {  // 32 tokens: all loads, then up to 8 E MFMAs
     const int nv = min(2, (te - t32 + 15) / 16);  // 16-token groups with tokens (wave-uniform)
-    f4 xv[2][4];
+    V xv[2][4];
     float hv[2][4];
 #pragma unroll
     for (int v = 0; v < 2; v++)
@@ -2037,11 +2067,12 @@ __device__ __forceinline__ void lora_grad_tile(const LoraGradArgs& a, int b, flo
           const bool tin = t < te;
           const float* xr = X + (int64_t)tc * M;
           if (vec) {
-            const f4 x4 = *reinterpret_cast<const f4*>(xr + min(mc, M - 4));
-            xv[v][u] = (tin && mc < M) ? x4 : f4{0.0f, 0.0f, 0.0f, 0.0f};
+            const V x4 = *reinterpret_cast<const V*>(xr + min(mc, M - E));
+            xv[v][u] = (tin && mc < M) ? x4 : V{};
           } else {
+            float* xe = reinterpret_cast<float*>(&xv[v][u]);
 #pragma unroll
-            for (int e = 0; e < 4; e++) xv[v][u][e] = (tin && mc + e < M) ? xr[min(mc + e, M - 1)] : 0.0f;
+            for (int e = 0; e < E; e++) xe[e] = (tin && mc + e < M) ? xr[min(mc + e, M - 1)] : 0.0f;
           }
           const float hh = H[(int64_t)tc * a.r + min(jc, a.r - 1)];
           hv[v][u] = (tin && jc < a.r) ? hh : 0.0f;
@@ -2051,36 +2082,33 @@ __device__ __forceinline__ void lora_grad_tile(const LoraGradArgs& a, int b, flo
       if (v < nv)
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-          f4 x4 = xv[v][u];
-          if (GB) x4 = f4{__fmul_rn(x4.x, a.s), __fmul_rn(x4.y, a.s), __fmul_rn(x4.z, a.s), __fmul_rn(x4.w, a.s)};
-          acc0 = mfma_f32(x4.x, hv[v][u], acc0);  // s.dy (src/linear.rs:108) for gb; x for ga
-          acc1 = mfma_f32(x4.y, hv[v][u], acc1);
-          acc2 = mfma_f32(x4.z, hv[v][u], acc2);
-          acc3 = mfma_f32(x4.w, hv[v][u], acc3);
+          const float* xe = reinterpret_cast<const float*>(&xv[v][u]);
+#pragma unroll
+          for (int e = 0; e < E; e++)  // s.dy (src/linear.rs:108) for gb; x for ga
+            acc[e] = mfma_f32(GB ? __fmul_rn(xe[e], a.s) : xe[e], hv[v][u], acc[e]);
         }
   }
-  // lane (rank li, group g): element i of acc<e> is row m0 + 4 (4g + i) + e
+  // lane (rank li, group g): element i of acc[e] is row m0 + E (4g + i) + e
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    float* rr = red + w * 64 * LDR + (16 * g + 4 * i) * LDR + li;
-    rr[0] = acc0[i];
-    rr[LDR] = acc1[i];
-    rr[2 * LDR] = acc2[i];
-    rr[3 * LDR] = acc3[i];
-  }
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int e = 0; e < E; e++) red[w * R * LDR + (E * (4 * g + i) + e) * LDR + li] = acc[e][i];
   __syncthreads();
-  for (int o = threadIdx.x; o < 1024; o += NW * 64) {
-    // gb: consecutive threads take consecutive ranks of a row; ga: consecutive columns of a rank
-    const int mr = GB ? o >> 4 : o & 63, jr = GB ? o & 15 : o >> 6;
+#pragma unroll
+  for (int q = 0; q < NO; q++) {
+    const int o = threadIdx.x + q * NW * 64;
+    if (o >= R * 16) break;
+    const int mr = GB ? o >> 4 : o % R, jr = GB ? o & 15 : o / R;
     float sum = 0.0f;
 #pragma unroll
-    for (int ww = 0; ww < NW; ww++) sum += red[ww * 64 * LDR + mr * LDR + jr];
-    const int m = m0 + mr, j = j0 + jr;
+    for (int ww = 0; ww < NW; ww++) sum += red[ww * R * LDR + mr * LDR + jr];
+    int m, j;
+    out_at(o, m, j);
     if (m < M && j < a.r) {
       if (GB) {
-        if (rb_keep(a.rb, m, j)) a.gb[(int64_t)m * a.r + j] += sum;
+        if (rb_keep(a.rb, m, j)) a.gb[(int64_t)m * a.r + j] = prev[q] + sum;
       } else {
-        a.ga[(int64_t)j * a.K + m] += sum;
+        a.ga[(int64_t)j * a.K + m] = prev[q] + sum;
       }
     }
   }
@@ -2089,15 +2117,15 @@ __device__ __forceinline__ void lora_grad_tile(const LoraGradArgs& a, int b, flo
 // One grid, three kinds of workgroups: gb tiles, ga tiles (lora_grad_tile), then dx: one wave per
 // 16 x 16 quarter of a dx-kernel fragment (the dx kernel's partial layout) or per token and 64
 // columns (row-major partials).  NW = 4, or 16 for long token ranges.
-template <int NW>
+template <int NW, int E>
 __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
-  __shared__ float red[NW * 64 * 17];
+  __shared__ float red[NW * 16 * E * 17];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
   const int b = blockIdx.x;
   if (b < a.n_gb) {
-    lora_grad_tile<NW, true>(a, b, red);
+    lora_grad_tile<NW, E, true>(a, b, red);
   } else if (b < a.n_gb + a.n_ga) {
-    lora_grad_tile<NW, false>(a, b - a.n_gb, red);
+    lora_grad_tile<NW, E, false>(a, b - a.n_gb, red);
   } else if (a.part_rows) {
     // dx from row-major partials: wave per (token t, 64 columns); lane (k4 = li, split subset g)
     // sums splits g, g+4, ... of four columns, the subsets are combined by shuffles (fixed order)
@@ -2150,33 +2178,48 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
     const int t0 = (tile / Kc) * 64 + wt * 32 + ts * 16, k0 = (tile % Kc) * 128 + wk * 32 + ks * 16;
     const f4* pp = reinterpret_cast<const f4*>(a.part) + (int64_t)f * 256 + q * 64 + lane;
     const int64_t sstride = (int64_t)ntt * Kc * 8 * 256;  // f4 per split
+    const int trow = t0 + li, kcol = k0 + li;
+    // g . A operands (f32 MFMA; lane: token 4g + i, column li) of rank chunk jj; the first MAXJ
+    // chunks' loads are issued with the partials', so the tile waits for one round of loads
+    auto ga_ops = [&](int jj, float* gv, float* av) {
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int j = 16 * jj + 4 * u + g, jc = min(j, a.r - 1);
+        const float x = a.g[(int64_t)min(trow, a.T - 1) * a.r + jc];
+        const float y = a.la[(int64_t)jc * a.K + min(kcol, a.K - 1)];
+        gv[u] = (trow < a.T && j < a.r) ? x : 0.0f;
+        av[u] = (kcol < a.K && j < a.r) ? y : 0.0f;
+      }
+    };
+    constexpr int MAXJ = 4;
+    const int nj = a.g ? (a.r + 15) / 16 : 0;
+    float gv[MAXJ][4], av[MAXJ][4];
+#pragma unroll
+    for (int jj = 0; jj < MAXJ; jj++)
+      if (jj < nj) ga_ops(jj, gv[jj], av[jj]);
     constexpr int MAXS = 16;  // partials loaded at once; more splits are summed 16 at a time
     f4 ps = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int c0 = 0; c0 < a.nsplit; c0 += MAXS) {
       f4 v[MAXS];
 #pragma unroll
-      for (int sp = 0; sp < MAXS; sp++) v[sp] = pp[(int64_t)min(c0 + sp, a.nsplit - 1) * sstride];
+      for (int sp = 0; sp < MAXS; sp++)
+        if (c0 + sp < a.nsplit) v[sp] = pp[(int64_t)(c0 + sp) * sstride];
       if (c0 == 0) ps = v[0];
 #pragma unroll
       for (int sp = 0; sp < MAXS; sp++)
         if ((c0 > 0 || sp > 0) && c0 + sp < a.nsplit) ps += v[sp];  // split order
     }
-    const int trow = t0 + li, kcol = k0 + li;
     f4 ga = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (a.g) {  // + g . A for this 16 x 16 tile (f32 MFMA; lane: token 4g + i, column li)
-      for (int j0 = 0; j0 < a.r; j0 += 16) {
-        float gv[4], av[4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const int j = j0 + 4 * u + g, jc = min(j, a.r - 1);
-          const float x = a.g[(int64_t)min(trow, a.T - 1) * a.r + jc];
-          const float y = a.la[(int64_t)jc * a.K + min(kcol, a.K - 1)];
-          gv[u] = (trow < a.T && j < a.r) ? x : 0.0f;
-          av[u] = (kcol < a.K && j < a.r) ? y : 0.0f;
-        }
+    for (int jj = 0; jj < MAXJ; jj++)
+      if (jj < nj)
 #pragma unroll
-        for (int u = 0; u < 4; u++) ga = mfma_f32(gv[u], av[u], ga);
-      }
+        for (int u = 0; u < 4; u++) ga = mfma_f32(gv[jj][u], av[jj][u], ga);
+    for (int jj = MAXJ; jj < nj; jj++) {
+      float gq[4], aq[4];
+      ga_ops(jj, gq, aq);
+#pragma unroll
+      for (int u = 0; u < 4; u++) ga = mfma_f32(gq[u], aq[u], ga);
     }
     if (kcol < a.K)
 #pragma unroll
@@ -2192,8 +2235,27 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
   }
 }
 
-extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a) { bwd_finish<4>(a); }
-extern "C" __global__ __launch_bounds__(1024) void rtq_bwd_finish16(LoraGradArgs a) { bwd_finish<16>(a); }
+// the dA / dB tiles of several linears (a decoder block's, deferred to one launch so that their
+// load -> contract -> reduce chains overlap instead of running one launch after another)
+template <int NW>
+__device__ __forceinline__ void lora_grads(const LoraGradBatch& B) {
+  __shared__ float red[NW * 64 * 17];
+  const int b = blockIdx.x;
+  int j = 0;
+  while (j + 1 < B.njobs && b >= B.start[j + 1]) j++;  // uniform over the workgroup
+  const LoraGradArgs& a = B.job[j];
+  const int lb = b - B.start[j];
+  if (lb < a.n_gb)
+    lora_grad_tile<NW, 4, true>(a, lb, red);
+  else if (lb < a.n_gb + a.n_ga)
+    lora_grad_tile<NW, 4, false>(a, lb - a.n_gb, red);
+}
+
+extern "C" __global__ __launch_bounds__(256) void rtq_lora_grads(LoraGradBatch b) { lora_grads<4>(b); }
+extern "C" __global__ __launch_bounds__(1024) void rtq_lora_grads16(LoraGradBatch b) { lora_grads<16>(b); }
+extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a) { bwd_finish<4, 4>(a); }
+extern "C" __global__ __launch_bounds__(1024) void rtq_bwd_finish16(LoraGradArgs a) { bwd_finish<16, 4>(a); }
+
 
 // ============================================================== trainer-native weights
 // rows [r0, r0 + count) of an F32 (copy) or TQ8_0 weight (0 + d * q: q8_axpy(1) into zeros,

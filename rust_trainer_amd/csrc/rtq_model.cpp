@@ -115,6 +115,13 @@ struct rtq_model {
   size_t grad_bytes = 0;
   void* hpk_mem = nullptr;  // every group's kept LoRA-down partials
   size_t hpk_cap = 0;
+  // each adapted group's h and g [t x rank] of one block's backward, kept from its dx kernel to
+  // the block's one dA / dB launch (slot = group index within a layer, shared by the layers);
+  // lora_batch false (RTQ_LORA_BATCH=0 at load time): dA / dB launched per linear, for comparison
+  void* lg_mem = nullptr;
+  size_t lg_cap = 0;
+  std::vector<float*> lg_h, lg_g;
+  bool lora_batch = true;
   float *X = nullptr, *cos_ = nullptr, *sin_ = nullptr;
   std::vector<Cache> cache;
   int64_t cache_cap = 0;      // Cache sets allocated (n_layer when keeping, 1 when recomputing)
@@ -313,11 +320,23 @@ rtq_status lin_fwd(rtq_model* m, const Group& l, const float* x, int64_t t, floa
 
 // a fused group's adapter is block-diagonal (each member's rows see only its own ranks): the
 // quantised backward computes gb and g = s dy.B inside the blocks only; the dense (f32 GEMM) one
-// computes every pair and the off-block gb entries are cleared after it
-rtq_status lin_bwd(rtq_model* m, const Group& l, const float* x, const float* dy, int64_t t, float* dx) {
+// computes every pair and the off-block gb entries are cleared after it.  jobs (or null): a
+// quantised adapted group's dA / dB are appended there (h, g in the group's slot gi) for the
+// block's batched launch instead of being launched here.
+rtq_status lin_bwd(rtq_model* m, const Layer& L, int gi, const float* x, const float* dy, int64_t t, float* dx,
+                   std::vector<LoraGradArgs>* jobs = nullptr) {
+  const Group& l = L.groups[(size_t)gi];
   const rtq_lora lv = lora_view(l);
   const int wt = rtq_weight_type(l.w);
   const bool dense = wt == RTQ_TYPE_F32 || wt == RTQ_TYPE_TQ8_0;
+  if (jobs && m->lora_batch && !dense && l.rank > 0 && jobs->size() < RTQ_LORA_JOBS) {
+    const RankBlocks rb = rank_blocks(l);
+    LoraGradArgs job{};
+    M_TRY(rtq_linear_backward_defer_d(m->ctx, l.w, &lv, l.nm < 2 ? nullptr : &rb, x, dy, t, dx, l.ga, l.gb, l.hpk,
+                                      m->lg_h[(size_t)gi], m->lg_g[(size_t)gi], &job, stream_of(m)));
+    jobs->push_back(job);
+    return RTQ_OK;
+  }
   if (l.rank == 0 || dense)
     M_TRY(rtq_linear_backward_d(m->ctx, l.w, l.rank > 0 ? &lv : nullptr, x, dy, t, dx, l.ga, l.gb, stream_of(m)));
   if (l.rank == 0 || (dense && l.nm < 2)) return RTQ_OK;
@@ -362,6 +381,36 @@ rtq_status ensure_hpk(rtq_model* m, int64_t t) {
       G.hpk = f ? (float*)p : nullptr;
       p += (f * 4 + 255) / 256 * 256;
     }
+  return RTQ_OK;
+}
+
+// the h / g slots of the batched dA / dB launches (ensure_hpk's sizing rule: per step)
+rtq_status ensure_lgrad(rtq_model* m, int64_t t) {
+  std::vector<int64_t> rmax;
+  for (auto& L : m->layers) {
+    if (rmax.size() < L.groups.size()) rmax.resize(L.groups.size(), 0);
+    for (size_t i = 0; i < L.groups.size(); i++) rmax[i] = std::max(rmax[i], L.groups[i].rank);
+  }
+  size_t need = 0;
+  for (int64_t r : rmax) need += ((size_t)(2 * t * r) * 4 + 255) / 256 * 256;
+  if (need > m->lg_cap) {
+    if (m->lg_mem) {
+      M_HIP(hipStreamSynchronize(stream_of(m)));
+      M_HIP(hipFree(m->lg_mem));
+      m->lg_mem = nullptr;
+      m->lg_cap = 0;
+    }
+    M_HIP(hipMalloc(&m->lg_mem, need));
+    m->lg_cap = need;
+  }
+  m->lg_h.assign(rmax.size(), nullptr);
+  m->lg_g.assign(rmax.size(), nullptr);
+  char* p = (char*)m->lg_mem;
+  for (size_t i = 0; i < rmax.size(); i++) {
+    m->lg_h[i] = (float*)p;
+    m->lg_g[i] = (float*)p + t * rmax[i];
+    p += ((size_t)(2 * t * rmax[i]) * 4 + 255) / 256 * 256;
+  }
   return RTQ_OK;
 }
 
@@ -747,22 +796,23 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
   const int64_t qd = nh * hd, kd = nkv * hd;
   const float scale = 1.0f / sqrtf((float)hd);
   // Mlp::backward (src/model.rs:120-133)
-  M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LDOWN]], k.hm, dy, t, m->dhm));
+  std::vector<LoraGradArgs> jobs;  // this block's dA / dB, launched together before its last kernel
+  M_TRY(lin_bwd(m, L, L.gi[LDOWN], k.hm, dy, t, m->dhm, &jobs));
   float *g, *u, *dg, *du;
   int64_t ldg;
   gu_view(m, L, k.gu, t, &g, &u, &ldg);
   gu_view(m, L, m->dgu, t, &dg, &du, &ldg);
   M_TRY(k_elt2(m, KM_SWIGLU_BWD, g, u, m->dhm, dg, du, t, c.n_ff, ldg, c.n_ff, ldg));
   if (L.gu_fused) {
-    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LGATE]], k.n2, m->dgu, t, m->dn2));  // dgate.Wg + dup.Wu in one pass
+    M_TRY(lin_bwd(m, L, L.gi[LGATE], k.n2, m->dgu, t, m->dn2, &jobs));  // dgate.Wg + dup.Wu in one pass
   } else {
-    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LGATE]], k.n2, dg, t, m->dn2));
-    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LUP]], k.n2, du, t, m->dxu));
+    M_TRY(lin_bwd(m, L, L.gi[LGATE], k.n2, dg, t, m->dn2, &jobs));
+    M_TRY(lin_bwd(m, L, L.gi[LUP], k.n2, du, t, m->dxu, &jobs));
     M_TRY(k_elt(m, KM_ADD, m->dn2, m->dxu, nullptr, m->dn2, nullptr, t * d));
   }
   M_TRY(k_norm_bwd(m, k.h, L.ffn_norm, k.inv2, m->dn2, dy, m->dh, t, d));  // dh = dy + rmsnorm_backward
   // Attention::backward (src/attention.rs:243-355)
-  M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LO]], k.o, m->dh, t, m->d_o));
+  M_TRY(lin_bwd(m, L, L.gi[LO], k.o, m->dh, t, m->d_o, &jobs));
   const QkvView dv = qkv_view(m, L, m->dqkv, t);
   if (m->attn_fused) {  // D = dO . o; dq over key tiles; dk, dv over (group head, query tile) pairs
     MAttnArgs aa = attn_args(m, k, t);
@@ -796,13 +846,17 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
   const MQkArgs qa = qk_args(m, L, k, t);
   M_TRY(rtq_model_launch(m->ctx, KM_QK_BWD, dim3((unsigned)((t * (nh + nkv) + 3) / 4)), dim3(256), stream_of(m), &qa));
   if (L.qkv_fused) {
-    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LQ]], k.n1, m->dqkv, t, m->dn1));  // dq.Wq + dk.Wk + dv.Wv in one pass
+    M_TRY(lin_bwd(m, L, L.gi[LQ], k.n1, m->dqkv, t, m->dn1, &jobs));  // dq.Wq + dk.Wk + dv.Wv in one pass
   } else {
-    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LQ]], k.n1, dv.q, t, m->dn1));
-    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LK]], k.n1, dv.k, t, m->dxk));
-    M_TRY(lin_bwd(m, L.groups[(size_t)L.gi[LV]], k.n1, dv.v, t, m->dxv));
+    M_TRY(lin_bwd(m, L, L.gi[LQ], k.n1, dv.q, t, m->dn1, &jobs));
+    M_TRY(lin_bwd(m, L, L.gi[LK], k.n1, dv.k, t, m->dxk, &jobs));
+    M_TRY(lin_bwd(m, L, L.gi[LV], k.n1, dv.v, t, m->dxv, &jobs));
     M_TRY(k_elt(m, KM_ADD, m->dn1, m->dxk, m->dxv, m->dn1, nullptr, t * d));  // dq + (dk + dv)
   }
+  // every input of the deferred dA / dB (dy, x of each linear, the h / g slots) is still intact here.
+  // (Run on a second stream, overlapping the next block's backward, the batch measured slower:
+  // 13.79 against 13.45 ms per configs[2] step - its workgroups hold CUs the next dx kernels need.)
+  M_TRY(rtq_lora_grads_d(m->ctx, jobs.data(), (int)jobs.size(), stream_of(m)));
   return k_norm_bwd(m, x, L.attn_norm, k.inv1, m->dn1, m->dh, dx, t, d);  // dx = dh + rmsnorm_backward
 }
 
@@ -1093,6 +1147,7 @@ rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out)
   M_TRY(parse_config(g, &cfg, &factors));
   rtq_model* m = new rtq_model();
   if (const char* e = getenv("RTQ_ATTN_F32")) m->attn_f32 = atoi(e) != 0;
+  if (const char* e = getenv("RTQ_LORA_BATCH")) m->lora_batch = atoi(e) != 0;
   m->ctx = ctx;
   m->cfg = cfg;
   m->rope_factors = factors;
@@ -1135,6 +1190,7 @@ void rtq_model_destroy(rtq_model* m) {
   for (void* p : m->owned) (void)hipFree(p);
   if (m->step_mem) (void)hipFree(m->step_mem);
   if (m->hpk_mem) (void)hipFree(m->hpk_mem);
+  if (m->lg_mem) (void)hipFree(m->lg_mem);
   if (m->attn_mem) (void)hipFree(m->attn_mem);
   delete m;
 }
@@ -1369,6 +1425,7 @@ rtq_status step(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* p
   M_TRY(choose_ckpt(m, t, n));
   M_TRY(ensure_step(m, t, n));
   M_TRY(ensure_hpk(m, t));
+  M_TRY(ensure_lgrad(m, t));
   M_TRY(ensure_rope(m, t, positions));
   M_TRY(upload_layout(m, segments, t));
   if (m->attn_fused) M_TRY(ensure_attn_plan(m, t, segments));

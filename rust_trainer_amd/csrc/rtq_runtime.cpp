@@ -131,6 +131,8 @@ enum Kid {
   K_DXW = K_DX16 + F_COUNT,  // + format: large t, 256-token tiles
   K_BWD_FINISH = K_DXW + F_COUNT,
   K_BWD_FINISH16,  // 16 waves per workgroup: long token reductions of dA / dB
+  K_LORA_GRADS,    // dA / dB of several linears in one launch (4 / 16 waves per workgroup)
+  K_LORA_GRADS16,
   K_DENSE_ROWS,    // trainer-native weights: rows / dequantisation, bias
   K_DENSE_BIAS,
   K_HEAD_NORM,   // LM head + cross-entropy (Model::head)
@@ -156,7 +158,8 @@ constexpr const char* kKernelNames[] = {
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
     "rtq_dxw_q4_0",         "rtq_dxw_q8_0",         "rtq_dxw_q4_k",         "rtq_dxw_q6_k",
-    "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_dense_rows",       "rtq_dense_bias",
+    "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_lora_grads",       "rtq_lora_grads16",
+    "rtq_dense_rows",       "rtq_dense_bias",
     "rtq_head_norm",        "rtq_head_max",         "rtq_head_sum",         "rtq_head_grad",
     "rtq_head_norm_bwd",
     "rtq_rows_q4_0",        "rtq_rows_q8_0",        "rtq_rows_q4_k",        "rtq_rows_q6_k",
@@ -670,10 +673,17 @@ int64_t lora_slices(int64_t n) { return roundup(cdiv(std::max<int64_t>(n, 1), RT
 // Linear::backward returns a fresh dx); with LoRA also dx += g.A, ga += g^T x, gb += (s dy)^T h
 // (g = s dy.B, h = x.A^T).  Kernels: [rtq_bwd_prep: slice partials of h, g] -> rtq_dx_* (per-split
 // partials of dx; its last grid row sums the h, g partials) -> rtq_bwd_finish.
+// defer (or null): the dA / dB tiles are not launched but described in defer->job, with h and g in
+// defer->h / defer->g (rtq_linear_backward_defer_d)
+struct LoraDefer {
+  float* h;
+  float* g;
+  LoraGradArgs* job;
+};
 rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, int64_t t, float* dx, bool accumulate,
                             const float* x, const float* la, const float* lb, int64_t r, float s, float* ga,
                             float* gb, Arena& ar, hipStream_t st, const RankBlocks* rb = nullptr,
-                            const float* hp_have = nullptr) {
+                            const float* hp_have = nullptr, const LoraDefer* defer = nullptr) {
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
   if (is_dense(w->type))
@@ -683,8 +693,10 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
     return fail(RTQ_ERR_INVALID, "dy of %lld x %d floats exceeds the 2 GiB buffer-offset range", (long long)t, N);
   const DxPlan dp = dx_plan(c, w, t);
   const int64_t nhq = lora_slices(K), ngq = lora_slices(N);
-  float* h = lora ? ar.take<float>((size_t)(t * r)) : nullptr;
-  float* g = lora ? ar.take<float>((size_t)(t * r)) : nullptr;
+  if (defer && defer->job) defer->job->n_gb = defer->job->n_ga = 0;
+  if (!lora) defer = nullptr;
+  float* h = lora ? (defer ? defer->h : ar.take<float>((size_t)(t * r))) : nullptr;
+  float* g = lora ? (defer ? defer->g : ar.take<float>((size_t)(t * r))) : nullptr;
   // hp_have: the forward's LoRA-down partials of this x (same slices), so only g is computed here
   const bool have_h = lora && hp_have != nullptr;
   float* hp = lora ? (have_h ? const_cast<float*>(hp_have) : ar.take<float>((size_t)(nhq * t * r))) : nullptr;
@@ -720,6 +732,14 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   fa.n_ga = lora ? (int)(cdiv(K, 64) * jt) : 0;
   const int nw = lora && t >= 256 ? 16 : 4;
   fa.n_dx = dp.tok16 ? (int)cdiv(t * cdiv(K, 64), nw) : (int)cdiv((w->Kp / 128) * cdiv(t, 64) * 32, nw);
+  if (defer) {  // dA / dB later, in a batch; here the dx partials (+ g.A) alone, 4 waves per workgroup
+    *defer->job = fa;
+    defer->job->n_dx = 0;
+    defer->job->part = nullptr;
+    fa.n_gb = fa.n_ga = 0;
+    fa.n_dx = dp.tok16 ? (int)cdiv(t * cdiv(K, 64), 4) : (int)cdiv((w->Kp / 128) * cdiv(t, 64) * 32, 4);
+    return launch(c, K_BWD_FINISH, dim3((unsigned)fa.n_dx), dim3(256), st, fa);
+  }
   return launch(c, nw == 16 ? K_BWD_FINISH16 : K_BWD_FINISH, dim3((unsigned)(fa.n_gb + fa.n_ga + fa.n_dx)),
                 dim3(64 * nw), st, fa);
 }
@@ -1175,7 +1195,8 @@ rtq_status rtq_frozen_backward_input_d(rtq_ctx* c, const rtq_weight* w, const fl
 
 static rtq_status linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const float* x,
                                     const float* dy, int64_t t, float* dx, float* ga, float* gb, void* stream,
-                                    const RankBlocks* rb, const float* hp_have = nullptr) {
+                                    const RankBlocks* rb, const float* hp_have = nullptr,
+                                    const LoraDefer* defer = nullptr) {
   RTQ_TRY(check_weight(c, w));
   RTQ_TRY(check_t(t));
   bool on;
@@ -1190,7 +1211,7 @@ static rtq_status linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_l
   RTQ_TRY(ensure_ws(c, bwd_ws_bytes(c, w, t, on ? r : 0)));
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   return enqueue_backward(c, w, dy, t, dx, false, x, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, ga, gb,
-                          ar, st, rb, hp_have);
+                          ar, st, rb, hp_have, defer);
 }
 
 rtq_status rtq_linear_backward_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const float* x,
@@ -1676,6 +1697,40 @@ rtq_status rtq_linear_forward_ws_d(rtq_ctx* c, const rtq_weight* w, const float*
   Arena ar{(char*)ws, ws_bytes, 0};
   return enqueue_forward(c, w, x, t, y, bias, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, nullptr, ar,
                          (hipStream_t)stream);
+}
+
+rtq_status rtq_linear_backward_defer_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const RankBlocks* rb,
+                                       const float* x, const float* dy, int64_t t, float* dx, float* ga, float* gb,
+                                       const float* hp_have, float* h_out, float* g_out, LoraGradArgs* job,
+                                       void* stream) {
+  RTQ_TRY(check_weight(c, w));
+  RTQ_TRY(check_blocks(w, lora, rb));
+  if (!job || !h_out || !g_out) return fail(RTQ_ERR_INVALID, "deferred backward needs h, g and a job");
+  if (is_dense(w->type)) return fail(RTQ_ERR_INVALID, "deferred backward: quantised weights only");
+  if (hp_have && rtq_lora_partial_floats(w, t, lora && lora->enabled ? lora->rank : 0) == 0) hp_have = nullptr;
+  const LoraDefer df{h_out, g_out, job};
+  return linear_backward_d(c, w, lora, x, dy, t, dx, ga, gb, stream, rb, hp_have, &df);
+}
+
+rtq_status rtq_lora_grads_d(rtq_ctx* c, const LoraGradArgs* jobs, int n, void* stream) {
+  if (!c) return fail(RTQ_ERR_INVALID, "null context");
+  if (n < 0 || n > RTQ_LORA_JOBS) return fail(RTQ_ERR_INVALID, "%d LoRA gradient jobs (at most %d)", n, RTQ_LORA_JOBS);
+  LoraGradBatch b{};
+  int64_t total = 0, tmax = 0;
+  for (int i = 0; i < n; i++) {
+    if (jobs[i].n_gb + jobs[i].n_ga == 0) continue;
+    b.start[b.njobs] = (int)total;
+    b.job[b.njobs++] = jobs[i];
+    total += jobs[i].n_gb + jobs[i].n_ga;
+    tmax = std::max<int64_t>(tmax, jobs[i].T);
+  }
+  b.start[b.njobs] = (int)total;
+  if (total == 0) return RTQ_OK;
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  const bool w16 = tmax >= 256;  // 16 waves split long token ranges, as in rtq_bwd_finish16
+  return launch(c, w16 ? K_LORA_GRADS16 : K_LORA_GRADS, dim3((unsigned)total), dim3(w16 ? 1024 : 256),
+                (hipStream_t)stream, b);
 }
 
 rtq_status rtq_linear_backward_blocks_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const RankBlocks* rb,
