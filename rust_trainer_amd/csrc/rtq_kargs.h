@@ -139,14 +139,16 @@ struct BwdPrepArgs {
   int nhq;
   float* gp;     // [ngq][T][r] partials of dy . B
   int ngq;
+  float* dymax;  // [ngq][T]: max |dy| over each 256-row slice (the dx kernels' f16 range), or null
   RankBlocks rb;  // g = dy . B restricted to each member's rows
   int y0;         // grid row offset: nhq when the h partials are already there (only g is computed)
   int gtok;       // tokens per g-partial workgroup: 64 (a wave per 16 tokens) or 16 (a wave per 64 rows)
 };
 
-// part[z][t][k] = sum over rows n of split z of dy[t][n] W[n][k], three bf16 MFMAs per product (hi/lo split of dy
-// and W).  rtq_dx_*: workgroup tile 64 tokens x 128 columns, partials in MFMA fragment order;
-// rtq_dx16_* (T <= 16): tile 16 tokens x 128 columns, partials row-major [nsplit][T][K].
+// part[z][t][k] = sum over rows n of split z of dy[t][n] W[n][k], three 16-bit MFMAs per product (hi / lo
+// split of dy and W: f16 with dy scaled per row by rtq_dx_* / rtq_dxw_*, bf16 by rtq_dx16_*).
+// rtq_dx_*: workgroup tile 64 tokens x 128 columns, partials in MFMA fragment order; rtq_dx16_*
+// (T <= 16): tile 16 tokens x 128 columns, partials row-major [nsplit][T][K].
 struct DxArgs {
   const void* wq;
   const uint16_t* wd;
@@ -164,6 +166,11 @@ struct DxArgs {
   float s;
   float* h;             // [T x r] = sum of hp
   float* g;             // [T x r] = s * sum of gp
+  // rtq_dx_* / rtq_dxw_*: f16 operands need dy's range: dymax [dmq][T] = max |dy[t][n]| over the
+  // 256-row slice q (rtq_bwd_prep); W's values scaled by wsc = 2^-sigma, the partials by wunsc
+  const float* dymax;
+  int dmq;
+  float wsc, wunsc;
 };
 
 // dx[t][k] = [dx +] sum_s part[s][t][k] [+ sum_j g[t][j] A[j][k]];

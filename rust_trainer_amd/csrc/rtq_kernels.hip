@@ -46,6 +46,10 @@ __device__ __forceinline__ f4 mfma_f32(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+// two floats -> f16 pair, rounded toward zero (v_cvt_pkrtz_f16_f32)
+__device__ __forceinline__ half2v pk_rtz(float a, float b) {
+  return __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
 __device__ __forceinline__ uint32_t comp(const u4v& v, int j) {
   return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w));
 }
@@ -360,6 +364,22 @@ __device__ __forceinline__ void lora_up_partial(const BwdPrepArgs& a, int t0, in
     }
   }
   const bool tok_ok = tw < a.T;  // wave-uniform
+  if (a.dymax) {  // max |dy| of each token over the slice: lane, then the four lane groups (then the waves)
+    float mx = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NU; u++) mx = fmaxf(mx, fabsf(v[u]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    if (TW == 64) {
+      if (g == 0 && t < a.T) a.dymax[(int64_t)q * a.T + t] = mx;
+    } else {
+      if (g == 0) red[w * 16 + li] = mx;
+      __syncthreads();
+      if (tid < 16 && t0 + tid < a.T)
+        a.dymax[(int64_t)q * a.T + t0 + tid] = fmaxf(fmaxf(red[tid], red[16 + tid]), fmaxf(red[32 + tid], red[48 + tid]));
+      // red is next written after the staging barrier below, which every reader has passed
+    }
+  }
   for (int j0 = 0; j0 < a.r; j0 += 16) {
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     const bool any = rb_any(a.rb, k0, min(k0 + KQ, a.N), j0, min(j0 + 16, a.r));  // uniform over the workgroup
@@ -1501,19 +1521,24 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_prep(BwdPrepArgs a) {
 
 // ============================================================== dx = dy . W
 // Workgroup: 8 waves, tile 64 tokens x 128 columns (one K chunk); wave (wt, wk) owns 32 tokens x
-// 32 columns (2 x 2 MFMA tiles).  Rows of W are split over blockIdx.z; each split writes its own
-// partial tile part[z][t][k] (plain stores; rtq_bwd_finish sums the splits in order).  Per
-// 32-row step the workgroup stages, double buffered in LDS:
-//   * dy[64 x 32] as bf16 hi/lo A fragments: each thread loads one float4 and splits it;
-//   * W[32 x 128] dequantised (Q4_0, Q8_0: d*q, at most 15 significant bits; Q6_K: (d*sc)*q, at
-//     most 23; Q4_K: (d*sc)*u - dmin*m rounded once, as ggml's dequantisation), split into bf16
-//     hi + lo by truncation (exact for Q4_0 / Q8_0), stored transposed ([k][n]) so a lane reads
-//     its B fragment (8 consecutive rows of one column) in 16 bytes.
-// Three bf16 MFMAs per product (dh.wh + dl.wh + dh.wl): the missing dl.wl term and the
-// truncation of dl leave a relative error near 2^-16 per product.
+// 32 columns (2 x 2 MFMA tiles).  Rows of W are split over workgroups; each split writes its own
+// partial tile (plain stores; rtq_bwd_finish sums the splits in order).  Per 32-row step the
+// workgroup stages, double buffered in LDS, f16 hi / lo MFMA operands:
+//   * dy[64 x 32]: each thread loads one float4, scales it by 2^e (e per token row and split, so
+//     that the split's largest |dy| of the row lands in [2^14, 2^15): the f16 range holds every
+//     value of the row) and splits it into hi = f16 (round toward zero) and lo = f16 of the rest;
+//   * W[32 x 128]: Q4_0 / Q8_0 d * q exactly as hi = f16(d * q) and lo = d * q - hi (packed f16
+//     multiply and fused multiply-add on the two rows a thread converts: the residual of an f16
+//     product is exact); K-quants: the f32 value of ggml's dequantisation ((d*sc)*u - dmin*m, or
+//     (d*sc)*q) split like dy.  Stored transposed ([k][n]), so a lane reads its B fragment (8
+//     consecutive rows of one column) in 16 bytes.
+// Three f16 MFMAs per product (dh.wh + dl.wh + dh.wl): the missing dl.wl term and the rounding
+// of dl leave a relative error near 2^-21 per product; the partial is scaled back by 2^-e (exact).
+// Weights whose values could reach 2^15 are pre-scaled by 2^-sigma (wsc) and scaled back in the
+// same multiply (wunsc); sigma is 0 for every realistic weight.
 // Global loads go through buffer descriptors: a per-thread 32-bit offset plus a per-step scalar
-// offset, with out-of-range reads (tokens >= T) returning zero.  A 4-deep register ring keeps
-// the loads of step s + 3 in flight while step s is staged and multiplied.
+// offset, with out-of-range reads (tokens >= T) returning zero.  A register ring keeps the loads
+// D - 1 steps ahead of the MFMAs.
 // W staging: thread -> half hh = tid/256 (hh 0: elements 4gg..4gg+3 of the block, hh 1:
 // 16+4gg..16+4gg+3), row group rgl, rows 2p, 2p+1, k-group gg and block jb, ordered so the code
 // words a wave loads lie in one 512-byte span; the two rows' scales are adjacent (one load).
@@ -1594,8 +1619,9 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
     return;  // uniform over the workgroup, before any barrier
   }
   constexpr int D = TW == 64 ? 4 : 3;
-  __shared__ u4v sA[2][TW / 16][2][64];                             // [buf][tile][hi/lo][lane]
-  __shared__ __attribute__((aligned(16))) __bf16 sW[2][2][128][40];   // [buf][hi/lo][k][n]
+  __shared__ u4v sA[2][TW / 16][2][64];                               // [buf][tile][hi/lo][lane]
+  __shared__ __attribute__((aligned(16))) _Float16 sW[2][2][128][40];   // [buf][hi/lo][k][n]
+  __shared__ float sInv[TW];  // 2^-e (times wunsc) of each token row of the tile
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
   const int wt = TW == 64 ? w >> 2 : w >> 1, wk = TW == 64 ? w & 3 : w & 1;
   // id -> (XCD id % 8, slot id / 8) -> K chunk slot % Kc of unit u = (slot / Kc) * 8 + XCD: the Kc
@@ -1647,6 +1673,27 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   const uint32_t q_rg = (uint32_t)Kc * 64 * 16 * (B8 ? 2 : 1);  // bytes per row group
   const uint32_t d_rg = (uint32_t)Kc * 128, e_rg = (uint32_t)Kc * 32;
 
+  // 2^e of this thread's dy rows tl + 64 m: e from the largest |dy| of the row over the slices of
+  // 256 rows that meet this split (their maxima from rtq_bwd_prep); 1 for a zero row
+  float dsc[NQ];
+  {
+    const int q0 = n0 / 256, q1 = min((n0 + a.n_per_split + 255) / 256, a.dmq);
+#pragma unroll
+    for (int m = 0; m < NQ; m++) {
+      const int t = t0 + tl + 64 * m;
+      float mx = 0.0f;
+      if (t < a.T)
+        for (int q = q0; q < q1; q++) mx = fmaxf(mx, a.dymax[(int64_t)q * a.T + t]);
+      int ex = 0;
+      (void)frexpf(mx, &ex);  // mx = f 2^ex, f in [0.5, 1)
+      const bool ok = mx > 0.0f && mx <= 3.0e38f;
+      dsc[m] = ok ? ldexpf(1.0f, 15 - ex) : 1.0f;
+      if (q4 == 0) sInv[tl + 64 * m] = (ok ? ldexpf(1.0f, ex - 15) : 1.0f) * a.wunsc;
+    }
+  }
+  // -1 as a run-time value (wsc * wunsc = 1 exactly), so v - hi stays one mixed-precision FMA
+  const float neg1 = -(a.wsc * a.wunsc);
+
   DxSlot<FMT, NQ> sl[D];
   auto issue = [&](DxSlot<FMT, NQ>& S, int step) {
     const int ns = n0 + 32 * min(step, max(nsteps - 1, 0));  // clamped: always a real step
@@ -1679,65 +1726,81 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   auto stage = [&](const DxSlot<FMT, NQ>& S, int buf) {
 #pragma unroll
     for (int m = 0; m < NQ; m++) {  // dy: A fragment tile (tl>>4) + 4m, lane (tl&15) + 16*(q4>>1), slots 4*(q4&1) ..
-      // bit view of the whole vector: masking bit_casts of single float4 lanes is miscompiled
-      // by this compiler (every lane gets lane 0's mask)
-      const u4v vb = __builtin_bit_cast(u4v, S.dy[m]);
-      uint32_t lb[4];
-#pragma unroll
-      for (int c = 0; c < 4; c++) lb[c] = __builtin_bit_cast(uint32_t, S.dy[m][c] - __builtin_bit_cast(float, vb[c] & 0xffff0000u));
-      u2v hv, lv;
-      hv.x = __builtin_amdgcn_perm(vb[1], vb[0], 0x07060302u);  // high halves: bf16 by truncation
-      hv.y = __builtin_amdgcn_perm(vb[3], vb[2], 0x07060302u);
-      lv.x = __builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u);
-      lv.y = __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u);
+      const float x0 = S.dy[m][0] * dsc[m], x1 = S.dy[m][1] * dsc[m], x2 = S.dy[m][2] * dsc[m], x3 = S.dy[m][3] * dsc[m];
+      const half2v h01 = pk_rtz(x0, x1), h23 = pk_rtz(x2, x3);
+      // x - hi = dy 2^e - hi exactly (at most 13 significant bits): one mixed-precision FMA each
+      const half2v l01 = pk_rtz(fmaf(S.dy[m][0], dsc[m], -(float)h01.x), fmaf(S.dy[m][1], dsc[m], -(float)h01.y));
+      const half2v l23 = pk_rtz(fmaf(S.dy[m][2], dsc[m], -(float)h23.x), fmaf(S.dy[m][3], dsc[m], -(float)h23.y));
+      const u2v hv = {__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)};
+      const u2v lv = {__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)};
       const int fl = (tl & 15) + 16 * (q4 >> 1);
       reinterpret_cast<u2v*>(&sA[buf][(tl >> 4) + 4 * m][0][fl])[q4 & 1] = hv;
       reinterpret_cast<u2v*>(&sA[buf][(tl >> 4) + 4 * m][1][fl])[q4 & 1] = lv;
     }
-    {  // W: rows 2p, 2p+1 -> bf16 hi / lo planes, one 32-bit word (both rows) per column
-      uint32_t vb[2][4], lb[2][4];
+    // W: rows 2p, 2p+1 -> f16 hi / lo planes, one 32-bit word (both rows) per column
+    uint32_t hw[4], lw[4];
+    if constexpr (KQ) {
+      float v[2][4];
 #pragma unroll
       for (int r = 0; r < 2; r++) {
         float d, m;
-        if constexpr (KQ)
-          dq_params<FMT>(0u, comp(S.k, 2 * r + (jb >> 1)), r ? S.e.y : S.e.x, jb, hh, d, m);
-        else
-          dq_params<FMT>(r ? (S.d >> 16) : (S.d & 0xffffu), 0u, 0u, jb, hh, d, m);
+        dq_params<FMT>(0u, comp(S.k, 2 * r + (jb >> 1)), r ? S.e.y : S.e.x, jb, hh, d, m);
+        d *= a.wsc;  // exact (a power of two; 1 unless a scale is huge)
+        m *= a.wsc;
         const uint32_t u = B8 ? S.q[r] ^ 0x80808080u : (hh ? (S.q[r] >> 4) : S.q[r]) & 0x0f0f0f0fu;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          // the dequantised value, rounded once (exact for Q4_0, Q8_0 and Q6_K)
-          const float v = fmaf((float)((u >> (8 * e)) & 0xffu), d, m);
-          vb[r][e] = __builtin_bit_cast(uint32_t, v);
-          lb[r][e] = __builtin_bit_cast(uint32_t, v - __builtin_bit_cast(float, vb[r][e] & 0xffff0000u));
-        }
+        for (int e = 0; e < 4; e++) v[r][e] = fmaf((float)((u >> (8 * e)) & 0xffu), d, m);  // rounded once, as ggml
       }
-      const int kb = 32 * jb + 16 * hh + 4 * wgg;
-      const int ns = nloc ^ (8 * jb);  // swizzled row (pair start stays even)
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        *reinterpret_cast<uint32_t*>(&sW[buf][0][kb + e][ns]) = __builtin_amdgcn_perm(vb[1][e], vb[0][e], 0x07060302u);
-        *reinterpret_cast<uint32_t*>(&sW[buf][1][kb + e][ns]) = __builtin_amdgcn_perm(lb[1][e], lb[0][e], 0x07060302u);
+        const half2v h = pk_rtz(v[0][e], v[1][e]);
+        hw[e] = __builtin_bit_cast(uint32_t, h);
+        lw[e] = __builtin_bit_cast(uint32_t, pk_rtz(fmaf((float)h.x, neg1, v[0][e]), fmaf((float)h.y, neg1, v[1][e])));
       }
+    } else {
+      // codes as exact f16 pairs (1024 + u of row 2p, of row 2p+1): bytes interleaved by row, then
+      // each pair of bytes widened with 0x64, the high byte of 1024.0; c = that - (1024 + offset)
+      const uint32_t u0 = B8 ? S.q[0] ^ 0x80808080u : (hh ? (S.q[0] >> 4) : S.q[0]) & 0x0f0f0f0fu;
+      const uint32_t u1 = B8 ? S.q[1] ^ 0x80808080u : (hh ? (S.q[1] >> 4) : S.q[1]) & 0x0f0f0f0fu;
+      const uint32_t i01 = __builtin_amdgcn_perm(u1, u0, 0x05010400u), i23 = __builtin_amdgcn_perm(u1, u0, 0x07030602u);
+      half2v dp = __builtin_bit_cast(half2v, S.d);  // fp16 scales of rows 2p, 2p+1
+      dp = dp * half2v{(_Float16)a.wsc, (_Float16)a.wsc};  // exact, as for the K-quants
+      constexpr _Float16 OFF = B8 ? (_Float16)1152.0f : (_Float16)1032.0f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t src = e < 2 ? i01 : i23;
+        const half2v c = sub_h2((e & 1) ? bytes23_to_h2(src) : bytes01_to_h2(src), OFF);
+        const half2v h = dp * c;                                // f16 product, rounded
+        const half2v l = __builtin_elementwise_fma(dp, c, -h);  // its exact residual
+        hw[e] = __builtin_bit_cast(uint32_t, h);
+        lw[e] = __builtin_bit_cast(uint32_t, l);
+      }
+    }
+    const int kb = 32 * jb + 16 * hh + 4 * wgg;
+    const int ns = nloc ^ (8 * jb);  // swizzled row (pair start stays even)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      *reinterpret_cast<uint32_t*>(&sW[buf][0][kb + e][ns]) = hw[e];
+      *reinterpret_cast<uint32_t*>(&sW[buf][1][kb + e][ns]) = lw[e];
     }
   };
   // the wave's operand fragments of one step: A (dy) hi / lo of its two token tiles, B (W) hi / lo
   // of its two column tiles
   struct Frags {
-    bf8 a[TS][2], b[KS][2];
+    half8 a[TS][2], b[KS][2];
   };
   auto load_frags = [&](int buf, Frags& F) {
 #pragma unroll
     for (int ts = 0; ts < TS; ts++) {
-      F.a[ts][0] = __builtin_bit_cast(bf8, sA[buf][wt * TS + ts][0][lane]);
-      F.a[ts][1] = __builtin_bit_cast(bf8, sA[buf][wt * TS + ts][1][lane]);
+      F.a[ts][0] = __builtin_bit_cast(half8, sA[buf][wt * TS + ts][0][lane]);
+      F.a[ts][1] = __builtin_bit_cast(half8, sA[buf][wt * TS + ts][1][lane]);
     }
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
       // column kl lies in block kl / 32, whose rows are swizzled by 8 (kl / 32)
       const int kl = wk * 16 * KS + ks * 16 + li, jbk = (wk * 16 * KS + ks * 16) >> 5;
-      F.b[ks][0] = *reinterpret_cast<const bf8*>(&sW[buf][0][kl][8 * (g ^ jbk)]);
-      F.b[ks][1] = *reinterpret_cast<const bf8*>(&sW[buf][1][kl][8 * (g ^ jbk)]);
+      F.b[ks][0] = *reinterpret_cast<const half8*>(&sW[buf][0][kl][8 * (g ^ jbk)]);
+      F.b[ks][1] = *reinterpret_cast<const half8*>(&sW[buf][1][kl][8 * (g ^ jbk)]);
     }
   };
   auto compute = [&](const Frags& F) {
@@ -1745,9 +1808,9 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
     for (int ts = 0; ts < TS; ts++)
 #pragma unroll
       for (int ks = 0; ks < KS; ks++) {
-        acc[ts][ks] = mfma_bf16(F.a[ts][0], F.b[ks][0], acc[ts][ks]);
-        acc[ts][ks] = mfma_bf16(F.a[ts][1], F.b[ks][0], acc[ts][ks]);
-        acc[ts][ks] = mfma_bf16(F.a[ts][0], F.b[ks][1], acc[ts][ks]);
+        acc[ts][ks] = mfma_f16(F.a[ts][0], F.b[ks][0], acc[ts][ks]);
+        acc[ts][ks] = mfma_f16(F.a[ts][1], F.b[ks][0], acc[ts][ks]);
+        acc[ts][ks] = mfma_f16(F.a[ts][0], F.b[ks][1], acc[ts][ks]);
       }
   };
   // Step s: one barrier (buffer s & 1 is staged by all waves, buffer (s + 1) & 1 is free: every
@@ -1786,6 +1849,16 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
 #pragma unroll
     for (int s0 = 0; s0 < D; s0++) step_body(s0, nfull + s0, false);
   }
+  // rows back to dy's scale (and W's): element i of acc[ts][ks] is tile row TW == 64 ? 32wt + 16ts + 4g + i
+  // : 64wt + 16ts + 4g + i (sInv was written before the loop's first barrier)
+#pragma unroll
+  for (int ts = 0; ts < TS; ts++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float sv = sInv[(TW == 64 ? 32 : 64) * wt + 16 * ts + 4 * g + i];
+#pragma unroll
+      for (int ks = 0; ks < KS; ks++) acc[ts][ks][i] *= sv;
+    }
   // partial tile of this split in fragment order: part[sp][tile][wave][q][lane] (float4 each),
   // tile = 64-token tile * Kc + K chunk, wave = 4 wt' + wk', q = 2 ts' + ks' in the TW = 64 layout:
   // element i is row 64 tile + 32wt' + 16ts' + 4g + i, column 128kc + 32wk' + 16ks' + li.  Each

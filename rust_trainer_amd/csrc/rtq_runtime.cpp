@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -220,6 +221,9 @@ struct rtq_weight {
   uint16_t* wdr = nullptr;  // row-major scales for the GEMV (the K-quants' wd itself)
   uint32_t* wsb = nullptr;  // K-quant super-block scales, else null
   const float* wsc = nullptr;  // TQ8_0: f32 block scales (wq: the i8 codes; F32: wq is the weight)
+  // the dx kernels' f16 range: dequantised values times dx_wsc = 2^-sigma stay below 2^15 (sigma 0
+  // unless a scale is huge); their partials are multiplied by dx_wunsc = 2^sigma
+  float dx_wsc = 1.0f, dx_wunsc = 1.0f;
 };
 
 namespace {
@@ -657,17 +661,18 @@ DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
   return p;
 }
 
+// partial-product slices of the LoRA reductions over n columns (multiple of 4, see sum_partials)
+int64_t lora_slices(int64_t n) { return roundup(cdiv(std::max<int64_t>(n, 1), RTQ_ACT_KQ), 4); }
+
 // backward workspace: h, g [t x r], their slice partials [t][r][slices], dx split partials
 size_t bwd_ws_bytes(const rtq_ctx* c, const rtq_weight* w, int64_t t, int64_t r) {
   const int64_t n = w->rows, k = w->cols;
   if (is_dense(w->type)) return (size_t)(2 * t * std::max<int64_t>(r, 0)) * 4 + 3 * 256;
   const int64_t sl = roundup(cdiv(std::max<int64_t>(n, 1), RTQ_ACT_KQ), 4) + roundup(cdiv(std::max<int64_t>(k, 1), RTQ_ACT_KQ), 4);
   return (size_t)((2 + sl) * t * std::max<int64_t>(r, 0)) * 4 + dx_plan(c, w, std::max<int64_t>(t, 1)).part_floats * 4 +
-         6 * 256;
+         (size_t)(lora_slices(n) * t) * 4 + 7 * 256;
 }
 
-// partial-product slices of the LoRA reductions over n columns (multiple of 4, see sum_partials)
-int64_t lora_slices(int64_t n) { return roundup(cdiv(std::max<int64_t>(n, 1), RTQ_ACT_KQ), 4); }
 
 // dx (+)= dy.W (accumulate: FrozenMatmul::backward_input; otherwise dx is overwritten, as
 // Linear::backward returns a fresh dx); with LoRA also dx += g.A, ga += g^T x, gb += (s dy)^T h
@@ -702,19 +707,28 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   float* hp = lora ? (have_h ? const_cast<float*>(hp_have) : ar.take<float>((size_t)(nhq * t * r))) : nullptr;
   float* gp = lora ? ar.take<float>((size_t)(ngq * t * r)) : nullptr;
   float* part = ar.take<float>(dp.part_floats);
+  // row maxima of dy per 256-row slice, for the f16 range of rtq_dx_* / rtq_dxw_* (from the LoRA g
+  // partial kernel, or the same kernel with no adapter)
+  float* dymax = dp.tok16 ? nullptr : ar.take<float>((size_t)(ngq * t));
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   if (lora) {
     // h partials: 16 tokens per workgroup; g partials: 64, or 16 where 64-token workgroups would
     // leave more than half of the CUs without one
     const int gtok = cdiv(t, 64) * ngq * 2 >= c->cu_count ? 64 : 16;
-    BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq, RankBlocks{},
+    BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq, dymax, RankBlocks{},
                    have_h ? (int)nhq : 0, gtok};
     if (rb) pa.rb = *rb;
     RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, have_h ? gtok : 16), (unsigned)(have_h ? ngq : nhq + ngq)),
                    dim3(256), st, pa));
+  } else if (dymax) {
+    const int gtok = cdiv(t, 64) * ngq * 2 >= c->cu_count ? 64 : 16;
+    BwdPrepArgs pa{nullptr, nullptr, K, dy, nullptr, N, (int)t, 0, nullptr, 0, nullptr, (int)ngq, dymax, RankBlocks{},
+                   0, gtok};
+    RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, gtok), (unsigned)ngq), dim3(256), st, pa));
   }
   DxArgs xa{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, (int)dp.splits, part,
-            lora ? hp : nullptr, lora ? gp : nullptr, (int)nhq, (int)ngq, (int)r, s, h, g};
+            lora ? hp : nullptr, lora ? gp : nullptr, (int)nhq, (int)ngq, (int)r, s, h, g, dymax, (int)ngq,
+            w->dx_wsc, w->dx_wunsc};
   const int kid = (dp.tok16 ? K_DX16 : (dp.wide ? K_DXW : K_DX)) + fmt_index(w->type);
   set_work(c, w, t, 0, true);
   // t > 16: (token group, split) units of K-chunk workgroups, padded to a multiple of 8 (XCD order)
@@ -1122,6 +1136,25 @@ rtq_status rtq_weight_create(rtq_ctx* c, int type, const void* blocks, size_t nb
   else
     repack_q32(type, (const uint8_t*)blocks, rows, cols, w->Np, w->Kp, host.data() + q_off,
                reinterpret_cast<uint16_t*>(host.data() + d_off), reinterpret_cast<uint16_t*>(host.data() + r_off));
+  {  // bound of |dequantised value| -> sigma
+    double bound = 0.0;
+    if (is_kquant(type)) {
+      const uint32_t* sb = reinterpret_cast<const uint32_t*>(host.data() + e_off);
+      for (size_t i = 0; i < e_bytes / 4; i++) {
+        const double d = fabs((double)f16_bits_to_f32((uint16_t)(sb[i] & 0xffffu)));
+        const double dm = fabs((double)f16_bits_to_f32((uint16_t)(sb[i] >> 16)));
+        bound = std::max(bound, type == RTQ_TYPE_Q4_K ? d * 63.0 * 15.0 + dm * 63.0 : d * 128.0 * 32.0);
+      }
+    } else {
+      const uint16_t* dd = reinterpret_cast<const uint16_t*>(host.data() + d_off);
+      for (size_t i = 0; i < d_bytes / 2; i++)
+        bound = std::max(bound, fabs((double)f16_bits_to_f32(dd[i])) * (type == RTQ_TYPE_Q4_0 ? 8.0 : 128.0));
+    }
+    int sigma = 0;
+    while (sigma < 60 && bound * std::ldexp(1.0, -sigma) >= 32768.0) sigma++;
+    w->dx_wsc = std::ldexp(1.0f, -sigma);
+    w->dx_wunsc = std::ldexp(1.0f, sigma);
+  }
   hipError_t e = hipMalloc(&w->dmem, total);
   if (e != hipSuccess) {
     delete w;
