@@ -221,7 +221,7 @@ int rtq_model_checkpointing(const rtq_model* m); /* 1 when the last step recompu
 /* Attention kernels of the step (the results agree within f32 rounding): 1 the fused kernels
  * (online softmax, no probability matrix; head_dim 64 or 128 only), 0 the probability-matrix path
  * (S, softmax, P V and their backward as separate launches, P [heads x t x t] kept per layer), -1
- * (default) fused for packed batches and sequences of 2048 tokens or more. */
+ * (default) fused whenever the head size allows. */
 rtq_status rtq_model_set_attention(rtq_model* m, int mode);
 int rtq_model_attention_fused(const rtq_model* m); /* 1 when the last step used the fused kernels */
 /* parity / debug: while layer >= 0 (-1: off), each step copies that block's tensors in the forward

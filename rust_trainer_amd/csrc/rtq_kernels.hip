@@ -1674,22 +1674,35 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   const uint32_t d_rg = (uint32_t)Kc * 128, e_rg = (uint32_t)Kc * 32;
 
   // 2^e of this thread's dy rows tl + 64 m: e from the largest |dy| of the row over the slices of
-  // 256 rows that meet this split (their maxima from rtq_bwd_prep); 1 for a zero row
+  // 256 rows that meet this split (their maxima from rtq_bwd_prep); 1 for a zero row.  All threads
+  // reduce the tile's rows: thread (row tid % TW, slices tid / TW + k (512 / TW)), then the partial
+  // maxima in LDS (a split may span many slices: 76 for a 19456-row weight).
   float dsc[NQ];
   {
+    __shared__ float sRed[512];
+    constexpr int PER = 512 / TW;
     const int q0 = n0 / 256, q1 = min((n0 + a.n_per_split + 255) / 256, a.dmq);
-#pragma unroll
-    for (int m = 0; m < NQ; m++) {
-      const int t = t0 + tl + 64 * m;
-      float mx = 0.0f;
-      if (t < a.T)
-        for (int q = q0; q < q1; q++) mx = fmaxf(mx, a.dymax[(int64_t)q * a.T + t]);
-      int ex = 0;
-      (void)frexpf(mx, &ex);  // mx = f 2^ex, f in [0.5, 1)
-      const bool ok = mx > 0.0f && mx <= 3.0e38f;
-      dsc[m] = ok ? ldexpf(1.0f, 15 - ex) : 1.0f;
-      if (q4 == 0) sInv[tl + 64 * m] = (ok ? ldexpf(1.0f, ex - 15) : 1.0f) * a.wunsc;
+    const int tok = tid % TW, t = t0 + tok;
+    float mx = 0.0f;
+    if (t < a.T) {
+#pragma unroll 4
+      for (int q = q0 + tid / TW; q < q1; q += PER) mx = fmaxf(mx, a.dymax[(int64_t)q * a.T + t]);
     }
+    sRed[tid] = mx;
+    __syncthreads();
+    if (tid < TW) {
+      float m = sRed[tid];
+#pragma unroll
+      for (int k = 1; k < PER; k++) m = fmaxf(m, sRed[tid + k * TW]);
+      int ex = 0;
+      (void)frexpf(m, &ex);  // m = f 2^ex, f in [0.5, 1)
+      const bool ok = m > 0.0f && m <= 3.0e38f;
+      sRed[tid] = ok ? ldexpf(1.0f, 15 - ex) : 1.0f;
+      sInv[tid] = (ok ? ldexpf(1.0f, ex - 15) : 1.0f) * a.wunsc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < NQ; m++) dsc[m] = sRed[tl + 64 * m];
   }
   // -1 as a run-time value (wsc * wunsc = 1 exactly), so v - hi stays one mixed-precision FMA
   const float neg1 = -(a.wsc * a.wunsc);
@@ -2062,10 +2075,11 @@ extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q8_0(DxArgs a) { dx16
 extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q4_k(DxArgs a) { dx16_tile<FMT_Q4_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q6_k(DxArgs a) { dx16_tile<FMT_Q6_K>(a); }
 
-extern "C" __global__ __launch_bounds__(512) void rtq_dx_q4_0(DxArgs a) { dx_tile<FMT_Q4_0, 64>(a); }
-extern "C" __global__ __launch_bounds__(512) void rtq_dx_q8_0(DxArgs a) { dx_tile<FMT_Q8_0, 64>(a); }
-extern "C" __global__ __launch_bounds__(512) void rtq_dx_q4_k(DxArgs a) { dx_tile<FMT_Q4_K, 64>(a); }
-extern "C" __global__ __launch_bounds__(512) void rtq_dx_q6_k(DxArgs a) { dx_tile<FMT_Q6_K, 64>(a); }
+// two 64-token workgroups per CU (four waves per SIMD: at most 128 VGPRs)
+extern "C" __global__ __launch_bounds__(512, 4) void rtq_dx_q4_0(DxArgs a) { dx_tile<FMT_Q4_0, 64>(a); }
+extern "C" __global__ __launch_bounds__(512, 4) void rtq_dx_q8_0(DxArgs a) { dx_tile<FMT_Q8_0, 64>(a); }
+extern "C" __global__ __launch_bounds__(512, 4) void rtq_dx_q4_k(DxArgs a) { dx_tile<FMT_Q4_K, 64>(a); }
+extern "C" __global__ __launch_bounds__(512, 4) void rtq_dx_q6_k(DxArgs a) { dx_tile<FMT_Q6_K, 64>(a); }
 extern "C" __global__ __launch_bounds__(512) void rtq_dxw_q4_0(DxArgs a) { dx_tile<FMT_Q4_0, 256>(a); }
 extern "C" __global__ __launch_bounds__(512) void rtq_dxw_q8_0(DxArgs a) { dx_tile<FMT_Q8_0, 256>(a); }
 extern "C" __global__ __launch_bounds__(512) void rtq_dxw_q4_k(DxArgs a) { dx_tile<FMT_Q4_K, 256>(a); }

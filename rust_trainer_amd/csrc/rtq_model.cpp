@@ -135,15 +135,16 @@ struct rtq_model {
   bool packed = false;
   bool rope_plain = false;  // the uploaded RoPE tables are for positions 0..rope_t-1
   // fused attention (head_dim 64 or 128): work tables of the current layout, partial slots.
-  // attn_mode -1 (default): fused for packed layouts and sequences of 2048 tokens or more (below
-  // that, at 512 tokens, the probability-matrix path's larger product tiles and fewer merges win);
-  // 0 / 1 force one (rtq_model_set_attention).  attn_fused: this step's choice.
+  // attn_mode -1 (default) and 1: fused whenever the head size allows (measured on the
+  // Qwen3-0.6B-shaped step from 128 to 2048 tokens it ties or beats the probability-matrix path,
+  // which 0 forces; rtq_model_set_attention).  attn_fused: this step's choice.
   bool attn_hd_ok = false;
   int attn_mode = -1;
   bool attn_fused = false;
   // the probability-matrix path's products on split 16-bit MFMA (rtq_m_gemm*_hf forward, *_bf
   // backward); RTQ_ATTN_F32=1 at load time keeps them on f32 MFMA (rtq_m_gemm*), for comparison
   bool attn_f32 = false;
+  int attn_items = 2;  // fused attention work items per CU aimed at (RTQ_ATTN_ITEMS; 0: rows never cut)
   int64_t layout_fused = -1;  // attn_fused the step buffers were laid out for
   float* attn_D = nullptr;  // [nh x t] dO . o per query row
   void* attn_mem = nullptr;
@@ -603,9 +604,16 @@ rtq_status ensure_attn_plan(rtq_model* m, int64_t t, const int32_t* seg) {
         if (lv(qt, kb)) kl[(size_t)kb].push_back((int)(hr * nkt + qt));
     ku += (int64_t)kl[(size_t)kb].size() * nkv;
   }
-  // about two workgroups per CU: longer ranges are cut into pieces whose partials are merged
-  const int64_t target = 2 * (int64_t)rtq_ctx_cu_count(m->ctx);
-  const int64_t cf = std::max<int64_t>(1, (fu + target - 1) / target), ck = std::max<int64_t>(1, (ku + target - 1) / target);
+  // ranges are cut into pieces (partials merged after) of about the length that gives attn_items
+  // workgroups per CU, kept within 3 .. 6 tiles: measured on the Qwen3-0.6B-shaped step from 512 to
+  // 2048 tokens, shorter pieces cost more in merges than they gain, longer ones leave the longest
+  // rows as the tail (2048 tokens: 48.2 ms at 6 tiles, 52.0 uncut; 512: 12.98 at 3, 13.44 at 2).
+  // attn_items 0: no cuts, no merges.
+  const int64_t target = (int64_t)m->attn_items * rtq_ctx_cu_count(m->ctx);
+  auto piece = [&](int64_t units, int64_t whole) {
+    return target > 0 ? std::min<int64_t>(6, std::max<int64_t>(3, (units + target - 1) / target)) : whole;
+  };
+  const int64_t cf = piece(fu, nkt + 1), ck = piece(ku, (int64_t)grp * nkt + 1);
   std::vector<MAttnItem> itf, itk;
   std::vector<MAttnMerge> mf, mk;
   int slots_f = 0, slots_k = 0;
@@ -1147,6 +1155,7 @@ rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out)
   M_TRY(parse_config(g, &cfg, &factors));
   rtq_model* m = new rtq_model();
   if (const char* e = getenv("RTQ_ATTN_F32")) m->attn_f32 = atoi(e) != 0;
+  if (const char* e = getenv("RTQ_ATTN_ITEMS")) m->attn_items = std::max(0, atoi(e));
   if (const char* e = getenv("RTQ_LORA_BATCH")) m->lora_batch = atoi(e) != 0;
   m->ctx = ctx;
   m->cfg = cfg;
@@ -1421,7 +1430,7 @@ rtq_status step(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* p
     for (int64_t i = 0; i < t; i++)
       if (segments[i] < 0) return rtq_fail(RTQ_ERR_INVALID, "segment %lld is negative", (long long)i);
   M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
-  m->attn_fused = m->attn_hd_ok && (m->attn_mode == 1 || (m->attn_mode < 0 && (segments || t >= 2048)));
+  m->attn_fused = m->attn_hd_ok && m->attn_mode != 0;
   M_TRY(choose_ckpt(m, t, n));
   M_TRY(ensure_step(m, t, n));
   M_TRY(ensure_hpk(m, t));

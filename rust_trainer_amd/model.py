@@ -169,8 +169,8 @@ class GpuModel:
     @property
     def fused_attention(self):
         """Attention kernels: True the fused kernels (no probability matrix; head_dim 64 / 128),
-        False the probability-matrix path, None (default) chosen per step (fused for packed batches
-        and 2048+ tokens).  Reading it gives the last step's choice (None before any step)."""
+        False the probability-matrix path, None (default) the fused kernels whenever the head size
+        allows.  Reading it gives the last step's choice (None before any step)."""
         v = int(_ffi.lib().rtq_model_attention_fused(self._h))
         return None if not getattr(self, "_stepped", False) else bool(v)
 

@@ -186,10 +186,12 @@ CONFIG2_BLOCK = dict(n_layer=2, n_embd=1024, n_head=16, n_head_kv=8, head_dim=12
 ALL = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
 
 
+@pytest.mark.parametrize("fused", [None, False])  # None: the default (fused kernels); False: probability matrix
 @pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0, O.Q4_K, O.Q6_K])
-def test_config2_block_ops_match_oracle(ctx, wtype):
+def test_config2_block_ops_match_oracle(ctx, wtype, fused):
     spec = tiny_spec(wtype, **CONFIG2_BLOCK)
     g, model, m = build(ctx, spec, 16, 32.0, ALL)
+    model.fused_attention = fused
     t, n = 512, 256
     toks, pos, tok = sequence(spec.n_vocab, t, n, 5)
     wts = np.linspace(0.5, 1.5, n).astype(np.float32)
@@ -203,8 +205,7 @@ def test_config2_block_ops_match_oracle(ctx, wtype):
 
 
 def test_config2_block_ops_fused_attention_match_oracle(ctx):
-    """the configs[2] block with the fused attention kernels forced (the default picks them for
-    packed batches and 4096+ tokens only)"""
+    """the configs[2] block with the fused attention kernels forced, equal target weights"""
     spec = tiny_spec(O.Q4_K, **CONFIG2_BLOCK)
     g, model, m = build(ctx, spec, 16, 32.0, ALL)
     model.fused_attention = True
@@ -297,7 +298,7 @@ def test_config3_block_ops_packed_match_oracle(ctx):
     model.close()
 
 
-@pytest.mark.parametrize("fused", [False, None])  # None: the default, fused at 2048 tokens
+@pytest.mark.parametrize("fused", [False, None])  # None: the default (fused kernels)
 def test_config4_block_ops_match_oracle_recomputed(ctx, fused):
     spec = tiny_spec(O.Q8_0, n_layer=2, arch="llama", tied=False, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128,
                      rope_dim=128, n_ff=14336, n_vocab=4096, rope_base=5e5)
