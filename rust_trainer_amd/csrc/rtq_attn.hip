@@ -88,7 +88,20 @@ __device__ __forceinline__ void attn_merge_sum(const MAttnArgs& a, const MAttnMe
     if (mi < a.n_merges && e < NEL) CALL;                                               \
   }
 RTQ_ATTN_MERGE_KERNEL(rtq_m_attn_merge_fwd, 16 * a.hd, attn_merge_fwd(a, a.merges[mi], e))
-RTQ_ATTN_MERGE_KERNEL(rtq_m_attn_merge_dq, 16 * a.hd, attn_merge_sum(a, a.merges[mi], e, false))
-RTQ_ATTN_MERGE_KERNEL(rtq_m_attn_merge_dkv, 32 * a.hd, attn_merge_sum(a, a.merges[mi], e, true))
 #undef RTQ_ATTN_MERGE_KERNEL
+// the backward's merges in one launch: the dk / dv blocks (merges2, slots in part2; 32 x hd
+// elements each) then the dq blocks (merges; 16 x hd)
+extern "C" __global__ __launch_bounds__(256) void rtq_m_attn_merge_bwd(MAttnArgs a) {
+  const int pk = (32 * a.hd + 255) / 256, pq = (16 * a.hd + 255) / 256;
+  const int b = (int)blockIdx.x;
+  if (b < a.n_merges2 * pk) {
+    const int e = (b % pk) * 256 + threadIdx.x;
+    MAttnArgs k = a;
+    k.part = a.part2;
+    if (e < 32 * a.hd) attn_merge_sum(k, a.merges2[b / pk], e, true);
+  } else {
+    const int bq = b - a.n_merges2 * pk, mi = bq / pq, e = (bq % pq) * 256 + threadIdx.x;
+    if (mi < a.n_merges && e < 16 * a.hd) attn_merge_sum(a, a.merges[mi], e, false);
+  }
+}
 extern "C" __global__ __launch_bounds__(256) void rtq_m_attn_bwd_d(MAttnArgs a) { attn_bwd_d(a); }

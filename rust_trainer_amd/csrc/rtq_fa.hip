@@ -696,8 +696,27 @@ __device__ __forceinline__ void fa_dkv(const MAttnArgs& a, const MAttnItem& it, 
   }
 RTQ_FA_KERNEL(rtq_m_fa_fwd64, fa_fwd, FaFwdLds, 64)
 RTQ_FA_KERNEL(rtq_m_fa_fwd128, fa_fwd, FaFwdLds, 128)
-RTQ_FA_KERNEL(rtq_m_fa_dq64, fa_dq, FaDqLds, 64)
-RTQ_FA_KERNEL(rtq_m_fa_dq128, fa_dq, FaDqLds, 128)
-RTQ_FA_KERNEL(rtq_m_fa_dkv64, fa_dkv, FaKvLds, 64)
-RTQ_FA_KERNEL(rtq_m_fa_dkv128, fa_dkv, FaKvLds, 128)
 #undef RTQ_FA_KERNEL
+
+// the backward: the dk / dv items (the longer ones) then the dq items in one launch, each kind with
+// its own partial slots; LDS sized for the larger of the two layouts
+template <int HD>
+union FaBwdLds {
+  FaDqLds<HD> dq;
+  FaKvLds<HD> kv;
+};
+#define RTQ_FA_BWD_KERNEL(NAME, HD)                                            \
+  extern "C" __global__ __launch_bounds__(256) void NAME(MAttnArgs a) {       \
+    __shared__ __attribute__((aligned(16))) FaBwdLds<HD> L;                   \
+    const int b = (int)blockIdx.x;                                            \
+    if (b < a.n_items2) {                                                     \
+      MAttnArgs k = a;                                                        \
+      k.part = a.part2;                                                       \
+      fa_dkv<HD>(k, a.items2[b], L.kv);                                       \
+    } else if (b < a.n_items2 + a.n_items) {                                  \
+      fa_dq<HD>(a, a.items[b - a.n_items2], L.dq);                            \
+    }                                                                         \
+  }
+RTQ_FA_BWD_KERNEL(rtq_m_fa_bwd64, 64)
+RTQ_FA_BWD_KERNEL(rtq_m_fa_bwd128, 128)
+#undef RTQ_FA_BWD_KERNEL

@@ -26,8 +26,7 @@ enum RtqModelKernel {
   KM_GEMM_Q8,
   KM_GEMM32_Q8,
   KM_ATTN_MERGE_FWD,
-  KM_ATTN_MERGE_DQ,
-  KM_ATTN_MERGE_DKV,
+  KM_ATTN_MERGE_BWD,
   KM_ATTN_BWD_D,
   KM_GEMM_BF,
   KM_GEMM32_BF,
@@ -36,10 +35,8 @@ enum RtqModelKernel {
   KM_GEMM32_HF,
   KM_FA_FWD64,
   KM_FA_FWD128,
-  KM_FA_DQ64,
-  KM_FA_DQ128,
-  KM_FA_DKV64,
-  KM_FA_DKV128,
+  KM_FA_BWD64,
+  KM_FA_BWD128,
   KM_COUNT
 };
 

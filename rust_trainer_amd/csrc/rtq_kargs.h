@@ -370,6 +370,12 @@ struct MAttnArgs {
   const MAttnItem* items;
   const MAttnMerge* merges;
   int n_items, n_merges;
+  // the backward's second item kind (dk, dv: items2, their partial slots part2, merges2), run in
+  // the same launch as the dq items (rtq_m_fa_bwd*) and merged in the same launch
+  const MAttnItem* items2;
+  const MAttnMerge* merges2;
+  float* part2;
+  int n_items2, n_merges2;
   const int32_t* seg;  // packed layout (or null): segment per token
   const uint8_t* live; // and the 64 x 64 block liveness map (nlb blocks per side)
   int nlb;

@@ -152,7 +152,8 @@ struct rtq_model {
   MAttnItem *it_fwd = nullptr, *it_kv = nullptr;
   MAttnMerge *mg_fwd = nullptr, *mg_kv = nullptr;
   int n_fwd = 0, n_kv = 0, n_mfwd = 0, n_mkv = 0;
-  float* attn_part = nullptr;
+  float* attn_part = nullptr;     // forward and dq partial slots
+  float* attn_part_kv = nullptr;  // dk / dv partial slots
   int64_t attn_t = -1;
   bool attn_packed = false;
   std::vector<int32_t> attn_seg;  // the segments the tables were built for
@@ -639,7 +640,7 @@ rtq_status ensure_attn_plan(rtq_model* m, int64_t t, const int32_t* seg) {
   for (int g = 0; g < nkv; g++)
     for (int64_t kb = 0; kb < nlb; kb++) cut(kl[(size_t)kb], ck, g, (int)kb, slots_k, itk, mk);
   const auto al = [](size_t b) { return (b + 255) / 256 * 256; };
-  const size_t slots = (size_t)std::max(slots_f, slots_k);
+  const size_t slots = (size_t)slots_f + (size_t)slots_k;  // the dq and dk / dv items run together
   const size_t bytes = al(itf.size() * sizeof(MAttnItem)) + al(itk.size() * sizeof(MAttnItem)) +
                        al(mf.size() * sizeof(MAttnMerge)) + al(mk.size() * sizeof(MAttnMerge)) +
                        al(std::max<size_t>(slots, 1) * 32 * (size_t)c.head_dim * 4);
@@ -661,6 +662,7 @@ rtq_status ensure_attn_plan(rtq_model* m, int64_t t, const int32_t* seg) {
   m->mg_kv = (MAttnMerge*)p;
   p += al(mk.size() * sizeof(MAttnMerge));
   m->attn_part = (float*)p;
+  m->attn_part_kv = m->attn_part + (size_t)slots_f * 32 * (size_t)c.head_dim;
   M_HIP(hipMemcpy(m->it_fwd, itf.data(), itf.size() * sizeof(MAttnItem), hipMemcpyHostToDevice));
   M_HIP(hipMemcpy(m->it_kv, itk.data(), itk.size() * sizeof(MAttnItem), hipMemcpyHostToDevice));
   M_HIP(hipMemcpy(m->mg_fwd, mf.data(), mf.size() * sizeof(MAttnMerge), hipMemcpyHostToDevice));
@@ -706,12 +708,12 @@ rtq_status attn_launch(rtq_model* m, int km, MAttnArgs a, const MAttnItem* items
   a.n_items = n;
   return rtq_model_launch(m->ctx, km, dim3((unsigned)n), dim3(256), stream_of(m), &a);
 }
-// one thread per element of each merged block (16 x hd, or 2 x 16 x hd for dk and dv)
+// one thread per element of each merged block (16 x hd)
 rtq_status attn_merge(rtq_model* m, int km, MAttnArgs a, const MAttnMerge* mg, int n) {
   if (n <= 0) return RTQ_OK;
   a.merges = mg;
   a.n_merges = n;
-  const int64_t nel = (km == KM_ATTN_MERGE_DKV ? 32 : 16) * (int64_t)a.hd;
+  const int64_t nel = 16 * (int64_t)a.hd;
   return rtq_model_launch(m->ctx, km, dim3((unsigned)(n * ((nel + 255) / 256))), dim3(256), stream_of(m), &a);
 }
 
@@ -830,10 +832,20 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
     aa.dv = dv.v;
     aa.ld_dv = dv.ldv;
     M_TRY(rtq_model_launch(m->ctx, KM_ATTN_BWD_D, dim3((unsigned)((t * nh + 3) / 4)), dim3(256), stream_of(m), &aa));
-    M_TRY(attn_launch(m, hd == 64 ? KM_FA_DQ64 : KM_FA_DQ128, aa, m->it_fwd, m->n_fwd));
-    M_TRY(attn_merge(m, KM_ATTN_MERGE_DQ, aa, m->mg_fwd, m->n_mfwd));
-    M_TRY(attn_launch(m, hd == 64 ? KM_FA_DKV64 : KM_FA_DKV128, aa, m->it_kv, m->n_kv));
-    M_TRY(attn_merge(m, KM_ATTN_MERGE_DKV, aa, m->mg_kv, m->n_mkv));
+    aa.items = m->it_fwd;  // dq over key tiles, and dk, dv over (group head, query tile) pairs: one launch
+    aa.n_items = m->n_fwd;
+    aa.items2 = m->it_kv;
+    aa.n_items2 = m->n_kv;
+    aa.part2 = m->attn_part_kv;
+    M_TRY(rtq_model_launch(m->ctx, hd == 64 ? KM_FA_BWD64 : KM_FA_BWD128, dim3((unsigned)(m->n_fwd + m->n_kv)),
+                           dim3(256), stream_of(m), &aa));
+    aa.merges = m->mg_fwd;
+    aa.n_merges = m->n_mfwd;
+    aa.merges2 = m->mg_kv;
+    aa.n_merges2 = m->n_mkv;
+    const int64_t nmb = m->n_mkv * ((32 * hd + 255) / 256) + m->n_mfwd * ((16 * hd + 255) / 256);
+    if (nmb > 0)
+      M_TRY(rtq_model_launch(m->ctx, KM_ATTN_MERGE_BWD, dim3((unsigned)nmb), dim3(256), stream_of(m), &aa));
   } else {
   M_TRY(k_gemm(m, t, t, hd, nh, Op{m->d_o, hd, qd, 1, 1}, Op{k.v, hd, 1, kd, (int)grp}, m->dP, t * t, t, 1, 1.0f, 1,
                0, SPLIT_BF));  // dP = dO V^T
