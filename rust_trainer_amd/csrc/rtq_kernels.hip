@@ -1721,11 +1721,6 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
         for (int c = 0; c < 4; c++)
           S.dy[m][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rdy, mo + 4u * c, (uint32_t)ns * 4u, 0));
       }
-      if (ns + 32 > a.N) {  // ragged tail of N: columns >= N hold the next row's values
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-          if (ns + 4 * q4 + c >= a.N) S.dy[m][c] = 0.0f;
-      }
     }
 #pragma unroll
     for (int r = 0; r < 2; r++) S.q[r] = __builtin_amdgcn_raw_buffer_load_b32(rq, q_off[r], srg * q_rg, 0);
@@ -1736,14 +1731,24 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
       S.d = __builtin_amdgcn_raw_buffer_load_b32(rd, d_off, srg * d_rg, 0);
     }
   };
-  auto stage = [&](const DxSlot<FMT, NQ>& S, int buf) {
+  // The ragged tail of N (columns >= N of the last step hold the next row's values) is cleared here,
+  // where the step's loads are consumed: clearing the load destinations right after issuing them
+  // makes the compiler wait for every load in flight, the prefetched steps' included.
+  auto stage = [&](const DxSlot<FMT, NQ>& S, int buf, int step) {
+    const int nst = n0 + 32 * min(step, max(nsteps - 1, 0));
 #pragma unroll
     for (int m = 0; m < NQ; m++) {  // dy: A fragment tile (tl>>4) + 4m, lane (tl&15) + 16*(q4>>1), slots 4*(q4&1) ..
-      const float x0 = S.dy[m][0] * dsc[m], x1 = S.dy[m][1] * dsc[m], x2 = S.dy[m][2] * dsc[m], x3 = S.dy[m][3] * dsc[m];
+      f4 dv = S.dy[m];
+      if (nst + 32 > a.N) {
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          if (nst + 4 * q4 + c >= a.N) dv[c] = 0.0f;
+      }
+      const float x0 = dv[0] * dsc[m], x1 = dv[1] * dsc[m], x2 = dv[2] * dsc[m], x3 = dv[3] * dsc[m];
       const half2v h01 = pk_rtz(x0, x1), h23 = pk_rtz(x2, x3);
       // x - hi = dy 2^e - hi exactly (at most 13 significant bits): one mixed-precision FMA each
-      const half2v l01 = pk_rtz(fmaf(S.dy[m][0], dsc[m], -(float)h01.x), fmaf(S.dy[m][1], dsc[m], -(float)h01.y));
-      const half2v l23 = pk_rtz(fmaf(S.dy[m][2], dsc[m], -(float)h23.x), fmaf(S.dy[m][3], dsc[m], -(float)h23.y));
+      const half2v l01 = pk_rtz(fmaf(dv[0], dsc[m], -(float)h01.x), fmaf(dv[1], dsc[m], -(float)h01.y));
+      const half2v l23 = pk_rtz(fmaf(dv[2], dsc[m], -(float)h23.x), fmaf(dv[3], dsc[m], -(float)h23.y));
       const u2v hv = {__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)};
       const u2v lv = {__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)};
       const int fl = (tl & 15) + 16 * (q4 >> 1);
@@ -1832,7 +1837,7 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   // step s's MFMAs run under the staging's tail.  Loads run D - 1 steps ahead of the MFMAs.
 #pragma unroll
   for (int s0 = 0; s0 < D - 1; s0++) issue(sl[s0], s0);
-  if (nsteps > 0) stage(sl[0], 0);
+  if (nsteps > 0) stage(sl[0], 0, 0);
   // one step of the loop; `full`: a step of a complete group of D (no guards, one basic block, so
   // the scheduler can interleave the MFMAs with the staging arithmetic; staging past the last step
   // only writes the unused buffer)
@@ -1842,7 +1847,7 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
     __syncthreads();
     Frags F;
     if (full || step < nsteps) load_frags(step & 1, F);
-    if (full || step + 1 < nsteps) stage(sl[(s0 + 1) % D], (step + 1) & 1);
+    if (full || step + 1 < nsteps) stage(sl[(s0 + 1) % D], (step + 1) & 1, step + 1);
     if (full || step < nsteps) compute(F);
     if (full) {
 #pragma unroll
