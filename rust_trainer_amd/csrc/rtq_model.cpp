@@ -748,13 +748,19 @@ void gu_view(const rtq_model* m, const Layer& L, float* base, int64_t t, float**
   *ld = L.gu_fused ? 2 * ff : ff;
 }
 
-rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* y) {
+// add_in: x is not written yet: it is the previous block's output h + mlp (its h in its cache, mlp
+// in f), summed by this block's first norm kernel (which writes x); add_out: this block writes y,
+// else it leaves h (cache) and mlp (f) for the next block's first norm
+rtq_status block_forward(rtq_model* m, int l, int64_t t, float* x, float* y, bool add_in, bool add_out) {
   const rtq_model_config& c = m->cfg;
   const Layer& L = m->layers[(size_t)l];
   Cache& k = m->cache[m->ckpt ? 0 : (size_t)l];
   const int64_t d = c.n_embd, nh = c.n_head, nkv = c.n_head_kv, hd = c.head_dim, grp = nh / nkv;
   const int64_t qd = nh * hd, kd = nkv * hd;
-  M_TRY(k_norm(m, x, nullptr, nullptr, L.attn_norm, k.n1, k.inv1, t, d, 0));
+  if (add_in)  // x = h + mlp of block l - 1 (src/model.rs:196), n1 = rmsnorm(x)
+    M_TRY(k_norm(m, m->cache[m->ckpt ? 0 : (size_t)(l - 1)].h, m->f, x, L.attn_norm, k.n1, k.inv1, t, d, 0));
+  else
+    M_TRY(k_norm(m, x, nullptr, nullptr, L.attn_norm, k.n1, k.inv1, t, d, 0));
   const QkvView qv = qkv_view(m, L, k.qkv, t);
   if (L.qkv_fused) {
     M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LQ]], k.n1, t, k.qkv));
@@ -795,6 +801,7 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, const float* x, float* 
   }
   M_TRY(k_elt2(m, KM_SWIGLU, g, u, nullptr, k.hm, nullptr, t, c.n_ff, ldg, c.n_ff, c.n_ff));
   M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LDOWN]], k.hm, t, m->f));
+  if (!add_out) return RTQ_OK;
   return k_elt(m, KM_ADD, k.h, m->f, nullptr, y, nullptr, t * d);  // y = h + mlp
 }
 
@@ -1459,9 +1466,14 @@ rtq_status step(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* p
     if (weights) M_HIP(hipMemcpyAsync(m->wts_d, weights, (size_t)n * 4, hipMemcpyHostToDevice, st));
   }
   M_TRY(rtq_frozen_gather_d(m->ctx, m->embed, m->tok_d, t, m->X, st));  // embed_tokens
+  bool pending = false;  // block l's output sum left to block l + 1's first norm
   for (int64_t l = 0; l < c.n_layer; l++) {
     float *x = m->X + l * t * d, *y = m->X + (l + 1) * t * d;
-    M_TRY(block_forward(m, (int)l, t, x, y));
+    // the residual sum of a block's output is formed by the next block's first norm, except where
+    // the output itself is read next (the last block: the LM head; a captured block)
+    const bool out = l == c.n_layer - 1 || l == m->dbg_layer;
+    M_TRY(block_forward(m, (int)l, t, x, y, pending, out));
+    pending = !out;
     if (l == m->dbg_layer) M_TRY(dbg_forward(m, (int)l, t, x, y));
   }
   if (n > 0) {
@@ -1471,7 +1483,7 @@ rtq_status step(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* p
     if (weights)
       for (int64_t l = c.n_layer - 1; l >= 0; l--) {
         const float* x = m->X + l * t * d;
-        if (m->ckpt) M_TRY(block_forward(m, (int)l, t, x, m->f));  // recompute (output unused: f is scratch)
+        if (m->ckpt) M_TRY(block_forward(m, (int)l, t, const_cast<float*>(x), m->f, false, false));  // recompute
         M_TRY(block_backward(m, (int)l, t, x, m->dY, m->dX));
         if (l == m->dbg_layer) M_TRY(dbg_backward(m, (int)l, t, m->dY, m->dX));
         std::swap(m->dY, m->dX);
