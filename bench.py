@@ -813,12 +813,12 @@ def step_layer_calls(cfg: dict, t: int) -> list[tuple[int, int, int]]:
 
 def step_calls_for(name: str, cfg: dict):
     """(calls, backward) of the block linears a kernel serves in the step, by the runtime's choice at
-    T = 512: rtq_mm64_* the wide fused forwards (q | k | v, gate | up), rtq_fwd_*_w8 the others (o,
+    T = 512: rtq_mm32_* the wide fused forwards (q | k | v, gate | up), rtq_fwd_*_w8 the others (o,
     down), rtq_dx_* every input gradient."""
     qkv, o, gu, down = step_layer_calls(cfg, STEP_T)
     if name.startswith("rtq_dx_"):
         return [qkv, o, gu, down], True
-    if name.startswith("rtq_mm64_"):
+    if name.startswith("rtq_mm32_"):
         return [qkv, gu], False
     if name.startswith("rtq_fwd_"):
         return [o, down], False

@@ -36,6 +36,9 @@
 #define RTQ_CHUNK_Q 128   // K chunk of Q4_0 / Q8_0
 #define RTQ_ACT_KQ 256    // columns per activation-prep workgroup (one LoRA-down partial each)
 #define RTQ_LDS_RANK 64   // LoRA ranks up to this are staged in LDS by the forward kernels
+#define RTQ_MM_RING 3     // rtq_mm_* (128 x 128 tiles): stages of the operand ring in LDS
+#define RTQ_MM64_RING 3   // rtq_mm64_* (128 x 64 tiles)
+#define RTQ_MM32_RING 3   // rtq_mm32_* (128 x 32 tiles)
 
 // index of the row-major scale (K-quants: sub-block scale word) of row li of row group rg, block j
 // of chunk kc

@@ -962,16 +962,19 @@ RTQ_FWD(rtq_fwd_q6_k_w_isums, FMT_Q6_K, 4, 2, 2, true)
 RTQ_FWD(rtq_fwd_q6_k_s_isums, FMT_Q6_K, 1, 4, 4, true)
 
 // ============================================================== forward GEMM, large grids (Q4_0 / Q8_0)
-// For outputs of at least a workgroup per CU in 128 x 128 tiles (128 x 64: rtq_mm64_*).  Workgroup
-// = 4 waves, tile 128 weight rows (8 row groups) x 16 TTN tokens (TTN = 8 or 4 token tiles); wave w
-// computes row groups 2w, 2w+1 x all TTN token tiles: a weight fragment is unpacked once per TTN
-// token tiles, the
-// activation fragments are shared by the four waves through LDS.  Per half chunk (64 columns,
-// two blocks) the workgroup's operands - weight codes and scales, activation codes and scales -
-// are copied global -> LDS by buffer loads with an LDS destination (no VGPR staging) into a
-// 3-stage ring: while stage s is computed, the loads of stages s + 1 and s + 2 are in flight.  One
-// barrier per stage; the wait before it names the loads of stage s only (the raw s_barrier keeps
-// the compiler from draining every load there).  The 1D grid deals the tiles, ordered token block
+// For outputs of at least a workgroup per CU in 128 x 128 tiles (128 x 64: rtq_mm64_*, 128 x 32:
+// rtq_mm32_*).  Workgroup = 4 waves, tile 128 weight rows (8 row groups) x 16 TTN tokens (TTN = 8,
+// 4 or 2 token tiles); wave w computes row groups 2w, 2w+1 x all TTN token tiles: a weight
+// fragment is unpacked once per TTN token tiles, the activation fragments are shared by the four
+// waves through LDS.  Per half chunk (64 columns, two blocks) the workgroup's operands - weight
+// codes and scales, activation codes and scales - are copied global -> LDS by buffer loads with an
+// LDS destination (no VGPR staging) into a RING-stage ring: while stage s is computed, the loads
+// of stages s + 1 .. s + RING - 2 are in flight.  One barrier per stage; the wait before it names
+// the loads of stage s only (the raw s_barrier keeps the compiler from draining every load there).
+// The kernel is bound by issue and latency more than by either pipe (128 x 64 tiles at the
+// Qwen3-0.6B q|k|v shape, 512 tokens: one workgroup per CU, VALU busy ~25 %, MFMA ~10 %): 32-token tiles, at
+// two or three workgroups per CU, beat them there, while a deeper ring (6) and eight waves per
+// workgroup did not.  The 1D grid deals the tiles, ordered token block
 // by token block, to the eight XCDs in contiguous ranges: the workgroups running on one XCD share
 // one token block's activations in that XCD's L2 while they stream weight rows.  Arithmetic as
 // fwd_tile: exact integer block sums from the f16 MFMA, acc += isum * (d_w * d_x), with the scale
@@ -984,15 +987,31 @@ struct MmStage {  // one half chunk in LDS, in 16-byte units; TTN token tiles of
   static constexpr int WQ = TTN * 2 * 64;                            // [rg 8][lane 64] Q4_0 8 B, Q8_0 16 B
   static constexpr int WD = WQ + (FMT == FMT_Q4_0 ? 8 * 64 / 2 : 8 * 64);  // [rg 8][row 16] fp16 scale pairs
   static constexpr int XD = WD + 8 * 4;                              // [t 16 TTN] fp16 activation scale pairs
-  static constexpr int SIZE = XD + 16 * TTN / 4;
+  static constexpr int NXD = TTN >= 4 ? TTN / 4 : 1;                 // loads of activation scales (64 tokens each)
+  static constexpr int SIZE = XD + 16 * NXD;                         // (TTN 2: the load's last 32 tokens unused)
   static constexpr int NX = 2 * TTN;                                 // loads of activation fragments
   static constexpr int NWQ = FMT == FMT_Q4_0 ? 16 : 8;               // loads of weight codes
-  static constexpr int NXD = TTN / 4;                                // loads of activation scales
   static constexpr int LOADS = NX + NWQ + 2 + NXD;                   // wave-wide loads per stage
-  static constexpr int RING = 3;
 };
 
-template <int FMT, int TTN>
+// s_waitcnt immediate: vmcnt <= n (0..63; low four bits, then bits 15:14), expcnt and lgkmcnt free
+constexpr int vm_wait_imm(int n) { return 0x0F70 | (n & 15) | (((n >> 4) & 3) << 14); }
+
+// wait until at most after * L vector-memory loads of this wave are outstanding (after: 0 .. 6)
+template <int L>
+__device__ __forceinline__ void vm_wait_stages(int after) {
+  switch (after) {
+    case 0: __builtin_amdgcn_s_waitcnt(vm_wait_imm(0)); break;
+    case 1: __builtin_amdgcn_s_waitcnt(vm_wait_imm(L)); break;
+    case 2: __builtin_amdgcn_s_waitcnt(vm_wait_imm(2 * L)); break;
+    case 3: __builtin_amdgcn_s_waitcnt(vm_wait_imm(3 * L)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(vm_wait_imm(4 * L)); break;
+    case 5: __builtin_amdgcn_s_waitcnt(vm_wait_imm(5 * L)); break;
+    default: __builtin_amdgcn_s_waitcnt(vm_wait_imm(6 * L)); break;
+  }
+}
+
+template <int FMT, int TTN, int RING>
 __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
   using St = MmStage<FMT, TTN>;
   extern __shared__ u4v mm_lds[];
@@ -1149,24 +1168,24 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
     }
   };
 
-  // 3-stage ring over half chunks; each wave issues at least MINL loads per stage, so "at most
-  // that many outstanding" at the top of step s means stage s has landed.  The loop is unrolled by
+  // RING-stage ring over half chunks: stages s + 1 .. s + RING - 2 are in flight while stage s is
+  // computed.  Each wave issues at least MINL loads per stage, so "at most MINL x (stages issued
+  // after s) outstanding" at the top of step s means stage s has landed.  The loop is unrolled by
   // the ring size so that every stage's LDS offsets are immediates.
+  static_assert(RING >= 3 && (RING - 2) * (KX + KW + 2) <= 63, "ring depth within the load counter");
   constexpr int MINL = KX + KW + (St::NXD >= 2 ? 1 : 0);
-  issue(0, 0);
-  if (nhc > 1) issue(1, 1);
-  for (int hc0 = 0; hc0 < nhc; hc0 += St::RING) {
 #pragma unroll
-    for (int u = 0; u < St::RING; u++) {
+  for (int s = 0; s < RING - 1; s++)
+    if (s < nhc) issue(s, s);
+  for (int hc0 = 0; hc0 < nhc; hc0 += RING) {
+#pragma unroll
+    for (int u = 0; u < RING; u++) {
       const int hc = hc0 + u;
       if (hc < nhc) {
-        if (hc + 1 < nhc)
-          __builtin_amdgcn_s_waitcnt(0x0F70 | MINL);  // vmcnt <= loads of stage s + 1
-        else
-          __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        vm_wait_stages<MINL>(min(RING - 2, nhc - 1 - hc));
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (hc + 2 < nhc) issue((u + 2) % St::RING, hc + 2);
+        if (hc + RING - 1 < nhc) issue((u + RING - 1) % RING, hc + RING - 1);
         compute(u);
       }
     }
@@ -1177,7 +1196,7 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
   // the tile's rank span are staged in LDS over the ring, RTQ_LDS_RANK ranks at a time.
   const bool lora = a.hp != nullptr;
   float(*sh)[RTQ_LDS_RANK + 1] = reinterpret_cast<float(*)[RTQ_LDS_RANK + 1]>(mm_lds);
-  float(*sb)[RTQ_LDS_RANK + 1] = sh + 128;
+  float(*sb)[RTQ_LDS_RANK + 1] = sh + 16 * TTN;
   int span0 = 0, span1 = 0;  // ranks read by the tile's rows (workgroup-uniform)
   int win0[2] = {0, 0}, win1[2] = {0, 0};  // ranks read by row group 2w + r (wave-uniform)
   if (lora) {
@@ -1256,11 +1275,14 @@ __device__ __forceinline__ void mm_tile(const FwdArgs& a) {
   }
 }
 
-extern "C" __global__ __launch_bounds__(256) void rtq_mm_q4_0(FwdArgs a) { mm_tile<FMT_Q4_0, 8>(a); }
-extern "C" __global__ __launch_bounds__(256) void rtq_mm_q8_0(FwdArgs a) { mm_tile<FMT_Q8_0, 8>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_mm_q4_0(FwdArgs a) { mm_tile<FMT_Q4_0, 8, RTQ_MM_RING>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_mm_q8_0(FwdArgs a) { mm_tile<FMT_Q8_0, 8, RTQ_MM_RING>(a); }
 // 128 rows x 64 tokens: twice the grid, for outputs whose 128 x 128 tiles would leave CUs idle
-extern "C" __global__ __launch_bounds__(256) void rtq_mm64_q4_0(FwdArgs a) { mm_tile<FMT_Q4_0, 4>(a); }
-extern "C" __global__ __launch_bounds__(256) void rtq_mm64_q8_0(FwdArgs a) { mm_tile<FMT_Q8_0, 4>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_mm64_q4_0(FwdArgs a) { mm_tile<FMT_Q4_0, 4, RTQ_MM64_RING>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_mm64_q8_0(FwdArgs a) { mm_tile<FMT_Q8_0, 4, RTQ_MM64_RING>(a); }
+// 128 rows x 32 tokens: two or more workgroups per CU where 128 x 64 tiles give about one
+extern "C" __global__ __launch_bounds__(256) void rtq_mm32_q4_0(FwdArgs a) { mm_tile<FMT_Q4_0, 2, RTQ_MM32_RING>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_mm32_q8_0(FwdArgs a) { mm_tile<FMT_Q8_0, 2, RTQ_MM32_RING>(a); }
 
 // ============================================================== forward GEMV (T <= 16)
 // MFMA orientation transposed against fwd_tile: A operand = the 16 token slots x 32 columns of the

@@ -126,6 +126,8 @@ enum Kid {
   K_MM_Q8_0,
   K_MM64_Q4_0,   // the same with 128 x 64 tiles
   K_MM64_Q8_0,
+  K_MM32_Q4_0,   // the same with 128 x 32 tiles
+  K_MM32_Q8_0,
   K_BWD_PREP,
   K_DX,          // + format
   K_DX16 = K_DX + F_COUNT,  // + format: t <= 16
@@ -154,7 +156,7 @@ constexpr const char* kKernelNames[] = {
     "rtq_gemv_q4_0",        "rtq_gemv_q8_0",        "rtq_gemv_q4_k",        "rtq_gemv_q6_k",
     "rtq_fwd_q4_0_w8",      "rtq_fwd_q8_0_w8",      "rtq_fwd_q4_0_w8r2",    "rtq_fwd_q8_0_w8r2",
     "rtq_mm_q4_0",          "rtq_mm_q8_0",
-    "rtq_mm64_q4_0",        "rtq_mm64_q8_0",
+    "rtq_mm64_q4_0",        "rtq_mm64_q8_0",        "rtq_mm32_q4_0",        "rtq_mm32_q8_0",
     "rtq_bwd_prep",
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
@@ -199,8 +201,9 @@ struct rtq_ctx {
   int dx_wide = -1;   // 256-token dx tiles: -1 automatic, 0 never, 1 for every t > 16 (RTQ_DX_WIDE)
   int fwd_waves = 8;  // waves splitting K in the wide Q4_0 / Q8_0 forward (RTQ_FWD_WAVES: 4 or 8)
   int fwd_rg = -1;    // row groups of 16 per eight-wave forward tile: -1 automatic, 2 or 3 (RTQ_FWD_RG)
-  int fwd_mm = -1;    // large-grid forward: -1 automatic, 0 never, 1 / 2 the 128- / 64-token tiles whenever
-                      // the format allows (RTQ_FWD_MM)
+  int g64_min = -1;   // fewest 64-token g-partial workgroups (else 16-token ones): -1 = CUs / 2 (RTQ_G64_MIN)
+  int fwd_mm = -1;    // large-grid forward: -1 automatic, 0 never, 1 / 2 / 3 the 128- / 64- / 32-token tiles
+                      // whenever the format allows (RTQ_FWD_MM)
   int64_t t_launches[K_COUNT] = {};
   double t_ms[K_COUNT] = {};
   double t_flops[K_COUNT] = {}, t_bytes[K_COUNT] = {};
@@ -347,10 +350,10 @@ constexpr int kFwdWideTT = 4;     // rtq_fwd_*_w: 64 tokens x (16 * wide_rg) row
 constexpr int kMmTile = 128;      // rtq_mm_*: 128 rows x 128 tokens per workgroup
 // rtq_mm_* dynamic LDS: a 3-stage ring of half-chunk operands (codes, scales), reused after the
 // K loop for the LoRA h and B rows of the tile (128 rows each, RTQ_LDS_RANK + 1 floats)
-unsigned mm_lds_bytes(int type, int ttn) {  // ttn: token tiles of 16 per workgroup (8 or 4)
+unsigned mm_lds_bytes(int type, int ttn, int ring) {  // ttn: token tiles of 16 per workgroup (8, 4 or 2)
   const unsigned stage =
-      16u * (ttn * 2 * 64 + (type == RTQ_TYPE_Q4_0 ? 8 * 64 / 2 : 8 * 64) + 8 * 4 + 16 * ttn / 4);
-  return std::max(3 * stage, 2u * 128u * (RTQ_LDS_RANK + 1) * 4u);
+      16u * (ttn * 2 * 64 + (type == RTQ_TYPE_Q4_0 ? 8 * 64 / 2 : 8 * 64) + 8 * 4 + 16 * std::max(ttn / 4, 1));
+  return std::max((unsigned)ring * stage, (16u * ttn + 128u) * (RTQ_LDS_RANK + 1) * 4u);
 }
 constexpr int kFwdSkinnyRG = 4;   // rtq_fwd_*_s: 16 tokens x 64 rows per workgroup
 int wide_rg(int type) { return is_kquant(type) ? 2 : 3; }
@@ -552,15 +555,19 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   // the large-grid kernel once its 128 x 128 tiles alone give a workgroup per CU, else its
   // 128 x 64 tiles if those do
   const int64_t mm_rows = cdiv(w->Np / 16, 8);
-  const int64_t mm128 = mm_rows * (p.Tp / kMmTile), mm64 = mm_rows * (p.Tp / 64);
+  const int64_t mm128 = mm_rows * (p.Tp / kMmTile), mm64 = mm_rows * (p.Tp / 64), mm32 = mm_rows * (p.Tp / 32);
   int mm_ttn = 0;  // token tiles per workgroup of the chosen rtq_mm kernel, 0: none
   if (!p.skinny && !isums && !is_kquant(w->type)) {
     if (c->fwd_mm == 1) mm_ttn = 8;
     else if (c->fwd_mm == 2) mm_ttn = 4;
-    else if (c->fwd_mm < 0) mm_ttn = mm128 >= c->cu_count ? 8 : (mm64 >= c->cu_count ? 4 : 0);
+    else if (c->fwd_mm == 3) mm_ttn = 2;
+    // automatic: 128-token tiles when they give every CU a workgroup; else 32-token tiles when 64-token
+    // ones would (two or more workgroups per CU hide the K loop's latencies better than one: 1.15
+    // against 1.27 ms per Qwen3-0.6B-shaped 512-token step over its q|k|v and gate|up products)
+    else if (c->fwd_mm < 0) mm_ttn = mm128 >= c->cu_count ? 8 : (mm64 >= c->cu_count ? 2 : 0);
   }
   const bool mm = mm_ttn > 0;
-  const int64_t mm_tiles = mm_ttn == 8 ? mm128 : mm64;
+  const int64_t mm_tiles = mm_ttn == 8 ? mm128 : mm_ttn == 4 ? mm64 : mm32;
   const int64_t tiles = gx * gy;
   // split K across workgroups when the output alone gives too few of them (atomics into a
   // zeroed y); every split keeps at least one half chunk per wave (K-quants: one super-block of
@@ -606,9 +613,11 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   if (mm && (!fa.wq || !fa.wdr || !fa.xq || !fa.xdh || !fa.y))
     return fail(RTQ_ERR_INVALID, "internal: rtq_mm_* operand missing");
   set_work(c, w, t, lora ? r : 0, false);
-  if (mm)
-    return launch(c, (mm_ttn == 8 ? K_MM_Q4_0 : K_MM64_Q4_0) + (w->type == RTQ_TYPE_Q4_0 ? 0 : 1),
-                  dim3((unsigned)mm_tiles), dim3(256), st, fa, mm_lds_bytes(w->type, mm_ttn));
+  if (mm) {
+    const int ring = mm_ttn == 8 ? RTQ_MM_RING : mm_ttn == 4 ? RTQ_MM64_RING : RTQ_MM32_RING;
+    return launch(c, (mm_ttn == 8 ? K_MM_Q4_0 : mm_ttn == 4 ? K_MM64_Q4_0 : K_MM32_Q4_0) + (w->type == RTQ_TYPE_Q4_0 ? 0 : 1),
+                  dim3((unsigned)mm_tiles), dim3(256), st, fa, mm_lds_bytes(w->type, mm_ttn, ring));
+  }
   int kid = (p.skinny ? (isums ? K_FWD_S_ISUMS : K_FWD_S) : (isums ? K_FWD_W_ISUMS : K_FWD_W)) + fmt_index(w->type);
   int threads = 256;
   if (w8) {
@@ -713,14 +722,14 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   if (lora) {
     // h partials: 16 tokens per workgroup; g partials: 64, or 16 where 64-token workgroups would
     // leave more than half of the CUs without one
-    const int gtok = cdiv(t, 64) * ngq * 2 >= c->cu_count ? 64 : 16;
+    const int gtok = cdiv(t, 64) * ngq >= (c->g64_min >= 0 ? c->g64_min : c->cu_count / 2) ? 64 : 16;
     BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq, dymax, RankBlocks{},
                    have_h ? (int)nhq : 0, gtok};
     if (rb) pa.rb = *rb;
     RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, have_h ? gtok : 16), (unsigned)(have_h ? ngq : nhq + ngq)),
                    dim3(256), st, pa));
   } else if (dymax) {
-    const int gtok = cdiv(t, 64) * ngq * 2 >= c->cu_count ? 64 : 16;
+    const int gtok = cdiv(t, 64) * ngq >= (c->g64_min >= 0 ? c->g64_min : c->cu_count / 2) ? 64 : 16;
     BwdPrepArgs pa{nullptr, nullptr, K, dy, nullptr, N, (int)t, 0, nullptr, 0, nullptr, (int)ngq, dymax, RankBlocks{},
                    0, gtok};
     RTQ_TRY(launch(c, K_BWD_PREP, dim3((unsigned)cdiv(t, gtok), (unsigned)ngq), dim3(256), st, pa));
@@ -936,8 +945,9 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   if (const char* e = getenv("RTQ_DX_SPLITS")) c->dx_splits = atoi(e);
   if (const char* e = getenv("RTQ_DX_WIDE")) c->dx_wide = atoi(e) ? 1 : 0;
   if (const char* e = getenv("RTQ_FWD_WAVES")) c->fwd_waves = atoi(e) == 4 ? 4 : 8;
-  if (const char* e = getenv("RTQ_FWD_MM")) c->fwd_mm = std::min(std::max(atoi(e), 0), 2);
+  if (const char* e = getenv("RTQ_FWD_MM")) c->fwd_mm = std::min(std::max(atoi(e), 0), 3);
   if (const char* e = getenv("RTQ_FWD_RG")) c->fwd_rg = atoi(e) == 2 ? 2 : 3;
+  if (const char* e = getenv("RTQ_G64_MIN")) c->g64_min = atoi(e);
   hipError_t e = hipModuleLoadData(&c->mod, rtq_hsaco_begin);
   if (e != hipSuccess) {
     delete c;

@@ -336,11 +336,11 @@ def test_config1_lm_head_matches_oracle(ctx, wtype, t):
 
 
 # ---------------------------------------------------------------- large-grid forward (rtq_mm_*)
-@pytest.fixture(scope="module", params=["1", "2"], ids=["mm128", "mm64"])
+@pytest.fixture(scope="module", params=["1", "2", "3"], ids=["mm128", "mm64", "mm32"])
 def ctx_mm(request):
     """A context that sends every wide Q4_0 / Q8_0 forward through the 128 x 128-tile kernel
-    (RTQ_FWD_MM=1) or its 128 x 64-tile variant (RTQ_FWD_MM=2), so small shapes cover their
-    padding and epilogue cases."""
+    (RTQ_FWD_MM=1) or its 128 x 64- or 128 x 32-tile variant (RTQ_FWD_MM=2, 3), so small shapes
+    cover their padding and epilogue cases."""
     import os
 
     old = os.environ.get("RTQ_FWD_MM")
@@ -388,9 +388,10 @@ def test_forward_mm_selected_by_grid_size(ctx, wtype):
 
 @pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
 @pytest.mark.parametrize("r", [0, 48])
-def test_forward_mm64_selected_by_grid_size(ctx, wtype, r):
+def test_forward_mm32_selected_by_grid_size(ctx, wtype, r):
     # the fused q|k|v shape of the configs[2] step: 4096 rows x 512 tokens is 128 tiles of 128 x
-    # 128 (half the CUs) but 256 of 128 x 64, so the default context picks rtq_mm64_*
+    # 128 (half the CUs) but 256 of 128 x 64, so the default context picks the 128 x 32 tiles
+    # (rtq_mm32_*, two workgroups per CU)
     n, k, t = 4096, 1024, 512
     blocks, x, _ = make(wtype, n, k, t)
     lin = rt.Linear("blk.0.attn_qkv", hip(ctx, wtype, blocks, n, k))
@@ -404,7 +405,7 @@ def test_forward_mm64_selected_by_grid_size(ctx, wtype, r):
     y = lin.forward(x, t)
     ran = ctx.timing()
     ctx.set_timing(False)
-    assert any(name.startswith("rtq_mm64_") for name in ran), ran
+    assert any(name.startswith("rtq_mm32_") for name in ran), ran
     want = O.linear_forward(wtype, blocks, n, k, x, nthreads=16, **kw)
     assert rel_err(y, want) <= TOL
 
