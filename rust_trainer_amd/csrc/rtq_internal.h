@@ -55,6 +55,12 @@ int64_t rtq_lora_partial_floats(const rtq_weight* w, int64_t t, int64_t r);
 rtq_status rtq_linear_forward_keep_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
                                      const RankBlocks* rb, const float* x, int64_t t, float* y, float* hp_keep,
                                      void* stream);
+// rtq_linear_forward_keep_d of x = silu(g) * u (SwiGLU, src/model.rs:124; g and u rows of stride
+// ldg floats, 16-byte aligned): the activation kernel forms x and writes it to x_out [t x cols] for
+// the backward.  Quantised weights only (a dense one: RTQ_ERR_UNSUPPORTED, the caller forms x).
+rtq_status rtq_linear_forward_swiglu_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
+                                       const RankBlocks* rb, const float* g, const float* u, int64_t ldg,
+                                       float* x_out, int64_t t, float* y, float* hp_keep, void* stream);
 // rtq_linear_backward_d for a block-diagonal adapter over row-concatenated weights (rb; null: a
 // plain adapter): gb and g = s dy.B only inside rb's blocks (gb outside them is left untouched).
 // Quantised weights only; a dense weight computes every pair (the caller clears gb outside the

@@ -75,6 +75,11 @@ struct ActArgs {
   float* zero_y;
   int N;
   uint16_t* xdh;  // or null: the fp16 bits of xd, same layout (rtq_mm_*'s scale MFMA operand)
+  // or null: the activation is SwiGLU's silu(sg) * su (src/model.rs:124, rows of stride ldsg),
+  // computed here and written to x (then an output) for the backward
+  const float* sg;
+  const float* su;
+  int ldsg;
 };
 
 // ---------------------------------------------------------------- trainer-native weights

@@ -444,6 +444,10 @@ __device__ __forceinline__ float sum_slices(const float* p, int64_t e, int np, i
   return s;
 }
 
+// SiLU of the training step's MLP, x / (1 + e^-x) (src/tensor.rs:123-143; the decoder block's
+// kernels use the same function)
+__device__ __forceinline__ float rtq_silu(float x) { return __fdiv_rn(x, 1.0f + expf(-x)); }
+
 template <bool QK>
 __device__ __forceinline__ void act_prep(const ActArgs& a) {
   constexpr int KQ = RTQ_ACT_KQ, LDX = KQ + 1;
@@ -457,7 +461,20 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
   {
     const int kk = k0 + sg * 16;  // first column of this thread's segment
     float v[16];
-    load_seg(a.x + (int64_t)t * a.K + kk, t < a.T && kk < a.K, v);  // K % 32 == 0: all in or all out
+    if (a.sg) {  // uniform: v = silu(g) * u, written to x for the LoRA partial below and the backward
+      float gv[16], uv[16];
+      load_seg(a.sg + (int64_t)t * a.ldsg + kk, t < a.T && kk < a.K, gv);
+      load_seg(a.su + (int64_t)t * a.ldsg + kk, t < a.T && kk < a.K, uv);
+#pragma unroll
+      for (int i = 0; i < 16; i++) v[i] = rtq_silu(gv[i]) * uv[i];
+      if (t < a.T && kk < a.K) {
+        f4* xo = reinterpret_cast<f4*>(const_cast<float*>(a.x) + (int64_t)t * a.K + kk);
+#pragma unroll
+        for (int i = 0; i < 4; i++) xo[i] = f4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+      }
+    } else {
+      load_seg(a.x + (int64_t)t * a.K + kk, t < a.T && kk < a.K, v);  // K % 32 == 0: all in or all out
+    }
     _Float16 q[16];  // codes: exact small integers
     float dstore;    // the block scale as the dot products use it
     if (!QK) {

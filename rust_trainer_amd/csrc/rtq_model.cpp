@@ -320,6 +320,24 @@ rtq_status lin_fwd(rtq_model* m, const Group& l, const float* x, int64_t t, floa
                                    stream_of(m));
 }
 
+// the down projection of SwiGLU's hm = silu(g) * u (src/model.rs:124-125): quantised weights form hm
+// in their activation kernel (one launch less); dense ones, or operands off 16-byte alignment, run
+// the elementwise kernel first.  hm is written either way (the backward reads it).
+rtq_status lin_fwd_swiglu(rtq_model* m, const Group& l, const float* g, const float* u, int64_t ldg, float* hm,
+                          int64_t t, float* y) {
+  const int64_t ff = m->cfg.n_ff;
+  const int wt = rtq_weight_type(l.w);
+  const bool aligned = ldg % 4 == 0 && ((uintptr_t)g | (uintptr_t)u | (uintptr_t)hm) % 16 == 0;
+  if (wt != RTQ_TYPE_F32 && wt != RTQ_TYPE_TQ8_0 && aligned) {
+    const rtq_lora lv = lora_view(l);
+    const RankBlocks rb = rank_blocks(l);
+    return rtq_linear_forward_swiglu_d(m->ctx, l.w, l.bias, l.rank > 0 ? &lv : nullptr, &rb, g, u, ldg, hm, t, y,
+                                       l.hpk, stream_of(m));
+  }
+  M_TRY(k_elt2(m, KM_SWIGLU, g, u, nullptr, hm, nullptr, t, ff, ldg, ff, ff));
+  return lin_fwd(m, l, hm, t, y);
+}
+
 // a fused group's adapter is block-diagonal (each member's rows see only its own ranks): the
 // quantised backward computes gb and g = s dy.B inside the blocks only; the dense (f32 GEMM) one
 // computes every pair and the off-block gb entries are cleared after it.  jobs (or null): a
@@ -799,8 +817,7 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, float* x, float* y, boo
     M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LGATE]], k.n2, t, g));
     M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LUP]], k.n2, t, u));
   }
-  M_TRY(k_elt2(m, KM_SWIGLU, g, u, nullptr, k.hm, nullptr, t, c.n_ff, ldg, c.n_ff, c.n_ff));
-  M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LDOWN]], k.hm, t, m->f));
+  M_TRY(lin_fwd_swiglu(m, L.groups[(size_t)L.gi[LDOWN]], g, u, ldg, k.hm, t, m->f));
   if (!add_out) return RTQ_OK;
   return k_elt(m, KM_ADD, k.h, m->f, nullptr, y, nullptr, t * d);  // y = h + mlp
 }

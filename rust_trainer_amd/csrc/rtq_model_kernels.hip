@@ -28,7 +28,7 @@ __device__ __forceinline__ float m_sigmoid(float x) {
   const float e = expf(x);
   return __fdiv_rn(e, 1.0f + e);
 }
-__device__ __forceinline__ float m_silu(float x) { return __fdiv_rn(x, 1.0f + expf(-x)); }
+__device__ __forceinline__ float m_silu(float x) { return rtq_silu(x); }
 __device__ __forceinline__ float m_silu_grad(float x) {
   const float s = m_sigmoid(x);
   return s * (1.0f + x * (1.0f - s));
@@ -41,15 +41,22 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // ------------------------------------------------------------------ RMSNorm
+// One workgroup of 256 threads per row; thread i takes columns i, i + 256, ...
+// The backward holds rows up to 256 NPT columns in registers, so that all of its loads are issued
+// up front (one memory round trip before the row sum; 401 -> 331 us per Qwen3-0.6B-shaped
+// 512-token step); longer rows stream twice.  (The same in the forward measured slower: 342 -> 382.)
+constexpr int RTQ_NORM_NPT = 16;
+
 // grid rows, 256 threads: y = rmsnorm(a (+ b)); with b, h = a + b is written too
 extern "C" __global__ __launch_bounds__(256) void rtq_m_rmsnorm(MNormArgs a) {
   __shared__ float red[4];
-  const int r = blockIdx.x;
+  const int r = blockIdx.x, tid = threadIdx.x;
   const float* ar = a.a + (int64_t)r * a.d;
   const float* br = a.b ? a.b + (int64_t)r * a.d : nullptr;
   float* hr = a.b ? a.h + (int64_t)r * a.d : nullptr;
+  float* yr = a.y + (int64_t)r * a.d;
   float s = 0.0f;
-  for (int k = threadIdx.x; k < a.d; k += 256) {
+  for (int k = tid; k < a.d; k += 256) {
     float x = ar[k];
     if (br) {
       x = x + br[k];
@@ -60,28 +67,51 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_rmsnorm(MNormArgs a) {
   s = block_sum256(s, red);
   const float ir = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(s, (float)a.d) + a.eps));
   const float* xr = br ? hr : ar;
-  float* yr = a.y + (int64_t)r * a.d;
-  for (int k = threadIdx.x; k < a.d; k += 256) {
+  for (int k = tid; k < a.d; k += 256) {
     const float x = xr[k], wo = a.w[k] + a.off;
     yr[k] = a.fused ? x * (ir * wo) : (x * ir) * wo;
   }
-  if (threadIdx.x == 0) a.inv[r] = ir;
+  if (tid == 0) a.inv[r] = ir;
 }
 
 // grid rows, 256 threads: out = (res +) rmsnorm_backward(x, w, inv, dy)
 extern "C" __global__ __launch_bounds__(256) void rtq_m_rmsnorm_bwd(MNormBwdArgs a) {
   __shared__ float red[4];
-  const int r = blockIdx.x;
+  const int r = blockIdx.x, tid = threadIdx.x;
   const float* xr = a.x + (int64_t)r * a.d;
   const float* dr = a.dy + (int64_t)r * a.d;
-  float s = 0.0f;
-  for (int k = threadIdx.x; k < a.d; k += 256) s = s + (dr[k] * (a.w[k] + a.off)) * xr[k];
-  s = block_sum256(s, red);
-  const float ir = a.inv[r];
-  const float c = __fdiv_rn(((s * ir) * ir) * ir, (float)a.d);
   float* o = a.out + (int64_t)r * a.d;
   const float* rr = a.res ? a.res + (int64_t)r * a.d : nullptr;
-  for (int k = threadIdx.x; k < a.d; k += 256) {
+  const float ir = a.inv[r];
+  if (a.d <= 256 * RTQ_NORM_NPT) {
+    float gv[RTQ_NORM_NPT], xv[RTQ_NORM_NPT], rv[RTQ_NORM_NPT];
+#pragma unroll
+    for (int i = 0; i < RTQ_NORM_NPT; i++) {
+      const int k = tid + 256 * i;
+      const bool in = k < a.d;
+      xv[i] = in ? xr[k] : 0.0f;
+      gv[i] = in ? dr[k] * (a.w[k] + a.off) : 0.0f;
+      rv[i] = in && rr ? rr[k] : 0.0f;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RTQ_NORM_NPT; i++)
+      if (tid + 256 * i < a.d) s = s + gv[i] * xv[i];
+    s = block_sum256(s, red);
+    const float c = __fdiv_rn(((s * ir) * ir) * ir, (float)a.d);
+#pragma unroll
+    for (int i = 0; i < RTQ_NORM_NPT; i++) {
+      const int k = tid + 256 * i;
+      const float v = gv[i] * ir - xv[i] * c;
+      if (k < a.d) o[k] = rr ? rv[i] + v : v;
+    }
+    return;
+  }
+  float s = 0.0f;
+  for (int k = tid; k < a.d; k += 256) s = s + (dr[k] * (a.w[k] + a.off)) * xr[k];
+  s = block_sum256(s, red);
+  const float c = __fdiv_rn(((s * ir) * ir) * ir, (float)a.d);
+  for (int k = tid; k < a.d; k += 256) {
     const float g = dr[k] * (a.w[k] + a.off);
     const float v = g * ir - xr[k] * c;
     o[k] = rr ? rr[k] + v : v;

@@ -491,13 +491,24 @@ rtq_status enqueue_backward_dense(rtq_ctx* c, const rtq_weight* w, const float* 
 // y = x.W^T (+bias) (+ s h.B^T);  isums (debug) receives the per-block integer sums.
 // hp_keep (optional, nhp * t * r floats): the LoRA-down partials go there instead of the workspace,
 // for a later enqueue_backward of the same x to reuse
+// sw_g / sw_u (optional, quantised weights): x is SwiGLU's silu(g) * u (rows of stride sw_ld), formed
+// by the activation kernel and written to x
+struct SwiGluIn {
+  const float* g;
+  const float* u;
+  int64_t ld;
+};
 rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int64_t t, float* y, const float* bias,
                            const float* la, const float* lb, int64_t r, float s, int32_t* isums, Arena& ar,
-                           hipStream_t st, float* hp_keep = nullptr, const RankBlocks* rb = nullptr) {
+                           hipStream_t st, float* hp_keep = nullptr, const RankBlocks* rb = nullptr,
+                           const SwiGluIn* sw = nullptr) {
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
   const RankBlocks rbv = lora && rb ? *rb : RankBlocks{};
-  if (is_dense(w->type)) return enqueue_forward_dense(c, w, x, t, y, bias, la, lb, lora ? r : 0, s, ar, st);
+  if (is_dense(w->type)) {
+    if (sw) return fail(RTQ_ERR_UNSUPPORTED, "internal: SwiGLU input of a dense weight");
+    return enqueue_forward_dense(c, w, x, t, y, bias, la, lb, lora ? r : 0, s, ar, st);
+  }
   FwdPlan p = fwd_plan(w, t, lora ? r : 0);
   // the debug sums come from the skinny / wide kernels; the GEMV pays off once its row tiles alone
   // give a workgroup per CU (an LM head), below that the skinny kernel's K split wins
@@ -512,6 +523,11 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
     const float gbias = w->type == RTQ_TYPE_Q4_0 ? 1032.0f : (w->type == RTQ_TYPE_Q8_0 ? 1152.0f : 0.0f);
     ActArgs aa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xq, xd, xg, gbias, lora ? la : nullptr, (int)r, hp,
                gp.gy > 1 ? y : nullptr, (int)w->rows, nullptr};
+    if (sw) {
+      aa.sg = sw->g;
+      aa.su = sw->u;
+      aa.ldsg = (int)sw->ld;
+    }
     RTQ_TRY(launch(c, is_kquant(w->type) ? K_ACT_PREP_K : K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp),
                    dim3(256), st, aa));
     FwdArgs fa{};
@@ -585,6 +601,11 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   ActArgs aa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xq, xd, nullptr, 0.0f, lora ? la : nullptr, (int)r, hp,
              ks > 1 ? y : nullptr, (int)w->rows, xdh};
+  if (sw) {
+    aa.sg = sw->g;
+    aa.su = sw->u;
+    aa.ldsg = (int)sw->ld;
+  }
   RTQ_TRY(launch(c, kq ? K_ACT_PREP_K : K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp), dim3(256), st, aa));
   FwdArgs fa{};
   fa.wq = w->wq;
@@ -1719,6 +1740,32 @@ rtq_status rtq_linear_forward_keep_d(rtq_ctx* c, const rtq_weight* w, const floa
   Arena ar{(char*)c->ws, c->ws_bytes, 0};
   return enqueue_forward(c, w, x, t, y, bias, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, nullptr, ar, st,
                          hp_keep, rb);
+}
+
+rtq_status rtq_linear_forward_swiglu_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
+                                       const RankBlocks* rb, const float* g, const float* u, int64_t ldg,
+                                       float* x_out, int64_t t, float* y, float* hp_keep, void* stream) {
+  RTQ_TRY(check_weight(c, w));
+  RTQ_TRY(check_t(t));
+  RTQ_TRY(check_blocks(w, lora, rb));
+  if (is_dense(w->type)) return fail(RTQ_ERR_UNSUPPORTED, "SwiGLU input: quantised weights only");
+  bool on;
+  int64_t r;
+  float s;
+  RTQ_TRY(check_lora(lora, &on, &r, &s));
+  if (t > 0 && (!g || !u || !x_out || !y)) return fail(RTQ_ERR_INVALID, "null g/u/x/y");
+  if (ldg < w->cols || ldg % 4 != 0 || ((uintptr_t)g | (uintptr_t)u | (uintptr_t)x_out) % 16 != 0)
+    return fail(RTQ_ERR_INVALID, "SwiGLU input: rows of at least cols floats, 16-byte aligned");
+  if (hp_keep && rtq_lora_partial_floats(w, t, on ? r : 0) == 0) hp_keep = nullptr;
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = (hipStream_t)stream;
+  FwdPlan p = fwd_plan(w, t, on ? r : 0);
+  RTQ_TRY(ensure_ws(c, fwd_ws_bytes(p)));
+  Arena ar{(char*)c->ws, c->ws_bytes, 0};
+  const SwiGluIn sw{g, u, ldg};
+  return enqueue_forward(c, w, x_out, t, y, bias, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, nullptr, ar,
+                         st, hp_keep, rb, &sw);
 }
 
 rtq_status rtq_linear_forward_ws_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
