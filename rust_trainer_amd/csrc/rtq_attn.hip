@@ -26,6 +26,8 @@ __device__ __forceinline__ bool attn_tile_live(const MAttnArgs& a, int qblk64, i
 }
 
 // ------------------------------------------------------------------ forward
+constexpr int kMergeBatch = 8;  // merges of up to this many slots issue all their loads at once
+
 // a block's partials (o, m, l; m a base-2 maximum) combined in slot order: m* = max m_s,
 // l* = sum l_s 2^(m_s - m*), o = (sum o_s 2^(m_s - m*)) / l*, lse = m* ln 2 + log l*; one thread per
 // output element e of the 16 x hd block (its row's m*, l* recomputed by each thread of the row)
@@ -34,8 +36,31 @@ __device__ __forceinline__ void attn_merge_fwd(const MAttnArgs& a, const MAttnMe
   if (row >= a.t) return;
   const float* p0 = a.part + (int64_t)mg.s0 * (32 * HD);
   float m = -__builtin_inff();
-  for (int s = 0; s < mg.n; s++) m = fmaxf(m, p0[(int64_t)s * 32 * HD + 16 * HD + rl]);
   float l = 0.0f, o = 0.0f;
+  if (mg.n <= kMergeBatch) {  // every slot's loads issued together, then the same arithmetic in slot order
+    float mv[kMergeBatch], lv[kMergeBatch], ov[kMergeBatch];
+#pragma unroll
+    for (int s = 0; s < kMergeBatch; s++) {  // (n is uniform: the slots past it are not read)
+      const float* ps = p0 + (int64_t)s * 32 * HD;
+      mv[s] = s < mg.n ? ps[16 * HD + rl] : -__builtin_inff();
+      lv[s] = s < mg.n ? ps[16 * HD + 16 + rl] : 0.0f;
+      ov[s] = s < mg.n ? ps[rl * HD + c] : 0.0f;
+    }
+#pragma unroll
+    for (int s = 0; s < kMergeBatch; s++)
+      if (s < mg.n) m = fmaxf(m, mv[s]);
+#pragma unroll
+    for (int s = 0; s < kMergeBatch; s++) {
+      if (s >= mg.n || mv[s] == -__builtin_inff()) continue;
+      const float w = __builtin_amdgcn_exp2f(mv[s] - m);
+      l = l + lv[s] * w;
+      o = o + ov[s] * w;
+    }
+    a.o[(int64_t)row * a.ldq + (int64_t)mg.head * HD + c] = __fdiv_rn(o, l);
+    if (c == 0) a.lse[(int64_t)mg.head * a.t + row] = m * 0.693147180559945309417f + logf(l);
+    return;
+  }
+  for (int s = 0; s < mg.n; s++) m = fmaxf(m, p0[(int64_t)s * 32 * HD + 16 * HD + rl]);
   for (int s = 0; s < mg.n; s++) {
     const float* ps = p0 + (int64_t)s * 32 * HD;
     const float ms = ps[16 * HD + rl];
@@ -58,7 +83,20 @@ __device__ __forceinline__ void attn_bwd_d(const MAttnArgs& a) {
   const float* d = a.dO + (int64_t)i * a.ldq + (int64_t)h * a.hd;
   const float* o = a.o + (int64_t)i * a.ldq + (int64_t)h * a.hd;
   float s = 0.0f;
-  for (int e = lane; e < a.hd; e += 64) s = s + d[e] * o[e];
+  if (a.hd <= 256) {  // loads together
+    float dv[4], ov[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int e = min(lane + 64 * u, a.hd - 1);
+      dv[u] = d[e];
+      ov[u] = o[e];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      if (lane + 64 * u < a.hd) s = s + dv[u] * ov[u];
+  } else {
+    for (int e = lane; e < a.hd; e += 64) s = s + d[e] * o[e];
+  }
   s = wave_sum(s);
   if (lane == 0) a.D[(int64_t)h * a.t + i] = s;
 }
@@ -71,7 +109,16 @@ __device__ __forceinline__ void attn_merge_sum(const MAttnArgs& a, const MAttnMe
   if (row >= a.t) return;
   const float* p0 = a.part + (int64_t)mg.s0 * (32 * HD) + e;
   float s = 0.0f;
-  for (int k = 0; k < mg.n; k++) s = s + p0[(int64_t)k * 32 * HD];
+  if (mg.n <= kMergeBatch) {  // loads together, summed in slot order
+    float v[kMergeBatch];
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; k++) v[k] = k < mg.n ? p0[(int64_t)k * 32 * HD] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; k++)
+      if (k < mg.n) s = s + v[k];
+  } else {
+    for (int k = 0; k < mg.n; k++) s = s + p0[(int64_t)k * 32 * HD];
+  }
   if (!kv)
     a.dq[(int64_t)row * a.ldq + (int64_t)mg.head * HD + c] = s;
   else if (part == 0)

@@ -325,25 +325,32 @@ __device__ __forceinline__ void fa_fwd(const MAttnArgs& a, const MAttnItem& it, 
 }
 
 // ------------------------------------------------------------------ dq
+// Item: 64 queries (it.blk) of head it.head over the 64-key tiles [b0, b1).  Wave w = (wq, wh) =
+// (w / 2, w % 2) owns queries 32 wq .. 32 wq + 31 (two 16-row tiles, their q scale and dO operand
+// fragments in registers); it forms S and dP for the key half 32 wh .. 32 wh + 31 of each tile and
+// dq for the column half (HD / 2) wh .. of its queries, so every K / V fragment read from LDS feeds
+// both row tiles.  dS of the whole 64 x 64 tile passes between the two phases through LDS.
 template <int HD>
 struct FaDqLds {
   static constexpr int LDK = HD + kFaPad, LDT = 64 + kFaPad;
   uint16_t k[64 * LDK];                  // K [key][d], f16 (S)
   uint16_t vh[64 * LDK], vl[64 * LDK];   // V [key][d], bf16 hi / lo (dP = dO V^T)
   uint16_t kth[HD * LDT], ktl[HD * LDT]; // K [d][key], bf16 hi / lo (dq = dS K)
-  uint16_t sh[4][16 * LDT], sl[4][16 * LDT];  // per wave: dS [row][key], bf16 hi / lo
+  uint16_t sh[64 * LDT], sl[64 * LDT];   // dS [query][key], bf16 hi / lo
 };
 
 template <int HD>
 __device__ __forceinline__ void fa_dq(const MAttnArgs& a, const MAttnItem& it, FaDqLds<HD>& L) {
-  constexpr int NC = HD / 16, NK = HD / 32, LDK = FaDqLds<HD>::LDK, LDT = FaDqLds<HD>::LDT;
+  constexpr int NC = HD / 16, NH = NC / 2, NK = HD / 32, LDK = FaDqLds<HD>::LDK, LDT = FaDqLds<HD>::LDT;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
-  const int h = it.head, kvh = h / (a.nh / a.nkv), qb = it.blk, r0 = qb * 64 + 16 * w;
+  const int wq = w >> 1, wh = w & 1;
+  const int h = it.head, kvh = h / (a.nh / a.nkv), qb = it.blk, r0 = qb * 64 + 32 * wq;
   const float qs2 = a.scale * kLog2e;  // scores in base 2, as the forward
-  half8 qh[NK], ql[NK];
-  bf8 dh[NK], dl[NK];
-  {
-    const int rc = min(r0 + li, a.t - 1);
+  half8 qh[2][NK], ql[2][NK];
+  bf8 dh[2][NK], dl[2][NK];
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int rc = min(r0 + 16 * u + li, a.t - 1);
     const float* qr = a.q + (int64_t)rc * a.ldq + (int64_t)h * HD + 8 * g;
     const float* dr = a.dO + (int64_t)rc * a.ldq + (int64_t)h * HD + 8 * g;
 #pragma unroll
@@ -351,28 +358,32 @@ __device__ __forceinline__ void fa_dq(const MAttnArgs& a, const MAttnItem& it, F
       u2v h0, l0, h1, l1;
       fa_split_f16(*reinterpret_cast<const f4*>(qr + 32 * c) * qs2, h0, l0);
       fa_split_f16(*reinterpret_cast<const f4*>(qr + 32 * c + 4) * qs2, h1, l1);
-      qh[c] = __builtin_bit_cast(half8, u4v{h0.x, h0.y, h1.x, h1.y});
-      ql[c] = __builtin_bit_cast(half8, u4v{l0.x, l0.y, l1.x, l1.y});
+      qh[u][c] = __builtin_bit_cast(half8, u4v{h0.x, h0.y, h1.x, h1.y});
+      ql[u][c] = __builtin_bit_cast(half8, u4v{l0.x, l0.y, l1.x, l1.y});
       uint32_t eh[8], el[8];
 #pragma unroll
       for (int e = 0; e < 8; e++) fa_split_bf(dr[32 * c + e], eh[e], el[e]);
-      dh[c] = __builtin_bit_cast(bf8, u4v{eh[0] | (eh[1] << 16), eh[2] | (eh[3] << 16), eh[4] | (eh[5] << 16), eh[6] | (eh[7] << 16)});
-      dl[c] = __builtin_bit_cast(bf8, u4v{el[0] | (el[1] << 16), el[2] | (el[3] << 16), el[4] | (el[5] << 16), el[6] | (el[7] << 16)});
+      dh[u][c] = __builtin_bit_cast(bf8, u4v{eh[0] | (eh[1] << 16), eh[2] | (eh[3] << 16), eh[4] | (eh[5] << 16), eh[6] | (eh[7] << 16)});
+      dl[u][c] = __builtin_bit_cast(bf8, u4v{el[0] | (el[1] << 16), el[2] | (el[3] << 16), el[4] | (el[5] << 16), el[6] | (el[7] << 16)});
     }
   }
-  int si[4];
-  float lq[4], Dq[4];
+  int si[2][4];
+  float lq[2][4], Dq[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int row = min(r0 + 4 * g + i, a.t - 1);
-    si[i] = attn_seg(a, row);
-    lq[i] = a.lse[(int64_t)h * a.t + row] * kLog2e;
-    Dq[i] = a.D[(int64_t)h * a.t + row];
-  }
+  for (int u = 0; u < 2; u++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = min(r0 + 16 * u + 4 * g + i, a.t - 1);
+      si[u][i] = attn_seg(a, row);
+      lq[u][i] = a.lse[(int64_t)h * a.t + row] * kLog2e;
+      Dq[u][i] = a.D[(int64_t)h * a.t + row];
+    }
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f4 acc[NC];
+  f4 acc[2][NH];  // [query tile][column tile NH wh + cc]
 #pragma unroll
-  for (int c = 0; c < NC; c++) acc[c] = zero;
+  for (int u = 0; u < 2; u++)
+#pragma unroll
+    for (int c = 0; c < NH; c++) acc[u][c] = zero;
   const float* kb = a.k + (int64_t)kvh * HD;
   const float* vb = a.v + (int64_t)kvh * HD;
   FaNat<HD> kn, vn;
@@ -395,45 +406,64 @@ __device__ __forceinline__ void fa_dq(const MAttnArgs& a, const MAttnItem& it, F
       vn.load(vb, a.ldv, kt2 * 64, a.t);
       kt_.load(kb, a.ldk, kt2 * 64, a.t);
     }
-    f4 s[4] = {zero, zero, zero, zero}, dp[4] = {zero, zero, zero, zero};
+    // S and dP of the two query tiles x keys 32 wh + 16 j (j = 0, 1)
+    f4 s[2][2] = {{zero, zero}, {zero, zero}}, dp[2][2] = {{zero, zero}, {zero, zero}};
 #pragma unroll
     for (int c = 0; c < NK; c++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int o = (16 * j + li) * LDK + 32 * c + 8 * g;
+      for (int j = 0; j < 2; j++) {
+        const int o = (32 * wh + 16 * j + li) * LDK + 32 * c + 8 * g;
         const half8 kf = fa_h8(L.k + o);
-        s[j] = mfma_f16(qh[c], kf, s[j]);
-        s[j] = mfma_f16(ql[c], kf, s[j]);
         const bf8 vh = fa_b8(L.vh + o), vl = fa_b8(L.vl + o);
-        dp[j] = mfma_bf16(dh[c], vh, dp[j]);
-        dp[j] = mfma_bf16(dl[c], vh, dp[j]);
-        dp[j] = mfma_bf16(dh[c], vl, dp[j]);
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          s[u][j] = mfma_f16(qh[u][c], kf, s[u][j]);
+          s[u][j] = mfma_f16(ql[u][c], kf, s[u][j]);
+          dp[u][j] = mfma_bf16(dh[u][c], vh, dp[u][j]);
+          dp[u][j] = mfma_bf16(dl[u][c], vh, dp[u][j]);
+          dp[u][j] = mfma_bf16(dh[u][c], vl, dp[u][j]);
+        }
       }
-    float ds[4][4];
-    int sk[4];
+    int sk[2];
 #pragma unroll
-    for (int j = 0; j < 4; j++) sk[j] = attn_seg(a, k0 + 16 * j + li);
+    for (int j = 0; j < 2; j++) sk[j] = attn_seg(a, k0 + 32 * wh + 16 * j + li);
+    // dS -> LDS [query 32 wq + 16 u + 4 g + i][key 32 wh + 16 j + li], bf16 hi / lo
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int u = 0; u < 2; u++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const bool ok = fa_ok(r0 + 4 * g + i, k0 + 16 * j + li, si[i], sk[j], a.t);
-        const float p = __builtin_amdgcn_exp2f(s[j][i] - lq[i]);
-        ds[j][i] = ok ? (p * (dp[j][i] - Dq[i])) * a.scale : 0.0f;
-      }
-    fa_put_tile<false>(ds, L.sh[w], L.sl[w]);
-    __builtin_amdgcn_wave_barrier();
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int qrow = r0 + 16 * u + 4 * g + i, key = k0 + 32 * wh + 16 * j + li;
+          const bool ok = fa_ok(qrow, key, si[u][i], sk[j], a.t);
+          const float p = __builtin_amdgcn_exp2f(s[u][j][i] - lq[u][i]);
+          const float ds = ok ? (p * (dp[u][j][i] - Dq[u][i])) * a.scale : 0.0f;
+          uint32_t hb, lb;
+          fa_split_bf(ds, hb, lb);
+          const int o = (32 * wq + 16 * u + 4 * g + i) * LDT + 32 * wh + 16 * j + li;
+          L.sh[o] = (uint16_t)hb;
+          L.sl[o] = (uint16_t)lb;
+        }
+    __syncthreads();
+    // dq[query tile u][column tile NH wh + cc] += dS K over the tile's 64 keys (two 32-key steps)
 #pragma unroll
     for (int c = 0; c < 2; c++) {
-      const bf8 sh = fa_b8(L.sh[w] + li * LDT + 32 * c + 8 * g);
-      const bf8 sl = fa_b8(L.sl[w] + li * LDT + 32 * c + 8 * g);
+      bf8 sh[2], sl[2];
 #pragma unroll
-      for (int cc = 0; cc < NC; cc++) {
-        const int o = (16 * cc + li) * LDT + 32 * c + 8 * g;
+      for (int u = 0; u < 2; u++) {
+        sh[u] = fa_b8(L.sh + (32 * wq + 16 * u + li) * LDT + 32 * c + 8 * g);
+        sl[u] = fa_b8(L.sl + (32 * wq + 16 * u + li) * LDT + 32 * c + 8 * g);
+      }
+#pragma unroll
+      for (int cc = 0; cc < NH; cc++) {
+        const int o = (16 * (NH * wh + cc) + li) * LDT + 32 * c + 8 * g;
         const bf8 kh = fa_b8(L.kth + o), kl = fa_b8(L.ktl + o);
-        acc[cc] = mfma_bf16(sh, kh, acc[cc]);
-        acc[cc] = mfma_bf16(sl, kh, acc[cc]);
-        acc[cc] = mfma_bf16(sh, kl, acc[cc]);
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          acc[u][cc] = mfma_bf16(sh[u], kh, acc[u][cc]);
+          acc[u][cc] = mfma_bf16(sl[u], kh, acc[u][cc]);
+          acc[u][cc] = mfma_bf16(sh[u], kl, acc[u][cc]);
+        }
       }
     }
     __syncthreads();
@@ -441,27 +471,36 @@ __device__ __forceinline__ void fa_dq(const MAttnArgs& a, const MAttnItem& it, F
   }
   if (it.slot < 0) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int row = r0 + 4 * g + i;
-      if (row >= a.t) continue;
-      float* q = a.dq + (int64_t)row * a.ldq + (int64_t)h * HD + li;
+    for (int u = 0; u < 2; u++)
 #pragma unroll
-      for (int c = 0; c < NC; c++) q[16 * c] = acc[c][i];
+      for (int i = 0; i < 4; i++) {
+        const int row = r0 + 16 * u + 4 * g + i;
+        if (row >= a.t) continue;
+        float* q = a.dq + (int64_t)row * a.ldq + (int64_t)h * HD + 16 * NH * wh + li;
+#pragma unroll
+        for (int c = 0; c < NH; c++) q[16 * c] = acc[u][c][i];
+      }
+  } else {  // 16-row sub-block 2 wq + u of the item -> its slot; this wave's column half
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      float* pp = a.part + (int64_t)(it.slot + (2 * wq + u) * it.pad0) * (32 * HD) + 16 * NH * wh + li;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int c = 0; c < NH; c++) pp[(4 * g + i) * HD + 16 * c] = acc[u][c][i];
     }
-  } else {
-    float* pp = a.part + (int64_t)(it.slot + w * it.pad0) * (32 * HD);
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int c = 0; c < NC; c++) pp[(4 * g + i) * HD + 16 * c + li] = acc[c][i];
   }
 }
 
 // ------------------------------------------------------------------ dk, dv
 // Item: 64 keys (it.blk) of KV head it.head over (group head, 64-query tile) pairs [b0, b1); each
-// pair is taken as two 32-query halves, staged as q scale (f16 hi / lo, [q][d], for S^T = k q^T),
-// q (bf16 hi / lo, [d][q], for dk += dS^T q), dO (bf16 hi / lo, [q][d] for dP^T = v dO^T and [d][q]
-// for dv += p^T dO).
+// pair is taken as two 32-query halves (steps), staged as q scale (f16 hi / lo, [q][d], for S^T =
+// k q^T), q (bf16 hi / lo, [d][q], for dk += dS^T q), dO (bf16 hi / lo, [q][d] for dP^T = v dO^T
+// and [d][q] for dv += p^T dO).  Wave w = (wk, wh) = (w / 2, w % 2) owns keys 32 wk .. 32 wk + 31
+// (two 16-key tiles, their k / v operand fragments in registers); it forms S^T and dP^T for the
+// query half 16 wh .. 16 wh + 15 of the step and dk / dv for the column half (HD / 2) wh .. of its
+// keys, so every q / dO fragment read from LDS feeds both key tiles.  p^T and dS^T of the whole
+// 64 x 32 step pass between the two phases through LDS.
 template <int HD>
 struct FaKvLds {
   static constexpr int LDN = HD + kFaPad, LDT = 32 + kFaPad, LDP = 32 + kFaPad;
@@ -469,7 +508,7 @@ struct FaKvLds {
   uint16_t qth[HD * LDT], qtl[HD * LDT];    // q [d][q], bf16 hi / lo
   uint16_t dsh_[32 * LDN], dsl_[32 * LDN];  // dO [q][d], bf16 hi / lo
   uint16_t dth[HD * LDT], dtl[HD * LDT];    // dO [d][q], bf16 hi / lo
-  uint16_t ph[4][16 * LDP], pl[4][16 * LDP], sh[4][16 * LDP], sl[4][16 * LDP];  // per wave: p^T, dS^T [key][q]
+  uint16_t ph[64 * LDP], pl[64 * LDP], sh[64 * LDP], sl[64 * LDP];  // p^T, dS^T [key][q], bf16 hi / lo
 };
 // 32 rows x HD staging (natural: thread -> row tid / 8, columns (tid % 8) HD / 8 ..; transposed:
 // thread -> rows KPT kg .., columns 4 (tid % (HD / 4)) .., KPT = HD / 32)
@@ -532,54 +571,44 @@ __device__ __forceinline__ void fa_store32_tr_bf(const FaTr32<HD>& s, uint16_t* 
     }
   }
 }
-// a 16 x 32 tile in MFMA output order (tv[j][i]: row 4 g + i, column 16 j + li, j < 2) -> bf16 hi / lo
-// planes [row][col] (stride 32 + kFaPad)
-__device__ __forceinline__ void fa_put_tile32(const float (&tv)[2][4], uint16_t* Th, uint16_t* Tl) {
-  constexpr int LD = 32 + kFaPad;
-  const int lane = threadIdx.x & 63, li = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      uint32_t h, l;
-      fa_split_bf(tv[j][i], h, l);
-      Th[(4 * g + i) * LD + 16 * j + li] = (uint16_t)h;
-      Tl[(4 * g + i) * LD + 16 * j + li] = (uint16_t)l;
-    }
-}
-
 template <int HD>
 __device__ __forceinline__ void fa_dkv(const MAttnArgs& a, const MAttnItem& it, FaKvLds<HD>& L) {
-  constexpr int NC = HD / 16, NK = HD / 32;
+  constexpr int NC = HD / 16, NH = NC / 2, NK = HD / 32;
   constexpr int LDN = FaKvLds<HD>::LDN, LDT = FaKvLds<HD>::LDT, LDP = FaKvLds<HD>::LDP;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
-  const int kvh = it.head, grp = a.nh / a.nkv, kbk = it.blk, c0 = kbk * 64 + 16 * w, nqt = (a.t + 63) / 64;
-  // the wave's 16 keys: k (f16, exact) and v (bf16 hi / lo) operand fragments
-  half8 kf[NK];
-  bf8 vh[NK], vl[NK];
-  {
-    const int kc = min(c0 + li, a.t - 1);
+  const int wk = w >> 1, wh = w & 1;
+  const int kvh = it.head, grp = a.nh / a.nkv, kbk = it.blk, c0 = kbk * 64 + 32 * wk, nqt = (a.t + 63) / 64;
+  // the wave's 32 keys: k (f16, exact) and v (bf16 hi / lo) operand fragments of its two key tiles
+  half8 kf[2][NK];
+  bf8 vh[2][NK], vl[2][NK];
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int kc = min(c0 + 16 * u + li, a.t - 1);
     const float* kr = a.k + (int64_t)kc * a.ldk + (int64_t)kvh * HD + 8 * g;
     const float* vr = a.v + (int64_t)kc * a.ldv + (int64_t)kvh * HD + 8 * g;
 #pragma unroll
     for (int c = 0; c < NK; c++) {
       const u2v k0 = fa_f16(*reinterpret_cast<const f4*>(kr + 32 * c));
       const u2v k1 = fa_f16(*reinterpret_cast<const f4*>(kr + 32 * c + 4));
-      kf[c] = __builtin_bit_cast(half8, u4v{k0.x, k0.y, k1.x, k1.y});
+      kf[u][c] = __builtin_bit_cast(half8, u4v{k0.x, k0.y, k1.x, k1.y});
       uint32_t eh[8], el[8];
 #pragma unroll
       for (int e = 0; e < 8; e++) fa_split_bf(vr[32 * c + e], eh[e], el[e]);
-      vh[c] = __builtin_bit_cast(bf8, u4v{eh[0] | (eh[1] << 16), eh[2] | (eh[3] << 16), eh[4] | (eh[5] << 16), eh[6] | (eh[7] << 16)});
-      vl[c] = __builtin_bit_cast(bf8, u4v{el[0] | (el[1] << 16), el[2] | (el[3] << 16), el[4] | (el[5] << 16), el[6] | (el[7] << 16)});
+      vh[u][c] = __builtin_bit_cast(bf8, u4v{eh[0] | (eh[1] << 16), eh[2] | (eh[3] << 16), eh[4] | (eh[5] << 16), eh[6] | (eh[7] << 16)});
+      vl[u][c] = __builtin_bit_cast(bf8, u4v{el[0] | (el[1] << 16), el[2] | (el[3] << 16), el[4] | (el[5] << 16), el[6] | (el[7] << 16)});
     }
   }
-  int skey[4];  // segments of the lane's keys c0 + 4 g + i
+  int skey[2][4];  // segments of the lane's keys c0 + 16 u + 4 g + i
 #pragma unroll
-  for (int i = 0; i < 4; i++) skey[i] = attn_seg(a, c0 + 4 * g + i);
+  for (int u = 0; u < 2; u++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) skey[u][i] = attn_seg(a, c0 + 16 * u + 4 * g + i);
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f4 dk[NC], dv[NC];
+  f4 dk[2][NH], dv[2][NH];  // [key tile][column tile NH wh + cc]
 #pragma unroll
-  for (int c = 0; c < NC; c++) dk[c] = dv[c] = zero;
+  for (int u = 0; u < 2; u++)
+#pragma unroll
+    for (int c = 0; c < NH; c++) dk[u][c] = dv[u][c] = zero;
   // (pair, half) steps: pair pr = (group head, 64-query tile), half hf = 32-query half
   auto live_pair = [&](int pr) {
     const int qt = pr % nqt;
@@ -611,52 +640,68 @@ __device__ __forceinline__ void fa_dkv(const MAttnArgs& a, const MAttnItem& it, 
     __syncthreads();
     const int st2 = next_step(st + 1);
     if (st2 < 2 * it.b1) load_step(st2);
-    // S^T = k (q scale)^T and dP^T = v dO^T: 16 keys x 32 queries
+    // S^T = k (q scale)^T and dP^T = v dO^T: the two key tiles x queries 16 wh .. 16 wh + 15
     f4 s[2] = {zero, zero}, dp[2] = {zero, zero};
 #pragma unroll
-    for (int c = 0; c < NK; c++)
+    for (int c = 0; c < NK; c++) {
+      const int o = (16 * wh + li) * LDN + 32 * c + 8 * g;
+      const half8 qhf = fa_h8(L.qsh + o), qlf = fa_h8(L.qsl + o);
+      const bf8 dhf = fa_b8(L.dsh_ + o), dlf = fa_b8(L.dsl_ + o);
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const int o = (16 * j + li) * LDN + 32 * c + 8 * g;
-        const half8 qhf = fa_h8(L.qsh + o), qlf = fa_h8(L.qsl + o);
-        s[j] = mfma_f16(kf[c], qhf, s[j]);
-        s[j] = mfma_f16(kf[c], qlf, s[j]);
-        const bf8 dhf = fa_b8(L.dsh_ + o), dlf = fa_b8(L.dsl_ + o);
-        dp[j] = mfma_bf16(vh[c], dhf, dp[j]);
-        dp[j] = mfma_bf16(vl[c], dhf, dp[j]);
-        dp[j] = mfma_bf16(vh[c], dlf, dp[j]);
+      for (int u = 0; u < 2; u++) {
+        s[u] = mfma_f16(kf[u][c], qhf, s[u]);
+        s[u] = mfma_f16(kf[u][c], qlf, s[u]);
+        dp[u] = mfma_bf16(vh[u][c], dhf, dp[u]);
+        dp[u] = mfma_bf16(vl[u][c], dhf, dp[u]);
+        dp[u] = mfma_bf16(vh[u][c], dlf, dp[u]);
       }
-    float pt[2][4], dst[2][4];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int qr = q0 + 16 * j + li, qc = min(qr, a.t - 1);
+    }
+    {  // p^T, dS^T -> LDS [key 32 wk + 16 u + 4 g + i][query 16 wh + li], bf16 hi / lo
+      const int qr = q0 + 16 * wh + li, qc = min(qr, a.t - 1);
       const float lq = a.lse[(int64_t)h * a.t + qc] * kLog2e, Dq = a.D[(int64_t)h * a.t + qc];
       const int sq = attn_seg(a, qc);
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const bool ok = fa_ok(qr, c0 + 4 * g + i, sq, skey[i], a.t);
-        const float p = ok ? __builtin_amdgcn_exp2f(s[j][i] - lq) : 0.0f;
-        pt[j][i] = p;
-        dst[j][i] = ok ? (p * (dp[j][i] - Dq)) * a.scale : 0.0f;
-      }
-    }
-    fa_put_tile32(pt, L.ph[w], L.pl[w]);
-    fa_put_tile32(dst, L.sh[w], L.sl[w]);
-    __builtin_amdgcn_wave_barrier();
-    {  // dV += P^T dO, dK += dS^T q over the 32 queries (one 32-deep step)
-      const bf8 phf = fa_b8(L.ph[w] + li * LDP + 8 * g), plf = fa_b8(L.pl[w] + li * LDP + 8 * g);
-      const bf8 shf = fa_b8(L.sh[w] + li * LDP + 8 * g), slf = fa_b8(L.sl[w] + li * LDP + 8 * g);
+      for (int u = 0; u < 2; u++)
 #pragma unroll
-      for (int cc = 0; cc < NC; cc++) {
-        const int o = (16 * cc + li) * LDT + 8 * g;
+        for (int i = 0; i < 4; i++) {
+          const bool ok = fa_ok(qr, c0 + 16 * u + 4 * g + i, sq, skey[u][i], a.t);
+          const float p = ok ? __builtin_amdgcn_exp2f(s[u][i] - lq) : 0.0f;
+          const float ds = ok ? (p * (dp[u][i] - Dq)) * a.scale : 0.0f;
+          uint32_t h0, l0, h1, l1;
+          fa_split_bf(p, h0, l0);
+          fa_split_bf(ds, h1, l1);
+          const int o = (32 * wk + 16 * u + 4 * g + i) * LDP + 16 * wh + li;
+          L.ph[o] = (uint16_t)h0;
+          L.pl[o] = (uint16_t)l0;
+          L.sh[o] = (uint16_t)h1;
+          L.sl[o] = (uint16_t)l1;
+        }
+    }
+    __syncthreads();
+    {  // dV += P^T dO, dK += dS^T q over the step's 32 queries (one 32-deep MFMA step)
+      bf8 phf[2], plf[2], shf[2], slf[2];
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int o = (32 * wk + 16 * u + li) * LDP + 8 * g;
+        phf[u] = fa_b8(L.ph + o);
+        plf[u] = fa_b8(L.pl + o);
+        shf[u] = fa_b8(L.sh + o);
+        slf[u] = fa_b8(L.sl + o);
+      }
+#pragma unroll
+      for (int cc = 0; cc < NH; cc++) {
+        const int o = (16 * (NH * wh + cc) + li) * LDT + 8 * g;
         const bf8 doh = fa_b8(L.dth + o), dol = fa_b8(L.dtl + o);
-        dv[cc] = mfma_bf16(phf, doh, dv[cc]);
-        dv[cc] = mfma_bf16(plf, doh, dv[cc]);
-        dv[cc] = mfma_bf16(phf, dol, dv[cc]);
         const bf8 qh2 = fa_b8(L.qth + o), ql2 = fa_b8(L.qtl + o);
-        dk[cc] = mfma_bf16(shf, qh2, dk[cc]);
-        dk[cc] = mfma_bf16(slf, qh2, dk[cc]);
-        dk[cc] = mfma_bf16(shf, ql2, dk[cc]);
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          dv[u][cc] = mfma_bf16(phf[u], doh, dv[u][cc]);
+          dv[u][cc] = mfma_bf16(plf[u], doh, dv[u][cc]);
+          dv[u][cc] = mfma_bf16(phf[u], dol, dv[u][cc]);
+          dk[u][cc] = mfma_bf16(shf[u], qh2, dk[u][cc]);
+          dk[u][cc] = mfma_bf16(slf[u], qh2, dk[u][cc]);
+          dk[u][cc] = mfma_bf16(shf[u], ql2, dk[u][cc]);
+        }
       }
     }
     __syncthreads();
@@ -664,26 +709,31 @@ __device__ __forceinline__ void fa_dkv(const MAttnArgs& a, const MAttnItem& it, 
   }
   if (it.slot < 0) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int key = c0 + 4 * g + i;
-      if (key >= a.t) continue;
-      float* kr = a.dk + (int64_t)key * a.ldk + (int64_t)kvh * HD + li;
-      float* vr = a.dv + (int64_t)key * a.ld_dv + (int64_t)kvh * HD + li;
+    for (int u = 0; u < 2; u++)
 #pragma unroll
-      for (int c = 0; c < NC; c++) {
-        kr[16 * c] = dk[c][i];
-        vr[16 * c] = dv[c][i];
+      for (int i = 0; i < 4; i++) {
+        const int key = c0 + 16 * u + 4 * g + i;
+        if (key >= a.t) continue;
+        float* kr = a.dk + (int64_t)key * a.ldk + (int64_t)kvh * HD + 16 * NH * wh + li;
+        float* vr = a.dv + (int64_t)key * a.ld_dv + (int64_t)kvh * HD + 16 * NH * wh + li;
+#pragma unroll
+        for (int c = 0; c < NH; c++) {
+          kr[16 * c] = dk[u][c][i];
+          vr[16 * c] = dv[u][c][i];
+        }
       }
+  } else {  // 16-key sub-block 2 wk + u of the item -> its slot (dk rows, then dv rows); this wave's column half
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      float* pp = a.part + (int64_t)(it.slot + (2 * wk + u) * it.pad0) * (32 * HD) + 16 * NH * wh + li;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int c = 0; c < NH; c++) {
+          pp[(4 * g + i) * HD + 16 * c] = dk[u][c][i];
+          pp[16 * HD + (4 * g + i) * HD + 16 * c] = dv[u][c][i];
+        }
     }
-  } else {
-    float* pp = a.part + (int64_t)(it.slot + w * it.pad0) * (32 * HD);
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int c = 0; c < NC; c++) {
-        pp[(4 * g + i) * HD + 16 * c + li] = dk[c][i];
-        pp[16 * HD + (4 * g + i) * HD + 16 * c + li] = dv[c][i];
-      }
   }
 }
 

@@ -156,7 +156,25 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_qk_prep(MQkArgs a) {
   const int p = (int)(r / heads);
   const float* x = (isq ? a.q_raw + p * a.ldq : a.k_raw + p * a.ldk) + (r % heads) * a.hd;
   const float* w = isq ? a.q_norm : a.k_norm;
-  if (w) {
+  if (w && a.hd <= 256) {  // the row in registers: its loads issued together
+    float xv[4], wv[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int e = min(lane + 64 * u, a.hd - 1);
+      xv[u] = x[e];
+      wv[u] = w[e];
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      if (lane + 64 * u < a.hd) s = s + xv[u] * xv[u];
+    s = wave_sum(s);
+    const float ir = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(s, (float)a.hd) + a.eps));
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      if (lane + 64 * u < a.hd) sb[lane + 64 * u] = xv[u] * (ir * (wv[u] + a.off));
+    if (lane == 0) (isq ? a.q_inv : a.k_inv)[r] = ir;
+  } else if (w) {
     float s = 0.0f;
     for (int e = lane; e < a.hd; e += 64) s = s + x[e] * x[e];
     s = wave_sum(s);
@@ -182,16 +200,41 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_qk_bwd(MQkArgs a) {
   const int heads = isq ? a.nh : a.nkv;
   const int p = (int)(r / heads);
   float* sb = buf[wv];
-  m_rope_row(a, (isq ? a.dq : a.dk) + r * a.hd, sb, p, -1.0f, false);
-  __builtin_amdgcn_wave_barrier();
   const int64_t roff = (isq ? p * a.ldq : p * a.ldk) + (r % heads) * a.hd;
   float* out = (isq ? a.dq_raw : a.dk_raw) + roff;
   const float* w = isq ? a.q_norm : a.k_norm;
+  const float* x = (isq ? a.q_raw : a.k_raw) + roff;
+  if (w && a.hd <= 256) {  // the norm's operands loaded before the rotation, all together
+    float xv[4], wv[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int e = min(lane + 64 * u, a.hd - 1);
+      xv[u] = x[e];
+      wv[u] = w[e];
+    }
+    const float ir = (isq ? a.q_inv : a.k_inv)[r];
+    m_rope_row(a, (isq ? a.dq : a.dk) + r * a.hd, sb, p, -1.0f, false);
+    __builtin_amdgcn_wave_barrier();
+    float gv[4];
+    float s = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      gv[u] = lane + 64 * u < a.hd ? sb[lane + 64 * u] * (wv[u] + a.off) : 0.0f;
+      if (lane + 64 * u < a.hd) s = s + gv[u] * xv[u];
+    }
+    s = wave_sum(s);
+    const float c = __fdiv_rn(((s * ir) * ir) * ir, (float)a.hd);
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      if (lane + 64 * u < a.hd) out[lane + 64 * u] = gv[u] * ir - xv[u] * c;
+    return;
+  }
+  m_rope_row(a, (isq ? a.dq : a.dk) + r * a.hd, sb, p, -1.0f, false);
+  __builtin_amdgcn_wave_barrier();
   if (!w) {
     for (int e = lane; e < a.hd; e += 64) out[e] = sb[e];
     return;
   }
-  const float* x = (isq ? a.q_raw : a.k_raw) + roff;
   const float ir = (isq ? a.q_inv : a.k_inv)[r];
   float s = 0.0f;
   for (int e = lane; e < a.hd; e += 64) s = s + (sb[e] * (w[e] + a.off)) * x[e];
