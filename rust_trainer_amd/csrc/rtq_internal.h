@@ -71,10 +71,20 @@ rtq_status rtq_linear_backward_blocks_d(rtq_ctx* c, const rtq_weight* w, const r
 // rtq_linear_backward_blocks_d whose dA / dB are not launched but described in *job, for one
 // rtq_lora_grads_d over several linears; h and g are written to h_out / g_out ([t x r] each), which,
 // like x, dy, ga and gb, must stay untouched until that launch has run (quantised weights only)
+// sw (or null): dx is SwiGLU's dh (src/model.rs:126-131); it is not stored, the dx kernels' finish
+// writes dg = (dh u) silu'(g) and du = dh silu(g) instead (rows of stride ld)
+struct SwiGluBwd {
+  const float* g;
+  const float* u;
+  float* dg;
+  float* du;
+  int64_t ld;
+  bool keep_dh;  // dh is stored to dx as well
+};
 rtq_status rtq_linear_backward_defer_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const RankBlocks* rb,
                                        const float* x, const float* dy, int64_t t, float* dx, float* ga, float* gb,
                                        const float* hp_have, float* h_out, float* g_out, LoraGradArgs* job,
-                                       void* stream);
+                                       void* stream, const SwiGluBwd* sw = nullptr);
 // dA / dB of n (<= RTQ_LORA_JOBS) deferred linears in one launch (jobs with no tiles are skipped)
 rtq_status rtq_lora_grads_d(rtq_ctx* c, const LoraGradArgs* jobs, int n, void* stream);
 // rtq_noalloc.hip: resolves the no-allocation scratch array's address on `device` (current)

@@ -200,6 +200,14 @@ struct LoraGradArgs {
   int accumulate;        // 1: dx += (FrozenMatmul::backward_input); 0: dx = (Linear::backward)
   int part_rows;         // 1: partials row-major [nsplit][T][K] (rtq_dx16_*); 0: fragment order (rtq_dx_*)
   RankBlocks rb;         // gb written only inside the members' blocks
+  // or null: dx is SwiGLU's dh (src/model.rs:126-131) and is not stored; dg = (dh u) silu'(g) and
+  // du = dh silu(g) go to swdg / swdu instead (g, u, dg, du: rows of stride swld)
+  const float* swg;
+  const float* swu;
+  float* swdg;
+  float* swdu;
+  int64_t swld;
+  int sw_keep;  // 1: dh is stored to dx as well (a layer whose activations are being captured)
 };
 
 // dA / dB of up to RTQ_LORA_JOBS linears in one launch (rtq_lora_grads[16]): workgroups

@@ -447,6 +447,15 @@ __device__ __forceinline__ float sum_slices(const float* p, int64_t e, int np, i
 // SiLU of the training step's MLP, x / (1 + e^-x) (src/tensor.rs:123-143; the decoder block's
 // kernels use the same function)
 __device__ __forceinline__ float rtq_silu(float x) { return __fdiv_rn(x, 1.0f + expf(-x)); }
+__device__ __forceinline__ float rtq_sigmoid(float x) {
+  if (x >= 0.0f) return __fdiv_rn(1.0f, 1.0f + expf(-x));
+  const float e = expf(x);
+  return __fdiv_rn(e, 1.0f + e);
+}
+__device__ __forceinline__ float rtq_silu_grad(float x) {
+  const float s = rtq_sigmoid(x);
+  return s * (1.0f + x * (1.0f - s));
+}
 
 template <bool QK>
 __device__ __forceinline__ void act_prep(const ActArgs& a) {
@@ -2292,9 +2301,20 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
         }
         sum += ga;
       }
-      float* p = a.dx + (int64_t)t * a.K + k0;
+      if (NW == 4 && a.swg) {  // SwiGLU backward of dh = sum (accumulate is off; 4-wave finish only)
+        const int64_t o = (int64_t)t * a.swld + k0;
 #pragma unroll
-      for (int e = 0; e < 4; e++) p[e] = a.accumulate ? p[e] + sum[e] : sum[e];
+        for (int e = 0; e < 4; e++) {
+          const float gv = a.swg[o + e], uv = a.swu[o + e];
+          a.swdg[o + e] = (sum[e] * uv) * rtq_silu_grad(gv);
+          a.swdu[o + e] = sum[e] * rtq_silu(gv);
+          if (a.sw_keep) a.dx[(int64_t)t * a.K + k0 + e] = sum[e];
+        }
+      } else {
+        float* p = a.dx + (int64_t)t * a.K + k0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) p[e] = a.accumulate ? p[e] + sum[e] : sum[e];
+      }
     }
   } else {
     // dx quarter fq = (b - n_gb - n_ga) * NW + w: fragment f = fq / 4 of the dx kernel's partials
@@ -2352,17 +2372,39 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
 #pragma unroll
       for (int u = 0; u < 4; u++) ga = mfma_f32(gq[u], aq[u], ga);
     }
-    if (kcol < a.K)
+    if (kcol < a.K) {
+      if (NW == 4 && a.swg) {  // SwiGLU backward of dh = the sum (accumulate off, 4-wave finish only); g, u loaded together
+        float gv[4], uv[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int t = t0 + 4 * g + i;
-        if (t < a.T) {
-          float* p = &a.dx[(int64_t)t * a.K + kcol];
-          float o = a.accumulate ? *p + ps[i] : ps[i];
-          if (a.g) o += ga[i];
-          *p = o;
+        for (int i = 0; i < 4; i++) {
+          const int64_t o = (int64_t)min(t0 + 4 * g + i, a.T - 1) * a.swld + kcol;
+          gv[i] = a.swg[o];
+          uv[i] = a.swu[o];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int t = t0 + 4 * g + i;
+          if (t < a.T) {
+            const float dh = a.g ? ps[i] + ga[i] : ps[i];
+            const int64_t o = (int64_t)t * a.swld + kcol;
+            a.swdg[o] = (dh * uv[i]) * rtq_silu_grad(gv[i]);
+            a.swdu[o] = dh * rtq_silu(gv[i]);
+            if (a.sw_keep) a.dx[(int64_t)t * a.K + kcol] = dh;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int t = t0 + 4 * g + i;
+          if (t < a.T) {
+            float* p = &a.dx[(int64_t)t * a.K + kcol];
+            float o = a.accumulate ? *p + ps[i] : ps[i];
+            if (a.g) o += ga[i];
+            *p = o;
+          }
         }
       }
+    }
   }
 }
 

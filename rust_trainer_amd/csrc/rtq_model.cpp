@@ -343,18 +343,22 @@ rtq_status lin_fwd_swiglu(rtq_model* m, const Group& l, const float* g, const fl
 // computes every pair and the off-block gb entries are cleared after it.  jobs (or null): a
 // quantised adapted group's dA / dB are appended there (h, g in the group's slot gi) for the
 // block's batched launch instead of being launched here.
+// sw (or null): dx is SwiGLU's dh; where the deferred path runs, its finish writes sw's dg / du
+// instead of dx and *sw_done is set (else dx is written and the caller runs the SwiGLU backward)
 rtq_status lin_bwd(rtq_model* m, const Layer& L, int gi, const float* x, const float* dy, int64_t t, float* dx,
-                   std::vector<LoraGradArgs>* jobs = nullptr) {
+                   std::vector<LoraGradArgs>* jobs = nullptr, const SwiGluBwd* sw = nullptr, bool* sw_done = nullptr) {
   const Group& l = L.groups[(size_t)gi];
   const rtq_lora lv = lora_view(l);
   const int wt = rtq_weight_type(l.w);
   const bool dense = wt == RTQ_TYPE_F32 || wt == RTQ_TYPE_TQ8_0;
+  if (sw_done) *sw_done = false;
   if (jobs && m->lora_batch && !dense && l.rank > 0 && jobs->size() < RTQ_LORA_JOBS) {
     const RankBlocks rb = rank_blocks(l);
     LoraGradArgs job{};
     M_TRY(rtq_linear_backward_defer_d(m->ctx, l.w, &lv, l.nm < 2 ? nullptr : &rb, x, dy, t, dx, l.ga, l.gb, l.hpk,
-                                      m->lg_h[(size_t)gi], m->lg_g[(size_t)gi], &job, stream_of(m)));
+                                      m->lg_h[(size_t)gi], m->lg_g[(size_t)gi], &job, stream_of(m), sw));
     jobs->push_back(job);
+    if (sw_done) *sw_done = sw != nullptr;
     return RTQ_OK;
   }
   if (l.rank == 0 || dense)
@@ -831,12 +835,15 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
   const float scale = 1.0f / sqrtf((float)hd);
   // Mlp::backward (src/model.rs:120-133)
   std::vector<LoraGradArgs> jobs;  // this block's dA / dB, launched together before its last kernel
-  M_TRY(lin_bwd(m, L, L.gi[LDOWN], k.hm, dy, t, m->dhm, &jobs));
   float *g, *u, *dg, *du;
   int64_t ldg;
   gu_view(m, L, k.gu, t, &g, &u, &ldg);
   gu_view(m, L, m->dgu, t, &dg, &du, &ldg);
-  M_TRY(k_elt2(m, KM_SWIGLU_BWD, g, u, m->dhm, dg, du, t, c.n_ff, ldg, c.n_ff, ldg));
+  // dhm's SwiGLU backward in the down projection's dx finish (dhm itself kept for a captured layer)
+  const SwiGluBwd sw{g, u, dg, du, ldg, l == m->dbg_layer};
+  bool sw_done = false;
+  M_TRY(lin_bwd(m, L, L.gi[LDOWN], k.hm, dy, t, m->dhm, &jobs, &sw, &sw_done));
+  if (!sw_done) M_TRY(k_elt2(m, KM_SWIGLU_BWD, g, u, m->dhm, dg, du, t, c.n_ff, ldg, c.n_ff, ldg));
   if (L.gu_fused) {
     M_TRY(lin_bwd(m, L, L.gi[LGATE], k.n2, m->dgu, t, m->dn2, &jobs));  // dgate.Wg + dup.Wu in one pass
   } else {

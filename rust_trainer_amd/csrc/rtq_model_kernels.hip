@@ -23,16 +23,9 @@ __device__ __forceinline__ float m_round_f16(float x) {
   return __uint_as_float(sign | __float_as_uint(r));
 }
 
-__device__ __forceinline__ float m_sigmoid(float x) {
-  if (x >= 0.0f) return __fdiv_rn(1.0f, 1.0f + expf(-x));
-  const float e = expf(x);
-  return __fdiv_rn(e, 1.0f + e);
-}
+__device__ __forceinline__ float m_sigmoid(float x) { return rtq_sigmoid(x); }
 __device__ __forceinline__ float m_silu(float x) { return rtq_silu(x); }
-__device__ __forceinline__ float m_silu_grad(float x) {
-  const float s = m_sigmoid(x);
-  return s * (1.0f + x * (1.0f - s));
-}
+__device__ __forceinline__ float m_silu_grad(float x) { return rtq_silu_grad(x); }
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -713,6 +713,7 @@ struct LoraDefer {
   float* h;
   float* g;
   LoraGradArgs* job;
+  const SwiGluBwd* sw;  // or null: the finish applies SwiGLU's backward to dx instead of storing it
 };
 rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, int64_t t, float* dx, bool accumulate,
                             const float* x, const float* la, const float* lb, int64_t r, float s, float* ga,
@@ -781,6 +782,14 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
     defer->job->part = nullptr;
     fa.n_gb = fa.n_ga = 0;
     fa.n_dx = dp.tok16 ? (int)cdiv(t * cdiv(K, 64), 4) : (int)cdiv((w->Kp / 128) * cdiv(t, 64) * 32, 4);
+    if (defer->sw) {
+      fa.swg = defer->sw->g;
+      fa.swu = defer->sw->u;
+      fa.swdg = defer->sw->dg;
+      fa.swdu = defer->sw->du;
+      fa.swld = defer->sw->ld;
+      fa.sw_keep = defer->sw->keep_dh ? 1 : 0;
+    }
     return launch(c, K_BWD_FINISH, dim3((unsigned)fa.n_dx), dim3(256), st, fa);
   }
   return launch(c, nw == 16 ? K_BWD_FINISH16 : K_BWD_FINISH, dim3((unsigned)(fa.n_gb + fa.n_ga + fa.n_dx)),
@@ -1791,13 +1800,15 @@ rtq_status rtq_linear_forward_ws_d(rtq_ctx* c, const rtq_weight* w, const float*
 rtq_status rtq_linear_backward_defer_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const RankBlocks* rb,
                                        const float* x, const float* dy, int64_t t, float* dx, float* ga, float* gb,
                                        const float* hp_have, float* h_out, float* g_out, LoraGradArgs* job,
-                                       void* stream) {
+                                       void* stream, const SwiGluBwd* sw) {
   RTQ_TRY(check_weight(c, w));
   RTQ_TRY(check_blocks(w, lora, rb));
   if (!job || !h_out || !g_out) return fail(RTQ_ERR_INVALID, "deferred backward needs h, g and a job");
+  if (sw && (!sw->g || !sw->u || !sw->dg || !sw->du || sw->ld < w->cols))
+    return fail(RTQ_ERR_INVALID, "SwiGLU backward: null g/u/dg/du or rows shorter than cols");
   if (is_dense(w->type)) return fail(RTQ_ERR_INVALID, "deferred backward: quantised weights only");
   if (hp_have && rtq_lora_partial_floats(w, t, lora && lora->enabled ? lora->rank : 0) == 0) hp_have = nullptr;
-  const LoraDefer df{h_out, g_out, job};
+  const LoraDefer df{h_out, g_out, job, sw};
   return linear_backward_d(c, w, lora, x, dy, t, dx, ga, gb, stream, rb, hp_have, &df);
 }
 
