@@ -273,6 +273,7 @@ struct MNormArgs {
   int rows, d;
   float eps, off;
   int fused;         // 1: x * (ir * (w + off)) (QK-norm order), 0: (x * ir) * (w + off)
+  int wave;          // 1: one wave per row, four rows per workgroup (d % 256 == 0, d <= 2048, 16-byte aligned rows)
 };
 
 struct MNormBwdArgs {
@@ -284,6 +285,7 @@ struct MNormBwdArgs {
   float* out;        // [rows x d]
   int rows, d;
   float off;
+  int wave;          // as MNormArgs::wave
 };
 
 // per (token, head) row of width hd: QK-norm, RoPE, f16 rounding of K and V

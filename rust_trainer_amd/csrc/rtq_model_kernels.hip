@@ -40,8 +40,47 @@ __device__ __forceinline__ float wave_sum(float v) {
 // 512-token step); longer rows stream twice.  (The same in the forward measured slower: 342 -> 382.)
 constexpr int RTQ_NORM_NPT = 16;
 
-// grid rows, 256 threads: y = rmsnorm(a (+ b)); with b, h = a + b is written too
+// wave-per-row layout: lane l takes the float4 columns 4 l + 256 i (i < d / 256, at most 8)
+constexpr int RTQ_NORM_WV = 8;
+
+// grid rows (wave: rows / 4), 256 threads: y = rmsnorm(a (+ b)); with b, h = a + b is written too
 extern "C" __global__ __launch_bounds__(256) void rtq_m_rmsnorm(MNormArgs a) {
+  if (a.wave) {  // one wave per row: no workgroup barrier, every load issued at once
+    const int r = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63, nv = a.d / 256;
+    if (r >= a.rows) return;
+    const int64_t ro = (int64_t)r * a.d + 4 * lane;
+    f4 xv[RTQ_NORM_WV], wv[RTQ_NORM_WV];
+#pragma unroll
+    for (int i = 0; i < RTQ_NORM_WV; i++)
+      if (i < nv) {
+        xv[i] = *reinterpret_cast<const f4*>(a.a + ro + 256 * i);
+        wv[i] = *reinterpret_cast<const f4*>(a.w + 4 * lane + 256 * i);
+        if (a.b) xv[i] += *reinterpret_cast<const f4*>(a.b + ro + 256 * i);
+      }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RTQ_NORM_WV; i++)
+      if (i < nv) {
+        if (a.b) *reinterpret_cast<f4*>(a.h + ro + 256 * i) = xv[i];
+#pragma unroll
+        for (int e = 0; e < 4; e++) s = s + xv[i][e] * xv[i][e];
+      }
+    s = wave_sum(s);
+    const float ir = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(s, (float)a.d) + a.eps));
+#pragma unroll
+    for (int i = 0; i < RTQ_NORM_WV; i++)
+      if (i < nv) {
+        f4 y;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float x = xv[i][e], wo = wv[i][e] + a.off;
+          y[e] = a.fused ? x * (ir * wo) : (x * ir) * wo;
+        }
+        *reinterpret_cast<f4*>(a.y + ro + 256 * i) = y;
+      }
+    if (lane == 0) a.inv[r] = ir;
+    return;
+  }
   __shared__ float red[4];
   const int r = blockIdx.x, tid = threadIdx.x;
   const float* ar = a.a + (int64_t)r * a.d;
@@ -67,8 +106,45 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_rmsnorm(MNormArgs a) {
   if (tid == 0) a.inv[r] = ir;
 }
 
-// grid rows, 256 threads: out = (res +) rmsnorm_backward(x, w, inv, dy)
+// grid rows (wave: rows / 4), 256 threads: out = (res +) rmsnorm_backward(x, w, inv, dy)
 extern "C" __global__ __launch_bounds__(256) void rtq_m_rmsnorm_bwd(MNormBwdArgs a) {
+  if (a.wave) {  // one wave per row, as the forward
+    const int r = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63, nv = a.d / 256;
+    if (r >= a.rows) return;
+    const int64_t ro = (int64_t)r * a.d + 4 * lane;
+    const float ir = a.inv[r];
+    f4 xv[RTQ_NORM_WV], gv[RTQ_NORM_WV], rv[RTQ_NORM_WV];
+#pragma unroll
+    for (int i = 0; i < RTQ_NORM_WV; i++)
+      if (i < nv) {
+        xv[i] = *reinterpret_cast<const f4*>(a.x + ro + 256 * i);
+        const f4 dv = *reinterpret_cast<const f4*>(a.dy + ro + 256 * i);
+        const f4 wv = *reinterpret_cast<const f4*>(a.w + 4 * lane + 256 * i);
+#pragma unroll
+        for (int e = 0; e < 4; e++) gv[i][e] = dv[e] * (wv[e] + a.off);
+        if (a.res) rv[i] = *reinterpret_cast<const f4*>(a.res + ro + 256 * i);
+      }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RTQ_NORM_WV; i++)
+      if (i < nv)
+#pragma unroll
+        for (int e = 0; e < 4; e++) s = s + gv[i][e] * xv[i][e];
+    s = wave_sum(s);
+    const float c = __fdiv_rn(((s * ir) * ir) * ir, (float)a.d);
+#pragma unroll
+    for (int i = 0; i < RTQ_NORM_WV; i++)
+      if (i < nv) {
+        f4 o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float v = gv[i][e] * ir - xv[i][e] * c;
+          o[e] = a.res ? rv[i][e] + v : v;
+        }
+        *reinterpret_cast<f4*>(a.out + ro + 256 * i) = o;
+      }
+    return;
+  }
   __shared__ float red[4];
   const int r = blockIdx.x, tid = threadIdx.x;
   const float* xr = a.x + (int64_t)r * a.d;
