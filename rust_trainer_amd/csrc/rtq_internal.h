@@ -87,6 +87,10 @@ rtq_status rtq_linear_backward_defer_d(rtq_ctx* c, const rtq_weight* w, const rt
                                        void* stream, const SwiGluBwd* sw = nullptr);
 // dA / dB of n (<= RTQ_LORA_JOBS) deferred linears in one launch (jobs with no tiles are skipped)
 rtq_status rtq_lora_grads_d(rtq_ctx* c, const LoraGradArgs* jobs, int n, void* stream);
+// the dA / dB tiles of a job table already in device memory: workgroup b runs tile map_d[2 b + 1] of
+// job map_d[2 b] (nwg workgroups; w16: 16 waves per workgroup, for token counts of 256 and more)
+rtq_status rtq_lora_grads_table_d(rtq_ctx* c, const LoraGradArgs* jobs_d, const int* map_d, int64_t nwg, bool w16,
+                                  void* stream);
 // rtq_noalloc.hip: resolves the no-allocation scratch array's address on `device` (current)
 rtq_status rtq_scratch_setup(int device);
 // rtq_linear_forward_d with the caller's workspace ws (ws_bytes) instead of the context's: never

@@ -219,6 +219,13 @@ struct LoraGradBatch {
   LoraGradArgs job[RTQ_LORA_JOBS];
 };
 
+// dA / dB tiles of any number of linears from a job table in device memory (rtq_lora_grads_t[16]):
+// workgroup b runs tile map[2 b + 1] of job map[2 b] (its gb tiles, then its ga tiles)
+struct LoraGradTable {
+  const LoraGradArgs* job;
+  const int* map;
+};
+
 // rows [r0, r0+count) dequantised to f32 (bit-exact ggml dequant)
 struct RowArgs {
   const void* wq;

@@ -2426,6 +2426,21 @@ __device__ __forceinline__ void lora_grads(const LoraGradBatch& B) {
 
 extern "C" __global__ __launch_bounds__(256) void rtq_lora_grads(LoraGradBatch b) { lora_grads<4>(b); }
 extern "C" __global__ __launch_bounds__(1024) void rtq_lora_grads16(LoraGradBatch b) { lora_grads<16>(b); }
+
+// the same over a device job table (a whole step's adapted linears in one launch)
+template <int NW>
+__device__ __forceinline__ void lora_grads_t(const LoraGradTable& T) {
+  __shared__ float red[NW * 64 * 17];
+  const int b = blockIdx.x;
+  const int j = __builtin_amdgcn_readfirstlane(T.map[2 * b]), lb = __builtin_amdgcn_readfirstlane(T.map[2 * b + 1]);
+  const LoraGradArgs a = T.job[j];
+  if (lb < a.n_gb)
+    lora_grad_tile<NW, 4, true>(a, lb, red);
+  else if (lb < a.n_gb + a.n_ga)
+    lora_grad_tile<NW, 4, false>(a, lb - a.n_gb, red);
+}
+extern "C" __global__ __launch_bounds__(256) void rtq_lora_grads_t(LoraGradTable t) { lora_grads_t<4>(t); }
+extern "C" __global__ __launch_bounds__(1024) void rtq_lora_grads_t16(LoraGradTable t) { lora_grads_t<16>(t); }
 extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a) { bwd_finish<4, 4>(a); }
 extern "C" __global__ __launch_bounds__(1024) void rtq_bwd_finish16(LoraGradArgs a) { bwd_finish<16, 4>(a); }
 

@@ -80,6 +80,10 @@ struct Layer {
 struct Cache {
   float *n1, *inv1, *qkv, *q, *k, *v, *q_inv, *k_inv, *P, *o, *h, *n2, *inv2, *gu, *hm;
   float* lse;  // fused attention: log-sum-exp per (head, query) [nh x t] (P is then not kept)
+  // with the step's dA / dB deferred to its end (defer_lg): the block's gradients that those read -
+  // of gate | up, q | k | v, the attention output's residual branch and the block input - kept
+  // per layer (null otherwise: the step-wide buffers are reused block after block)
+  float *dgu = nullptr, *dqkv = nullptr, *dh = nullptr, *gx = nullptr;
 };
 
 // SplitMix64 + uniform of the reference Rng (src/tensor.rs:155-180)
@@ -120,8 +124,19 @@ struct rtq_model {
   // lora_batch false (RTQ_LORA_BATCH=0 at load time): dA / dB launched per linear, for comparison
   void* lg_mem = nullptr;
   size_t lg_cap = 0;
-  std::vector<float*> lg_h, lg_g;
+  std::vector<float*> lg_h, lg_g;  // slot (layer if deferring, else 0) * lg_groups + group
+  int64_t lg_groups = 0;
   bool lora_batch = true;
+  // defer_lg: every block's dA / dB left to one launch after the backward (their inputs kept per
+  // layer: h / g slots per (layer, group), Cache gradient buffers), where the activations are kept
+  // and the per-layer gradients fit a budget; RTQ_LORA_DEFER=0 at load time keeps per-block launches.
+  // The job table and its workgroup map live in device memory, uploaded when they change.
+  bool lora_defer = true, defer_lg = false;
+  int64_t layout_defer = -1;  // defer_lg the step buffers were laid out for
+  std::vector<LoraGradArgs> lg_all;
+  void *lgt_mem = nullptr, *lgt_host = nullptr;
+  size_t lgt_cap = 0, lgt_bytes = 0;
+  std::vector<uintptr_t> lgt_key;  // the jobs' pointers and sizes when the table was last uploaded
   float *X = nullptr, *cos_ = nullptr, *sin_ = nullptr;
   std::vector<Cache> cache;
   int64_t cache_cap = 0;      // Cache sets allocated (n_layer when keeping, 1 when recomputing)
@@ -362,8 +377,9 @@ rtq_status lin_bwd(rtq_model* m, const Layer& L, int gi, const float* x, const f
   if (jobs && m->lora_batch && !dense && l.rank > 0 && jobs->size() < RTQ_LORA_JOBS) {
     const RankBlocks rb = rank_blocks(l);
     LoraGradArgs job{};
+    const size_t slot = (size_t)(m->defer_lg ? &L - m->layers.data() : 0) * (size_t)m->lg_groups + (size_t)gi;
     M_TRY(rtq_linear_backward_defer_d(m->ctx, l.w, &lv, l.nm < 2 ? nullptr : &rb, x, dy, t, dx, l.ga, l.gb, l.hpk,
-                                      m->lg_h[(size_t)gi], m->lg_g[(size_t)gi], &job, stream_of(m), sw));
+                                      m->lg_h[slot], m->lg_g[slot], &job, stream_of(m), sw));
     jobs->push_back(job);
     if (sw_done) *sw_done = sw != nullptr;
     return RTQ_OK;
@@ -422,8 +438,10 @@ rtq_status ensure_lgrad(rtq_model* m, int64_t t) {
     if (rmax.size() < L.groups.size()) rmax.resize(L.groups.size(), 0);
     for (size_t i = 0; i < L.groups.size(); i++) rmax[i] = std::max(rmax[i], L.groups[i].rank);
   }
-  size_t need = 0;
-  for (int64_t r : rmax) need += ((size_t)(2 * t * r) * 4 + 255) / 256 * 256;
+  const int64_t nl = m->defer_lg ? m->cfg.n_layer : 1;  // slot sets: one per layer when deferring
+  size_t per = 0;
+  for (int64_t r : rmax) per += ((size_t)(2 * t * r) * 4 + 255) / 256 * 256;
+  const size_t need = per * (size_t)nl;
   if (need > m->lg_cap) {
     if (m->lg_mem) {
       M_HIP(hipStreamSynchronize(stream_of(m)));
@@ -434,14 +452,16 @@ rtq_status ensure_lgrad(rtq_model* m, int64_t t) {
     M_HIP(hipMalloc(&m->lg_mem, need));
     m->lg_cap = need;
   }
-  m->lg_h.assign(rmax.size(), nullptr);
-  m->lg_g.assign(rmax.size(), nullptr);
+  m->lg_groups = (int64_t)rmax.size();
+  m->lg_h.assign((size_t)nl * rmax.size(), nullptr);
+  m->lg_g.assign((size_t)nl * rmax.size(), nullptr);
   char* p = (char*)m->lg_mem;
-  for (size_t i = 0; i < rmax.size(); i++) {
-    m->lg_h[i] = (float*)p;
-    m->lg_g[i] = (float*)p + t * rmax[i];
-    p += ((size_t)(2 * t * rmax[i]) * 4 + 255) / 256 * 256;
-  }
+  for (int64_t l = 0; l < nl; l++)
+    for (size_t i = 0; i < rmax.size(); i++) {
+      m->lg_h[(size_t)l * rmax.size() + i] = (float*)p;
+      m->lg_g[(size_t)l * rmax.size() + i] = (float*)p + t * rmax[i];
+      p += ((size_t)(2 * t * rmax[i]) * 4 + 255) / 256 * 256;
+    }
   return RTQ_OK;
 }
 
@@ -472,6 +492,7 @@ size_t step_layout(rtq_model* dst, int64_t T, int64_t N, int64_t caches, uintptr
     fl(&k.v, T * kd), fl(&k.q_inv, T * c.n_head), fl(&k.k_inv, T * c.n_head_kv), fl(&k.P, att), fl(&k.o, T * qd);
     fl(&k.h, T * d), fl(&k.n2, T * d), fl(&k.inv2, T), fl(&k.gu, T * 2 * ff), fl(&k.hm, T * ff);
     fl(&k.lse, fz ? c.n_head * T : 1);
+    if (dst->defer_lg) fl(&k.dgu, T * 2 * ff), fl(&k.dqkv, T * (qd + 2 * kd)), fl(&k.dh, T * d), fl(&k.gx, T * d);
   }
   fl(&dst->attn_D, fz ? c.n_head * T : 1);
   fl(&dst->dY, T * d), fl(&dst->dX, T * d), fl(&dst->mo, T * d), fl(&dst->f, T * d), fl(&dst->dhm, T * ff);
@@ -509,9 +530,28 @@ rtq_status choose_ckpt(rtq_model* m, int64_t t, int64_t n) {
   return RTQ_OK;
 }
 
+// whether this step defers every block's dA / dB to one launch after the backward: activations
+// kept, some adapter attached, and the per-layer gradient buffers within min(4 GiB, free / 4)
+rtq_status choose_defer(rtq_model* m, int64_t t) {
+  const rtq_model_config& c = m->cfg;
+  bool adapted = false;
+  for (const Layer& L : m->layers)
+    for (const Group& g : L.groups) adapted = adapted || g.rank > 0;
+  m->defer_lg = false;
+  if (m->ckpt || !m->lora_batch || !m->lora_defer || !adapted || c.n_layer < 2) return RTQ_OK;
+  const int64_t T = std::max(t, m->t_cap), qd = c.n_head * c.head_dim, kd = c.n_head_kv * c.head_dim;
+  const size_t extra = (size_t)c.n_layer * (size_t)T * (size_t)(2 * c.n_ff + qd + 2 * kd + 2 * c.n_embd) * 4;
+  size_t free_b = 0, total_b = 0;
+  M_HIP(hipMemGetInfo(&free_b, &total_b));
+  const size_t held = m->layout_defer == 1 ? extra : 0;  // already allocated: counts as free
+  m->defer_lg = extra <= std::min<size_t>((size_t)4 << 30, (free_b + held) / 4);
+  return RTQ_OK;
+}
+
 rtq_status ensure_step(rtq_model* m, int64_t t, int64_t n) {
   const int64_t caches = m->ckpt ? 1 : m->cfg.n_layer;
-  if (t <= m->t_cap && n <= m->n_cap && caches == m->cache_cap && m->layout_fused == (int64_t)m->attn_fused)
+  if (t <= m->t_cap && n <= m->n_cap && caches == m->cache_cap && m->layout_fused == (int64_t)m->attn_fused &&
+      m->layout_defer == (int64_t)m->defer_lg)
     return RTQ_OK;
   const int64_t T = std::max(t, m->t_cap), N = std::max<int64_t>(std::max(n, m->n_cap), 1);
   if (m->step_mem) {
@@ -527,6 +567,7 @@ rtq_status ensure_step(rtq_model* m, int64_t t, int64_t n) {
   m->n_cap = N;
   m->cache_cap = caches;
   m->layout_fused = m->attn_fused;
+  m->layout_defer = m->defer_lg;
   m->rope_t = -1;
   return RTQ_OK;
 }
@@ -760,9 +801,63 @@ QkvView qkv_view(const rtq_model* m, const Layer& L, float* base, int64_t t) {
   return QkvView{base, base + t * qd, base + t * (qd + kd), qd, kd, kd};
 }
 
+// a block's gradient buffers: its own (deferred dA / dB) or the step-wide ones
+float* g_dqkv(rtq_model* m, const Cache& k) { return k.dqkv ? k.dqkv : m->dqkv; }
+float* g_dgu(rtq_model* m, const Cache& k) { return k.dgu ? k.dgu : m->dgu; }
+float* g_dh(rtq_model* m, const Cache& k) { return k.dh ? k.dh : m->dh; }
+
+// the deferred dA / dB of the whole step in one launch: the job table and its workgroup map
+// (job, tile) are uploaded to device memory when the jobs differ from the last upload (a new
+// shape; a captured or replayed step reuses the table)
+rtq_status lora_grads_all(rtq_model* m) {
+  std::vector<LoraGradArgs> jobs;
+  std::vector<int> map;
+  std::vector<uintptr_t> key;
+  int64_t tmax = 0;
+  for (const LoraGradArgs& j : m->lg_all) {
+    const int n = j.n_gb + j.n_ga;
+    if (n == 0) continue;
+    const int ji = (int)jobs.size();
+    jobs.push_back(j);
+    for (int b = 0; b < n; b++) {
+      map.push_back(ji);
+      map.push_back(b);
+    }
+    tmax = std::max<int64_t>(tmax, j.T);
+    for (uintptr_t v : {(uintptr_t)j.dy, (uintptr_t)j.h, (uintptr_t)j.g, (uintptr_t)j.x, (uintptr_t)j.la,
+                        (uintptr_t)j.gb, (uintptr_t)j.ga, (uintptr_t)j.T, (uintptr_t)j.N, (uintptr_t)j.K,
+                        (uintptr_t)j.r, (uintptr_t)j.n_gb, (uintptr_t)j.n_ga, (uintptr_t)__builtin_bit_cast(uint32_t, j.s)})
+      key.push_back(v);
+  }
+  m->lg_all.clear();
+  if (jobs.empty()) return RTQ_OK;
+  const size_t jb = (jobs.size() * sizeof(LoraGradArgs) + 255) / 256 * 256, bytes = jb + map.size() * sizeof(int);
+  hipStream_t st = stream_of(m);
+  if (bytes > m->lgt_cap) {
+    M_HIP(hipStreamSynchronize(st));
+    if (m->lgt_mem) M_HIP(hipFree(m->lgt_mem));
+    if (m->lgt_host) M_HIP(hipHostFree(m->lgt_host));
+    m->lgt_mem = m->lgt_host = nullptr;
+    m->lgt_cap = 0;
+    M_HIP(hipMalloc(&m->lgt_mem, bytes));
+    M_HIP(hipHostMalloc(&m->lgt_host, bytes));
+    m->lgt_cap = bytes;
+    m->lgt_key.clear();
+  }
+  if (key != m->lgt_key) {
+    M_HIP(hipStreamSynchronize(st));  // an earlier upload may still read the staging buffer
+    std::memcpy(m->lgt_host, jobs.data(), jobs.size() * sizeof(LoraGradArgs));
+    std::memcpy((char*)m->lgt_host + jb, map.data(), map.size() * sizeof(int));
+    M_HIP(hipMemcpyAsync(m->lgt_mem, m->lgt_host, bytes, hipMemcpyHostToDevice, st));
+    m->lgt_key = key;
+  }
+  return rtq_lora_grads_table_d(m->ctx, (const LoraGradArgs*)m->lgt_mem, (const int*)((char*)m->lgt_mem + jb),
+                                (int64_t)(map.size() / 2), tmax >= 256, st);
+}
+
 MQkArgs qk_args(rtq_model* m, const Layer& L, Cache& k, int64_t t) {
   const rtq_model_config& c = m->cfg;
-  const QkvView x = qkv_view(m, L, k.qkv, t), dx = qkv_view(m, L, m->dqkv, t);
+  const QkvView x = qkv_view(m, L, k.qkv, t), dx = qkv_view(m, L, g_dqkv(m, k), t);
   return MQkArgs{x.q,   x.k,   x.v,   L.q_norm, L.k_norm, m->cos_,          m->sin_,          k.q,
                  k.k,   k.v,   k.q_inv, k.k_inv, m->dq,     m->dk,            dx.q,             dx.k,
                  (int)t, (int)c.n_head, (int)c.n_head_kv, (int)c.head_dim, (int)c.rope_dim, c.rope_neox,
@@ -841,27 +936,30 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
   const int64_t qd = nh * hd, kd = nkv * hd;
   const float scale = 1.0f / sqrtf((float)hd);
   // Mlp::backward (src/model.rs:120-133)
-  std::vector<LoraGradArgs> jobs;  // this block's dA / dB, launched together before its last kernel
+  std::vector<LoraGradArgs> jobs;  // this block's dA / dB: launched before its last kernel, or deferred
+  float* const dgu = g_dgu(m, k);
+  float* const dqkv = g_dqkv(m, k);
+  float* const dh = g_dh(m, k);
   float *g, *u, *dg, *du;
   int64_t ldg;
   gu_view(m, L, k.gu, t, &g, &u, &ldg);
-  gu_view(m, L, m->dgu, t, &dg, &du, &ldg);
+  gu_view(m, L, dgu, t, &dg, &du, &ldg);
   // dhm's SwiGLU backward in the down projection's dx finish (dhm itself kept for a captured layer)
   const SwiGluBwd sw{g, u, dg, du, ldg, l == m->dbg_layer};
   bool sw_done = false;
   M_TRY(lin_bwd(m, L, L.gi[LDOWN], k.hm, dy, t, m->dhm, &jobs, &sw, &sw_done));
   if (!sw_done) M_TRY(k_elt2(m, KM_SWIGLU_BWD, g, u, m->dhm, dg, du, t, c.n_ff, ldg, c.n_ff, ldg));
   if (L.gu_fused) {
-    M_TRY(lin_bwd(m, L, L.gi[LGATE], k.n2, m->dgu, t, m->dn2, &jobs));  // dgate.Wg + dup.Wu in one pass
+    M_TRY(lin_bwd(m, L, L.gi[LGATE], k.n2, dgu, t, m->dn2, &jobs));  // dgate.Wg + dup.Wu in one pass
   } else {
     M_TRY(lin_bwd(m, L, L.gi[LGATE], k.n2, dg, t, m->dn2, &jobs));
     M_TRY(lin_bwd(m, L, L.gi[LUP], k.n2, du, t, m->dxu, &jobs));
     M_TRY(k_elt(m, KM_ADD, m->dn2, m->dxu, nullptr, m->dn2, nullptr, t * d));
   }
-  M_TRY(k_norm_bwd(m, k.h, L.ffn_norm, k.inv2, m->dn2, dy, m->dh, t, d));  // dh = dy + rmsnorm_backward
+  M_TRY(k_norm_bwd(m, k.h, L.ffn_norm, k.inv2, m->dn2, dy, dh, t, d));  // dh = dy + rmsnorm_backward
   // Attention::backward (src/attention.rs:243-355)
-  M_TRY(lin_bwd(m, L, L.gi[LO], k.o, m->dh, t, m->d_o, &jobs));
-  const QkvView dv = qkv_view(m, L, m->dqkv, t);
+  M_TRY(lin_bwd(m, L, L.gi[LO], k.o, dh, t, m->d_o, &jobs));
+  const QkvView dv = qkv_view(m, L, dqkv, t);
   if (m->attn_fused) {  // D = dO . o; dq over key tiles; dk, dv over (group head, query tile) pairs
     MAttnArgs aa = attn_args(m, k, t);
     aa.dO = m->d_o;
@@ -904,7 +1002,7 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
   const MQkArgs qa = qk_args(m, L, k, t);
   M_TRY(rtq_model_launch(m->ctx, KM_QK_BWD, dim3((unsigned)((t * (nh + nkv) + 3) / 4)), dim3(256), stream_of(m), &qa));
   if (L.qkv_fused) {
-    M_TRY(lin_bwd(m, L, L.gi[LQ], k.n1, m->dqkv, t, m->dn1, &jobs));  // dq.Wq + dk.Wk + dv.Wv in one pass
+    M_TRY(lin_bwd(m, L, L.gi[LQ], k.n1, dqkv, t, m->dn1, &jobs));  // dq.Wq + dk.Wk + dv.Wv in one pass
   } else {
     M_TRY(lin_bwd(m, L, L.gi[LQ], k.n1, dv.q, t, m->dn1, &jobs));
     M_TRY(lin_bwd(m, L, L.gi[LK], k.n1, dv.k, t, m->dxk, &jobs));
@@ -914,8 +1012,11 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
   // every input of the deferred dA / dB (dy, x of each linear, the h / g slots) is still intact here.
   // (Run on a second stream, overlapping the next block's backward, the batch measured slower:
   // 13.79 against 13.45 ms per configs[2] step - its workgroups hold CUs the next dx kernels need.)
-  M_TRY(rtq_lora_grads_d(m->ctx, jobs.data(), (int)jobs.size(), stream_of(m)));
-  return k_norm_bwd(m, x, L.attn_norm, k.inv1, m->dn1, m->dh, dx, t, d);  // dx = dh + rmsnorm_backward
+  if (m->defer_lg)  // every input (dy, x of each linear, the layer's h / g slots) stays intact to the end
+    m->lg_all.insert(m->lg_all.end(), jobs.begin(), jobs.end());
+  else
+    M_TRY(rtq_lora_grads_d(m->ctx, jobs.data(), (int)jobs.size(), stream_of(m)));
+  return k_norm_bwd(m, x, L.attn_norm, k.inv1, m->dn1, dh, dx, t, d);  // dx = dh + rmsnorm_backward
 }
 
 // ---------------------------------------------------------------- debug capture
@@ -984,16 +1085,17 @@ rtq_status dbg_backward(rtq_model* m, int l, int64_t t, const float* dy, const f
   const rtq_model_config& c = m->cfg;
   const Layer& L = m->layers[(size_t)l];
   const int64_t d = c.n_embd, qd = c.n_head * c.head_dim, kd = c.n_head_kv * c.head_dim, ff = c.n_ff;
-  const QkvView dv = qkv_view(m, L, m->dqkv, t);
+  Cache& k = m->cache[m->ckpt ? 0 : (size_t)l];
+  const QkvView dv = qkv_view(m, L, g_dqkv(m, k), t);
   float *dg, *du;
   int64_t ldg;
-  gu_view(m, L, m->dgu, t, &dg, &du, &ldg);
+  gu_view(m, L, g_dgu(m, k), t, &dg, &du, &ldg);
   M_TRY(dbg_put(m, "dy", dy, t, d, d));
   M_TRY(dbg_put(m, "dhm", m->dhm, t, ff, ff));
   M_TRY(dbg_put(m, "dgate", dg, t, ff, ldg));
   M_TRY(dbg_put(m, "dup", du, t, ff, ldg));
   M_TRY(dbg_put(m, "dn2", m->dn2, t, d, d));
-  M_TRY(dbg_put(m, "dh", m->dh, t, d, d));
+  M_TRY(dbg_put(m, "dh", g_dh(m, k), t, d, d));
   M_TRY(dbg_put(m, "d_o", m->d_o, t, qd, qd));
   if (!m->attn_fused) M_TRY(dbg_put(m, "dS", m->dP, c.n_head * t, t, t));
   M_TRY(dbg_put(m, "dq", m->dq, t, qd, qd));
@@ -1207,6 +1309,7 @@ rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out)
   if (const char* e = getenv("RTQ_ATTN_F32")) m->attn_f32 = atoi(e) != 0;
   if (const char* e = getenv("RTQ_ATTN_ITEMS")) m->attn_items = std::max(0, atoi(e));
   if (const char* e = getenv("RTQ_LORA_BATCH")) m->lora_batch = atoi(e) != 0;
+  if (const char* e = getenv("RTQ_LORA_DEFER")) m->lora_defer = atoi(e) != 0;
   m->ctx = ctx;
   m->cfg = cfg;
   m->rope_factors = factors;
@@ -1250,6 +1353,8 @@ void rtq_model_destroy(rtq_model* m) {
   if (m->step_mem) (void)hipFree(m->step_mem);
   if (m->hpk_mem) (void)hipFree(m->hpk_mem);
   if (m->lg_mem) (void)hipFree(m->lg_mem);
+  if (m->lgt_mem) (void)hipFree(m->lgt_mem);
+  if (m->lgt_host) (void)hipHostFree(m->lgt_host);
   if (m->attn_mem) (void)hipFree(m->attn_mem);
   delete m;
 }
@@ -1482,6 +1587,7 @@ rtq_status step(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* p
   M_HIP(hipSetDevice(rtq_ctx_device_id(m->ctx)));
   m->attn_fused = m->attn_hd_ok && m->attn_mode != 0;
   M_TRY(choose_ckpt(m, t, n));
+  M_TRY(choose_defer(m, t));
   M_TRY(ensure_step(m, t, n));
   M_TRY(ensure_hpk(m, t));
   M_TRY(ensure_lgrad(m, t));
@@ -1511,14 +1617,21 @@ rtq_status step(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* p
     M_TRY(rtq_lm_head_d(m->ctx, m->head, m->out_norm, c.rms_eps, c.norm_offset, m->X + c.n_layer * t * d, t,
                         m->pos_d, m->tgt_d, weights ? m->wts_d : nullptr, n, m->logp_d, m->hit_d,
                         weights ? m->dY : nullptr, st));
-    if (weights)
+    if (weights) {
+      m->lg_all.clear();
       for (int64_t l = c.n_layer - 1; l >= 0; l--) {
         const float* x = m->X + l * t * d;
         if (m->ckpt) M_TRY(block_forward(m, (int)l, t, const_cast<float*>(x), m->f, false, false));  // recompute
-        M_TRY(block_backward(m, (int)l, t, x, m->dY, m->dX));
-        if (l == m->dbg_layer) M_TRY(dbg_backward(m, (int)l, t, m->dY, m->dX));
-        std::swap(m->dY, m->dX);
+        // deferring: each block's input gradient stays in its own buffer (the block below reads it
+        // as its dy, the deferred dB of its down projection at the end)
+        float* gy = m->defer_lg && l < c.n_layer - 1 ? m->cache[(size_t)l + 1].gx : m->dY;
+        float* gx = m->defer_lg ? m->cache[(size_t)l].gx : m->dX;
+        M_TRY(block_backward(m, (int)l, t, x, gy, gx));
+        if (l == m->dbg_layer) M_TRY(dbg_backward(m, (int)l, t, gy, gx));
+        if (!m->defer_lg) std::swap(m->dY, m->dX);
       }
+      if (m->defer_lg) M_TRY(lora_grads_all(m));
+    }
     std::vector<int32_t> hv((size_t)n);
     M_HIP(hipMemcpyAsync(logp, m->logp_d, (size_t)n * 4, hipMemcpyDeviceToHost, st));
     M_HIP(hipMemcpyAsync(hv.data(), m->hit_d, (size_t)n * 4, hipMemcpyDeviceToHost, st));

@@ -136,6 +136,8 @@ enum Kid {
   K_BWD_FINISH16,  // 16 waves per workgroup: long token reductions of dA / dB
   K_LORA_GRADS,    // dA / dB of several linears in one launch (4 / 16 waves per workgroup)
   K_LORA_GRADS16,
+  K_LORA_GRADS_T,    // the same from a device job table
+  K_LORA_GRADS_T16,
   K_DENSE_ROWS,    // trainer-native weights: rows / dequantisation, bias
   K_DENSE_BIAS,
   K_HEAD_NORM,   // LM head + cross-entropy (Model::head)
@@ -161,7 +163,7 @@ constexpr const char* kKernelNames[] = {
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
     "rtq_dxw_q4_0",         "rtq_dxw_q8_0",         "rtq_dxw_q4_k",         "rtq_dxw_q6_k",
-    "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_lora_grads",       "rtq_lora_grads16",
+    "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_lora_grads",       "rtq_lora_grads16",     "rtq_lora_grads_t",     "rtq_lora_grads_t16",
     "rtq_dense_rows",       "rtq_dense_bias",
     "rtq_head_norm",        "rtq_head_max",         "rtq_head_sum",         "rtq_head_grad",
     "rtq_head_norm_bwd",
@@ -1831,6 +1833,18 @@ rtq_status rtq_lora_grads_d(rtq_ctx* c, const LoraGradArgs* jobs, int n, void* s
   const bool w16 = tmax >= 256;  // 16 waves split long token ranges, as in rtq_bwd_finish16
   return launch(c, w16 ? K_LORA_GRADS16 : K_LORA_GRADS, dim3((unsigned)total), dim3(w16 ? 1024 : 256),
                 (hipStream_t)stream, b);
+}
+
+rtq_status rtq_lora_grads_table_d(rtq_ctx* c, const LoraGradArgs* jobs_d, const int* map_d, int64_t nwg, bool w16,
+                                  void* stream) {
+  if (!c) return fail(RTQ_ERR_INVALID, "null context");
+  if (nwg <= 0) return RTQ_OK;
+  if (!jobs_d || !map_d || nwg > INT32_MAX) return fail(RTQ_ERR_INVALID, "LoRA gradient table: null or too large");
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  const LoraGradTable tb{jobs_d, map_d};
+  return launch(c, w16 ? K_LORA_GRADS_T16 : K_LORA_GRADS_T, dim3((unsigned)nwg), dim3(w16 ? 1024 : 256),
+                (hipStream_t)stream, tb);
 }
 
 rtq_status rtq_linear_backward_blocks_d(rtq_ctx* c, const rtq_weight* w, const rtq_lora* lora, const RankBlocks* rb,
