@@ -2342,13 +2342,13 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
         av[u] = (kcol < a.K && j < a.r) ? y : 0.0f;
       }
     };
-    constexpr int MAXJ = 4;
+    constexpr int MAXJ = NW == 16 ? 2 : 4;  // (sixteen-wave workgroups hold 128 VGPRs per lane)
     const int nj = a.g ? (a.r + 15) / 16 : 0;
     float gv[MAXJ][4], av[MAXJ][4];
 #pragma unroll
     for (int jj = 0; jj < MAXJ; jj++)
       if (jj < nj) ga_ops(jj, gv[jj], av[jj]);
-    constexpr int MAXS = 16;  // partials loaded at once; more splits are summed 16 at a time
+    constexpr int MAXS = NW == 16 ? 8 : 16;  // partials loaded at once; more splits are summed MAXS at a time
     f4 ps = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int c0 = 0; c0 < a.nsplit; c0 += MAXS) {
       f4 v[MAXS];
