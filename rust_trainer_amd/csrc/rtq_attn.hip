@@ -1,7 +1,7 @@
 // rtq_attn.hip — pieces of the fused causal GQA attention of the training step (Attention::forward /
 // backward, src/attention.rs:187-235, :262-320) shared by the kernels of rtq_fa.hip: the mask
 // (causal; packed layouts: the segment rule and the 64 x 64 block liveness map), lane-group
-// reductions, D = dO . o per query row, and the merges of the partials that items covering part of
+// reductions, and the merges of the partials that items covering part of
 // a block's range leave in slots: a 16-row block's slots combined in slot order (deterministic).
 // Included by rtq_model_kernels.hip (one code object).
 
@@ -74,33 +74,6 @@ __device__ __forceinline__ void attn_merge_fwd(const MAttnArgs& a, const MAttnMe
 }
 
 // ------------------------------------------------------------------ backward
-// D[h][i] = sum_e dO[i][h][e] o[i][h][e]: one wave per (query, head)
-__device__ __forceinline__ void attn_bwd_d(const MAttnArgs& a) {
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (r >= (int64_t)a.t * a.nh) return;
-  const int i = (int)(r / a.nh), h = (int)(r % a.nh);
-  const float* d = a.dO + (int64_t)i * a.ldq + (int64_t)h * a.hd;
-  const float* o = a.o + (int64_t)i * a.ldq + (int64_t)h * a.hd;
-  float s = 0.0f;
-  if (a.hd <= 256) {  // loads together
-    float dv[4], ov[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int e = min(lane + 64 * u, a.hd - 1);
-      dv[u] = d[e];
-      ov[u] = o[e];
-    }
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-      if (lane + 64 * u < a.hd) s = s + dv[u] * ov[u];
-  } else {
-    for (int e = lane; e < a.hd; e += 64) s = s + d[e] * o[e];
-  }
-  s = wave_sum(s);
-  if (lane == 0) a.D[(int64_t)h * a.t + i] = s;
-}
-
 // sums of a block's partials in slot order, one thread per element e: dq (kv = false, 16 x hd) or
 // dk then dv (kv = true, 2 x 16 x hd)
 __device__ __forceinline__ void attn_merge_sum(const MAttnArgs& a, const MAttnMerge& mg, int e, bool kv) {
@@ -151,4 +124,3 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_attn_merge_bwd(MAttnArgs
     if (mi < a.n_merges && e < 16 * a.hd) attn_merge_sum(a, a.merges[mi], e, false);
   }
 }
-extern "C" __global__ __launch_bounds__(256) void rtq_m_attn_bwd_d(MAttnArgs a) { attn_bwd_d(a); }

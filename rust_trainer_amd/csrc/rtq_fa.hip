@@ -88,32 +88,7 @@ __device__ __forceinline__ void fa_store_nat_f16(const FaNat<HD>& s, uint16_t* P
 #pragma unroll
   for (int i = 0; i < FaNat<HD>::NF; i++) *reinterpret_cast<u2v*>(p + 4 * i) = fa_f16(s.v[i]);
 }
-// f16 hi / lo planes, natural, values times mul
-template <int HD, int LD>
-__device__ __forceinline__ void fa_store_nat_f16x2(const FaNat<HD>& s, float mul, uint16_t* Ph, uint16_t* Pl) {
-  const int o = (threadIdx.x >> 2) * LD + (threadIdx.x & 3) * (HD / 4);
-#pragma unroll
-  for (int i = 0; i < FaNat<HD>::NF; i++) {
-    u2v hi, lo;
-    fa_split_f16(mul == 1.0f ? s.v[i] : s.v[i] * mul, hi, lo);
-    *reinterpret_cast<u2v*>(Ph + o + 4 * i) = hi;
-    *reinterpret_cast<u2v*>(Pl + o + 4 * i) = lo;
-  }
-}
-// bf16 hi / lo planes, natural
-template <int HD, int LD>
-__device__ __forceinline__ void fa_store_nat_bf(const FaNat<HD>& s, uint16_t* Ph, uint16_t* Pl) {
-  const int o = (threadIdx.x >> 2) * LD + (threadIdx.x & 3) * (HD / 4);
-#pragma unroll
-  for (int i = 0; i < FaNat<HD>::NF; i++) {
-    uint32_t h[4], l[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) fa_split_bf(s.v[i][c], h[c], l[c]);
-    *reinterpret_cast<u2v*>(Ph + o + 4 * i) = u2v{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-    *reinterpret_cast<u2v*>(Pl + o + 4 * i) = u2v{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
-  }
-}
-// transposed stores [d][row] (row stride LD): f16 one plane, or bf16 hi / lo planes
+// transposed store [d][row] (row stride LD): f16 one plane
 template <int HD, int LD>
 __device__ __forceinline__ void fa_store_tr_f16(const FaTr<HD>& s, uint16_t* P) {
   constexpr int KPT = FaTr<HD>::KPT;
@@ -128,26 +103,6 @@ __device__ __forceinline__ void fa_store_tr_f16(const FaTr<HD>& s, uint16_t* P) 
       *reinterpret_cast<u2v*>(p) = u2v{fa_pk(s.v[0][c], s.v[1][c]), fa_pk(s.v[2][c], s.v[3][c])};
   }
 }
-template <int HD, int LD>
-__device__ __forceinline__ void fa_store_tr_bf(const FaTr<HD>& s, uint16_t* Ph, uint16_t* Pl) {
-  constexpr int KPT = FaTr<HD>::KPT;
-  const int kg = threadIdx.x / (HD / 4), d4 = threadIdx.x % (HD / 4);
-#pragma unroll
-  for (int c = 0; c < 4; c++) {
-    uint32_t h[KPT], l[KPT];
-#pragma unroll
-    for (int i = 0; i < KPT; i++) fa_split_bf(s.v[i][c], h[i], l[i]);
-    const int o = (4 * d4 + c) * LD + kg * KPT;
-    if constexpr (KPT == 8) {
-      *reinterpret_cast<u4v*>(Ph + o) = u4v{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-      *reinterpret_cast<u4v*>(Pl + o) = u4v{l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16)};
-    } else {
-      *reinterpret_cast<u2v*>(Ph + o) = u2v{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-      *reinterpret_cast<u2v*>(Pl + o) = u2v{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
-    }
-  }
-}
-
 // a 16 x 64 tile in MFMA output order (tv[j][i]: row 4 g + i, column 16 j + li) -> two 16-bit planes
 // [row][col] (stride 64 + kFaPad) of the wave: f16 hi / lo (HF) or bf16 hi / lo
 template <bool HF>
@@ -324,6 +279,129 @@ __device__ __forceinline__ void fa_fwd(const MAttnArgs& a, const MAttnItem& it, 
   }
 }
 
+// ------------------------------------------------------------------ backward operand planes
+// One workgroup per (16-token group, head) of q / dO / o (heads [0, nh)) or of k / v (kv heads
+// after them), 256 threads, in two independent parts (no barrier):
+//   natural planes and D = dO . o: thread -> token tid / 16 of the group, columns (tid % 16) HD / 16
+//     .. (rows past t not written: the readers clamp rows to t - 1);
+//   transposed planes: thread -> column d = tid / (256 / HD), tokens TPT (tid % (256 / HD)) .. of
+//     the group (TPT = HD / 16), read down the column (each load instruction of a wave covers whole
+//     row segments) and written as one TPT-half piece per plane (tokens past t zero).
+template <int HD>
+__device__ __forceinline__ void fa_bwd_prep(const MAttnArgs& a) {
+  constexpr int NC = HD / 16, TPT = HD / 16, TPD = 256 / HD;  // columns per thread; tokens per thread
+  const int tg = blockIdx.x, hb = blockIdx.y, tid = threadIdx.x;
+  const bool kvs = hb >= a.nh;
+  const int h = kvs ? hb - a.nh : hb, heads = kvs ? a.nkv : a.nh;
+  {  // natural planes (+ D)
+    const int t = tg * 16 + (tid >> 4), c0 = (tid & 15) * NC;
+    const bool in = t < a.t;
+    const int tc = min(t, a.t - 1);
+    const int64_t no = ((int64_t)t * heads + h) * HD + c0;
+    auto ld = [&](const float* X, int64_t ldx, float (&v)[NC]) {
+      const float* p = X + (int64_t)tc * ldx + (int64_t)h * HD + c0;
+#pragma unroll
+      for (int i = 0; i < NC; i += 4) {
+        const f4 q = *reinterpret_cast<const f4*>(p + i);
+        v[i] = q.x, v[i + 1] = q.y, v[i + 2] = q.z, v[i + 3] = q.w;
+      }
+    };
+    auto put_bf = [&](const float (&v)[NC], uint16_t* Ph, uint16_t* Pl) {
+#pragma unroll
+      for (int i = 0; i < NC; i += 4) {
+        uint32_t bh[4], bl[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) fa_split_bf(v[i + e], bh[e], bl[e]);
+        *reinterpret_cast<u2v*>(Ph + no + i) = u2v{bh[0] | (bh[1] << 16), bh[2] | (bh[3] << 16)};
+        *reinterpret_cast<u2v*>(Pl + no + i) = u2v{bl[0] | (bl[1] << 16), bl[2] | (bl[3] << 16)};
+      }
+    };
+    if (!kvs) {
+      float qv[NC], dv[NC], ov[NC];
+      ld(a.q, a.ldq, qv);
+      ld(a.dO, a.ldq, dv);
+      ld(a.o, a.ldq, ov);
+      float s = 0.0f;  // D: the thread's columns in order, then the token's 16 lanes (fixed order)
+#pragma unroll
+      for (int i = 0; i < NC; i++) s = s + dv[i] * ov[i];
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) s = s + __shfl_xor(s, m);
+      if (in) {
+        if ((tid & 15) == 0) a.D[(int64_t)h * a.t + t] = s;
+        const float qs2 = a.scale * kLog2e;  // scores in base 2
+#pragma unroll
+        for (int i = 0; i < NC; i += 4) {
+          u2v hi, lo;
+          fa_split_f16(f4{qv[i], qv[i + 1], qv[i + 2], qv[i + 3]} * qs2, hi, lo);
+          *reinterpret_cast<u2v*>(a.pqsh + no + i) = hi;
+          *reinterpret_cast<u2v*>(a.pqsl + no + i) = lo;
+        }
+        put_bf(dv, a.pdoh, a.pdol);
+      }
+    } else {
+      float kv[NC], vv[NC];
+      ld(a.k, a.ldk, kv);
+      ld(a.v, a.ldv, vv);
+      if (in) {
+#pragma unroll
+        for (int i = 0; i < NC; i += 4) *reinterpret_cast<u2v*>(a.pkf + no + i) = fa_f16(f4{kv[i], kv[i + 1], kv[i + 2], kv[i + 3]});
+        put_bf(vv, a.pvh, a.pvl);
+      }
+    }
+  }
+  {  // transposed planes: column d, tokens t0 .. t0 + TPT - 1
+    const int d = tid / TPD, t0 = tg * 16 + (tid % TPD) * TPT;
+    auto col = [&](const float* X, int64_t ldx, uint16_t* Ph, uint16_t* Pl) {
+      float v[TPT];
+#pragma unroll
+      for (int j = 0; j < TPT; j++)
+        v[j] = t0 + j < a.t ? X[(int64_t)(t0 + j) * ldx + (int64_t)h * HD + d] : 0.0f;
+      uint32_t bh[TPT], bl[TPT];
+#pragma unroll
+      for (int j = 0; j < TPT; j++) fa_split_bf(v[j], bh[j], bl[j]);
+      const int64_t go = ((int64_t)h * HD + d) * a.tp + t0;
+      if constexpr (TPT == 8) {
+        *reinterpret_cast<u4v*>(Ph + go) = u4v{bh[0] | (bh[1] << 16), bh[2] | (bh[3] << 16), bh[4] | (bh[5] << 16), bh[6] | (bh[7] << 16)};
+        *reinterpret_cast<u4v*>(Pl + go) = u4v{bl[0] | (bl[1] << 16), bl[2] | (bl[3] << 16), bl[4] | (bl[5] << 16), bl[6] | (bl[7] << 16)};
+      } else {
+        *reinterpret_cast<u2v*>(Ph + go) = u2v{bh[0] | (bh[1] << 16), bh[2] | (bh[3] << 16)};
+        *reinterpret_cast<u2v*>(Pl + go) = u2v{bl[0] | (bl[1] << 16), bl[2] | (bl[3] << 16)};
+      }
+    };
+    if (!kvs) {
+      col(a.q, a.ldq, a.pqth, a.pqtl);
+      col(a.dO, a.ldq, a.pdth, a.pdtl);
+    } else {
+      col(a.k, a.ldk, a.pkth, a.pktl);
+    }
+  }
+}
+extern "C" __global__ __launch_bounds__(256) void rtq_m_attn_bwd_prep64(MAttnArgs a) { fa_bwd_prep<64>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_m_attn_bwd_prep128(MAttnArgs a) { fa_bwd_prep<128>(a); }
+
+// 16-byte copies of plane rows into LDS: n16 pieces of a row-major [rows][rowlen] source (row
+// stride ld halves, rows clamped to rmax) -> [rows][LD] in LDS, rowlen a multiple of 8 halves
+template <int ROWS, int ROWLEN, int LD>
+struct FaCopy {
+  static constexpr int PIECES = ROWS * ROWLEN / 8, PER = (PIECES + 255) / 256;
+  u4v v[PER];
+  __device__ __forceinline__ void load(const uint16_t* P, int64_t ld, int r0, int rmax) {
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const int u = threadIdx.x + 256 * k, row = u / (ROWLEN / 8), p8 = u % (ROWLEN / 8);
+      if (PIECES % 256 == 0 || u < PIECES)
+        v[k] = *reinterpret_cast<const u4v*>(P + (int64_t)min(r0 + row, rmax) * ld + 8 * p8);
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t* L) const {
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const int u = threadIdx.x + 256 * k, row = u / (ROWLEN / 8), p8 = u % (ROWLEN / 8);
+      if (PIECES % 256 == 0 || u < PIECES) *reinterpret_cast<u4v*>(L + row * LD + 8 * p8) = v[k];
+    }
+  }
+};
+
 // ------------------------------------------------------------------ dq
 // Item: 64 queries (it.blk) of head it.head over the 64-key tiles [b0, b1).  Wave w = (wq, wh) =
 // (w / 2, w % 2) owns queries 32 wq .. 32 wq + 31 (two 16-row tiles, their q scale and dO operand
@@ -345,26 +423,17 @@ __device__ __forceinline__ void fa_dq(const MAttnArgs& a, const MAttnItem& it, F
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
   const int wq = w >> 1, wh = w & 1;
   const int h = it.head, kvh = h / (a.nh / a.nkv), qb = it.blk, r0 = qb * 64 + 32 * wq;
-  const float qs2 = a.scale * kLog2e;  // scores in base 2, as the forward
-  half8 qh[2][NK], ql[2][NK];
+  half8 qh[2][NK], ql[2][NK];  // q scale log2(e) (f16 hi / lo) and dO (bf16 hi / lo) from the planes
   bf8 dh[2][NK], dl[2][NK];
 #pragma unroll
   for (int u = 0; u < 2; u++) {
-    const int rc = min(r0 + 16 * u + li, a.t - 1);
-    const float* qr = a.q + (int64_t)rc * a.ldq + (int64_t)h * HD + 8 * g;
-    const float* dr = a.dO + (int64_t)rc * a.ldq + (int64_t)h * HD + 8 * g;
+    const int64_t o = ((int64_t)min(r0 + 16 * u + li, a.t - 1) * a.nh + h) * HD + 8 * g;
 #pragma unroll
     for (int c = 0; c < NK; c++) {
-      u2v h0, l0, h1, l1;
-      fa_split_f16(*reinterpret_cast<const f4*>(qr + 32 * c) * qs2, h0, l0);
-      fa_split_f16(*reinterpret_cast<const f4*>(qr + 32 * c + 4) * qs2, h1, l1);
-      qh[u][c] = __builtin_bit_cast(half8, u4v{h0.x, h0.y, h1.x, h1.y});
-      ql[u][c] = __builtin_bit_cast(half8, u4v{l0.x, l0.y, l1.x, l1.y});
-      uint32_t eh[8], el[8];
-#pragma unroll
-      for (int e = 0; e < 8; e++) fa_split_bf(dr[32 * c + e], eh[e], el[e]);
-      dh[u][c] = __builtin_bit_cast(bf8, u4v{eh[0] | (eh[1] << 16), eh[2] | (eh[3] << 16), eh[4] | (eh[5] << 16), eh[6] | (eh[7] << 16)});
-      dl[u][c] = __builtin_bit_cast(bf8, u4v{el[0] | (el[1] << 16), el[2] | (el[3] << 16), el[4] | (el[5] << 16), el[6] | (el[7] << 16)});
+      qh[u][c] = fa_h8(a.pqsh + o + 32 * c);
+      ql[u][c] = fa_h8(a.pqsl + o + 32 * c);
+      dh[u][c] = fa_b8(a.pdoh + o + 32 * c);
+      dl[u][c] = fa_b8(a.pdol + o + 32 * c);
     }
   }
   int si[2][4];
@@ -384,28 +453,30 @@ __device__ __forceinline__ void fa_dq(const MAttnArgs& a, const MAttnItem& it, F
   for (int u = 0; u < 2; u++)
 #pragma unroll
     for (int c = 0; c < NH; c++) acc[u][c] = zero;
-  const float* kb = a.k + (int64_t)kvh * HD;
-  const float* vb = a.v + (int64_t)kvh * HD;
-  FaNat<HD> kn, vn;
-  FaTr<HD> kt_;
+  // staging: plain copies of the planes (K f16, V bf16 hi / lo natural; K bf16 hi / lo transposed)
+  const int64_t kvo = (int64_t)kvh * HD, ldn = (int64_t)a.nkv * HD;
+  FaCopy<64, HD, LDK> ck, cvh, cvl;
+  FaCopy<HD, 64, LDT> ckh, ckl;
+  auto load_tile = [&](int ktile) {
+    const int k0 = ktile * 64;
+    ck.load(a.pkf + kvo, ldn, k0, a.t - 1);
+    cvh.load(a.pvh + kvo, ldn, k0, a.t - 1);
+    cvl.load(a.pvl + kvo, ldn, k0, a.t - 1);
+    ckh.load(a.pkth + k0, a.tp, (int)kvo, 1 << 30);
+    ckl.load(a.pktl + k0, a.tp, (int)kvo, 1 << 30);
+  };
   int kt = fa_next_live(a, qb, it.b0, it.b1);
-  if (kt < it.b1) {
-    kn.load(kb, a.ldk, kt * 64, a.t);
-    vn.load(vb, a.ldv, kt * 64, a.t);
-    kt_.load(kb, a.ldk, kt * 64, a.t);
-  }
+  if (kt < it.b1) load_tile(kt);
   while (kt < it.b1) {
     const int k0 = kt * 64;
-    fa_store_nat_f16<HD, LDK>(kn, L.k);
-    fa_store_nat_bf<HD, LDK>(vn, L.vh, L.vl);
-    fa_store_tr_bf<HD, LDT>(kt_, L.kth, L.ktl);
+    ck.store(L.k);
+    cvh.store(L.vh);
+    cvl.store(L.vl);
+    ckh.store(L.kth);
+    ckl.store(L.ktl);
     __syncthreads();
     const int kt2 = fa_next_live(a, qb, kt + 1, it.b1);
-    if (kt2 < it.b1) {
-      kn.load(kb, a.ldk, kt2 * 64, a.t);
-      vn.load(vb, a.ldv, kt2 * 64, a.t);
-      kt_.load(kb, a.ldk, kt2 * 64, a.t);
-    }
+    if (kt2 < it.b1) load_tile(kt2);
     // S and dP of the two query tiles x keys 32 wh + 16 j (j = 0, 1)
     f4 s[2][2] = {{zero, zero}, {zero, zero}}, dp[2][2] = {{zero, zero}, {zero, zero}};
 #pragma unroll
@@ -510,67 +581,6 @@ struct FaKvLds {
   uint16_t dth[HD * LDT], dtl[HD * LDT];    // dO [d][q], bf16 hi / lo
   uint16_t ph[64 * LDP], pl[64 * LDP], sh[64 * LDP], sl[64 * LDP];  // p^T, dS^T [key][q], bf16 hi / lo
 };
-// 32 rows x HD staging (natural: thread -> row tid / 8, columns (tid % 8) HD / 8 ..; transposed:
-// thread -> rows KPT kg .., columns 4 (tid % (HD / 4)) .., KPT = HD / 32)
-template <int HD>
-struct FaNat32 {
-  static constexpr int NF = HD / 32;
-  f4 v[NF];
-  __device__ __forceinline__ void load(const float* X, int64_t ld, int r0, int t) {
-    const float* p = X + (int64_t)min(r0 + (int)(threadIdx.x >> 3), t - 1) * ld + (threadIdx.x & 7) * (HD / 8);
-#pragma unroll
-    for (int i = 0; i < NF; i++) v[i] = *reinterpret_cast<const f4*>(p + 4 * i);
-  }
-};
-template <int HD>
-struct FaTr32 {
-  static constexpr int KPT = HD / 32;  // 4 (HD 128) or 2 (HD 64)
-  f4 v[KPT];
-  __device__ __forceinline__ void load(const float* X, int64_t ld, int r0, int t) {
-    const int kg = threadIdx.x / (HD / 4), d4 = threadIdx.x % (HD / 4);
-#pragma unroll
-    for (int i = 0; i < KPT; i++)
-      v[i] = *reinterpret_cast<const f4*>(X + (int64_t)min(r0 + kg * KPT + i, t - 1) * ld + 4 * d4);
-  }
-};
-template <int HD, int LD>
-__device__ __forceinline__ void fa_store32_nat(const FaNat32<HD>& s, bool f16, float mul, uint16_t* Ph, uint16_t* Pl) {
-  const int o = (threadIdx.x >> 3) * LD + (threadIdx.x & 7) * (HD / 8);
-#pragma unroll
-  for (int i = 0; i < FaNat32<HD>::NF; i++) {
-    u2v hi, lo;
-    if (f16) {
-      fa_split_f16(mul == 1.0f ? s.v[i] : s.v[i] * mul, hi, lo);
-    } else {
-      uint32_t h[4], l[4];
-#pragma unroll
-      for (int c = 0; c < 4; c++) fa_split_bf(s.v[i][c], h[c], l[c]);
-      hi = u2v{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-      lo = u2v{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
-    }
-    *reinterpret_cast<u2v*>(Ph + o + 4 * i) = hi;
-    *reinterpret_cast<u2v*>(Pl + o + 4 * i) = lo;
-  }
-}
-template <int HD, int LD>
-__device__ __forceinline__ void fa_store32_tr_bf(const FaTr32<HD>& s, uint16_t* Ph, uint16_t* Pl) {
-  constexpr int KPT = FaTr32<HD>::KPT;
-  const int kg = threadIdx.x / (HD / 4), d4 = threadIdx.x % (HD / 4);
-#pragma unroll
-  for (int c = 0; c < 4; c++) {
-    uint32_t h[KPT], l[KPT];
-#pragma unroll
-    for (int i = 0; i < KPT; i++) fa_split_bf(s.v[i][c], h[i], l[i]);
-    const int o = (4 * d4 + c) * LD + kg * KPT;
-    if constexpr (KPT == 4) {
-      *reinterpret_cast<u2v*>(Ph + o) = u2v{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-      *reinterpret_cast<u2v*>(Pl + o) = u2v{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
-    } else {
-      *reinterpret_cast<uint32_t*>(Ph + o) = h[0] | (h[1] << 16);
-      *reinterpret_cast<uint32_t*>(Pl + o) = l[0] | (l[1] << 16);
-    }
-  }
-}
 template <int HD>
 __device__ __forceinline__ void fa_dkv(const MAttnArgs& a, const MAttnItem& it, FaKvLds<HD>& L) {
   constexpr int NC = HD / 16, NH = NC / 2, NK = HD / 32;
@@ -579,23 +589,16 @@ __device__ __forceinline__ void fa_dkv(const MAttnArgs& a, const MAttnItem& it, 
   const int wk = w >> 1, wh = w & 1;
   const int kvh = it.head, grp = a.nh / a.nkv, kbk = it.blk, c0 = kbk * 64 + 32 * wk, nqt = (a.t + 63) / 64;
   // the wave's 32 keys: k (f16, exact) and v (bf16 hi / lo) operand fragments of its two key tiles
-  half8 kf[2][NK];
+  half8 kf[2][NK];  // k (f16) and v (bf16 hi / lo) from the planes
   bf8 vh[2][NK], vl[2][NK];
 #pragma unroll
   for (int u = 0; u < 2; u++) {
-    const int kc = min(c0 + 16 * u + li, a.t - 1);
-    const float* kr = a.k + (int64_t)kc * a.ldk + (int64_t)kvh * HD + 8 * g;
-    const float* vr = a.v + (int64_t)kc * a.ldv + (int64_t)kvh * HD + 8 * g;
+    const int64_t o = ((int64_t)min(c0 + 16 * u + li, a.t - 1) * a.nkv + kvh) * HD + 8 * g;
 #pragma unroll
     for (int c = 0; c < NK; c++) {
-      const u2v k0 = fa_f16(*reinterpret_cast<const f4*>(kr + 32 * c));
-      const u2v k1 = fa_f16(*reinterpret_cast<const f4*>(kr + 32 * c + 4));
-      kf[u][c] = __builtin_bit_cast(half8, u4v{k0.x, k0.y, k1.x, k1.y});
-      uint32_t eh[8], el[8];
-#pragma unroll
-      for (int e = 0; e < 8; e++) fa_split_bf(vr[32 * c + e], eh[e], el[e]);
-      vh[u][c] = __builtin_bit_cast(bf8, u4v{eh[0] | (eh[1] << 16), eh[2] | (eh[3] << 16), eh[4] | (eh[5] << 16), eh[6] | (eh[7] << 16)});
-      vl[u][c] = __builtin_bit_cast(bf8, u4v{el[0] | (el[1] << 16), el[2] | (el[3] << 16), el[4] | (el[5] << 16), el[6] | (el[7] << 16)});
+      kf[u][c] = fa_h8(a.pkf + o + 32 * c);
+      vh[u][c] = fa_b8(a.pvh + o + 32 * c);
+      vl[u][c] = fa_b8(a.pvl + o + 32 * c);
     }
   }
   int skey[2][4];  // segments of the lane's keys c0 + 16 u + 4 g + i
@@ -618,25 +621,35 @@ __device__ __forceinline__ void fa_dkv(const MAttnArgs& a, const MAttnItem& it, 
     while (st < 2 * it.b1 && !live_pair(st >> 1)) st = ((st >> 1) + 1) * 2;
     return st;
   };
-  FaNat32<HD> qn, dn;
-  FaTr32<HD> qtn, dtn;
+  // staging: plain copies of the planes (q scale f16 and dO bf16 hi / lo natural; q, dO bf16 hi /
+  // lo transposed)
+  FaCopy<32, HD, LDN> cqh, cql, cdh, cdl;
+  FaCopy<HD, 32, LDT> cqth, cqtl, cdth, cdtl;
+  const int64_t ldn = (int64_t)a.nh * HD;
   auto load_step = [&](int st) {
     const int pr = st >> 1, h = kvh * grp + pr / nqt, q0 = (pr % nqt) * 64 + 32 * (st & 1);
-    const float* qh = a.q + (int64_t)h * HD;
-    const float* dh = a.dO + (int64_t)h * HD;
-    qn.load(qh, a.ldq, q0, a.t);
-    dn.load(dh, a.ldq, q0, a.t);
-    qtn.load(qh, a.ldq, q0, a.t);
-    dtn.load(dh, a.ldq, q0, a.t);
+    const int64_t ho = (int64_t)h * HD;
+    cqh.load(a.pqsh + ho, ldn, q0, a.t - 1);
+    cql.load(a.pqsl + ho, ldn, q0, a.t - 1);
+    cdh.load(a.pdoh + ho, ldn, q0, a.t - 1);
+    cdl.load(a.pdol + ho, ldn, q0, a.t - 1);
+    cqth.load(a.pqth + q0, a.tp, (int)ho, 1 << 30);
+    cqtl.load(a.pqtl + q0, a.tp, (int)ho, 1 << 30);
+    cdth.load(a.pdth + q0, a.tp, (int)ho, 1 << 30);
+    cdtl.load(a.pdtl + q0, a.tp, (int)ho, 1 << 30);
   };
   int st = next_step(2 * it.b0);
   if (st < 2 * it.b1) load_step(st);
   while (st < 2 * it.b1) {  // workgroup-uniform
     const int pr = st >> 1, h = kvh * grp + pr / nqt, q0 = (pr % nqt) * 64 + 32 * (st & 1);
-    fa_store32_nat<HD, LDN>(qn, true, a.scale * kLog2e, L.qsh, L.qsl);  // scores in base 2
-    fa_store32_tr_bf<HD, LDT>(qtn, L.qth, L.qtl);
-    fa_store32_nat<HD, LDN>(dn, false, 1.0f, L.dsh_, L.dsl_);
-    fa_store32_tr_bf<HD, LDT>(dtn, L.dth, L.dtl);
+    cqh.store(L.qsh);  // q scale log2(e): scores in base 2
+    cql.store(L.qsl);
+    cdh.store(L.dsh_);
+    cdl.store(L.dsl_);
+    cqth.store(L.qth);
+    cqtl.store(L.qtl);
+    cdth.store(L.dth);
+    cdtl.store(L.dtl);
     __syncthreads();
     const int st2 = next_step(st + 1);
     if (st2 < 2 * it.b1) load_step(st2);

@@ -27,7 +27,7 @@ enum RtqModelKernel {
   KM_GEMM32_Q8,
   KM_ATTN_MERGE_FWD,
   KM_ATTN_MERGE_BWD,
-  KM_ATTN_BWD_D,
+  KM_ATTN_BWD_PREP64,  // the fused backward's operand planes and D = dO . o (head size 64, 128)
   KM_GEMM_BF,
   KM_GEMM32_BF,
   KM_GEMM32G_BF,
@@ -37,6 +37,7 @@ enum RtqModelKernel {
   KM_FA_FWD128,
   KM_FA_BWD64,
   KM_FA_BWD128,
+  KM_ATTN_BWD_PREP128,
   KM_COUNT
 };
 

@@ -407,6 +407,12 @@ struct MAttnArgs {
   int t, nh, nkv, hd;
   int64_t ldq, ldk, ldv, ld_dv;
   float scale;
+  // the fused backward's 16-bit operand planes, formed once per layer by rtq_m_attn_bwd_prep*:
+  // natural [t][heads][hd]: q scale log2(e) (f16 hi / lo), dO (bf16 hi / lo), k (f16), v (bf16
+  // hi / lo); transposed [heads][hd][tp] (tp = t rounded up to 64, columns past t zero): q, dO, k
+  // (bf16 hi / lo)
+  uint16_t *pqsh, *pqsl, *pdoh, *pdol, *pkf, *pvh, *pvl, *pqth, *pqtl, *pdth, *pdtl, *pkth, *pktl;
+  int tp;
 };
 
 struct MGroupArgs {

@@ -162,6 +162,7 @@ struct rtq_model {
   int attn_items = 2;  // fused attention work items per CU aimed at (RTQ_ATTN_ITEMS; 0: rows never cut)
   int64_t layout_fused = -1;  // attn_fused the step buffers were laid out for
   float* attn_D = nullptr;  // [nh x t] dO . o per query row
+  uint16_t* attn_planes = nullptr;  // the fused backward's 16-bit operand planes (MAttnArgs::p*)
   void* attn_mem = nullptr;
   size_t attn_cap = 0;
   MAttnItem *it_fwd = nullptr, *it_kv = nullptr;
@@ -465,6 +466,14 @@ rtq_status ensure_lgrad(rtq_model* m, int64_t t) {
   return RTQ_OK;
 }
 
+// halves of the fused backward's operand planes for T tokens: natural q scale (2), dO (2), k (1),
+// v (2) planes of [T][heads][hd]; transposed q (2), dO (2), k (2) planes of [heads][hd][T rounded
+// up to 64]
+int64_t attn_plane_halves(const rtq_model_config& c, int64_t T) {
+  const int64_t qd = c.n_head * c.head_dim, kd = c.n_head_kv * c.head_dim, tp = (T + 63) / 64 * 64;
+  return T * (4 * qd + 3 * kd) + tp * (4 * qd + 2 * kd);
+}
+
 // Assigns every step buffer of `dst` for T tokens, N targets and `caches` sets of block activations
 // (n_layer when keeping them, 1 when recomputing) from `base` (0: only counts) and returns the
 // bytes.  Each buffer starts on a 256-byte boundary.
@@ -495,6 +504,7 @@ size_t step_layout(rtq_model* dst, int64_t T, int64_t N, int64_t caches, uintptr
     if (dst->defer_lg) fl(&k.dgu, T * 2 * ff), fl(&k.dqkv, T * (qd + 2 * kd)), fl(&k.dh, T * d), fl(&k.gx, T * d);
   }
   fl(&dst->attn_D, fz ? c.n_head * T : 1);
+  dst->attn_planes = reinterpret_cast<uint16_t*>(take((size_t)(fz ? attn_plane_halves(c, T) : 1) * 2));
   fl(&dst->dY, T * d), fl(&dst->dX, T * d), fl(&dst->mo, T * d), fl(&dst->f, T * d), fl(&dst->dhm, T * ff);
   fl(&dst->dgu, T * 2 * ff), fl(&dst->dn2, T * d), fl(&dst->dxu, T * d), fl(&dst->dh, T * d), fl(&dst->d_o, T * qd);
   fl(&dst->dP, att), fl(&dst->dq, T * qd), fl(&dst->dkh, hdh), fl(&dst->dvh, hdh), fl(&dst->dk, T * kd);
@@ -767,6 +777,18 @@ MAttnArgs attn_args(rtq_model* m, Cache& k, int64_t t) {
   a.ldq = c.n_head * c.head_dim;
   a.ldk = a.ldv = c.n_head_kv * c.head_dim;
   a.scale = 1.0f / sqrtf((float)c.head_dim);
+  const int64_t qd = c.n_head * c.head_dim, kd = c.n_head_kv * c.head_dim, tp = (t + 63) / 64 * 64;
+  a.tp = (int)tp;
+  if (m->attn_fused) {  // planes for t tokens laid out back to back (the buffer holds t_cap)
+    uint16_t* p = m->attn_planes;
+    for (uint16_t** q : {&a.pqsh, &a.pqsl, &a.pdoh, &a.pdol}) *q = p, p += t * qd;
+    a.pkf = p, p += t * kd;
+    a.pvh = p, p += t * kd;
+    a.pvl = p, p += t * kd;
+    for (uint16_t** q : {&a.pqth, &a.pqtl, &a.pdth, &a.pdtl}) *q = p, p += tp * qd;
+    a.pkth = p, p += tp * kd;
+    a.pktl = p;
+  }
   return a;
 }
 
@@ -967,7 +989,9 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
     aa.dk = m->dk;
     aa.dv = dv.v;
     aa.ld_dv = dv.ldv;
-    M_TRY(rtq_model_launch(m->ctx, KM_ATTN_BWD_D, dim3((unsigned)((t * nh + 3) / 4)), dim3(256), stream_of(m), &aa));
+    // D and the 16-bit operand planes of q, dO, k, v, once per layer
+    M_TRY(rtq_model_launch(m->ctx, hd == 64 ? KM_ATTN_BWD_PREP64 : KM_ATTN_BWD_PREP128,
+                           dim3((unsigned)((t + 63) / 64 * 4), (unsigned)(nh + nkv)), dim3(256), stream_of(m), &aa));
     aa.items = m->it_fwd;  // dq over key tiles, and dk, dv over (group head, query tile) pairs: one launch
     aa.n_items = m->n_fwd;
     aa.items2 = m->it_kv;

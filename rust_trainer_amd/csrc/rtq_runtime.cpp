@@ -173,9 +173,9 @@ constexpr const char* kKernelNames[] = {
     "rtq_m_swiglu",         "rtq_m_swiglu_bwd",     "rtq_m_add",            "rtq_m_gemm32",
     "rtq_m_lora_mask",      "rtq_m_gemm32g",        "rtq_m_gemm_q8",        "rtq_m_gemm32_q8",
     "rtq_m_attn_merge_fwd", "rtq_m_attn_merge_bwd",
-    "rtq_m_attn_bwd_d",     "rtq_m_gemm_bf",        "rtq_m_gemm32_bf",
+    "rtq_m_attn_bwd_prep64", "rtq_m_gemm_bf",       "rtq_m_gemm32_bf",
     "rtq_m_gemm32g_bf",     "rtq_m_gemm_hf",        "rtq_m_gemm32_hf",      "rtq_m_fa_fwd64",
-    "rtq_m_fa_fwd128",      "rtq_m_fa_bwd64",       "rtq_m_fa_bwd128"};
+    "rtq_m_fa_fwd128",      "rtq_m_fa_bwd64",       "rtq_m_fa_bwd128",      "rtq_m_attn_bwd_prep128"};
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT, "one name per kernel id, in id order");
 
 struct TimedLaunch {
