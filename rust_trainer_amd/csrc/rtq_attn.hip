@@ -30,21 +30,23 @@ constexpr int kMergeBatch = 8;  // merges of up to this many slots issue all the
 
 // a block's partials (o, m, l; m a base-2 maximum) combined in slot order: m* = max m_s,
 // l* = sum l_s 2^(m_s - m*), o = (sum o_s 2^(m_s - m*)) / l*, lse = m* ln 2 + log l*; one thread per
-// output element e of the 16 x hd block (its row's m*, l* recomputed by each thread of the row)
-__device__ __forceinline__ void attn_merge_fwd(const MAttnArgs& a, const MAttnMerge& mg, int e) {
-  const int HD = a.hd, rl = e / HD, c = e % HD, row = mg.blk * 16 + rl;
+// four consecutive output elements 4 e4 .. of the 16 x hd block (its row's m*, l* recomputed by
+// each thread of the row)
+__device__ __forceinline__ void attn_merge_fwd(const MAttnArgs& a, const MAttnMerge& mg, int e4) {
+  const int HD = a.hd, rl = 4 * e4 / HD, c = 4 * e4 % HD, row = mg.blk * 16 + rl;
   if (row >= a.t) return;
   const float* p0 = a.part + (int64_t)mg.s0 * (32 * HD);
-  float m = -__builtin_inff();
-  float l = 0.0f, o = 0.0f;
+  float m = -__builtin_inff(), l = 0.0f;
+  f4 o = {0.0f, 0.0f, 0.0f, 0.0f};
   if (mg.n <= kMergeBatch) {  // every slot's loads issued together, then the same arithmetic in slot order
-    float mv[kMergeBatch], lv[kMergeBatch], ov[kMergeBatch];
+    float mv[kMergeBatch], lv[kMergeBatch];
+    f4 ov[kMergeBatch];
 #pragma unroll
     for (int s = 0; s < kMergeBatch; s++) {  // (n is uniform: the slots past it are not read)
       const float* ps = p0 + (int64_t)s * 32 * HD;
       mv[s] = s < mg.n ? ps[16 * HD + rl] : -__builtin_inff();
       lv[s] = s < mg.n ? ps[16 * HD + 16 + rl] : 0.0f;
-      ov[s] = s < mg.n ? ps[rl * HD + c] : 0.0f;
+      ov[s] = s < mg.n ? *reinterpret_cast<const f4*>(ps + rl * HD + c) : f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 #pragma unroll
     for (int s = 0; s < kMergeBatch; s++)
@@ -54,73 +56,74 @@ __device__ __forceinline__ void attn_merge_fwd(const MAttnArgs& a, const MAttnMe
       if (s >= mg.n || mv[s] == -__builtin_inff()) continue;
       const float w = __builtin_amdgcn_exp2f(mv[s] - m);
       l = l + lv[s] * w;
-      o = o + ov[s] * w;
+#pragma unroll
+      for (int e = 0; e < 4; e++) o[e] = o[e] + ov[s][e] * w;
     }
-    a.o[(int64_t)row * a.ldq + (int64_t)mg.head * HD + c] = __fdiv_rn(o, l);
-    if (c == 0) a.lse[(int64_t)mg.head * a.t + row] = m * 0.693147180559945309417f + logf(l);
-    return;
+  } else {
+    for (int s = 0; s < mg.n; s++) m = fmaxf(m, p0[(int64_t)s * 32 * HD + 16 * HD + rl]);
+    for (int s = 0; s < mg.n; s++) {
+      const float* ps = p0 + (int64_t)s * 32 * HD;
+      const float ms = ps[16 * HD + rl];
+      if (ms == -__builtin_inff()) continue;
+      const float w = __builtin_amdgcn_exp2f(ms - m);
+      l = l + ps[16 * HD + 16 + rl] * w;
+      const f4 os = *reinterpret_cast<const f4*>(ps + rl * HD + c);
+#pragma unroll
+      for (int e = 0; e < 4; e++) o[e] = o[e] + os[e] * w;
+    }
   }
-  for (int s = 0; s < mg.n; s++) m = fmaxf(m, p0[(int64_t)s * 32 * HD + 16 * HD + rl]);
-  for (int s = 0; s < mg.n; s++) {
-    const float* ps = p0 + (int64_t)s * 32 * HD;
-    const float ms = ps[16 * HD + rl];
-    if (ms == -__builtin_inff()) continue;
-    const float w = __builtin_amdgcn_exp2f(ms - m);
-    l = l + ps[16 * HD + 16 + rl] * w;
-    o = o + ps[rl * HD + c] * w;
-  }
-  a.o[(int64_t)row * a.ldq + (int64_t)mg.head * HD + c] = __fdiv_rn(o, l);
+  f4 y;
+#pragma unroll
+  for (int e = 0; e < 4; e++) y[e] = __fdiv_rn(o[e], l);
+  *reinterpret_cast<f4*>(a.o + (int64_t)row * a.ldq + (int64_t)mg.head * HD + c) = y;
   if (c == 0) a.lse[(int64_t)mg.head * a.t + row] = m * 0.693147180559945309417f + logf(l);
 }
 
 // ------------------------------------------------------------------ backward
-// sums of a block's partials in slot order, one thread per element e: dq (kv = false, 16 x hd) or
-// dk then dv (kv = true, 2 x 16 x hd)
-__device__ __forceinline__ void attn_merge_sum(const MAttnArgs& a, const MAttnMerge& mg, int e, bool kv) {
-  const int HD = a.hd;
+// sums of a block's partials in slot order, one thread per four consecutive elements 4 e4 ..: dq
+// (kv = false, 16 x hd) or dk then dv (kv = true, 2 x 16 x hd)
+__device__ __forceinline__ void attn_merge_sum(const MAttnArgs& a, const MAttnMerge& mg, int e4, bool kv) {
+  const int HD = a.hd, e = 4 * e4;
   const int part = e / (16 * HD), rl = (e % (16 * HD)) / HD, c = e % HD, row = mg.blk * 16 + rl;
   if (row >= a.t) return;
   const float* p0 = a.part + (int64_t)mg.s0 * (32 * HD) + e;
-  float s = 0.0f;
+  f4 s = {0.0f, 0.0f, 0.0f, 0.0f};
   if (mg.n <= kMergeBatch) {  // loads together, summed in slot order
-    float v[kMergeBatch];
-#pragma unroll
-    for (int k = 0; k < kMergeBatch; k++) v[k] = k < mg.n ? p0[(int64_t)k * 32 * HD] : 0.0f;
+    f4 v[kMergeBatch];
 #pragma unroll
     for (int k = 0; k < kMergeBatch; k++)
-      if (k < mg.n) s = s + v[k];
+      v[k] = k < mg.n ? *reinterpret_cast<const f4*>(p0 + (int64_t)k * 32 * HD) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; k++)
+      if (k < mg.n) s += v[k];
   } else {
-    for (int k = 0; k < mg.n; k++) s = s + p0[(int64_t)k * 32 * HD];
+    for (int k = 0; k < mg.n; k++) s += *reinterpret_cast<const f4*>(p0 + (int64_t)k * 32 * HD);
   }
-  if (!kv)
-    a.dq[(int64_t)row * a.ldq + (int64_t)mg.head * HD + c] = s;
-  else if (part == 0)
-    a.dk[(int64_t)row * a.ldk + (int64_t)mg.head * HD + c] = s;
-  else
-    a.dv[(int64_t)row * a.ld_dv + (int64_t)mg.head * HD + c] = s;
+  float* dst = !kv ? a.dq + (int64_t)row * a.ldq : part == 0 ? a.dk + (int64_t)row * a.ldk : a.dv + (int64_t)row * a.ld_dv;
+  *reinterpret_cast<f4*>(dst + (int64_t)mg.head * HD + c) = s;
 }
 
-// merges: grid n_merges x ceil(elements / 256) (flat), one thread per element of a block
+// merges: grid n_merges x ceil(elements / 1024) (flat), one thread per four elements of a block
 #define RTQ_ATTN_MERGE_KERNEL(NAME, NEL, CALL)                                          \
   extern "C" __global__ __launch_bounds__(256) void NAME(MAttnArgs a) {                 \
-    const int per = (NEL + 255) / 256, mi = blockIdx.x / per;                           \
-    const int e = (blockIdx.x % per) * 256 + threadIdx.x;                               \
-    if (mi < a.n_merges && e < NEL) CALL;                                               \
+    const int per = (NEL / 4 + 255) / 256, mi = blockIdx.x / per;                       \
+    const int e4 = (blockIdx.x % per) * 256 + threadIdx.x;                              \
+    if (mi < a.n_merges && e4 < NEL / 4) CALL;                                          \
   }
-RTQ_ATTN_MERGE_KERNEL(rtq_m_attn_merge_fwd, 16 * a.hd, attn_merge_fwd(a, a.merges[mi], e))
+RTQ_ATTN_MERGE_KERNEL(rtq_m_attn_merge_fwd, 16 * a.hd, attn_merge_fwd(a, a.merges[mi], e4))
 #undef RTQ_ATTN_MERGE_KERNEL
 // the backward's merges in one launch: the dk / dv blocks (merges2, slots in part2; 32 x hd
 // elements each) then the dq blocks (merges; 16 x hd)
 extern "C" __global__ __launch_bounds__(256) void rtq_m_attn_merge_bwd(MAttnArgs a) {
-  const int pk = (32 * a.hd + 255) / 256, pq = (16 * a.hd + 255) / 256;
+  const int pk = (8 * a.hd + 255) / 256, pq = (4 * a.hd + 255) / 256;
   const int b = (int)blockIdx.x;
   if (b < a.n_merges2 * pk) {
-    const int e = (b % pk) * 256 + threadIdx.x;
+    const int e4 = (b % pk) * 256 + threadIdx.x;
     MAttnArgs k = a;
     k.part = a.part2;
-    if (e < 32 * a.hd) attn_merge_sum(k, a.merges2[b / pk], e, true);
+    if (e4 < 8 * a.hd) attn_merge_sum(k, a.merges2[b / pk], e4, true);
   } else {
-    const int bq = b - a.n_merges2 * pk, mi = bq / pq, e = (bq % pq) * 256 + threadIdx.x;
-    if (mi < a.n_merges && e < 16 * a.hd) attn_merge_sum(a, a.merges[mi], e, false);
+    const int bq = b - a.n_merges2 * pk, mi = bq / pq, e4 = (bq % pq) * 256 + threadIdx.x;
+    if (mi < a.n_merges && e4 < 4 * a.hd) attn_merge_sum(a, a.merges[mi], e4, false);
   }
 }

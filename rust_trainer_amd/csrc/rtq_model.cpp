@@ -805,8 +805,8 @@ rtq_status attn_merge(rtq_model* m, int km, MAttnArgs a, const MAttnMerge* mg, i
   if (n <= 0) return RTQ_OK;
   a.merges = mg;
   a.n_merges = n;
-  const int64_t nel = 16 * (int64_t)a.hd;
-  return rtq_model_launch(m->ctx, km, dim3((unsigned)(n * ((nel + 255) / 256))), dim3(256), stream_of(m), &a);
+  const int64_t nel4 = 4 * (int64_t)a.hd;  // threads per 16 x hd block: four elements each
+  return rtq_model_launch(m->ctx, km, dim3((unsigned)(n * ((nel4 + 255) / 256))), dim3(256), stream_of(m), &a);
 }
 
 // ---------------------------------------------------------------- one block
@@ -1003,7 +1003,7 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
     aa.n_merges = m->n_mfwd;
     aa.merges2 = m->mg_kv;
     aa.n_merges2 = m->n_mkv;
-    const int64_t nmb = m->n_mkv * ((32 * hd + 255) / 256) + m->n_mfwd * ((16 * hd + 255) / 256);
+    const int64_t nmb = m->n_mkv * ((8 * hd + 255) / 256) + m->n_mfwd * ((4 * hd + 255) / 256);
     if (nmb > 0)
       M_TRY(rtq_model_launch(m->ctx, KM_ATTN_MERGE_BWD, dim3((unsigned)nmb), dim3(256), stream_of(m), &aa));
   } else {
