@@ -317,6 +317,7 @@ struct MQkArgs {
   int t, nh, nkv, hd, rot, neox, kv_f16;
   float eps, off;
   int64_t ldq, ldk, ldv;  // per-token row strides of q_raw / dq_raw, k_raw / dk_raw, v_raw (fused q|k|v rows)
+  int half;               // 1: hd = rot = 128, a half-wave (32 lanes x 4 elements) per row, 8 rows per workgroup
 };
 
 // C(b, m, n) (+)= sum_k A(b, m, k) * B(b, k, n), A(b, m, k) = A[(b / divA) * sAb + m * sAm + k * sAk]

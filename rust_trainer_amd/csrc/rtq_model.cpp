@@ -877,13 +877,18 @@ rtq_status lora_grads_all(rtq_model* m) {
                                 (int64_t)(map.size() / 2), tmax >= 256, st);
 }
 
+// the QK kernels' half-wave rows: head size and rotary width 128 (16-byte aligned rows follow)
+bool qk_half(const rtq_model* m) { return m->cfg.head_dim == 128 && m->cfg.rope_dim == 128; }
+// workgroups of the QK kernels for `rows` (token, head) rows: 8 per workgroup (half-wave rows) or 4
+unsigned qk_grid(const rtq_model* m, int64_t rows) { return (unsigned)(qk_half(m) ? (rows + 7) / 8 : (rows + 3) / 4); }
+
 MQkArgs qk_args(rtq_model* m, const Layer& L, Cache& k, int64_t t) {
   const rtq_model_config& c = m->cfg;
   const QkvView x = qkv_view(m, L, k.qkv, t), dx = qkv_view(m, L, g_dqkv(m, k), t);
   return MQkArgs{x.q,   x.k,   x.v,   L.q_norm, L.k_norm, m->cos_,          m->sin_,          k.q,
                  k.k,   k.v,   k.q_inv, k.k_inv, m->dq,     m->dk,            dx.q,             dx.k,
                  (int)t, (int)c.n_head, (int)c.n_head_kv, (int)c.head_dim, (int)c.rope_dim, c.rope_neox,
-                 c.kv_f16, c.rms_eps, c.norm_offset, x.ldq, x.ldk, x.ldv};
+                 c.kv_f16, c.rms_eps, c.norm_offset, x.ldq, x.ldk, x.ldv, qk_half(m) ? 1 : 0};
 }
 
 // gate | u views of a cache's gu buffer (or the gradient buffer of the same layout)
@@ -916,7 +921,7 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, float* x, float* y, boo
     M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LV]], k.n1, t, qv.v));
   }
   const MQkArgs qa = qk_args(m, L, k, t);
-  M_TRY(rtq_model_launch(m->ctx, KM_QK_PREP, dim3((unsigned)((t * (nh + 2 * nkv) + 3) / 4)), dim3(256), stream_of(m),
+  M_TRY(rtq_model_launch(m->ctx, KM_QK_PREP, dim3(qk_grid(m, t * (nh + 2 * nkv))), dim3(256), stream_of(m),
                          &qa));
   const float scale = 1.0f / sqrtf((float)hd);
   if (m->attn_fused) {  // fused: o and each row's log-sum-exp, no probability matrix
@@ -1024,7 +1029,7 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
                          dim3(256), stream_of(m), &gsa));
   }
   const MQkArgs qa = qk_args(m, L, k, t);
-  M_TRY(rtq_model_launch(m->ctx, KM_QK_BWD, dim3((unsigned)((t * (nh + nkv) + 3) / 4)), dim3(256), stream_of(m), &qa));
+  M_TRY(rtq_model_launch(m->ctx, KM_QK_BWD, dim3(qk_grid(m, t * (nh + nkv))), dim3(256), stream_of(m), &qa));
   if (L.qkv_fused) {
     M_TRY(lin_bwd(m, L, L.gi[LQ], k.n1, dqkv, t, m->dn1, &jobs));  // dq.Wq + dk.Wk + dv.Wv in one pass
   } else {

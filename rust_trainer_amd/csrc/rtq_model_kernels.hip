@@ -206,7 +206,75 @@ __device__ __forceinline__ void m_rope_row(const MQkArgs& a, const float* src, f
   for (int e = a.rot + lane; e < a.hd; e += 64) dst[e] = rnd ? m_round_f16(src[e]) : src[e];
 }
 
+// half-wave rows (hd = rot = 128): lane l (of 32) holds elements 4 l .. 4 l + 3.  RoPE of those four
+// (sgn -1: the inverse rotation); NEOX pairs (i, i + 64) sit in lanes l and l ^ 16 of the half-wave
+__device__ __forceinline__ f4 m_rope_h(const MQkArgs& a, f4 y, int p, float sgn) {
+  const int l = threadIdx.x & 31;
+  f4 out;
+  if (a.neox) {
+    const int i0 = 4 * (l & 15);
+    const f4 c = *reinterpret_cast<const f4*>(a.cos_ + (int64_t)p * 64 + i0);
+    const f4 sn = *reinterpret_cast<const f4*>(a.sin_ + (int64_t)p * 64 + i0);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float other = __shfl_xor(y[e], 16), s = sgn * sn[e];
+      out[e] = l < 16 ? y[e] * c[e] - other * s : y[e] * c[e] + other * s;  // x1 c - x2 s | x2 c + x1 s
+    }
+  } else {
+    const float2 c = *reinterpret_cast<const float2*>(a.cos_ + (int64_t)p * 64 + 2 * l);
+    const float2 sn = *reinterpret_cast<const float2*>(a.sin_ + (int64_t)p * 64 + 2 * l);
+    const float s0 = sgn * sn.x, s1 = sgn * sn.y;
+    out[0] = y[0] * c.x - y[1] * s0;
+    out[1] = y[1] * c.x + y[0] * s0;
+    out[2] = y[2] * c.y - y[3] * s1;
+    out[3] = y[3] * c.y + y[2] * s1;
+  }
+  return out;
+}
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+  for (int m = 1; m <= 16; m <<= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
 extern "C" __global__ __launch_bounds__(256) void rtq_m_qk_prep(MQkArgs a) {
+  if (a.half) {  // half-wave per row, every load issued at once
+    const int l = threadIdx.x & 31;
+    const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int64_t nq = (int64_t)a.t * a.nh, nk = (int64_t)a.t * a.nkv;
+    if (row >= nq + 2 * nk) return;  // the whole half-wave
+    if (row >= nq + nk) {  // v: f16 rounding only
+      const int64_t rv = row - nq - nk;
+      f4 x = *reinterpret_cast<const f4*>(a.v_raw + (rv / a.nkv) * a.ldv + (rv % a.nkv) * 128 + 4 * l);
+      if (a.kv_f16)
+#pragma unroll
+        for (int e = 0; e < 4; e++) x[e] = m_round_f16(x[e]);
+      *reinterpret_cast<f4*>(a.v + rv * 128 + 4 * l) = x;
+      return;
+    }
+    const bool isq = row < nq;
+    const int64_t r = isq ? row : row - nq;
+    const int heads = isq ? a.nh : a.nkv, p = (int)(r / heads);
+    f4 y = *reinterpret_cast<const f4*>((isq ? a.q_raw + p * a.ldq : a.k_raw + p * a.ldk) + (r % heads) * 128 + 4 * l);
+    const float* w = isq ? a.q_norm : a.k_norm;
+    if (w) {
+      const f4 wv = *reinterpret_cast<const f4*>(w + 4 * l);
+      float s = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) s = s + y[e] * y[e];
+      s = half_sum(s);
+      const float ir = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(s, 128.0f) + a.eps));
+#pragma unroll
+      for (int e = 0; e < 4; e++) y[e] = y[e] * (ir * (wv[e] + a.off));
+      if (l == 0) (isq ? a.q_inv : a.k_inv)[r] = ir;
+    }
+    f4 o = m_rope_h(a, y, p, 1.0f);
+    if (!isq && a.kv_f16)
+#pragma unroll
+      for (int e = 0; e < 4; e++) o[e] = m_round_f16(o[e]);
+    *reinterpret_cast<f4*>((isq ? a.q : a.k) + r * 128 + 4 * l) = o;
+    return;
+  }
   __shared__ float buf[4][512];
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + wv;
@@ -259,6 +327,44 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_qk_prep(MQkArgs a) {
 
 // backward: dq_raw / dk_raw = rmsnorm_backward(inverse RoPE of dq / dk); rows [0, t nh) q, then k
 extern "C" __global__ __launch_bounds__(256) void rtq_m_qk_bwd(MQkArgs a) {
+  if (a.half) {  // half-wave per row, as the forward
+    const int l = threadIdx.x & 31;
+    const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int64_t nq = (int64_t)a.t * a.nh, nk = (int64_t)a.t * a.nkv;
+    if (row >= nq + nk) return;
+    const bool isq = row < nq;
+    const int64_t r = isq ? row : row - nq;
+    const int heads = isq ? a.nh : a.nkv, p = (int)(r / heads);
+    const int64_t roff = (isq ? p * a.ldq : p * a.ldk) + (r % heads) * 128 + 4 * l;
+    const float* w = isq ? a.q_norm : a.k_norm;
+    f4 xv = {0.0f, 0.0f, 0.0f, 0.0f}, wv = xv;
+    if (w) {
+      xv = *reinterpret_cast<const f4*>((isq ? a.q_raw : a.k_raw) + roff);
+      wv = *reinterpret_cast<const f4*>(w + 4 * l);
+    }
+    const f4 g = *reinterpret_cast<const f4*>((isq ? a.dq : a.dk) + r * 128 + 4 * l);
+    const f4 sb = m_rope_h(a, g, p, -1.0f);
+    float* out = (isq ? a.dq_raw : a.dk_raw) + roff;
+    if (!w) {
+      *reinterpret_cast<f4*>(out) = sb;
+      return;
+    }
+    const float ir = (isq ? a.q_inv : a.k_inv)[r];
+    f4 gv;
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      gv[e] = sb[e] * (wv[e] + a.off);
+      s = s + gv[e] * xv[e];
+    }
+    s = half_sum(s);
+    const float c = __fdiv_rn(((s * ir) * ir) * ir, 128.0f);
+    f4 o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[e] = gv[e] * ir - xv[e] * c;
+    *reinterpret_cast<f4*>(out) = o;
+    return;
+  }
   __shared__ float buf[4][512];
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + wv;
