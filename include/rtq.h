@@ -224,6 +224,13 @@ int rtq_model_checkpointing(const rtq_model* m); /* 1 when the last step recompu
  * (default) fused whenever the head size allows. */
 rtq_status rtq_model_set_attention(rtq_model* m, int mode);
 int rtq_model_attention_fused(const rtq_model* m); /* 1 when the last step used the fused kernels */
+/* Steps run as one HIP graph where they can: a step whose launch key (t, n, with or without
+ * weights, the packed layout, the checkpointing and attention choices, adapters and buffers) equals
+ * the previous step's is captured, and later steps with that key replay it; the inputs' upload and
+ * the outputs' download stay outside.  RTQ_STEP_GRAPH=0 in the environment when the model is
+ * loaded keeps every step eager.  No counterpart in the reference (its steps are eager host code):
+ * the number of replays so far, for tests and profiling. */
+int64_t rtq_model_graph_replays(const rtq_model* m);
 /* parity / debug: while layer >= 0 (-1: off), each step copies that block's tensors in the forward
  * (x, n1, inv1, q_raw, k_raw, v_raw, q, k, v, q_inv, k_inv, P [nh x t x t], o, h, n2, inv2, gate,
  * up, hm, y) and its backward (dy, dhm, dgate, dup, dn2, dh, d_o, dS, dq, dk, dv, dq_raw, dk_raw,

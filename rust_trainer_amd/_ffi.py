@@ -98,6 +98,7 @@ SIGNATURES = {
     "rtq_model_checkpointing": (_i, [_p]),
     "rtq_model_set_attention": (_i, [_p, _i]),
     "rtq_model_attention_fused": (_i, [_p]),
+    "rtq_model_graph_replays": (_i64, [_p]),
     "rtq_model_debug_capture": (_i, [_p, _i64]),
     "rtq_model_debug_tensor": (_i, [_p, ctypes.c_char_p, _p, _i64]),
     # GGUF v3 container

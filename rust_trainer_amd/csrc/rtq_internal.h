@@ -47,6 +47,10 @@ rtq_status rtq_fail(rtq_status st, const char* fmt, ...);
 rtq_status rtq_model_launch(rtq_ctx* c, int km, dim3 grid, dim3 block, hipStream_t s, const void* args);
 int rtq_ctx_device_id(const rtq_ctx* c);
 int rtq_ctx_cu_count(const rtq_ctx* c);
+// generation of the context's workspace (changes whenever it is reallocated)
+uint64_t rtq_ctx_ws_gen(const rtq_ctx* c);
+// per-launch timing is on (rtq_ctx_set_timing): launches record events
+bool rtq_ctx_timing_on(const rtq_ctx* c);
 // floats of the LoRA-down partials a forward of t tokens at rank r can keep for the backward of the
 // same x (0: not kept for this weight - dense, or slicings that differ)
 int64_t rtq_lora_partial_floats(const rtq_weight* w, int64_t t, int64_t r);

@@ -24,6 +24,7 @@
 // backward.  Each member adapter stays addressable (rtq_model_lora_*), its B as a strided block.
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -180,6 +181,20 @@ struct rtq_model {
   int32_t *tok_d = nullptr, *pos_d = nullptr, *tgt_d = nullptr, *hit_d = nullptr;
   float *wts_d = nullptr, *logp_d = nullptr;
   int64_t rope_t = -1;  // t of the uploaded RoPE tables
+  // the step's kernels as one HIP graph (RTQ_STEP_GRAPH=0 at load: every step eager).  A step
+  // whose launch key (sizes, choices, plan counts, gen and the context's workspace generation)
+  // equals the previous step's is captured; later steps with that key replay it.  gen is bumped
+  // by everything else a launch's arguments depend on: a (re)allocation, a rebuilt attention plan,
+  // new adapters, a setter.
+  bool graph_on = true;
+  hipGraphExec_t gexec = nullptr;
+  std::vector<uint64_t> gkey, prev_key;
+  uint64_t gen = 0;
+  int64_t graph_replays = 0;
+  // pinned staging of the step's host inputs (tokens, target positions and tokens, weights) and
+  // outputs (log-probs, hits)
+  void* io_host = nullptr;
+  size_t io_cap = 0;
 };
 
 namespace {
@@ -187,6 +202,7 @@ namespace {
 rtq_status dev_alloc(rtq_model* m, size_t bytes, void** out) {
   M_HIP(hipMalloc(out, bytes ? bytes : 4));
   m->owned.push_back(*out);
+  m->gen++;
   return RTQ_OK;
 }
 
@@ -196,6 +212,7 @@ void dev_free(rtq_model* m, void* p) {
     if (m->owned[i] == p) {
       m->owned.erase(m->owned.begin() + (ptrdiff_t)i);
       (void)hipFree(p);
+      m->gen++;
       return;
     }
 }
@@ -421,6 +438,7 @@ rtq_status ensure_hpk(rtq_model* m, int64_t t) {
     }
     M_HIP(hipMalloc(&m->hpk_mem, need));
     m->hpk_cap = need;
+    m->gen++;
   }
   char* p = (char*)m->hpk_mem;
   for (auto& L : m->layers)
@@ -452,6 +470,7 @@ rtq_status ensure_lgrad(rtq_model* m, int64_t t) {
     }
     M_HIP(hipMalloc(&m->lg_mem, need));
     m->lg_cap = need;
+    m->gen++;
   }
   m->lg_groups = (int64_t)rmax.size();
   m->lg_h.assign((size_t)nl * rmax.size(), nullptr);
@@ -579,6 +598,7 @@ rtq_status ensure_step(rtq_model* m, int64_t t, int64_t n) {
   m->layout_fused = m->attn_fused;
   m->layout_defer = m->defer_lg;
   m->rope_t = -1;
+  m->gen++;
   return RTQ_OK;
 }
 
@@ -753,6 +773,7 @@ rtq_status ensure_attn_plan(rtq_model* m, int64_t t, const int32_t* seg) {
   m->n_mkv = (int)mk.size();
   m->attn_t = t;
   m->attn_packed = packed;
+  m->gen++;
   m->attn_seg.assign(seg ? seg : seg, seg ? seg + t : seg);
   return RTQ_OK;
 }
@@ -864,6 +885,7 @@ rtq_status lora_grads_all(rtq_model* m) {
     M_HIP(hipMalloc(&m->lgt_mem, bytes));
     M_HIP(hipHostMalloc(&m->lgt_host, bytes));
     m->lgt_cap = bytes;
+    m->gen++;
     m->lgt_key.clear();
   }
   if (key != m->lgt_key) {
@@ -1339,6 +1361,7 @@ rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out)
   if (const char* e = getenv("RTQ_ATTN_ITEMS")) m->attn_items = std::max(0, atoi(e));
   if (const char* e = getenv("RTQ_LORA_BATCH")) m->lora_batch = atoi(e) != 0;
   if (const char* e = getenv("RTQ_LORA_DEFER")) m->lora_defer = atoi(e) != 0;
+  if (const char* e = getenv("RTQ_STEP_GRAPH")) m->graph_on = atoi(e) != 0;
   m->ctx = ctx;
   m->cfg = cfg;
   m->rope_factors = factors;
@@ -1377,6 +1400,8 @@ void rtq_model_destroy(rtq_model* m) {
   if (!m) return;
   (void)hipSetDevice(rtq_ctx_device_id(m->ctx));
   (void)hipStreamSynchronize(stream_of(m));
+  if (m->gexec) (void)hipGraphExecDestroy(m->gexec);
+  if (m->io_host) (void)hipHostFree(m->io_host);
   for (rtq_weight* w : m->weights) rtq_weight_destroy(w);
   for (void* p : m->owned) (void)hipFree(p);
   if (m->step_mem) (void)hipFree(m->step_mem);
@@ -1493,6 +1518,7 @@ rtq_status rtq_model_attach_lora(rtq_model* m, int64_t rank, float alpha, uint32
       gp += (nb + 255) / 256 * 256;
     }
   m->grads = gmem;
+  m->gen++;
   m->grad_bytes = gbytes;
   if (n_params) *n_params = n;
   return RTQ_OK;
@@ -1593,8 +1619,82 @@ rtq_status rtq_model_zero_grad(rtq_model* m) {
 }  // extern "C"
 
 namespace {
-// forward_backward_layout (src/model.rs:644-687): embed, blocks (activations kept, or only the
-// block inputs when recomputing), head, blocks in reverse (recomputing each block's forward first)
+// the kernels of a step (forward_backward_layout, src/model.rs:644-687): embed, blocks (activations
+// kept, or only the block inputs when recomputing), head, blocks in reverse (recomputing each
+// block's forward first).  Inputs are on the device; nothing here allocates or synchronises once an
+// identical step has run before (its buffers, job tables and workspace are in place), so it can be
+// captured into a graph.
+rtq_status step_kernels(rtq_model* m, int64_t t, int64_t n, bool weights) {
+  const rtq_model_config& c = m->cfg;
+  hipStream_t st = stream_of(m);
+  const int64_t d = c.n_embd;
+  M_TRY(rtq_frozen_gather_d(m->ctx, m->embed, m->tok_d, t, m->X, st));  // embed_tokens
+  bool pending = false;  // block l's output sum left to block l + 1's first norm
+  for (int64_t l = 0; l < c.n_layer; l++) {
+    float *x = m->X + l * t * d, *y = m->X + (l + 1) * t * d;
+    // the residual sum of a block's output is formed by the next block's first norm, except where
+    // the output itself is read next (the last block: the LM head; a captured block)
+    const bool out = l == c.n_layer - 1 || l == m->dbg_layer;
+    M_TRY(block_forward(m, (int)l, t, x, y, pending, out));
+    pending = !out;
+    if (l == m->dbg_layer) M_TRY(dbg_forward(m, (int)l, t, x, y));
+  }
+  if (n == 0) return RTQ_OK;
+  M_TRY(rtq_lm_head_d(m->ctx, m->head, m->out_norm, c.rms_eps, c.norm_offset, m->X + c.n_layer * t * d, t, m->pos_d,
+                      m->tgt_d, weights ? m->wts_d : nullptr, n, m->logp_d, m->hit_d, weights ? m->dY : nullptr, st));
+  if (!weights) return RTQ_OK;
+  m->lg_all.clear();
+  for (int64_t l = c.n_layer - 1; l >= 0; l--) {
+    const float* x = m->X + l * t * d;
+    if (m->ckpt) M_TRY(block_forward(m, (int)l, t, const_cast<float*>(x), m->f, false, false));  // recompute
+    // deferring: each block's input gradient stays in its own buffer (the block below reads it
+    // as its dy, the deferred dB of its down projection at the end)
+    float* gy = m->defer_lg && l < c.n_layer - 1 ? m->cache[(size_t)l + 1].gx : m->dY;
+    float* gx = m->defer_lg ? m->cache[(size_t)l].gx : m->dX;
+    M_TRY(block_backward(m, (int)l, t, x, gy, gx));
+    if (l == m->dbg_layer) M_TRY(dbg_backward(m, (int)l, t, gy, gx));
+    if (!m->defer_lg) std::swap(m->dY, m->dX);
+  }
+  if (m->defer_lg) M_TRY(lora_grads_all(m));
+  return RTQ_OK;
+}
+
+// captures step_kernels into the model's graph (replacing the one it held) and launches it.  A
+// step that cannot be captured (the runtime refuses an operation in it) runs eagerly, and the model
+// stays eager from then on.
+rtq_status capture_step(rtq_model* m, int64_t t, int64_t n, bool weights, const std::vector<uint64_t>& key) {
+  hipStream_t st = stream_of(m);
+  if (m->gexec) {
+    M_HIP(hipGraphExecDestroy(m->gexec));
+    m->gexec = nullptr;
+    m->gkey.clear();
+  }
+  const char* why = nullptr;
+  if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+    why = "hipStreamBeginCapture";
+  } else {
+    const rtq_status s = step_kernels(m, t, n, weights);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(st, &g);
+    hipGraphExec_t x = nullptr;
+    if (s != RTQ_OK || e != hipSuccess || !g) why = s != RTQ_OK ? rtq_last_error() : "hipStreamEndCapture";
+    else if (hipGraphInstantiate(&x, g, nullptr, nullptr, 0) != hipSuccess) why = "hipGraphInstantiate";
+    if (g) (void)hipGraphDestroy(g);
+    if (!why) {
+      m->gexec = x;
+      m->gkey = key;
+      M_HIP(hipGraphLaunch(x, st));
+      return RTQ_OK;
+    }
+  }
+  (void)hipGetLastError();
+  fprintf(stderr, "rtq: the step could not be captured as a graph (%s); steps run eagerly\n", why);
+  m->graph_on = false;
+  return step_kernels(m, t, n, weights);
+}
+
+// one step (forward_backward_layout, src/model.rs:644-687): checks, buffers and tables, the
+// inputs' upload, the kernels (eager, captured or replayed), the outputs' download
 rtq_status step(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* positions, const int32_t* segments,
                 const int32_t* pos, const int32_t* tok, const float* weights, int64_t n, float* logp, int64_t* hits) {
   if (!m || !tokens || t <= 0 || n < 0 || (n > 0 && (!pos || !tok || !logp)))
@@ -1624,50 +1724,56 @@ rtq_status step(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* p
   M_TRY(upload_layout(m, segments, t));
   if (m->attn_fused) M_TRY(ensure_attn_plan(m, t, segments));
   hipStream_t st = stream_of(m);
-  const int64_t d = c.n_embd;
-  M_HIP(hipMemcpyAsync(m->tok_d, tokens, (size_t)t * 4, hipMemcpyHostToDevice, st));
-  if (n > 0) {
-    M_HIP(hipMemcpyAsync(m->pos_d, pos, (size_t)n * 4, hipMemcpyHostToDevice, st));
-    M_HIP(hipMemcpyAsync(m->tgt_d, tok, (size_t)n * 4, hipMemcpyHostToDevice, st));
-    if (weights) M_HIP(hipMemcpyAsync(m->wts_d, weights, (size_t)n * 4, hipMemcpyHostToDevice, st));
+  // host inputs and outputs pass through pinned staging, so the copies are asynchronous; the
+  // staging is free again once the step's synchronisation below returns
+  const size_t io_need = (size_t)(t + 5 * n) * 4;
+  if (io_need > m->io_cap) {
+    if (m->io_host) M_HIP(hipHostFree(m->io_host));
+    m->io_host = nullptr;
+    m->io_cap = 0;
+    const size_t cap = std::max<size_t>(io_need, 1 << 16);
+    M_HIP(hipHostMalloc(&m->io_host, cap));
+    m->io_cap = cap;
   }
-  M_TRY(rtq_frozen_gather_d(m->ctx, m->embed, m->tok_d, t, m->X, st));  // embed_tokens
-  bool pending = false;  // block l's output sum left to block l + 1's first norm
-  for (int64_t l = 0; l < c.n_layer; l++) {
-    float *x = m->X + l * t * d, *y = m->X + (l + 1) * t * d;
-    // the residual sum of a block's output is formed by the next block's first norm, except where
-    // the output itself is read next (the last block: the LM head; a captured block)
-    const bool out = l == c.n_layer - 1 || l == m->dbg_layer;
-    M_TRY(block_forward(m, (int)l, t, x, y, pending, out));
-    pending = !out;
-    if (l == m->dbg_layer) M_TRY(dbg_forward(m, (int)l, t, x, y));
-  }
+  int32_t* io = (int32_t*)m->io_host;  // tokens [t] | pos [n] | tok [n] | weights [n] | logp [n] | hits [n]
+  std::memcpy(io, tokens, (size_t)t * 4);
+  M_HIP(hipMemcpyAsync(m->tok_d, io, (size_t)t * 4, hipMemcpyHostToDevice, st));
   if (n > 0) {
-    M_TRY(rtq_lm_head_d(m->ctx, m->head, m->out_norm, c.rms_eps, c.norm_offset, m->X + c.n_layer * t * d, t,
-                        m->pos_d, m->tgt_d, weights ? m->wts_d : nullptr, n, m->logp_d, m->hit_d,
-                        weights ? m->dY : nullptr, st));
+    std::memcpy(io + t, pos, (size_t)n * 4);
+    std::memcpy(io + t + n, tok, (size_t)n * 4);
+    M_HIP(hipMemcpyAsync(m->pos_d, io + t, (size_t)n * 4, hipMemcpyHostToDevice, st));
+    M_HIP(hipMemcpyAsync(m->tgt_d, io + t + n, (size_t)n * 4, hipMemcpyHostToDevice, st));
     if (weights) {
-      m->lg_all.clear();
-      for (int64_t l = c.n_layer - 1; l >= 0; l--) {
-        const float* x = m->X + l * t * d;
-        if (m->ckpt) M_TRY(block_forward(m, (int)l, t, const_cast<float*>(x), m->f, false, false));  // recompute
-        // deferring: each block's input gradient stays in its own buffer (the block below reads it
-        // as its dy, the deferred dB of its down projection at the end)
-        float* gy = m->defer_lg && l < c.n_layer - 1 ? m->cache[(size_t)l + 1].gx : m->dY;
-        float* gx = m->defer_lg ? m->cache[(size_t)l].gx : m->dX;
-        M_TRY(block_backward(m, (int)l, t, x, gy, gx));
-        if (l == m->dbg_layer) M_TRY(dbg_backward(m, (int)l, t, gy, gx));
-        if (!m->defer_lg) std::swap(m->dY, m->dX);
-      }
-      if (m->defer_lg) M_TRY(lora_grads_all(m));
+      std::memcpy(io + t + 2 * n, weights, (size_t)n * 4);
+      M_HIP(hipMemcpyAsync(m->wts_d, io + t + 2 * n, (size_t)n * 4, hipMemcpyHostToDevice, st));
     }
-    std::vector<int32_t> hv((size_t)n);
-    M_HIP(hipMemcpyAsync(logp, m->logp_d, (size_t)n * 4, hipMemcpyDeviceToHost, st));
-    M_HIP(hipMemcpyAsync(hv.data(), m->hit_d, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+  }
+  // the launch key: everything the step's launches depend on besides gen (bumped by the rest)
+  const bool graphable = m->graph_on && m->dbg_layer < 0 && !rtq_ctx_timing_on(m->ctx);
+  std::vector<uint64_t> key;
+  if (graphable)
+    key = {(uint64_t)t, (uint64_t)n, weights ? 1u : 0u, m->packed ? 1u : 0u, (uint64_t)m->nlb,
+           m->ckpt ? 1u : 0u, m->defer_lg ? 1u : 0u, m->attn_fused ? 1u : 0u, (uint64_t)m->n_fwd,
+           (uint64_t)m->n_kv, (uint64_t)m->n_mfwd, (uint64_t)m->n_mkv, m->gen, rtq_ctx_ws_gen(m->ctx)};
+  if (graphable && m->gexec && key == m->gkey) {
+    M_HIP(hipGraphLaunch(m->gexec, st));
+    m->graph_replays++;
+  } else if (graphable && key == m->prev_key) {
+    M_TRY(capture_step(m, t, n, weights != nullptr, key));
+  } else {
+    M_TRY(step_kernels(m, t, n, weights != nullptr));
+  }
+  m->prev_key = key;
+  if (n > 0) {
+    float* lp = (float*)(io + t + 3 * n);
+    int32_t* hv = io + t + 4 * n;
+    M_HIP(hipMemcpyAsync(lp, m->logp_d, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+    M_HIP(hipMemcpyAsync(hv, m->hit_d, (size_t)n * 4, hipMemcpyDeviceToHost, st));
     M_HIP(hipStreamSynchronize(st));
+    std::memcpy(logp, lp, (size_t)n * 4);
     if (hits) {
       int64_t s = 0;
-      for (int32_t h : hv) s += h;
+      for (int64_t i = 0; i < n; i++) s += hv[i];
       *hits = s;
     }
   } else {
@@ -1697,6 +1803,7 @@ rtq_status rtq_model_forward_backward_packed(rtq_model* m, const int32_t* tokens
 rtq_status rtq_model_set_checkpointing(rtq_model* m, int mode) {
   if (!m || mode < -1 || mode > 1) return rtq_fail(RTQ_ERR_INVALID, "bad model/checkpointing mode %d", mode);
   m->ckpt_mode = mode;
+  m->gen++;
   return RTQ_OK;
 }
 
@@ -1705,14 +1812,18 @@ int rtq_model_checkpointing(const rtq_model* m) { return m ? (m->ckpt ? 1 : 0) :
 rtq_status rtq_model_set_attention(rtq_model* m, int mode) {
   if (!m || mode < -1 || mode > 1) return rtq_fail(RTQ_ERR_INVALID, "bad model/attention mode %d", mode);
   m->attn_mode = mode;
+  m->gen++;
   return RTQ_OK;
 }
 
 int rtq_model_attention_fused(const rtq_model* m) { return m ? (m->attn_fused ? 1 : 0) : -1; }
 
+int64_t rtq_model_graph_replays(const rtq_model* m) { return m ? m->graph_replays : -1; }
+
 rtq_status rtq_model_debug_capture(rtq_model* m, int64_t layer) {
   if (!m || layer < -1 || layer >= m->cfg.n_layer) return rtq_fail(RTQ_ERR_INVALID, "bad model/layer");
   m->dbg_layer = layer;
+  m->gen++;
   return RTQ_OK;
 }
 

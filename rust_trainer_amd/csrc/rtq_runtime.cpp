@@ -195,6 +195,7 @@ struct rtq_ctx {
   std::mutex mu;
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  uint64_t ws_gen = 0;  // bumped whenever ws moves (graphs that captured its address are stale)
   bool timing = false;
   int timing_only = -1;  // -1: every kernel
   std::vector<TimedLaunch> pending;
@@ -305,6 +306,7 @@ rtq_status ensure_ws(rtq_ctx* c, size_t bytes) {
   }
   HIP_TRY(hipMalloc(&c->ws, want));
   c->ws_bytes = want;
+  c->ws_gen++;
   return RTQ_OK;
 }
 
@@ -942,6 +944,8 @@ rtq_status rtq_model_launch(rtq_ctx* c, int km, dim3 grid, dim3 block, hipStream
 
 int rtq_ctx_device_id(const rtq_ctx* c) { return c ? c->device : -1; }
 int rtq_ctx_cu_count(const rtq_ctx* c) { return c ? (int)c->cu_count : 256; }
+uint64_t rtq_ctx_ws_gen(const rtq_ctx* c) { return c ? c->ws_gen : 0; }
+bool rtq_ctx_timing_on(const rtq_ctx* c) { return c && c->timing; }
 
 // error reporting shared with the other translation units of the library (rtq_gguf.cpp, rtq_model.cpp)
 rtq_status rtq_fail(rtq_status st, const char* fmt, ...) {

@@ -179,6 +179,12 @@ class GpuModel:
         mode = -1 if on is None else (1 if on else 0)
         _ffi.check(_ffi.lib().rtq_model_set_attention(self._h, mode), "rtq_model_set_attention")
 
+    @property
+    def graph_replays(self) -> int:
+        """Steps so far that replayed the captured step graph (a step whose sizes, layout, choices,
+        adapters and buffers equal the previous step's is captured; later ones replay it)."""
+        return int(_ffi.lib().rtq_model_graph_replays(self._h))
+
     def debug_capture(self, layer: int) -> None:
         """Copy block ``layer``'s tensors during each step (-1: off); read them with ``debug_tensor``."""
         _ffi.check(_ffi.lib().rtq_model_debug_capture(self._h, layer), "rtq_model_debug_capture")
