@@ -296,6 +296,7 @@ struct MNormBwdArgs {
 };
 
 // per (token, head) row of width hd: QK-norm, RoPE, f16 rounding of K and V
+struct MAttnMerge;
 struct MQkArgs {
   const float* q_raw;  // [t x nh x hd]
   const float* k_raw;  // [t x nkv x hd]
@@ -318,6 +319,17 @@ struct MQkArgs {
   float eps, off;
   int64_t ldq, ldk, ldv;  // per-token row strides of q_raw / dq_raw, k_raw / dk_raw, v_raw (fused q|k|v rows)
   int half;               // 1: hd = rot = 128, a half-wave (32 lanes x 4 elements) per row, 8 rows per workgroup
+  // backward, half-wave rows: the fused attention's partial slots of cut blocks summed here (in slot
+  // order, as rtq_m_attn_merge_bwd) instead of by a merge launch; qmi null: dq, dk, dv are whole
+  const int* qmi;                   // [nh x nb16]: index into qmerges of (head, 16-row block), or -1
+  const int* kmi;                   // [nkv x nb16]: into kmerges (dk slots, then dv at + 16 x 128)
+  const MAttnMerge* qmerges;
+  const MAttnMerge* kmerges;
+  const float* qpart;               // slots of 32 x 128 floats
+  const float* kpart;
+  float* dv;                        // merged dv rows of cut blocks, row stride ld_dv
+  int64_t ld_dv;
+  int nb16;
 };
 
 // C(b, m, n) (+)= sum_k A(b, m, k) * B(b, k, n), A(b, m, k) = A[(b / divA) * sAb + m * sAm + k * sAk]

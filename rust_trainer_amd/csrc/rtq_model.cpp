@@ -168,6 +168,7 @@ struct rtq_model {
   size_t attn_cap = 0;
   MAttnItem *it_fwd = nullptr, *it_kv = nullptr;
   MAttnMerge *mg_fwd = nullptr, *mg_kv = nullptr;
+  int32_t *qmi = nullptr, *kmi = nullptr;  // (head, 16-row block) -> index into mg_fwd / mg_kv, or -1
   int n_fwd = 0, n_kv = 0, n_mfwd = 0, n_mkv = 0;
   float* attn_part = nullptr;     // forward and dq partial slots
   float* attn_part_kv = nullptr;  // dk / dv partial slots
@@ -739,11 +740,16 @@ rtq_status ensure_attn_plan(rtq_model* m, int64_t t, const int32_t* seg) {
     for (int64_t qb = 0; qb < nlb; qb++) cut(fl[(size_t)qb], cf, h, (int)qb, slots_f, itf, mf);
   for (int g = 0; g < nkv; g++)
     for (int64_t kb = 0; kb < nlb; kb++) cut(kl[(size_t)kb], ck, g, (int)kb, slots_k, itk, mk);
+  // the merges by (head, 16-row block), for the QK backward that sums the slots itself
+  const int64_t nb16 = (t + 15) / 16;
+  std::vector<int32_t> qmi((size_t)(nh * nb16), -1), kmi((size_t)(nkv * nb16), -1);
+  for (size_t i = 0; i < mf.size(); i++) qmi[(size_t)(mf[i].head * nb16 + mf[i].blk)] = (int32_t)i;
+  for (size_t i = 0; i < mk.size(); i++) kmi[(size_t)(mk[i].head * nb16 + mk[i].blk)] = (int32_t)i;
   const auto al = [](size_t b) { return (b + 255) / 256 * 256; };
   const size_t slots = (size_t)slots_f + (size_t)slots_k;  // the dq and dk / dv items run together
   const size_t bytes = al(itf.size() * sizeof(MAttnItem)) + al(itk.size() * sizeof(MAttnItem)) +
                        al(mf.size() * sizeof(MAttnMerge)) + al(mk.size() * sizeof(MAttnMerge)) +
-                       al(std::max<size_t>(slots, 1) * 32 * (size_t)c.head_dim * 4);
+                       al(qmi.size() * 4) + al(kmi.size() * 4) + al(std::max<size_t>(slots, 1) * 32 * (size_t)c.head_dim * 4);
   M_HIP(hipStreamSynchronize(stream_of(m)));
   if (bytes > m->attn_cap) {
     if (m->attn_mem) M_HIP(hipFree(m->attn_mem));
@@ -761,12 +767,18 @@ rtq_status ensure_attn_plan(rtq_model* m, int64_t t, const int32_t* seg) {
   p += al(mf.size() * sizeof(MAttnMerge));
   m->mg_kv = (MAttnMerge*)p;
   p += al(mk.size() * sizeof(MAttnMerge));
+  m->qmi = (int32_t*)p;
+  p += al(qmi.size() * 4);
+  m->kmi = (int32_t*)p;
+  p += al(kmi.size() * 4);
   m->attn_part = (float*)p;
   m->attn_part_kv = m->attn_part + (size_t)slots_f * 32 * (size_t)c.head_dim;
   M_HIP(hipMemcpy(m->it_fwd, itf.data(), itf.size() * sizeof(MAttnItem), hipMemcpyHostToDevice));
   M_HIP(hipMemcpy(m->it_kv, itk.data(), itk.size() * sizeof(MAttnItem), hipMemcpyHostToDevice));
   M_HIP(hipMemcpy(m->mg_fwd, mf.data(), mf.size() * sizeof(MAttnMerge), hipMemcpyHostToDevice));
   M_HIP(hipMemcpy(m->mg_kv, mk.data(), mk.size() * sizeof(MAttnMerge), hipMemcpyHostToDevice));
+  M_HIP(hipMemcpy(m->qmi, qmi.data(), qmi.size() * 4, hipMemcpyHostToDevice));
+  M_HIP(hipMemcpy(m->kmi, kmi.data(), kmi.size() * 4, hipMemcpyHostToDevice));
   m->n_fwd = (int)itf.size();
   m->n_kv = (int)itk.size();
   m->n_mfwd = (int)mf.size();
@@ -1031,7 +1043,9 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
     aa.merges2 = m->mg_kv;
     aa.n_merges2 = m->n_mkv;
     const int64_t nmb = m->n_mkv * ((8 * hd + 255) / 256) + m->n_mfwd * ((4 * hd + 255) / 256);
-    if (nmb > 0)
+    // the QK backward's half-wave rows sum the slots of cut blocks themselves (a captured layer
+    // keeps the merge launch, so that its dq, dk are whole)
+    if (nmb > 0 && !(qk_half(m) && l != m->dbg_layer))
       M_TRY(rtq_model_launch(m->ctx, KM_ATTN_MERGE_BWD, dim3((unsigned)nmb), dim3(256), stream_of(m), &aa));
   } else {
   M_TRY(k_gemm(m, t, t, hd, nh, Op{m->d_o, hd, qd, 1, 1}, Op{k.v, hd, 1, kd, (int)grp}, m->dP, t * t, t, 1, 1.0f, 1,
@@ -1050,7 +1064,18 @@ rtq_status block_backward(rtq_model* m, int l, int64_t t, const float* x, const 
   M_TRY(rtq_model_launch(m->ctx, KM_GROUP_SUM, dim3((unsigned)std::min<int64_t>((t * kd + 255) / 256, 4096)),
                          dim3(256), stream_of(m), &gsa));
   }
-  const MQkArgs qa = qk_args(m, L, k, t);
+  MQkArgs qa = qk_args(m, L, k, t);
+  if (m->attn_fused && qk_half(m) && l != m->dbg_layer) {
+    qa.qmi = m->qmi;
+    qa.kmi = m->kmi;
+    qa.qmerges = m->mg_fwd;
+    qa.kmerges = m->mg_kv;
+    qa.qpart = m->attn_part;
+    qa.kpart = m->attn_part_kv;
+    qa.dv = dv.v;
+    qa.ld_dv = dv.ldv;
+    qa.nb16 = (int)((t + 15) / 16);
+  }
   M_TRY(rtq_model_launch(m->ctx, KM_QK_BWD, dim3(qk_grid(m, t * (nh + nkv))), dim3(256), stream_of(m), &qa));
   if (L.qkv_fused) {
     M_TRY(lin_bwd(m, L, L.gi[LQ], k.n1, dqkv, t, m->dn1, &jobs));  // dq.Wq + dk.Wk + dv.Wv in one pass

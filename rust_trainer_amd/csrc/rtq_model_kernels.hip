@@ -342,7 +342,21 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_qk_bwd(MQkArgs a) {
       xv = *reinterpret_cast<const f4*>((isq ? a.q_raw : a.k_raw) + roff);
       wv = *reinterpret_cast<const f4*>(w + 4 * l);
     }
-    const f4 g = *reinterpret_cast<const f4*>((isq ? a.dq : a.dk) + r * 128 + 4 * l);
+    f4 g;
+    const int mi = a.qmi ? (isq ? a.qmi : a.kmi)[(r % heads) * a.nb16 + (p >> 4)] : -1;
+    if (mi >= 0) {  // a cut block: its slots in order (dq; dk, and the row's dv written here)
+      const MAttnMerge mg = (isq ? a.qmerges : a.kmerges)[mi];
+      const float* s0 = (isq ? a.qpart : a.kpart) + (int64_t)mg.s0 * 4096 + (p & 15) * 128 + 4 * l;
+      g = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      f4 dvs = g;
+      for (int k = 0; k < mg.n; k++) {
+        g += *reinterpret_cast<const f4*>(s0 + (int64_t)k * 4096);
+        if (!isq) dvs += *reinterpret_cast<const f4*>(s0 + (int64_t)k * 4096 + 2048);
+      }
+      if (!isq) *reinterpret_cast<f4*>(a.dv + p * a.ld_dv + (r % heads) * 128 + 4 * l) = dvs;
+    } else {
+      g = *reinterpret_cast<const f4*>((isq ? a.dq : a.dk) + r * 128 + 4 * l);
+    }
     const f4 sb = m_rope_h(a, g, p, -1.0f);
     float* out = (isq ? a.dq_raw : a.dk_raw) + roff;
     if (!w) {
