@@ -293,6 +293,20 @@ __device__ __forceinline__ void fa_bwd_prep(const MAttnArgs& a) {
   const int tg = blockIdx.x, hb = blockIdx.y, tid = threadIdx.x;
   const bool kvs = hb >= a.nh;
   const int h = kvs ? hb - a.nh : hb, heads = kvs ? a.nkv : a.nh;
+  // the transposed planes' values (column d, tokens t0 .. t0 + TPT - 1) are loaded first, so that
+  // their round trip overlaps the natural planes' (stores to the planes could alias the sources)
+  const int d = tid / TPD, t0 = tg * 16 + (tid % TPD) * TPT;
+  auto col_ld = [&](const float* X, int64_t ldx, float (&v)[TPT]) {
+#pragma unroll
+    for (int j = 0; j < TPT; j++) v[j] = t0 + j < a.t ? X[(int64_t)(t0 + j) * ldx + (int64_t)h * HD + d] : 0.0f;
+  };
+  float c1[TPT], c2[TPT];
+  if (!kvs) {
+    col_ld(a.q, a.ldq, c1);
+    col_ld(a.dO, a.ldq, c2);
+  } else {
+    col_ld(a.k, a.ldk, c1);
+  }
   {  // natural planes (+ D)
     const int t = tg * 16 + (tid >> 4), c0 = (tid & 15) * NC;
     const bool in = t < a.t;
@@ -350,12 +364,7 @@ __device__ __forceinline__ void fa_bwd_prep(const MAttnArgs& a) {
     }
   }
   {  // transposed planes: column d, tokens t0 .. t0 + TPT - 1
-    const int d = tid / TPD, t0 = tg * 16 + (tid % TPD) * TPT;
-    auto col = [&](const float* X, int64_t ldx, uint16_t* Ph, uint16_t* Pl) {
-      float v[TPT];
-#pragma unroll
-      for (int j = 0; j < TPT; j++)
-        v[j] = t0 + j < a.t ? X[(int64_t)(t0 + j) * ldx + (int64_t)h * HD + d] : 0.0f;
+    auto col = [&](const float (&v)[TPT], uint16_t* Ph, uint16_t* Pl) {
       uint32_t bh[TPT], bl[TPT];
 #pragma unroll
       for (int j = 0; j < TPT; j++) fa_split_bf(v[j], bh[j], bl[j]);
@@ -369,10 +378,10 @@ __device__ __forceinline__ void fa_bwd_prep(const MAttnArgs& a) {
       }
     };
     if (!kvs) {
-      col(a.q, a.ldq, a.pqth, a.pqtl);
-      col(a.dO, a.ldq, a.pdth, a.pdtl);
+      col(c1, a.pqth, a.pqtl);
+      col(c2, a.pdth, a.pdtl);
     } else {
-      col(a.k, a.ldk, a.pkth, a.pktl);
+      col(c1, a.pkth, a.pktl);
     }
   }
 }
