@@ -280,7 +280,7 @@ struct MNormArgs {
   int rows, d;
   float eps, off;
   int fused;         // 1: x * (ir * (w + off)) (QK-norm order), 0: (x * ir) * (w + off)
-  int wave;          // 1: one wave per row, four rows per workgroup (d % 256 == 0, d <= 2048, 16-byte aligned rows)
+  int wave;          // 1: one wave per row, one-wave workgroups (d % 256 == 0, d <= 2048, 16-byte aligned rows)
 };
 
 struct MNormBwdArgs {

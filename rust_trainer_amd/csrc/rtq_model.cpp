@@ -257,12 +257,11 @@ hipStream_t stream_of(rtq_model* m) { return (hipStream_t)rtq_ctx_stream(m->ctx)
 // ---------------------------------------------------------------- launches
 rtq_status k_norm(rtq_model* m, const float* a, const float* b, float* h, const float* w, float* y, float* inv,
                   int64_t rows, int64_t d, int fused) {
-  // a wave per row where the row fits the wave layout (four rows per workgroup, no barrier)
+  // a wave per row where the row fits the wave layout (one-wave workgroups, no barrier)
   const bool wave = d % 256 == 0 && d <= 2048 && ((uintptr_t)a | (uintptr_t)b | (uintptr_t)h | (uintptr_t)w |
                                                    (uintptr_t)y) % 16 == 0;
   MNormArgs na{a, b, h, w, y, inv, (int)rows, (int)d, m->cfg.rms_eps, m->cfg.norm_offset, fused, wave ? 1 : 0};
-  return rtq_model_launch(m->ctx, KM_RMSNORM, dim3((unsigned)(wave ? (rows + 3) / 4 : rows)), dim3(256),
-                          stream_of(m), &na);
+  return rtq_model_launch(m->ctx, KM_RMSNORM, dim3((unsigned)rows), dim3(wave ? 64 : 256), stream_of(m), &na);
 }
 
 rtq_status k_norm_bwd(rtq_model* m, const float* x, const float* w, const float* inv, const float* dy, const float* res,
@@ -270,8 +269,7 @@ rtq_status k_norm_bwd(rtq_model* m, const float* x, const float* w, const float*
   const bool wave = d % 256 == 0 && d <= 2048 && ((uintptr_t)x | (uintptr_t)w | (uintptr_t)dy | (uintptr_t)res |
                                                    (uintptr_t)out) % 16 == 0;
   MNormBwdArgs na{x, w, inv, dy, res, out, (int)rows, (int)d, m->cfg.norm_offset, wave ? 1 : 0};
-  return rtq_model_launch(m->ctx, KM_RMSNORM_BWD, dim3((unsigned)(wave ? (rows + 3) / 4 : rows)), dim3(256),
-                          stream_of(m), &na);
+  return rtq_model_launch(m->ctx, KM_RMSNORM_BWD, dim3((unsigned)rows), dim3(wave ? 64 : 256), stream_of(m), &na);
 }
 
 // elementwise over rows x cols (a, b at row stride lda, c at ldc, y, z at ldy)

@@ -46,7 +46,7 @@ constexpr int RTQ_NORM_WV = 8;
 // grid rows (wave: rows / 4), 256 threads: y = rmsnorm(a (+ b)); with b, h = a + b is written too
 extern "C" __global__ __launch_bounds__(256) void rtq_m_rmsnorm(MNormArgs a) {
   if (a.wave) {  // one wave per row: no workgroup barrier, every load issued at once
-    const int r = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63, nv = a.d / 256;
+    const int r = (int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)), lane = threadIdx.x & 63, nv = a.d / 256;
     if (r >= a.rows) return;
     const int64_t ro = (int64_t)r * a.d + 4 * lane;
     f4 xv[RTQ_NORM_WV], wv[RTQ_NORM_WV];
@@ -109,7 +109,7 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_rmsnorm(MNormArgs a) {
 // grid rows (wave: rows / 4), 256 threads: out = (res +) rmsnorm_backward(x, w, inv, dy)
 extern "C" __global__ __launch_bounds__(256) void rtq_m_rmsnorm_bwd(MNormBwdArgs a) {
   if (a.wave) {  // one wave per row, as the forward
-    const int r = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63, nv = a.d / 256;
+    const int r = (int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)), lane = threadIdx.x & 63, nv = a.d / 256;
     if (r >= a.rows) return;
     const int64_t ro = (int64_t)r * a.d + 4 * lane;
     const float ir = a.inv[r];
