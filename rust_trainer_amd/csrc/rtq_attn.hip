@@ -34,7 +34,7 @@ constexpr int kMergeBatch = 8;  // merges of up to this many slots issue all the
 // each thread of the row)
 __device__ __forceinline__ void attn_merge_fwd(const MAttnArgs& a, const MAttnMerge& mg, int e4) {
   const int HD = a.hd, rl = 4 * e4 / HD, c = 4 * e4 % HD, row = mg.blk * 16 + rl;
-  if (row >= a.t) return;
+  if (row >= mg.rlen) return;  // rows of the block's sequence (rbase, rlen: MAttnItem)
   const float* p0 = a.part + (int64_t)mg.s0 * (32 * HD);
   float m = -__builtin_inff(), l = 0.0f;
   f4 o = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -75,8 +75,8 @@ __device__ __forceinline__ void attn_merge_fwd(const MAttnArgs& a, const MAttnMe
   f4 y;
 #pragma unroll
   for (int e = 0; e < 4; e++) y[e] = __fdiv_rn(o[e], l);
-  *reinterpret_cast<f4*>(a.o + (int64_t)row * a.ldq + (int64_t)mg.head * HD + c) = y;
-  if (c == 0) a.lse[(int64_t)mg.head * a.t + row] = m * 0.693147180559945309417f + logf(l);
+  *reinterpret_cast<f4*>(a.o + ((int64_t)mg.rbase + row) * a.ldq + (int64_t)mg.head * HD + c) = y;
+  if (c == 0) a.lse[(int64_t)mg.head * a.t + mg.rbase + row] = m * 0.693147180559945309417f + logf(l);
 }
 
 // ------------------------------------------------------------------ backward
@@ -126,4 +126,42 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_attn_merge_bwd(MAttnArgs
     const int bq = b - a.n_merges2 * pk, mi = bq / pq, e4 = (bq % pq) * 256 + threadIdx.x;
     if (mi < a.n_merges && e4 < 4 * a.hd) attn_merge_sum(a, a.merges[mi], e4, false);
   }
+}
+
+// ------------------------------------------------------------------ packed forward: sequences
+// gather: one workgroup per gathered row r of q (nh hd floats), k, v (nkv hd each) from packed row
+// gmap[r] (rows with gmap[r] < 0 are zero), 16-byte loads and stores
+extern "C" __global__ __launch_bounds__(256) void rtq_m_seq_gather(MSeqArgs a) {
+  const int r = blockIdx.x;
+  if (r >= a.tv) return;
+  const int src = a.gmap[r];
+  const int qd4 = a.nh * a.hd / 4, kd4 = a.nkv * a.hd / 4;
+  const f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int e = threadIdx.x; e < qd4 + 2 * kd4; e += 256) {
+    const float* s;
+    float* d;
+    if (e < qd4) {
+      s = a.q + (int64_t)src * a.ldq + 4 * e;
+      d = a.gq + (int64_t)r * (4 * qd4) + 4 * e;
+    } else if (e < qd4 + kd4) {
+      s = a.k + (int64_t)src * a.ldk + 4 * (e - qd4);
+      d = a.gk + (int64_t)r * (4 * kd4) + 4 * (e - qd4);
+    } else {
+      s = a.v + (int64_t)src * a.ldv + 4 * (e - qd4 - kd4);
+      d = a.gv + (int64_t)r * (4 * kd4) + 4 * (e - qd4 - kd4);
+    }
+    *reinterpret_cast<f4*>(d) = src >= 0 ? *reinterpret_cast<const f4*>(s) : z;
+  }
+}
+// scatter: one workgroup per packed row i: o row from gathered row sidx[i] (and lse per head)
+extern "C" __global__ __launch_bounds__(256) void rtq_m_seq_scatter(MSeqArgs a) {
+  const int i = blockIdx.x;
+  if (i >= a.t) return;
+  const int src = a.sidx[i];
+  const int qd4 = a.nh * a.hd / 4;
+  for (int e = threadIdx.x; e < qd4; e += 256)
+    *reinterpret_cast<f4*>(a.o + (int64_t)i * a.ldq + 4 * e) =
+        *reinterpret_cast<const f4*>(a.go + (int64_t)src * (4 * qd4) + 4 * e);
+  if (a.glse)
+    for (int h = threadIdx.x; h < a.nh; h += 256) a.lse[(int64_t)h * a.t + i] = a.glse[(int64_t)h * a.tv + src];
 }

@@ -154,12 +154,16 @@ __device__ __forceinline__ void fa_fwd(const MAttnArgs& a, const MAttnItem& it, 
   constexpr int NC = HD / 16, NK = HD / 32, LDK = FaFwdLds<HD>::LDK, LDV = FaFwdLds<HD>::LDV;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
   const int h = it.head, kvh = h / (a.nh / a.nkv), qb = it.blk, r0 = qb * 64 + 16 * w;
+  // the item's sequence: rows [rbase, rbase + tl) (the whole step, or a packed layout's segment
+  // gathered; the mask and the clamps work on its rows)
+  const int tl = it.rlen;
+  const int64_t rb = it.rbase;
   // q rows of the wave times scale log2(e) (scores in base 2: p = 2^(s2 - m2)), f16 hi / lo
   // operand fragments
   const float qs2 = a.scale * kLog2e;
   half8 qh[NK], ql[NK];
   {
-    const float* qr = a.q + (int64_t)min(r0 + li, a.t - 1) * a.ldq + (int64_t)h * HD + 8 * g;
+    const float* qr = a.q + (rb + min(r0 + li, tl - 1)) * a.ldq + (int64_t)h * HD + 8 * g;
 #pragma unroll
     for (int c = 0; c < NK; c++) {
       u2v h0, l0, h1, l1;
@@ -182,14 +186,14 @@ __device__ __forceinline__ void fa_fwd(const MAttnArgs& a, const MAttnItem& it, 
     mr[i] = -__builtin_inff();
     lr[i] = 0.0f;
   }
-  const float* kb = a.k + (int64_t)kvh * HD;
-  const float* vb = a.v + (int64_t)kvh * HD;
+  const float* kb = a.k + rb * a.ldk + (int64_t)kvh * HD;
+  const float* vb = a.v + rb * a.ldv + (int64_t)kvh * HD;
   FaNat<HD> kn;
   FaTr<HD> vn;
   int kt = fa_next_live(a, qb, it.b0, it.b1);
   if (kt < it.b1) {
-    kn.load(kb, a.ldk, kt * 64, a.t);
-    vn.load(vb, a.ldv, kt * 64, a.t);
+    kn.load(kb, a.ldk, kt * 64, tl);
+    vn.load(vb, a.ldv, kt * 64, tl);
   }
   while (kt < it.b1) {  // kt is workgroup-uniform: every wave runs the same barriers
     const int k0 = kt * 64;
@@ -198,8 +202,8 @@ __device__ __forceinline__ void fa_fwd(const MAttnArgs& a, const MAttnItem& it, 
     __syncthreads();
     const int kt2 = fa_next_live(a, qb, kt + 1, it.b1);
     if (kt2 < it.b1) {
-      kn.load(kb, a.ldk, kt2 * 64, a.t);
-      vn.load(vb, a.ldv, kt2 * 64, a.t);
+      kn.load(kb, a.ldk, kt2 * 64, tl);
+      vn.load(vb, a.ldv, kt2 * 64, tl);
     }
     f4 s[4] = {zero, zero, zero, zero};
 #pragma unroll
@@ -220,7 +224,7 @@ __device__ __forceinline__ void fa_fwd(const MAttnArgs& a, const MAttnItem& it, 
       float mx = -__builtin_inff();
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        p[j][i] = fa_ok(row, k0 + 16 * j + li, si[i], sk[j], a.t) ? s[j][i] : -__builtin_inff();
+        p[j][i] = fa_ok(row, k0 + 16 * j + li, si[i], sk[j], tl) ? s[j][i] : -__builtin_inff();
         mx = fmaxf(mx, p[j][i]);
       }
       mx = group16_max(mx);
@@ -259,11 +263,11 @@ __device__ __forceinline__ void fa_fwd(const MAttnArgs& a, const MAttnItem& it, 
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int row = r0 + 4 * g + i;
-      if (row >= a.t) continue;
-      float* orow = a.o + (int64_t)row * a.ldq + (int64_t)h * HD + li;
+      if (row >= tl) continue;
+      float* orow = a.o + (rb + row) * a.ldq + (int64_t)h * HD + li;
 #pragma unroll
       for (int c = 0; c < NC; c++) orow[16 * c] = __fdiv_rn(oacc[c][i], lr[i]);
-      if (li == 0) a.lse[(int64_t)h * a.t + row] = mr[i] * kLn2 + logf(lr[i]);  // natural log-sum-exp
+      if (li == 0) a.lse[(int64_t)h * a.t + rb + row] = mr[i] * kLn2 + logf(lr[i]);  // natural log-sum-exp
     }
   } else {  // partials: o, m (base 2), l
     float* pp = a.part + (int64_t)(it.slot + w * it.pad0) * (32 * HD);

@@ -38,6 +38,8 @@ enum RtqModelKernel {
   KM_FA_BWD64,
   KM_FA_BWD128,
   KM_ATTN_BWD_PREP128,
+  KM_SEQ_GATHER,  // the forward attention of a packed layout over each segment's logical sequence
+  KM_SEQ_SCATTER,
   KM_COUNT
 };
 

@@ -385,13 +385,39 @@ struct MSoftArgs {
 // forward and dQ passes; (KV head, 16-key block, range of (group head, 64-query tile) pairs
 // p = head_in_group * ceil(t / 64) + tile) for the dK / dV pass.  slot >= 0: the item covers part
 // of its block's range and writes a partial to part[slot] (merged by rtq_m_attn_merge in slot
-// order); slot < 0: it covers the whole range and writes the result.
+// order); slot < 0: it covers the whole range and writes the result.  pad0: the number of items
+// of the item's block.  rbase, rlen: the item's sequence is rows [rbase, rbase + rlen) of q, k,
+// v, o (and columns of lse): the whole step (0, t), or, for the forward of a packed layout, one
+// segment's logical sequence gathered to those rows (MSeqArgs); blk and b0, b1 count from rbase.
 struct MAttnItem {
-  int head, blk, b0, b1, slot, pad0, pad1, pad2;
+  int head, blk, b0, b1, slot, pad0, rbase, rlen;
 };
-// one block whose items wrote partials to slots [s0, s0 + n)
+// one block whose items wrote partials to slots [s0, s0 + n); rbase, rlen as its items'
 struct MAttnMerge {
-  int head, blk, s0, n;
+  int head, blk, s0, n, rbase, rlen;
+};
+// the forward attention of a packed layout runs over each segment's logical sequence: the rows
+// whose segment is 0 or that segment, in packed order (for segment 0, its rows alone), gathered
+// to back-to-back runs of rows that start at multiples of 64 (Rope::allowed, src/ops.rs:158-164:
+// a row attends to exactly the earlier rows of its sequence, so each key tile covers the same
+// logical positions as in the example's own run).  gather: q, k, v rows gmap[r] (-1: zero) to
+// row r of gq, gk, gv for r < tv; scatter: each packed row i's own copy, row sidx[i] of go (and of
+// glse, when not null), back to o (lse).
+struct MSeqArgs {
+  const float* q;    // packed [t][nh][hd] (ldq)
+  const float* k;    // [t][nkv][hd] (ldk)
+  const float* v;    // (ldv)
+  float* gq;         // gathered [tv][nh][hd] (row stride nh hd), gk, gv [tv][nkv][hd]
+  float* gk;
+  float* gv;
+  const float* go;   // gathered output [tv][nh][hd], log-sum-exp [nh][tv] (or null)
+  const float* glse;
+  float* o;          // packed output (ldq), lse [nh][t]
+  float* lse;
+  const int32_t* gmap;  // [tv]
+  const int32_t* sidx;  // [t]
+  int t, tv, nh, nkv, hd;
+  int64_t ldq, ldk, ldv;
 };
 struct MAttnArgs {
   const float* q;   // [t][nh][hd] (rotated, row stride ldq)

@@ -160,7 +160,9 @@ struct rtq_model {
   // the probability-matrix path's products on split 16-bit MFMA (rtq_m_gemm*_hf forward, *_bf
   // backward); RTQ_ATTN_F32=1 at load time keeps them on f32 MFMA (rtq_m_gemm*), for comparison
   bool attn_f32 = false;
-  int attn_items = 2;  // fused attention work items per CU aimed at (RTQ_ATTN_ITEMS; 0: rows never cut)
+  // fused attention: long query rows cut into pieces (attn_piece) and dk / dv ranges into pieces
+  // aiming at attn_items work items per CU (RTQ_ATTN_ITEMS; 0: nothing is cut)
+  int attn_items = 2;
   int64_t layout_fused = -1;  // attn_fused the step buffers were laid out for
   float* attn_D = nullptr;  // [nh x t] dO . o per query row
   uint16_t* attn_planes = nullptr;  // the fused backward's 16-bit operand planes (MAttnArgs::p*)
@@ -175,6 +177,26 @@ struct rtq_model {
   int64_t attn_t = -1;
   bool attn_packed = false;
   std::vector<int32_t> attn_seg;  // the segments the tables were built for
+  // packed layouts: the forward attention over each segment's logical sequence (MSeqArgs): the
+  // sequences' rows gathered back to back (gmap: packed row of each gathered row; sidx: each
+  // packed row's own copy), the gathered q, k, v, o (and lse), and for the fused kernels the
+  // sequences' items, merges and partial slots.  seq_on: this layout's forward runs that way
+  // (off when the gathered rows would exceed 4 t + 64 per sequence: the packed rows' own tiles)
+  struct SeqRun {
+    int64_t base, len;
+  };
+  std::vector<SeqRun> seqs;
+  std::vector<int32_t> seq_seg;  // the segments the sequences were built for
+  bool seq_on = false, seq_fused = false;
+  int64_t tv = 0;
+  void* seq_mem = nullptr;
+  size_t seq_cap = 0;
+  int32_t *gmap_d = nullptr, *sidx_d = nullptr;
+  float *gq = nullptr, *gk = nullptr, *gv = nullptr, *go = nullptr, *glse = nullptr, *seq_part = nullptr;
+  MAttnItem* it_seq = nullptr;
+  MAttnMerge* mg_seq = nullptr;
+  int n_sit = 0, n_smg = 0;
+  bool seq_pass = false;  // a sequence's unfused forward is running: its products take no liveness map
   // rtq_model_debug_capture: one layer's tensors copied during the step
   int64_t dbg_layer = -1;
   std::vector<std::pair<std::string, std::pair<float*, int64_t>>> dbg;
@@ -298,7 +320,8 @@ enum GemmSplit { SPLIT_HF, SPLIT_BF };
 rtq_status k_gemm(rtq_model* m, int64_t M, int64_t N, int64_t K, int64_t batch, Op A, Op B, float* C, int64_t sCb,
                   int64_t sCm, int64_t sCn, float a_scale, int causal, int acc, GemmSplit split) {
   MGemmArgs ga{A.p, B.p, C, (int)M, (int)N, (int)K, A.sb, A.s0, A.s1, B.sb, B.s0, B.s1, sCb, sCm, sCn, A.div, B.div,
-               a_scale, causal, acc, (int)batch, causal && m->packed ? m->live_d : nullptr, (int)m->nlb, nullptr};
+               a_scale, causal, acc, (int)batch, causal && m->packed && !m->seq_pass ? m->live_d : nullptr,
+               (int)m->nlb, nullptr};
   // 64-row tiles when the grid fills the chip twice over, else 32-row tiles (twice the workgroups)
   const int64_t tiles64 = (N + 63) / 64 * ((M + 63) / 64) * batch / (causal == 1 ? 2 : 1);
   const int bm = tiles64 >= 2 * 256 ? 64 : 32;
@@ -669,6 +692,35 @@ rtq_status upload_layout(rtq_model* m, const int32_t* seg, int64_t t) {
   return RTQ_OK;
 }
 
+// tiles per piece of query block qb's key range (the forward and dq items): 3 for the first eight
+// blocks, 6 after (never cut with attn_items 0).  A rule of the block index alone, so that a query
+// row's pieces, and so its bits, are the same at every sequence length and in a packed layout's
+// logical sequences.  Measured on the Qwen3-0.6B-shaped step: shorter pieces cost more in merges
+// than they gain, longer ones leave the longest rows as the tail (2048 tokens: 48.2 ms at 6 tiles,
+// 52.0 uncut; 512: 12.98 at 3, 13.44 at 2).
+int64_t attn_piece(const rtq_model* m, int64_t qb) {
+  return m->attn_items > 0 ? (qb < 8 ? 3 : 6) : INT32_MAX;
+}
+
+// appends the items of one block (live tiles L, cut into pieces of `chunk`) of the sequence at
+// rows [rbase, rbase + rlen): a block cut into n > 1 pieces takes 4 n slots, 16-row sub-block w of
+// piece i writing slot s0 + i + w n, so each sub-block's n partials are contiguous (one merge each)
+void attn_cut(const std::vector<int>& L, int64_t chunk, int head, int blk, int rbase, int rlen, int& slots,
+              std::vector<MAttnItem>& items, std::vector<MAttnMerge>& merges) {
+  const int n = (int)((L.size() + chunk - 1) / chunk);
+  if (n == 0) return;
+  const int s0 = n > 1 ? slots : -1;
+  for (int i = 0; i < n; i++) {
+    const int a0 = L[(size_t)(i * chunk)], a1 = L[std::min(L.size(), (size_t)((i + 1) * chunk)) - 1] + 1;
+    items.push_back(MAttnItem{head, blk, a0, a1, n > 1 ? s0 + i : -1, n, rbase, rlen});
+  }
+  if (n > 1) {
+    for (int w = 0; w < 4; w++)
+      if ((4 * blk + w) * 16 < rlen) merges.push_back(MAttnMerge{head, 4 * blk + w, s0 + w * n, n, rbase, rlen});
+    slots += 4 * n;
+  }
+}
+
 // work tables of the fused attention for t tokens and the current layout (segments or null):
 // forward / dq items (head, 16-row query block, range of its live 64-key tiles) and dk / dv items
 // (KV head, 16-key block, range of its live (group head, 64-query tile) pairs), each block's list
@@ -692,52 +744,30 @@ rtq_status ensure_attn_plan(rtq_model* m, int64_t t, const int32_t* seg) {
   // items of 64 rows (one workgroup of four waves each): a query block's live key tiles (forward,
   // dq), a key block's live (group head, query tile) pairs (dk, dv)
   std::vector<std::vector<int>> fl((size_t)nlb), kl((size_t)nlb);
-  int64_t fu = 0, ku = 0;
-  for (int64_t qb = 0; qb < nlb; qb++) {
+  int64_t ku = 0;
+  for (int64_t qb = 0; qb < nlb; qb++)
     for (int64_t kt = 0; kt <= qb; kt++)
       if (lv(qb, kt)) fl[(size_t)qb].push_back((int)kt);
-    fu += (int64_t)fl[(size_t)qb].size() * nh;
-  }
   for (int64_t kb = 0; kb < nlb; kb++) {
     for (int hr = 0; hr < grp; hr++)
       for (int64_t qt = kb; qt < nkt; qt++)
         if (lv(qt, kb)) kl[(size_t)kb].push_back((int)(hr * nkt + qt));
     ku += (int64_t)kl[(size_t)kb].size() * nkv;
   }
-  // ranges are cut into pieces (partials merged after) of about the length that gives attn_items
-  // workgroups per CU, kept within 3 .. 6 tiles: measured on the Qwen3-0.6B-shaped step from 512 to
-  // 2048 tokens, shorter pieces cost more in merges than they gain, longer ones leave the longest
-  // rows as the tail (2048 tokens: 48.2 ms at 6 tiles, 52.0 uncut; 512: 12.98 at 3, 13.44 at 2).
-  // attn_items 0: no cuts, no merges.
+  // dk / dv ranges are cut into pieces (partials merged after) of about the length that gives
+  // attn_items workgroups per CU, kept within 3 .. 6 tiles; query blocks by attn_piece (a rule of
+  // the block index alone).  attn_items 0: no cuts, no merges.
   const int64_t target = (int64_t)m->attn_items * rtq_ctx_cu_count(m->ctx);
-  auto piece = [&](int64_t units, int64_t whole) {
-    return target > 0 ? std::min<int64_t>(6, std::max<int64_t>(3, (units + target - 1) / target)) : whole;
-  };
-  const int64_t cf = piece(fu, nkt + 1), ck = piece(ku, (int64_t)grp * nkt + 1);
+  const int64_t ck = target > 0 ? std::min<int64_t>(6, std::max<int64_t>(3, (ku + target - 1) / target))
+                                : (int64_t)grp * nkt + 1;
   std::vector<MAttnItem> itf, itk;
   std::vector<MAttnMerge> mf, mk;
   int slots_f = 0, slots_k = 0;
-  // a block cut into n > 1 pieces takes 4 n slots: 16-row sub-block w of piece i writes slot
-  // s0 + i + w n, so each sub-block's n partials are contiguous (one merge per sub-block)
-  auto cut = [t](const std::vector<int>& L, int64_t chunk, int head, int blk, int& slots, std::vector<MAttnItem>& items,
-                 std::vector<MAttnMerge>& merges) {
-    const int n = (int)((L.size() + chunk - 1) / chunk);
-    if (n == 0) return;
-    const int s0 = n > 1 ? slots : -1;
-    for (int i = 0; i < n; i++) {
-      const int a0 = L[(size_t)(i * chunk)], a1 = L[std::min(L.size(), (size_t)((i + 1) * chunk)) - 1] + 1;
-      items.push_back(MAttnItem{head, blk, a0, a1, n > 1 ? s0 + i : -1, n, 0, 0});
-    }
-    if (n > 1) {
-      for (int w = 0; w < 4; w++)
-        if ((int64_t)(4 * blk + w) * 16 < t) merges.push_back(MAttnMerge{head, 4 * blk + w, s0 + w * n, n});
-      slots += 4 * n;
-    }
-  };
   for (int h = 0; h < nh; h++)
-    for (int64_t qb = 0; qb < nlb; qb++) cut(fl[(size_t)qb], cf, h, (int)qb, slots_f, itf, mf);
+    for (int64_t qb = 0; qb < nlb; qb++)
+      attn_cut(fl[(size_t)qb], attn_piece(m, qb), h, (int)qb, 0, (int)t, slots_f, itf, mf);
   for (int g = 0; g < nkv; g++)
-    for (int64_t kb = 0; kb < nlb; kb++) cut(kl[(size_t)kb], ck, g, (int)kb, slots_k, itk, mk);
+    for (int64_t kb = 0; kb < nlb; kb++) attn_cut(kl[(size_t)kb], ck, g, (int)kb, 0, (int)t, slots_k, itk, mk);
   // the merges by (head, 16-row block), for the QK backward that sums the slots itself
   const int64_t nb16 = (t + 15) / 16;
   std::vector<int32_t> qmi((size_t)(nh * nb16), -1), kmi((size_t)(nkv * nb16), -1);
@@ -785,6 +815,110 @@ rtq_status ensure_attn_plan(rtq_model* m, int64_t t, const int32_t* seg) {
   m->attn_packed = packed;
   m->gen++;
   m->attn_seg.assign(seg ? seg : seg, seg ? seg + t : seg);
+  return RTQ_OK;
+}
+
+// the packed layout's logical sequences (MSeqArgs) for t tokens of segments seg: for each segment
+// value s present, in increasing order, the rows whose segment is 0 or s in packed order, at rows
+// [base, base + len) of the gathered buffers (base a multiple of 64); each packed row's own copy
+// is the one in its segment's sequence.  With the fused kernels, also the sequences' items: for
+// every head and 64-row block of a sequence holding one of its own rows, key tiles 0 .. qb cut by
+// attn_piece, exactly the items an unpacked step of that sequence alone would run (its rows at
+// rbase = base).  Rebuilt when the segments or the attention path change.
+rtq_status ensure_seq_plan(rtq_model* m, int64_t t, const int32_t* seg) {
+  if (!seg) {
+    m->seq_on = false;
+    return RTQ_OK;
+  }
+  if (m->seq_fused == m->attn_fused && (int64_t)m->seq_seg.size() == t && std::equal(m->seq_seg.begin(), m->seq_seg.end(), seg))
+    return RTQ_OK;
+  const rtq_model_config& c = m->cfg;
+  const int64_t nh = c.n_head, qd = nh * c.head_dim, kd = c.n_head_kv * c.head_dim;
+  std::vector<int32_t> vals(seg, seg + t);
+  std::sort(vals.begin(), vals.end());
+  vals.erase(std::unique(vals.begin(), vals.end()), vals.end());
+  int64_t n0 = 0;
+  for (int64_t i = 0; i < t; i++) n0 += seg[i] == 0;
+  int64_t tv = 0;
+  for (int32_t v : vals) {
+    int64_t len = n0;
+    if (v != 0)
+      for (int64_t i = 0; i < t; i++) len += seg[i] == v;
+    tv += (len + 63) / 64 * 64;
+  }
+  m->seq_seg.assign(seg, seg + t);
+  m->seq_fused = m->attn_fused;
+  m->seqs.clear();
+  m->gen++;
+  m->seq_on = tv <= 4 * t + 64 * (int64_t)vals.size();
+  if (!m->seq_on) return RTQ_OK;
+  std::vector<int32_t> gmap, sidx((size_t)t, -1);
+  gmap.reserve((size_t)tv);
+  for (int32_t v : vals) {
+    const int64_t base = (int64_t)gmap.size();
+    for (int64_t i = 0; i < t; i++)
+      if (seg[i] == 0 || seg[i] == v) {
+        if (seg[i] == v) sidx[(size_t)i] = (int32_t)gmap.size();
+        gmap.push_back((int32_t)i);
+      }
+    m->seqs.push_back(rtq_model::SeqRun{base, (int64_t)gmap.size() - base});
+    while (gmap.size() % 64) gmap.push_back(-1);
+  }
+  std::vector<MAttnItem> its;
+  std::vector<MAttnMerge> mgs;
+  int slots = 0;
+  if (m->attn_fused) {
+    std::vector<int> L;
+    for (int64_t h = 0; h < nh; h++)
+      for (size_t q = 0; q < m->seqs.size(); q++) {
+        const rtq_model::SeqRun& r = m->seqs[q];
+        for (int64_t qb = 0; qb * 64 < r.len; qb++) {
+          bool own = false;
+          for (int64_t p = qb * 64; p < std::min(r.len, qb * 64 + 64) && !own; p++)
+            own = seg[gmap[(size_t)(r.base + p)]] == vals[q];
+          if (!own) continue;
+          L.resize((size_t)qb + 1);
+          for (int64_t kt = 0; kt <= qb; kt++) L[(size_t)kt] = (int)kt;
+          attn_cut(L, attn_piece(m, qb), (int)h, (int)qb, (int)r.base, (int)r.len, slots, its, mgs);
+        }
+      }
+  }
+  const auto al = [](size_t b) { return (b + 255) / 256 * 256; };
+  const size_t bytes = al((size_t)tv * 4) + al((size_t)t * 4) + al(its.size() * sizeof(MAttnItem)) +
+                       al(mgs.size() * sizeof(MAttnMerge)) + al((size_t)(tv * qd) * 4) * 2 +
+                       al((size_t)(tv * kd) * 4) * 2 + al((size_t)(nh * tv) * 4) +
+                       al((size_t)std::max(slots, 1) * 32 * (size_t)c.head_dim * 4);
+  M_HIP(hipStreamSynchronize(stream_of(m)));
+  if (bytes > m->seq_cap) {
+    if (m->seq_mem) M_HIP(hipFree(m->seq_mem));
+    m->seq_mem = nullptr;
+    m->seq_cap = 0;
+    M_HIP(hipMalloc(&m->seq_mem, bytes));
+    m->seq_cap = bytes;
+  }
+  char* p = (char*)m->seq_mem;
+  auto take = [&](size_t b) {
+    char* q = p;
+    p += al(b);
+    return q;
+  };
+  m->gmap_d = (int32_t*)take((size_t)tv * 4);
+  m->sidx_d = (int32_t*)take((size_t)t * 4);
+  m->it_seq = (MAttnItem*)take(its.size() * sizeof(MAttnItem));
+  m->mg_seq = (MAttnMerge*)take(mgs.size() * sizeof(MAttnMerge));
+  m->gq = (float*)take((size_t)(tv * qd) * 4);
+  m->go = (float*)take((size_t)(tv * qd) * 4);
+  m->gk = (float*)take((size_t)(tv * kd) * 4);
+  m->gv = (float*)take((size_t)(tv * kd) * 4);
+  m->glse = (float*)take((size_t)(nh * tv) * 4);
+  m->seq_part = (float*)take((size_t)std::max(slots, 1) * 32 * (size_t)c.head_dim * 4);
+  M_HIP(hipMemcpy(m->gmap_d, gmap.data(), gmap.size() * 4, hipMemcpyHostToDevice));
+  M_HIP(hipMemcpy(m->sidx_d, sidx.data(), sidx.size() * 4, hipMemcpyHostToDevice));
+  if (!its.empty()) M_HIP(hipMemcpy(m->it_seq, its.data(), its.size() * sizeof(MAttnItem), hipMemcpyHostToDevice));
+  if (!mgs.empty()) M_HIP(hipMemcpy(m->mg_seq, mgs.data(), mgs.size() * sizeof(MAttnMerge), hipMemcpyHostToDevice));
+  m->tv = tv;
+  m->n_sit = (int)its.size();
+  m->n_smg = (int)mgs.size();
   return RTQ_OK;
 }
 
@@ -959,21 +1093,52 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, float* x, float* y, boo
   M_TRY(rtq_model_launch(m->ctx, KM_QK_PREP, dim3(qk_grid(m, t * (nh + 2 * nkv))), dim3(256), stream_of(m),
                          &qa));
   const float scale = 1.0f / sqrtf((float)hd);
-  if (m->attn_fused) {  // fused: o and each row's log-sum-exp, no probability matrix
+  // a packed layout's forward runs over each segment's logical sequence (ensure_seq_plan): every
+  // row gets the bits of its example's own unpacked step
+  const bool seq = m->packed && m->seq_on;
+  const MSeqArgs sq{k.q, k.k, k.v, m->gq, m->gk, m->gv, m->go, m->attn_fused ? m->glse : nullptr, k.o, k.lse,
+                    m->gmap_d, m->sidx_d, (int)t, (int)m->tv, (int)nh, (int)nkv, (int)hd, qd, kd, kd};
+  if (seq)
+    M_TRY(rtq_model_launch(m->ctx, KM_SEQ_GATHER, dim3((unsigned)m->tv), dim3(256), stream_of(m), &sq));
+  if (m->attn_fused && seq) {
+    MAttnArgs aa = attn_args(m, k, t);
+    aa.q = m->gq, aa.k = m->gk, aa.v = m->gv, aa.o = m->go, aa.lse = m->glse, aa.part = m->seq_part;
+    aa.seg = nullptr, aa.live = nullptr, aa.nlb = 0, aa.t = (int)m->tv;
+    M_TRY(attn_launch(m, hd == 64 ? KM_FA_FWD64 : KM_FA_FWD128, aa, m->it_seq, m->n_sit));
+    M_TRY(attn_merge(m, KM_ATTN_MERGE_FWD, aa, m->mg_seq, m->n_smg));
+  } else if (m->attn_fused) {  // fused: o and each row's log-sum-exp, no probability matrix
     const MAttnArgs aa = attn_args(m, k, t);
     M_TRY(attn_launch(m, hd == 64 ? KM_FA_FWD64 : KM_FA_FWD128, aa, m->it_fwd, m->n_fwd));
     M_TRY(attn_merge(m, KM_ATTN_MERGE_FWD, aa, m->mg_fwd, m->n_mfwd));
   } else {
-  // S = (q scale) K^T per head (causal), softmax in place, O = P V
+  if (seq) {  // each sequence as an unpacked step of its own length (dP holds its probabilities)
+    m->seq_pass = true;
+    for (const rtq_model::SeqRun& r : m->seqs) {
+      const int64_t n = r.len;
+      const float *gq = m->gq + r.base * qd, *gk = m->gk + r.base * kd, *gv = m->gv + r.base * kd;
+      M_TRY(k_gemm(m, n, n, hd, nh, Op{gq, hd, qd, 1, 1}, Op{gk, hd, 1, kd, (int)grp}, m->dP, n * n, n, 1, scale, 1,
+                   0, SPLIT_HF));
+      MSoftArgs ss{m->dP, nullptr, nullptr, (int)n, (int)nh, scale, nullptr, nullptr, 0};
+      M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX, dim3((unsigned)((n + 3) / 4), (unsigned)nh), dim3(256),
+                             stream_of(m), &ss));
+      M_TRY(k_gemm(m, n, hd, n, nh, Op{m->dP, n * n, n, 1, 1}, Op{gv, hd, kd, 1, (int)grp}, m->go + r.base * qd, hd,
+                   qd, 1, 1.0f, 2, 0, SPLIT_HF));
+    }
+    m->seq_pass = false;
+  }
+  // S = (q scale) K^T per head (causal), softmax in place, O = P V (a packed layout's P, for the
+  // backward, over the packed rows)
   M_TRY(k_gemm(m, t, t, hd, nh, Op{k.q, hd, qd, 1, 1}, Op{k.k, hd, 1, kd, (int)grp}, k.P, t * t, t, 1, scale, 1, 0,
                SPLIT_HF));
   MSoftArgs sa{k.P, nullptr, nullptr, (int)t, (int)nh, scale, m->packed ? m->seg_d : nullptr,
                m->packed ? m->live_d : nullptr, (int)m->nlb};
   M_TRY(rtq_model_launch(m->ctx, KM_SOFTMAX, dim3((unsigned)((t + 3) / 4), (unsigned)nh), dim3(256), stream_of(m),
                          &sa));
-  M_TRY(k_gemm(m, t, hd, t, nh, Op{k.P, t * t, t, 1, 1}, Op{k.v, hd, kd, 1, (int)grp}, k.o, hd, qd, 1, 1.0f, 2, 0,
-               SPLIT_HF));
+  if (!seq)
+    M_TRY(k_gemm(m, t, hd, t, nh, Op{k.P, t * t, t, 1, 1}, Op{k.v, hd, kd, 1, (int)grp}, k.o, hd, qd, 1, 1.0f, 2, 0,
+                 SPLIT_HF));
   }
+  if (seq) M_TRY(rtq_model_launch(m->ctx, KM_SEQ_SCATTER, dim3((unsigned)t), dim3(256), stream_of(m), &sq));
   M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LO]], k.o, t, m->mo));
   M_TRY(k_norm(m, x, m->mo, k.h, L.ffn_norm, k.n2, k.inv2, t, d, 0));  // h = x + attn, n2 = rmsnorm(h)
   float *g, *u;
@@ -1436,6 +1601,7 @@ void rtq_model_destroy(rtq_model* m) {
   if (m->lgt_mem) (void)hipFree(m->lgt_mem);
   if (m->lgt_host) (void)hipHostFree(m->lgt_host);
   if (m->attn_mem) (void)hipFree(m->attn_mem);
+  if (m->seq_mem) (void)hipFree(m->seq_mem);
   delete m;
 }
 
@@ -1749,6 +1915,7 @@ rtq_status step(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* p
   M_TRY(ensure_rope(m, t, positions));
   M_TRY(upload_layout(m, segments, t));
   if (m->attn_fused) M_TRY(ensure_attn_plan(m, t, segments));
+  M_TRY(ensure_seq_plan(m, t, segments));
   hipStream_t st = stream_of(m);
   // host inputs and outputs pass through pinned staging, so the copies are asynchronous; the
   // staging is free again once the step's synchronisation below returns
@@ -1780,7 +1947,8 @@ rtq_status step(rtq_model* m, const int32_t* tokens, int64_t t, const int32_t* p
   if (graphable)
     key = {(uint64_t)t, (uint64_t)n, weights ? 1u : 0u, m->packed ? 1u : 0u, (uint64_t)m->nlb,
            m->ckpt ? 1u : 0u, m->defer_lg ? 1u : 0u, m->attn_fused ? 1u : 0u, (uint64_t)m->n_fwd,
-           (uint64_t)m->n_kv, (uint64_t)m->n_mfwd, (uint64_t)m->n_mkv, m->gen, rtq_ctx_ws_gen(m->ctx)};
+           (uint64_t)m->n_kv, (uint64_t)m->n_mfwd, (uint64_t)m->n_mkv, m->packed && m->seq_on ? 1u : 0u,
+           (uint64_t)m->tv, (uint64_t)m->n_sit, (uint64_t)m->n_smg, m->gen, rtq_ctx_ws_gen(m->ctx)};
   if (graphable && m->gexec && key == m->gkey) {
     M_HIP(hipGraphLaunch(m->gexec, st));
     m->graph_replays++;

@@ -175,7 +175,8 @@ constexpr const char* kKernelNames[] = {
     "rtq_m_attn_merge_fwd", "rtq_m_attn_merge_bwd",
     "rtq_m_attn_bwd_prep64", "rtq_m_gemm_bf",       "rtq_m_gemm32_bf",
     "rtq_m_gemm32g_bf",     "rtq_m_gemm_hf",        "rtq_m_gemm32_hf",      "rtq_m_fa_fwd64",
-    "rtq_m_fa_fwd128",      "rtq_m_fa_bwd64",       "rtq_m_fa_bwd128",      "rtq_m_attn_bwd_prep128"};
+    "rtq_m_fa_fwd128",      "rtq_m_fa_bwd64",       "rtq_m_fa_bwd128",      "rtq_m_attn_bwd_prep128",
+    "rtq_m_seq_gather",     "rtq_m_seq_scatter"};
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT, "one name per kernel id, in id order");
 
 struct TimedLaunch {

@@ -162,6 +162,30 @@ def test_model_step_config3_layer_shape(ctx):
     model.close()
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_model_step_f32_hd128_long_rows_matches_oracle(ctx, fused, monkeypatch):
+    """head size = RoPE size = 128 (the half-wave QK-norm + RoPE kernels, whose backward also sums
+    the cut blocks' partial slots on every layer but a captured one) at 600 tokens (fused: rows of
+    up to ten key tiles cut into pieces and merged), F32 weights against the oracle at 1e-3; then
+    the same step with nothing cut (RTQ_ATTN_ITEMS=0) against the default: log-probs within 1e-5
+    (f32 rounding of the forward merges), gradients within 5e-5 (the attention backward's products
+    carry 16 significant bits, about 2^-16 each, and cut rows sum them in another order; measured
+    1.5e-5)"""
+    spec = tiny_spec(O.F32, n_layer=2, head_dim=128, rope_dim=128)
+    model, logp, hits, lp_o, hits_o, grads = run_both(ctx, spec, t=600, n=200, fused=fused)
+    assert rel_err(logp, lp_o) <= TOL and hits == hits_o
+    assert grad_err(model, grads) <= TOL
+    monkeypatch.setenv("RTQ_ATTN_ITEMS", "0")
+    whole, lp_w, hits_w, _, _, _ = run_both(ctx, spec, t=600, n=200, fused=fused)
+    monkeypatch.delenv("RTQ_ATTN_ITEMS")
+    assert rel_err(lp_w, logp) <= 1e-5 and hits_w == hits
+    for i in range(model.lora_count()):
+        for a, b in zip(whole.lora(i)[2:], model.lora(i)[2:]):
+            assert rel_err(a, b) <= 5e-5
+    whole.close()
+    model.close()
+
+
 def test_model_step_llama_untied_and_score(ctx):
     """normal (adjacent-pair) RoPE, no QK-norm, untied output head (F32 weights: the 1e-3 bar);
     score() = log-probs only"""

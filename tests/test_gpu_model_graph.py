@@ -135,3 +135,31 @@ def test_step_graph_replays_equal_eager_steps(ctx, wtype, monkeypatch):
     print(f"{wtype}: {mg.graph_replays} replays, worst log-prob {worst[0]:.2e}, gradient {worst[1]:.2e}")
     mg.close()
     me.close()
+
+
+@pytest.mark.parametrize("ckpt", [False, True])
+def test_step_graph_replays_hd128_cut_rows(ctx, ckpt, monkeypatch):
+    """the launch sequences of the larger configurations: head size 128 (half-wave QK kernels, whose
+    backward sums the cut blocks' partial slots), 320 tokens (rows cut into pieces), activations
+    kept or recomputed; F32 weights, 1e-4 as above"""
+    spec = tiny_spec(O.F32, n_layer=2, head_dim=128, rope_dim=128)
+    g = G.GgufFile.from_bytes(spec.build())
+    lora = adapters(g, 4, 8.0, b_std=0.05)
+    mg = load(ctx, g, lora, monkeypatch, graph=True)
+    me = load(ctx, g, lora, monkeypatch, graph=False)
+    for m in (mg, me):
+        m.checkpointing = ckpt
+    for seed in range(1, 7):
+        toks, pos, tok = sequence(spec.n_vocab, 320, 64, seed)
+        tg = [rt.Target(int(p), int(k)) for p, k in zip(pos, tok)]
+        w = np.linspace(0.5, 1.5, 64).astype(np.float32) * seed
+        out = []
+        for m in (mg, me):
+            m.zero_grad()
+            out.append(m.forward_backward(toks, tg, w))
+        assert rel(out[0][0], out[1][0]) <= 1e-4 and out[0][1] == out[1][1]
+        for a, b in zip(grads(mg), grads(me)):
+            assert rel(a, b) <= 1e-4
+    assert mg.checkpointing is ckpt and mg.graph_replays >= 3 and me.graph_replays == 0
+    mg.close()
+    me.close()
