@@ -71,6 +71,14 @@ if ROOT not in sys.path:
 METRIC = "trained tokens/s fwd+bwd, Qwen3-0.6B Q4_0 LoRA r16; quant-matmul % roofline"
 N, K, T, R, ALPHA = 3072, 1024, 256, 16, 32.0
 HBM_PEAK_GBS = 8000.0
+# the arithmetic each part of the path computes in (the bench records' "dtype")
+ARITH_FWD = ("Q8 activation codes x weight codes: exact integer block sums on f16 MFMA 16x16x32, f32 scale "
+             "epilogue (frozen forward)")
+ARITH_DX = ("f16 MFMA on f16 hi / lo splits of dy 2^e (per token row) and of W, about 2^-21 per product, "
+            "f32 accumulation (frozen dx)")
+ARITH_ATTN = ("attention forward on f16 MFMA over f16 hi / lo splits (22 bits), backward on bf16 MFMA over "
+              "bf16 hi / lo splits rounded to nearest (about 2^-16 per product)")
+ARITH_REST = "f32 MFMA (LoRA), f32 (norms, RoPE, SwiGLU), f32 / f64 softmax (LM head)"
 F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16 MFMA (the forward's integer block dots and dx run on it)
 
 
@@ -686,7 +694,8 @@ def head_bench(steps: int, warmup: int, cpu_seconds: float, no_cpu: bool) -> Non
         "metric": "LM head + cross-entropy fwd+bwd (Model::head), targets/s", "value": round(N_ / (ms * 1e-3), 1),
         "unit": "targets/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "data": "synthetic",
-        "dtype": "int8 x int4 block dots -> f32 (logits); f32 / f64 softmax; bf16x3 -> f32 (dlogits . W)",
+        "dtype": f"{ARITH_FWD.replace('frozen forward', 'logits')}; f32 / f64 softmax; "
+                 f"{ARITH_DX.replace('frozen dx', 'dlogits . W')}",
         "config": {"workload": "configs[2] head: tied LM head Q4_0 151936x1024, 512 positions, loss on the "
                                "last 256 (answer_targets), weights 1/256",
                    "vocab": V, "hidden": D, "positions": T_, "targets": N_},
@@ -872,8 +881,7 @@ def step_line(args) -> dict:
         "metric": METRIC, "value": r["value"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": r["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 x int4 block dots -> f32 (frozen forward); bf16x3 -> f32 (frozen dx); f32 (LoRA, norms, "
-                 "attention on f32 MFMA)",
+        "dtype": f"{ARITH_FWD}; {ARITH_DX}; {ARITH_ATTN}; {ARITH_REST}",
         "data": "synthetic",
         "config": r["config"],
         "roofline": step_roofline(cfg, r["kernels"]),
@@ -1008,8 +1016,7 @@ def config_bench(idx: int, steps: int, warmup: int) -> dict:
         "metric": f"trained tokens/s fwd+bwd, BASELINE configs[{idx}]", "value": round(seq_tokens / (ms * 1e-3), 1),
         "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8 x int4/int6/int8 block dots -> f32 (frozen forward); bf16x3 -> f32 (frozen dx); f32 (LoRA, "
-                 "norms, attention on f32 MFMA)",
+        "dtype": f"{ARITH_FWD}; {ARITH_DX}; {ARITH_ATTN}; {ARITH_REST}",
         "data": "synthetic (weights N(0, 0.02) from numpy PCG64, quantised with the synthetic encoders)",
         "config": dict({"workload": desc, "lora_params": n_params}, **extra),
         "mean_loss": float(-lp.mean()),
@@ -1306,7 +1313,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 x int4 block dots -> f32 (forward); bf16x3 -> f32 (dx); f32 (LoRA)",
+        "dtype": f"{ARITH_FWD}; {ARITH_DX}; f32 MFMA (LoRA)",
         "data": "synthetic",
         "config": {"workload": "configs[0]: Qwen3-0.6B gate_proj frozen linear, Q4_0 W 3072x1024, T=256, "
                                "LoRA r=16 alpha=32; Linear forward (y) + backward (dx, dA, dB)",

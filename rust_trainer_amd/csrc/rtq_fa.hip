@@ -13,8 +13,9 @@
 //     v are f16 values (kv_f16), staged exactly as one f16 plane; q scale and p are split into f16
 //     hi = f16(x) and lo = f16(x - hi) (22 significant bits): acc += xh y + xl y;
 //   backward dP = dO v^T, dq = dS k, dk = dS^T q, dv = p^T dO: bf16 MFMA, both operands split into
-//     bf16 hi / lo by truncation (f16 k and v split exactly), acc += xh yh + xl yh + xh yl (a
-//     relative error near 2^-16 per product; gradients may lie below f16's range).
+//     bf16 hi / lo, each rounded to nearest (f16 k and v split exactly), acc += xh yh + xl yh +
+//     xh yl (a relative error near 2^-16 per product; bf16 keeps f32's exponent range, so gradients
+//     below f16's range need no scaling).
 // The scores are taken in base 2: q is scaled by scale log2(e), so p = 2^(s2 - m2) with the hardware
 // exp2 (v_exp_f32); the stored lse stays natural (m2 ln 2 + log l) and the backward recomputes
 // p = 2^(s2 - lse log2(e)).  Masks, online softmax (running max m2 and sum l per query row,
@@ -48,11 +49,12 @@ __device__ __forceinline__ void fa_split_f16(const f4 v, u2v& hi, u2v& lo) {
 }
 // four floats -> f16 (exact for f16 values), packed
 __device__ __forceinline__ u2v fa_f16(const f4 v) { return u2v{fa_pk(v[0], v[1]), fa_pk(v[2], v[3])}; }
-// one float -> bf16 hi / lo bits (truncation)
+// one float -> bf16 hi / lo bits, each rounded to nearest even (v_cvt_pk_bf16_f32; x - hi is
+// exact in f32): hi + lo holds x within 2^-17 of |x|
 __device__ __forceinline__ void fa_split_bf(float x, uint32_t& hi, uint32_t& lo) {
-  const uint32_t b = __builtin_bit_cast(uint32_t, x);
-  hi = b >> 16;
-  lo = __builtin_bit_cast(uint32_t, x - __builtin_bit_cast(float, b & 0xffff0000u)) >> 16;
+  const __bf16 h = (__bf16)x;
+  hi = __builtin_bit_cast(uint16_t, h);
+  lo = __builtin_bit_cast(uint16_t, (__bf16)(x - (float)h));
 }
 __device__ __forceinline__ half8 fa_h8(const uint16_t* p) { return *reinterpret_cast<const half8*>(p); }
 __device__ __forceinline__ bf8 fa_b8(const uint16_t* p) { return *reinterpret_cast<const bf8*>(p); }

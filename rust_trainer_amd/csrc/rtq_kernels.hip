@@ -10,10 +10,12 @@
 //    f32 accumulator and so is the 32-term sum (|isum| <= 32*127*127 < 2^24), so the MFMA output
 //    is the integer block sum itself, with no i32->f32 conversion to pay in the epilogue;
 //  * block sums are scaled by d_w * d_x in f32 (the epilogue order is unpinned in the reference);
-//  * dx = dy . W (no dy quantisation, straight-through as in the reference) runs on bf16 MFMA with
-//    both operands split into hi + lo bf16 parts (dy = dh + dl, W = wh + wl exactly for Q4_0):
-//    dh.wh + dl.wh + dh.wl leaves a relative error near 2^-16 per product, far inside the f32
-//    tolerance, and needs no range scaling (bf16 has the f32 exponent range);
+//  * dx = dy . W (no dy quantisation, straight-through as in the reference) runs on f16 MFMA with
+//    both operands split into hi + lo f16 parts: each dy row scaled by a power of two 2^e that
+//    puts its largest |value| in [2^14, 2^15) (the whole row then lies in f16's range; the partial
+//    is scaled back exactly), W's dequantised values split as hi = f16(d q), lo = the exact
+//    residual (K-quants: of ggml's f32 value); dh.wh + dl.wh + dh.wl leaves a relative error near
+//    2^-21 per product (the reference's f32 axpy, src/rie.rs:99-107: 2^-24);
 //  * the LoRA products run on f32 MFMA (exact f32 products, f32 accumulation).
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
@@ -92,11 +94,6 @@ __device__ __forceinline__ half8 q8_frag(uint32_t lo, uint32_t hi) {
   return r;
 }
 
-// f32 -> bf16 hi + bf16 lo (hi = RNE(x), lo = RNE(x - hi); x - hi is exact in f32)
-__device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
-  hi = (__bf16)x;
-  lo = (__bf16)(x - (float)hi);
-}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -1954,7 +1951,9 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
 // Same arithmetic as dx_tile with one 16-token tile: workgroup of 4 waves, tile 16 tokens x 128
 // columns (wave w: the 32 columns of block w), 32 rows per step, many row splits (a GEMV-shaped
 // product needs them to fill the GPU).  Each thread stages both halves of its W words, and the
-// partials are written row-major for the real tokens only: part[split][t][k].
+// partials are written row-major for the real tokens only: part[split][t][k].  f16 hi / lo operands
+// as in dx_tile; dy's scale 2^e per token from the largest |dy| over this split's rows, found by the
+// workgroup itself (wave w: tokens w, w + 4, ..), while the first steps' loads are in flight.
 template <int FMT>
 struct Dx16Slot {
   float2 dy;          // rows 2p, 2p+1 of the step, token tid / 16
@@ -1975,8 +1974,9 @@ __device__ __forceinline__ void dx16_tile(const DxArgs& a) {
   }
   constexpr bool KQ = is_kquant(FMT), B8 = byte_codes(FMT);
   constexpr int D = 4;
-  __shared__ u4v sA[2][2][64];                                       // [buf][hi/lo][lane]
-  __shared__ __attribute__((aligned(16))) __bf16 sW[2][2][128][40];  // [buf][hi/lo][k][n]
+  __shared__ u4v sA[2][2][64];                                          // [buf][hi/lo][lane]
+  __shared__ __attribute__((aligned(16))) _Float16 sW[2][2][128][40];   // [buf][hi/lo][k][n]
+  __shared__ float sSc[16], sInv[16];  // 2^e of each token row, 2^-e (times wunsc)
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
   // id -> (split, K chunk), XCD-aware as in dx_tile
   int sp, kc;
@@ -2020,6 +2020,8 @@ __device__ __forceinline__ void dx16_tile(const DxArgs& a) {
   const uint32_t e_off = (uint32_t)RTQ_WSB_INDEX(rgl, kc >> 1, Kc >> 1, li0) * 4u;
   const uint32_t q_rg = (uint32_t)Kc * 64 * 16 * (B8 ? 2 : 1);
   const uint32_t d_rg = (uint32_t)Kc * 128, e_rg = (uint32_t)Kc * 32;
+  // -1 as a run-time value (wsc * wunsc = 1 exactly), so v - hi stays one mixed-precision FMA
+  const float neg1 = -(a.wsc * a.wunsc);
 
   Dx16Slot<FMT> sl[D];
   auto issue = [&](Dx16Slot<FMT>& S, int step) {
@@ -2052,56 +2054,97 @@ __device__ __forceinline__ void dx16_tile(const DxArgs& a) {
       S.d = __builtin_amdgcn_raw_buffer_load_b32(rd, d_off, srg * d_rg, 0);
     }
   };
+  float dsc = 1.0f;  // 2^e of this thread's token tl
   auto stage_compute = [&](const Dx16Slot<FMT>& S, int buf) {
-    {  // dy: A fragment lane tl + 16 (pp >> 2), bf16 slots 2 (pp & 3), +1 (whole-vector bit view)
-      const u2v vb = __builtin_bit_cast(u2v, S.dy);
-      const uint32_t l0 = __builtin_bit_cast(uint32_t, S.dy.x - __builtin_bit_cast(float, vb.x & 0xffff0000u));
-      const uint32_t l1 = __builtin_bit_cast(uint32_t, S.dy.y - __builtin_bit_cast(float, vb.y & 0xffff0000u));
+    {  // dy 2^e -> f16 hi / lo: A fragment lane tl + 16 (pp >> 2), slots 2 (pp & 3), +1
+      const half2v h = pk_rtz(S.dy.x * dsc, S.dy.y * dsc);
+      // dy 2^e - hi exactly (at most 13 significant bits): one mixed-precision FMA each
+      const half2v l = pk_rtz(fmaf(S.dy.x, dsc, -(float)h.x), fmaf(S.dy.y, dsc, -(float)h.y));
       const int fl = tl + 16 * (pp >> 2);
-      reinterpret_cast<uint32_t*>(&sA[buf][0][fl])[pp & 3] = __builtin_amdgcn_perm(vb.y, vb.x, 0x07060302u);
-      reinterpret_cast<uint32_t*>(&sA[buf][1][fl])[pp & 3] = __builtin_amdgcn_perm(l1, l0, 0x07060302u);
+      reinterpret_cast<uint32_t*>(&sA[buf][0][fl])[pp & 3] = __builtin_bit_cast(uint32_t, h);
+      reinterpret_cast<uint32_t*>(&sA[buf][1][fl])[pp & 3] = __builtin_bit_cast(uint32_t, l);
     }
 #pragma unroll
-    for (int hh = 0; hh < 2; hh++) {  // W: rows li0, li0+1, half hh
-      uint32_t vb[2][4], lb[2][4];
+    for (int hh = 0; hh < 2; hh++) {  // W: rows li0, li0+1, half hh -> f16 hi / lo (as dx_tile)
+      uint32_t hw[4], lw[4];
+      if constexpr (KQ) {
+        float v[2][4];
 #pragma unroll
-      for (int r = 0; r < 2; r++) {
-        float d, m;
-        if constexpr (KQ)
+        for (int r = 0; r < 2; r++) {
+          float d, m;
           dq_params<FMT>(0u, comp(S.k, 2 * r + (jb >> 1)), r ? S.e.y : S.e.x, jb, hh, d, m);
-        else
-          dq_params<FMT>(r ? (S.d >> 16) : (S.d & 0xffffu), 0u, 0u, jb, hh, d, m);
-        const uint32_t u = B8 ? S.q[r][hh] ^ 0x80808080u : (hh ? (S.q[r][0] >> 4) : S.q[r][0]) & 0x0f0f0f0fu;
+          d *= a.wsc;  // exact (a power of two; 1 unless a scale is huge)
+          m *= a.wsc;
+          const uint32_t u = B8 ? S.q[r][hh] ^ 0x80808080u : (hh ? (S.q[r][0] >> 4) : S.q[r][0]) & 0x0f0f0f0fu;
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[r][e] = fmaf((float)((u >> (8 * e)) & 0xffu), d, m);  // rounded once, as ggml
+        }
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          const float v = fmaf((float)((u >> (8 * e)) & 0xffu), d, m);
-          vb[r][e] = __builtin_bit_cast(uint32_t, v);
-          lb[r][e] = __builtin_bit_cast(uint32_t, v - __builtin_bit_cast(float, vb[r][e] & 0xffff0000u));
+          const half2v h = pk_rtz(v[0][e], v[1][e]);
+          hw[e] = __builtin_bit_cast(uint32_t, h);
+          lw[e] = __builtin_bit_cast(uint32_t, pk_rtz(fmaf((float)h.x, neg1, v[0][e]), fmaf((float)h.y, neg1, v[1][e])));
+        }
+      } else {
+        // codes as exact f16 pairs (1024 + u of row 2p, of row 2p+1), c = that - (1024 + offset);
+        // hi = f16(d c), lo its exact residual
+        const uint32_t u0 = B8 ? S.q[0][hh] ^ 0x80808080u : (hh ? (S.q[0][0] >> 4) : S.q[0][0]) & 0x0f0f0f0fu;
+        const uint32_t u1 = B8 ? S.q[1][hh] ^ 0x80808080u : (hh ? (S.q[1][0] >> 4) : S.q[1][0]) & 0x0f0f0f0fu;
+        const uint32_t i01 = __builtin_amdgcn_perm(u1, u0, 0x05010400u), i23 = __builtin_amdgcn_perm(u1, u0, 0x07030602u);
+        half2v dp = __builtin_bit_cast(half2v, S.d);  // fp16 scales of rows 2p, 2p+1
+        dp = dp * half2v{(_Float16)a.wsc, (_Float16)a.wsc};  // exact, as for the K-quants
+        constexpr _Float16 OFF = B8 ? (_Float16)1152.0f : (_Float16)1032.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const uint32_t src = e < 2 ? i01 : i23;
+          const half2v c = sub_h2((e & 1) ? bytes23_to_h2(src) : bytes01_to_h2(src), OFF);
+          const half2v h = dp * c;
+          const half2v l = __builtin_elementwise_fma(dp, c, -h);
+          hw[e] = __builtin_bit_cast(uint32_t, h);
+          lw[e] = __builtin_bit_cast(uint32_t, l);
         }
       }
       const int kb = 32 * jb + 16 * hh + 4 * wgg;
       const int nsw = nloc ^ (8 * jb);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        *reinterpret_cast<uint32_t*>(&sW[buf][0][kb + e][nsw]) = __builtin_amdgcn_perm(vb[1][e], vb[0][e], 0x07060302u);
-        *reinterpret_cast<uint32_t*>(&sW[buf][1][kb + e][nsw]) = __builtin_amdgcn_perm(lb[1][e], lb[0][e], 0x07060302u);
+        *reinterpret_cast<uint32_t*>(&sW[buf][0][kb + e][nsw]) = hw[e];
+        *reinterpret_cast<uint32_t*>(&sW[buf][1][kb + e][nsw]) = lw[e];
       }
     }
     __syncthreads();
-    const bf8 ah = __builtin_bit_cast(bf8, sA[buf][0][lane]);
-    const bf8 al = __builtin_bit_cast(bf8, sA[buf][1][lane]);
+    const half8 ah = __builtin_bit_cast(half8, sA[buf][0][lane]);
+    const half8 al = __builtin_bit_cast(half8, sA[buf][1][lane]);
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
       const int kl = w * 32 + ks * 16 + li;  // column kl lies in block w: rows swizzled by 8 w
-      const bf8 bh = *reinterpret_cast<const bf8*>(&sW[buf][0][kl][8 * (g ^ w)]);
-      const bf8 bl = *reinterpret_cast<const bf8*>(&sW[buf][1][kl][8 * (g ^ w)]);
-      acc[ks] = mfma_bf16(ah, bh, acc[ks]);
-      acc[ks] = mfma_bf16(al, bh, acc[ks]);
-      acc[ks] = mfma_bf16(ah, bl, acc[ks]);
+      const half8 bh = *reinterpret_cast<const half8*>(&sW[buf][0][kl][8 * (g ^ w)]);
+      const half8 bl = *reinterpret_cast<const half8*>(&sW[buf][1][kl][8 * (g ^ w)]);
+      acc[ks] = mfma_f16(ah, bh, acc[ks]);
+      acc[ks] = mfma_f16(al, bh, acc[ks]);
+      acc[ks] = mfma_f16(ah, bl, acc[ks]);
     }
   };
 #pragma unroll
   for (int s0 = 0; s0 < D - 1; s0++) issue(sl[s0], s0);
+  {  // the tokens' scales while those loads are in flight: wave w reduces tokens w, w + 4, ..
+    const int r1 = min(n0 + a.n_per_split, a.N);
+    for (int t = w; t < a.T; t += 4) {
+      float mx = 0.0f;
+      const float* row = a.dy + (int64_t)t * a.N;
+      for (int n = n0 + lane; n < r1; n += 64) mx = fmaxf(mx, fabsf(row[n]));
+      mx = wave_max(mx);
+      if (lane == 0) {
+        int ex = 0;
+        (void)frexpf(mx, &ex);  // mx = f 2^ex, f in [0.5, 1): mx 2^(15 - ex) in [2^14, 2^15)
+        const bool ok = mx > 0.0f && mx <= 3.0e38f;
+        sSc[t] = ok ? ldexpf(1.0f, 15 - ex) : 1.0f;
+        sInv[t] = (ok ? ldexpf(1.0f, ex - 15) : 1.0f) * a.wunsc;
+      }
+    }
+    __syncthreads();
+    if (tl < a.T) dsc = sSc[tl];
+  }
   for (int st0 = 0; st0 < nsteps; st0 += D) {
 #pragma unroll
     for (int s0 = 0; s0 < D; s0++) {
@@ -2111,14 +2154,14 @@ __device__ __forceinline__ void dx16_tile(const DxArgs& a) {
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  // lane holds tokens 4g .. 4g+3 of column 128 kc + 32 w + 16 ks + li
+  // lane holds tokens 4g .. 4g+3 of column 128 kc + 32 w + 16 ks + li, at dy's scale 2^e (and W's)
 #pragma unroll
   for (int ks = 0; ks < 2; ks++) {
     const int col = kc * 128 + w * 32 + ks * 16 + li;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       const int t = 4 * g + e;
-      if (t < a.T && col < a.K) a.part[((int64_t)sp * a.T + t) * a.K + col] = acc[ks][e];
+      if (t < a.T && col < a.K) a.part[((int64_t)sp * a.T + t) * a.K + col] = acc[ks][e] * sInv[t];
     }
   }
 }

@@ -697,8 +697,8 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32g(MGemmGroupArgs g
 // near 2^-22 per product (k and v, stored as f16 values, split exactly), close enough to f32 that
 // the activations the next quantised linear sees keep their Q8 codes; the operands there are
 // bounded (q scaled, probabilities, f16 k and v).  BF (the backward's products of score and output
-// gradients, whose magnitudes can lie below f16's range): bf16 parts by truncation, a relative
-// error near 2^-16 per product.  Same tiles, grids, load modes, causal ranges and liveness skipping
+// gradients, whose magnitudes can lie below f16's range): bf16 parts, each rounded to nearest, a
+// relative error near 2^-16 per product.  Same tiles, grids, load modes, causal ranges and liveness skipping
 // as m_gemm; LDS holds each operand as hi and lo planes [row][k] (k unit stride, rows padded to
 // BK + 8 elements), so a lane's fragment (row li, k = 32 c + 8 g .. + 7) is one 16-byte read per
 // plane (the padding puts the 16 rows of one lane group on distinct banks).  Mode-2 operands
@@ -706,17 +706,20 @@ extern "C" __global__ __launch_bounds__(256) void rtq_m_gemm32g(MGemmGroupArgs g
 template <int R, int BK>
 constexpr int m_bf_ld() { return BK + 8; }
 
-// hi / lo bf16 halves of four floats (bit view of the whole vector: single-lane masks of a float4
-// bit_cast are miscompiled by this compiler)
+// hi / lo bf16 halves of four floats, each rounded to nearest even (v_cvt_pk_bf16_f32; v - hi is
+// exact in f32): hi + lo holds v within 2^-17 of |v|
 __device__ __forceinline__ void m_split4(const f4 v, u2v& hi, u2v& lo) {
-  const u4v vb = __builtin_bit_cast(u4v, v);
-  uint32_t lb[4];
+  uint32_t hb[4], lb[4];
 #pragma unroll
-  for (int c = 0; c < 4; c++) lb[c] = __builtin_bit_cast(uint32_t, v[c] - __builtin_bit_cast(float, vb[c] & 0xffff0000u));
-  hi.x = __builtin_amdgcn_perm(vb[1], vb[0], 0x07060302u);
-  hi.y = __builtin_amdgcn_perm(vb[3], vb[2], 0x07060302u);
-  lo.x = __builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u);
-  lo.y = __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u);
+  for (int c = 0; c < 4; c++) {
+    const __bf16 h = (__bf16)v[c];
+    hb[c] = __builtin_bit_cast(uint16_t, h);
+    lb[c] = __builtin_bit_cast(uint16_t, (__bf16)(v[c] - (float)h));
+  }
+  hi.x = hb[0] | (hb[1] << 16);
+  hi.y = hb[2] | (hb[3] << 16);
+  lo.x = lb[0] | (lb[1] << 16);
+  lo.y = lb[2] | (lb[3] << 16);
 }
 
 // the same split into f16 parts rounded to nearest
