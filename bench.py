@@ -484,81 +484,6 @@ def counters_report(sq_dir: str, fetch_dir: str | None, write_dir: str | None, t
     print(text)
 
 
-# ---------------------------------------------------------------- MFMA instruction-mix probes
-PROBES = (("rtq_probe_f16", "f16 16x16x32 + 4 FMA / lane", 8, 256),
-          ("rtq_probe_i8", "i8 32x32x32 + 16 cvt + 16 FMA / lane", 2, 1024),
-          ("rtq_probe_i8x64", "i8 16x16x64 (half K zero) + 4 cvt + 4 FMA / lane", 8, 256),
-          ("rtq_probe_f16s", "f16 16x16x32 + 4 FMA / lane, scale products by one 16x16x4 f16 MFMA per 4 tile-blocks", 8, 256),
-          ("rtq_probe_i8m", "i8 32x32x32 + 16 cvt + 16 FMA / lane, scale products by a 32x32x8 f16 MFMA", 2, 1024),
-          ("rtq_probe_i8v", "i8 32x32x32 + 16 cvt + 16 FMA / lane, scale products by 16 VALU multiplies", 2, 1024),
-          ("rtq_probe_f16_mfma", "f16 16x16x32 alone", 8, 256),
-          ("rtq_probe_i8_mfma", "i8 32x32x32 alone", 2, 1024),
-          ("rtq_probe_i8x64_mfma", "i8 16x16x64 alone", 8, 256))
-
-
-def hip_runtime() -> ctypes.CDLL:
-    """The HIP runtime torch loaded (the same one librtq.so uses), for the module API."""
-    import torch
-
-    torch.cuda.init()
-    for line in open("/proc/self/maps"):
-        if "libamdhip64.so" in line:
-            return ctypes.CDLL(line.split()[-1])
-    raise RuntimeError("libamdhip64 is not loaded")
-
-
-def mfma_mix(iters: int) -> None:
-    """--mfma-mix: the rtq_probe.hip probes (the forward's block dot in its f16 and int8 MFMA forms,
-    with and without the per-block scale epilogue and the scale products), 2048 workgroups of 4 waves each, timed with HIP
-    events; one JSON line per probe with its rate in output-blocks (32-column block dots of one
-    output element) and the equivalent int8 dot TOPS (64 ops per output-block)."""
-    import torch
-
-    path = os.path.join(ROOT, "rust_trainer_amd", "rtq_probe.hsaco")
-    if not os.path.exists(path):
-        raise RuntimeError(f"{path} is not built: run __graft_entry__.build()")
-    hip = hip_runtime()
-    mod = ctypes.c_void_p()
-    if hip.hipModuleLoad(ctypes.byref(mod), path.encode()) != 0:
-        raise RuntimeError("hipModuleLoad failed")
-
-    class ProbeArgs(ctypes.Structure):
-        _fields_ = [("inp", ctypes.c_void_p), ("out", ctypes.c_void_p), ("iters", ctypes.c_int)]
-
-    seeds = torch.randint(-127, 128, (4096,), dtype=torch.int32, device="cuda")
-    grid, block = 2048, 256
-    out = torch.empty(grid * block, device="cuda")
-    st = torch.cuda.current_stream()
-    hip.hipModuleLaunchKernel.argtypes = [ctypes.c_void_p] + [ctypes.c_uint] * 6 + \
-        [ctypes.c_uint, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)]
-    for name, desc, tiles, tile_out in PROBES:
-        fn = ctypes.c_void_p()
-        if hip.hipModuleGetFunction(ctypes.byref(fn), mod, name.encode()) != 0:
-            raise RuntimeError(f"no kernel {name}")
-        args = ProbeArgs(seeds.data_ptr(), out.data_ptr(), iters)
-        params = (ctypes.c_void_p * 1)(ctypes.cast(ctypes.pointer(args), ctypes.c_void_p))
-
-        def launch():
-            rc = hip.hipModuleLaunchKernel(fn, grid, 1, 1, block, 1, 1, 0, ctypes.c_void_p(st.cuda_stream), params, None)
-            if rc != 0:
-                raise RuntimeError(f"launch of {name} failed ({rc})")
-
-        launch()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(st)
-        for _ in range(5):
-            launch()
-        e1.record(st)
-        torch.cuda.synchronize()
-        sec = e0.elapsed_time(e1) * 1e-3 / 5
-        blocks = grid * (block // 64) * iters * tiles * tile_out
-        print(json.dumps({"probe": name, "form": desc, "us": round(sec * 1e6, 1),
-                          "output_blocks_per_s": round(blocks / sec / 1e12, 3) * 1e12,
-                          "dot_tops": round(blocks * 64 / sec / 1e12, 1)}), flush=True)
-    hip.hipModuleUnload(mod)
-
-
 def host_threads() -> int:
     """Host threads the CPU baselines use: the CPUs of this process's affinity mask, at most 16 (one
     GPU's share of the GPU box's host cores, whatever the machine's total)."""
@@ -567,6 +492,17 @@ def host_threads() -> int:
     except AttributeError:
         n = os.cpu_count() or 1
     return max(1, min(16, n))
+
+
+def host_info() -> dict:
+    """The host the CPU baseline ran on: the machine's CPU count (nproc), this process's affinity
+    mask, and why the threads stop at 16 (a GPU box runs one GPU's share of its host cores)."""
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = os.cpu_count() or 1
+    return {"nproc": os.cpu_count(), "affinity_cpus": aff, "threads_cap": 16,
+            "cap": "worker pools on a GPU box stay within one GPU's share of its host cores (16)"}
 
 
 def timed_runs(fn, warmup: int, runs: int, threads: int) -> list[float]:
@@ -614,7 +550,7 @@ def cpu_baseline(inputs, seconds: float) -> dict:
                             "gflops": round((ff + bf) / med / 1e9, 2), "gb_per_s": round((fb + bb) / med / 1e9, 3),
                             "runs_ms": [round(t * 1e3, 3) for t in ts]}
     return {"value": by[str(nproc)]["tokens_per_s"], "unit": "tokens/s", "cores": nproc, "kind": "port",
-            "cpu_model": O.cpu_model(), "by_threads": by,
+            "cpu_model": O.cpu_model(), "host": host_info(), "by_threads": by,
             "method": "threads pinned one per CPU (sched_setaffinity), AVX2 + FMA build (-march=x86-64-v3), "
                       "2 warm-up calls then the median of 10",
             "sample": f"configs[0] whole: Linear forward + backward (y, dx, dA, dB), Q4_0 {N}x{K}, T={T}, "
@@ -709,7 +645,7 @@ def head_bench(steps: int, warmup: int, cpu_seconds: float, no_cpu: bool) -> Non
     if not no_cpu:
         import oracle as O
 
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = host_threads()
         n_s, calls, t0 = 16, 0, time.perf_counter()
         while True:
             O.lm_head(O.Q4_0, blocks, V, D, norm, X, pos[:n_s], tok[:n_s], wts[:n_s], nthreads=threads)
@@ -718,7 +654,7 @@ def head_bench(steps: int, warmup: int, cpu_seconds: float, no_cpu: bool) -> Non
             if el >= cpu_seconds:
                 break
         result["cpu_baseline"] = {"value": round(n_s * calls / el, 1), "unit": "targets/s", "cores": threads,
-                                  "kind": "port",
+                                  "kind": "port", "host": host_info(),
                                   "sample": f"{calls} calls of Model::head on {n_s} targets in {el:.1f} s "
                                             f"(oracle/rtq_oracle.c or_lm_head, -O3 AVX2, OpenMP)"}
     f.close()
@@ -1062,7 +998,7 @@ def model_cpu_baseline(spec, g, seconds: float) -> dict:
     ts = timed_runs(lambda: O.model_forward_backward(full, tokens, pos, tok, wts, nthreads=threads), 0, 3, threads)
     med = statistics.median(ts)
     return {"value": round(STEP_T / med, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "cpu_model": O.cpu_model(),
+            "cpu_model": O.cpu_model(), "host": host_info(),
             "method": "threads pinned one per CPU (sched_setaffinity), AVX2 + FMA build (-march=x86-64-v3), one "
                       "warm-up step of a 2-block cut of the model, then the median of 3 full steps",
             "runs_s": [round(t, 2) for t in ts],
@@ -1143,8 +1079,6 @@ def main() -> int:
                     help="per-kernel counter table (SQ pass + traffic passes) -> profiles/OUT_MD")
     ap.add_argument("--attention", choices=("fused", "unfused"), default=None,
                     help="training-step benches: force the fused or the unfused attention kernels")
-    ap.add_argument("--mfma-mix", type=int, default=None, metavar="ITERS",
-                    help="instruction-mix probes of the forward's block dot (f16 vs int8 MFMA), ITERS loop trips")
     ap.add_argument("--traffic-step", action="store_true",
                     help="configs[2] steps + calibration copies for --pmc passes (with --traffic-report: the step)")
     ap.add_argument("--head", action="store_true", help="configs[2] LM head + cross-entropy (Model::head)")
@@ -1165,9 +1099,6 @@ def main() -> int:
     global ATTENTION_MODE
     if args.attention:
         ATTENTION_MODE = args.attention == "fused"
-    if args.mfma_mix:
-        mfma_mix(args.mfma_mix)
-        return 0
     if args.counters_report:
         sq_d, f_d, w_d, out_md = args.counters_report
         title = ("configs[2] training step: counters per kernel" if args.traffic_step

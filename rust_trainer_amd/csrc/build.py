@@ -4,9 +4,7 @@
 2. ``rtq_runtime.cpp`` + ``rtq_gguf.cpp`` + ``rtq_model.cpp`` -> ``rust_trainer_amd/librtq.so`` (g++ against the HIP runtime), with the
    code object embedded (``.incbin``) and loaded at run time with ``hipModuleLoadData``, plus
    ``rtq_noalloc.hip`` compiled by hipcc (its device array is registered with the HIP runtime);
-3. ``rtq_probe.hip`` -> ``rust_trainer_amd/rtq_probe.hsaco`` (instruction-mix probes for
-   ``bench.py --mfma-mix``; not part of the library);
-4. ``oracle/`` -> ``oracle/liboracle.so`` (test infrastructure, plain gcc).
+3. ``oracle/`` -> ``oracle/liboracle.so`` (test infrastructure, plain gcc).
 
 Everything is built in-tree so the shared objects travel with the repository snapshot.
 """
@@ -54,17 +52,6 @@ def build_kernels() -> str:
     return out
 
 
-def build_probe() -> str:
-    """rtq_probe.hip -> its own gfx950 code object beside librtq.so (bench.py --mfma-mix loads it;
-    not part of the library)"""
-    out = os.path.join(PKG, "rtq_probe.hsaco")
-    tmp = out + ".tmp"
-    _run([os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, "--genco", "--no-gpu-bundle-output",
-          os.path.join(CSRC, "rtq_probe.hip"), "-o", tmp])
-    os.replace(tmp, out)
-    return out
-
-
 def build_noalloc() -> str:
     """rtq_noalloc.hip (host + gfx950 device code: the no-allocation entry point's scratch array)
     -> an object linked into librtq.so"""
@@ -98,7 +85,6 @@ def build_oracle() -> None:
 def build() -> None:
     hsaco = build_kernels()
     build_runtime(hsaco, build_noalloc())
-    build_probe()
     build_oracle()
 
 
