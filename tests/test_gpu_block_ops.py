@@ -19,7 +19,7 @@ of 252 rows and gate|up of 320, neither a multiple of 64) at t = 16 and 700 with
 up_proj unadapted (the block-diagonal fused adapter with an unadapted member); a packed
 shared-prompt batch at the configs[2] shape with activations recomputed; the configs[3] block
 shape (Qwen3-4B: hidden 2560, 32 / 8 heads, FFN 9728, Q4_K attention / gate / up, Q6_K down) on a
-packed batch of eight examples sharing a 200-token prompt (680 tokens); the configs[4] block shape
+packed batch of eight examples sharing a 200-token prompt (680 tokens, and the configuration's 6792); the configs[4] block shape
 (Llama-3-8B: hidden 4096, 32 / 8 heads, FFN 14336, adjacent-pair RoPE 5e5, Q8_0, rank 64,
 untied head) at 2048 tokens with loss on the last 1024, recomputed.
 """
@@ -278,23 +278,28 @@ def test_packed_block_ops_match_oracle_recomputed(ctx):
     model.close()
 
 
-def test_config3_block_ops_packed_match_oracle(ctx):
+@pytest.mark.parametrize("extra,start", [(60, 230), (824, 724)], ids=["680", "6792"])
+def test_config3_block_ops_packed_match_oracle(ctx, extra, start):
+    """the configs[3] block shape on a packed batch of eight examples sharing a 200-token prompt:
+    680 tokens, and the configuration's own 8 x 1024 tokens (6792 packed, loss on each example's
+    last 300 positions)"""
     spec = tiny_spec(O.Q4_K, n_layer=1, n_embd=2560, n_head=32, n_head_kv=8, head_dim=128, rope_dim=128, n_ff=9728,
                      n_vocab=4096, tensor_types={"ffn_down": O.Q6_K, "token_embd": O.Q6_K})
     g, model, m = build(ctx, spec, 16, 32.0, ALL)
     rng = O.Rng(33)
     V = spec.n_vocab
     prompt = [int(v) for v in (rng.vec_uniform_sym(200, 1.0) * 0.5 + 0.5) * (V - 1)]
-    seqs = [prompt + [int(v) for v in (rng.vec_uniform_sym(60, 1.0) * 0.5 + 0.5) * (V - 1)] for _ in range(8)]
+    seqs = [prompt + [int(v) for v in (rng.vec_uniform_sym(extra, 1.0) * 0.5 + 0.5) * (V - 1)] for _ in range(8)]
     p = pack(seqs)
-    assert len(p.tokens) == 680 and p.shared == 200
+    t = 200 + 8 * extra
+    assert len(p.tokens) == t and p.shared == 200
     targets = []
     for k, s in enumerate(seqs):
-        targets += p.map_targets(k, answer_targets(s, 230))
+        targets += p.map_targets(k, answer_targets(s, start))
     model.debug_capture(0)
     model.zero_grad()
     model.forward_backward_packed(p, targets, np.full(len(targets), 1.0 / len(targets), np.float32))
-    check_block(ctx, g, model, m, 0, 680, np.array(p.segments), {}, {"positions": p.positions})
+    check_block(ctx, g, model, m, 0, t, np.array(p.segments), {}, {"positions": p.positions})
     model.close()
 
 

@@ -314,11 +314,12 @@ def test_config1_sweep_t2048_matches_oracle(ctx, wtype, shape):
     _dense_dx_check(wtype, blocks, n, k, dy, dxf)
 
 
-@pytest.mark.parametrize("wtype,t", [(O.Q4_0, 16), (O.Q8_0, 16), (O.Q4_K, 16), (O.Q6_K, 16), (O.Q4_K, 256)])
+@pytest.mark.parametrize("wtype,t", [(f, 16) for f in FORMATS] + [(O.Q4_K, 256), (O.Q8_0, 256), (O.Q6_K, 256)] +
+                         [(f, 2048) for f in FORMATS])
 def test_config1_lm_head_matches_oracle(ctx, wtype, t):
-    """configs[1]'s tied LM head 151936 x 1024 (no adapter) at T = 16 in every format and T = 256
-    (Q4_K): forward and FrozenMatmul::backward_input against the oracle and, per element, against
-    the dense product"""
+    """configs[1]'s tied LM head 151936 x 1024 (no adapter) at T = 16 and 2048 in every format and
+    T = 256 (Q4_K, Q8_0, Q6_K): forward and FrozenMatmul::backward_input against the oracle and, per
+    element, against the dense product"""
     import time
 
     n, k = 151936, 1024
