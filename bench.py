@@ -1070,6 +1070,7 @@ def main() -> int:
     ap.add_argument("--sets", type=int, default=40, help="rotating operand sets (~10 MB each)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--title", default=None, help="--counters-report: the table's title")
     ap.add_argument("--sweep", action="store_true", help="configs[1] sweep: one JSON line per case")
     ap.add_argument("--case", default=None, help="one sweep case FMT:SHAPE:T, e.g. Q4_K:lm_head:1")
     ap.add_argument("--calls", type=int, default=50, help="sweep: calls per timed graph (at least the sets)")
@@ -1101,9 +1102,9 @@ def main() -> int:
         ATTENTION_MODE = args.attention == "fused"
     if args.counters_report:
         sq_d, f_d, w_d, out_md = args.counters_report
-        title = ("configs[2] training step: counters per kernel" if args.traffic_step
-                 else "configs[0] Linear forward + backward: counters per kernel")
-        counters_report(sq_d, f_d, w_d, title, out_md)
+        title = args.title or ("configs[2] training step: counters per kernel" if args.traffic_step
+                               else "configs[0] Linear forward + backward: counters per kernel")
+        counters_report(sq_d, None if f_d == "-" else f_d, None if w_d == "-" else w_d, title, out_md)
         return 0
     if args.traffic_report:
         traffic_report(*args.traffic_report, step=args.traffic_step)

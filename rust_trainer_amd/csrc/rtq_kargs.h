@@ -80,6 +80,9 @@ struct ActArgs {
   const float* sg;
   const float* su;
   int ldsg;
+  // 1: the codes go to xq as int8 fragments of rtq_mmi8_* ([Tp/32][Kc][4][64] x 16 bytes, lane l:
+  // token l % 32, the block's codes of k-groups 2 (l / 32) and 2 (l / 32) + 1), not f16 ones
+  int xq_i8;
 };
 
 // ---------------------------------------------------------------- trainer-native weights

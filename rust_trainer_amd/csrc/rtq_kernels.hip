@@ -531,6 +531,15 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
     }
     if (kk < a.Kp) {
       const int b = kk >> 5, hf = sg & 1, kc = b >> 2, j = b & 3;
+      if (a.xq_i8) {  // uniform: int8 fragments of rtq_mmi8_*, k-group g at byte 8 (g % 2) + 4 hf of lane (t % 32) + 32 (g / 2)
+        uint32_t* xq = reinterpret_cast<uint32_t*>(a.xq) + ((((int64_t)(t >> 5) * Kc + kc) * 4 + j) * 64 + (t & 31)) * 4 + hf;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const uint32_t w = ((uint32_t)(int)q[4 * g] & 0xffu) | (((uint32_t)(int)q[4 * g + 1] & 0xffu) << 8) |
+                             (((uint32_t)(int)q[4 * g + 2] & 0xffu) << 16) | ((uint32_t)(int)q[4 * g + 3] << 24);
+          xq[(g >> 1) * 32 * 4 + (g & 1) * 2] = w;
+        }
+      } else {
       // this half block gives, for each k-group g, the four codes of one 8-element fragment half
       u2v* xq = reinterpret_cast<u2v*>(a.xq) + ((((int64_t)(t >> 4) * Kc + kc) * 4 + j) * 64 + (t & 15)) * 2 + hf;
 #pragma unroll
@@ -540,6 +549,7 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
         w.x = __builtin_bit_cast(uint32_t, lo);
         w.y = __builtin_bit_cast(uint32_t, hi);
         xq[g * 16 * 2] = w;
+      }
       }
       const bool real = t < a.T && kk < a.K;
       if (hf == 0) a.xd[((int64_t)kc * a.Tp + t) * 4 + j] = real ? dstore : 0.0f;
@@ -1306,6 +1316,285 @@ extern "C" __global__ __launch_bounds__(256) void rtq_mm64_q8_0(FwdArgs a) { mm_
 // 128 rows x 32 tokens: two or more workgroups per CU where 128 x 64 tiles give about one
 extern "C" __global__ __launch_bounds__(256) void rtq_mm32_q4_0(FwdArgs a) { mm_tile<FMT_Q4_0, 2, RTQ_MM32_RING>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_mm32_q8_0(FwdArgs a) { mm_tile<FMT_Q8_0, 2, RTQ_MM32_RING>(a); }
+
+// ============================================================== forward GEMM on int8 MFMA (Q4_0 / Q8_0)
+// rtq_mm64_*'s tiles (128 weight rows x 16 TTN tokens, TTN 4 here, four waves, the same RING-stage
+// ring of half-chunk operands copied global -> LDS by buffer loads with an LDS destination), with
+// the block sums on v_mfma_i32_32x32x32_i8: wave w owns weight rows 32 w .. 32 w + 31 (row groups
+// 2w, 2w+1) x all tokens, in 32 x 32 tiles, one i8 MFMA per tile and block (K = 32 = one block).
+// The weight codes are the device's codes as they lie in LDS (a lane's 16 codes are those of k-groups
+// 2 (l / 32), 2 (l / 32) + 1 of its row: two reads; Q8_0 needs no conversion, Q4_0 nibbles become
+// u - 8 bytes with three VALU operations per four codes); the activation
+// codes are act_prep's int8 fragments in the same k order (xq_i8), half the bytes of the f16 ones.
+// Per tile and block: isum (i32, exact) and the scale products d_w d_x from one f16 32x32x16 MFMA
+// (operands in k slot 0: an outer product, exact in f32), then acc += f32(isum) * (d_w d_x) - the
+// same arithmetic as rtq_mm_*, so the outputs agree with it bit for bit.  The epilogue costs two
+// VALU operations (convert, FMA) per output element and block against the f16 kernel's one FMA.
+// MFMA 32 x 32 output layout: lane l holds column l % 32 (token) and rows 8 (e / 4) + 4 (l / 32) +
+// e % 4, e < 16 (weight rows).
+typedef int32_t i4v __attribute__((ext_vector_type(4)));
+typedef int32_t i16v __attribute__((ext_vector_type(16)));
+
+template <int FMT, int TTN>
+struct MmI8Stage {  // one half chunk in LDS, in 16-byte units
+  static constexpr int TT32 = TTN / 2;                // token tiles of 32
+  static constexpr int XQ = 0;                        // [tt32][j2 2][lane 64] int8 codes
+  static constexpr int WQ = TT32 * 2 * 64;            // [rg 8][lane 64] codes: Q8_0 16 B, Q4_0 8 B
+  static constexpr int WD = WQ + (FMT == FMT_Q4_0 ? 8 * 64 / 2 : 8 * 64);  // [rg 8][row 16] fp16 scale pairs
+  static constexpr int XD = WD + 8 * 4;               // [t 16 TTN] fp16 activation scale pairs
+  static constexpr int NXD = TTN / 4;                 // loads of activation scales (64 tokens each)
+  static constexpr int SIZE = XD + 16 * NXD;
+  static constexpr int NX = 2 * TT32;                 // loads of activation fragments (1 KB each)
+  static constexpr int NWQ = FMT == FMT_Q4_0 ? 16 : 8;  // loads of weight codes
+};
+
+// Q4_0 codes of a word (low nibbles: 4 elements, high nibbles: the 4 elements 16 on) -> signed
+// int8 codes u - 8: (u | 0x80) - 8 per byte cannot borrow across bytes, then the sign bit flipped
+__device__ __forceinline__ uint32_t q4_i8(uint32_t u) { return ((u | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
+
+template <int FMT, int TTN, int RING>
+__device__ __forceinline__ void mmi8_tile(const FwdArgs& a) {
+  static_assert(TTN == 8 || TTN == 4, "128- or 64-token tiles");
+  using St = MmI8Stage<FMT, TTN>;
+  constexpr int TT32 = St::TT32;
+  extern __shared__ u4v mm_lds[];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int Kc = a.Kp / 128, nhc = a.Kp / 64;
+  const int ngroups = a.Np / 16, ntt = a.Tp / 16, ntt32 = a.Tp / 32;
+  // tile order as rtq_mm_*: XCD-aware, row blocks in groups of MM_GR per token-block sweep
+  constexpr int MM_GR = 8;
+  const int nrb = (ngroups + 7) / 8, ntb = ntt / TTN, ntiles = nrb * ntb;
+  const int id = blockIdx.x, xcd = id & 7, per = ntiles >> 3, rem = ntiles & 7;
+  const int q = xcd * per + min(xcd, rem) + (id >> 3);
+  const int gfull = nrb / MM_GR, q0 = gfull * MM_GR * ntb;
+  int rb, tb;
+  if (q < q0) {
+    const int in = q % (MM_GR * ntb);
+    rb = (q / (MM_GR * ntb)) * MM_GR + in % MM_GR;
+    tb = in / MM_GR;
+  } else {
+    const int gr = nrb - gfull * MM_GR, in = q - q0;
+    rb = gfull * MM_GR + in % gr;
+    tb = in / gr;
+  }
+  const int rg0 = rb * 8, tt0 = tb * TTN;
+
+  const uint32_t nb_x = (uint32_t)a.Tp * a.Kp, nb_xd = (uint32_t)Kc * a.Tp * 8;
+  const uint32_t nb_w = (uint32_t)a.Np * a.Kp / (FMT == FMT_Q4_0 ? 2 : 1), nb_wd = (uint32_t)a.Np * a.Kp / 16;
+  const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.xq), (short)0, nb_x, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_xd = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.xdh), (short)0, nb_xd, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_w = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.wq), (short)0, nb_w, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_wd = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.wdr), (short)0, nb_wd, 0x00020000);
+  constexpr int KX = St::NX / 4, KW = St::NWQ / 4;
+  static_assert(St::NX % 4 == 0 && St::NWQ % 4 == 0 && St::NXD <= 2, "load split over four waves");
+  uint32_t vx[KX], vw[KW], ve = 0;
+#pragma unroll
+  for (int k = 0; k < KX; k++) {  // activation fragments: 32-token tile i / 2, block 2h + i % 2
+    const int i = w + 4 * k;
+    const uint32_t ttg = (uint32_t)min(tt0 / 2 + (i >> 1), ntt32 - 1);
+    vx[k] = ((ttg * Kc * 4 + (i & 1)) * 64 + lane) * 16;
+  }
+#pragma unroll
+  for (int k = 0; k < KW; k++) {  // weight codes (as rtq_mm_*)
+    const int iw = w + 4 * k;
+    if (FMT == FMT_Q4_0) {  // row group iw / 2, words 64 m .. 64 m + 63 of its 128
+      const int wi = (iw & 1) * 64 + lane;
+      const uint32_t rgg = (uint32_t)min(rg0 + (iw >> 1), ngroups - 1);
+      vw[k] = ((rgg * Kc * 64 + (wi >> 1)) * 4 + (wi & 1)) * 4;
+    } else {
+      const uint32_t rgg = (uint32_t)min(rg0 + iw, ngroups - 1);
+      vw[k] = (rgg * Kc * 2 * 64 + lane) * 16;
+    }
+  }
+  if (w < 2) {  // weight scale pairs: word wi -> row wi % 16 of row group wi / 16
+    const int wi = w * 64 + lane;
+    const uint32_t rgg = (uint32_t)min(rg0 + (wi >> 4), ngroups - 1);
+    ve = ((rgg * Kc * 16 + (wi & 15)) * 2) * 4;
+  } else if (w - 2 < St::NXD) {  // fp16 activation scales of blocks 2h, 2h+1: word wi -> token wi
+    const int wi = (w - 2) * 64 + lane;
+    ve = (uint32_t)min(tt0 * 16 + wi, a.Tp - 1) * 8;
+  }
+  auto issue = [&](int st, int hc) {
+    u4v* S = mm_lds + st * St::SIZE;
+    const uint32_t kc = hc >> 1, h = hc & 1;
+#pragma unroll
+    for (int k = 0; k < KX; k++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, RTQ_LDSP(S + St::XQ + (w + 4 * k) * 64), 16, vx[k], hc * 2048u, 0, 0);
+#pragma unroll
+    for (int k = 0; k < KW; k++) {
+      const int iw = w + 4 * k;
+      if (FMT == FMT_Q4_0)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + (iw >> 1) * 32 + (iw & 1) * 16), 4, vw[k],
+                                                 kc * 1024u + h * 8u, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + iw * 64), 16, vw[k], hc * 1024u, 0, 0);
+    }
+    if (w < 2)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_wd, RTQ_LDSP(S + St::WD + w * 16), 4, ve, kc * 128u + h * 4u, 0, 0);
+    else if (w - 2 < St::NXD)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_xd, RTQ_LDSP(S + St::XD + (w - 2) * 16), 4, ve,
+                                               kc * (uint32_t)a.Tp * 8u + h * 4u, 0, 0);
+  };
+
+  const f16v zero16 = {};
+  const i16v izero = {};
+  f16v acc[TT32];
+#pragma unroll
+  for (int i = 0; i < TT32; i++) acc[i] = zero16;
+  const int r32 = lane & 31, hl = lane >> 5;
+  const int rgw = 2 * w + (r32 >> 4), rho = r32 & 15;  // this lane's A row: row rho of row group rgw
+  // the scale MFMAs' operands: one value in k slot 0, the other slots zero for the whole loop
+  u4v sop[2][1 + TT32];
+#pragma unroll
+  for (int j2 = 0; j2 < 2; j2++)
+#pragma unroll
+    for (int i = 0; i <= TT32; i++) sop[j2][i] = u4v{0u, 0u, 0u, 0u};
+  auto compute = [&](int st) {
+    const u4v* S = mm_lds + st * St::SIZE;
+    i4v wa[2];
+    if (FMT == FMT_Q4_0) {  // lanes rho + 32 hl, + 16 of the row group's 64: one word per block
+      const u2v* W2 = reinterpret_cast<const u2v*>(S + St::WQ) + rgw * 64 + rho + 32 * hl;
+      const u2v e0 = W2[0], e1 = W2[16];
+#pragma unroll
+      for (int j2 = 0; j2 < 2; j2++) {
+        const uint32_t a0 = j2 ? e0.y : e0.x, a1 = j2 ? e1.y : e1.x;
+        wa[j2] = __builtin_bit_cast(i4v, u4v{q4_i8(a0 & 0x0f0f0f0fu), q4_i8((a0 >> 4) & 0x0f0f0f0fu),
+                                               q4_i8(a1 & 0x0f0f0f0fu), q4_i8((a1 >> 4) & 0x0f0f0f0fu)});
+      }
+    } else {  // block j of lane lam at bytes 16 lam + 8 j: one 8-byte read per half fragment
+      const u2v* W2 = reinterpret_cast<const u2v*>(S + St::WQ) + 2 * (rgw * 64 + rho + 32 * hl);
+#pragma unroll
+      for (int j2 = 0; j2 < 2; j2++) {
+        const u2v p0 = W2[j2], p1 = W2[32 + j2];
+        wa[j2] = __builtin_bit_cast(i4v, u4v{p0.x, p0.y, p1.x, p1.y});
+      }
+    }
+    // scale operands: d_w of this lane's row, d_x of its token, in k slot 0 (lanes 0 .. 31; the
+    // upper lanes' words stay zero)
+    const uint32_t* wdw = reinterpret_cast<const uint32_t*>(S + St::WD);
+    const uint32_t* xdw = reinterpret_cast<const uint32_t*>(S + St::XD);
+    if (hl == 0) {
+      const uint32_t dwp = wdw[rgw * 16 + rho];
+      sop[0][0].x = dwp & 0xffffu;
+      sop[1][0].x = dwp >> 16;
+#pragma unroll
+      for (int i = 0; i < TT32; i++) {
+        const uint32_t xsv = xdw[i * 32 + r32];
+        sop[0][1 + i].x = xsv & 0xffffu;
+        sop[1][1 + i].x = xsv >> 16;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < TT32; i++) {
+#pragma unroll
+      for (int j2 = 0; j2 < 2; j2++) {
+        const i4v xf = __builtin_bit_cast(i4v, S[St::XQ + (i * 2 + j2) * 64 + lane]);
+        const i16v c = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa[j2], xf, izero, 0, 0, 0);
+        const f16v sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, sop[j2][0]),
+                                                              __builtin_bit_cast(half8, sop[j2][1 + i]), zero16, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[i][e] = fmaf((float)c[e], sc[e], acc[i][e]);
+      }
+    }
+  };
+
+  static_assert(RING >= 3 && (RING - 2) * (KX + KW + 2) <= 63, "ring depth within the load counter");
+  constexpr int MINL = KX + KW + (St::NXD >= 2 ? 1 : 0);
+#pragma unroll
+  for (int s = 0; s < RING - 1; s++)
+    if (s < nhc) issue(s, s);
+  for (int hc0 = 0; hc0 < nhc; hc0 += RING) {
+#pragma unroll
+    for (int u = 0; u < RING; u++) {
+      const int hc = hc0 + u;
+      if (hc < nhc) {
+        vm_wait_stages<MINL>(min(RING - 2, nhc - 1 - hc));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (hc + RING - 1 < nhc) issue((u + RING - 1) % RING, hc + RING - 1);
+        compute(u);
+      }
+    }
+  }
+
+  // ---- epilogue: bias, LoRA up-projection (f32 MFMA 32x32x2 in the same output layout), y.  The
+  // wave's 32 rows read the ranks of their row groups' members (B is zero outside them).
+  const bool lora = a.hp != nullptr;
+  float(*sh)[RTQ_LDS_RANK + 1] = reinterpret_cast<float(*)[RTQ_LDS_RANK + 1]>(mm_lds);
+  float(*sb)[RTQ_LDS_RANK + 1] = sh + 16 * TTN;
+  int span0 = 0, span1 = 0, win0 = 0, win1 = 0;
+  if (lora) {
+    rb_span(a.rb, a.r, rg0 * 16, min(rg0 * 16 + 128, a.N), span0, span1);
+    rb_span(a.rb, a.r, (rg0 + 2 * w) * 16, (rg0 + 2 * w) * 16 + 32, win0, win1);
+  }
+  f16v lacc[TT32];
+#pragma unroll
+  for (int i = 0; i < TT32; i++) lacc[i] = zero16;
+  for (int c0 = span0; c0 < span1; c0 += RTQ_LDS_RANK) {
+    const int c1 = min(c0 + RTQ_LDS_RANK, span1);
+    __builtin_amdgcn_s_barrier();  // every wave is past its last read of the ring / previous chunk
+    asm volatile("" ::: "memory");
+    for (int j0 = c0; j0 < c1; j0 += 16) {
+      float hv[8], bv[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) {  // rows e / 16: 16 TTN token rows of h, 128 weight rows of B
+        const int e = threadIdx.x + 256 * k, tl = e >> 4, j = min(j0 + (e & 15), a.r - 1);
+        hv[k] = tl < 16 * TTN ? sum_partials(a.hp, (int64_t)min(tt0 * 16 + tl, a.T - 1) * a.r + j, a.nhp) : 0.0f;
+        bv[k] = a.lb[(int64_t)min(rg0 * 16 + tl, a.N - 1) * a.r + j];
+      }
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const int e = threadIdx.x + 256 * k, jl = j0 - c0 + (e & 15);
+        if ((e >> 4) < 16 * TTN) sh[e >> 4][jl] = hv[k];
+        sb[e >> 4][jl] = bv[k];
+      }
+    }
+    __syncthreads();
+    const int lo = max(win0, c0), hi = min(win1, c1);
+    const int nrow = (rg0 + 2 * w) * 16 + r32;
+    for (int j0 = lo; j0 < hi; j0 += 2) {
+      const int j = j0 + hl, jl = min(j, hi - 1) - c0;
+      const float bv = (nrow < a.N && j < hi) ? sb[32 * w + r32][jl] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < TT32; i++) {
+        const float hv = (tt0 * 16 + i * 32 + r32 < a.T && j < hi) ? sh[i * 32 + r32][jl] : 0.0f;
+        lacc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv, hv, lacc[i], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TT32; i++) {
+    const int t = tt0 * 16 + i * 32 + r32;
+    if (t >= a.T) continue;
+    float* yr = a.y + (int64_t)t * a.N;
+#pragma unroll
+    for (int e4 = 0; e4 < 4; e4++) {
+      const int n0 = (rg0 + 2 * w) * 16 + 8 * e4 + 4 * hl;
+      if (n0 >= a.N) continue;
+      f4 v;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        float o = acc[i][4 * e4 + e];
+        if (a.bias) o = o + a.bias[min(n0 + e, a.N - 1)];
+        if (lora) o = o + a.s * lacc[i][4 * e4 + e];
+        v[e] = o;
+      }
+      if ((a.N & 3) == 0 && n0 + 3 < a.N) {
+        *reinterpret_cast<f4*>(yr + n0) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (n0 + e < a.N) yr[n0 + e] = v[e];
+      }
+    }
+  }
+}
+
+// 128 x 64 tiles (127 VGPRs, several waves per SIMD; the 128 x 128 form of this kernel holds 300,
+// one wave per SIMD, and measured 1.5x slower)
+extern "C" __global__ __launch_bounds__(256) void rtq_mmi8_64_q4_0(FwdArgs a) { mmi8_tile<FMT_Q4_0, 4, RTQ_MM64_RING>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_mmi8_64_q8_0(FwdArgs a) { mmi8_tile<FMT_Q8_0, 4, RTQ_MM64_RING>(a); }
 
 // ============================================================== forward GEMV (T <= 16)
 // MFMA orientation transposed against fwd_tile: A operand = the 16 token slots x 32 columns of the

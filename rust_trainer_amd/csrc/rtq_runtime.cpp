@@ -128,6 +128,8 @@ enum Kid {
   K_MM64_Q8_0,
   K_MM32_Q4_0,   // the same with 128 x 32 tiles
   K_MM32_Q8_0,
+  K_MMI8_64_Q4_0,  // the 128 x 64 tiles with the block sums on int8 MFMA
+  K_MMI8_64_Q8_0,
   K_BWD_PREP,
   K_DX,          // + format
   K_DX16 = K_DX + F_COUNT,  // + format: t <= 16
@@ -159,6 +161,7 @@ constexpr const char* kKernelNames[] = {
     "rtq_fwd_q4_0_w8",      "rtq_fwd_q8_0_w8",      "rtq_fwd_q4_0_w8r2",    "rtq_fwd_q8_0_w8r2",
     "rtq_mm_q4_0",          "rtq_mm_q8_0",
     "rtq_mm64_q4_0",        "rtq_mm64_q8_0",        "rtq_mm32_q4_0",        "rtq_mm32_q8_0",
+    "rtq_mmi8_64_q4_0",     "rtq_mmi8_64_q8_0",
     "rtq_bwd_prep",
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
@@ -208,6 +211,8 @@ struct rtq_ctx {
   int g64_min = -1;   // fewest 64-token g-partial workgroups (else 16-token ones): -1 = CUs / 2 (RTQ_G64_MIN)
   int fwd_mm = -1;    // large-grid forward: -1 automatic, 0 never, 1 / 2 / 3 the 128- / 64- / 32-token tiles
                       // whenever the format allows (RTQ_FWD_MM)
+  int fwd_i8 = -1;    // int8-MFMA forwards (rtq_mmi8_*; RTQ_FWD_I8): -1 automatic (Q8_0 weights), 0 never,
+                      // 1 every Q4_0 / Q8_0 weight, wherever the 128- or 64-token tiles are chosen
   int64_t t_launches[K_COUNT] = {};
   double t_ms[K_COUNT] = {};
   double t_flops[K_COUNT] = {}, t_bytes[K_COUNT] = {};
@@ -358,6 +363,11 @@ constexpr int kMmTile = 128;      // rtq_mm_*: 128 rows x 128 tokens per workgro
 unsigned mm_lds_bytes(int type, int ttn, int ring) {  // ttn: token tiles of 16 per workgroup (8, 4 or 2)
   const unsigned stage =
       16u * (ttn * 2 * 64 + (type == RTQ_TYPE_Q4_0 ? 8 * 64 / 2 : 8 * 64) + 8 * 4 + 16 * std::max(ttn / 4, 1));
+  return std::max((unsigned)ring * stage, (16u * ttn + 128u) * (RTQ_LDS_RANK + 1) * 4u);
+}
+// rtq_mmi8_* (ttn 4): int8 activation fragments, half the f16 ones' bytes
+unsigned mmi8_lds_bytes(int type, int ttn, int ring) {
+  const unsigned stage = 16u * (ttn * 64 + (type == RTQ_TYPE_Q4_0 ? 8 * 64 / 2 : 8 * 64) + 8 * 4 + 16 * (ttn / 4));
   return std::max((unsigned)ring * stage, (16u * ttn + 128u) * (RTQ_LDS_RANK + 1) * 4u);
 }
 constexpr int kFwdSkinnyRG = 4;   // rtq_fwd_*_s: 16 tokens x 64 rows per workgroup
@@ -588,6 +598,16 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
     else if (c->fwd_mm < 0) mm_ttn = mm128 >= c->cu_count ? 8 : (mm64 >= c->cu_count ? 2 : 0);
   }
   const bool mm = mm_ttn > 0;
+  // the int8-MFMA kernel where the 128- or 64-token tiles are chosen, on 64-token tiles (its 128-token
+  // form holds 300 VGPRs, one wave per SIMD).  Automatic: for Q8_0 weights, whose codes reach the
+  // i8 MFMA as they lie in LDS; measured per forward call (activation kernel included) at 2048
+  // tokens: LM head 151936 x 1024 980 against 1020 us (f16, 128-token tiles), 28672 x 4096 848
+  // against 897, 6144 x 4096 241 against 259 (f16, 64-token tiles); Q4_0 mixed (1043 against
+  // 1005 us on the LM head, 864 against 906 on 28672 x 4096), so Q4_0 keeps the f16 kernels.
+  // Both agree bit for bit without an adapter.
+  const bool mmi8 = mm && (mm_ttn == 8 || mm_ttn == 4) &&
+                    (c->fwd_i8 == 1 || (c->fwd_i8 < 0 && w->type == RTQ_TYPE_Q8_0));
+  if (mmi8) mm_ttn = 4;
   const int64_t mm_tiles = mm_ttn == 8 ? mm128 : mm_ttn == 4 ? mm64 : mm32;
   const int64_t tiles = gx * gy;
   // split K across workgroups when the output alone gives too few of them (atomics into a
@@ -611,6 +631,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
     aa.su = sw->u;
     aa.ldsg = (int)sw->ld;
   }
+  aa.xq_i8 = mmi8 ? 1 : 0;
   RTQ_TRY(launch(c, kq ? K_ACT_PREP_K : K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp), dim3(256), st, aa));
   FwdArgs fa{};
   fa.wq = w->wq;
@@ -639,6 +660,9 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   if (mm && (!fa.wq || !fa.wdr || !fa.xq || !fa.xdh || !fa.y))
     return fail(RTQ_ERR_INVALID, "internal: rtq_mm_* operand missing");
   set_work(c, w, t, lora ? r : 0, false);
+  if (mmi8)
+    return launch(c, K_MMI8_64_Q4_0 + (w->type == RTQ_TYPE_Q4_0 ? 0 : 1), dim3((unsigned)mm_tiles), dim3(256), st, fa,
+                  mmi8_lds_bytes(w->type, 4, RTQ_MM64_RING));
   if (mm) {
     const int ring = mm_ttn == 8 ? RTQ_MM_RING : mm_ttn == 4 ? RTQ_MM64_RING : RTQ_MM32_RING;
     return launch(c, (mm_ttn == 8 ? K_MM_Q4_0 : mm_ttn == 4 ? K_MM64_Q4_0 : K_MM32_Q4_0) + (w->type == RTQ_TYPE_Q4_0 ? 0 : 1),
@@ -983,6 +1007,7 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   if (const char* e = getenv("RTQ_DX_WIDE")) c->dx_wide = atoi(e) ? 1 : 0;
   if (const char* e = getenv("RTQ_FWD_WAVES")) c->fwd_waves = atoi(e) == 4 ? 4 : 8;
   if (const char* e = getenv("RTQ_FWD_MM")) c->fwd_mm = std::min(std::max(atoi(e), 0), 3);
+  if (const char* e = getenv("RTQ_FWD_I8")) c->fwd_i8 = std::min(std::max(atoi(e), -1), 1);
   if (const char* e = getenv("RTQ_FWD_RG")) c->fwd_rg = atoi(e) == 2 ? 2 : 3;
   if (const char* e = getenv("RTQ_G64_MIN")) c->g64_min = atoi(e);
   hipError_t e = hipModuleLoadData(&c->mod, rtq_hsaco_begin);

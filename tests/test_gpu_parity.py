@@ -430,6 +430,94 @@ def test_forward_mm_many_tiles(ctx, wtype, r):
     assert rel_err(y, want) <= TOL
 
 
+# ---------------------------------------------------------------- int8-MFMA forward (rtq_mmi8_*)
+def _context(env):
+    import os
+
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return rt.Context(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+
+
+@pytest.fixture(scope="module")
+def ctx_i8_pair():
+    """Two contexts forcing the 128 x 64 tiles (RTQ_FWD_MM=2): one on the f16 MFMA kernels
+    (rtq_mm64_*), one on their int8-MFMA variants for both formats (RTQ_FWD_I8=1, rtq_mmi8_64_*)"""
+    f16 = _context({"RTQ_FWD_MM": "2", "RTQ_FWD_I8": "0"})
+    i8 = _context({"RTQ_FWD_MM": "2", "RTQ_FWD_I8": "1"})
+    yield f16, i8
+    i8.close()
+    f16.close()
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
+@pytest.mark.parametrize("n,k,t,r", [(200, 256, 130, 16), (320, 512, 256, 0), (1000, 1024, 300, 80), (130, 128, 129, 16),
+                                     (64, 128, 17, 4), (4096, 1024, 512, 64)])
+def test_linear_forward_int8_mfma_matches_oracle(ctx_i8_pair, wtype, n, k, t, r):
+    """Forward with the block sums on v_mfma_i32_32x32x32_i8: against the oracle (1e-3), and
+    against the f16-MFMA kernel of the same tiles - the integer block sums, scale products and the
+    epilogue's FMA order are the same, so without an adapter y is bit-identical; with one, the
+    LoRA up-projection sums its ranks in another MFMA shape (f32 rounding)"""
+    c16, c8 = ctx_i8_pair
+    blocks, x, _ = make(wtype, n, k, t)
+    bias = O.Rng(6).vec_normal(n, 0.1)
+    out = []
+    for c in (c16, c8):
+        lin = rt.Linear("blk.0.attn_q", hip(c, wtype, blocks, n, k), bias=bias)
+        if r:
+            A, B = lora(n, k, r)
+            lin.lora = rt.Lora(r, 2.0 * r, A, B)
+        c.set_timing(True)
+        c.reset_timing()
+        out.append(lin.forward(x, t))
+        ran = c.timing()
+        c.set_timing(False)
+        assert any(name.startswith("rtq_mmi8") == (c is c8) and name.startswith("rtq_mm") for name in ran), ran
+    kw = dict(A=A, B=B, alpha=2.0 * r) if r else {}
+    want = O.linear_forward(wtype, blocks, n, k, x, bias=bias, nthreads=8, **kw)
+    assert rel_err(out[1], want) <= TOL
+    if r == 0:
+        np.testing.assert_array_equal(out[1], out[0])
+    else:
+        assert rel_err(out[1], out[0]) <= 1e-6
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
+def test_frozen_forward_int8_mfma_block_sums_bit_identical(ctx_i8_pair, wtype):
+    """FrozenMatmul::forward of the LM-head-like shape 8192 x 1024 at T = 384 (several token blocks,
+    padding in the last): the int8 and f16 kernels return the same bits"""
+    c16, c8 = ctx_i8_pair
+    n, k, t = 8192, 1024, 384
+    blocks, x, _ = make(wtype, n, k, t)
+    y16 = hip(c16, wtype, blocks, n, k).forward(x, t)
+    y8 = hip(c8, wtype, blocks, n, k).forward(x, t)
+    np.testing.assert_array_equal(y8, y16)
+    assert rel_err(y8, O.frozen_forward(wtype, blocks, n, k, x, nthreads=16)) <= TOL
+
+
+def test_forward_int8_mfma_is_the_q8_0_default(ctx):
+    """the default context runs a Q8_0 weight's large-grid forward on int8 MFMA (the 128 x 128 choice
+    taken as 128 x 64 int8 tiles) and a Q4_0 weight's on the f16 kernel"""
+    n, k, t = 4096, 256, 1024
+    for wtype, prefix in ((O.Q8_0, "rtq_mmi8_64_q8_0"), (O.Q4_0, "rtq_mm_q4_0")):
+        blocks, x, _ = make(wtype, n, k, t)
+        w = hip(ctx, wtype, blocks, n, k)
+        ctx.set_timing(True)
+        ctx.reset_timing()
+        y = w.forward(x, t)
+        ran = ctx.timing()
+        ctx.set_timing(False)
+        assert prefix in ran, ran
+        assert rel_err(y, O.frozen_forward(wtype, blocks, n, k, x, nthreads=8)) <= TOL
+
+
 # ---------------------------------------------------------------- eight-wave forward, 32-row tiles
 @pytest.fixture(scope="module")
 def ctx_rg2():
