@@ -1317,6 +1317,283 @@ extern "C" __global__ __launch_bounds__(256) void rtq_mm64_q8_0(FwdArgs a) { mm_
 extern "C" __global__ __launch_bounds__(256) void rtq_mm32_q4_0(FwdArgs a) { mm_tile<FMT_Q4_0, 2, RTQ_MM32_RING>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_mm32_q8_0(FwdArgs a) { mm_tile<FMT_Q8_0, 2, RTQ_MM32_RING>(a); }
 
+// ============================================================== forward GEMM, large grids (Q4_K / Q6_K)
+// rtq_mm_*'s ring kernel for the K-quants: 128 weight rows x 16 TTN tokens (TTN 4 or 2), four
+// waves, wave w owning row groups 2w, 2w+1 x all token tiles, the half-chunk operands - codes
+// (Q4_K in the Q4_0 layout, Q6_K in the Q8_0 layout), the sub-block scale words of the 128 rows,
+// the activation codes (Q8_K values as exact f16) - copied global -> LDS by buffer loads with an
+// LDS destination into a RING-stage ring.  Arithmetic as fwd_tile's K-quant path: the 6-bit scales
+// folded into the f16 weight fragments (Q4_K: sc u and m; Q6_K: sh q and sl q), two f16 MFMAs per
+// block accumulate the super-block's exact integer sums S1, S2 over its four half chunks, and the
+// f32 epilogue runs once per super-block: Q4_K y += (d d_x) S1 - (dmin d_x) S2, Q6_K
+// y += (d d_x) (16 S1 + S2).  The super-block scales (d, dmin) of the lane's rows and the tokens'
+// Q8_K d are loaded from global memory at the super-block's first half chunk and used at its last.
+template <int FMT, int TTN>
+struct MmkStage {  // one half chunk in LDS, in 16-byte units
+  static constexpr int XQ = 0;                                           // [tt TTN][j2 2][lane 64] codes
+  static constexpr int WQ = TTN * 2 * 64;                                // [rg 8][lane 64] Q4_K 8 B, Q6_K 16 B
+  static constexpr int WK = WQ + (FMT == FMT_Q4_K ? 8 * 64 / 2 : 8 * 64);  // [rg 8][row 16] sub-block scale words
+  static constexpr int SIZE = WK + 8 * 4;
+  static constexpr int NX = 2 * TTN;
+  static constexpr int NWQ = FMT == FMT_Q4_K ? 16 : 8;
+};
+
+template <int FMT, int TTN, int RING>
+__device__ __forceinline__ void mmk_tile(const FwdArgs& a) {
+  static_assert(TTN == 4 || TTN == 2, "64- or 32-token tiles");
+  using St = MmkStage<FMT, TTN>;
+  extern __shared__ u4v mm_lds[];
+  const int lane = threadIdx.x & 63, li = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int Kc = a.Kp / 128, nhc = a.Kp / 64;
+  const int ngroups = a.Np / 16, ntt = a.Tp / 16;
+  constexpr int MM_GR = 8;
+  const int nrb = (ngroups + 7) / 8, ntb = ntt / TTN, ntiles = nrb * ntb;
+  const int id = blockIdx.x, xcd = id & 7, per = ntiles >> 3, rem = ntiles & 7;
+  const int q = xcd * per + min(xcd, rem) + (id >> 3);
+  const int gfull = nrb / MM_GR, q0 = gfull * MM_GR * ntb;
+  int rb, tb;
+  if (q < q0) {
+    const int in = q % (MM_GR * ntb);
+    rb = (q / (MM_GR * ntb)) * MM_GR + in % MM_GR;
+    tb = in / MM_GR;
+  } else {
+    const int gr = nrb - gfull * MM_GR, in = q - q0;
+    rb = gfull * MM_GR + in % gr;
+    tb = in / gr;
+  }
+  const int rg0 = rb * 8, tt0 = tb * TTN;
+
+  const uint32_t nb_x = (uint32_t)a.Tp * a.Kp * 2;
+  const uint32_t nb_w = (uint32_t)a.Np * a.Kp / (FMT == FMT_Q4_K ? 2 : 1), nb_wd = (uint32_t)a.Np * a.Kp / 16;
+  const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.xq), (short)0, nb_x, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_w = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.wq), (short)0, nb_w, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_wd = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.wd), (short)0, nb_wd, 0x00020000);
+  constexpr int KX = St::NX / 4, KW = St::NWQ / 4;
+  static_assert(St::NX % 4 == 0 && St::NWQ % 4 == 0, "load split over four waves");
+  uint32_t vx[KX], vw[KW], ve = 0;
+#pragma unroll
+  for (int k = 0; k < KX; k++) {
+    const int i = w + 4 * k;
+    const uint32_t ttg = (uint32_t)min(tt0 + (i >> 1), ntt - 1);
+    vx[k] = ((ttg * Kc * 4 + (i & 1)) * 64 + lane) * 16;
+  }
+#pragma unroll
+  for (int k = 0; k < KW; k++) {
+    const int iw = w + 4 * k;
+    if (FMT == FMT_Q4_K) {
+      const int wi = (iw & 1) * 64 + lane;
+      const uint32_t rgg = (uint32_t)min(rg0 + (iw >> 1), ngroups - 1);
+      vw[k] = ((rgg * Kc * 64 + (wi >> 1)) * 4 + (wi & 1)) * 4;
+    } else {
+      const uint32_t rgg = (uint32_t)min(rg0 + iw, ngroups - 1);
+      vw[k] = (rgg * Kc * 2 * 64 + lane) * 16;
+    }
+  }
+  if (w < 2) {  // sub-block scale words (blocks 2h, 2h+1): word wi -> row wi % 16 of row group wi / 16
+    const int wi = w * 64 + lane;
+    const uint32_t rgg = (uint32_t)min(rg0 + (wi >> 4), ngroups - 1);
+    ve = ((rgg * Kc * 16 + (wi & 15)) * 2) * 4;
+  }
+  auto issue = [&](int st, int hc) {
+    u4v* S = mm_lds + st * St::SIZE;
+    const uint32_t kc = hc >> 1, h = hc & 1;
+#pragma unroll
+    for (int k = 0; k < KX; k++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, RTQ_LDSP(S + St::XQ + (w + 4 * k) * 64), 16, vx[k], hc * 2048u, 0, 0);
+#pragma unroll
+    for (int k = 0; k < KW; k++) {
+      const int iw = w + 4 * k;
+      if (FMT == FMT_Q4_K)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + (iw >> 1) * 32 + (iw & 1) * 16), 4, vw[k],
+                                                 kc * 1024u + h * 8u, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, RTQ_LDSP(S + St::WQ + iw * 64), 16, vw[k], hc * 1024u, 0, 0);
+    }
+    if (w < 2)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_wd, RTQ_LDSP(S + St::WK + w * 16), 4, ve, kc * 128u + h * 4u, 0, 0);
+  };
+
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 acc[TTN][2], s1[TTN][2], s2[TTN][2];
+#pragma unroll
+  for (int i = 0; i < TTN; i++)
+#pragma unroll
+    for (int r = 0; r < 2; r++) acc[i][r] = s1[i][r] = s2[i][r] = zero;
+  u4v esb[2];     // (d | dmin << 16) of rows 4g .. 4g + 3 of row groups 2w, 2w + 1, this super-block
+  float xsb[TTN]; // the tokens' Q8_K d of this super-block (token li of each tile)
+  auto compute = [&](int st, int hc) {
+    const u4v* S = mm_lds + st * St::SIZE;
+    if ((hc & 3) == 0) {  // a super-block starts: its scales, consumed at its last half chunk
+      const int sb = hc >> 2;
+#pragma unroll
+      for (int r = 0; r < 2; r++)
+        esb[r] = reinterpret_cast<const u4v*>(a.wsb)[((uint32_t)min(rg0 + 2 * w + r, ngroups - 1) * (Kc >> 1) + sb) * 4 + g];
+#pragma unroll
+      for (int i = 0; i < TTN; i++)
+        xsb[i] = a.xd[((int64_t)(2 * sb) * a.Tp + min((tt0 + i) * 16 + li, a.Tp - 1)) * 4];
+    }
+#pragma unroll
+    for (int j2 = 0; j2 < 2; j2++) {
+      half8 f1[2], f2[2];
+#pragma unroll
+      for (int r = 0; r < 2; r++) {
+        const int rl = 2 * w + r;
+        const uint32_t kw = reinterpret_cast<const uint32_t*>(S + St::WK)[rl * 16 + li];
+        const uint32_t wv = j2 ? (kw >> 16) : kw;
+        if (FMT == FMT_Q4_K) {
+          const u2v q2 = reinterpret_cast<const u2v*>(S + St::WQ)[rl * 64 + lane];
+          const _Float16 sc = (_Float16)(float)(wv & 0x3fu), m = (_Float16)(float)((wv >> 8) & 0x3fu);
+          f1[r] = q4_0_frag<0>(j2 ? q2.y : q2.x) * sc;
+          const half8 mm = {m, m, m, m, m, m, m, m};
+          f2[r] = mm;
+        } else {
+          const u4v qv = S[St::WQ + rl * 64 + lane];
+          const int s0 = (int)(int8_t)(wv & 0xffu), s1v = (int)(int8_t)((wv >> 8) & 0xffu);
+          const _Float16 h0 = (_Float16)(float)(s0 >> 4), h1 = (_Float16)(float)(s1v >> 4);
+          const _Float16 l0 = (_Float16)(float)(s0 & 15), l1 = (_Float16)(float)(s1v & 15);
+          const half8 qf = j2 ? q8_frag(qv.z, qv.w) : q8_frag(qv.x, qv.y);
+          const half8 sh = {h0, h0, h0, h0, h1, h1, h1, h1}, sl = {l0, l0, l0, l0, l1, l1, l1, l1};
+          f1[r] = qf * sh;
+          f2[r] = qf * sl;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TTN; i++) {
+        const half8 xf = __builtin_bit_cast(half8, S[St::XQ + (i * 2 + j2) * 64 + lane]);
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+          s1[i][r] = mfma_f16(f1[r], xf, s1[i][r]);
+          s2[i][r] = mfma_f16(f2[r], xf, s2[i][r]);
+        }
+      }
+    }
+    if ((hc & 3) == 3) {  // the super-block's f32 epilogue, then the sums restart
+#pragma unroll
+      for (int i = 0; i < TTN; i++)
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const uint32_t ev = comp(esb[r], e);
+            const float dd = h2f((uint16_t)(ev & 0xffffu)) * xsb[i];
+            if (FMT == FMT_Q4_K) {
+              const float dm = h2f((uint16_t)(ev >> 16)) * xsb[i];
+              acc[i][r][e] = fmaf(dd, s1[i][r][e], fmaf(-dm, s2[i][r][e], acc[i][r][e]));
+            } else {
+              acc[i][r][e] = fmaf(dd, fmaf(16.0f, s1[i][r][e], s2[i][r][e]), acc[i][r][e]);
+            }
+          }
+          s1[i][r] = zero;
+          s2[i][r] = zero;
+        }
+    }
+  };
+
+  static_assert(RING >= 3 && (RING - 2) * (KX + KW + 1) <= 63, "ring depth within the load counter");
+  constexpr int MINL = KX + KW;
+#pragma unroll
+  for (int s = 0; s < RING - 1; s++)
+    if (s < nhc) issue(s, s);
+  for (int hc0 = 0; hc0 < nhc; hc0 += RING) {
+#pragma unroll
+    for (int u = 0; u < RING; u++) {
+      const int hc = hc0 + u;
+      if (hc < nhc) {
+        vm_wait_stages<MINL>(min(RING - 2, nhc - 1 - hc));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (hc + RING - 1 < nhc) issue((u + RING - 1) % RING, hc + RING - 1);
+        compute(u, hc);
+      }
+    }
+  }
+
+  // ---- epilogue as rtq_mm_*: bias, LoRA up-projection per row group, y
+  const bool lora = a.hp != nullptr;
+  float(*sh)[RTQ_LDS_RANK + 1] = reinterpret_cast<float(*)[RTQ_LDS_RANK + 1]>(mm_lds);
+  float(*sbm)[RTQ_LDS_RANK + 1] = sh + 16 * TTN;
+  int span0 = 0, span1 = 0;
+  int win0[2] = {0, 0}, win1[2] = {0, 0};
+  if (lora) {
+    rb_span(a.rb, a.r, rg0 * 16, min(rg0 * 16 + 128, a.N), span0, span1);
+#pragma unroll
+    for (int r = 0; r < 2; r++) rb_span(a.rb, a.r, (rg0 + 2 * w + r) * 16, (rg0 + 2 * w + r) * 16 + 16, win0[r], win1[r]);
+  }
+  f4 lacc[TTN][2];
+#pragma unroll
+  for (int i = 0; i < TTN; i++)
+#pragma unroll
+    for (int r = 0; r < 2; r++) lacc[i][r] = zero;
+  for (int c0 = span0; c0 < span1; c0 += RTQ_LDS_RANK) {
+    const int c1 = min(c0 + RTQ_LDS_RANK, span1);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    for (int j0 = c0; j0 < c1; j0 += 16) {
+      float hv[8], bv[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const int e = threadIdx.x + 256 * k, tl = e >> 4, j = min(j0 + (e & 15), a.r - 1);
+        hv[k] = tl < 16 * TTN ? sum_partials(a.hp, (int64_t)min(tt0 * 16 + tl, a.T - 1) * a.r + j, a.nhp) : 0.0f;
+        bv[k] = a.lb[(int64_t)min(rg0 * 16 + tl, a.N - 1) * a.r + j];
+      }
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const int e = threadIdx.x + 256 * k, jl = j0 - c0 + (e & 15);
+        if ((e >> 4) < 16 * TTN) sh[e >> 4][jl] = hv[k];
+        sbm[e >> 4][jl] = bv[k];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int lo = max(win0[r], c0), hi = min(win1[r], c1);
+      const int nb0 = (rg0 + 2 * w + r) * 16, rl = (2 * w + r) * 16;
+      for (int j0 = lo; j0 < hi; j0 += 4) {
+        const int j = j0 + g, jl = min(j, hi - 1) - c0;
+        const float bv = (nb0 + li < a.N && j < hi) ? sbm[rl + li][jl] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TTN; i++) {
+          const float hv = (tt0 * 16 + i * 16 + li < a.T && j < hi) ? sh[i * 16 + li][jl] : 0.0f;
+          lacc[i][r] = mfma_f32(bv, hv, lacc[i][r]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TTN; i++) {
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int t = tt0 * 16 + i * 16 + li;
+      const int nb0 = (rg0 + 2 * w + r) * 16, n0 = nb0 + 4 * g;
+      if (nb0 >= a.N) continue;
+      if (t < a.T) {
+        f4 v = acc[i][r];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          float o = v[e];
+          if (a.bias) o = o + a.bias[min(n0 + e, a.N - 1)];
+          if (lora) o = o + a.s * lacc[i][r][e];
+          v[e] = o;
+        }
+        float* yr = a.y + (int64_t)t * a.N;
+        if ((a.N & 3) == 0 && n0 + 3 < a.N) {
+          *reinterpret_cast<f4*>(yr + n0) = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (n0 + e < a.N) yr[n0 + e] = v[e];
+        }
+      }
+    }
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void rtq_mmk64_q4_k(FwdArgs a) { mmk_tile<FMT_Q4_K, 4, RTQ_MM64_RING>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_mmk64_q6_k(FwdArgs a) { mmk_tile<FMT_Q6_K, 4, RTQ_MM64_RING>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_mmk32_q4_k(FwdArgs a) { mmk_tile<FMT_Q4_K, 2, RTQ_MM32_RING>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_mmk32_q6_k(FwdArgs a) { mmk_tile<FMT_Q6_K, 2, RTQ_MM32_RING>(a); }
+
 // ============================================================== forward GEMM on int8 MFMA (Q4_0 / Q8_0)
 // rtq_mm64_*'s tiles (128 weight rows x 16 TTN tokens, TTN 4 here, four waves, the same RING-stage
 // ring of half-chunk operands copied global -> LDS by buffer loads with an LDS destination), with

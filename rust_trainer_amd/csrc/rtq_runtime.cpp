@@ -130,6 +130,10 @@ enum Kid {
   K_MM32_Q8_0,
   K_MMI8_64_Q4_0,  // the 128 x 64 tiles with the block sums on int8 MFMA
   K_MMI8_64_Q8_0,
+  K_MMK64_Q4_K,    // the LDS-ring kernel for the K-quants: 128 x 64 and 128 x 32 tiles
+  K_MMK64_Q6_K,
+  K_MMK32_Q4_K,
+  K_MMK32_Q6_K,
   K_BWD_PREP,
   K_DX,          // + format
   K_DX16 = K_DX + F_COUNT,  // + format: t <= 16
@@ -162,6 +166,7 @@ constexpr const char* kKernelNames[] = {
     "rtq_mm_q4_0",          "rtq_mm_q8_0",
     "rtq_mm64_q4_0",        "rtq_mm64_q8_0",        "rtq_mm32_q4_0",        "rtq_mm32_q8_0",
     "rtq_mmi8_64_q4_0",     "rtq_mmi8_64_q8_0",
+    "rtq_mmk64_q4_k",       "rtq_mmk64_q6_k",       "rtq_mmk32_q4_k",       "rtq_mmk32_q6_k",
     "rtq_bwd_prep",
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
@@ -211,6 +216,8 @@ struct rtq_ctx {
   int g64_min = -1;   // fewest 64-token g-partial workgroups (else 16-token ones): -1 = CUs / 2 (RTQ_G64_MIN)
   int fwd_mm = -1;    // large-grid forward: -1 automatic, 0 never, 1 / 2 / 3 the 128- / 64- / 32-token tiles
                       // whenever the format allows (RTQ_FWD_MM)
+  int fwd_mmk = -1;   // K-quant ring forward (rtq_mmk*_*; RTQ_FWD_MMK): -1 automatic, 0 never, 1 / 2 the 64- /
+                      // 32-token tiles whenever the shape allows
   int fwd_i8 = -1;    // int8-MFMA forwards (rtq_mmi8_*; RTQ_FWD_I8): -1 automatic (Q8_0 weights), 0 never,
                       // 1 every Q4_0 / Q8_0 weight, wherever the 128- or 64-token tiles are chosen
   int64_t t_launches[K_COUNT] = {};
@@ -363,6 +370,11 @@ constexpr int kMmTile = 128;      // rtq_mm_*: 128 rows x 128 tokens per workgro
 unsigned mm_lds_bytes(int type, int ttn, int ring) {  // ttn: token tiles of 16 per workgroup (8, 4 or 2)
   const unsigned stage =
       16u * (ttn * 2 * 64 + (type == RTQ_TYPE_Q4_0 ? 8 * 64 / 2 : 8 * 64) + 8 * 4 + 16 * std::max(ttn / 4, 1));
+  return std::max((unsigned)ring * stage, (16u * ttn + 128u) * (RTQ_LDS_RANK + 1) * 4u);
+}
+// rtq_mmk*_* (K-quants, ttn 4 or 2): codes, sub-block scale words and activation codes per stage
+unsigned mmk_lds_bytes(int type, int ttn, int ring) {
+  const unsigned stage = 16u * (ttn * 2 * 64 + (type == RTQ_TYPE_Q4_K ? 8 * 64 / 2 : 8 * 64) + 8 * 4);
   return std::max((unsigned)ring * stage, (16u * ttn + 128u) * (RTQ_LDS_RANK + 1) * 4u);
 }
 // rtq_mmi8_* (ttn 4): int8 activation fragments, half the f16 ones' bytes
@@ -608,13 +620,23 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   const bool mmi8 = mm && (mm_ttn == 8 || mm_ttn == 4) &&
                     (c->fwd_i8 == 1 || (c->fwd_i8 < 0 && w->type == RTQ_TYPE_Q8_0));
   if (mmi8) mm_ttn = 4;
+  // K-quants: the LDS-ring kernel on 64-token tiles where they give every CU a workgroup, else on
+  // 32-token tiles where those do.  Measured per forward call at 2048 tokens against the tile
+  // kernel (rtq_fwd_*_w): Qwen3-4B q | k | v 226 -> 179 us, gate | up 641 -> 464, down (Q6_K) 384
+  // -> 323, LM head Q4_K 1778 -> 1307 (32-token tiles: 214, 585, 375, 1673)
+  int mmk_ttn = 0;
+  if (!p.skinny && !isums && is_kquant(w->type)) {
+    if (c->fwd_mmk == 1) mmk_ttn = 4;
+    else if (c->fwd_mmk == 2) mmk_ttn = 2;
+    else if (c->fwd_mmk < 0) mmk_ttn = mm64 >= c->cu_count ? 4 : (mm32 >= c->cu_count ? 2 : 0);
+  }
   const int64_t mm_tiles = mm_ttn == 8 ? mm128 : mm_ttn == 4 ? mm64 : mm32;
   const int64_t tiles = gx * gy;
   // split K across workgroups when the output alone gives too few of them (atomics into a
   // zeroed y); every split keeps at least one half chunk per wave (K-quants: one super-block of
   // two chunks per wave, and splits on super-block boundaries)
   int64_t ks = 1;
-  if (!isums && !mm && tiles < c->cu_count) {
+  if (!isums && !mm && !mmk_ttn && tiles < c->cu_count) {
     const int64_t want = cdiv(p.skinny ? 2 * c->cu_count : c->cu_count, tiles);
     ks = std::max<int64_t>(1, std::min<int64_t>(want, Kc / (kq ? 8 : 2)));
   }
@@ -663,6 +685,13 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   if (mmi8)
     return launch(c, K_MMI8_64_Q4_0 + (w->type == RTQ_TYPE_Q4_0 ? 0 : 1), dim3((unsigned)mm_tiles), dim3(256), st, fa,
                   mmi8_lds_bytes(w->type, 4, RTQ_MM64_RING));
+  if (mmk_ttn) {
+    if (!fa.wq || !fa.wd || !fa.wsb || !fa.xq || !fa.xd || !fa.y)
+      return fail(RTQ_ERR_INVALID, "internal: rtq_mmk_* operand missing");
+    const int kid = (mmk_ttn == 4 ? K_MMK64_Q4_K : K_MMK32_Q4_K) + (w->type == RTQ_TYPE_Q4_K ? 0 : 1);
+    return launch(c, kid, dim3((unsigned)(mmk_ttn == 4 ? mm64 : mm32)), dim3(256), st, fa,
+                  mmk_lds_bytes(w->type, mmk_ttn, mmk_ttn == 4 ? RTQ_MM64_RING : RTQ_MM32_RING));
+  }
   if (mm) {
     const int ring = mm_ttn == 8 ? RTQ_MM_RING : mm_ttn == 4 ? RTQ_MM64_RING : RTQ_MM32_RING;
     return launch(c, (mm_ttn == 8 ? K_MM_Q4_0 : mm_ttn == 4 ? K_MM64_Q4_0 : K_MM32_Q4_0) + (w->type == RTQ_TYPE_Q4_0 ? 0 : 1),
@@ -1008,6 +1037,7 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   if (const char* e = getenv("RTQ_FWD_WAVES")) c->fwd_waves = atoi(e) == 4 ? 4 : 8;
   if (const char* e = getenv("RTQ_FWD_MM")) c->fwd_mm = std::min(std::max(atoi(e), 0), 3);
   if (const char* e = getenv("RTQ_FWD_I8")) c->fwd_i8 = std::min(std::max(atoi(e), -1), 1);
+  if (const char* e = getenv("RTQ_FWD_MMK")) c->fwd_mmk = std::min(std::max(atoi(e), -1), 2);
   if (const char* e = getenv("RTQ_FWD_RG")) c->fwd_rg = atoi(e) == 2 ? 2 : 3;
   if (const char* e = getenv("RTQ_G64_MIN")) c->g64_min = atoi(e);
   hipError_t e = hipModuleLoadData(&c->mod, rtq_hsaco_begin);

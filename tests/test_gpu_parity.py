@@ -518,6 +518,61 @@ def test_forward_int8_mfma_is_the_q8_0_default(ctx):
         assert rel_err(y, O.frozen_forward(wtype, blocks, n, k, x, nthreads=8)) <= TOL
 
 
+# ---------------------------------------------------------------- K-quant LDS-ring forward (rtq_mmk*)
+@pytest.fixture(scope="module", params=["1", "2"], ids=["mmk64", "mmk32"])
+def ctx_mmk(request):
+    """A context that sends every wide K-quant forward through the LDS-ring kernel's 64-token
+    (RTQ_FWD_MMK=1) or 32-token (2) tiles"""
+    c = _context({"RTQ_FWD_MMK": request.param})
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("n,k,t,r", [(200, 256, 130, 16), (320, 512, 256, 0), (1000, 1024, 300, 80), (130, 256, 129, 16),
+                                     (64, 512, 17, 4), (2560, 2560, 192, 16)])
+def test_linear_forward_kquant_ring_matches_oracle(ctx_mmk, wtype, n, k, t, r):
+    """K-quant forward on the LDS-ring kernel (super-block sums of f16 MFMAs on scale-folded
+    fragments, one f32 epilogue per super-block): partial row groups and blocks, token padding,
+    no LoRA, LoRA above the LDS staging limit (80), the configs[3] o_proj-like shape"""
+    blocks, x, _ = make(wtype, n, k, t)
+    bias = O.Rng(6).vec_normal(n, 0.1)
+    lin = rt.Linear("blk.0.attn_q", hip(ctx_mmk, wtype, blocks, n, k), bias=bias)
+    kw = {}
+    if r:
+        A, B = lora(n, k, r)
+        lin.lora = rt.Lora(r, 2.0 * r, A, B)
+        kw = dict(A=A, B=B, alpha=2.0 * r)
+    ctx_mmk.set_timing(True)
+    ctx_mmk.reset_timing()
+    y = lin.forward(x, t)
+    ran = ctx_mmk.timing()
+    ctx_mmk.set_timing(False)
+    assert any(name.startswith("rtq_mmk") for name in ran), ran
+    want = O.linear_forward(wtype, blocks, n, k, x, bias=bias, nthreads=8, **kw)
+    assert rel_err(y, want) <= TOL
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_K, O.Q6_K])
+def test_forward_kquant_ring_selected_and_equal_to_tile_kernel(ctx, wtype):
+    """at 6144 x 2560 and 1024 tokens the default context picks the ring kernel by itself; its
+    super-block sums are the tile kernel's (RTQ_FWD_MMK=0), so y agrees to f32 rounding of the same
+    per-super-block epilogue (bitwise where the sums are exact)"""
+    n, k, t = 6144, 2560, 1024
+    blocks, x, _ = make(wtype, n, k, t)
+    ctx.set_timing(True)
+    ctx.reset_timing()
+    y = hip(ctx, wtype, blocks, n, k).forward(x, t)
+    ran = ctx.timing()
+    ctx.set_timing(False)
+    assert any(name.startswith("rtq_mmk64") for name in ran), ran
+    c0 = _context({"RTQ_FWD_MMK": "0"})
+    y0 = hip(c0, wtype, blocks, n, k).forward(x, t)
+    c0.close()
+    assert rel_err(y, y0) <= 1e-6
+    assert rel_err(y, O.frozen_forward(wtype, blocks, n, k, x, nthreads=16)) <= TOL
+
+
 # ---------------------------------------------------------------- eight-wave forward, 32-row tiles
 @pytest.fixture(scope="module")
 def ctx_rg2():
