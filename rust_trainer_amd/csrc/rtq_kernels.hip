@@ -2732,6 +2732,246 @@ __device__ __forceinline__ void dx16_tile(const DxArgs& a) {
   }
 }
 
+// ============================================================== dx = dy . W, 32-token tiles
+// dx_tile's arithmetic and partial layout on four-wave workgroups of 32 tokens x 128 columns (wave
+// w: columns 32 w .. 32 w + 31, both 16-token MFMA tiles): twice the workgroups of the 64-token
+// tiles for the same row splits, so that short token ranges (the training step's 512) give the CUs
+// two independent workgroups each.  Each thread stages both halves of its W words (as rtq_dx16_*)
+// and one float4 of dy; the partials keep the 64-token fragment order (this workgroup's waves are
+// waves 4 wt + wk of the 64-token tile, wt = (t0 % 64) / 32), so rtq_bwd_finish reads them alike.
+template <int FMT>
+__device__ __forceinline__ void dx32_tile(const DxArgs& a) {
+  const int Kc = a.Kp / 128, ntt = (a.T + 63) / 64, nwt = (a.T + 31) / 32;
+  const int nunit = a.nsplit * nwt;
+  const int nmain = (nunit + 7) / 8 * 8 * Kc;
+  const int id = blockIdx.x;
+  if (id >= nmain) {
+    dx_lora_sums(a, id - nmain, gridDim.x - nmain);
+    return;  // uniform over the workgroup, before any barrier
+  }
+  constexpr bool KQ = is_kquant(FMT), B8 = byte_codes(FMT);
+  constexpr int D = 4;
+  __shared__ u4v sA[2][2][2][64];                                       // [buf][token tile][hi/lo][lane]
+  __shared__ __attribute__((aligned(16))) _Float16 sW[2][2][128][40];   // [buf][hi/lo][k][n]
+  __shared__ float sInv[32];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
+  // id -> unit and K chunk as dx_tile (the Kc workgroups of a unit back to back on one XCD)
+  const int kc = (id >> 3) % Kc, u = (id >> 3) / Kc * 8 + (id & 7);
+  if (u >= nunit) return;  // padding of the unit count to a multiple of 8 (uniform, before any barrier)
+  const int sp = u % a.nsplit;
+  const int t0 = (u / a.nsplit) * 32;
+  const int n0 = sp * a.n_per_split;
+  const int nsteps = (min(n0 + a.n_per_split, a.Np) - n0) / 32;
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 acc[2][2] = {{zero, zero}, {zero, zero}};
+
+  // dy loader: token tl, float4 q4 (rows ns + 4 q4 .. +3 of the step); a wave covers 16 tokens and
+  // four float4 columns, so its lanes write 32 consecutive A-fragment lanes' halves
+  const int tl = 16 * (w & 1) + (tid & 15), q4 = 4 * (w >> 1) + ((tid >> 4) & 3);
+  const __amdgpu_buffer_rsrc_t rdy = make_rsrc(a.dy, (uint32_t)a.T * a.N * 4u);
+  const uint32_t dy_off = ((uint32_t)(t0 + tl) * a.N + 4 * q4) * 4u;
+  const bool dy_vec = (a.N & 3) == 0;
+  // W loader (as rtq_dx16_*): row group rgl, rows 2wp, 2wp+1, k-group wgg, block jb, both halves
+  const int rgl = tid >> 7, qp = (tid >> 2) & 31, jb = tid & 3;
+  const int wp = qp & 7, wgg = qp >> 3;
+  const int li0 = 2 * wp, FL0 = 16 * wgg + li0;
+  const int nloc = rgl * 16 + li0;
+  const uint32_t wq_bytes = (uint32_t)(a.Np / 16) * Kc * 64 * 16 * (B8 ? 2 : 1);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.wq, wq_bytes);
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.wd, (uint32_t)(a.Np / 16) * Kc * 128);
+  const __amdgpu_buffer_rsrc_t re = make_rsrc(a.wsb, KQ ? (uint32_t)(a.Np / 16) * Kc * 32 : 0u);
+  uint32_t q_off[2];
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    if (!B8)
+      q_off[r] = ((((uint32_t)rgl * Kc + kc) * 64 + FL0 + r) * 4 + jb) * 4u;
+    else
+      q_off[r] = (((((uint32_t)rgl * Kc + kc) * 2 + (jb >> 1)) * 64 + FL0 + r) * 2 + (jb & 1)) * 8u;
+  }
+  const uint32_t d_off = KQ ? (uint32_t)RTQ_WR_INDEX(rgl, kc, Kc, li0, 0) * 2u
+                            : (uint32_t)RTQ_WD_INDEX(rgl, kc, Kc, li0, jb) * 2u;
+  const uint32_t e_off = (uint32_t)RTQ_WSB_INDEX(rgl, kc >> 1, Kc >> 1, li0) * 4u;
+  const uint32_t q_rg = (uint32_t)Kc * 64 * 16 * (B8 ? 2 : 1);
+  const uint32_t d_rg = (uint32_t)Kc * 128, e_rg = (uint32_t)Kc * 32;
+
+  // 2^e of this thread's dy row from the row maxima of the 256-row slices meeting this split
+  // (rtq_bwd_prep), reduced by all threads: thread (row tid % 32, slices tid / 32 + 8 k)
+  float dsc;
+  {
+    __shared__ float sRed[256];
+    const int q0 = n0 / 256, q1 = min((n0 + a.n_per_split + 255) / 256, a.dmq);
+    const int tok = tid % 32, t = t0 + tok;
+    float mx = 0.0f;
+    if (t < a.T) {
+#pragma unroll 4
+      for (int qq = q0 + tid / 32; qq < q1; qq += 8) mx = fmaxf(mx, a.dymax[(int64_t)qq * a.T + t]);
+    }
+    sRed[tid] = mx;
+    __syncthreads();
+    if (tid < 32) {
+      float m = sRed[tid];
+#pragma unroll
+      for (int k = 1; k < 8; k++) m = fmaxf(m, sRed[tid + k * 32]);
+      int ex = 0;
+      (void)frexpf(m, &ex);  // m = f 2^ex, f in [0.5, 1)
+      const bool ok = m > 0.0f && m <= 3.0e38f;
+      sRed[tid] = ok ? ldexpf(1.0f, 15 - ex) : 1.0f;
+      sInv[tid] = (ok ? ldexpf(1.0f, ex - 15) : 1.0f) * a.wunsc;
+    }
+    __syncthreads();
+    dsc = sRed[tl];
+  }
+  const float neg1 = -(a.wsc * a.wunsc);
+
+  Dx16Slot<FMT> sl[D];  // (its float2 dy unused here: a float4 in dy4)
+  f4 dy4[D];
+  auto issue = [&](int slot, int step) {
+    Dx16Slot<FMT>& S = sl[slot];
+    const int ns = n0 + 32 * min(step, max(nsteps - 1, 0));  // clamped: always a real step
+    const uint32_t srg = (uint32_t)(ns >> 4);
+    if (dy_vec) {
+      dy4[slot] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rdy, dy_off, (uint32_t)ns * 4u, 0));
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        dy4[slot][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rdy, dy_off + 4u * c, (uint32_t)ns * 4u, 0));
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      if (B8) {
+        const u2v v = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(rq, q_off[r], srg * q_rg, 0));
+        S.q[r][0] = v.x;
+        S.q[r][1] = v.y;
+      } else {
+        S.q[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rq, q_off[r], srg * q_rg, 0);
+      }
+    }
+    if constexpr (KQ) {
+      S.k = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rd, d_off, srg * d_rg, 0));
+      S.e = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(re, e_off, srg * e_rg, 0));
+    } else {
+      S.d = __builtin_amdgcn_raw_buffer_load_b32(rd, d_off, srg * d_rg, 0);
+    }
+  };
+  auto stage_compute = [&](int slot, int buf, int step) {
+    const Dx16Slot<FMT>& S = sl[slot];
+    {  // dy 2^e -> f16 hi / lo: A fragment tile tl >> 4, lane (tl & 15) + 16 (q4 >> 1), half q4 & 1
+      const int nst = n0 + 32 * min(step, max(nsteps - 1, 0));
+      f4 dv = dy4[slot];
+      if (nst + 32 > a.N) {  // ragged tail of N: columns >= N hold the next token's values
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          if (nst + 4 * q4 + c >= a.N) dv[c] = 0.0f;
+      }
+      const half2v h01 = pk_rtz(dv[0] * dsc, dv[1] * dsc), h23 = pk_rtz(dv[2] * dsc, dv[3] * dsc);
+      const half2v l01 = pk_rtz(fmaf(dv[0], dsc, -(float)h01.x), fmaf(dv[1], dsc, -(float)h01.y));
+      const half2v l23 = pk_rtz(fmaf(dv[2], dsc, -(float)h23.x), fmaf(dv[3], dsc, -(float)h23.y));
+      const u2v hv = {__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)};
+      const u2v lv = {__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)};
+      const int fl = (tl & 15) + 16 * (q4 >> 1);
+      reinterpret_cast<u2v*>(&sA[buf][tl >> 4][0][fl])[q4 & 1] = hv;
+      reinterpret_cast<u2v*>(&sA[buf][tl >> 4][1][fl])[q4 & 1] = lv;
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {  // W: rows li0, li0+1, half hh -> f16 hi / lo (as dx_tile)
+      uint32_t hw[4], lw[4];
+      if constexpr (KQ) {
+        float v[2][4];
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+          float d, m;
+          dq_params<FMT>(0u, comp(S.k, 2 * r + (jb >> 1)), r ? S.e.y : S.e.x, jb, hh, d, m);
+          d *= a.wsc;
+          m *= a.wsc;
+          const uint32_t uu = B8 ? S.q[r][hh] ^ 0x80808080u : (hh ? (S.q[r][0] >> 4) : S.q[r][0]) & 0x0f0f0f0fu;
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[r][e] = fmaf((float)((uu >> (8 * e)) & 0xffu), d, m);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const half2v h = pk_rtz(v[0][e], v[1][e]);
+          hw[e] = __builtin_bit_cast(uint32_t, h);
+          lw[e] = __builtin_bit_cast(uint32_t, pk_rtz(fmaf((float)h.x, neg1, v[0][e]), fmaf((float)h.y, neg1, v[1][e])));
+        }
+      } else {
+        const uint32_t u0 = B8 ? S.q[0][hh] ^ 0x80808080u : (hh ? (S.q[0][0] >> 4) : S.q[0][0]) & 0x0f0f0f0fu;
+        const uint32_t u1 = B8 ? S.q[1][hh] ^ 0x80808080u : (hh ? (S.q[1][0] >> 4) : S.q[1][0]) & 0x0f0f0f0fu;
+        const uint32_t i01 = __builtin_amdgcn_perm(u1, u0, 0x05010400u), i23 = __builtin_amdgcn_perm(u1, u0, 0x07030602u);
+        half2v dp = __builtin_bit_cast(half2v, S.d);
+        dp = dp * half2v{(_Float16)a.wsc, (_Float16)a.wsc};
+        constexpr _Float16 OFF = B8 ? (_Float16)1152.0f : (_Float16)1032.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const uint32_t src = e < 2 ? i01 : i23;
+          const half2v c = sub_h2((e & 1) ? bytes23_to_h2(src) : bytes01_to_h2(src), OFF);
+          const half2v h = dp * c;
+          const half2v l = __builtin_elementwise_fma(dp, c, -h);
+          hw[e] = __builtin_bit_cast(uint32_t, h);
+          lw[e] = __builtin_bit_cast(uint32_t, l);
+        }
+      }
+      const int kb = 32 * jb + 16 * hh + 4 * wgg;
+      const int nsw = nloc ^ (8 * jb);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        *reinterpret_cast<uint32_t*>(&sW[buf][0][kb + e][nsw]) = hw[e];
+        *reinterpret_cast<uint32_t*>(&sW[buf][1][kb + e][nsw]) = lw[e];
+      }
+    }
+    __syncthreads();
+    half8 ah[2], al[2];
+#pragma unroll
+    for (int ts = 0; ts < 2; ts++) {
+      ah[ts] = __builtin_bit_cast(half8, sA[buf][ts][0][lane]);
+      al[ts] = __builtin_bit_cast(half8, sA[buf][ts][1][lane]);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      const int kl = w * 32 + ks * 16 + li;  // column kl lies in block w: rows swizzled by 8 w
+      const half8 bh = *reinterpret_cast<const half8*>(&sW[buf][0][kl][8 * (g ^ w)]);
+      const half8 bl = *reinterpret_cast<const half8*>(&sW[buf][1][kl][8 * (g ^ w)]);
+#pragma unroll
+      for (int ts = 0; ts < 2; ts++) {
+        acc[ts][ks] = mfma_f16(ah[ts], bh, acc[ts][ks]);
+        acc[ts][ks] = mfma_f16(al[ts], bh, acc[ts][ks]);
+        acc[ts][ks] = mfma_f16(ah[ts], bl, acc[ts][ks]);
+      }
+    }
+  };
+#pragma unroll
+  for (int s0 = 0; s0 < D - 1; s0++) issue(s0, s0);
+  for (int st0 = 0; st0 < nsteps; st0 += D) {
+#pragma unroll
+    for (int s0 = 0; s0 < D; s0++) {
+      issue((s0 + D - 1) % D, st0 + s0 + D - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (st0 + s0 < nsteps) stage_compute(s0, (st0 + s0) & 1, st0 + s0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // rows back to dy's scale (and W's), then the partial in the 64-token fragment order: this
+  // workgroup's wave w is wave 4 wt + w of the 64-token tile t0 / 64 (wt = (t0 % 64) / 32)
+#pragma unroll
+  for (int ts = 0; ts < 2; ts++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float sv = sInv[16 * ts + 4 * g + i];
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) acc[ts][ks][i] *= sv;
+    }
+  const int wt = (t0 >> 5) & 1;
+  f4* out = reinterpret_cast<f4*>(a.part) + ((((int64_t)sp * ntt + (t0 >> 6)) * Kc + kc) * 8 + 4 * wt + w) * 256 + lane;
+#pragma unroll
+  for (int ts = 0; ts < 2; ts++)
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) out[(ts * 2 + ks) * 64] = acc[ts][ks];
+}
+
+extern "C" __global__ __launch_bounds__(256) void rtq_dx32_q4_0(DxArgs a) { dx32_tile<FMT_Q4_0>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_dx32_q8_0(DxArgs a) { dx32_tile<FMT_Q8_0>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_dx32_q4_k(DxArgs a) { dx32_tile<FMT_Q4_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_dx32_q6_k(DxArgs a) { dx32_tile<FMT_Q6_K>(a); }
+
 extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q4_0(DxArgs a) { dx16_tile<FMT_Q4_0>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q8_0(DxArgs a) { dx16_tile<FMT_Q8_0>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q4_k(DxArgs a) { dx16_tile<FMT_Q4_K>(a); }

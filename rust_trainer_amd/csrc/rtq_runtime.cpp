@@ -138,7 +138,8 @@ enum Kid {
   K_DX,          // + format
   K_DX16 = K_DX + F_COUNT,  // + format: t <= 16
   K_DXW = K_DX16 + F_COUNT,  // + format: large t, 256-token tiles
-  K_BWD_FINISH = K_DXW + F_COUNT,
+  K_DX32 = K_DXW + F_COUNT,  // + format: 32-token tiles on four-wave workgroups
+  K_BWD_FINISH = K_DX32 + F_COUNT,
   K_BWD_FINISH16,  // 16 waves per workgroup: long token reductions of dA / dB
   K_LORA_GRADS,    // dA / dB of several linears in one launch (4 / 16 waves per workgroup)
   K_LORA_GRADS16,
@@ -171,6 +172,7 @@ constexpr const char* kKernelNames[] = {
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
     "rtq_dxw_q4_0",         "rtq_dxw_q8_0",         "rtq_dxw_q4_k",         "rtq_dxw_q6_k",
+    "rtq_dx32_q4_0",        "rtq_dx32_q8_0",        "rtq_dx32_q4_k",        "rtq_dx32_q6_k",
     "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_lora_grads",       "rtq_lora_grads16",     "rtq_lora_grads_t",     "rtq_lora_grads_t16",
     "rtq_dense_rows",       "rtq_dense_bias",
     "rtq_head_norm",        "rtq_head_max",         "rtq_head_sum",         "rtq_head_grad",
@@ -211,6 +213,8 @@ struct rtq_ctx {
   std::vector<hipEvent_t> free_events;
   int dx_splits = 0;  // 0: automatic; RTQ_DX_SPLITS overrides (tuning)
   int dx_wide = -1;   // 256-token dx tiles: -1 automatic, 0 never, 1 for every t > 16 (RTQ_DX_WIDE)
+  int dx_32 = 0;      // 32-token dx tiles (RTQ_DX_32): 0 never, 1 with the 64-token plan's splits, 2 with
+                      // half of them
   int fwd_waves = 8;  // waves splitting K in the wide Q4_0 / Q8_0 forward (RTQ_FWD_WAVES: 4 or 8)
   int fwd_rg = -1;    // row groups of 16 per eight-wave forward tile: -1 automatic, 2 or 3 (RTQ_FWD_RG)
   int g64_min = -1;   // fewest 64-token g-partial workgroups (else 16-token ones): -1 = CUs / 2 (RTQ_G64_MIN)
@@ -718,6 +722,7 @@ struct DxPlan {
   int64_t splits, nps;
   bool tok16;
   bool wide;  // rtq_dxw_*: 256-token tiles (each dequantised weight element feeds 4x the MFMAs)
+  bool t32;   // rtq_dx32_*: 32-token tiles on four-wave workgroups (same partial layout as rtq_dx_*)
   size_t part_floats;
 };
 DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
@@ -732,6 +737,7 @@ DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
   const int64_t wgrid = roundup(cdiv(t, 256) * wsplits, 8) * Kc;
   const bool wide_fits = 100 * wgrid >= 85 * cdiv(wgrid, c->cu_count) * c->cu_count && steps / wsplits >= 16;
   p.wide = !p.tok16 && (c->dx_wide == 1 || (c->dx_wide < 0 && wide_fits));
+  p.t32 = !p.tok16 && !p.wide && c->dx_32 > 0;
   int64_t splits;
   if (p.tok16)
     splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(std::max<int64_t>(steps / 4, 1), 256),
@@ -740,6 +746,7 @@ DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
     splits = wsplits;
   else
     splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16), cdiv(c->cu_count, Kc * cdiv(t, 64))));
+  if (p.t32 && c->dx_32 == 2) splits = std::max<int64_t>(1, splits / 2);
   if (c->dx_splits > 0)
     splits = std::min<int64_t>(std::min<int64_t>(steps, p.tok16 ? 256 : (p.wide ? 64 : 16)), c->dx_splits);
   p.nps = cdiv(steps, splits) * 32;
@@ -817,13 +824,13 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   DxArgs xa{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, (int)dp.splits, part,
             lora ? hp : nullptr, lora ? gp : nullptr, (int)nhq, (int)ngq, (int)r, s, h, g, dymax, (int)ngq,
             w->dx_wsc, w->dx_wunsc};
-  const int kid = (dp.tok16 ? K_DX16 : (dp.wide ? K_DXW : K_DX)) + fmt_index(w->type);
+  const int kid = (dp.tok16 ? K_DX16 : (dp.wide ? K_DXW : (dp.t32 ? K_DX32 : K_DX))) + fmt_index(w->type);
   set_work(c, w, t, 0, true);
   // t > 16: (token group, split) units of K-chunk workgroups, padded to a multiple of 8 (XCD order)
   const int64_t nmain = dp.tok16 ? (w->Kp / 128) * dp.splits
-                                 : roundup(cdiv(t, dp.wide ? 256 : 64) * dp.splits, 8) * (w->Kp / 128);
+                                 : roundup(cdiv(t, dp.wide ? 256 : (dp.t32 ? 32 : 64)) * dp.splits, 8) * (w->Kp / 128);
   const int64_t nfin = lora ? std::min<int64_t>(64, cdiv(t * r, 512)) : 0;  // LoRA finalisers
-  RTQ_TRY(launch(c, kid, dim3((unsigned)(nmain + nfin)), dim3(dp.tok16 ? 256 : 512), st, xa));
+  RTQ_TRY(launch(c, kid, dim3((unsigned)(nmain + nfin)), dim3(dp.tok16 || dp.t32 ? 256 : 512), st, xa));
   const int64_t jt = cdiv(r, 16);
   LoraGradArgs fa{dy, h, g, x, la, (int)t, N, K, (int)r, s, gb, ga, dx, 0, 0, 0, part, (int)dp.splits, accumulate ? 1 : 0,
                   dp.tok16 ? 1 : 0, RankBlocks{}};
@@ -1034,6 +1041,7 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   c->cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   if (const char* e = getenv("RTQ_DX_SPLITS")) c->dx_splits = atoi(e);
   if (const char* e = getenv("RTQ_DX_WIDE")) c->dx_wide = atoi(e) ? 1 : 0;
+  if (const char* e = getenv("RTQ_DX_32")) c->dx_32 = std::min(std::max(atoi(e), 0), 2);
   if (const char* e = getenv("RTQ_FWD_WAVES")) c->fwd_waves = atoi(e) == 4 ? 4 : 8;
   if (const char* e = getenv("RTQ_FWD_MM")) c->fwd_mm = std::min(std::max(atoi(e), 0), 3);
   if (const char* e = getenv("RTQ_FWD_I8")) c->fwd_i8 = std::min(std::max(atoi(e), -1), 1);

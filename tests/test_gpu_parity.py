@@ -651,11 +651,24 @@ def ctx_dxw():
     c.close()
 
 
+@pytest.fixture(scope="module")
+def ctx_dx32():
+    """A context that sends every t > 16 dx through the 32-token-tile kernel (RTQ_DX_32=1,
+    rtq_dx32_*, four-wave workgroups writing the 64-token kernel's partial layout)."""
+    c = _context({"RTQ_DX_32": "1"})
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("which", ["ctx_dxw", "ctx_dx32"])
 @pytest.mark.parametrize("wtype,n,k,t", cases([(256, 512, 37), (100, 256, 300), (80, 2048, 130), (3072, 1024, 256),
-                                               (1024, 3072, 64)]))
-def test_backward_input_dxw_matches_oracle(ctx_dxw, wtype, n, k, t):
+                                               (1024, 3072, 64), (512, 1024, 20)]))
+def test_backward_input_dxw_matches_oracle(request, which, wtype, n, k, t):
+    # the 256- and 32-token-tile dx kernels: token padding inside a tile (37, 130, 20: half of a
+    # 64-token fragment never written by the 32-token kernel), ragged N, several splits
+    c = request.getfixturevalue(which)
     blocks, _, dy = make(wtype, n, k, t)
-    w = hip(ctx_dxw, wtype, blocks, n, k)
+    w = hip(c, wtype, blocks, n, k)
     dx0 = O.Rng(7).vec_normal(t * k, 1.0)
     dx = dx0.copy()
     w.backward_input(dy, t, dx)
@@ -671,7 +684,7 @@ def _dense(wtype, blocks, n, k):
     return np.stack([O.frozen_row(wtype, blocks, n, k, r) for r in range(n)]).astype(np.float64)
 
 
-@pytest.mark.parametrize("which", ["ctx", "ctx_dxw"])
+@pytest.mark.parametrize("which", ["ctx", "ctx_dxw", "ctx_dx32"])
 @pytest.mark.parametrize("wtype", FORMATS)
 @pytest.mark.parametrize("t", [1, 7, 16, 64, 300])
 def test_backward_input_precision(request, which, wtype, t):
@@ -717,12 +730,13 @@ def test_backward_input_huge_weight_scales(ctx, wtype, std, t):
     assert rel_err(dx, dense) <= 2e-6
 
 
+@pytest.mark.parametrize("which", ["ctx_dxw", "ctx_dx32"])
 @pytest.mark.parametrize("wtype", FORMATS)
-def test_linear_backward_dxw_lora(ctx_dxw, wtype):
+def test_linear_backward_dxw_lora(request, which, wtype):
     n, k, t, r = 512, 1024 if BLOCK[wtype] == 256 else 768, 300, 16
     blocks, x, dy = make(wtype, n, k, t)
     A, B = lora(n, k, r)
-    lin = rt.Linear("blk.0.attn_v", hip(ctx_dxw, wtype, blocks, n, k))
+    lin = rt.Linear("blk.0.attn_v", hip(request.getfixturevalue(which), wtype, blocks, n, k))
     lin.lora = rt.Lora(r, 32.0, A, B)
     dx = lin.backward(x, dy, t)
     wdx, wga, wgb = O.linear_backward(wtype, blocks, n, k, x, dy, A=A, B=B, alpha=32.0, nthreads=8)
