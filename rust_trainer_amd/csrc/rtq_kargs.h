@@ -136,6 +136,37 @@ struct FwdArgs {
   RankBlocks rb;        // LoRA B's block structure: a row's up-projection reads its member's ranks only
 };
 
+// rtq_gemvq{1,4}_*: row groups per tile (nibble codes, byte codes) and register-ring depth
+#ifndef RTQ_GQ_RG4
+#define RTQ_GQ_RG4 2
+#endif
+#ifndef RTQ_GQ_RG8
+#define RTQ_GQ_RG8 1
+#endif
+#ifndef RTQ_GQ_D
+#define RTQ_GQ_D 4
+#endif
+// rtq_gemvq{1,4}_*: y = x W^T (+ bias) (+ s (x A^T) B^T) for T <= 1 / 4 tokens in one launch (the
+// kernel quantises x itself).  Dynamic LDS: NT Kp bytes of codes, NT Kp / 32 block scales, NT Kp / 32
+// code sums (Q4_0: NT Kp / 8, one per k-group), NT * RTQ_LDS_RANK floats of h.
+struct GemvqArgs {
+  const void* wq;
+  const uint16_t* wdr;  // row-major scales (RTQ_WR_INDEX; the K-quants' sub-block scale words)
+  const uint32_t* wsb;  // K-quant super-block scales (RTQ_WSB_INDEX)
+  int Np, Kp;
+  const float* x;       // [T x K]
+  int T, N, K;
+  float* y;             // [T x N]
+  const float* bias;    // [N] or null
+  const float* la;      // LoRA A [r x K], or null (no adapter)
+  const float* lb;      // LoRA B [N x r]
+  int r;
+  float s;
+  RankBlocks rb;
+  int ntiles;           // row tiles of the weight (its row groups in runs of the kernel's RG)
+  int tiles_per_wave;   // wave v takes tiles v, v + waves, ... (at most this many)
+};
+
 // ---------------------------------------------------------------- backward
 // rtq_bwd_prep: partials of h = x . A^T and of dy . B per 256-column slice (src/linear.rs:106-111)
 struct BwdPrepArgs {

@@ -2102,6 +2102,308 @@ RTQ_GEMV(rtq_gemv_q8_0, FMT_Q8_0, 2, 4)
 RTQ_GEMV(rtq_gemv_q4_k, FMT_Q4_K, 4, 4)
 RTQ_GEMV(rtq_gemv_q6_k, FMT_Q6_K, 2, 4)
 
+// ============================================================== forward GEMV for T <= 4, one launch
+// y = x W^T (+ bias) (+ s (x A^T) B^T) for T <= NT tokens (NT 1 or 4).  Each workgroup first
+// quantises x into LDS with the activation kernel's arithmetic (Q8_0 per 32 columns for Q4_0 /
+// Q8_0 weights, Q8_K per 256 for the K-quants: the same codes and scales bit for bit), forms
+// h = x A^T there when adapted, then each wave streams its row tiles (RG row groups of 16 rows over
+// every chunk; tiles v, v + waves, .. for wave v) through a D-deep register ring that runs on
+// across tiles.  Lane (row li, k-group g) holds, per block j of a chunk, the codes of elements
+// 32j + 4g .. + 3 and 32j + 16 + 4g .. + 3 (the device layout): two v_dot4_i32_i8 with the
+// activation codes of the same elements (laid out in LDS per (token, chunk, k-group): 32 bytes)
+// give its share of the block's integer sum, exactly.  Q4_0 / Q8_0: each lane accumulates its
+// shares times the block's d_w d_x in f32 (Q4_0's code offset -8 enters as 8 times the lane's
+// activation code sum, kept in LDS per block), and the four k-groups' sums are added across
+// lanes once per tile (a fixed order; within 1e-6 of rtq_gemv_*, which adds the block's whole
+// integer sum first).  K-quants: the super-block sums S1, S2 are exact integers added across lanes
+// once per super-block, then rtq_gemv_*'s epilogue operation for operation (the same bits).  The
+// four lanes of a row hold the same sums; lane g stores token g.
+template <int FMT, int RG, int D, int NT>
+__device__ __forceinline__ void gemvq(const GemvqArgs& a) {
+  constexpr bool KQ = is_kquant(FMT), B8 = byte_codes(FMT);
+  extern __shared__ __attribute__((aligned(16))) char gqs[];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
+  const int nw = (int)(blockDim.x >> 6), Kc = a.Kp / 128, Kb = a.Kp / 32, ngroups = a.Np / 16;
+  uint32_t* xs = reinterpret_cast<uint32_t*>(gqs);                       // [NT][Kc][4 g][4 j][2]
+  float* sdx = reinterpret_cast<float*>(gqs + (size_t)NT * a.Kp);        // [NT][Kb] block scales
+  int* ssum = reinterpret_cast<int*>(sdx + NT * Kb);                     // [NT][Kb]: code sums (Q4_0: 8 x
+                                                                         //   the k-group's, [NT][Kc][4 g][4 j])
+  float* sh = reinterpret_cast<float*>(ssum + NT * Kb * (FMT == FMT_Q4_0 ? 4 : 1));  // [NT][RTQ_LDS_RANK] h
+  // ---- the weight stream: its first D - 1 items are requested before the activation work
+  const int wv = blockIdx.x * nw + w, nwv = gridDim.x * nw;
+  const int ntw = wv < a.ntiles ? min(a.tiles_per_wave, (a.ntiles - wv + nwv - 1) / nwv) : 0;
+  const int nit = ntw * Kc;
+  auto item = [&](int it, int& tile, int& kc) {
+    const int c = min(it, max(nit - 1, 0));  // clamped: always a real item
+    tile = wv + (c / Kc) * nwv;
+    kc = c % Kc;
+  };
+  auto issue = [&](GSlot<FMT, RG>& S, int it) {
+    int tile, kc;
+    item(it, tile, kc);
+#pragma unroll
+    for (int r = 0; r < RG; r++) {
+      const uint32_t rg = (uint32_t)min(tile * RG + r, ngroups - 1), base = rg * Kc + kc;
+      if (B8) {
+        S.w[r].q[0] = reinterpret_cast<const u4v*>(a.wq)[(base * 2) * 64 + lane];
+        S.w[r].q[B8 ? 1 : 0] = reinterpret_cast<const u4v*>(a.wq)[(base * 2 + 1) * 64 + lane];
+      } else {
+        S.w[r].q[0] = reinterpret_cast<const u4v*>(a.wq)[base * 64 + lane];
+      }
+      S.w[r].d = reinterpret_cast<const u2v*>(a.wdr)[base * 16 + li];
+      if (KQ) S.w[r].e = a.wsb[(rg * (Kc >> 1) + (kc >> 1)) * 16 + li];
+    }
+  };
+  GSlot<FMT, RG> sl[D];
+#pragma unroll
+  for (int s0 = 0; s0 < D - 1; s0++) issue(sl[s0], s0);
+  // ---- activation codes: one 32-column block (token t, block b) per thread and pass
+  for (int u0 = 0; u0 < NT * Kb; u0 += (int)blockDim.x) {
+    const int u = u0 + tid, t = u / Kb, b = u % Kb, k0 = 32 * b;
+    const bool real = u < NT * Kb && t < a.T && k0 < a.K;  // K % 32 == 0: a block is in or out
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      f4 q = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (real) q = reinterpret_cast<const f4*>(a.x + (int64_t)t * a.K + k0)[i];
+      v[4 * i] = q.x;
+      v[4 * i + 1] = q.y;
+      v[4 * i + 2] = q.z;
+      v[4 * i + 3] = q.w;
+    }
+    int q[32];
+    float dstore;
+    if (!KQ) {  // Q8_0: d = amax / 127, codes round(x / d) (half away from zero)
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+      const float d = __fdiv_rn(amax, 127.0f);
+      const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 32; i++) q[i] = (int)roundf(__fmul_rn(v[i], id));
+      dstore = (float)(_Float16)d;
+    } else {
+      // Q8_K: the first element of largest |x| of the super-block (eight adjacent lanes: larger
+      // |x| wins, equal |x| the lower column), iscale = -127 / that element, codes
+      // min(127, rint(iscale x)) (half to even), d = 1 / iscale
+      float best = 0.0f, bmax = 0.0f;
+      int bi = 0;
+#pragma unroll
+      for (int i = 0; i < 32; i++) {
+        const float ax = fabsf(v[i]);
+        if (ax > best) {
+          best = ax;
+          bmax = v[i];
+          bi = i;
+        }
+      }
+      bi += k0;
+#pragma unroll
+      for (int m = 1; m < 8; m <<= 1) {
+        const float ob = __shfl_xor(best, m), om = __shfl_xor(bmax, m);
+        const int oi = __shfl_xor(bi, m);
+        if (ob > best || (ob == best && oi < bi)) {
+          best = ob;
+          bmax = om;
+          bi = oi;
+        }
+      }
+      const float iscale = best != 0.0f ? __fdiv_rn(-127.0f, bmax) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 32; i++) q[i] = (int)fminf(127.0f, rintf(__fmul_rn(iscale, v[i])));
+      dstore = best != 0.0f ? __fdiv_rn(1.0f, iscale) : 0.0f;
+    }
+    if (u < NT * Kb) {
+      int cs = 0;
+#pragma unroll
+      for (int i = 0; i < 32; i++) cs += q[i];
+      const int kc = b >> 2, j = b & 3;
+#pragma unroll
+      for (int gg = 0; gg < 4; gg++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const int e = 16 * h + 4 * gg;
+          xs[(((t * Kc + kc) * 4 + gg) * 4 + j) * 2 + h] =
+              ((uint32_t)q[e] & 0xffu) | (((uint32_t)q[e + 1] & 0xffu) << 8) | (((uint32_t)q[e + 2] & 0xffu) << 16) |
+              ((uint32_t)q[e + 3] << 24);
+        }
+      sdx[t * Kb + b] = real ? dstore : 0.0f;
+      if (FMT == FMT_Q4_0) {  // 8 x (codes of k-group gg in this block), at [t][kc][gg][j]
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) {
+          int sg = 0;
+#pragma unroll
+          for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) sg += q[16 * h + 4 * gg + i];
+          ssum[((t * Kc + kc) * 4 + gg) * 4 + j] = real ? 8 * sg : 0;
+        }
+      } else {
+        ssum[t * Kb + b] = real ? cs : 0;
+      }
+    }
+  }
+  // ---- h = x A^T (LoRA down, f32): wave w takes pairs (t, j) w, w + nw, ..; lanes stride over K
+  if (a.la) {
+    for (int pr = w; pr < a.T * a.r; pr += nw) {
+      const int t = pr / a.r, j = pr % a.r;
+      const float* xr = a.x + (int64_t)t * a.K;
+      const float* ar = a.la + (int64_t)j * a.K;
+      float acc = 0.0f;
+      for (int k = lane; k < a.K; k += 64) acc = fmaf(xr[k], ar[k], acc);
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+      if (lane == 0) sh[t * RTQ_LDS_RANK + j] = acc;
+    }
+  }
+  __syncthreads();
+
+  float acc[RG][NT];
+  int s1[KQ ? RG : 1][NT], s2[KQ ? RG : 1][NT];
+#pragma unroll
+  for (int r = 0; r < RG; r++)
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[r][t] = 0.0f;
+#pragma unroll
+  for (int r = 0; r < (KQ ? RG : 1); r++)
+#pragma unroll
+    for (int t = 0; t < NT; t++) s1[r][t] = s2[r][t] = 0;
+  auto compute = [&](const GSlot<FMT, RG>& S, int it) {
+    int tile, kc;
+    item(it, tile, kc);
+    u4v xv[NT][2];  // this k-group's codes of the chunk: block j at words 2j (low four), 2j + 1
+    f4 xd[NT];      // the chunk's block scales
+    u4v x8[NT];     // Q4_0: 8 x this k-group's code sums of the chunk's blocks
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const u4v* xp = reinterpret_cast<const u4v*>(xs + ((t * Kc + kc) * 4 + g) * 8);
+      xv[t][0] = xp[0];
+      xv[t][1] = xp[1];
+      xd[t] = *reinterpret_cast<const f4*>(sdx + t * Kb + kc * 4);
+      if (FMT == FMT_Q4_0) x8[t] = *reinterpret_cast<const u4v*>(ssum + ((t * Kc + kc) * 4 + g) * 4);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int b = kc * 4 + j;
+#pragma unroll
+      for (int r = 0; r < RG; r++) {
+        uint32_t lo, hi;
+        if (B8) {
+          const u4v& qq = S.w[r].q[j >> 1];
+          lo = (j & 1) ? qq.z : qq.x;
+          hi = (j & 1) ? qq.w : qq.y;
+        } else {
+          const uint32_t cw = comp(S.w[r].q[0], j);
+          lo = cw & 0x0f0f0f0fu;
+          hi = (cw >> 4) & 0x0f0f0f0fu;
+        }
+        const uint32_t wvd = hcomp(S.w[r].d, j);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          const uint32_t xl = comp(xv[t][j >> 1], 2 * (j & 1)), xh = comp(xv[t][j >> 1], 2 * (j & 1) + 1);
+          if constexpr (!KQ) {  // this k-group's share of the block sum (Q4_0: codes u - 8)
+            const int x0 = FMT == FMT_Q4_0 ? -(int)comp(x8[t], j) : 0;
+            const int is = __builtin_amdgcn_sdot4((int)hi, (int)xh, __builtin_amdgcn_sdot4((int)lo, (int)xl, x0, false), false);
+            acc[r][t] = fmaf((float)is, h2f((uint16_t)wvd) * xd[t][j], acc[r][t]);
+          } else {
+          const int dl = __builtin_amdgcn_sdot4((int)lo, (int)xl, 0, false);
+          const int dh = __builtin_amdgcn_sdot4((int)hi, (int)xh, 0, false);
+          if constexpr (FMT == FMT_Q4_K) {
+            s1[r][t] += (int)(wvd & 0x3fu) * (dl + dh);  // sc * sum u x; m * sum x of block g below
+          } else {
+            const int sa = (int)(int8_t)(wvd & 0xffu), sb = (int)(int8_t)((wvd >> 8) & 0xffu);
+            s1[r][t] += (sa >> 4) * dl + (sb >> 4) * dh;  // sc = 16 (sc >> 4) + (sc & 15)
+            s2[r][t] += (sa & 15) * dl + (sb & 15) * dh;
+          }
+          }
+        }
+      }
+    }
+    if constexpr (FMT == FMT_Q4_K) {  // m_j * (sum of block j's codes) for block j = g, once per block
+#pragma unroll
+      for (int r = 0; r < RG; r++) {
+        const uint32_t dw2 = (g & 2) ? S.w[r].d.y : S.w[r].d.x, wvg = (g & 1) ? dw2 >> 16 : dw2;
+#pragma unroll
+        for (int t = 0; t < NT; t++) s2[r][t] += (int)((wvg >> 8) & 0x3fu) * ssum[t * Kb + kc * 4 + g];
+      }
+    }
+    if constexpr (KQ) {
+      if (kc & 1) {  // last chunk of the super-block
+#pragma unroll
+        for (int r = 0; r < RG; r++) {
+          const uint32_t ev = S.w[r].e;
+          const float dsb = h2f((uint16_t)(ev & 0xffffu));
+#pragma unroll
+          for (int t = 0; t < NT; t++) {
+            int v1 = s1[r][t], v2 = s2[r][t];
+            v1 += __shfl_xor(v1, 16);
+            v1 += __shfl_xor(v1, 32);
+            v2 += __shfl_xor(v2, 16);
+            v2 += __shfl_xor(v2, 32);
+            const float dxv = sdx[t * Kb + kc * 4];
+            if (FMT == FMT_Q4_K) {
+              const float dm = h2f((uint16_t)(ev >> 16)) * dxv;
+              acc[r][t] = fmaf(dsb * dxv, (float)v1, fmaf(-dm, (float)v2, acc[r][t]));
+            } else {
+              acc[r][t] = fmaf(dsb * dxv, fmaf(16.0f, (float)v1, (float)v2), acc[r][t]);
+            }
+            s1[r][t] = s2[r][t] = 0;
+          }
+        }
+      }
+    }
+    if (kc == Kc - 1) {  // the tile's last chunk: y (+ bias) (+ LoRA up), lane g storing token g
+#pragma unroll
+      for (int r = 0; r < RG; r++) {
+        const int n = (tile * RG + r) * 16 + li;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          if constexpr (!KQ) {  // the four k-groups' sums: (g0 + g1) + (g2 + g3)
+            acc[r][t] += __shfl_xor(acc[r][t], 16);
+            acc[r][t] += __shfl_xor(acc[r][t], 32);
+          }
+          if (g == t && t < a.T && n < a.N && it < nit) {
+            float o = acc[r][t];
+            if (a.bias) o = o + a.bias[n];
+            if (a.la) {
+              float lo = 0.0f;
+              for (int j = 0; j < a.r; j++)
+                if (rb_keep(a.rb, n, j)) lo = fmaf(a.lb[(int64_t)n * a.r + j], sh[t * RTQ_LDS_RANK + j], lo);
+              o = o + a.s * lo;
+            }
+            a.y[(int64_t)t * a.N + n] = o;
+          }
+          acc[r][t] = 0.0f;
+        }
+      }
+    }
+  };
+  for (int it0 = 0; it0 < nit; it0 += D) {
+#pragma unroll
+    for (int s0 = 0; s0 < D; s0++) {
+      issue(sl[(s0 + D - 1) % D], it0 + s0 + D - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (it0 + s0 < nit) compute(sl[s0], it0 + s0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+// nibble layouts: RTQ_GQ_RG4 row groups per tile; byte layouts: RTQ_GQ_RG8; NT = 1 or 4 tokens
+#define RTQ_GEMVQ(NAME, FMT, RG, NT)                                       \
+  extern "C" __global__ __launch_bounds__(256) void NAME(GemvqArgs a) {    \
+    gemvq<FMT, RG, RTQ_GQ_D, NT>(a);                                       \
+  }
+RTQ_GEMVQ(rtq_gemvq1_q4_0, FMT_Q4_0, RTQ_GQ_RG4, 1)
+RTQ_GEMVQ(rtq_gemvq1_q8_0, FMT_Q8_0, RTQ_GQ_RG8, 1)
+RTQ_GEMVQ(rtq_gemvq1_q4_k, FMT_Q4_K, RTQ_GQ_RG4, 1)
+RTQ_GEMVQ(rtq_gemvq1_q6_k, FMT_Q6_K, RTQ_GQ_RG8, 1)
+RTQ_GEMVQ(rtq_gemvq4_q4_0, FMT_Q4_0, RTQ_GQ_RG4, 4)
+RTQ_GEMVQ(rtq_gemvq4_q8_0, FMT_Q8_0, RTQ_GQ_RG8, 4)
+RTQ_GEMVQ(rtq_gemvq4_q4_k, FMT_Q4_K, RTQ_GQ_RG4, 4)
+RTQ_GEMVQ(rtq_gemvq4_q6_k, FMT_Q6_K, RTQ_GQ_RG8, 4)
+#undef RTQ_GEMVQ
+
 // ============================================================== backward preparation
 // LoRA partial products of src/linear.rs:106-111, 256 threads per workgroup, grid
 // (ceil(T / 16), nhq + ngq) offset by y0 (nhq 0: the forward kept the h partials):

@@ -118,7 +118,9 @@ enum Kid {
   K_FWD_W_ISUMS = K_FWD_S + F_COUNT,      // debug variants writing the integer sums
   K_FWD_S_ISUMS = K_FWD_W_ISUMS + F_COUNT,
   K_GEMV = K_FWD_S_ISUMS + F_COUNT,       // + format: t <= 16, large N
-  K_FWD_Q4_0_W8 = K_GEMV + F_COUNT,       // wide forward with eight waves splitting K
+  K_GEMVQ1 = K_GEMV + F_COUNT,            // + format: t == 1, one launch (its own activation codes)
+  K_GEMVQ4 = K_GEMVQ1 + F_COUNT,          // + format: t <= 4, one launch
+  K_FWD_Q4_0_W8 = K_GEMVQ4 + F_COUNT,     // wide forward with eight waves splitting K
   K_FWD_Q8_0_W8,
   K_FWD_Q4_0_W8R2,  // the same with 32-row tiles
   K_FWD_Q8_0_W8R2,
@@ -163,6 +165,8 @@ constexpr const char* kKernelNames[] = {
     "rtq_fwd_q4_0_w_isums", "rtq_fwd_q8_0_w_isums", "rtq_fwd_q4_k_w_isums", "rtq_fwd_q6_k_w_isums",
     "rtq_fwd_q4_0_s_isums", "rtq_fwd_q8_0_s_isums", "rtq_fwd_q4_k_s_isums", "rtq_fwd_q6_k_s_isums",
     "rtq_gemv_q4_0",        "rtq_gemv_q8_0",        "rtq_gemv_q4_k",        "rtq_gemv_q6_k",
+    "rtq_gemvq1_q4_0",      "rtq_gemvq1_q8_0",      "rtq_gemvq1_q4_k",      "rtq_gemvq1_q6_k",
+    "rtq_gemvq4_q4_0",      "rtq_gemvq4_q8_0",      "rtq_gemvq4_q4_k",      "rtq_gemvq4_q6_k",
     "rtq_fwd_q4_0_w8",      "rtq_fwd_q8_0_w8",      "rtq_fwd_q4_0_w8r2",    "rtq_fwd_q8_0_w8r2",
     "rtq_mm_q4_0",          "rtq_mm_q8_0",
     "rtq_mm64_q4_0",        "rtq_mm64_q8_0",        "rtq_mm32_q4_0",        "rtq_mm32_q8_0",
@@ -222,6 +226,8 @@ struct rtq_ctx {
                       // whenever the format allows (RTQ_FWD_MM)
   int fwd_mmk = -1;   // K-quant ring forward (rtq_mmk*_*; RTQ_FWD_MMK): -1 automatic, 0 never, 1 / 2 the 64- /
                       // 32-token tiles whenever the shape allows
+  int gemvq = 1;      // one-launch GEMV for t <= 4 (rtq_gemvq*_*; RTQ_GEMVQ=0: activation kernel + GEMM)
+  int gemvq_wpc = 0;  // its waves per CU (RTQ_GEMVQ_WPC; 0: automatic)
   int fwd_i8 = -1;    // int8-MFMA forwards (rtq_mmi8_*; RTQ_FWD_I8): -1 automatic (Q8_0 weights), 0 never,
                       // 1 every Q4_0 / Q8_0 weight, wherever the 128- or 64-token tiles are chosen
   int64_t t_launches[K_COUNT] = {};
@@ -539,6 +545,28 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   if (is_dense(w->type)) {
     if (sw) return fail(RTQ_ERR_UNSUPPORTED, "internal: SwiGLU input of a dense weight");
     return enqueue_forward_dense(c, w, x, t, y, bias, la, lb, lora ? r : 0, s, ar, st);
+  }
+  // t <= 4: one launch that quantises x itself (codes, scales and h in LDS, at most 64 KB)
+  // (not where a later backward reads the LoRA-down partials: this kernel keeps none)
+  if (c->gemvq && t <= 4 && !isums && !sw && !hp_keep && (!lora || r <= RTQ_LDS_RANK)) {
+    const int nt = t == 1 ? 1 : 4;
+    const size_t lds = (size_t)nt * w->Kp + (size_t)nt * (w->Kp / 32) * 4 * (w->type == RTQ_TYPE_Q4_0 ? 5 : 2) +
+                       (size_t)nt * RTQ_LDS_RANK * 4;
+    if (lds <= 65536) {
+      const int rg = byte_codes(w->type) ? RTQ_GQ_RG8 : RTQ_GQ_RG4;
+      const int64_t ntiles = cdiv(w->Np / 16, rg);
+      // waves per CU: 24 for the nibble layouts (their VGPRs allow 20 - 24 resident), 8 for the byte
+      // ones (longer streams per wave; LM head at t = 1, one MI355X: Q4_0 21.1 us at 24 against 23.4
+      // at 16, Q4_K 24.8 against 26.7, Q6_K 34.0 at 8 against 39.2 at 16, Q8_0 32.7 at 8 or 24);
+      // every wave takes the same number of tiles (the last ones fewer)
+      const int64_t wpc = c->gemvq_wpc > 0 ? c->gemvq_wpc : (byte_codes(w->type) ? 8 : 24);
+      const int64_t maxw = (int64_t)c->cu_count * wpc, per = cdiv(ntiles, maxw), nwaves = cdiv(ntiles, per);
+      GemvqArgs ga{w->wq, w->wdr, w->wsb, (int)w->Np, (int)w->Kp, x, (int)t, (int)w->rows, (int)w->cols, y, bias,
+                   lora ? la : nullptr, lb, lora ? (int)r : 0, s, rbv, (int)ntiles, (int)per};
+      set_work(c, w, t, lora ? r : 0, false);
+      return launch(c, (nt == 1 ? K_GEMVQ1 : K_GEMVQ4) + fmt_index(w->type), dim3((unsigned)cdiv(nwaves, 4)),
+                    dim3(256), st, ga, (unsigned)lds);
+    }
   }
   FwdPlan p = fwd_plan(w, t, lora ? r : 0);
   // the debug sums come from the skinny / wide kernels; the GEMV pays off once its row tiles alone
@@ -1046,6 +1074,8 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   if (const char* e = getenv("RTQ_FWD_MM")) c->fwd_mm = std::min(std::max(atoi(e), 0), 3);
   if (const char* e = getenv("RTQ_FWD_I8")) c->fwd_i8 = std::min(std::max(atoi(e), -1), 1);
   if (const char* e = getenv("RTQ_FWD_MMK")) c->fwd_mmk = std::min(std::max(atoi(e), -1), 2);
+  if (const char* e = getenv("RTQ_GEMVQ")) c->gemvq = atoi(e) ? 1 : 0;
+  if (const char* e = getenv("RTQ_GEMVQ_WPC")) c->gemvq_wpc = std::min(std::max(atoi(e), 0), 32);
   if (const char* e = getenv("RTQ_FWD_RG")) c->fwd_rg = atoi(e) == 2 ? 2 : 3;
   if (const char* e = getenv("RTQ_G64_MIN")) c->g64_min = atoi(e);
   hipError_t e = hipModuleLoadData(&c->mod, rtq_hsaco_begin);

@@ -835,3 +835,78 @@ def test_trainer_q8_0_falls_back_to_f32(ctx):
     assert hw.ggml_type == rt.TYPE_F32 and hw.nbytes() == 8 * 40 * 4
     x = O.Rng(2).vec_normal(3 * 40, 1.0).reshape(3, 40)
     assert rel_err(hw.forward(x, 3), x.astype(np.float64) @ w.T.astype(np.float64)) <= 1e-5
+
+
+# ---------------------------------------------------------------- one-launch GEMV (t <= 4)
+@pytest.fixture(scope="module")
+def ctx_no_gemvq():
+    """A context without the one-launch GEMV (RTQ_GEMVQ=0): activation kernel + rtq_gemv_* / rtq_fwd_*_s"""
+    c = _context({"RTQ_GEMVQ": "0"})
+    yield c
+    c.close()
+
+
+def _ran(c, fn):
+    c.set_timing(True)
+    c.reset_timing()
+    out = fn()
+    names = c.timing()
+    c.set_timing(False)
+    return out, names
+
+
+@pytest.mark.parametrize("r", [0, 16])
+@pytest.mark.parametrize("wtype,n,k,t", cases([(64, 128, 1), (100, 96, 3), (2048, 1024, 1), (1024, 3072, 4),
+                                               (300, 512, 2), (1000, 256, 4), (4100, 768, 1)]))
+def test_gemvq_matches_oracle(ctx, wtype, n, k, t, r):
+    """rtq_gemvq*_* (t <= 4: activation codes formed in the kernel, integer block sums by
+    v_dot4_i32_i8) against the oracle: ragged N (100, 300, 1000, 4100 rows), K padded to a chunk
+    (96, 768), a bias, tokens 2 and 3 of the four-token kernel, LoRA r=16"""
+    blocks, x, _ = make(wtype, n, k, t)
+    bias = O.Rng(6).vec_normal(n, 0.1)
+    lin = rt.Linear("blk.0.attn_q", hip(ctx, wtype, blocks, n, k), bias=bias)
+    if r:
+        A, B = lora(n, k, r)
+        lin.lora = rt.Lora(r, 2.0 * r, A, B)
+    y, names = _ran(ctx, lambda: lin.forward(x, t))
+    assert names and all(nm.startswith("rtq_gemvq") for nm in names), names
+    kw = dict(A=A, B=B, alpha=2.0 * r) if r else {}
+    want = O.linear_forward(wtype, blocks, n, k, x, bias=bias, nthreads=8, **kw)
+    assert rel_err(y, want) <= TOL
+
+
+@pytest.mark.parametrize("wtype", FORMATS)
+@pytest.mark.parametrize("t", [1, 3, 4])
+def test_gemvq_against_mfma_gemv(ctx, ctx_no_gemvq, wtype, t):
+    """The one-launch kernel against the MFMA GEMV (rtq_gemv_*: the same activation codes and
+    exact integer sums), on a weight tall enough for the MFMA GEMV to run without splitting K
+    (131072 rows: its split adds chunk partials with atomics).  K-quants without an adapter: the
+    same bits (the same super-block sums and epilogue operations); Q4_0 / Q8_0 (k-group shares
+    scaled before they are added) and LoRA (h summed in another order): within 1e-6"""
+    n, k = 131072, 256
+    blocks, x, _ = make(wtype, n, k, t)
+    outs = []
+    for c, pre in ((ctx, "rtq_gemvq"), (ctx_no_gemvq, "rtq_gemv_")):
+        lin = rt.Linear("output", hip(c, wtype, blocks, n, k))
+        y, names = _ran(c, lambda: lin.forward(x, t))
+        assert any(nm.startswith(pre) for nm in names), names
+        A, B = lora(n, k, 16)
+        lin.lora = rt.Lora(16, 32.0, A, B)
+        outs.append((y, lin.forward(x, t)))
+    if BLOCK[wtype] == 256:
+        np.testing.assert_array_equal(outs[0][0], outs[1][0])
+    else:
+        assert rel_err(outs[0][0], outs[1][0]) <= 1e-6
+    assert rel_err(outs[0][1], outs[1][1]) <= 1e-6
+    assert rel_err(outs[0][0], O.frozen_forward(wtype, blocks, n, k, x, nthreads=16)) <= TOL
+
+
+@pytest.mark.parametrize("wtype", FORMATS)
+def test_gemvq_lm_head_t1(ctx, wtype):
+    """The LM head shape at t = 1 (151936 x 1024): tiles spread over every CU, several per wave"""
+    n, k, t = 151936, 1024, 1
+    blocks, x, _ = make(wtype, n, k, t)
+    w = hip(ctx, wtype, blocks, n, k)
+    y, names = _ran(ctx, lambda: w.forward(x, t))
+    assert all(nm.startswith("rtq_gemvq1") for nm in names), names
+    assert rel_err(y, O.frozen_forward(wtype, blocks, n, k, x, nthreads=16)) <= TOL
