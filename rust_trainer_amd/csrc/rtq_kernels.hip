@@ -48,6 +48,10 @@ __device__ __forceinline__ f4 mfma_f32(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+// a raw buffer descriptor over [p, p + bytes): loads past the end return zero
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
 // two floats -> f16 pair, rounded toward zero (v_cvt_pkrtz_f16_f32)
 __device__ __forceinline__ half2v pk_rtz(float a, float b) {
   return __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a, b));
@@ -2130,7 +2134,8 @@ __device__ __forceinline__ void gemvq(const GemvqArgs& a) {
                                                                          //   the k-group's, [NT][Kc][4 g][4 j])
   float* sh = reinterpret_cast<float*>(ssum + NT * Kb * (FMT == FMT_Q4_0 ? 4 : 1));  // [NT][RTQ_LDS_RANK] h
   // ---- the weight stream: its first D - 1 items are requested before the activation work
-  const int wv = blockIdx.x * nw + w, nwv = gridDim.x * nw;
+  // (the wave index through readfirstlane: the tile and chunk arithmetic stays scalar)
+  const int wv = blockIdx.x * nw + __builtin_amdgcn_readfirstlane(w), nwv = gridDim.x * nw;
   const int ntw = wv < a.ntiles ? min(a.tiles_per_wave, (a.ntiles - wv + nwv - 1) / nwv) : 0;
   const int nit = ntw * Kc;
   auto item = [&](int it, int& tile, int& kc) {
@@ -2138,6 +2143,10 @@ __device__ __forceinline__ void gemvq(const GemvqArgs& a) {
     tile = wv + (c / Kc) * nwv;
     kc = c % Kc;
   };
+  // buffer loads: a per-lane offset and a per-item scalar one (the weight is below 4 GB: the caller checks)
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.wq, (uint32_t)ngroups * Kc * 1024u * (B8 ? 2u : 1u));
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.wdr, (uint32_t)ngroups * Kc * 128u);
+  const __amdgpu_buffer_rsrc_t re = make_rsrc(a.wsb, KQ ? (uint32_t)ngroups * (Kc >> 1) * 64u : 0u);
   auto issue = [&](GSlot<FMT, RG>& S, int it) {
     int tile, kc;
     item(it, tile, kc);
@@ -2145,13 +2154,13 @@ __device__ __forceinline__ void gemvq(const GemvqArgs& a) {
     for (int r = 0; r < RG; r++) {
       const uint32_t rg = (uint32_t)min(tile * RG + r, ngroups - 1), base = rg * Kc + kc;
       if (B8) {
-        S.w[r].q[0] = reinterpret_cast<const u4v*>(a.wq)[(base * 2) * 64 + lane];
-        S.w[r].q[B8 ? 1 : 0] = reinterpret_cast<const u4v*>(a.wq)[(base * 2 + 1) * 64 + lane];
+        S.w[r].q[0] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16u, base * 2048u, 0));
+        S.w[r].q[B8 ? 1 : 0] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16u, base * 2048u + 1024u, 0));
       } else {
-        S.w[r].q[0] = reinterpret_cast<const u4v*>(a.wq)[base * 64 + lane];
+        S.w[r].q[0] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16u, base * 1024u, 0));
       }
-      S.w[r].d = reinterpret_cast<const u2v*>(a.wdr)[base * 16 + li];
-      if (KQ) S.w[r].e = a.wsb[(rg * (Kc >> 1) + (kc >> 1)) * 16 + li];
+      S.w[r].d = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(rd, li * 8u, base * 128u, 0));
+      if (KQ) S.w[r].e = __builtin_amdgcn_raw_buffer_load_b32(re, li * 4u, (rg * (Kc >> 1) + (kc >> 1)) * 64u, 0);
     }
   };
   GSlot<FMT, RG> sl[D];
@@ -2306,14 +2315,15 @@ __device__ __forceinline__ void gemvq(const GemvqArgs& a) {
             const int is = __builtin_amdgcn_sdot4((int)hi, (int)xh, __builtin_amdgcn_sdot4((int)lo, (int)xl, x0, false), false);
             acc[r][t] = fmaf((float)is, h2f((uint16_t)wvd) * xd[t][j], acc[r][t]);
           } else {
-          const int dl = __builtin_amdgcn_sdot4((int)lo, (int)xl, 0, false);
-          const int dh = __builtin_amdgcn_sdot4((int)hi, (int)xh, 0, false);
-          if constexpr (FMT == FMT_Q4_K) {
-            s1[r][t] += (int)(wvd & 0x3fu) * (dl + dh);  // sc * sum u x; m * sum x of block g below
+          if constexpr (FMT == FMT_Q4_K) {  // sc * sum u x (24-bit products); m * sum x of block g below
+            const int d2 = __builtin_amdgcn_sdot4((int)hi, (int)xh, __builtin_amdgcn_sdot4((int)lo, (int)xl, 0, false), false);
+            s1[r][t] += __mul24((int)(wvd & 0x3fu), d2);
           } else {
+            const int dl = __builtin_amdgcn_sdot4((int)lo, (int)xl, 0, false);
+            const int dh = __builtin_amdgcn_sdot4((int)hi, (int)xh, 0, false);
             const int sa = (int)(int8_t)(wvd & 0xffu), sb = (int)(int8_t)((wvd >> 8) & 0xffu);
-            s1[r][t] += (sa >> 4) * dl + (sb >> 4) * dh;  // sc = 16 (sc >> 4) + (sc & 15)
-            s2[r][t] += (sa & 15) * dl + (sb & 15) * dh;
+            s1[r][t] += __mul24(sa >> 4, dl) + __mul24(sb >> 4, dh);  // sc = 16 (sc >> 4) + (sc & 15)
+            s2[r][t] += __mul24(sa & 15, dl) + __mul24(sb & 15, dh);
           }
           }
         }
@@ -2324,7 +2334,7 @@ __device__ __forceinline__ void gemvq(const GemvqArgs& a) {
       for (int r = 0; r < RG; r++) {
         const uint32_t dw2 = (g & 2) ? S.w[r].d.y : S.w[r].d.x, wvg = (g & 1) ? dw2 >> 16 : dw2;
 #pragma unroll
-        for (int t = 0; t < NT; t++) s2[r][t] += (int)((wvg >> 8) & 0x3fu) * ssum[t * Kb + kc * 4 + g];
+        for (int t = 0; t < NT; t++) s2[r][t] += __mul24((int)((wvg >> 8) & 0x3fu), ssum[t * Kb + kc * 4 + g]);
       }
     }
     if constexpr (KQ) {
@@ -2457,9 +2467,6 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_prep(BwdPrepArgs a) {
 // words a wave loads lie in one 512-byte span; the two rows' scales are adjacent (one load).
 // The converted pair of rows goes to LDS as one 32-bit word per column.  Within a column the
 // 8-row groups are XOR-swizzled by the block index so the four blocks' writes use different banks.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
 
 template <int FMT, int NQ = 1>
 struct DxSlot {
