@@ -213,6 +213,7 @@ struct DxArgs {
   const float* dymax;
   int dmq;
   float wsc, wunsc;
+  const uint16_t* wdr;  // row-major scales (RTQ_WR_INDEX): rtq_dxv1_*
 };
 
 // dx[t][k] = [dx +] sum_s part[s][t][k] [+ sum_j g[t][j] A[j][k]];

@@ -48,6 +48,12 @@ __device__ __forceinline__ f4 mfma_f32(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+// v from the lane that DPP control CTRL names, within each row of 16 lanes (0xB1: lane ^ 1, 0x4E:
+// lane ^ 2, 0x141: the mirror lane within each group of eight, 0x140: the mirror lane within the row)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
 // a raw buffer descriptor over [p, p + bytes): loads past the end return zero
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
@@ -2822,6 +2828,139 @@ __device__ __forceinline__ void dx_tile(const DxArgs& a) {
   }
 }
 
+// ============================================================== dx = dy . W for T = 1
+// One token: dx[k] = sum_n dy[n] W[n][k] with f32 FMAs, no MFMA.  Workgroup (K chunk kc, row split
+// sp) of four waves; wave w takes the row groups rg0 + w, rg0 + w + 4, .. of the split through a
+// D-deep register ring.  Lane (row li, k-group g) holds, per row group, the codes of row
+// n = 16 rg + li for the 32 columns {32j + 4g .. + 3, 32j + 16 + 4g .. + 3} (j < 4) of the chunk (the
+// device layout), turns them into exact f16 values (the code less its offset: Q4_0 u - 8, Q8_0 /
+// Q6_K q, Q4_K u) and adds c * value into its 32 column sums by mixed-precision FMA, c = dy[n] times
+// the row's scale for that block (Q4_K: d sc; its - dmin m part enters as dy[n] dmin m summed per
+// block and subtracted once; Q6_K: d sc of each 16-element half).  The 16 rows of a k-group (one
+// DPP row of lanes) are added by four DPP steps, the four waves in wave order through LDS, and the
+// workgroup writes part[sp][0][128 kc ..] row-major (rtq_bwd_finish adds the splits in order).
+template <int FMT>
+struct Dxv1Slot {
+  u4v q[byte_codes(FMT) ? 2 : 1];  // codes (nibble layout, or byte layout in two parts)
+  u2v d;                           // row li, blocks 0..3: fp16 scales / K-quant sub-block words
+  uint32_t e;                      // K-quants: the row's super-block (d, dmin)
+  float dy;                        // dy of the row
+};
+
+template <int FMT>
+__device__ __forceinline__ void dxv1_tile(const DxArgs& a) {
+  constexpr bool KQ = is_kquant(FMT), B8 = byte_codes(FMT);
+  constexpr int D = 4;
+  const int Kc = a.Kp / 128, ngroups = a.Np / 16;
+  const int nmain = Kc * a.nsplit;
+  const int id = blockIdx.x;
+  if (id >= nmain) {
+    dx_lora_sums(a, id - nmain, gridDim.x - nmain);
+    return;  // uniform over the workgroup, before any barrier
+  }
+  __shared__ float red[4][128];
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kc = id % Kc, sp = id / Kc;
+  const int rps = a.n_per_split / 16;  // row groups per split
+  const int rg0 = sp * rps, rg1 = min(rg0 + rps, ngroups);
+  const int nit = rg1 - rg0 > w ? (rg1 - rg0 - w + 3) / 4 : 0;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.wq, (uint32_t)ngroups * Kc * 1024u * (B8 ? 2u : 1u));
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.wdr, (uint32_t)ngroups * Kc * 128u);
+  const __amdgpu_buffer_rsrc_t re = make_rsrc(a.wsb, KQ ? (uint32_t)ngroups * (Kc >> 1) * 64u : 0u);
+  const __amdgpu_buffer_rsrc_t rdy = make_rsrc(a.dy, (uint32_t)a.N * 4u);  // rows >= N read zero
+  auto issue = [&](Dxv1Slot<FMT>& S, int it) {
+    const uint32_t rg = (uint32_t)(rg0 + w + 4 * min(it, max(nit - 1, 0))), base = rg * Kc + kc;  // clamped
+    if (B8) {
+      S.q[0] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16u, base * 2048u, 0));
+      S.q[B8 ? 1 : 0] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16u, base * 2048u + 1024u, 0));
+    } else {
+      S.q[0] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16u, base * 1024u, 0));
+    }
+    S.d = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(rd, li * 8u, base * 128u, 0));
+    if (KQ) S.e = __builtin_amdgcn_raw_buffer_load_b32(re, li * 4u, (rg * (Kc >> 1) + (kc >> 1)) * 64u, 0);
+    S.dy = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rdy, li * 4u, rg * 64u, 0));
+  };
+  float acc[4][8], bias[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    bias[j] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[j][e] = 0.0f;
+  }
+  auto compute = [&](const Dxv1Slot<FMT>& S) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t wv = hcomp(S.d, j);
+      half8 f;
+      float c, c2 = 0.0f;  // c2: Q6_K, the second half's factor
+      if constexpr (FMT == FMT_Q4_0 || FMT == FMT_Q8_0) {
+        c = S.dy * h2f((uint16_t)wv);
+        if (FMT == FMT_Q4_0) {
+          f = q4_0_frag<8>(comp(S.q[0], j));
+        } else {
+          const u4v& qq = S.q[j >> 1];
+          f = (j & 1) ? q8_frag(qq.z, qq.w) : q8_frag(qq.x, qq.y);
+        }
+      } else if constexpr (FMT == FMT_Q4_K) {  // value d sc u - dmin m
+        const float dsb = h2f((uint16_t)(S.e & 0xffffu)), dmin = h2f((uint16_t)(S.e >> 16));
+        c = S.dy * (dsb * (float)(wv & 0x3fu));
+        bias[j] = fmaf(S.dy, dmin * (float)((wv >> 8) & 0x3fu), bias[j]);
+        f = q4_0_frag<0>(comp(S.q[0], j));
+      } else {  // Q6_K: value d sc q, sc per 16 elements (low byte: elements 0..15 of the block)
+        const float dsb = h2f((uint16_t)(S.e & 0xffffu));
+        c = S.dy * (dsb * (float)(int)(int8_t)(wv & 0xffu));
+        c2 = S.dy * (dsb * (float)(int)(int8_t)((wv >> 8) & 0xffu));
+        const u4v& qq = S.q[j >> 1];
+        f = (j & 1) ? q8_frag(qq.z, qq.w) : q8_frag(qq.x, qq.y);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc[j][e] = fmaf(FMT == FMT_Q6_K && e >= 4 ? c2 : c, (float)f[e], acc[j][e]);
+    }
+  };
+  Dxv1Slot<FMT> sl[D];
+#pragma unroll
+  for (int s0 = 0; s0 < D - 1; s0++) issue(sl[s0], s0);
+  for (int it0 = 0; it0 < nit; it0 += D) {
+#pragma unroll
+    for (int s0 = 0; s0 < D; s0++) {
+      issue(sl[(s0 + D - 1) % D], it0 + s0 + D - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (it0 + s0 < nit) compute(sl[s0]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // the 16 rows of each k-group: lanes i ^ 1, the quad, the other quad of the eight, the other eight
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    if (FMT == FMT_Q4_K) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc[j][e] -= bias[j];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      float v = acc[j][e];
+      v += dpp_f<0xB1>(v);
+      v += dpp_f<0x4E>(v);
+      v += dpp_f<0x141>(v);
+      v += dpp_f<0x140>(v);
+      acc[j][e] = v;
+    }
+  }
+  if (li == 0) {  // lane (0, g): columns 32j + 4g + e (e < 4) and 32j + 16 + 4g + e - 4 (e >= 4)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) red[w][32 * j + (e < 4 ? 4 * g + e : 16 + 4 * g + e - 4)] = acc[j][e];
+  }
+  __syncthreads();
+  if (tid < 128) {
+    const int col = kc * 128 + tid;
+    const float v = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+    if (col < a.K) a.part[(int64_t)sp * a.K + col] = v;  // (no f16 weight values: no pre-scaling to undo)
+  }
+}
+
 // ============================================================== dx = dy . W for T <= 16
 // Same arithmetic as dx_tile with one 16-token tile: workgroup of 4 waves, tile 16 tokens x 128
 // columns (wave w: the 32 columns of block w), 32 rows per step, many row splits (a GEMV-shaped
@@ -3281,6 +3420,10 @@ extern "C" __global__ __launch_bounds__(256) void rtq_dx32_q8_0(DxArgs a) { dx32
 extern "C" __global__ __launch_bounds__(256) void rtq_dx32_q4_k(DxArgs a) { dx32_tile<FMT_Q4_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_dx32_q6_k(DxArgs a) { dx32_tile<FMT_Q6_K>(a); }
 
+extern "C" __global__ __launch_bounds__(256) void rtq_dxv1_q4_0(DxArgs a) { dxv1_tile<FMT_Q4_0>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_dxv1_q8_0(DxArgs a) { dxv1_tile<FMT_Q8_0>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_dxv1_q4_k(DxArgs a) { dxv1_tile<FMT_Q4_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_dxv1_q6_k(DxArgs a) { dxv1_tile<FMT_Q6_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q4_0(DxArgs a) { dx16_tile<FMT_Q4_0>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q8_0(DxArgs a) { dx16_tile<FMT_Q8_0>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_dx16_q4_k(DxArgs a) { dx16_tile<FMT_Q4_K>(a); }

@@ -139,7 +139,8 @@ enum Kid {
   K_BWD_PREP,
   K_DX,          // + format
   K_DX16 = K_DX + F_COUNT,  // + format: t <= 16
-  K_DXW = K_DX16 + F_COUNT,  // + format: large t, 256-token tiles
+  K_DXV1 = K_DX16 + F_COUNT,  // + format: t == 1, f32 FMAs
+  K_DXW = K_DXV1 + F_COUNT,  // + format: large t, 256-token tiles
   K_DX32 = K_DXW + F_COUNT,  // + format: 32-token tiles on four-wave workgroups
   K_BWD_FINISH = K_DX32 + F_COUNT,
   K_BWD_FINISH16,  // 16 waves per workgroup: long token reductions of dA / dB
@@ -175,6 +176,7 @@ constexpr const char* kKernelNames[] = {
     "rtq_bwd_prep",
     "rtq_dx_q4_0",          "rtq_dx_q8_0",          "rtq_dx_q4_k",          "rtq_dx_q6_k",
     "rtq_dx16_q4_0",        "rtq_dx16_q8_0",        "rtq_dx16_q4_k",        "rtq_dx16_q6_k",
+    "rtq_dxv1_q4_0",        "rtq_dxv1_q8_0",        "rtq_dxv1_q4_k",        "rtq_dxv1_q6_k",
     "rtq_dxw_q4_0",         "rtq_dxw_q8_0",         "rtq_dxw_q4_k",         "rtq_dxw_q6_k",
     "rtq_dx32_q4_0",        "rtq_dx32_q8_0",        "rtq_dx32_q4_k",        "rtq_dx32_q6_k",
     "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_lora_grads",       "rtq_lora_grads16",     "rtq_lora_grads_t",     "rtq_lora_grads_t16",
@@ -226,6 +228,7 @@ struct rtq_ctx {
                       // whenever the format allows (RTQ_FWD_MM)
   int fwd_mmk = -1;   // K-quant ring forward (rtq_mmk*_*; RTQ_FWD_MMK): -1 automatic, 0 never, 1 / 2 the 64- /
                       // 32-token tiles whenever the shape allows
+  int dxv = 1;        // t == 1 dx on f32 FMAs (rtq_dxv1_*; RTQ_DXV=0: rtq_dx16_*)
   int gemvq = 1;      // one-launch GEMV for t <= 4 (rtq_gemvq*_*; RTQ_GEMVQ=0: activation kernel + GEMM)
   int gemvq_wpc = 0;  // its waves per CU (RTQ_GEMVQ_WPC; 0: automatic)
   int fwd_i8 = -1;    // int8-MFMA forwards (rtq_mmi8_*; RTQ_FWD_I8): -1 automatic (Q8_0 weights), 0 never,
@@ -751,6 +754,7 @@ struct DxPlan {
   bool tok16;
   bool wide;  // rtq_dxw_*: 256-token tiles (each dequantised weight element feeds 4x the MFMAs)
   bool t32;   // rtq_dx32_*: 32-token tiles on four-wave workgroups (same partial layout as rtq_dx_*)
+  bool v1;    // rtq_dxv1_*: t == 1 on f32 FMAs (partials as rtq_dx16_*)
   size_t part_floats;
 };
 DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
@@ -778,6 +782,12 @@ DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
   if (c->dx_splits > 0)
     splits = std::min<int64_t>(std::min<int64_t>(steps, p.tok16 ? 256 : (p.wide ? 64 : 16)), c->dx_splits);
   p.nps = cdiv(steps, splits) * 32;
+  p.v1 = t == 1 && c->dxv && (uint64_t)(w->Np / 16) * (w->Kp / 128) * 2048u < (1ull << 32);
+  if (p.v1) {  // about four four-wave workgroups per CU, each split at least 8 row groups of 16
+    const int64_t ngr = w->Np / 16;
+    const int64_t sv = std::max<int64_t>(1, std::min<int64_t>(cdiv(4 * c->cu_count, Kc), cdiv(ngr, 8)));
+    p.nps = cdiv(ngr, sv) * 16;
+  }
   p.splits = cdiv(w->Np, p.nps);
   p.part_floats = p.tok16 ? (size_t)(p.splits * t * w->cols) : (size_t)(p.splits * roundup(t, 64) * w->Kp);
   return p;
@@ -851,8 +861,8 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   }
   DxArgs xa{w->wq, w->wd, w->wsb, (int)w->Np, (int)w->Kp, dy, (int)t, N, K, (int)dp.nps, (int)dp.splits, part,
             lora ? hp : nullptr, lora ? gp : nullptr, (int)nhq, (int)ngq, (int)r, s, h, g, dymax, (int)ngq,
-            w->dx_wsc, w->dx_wunsc};
-  const int kid = (dp.tok16 ? K_DX16 : (dp.wide ? K_DXW : (dp.t32 ? K_DX32 : K_DX))) + fmt_index(w->type);
+            w->dx_wsc, w->dx_wunsc, w->wdr};
+  const int kid = (dp.v1 ? K_DXV1 : dp.tok16 ? K_DX16 : (dp.wide ? K_DXW : (dp.t32 ? K_DX32 : K_DX))) + fmt_index(w->type);
   set_work(c, w, t, 0, true);
   // t > 16: (token group, split) units of K-chunk workgroups, padded to a multiple of 8 (XCD order)
   const int64_t nmain = dp.tok16 ? (w->Kp / 128) * dp.splits
@@ -1075,6 +1085,7 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   if (const char* e = getenv("RTQ_FWD_I8")) c->fwd_i8 = std::min(std::max(atoi(e), -1), 1);
   if (const char* e = getenv("RTQ_FWD_MMK")) c->fwd_mmk = std::min(std::max(atoi(e), -1), 2);
   if (const char* e = getenv("RTQ_GEMVQ")) c->gemvq = atoi(e) ? 1 : 0;
+  if (const char* e = getenv("RTQ_DXV")) c->dxv = atoi(e) ? 1 : 0;
   if (const char* e = getenv("RTQ_GEMVQ_WPC")) c->gemvq_wpc = std::min(std::max(atoi(e), 0), 32);
   if (const char* e = getenv("RTQ_FWD_RG")) c->fwd_rg = atoi(e) == 2 ? 2 : 3;
   if (const char* e = getenv("RTQ_G64_MIN")) c->g64_min = atoi(e);

@@ -910,3 +910,37 @@ def test_gemvq_lm_head_t1(ctx, wtype):
     y, names = _ran(ctx, lambda: w.forward(x, t))
     assert all(nm.startswith("rtq_gemvq1") for nm in names), names
     assert rel_err(y, O.frozen_forward(wtype, blocks, n, k, x, nthreads=16)) <= TOL
+
+
+# ---------------------------------------------------------------- t = 1 dx on f32 FMAs
+@pytest.mark.parametrize("wtype,n,k", cases([(64, 128), (100, 96), (2048, 1024), (1000, 256), (4100, 768),
+                                             (151936, 1024)]))
+def test_dxv1_matches_oracle(ctx, wtype, n, k):
+    """rtq_dxv1_* (t = 1: codes as exact f16 values into f32 mixed-precision FMAs, k-group rows
+    added by DPP steps): against the oracle and, per element, the dense dy . W (1e-6 of the largest
+    |dx|); ragged N, K padded to a chunk, the LM head shape"""
+    blocks, _, dy = make(wtype, n, k, 1)
+    w = hip(ctx, wtype, blocks, n, k)
+    dx = np.zeros(k, np.float32)
+    _, names = _ran(ctx, lambda: w.backward_input(dy, 1, dx))
+    assert any(nm.startswith("rtq_dxv1") for nm in names), names
+    want = O.frozen_backward_input(wtype, blocks, n, k, dy, dx=np.zeros((1, k), np.float32), nthreads=16)
+    assert rel_err(dx, want) <= TOL
+    if n <= 4100:
+        dense = dy.astype(np.float64) @ _dense(wtype, blocks, n, k)
+        assert np.abs(dx - dense.reshape(-1)).max() <= 1e-6 * np.abs(dense).max()
+
+
+@pytest.mark.parametrize("wtype", FORMATS)
+def test_dxv1_lora_backward(ctx, wtype):
+    """Linear::backward at t = 1 through rtq_dxv1_* with LoRA r=16 (g . A added by the finish)"""
+    n, k, r = 512, 1024 if BLOCK[wtype] == 256 else 768, 16
+    blocks, x, dy = make(wtype, n, k, 1)
+    A, B = lora(n, k, r)
+    lin = rt.Linear("blk.0.attn_v", hip(ctx, wtype, blocks, n, k))
+    lin.lora = rt.Lora(r, 2.0 * r, A, B)
+    dx = lin.backward(x, dy, 1)
+    wdx, wga, wgb = O.linear_backward(wtype, blocks, n, k, x, dy, A=A, B=B, alpha=2.0 * r, nthreads=8)
+    assert rel_err(dx, wdx) <= TOL
+    assert rel_err(lin.lora.ga, wga) <= TOL
+    assert rel_err(lin.lora.gb, wgb) <= TOL
