@@ -3578,12 +3578,12 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
     f4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
     const f4* pp = reinterpret_cast<const f4*>(a.part + (int64_t)t * a.K + min(k0, a.K - 4));
     const int64_t sstride = (int64_t)a.T * a.K / 4;  // f4 per split
-    for (int s0 = g; s0 < a.nsplit; s0 += 16) {  // up to four loads in flight, summed in order
-      f4 v[4];
+    for (int s0 = g; s0 < a.nsplit; s0 += 64) {  // up to sixteen loads in flight, summed in order
+      f4 v[16];
 #pragma unroll
-      for (int q = 0; q < 4; q++) v[q] = pp[(int64_t)min(s0 + 4 * q, a.nsplit - 1) * sstride];
+      for (int q = 0; q < 16; q++) v[q] = pp[(int64_t)min(s0 + 4 * q, a.nsplit - 1) * sstride];
 #pragma unroll
-      for (int q = 0; q < 4; q++)
+      for (int q = 0; q < 16; q++)
         if (s0 + 4 * q < a.nsplit) sum += v[q];
     }
 #pragma unroll
