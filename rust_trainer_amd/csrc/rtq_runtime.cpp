@@ -624,10 +624,10 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   const bool kq = is_kquant(w->type);
   const bool w8 = !p.skinny && !isums && !kq && c->fwd_waves == 8;  // rtq_fwd_*_w8[r2]
   const int64_t gy = p.skinny ? p.Tp / 16 : cdiv(t, 16 * kFwdWideTT);
-  // the eight-wave forward with 32-row tiles where 48-row tiles would leave CUs without a workgroup
-  // and 32-row tiles would not (RTQ_FWD_RG: 2 or 3 forces one)
-  const bool rg2 = w8 && (c->fwd_rg == 2 || (c->fwd_rg < 0 && cdiv(w->Np / 16, 3) * gy < c->cu_count &&
-                                                cdiv(w->Np / 16, 2) * gy >= c->cu_count));
+  // the eight-wave forward with 32-row tiles wherever 48-row tiles would leave CUs without a
+  // workgroup (RTQ_FWD_RG: 2 or 3 forces one).  Measured at 256 tokens (one MI355X, per forward
+  // call): kv_proj 1024 x 1024 24.8 -> 20.3 us, down_proj 1024 x 3072 32.7 -> 24.4 (both still split K)
+  const bool rg2 = w8 && (c->fwd_rg == 2 || (c->fwd_rg < 0 && cdiv(w->Np / 16, 3) * gy < c->cu_count));
   const int64_t rg_per_wg = p.skinny ? kFwdSkinnyRG : (rg2 ? 2 : wide_rg(w->type));
   const int64_t gx = cdiv(w->Np / 16, rg_per_wg);
   // the large-grid kernel once its 128 x 128 tiles alone give a workgroup per CU, else its
