@@ -95,7 +95,9 @@ def test_head_rejects_bad_targets_and_handles_none(ctx):
 
 def test_head_device_api_marks_invalid_targets(ctx):
     """rtq_lm_head_d: out-of-range targets read nothing (logp NaN, hit 0, no gradient); the
-    valid targets match the host API."""
+    valid targets match the host API.  The host call has 2 targets and the device call 5, so their
+    logit products run on different kernels (t <= 4: rtq_gemvq4_*, whose Q4_0 sums add the
+    k-groups' scaled shares in another order): equal to 1e-5, not bit for bit."""
     import torch
 
     wtype, V, d, t = O.Q4_0, 4096, 256, 6
@@ -118,8 +120,9 @@ def test_head_device_api_marks_invalid_targets(ctx):
     assert np.isnan(lp[[1, 2, 3]]).all() and not hit[[1, 2, 3]].any()
     good = [0, 4]
     lp_h, dx_h, _ = rt.head(f, norm, x, [rt.Target(int(pos[i]), int(tok[i])) for i in good], wts[good])
-    np.testing.assert_array_equal(lp[good], lp_h)
-    np.testing.assert_array_equal(dxd.reshape(-1), dx_h)  # every other row cleared
+    np.testing.assert_allclose(lp[good], lp_h, rtol=1e-5, atol=0)
+    np.testing.assert_allclose(dxd.reshape(-1), dx_h, rtol=1e-5, atol=1e-5 * np.abs(dx_h).max())
+    assert not dxd.reshape(t, d)[[0, 2, 3, 4]].any()  # the rows without a valid target are cleared
     f.close()
 
 
