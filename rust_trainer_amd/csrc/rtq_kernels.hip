@@ -3144,9 +3144,18 @@ __device__ __forceinline__ void dx16_tile(const DxArgs& a) {
   {  // the tokens' scales while those loads are in flight: wave w reduces tokens w, w + 4, ..
     const int r1 = min(n0 + a.n_per_split, a.N);
     for (int t = w; t < a.T; t += 4) {
-      float mx = 0.0f;
       const float* row = a.dy + (int64_t)t * a.N;
-      for (int n = n0 + lane; n < r1; n += 64) mx = fmaxf(mx, fabsf(row[n]));
+      float m8[8];  // eight loads in flight per lane
+#pragma unroll
+      for (int u = 0; u < 8; u++) m8[u] = 0.0f;
+      for (int n = n0 + lane; n < r1; n += 512) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = n + 64 * u < r1 ? row[n + 64 * u] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; u++) m8[u] = fmaxf(m8[u], fabsf(v[u]));
+      }
+      float mx = fmaxf(fmaxf(fmaxf(m8[0], m8[1]), fmaxf(m8[2], m8[3])), fmaxf(fmaxf(m8[4], m8[5]), fmaxf(m8[6], m8[7])));
       mx = wave_max(mx);
       if (lane == 0) {
         int ex = 0;

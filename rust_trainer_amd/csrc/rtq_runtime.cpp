@@ -550,8 +550,10 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
     return enqueue_forward_dense(c, w, x, t, y, bias, la, lb, lora ? r : 0, s, ar, st);
   }
   // t <= 4: one launch that quantises x itself (codes, scales and h in LDS, at most 64 KB)
-  // (not where a later backward reads the LoRA-down partials: this kernel keeps none)
-  if (c->gemvq && t <= 4 && !isums && !sw && !hp_keep && (!lora || r <= RTQ_LDS_RANK)) {
+  // (not where a later backward reads the LoRA-down partials: this kernel keeps none; not with an
+  // adapter: every workgroup would form h = x A^T again, and the small adapted shapes are faster on
+  // the activation kernel's partials - q_proj 2048 x 1024 at t = 1: 33 against 12 us)
+  if (c->gemvq && t <= 4 && !isums && !sw && !hp_keep && !lora) {
     const int nt = t == 1 ? 1 : 4;
     const size_t lds = (size_t)nt * w->Kp + (size_t)nt * (w->Kp / 32) * 4 * (w->type == RTQ_TYPE_Q4_0 ? 5 : 2) +
                        (size_t)nt * RTQ_LDS_RANK * 4;
