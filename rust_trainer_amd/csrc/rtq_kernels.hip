@@ -282,36 +282,35 @@ __device__ __forceinline__ void rb_span(const RankBlocks& b, int r, int n0, int 
 //   P[t][j] = sum over k in [k0, k0 + 256) of S[t][k] * M[j * ldm + k],  t in [t0, t0 + 16), j < r
 // (h = x . A^T, src/linear.rs:85,106).  Written to out[(t * r + j) * pstride + pidx] (slice index
 // fastest, so a consumer sums a token's partials in slice order with a few wide loads).  Columns
-// beyond kend count as zero.
-__device__ __forceinline__ void lora_partial(const float* S, int T, int ks, const float* M, int ldm, int r, int k0,
-                                             int kend, int t0, float* out, int pstride, int pidx, float* sx,
-                                             float* sm, float* red) {
-  constexpr int LDX = RTQ_ACT_KQ + 1;
-  const int tid = threadIdx.x, tl = tid >> 4, sg = tid & 15, t = t0 + tl;
-  const int lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
-  {
-    float v[16];
-    const int kk = k0 + sg * 16;
-    load_seg(S + (int64_t)t * ks + kk, t < T && kk + 16 <= kend, v);
-    if (t < T && kk < kend && kk + 16 > kend) {  // ragged tail
+// beyond kend count as zero.  Thread (row tid / 16, segment tid % 16) holds 16 columns of one row
+// of S and of one rank tile of M.
+
+// thread (row tl, segment sg)'s 16 values of M's rank row j0 + tl, columns k0 + 16 sg .. (zero past
+// r and kend)
+__device__ __forceinline__ void lora_load_m(const float* M, int ldm, int r, int j0, int k0, int kend, float v[16]) {
+  const int tid = threadIdx.x, jr = j0 + (tid >> 4), kk = k0 + (tid & 15) * 16;
+  load_seg(M + (int64_t)jr * ldm + kk, jr < r && kk + 16 <= kend, v);
+  if (jr < r && kk < kend && kk + 16 > kend) {
 #pragma unroll
-      for (int i = 0; i < 16; i++) v[i] = kk + i < kend ? S[(int64_t)t * ks + kk + i] : 0.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; i++) sx[tl * LDX + sg * 16 + i] = v[i];
+    for (int i = 0; i < 16; i++) v[i] = kk + i < kend ? M[(int64_t)jr * ldm + kk + i] : 0.0f;
   }
+}
+
+// The product for this thread's S values sv (its row's columns k0 + 16 sg .., zero past T and kend)
+// and the first rank tile's M values mv (lora_load_m at j0 = 0, loaded by the caller so that they
+// travel with its own loads); each next tile's loads are issued before the current one is contracted.
+__device__ __forceinline__ void lora_partial_v(const float sv[16], float mv[16], int T, const float* M, int ldm,
+                                               int r, int k0, int kend, int t0, float* out, int pstride, int pidx,
+                                               float* sx, float* sm, float* red) {
+  constexpr int LDX = RTQ_ACT_KQ + 1;
+  const int tid = threadIdx.x, tl = tid >> 4, sg = tid & 15;
+  const int lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 16; i++) sx[tl * LDX + sg * 16 + i] = sv[i];
   for (int j0 = 0; j0 < r; j0 += 16) {
-    {  // A rows j0 .. j0+15, columns k0 .. k0+255: thread (row tl, segment sg)
-      float v[16];
-      const int jr = j0 + tl, kk = k0 + sg * 16;
-      load_seg(M + (int64_t)jr * ldm + kk, jr < r && kk + 16 <= kend, v);
-      if (jr < r && kk < kend && kk + 16 > kend) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) v[i] = kk + i < kend ? M[(int64_t)jr * ldm + kk + i] : 0.0f;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; i++) sm[tl * LDX + sg * 16 + i] = v[i];
-    }
+    for (int i = 0; i < 16; i++) sm[tl * LDX + sg * 16 + i] = mv[i];
+    if (j0 + 16 < r) lora_load_m(M, ldm, r, j0 + 16, k0, kend, mv);
     __syncthreads();
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -331,6 +330,20 @@ __device__ __forceinline__ void lora_partial(const float* S, int T, int ks, cons
   }
 }
 
+__device__ __forceinline__ void lora_partial(const float* S, int T, int ks, const float* M, int ldm, int r, int k0,
+                                             int kend, int t0, float* out, int pstride, int pidx, float* sx,
+                                             float* sm, float* red) {
+  const int tid = threadIdx.x, t = t0 + (tid >> 4), kk = k0 + (tid & 15) * 16;
+  float v[16], mv[16];
+  load_seg(S + (int64_t)t * ks + kk, t < T && kk + 16 <= kend, v);
+  if (t < T && kk < kend && kk + 16 > kend) {  // ragged tail
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = kk + i < kend ? S[(int64_t)t * ks + kk + i] : 0.0f;
+  }
+  lora_load_m(M, ldm, r, 0, k0, kend, mv);
+  lora_partial_v(v, mv, T, M, ldm, r, k0, kend, t0, out, pstride, pidx, sx, sm, red);
+}
+
 // LoRA-up input-gradient partial over one 256-row slice q of B (g = dy . B, src/linear.rs:111),
 // for TW tokens t0 .. t0+TW-1, by one 256-thread workgroup (f32 MFMA):
 //   gp[(q * T + t) * r + j] = sum over n in [256q, 256q + 256) of dy[t][n] * B[n][j]
@@ -345,6 +358,25 @@ __device__ __forceinline__ void lora_partial(const float* S, int T, int ks, cons
 //   TW = 16: wave w owns rows 64w .. 64w+63 of the 16 tokens; lane (li, g) loads rows
 //            64w + 16g .. +15, step u contracts row 64w + 16g + u; the four waves' sums are added
 //            in LDS in wave order (for grids too small to fill the chip with 64-token workgroups).
+// thread tid's row k0 + tid of B, ranks j0 .. j0+15 (clamped addresses; masked when staged)
+__device__ __forceinline__ void lora_load_b(const BwdPrepArgs& a, int k0, int j0, float bv[16]) {
+  const float* brow = a.B + (int64_t)min(k0 + (int)threadIdx.x, a.N - 1) * a.r;
+  if ((a.r & 3) == 0 && j0 + 16 <= a.r && (reinterpret_cast<uintptr_t>(a.B) & 15) == 0) {  // uniform
+    const f4* b4 = reinterpret_cast<const f4*>(brow + j0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const f4 e = b4[i];
+      bv[4 * i] = e.x;
+      bv[4 * i + 1] = e.y;
+      bv[4 * i + 2] = e.z;
+      bv[4 * i + 3] = e.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; i++) bv[i] = brow[min(j0 + i, a.r - 1)];
+  }
+}
+
 template <int TW>
 __device__ __forceinline__ void lora_up_partial(const BwdPrepArgs& a, int t0, int q, float* sb, float* red) {
   constexpr int KQ = RTQ_ACT_KQ, NU = TW == 64 ? 64 : 16;
@@ -371,6 +403,11 @@ __device__ __forceinline__ void lora_up_partial(const BwdPrepArgs& a, int t0, in
     }
   }
   const bool tok_ok = tw < a.T;  // wave-uniform
+  // B's first rank tile travels with dy; each next one is loaded before the current one is contracted
+  // (r = 0: the row maxima alone, B is null)
+  float bv[16];
+  bool any = a.r > 0 && rb_any(a.rb, k0, min(k0 + KQ, a.N), 0, min(16, a.r));  // uniform over the workgroup
+  if (any) lora_load_b(a, k0, 0, bv);
   if (a.dymax) {  // max |dy| of each token over the slice: lane, then the four lane groups (then the waves)
     float mx = 0.0f;
 #pragma unroll
@@ -389,19 +426,21 @@ __device__ __forceinline__ void lora_up_partial(const BwdPrepArgs& a, int t0, in
   }
   for (int j0 = 0; j0 < a.r; j0 += 16) {
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    const bool any = rb_any(a.rb, k0, min(k0 + KQ, a.N), j0, min(j0 + 16, a.r));  // uniform over the workgroup
-    if (any) {
-      {
-        const int k = k0 + tid;
-        const float* brow = a.B + (int64_t)min(k, a.N - 1) * a.r;
-        float* dst = sb + 16 * tid + 16 * (tid >> 6);
+    const bool cur = any;
+    if (cur) {
+      const int k = k0 + tid;
+      float* dst = sb + 16 * tid + 16 * (tid >> 6);
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-          const int j = j0 + i;
-          const float bv = brow[min(j, a.r - 1)];
-          dst[i] = (k < a.N && j < a.r && rb_keep(a.rb, k, j)) ? bv : 0.0f;
-        }
+      for (int i = 0; i < 16; i++) {
+        const int j = j0 + i;
+        dst[i] = (k < a.N && j < a.r && rb_keep(a.rb, k, j)) ? bv[i] : 0.0f;
       }
+    }
+    if (j0 + 16 < a.r) {
+      any = rb_any(a.rb, k0, min(k0 + KQ, a.N), j0 + 16, min(j0 + 32, a.r));
+      if (any) lora_load_b(a, k0, j0 + 16, bv);
+    }
+    if (cur) {
       __syncthreads();
       if (tok_ok) {
         const float* sg = sb + 16 * kl0 + 16 * (kl0 >> 6) + li;
@@ -424,7 +463,7 @@ __device__ __forceinline__ void lora_up_partial(const BwdPrepArgs& a, int t0, in
         }
     } else {  // thread (token tid / 16, rank tid % 16)
       const int tt = t0 + (tid >> 4), j = j0 + (tid & 15);
-      const float ps = any ? (red[tid] + red[256 + tid]) + (red[512 + tid] + red[768 + tid]) : 0.0f;
+      const float ps = cur ? (red[tid] + red[256 + tid]) + (red[512 + tid] + red[768 + tid]) : 0.0f;
       if (tt < a.T && j < a.r) a.gp[((int64_t)q * a.T + tt) * a.r + j] = ps;
     }
   }
@@ -476,8 +515,8 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
   const int k0 = blockIdx.y * KQ;
   {
     const int kk = k0 + sg * 16;  // first column of this thread's segment
-    float v[16];
-    if (a.sg) {  // uniform: v = silu(g) * u, written to x for the LoRA partial below and the backward
+    float v[16], mv[16];
+    if (a.sg) {  // uniform: v = silu(g) * u, written to x for the backward
       float gv[16], uv[16];
       load_seg(a.sg + (int64_t)t * a.ldsg + kk, t < a.T && kk < a.K, gv);
       load_seg(a.su + (int64_t)t * a.ldsg + kk, t < a.T && kk < a.K, uv);
@@ -491,6 +530,7 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
     } else {
       load_seg(a.x + (int64_t)t * a.K + kk, t < a.T && kk < a.K, v);  // K % 32 == 0: all in or all out
     }
+    if (a.A) lora_load_m(a.A, a.K, a.r, 0, k0, a.K, mv);  // uniform; in flight during the quantisation
     _Float16 q[16];  // codes: exact small integers
     float dstore;    // the block scale as the dot products use it
     if (!QK) {
@@ -570,6 +610,10 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
         a.xg[(int64_t)(b * 2 + 1) * 16 + t] = real ? -a.gbias * csum : 0.0f;
       }
     }
+    // LoRA-down partial of these columns from the values in registers (zero past T and K, like the
+    // codes; quarters beyond K write zero partials)
+    if (a.A)  // uniform
+      lora_partial_v(v, mv, a.T, a.A, a.K, a.r, k0, a.K, t0, a.hp, gridDim.y, blockIdx.y, sx, sa, red);
   }
   if (a.zero_y && blockIdx.y == 0) {
     for (int tt = 0; tt < 16; tt++) {
@@ -578,8 +622,6 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
         for (int n = tid; n < a.N; n += 256) a.zero_y[(int64_t)ty * a.N + n] = 0.0f;
     }
   }
-  if (a.A)  // uniform; quarters beyond K write zero partials
-    lora_partial(a.x, a.T, a.K, a.A, a.K, a.r, k0, a.K, t0, a.hp, gridDim.y, blockIdx.y, sx, sa, red);
 }
 
 extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_0(ActArgs a) { act_prep<false>(a); }
