@@ -3608,15 +3608,17 @@ __device__ __forceinline__ void lora_grad_tile(const LoraGradArgs& a, int b, flo
 
 // One grid, three kinds of workgroups: gb tiles, ga tiles (lora_grad_tile), then dx: one wave per
 // 16 x 16 quarter of a dx-kernel fragment (the dx kernel's partial layout) or per token and 64
-// columns (row-major partials).  NW = 4, or 16 for long token ranges.
-template <int NW, int E>
+// columns (row-major partials).  NW = 4, or 16 for long token ranges.  DXO: dx workgroups alone
+// (n_gb = n_ga = 0: dA / dB deferred or no adapter) over at most four splits, loading four
+// partials at a time (the same split order; a quarter of the load registers).
+template <int NW, int E, bool DXO = false>
 __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
-  __shared__ float red[NW * 16 * E * 17];
+  __shared__ float red[DXO ? 1 : NW * 16 * E * 17];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
   const int b = blockIdx.x;
-  if (b < a.n_gb) {
+  if (!DXO && b < a.n_gb) {
     lora_grad_tile<NW, E, true>(a, b, red);
-  } else if (b < a.n_gb + a.n_ga) {
+  } else if (!DXO && b < a.n_gb + a.n_ga) {
     lora_grad_tile<NW, E, false>(a, b - a.n_gb, red);
   } else if (a.part_rows) {
     // dx from row-major partials: wave per (token t, 64 columns); lane (k4 = li, split subset g)
@@ -3629,12 +3631,13 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
     f4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
     const f4* pp = reinterpret_cast<const f4*>(a.part + (int64_t)t * a.K + min(k0, a.K - 4));
     const int64_t sstride = (int64_t)a.T * a.K / 4;  // f4 per split
-    for (int s0 = g; s0 < a.nsplit; s0 += 64) {  // up to sixteen loads in flight, summed in order
-      f4 v[16];
+    constexpr int PRL = DXO ? 1 : 16;  // loads in flight per lane, summed in order
+    for (int s0 = g; s0 < a.nsplit; s0 += 4 * PRL) {
+      f4 v[PRL];
 #pragma unroll
-      for (int q = 0; q < 16; q++) v[q] = pp[(int64_t)min(s0 + 4 * q, a.nsplit - 1) * sstride];
+      for (int q = 0; q < PRL; q++) v[q] = pp[(int64_t)min(s0 + 4 * q, a.nsplit - 1) * sstride];
 #pragma unroll
-      for (int q = 0; q < 16; q++)
+      for (int q = 0; q < PRL; q++)
         if (s0 + 4 * q < a.nsplit) sum += v[q];
     }
 #pragma unroll
@@ -3700,7 +3703,18 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
 #pragma unroll
     for (int jj = 0; jj < MAXJ; jj++)
       if (jj < nj) ga_ops(jj, gv[jj], av[jj]);
-    constexpr int MAXS = NW == 16 ? 8 : 16;  // partials loaded at once; more splits are summed MAXS at a time
+    // SwiGLU's g, u of these outputs (accumulate off, 4-wave finish only), loaded with the partials
+    const bool sw = NW == 4 && a.swg;  // uniform
+    float swgv[4], swuv[4];
+    if (sw) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int64_t o = (int64_t)min(t0 + 4 * g + i, a.T - 1) * a.swld + min(kcol, a.K - 1);
+        swgv[i] = a.swg[o];
+        swuv[i] = a.swu[o];
+      }
+    }
+    constexpr int MAXS = DXO ? 4 : NW == 16 ? 8 : 16;  // partials loaded at once; more splits are summed MAXS at a time
     f4 ps = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int c0 = 0; c0 < a.nsplit; c0 += MAXS) {
       f4 v[MAXS];
@@ -3725,22 +3739,15 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
       for (int u = 0; u < 4; u++) ga = mfma_f32(gq[u], aq[u], ga);
     }
     if (kcol < a.K) {
-      if (NW == 4 && a.swg) {  // SwiGLU backward of dh = the sum (accumulate off, 4-wave finish only); g, u loaded together
-        float gv[4], uv[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int64_t o = (int64_t)min(t0 + 4 * g + i, a.T - 1) * a.swld + kcol;
-          gv[i] = a.swg[o];
-          uv[i] = a.swu[o];
-        }
+      if (sw) {  // SwiGLU backward of dh = the sum
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const int t = t0 + 4 * g + i;
           if (t < a.T) {
             const float dh = a.g ? ps[i] + ga[i] : ps[i];
             const int64_t o = (int64_t)t * a.swld + kcol;
-            a.swdg[o] = (dh * uv[i]) * rtq_silu_grad(gv[i]);
-            a.swdu[o] = dh * rtq_silu(gv[i]);
+            a.swdg[o] = (dh * swuv[i]) * rtq_silu_grad(swgv[i]);
+            a.swdu[o] = dh * rtq_silu(swgv[i]);
             if (a.sw_keep) a.dx[(int64_t)t * a.K + kcol] = dh;
           }
         }
@@ -3795,6 +3802,7 @@ extern "C" __global__ __launch_bounds__(256) void rtq_lora_grads_t(LoraGradTable
 extern "C" __global__ __launch_bounds__(1024) void rtq_lora_grads_t16(LoraGradTable t) { lora_grads_t<16>(t); }
 extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a) { bwd_finish<4, 4>(a); }
 extern "C" __global__ __launch_bounds__(1024) void rtq_bwd_finish16(LoraGradArgs a) { bwd_finish<16, 4>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish_dx(LoraGradArgs a) { bwd_finish<4, 4, true>(a); }
 
 
 // ============================================================== trainer-native weights

@@ -144,6 +144,7 @@ enum Kid {
   K_DX32 = K_DXW + F_COUNT,  // + format: 32-token tiles on four-wave workgroups
   K_BWD_FINISH = K_DX32 + F_COUNT,
   K_BWD_FINISH16,  // 16 waves per workgroup: long token reductions of dA / dB
+  K_BWD_FINISH_DX,  // dx workgroups alone (no dA / dB tiles in the grid)
   K_LORA_GRADS,    // dA / dB of several linears in one launch (4 / 16 waves per workgroup)
   K_LORA_GRADS16,
   K_LORA_GRADS_T,    // the same from a device job table
@@ -179,7 +180,7 @@ constexpr const char* kKernelNames[] = {
     "rtq_dxv1_q4_0",        "rtq_dxv1_q8_0",        "rtq_dxv1_q4_k",        "rtq_dxv1_q6_k",
     "rtq_dxw_q4_0",         "rtq_dxw_q8_0",         "rtq_dxw_q4_k",         "rtq_dxw_q6_k",
     "rtq_dx32_q4_0",        "rtq_dx32_q8_0",        "rtq_dx32_q4_k",        "rtq_dx32_q6_k",
-    "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_lora_grads",       "rtq_lora_grads16",     "rtq_lora_grads_t",     "rtq_lora_grads_t16",
+    "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_bwd_finish_dx",    "rtq_lora_grads",       "rtq_lora_grads16",     "rtq_lora_grads_t",     "rtq_lora_grads_t16",
     "rtq_dense_rows",       "rtq_dense_bias",
     "rtq_head_norm",        "rtq_head_max",         "rtq_head_sum",         "rtq_head_grad",
     "rtq_head_norm_bwd",
@@ -895,8 +896,9 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
       fa.swld = defer->sw->ld;
       fa.sw_keep = defer->sw->keep_dh ? 1 : 0;
     }
-    return launch(c, K_BWD_FINISH, dim3((unsigned)fa.n_dx), dim3(256), st, fa);
+    return launch(c, dp.splits <= 4 ? K_BWD_FINISH_DX : K_BWD_FINISH, dim3((unsigned)fa.n_dx), dim3(256), st, fa);
   }
+  if (!lora) return launch(c, dp.splits <= 4 ? K_BWD_FINISH_DX : K_BWD_FINISH, dim3((unsigned)fa.n_dx), dim3(256), st, fa);
   return launch(c, nw == 16 ? K_BWD_FINISH16 : K_BWD_FINISH, dim3((unsigned)(fa.n_gb + fa.n_ga + fa.n_dx)),
                 dim3(64 * nw), st, fa);
 }
