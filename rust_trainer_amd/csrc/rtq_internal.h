@@ -68,6 +68,23 @@ rtq_status rtq_linear_forward_keep_d(rtq_ctx* c, const rtq_weight* w, const floa
 rtq_status rtq_linear_forward_swiglu_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
                                        const RankBlocks* rb, const float* g, const float* u, int64_t ldg,
                                        float* x_out, int64_t t, float* y, float* hp_keep, void* stream);
+// rtq_linear_forward_keep_d of x = RMSNorm(a (+ b)) (src/ops.rs:14-35: (x / rms) (w + off), the
+// one-wave row order of the model's norm kernel): the activation kernel forms the rows and writes
+// them to x_out [t x cols], a + b to h (with b) and 1 / rms to inv [t].  Quantised weights with
+// cols % 256 == 0, cols <= 1024 and 16-byte aligned rows (else RTQ_ERR_UNSUPPORTED: the caller
+// normalises first).
+struct NormIn {
+  const float* a;
+  const float* b;  // or null
+  float* h;        // a + b (with b)
+  const float* w;
+  float* inv;
+  float eps, off;
+};
+bool rtq_norm_fusable(const rtq_weight* w, const NormIn& n, const float* x_out);
+rtq_status rtq_linear_forward_norm_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
+                                     const RankBlocks* rb, const NormIn* n, float* x_out, int64_t t, float* y,
+                                     float* hp_keep, void* stream);
 // rtq_linear_backward_d for a block-diagonal adapter over row-concatenated weights (rb; null: a
 // plain adapter): gb and g = s dy.B only inside rb's blocks (gb outside them is left untouched).
 // Quantised weights only; a dense weight computes every pair (the caller clears gb outside the

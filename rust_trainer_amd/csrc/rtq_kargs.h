@@ -83,6 +83,15 @@ struct ActArgs {
   // 1: the codes go to xq as int8 fragments of rtq_mmi8_* ([Tp/32][Kc][4][64] x 16 bytes, lane l:
   // token l % 32, the block's codes of k-groups 2 (l / 32) and 2 (l / 32) + 1), not f16 ones
   int xq_i8;
+  // or null: the activation is RMSNorm of na (+ nb) (src/ops.rs:14-35) with weight nw (+ noff), in
+  // the order of rtq_m_rmsnorm's one-wave rows (K % 256 == 0, K <= 1024), formed here; the rows go
+  // to x (then an output), na + nb to nh (with nb), 1 / rms to ninv (rows [T])
+  const float* na;
+  const float* nb;
+  float* nh;
+  const float* nw;
+  float* ninv;
+  float neps, noff;
 };
 
 // ---------------------------------------------------------------- trainer-native weights

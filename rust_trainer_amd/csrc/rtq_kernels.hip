@@ -516,7 +516,71 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
   {
     const int kk = k0 + sg * 16;  // first column of this thread's segment
     float v[16], mv[16];
-    if (a.sg) {  // uniform: v = silu(g) * u, written to x for the backward
+    if (a.na) {  // uniform: v = RMSNorm rows, in the order of rtq_m_rmsnorm's one-wave rows
+      // wave w normalises rows t0 + 4w .. t0 + 4w + 3 whole (lane l: float4 columns 4l + 256i, i <
+      // K / 256), then writes quarter blockIdx.y of each (x, nh) and passes it through LDS (sx) to
+      // the thread layout below; quarters beyond K give zeros.  The 1 / rms is written once.
+      // every load issued before any is used: addresses clamped into the rows (no branches between
+      // the loads), out-of-range values replaced by zeros afterwards
+      const int lane = tid & 63, w = tid >> 6, nv = a.K / 256, qy = blockIdx.y;
+      const f4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+      const bool has_b = a.nb != nullptr;
+      const float* pb = has_b ? a.nb : a.na;
+      f4 wv[4], xv[4][4], bv[4][4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) wv[i] = *reinterpret_cast<const f4*>(a.nw + 4 * lane + 256 * min(i, nv - 1));
+#pragma unroll
+      for (int rr = 0; rr < 4; rr++) {
+        const int64_t ro = (int64_t)min(t0 + 4 * w + rr, a.T - 1) * a.K + 4 * lane;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          xv[rr][i] = *reinterpret_cast<const f4*>(a.na + ro + 256 * min(i, nv - 1));
+          bv[rr][i] = *reinterpret_cast<const f4*>(pb + ro + 256 * min(i, nv - 1));
+        }
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; rr++) {
+        const bool rin = t0 + 4 * w + rr < a.T;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const float xs = has_b ? xv[rr][i][e] + bv[rr][i][e] : xv[rr][i][e];
+            xv[rr][i][e] = (rin && i < nv) ? xs : 0.0f;
+          }
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; rr++) {
+        const int row = t0 + 4 * w + rr;
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (i < nv)
+#pragma unroll
+            for (int e = 0; e < 4; e++) s = s + xv[rr][i][e] * xv[rr][i][e];
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+        const float ir = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(s, (float)a.K) + a.neps));
+        f4 y = z4;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (i < nv && i == qy) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[e] = (xv[rr][i][e] * ir) * (wv[i][e] + a.noff);
+            if (row < a.T) {
+              const int64_t o = (int64_t)row * a.K + 256 * i + 4 * lane;
+              if (a.nb) *reinterpret_cast<f4*>(a.nh + o) = xv[rr][i];
+              *reinterpret_cast<f4*>(const_cast<float*>(a.x) + o) = y;
+            }
+          }
+        if (qy == 0 && lane == 0 && row < a.T) a.ninv[row] = ir;
+#pragma unroll
+        for (int e = 0; e < 4; e++) sx[(4 * w + rr) * LDX + 4 * lane + e] = y[e];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 16; i++) v[i] = sx[tl * LDX + sg * 16 + i];
+    } else if (a.sg) {  // uniform: v = silu(g) * u, written to x for the backward
       float gv[16], uv[16];
       load_seg(a.sg + (int64_t)t * a.ldsg + kk, t < a.T && kk < a.K, gv);
       load_seg(a.su + (int64_t)t * a.ldsg + kk, t < a.T && kk < a.K, uv);

@@ -128,6 +128,9 @@ struct rtq_model {
   std::vector<float*> lg_h, lg_g;  // slot (layer if deferring, else 0) * lg_groups + group
   int64_t lg_groups = 0;
   bool lora_batch = true;
+  // norm_fuse: a block's two RMSNorms formed by the next linear's activation kernel where the shape
+  // allows (RTQ_NORM_FUSE=0 at load time: the norm kernel, then the linear)
+  bool norm_fuse = true;
   // defer_lg: every block's dA / dB left to one launch after the backward (their inputs kept per
   // layer: h / g slots per (layer, group), Cache gradient buffers), where the activations are kept
   // and the per-layer gradients fit a budget; RTQ_LORA_DEFER=0 at load time keeps per-block launches.
@@ -380,6 +383,22 @@ rtq_status lin_fwd(rtq_model* m, const Group& l, const float* x, int64_t t, floa
   const RankBlocks rb = rank_blocks(l);
   return rtq_linear_forward_keep_d(m->ctx, l.w, l.bias, l.rank > 0 ? &lv : nullptr, &rb, x, t, y, l.hpk,
                                    stream_of(m));
+}
+
+// n = rmsnorm(a (+ b)) (h = a + b, inv = 1 / rms), then y = the linear of n: the linear's activation
+// kernel forms n where the shape allows (the same bits as the norm kernel's one-wave rows), else
+// the norm kernel runs first.  n, h and inv are written either way.
+rtq_status lin_fwd_norm(rtq_model* m, const Group& l, const float* a, const float* b, float* h, const float* nw,
+                        float* n, float* inv, int64_t t, float* y) {
+  const NormIn ni{a, b, h, nw, inv, m->cfg.rms_eps, m->cfg.norm_offset};
+  if (m->norm_fuse && rtq_norm_fusable(l.w, ni, n)) {
+    const rtq_lora lv = lora_view(l);
+    const RankBlocks rb = rank_blocks(l);
+    return rtq_linear_forward_norm_d(m->ctx, l.w, l.bias, l.rank > 0 ? &lv : nullptr, &rb, &ni, n, t, y, l.hpk,
+                                     stream_of(m));
+  }
+  M_TRY(k_norm(m, a, b, h, nw, n, inv, t, m->cfg.n_embd, 0));
+  return lin_fwd(m, l, n, t, y);
 }
 
 // the down projection of SwiGLU's hm = silu(g) * u (src/model.rs:124-125): quantised weights form hm
@@ -1077,15 +1096,15 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, float* x, float* y, boo
   Cache& k = m->cache[m->ckpt ? 0 : (size_t)l];
   const int64_t d = c.n_embd, nh = c.n_head, nkv = c.n_head_kv, hd = c.head_dim, grp = nh / nkv;
   const int64_t qd = nh * hd, kd = nkv * hd;
-  if (add_in)  // x = h + mlp of block l - 1 (src/model.rs:196), n1 = rmsnorm(x)
-    M_TRY(k_norm(m, m->cache[m->ckpt ? 0 : (size_t)(l - 1)].h, m->f, x, L.attn_norm, k.n1, k.inv1, t, d, 0));
-  else
-    M_TRY(k_norm(m, x, nullptr, nullptr, L.attn_norm, k.n1, k.inv1, t, d, 0));
+  // x = h + mlp of block l - 1 (src/model.rs:196), n1 = rmsnorm(x)
+  const float* in_a = add_in ? m->cache[m->ckpt ? 0 : (size_t)(l - 1)].h : x;
+  const float* in_b = add_in ? m->f : nullptr;
+  float* in_h = add_in ? x : nullptr;
   const QkvView qv = qkv_view(m, L, k.qkv, t);
   if (L.qkv_fused) {
-    M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LQ]], k.n1, t, k.qkv));
+    M_TRY(lin_fwd_norm(m, L.groups[(size_t)L.gi[LQ]], in_a, in_b, in_h, L.attn_norm, k.n1, k.inv1, t, k.qkv));
   } else {
-    M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LQ]], k.n1, t, qv.q));
+    M_TRY(lin_fwd_norm(m, L.groups[(size_t)L.gi[LQ]], in_a, in_b, in_h, L.attn_norm, k.n1, k.inv1, t, qv.q));
     M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LK]], k.n1, t, qv.k));
     M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LV]], k.n1, t, qv.v));
   }
@@ -1140,14 +1159,14 @@ rtq_status block_forward(rtq_model* m, int l, int64_t t, float* x, float* y, boo
   }
   if (seq) M_TRY(rtq_model_launch(m->ctx, KM_SEQ_SCATTER, dim3((unsigned)t), dim3(256), stream_of(m), &sq));
   M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LO]], k.o, t, m->mo));
-  M_TRY(k_norm(m, x, m->mo, k.h, L.ffn_norm, k.n2, k.inv2, t, d, 0));  // h = x + attn, n2 = rmsnorm(h)
   float *g, *u;
   int64_t ldg;
   gu_view(m, L, k.gu, t, &g, &u, &ldg);
+  // h = x + attn, n2 = rmsnorm(h)
   if (L.gu_fused) {
-    M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LGATE]], k.n2, t, k.gu));
+    M_TRY(lin_fwd_norm(m, L.groups[(size_t)L.gi[LGATE]], x, m->mo, k.h, L.ffn_norm, k.n2, k.inv2, t, k.gu));
   } else {
-    M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LGATE]], k.n2, t, g));
+    M_TRY(lin_fwd_norm(m, L.groups[(size_t)L.gi[LGATE]], x, m->mo, k.h, L.ffn_norm, k.n2, k.inv2, t, g));
     M_TRY(lin_fwd(m, L.groups[(size_t)L.gi[LUP]], k.n2, t, u));
   }
   M_TRY(lin_fwd_swiglu(m, L.groups[(size_t)L.gi[LDOWN]], g, u, ldg, k.hm, t, m->f));
@@ -1551,6 +1570,7 @@ rtq_status rtq_model_from_gguf(rtq_ctx* ctx, const rtq_gguf* g, rtq_model** out)
   if (const char* e = getenv("RTQ_ATTN_F32")) m->attn_f32 = atoi(e) != 0;
   if (const char* e = getenv("RTQ_ATTN_ITEMS")) m->attn_items = std::max(0, atoi(e));
   if (const char* e = getenv("RTQ_LORA_BATCH")) m->lora_batch = atoi(e) != 0;
+  if (const char* e = getenv("RTQ_NORM_FUSE")) m->norm_fuse = atoi(e) != 0;
   if (const char* e = getenv("RTQ_LORA_DEFER")) m->lora_defer = atoi(e) != 0;
   if (const char* e = getenv("RTQ_STEP_GRAPH")) m->graph_on = atoi(e) != 0;
   m->ctx = ctx;

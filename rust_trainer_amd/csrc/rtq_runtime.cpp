@@ -542,19 +542,36 @@ struct SwiGluIn {
 rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int64_t t, float* y, const float* bias,
                            const float* la, const float* lb, int64_t r, float s, int32_t* isums, Arena& ar,
                            hipStream_t st, float* hp_keep = nullptr, const RankBlocks* rb = nullptr,
-                           const SwiGluIn* sw = nullptr) {
+                           const SwiGluIn* sw = nullptr, const NormIn* nf = nullptr) {
   if (t <= 0) return RTQ_OK;
   const bool lora = la && lb && r > 0;
   const RankBlocks rbv = lora && rb ? *rb : RankBlocks{};
   if (is_dense(w->type)) {
-    if (sw) return fail(RTQ_ERR_UNSUPPORTED, "internal: SwiGLU input of a dense weight");
+    if (sw || nf) return fail(RTQ_ERR_UNSUPPORTED, "internal: SwiGLU / norm input of a dense weight");
     return enqueue_forward_dense(c, w, x, t, y, bias, la, lb, lora ? r : 0, s, ar, st);
   }
+  // the activation kernel's inputs: x, or SwiGLU's g / u, or RMSNorm's a (+ b) (x then an output)
+  auto act_in = [&](ActArgs& aa) {
+    if (sw) {
+      aa.sg = sw->g;
+      aa.su = sw->u;
+      aa.ldsg = (int)sw->ld;
+    }
+    if (nf) {
+      aa.na = nf->a;
+      aa.nb = nf->b;
+      aa.nh = nf->h;
+      aa.nw = nf->w;
+      aa.ninv = nf->inv;
+      aa.neps = nf->eps;
+      aa.noff = nf->off;
+    }
+  };
   // t <= 4: one launch that quantises x itself (codes, scales and h in LDS, at most 64 KB)
   // (not where a later backward reads the LoRA-down partials: this kernel keeps none; not with an
   // adapter: every workgroup would form h = x A^T again, and the small adapted shapes are faster on
   // the activation kernel's partials - q_proj 2048 x 1024 at t = 1: 33 against 12 us)
-  if (c->gemvq && t <= 4 && !isums && !sw && !hp_keep && !lora) {
+  if (c->gemvq && t <= 4 && !isums && !sw && !nf && !hp_keep && !lora) {
     const int nt = t == 1 ? 1 : 4;
     const size_t lds = (size_t)nt * w->Kp + (size_t)nt * (w->Kp / 32) * 4 * (w->type == RTQ_TYPE_Q4_0 ? 5 : 2) +
                        (size_t)nt * RTQ_LDS_RANK * 4;
@@ -588,11 +605,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
     const float gbias = w->type == RTQ_TYPE_Q4_0 ? 1032.0f : (w->type == RTQ_TYPE_Q8_0 ? 1152.0f : 0.0f);
     ActArgs aa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xq, xd, xg, gbias, lora ? la : nullptr, (int)r, hp,
                gp.gy > 1 ? y : nullptr, (int)w->rows, nullptr};
-    if (sw) {
-      aa.sg = sw->g;
-      aa.su = sw->u;
-      aa.ldsg = (int)sw->ld;
-    }
+    act_in(aa);
     RTQ_TRY(launch(c, is_kquant(w->type) ? K_ACT_PREP_K : K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp),
                    dim3(256), st, aa));
     FwdArgs fa{};
@@ -686,11 +699,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   ActArgs aa{x, (int)t, (int)w->cols, (int)p.Tp, (int)w->Kp, xq, xd, nullptr, 0.0f, lora ? la : nullptr, (int)r, hp,
              ks > 1 ? y : nullptr, (int)w->rows, xdh};
-  if (sw) {
-    aa.sg = sw->g;
-    aa.su = sw->u;
-    aa.ldsg = (int)sw->ld;
-  }
+  act_in(aa);
   aa.xq_i8 = mmi8 ? 1 : 0;
   RTQ_TRY(launch(c, kq ? K_ACT_PREP_K : K_ACT_PREP, dim3((unsigned)(p.Tp / 16), (unsigned)p.nhp), dim3(256), st, aa));
   FwdArgs fa{};
@@ -1890,6 +1899,35 @@ rtq_status rtq_linear_forward_swiglu_d(rtq_ctx* c, const rtq_weight* w, const fl
   const SwiGluIn sw{g, u, ldg};
   return enqueue_forward(c, w, x_out, t, y, bias, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, nullptr, ar,
                          st, hp_keep, rb, &sw);
+}
+
+bool rtq_norm_fusable(const rtq_weight* w, const NormIn& n, const float* x_out) {
+  return w && !is_dense(w->type) && w->cols % 256 == 0 && w->cols <= 1024 && n.a && n.w && n.inv && x_out &&
+         (!n.b || n.h) && ((uintptr_t)n.a | (uintptr_t)n.b | (uintptr_t)n.h | (uintptr_t)n.w | (uintptr_t)x_out) % 16 == 0;
+}
+
+rtq_status rtq_linear_forward_norm_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,
+                                     const RankBlocks* rb, const NormIn* n, float* x_out, int64_t t, float* y,
+                                     float* hp_keep, void* stream) {
+  RTQ_TRY(check_weight(c, w));
+  RTQ_TRY(check_t(t));
+  RTQ_TRY(check_blocks(w, lora, rb));
+  if (!n || !rtq_norm_fusable(w, *n, x_out))
+    return fail(RTQ_ERR_UNSUPPORTED, "norm input: quantised weights, cols %% 256 == 0 and <= 1024, 16-byte aligned rows");
+  bool on;
+  int64_t r;
+  float s;
+  RTQ_TRY(check_lora(lora, &on, &r, &s));
+  if (t > 0 && !y) return fail(RTQ_ERR_INVALID, "null y");
+  if (hp_keep && rtq_lora_partial_floats(w, t, on ? r : 0) == 0) hp_keep = nullptr;
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = (hipStream_t)stream;
+  FwdPlan p = fwd_plan(w, t, on ? r : 0);
+  RTQ_TRY(ensure_ws(c, fwd_ws_bytes(p)));
+  Arena ar{(char*)c->ws, c->ws_bytes, 0};
+  return enqueue_forward(c, w, x_out, t, y, bias, on ? lora->a : nullptr, on ? lora->b : nullptr, r, s, nullptr, ar,
+                         st, hp_keep, rb, nullptr, n);
 }
 
 rtq_status rtq_linear_forward_ws_d(rtq_ctx* c, const rtq_weight* w, const float* bias, const rtq_lora* lora,

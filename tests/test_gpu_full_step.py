@@ -8,7 +8,9 @@ per-op parity of one block at this shape is in tests/test_gpu_block_ops.py):
 * activation recomputation changes nothing beyond f32 rounding (tests/gradcheck.rs:199-212:
   log-probs and every adapter gradient within 1e-5 x max(|a|, 1));
 * a step replayed from the captured HIP graph equals the same step run eagerly, bit for bit;
-* the same step repeated reproduces every bit (no atomics in the step's reductions).
+* the same step repeated reproduces every bit (no atomics in the step's reductions);
+* the block's RMSNorms formed inside the next linear's activation kernel give the bits of the norm
+  kernel run first (a model loaded with RTQ_NORM_FUSE=0).
 """
 import numpy as np
 import pytest
@@ -75,6 +77,15 @@ def test_config2_full_step_properties(ctx, monkeypatch):
     for a, b in zip(gr_e, gr):
         np.testing.assert_array_equal(a, b)
     eager.close()
+    monkeypatch.setenv("RTQ_NORM_FUSE", "0")
+    unfused = load(graph=False)
+    monkeypatch.delenv("RTQ_NORM_FUSE")
+    lp_u, hits_u, gr_u = step(unfused)
+    np.testing.assert_array_equal(lp_u, lp)
+    assert hits_u == hits
+    for a, b in zip(gr_u, gr):
+        np.testing.assert_array_equal(a, b)
+    unfused.close()
     model.checkpointing = True
     lp_c, hits_c, gr_c = step(model)
     assert model.checkpointing is True and hits_c == hits
