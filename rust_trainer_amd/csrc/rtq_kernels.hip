@@ -516,6 +516,7 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
   {
     const int kk = k0 + sg * 16;  // first column of this thread's segment
     float v[16], mv[16];
+    if (a.A) lora_load_m(a.A, a.K, a.r, 0, k0, a.K, mv);  // uniform; in flight during the activation work
     if (a.na) {  // uniform: v = RMSNorm rows, in the order of rtq_m_rmsnorm's one-wave rows
       // wave w normalises rows t0 + 4w .. t0 + 4w + 3 whole (lane l: float4 columns 4l + 256i, i <
       // K / 256), then writes quarter blockIdx.y of each (x, nh) and passes it through LDS (sx) to
@@ -594,7 +595,6 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
     } else {
       load_seg(a.x + (int64_t)t * a.K + kk, t < a.T && kk < a.K, v);  // K % 32 == 0: all in or all out
     }
-    if (a.A) lora_load_m(a.A, a.K, a.r, 0, k0, a.K, mv);  // uniform; in flight during the quantisation
     _Float16 q[16];  // codes: exact small integers
     float dstore;    // the block scale as the dot products use it
     if (!QK) {
