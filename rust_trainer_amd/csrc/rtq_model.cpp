@@ -1025,9 +1025,19 @@ rtq_status lora_grads_all(rtq_model* m) {
     if (n == 0) continue;
     const int ji = (int)jobs.size();
     jobs.push_back(j);
-    for (int b = 0; b < n; b++) {
-      map.push_back(ji);
-      map.push_back(b);
+    // tile b = row tile * jt + rank tile: the jt rank tiles of a row tile (which read the same dy or
+    // x rows) placed 8 workgroups apart, so that they run on one XCD and share its L2 (workgroups
+    // go to the 8 XCDs in turn): per section (gb, then ga), blocks of 8 row tiles, rank tile by
+    // rank tile.  Each tile writes its own outputs: the order changes no result.
+    const int jt = (j.r + 15) / 16;
+    for (int sec = 0; sec < 2; sec++) {
+      const int b0 = sec ? j.n_gb : 0, nrt = (sec ? j.n_ga : j.n_gb) / std::max(jt, 1);
+      for (int r0 = 0; r0 < nrt; r0 += 8)
+        for (int jj = 0; jj < jt; jj++)
+          for (int rt = r0; rt < std::min(r0 + 8, nrt); rt++) {
+            map.push_back(ji);
+            map.push_back(b0 + rt * jt + jj);
+          }
     }
     tmax = std::max<int64_t>(tmax, j.T);
     for (uintptr_t v : {(uintptr_t)j.dy, (uintptr_t)j.h, (uintptr_t)j.g, (uintptr_t)j.x, (uintptr_t)j.la,
