@@ -193,7 +193,8 @@ struct BwdPrepArgs {
   float* dymax;  // [ngq][T]: max |dy| over each 256-row slice (the dx kernels' f16 range), or null
   RankBlocks rb;  // g = dy . B restricted to each member's rows
   int y0;         // grid row offset: nhq when the h partials are already there (only g is computed)
-  int gtok;       // tokens per g-partial workgroup: 64 (a wave per 16 tokens) or 16 (a wave per 64 rows)
+  int gtok;       // tokens per g-partial workgroup: 64 (a wave per 16 tokens), 32 (a wave per 16 tokens
+                  // and 128 rows) or 16 (a wave per 64 rows)
 };
 
 // part[z][t][k] = sum over rows n of split z of dy[t][n] W[n][k], three 16-bit MFMAs per product (hi / lo

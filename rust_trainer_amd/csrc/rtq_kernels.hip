@@ -355,6 +355,9 @@ __device__ __forceinline__ void lora_partial(const float* S, int T, int ks, cons
 //   TW = 64: wave w owns tokens t0 + 16w .. +15 and all 256 rows; lane (token li, group g) loads
 //            rows 64g .. 64g+63 of the slice (256 contiguous bytes), step u contracts row 64g + u;
 //            no cross-wave reduction;
+//   TW = 32: wave w = (wt, wh) = (w % 2, w / 2) owns tokens t0 + 16wt .. +15 and rows 128wh ..
+//            128wh+127; lane (li, g) loads rows 128wh + 32g .. +31, step u contracts row
+//            128wh + 32g + u; wave (wt, 0) adds wave (wt, 1)'s sums (through LDS) to its own;
 //   TW = 16: wave w owns rows 64w .. 64w+63 of the 16 tokens; lane (li, g) loads rows
 //            64w + 16g .. +15, step u contracts row 64w + 16g + u; the four waves' sums are added
 //            in LDS in wave order (for grids too small to fill the chip with 64-token workgroups).
@@ -379,11 +382,13 @@ __device__ __forceinline__ void lora_load_b(const BwdPrepArgs& a, int k0, int j0
 
 template <int TW>
 __device__ __forceinline__ void lora_up_partial(const BwdPrepArgs& a, int t0, int q, float* sb, float* red) {
-  constexpr int KQ = RTQ_ACT_KQ, NU = TW == 64 ? 64 : 16;
+  constexpr int KQ = RTQ_ACT_KQ, NU = TW;
   static_assert(KQ == 256, "one slice row per thread, four 64-row lane groups");
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
-  const int k0 = q * KQ, tw = TW == 64 ? t0 + 16 * w : t0, t = tw + li;
-  const int kl0 = TW == 64 ? 64 * g : 64 * w + 16 * g, kb = k0 + kl0;  // first slice row of this lane
+  const int wt = w & 1, wh = w >> 1;  // TW = 32
+  const int k0 = q * KQ, tw = TW == 64 ? t0 + 16 * w : TW == 32 ? t0 + 16 * wt : t0, t = tw + li;
+  // first slice row of this lane
+  const int kl0 = TW == 64 ? 64 * g : TW == 32 ? 128 * wh + 32 * g : 64 * w + 16 * g, kb = k0 + kl0;
   float v[NU];
   {
     const float* row = a.dy + (int64_t)min(t, a.T - 1) * a.N;
@@ -416,6 +421,12 @@ __device__ __forceinline__ void lora_up_partial(const BwdPrepArgs& a, int t0, in
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     if (TW == 64) {
       if (g == 0 && t < a.T) a.dymax[(int64_t)q * a.T + t] = mx;
+    } else if (TW == 32) {
+      if (g == 0) red[w * 16 + li] = mx;
+      __syncthreads();
+      if (tid < 32 && t0 + tid < a.T)  // token tid: waves (tid / 16, 0) and (tid / 16, 1)
+        a.dymax[(int64_t)q * a.T + t0 + tid] = fmaxf(red[(tid >> 4) * 16 + (tid & 15)], red[((tid >> 4) + 2) * 16 + (tid & 15)]);
+      // red is next written after the staging barrier below, which every reader has passed
     } else {
       if (g == 0) red[w * 16 + li] = mx;
       __syncthreads();
@@ -447,13 +458,17 @@ __device__ __forceinline__ void lora_up_partial(const BwdPrepArgs& a, int t0, in
 #pragma unroll
         for (int u = 0; u < NU; u++) acc = mfma_f32(v[u], sg[16 * u], acc);
       }
-      if (TW == 16) {
+      if (TW == 16 || (TW == 32 && wh == 1)) {
 #pragma unroll
         for (int i = 0; i < 4; i++) red[w * 256 + (4 * g + i) * 16 + li] = acc[i];
       }
       __syncthreads();  // red is complete; sb may be restaged (red is rewritten only after the next staging barrier)
+      if (TW == 32 && wh == 0) {  // rows 0 .. 127, then rows 128 .. 255
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = acc[i] + red[(w + 2) * 256 + (4 * g + i) * 16 + li];
+      }
     }
-    if (TW == 64) {  // lane (rank li, token group g) holds tokens tw + 4g + i
+    if (TW == 64 || (TW == 32 && wh == 0)) {  // lane (rank li, token group g) holds tokens tw + 4g + i
       const int j = j0 + li;
       if (j < a.r)
 #pragma unroll
@@ -461,7 +476,7 @@ __device__ __forceinline__ void lora_up_partial(const BwdPrepArgs& a, int t0, in
           const int tt = tw + 4 * g + i;
           if (tt < a.T) a.gp[((int64_t)q * a.T + tt) * a.r + j] = acc[i];
         }
-    } else {  // thread (token tid / 16, rank tid % 16)
+    } else if (TW == 16) {  // thread (token tid / 16, rank tid % 16)
       const int tt = t0 + (tid >> 4), j = j0 + (tid & 15);
       const float ps = cur ? (red[tid] + red[256 + tid]) + (red[512 + tid] + red[768 + tid]) : 0.0f;
       if (tt < a.T && j < a.r) a.gp[((int64_t)q * a.T + tt) * a.r + j] = ps;
@@ -2531,7 +2546,7 @@ RTQ_GEMVQ(rtq_gemvq4_q6_k, FMT_Q6_K, RTQ_GQ_RG8, 4)
 // (ceil(T / 16), nhq + ngq) offset by y0 (nhq 0: the forward kept the h partials):
 //   grid row y < nhq:     h partial over columns [256y, 256y + 256) of x . A^T for the 16 tokens
 //                         16x .. 16x + 15 -> hp[(t * r + j) * nhq + y] (slice index fastest);
-//   grid row y = nhq + q: g partial over rows [256q, 256q + 256) of dy . B for the gtok (64 or 16)
+//   grid row y = nhq + q: g partial over rows [256q, 256q + 256) of dy . B for the gtok (64, 32 or 16)
 //                         tokens gtok x .. -> gp[(q * T + t) * r + j] (slice-major); workgroups
 //                         with gtok x >= T exit.
 // The dx kernel's extra workgroups sum the partials in slice order (h, and g scaled by s).
@@ -2549,6 +2564,8 @@ extern "C" __global__ __launch_bounds__(256) void rtq_bwd_prep(BwdPrepArgs a) {
     if (t0 >= a.T) return;  // whole workgroup
     if (a.gtok == 64)
       lora_up_partial<64>(a, t0, y - a.nhq, sm, red);
+    else if (a.gtok == 32)
+      lora_up_partial<32>(a, t0, y - a.nhq, sm, red);
     else
       lora_up_partial<16>(a, t0, y - a.nhq, sm, red);
   }

@@ -219,6 +219,8 @@ struct rtq_ctx {
   std::vector<TimedLaunch> pending;
   std::vector<hipEvent_t> free_events;
   int dx_splits = 0;  // 0: automatic; RTQ_DX_SPLITS overrides (tuning)
+  int gtok = 0;       // g-partial tokens per workgroup: 0 automatic, else 16 / 32 / 64 (RTQ_GTOK)
+  int dx_wpc = 1;     // 64-token dx tiles: row splits for about this many workgroups per CU (RTQ_DX_WPC)
   int dx_wide = -1;   // 256-token dx tiles: -1 automatic, 0 never, 1 for every t > 16 (RTQ_DX_WIDE)
   int dx_32 = 0;      // 32-token dx tiles (RTQ_DX_32): 0 never, 1 with the 64-token plan's splits, 2 with
                       // half of them
@@ -789,7 +791,8 @@ DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
   else if (p.wide)
     splits = wsplits;
   else
-    splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16), cdiv(c->cu_count, Kc * cdiv(t, 64))));
+    splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(steps, 16),
+                                                    cdiv(c->dx_wpc * c->cu_count, Kc * cdiv(t, 64))));
   if (p.t32 && c->dx_32 == 2) splits = std::max<int64_t>(1, splits / 2);
   if (c->dx_splits > 0)
     splits = std::min<int64_t>(std::min<int64_t>(steps, p.tok16 ? 256 : (p.wide ? 64 : 16)), c->dx_splits);
@@ -857,9 +860,15 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   float* dymax = dp.tok16 ? nullptr : ar.take<float>((size_t)(ngq * t));
   if (ar.off > ar.cap) return fail(RTQ_ERR_INVALID, "internal: workspace too small");
   if (lora) {
-    // h partials: 16 tokens per workgroup; g partials: 64, or 16 where 64-token workgroups would
-    // leave more than half of the CUs without one
-    const int gtok = cdiv(t, 64) * ngq >= (c->g64_min >= 0 ? c->g64_min : c->cu_count / 2) ? 64 : 16;
+    // h partials: 16 tokens per workgroup; g partials: 64 where those workgroups alone give every
+    // CU one; else 32 where those give at least half of the CUs one and no CU two (the 32-token
+    // form splits each slice's rows over two waves, so twice the workgroups run half the MFMA
+    // chain); else 64 where those give at least half of the CUs one; else 16.  Measured per
+    // configs[2] call (512 tokens): q|k|v (16 slices, r 48) 8.33 -> 7.46 us at 32; gate|up (24
+    // slices, r 32, 384 workgroups at 32) 8.53 -> 9.41, so 64 there
+    const int64_t g64 = c->g64_min >= 0 ? c->g64_min : c->cu_count / 2, n64 = cdiv(t, 64) * ngq, n32 = cdiv(t, 32) * ngq;
+    int gtok = n64 >= std::max<int64_t>(g64, c->cu_count) ? 64 : (n32 >= g64 && n32 <= c->cu_count) ? 32 : n64 >= g64 ? 64 : 16;
+    if (c->gtok == 16 || c->gtok == 32 || c->gtok == 64) gtok = c->gtok;
     BwdPrepArgs pa{x, la, K, dy, lb, N, (int)t, (int)r, hp, (int)nhq, gp, (int)ngq, dymax, RankBlocks{},
                    have_h ? (int)nhq : 0, gtok};
     if (rb) pa.rb = *rb;
@@ -1091,6 +1100,8 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   c->device = device;
   c->cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   if (const char* e = getenv("RTQ_DX_SPLITS")) c->dx_splits = atoi(e);
+  if (const char* e = getenv("RTQ_DX_WPC")) c->dx_wpc = std::min(std::max(atoi(e), 1), 4);
+  if (const char* e = getenv("RTQ_GTOK")) c->gtok = atoi(e);
   if (const char* e = getenv("RTQ_DX_WIDE")) c->dx_wide = atoi(e) ? 1 : 0;
   if (const char* e = getenv("RTQ_DX_32")) c->dx_32 = std::min(std::max(atoi(e), 0), 2);
   if (const char* e = getenv("RTQ_FWD_WAVES")) c->fwd_waves = atoi(e) == 4 ? 4 : 8;

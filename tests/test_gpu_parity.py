@@ -950,3 +950,34 @@ def test_dxv1_lora_backward(ctx, wtype):
     assert rel_err(dx, wdx) <= TOL
     assert rel_err(lin.lora.ga, wga) <= TOL
     assert rel_err(lin.lora.gb, wgb) <= TOL
+
+
+# ---------------------------------------------------------------- g partials: 64 / 32 / 16 tokens per workgroup
+@pytest.fixture(scope="module", params=[16, 32, 64])
+def ctx_gtok(request):
+    """A context whose LoRA g partials (g = s dy.B per 256-row slice) run on one workgroup form
+    (RTQ_GTOK): 64 tokens (a wave per 16 tokens), 32 (two waves per 16 tokens, 128 rows each, summed
+    through LDS) or 16 (four waves per 64 rows)"""
+    c = _context({"RTQ_GTOK": str(request.param)})
+    yield request.param, c
+    c.close()
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q6_K])
+@pytest.mark.parametrize("t,r", [(100, 48), (512, 16), (45, 40)])
+def test_g_partial_forms_match_oracle(ctx_gtok, wtype, t, r):
+    """Linear::backward with LoRA on each g-partial form against the oracle: ragged tokens (45, 100),
+    rank tiles 1-3 with a ragged last one (r = 40), a ragged last slice of B (N = 1000)"""
+    gtok, c = ctx_gtok
+    n, k = 1000, 512 if BLOCK[wtype] == 256 else 384
+    if BLOCK[wtype] == 256:
+        n = 1024
+    blocks, x, dy = make(wtype, n, k, t)
+    A, B = lora(n, k, r)
+    lin = rt.Linear("blk.0.attn_q", hip(c, wtype, blocks, n, k))
+    lin.lora = rt.Lora(r, 2.0 * r, A, B)
+    dx = lin.backward(x, dy, t)
+    wdx, wga, wgb = O.linear_backward(wtype, blocks, n, k, x, dy, A=A, B=B, alpha=2.0 * r, nthreads=8)
+    assert rel_err(dx, wdx) <= TOL, gtok
+    assert rel_err(lin.lora.ga, wga) <= TOL, gtok
+    assert rel_err(lin.lora.gb, wgb) <= TOL, gtok
