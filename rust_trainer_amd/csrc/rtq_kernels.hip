@@ -1109,6 +1109,9 @@ RTQ_FWD8(rtq_fwd_q8_0_w8, FMT_Q8_0, 4, 3, 2)
 // 64 tokens x 32 rows: where 48-row tiles would leave CUs without a workgroup (thin outputs)
 RTQ_FWD8(rtq_fwd_q4_0_w8r2, FMT_Q4_0, 4, 2, 2)
 RTQ_FWD8(rtq_fwd_q8_0_w8r2, FMT_Q8_0, 4, 2, 2)
+// 64 tokens x 16 rows: where 32-row tiles would still leave CUs without a workgroup
+RTQ_FWD8(rtq_fwd_q4_0_w8r1, FMT_Q4_0, 4, 1, 2)
+RTQ_FWD8(rtq_fwd_q8_0_w8r1, FMT_Q8_0, 4, 1, 2)
 RTQ_FWD(rtq_fwd_q4_0_s, FMT_Q4_0, 1, 4, 4, false)
 RTQ_FWD(rtq_fwd_q8_0_w, FMT_Q8_0, 4, 3, 2, false)
 RTQ_FWD(rtq_fwd_q8_0_s, FMT_Q8_0, 1, 4, 4, false)

@@ -124,6 +124,8 @@ enum Kid {
   K_FWD_Q8_0_W8,
   K_FWD_Q4_0_W8R2,  // the same with 32-row tiles
   K_FWD_Q8_0_W8R2,
+  K_FWD_Q4_0_W8R1,  // the same with 16-row tiles
+  K_FWD_Q8_0_W8R1,
   K_MM_Q4_0,     // large-grid forward (128 x 128 tiles, LDS ring)
   K_MM_Q8_0,
   K_MM64_Q4_0,   // the same with 128 x 64 tiles
@@ -170,6 +172,7 @@ constexpr const char* kKernelNames[] = {
     "rtq_gemvq1_q4_0",      "rtq_gemvq1_q8_0",      "rtq_gemvq1_q4_k",      "rtq_gemvq1_q6_k",
     "rtq_gemvq4_q4_0",      "rtq_gemvq4_q8_0",      "rtq_gemvq4_q4_k",      "rtq_gemvq4_q6_k",
     "rtq_fwd_q4_0_w8",      "rtq_fwd_q8_0_w8",      "rtq_fwd_q4_0_w8r2",    "rtq_fwd_q8_0_w8r2",
+    "rtq_fwd_q4_0_w8r1",    "rtq_fwd_q8_0_w8r1",
     "rtq_mm_q4_0",          "rtq_mm_q8_0",
     "rtq_mm64_q4_0",        "rtq_mm64_q8_0",        "rtq_mm32_q4_0",        "rtq_mm32_q8_0",
     "rtq_mmi8_64_q4_0",     "rtq_mmi8_64_q8_0",
@@ -225,7 +228,7 @@ struct rtq_ctx {
   int dx_32 = 0;      // 32-token dx tiles (RTQ_DX_32): 0 never, 1 with the 64-token plan's splits, 2 with
                       // half of them
   int fwd_waves = 8;  // waves splitting K in the wide Q4_0 / Q8_0 forward (RTQ_FWD_WAVES: 4 or 8)
-  int fwd_rg = -1;    // row groups of 16 per eight-wave forward tile: -1 automatic, 2 or 3 (RTQ_FWD_RG)
+  int fwd_rg = -1;    // row groups of 16 per eight-wave forward tile: -1 automatic, 1, 2 or 3 (RTQ_FWD_RG)
   int g64_min = -1;   // fewest 64-token g-partial workgroups (else 16-token ones): -1 = CUs / 2 (RTQ_G64_MIN)
   int fwd_mm = -1;    // large-grid forward: -1 automatic, 0 never, 1 / 2 / 3 the 128- / 64- / 32-token tiles
                       // whenever the format allows (RTQ_FWD_MM)
@@ -643,10 +646,15 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   const bool w8 = !p.skinny && !isums && !kq && c->fwd_waves == 8;  // rtq_fwd_*_w8[r2]
   const int64_t gy = p.skinny ? p.Tp / 16 : cdiv(t, 16 * kFwdWideTT);
   // the eight-wave forward with 32-row tiles wherever 48-row tiles would leave CUs without a
-  // workgroup (RTQ_FWD_RG: 2 or 3 forces one).  Measured at 256 tokens (one MI355X, per forward
-  // call): kv_proj 1024 x 1024 24.8 -> 20.3 us, down_proj 1024 x 3072 32.7 -> 24.4 (both still split K)
-  const bool rg2 = w8 && (c->fwd_rg == 2 || (c->fwd_rg < 0 && cdiv(w->Np / 16, 3) * gy < c->cu_count));
-  const int64_t rg_per_wg = p.skinny ? kFwdSkinnyRG : (rg2 ? 2 : wide_rg(w->type));
+  // workgroup, 16-row tiles wherever 32-row ones still would (RTQ_FWD_RG: 1, 2 or 3 forces one).
+  // Measured at 256 tokens (one MI355X, per forward call): kv_proj 1024 x 1024 24.8 -> 20.3 us,
+  // down_proj 1024 x 3072 32.7 -> 24.4 at 32 rows (both still split K)
+  int wrg = 3;
+  if (w8) {
+    if (c->fwd_rg >= 1 && c->fwd_rg <= 3) wrg = c->fwd_rg;
+    else if (cdiv(w->Np / 16, 3) * gy < c->cu_count) wrg = cdiv(w->Np / 16, 2) * gy < c->cu_count ? 1 : 2;
+  }
+  const int64_t rg_per_wg = p.skinny ? kFwdSkinnyRG : (w8 ? wrg : wide_rg(w->type));
   const int64_t gx = cdiv(w->Np / 16, rg_per_wg);
   // the large-grid kernel once its 128 x 128 tiles alone give a workgroup per CU, else its
   // 128 x 64 tiles if those do
@@ -749,7 +757,7 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   int kid = (p.skinny ? (isums ? K_FWD_S_ISUMS : K_FWD_S) : (isums ? K_FWD_W_ISUMS : K_FWD_W)) + fmt_index(w->type);
   int threads = 256;
   if (w8) {
-    kid = (rg2 ? K_FWD_Q4_0_W8R2 : K_FWD_Q4_0_W8) + (w->type == RTQ_TYPE_Q4_0 ? 0 : 1);
+    kid = (wrg == 1 ? K_FWD_Q4_0_W8R1 : wrg == 2 ? K_FWD_Q4_0_W8R2 : K_FWD_Q4_0_W8) + (w->type == RTQ_TYPE_Q4_0 ? 0 : 1);
     threads = 512;
   }
   return launch(c, kid, dim3((unsigned)gx, (unsigned)gy, (unsigned)ks), dim3(threads), st, fa);
@@ -1111,7 +1119,7 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   if (const char* e = getenv("RTQ_GEMVQ")) c->gemvq = atoi(e) ? 1 : 0;
   if (const char* e = getenv("RTQ_DXV")) c->dxv = atoi(e) ? 1 : 0;
   if (const char* e = getenv("RTQ_GEMVQ_WPC")) c->gemvq_wpc = std::min(std::max(atoi(e), 0), 32);
-  if (const char* e = getenv("RTQ_FWD_RG")) c->fwd_rg = atoi(e) == 2 ? 2 : 3;
+  if (const char* e = getenv("RTQ_FWD_RG")) c->fwd_rg = std::min(std::max(atoi(e), 1), 3);
   if (const char* e = getenv("RTQ_G64_MIN")) c->g64_min = atoi(e);
   hipError_t e = hipModuleLoadData(&c->mod, rtq_hsaco_begin);
   if (e != hipSuccess) {

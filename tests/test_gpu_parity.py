@@ -573,46 +573,44 @@ def test_forward_kquant_ring_selected_and_equal_to_tile_kernel(ctx, wtype):
     assert rel_err(y, O.frozen_forward(wtype, blocks, n, k, x, nthreads=16)) <= TOL
 
 
-# ---------------------------------------------------------------- eight-wave forward, 32-row tiles
-@pytest.fixture(scope="module")
-def ctx_rg2():
-    """A context that sends every eight-wave Q4_0 / Q8_0 forward through its 32-row-tile variant
-    (RTQ_FWD_RG=2) and never through rtq_mm_* (RTQ_FWD_MM=0), so small shapes cover its padding."""
-    import os
-
-    old = {k: os.environ.get(k) for k in ("RTQ_FWD_RG", "RTQ_FWD_MM")}
-    os.environ["RTQ_FWD_RG"] = "2"
-    os.environ["RTQ_FWD_MM"] = "0"
-    try:
-        c = rt.Context(0)
-    finally:
-        for k, v in old.items():
-            if v is None:
-                del os.environ[k]
-            else:
-                os.environ[k] = v
-    yield c
+# ---------------------------------------------------------------- eight-wave forward, 32- and 16-row tiles
+@pytest.fixture(scope="module", params=[1, 2])
+def ctx_rg(request):
+    """A context that sends every eight-wave Q4_0 / Q8_0 forward through its 16- or 32-row-tile
+    variant (RTQ_FWD_RG=1 / 2) and never through rtq_mm_* (RTQ_FWD_MM=0), so small shapes cover its
+    padding."""
+    c = _context({"RTQ_FWD_RG": str(request.param), "RTQ_FWD_MM": "0"})
+    yield request.param, c
     c.close()
 
 
 @pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
 @pytest.mark.parametrize("n,k,t,r", [(200, 256, 130, 16), (1000, 1024, 300, 80), (130, 128, 17, 4), (1024, 2048, 512, 16)])
-def test_linear_forward_rg2_matches_oracle(ctx_rg2, wtype, n, k, t, r):
-    # partial 32-row tiles (N = 130, 200, 1000), token padding, LoRA ranks 4 / 16 / 80, the o_proj
-    # shape of the configs[2] step
+def test_linear_forward_rg_matches_oracle(ctx_rg, wtype, n, k, t, r):
+    # partial 16- / 32-row tiles (N = 130, 200, 1000), token padding, LoRA ranks 4 / 16 / 80, the
+    # o_proj shape of the configs[2] step
+    rg, c = ctx_rg
     blocks, x, _ = make(wtype, n, k, t)
     bias = O.Rng(6).vec_normal(n, 0.1)
-    lin = rt.Linear("blk.0.attn_output", hip(ctx_rg2, wtype, blocks, n, k), bias=bias)
+    lin = rt.Linear("blk.0.attn_output", hip(c, wtype, blocks, n, k), bias=bias)
     A, B = lora(n, k, r)
     lin.lora = rt.Lora(r, 2.0 * r, A, B)
-    ctx_rg2.set_timing(True)
-    ctx_rg2.reset_timing()
-    y = lin.forward(x, t)
-    ran = ctx_rg2.timing()
-    ctx_rg2.set_timing(False)
-    assert any(name.endswith("_w8r2") for name in ran), ran
+    y, ran = _ran(c, lambda: lin.forward(x, t))
+    assert any(name.endswith(f"_w8r{rg}") for name in ran), ran
     want = O.linear_forward(wtype, blocks, n, k, x, bias=bias, A=A, B=B, alpha=2.0 * r, nthreads=16)
     assert rel_err(y, want) <= TOL
+
+
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
+def test_forward_rg1_selected_by_grid_size(ctx, wtype):
+    # the kv_proj shape of configs[1] at 256 tokens: 64 row groups x 4 token tiles is 128 tiles of
+    # 32 rows (fewer than the CUs) but 256 of 16, so the default context picks the 16-row tiles
+    n, k, t = 1024, 1024, 256
+    blocks, x, _ = make(wtype, n, k, t)
+    w = hip(ctx, wtype, blocks, n, k)
+    y, ran = _ran(ctx, lambda: w.forward(x, t))
+    assert any(name.endswith("_w8r1") for name in ran), ran
+    assert rel_err(y, O.frozen_forward(wtype, blocks, n, k, x, nthreads=16)) <= TOL
 
 
 @pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
