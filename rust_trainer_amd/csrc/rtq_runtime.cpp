@@ -692,12 +692,15 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
     else if (c->fwd_mmk < 0) mmk_ttn = mm64 >= c->cu_count ? 4 : (mm32 >= c->cu_count ? 2 : 0);
   }
   const int64_t mm_tiles = mm_ttn == 8 ? mm128 : mm_ttn == 4 ? mm64 : mm32;
-  const int64_t tiles = gx * gy;
   // split K across workgroups when the output alone gives too few of them (atomics into a
   // zeroed y); every split keeps at least one half chunk per wave (K-quants: one super-block of
-  // two chunks per wave, and splits on super-block boundaries)
+  // two chunks per wave, and splits on super-block boundaries).  The eight-wave tiles never split
+  // K (smaller row tiles fill the CUs instead): each output is then summed by one workgroup in one
+  // order whatever the token count, so a packed batch and its examples, run at other token counts,
+  // get the same bits
+  const int64_t tiles = gx * gy;
   int64_t ks = 1;
-  if (!isums && !mm && !mmk_ttn && tiles < c->cu_count) {
+  if (!isums && !mm && !mmk_ttn && !w8 && tiles < c->cu_count) {
     const int64_t want = cdiv(p.skinny ? 2 * c->cu_count : c->cu_count, tiles);
     ks = std::max<int64_t>(1, std::min<int64_t>(want, Kc / (kq ? 8 : 2)));
   }
