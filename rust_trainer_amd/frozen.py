@@ -34,7 +34,9 @@ class Context:
         _ffi.check(L.rtq_ctx_create(device, ctypes.byref(h)), "rtq_ctx_create")
         self._h = h
         self.device = device
-        self._weights: weakref.WeakSet = weakref.WeakSet()
+        # weights and models created on this context, closed before it (a model or weight that
+        # outlives its context - held by a traceback, say - must not reach the freed context later)
+        self._owned: weakref.WeakSet = weakref.WeakSet()
 
     @property
     def handle(self) -> ctypes.c_void_p:
@@ -90,9 +92,9 @@ class Context:
         _ffi.lib().rtq_ctx_timing_reset(self.handle)
 
     def close(self) -> None:
-        """Destroys the weights still alive on this context, then the context itself."""
+        """Destroys the weights and models still alive on this context, then the context itself."""
         if self._h is not None:
-            for w in list(self._weights):
+            for w in list(self._owned):
                 w.close()
             _ffi.lib().rtq_ctx_destroy(self._h)
             self._h = None
@@ -217,7 +219,7 @@ class HipFrozen(FrozenMatmul):
         self._h = h
         self.ggml_type = ggml_type
         self._rows, self._cols = rows, cols
-        self.ctx._weights.add(self)
+        self.ctx._owned.add(self)
 
     @property
     def handle(self) -> ctypes.c_void_p:

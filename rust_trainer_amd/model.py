@@ -41,6 +41,7 @@ class GpuModel:
     def __init__(self, handle: ctypes.c_void_p, ctx: Context, keep=None):
         self._h = handle
         self.ctx = ctx
+        ctx._owned.add(self)
         self._keep = keep
         c = _ffi.RtqModelConfig()
         _ffi.check(_ffi.lib().rtq_model_get_config(handle, ctypes.byref(c)), "rtq_model_get_config")
