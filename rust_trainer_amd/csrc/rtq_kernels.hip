@@ -3113,7 +3113,7 @@ __device__ __forceinline__ void dx16_tile(const DxArgs& a) {
     return;  // uniform over the workgroup, before any barrier
   }
   constexpr bool KQ = is_kquant(FMT), B8 = byte_codes(FMT);
-  constexpr int D = 4;
+  constexpr int D = RTQ_DX16_D;
   __shared__ u4v sA[2][2][64];                                          // [buf][hi/lo][lane]
   __shared__ __attribute__((aligned(16))) _Float16 sW[2][2][128][40];   // [buf][hi/lo][k][n]
   __shared__ float sSc[16], sInv[16];  // 2^e of each token row, 2^-e (times wunsc)
@@ -3267,29 +3267,40 @@ __device__ __forceinline__ void dx16_tile(const DxArgs& a) {
   };
 #pragma unroll
   for (int s0 = 0; s0 < D - 1; s0++) issue(sl[s0], s0);
-  {  // the tokens' scales while those loads are in flight: wave w reduces tokens w, w + 4, ..
+  {  // the tokens' scales while those loads are in flight: the 16 threads of token tl (the dy
+     // loader's) scan its rows of the split together, 64 rows per pass (a float4 each, or four
+     // floats where N % 4 != 0), up to eight passes' loads in flight, then a max over the 16
     const int r1 = min(n0 + a.n_per_split, a.N);
-    for (int t = w; t < a.T; t += 4) {
-      const float* row = a.dy + (int64_t)t * a.N;
-      float m8[8];  // eight loads in flight per lane
+    float mx = 0.0f;
+    if (tl < a.T) {
+      const float* row = a.dy + (int64_t)tl * a.N;
+      const bool v4 = (a.N & 3) == 0 && (reinterpret_cast<uintptr_t>(a.dy) & 15) == 0;  // uniform: 16-byte aligned rows (n0 % 32 == 0)
+      for (int nb = n0 + 4 * pp; nb < r1; nb += 512) {
+        f4 v[8];
 #pragma unroll
-      for (int u = 0; u < 8; u++) m8[u] = 0.0f;
-      for (int n = n0 + lane; n < r1; n += 512) {
-        float v[8];
+        for (int u = 0; u < 8; u++) {
+          const int n = nb + 64 * u;
+          if (v4 && n + 4 <= r1) {
+            v[u] = *reinterpret_cast<const f4*>(row + n);
+          } else {
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = n + 64 * u < r1 ? row[n + 64 * u] : 0.0f;
+            for (int e = 0; e < 4; e++) v[u][e] = n + e < r1 ? row[n + e] : 0.0f;
+          }
+        }
 #pragma unroll
-        for (int u = 0; u < 8; u++) m8[u] = fmaxf(m8[u], fabsf(v[u]));
+        for (int u = 0; u < 8; u++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) mx = fmaxf(mx, fabsf(v[u][e]));
       }
-      float mx = fmaxf(fmaxf(fmaxf(m8[0], m8[1]), fmaxf(m8[2], m8[3])), fmaxf(fmaxf(m8[4], m8[5]), fmaxf(m8[6], m8[7])));
-      mx = wave_max(mx);
-      if (lane == 0) {
-        int ex = 0;
-        (void)frexpf(mx, &ex);  // mx = f 2^ex, f in [0.5, 1): mx 2^(15 - ex) in [2^14, 2^15)
-        const bool ok = mx > 0.0f && mx <= 3.0e38f;
-        sSc[t] = ok ? ldexpf(1.0f, 15 - ex) : 1.0f;
-        sInv[t] = (ok ? ldexpf(1.0f, ex - 15) : 1.0f) * a.wunsc;
-      }
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m));  // the token's 16 lanes
+    if (pp == 0 && tl < a.T) {
+      int ex = 0;
+      (void)frexpf(mx, &ex);  // mx = f 2^ex, f in [0.5, 1): mx 2^(15 - ex) in [2^14, 2^15)
+      const bool ok = mx > 0.0f && mx <= 3.0e38f;
+      sSc[tl] = ok ? ldexpf(1.0f, 15 - ex) : 1.0f;
+      sInv[tl] = (ok ? ldexpf(1.0f, ex - 15) : 1.0f) * a.wunsc;
     }
     __syncthreads();
     if (tl < a.T) dsc = sSc[tl];
