@@ -158,6 +158,9 @@ struct FwdArgs {
 #ifndef RTQ_DX16_D
 #define RTQ_DX16_D 4  // rtq_dx16_*: register ring depth (steps of 32 rows; loads D - 1 steps ahead)
 #endif
+#ifndef RTQ_DX16_SCAN
+#define RTQ_DX16_SCAN 8  // rtq_dx16_*: float4 loads in flight per thread in the dy range scan
+#endif
 // rtq_gemvq{1,4}_*: y = x W^T (+ bias) (+ s (x A^T) B^T) for T <= 1 / 4 tokens in one launch (the
 // kernel quantises x itself).  Dynamic LDS: NT Kp bytes of codes, NT Kp / 32 block scales, NT Kp / 32
 // code sums (Q4_0: NT Kp / 8, one per k-group), NT * RTQ_LDS_RANK floats of h.

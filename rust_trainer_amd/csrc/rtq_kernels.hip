@@ -3268,17 +3268,17 @@ __device__ __forceinline__ void dx16_tile(const DxArgs& a) {
 #pragma unroll
   for (int s0 = 0; s0 < D - 1; s0++) issue(sl[s0], s0);
   {  // the tokens' scales while those loads are in flight: the 16 threads of token tl (the dy
-     // loader's) scan its rows of the split together, 64 rows per pass (a float4 each, or four
-     // floats where N % 4 != 0), up to eight passes' loads in flight, then a max over the 16
+     // loader's) scan its rows of the split together, 64 rows per step (a float4 each, or four
+     // floats where N % 4 != 0), RTQ_DX16_SCAN steps' loads in flight, then a max over the 16
     const int r1 = min(n0 + a.n_per_split, a.N);
     float mx = 0.0f;
     if (tl < a.T) {
       const float* row = a.dy + (int64_t)tl * a.N;
       const bool v4 = (a.N & 3) == 0 && (reinterpret_cast<uintptr_t>(a.dy) & 15) == 0;  // uniform: 16-byte aligned rows (n0 % 32 == 0)
-      for (int nb = n0 + 4 * pp; nb < r1; nb += 512) {
-        f4 v[8];
+      for (int nb = n0 + 4 * pp; nb < r1; nb += 64 * RTQ_DX16_SCAN) {
+        f4 v[RTQ_DX16_SCAN];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < RTQ_DX16_SCAN; u++) {
           const int n = nb + 64 * u;
           if (v4 && n + 4 <= r1) {
             v[u] = *reinterpret_cast<const f4*>(row + n);
@@ -3288,7 +3288,7 @@ __device__ __forceinline__ void dx16_tile(const DxArgs& a) {
           }
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++)
+        for (int u = 0; u < RTQ_DX16_SCAN; u++)
 #pragma unroll
           for (int e = 0; e < 4; e++) mx = fmaxf(mx, fabsf(v[u][e]));
       }
