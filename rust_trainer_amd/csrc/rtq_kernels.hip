@@ -9,7 +9,10 @@
 //    f16 MFMA as exact small integers (|q8| <= 127, |q4| <= 8): every product is exact in the
 //    f32 accumulator and so is the 32-term sum (|isum| <= 32*127*127 < 2^24), so the MFMA output
 //    is the integer block sum itself, with no i32->f32 conversion to pay in the epilogue;
+//    The int8 MFMA (rtq_mmi8_*) and v_dot4_i32_i8 (rtq_gemvq*, T <= 4) form the same integer sums;
 //  * block sums are scaled by d_w * d_x in f32 (the epilogue order is unpinned in the reference);
+//  * dx = dy . W at T = 1 (rtq_dxv1_*) multiplies in f32: the codes are exact f16 values, each
+//    product fma(dy * scale, code, acc) by mixed-precision FMA;
 //  * dx = dy . W (no dy quantisation, straight-through as in the reference) runs on f16 MFMA with
 //    both operands split into hi + lo f16 parts: each dy row scaled by a power of two 2^e that
 //    puts its largest |value| in [2^14, 2^15) (the whole row then lies in f16's range; the partial
