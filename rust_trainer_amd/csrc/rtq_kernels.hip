@@ -3709,6 +3709,35 @@ __device__ __forceinline__ void lora_grad_tile(const LoraGradArgs& a, int b, flo
 // columns (row-major partials).  NW = 4, or 16 for long token ranges.  DXO: dx workgroups alone
 // (n_gb = n_ga = 0: dA / dB deferred or no adapter) over at most four splits, loading four
 // partials at a time (the same split order; a quarter of the load registers).
+// dx[t, k0 .. k0+3] from its summed partials: + g[t] . A[:, k0 .. k0+3] (src/linear.rs:115-118),
+// then stored / accumulated, or (sw) taken as SwiGLU's dh (accumulate is off there)
+__device__ __forceinline__ void finish_row4(const LoraGradArgs& a, int t, int k0, f4 sum, bool sw) {
+  if (a.g) {
+    f4 ga = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < a.r; j++) {
+      const float gv = a.g[(int64_t)t * a.r + j];
+      const float* av = a.la + (int64_t)j * a.K + k0;  // caller's A: no alignment assumed
+#pragma unroll
+      for (int e = 0; e < 4; e++) ga[e] = fmaf(gv, av[e], ga[e]);
+    }
+    sum += ga;
+  }
+  if (sw) {
+    const int64_t o = (int64_t)t * a.swld + k0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float gv = a.swg[o + e], uv = a.swu[o + e];
+      a.swdg[o + e] = (sum[e] * uv) * rtq_silu_grad(gv);
+      a.swdu[o + e] = sum[e] * rtq_silu(gv);
+      if (a.sw_keep) a.dx[(int64_t)t * a.K + k0 + e] = sum[e];
+    }
+  } else {
+    float* p = a.dx + (int64_t)t * a.K + k0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) p[e] = a.accumulate ? p[e] + sum[e] : sum[e];
+  }
+}
+
 template <int NW, int E, bool DXO = false>
 __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
   __shared__ float red[DXO ? 1 : NW * 16 * E * 17];
@@ -3743,32 +3772,7 @@ __device__ __forceinline__ void bwd_finish(const LoraGradArgs& a) {
       sum[e] += __shfl_xor(sum[e], 16);
       sum[e] += __shfl_xor(sum[e], 32);
     }
-    if (g == 0 && kin) {
-      if (a.g) {  // + g[t] . A[:, k0 .. k0+3]  (src/linear.rs:115-118)
-        f4 ga = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int j = 0; j < a.r; j++) {
-          const float gv = a.g[(int64_t)t * a.r + j];
-          const float* av = a.la + (int64_t)j * a.K + k0;  // caller's A: no alignment assumed
-#pragma unroll
-          for (int e = 0; e < 4; e++) ga[e] = fmaf(gv, av[e], ga[e]);
-        }
-        sum += ga;
-      }
-      if (NW == 4 && a.swg) {  // SwiGLU backward of dh = sum (accumulate is off; 4-wave finish only)
-        const int64_t o = (int64_t)t * a.swld + k0;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const float gv = a.swg[o + e], uv = a.swu[o + e];
-          a.swdg[o + e] = (sum[e] * uv) * rtq_silu_grad(gv);
-          a.swdu[o + e] = sum[e] * rtq_silu(gv);
-          if (a.sw_keep) a.dx[(int64_t)t * a.K + k0 + e] = sum[e];
-        }
-      } else {
-        float* p = a.dx + (int64_t)t * a.K + k0;
-#pragma unroll
-        for (int e = 0; e < 4; e++) p[e] = a.accumulate ? p[e] + sum[e] : sum[e];
-      }
-    }
+    if (g == 0 && kin) finish_row4(a, t, k0, sum, NW == 4 && a.swg);
   } else {
     // dx quarter fq = (b - n_gb - n_ga) * NW + w: fragment f = fq / 4 of the dx kernel's partials
     // (tile f / 8 = token tile * Kc + K chunk, its wave f % 8 = (wt, wk)), quarter q = fq % 4 =
@@ -3901,6 +3905,44 @@ extern "C" __global__ __launch_bounds__(1024) void rtq_lora_grads_t16(LoraGradTa
 extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish(LoraGradArgs a) { bwd_finish<4, 4>(a); }
 extern "C" __global__ __launch_bounds__(1024) void rtq_bwd_finish16(LoraGradArgs a) { bwd_finish<16, 4>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish_dx(LoraGradArgs a) { bwd_finish<4, 4, true>(a); }
+
+// dx from row-major partials of many splits (rtq_dx16_* / rtq_dxv1_* over a long weight; no dA / dB
+// tiles): a workgroup per (token t, 64 columns), four times the workgroups of the wave-per-segment
+// form.  Wave w, lane (k4 = li, g) sums splits 4w + g, 4w + g + 16, ... in order (eight loads in
+// flight); the sixteen subsets are combined by shuffles (g), then through LDS (w = 0, 1, 2, 3)
+extern "C" __global__ __launch_bounds__(256) void rtq_bwd_finish_rows(LoraGradArgs a) {
+  __shared__ f4 red[3][16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, g = lane >> 4;
+  const int nseg = (a.K + 63) / 64;
+  if ((int)blockIdx.x >= a.T * nseg) return;  // whole workgroup exits together, before the barrier
+  const int t = blockIdx.x / nseg, k0 = (blockIdx.x % nseg) * 64 + 4 * li;
+  const bool kin = k0 < a.K;  // K % 32 == 0: four columns in or out together
+  const f4* pp = reinterpret_cast<const f4*>(a.part + (int64_t)t * a.K + min(k0, a.K - 4));
+  const int64_t sstride = (int64_t)a.T * a.K / 4;  // f4 per split
+  constexpr int PRL = 8;
+  f4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 4 * w + g; s0 < a.nsplit; s0 += 16 * PRL) {
+    f4 v[PRL];
+#pragma unroll
+    for (int q = 0; q < PRL; q++) v[q] = pp[(int64_t)min(s0 + 16 * q, a.nsplit - 1) * sstride];
+#pragma unroll
+    for (int q = 0; q < PRL; q++)
+      if (s0 + 16 * q < a.nsplit) sum += v[q];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    sum[e] += __shfl_xor(sum[e], 16);
+    sum[e] += __shfl_xor(sum[e], 32);
+  }
+  if (w > 0 && g == 0) red[w - 1][li] = sum;
+  __syncthreads();
+  if (w == 0 && g == 0 && kin) {
+    sum += red[0][li];
+    sum += red[1][li];
+    sum += red[2][li];
+    finish_row4(a, t, k0, sum, a.swg != nullptr);
+  }
+}
 
 
 // ============================================================== trainer-native weights

@@ -147,6 +147,7 @@ enum Kid {
   K_BWD_FINISH = K_DX32 + F_COUNT,
   K_BWD_FINISH16,  // 16 waves per workgroup: long token reductions of dA / dB
   K_BWD_FINISH_DX,  // dx workgroups alone (no dA / dB tiles in the grid)
+  K_BWD_FINISH_ROWS,  // row-major partials of many splits: a workgroup per (token, 64 columns)
   K_LORA_GRADS,    // dA / dB of several linears in one launch (4 / 16 waves per workgroup)
   K_LORA_GRADS16,
   K_LORA_GRADS_T,    // the same from a device job table
@@ -183,7 +184,7 @@ constexpr const char* kKernelNames[] = {
     "rtq_dxv1_q4_0",        "rtq_dxv1_q8_0",        "rtq_dxv1_q4_k",        "rtq_dxv1_q6_k",
     "rtq_dxw_q4_0",         "rtq_dxw_q8_0",         "rtq_dxw_q4_k",         "rtq_dxw_q6_k",
     "rtq_dx32_q4_0",        "rtq_dx32_q8_0",        "rtq_dx32_q4_k",        "rtq_dx32_q6_k",
-    "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_bwd_finish_dx",    "rtq_lora_grads",       "rtq_lora_grads16",     "rtq_lora_grads_t",     "rtq_lora_grads_t16",
+    "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_bwd_finish_dx",    "rtq_bwd_finish_rows",  "rtq_lora_grads",       "rtq_lora_grads16",     "rtq_lora_grads_t",     "rtq_lora_grads_t16",
     "rtq_dense_rows",       "rtq_dense_bias",
     "rtq_head_norm",        "rtq_head_max",         "rtq_head_sum",         "rtq_head_grad",
     "rtq_head_norm_bwd",
@@ -911,6 +912,10 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
   fa.n_ga = lora ? (int)(cdiv(K, 64) * jt) : 0;
   const int nw = lora && t >= 256 ? 16 : 4;
   fa.n_dx = dp.tok16 ? (int)cdiv(t * cdiv(K, 64), nw) : (int)cdiv((w->Kp / 128) * cdiv(t, 64) * 32, nw);
+  // dx alone: row-major partials of more than 16 splits take a workgroup per (token, 64 columns)
+  const bool wide_rows = dp.tok16 && dp.splits > 16;
+  const Kid kdx = dp.splits <= 4 ? K_BWD_FINISH_DX : wide_rows ? K_BWD_FINISH_ROWS : K_BWD_FINISH;
+  const unsigned gdx = wide_rows ? (unsigned)(t * cdiv(K, 64)) : 0;
   if (defer) {  // dA / dB later, in a batch; here the dx partials (+ g.A) alone, 4 waves per workgroup
     *defer->job = fa;
     defer->job->n_dx = 0;
@@ -925,9 +930,9 @@ rtq_status enqueue_backward(rtq_ctx* c, const rtq_weight* w, const float* dy, in
       fa.swld = defer->sw->ld;
       fa.sw_keep = defer->sw->keep_dh ? 1 : 0;
     }
-    return launch(c, dp.splits <= 4 ? K_BWD_FINISH_DX : K_BWD_FINISH, dim3((unsigned)fa.n_dx), dim3(256), st, fa);
+    return launch(c, kdx, dim3(wide_rows ? gdx : (unsigned)fa.n_dx), dim3(256), st, fa);
   }
-  if (!lora) return launch(c, dp.splits <= 4 ? K_BWD_FINISH_DX : K_BWD_FINISH, dim3((unsigned)fa.n_dx), dim3(256), st, fa);
+  if (!lora) return launch(c, kdx, dim3(wide_rows ? gdx : (unsigned)fa.n_dx), dim3(256), st, fa);
   return launch(c, nw == 16 ? K_BWD_FINISH16 : K_BWD_FINISH, dim3((unsigned)(fa.n_gb + fa.n_ga + fa.n_dx)),
                 dim3(64 * nw), st, fa);
 }

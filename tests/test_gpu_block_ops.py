@@ -254,6 +254,28 @@ def test_odd_fused_groups_block_ops_match_oracle(ctx, wtype, t):
     model.close()
 
 
+def test_t16_many_split_finish_block_ops_match_oracle(ctx):
+    """16 tokens through a block with 2560 rows per projection: every dx has 20 or more row splits,
+    so each linear's partials (down_proj's as SwiGLU's dh) are summed by the workgroup-per-(token,
+    64 columns) finish"""
+    spec = tiny_spec(O.Q4_0, n_layer=1, n_embd=2560, n_head=20, n_head_kv=4, head_dim=128, rope_dim=128, n_ff=4096,
+                     n_vocab=512)
+    g, model, m = build(ctx, spec, 16, 32.0, ALL)
+    t, n = 16, 12
+    toks, pos, tok = sequence(spec.n_vocab, t, n, 11)
+    model.debug_capture(0)
+    model.zero_grad()
+    ctx.set_timing(True)
+    ctx.reset_timing()
+    model.forward_backward(toks, [rt.Target(int(p), int(k)) for p, k in zip(pos, tok)],
+                           np.linspace(0.5, 1.5, n).astype(np.float32))
+    ran = ctx.timing()
+    ctx.set_timing(False)
+    assert ran.get("rtq_bwd_finish_rows", (0,))[0] >= 3, ran  # o, gate|up, down (dh) at least
+    check_block(ctx, g, model, m, 0, t, None, {}, {})
+    model.close()
+
+
 def test_packed_block_ops_match_oracle_recomputed(ctx):
     """a packed batch of four examples sharing a 100-token prompt (512 tokens) at the configs[2]
     block shape, activations recomputed in the backward"""

@@ -928,11 +928,18 @@ def test_dxv1_matches_oracle(ctx, wtype, n, k):
     dx = np.zeros(k, np.float32)
     _, names = _ran(ctx, lambda: w.backward_input(dy, 1, dx))
     assert any(nm.startswith("rtq_dxv1") for nm in names), names
+    if n >= 4100:  # 33 and 128 row splits: the workgroup-per-(token, 64 columns) finish
+        assert "rtq_bwd_finish_rows" in names, names
     want = O.frozen_backward_input(wtype, blocks, n, k, dy, dx=np.zeros((1, k), np.float32), nthreads=16)
     assert rel_err(dx, want) <= TOL
     if n <= 4100:
         dense = dy.astype(np.float64) @ _dense(wtype, blocks, n, k)
         assert np.abs(dx - dense.reshape(-1)).max() <= 1e-6 * np.abs(dense).max()
+    # accumulation onto a non-zero dx: one f32 add of the same sum, bit for bit
+    dx0 = O.Rng(7).vec_normal(k, 1.0).astype(np.float32)
+    acc = dx0.copy()
+    w.backward_input(dy, 1, acc)
+    assert np.array_equal(acc, dx0 + dx)
 
 
 @pytest.mark.parametrize("wtype", FORMATS)
