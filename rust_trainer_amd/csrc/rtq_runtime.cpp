@@ -236,6 +236,7 @@ struct rtq_ctx {
   int fwd_mmk = -1;   // K-quant ring forward (rtq_mmk*_*; RTQ_FWD_MMK): -1 automatic, 0 never, 1 / 2 the 64- /
                       // 32-token tiles whenever the shape allows
   int dxv = 1;        // t == 1 dx on f32 FMAs (rtq_dxv1_*; RTQ_DXV=0: rtq_dx16_*)
+  int dxv_wpc = 3;    // rtq_dxv1_* row splits for about this many workgroups per CU (RTQ_DXV_WPC)
   int gemvq = 1;      // one-launch GEMV for t <= 4 (rtq_gemvq*_*; RTQ_GEMVQ=0: activation kernel + GEMM)
   int gemvq_wpc = 0;  // its waves per CU (RTQ_GEMVQ_WPC; 0: automatic)
   int fwd_i8 = -1;    // int8-MFMA forwards (rtq_mmi8_*; RTQ_FWD_I8): -1 automatic (Q8_0 weights), 0 never,
@@ -810,9 +811,13 @@ DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
     splits = std::min<int64_t>(std::min<int64_t>(steps, p.tok16 ? 256 : (p.wide ? 64 : 16)), c->dx_splits);
   p.nps = cdiv(steps, splits) * 32;
   p.v1 = t == 1 && c->dxv && (uint64_t)(w->Np / 16) * (w->Kp / 128) * 2048u < (1ull << 32);
-  if (p.v1) {  // about four four-wave workgroups per CU, each split at least 8 row groups of 16
+  // rtq_dxv1_*: about three four-wave workgroups per CU, each split at least 8 row groups of 16.
+  // Measured on the LM head (151936 x 1024) at t = 1, one backward call, two, three, four, six
+  // workgroups per CU: Q4_0 24.4 / 24.7 / 25.0 / 25.9 us, Q4_K 27.6 / 27.3 / 27.9 / 29.6, Q6_K
+  // 37.7 / 36.3 / 36.5 / 37.5, Q8_0 36.6 / 34.9 / 35.6 / 35.9
+  if (p.v1) {
     const int64_t ngr = w->Np / 16;
-    const int64_t sv = std::max<int64_t>(1, std::min<int64_t>(cdiv(4 * c->cu_count, Kc), cdiv(ngr, 8)));
+    const int64_t sv = std::max<int64_t>(1, std::min<int64_t>(cdiv(c->dxv_wpc * c->cu_count, Kc), cdiv(ngr, 8)));
     p.nps = cdiv(ngr, sv) * 16;
   }
   p.splits = cdiv(w->Np, p.nps);
@@ -1126,6 +1131,7 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   if (const char* e = getenv("RTQ_FWD_MMK")) c->fwd_mmk = std::min(std::max(atoi(e), -1), 2);
   if (const char* e = getenv("RTQ_GEMVQ")) c->gemvq = atoi(e) ? 1 : 0;
   if (const char* e = getenv("RTQ_DXV")) c->dxv = atoi(e) ? 1 : 0;
+  if (const char* e = getenv("RTQ_DXV_WPC")) c->dxv_wpc = std::max(1, std::min(16, atoi(e)));
   if (const char* e = getenv("RTQ_GEMVQ_WPC")) c->gemvq_wpc = std::min(std::max(atoi(e), 0), 32);
   if (const char* e = getenv("RTQ_FWD_RG")) c->fwd_rg = std::min(std::max(atoi(e), 1), 3);
   if (const char* e = getenv("RTQ_G64_MIN")) c->g64_min = atoi(e);
