@@ -3018,6 +3018,10 @@ __device__ __forceinline__ void dxv1_tile(const DxArgs& a) {
     for (int e = 0; e < 8; e++) acc[j][e] = 0.0f;
   }
   auto compute = [&](const Dxv1Slot<FMT>& S) {
+    // K-quants: dy times the row's super-block scales, once per item (then times each block's
+    // integer scale)
+    const float dyd = KQ ? S.dy * h2f((uint16_t)(S.e & 0xffffu)) : 0.0f;
+    const float dym = FMT == FMT_Q4_K ? S.dy * h2f((uint16_t)(S.e >> 16)) : 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const uint32_t wv = hcomp(S.d, j);
@@ -3032,14 +3036,12 @@ __device__ __forceinline__ void dxv1_tile(const DxArgs& a) {
           f = (j & 1) ? q8_frag(qq.z, qq.w) : q8_frag(qq.x, qq.y);
         }
       } else if constexpr (FMT == FMT_Q4_K) {  // value d sc u - dmin m
-        const float dsb = h2f((uint16_t)(S.e & 0xffffu)), dmin = h2f((uint16_t)(S.e >> 16));
-        c = S.dy * (dsb * (float)(wv & 0x3fu));
-        bias[j] = fmaf(S.dy, dmin * (float)((wv >> 8) & 0x3fu), bias[j]);
+        c = dyd * (float)(wv & 0x3fu);
+        bias[j] = fmaf(dym, (float)((wv >> 8) & 0x3fu), bias[j]);
         f = q4_0_frag<0>(comp(S.q[0], j));
       } else {  // Q6_K: value d sc q, sc per 16 elements (low byte: elements 0..15 of the block)
-        const float dsb = h2f((uint16_t)(S.e & 0xffffu));
-        c = S.dy * (dsb * (float)(int)(int8_t)(wv & 0xffu));
-        c2 = S.dy * (dsb * (float)(int)(int8_t)((wv >> 8) & 0xffu));
+        c = dyd * (float)(int)(int8_t)(wv & 0xffu);
+        c2 = dyd * (float)(int)(int8_t)((wv >> 8) & 0xffu);
         const u4v& qq = S.q[j >> 1];
         f = (j & 1) ? q8_frag(qq.z, qq.w) : q8_frag(qq.x, qq.y);
       }
