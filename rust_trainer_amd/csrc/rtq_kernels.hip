@@ -3035,9 +3035,9 @@ __device__ __forceinline__ void dxv1_tile(const DxArgs& a) {
           const u4v& qq = S.q[j >> 1];
           f = (j & 1) ? q8_frag(qq.z, qq.w) : q8_frag(qq.x, qq.y);
         }
-      } else if constexpr (FMT == FMT_Q4_K) {  // value d sc u - dmin m
-        c = dyd * (float)(wv & 0x3fu);
-        bias[j] = fmaf(dym, (float)((wv >> 8) & 0x3fu), bias[j]);
+      } else if constexpr (FMT == FMT_Q4_K) {  // value d sc u - dmin m (sc, m < 64: whole bytes)
+        c = dyd * (float)(wv & 0xffu);
+        bias[j] = fmaf(dym, (float)((wv >> 8) & 0xffu), bias[j]);
         f = q4_0_frag<0>(comp(S.q[0], j));
       } else {  // Q6_K: value d sc q, sc per 16 elements (low byte: elements 0..15 of the block)
         c = dyd * (float)(int)(int8_t)(wv & 0xffu);
