@@ -155,6 +155,10 @@ struct FwdArgs {
 #ifndef RTQ_GQ_D
 #define RTQ_GQ_D 4
 #endif
+#ifndef RTQ_DXV1_D
+#define RTQ_DXV1_D 4  // rtq_dxv1_*: register ring depth (row groups; loads D - 1 ahead); 6 and 8
+                      // measured slower (LM head backward at T = 1, Q4_0 24.1 -> 25.3 / 26.2 us)
+#endif
 #ifndef RTQ_DX16_D
 #define RTQ_DX16_D 4  // rtq_dx16_*: register ring depth (steps of 32 rows; loads D - 1 steps ahead)
 #endif

@@ -2979,7 +2979,7 @@ struct Dxv1Slot {
 template <int FMT>
 __device__ __forceinline__ void dxv1_tile(const DxArgs& a) {
   constexpr bool KQ = is_kquant(FMT), B8 = byte_codes(FMT);
-  constexpr int D = 4;
+  constexpr int D = RTQ_DXV1_D;
   const int Kc = a.Kp / 128, ngroups = a.Np / 16;
   const int nmain = Kc * a.nsplit;
   const int id = blockIdx.x;
