@@ -302,14 +302,19 @@ __device__ __forceinline__ void lora_load_m(const float* M, int ldm, int r, int 
 // The product for this thread's S values sv (its row's columns k0 + 16 sg .., zero past T and kend)
 // and the first rank tile's M values mv (lora_load_m at j0 = 0, loaded by the caller so that they
 // travel with its own loads); each next tile's loads are issued before the current one is contracted.
-__device__ __forceinline__ void lora_partial_v(const float sv[16], float mv[16], int T, const float* M, int ldm,
+// NTOK = 8: sx already holds the 8 token rows (and zeros in rows 8 .. 15), sv is not read, and only
+// tokens t0 .. t0 + 7 are written.
+template <int NTOK = 16>
+__device__ __forceinline__ void lora_partial_v(const float* sv, float mv[16], int T, const float* M, int ldm,
                                                int r, int k0, int kend, int t0, float* out, int pstride, int pidx,
                                                float* sx, float* sm, float* red) {
   constexpr int LDX = RTQ_ACT_KQ + 1;
   const int tid = threadIdx.x, tl = tid >> 4, sg = tid & 15;
   const int lane = tid & 63, w = tid >> 6, li = lane & 15, g = lane >> 4;
+  if (NTOK == 16) {
 #pragma unroll
-  for (int i = 0; i < 16; i++) sx[tl * LDX + sg * 16 + i] = sv[i];
+    for (int i = 0; i < 16; i++) sx[tl * LDX + sg * 16 + i] = sv[i];
+  }
   for (int j0 = 0; j0 < r; j0 += 16) {
 #pragma unroll
     for (int i = 0; i < 16; i++) sm[tl * LDX + sg * 16 + i] = mv[i];
@@ -327,7 +332,7 @@ __device__ __forceinline__ void lora_partial_v(const float sv[16], float mv[16],
     {
       const int tt = tid >> 4, jj = tid & 15, ty = t0 + tt, jo = j0 + jj;
       const float ps = (red[tid] + red[256 + tid]) + (red[512 + tid] + red[768 + tid]);
-      if (ty < T && jo < r) out[((int64_t)ty * r + jo) * pstride + pidx] = ps;
+      if (tt < NTOK && ty < T && jo < r) out[((int64_t)ty * r + jo) * pstride + pidx] = ps;
     }
     __syncthreads();
   }
@@ -708,6 +713,119 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
 
 extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_0(ActArgs a) { act_prep<false>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_k(ActArgs a) { act_prep<true>(a); }
+
+// The block-norm activation kernel on 8-token tiles: twice act_prep's workgroups for a given T, each
+// reading 8 rows whole for the sums of squares instead of 16.  RMSNorm rows (two per wave), Q8_0
+// codes as f16 fragments and the LoRA-down partials, each with act_prep's arithmetic in the same
+// order, so the outputs carry the same bits.  Thread (token tl = tid / 32, segment sg = tid % 32)
+// holds 8 columns k0 + 8 sg ..; the four threads of a 32-column block are adjacent lanes.  Only for
+// the norm input without the GEMV seed (xg), int8 fragments, SwiGLU input or a y to zero.
+extern "C" __global__ __launch_bounds__(256) void rtq_act_prep8_q8_0(ActArgs a) {
+  constexpr int KQ = RTQ_ACT_KQ, LDX = KQ + 1;
+  __shared__ float sx[16 * LDX];
+  __shared__ float sa[16 * LDX];
+  __shared__ float red[4 * 256];
+  const int tid = threadIdx.x, tl = tid >> 5, sg = tid & 31;
+  const int t0 = blockIdx.x * 8, t = t0 + tl;
+  const int Kc = a.Kp / 128;
+  const int k0 = blockIdx.y * KQ, kk = k0 + sg * 8;
+  float mv[16];
+  if (a.A) lora_load_m(a.A, a.K, a.r, 0, k0, a.K, mv);  // uniform; in flight during the norm
+  {
+    // wave w normalises rows t0 + 2w, t0 + 2w + 1 whole (as act_prep, every load issued first)
+    const int lane = tid & 63, w = tid >> 6, nv = a.K / 256, qy = blockIdx.y;
+    const bool has_b = a.nb != nullptr;
+    const float* pb = has_b ? a.nb : a.na;
+    f4 wv[4], xv[2][4], bv[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) wv[i] = *reinterpret_cast<const f4*>(a.nw + 4 * lane + 256 * min(i, nv - 1));
+#pragma unroll
+    for (int rr = 0; rr < 2; rr++) {
+      const int64_t ro = (int64_t)min(t0 + 2 * w + rr, a.T - 1) * a.K + 4 * lane;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        xv[rr][i] = *reinterpret_cast<const f4*>(a.na + ro + 256 * min(i, nv - 1));
+        bv[rr][i] = *reinterpret_cast<const f4*>(pb + ro + 256 * min(i, nv - 1));
+      }
+    }
+#pragma unroll
+    for (int rr = 0; rr < 2; rr++) {
+      const bool rin = t0 + 2 * w + rr < a.T;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float xs = has_b ? xv[rr][i][e] + bv[rr][i][e] : xv[rr][i][e];
+          xv[rr][i][e] = (rin && i < nv) ? xs : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < 2; rr++) {
+      const int row = t0 + 2 * w + rr;
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (i < nv)
+#pragma unroll
+          for (int e = 0; e < 4; e++) s = s + xv[rr][i][e] * xv[rr][i][e];
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+      const float ir = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(s, (float)a.K) + a.neps));
+      f4 y = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (i < nv && i == qy) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) y[e] = (xv[rr][i][e] * ir) * (wv[i][e] + a.noff);
+          if (row < a.T) {
+            const int64_t o = (int64_t)row * a.K + 256 * i + 4 * lane;
+            if (a.nb) *reinterpret_cast<f4*>(a.nh + o) = xv[rr][i];
+            *reinterpret_cast<f4*>(const_cast<float*>(a.x) + o) = y;
+          }
+        }
+      if (qy == 0 && lane == 0 && row < a.T) a.ninv[row] = ir;
+#pragma unroll
+      for (int e = 0; e < 4; e++) sx[(2 * w + rr) * LDX + 4 * lane + e] = y[e];
+    }
+    // rows 8 .. 15 of the LoRA product's token tile: zeros
+    for (int i = tid; i < 8 * LDX; i += 256) sx[8 * LDX + i] = 0.0f;
+  }
+  __syncthreads();
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) v[i] = sx[tl * LDX + sg * 8 + i];
+  // Q8_0 codes: d = amax / 127 over the block (four adjacent lanes), codes round(x / d)
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  const float d = __fdiv_rn(amax, 127.0f);
+  const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+  _Float16 q[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) q[i] = (_Float16)roundf(__fmul_rn(v[i], id));
+  const float dstore = (float)(_Float16)d;
+  if (kk < a.Kp) {
+    // block elements 8 qq .. 8 qq + 7: half hf = qq / 2, its k-groups 2 (qq % 2) and 2 (qq % 2) + 1
+    const int b = kk >> 5, qq = sg & 3, hf = qq >> 1, kc = b >> 2, j = b & 3;
+    u2v* xq = reinterpret_cast<u2v*>(a.xq) + ((((int64_t)(t >> 4) * Kc + kc) * 4 + j) * 64 + (t & 15)) * 2 + hf;
+#pragma unroll
+    for (int gg = 0; gg < 2; gg++) {
+      const half2v lo = {q[4 * gg], q[4 * gg + 1]}, hi = {q[4 * gg + 2], q[4 * gg + 3]};
+      u2v wd;
+      wd.x = __builtin_bit_cast(uint32_t, lo);
+      wd.y = __builtin_bit_cast(uint32_t, hi);
+      xq[(2 * (qq & 1) + gg) * 16 * 2] = wd;
+    }
+    const bool real = t < a.T && kk < a.K;
+    if (qq == 0) a.xd[((int64_t)kc * a.Tp + t) * 4 + j] = real ? dstore : 0.0f;
+    if (a.xdh && qq == 0)
+      a.xdh[((int64_t)kc * a.Tp + t) * 4 + j] = real ? __builtin_bit_cast(uint16_t, (_Float16)dstore) : (uint16_t)0;
+  }
+  if (a.A)  // uniform
+    lora_partial_v<8>(nullptr, mv, a.T, a.A, a.K, a.r, k0, a.K, t0, a.hp, gridDim.y, blockIdx.y, sx, sa, red);
+}
 
 // ============================================================== forward GEMM (Q4_0 / Q8_0)
 // MFMA orientation: A operand = 16 weight rows x 32 columns, B operand = 32 columns x 16 tokens,
