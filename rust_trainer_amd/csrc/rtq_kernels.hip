@@ -714,34 +714,38 @@ __device__ __forceinline__ void act_prep(const ActArgs& a) {
 extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_0(ActArgs a) { act_prep<false>(a); }
 extern "C" __global__ __launch_bounds__(256) void rtq_act_prep_q8_k(ActArgs a) { act_prep<true>(a); }
 
-// The block-norm activation kernel on 8-token tiles: twice act_prep's workgroups for a given T, each
-// reading 8 rows whole for the sums of squares instead of 16.  RMSNorm rows (two per wave), Q8_0
-// codes as f16 fragments and the LoRA-down partials, each with act_prep's arithmetic in the same
-// order, so the outputs carry the same bits.  Thread (token tl = tid / 32, segment sg = tid % 32)
-// holds 8 columns k0 + 8 sg ..; the four threads of a 32-column block are adjacent lanes.  Only for
-// the norm input without the GEMV seed (xg), int8 fragments, SwiGLU input or a y to zero.
-extern "C" __global__ __launch_bounds__(256) void rtq_act_prep8_q8_0(ActArgs a) {
+// The block-norm activation kernel on NT-token tiles (NT = 8 or 4): 16 / NT times act_prep's
+// workgroups for a given T, each reading NT rows whole for the sums of squares instead of 16.
+// RMSNorm rows (NT / 4 per wave), Q8_0 codes as f16 fragments and the LoRA-down partials, each with
+// act_prep's arithmetic in the same order, so the outputs carry the same bits.  Thread (token
+// tl = tid / (256 / NT), segment sg) holds NT columns k0 + NT sg ..; the 32 / NT threads of a
+// 32-column block are adjacent lanes.  Only for the norm input without the GEMV seed (xg), int8
+// fragments, SwiGLU input or a y to zero.
+template <int NT>
+__device__ __forceinline__ void act_prep_norm(const ActArgs& a) {
+  static_assert(NT == 8 || NT == 4, "8- or 4-token tiles");
+  constexpr int TPT = 256 / NT, RPW = NT / 4, BL = 32 / NT;  // threads per token, rows per wave, lanes per block
   constexpr int KQ = RTQ_ACT_KQ, LDX = KQ + 1;
   __shared__ float sx[16 * LDX];
   __shared__ float sa[16 * LDX];
   __shared__ float red[4 * 256];
-  const int tid = threadIdx.x, tl = tid >> 5, sg = tid & 31;
-  const int t0 = blockIdx.x * 8, t = t0 + tl;
+  const int tid = threadIdx.x, tl = tid / TPT, sg = tid % TPT;
+  const int t0 = blockIdx.x * NT, t = t0 + tl;
   const int Kc = a.Kp / 128;
-  const int k0 = blockIdx.y * KQ, kk = k0 + sg * 8;
+  const int k0 = blockIdx.y * KQ, kk = k0 + sg * NT;
   float mv[16];
   if (a.A) lora_load_m(a.A, a.K, a.r, 0, k0, a.K, mv);  // uniform; in flight during the norm
   {
-    // wave w normalises rows t0 + 2w, t0 + 2w + 1 whole (as act_prep, every load issued first)
+    // wave w normalises rows t0 + RPW w .. t0 + RPW w + RPW - 1 whole (as act_prep, every load issued first)
     const int lane = tid & 63, w = tid >> 6, nv = a.K / 256, qy = blockIdx.y;
     const bool has_b = a.nb != nullptr;
     const float* pb = has_b ? a.nb : a.na;
-    f4 wv[4], xv[2][4], bv[2][4];
+    f4 wv[4], xv[RPW][4], bv[RPW][4];
 #pragma unroll
     for (int i = 0; i < 4; i++) wv[i] = *reinterpret_cast<const f4*>(a.nw + 4 * lane + 256 * min(i, nv - 1));
 #pragma unroll
-    for (int rr = 0; rr < 2; rr++) {
-      const int64_t ro = (int64_t)min(t0 + 2 * w + rr, a.T - 1) * a.K + 4 * lane;
+    for (int rr = 0; rr < RPW; rr++) {
+      const int64_t ro = (int64_t)min(t0 + RPW * w + rr, a.T - 1) * a.K + 4 * lane;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         xv[rr][i] = *reinterpret_cast<const f4*>(a.na + ro + 256 * min(i, nv - 1));
@@ -749,8 +753,8 @@ extern "C" __global__ __launch_bounds__(256) void rtq_act_prep8_q8_0(ActArgs a) 
       }
     }
 #pragma unroll
-    for (int rr = 0; rr < 2; rr++) {
-      const bool rin = t0 + 2 * w + rr < a.T;
+    for (int rr = 0; rr < RPW; rr++) {
+      const bool rin = t0 + RPW * w + rr < a.T;
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -760,8 +764,8 @@ extern "C" __global__ __launch_bounds__(256) void rtq_act_prep8_q8_0(ActArgs a) 
         }
     }
 #pragma unroll
-    for (int rr = 0; rr < 2; rr++) {
-      const int row = t0 + 2 * w + rr;
+    for (int rr = 0; rr < RPW; rr++) {
+      const int row = t0 + RPW * w + rr;
       float s = 0.0f;
 #pragma unroll
       for (int i = 0; i < 4; i++)
@@ -785,38 +789,38 @@ extern "C" __global__ __launch_bounds__(256) void rtq_act_prep8_q8_0(ActArgs a) 
         }
       if (qy == 0 && lane == 0 && row < a.T) a.ninv[row] = ir;
 #pragma unroll
-      for (int e = 0; e < 4; e++) sx[(2 * w + rr) * LDX + 4 * lane + e] = y[e];
+      for (int e = 0; e < 4; e++) sx[(RPW * w + rr) * LDX + 4 * lane + e] = y[e];
     }
-    // rows 8 .. 15 of the LoRA product's token tile: zeros
-    for (int i = tid; i < 8 * LDX; i += 256) sx[8 * LDX + i] = 0.0f;
+    // rows NT .. 15 of the LoRA product's token tile: zeros
+    for (int i = tid; i < (16 - NT) * LDX; i += 256) sx[NT * LDX + i] = 0.0f;
   }
   __syncthreads();
-  float v[8];
+  float v[NT];
 #pragma unroll
-  for (int i = 0; i < 8; i++) v[i] = sx[tl * LDX + sg * 8 + i];
-  // Q8_0 codes: d = amax / 127 over the block (four adjacent lanes), codes round(x / d)
+  for (int i = 0; i < NT; i++) v[i] = sx[tl * LDX + sg * NT + i];
+  // Q8_0 codes: d = amax / 127 over the block (BL adjacent lanes), codes round(x / d)
   float amax = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
-  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  for (int i = 0; i < NT; i++) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int m = 1; m < BL; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
   const float d = __fdiv_rn(amax, 127.0f);
   const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-  _Float16 q[8];
+  _Float16 q[NT];
 #pragma unroll
-  for (int i = 0; i < 8; i++) q[i] = (_Float16)roundf(__fmul_rn(v[i], id));
+  for (int i = 0; i < NT; i++) q[i] = (_Float16)roundf(__fmul_rn(v[i], id));
   const float dstore = (float)(_Float16)d;
   if (kk < a.Kp) {
-    // block elements 8 qq .. 8 qq + 7: half hf = qq / 2, its k-groups 2 (qq % 2) and 2 (qq % 2) + 1
-    const int b = kk >> 5, qq = sg & 3, hf = qq >> 1, kc = b >> 2, j = b & 3;
+    // block elements e0 .. e0 + NT - 1 (e0 = NT qq): half hf = e0 / 16, its k-groups (e0 % 16) / 4 ..
+    const int b = kk >> 5, qq = sg % BL, e0 = NT * qq, hf = e0 >> 4, g0 = (e0 & 15) >> 2, kc = b >> 2, j = b & 3;
     u2v* xq = reinterpret_cast<u2v*>(a.xq) + ((((int64_t)(t >> 4) * Kc + kc) * 4 + j) * 64 + (t & 15)) * 2 + hf;
 #pragma unroll
-    for (int gg = 0; gg < 2; gg++) {
+    for (int gg = 0; gg < NT / 4; gg++) {
       const half2v lo = {q[4 * gg], q[4 * gg + 1]}, hi = {q[4 * gg + 2], q[4 * gg + 3]};
       u2v wd;
       wd.x = __builtin_bit_cast(uint32_t, lo);
       wd.y = __builtin_bit_cast(uint32_t, hi);
-      xq[(2 * (qq & 1) + gg) * 16 * 2] = wd;
+      xq[(g0 + gg) * 16 * 2] = wd;
     }
     const bool real = t < a.T && kk < a.K;
     if (qq == 0) a.xd[((int64_t)kc * a.Tp + t) * 4 + j] = real ? dstore : 0.0f;
@@ -824,8 +828,10 @@ extern "C" __global__ __launch_bounds__(256) void rtq_act_prep8_q8_0(ActArgs a) 
       a.xdh[((int64_t)kc * a.Tp + t) * 4 + j] = real ? __builtin_bit_cast(uint16_t, (_Float16)dstore) : (uint16_t)0;
   }
   if (a.A)  // uniform
-    lora_partial_v<8>(nullptr, mv, a.T, a.A, a.K, a.r, k0, a.K, t0, a.hp, gridDim.y, blockIdx.y, sx, sa, red);
+    lora_partial_v<NT>(nullptr, mv, a.T, a.A, a.K, a.r, k0, a.K, t0, a.hp, gridDim.y, blockIdx.y, sx, sa, red);
 }
+extern "C" __global__ __launch_bounds__(256) void rtq_act_prep8_q8_0(ActArgs a) { act_prep_norm<8>(a); }
+extern "C" __global__ __launch_bounds__(256) void rtq_act_prep4_q8_0(ActArgs a) { act_prep_norm<4>(a); }
 
 // ============================================================== forward GEMM (Q4_0 / Q8_0)
 // MFMA orientation: A operand = 16 weight rows x 32 columns, B operand = 32 columns x 16 tokens,

@@ -160,6 +160,7 @@ enum Kid {
   K_HEAD_GRAD,
   K_HEAD_NORM_BWD,
   K_ACT_PREP8,   // Q8_0 activations of the block norms on 8-token tiles
+  K_ACT_PREP4,   // the same on 4-token tiles
   K_ROWS,        // + format
   K_MODEL = K_ROWS + F_COUNT,  // + RtqModelKernel: the decoder block (rtq_model.cpp)
   K_COUNT = K_MODEL + KM_COUNT
@@ -188,7 +189,7 @@ constexpr const char* kKernelNames[] = {
     "rtq_bwd_finish",       "rtq_bwd_finish16",     "rtq_bwd_finish_dx",    "rtq_bwd_finish_rows",  "rtq_lora_grads",       "rtq_lora_grads16",     "rtq_lora_grads_t",     "rtq_lora_grads_t16",
     "rtq_dense_rows",       "rtq_dense_bias",
     "rtq_head_norm",        "rtq_head_max",         "rtq_head_sum",         "rtq_head_grad",
-    "rtq_head_norm_bwd",    "rtq_act_prep8_q8_0",
+    "rtq_head_norm_bwd",    "rtq_act_prep8_q8_0",   "rtq_act_prep4_q8_0",
     "rtq_rows_q4_0",        "rtq_rows_q8_0",        "rtq_rows_q4_k",        "rtq_rows_q6_k",
     "rtq_m_rmsnorm",        "rtq_m_rmsnorm_bwd",    "rtq_m_qk_prep",        "rtq_m_qk_bwd",
     "rtq_m_gemm",           "rtq_m_softmax",        "rtq_m_softmax_bwd",    "rtq_m_group_sum",
@@ -231,7 +232,8 @@ struct rtq_ctx {
                       // half of them
   int fwd_waves = 8;  // waves splitting K in the wide Q4_0 / Q8_0 forward (RTQ_FWD_WAVES: 4 or 8)
   int fwd_rg = -1;    // row groups of 16 per eight-wave forward tile: -1 automatic, 1, 2 or 3 (RTQ_FWD_RG)
-  int act8 = 1;       // the block norms' Q8_0 activation kernel on 8-token tiles (RTQ_ACT8=0: 16)
+  int act_tt = 8;     // token tile of the block norms' Q8_0 activation kernel: 16, 8 or 4 (RTQ_ACT_TT;
+                      // configs[2] step, activation kernels: 1.11 / 0.97-1.00 / 1.08 ms)
   int g64_min = -1;   // fewest 64-token g-partial workgroups (else 16-token ones): -1 = CUs / 2 (RTQ_G64_MIN)
   int fwd_mm = -1;    // large-grid forward: -1 automatic, 0 never, 1 / 2 / 3 the 128- / 64- / 32-token tiles
                       // whenever the format allows (RTQ_FWD_MM)
@@ -720,9 +722,9 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
   aa.xq_i8 = mmi8 ? 1 : 0;
   // the block norms' activations (Q8_0 f16 fragments) on 8-token tiles: twice the workgroups, each
   // reading half the rows whole for the sums of squares (the same bits as the 16-token kernel)
-  const bool act8 = c->act8 && nf && !kq && !mmi8 && !aa.zero_y && !aa.sg && !aa.xg;
-  RTQ_TRY(launch(c, act8 ? K_ACT_PREP8 : kq ? K_ACT_PREP_K : K_ACT_PREP,
-                 dim3((unsigned)(p.Tp / (act8 ? 8 : 16)), (unsigned)p.nhp), dim3(256), st, aa));
+  const int att = c->act_tt < 16 && nf && !kq && !mmi8 && !aa.zero_y && !aa.sg && !aa.xg ? c->act_tt : 16;
+  RTQ_TRY(launch(c, att == 8 ? K_ACT_PREP8 : att == 4 ? K_ACT_PREP4 : kq ? K_ACT_PREP_K : K_ACT_PREP,
+                 dim3((unsigned)(p.Tp / att), (unsigned)p.nhp), dim3(256), st, aa));
   FwdArgs fa{};
   fa.wq = w->wq;
   fa.wd = w->wd;
@@ -1140,7 +1142,7 @@ rtq_status rtq_ctx_create(int device, rtq_ctx** out) {
   if (const char* e = getenv("RTQ_DXV_WPC")) c->dxv_wpc = std::max(1, std::min(16, atoi(e)));
   if (const char* e = getenv("RTQ_GEMVQ_WPC")) c->gemvq_wpc = std::min(std::max(atoi(e), 0), 32);
   if (const char* e = getenv("RTQ_FWD_RG")) c->fwd_rg = std::min(std::max(atoi(e), 1), 3);
-  if (const char* e = getenv("RTQ_ACT8")) c->act8 = atoi(e) ? 1 : 0;
+  if (const char* e = getenv("RTQ_ACT_TT")) c->act_tt = atoi(e) <= 4 ? 4 : atoi(e) <= 8 ? 8 : 16;
   if (const char* e = getenv("RTQ_G64_MIN")) c->g64_min = atoi(e);
   hipError_t e = hipModuleLoadData(&c->mod, rtq_hsaco_begin);
   if (e != hipSuccess) {

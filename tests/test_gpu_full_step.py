@@ -10,7 +10,7 @@ per-op parity of one block at this shape is in tests/test_gpu_block_ops.py):
 * a step replayed from the captured HIP graph equals the same step run eagerly, bit for bit;
 * the same step repeated reproduces every bit (no atomics in the step's reductions);
 * the block's RMSNorms formed inside the next linear's activation kernel give the bits of the norm
-  kernel run first (a model loaded with RTQ_NORM_FUSE=0).
+  kernel run first (a model loaded with RTQ_NORM_FUSE=0), on 16-, 8- and 4-token tiles.
 """
 import numpy as np
 import pytest
@@ -38,12 +38,12 @@ def test_config2_full_step_properties(ctx, monkeypatch):
     targets = [rt.Target(int(p), int(toks[p + 1])) for p in range(t - n - 1, t - 1)]
     wts = np.full(n, 1.0 / n, np.float32)
 
-    def load(graph):
+    def load(graph, c=None):
         if graph:
             monkeypatch.delenv("RTQ_STEP_GRAPH", raising=False)
         else:
             monkeypatch.setenv("RTQ_STEP_GRAPH", "0")
-        m = rt.GpuModel.from_gguf(g, ctx=ctx)
+        m = rt.GpuModel.from_gguf(g, ctx=c or ctx)
         monkeypatch.delenv("RTQ_STEP_GRAPH", raising=False)
         m.attach_lora(16, 32.0, seed=1)
         for i in range(m.lora_count()):
@@ -86,6 +86,18 @@ def test_config2_full_step_properties(ctx, monkeypatch):
     for a, b in zip(gr_u, gr):
         np.testing.assert_array_equal(a, b)
     unfused.close()
+    for tt in ("16", "4"):  # the norms' activation kernel on 16- and 4-token tiles (default 8): same bits
+        monkeypatch.setenv("RTQ_ACT_TT", tt)
+        c2 = rt.Context(0)
+        monkeypatch.delenv("RTQ_ACT_TT")
+        other = load(graph=False, c=c2)
+        lp_o, hits_o, gr_o = step(other)
+        np.testing.assert_array_equal(lp_o, lp)
+        assert hits_o == hits
+        for a, b in zip(gr_o, gr):
+            np.testing.assert_array_equal(a, b)
+        other.close()
+        c2.close()
     model.checkpointing = True
     lp_c, hits_c, gr_c = step(model)
     assert model.checkpointing is True and hits_c == hits
