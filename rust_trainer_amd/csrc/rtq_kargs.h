@@ -52,7 +52,8 @@
 
 // ---------------------------------------------------------------- forward activation prep
 // Grid (Tp/16, nhp), nhp = Kp / RTQ_ACT_KQ rounded up to a multiple of 4; workgroup (x, y)
-// covers 16 tokens x columns [256y, 256y + 256).  x [T x K] f32 ->
+// covers 16 tokens x columns [256y, 256y + 256) (the block-norm kernels rtq_act_prep8 / 4: 8 or 4
+// tokens, grid (Tp/8 or Tp/4, nhp)).  x [T x K] f32 ->
 //   xq: Q8_0 codes as exact-f16 MFMA fragments: uint4 [Tp/16][Kp/128][4][64] (8 per lane per block)
 //   xd: f32 [Kp/128][Tp][4]  (value of the fp16 scale of block 4kc+j of token t; 0 for padding)
 //   hp: LoRA down-projection partials [T][r][nhp] (src/linear.rs:85): partial y sums the
