@@ -781,8 +781,10 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
 //   t > 16 (rtq_dx_*): K chunks x 64-token tiles x row splits, about one 8-wave workgroup per CU
 //     (more splits add partial-sum traffic: each split writes and the finish kernel reads a
 //     64-token-padded T x K block);
-//   t <= 16 (rtq_dx16_*): K chunks x row splits, about three 4-wave workgroups per CU with at least
-//     four 32-row steps each (partials are T x K floats per split);
+//   t <= 16 (rtq_dx16_*): K chunks x row splits, about two 4-wave workgroups per CU with at least
+//     four 32-row steps each (partials are T x K floats per split; LM head 151936 x 1024 at T = 16,
+//     one backward call, 64 against 96 splits: Q4_0 58.7 / 62.4 us, Q8_0 64.1 / 65.9, Q4_K 72.7 /
+//     73.7, Q6_K 75.1 / 76.1);
 //   rtq_dxw_*: as the first, with 256-token tiles, where that grid fills the CUs (see dx_plan).
 struct DxPlan {
   int64_t splits, nps;
@@ -808,7 +810,7 @@ DxPlan dx_plan(const rtq_ctx* c, const rtq_weight* w, int64_t t) {
   int64_t splits;
   if (p.tok16)
     splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(std::max<int64_t>(steps / 4, 1), 256),
-                                                    cdiv(3 * c->cu_count, Kc)));
+                                                    cdiv(2 * c->cu_count, Kc)));
   else if (p.wide)
     splits = wsplits;
   else
