@@ -589,11 +589,13 @@ rtq_status enqueue_forward(rtq_ctx* c, const rtq_weight* w, const float* x, int6
     if (lds <= 65536) {
       const int rg = byte_codes(w->type) ? RTQ_GQ_RG8 : RTQ_GQ_RG4;
       const int64_t ntiles = cdiv(w->Np / 16, rg);
-      // waves per CU: 24 for the nibble layouts (their VGPRs allow 20 - 24 resident), 8 for the byte
-      // ones (longer streams per wave; LM head at t = 1, one MI355X: Q4_0 21.1 us at 24 against 23.4
-      // at 16, Q4_K 24.8 against 26.7, Q6_K 34.0 at 8 against 39.2 at 16, Q8_0 32.7 at 8 or 24);
-      // every wave takes the same number of tiles (the last ones fewer)
-      const int64_t wpc = c->gemvq_wpc > 0 ? c->gemvq_wpc : (byte_codes(w->type) ? 8 : 24);
+      // waves per CU: 24 for the nibble layouts (their VGPRs allow 20 - 24 resident), 8 for Q6_K and 4
+      // for Q8_0 (longer streams per wave; LM head at t = 1, one MI355X: Q4_0 21.1 us at 24 against
+      // 23.4 at 16, Q4_K 24.8 against 26.7, Q6_K 34.4 at 8 against 36.8 at 6 and 37.4 at 10, Q8_0
+      // 30.7 at 4 against 31.9 at 8: 238 workgroups, one per CU, where 5 or 6 give some CUs two,
+      // 38.5 / 35.5 us); every wave takes the same number of tiles (the last ones fewer)
+      const int64_t wpc = c->gemvq_wpc > 0 ? c->gemvq_wpc
+                                            : (w->type == RTQ_TYPE_Q8_0 ? 4 : byte_codes(w->type) ? 8 : 24);
       const int64_t maxw = (int64_t)c->cu_count * wpc, per = cdiv(ntiles, maxw), nwaves = cdiv(ntiles, per);
       GemvqArgs ga{w->wq, w->wdr, w->wsb, (int)w->Np, (int)w->Kp, x, (int)t, (int)w->rows, (int)w->cols, y, bias,
                    lora ? la : nullptr, lb, lora ? (int)r : 0, s, rbv, (int)ntiles, (int)per};
