@@ -957,6 +957,24 @@ def test_dxv1_lora_backward(ctx, wtype):
     assert rel_err(lin.lora.gb, wgb) <= TOL
 
 
+@pytest.mark.parametrize("t", [1, 5, 16])
+@pytest.mark.parametrize("wtype", [O.Q4_0, O.Q8_0])
+def test_many_split_finish_ragged_columns(ctx, wtype, t):
+    """FrozenMatmul::backward_input at T <= 16 over 8192 rows and K = 160 (two and a half 64-column
+    segments): 64 row splits, summed by the workgroup-per-(token, 64 columns) finish with its last
+    segment half outside K; accumulated onto a non-zero dx, against the oracle and the dense dy . W"""
+    n, k = 8192, 160
+    blocks, _, dy = make(wtype, n, k, t)
+    w = hip(ctx, wtype, blocks, n, k)
+    dx0 = O.Rng(7).vec_normal(t * k, 1.0).astype(np.float32)
+    dx = dx0.copy()
+    _, names = _ran(ctx, lambda: w.backward_input(dy, t, dx))
+    assert "rtq_bwd_finish_rows" in names, names
+    want = O.frozen_backward_input(wtype, blocks, n, k, dy, dx=np.zeros((t, k), np.float32), nthreads=16)
+    assert rel_err(dx - dx0, want) <= TOL
+    _dense_dx_check(wtype, blocks, n, k, dy, (dx - dx0).astype(np.float32))
+
+
 # ---------------------------------------------------------------- g partials: 64 / 32 / 16 tokens per workgroup
 @pytest.fixture(scope="module", params=[16, 32, 64])
 def ctx_gtok(request):
