@@ -2421,8 +2421,11 @@ __device__ __forceinline__ void gemvq(const GemvqArgs& a) {
     }
   };
   GSlot<FMT, RG> sl[D];
+  // (Q4_K at T = 1: one item fewer in flight during the activation work, the last issued after it,
+  // so that the kernel fits five waves per SIMD)
+  constexpr int PRE = (FMT == FMT_Q4_K && NT == 1) ? D - 2 : D - 1;
 #pragma unroll
-  for (int s0 = 0; s0 < D - 1; s0++) issue(sl[s0], s0);
+  for (int s0 = 0; s0 < PRE; s0++) issue(sl[s0], s0);
   // ---- activation codes: one 32-column block (token t, block b) per thread and pass
   for (int u0 = 0; u0 < NT * Kb; u0 += (int)blockDim.x) {
     const int u = u0 + tid, t = u / Kb, b = u % Kb, k0 = 32 * b;
@@ -2523,6 +2526,8 @@ __device__ __forceinline__ void gemvq(const GemvqArgs& a) {
     }
   }
   __syncthreads();
+#pragma unroll
+  for (int s0 = PRE; s0 < D - 1; s0++) issue(sl[s0], s0);
 
   float acc[RG][NT];
   int s1[KQ ? RG : 1][NT], s2[KQ ? RG : 1][NT];
