@@ -2360,7 +2360,7 @@ __device__ __forceinline__ void gemv_tile(const FwdArgs& a) {
   }
 RTQ_GEMV(rtq_gemv_q4_0, FMT_Q4_0, 4, 4)
 RTQ_GEMV(rtq_gemv_q8_0, FMT_Q8_0, 2, 4)
-RTQ_GEMV(rtq_gemv_q4_k, FMT_Q4_K, 4, 4)
+RTQ_GEMV(rtq_gemv_q4_k, FMT_Q4_K, 4, 2)
 RTQ_GEMV(rtq_gemv_q6_k, FMT_Q6_K, 2, 4)
 
 // ============================================================== forward GEMV for T <= 4, one launch
