@@ -2360,8 +2360,11 @@ __device__ __forceinline__ void gemv_tile(const FwdArgs& a) {
   }
 RTQ_GEMV(rtq_gemv_q4_0, FMT_Q4_0, 4, 4)
 RTQ_GEMV(rtq_gemv_q8_0, FMT_Q8_0, 2, 4)
+// (Q4_K, Q6_K: 2-deep rings, Q6_K held to five waves per SIMD (96 VGPRs), so that an LM head's 594 /
+// 1187 workgroups are resident in one round; at 16 tokens Q4_K 42.6 -> 39.5 us, Q6_K 51.3 -> 49.0;
+// Q8_0 measured slower so: 43.1 -> 44.2)
 RTQ_GEMV(rtq_gemv_q4_k, FMT_Q4_K, 4, 2)
-RTQ_GEMV(rtq_gemv_q6_k, FMT_Q6_K, 2, 4)
+extern "C" __global__ __launch_bounds__(256, 5) void rtq_gemv_q6_k(FwdArgs a) { gemv_tile<FMT_Q6_K, 2, 2>(a); }
 
 // ============================================================== forward GEMV for T <= 4, one launch
 // y = x W^T (+ bias) (+ s (x A^T) B^T) for T <= NT tokens (NT 1 or 4).  Each workgroup first
